@@ -1,0 +1,234 @@
+// GDN fused recurrent forward (decode / speculative decode), GQA-native, with a
+// slot-indexed fp32 (or bf16) state pool updated in place.
+//
+// Per sequence n, query head h, token t (reference kernel
+// vllm-inference/src/primed_vllm/gdn/ops/fused_recurrent_gqa.py:111-144):
+//   q,k <- q/sqrt(|q|^2+1e-6), k/sqrt(|k|^2+1e-6);  q <- q*scale
+//   S <- exp(g) S;  u <- beta (v - S^T k);  S <- S + k u^T;  o <- S^T q
+//
+// Layout & mapping.  One workgroup per (sequence, head) with V/32 waves; wave w
+// owns the state columns [32w, 32w+32) for all K rows, kept in registers for
+// the whole token loop.  Lane l owns 4 consecutive columns (c = l&7) of
+// R = K/8 consecutive rows (r = l>>3).  One load instruction of the wave
+// touches 8 rows x 128 contiguous bytes, so the four waves of a workgroup
+// stream the head's K*V*4-byte state as full 512-byte rows.  Column sums over
+// k (S^T k, S^T q) are a per-lane partial over R rows plus a 3-step xor
+// butterfly over the row-group lane bits — no LDS, no barriers.
+//
+// Roofline: HBM-bound read-modify-write of the state, 2*K*V*sizeof(state)
+// bytes per (sequence, head) per call (q/k/v/o add 6*K*2 bytes).
+#include "common.hpp"
+
+namespace hmx {
+
+struct RecurrentParams {
+  const void* q; const void* k; const void* v;
+  const void* g; int g_dt;
+  const void* beta; int beta_dt; int beta_headwise;
+  void* o;
+  const void* h0; int64_t h0_rs;
+  void* ht; int64_t ht_rs;
+  const int32_t* cu_seqlens;
+  const int32_t* idx; int64_t idx_stride;
+  const int32_t* num_accepted;
+  int64_t T;
+  int H, HKV, V;
+  float scale;
+  int l2norm, inplace;
+};
+
+__device__ __forceinline__ float load_scalar(const void* p, int64_t i, int dtype) {
+  if (dtype == HMX_F32) return static_cast<const float*>(p)[i];
+  if (dtype == HMX_BF16) return (float)static_cast<const bf16*>(p)[i];
+  return (float)static_cast<const f16*>(p)[i];
+}
+
+// Sum a value over the 8 row-group lanes (lane bits 3..5) of a wave.
+__device__ __forceinline__ float rowgroup_sum(float x) {
+  x += shfl_xor(x, 8);
+  x += shfl_xor(x, 16);
+  x += shfl_xor(x, 32);
+  return x;
+}
+
+template <int K, typename TQ, typename TS>
+__global__ __launch_bounds__(256) void gdn_recurrent_kernel(RecurrentParams p) {
+  constexpr int R = K / 8;  // rows per lane
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int c = lane & 7, r = lane >> 3;
+  const int n = blockIdx.x / p.H;
+  const int h = blockIdx.x - n * p.H;
+  const int hk = h / (p.H / p.HKV);
+  const int V = p.V;
+  const int col = wave * 32 + c * 4;
+
+  int64_t bos, T;
+  if (p.cu_seqlens) {
+    bos = p.cu_seqlens[n];
+    T = (int64_t)p.cu_seqlens[n + 1] - bos;
+  } else {
+    bos = (int64_t)n * p.T;
+    T = p.T;
+  }
+  if (T <= 0) return;
+
+  // resolve state rows
+  int64_t read_row = -1, write_row;
+  if (p.h0) {
+    if (p.idx) {
+      const int64_t cidx = p.num_accepted ? (int64_t)p.num_accepted[n] - 1 : 0;
+      read_row = p.idx[(int64_t)n * p.idx_stride + cidx];
+      if (read_row < 0) return;
+    } else {
+      read_row = bos;
+    }
+  }
+  if (p.inplace) {
+    write_row = p.idx[(int64_t)n * p.idx_stride];
+    if (write_row < 0) return;
+  } else {
+    write_row = n;
+  }
+
+  float S[R][4];
+  if (read_row >= 0) {
+    const TS* src = static_cast<const TS*>(p.h0) + read_row * p.h0_rs + (int64_t)h * K * V +
+                    (int64_t)(r * R) * V + col;
+#pragma unroll
+    for (int i = 0; i < R; ++i) load_vec<4>(src + (int64_t)i * V, S[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < R; ++i) S[i][0] = S[i][1] = S[i][2] = S[i][3] = 0.f;
+  }
+
+  for (int64_t t = 0; t < T; ++t) {
+    const int64_t tok = bos + t;
+    float kr[R], qr[R], vv[4], bb[4];
+    load_vec<R>(static_cast<const TQ*>(p.k) + (tok * p.HKV + hk) * K + r * R, kr);
+    load_vec<R>(static_cast<const TQ*>(p.q) + (tok * p.H + h) * K + r * R, qr);
+    load_vec<4>(static_cast<const TQ*>(p.v) + (tok * p.HKV + hk) * V + col, vv);
+    const float gt = load_scalar(p.g, tok * p.H + h, p.g_dt);
+    if (p.beta_headwise) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        bb[j] = load_scalar(p.beta, (tok * p.H + h) * V + col + j, p.beta_dt);
+    } else {
+      const float bs = load_scalar(p.beta, tok * p.H + h, p.beta_dt);
+      bb[0] = bb[1] = bb[2] = bb[3] = bs;
+    }
+
+    float qs = p.scale;
+    if (p.l2norm) {
+      float sk = 0.f, sq = 0.f;
+#pragma unroll
+      for (int i = 0; i < R; ++i) { sk += kr[i] * kr[i]; sq += qr[i] * qr[i]; }
+      sk = rowgroup_sum(sk);
+      sq = rowgroup_sum(sq);
+      const float ik = 1.0f / sqrtf(sk + 1e-6f);
+#pragma unroll
+      for (int i = 0; i < R; ++i) kr[i] *= ik;
+      qs *= 1.0f / sqrtf(sq + 1e-6f);
+    }
+#pragma unroll
+    for (int i = 0; i < R; ++i) qr[i] *= qs;
+
+    const float eg = expf(gt);
+    float kv[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        S[i][j] *= eg;
+        kv[j] += S[i][j] * kr[i];
+      }
+    }
+    float u[4], ov[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) u[j] = (vv[j] - rowgroup_sum(kv[j])) * bb[j];
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        S[i][j] += kr[i] * u[j];
+        ov[j] += S[i][j] * qr[i];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ov[j] = rowgroup_sum(ov[j]);
+    if (r == 0) store_vec<4>(static_cast<TQ*>(p.o) + (tok * p.H + h) * V + col, ov);
+  }
+
+  TS* dst = static_cast<TS*>(p.ht) + write_row * p.ht_rs + (int64_t)h * K * V +
+            (int64_t)(r * R) * V + col;
+#pragma unroll
+  for (int i = 0; i < R; ++i) store_vec<4>(dst + (int64_t)i * V, S[i]);
+}
+
+template <int K, typename TQ, typename TS>
+static void launch(const RecurrentParams& p, int64_t N, hipStream_t s) {
+  hipLaunchKernelGGL((gdn_recurrent_kernel<K, TQ, TS>), dim3((unsigned)(N * p.H)),
+                     dim3(64 * (p.V / 32)), 0, s, p);
+}
+
+template <int K, typename TQ>
+static int dispatch_state(const RecurrentParams& p, int64_t N, int state_dt, hipStream_t s) {
+  if (state_dt == HMX_F32) launch<K, TQ, float>(p, N, s);
+  else if (state_dt == HMX_BF16) launch<K, TQ, bf16>(p, N, s);
+  else return set_error(HMX_EUNSUPPORTED, "hmx_gdn_recurrent_fwd: state dtype %d", state_dt);
+  return HMX_OK;
+}
+
+template <int K>
+static int dispatch_qkv(const RecurrentParams& p, int64_t N, int qkv_dt, int state_dt,
+                        hipStream_t s) {
+  if (qkv_dt == HMX_BF16) return dispatch_state<K, bf16>(p, N, state_dt, s);
+  if (qkv_dt == HMX_F16) return dispatch_state<K, f16>(p, N, state_dt, s);
+  if (qkv_dt == HMX_F32) return dispatch_state<K, float>(p, N, state_dt, s);
+  return set_error(HMX_EUNSUPPORTED, "hmx_gdn_recurrent_fwd: qkv dtype %d", qkv_dt);
+}
+
+}  // namespace hmx
+
+extern "C" int hmx_gdn_recurrent_fwd(
+    const void* q, const void* k, const void* v, int32_t qkv_dtype, const void* g,
+    int32_t g_dtype, const void* beta, int32_t beta_dtype, int32_t beta_headwise, void* o,
+    const void* h0, int64_t h0_row_stride, void* ht, int64_t ht_row_stride, int32_t state_dtype,
+    const int32_t* cu_seqlens, const int32_t* ssm_state_indices, int64_t idx_stride,
+    const int32_t* num_accepted_tokens, int64_t B, int64_t T, int64_t N, int32_t H, int32_t HKV,
+    int32_t K, int32_t V, float scale, int32_t use_qk_l2norm, int32_t inplace_final_state,
+    void* stream) {
+  using namespace hmx;
+  HMX_REQUIRE(H > 0 && HKV > 0 && H % HKV == 0, HMX_EINVAL,
+              "hmx_gdn_recurrent_fwd: H=%d must be a positive multiple of HKV=%d", H, HKV);
+  HMX_REQUIRE(K == 64 || K == 128 || K == 256, HMX_EUNSUPPORTED,
+              "hmx_gdn_recurrent_fwd: K=%d not in {64,128,256}", K);
+  HMX_REQUIRE(V > 0 && V % 32 == 0 && V <= 256, HMX_EUNSUPPORTED,
+              "hmx_gdn_recurrent_fwd: V=%d must be a multiple of 32 and <= 256", V);
+  HMX_REQUIRE(q && k && v && g && beta && o && ht, HMX_EINVAL,
+              "hmx_gdn_recurrent_fwd: null tensor pointer");
+  HMX_REQUIRE(!inplace_final_state || ssm_state_indices, HMX_EINVAL,
+              "hmx_gdn_recurrent_fwd: in-place final state needs ssm_state_indices");
+  HMX_REQUIRE(!num_accepted_tokens || ssm_state_indices, HMX_EINVAL,
+              "hmx_gdn_recurrent_fwd: num_accepted_tokens needs ssm_state_indices");
+  HMX_REQUIRE(cu_seqlens || N == B, HMX_EINVAL,
+              "hmx_gdn_recurrent_fwd: N=%lld must equal B=%lld without cu_seqlens",
+              (long long)N, (long long)B);
+  HMX_REQUIRE(g_dtype >= 0 && g_dtype <= 2 && beta_dtype >= 0 && beta_dtype <= 2, HMX_EUNSUPPORTED,
+              "hmx_gdn_recurrent_fwd: g/beta dtype");
+  if (N == 0) return HMX_OK;
+  RecurrentParams p;
+  p.q = q; p.k = k; p.v = v; p.g = g; p.g_dt = g_dtype;
+  p.beta = beta; p.beta_dt = beta_dtype; p.beta_headwise = beta_headwise;
+  p.o = o; p.h0 = h0; p.h0_rs = h0_row_stride; p.ht = ht; p.ht_rs = ht_row_stride;
+  p.cu_seqlens = cu_seqlens; p.idx = ssm_state_indices; p.idx_stride = idx_stride;
+  p.num_accepted = num_accepted_tokens; p.T = T; p.H = H; p.HKV = HKV; p.V = V;
+  p.scale = scale; p.l2norm = use_qk_l2norm; p.inplace = inplace_final_state;
+  hipStream_t s = (hipStream_t)stream;
+  int rc;
+  if (K == 64) rc = dispatch_qkv<64>(p, N, qkv_dtype, state_dtype, s);
+  else if (K == 128) rc = dispatch_qkv<128>(p, N, qkv_dtype, state_dtype, s);
+  else rc = dispatch_qkv<256>(p, N, qkv_dtype, state_dtype, s);
+  if (rc != HMX_OK) return rc;
+  return check_launch("hmx_gdn_recurrent_fwd");
+}

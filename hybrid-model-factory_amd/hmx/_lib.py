@@ -1,0 +1,101 @@
+"""ctypes binding of libhmx.so (the C ABI declared in include/hmx.h).
+
+The library is loaded lazily on first use.  There is no CPU fallback: calling
+an op without the built library, or with tensors that are not on a GPU,
+raises.  Status codes from the C side map to the Python exception types the
+reference ops raise (ValueError / NotImplementedError / RuntimeError).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libhmx.so"
+
+HMX_OK, HMX_EINVAL, HMX_EUNSUPPORTED, HMX_EHIP = 0, 1, 2, 3
+HMX_F32, HMX_BF16, HMX_F16 = 0, 1, 2
+
+_DTYPE_CODE = {torch.float32: HMX_F32, torch.bfloat16: HMX_BF16, torch.float16: HMX_F16}
+
+_P = ctypes.c_void_p
+_I32 = ctypes.c_int32
+_I64 = ctypes.c_int64
+_F32 = ctypes.c_float
+
+# name -> argtypes (restype is int unless listed in _RESTYPES)
+SIGNATURES: dict[str, list] = {
+    "hmx_abi_version": [],
+    "hmx_last_error": [],
+    "hmx_gdn_gating": [_P, _I32, _P, _I64, _I64, _P, _I64, _I64, _I32, _P, _I32, _P, _P, _I32,
+                       _I64, _I32, _F32, _F32, _P],
+    "hmx_gdn_recurrent_fwd": [_P, _P, _P, _I32, _P, _I32, _P, _I32, _I32, _P,
+                              _P, _I64, _P, _I64, _I32,
+                              _P, _P, _I64, _P,
+                              _I64, _I64, _I64, _I32, _I32, _I32, _I32,
+                              _F32, _I32, _I32, _P],
+}
+_RESTYPES = {"hmx_last_error": ctypes.c_char_p}
+
+_lib = None
+
+
+class HmxLibraryMissing(RuntimeError):
+    pass
+
+
+def load(path: str | os.PathLike | None = None):
+    """Load (once) and return the ctypes handle with argtypes installed."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path else LIB_PATH
+    if not p.exists():
+        raise HmxLibraryMissing(
+            f"libhmx.so not found at {p}; build it with `python hybrid-model-factory_amd/hmx/build.py`")
+    lib = ctypes.CDLL(str(p))
+    for name, argtypes in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = _RESTYPES.get(name, ctypes.c_int)
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPE_CODE[t.dtype]
+    except KeyError:
+        raise NotImplementedError(f"unsupported dtype {t.dtype}") from None
+
+
+def ptr(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_of(t: torch.Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def require_gpu(*tensors: torch.Tensor | None) -> None:
+    """The product path runs only on the GPU: refuse CPU tensors loudly."""
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError("hmx ops run only on GPU tensors (no CPU fallback); got a "
+                               f"{t.device} tensor")
+
+
+def call(name: str, *args) -> None:
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc == HMX_OK:
+        return
+    msg = (lib.hmx_last_error() or b"").decode(errors="replace")
+    if rc == HMX_EINVAL:
+        raise ValueError(msg)
+    if rc == HMX_EUNSUPPORTED:
+        raise NotImplementedError(msg)
+    raise RuntimeError(msg)

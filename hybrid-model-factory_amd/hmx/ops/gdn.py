@@ -1,0 +1,166 @@
+"""Gated delta rule (GDN) ops — the reference's Python signatures over libhmx.
+
+Entry points (reference paths relative to the reference repository root):
+
+- ``fused_gdn_gating``  — vllm-inference/src/primed_vllm/gdn/ops/fused_gdn_gating.py:79-125
+- ``fused_recurrent_gated_delta_rule_gqa`` — .../gdn/ops/fused_recurrent_gqa.py:227-277
+- ``chunk_gated_delta_rule_gqa`` — .../gdn/ops/chunk_gqa.py:15-83
+- fla-style training names ``chunk_gated_delta_rule`` / ``fused_recurrent_gated_delta_rule``
+  (called at training/src/hmf/model/hybrid_zoo/layers/gated_deltanet/gdn.py:462-489):
+  the GQA entries with HKV == H.
+
+Every op validates on the host with the reference's exception types, allocates
+its outputs through torch's caching allocator, and launches on torch's current
+stream.  There is no CPU fallback.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+
+
+def _i32(t: torch.Tensor | None) -> torch.Tensor | None:
+    if t is None:
+        return None
+    if t.dtype != torch.int32:
+        t = t.to(torch.int32)
+    return t.contiguous()
+
+
+def fused_gdn_gating(A_log: torch.Tensor, a: torch.Tensor, b: torch.Tensor,
+                     dt_bias: torch.Tensor, beta: float = 1.0,
+                     threshold: float = 20.0) -> tuple[torch.Tensor, torch.Tensor]:
+    """g = -exp(A_log) * softplus(a + dt_bias), beta = sigmoid(b).
+
+    a, b: [num_tokens, num_heads], any strides.  Returns (g, beta), each
+    [1, num_tokens, num_heads] in ``a.dtype`` (fused_gdn_gating.py:79-125).
+    """
+    _lib.require_gpu(A_log, a, b, dt_bias)
+    num_tokens, num_heads = a.shape
+    if b.shape != a.shape:
+        raise ValueError(f"a {tuple(a.shape)} and b {tuple(b.shape)} must match")
+    g = torch.empty(num_tokens, num_heads, dtype=a.dtype, device=a.device)
+    beta_out = torch.empty(num_tokens, num_heads, dtype=a.dtype, device=a.device)
+    _lib.call("hmx_gdn_gating",
+              _lib.ptr(A_log), _lib.dtype_code(A_log),
+              _lib.ptr(a), a.stride(0), a.stride(1),
+              _lib.ptr(b), b.stride(0), b.stride(1), _lib.dtype_code(a),
+              _lib.ptr(dt_bias), _lib.dtype_code(dt_bias),
+              _lib.ptr(g), _lib.ptr(beta_out), _lib.dtype_code(g),
+              num_tokens, num_heads, float(beta), float(threshold), _lib.stream_of(a))
+    return g.unsqueeze(0), beta_out.unsqueeze(0)
+
+
+def fused_recurrent_gated_delta_rule_gqa(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    g: torch.Tensor,
+    beta: torch.Tensor | None = None,
+    scale: float | None = None,
+    initial_state: torch.Tensor | None = None,
+    inplace_final_state: bool = True,
+    cu_seqlens: torch.Tensor | None = None,
+    ssm_state_indices: torch.Tensor | None = None,
+    num_accepted_tokens: torch.Tensor | None = None,
+    use_qk_l2norm_in_kernel: bool = False,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """GQA-native fused recurrent gated delta rule (decode).
+
+    q [B,T,H,K]; k [B,T,HKV,K]; v [B,T,HKV,V]; g [B,T,H]; beta [B,T,H] or
+    [B,T,H,V].  With ``inplace_final_state`` the state pool ``initial_state``
+    [slots,H,K,V] is updated in place at ``ssm_state_indices`` and returned;
+    otherwise a new [B,T,H,K,V] tensor holds sequence n's final state in flat
+    row n.  Returns (o [B,T,H,V], final_state)  (fused_recurrent_gqa.py:227-277).
+    """
+    if cu_seqlens is not None and q.shape[0] != 1:
+        raise ValueError(f"Batch size expected to be 1 with cu_seqlens, got {q.shape[0]}")
+    if scale is None:
+        scale = k.shape[-1] ** -0.5
+    if beta is None:
+        beta = torch.ones_like(g)
+    _lib.require_gpu(q, k, v, g, beta, initial_state, cu_seqlens, ssm_state_indices,
+                     num_accepted_tokens)
+    q, k, v, g, beta = (x.contiguous() for x in (q, k, v, g, beta))
+    if not (q.dtype == k.dtype == v.dtype):
+        raise AssertionError("q, k, v must share a dtype")
+    B, T, H, K = q.shape
+    HKV, V = k.shape[2], v.shape[-1]
+    if k.shape != (B, T, HKV, K) or v.shape[:3] != (B, T, HKV) or H % HKV != 0:
+        raise ValueError(f"bad GQA shapes q{tuple(q.shape)} k{tuple(k.shape)} v{tuple(v.shape)}")
+    N = B if cu_seqlens is None else len(cu_seqlens) - 1
+    beta_headwise = beta.dim() == q.dim()
+    if inplace_final_state:
+        if initial_state is None or ssm_state_indices is None:
+            raise ValueError("inplace_final_state=True needs initial_state (the state pool) "
+                             "and ssm_state_indices")
+        final_state = initial_state
+    else:
+        sdt = torch.float32 if initial_state is None else initial_state.dtype
+        final_state = q.new_empty(B, T, H, K, V, dtype=sdt)
+    if initial_state is not None:
+        if tuple(initial_state.shape[1:]) != (H, K, V) or not initial_state[0].is_contiguous():
+            raise ValueError(f"initial_state must be [rows,{H},{K},{V}] with contiguous rows, "
+                             f"got {tuple(initial_state.shape)}")
+        if initial_state.dtype != final_state.dtype:
+            raise AssertionError("state dtypes differ")
+    idx = _i32(ssm_state_indices)
+    idx_stride = 0 if idx is None else idx.stride(0)
+    o = q.new_empty(B, T, H, V)
+    state_dt = _lib.dtype_code(final_state)
+    _lib.call("hmx_gdn_recurrent_fwd",
+              _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.dtype_code(q),
+              _lib.ptr(g), _lib.dtype_code(g),
+              _lib.ptr(beta), _lib.dtype_code(beta), int(beta_headwise),
+              _lib.ptr(o),
+              _lib.ptr(initial_state), 0 if initial_state is None else initial_state.stride(0),
+              _lib.ptr(final_state), final_state.stride(0) if inplace_final_state else H * K * V,
+              state_dt,
+              _lib.ptr(_i32(cu_seqlens)), _lib.ptr(idx), idx_stride,
+              _lib.ptr(_i32(num_accepted_tokens)),
+              B, T, N, H, HKV, K, V, float(scale), int(bool(use_qk_l2norm_in_kernel)),
+              int(bool(inplace_final_state)), _lib.stream_of(q))
+    return o, final_state
+
+
+def fused_recurrent_gated_delta_rule(q, k, v, g, beta=None, scale=None, initial_state=None,
+                                     output_final_state=False, cu_seqlens=None,
+                                     use_qk_l2norm_in_kernel=False):
+    """fla-style decode entry (training/src/hmf/.../gated_deltanet/gdn.py:478-489).
+
+    k, v already carry H heads.  ``initial_state`` [N,H,K,V] is read, never
+    written; returns (o, final_state [N,H,K,V] fp32 or None).
+    """
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    N = B if cu_seqlens is None else len(cu_seqlens) - 1
+    if cu_seqlens is not None and B != 1:
+        raise ValueError(f"Batch size expected to be 1 with cu_seqlens, got {B}")
+    if initial_state is None:
+        pool = torch.zeros(N, H, K, V, dtype=torch.float32, device=q.device)
+    else:
+        pool = initial_state.to(torch.float32).clone()
+    idx = torch.arange(N, dtype=torch.int32, device=q.device)
+    if cu_seqlens is None:
+        cu_seqlens = torch.arange(0, (B + 1) * T, T, dtype=torch.int32, device=q.device)[:B + 1]
+        qf, kf, vf = (x.reshape(1, B * T, *x.shape[2:]) for x in (q, k, v))
+        gf = g.reshape(1, B * T, H)
+        bf = None if beta is None else beta.reshape(1, B * T, *beta.shape[2:])
+    else:
+        qf, kf, vf, gf, bf = q, k, v, g, beta
+    o, _ = fused_recurrent_gated_delta_rule_gqa(
+        qf, kf, vf, gf, bf, scale, pool, True, cu_seqlens, idx, None, use_qk_l2norm_in_kernel)
+    return o.reshape(B, T, H, V), (pool if output_final_state else None)
+
+
+def chunk_gated_delta_rule_gqa(q, k, v, g, beta, scale=None, initial_state=None,
+                               output_final_state=False, cu_seqlens=None,
+                               use_qk_l2norm_in_kernel=False):
+    raise NotImplementedError("chunked prefill kernel not built yet")
+
+
+def chunk_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None,
+                           output_final_state=False, cu_seqlens=None,
+                           use_qk_l2norm_in_kernel=False):
+    raise NotImplementedError("chunked prefill kernel not built yet")

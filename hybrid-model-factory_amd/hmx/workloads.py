@@ -1,0 +1,110 @@
+"""Seeded synthetic inputs for the benchmark configurations (C0-C4).
+
+Each config draws from ``torch.Generator().manual_seed(20260000 + config_id)`` on
+the CPU, in the order the tensors are listed, in fp32 and casts last, so the
+CPU checker and the GPU see identical bits.  ``device_gen=True`` draws on the
+GPU instead (different bits, same distributions) for large benchmark inputs.
+
+  C0  GDN fwd, B=1 T=2048 H=16 d=128 fp32 (CPU plumbing case)
+  C1  GDN chunked prefill, B=1 T=32768 H=32 d=128 bf16 (+ HKV=8, + varlen 8 seqs)
+  C2  GDN decode, 256 seqs x 1 token, H=32 d=128, fp32 pool N(0,0.02^2), randperm slots
+  C3  GKA prefill, C1 shape
+  C4  Mamba2 SSD, B=2 T=16384 H=64 P=64 N=128 G=8 chunk 256
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn.functional as F
+
+SEED_BASE = 20260000
+
+
+def gen(config_id: int, device: str | torch.device = "cpu") -> torch.Generator:
+    g = torch.Generator(device=device)
+    g.manual_seed(SEED_BASE + config_id)
+    return g
+
+
+def _randn(gen_, shape, device):
+    return torch.randn(*shape, generator=gen_, device=device, dtype=torch.float32)
+
+
+def _l2n(x):
+    return x / x.norm(dim=-1, keepdim=True)
+
+
+def gdn_inputs(T: int, H: int, HKV: int, D: int, dtype=torch.bfloat16, config_id: int = 1,
+               B: int = 1, device="cpu", gen_device="cpu"):
+    """q,k ~ N(0,1) L2-normalised per head; v ~ N(0,1); beta = sigmoid(N(0,1));
+    g = logsigmoid(N(0,1)).  Returns dict of tensors on ``device``."""
+    gd = gen(config_id, gen_device)
+    q = _l2n(_randn(gd, (B, T, H, D), gen_device))
+    k = _l2n(_randn(gd, (B, T, HKV, D), gen_device))
+    v = _randn(gd, (B, T, HKV, D), gen_device)
+    beta = torch.sigmoid(_randn(gd, (B, T, H), gen_device))
+    g = F.logsigmoid(_randn(gd, (B, T, H), gen_device))
+    out = dict(q=q.to(dtype), k=k.to(dtype), v=v.to(dtype), g=g, beta=beta)
+    return {n: t.to(device) for n, t in out.items()}
+
+
+def varlen_lengths(n_seqs: int = 8, lo: int = 1024, hi: int = 8192, config_id: int = 1):
+    """Sequence lengths ~ randint(lo, hi+1) from the config generator (drawn first)."""
+    gd = gen(config_id)
+    return torch.randint(lo, hi + 1, (n_seqs,), generator=gd)
+
+
+def cu_from_lengths(lengths: torch.Tensor) -> torch.Tensor:
+    return torch.cat([torch.zeros(1, dtype=torch.int64), lengths.cumsum(0)]).to(torch.int32)
+
+
+def decode_inputs(n_seqs: int = 256, H: int = 32, HKV: int = 32, D: int = 128, steps: int = 1,
+                  slots: int | None = None, dtype=torch.bfloat16, config_id: int = 2,
+                  device="cpu", gen_device="cpu"):
+    """C2: pool fp32 [slots,H,D,D] ~ N(0, 0.02^2); indices = randperm(slots)[:n_seqs];
+    per step q,k,v [1,n_seqs,*,D], g, beta [1,n_seqs,H] stacked over ``steps``."""
+    slots = slots or n_seqs
+    gd = gen(config_id, gen_device)
+    pool = _randn(gd, (slots, H, D, D), gen_device) * 0.02
+    idx = torch.randperm(slots, generator=gd, device=gen_device)[:n_seqs].to(torch.int32)
+    q = _l2n(_randn(gd, (steps, 1, n_seqs, H, D), gen_device)).to(dtype)
+    k = _l2n(_randn(gd, (steps, 1, n_seqs, HKV, D), gen_device)).to(dtype)
+    v = _randn(gd, (steps, 1, n_seqs, HKV, D), gen_device).to(dtype)
+    beta = torch.sigmoid(_randn(gd, (steps, 1, n_seqs, H), gen_device))
+    g = F.logsigmoid(_randn(gd, (steps, 1, n_seqs, H), gen_device))
+    cu = torch.arange(n_seqs + 1, dtype=torch.int32, device=gen_device)
+    out = dict(pool=pool, idx=idx, q=q, k=k, v=v, g=g, beta=beta, cu_seqlens=cu)
+    return {n: t.to(device) for n, t in out.items()}
+
+
+# ---------------------------------------------------------------------------
+# algorithmic work per unit (used for roofline.achieved)
+# ---------------------------------------------------------------------------
+def gdn_prefill_flops(T: int, H: int, K: int = 128, V: int = 128, C: int = 64) -> float:
+    """2*T*H*(5*C*d + 3*d^2) for d = K = V (KK^T, QK^T, T.(bK), T.(bV), P.Vnew: C x C x d;
+    W.h, Q.h, K^T.Vnew: C x d x d); the (I+A)^-1 term is excluded."""
+    d = K
+    return 2.0 * T * H * (5 * C * d + 3 * d * d)
+
+
+def gdn_prefill_bytes(T: int, H: int, HKV: int, K: int = 128, V: int = 128, n_seqs: int = 1,
+                      in_bytes: int = 2) -> float:
+    """q,o [T,H,d] + k,v [T,HKV,d] in bf16, g,beta fp32 [T,H], final state fp32."""
+    return (T * H * (K + V) * in_bytes + T * HKV * (K + V) * in_bytes + 2 * T * H * 4
+            + n_seqs * H * K * V * 4)
+
+
+def gdn_decode_bytes(n_seqs: int, H: int, HKV: int, K: int = 128, V: int = 128,
+                     state_bytes: int = 4, in_bytes: int = 2) -> float:
+    """State read + write per (seq, head) plus q,o [n,H,d] and k,v [n,HKV,d] and g,beta."""
+    return (2 * n_seqs * H * K * V * state_bytes + n_seqs * H * (K + V) * in_bytes
+            + n_seqs * HKV * (K + V) * in_bytes + 2 * n_seqs * H * 4)
+
+
+def ceil_div(a: int, b: int) -> int:
+    return -(-a // b)
+
+
+__all__ = ["gen", "gdn_inputs", "varlen_lengths", "cu_from_lengths", "decode_inputs",
+           "gdn_prefill_flops", "gdn_prefill_bytes", "gdn_decode_bytes", "ceil_div", "math"]

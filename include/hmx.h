@@ -1,0 +1,96 @@
+/*
+ * hmx.h — C ABI of libhmx.so, the MI355X (gfx950) linear-recurrent mixer kernels.
+ *
+ * Conventions shared by every entry point
+ *  - All pointers are device pointers unless stated otherwise; sizes and
+ *    strides are in ELEMENTS of the tensor they describe.
+ *  - Optional tensors are passed as NULL.
+ *  - `stream` is a hipStream_t (NULL = default stream).  Work is enqueued only:
+ *    the library never allocates, frees or synchronises, and keeps no global
+ *    mutable state, so calls are re-entrant and graph-capturable.
+ *  - Return value: HMX_OK, or an HMX_E* code with a message available from
+ *    hmx_last_error() (thread-local).
+ *  - Dtype codes: HMX_F32, HMX_BF16, HMX_F16; index tensors are int32.
+ *
+ * The reference has no native code: each entry point replaces one Python op
+ * (and the Triton kernels under it) of awslabs/hybrid-model-factory, cited
+ * below as path:line relative to the reference repository root.
+ */
+#ifndef HMX_H_
+#define HMX_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HMX_ABI_VERSION 1
+
+enum hmx_status {
+  HMX_OK = 0,
+  HMX_EINVAL = 1,       /* bad argument: maps to ValueError on the Python side */
+  HMX_EUNSUPPORTED = 2, /* unsupported shape/dtype: maps to NotImplementedError */
+  HMX_EHIP = 3          /* HIP launch/runtime error: maps to RuntimeError */
+};
+
+enum hmx_dtype { HMX_F32 = 0, HMX_BF16 = 1, HMX_F16 = 2 };
+
+int hmx_abi_version(void);
+const char* hmx_last_error(void);
+
+/*
+ * GDN gating: g = -exp(A_log) * softplus(a + dt_bias), beta_out = sigmoid(b).
+ * softplus(x) = log(1 + exp(sp_beta*x)) / sp_beta, or x when sp_beta*x > threshold.
+ * a, b: [num_tokens, num_heads] with arbitrary strides (the split of a fused
+ * projection); A_log, dt_bias: [num_heads]; g, beta_out: contiguous
+ * [num_tokens, num_heads] in out_dtype.
+ * Replaces: fused_gdn_gating
+ *   vllm-inference/src/primed_vllm/gdn/ops/fused_gdn_gating.py:79-125 (kernel :10-76).
+ */
+int hmx_gdn_gating(const void* A_log, int32_t A_log_dtype,
+                   const void* a, int64_t a_stride0, int64_t a_stride1,
+                   const void* b, int64_t b_stride0, int64_t b_stride1,
+                   int32_t ab_dtype,
+                   const void* dt_bias, int32_t dt_bias_dtype,
+                   void* g, void* beta_out, int32_t out_dtype,
+                   int64_t num_tokens, int32_t num_heads,
+                   float sp_beta, float threshold, void* stream);
+
+/*
+ * GDN fused recurrent (decode) forward, GQA-native, slot-indexed state pool.
+ *  q [B*T, H, K]; k [B*T, HKV, K]; v [B*T, HKV, V] (qkv_dtype, contiguous)
+ *  g [B*T, H] (g_dtype); beta [B*T, H] or [B*T, H, V] when beta_headwise
+ *  o [B*T, H, V] (qkv_dtype)
+ *  h0, ht: state tensors of state_dtype, rows of [H, K, V] with row strides
+ *    h0_row_stride / ht_row_stride (elements).  h0 may be NULL (zero state).
+ *  Sequences: cu_seqlens [N+1] (varlen, B == 1) or N = B sequences of T tokens.
+ *  Initial state of sequence n: row ssm_state_indices[n*idx_stride + c] with
+ *    c = num_accepted_tokens[n]-1 (or 0), or row bos_n without indices.
+ *  Final state: row ssm_state_indices[n*idx_stride] when inplace, else row n.
+ *  Zero-length sequences and negative slot indices are skipped.
+ *  Supported: K in {64,128,256}; V a multiple of 32, <= 256.
+ * Replaces: fused_recurrent_gated_delta_rule_gqa
+ *   vllm-inference/src/primed_vllm/gdn/ops/fused_recurrent_gqa.py:227-277
+ *   (wrapper :157-224, kernel :25-154).
+ */
+int hmx_gdn_recurrent_fwd(const void* q, const void* k, const void* v, int32_t qkv_dtype,
+                          const void* g, int32_t g_dtype,
+                          const void* beta, int32_t beta_dtype, int32_t beta_headwise,
+                          void* o,
+                          const void* h0, int64_t h0_row_stride,
+                          void* ht, int64_t ht_row_stride, int32_t state_dtype,
+                          const int32_t* cu_seqlens,
+                          const int32_t* ssm_state_indices, int64_t idx_stride,
+                          const int32_t* num_accepted_tokens,
+                          int64_t B, int64_t T, int64_t N,
+                          int32_t H, int32_t HKV, int32_t K, int32_t V,
+                          float scale, int32_t use_qk_l2norm, int32_t inplace_final_state,
+                          void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HMX_H_ */

@@ -1,0 +1,64 @@
+"""CPU checks of the C ABI boundary: the library loads, exports every entry
+point include/*.h declares, and the host wrappers raise the reference's
+exception types before any launch (no GPU needed)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+import hmx
+from hmx import _lib
+
+REPO = Path(__file__).resolve().parent.parent
+
+
+def _declared_symbols():
+    names = set()
+    for h in (REPO / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names |= set(re.findall(r"\b(hmx_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(_lib.LIB_PATH))
+    declared = _declared_symbols()
+    assert declared, "no declarations found"
+    missing = [n for n in declared if not hasattr(lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+    # and the Python binding knows every declared symbol's signature
+    assert set(declared) <= set(_lib.SIGNATURES), set(declared) - set(_lib.SIGNATURES)
+
+
+def test_abi_version_and_error_string():
+    lib = _lib.load()
+    assert lib.hmx_abi_version() == 1
+    assert isinstance(lib.hmx_last_error(), bytes)
+
+
+def test_invalid_args_map_to_status_codes():
+    """A bad shape is rejected by the C side before any launch (no GPU touched)."""
+    lib = _lib.load()
+    rc = lib.hmx_gdn_recurrent_fwd(None, None, None, 1, None, 0, None, 0, 0, None, None, 0, None, 0,
+                                   0, None, None, 0, None, 1, 1, 1, 4, 4, 96, 128, 1.0, 1, 0, None)
+    assert rc == _lib.HMX_EUNSUPPORTED
+    assert b"K=96" in lib.hmx_last_error()
+    with pytest.raises(NotImplementedError):
+        _lib.call("hmx_gdn_recurrent_fwd", None, None, None, 1, None, 0, None, 0, 0, None, None, 0,
+                  None, 0, 0, None, None, 0, None, 1, 1, 1, 4, 4, 96, 128, 1.0, 1, 0, None)
+    with pytest.raises(ValueError):
+        _lib.call("hmx_gdn_gating", None, 0, None, 0, 0, None, 0, 0, 1, None, 0, None, None, 1,
+                  -1, 4, 1.0, 20.0, None)
+
+
+def test_wrappers_raise_reference_errors_on_cpu():
+    q = torch.zeros(2, 3, 4, 128, dtype=torch.bfloat16)
+    g = torch.zeros(2, 3, 4)
+    cu = torch.tensor([0, 3, 6])
+    with pytest.raises(ValueError, match="Batch size expected to be 1"):
+        hmx.fused_recurrent_gated_delta_rule_gqa(q, q, q, g, g, cu_seqlens=cu)
+    with pytest.raises(RuntimeError, match="GPU"):
+        hmx.fused_recurrent_gated_delta_rule_gqa(q, q, q, g, g, initial_state=None,
+                                                 inplace_final_state=False)
