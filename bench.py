@@ -1,0 +1,174 @@
+"""Benchmark of the linear-recurrent mixer hot path on one MI355X.
+
+Headline (``value``): GDN chunked prefill at BASELINE config C1 — B=1, T=32768,
+H=32, d=128, chunk 64, bf16 q/k/v, fp32 g/beta, zero initial state, fp32 final
+state — in tokens/s; one "step" is one call of chunk_gated_delta_rule_gqa over
+the whole sequence with inputs resident in HBM.  Also reported: GDN decode at
+C2 (256 sequences x 1 token, H=32, fp32 state pool of 512 MiB through a random
+slot permutation, 512 consecutive steps) in steps/s, each with its roofline,
+and the CPU oracle timed on a bounded sample of the same workloads.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only prefill|decode]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+for _p in (REPO, REPO / "hybrid-model-factory_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+
+
+def _timed(fn, steps, warmup, stream=None):
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps  # ms per step
+
+
+def bench_prefill(dev, steps, warmup, HKV=32):
+    import torch
+    import hmx
+    from hmx import workloads as wl
+    T, H, D = 32768, 32, 128
+    d = wl.gdn_inputs(T=T, H=H, HKV=HKV, D=D, config_id=1, device=dev, gen_device=dev)
+    args = [d[n] for n in ("q", "k", "v", "g", "beta")]
+
+    def step():
+        hmx.chunk_gated_delta_rule_gqa(*args, output_final_state=True,
+                                       use_qk_l2norm_in_kernel=True)
+
+    ms = _timed(step, steps, warmup)
+    by = wl.gdn_prefill_bytes(T, H, HKV)
+    fl = wl.gdn_prefill_flops(T, H)
+    gbs = by / (ms * 1e-3) / 1e9
+    tfs = fl / (ms * 1e-3) / 1e12
+    return dict(ms=ms, tokens_per_s=T / (ms * 1e-3), bytes=by, flops=fl, GBps=gbs, TFLOPs=tfs)
+
+
+def bench_decode(dev, steps_total=512, warmup=8):
+    import torch
+    import hmx
+    from hmx import workloads as wl
+    N, H, D = 256, 32, 128
+    d = wl.decode_inputs(n_seqs=N, H=H, HKV=H, D=D, steps=steps_total, device=dev, gen_device=dev)
+    pool, idx, cu = d["pool"], d["idx"], d["cu_seqlens"]
+    it = {"s": 0}
+
+    def step():
+        s = it["s"] % steps_total
+        it["s"] += 1
+        hmx.fused_recurrent_gated_delta_rule_gqa(
+            d["q"][s], d["k"][s], d["v"][s], d["g"][s], d["beta"][s], initial_state=pool,
+            inplace_final_state=True, cu_seqlens=cu, ssm_state_indices=idx,
+            use_qk_l2norm_in_kernel=True)
+
+    ms = _timed(step, steps_total, warmup)
+    by = wl.gdn_decode_bytes(N, H, H)
+    gbs = by / (ms * 1e-3) / 1e9
+    return dict(ms=ms, steps_per_s=1e3 / ms, tokens_per_s=N * 1e3 / ms, bytes=by, GBps=gbs)
+
+
+def cpu_baseline(sample_tokens=4096):
+    """The oracle's chunked fp32 restatement on the host (a bounded sample of C1)."""
+    import torch
+    from hmx import workloads as wl
+    from oracle import gdn as ref
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    d = wl.gdn_inputs(T=sample_tokens, H=32, HKV=32, D=128, config_id=1)
+    args = [d[n] for n in ("q", "k", "v", "g", "beta")]
+    ref.chunk_gated_delta_rule_gqa(*[a[:, :256] for a in args], output_final_state=True,
+                                   use_qk_l2norm_in_kernel=True, dtype=torch.float32)
+    t0 = time.perf_counter()
+    ref.chunk_gated_delta_rule_gqa(*args, output_final_state=True, use_qk_l2norm_in_kernel=True,
+                                   dtype=torch.float32)
+    dt = time.perf_counter() - t0
+    return dict(value=sample_tokens / dt, unit="tokens/s", cores=torch.get_num_threads(),
+                kind="port", sample=f"C1 first {sample_tokens} tokens x 32 heads, oracle "
+                f"chunked form in fp32 torch on CPU, {dt:.2f} s")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", choices=["prefill", "decode"], default=None)
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the mixer ops shard by head/sequence with no "
+              "communication inside the op, so multi-GPU runs are not part of this build.",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    dev = torch.device("cuda:0")
+    out = {}
+    if a.only in (None, "prefill"):
+        pf = bench_prefill(dev, a.steps, a.warmup)
+        out["prefill"] = pf
+    if a.only in (None, "decode"):
+        out["decode"] = bench_decode(dev)
+    line = {
+        "metric": "mixer prefill tokens/sec + decode steps/sec at 8B shape; % of roofline (1 GPU)",
+        "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+    }
+    if "prefill" in out:
+        pf = out["prefill"]
+        line.update({
+            "value": round(pf["tokens_per_s"], 1), "unit": "tokens/s",
+            "ms_per_step": round(pf["ms"], 4),
+            "config": {"workload": "C1 GDN chunked prefill (chunk_gated_delta_rule_gqa)",
+                       "B": 1, "T": 32768, "H": 32, "HKV": 32, "d": 128, "chunk": 64,
+                       "qkv_dtype": "bf16", "state_dtype": "fp32"},
+            "roofline": {"bound": "hbm", "achieved": round(pf["GBps"], 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(pf["GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
+                         "kernel": "all launches of one prefill op call",
+                         "algorithmic_bytes": pf["bytes"],
+                         "mfma_TFLOPs": round(pf["TFLOPs"], 1),
+                         "mfma_frac": round(pf["TFLOPs"] / BF16_PEAK_TFLOPS, 4)},
+        })
+    if "decode" in out:
+        dc = out["decode"]
+        line["decode"] = {
+            "value": round(dc["steps_per_s"], 1), "unit": "steps/s",
+            "ms_per_step": round(dc["ms"], 4), "tokens_per_s": round(dc["tokens_per_s"], 1),
+            "config": {"workload": "C2 GDN fused recurrent decode", "seqs": 256, "H": 32,
+                       "d": 128, "steps": 512, "pool": "fp32 [256,32,128,128] randperm slots"},
+            "roofline": {"bound": "hbm", "achieved": round(dc["GBps"], 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(dc["GBps"] / HBM_PEAK_GBS, 4),
+                         "algorithmic_bytes": dc["bytes"]},
+        }
+        if "value" not in line:
+            line.update({"value": line["decode"]["value"], "unit": "steps/s",
+                         "ms_per_step": line["decode"]["ms_per_step"],
+                         "config": line["decode"]["config"],
+                         "roofline": line["decode"]["roofline"]})
+    if not a.no_cpu:
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

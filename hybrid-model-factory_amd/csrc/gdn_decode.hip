@@ -6,8 +6,8 @@
 //   q,k <- q/sqrt(|q|^2+1e-6), k/sqrt(|k|^2+1e-6);  q <- q*scale
 //   S <- exp(g) S;  u <- beta (v - S^T k);  S <- S + k u^T;  o <- S^T q
 //
-// Layout & mapping.  One workgroup per (sequence, head) with V/32 waves; wave w
-// owns the state columns [32w, 32w+32) for all K rows, kept in registers for
+// Layout & mapping.  One workgroup per (sequence, head, 128 state columns) with
+// up to 4 waves; wave w owns 32 state columns for all K rows, kept in registers for
 // the whole token loop.  Lane l owns 4 consecutive columns (c = l&7) of
 // R = K/8 consecutive rows (r = l>>3).  One load instruction of the wave
 // touches 8 rows x 128 contiguous bytes, so the four waves of a workgroup
@@ -61,7 +61,8 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(RecurrentParams p) {
   const int h = blockIdx.x - n * p.H;
   const int hk = h / (p.H / p.HKV);
   const int V = p.V;
-  const int col = wave * 32 + c * 4;
+  if ((int)(blockIdx.y * 4 + wave) * 32 >= p.V) return;  // tail workgroup of a V not a multiple of 128
+  const int col = (blockIdx.y * 4 + wave) * 32 + c * 4;
 
   int64_t bos, T;
   if (p.cu_seqlens) {
@@ -167,8 +168,11 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(RecurrentParams p) {
 
 template <int K, typename TQ, typename TS>
 static void launch(const RecurrentParams& p, int64_t N, hipStream_t s) {
-  hipLaunchKernelGGL((gdn_recurrent_kernel<K, TQ, TS>), dim3((unsigned)(N * p.H)),
-                     dim3(64 * (p.V / 32)), 0, s, p);
+  // at most 4 waves (128 state columns) per workgroup; wider V spans grid.y
+  const int waves = p.V / 32;
+  hipLaunchKernelGGL((gdn_recurrent_kernel<K, TQ, TS>),
+                     dim3((unsigned)(N * p.H), (unsigned)((waves + 3) / 4)),
+                     dim3(64 * (waves < 4 ? waves : 4)), 0, s, p);
 }
 
 template <int K, typename TQ>

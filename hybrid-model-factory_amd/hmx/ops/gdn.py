@@ -154,13 +154,115 @@ def fused_recurrent_gated_delta_rule(q, k, v, g, beta=None, scale=None, initial_
     return o.reshape(B, T, H, V), (pool if output_final_state else None)
 
 
-def chunk_gated_delta_rule_gqa(q, k, v, g, beta, scale=None, initial_state=None,
-                               output_final_state=False, cu_seqlens=None,
-                               use_qk_l2norm_in_kernel=False):
-    raise NotImplementedError("chunked prefill kernel not built yet")
+# Segmented chunk-scan planning (host side).  A segment is a run of 64-token
+# chunks of one sequence that one workgroup walks serially; more segments give
+# more parallelism at the cost of a short warm-up (or the exact scan) per
+# segment boundary.
+CHUNK = 64
+MIN_SEGMENT_CHUNKS = 8
+MAX_WARM_CHUNKS = 8
+DECAY_THRESHOLD = 60.0   # warm-up drops history bounded by exp(-60)
+_CU_COUNT: dict[int, int] = {}
+
+
+def _cu_count(device: torch.device) -> int:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if idx not in _CU_COUNT:
+        _CU_COUNT[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
+    return _CU_COUNT[idx]
+
+
+def _segment_table(bounds: list[tuple[int, int]], H: int, workgroups: int,
+                   segment_chunks: int | None = None) -> list[list[int]]:
+    """Rows (n, bos, eos, c_start, c_end, seg_idx, first_seg, nseg) for every sequence."""
+    chunks = [-(-(eos - bos) // CHUNK) for bos, eos in bounds]
+    if segment_chunks is None:
+        total = max(1, sum(chunks))
+        segment_chunks = max(MIN_SEGMENT_CHUNKS, -(-total * H // max(1, workgroups)))
+    rows: list[list[int]] = []
+    for n, ((bos, eos), nc) in enumerate(zip(bounds, chunks)):
+        ns = max(1, -(-nc // segment_chunks))
+        first = len(rows)
+        for i in range(ns):
+            rows.append([n, bos, eos, i * nc // ns, (i + 1) * nc // ns, i, first, ns])
+    return rows
+
+
+def chunk_gated_delta_rule_gqa(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    g: torch.Tensor,
+    beta: torch.Tensor,
+    scale: float | None = None,
+    initial_state: torch.Tensor | None = None,
+    output_final_state: bool = False,
+    cu_seqlens: torch.Tensor | None = None,
+    use_qk_l2norm_in_kernel: bool = False,
+    *,
+    _segment_chunks: int | None = None,
+) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """GQA-native chunked gated delta rule (prefill).
+
+    q [B,T,H,K]; k, v [B,T,HKV,K|V] (bf16; k/v NOT expanded); g, beta [B,T,H];
+    initial_state [N,H,K,V]; cu_seqlens [N+1] with B == 1.  Returns
+    (o [B,T,H,V] in q.dtype, final_state [N,H,K,V] fp32 or None)
+    (chunk_gqa.py:15-83).  ``_segment_chunks`` overrides the parallel
+    decomposition (tests); results do not depend on it beyond fp32 rounding.
+    """
+    assert q.dtype == k.dtype == v.dtype
+    assert q.dtype != torch.float32, "Does not support float32. Use bfloat16."
+    assert len(beta.shape) == 3, "beta must be [B, T, H]"
+    if cu_seqlens is not None and q.shape[0] != 1:
+        raise ValueError(f"Batch size expected to be 1 with cu_seqlens, got {q.shape[0]}")
+    if cu_seqlens is not None and initial_state is not None:
+        if initial_state.shape[0] != len(cu_seqlens) - 1:
+            raise ValueError(f"Initial states count mismatch: {initial_state.shape[0]} vs "
+                             f"{len(cu_seqlens) - 1}")
+    if scale is None:
+        scale = k.shape[-1] ** -0.5
+    _lib.require_gpu(q, k, v, g, beta, initial_state, cu_seqlens)
+    B, T, H, K = q.shape
+    HKV, V = k.shape[2], v.shape[-1]
+    if k.shape != (B, T, HKV, K) or v.shape[:3] != (B, T, HKV) or H % HKV != 0:
+        raise ValueError(f"bad GQA shapes q{tuple(q.shape)} k{tuple(k.shape)} v{tuple(v.shape)}")
+    if g.shape != (B, T, H) or beta.shape != (B, T, H):
+        raise ValueError(f"g {tuple(g.shape)} and beta {tuple(beta.shape)} must be [B,T,H]")
+    if cu_seqlens is None:
+        bounds = [(n * T, n * T + T) for n in range(B)]
+    else:
+        cs = [int(x) for x in cu_seqlens.tolist()]
+        bounds = [(cs[n], cs[n + 1]) for n in range(len(cs) - 1)]
+        if cs[0] != 0 or cs[-1] > T or any(b < a for a, b in bounds):
+            raise ValueError(f"cu_seqlens must be non-decreasing from 0 to <= {T}: {cs}")
+    N = len(bounds)
+    if initial_state is not None and tuple(initial_state.shape) != (N, H, K, V):
+        raise ValueError(f"initial_state must be [{N},{H},{K},{V}], got {tuple(initial_state.shape)}")
+    q, k, v, g, beta = (x.contiguous() for x in (q, k, v, g, beta))
+    h0 = None if initial_state is None else initial_state.to(torch.float32).contiguous()
+    o = torch.empty(B, T, H, V, dtype=q.dtype, device=q.device)
+    if cu_seqlens is not None and bounds and bounds[-1][1] < T:
+        o[:, bounds[-1][1]:].zero_()  # tokens past the last sequence are not computed
+    ht = torch.empty(N, H, K, V, dtype=torch.float32, device=q.device) if output_final_state else None
+    rows = _segment_table(bounds, H, _cu_count(q.device), _segment_chunks)
+    seg = torch.tensor(rows, dtype=torch.int32).to(q.device, non_blocking=True)
+    lib = _lib.load()
+    ws_bytes = int(lib.hmx_gdn_chunk_workspace_bytes(len(rows), N, H))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
+    _lib.call("hmx_gdn_chunk_fwd",
+              _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.dtype_code(q),
+              _lib.ptr(g), _lib.dtype_code(g), _lib.ptr(beta), _lib.dtype_code(beta),
+              _lib.ptr(o), _lib.ptr(h0), _lib.ptr(ht),
+              _lib.ptr(seg), len(rows), N, H, HKV, K, V, float(scale),
+              int(bool(use_qk_l2norm_in_kernel)), MAX_WARM_CHUNKS, DECAY_THRESHOLD,
+              _lib.ptr(ws), ws.numel(), _lib.stream_of(q))
+    return o, ht
 
 
 def chunk_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None,
                            output_final_state=False, cu_seqlens=None,
                            use_qk_l2norm_in_kernel=False):
-    raise NotImplementedError("chunked prefill kernel not built yet")
+    """fla-style prefill entry (training/src/hmf/.../gated_deltanet/gdn.py:462-476):
+    the GQA op with k, v already expanded to H heads."""
+    return chunk_gated_delta_rule_gqa(q, k, v, g, beta, scale, initial_state, output_final_state,
+                                      cu_seqlens, use_qk_l2norm_in_kernel)

@@ -89,6 +89,38 @@ int hmx_gdn_recurrent_fwd(const void* q, const void* k, const void* v, int32_t q
                           float scale, int32_t use_qk_l2norm, int32_t inplace_final_state,
                           void* stream);
 
+
+/*
+ * GDN chunked prefill forward (chunk 64), GQA-native, varlen via a segment table.
+ *  q [T_total, H, 128]; k, v [T_total, HKV, 128] (bf16, contiguous; T_total = B*T)
+ *  g, beta [T_total, H] (f32/bf16/f16); o [T_total, H, 128] (bf16)
+ *  h0 [N, H, 128, 128] fp32 or NULL; ht [N, H, 128, 128] fp32 or NULL
+ *  seg_table: int32 [nseg_total][8] rows (n, bos, eos, c_start, c_end, seg_idx,
+ *    first_seg, nseg) - the chunks [c_start, c_end) of sequence n (tokens
+ *    [bos, eos)) form segment seg_idx of nseg; rows sorted by sequence, every
+ *    sequence (even empty) has >= 1 segment.  Built by the host from cu_seqlens.
+ *  max_warm_chunks / decay_threshold: a segment's start state is recomputed
+ *    from zero over at most max_warm_chunks preceding chunks when the dropped
+ *    history is bounded below exp(-decay_threshold); otherwise the exact
+ *    segment scan runs.
+ *  workspace: device scratch of hmx_gdn_chunk_workspace_bytes(...) bytes.
+ * Replaces: chunk_gated_delta_rule_gqa
+ *   vllm-inference/src/primed_vllm/gdn/ops/chunk_gqa.py:15-83 (and its kernels
+ *   wy_fast_gqa.py:19-112, chunk_delta_h_gqa.py:29-215, chunk_o_gqa.py:30-114).
+ */
+int hmx_gdn_chunk_fwd(const void* q, const void* k, const void* v, int32_t qkv_dtype,
+                      const void* g, int32_t g_dtype, const void* beta, int32_t beta_dtype,
+                      void* o, const float* h0, float* ht,
+                      const int32_t* seg_table, int32_t nseg_total, int32_t N,
+                      int32_t H, int32_t HKV, int32_t K, int32_t V, float scale,
+                      int32_t use_qk_l2norm, int32_t max_warm_chunks, float decay_threshold,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes hmx_gdn_chunk_fwd needs for a given segment table (host-only
+ * arithmetic).  Companion of hmx_gdn_chunk_fwd; no reference counterpart (the
+ * reference allocates its intermediates inside the op, chunk_gqa.py:63-81). */
+size_t hmx_gdn_chunk_workspace_bytes(int32_t nseg_total, int32_t N, int32_t H);
+
 #ifdef __cplusplus
 }
 #endif

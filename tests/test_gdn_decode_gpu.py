@@ -28,7 +28,8 @@ def _mk(n_tok, H, HKV, K, V, dtype, seed):
 
 
 @pytest.mark.parametrize("K,V,H,HKV", [(128, 128, 4, 4), (128, 128, 8, 2), (64, 64, 4, 1),
-                                       (256, 128, 2, 2), (128, 256, 2, 1), (128, 32, 2, 2)])
+                                       (256, 128, 2, 2), (128, 256, 2, 1), (128, 32, 2, 2),
+                                       (128, 160, 2, 2)])
 def test_decode_pool_inplace(dev, K, V, H, HKV):
     N, slots = 7, 12
     q, k, v, g, beta, gen = _mk(N, H, HKV, K, V, torch.bfloat16, 1 + K + V + H)

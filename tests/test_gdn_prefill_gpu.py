@@ -1,0 +1,167 @@
+"""GPU parity: hmx GDN chunked prefill vs the CPU oracle (fp64) and vs the GPU
+recurrent kernel at the full C1 size.
+
+Covers: single segment with h0, ragged tails, GQA, multi-segment warm-up start
+states, the exact segment scan (weak decay, and use_qk_l2norm_in_kernel=False),
+heads mixing both, varlen with empty and 1-token sequences, B > 1 without
+cu_seqlens, bf16 g/beta, and C1 (T=32768, H=32, HKV 32 and 8) plus the
+8-sequence varlen C1 case.
+"""
+import pytest
+import torch
+import torch.nn.functional as F
+
+import hmx
+from hmx import workloads as wl
+from oracle import gdn as ref
+from util import assert_out_close, assert_state_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _mk(B, T, H, HKV, seed, gscale=1.0, gshift=0.0, normalize=True):
+    g0 = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, T, H, 128, generator=g0)
+    k = torch.randn(B, T, HKV, 128, generator=g0)
+    if normalize:
+        q, k = F.normalize(q, dim=-1), F.normalize(k, dim=-1)
+    v = torch.randn(B, T, HKV, 128, generator=g0)
+    g = F.logsigmoid(torch.randn(B, T, H, generator=g0) * gscale + gshift)
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=g0))
+    return q.bfloat16(), k.bfloat16(), v.bfloat16(), g, beta, g0
+
+
+def _run(dev, q, k, v, g, beta, h0=None, cu=None, l2=True, seg=None):
+    args = [x.to(dev) for x in (q, k, v, g, beta)]
+    o, s = hmx.chunk_gated_delta_rule_gqa(
+        *args, initial_state=None if h0 is None else h0.to(dev), output_final_state=True,
+        cu_seqlens=None if cu is None else cu.to(dev), use_qk_l2norm_in_kernel=l2,
+        _segment_chunks=seg)
+    torch.cuda.synchronize()
+    return o, s
+
+
+def _check(dev, q, k, v, g, beta, h0=None, cu=None, l2=True, seg=None):
+    o_ref, s_ref = ref.chunk_gated_delta_rule_gqa(q, k, v, g, beta, initial_state=h0,
+                                                 output_final_state=True, cu_seqlens=cu,
+                                                 use_qk_l2norm_in_kernel=l2)
+    o, s = _run(dev, q, k, v, g, beta, h0, cu, l2, seg)
+    assert o.shape == o_ref.shape and o.dtype == torch.bfloat16
+    assert_out_close(o, o_ref)
+    assert_state_close(s, s_ref)
+    return o, s
+
+
+@pytest.mark.parametrize("T,H,HKV", [(64, 2, 2), (200, 4, 2), (37, 2, 1), (1, 2, 2)])
+def test_prefill_single_segment(dev, T, H, HKV):
+    q, k, v, g, beta, g0 = _mk(1, T, H, HKV, T + H)
+    h0 = torch.randn(1, H, 128, 128, generator=g0) * 0.05
+    _check(dev, q, k, v, g, beta, h0=h0)
+
+
+def test_prefill_no_initial_state(dev):
+    q, k, v, g, beta, _ = _mk(1, 150, 2, 2, 3)
+    _check(dev, q, k, v, g, beta)
+
+
+def test_prefill_multi_segment_warmup(dev):
+    """Typical decay: every later segment starts from a warm-up (zero state)."""
+    q, k, v, g, beta, g0 = _mk(1, 64 * 20 + 17, 4, 2, 4)
+    h0 = torch.randn(1, 4, 128, 128, generator=g0) * 0.05
+    _check(dev, q, k, v, g, beta, h0=h0, seg=3)
+
+
+def test_prefill_multi_segment_exact_scan(dev):
+    """Weak decay (g ~ -1e-3): the warm-up bound is not met -> exact segment scan."""
+    q, k, v, g, beta, g0 = _mk(1, 64 * 9 + 5, 2, 2, 5, gscale=0.1, gshift=7.0)
+    assert g.mean() > -2e-3
+    h0 = torch.randn(1, 2, 128, 128, generator=g0) * 0.05
+    _check(dev, q, k, v, g, beta, h0=h0, seg=2)
+
+
+def test_prefill_mixed_heads(dev):
+    """Head 0 decays strongly (warm-up), head 1 weakly (exact scan) in one call."""
+    q, k, v, g, beta, g0 = _mk(1, 64 * 12, 2, 2, 6)
+    g[..., 1] = F.logsigmoid(torch.randn(1, 64 * 12, generator=g0) * 0.1 + 8.0)
+    _check(dev, q, k, v, g, beta, seg=4)
+
+
+def test_prefill_without_l2norm_uses_exact_scan(dev):
+    q, k, v, g, beta, _ = _mk(1, 64 * 8, 2, 2, 7)
+    _check(dev, q, k, v, g, beta, l2=False, seg=2)
+
+
+def test_prefill_varlen(dev):
+    lens = [130, 0, 64, 500, 1, 77]
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0)), dtype=torch.int32)
+    q, k, v, g, beta, g0 = _mk(1, int(cu[-1]), 4, 1, 8)
+    h0 = torch.randn(len(lens), 4, 128, 128, generator=g0) * 0.05
+    for seg in (None, 2):
+        o, s = _check(dev, q, k, v, g, beta, h0=h0, cu=cu, seg=seg)
+        assert torch.equal(s[1].cpu(), h0[1])  # empty sequence returns its initial state
+
+
+def test_prefill_batched_no_cu(dev):
+    q, k, v, g, beta, g0 = _mk(3, 100, 2, 2, 9)
+    h0 = torch.randn(3, 2, 128, 128, generator=g0) * 0.05
+    _check(dev, q, k, v, g, beta, h0=h0, seg=1)
+
+
+def test_prefill_bf16_gates(dev):
+    q, k, v, g, beta, _ = _mk(1, 96, 2, 2, 10)
+    g, beta = g.bfloat16(), beta.bfloat16()
+    o_ref, s_ref = ref.chunk_gated_delta_rule_gqa(q, k, v, g, beta, output_final_state=True,
+                                                 use_qk_l2norm_in_kernel=True)
+    o, s = _run(dev, q, k, v, g, beta)
+    assert_out_close(o, o_ref)
+    assert_state_close(s, s_ref)
+
+
+def test_prefill_errors(dev):
+    q, k, v, g, beta, _ = _mk(2, 8, 2, 2, 11)
+    d = lambda *xs: [x.to(dev) for x in xs]
+    with pytest.raises(AssertionError):
+        hmx.chunk_gated_delta_rule_gqa(*d(q.float(), k.float(), v.float(), g, beta))
+    with pytest.raises(ValueError, match="Batch size"):
+        hmx.chunk_gated_delta_rule_gqa(*d(q, k, v, g, beta),
+                                       cu_seqlens=torch.tensor([0, 8], device=dev))
+    with pytest.raises(ValueError, match="Initial states count"):
+        hmx.chunk_gated_delta_rule_gqa(*d(q[:1], k[:1], v[:1], g[:1], beta[:1]),
+                                       initial_state=torch.zeros(2, 2, 128, 128, device=dev),
+                                       cu_seqlens=torch.tensor([0, 8], device=dev))
+
+
+@pytest.mark.parametrize("HKV", [32, 8])
+def test_prefill_c1_full_size(dev, HKV):
+    """C1: T=32768, H=32.  All heads vs the GPU recurrent kernel (chunked == recurrent);
+    heads 0-3 vs the fp64 oracle."""
+    T, H = 32768, 32
+    d = wl.gdn_inputs(T=T, H=H, HKV=HKV, D=128, config_id=1)
+    q, k, v, g, beta = (d[n] for n in ("q", "k", "v", "g", "beta"))
+    o, s = _run(dev, q, k, v, g, beta)
+    # recurrent kernel over the same sequence through a 1-slot pool
+    pool = torch.zeros(1, H, 128, 128, device=dev)
+    o_r, _ = hmx.fused_recurrent_gated_delta_rule_gqa(
+        *[x.to(dev) for x in (q, k, v, g, beta)], initial_state=pool, inplace_final_state=True,
+        cu_seqlens=torch.tensor([0, T], dtype=torch.int32, device=dev),
+        ssm_state_indices=torch.zeros(1, dtype=torch.int32, device=dev),
+        use_qk_l2norm_in_kernel=True)
+    torch.cuda.synchronize()
+    assert_out_close(o, o_r.float(), what="chunked vs recurrent o")
+    assert_state_close(s, pool, what="chunked vs recurrent state")
+    # fp64 oracle on the first 4 query heads (they read kv heads 0..4/(H/HKV))
+    hs = 4
+    nkv = max(1, hs // (H // HKV))
+    o_ref, s_ref = ref.chunk_gated_delta_rule_gqa(
+        q[:, :, :hs], k[:, :, :nkv], v[:, :, :nkv], g[:, :, :hs], beta[:, :, :hs],
+        output_final_state=True, use_qk_l2norm_in_kernel=True)
+    assert_out_close(o[:, :, :hs], o_ref)
+    assert_state_close(s[:, :hs], s_ref)
+
+
+def test_prefill_c1_varlen(dev):
+    lens = wl.varlen_lengths()
+    cu = wl.cu_from_lengths(lens)
+    T = int(cu[-1])
+    d = wl.gdn_inputs(T=T, H=8, HKV=8, D=128, config_id=1)
+    _check(dev, *(d[n] for n in ("q", "k", "v", "g", "beta")), cu=cu)
