@@ -3,11 +3,16 @@
 //
 // Semantics: vllm-inference/src/primed_vllm/gdn/ops/chunk_gqa.py:15-83 (the op
 // chain l2norm -> chunk cumsum -> KK^T -> (I+A)^-1 -> w,u -> h,v_new -> o), with
-// per-chunk maths (C = 64 tokens, G = in-chunk cumsum of g):
+// per-chunk maths (C tokens per chunk, G = in-chunk cumsum of g):
 //   A_ij = beta_i (k_i.k_j) e^{G_i-G_j} (j<i);  T = (I+A)^-1
 //   U = T diag(beta) V;   W = T diag(beta e^G) K
 //   V_new = U - W S;      O = scale [e^G (Q S) + tril(Q K^T e^{G_i-G_j}) V_new]
 //   S <- e^{G_last} S + K^T (e^{G_last-G} V_new)
+//
+// The chunk length is an internal choice (the result is the same recurrence at
+// any chunk length, up to fp32 rounding): C = 32 keeps a workgroup's LDS under
+// 80 KB so two workgroups share a CU and overlap each other's latency-bound
+// phases (triangular solve, barriers) with MFMA work.
 //
 // Parallel decomposition (segmented chunk scan).  Each sequence's chunks are
 // split into segments; one 256-thread workgroup owns one (segment, head) and
@@ -36,33 +41,38 @@
 namespace hmx {
 namespace gdnp {
 
-constexpr int C = 64;          // chunk length
+constexpr int C = 32;          // chunk length (tokens); 32 keeps LDS at 2 workgroups/CU
+constexpr int MT = C / 16;     // 16-row tiles per chunk
+constexpr int KT = C / 32;     // 32-token MFMA k-steps per chunk
 constexpr int D = 128;         // head dim (K == V == 128)
 constexpr int NTHR = 256;      // 4 waves
-constexpr int LDQ = D + 8;     // bf16 [64][128] row stride (q, k, W, O staging)
-constexpr int LDT = C + 8;     // bf16 [128][64] row stride (K^T, V^T) and [64][64] (P, T hi/lo)
-constexpr int LDA = C + 8;     // fp32 [64][64] row stride (A, T)
+constexpr int LDQ = D + 8;     // bf16 [C][128] row stride (q, k, v, W, O staging)
+constexpr int LDT = C + 8;     // bf16 [C][C] row stride (P, T hi/lo)
+constexpr int LDA = C + 8;     // fp32 [C][C] row stride (A, T)
+constexpr int LDWT = C + 8;    // bf16 [128][C] row stride (W^T hi/lo)
+static_assert(C == 32 || C == 64, "chunk length");
 
 enum Mode { MODE_OUT = 0, MODE_S0 = 1, MODE_PHI = 2 };
 
 // shared-memory layout (bytes)
-constexpr int SZ_Q = C * LDQ * 2;           // 17408
-constexpr int SZ_KT = D * LDT * 2;          // 18432
-constexpr int SZ_F32 = C * LDA * 4;         // 18432
-constexpr int SZ_P = C * LDT * 2;           // 9216
+constexpr int SZ_Q = C * LDQ * 2;
+constexpr int SZ_F32 = C * LDA * 4;
+constexpr int SZ_P = C * LDT * 2;
 constexpr int OFF_Q = 0;
 constexpr int OFF_K = OFF_Q + SZ_Q;
-constexpr int OFF_KT = OFF_K + SZ_Q;
-constexpr int OFF_VT = OFF_KT + SZ_KT;      // also the O staging buffer
-constexpr int OFF_A = OFF_VT + SZ_KT;       // fp32 A, then bf16 T hi/lo (4 x SZ_P)
+constexpr int OFF_V = OFF_K + SZ_Q;         // also the O staging buffer
+constexpr int OFF_A = OFF_V + SZ_Q;         // fp32 A
 constexpr int OFF_T = OFF_A + SZ_F32;       // fp32 T
-constexpr int OFF_W = OFF_T + SZ_F32;
-constexpr int OFF_P = OFF_W + SZ_Q;
-constexpr int OFF_X = OFF_P + SZ_P;         // fp32 scratch 3 x 16 x 16
-constexpr int OFF_G = OFF_X + 3 * 256 * 4;  // fp32 G[64], beta[64], eG[64], edl[64]
+constexpr int OFF_TH = OFF_T + SZ_F32;      // bf16 T hi
+constexpr int OFF_TL = OFF_TH + SZ_P;       // bf16 T lo
+constexpr int SZ_WT = D * LDWT * 2;
+constexpr int OFF_W = OFF_TL + SZ_P;        // -W^T hi
+constexpr int OFF_WL = OFF_W + SZ_WT;       // -W^T lo
+constexpr int OFF_P = OFF_WL + SZ_WT;
+constexpr int OFF_X = OFF_P + SZ_P;         // fp32 32x32 scratch for the T merge
+constexpr int OFF_G = OFF_X + (C == 64 ? 32 * 33 * 4 : 0);  // fp32 G, beta, e^G, e^{Gl-G} [C]
 constexpr int SMEM = OFF_G + 4 * C * 4;
-static_assert(4 * SZ_P <= 2 * SZ_F32, "T hi/lo must fit over A and T");
-static_assert(SMEM <= 160 * 1024, "LDS budget");
+static_assert(SMEM <= 80 * 1024, "LDS budget: two workgroups per CU");
 
 struct SegInfo {     // one row of the host-built segment table (int32 x 8)
   int n, bos, eos, c_start, c_end, seg_idx, first_seg, nseg;
@@ -104,6 +114,10 @@ __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+__device__ __forceinline__ f32x4 mfma16f(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
 // A (or B^T) fragment in natural k order: lane holds row r0+(l&15), k0+8(l>>4)..+7.
 __device__ __forceinline__ bf16x8 frag(const bf16* base, int ld, int r0, int k0, int lane) {
   return *reinterpret_cast<const bf16x8*>(base + (r0 + (lane & 15)) * ld + k0 + 8 * (lane >> 4));
@@ -115,6 +129,38 @@ __device__ __forceinline__ bf16x8 frag_perm(const bf16* base, int ld, int r0, in
   const bf16* p = base + (r0 + (lane & 15)) * ld + k0 + 4 * (lane >> 4);
   const bf16x4 a = *reinterpret_cast<const bf16x4*>(p);
   const bf16x4 b = *reinterpret_cast<const bf16x4*>(p + 16);
+  return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// Transposing LDS read (gfx950 ds_read_b64_tr_b16) of a row-major bf16 matrix
+// M[row][col]: within each 16-lane group, lane i receives M[t0+j][c0+i] for
+// j = 0..3 (4 consecutive rows of one column), where the group reads rows
+// t0..t0+3 and columns c0..c0+15.  Each source lane s supplies the address of
+// M[t0 + s/4][c0 + 4(s%4)].
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ bf16x4 ld_tr(const bf16* base, int ld, int t0, int c0, int lane) {
+  const int s = lane & 15;
+  const bf16* a = base + (t0 + (s >> 2)) * ld + c0 + 4 * (s & 3);
+  const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(a));
+  return __builtin_bit_cast(bf16x4, r);
+}
+
+// B fragment of M[k=row][n=col] in natural k order (k = t0 + 8q + 0..7) from a
+// row-major bf16 matrix: column c0 + (l&15).
+__device__ __forceinline__ bf16x8 frag_t(const bf16* base, int ld, int t0, int c0, int lane) {
+  const int tq = t0 + 8 * (lane >> 4);
+  const bf16x4 a = ld_tr(base, ld, tq, c0, lane);
+  const bf16x4 b = ld_tr(base, ld, tq + 4, c0, lane);
+  return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// A fragment of M^T (rows = columns of M, k = rows of M) in the permuted k
+// order of frag_perm: k = t0+4q+{0..3} and t0+16+4q+{0..3}.
+__device__ __forceinline__ bf16x8 frag_t_perm(const bf16* base, int ld, int t0, int c0, int lane) {
+  const int tq = t0 + 4 * (lane >> 4);
+  const bf16x4 a = ld_tr(base, ld, tq, c0, lane);
+  const bf16x4 b = ld_tr(base, ld, tq + 16, c0, lane);
   return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
@@ -137,24 +183,208 @@ __device__ __forceinline__ void pack_b_hilo(const f32x4& t0, const f32x4& t1, bf
   }
 }
 
+// Sum over the 16 lanes of a DPP row (VALU lane permutes, no LDS traffic).
+__device__ __forceinline__ float row16_sum(float x) {
+  auto dpp = [](float v, int ctrl) -> float {
+    int r;
+    switch (ctrl) {
+      case 0: r = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false); break;
+      case 1: r = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false); break;
+      case 2: r = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false); break;
+      default: r = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false); break;
+    }
+    return __builtin_bit_cast(float, r);
+  };
+  x += dpp(x, 0);  // quad_perm [1,0,3,2]
+  x += dpp(x, 1);  // quad_perm [2,3,0,1]
+  x += dpp(x, 2);  // row_half_mirror
+  x += dpp(x, 3);  // row_mirror
+  return x;
+}
+
+// Inclusive prefix sum over lanes 0..31 (two DPP rows) with VALU lane shifts.
+#define HMX_DPP_F(v, ctrl, rmask) \
+  __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, (v)), (ctrl), \
+                                                        (rmask), 0xF, true))
+__device__ __forceinline__ float scan32(float x) {
+  x += HMX_DPP_F(x, 0x111, 0xF);  // row_shr:1
+  x += HMX_DPP_F(x, 0x112, 0xF);  // row_shr:2
+  x += HMX_DPP_F(x, 0x114, 0xF);  // row_shr:4
+  x += HMX_DPP_F(x, 0x118, 0xF);  // row_shr:8
+  x += HMX_DPP_F(x, 0x142, 0xA);  // row_bcast:15 into rows 1 and 3
+  return x;
+}
+#undef HMX_DPP_F
+
+// Workgroup barrier that orders LDS only: global loads issued before it stay in
+// flight (the next chunk's prefetch), unlike __syncthreads().
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// One chunk's raw inputs for this thread: 4 rows x 8 features of k, v, q and
+// (wave 0) one token's g and beta.  Loaded one chunk ahead.
+struct RawChunk {
+  bf16x8 k[MT], v[MT], q[MT];
+  float g, b;
+};
+
+template <int MODE>
+__device__ __forceinline__ void load_raw(RawChunk& r, const Params& p, const bf16* qh,
+                                         const bf16* kh, const bf16* vh, int64_t q_rs,
+                                         int64_t kv_rs, int tok0, int nval, bool need_q,
+                                         int tid, int h) {
+#pragma unroll
+  for (int pass = 0; pass < MT; ++pass) {
+    const int row = pass * 16 + (tid >> 4);
+    const int f0 = (tid & 15) * 8;
+    const bool ok = row < nval;
+    const int64_t tok = tok0 + row;
+    r.k[pass] = ok ? *reinterpret_cast<const bf16x8*>(kh + tok * kv_rs + f0) : bf16x8{};
+    if (MODE != MODE_PHI)
+      r.v[pass] = ok ? *reinterpret_cast<const bf16x8*>(vh + tok * kv_rs + f0) : bf16x8{};
+    if (MODE == MODE_OUT)
+      r.q[pass] = (ok && need_q) ? *reinterpret_cast<const bf16x8*>(qh + tok * q_rs + f0)
+                                 : bf16x8{};
+  }
+  if (tid < C) {
+    const bool ok = tid < nval;
+    const int64_t gi = (int64_t)(tok0 + tid) * p.H + h;
+    r.g = ok ? ld_scalar(p.g, gi, p.g_dt) : 0.f;
+    r.b = ok ? ld_scalar(p.beta, gi, p.beta_dt) : 0.f;
+  }
+}
+
+// Stage one 8-feature row slice: optionally L2-normalise across the 16 lanes
+// holding the row, round to bf16, write to LDS.
+__device__ __forceinline__ void stage_row(bf16* dst, const bf16x8& raw, bool norm) {
+  float f[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) f[j] = (float)raw[j];
+  if (norm) {
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss += f[j] * f[j];
+    const float inv = 1.0f / sqrtf(row16_sum(ss) + 1e-6f);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) f[j] *= inv;
+  }
+  bf16x8 b;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) b[j] = (bf16)f[j];
+  *reinterpret_cast<bf16x8*>(dst) = b;
+}
+
+// ---------------------------------------------------------------------------
+// T = (I + A)^-1 for the strictly-lower 64x64 A in sA (fp32), into sT (fp32).
+// 16x16 diagonal blocks by forward substitution (one wave each, register
+// resident), then the block merges with fp32 MFMA:
+//   T_10 = -T_11 A_10 T_00,  T_32 = -T_33 A_32 T_22            (16x16)
+//   T[32:,:32] = -T_HH A_HL T_LL                                (32x32)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void put_t(float* sT, bf16* sTh, bf16* sTl, int r, int c, float x) {
+  sT[r * LDA + c] = x;
+  const bf16 h = (bf16)x;
+  sTh[r * LDT + c] = h;
+  sTl[r * LDT + c] = (bf16)(x - (float)h);
+}
+
+__device__ __forceinline__ void tri_inverse(const float* sA, float* sT, bf16* sTh, bf16* sTl,
+                                           float* sX, int wave, int lane) {
+  const int q4 = lane >> 4, l16 = lane & 15;
+  if (wave < MT) {
+    // diagonal block b = wave: lane l16 solves column l16 of (I + A_bb) x = e
+    const int b = wave;
+    const float* Ab = sA + (16 * b) * LDA + 16 * b;
+    float x[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float arow[16];
+#pragma unroll
+      for (int m = 0; m < 16; m += 4) {
+        const float4 t = *reinterpret_cast<const float4*>(Ab + r * LDA + m);
+        arow[m] = t.x; arow[m + 1] = t.y; arow[m + 2] = t.z; arow[m + 3] = t.w;
+      }
+      float acc = (r == l16) ? 1.f : 0.f;
+#pragma unroll
+      for (int m = 0; m < r; ++m) acc -= arow[m] * x[m];
+      x[r] = acc;
+    }
+    // lanes 16..63 duplicate lanes 0..15.  Strictly-upper blocks of T are never
+    // read (hi/lo consumers skip them), so they are not written.
+    if (lane < 16) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) put_t(sT, sTh, sTl, 16 * b + r, 16 * b + l16, x[r]);
+    }
+  }
+  lds_barrier();
+  // 16x16 merges T_{2p+1,2p} = -T_{2p+1,2p+1} A_{2p+1,2p} T_{2p,2p}: wave p
+  if (wave < MT / 2) {
+    const int i = 2 * wave + 1, j = 2 * wave;
+    // X = A_ij T_jj  (A operand from sA, B operand from sT, k in natural order)
+    f32x4 X = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      X = mfma16f(sA[(16 * i + l16) * LDA + 16 * j + 4 * s + q4],
+                  sT[(16 * j + 4 * s + q4) * LDA + 16 * j + l16], X);
+    // Y = T_ii X: X is in C layout, usable as B operand with k = 4q + s
+    f32x4 Y = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) Y = mfma16f(sT[(16 * i + l16) * LDA + 16 * i + 4 * q4 + s], X[s], Y);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) put_t(sT, sTh, sTl, 16 * i + 4 * q4 + v, 16 * j + l16, -Y[v]);
+  }
+  lds_barrier();
+  if constexpr (C == 64) {
+    // 32x32 merge: X = A_HL T_LL (wave w -> tile (a, b) = (w>>1, w&1))
+    {
+      const int a = wave >> 1, b = wave & 1;
+      f32x4 X = {0.f, 0.f, 0.f, 0.f};
+      for (int c = b; c < 2; ++c) {  // T_LL is block lower-triangular
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          X = mfma16f(sA[(32 + 16 * a + l16) * LDA + 16 * c + 4 * s + q4],
+                      sT[(16 * c + 4 * s + q4) * LDA + 16 * b + l16], X);
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) sX[(16 * a + 4 * q4 + v) * 33 + 16 * b + l16] = X[v];
+    }
+    lds_barrier();
+    {
+      const int a = wave >> 1, b = wave & 1;
+      f32x4 Y = {0.f, 0.f, 0.f, 0.f};
+      for (int c = 0; c <= a; ++c) {  // T_HH is block lower-triangular
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          Y = mfma16f(sT[(32 + 16 * a + l16) * LDA + 32 + 16 * c + 4 * s + q4],
+                      sX[(16 * c + 4 * s + q4) * 33 + 16 * b + l16], Y);
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        put_t(sT, sTh, sTl, 32 + 16 * a + 4 * q4 + v, 16 * b + l16, -Y[v]);
+    }
+    lds_barrier();
+  }
+}
+
 // ---------------------------------------------------------------------------
 // the chunk-scan workgroup
 // ---------------------------------------------------------------------------
 template <int MODE>
-__global__ __launch_bounds__(NTHR, 1) void gdn_chunk_kernel(Params p) {
+__global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
   __shared__ __align__(16) unsigned char smem[SMEM];
   bf16* sQ = reinterpret_cast<bf16*>(smem + OFF_Q);
   bf16* sK = reinterpret_cast<bf16*>(smem + OFF_K);
-  bf16* sKt = reinterpret_cast<bf16*>(smem + OFF_KT);
-  bf16* sVt = reinterpret_cast<bf16*>(smem + OFF_VT);
-  bf16* sO = sVt;  // O staging reuses V^T after U is formed
+  bf16* sV = reinterpret_cast<bf16*>(smem + OFF_V);
+  bf16* sO = sV;  // O staging reuses V after U is formed
   float* sA = reinterpret_cast<float*>(smem + OFF_A);
   float* sT = reinterpret_cast<float*>(smem + OFF_T);
-  bf16* sTkh = reinterpret_cast<bf16*>(smem + OFF_A);
-  bf16* sTkl = sTkh + C * LDT;
-  bf16* sTvh = sTkl + C * LDT;
-  bf16* sTvl = sTvh + C * LDT;
+  bf16* sTh = reinterpret_cast<bf16*>(smem + OFF_TH);
+  bf16* sTl = reinterpret_cast<bf16*>(smem + OFF_TL);
   bf16* sW = reinterpret_cast<bf16*>(smem + OFF_W);
+  bf16* sWl = reinterpret_cast<bf16*>(smem + OFF_WL);
   bf16* sP = reinterpret_cast<bf16*>(smem + OFF_P);
   float* sX = reinterpret_cast<float*>(smem + OFF_X);
   float* sG = reinterpret_cast<float*>(smem + OFF_G);
@@ -163,6 +393,11 @@ __global__ __launch_bounds__(NTHR, 1) void gdn_chunk_kernel(Params p) {
   float* sEDL = sEG + C;  // e^{G_last - G}
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // T hi/lo upper-triangular 16x16 blocks are never written: zero them once
+  for (int i = tid; i < C * C; i += NTHR) {
+    const int r = i / C, c = i % C;
+    if ((c >> 4) > (r >> 4)) { sTh[r * LDT + c] = (bf16)0.f; sTl[r * LDT + c] = (bf16)0.f; }
+  }
   const int q4 = lane >> 4, l16 = lane & 15;
   const int s_id = blockIdx.x, h = blockIdx.y;
   const SegInfo si = load_seg(p.seg, s_id);
@@ -228,280 +463,219 @@ __global__ __launch_bounds__(NTHR, 1) void gdn_chunk_kernel(Params p) {
   const bf16* kh = p.k + (int64_t)hk * D;
   const bf16* vh = p.v + (int64_t)hk * D;
 
+  RawChunk raw;
+  if (c_begin < si.c_end)
+    load_raw<MODE>(raw, p, qh, kh, vh, q_rs, kv_rs, si.bos + c_begin * C,
+                   min(C, si.eos - (si.bos + c_begin * C)), c_begin >= c_out, tid, h);
+
   for (int c = c_begin; c < si.c_end; ++c) {
     const int tok0 = si.bos + c * C;
     const int nval = min(C, si.eos - tok0);
     const bool out_chunk = (MODE == MODE_OUT) && (c >= c_out);
 
-    // ---- phase 0: load the chunk (L2-normalise q,k rows), g cumsum --------
+    // ---- phase 0: stage the prefetched chunk in LDS (L2-normalise q,k rows),
+    //      g cumsum; then prefetch the next chunk into registers --------------
     {
-      // 16 threads per 128-wide row, 16 rows per pass, 4 passes
 #pragma unroll
-      for (int pass = 0; pass < 4; ++pass) {
+      for (int pass = 0; pass < MT; ++pass) {
         const int row = pass * 16 + (tid >> 4);
         const int f0 = (tid & 15) * 8;
-        const bool ok = row < nval;
-        const int64_t tok = tok0 + row;
-        // k
-        bf16x8 kv8 = {};
-        if (ok) kv8 = *reinterpret_cast<const bf16x8*>(kh + tok * kv_rs + f0);
-        float kf[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) kf[j] = (float)kv8[j];
-        if (p.l2norm) {
-          float ss = 0.f;
-#pragma unroll
-          for (int j = 0; j < 8; ++j) ss += kf[j] * kf[j];
-          ss += shfl_xor(ss, 1); ss += shfl_xor(ss, 2);
-          ss += shfl_xor(ss, 4); ss += shfl_xor(ss, 8);
-          const float inv = 1.0f / sqrtf(ss + 1e-6f);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) kf[j] *= inv;
-        }
-        bf16x8 kb;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) kb[j] = (bf16)kf[j];
-        *reinterpret_cast<bf16x8*>(sK + row * LDQ + f0) = kb;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) sKt[(f0 + j) * LDT + row] = kb[j];
-        // v (transposed only)
-        if (MODE != MODE_PHI) {
-          bf16x8 vv8 = {};
-          if (ok) vv8 = *reinterpret_cast<const bf16x8*>(vh + tok * kv_rs + f0);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) sVt[(f0 + j) * LDT + row] = vv8[j];
-        }
-        // q
-        if (out_chunk) {
-          bf16x8 qv8 = {};
-          if (ok) qv8 = *reinterpret_cast<const bf16x8*>(qh + tok * q_rs + f0);
-          float qf[8];
-#pragma unroll
-          for (int j = 0; j < 8; ++j) qf[j] = (float)qv8[j];
-          if (p.l2norm) {
-            float ss = 0.f;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) ss += qf[j] * qf[j];
-            ss += shfl_xor(ss, 1); ss += shfl_xor(ss, 2);
-            ss += shfl_xor(ss, 4); ss += shfl_xor(ss, 8);
-            const float inv = 1.0f / sqrtf(ss + 1e-6f);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) qf[j] *= inv;
-          }
-          bf16x8 qb;
-#pragma unroll
-          for (int j = 0; j < 8; ++j) qb[j] = (bf16)qf[j];
-          *reinterpret_cast<bf16x8*>(sQ + row * LDQ + f0) = qb;
-        }
+        stage_row(sK + row * LDQ + f0, raw.k[pass], p.l2norm);
+        if (MODE != MODE_PHI) *reinterpret_cast<bf16x8*>(sV + row * LDQ + f0) = raw.v[pass];
+        if (out_chunk) stage_row(sQ + row * LDQ + f0, raw.q[pass], p.l2norm);
       }
       if (wave == 0) {
-        const int t = lane;
-        const bool ok = t < nval;
-        const int64_t gi = (int64_t)(tok0 + t) * H + h;
-        float gv = ok ? ld_scalar(p.g, gi, p.g_dt) : 0.f;
-        float bv = ok ? ld_scalar(p.beta, gi, p.beta_dt) : 0.f;
-        // inclusive scan over the 64 lanes
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-          const float y = __shfl_up(gv, off, 64);
-          if (lane >= off) gv += y;
+        static_assert(C == 32, "the DPP scan covers 32 lanes");
+        const float gv = scan32(lane < C ? raw.g : 0.f);
+        const float glast = __builtin_bit_cast(
+            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gv), C - 1));
+        if (lane < C) {
+          sG[lane] = gv;
+          sB[lane] = raw.b;
+          sEG[lane] = fast_exp(gv);
+          sEDL[lane] = fast_exp(glast - gv);
         }
-        const float glast = __shfl(gv, 63, 64);
-        sG[t] = gv;
-        sB[t] = bv;
-        sEG[t] = fast_exp(gv);
-        sEDL[t] = fast_exp(glast - gv);
+      }
+      if (c + 1 < si.c_end) {
+        const int t1 = tok0 + C;
+        load_raw<MODE>(raw, p, qh, kh, vh, q_rs, kv_rs, t1, min(C, si.eos - t1), c + 1 >= c_out,
+                       tid, h);
       }
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---- phase 1: A = beta_i (k_i.k_j) e^{G_i-G_j} (j<i), P = q_i.k_j e^{G_i-G_j} (j<=i)
-    {
-      const int nitems = out_chunk ? 20 : 10;
-      for (int it = wave; it < nitems; it += 4) {
-        const int pair = out_chunk ? (it >> 1) : it;
-        const bool isP = out_chunk && (it & 1);
-        int i = 0, j = pair;
-        while (j > i) { j -= i + 1; ++i; }  // pair -> (i, j), 0 <= j <= i < 4
-        const bf16* Am = isP ? sQ : sK;
+    //      wave w < MT owns A's 16-row strip w; wave MT + w owns P's strip w
+    if (wave < MT || (out_chunk && wave < 2 * MT)) {
+      const bool isP = wave >= MT;
+      const int i = isP ? wave - MT : wave;
+      const bf16* Am = isP ? sQ : sK;
+      bf16x8 af[4];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) af[ks] = frag(Am, LDQ, 16 * i, 32 * ks, lane);
+      float gr[4], br[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        gr[v] = sG[16 * i + 4 * q4 + v];
+        br[v] = sB[16 * i + 4 * q4 + v];
+      }
+#pragma unroll
+      for (int j = 0; j < MT; ++j) {
+        if (j > i) break;
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
-          acc = mfma16(frag(Am, LDQ, 16 * i, 32 * ks, lane), frag(sK, LDQ, 16 * j, 32 * ks, lane),
-                       acc);
+        for (int ks = 0; ks < 4; ++ks) acc = mfma16(af[ks], frag(sK, LDQ, 16 * j, 32 * ks, lane), acc);
         const int col = 16 * j + l16;
         const float gc = sG[col];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int row = 16 * i + 4 * q4 + v;
-          const float dcy = (row >= col) ? fast_exp(sG[row] - gc) : 0.f;
-          if (isP) {
-            sP[row * LDT + col] = (bf16)(row >= col ? acc[v] * dcy : 0.f);
-          } else {
-            sA[row * LDA + col] = row > col ? sB[row] * acc[v] * dcy : 0.f;
+          const float dcy = (row >= col) ? fast_exp(gr[v] - gc) : 0.f;
+          if (isP) sP[row * LDT + col] = (bf16)(acc[v] * dcy);
+          else sA[row * LDA + col] = row > col ? br[v] * acc[v] * dcy : 0.f;
+        }
+      }
+    }
+    lds_barrier();
+
+    // ---- phase 2: T = (I + A)^-1 in fp32, also kept as bf16 hi + lo ------------
+    tri_inverse(sA, sT, sTh, sTl, sX, wave, lane);
+
+    // ---- phase 3: W = T diag(beta e^G) K (to LDS, negated hi/lo), U = T diag(beta) V
+    //      (registers).  The token scales are applied to the B fragments in fp32,
+    //      split into hi/lo, and multiplied by T hi/lo (3 products each).
+    f32x4 Vn[MT][2];  // U, then V_new: rows 16mt.., cols 32w+16ct..
+    {
+      float sk[KT][8], sv[KT][8];
+#pragma unroll
+      for (int ks = 0; ks < KT; ++ks)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int t = 32 * ks + 8 * q4 + j;
+          sv[ks][j] = sB[t];
+          sk[ks][j] = sv[ks][j] * sEG[t];
+        }
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        bf16x8 bkh[KT], bkl[KT], bvh[KT], bvl[KT];
+#pragma unroll
+        for (int ks = 0; ks < KT; ++ks) {
+          const bf16x8 kr = frag_t(sK, LDQ, 32 * ks, 32 * wave + 16 * ct, lane);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float x = (float)kr[j] * sk[ks][j];
+            const bf16 hx = (bf16)x;
+            bkh[ks][j] = hx;
+            bkl[ks][j] = (bf16)(x - (float)hx);
           }
-        }
-      }
-    }
-    __syncthreads();
-
-    // ---- phase 2: T = (I + A)^-1 in fp32 --------------------------------------
-    {
-      // 2a: 16x16 diagonal blocks by forward substitution, one wave per block
-      {
-        const int b = wave, cc = l16;
-        float x[16];
+          if (MODE != MODE_PHI) {
+            const bf16x8 vr = frag_t(sV, LDQ, 32 * ks, 32 * wave + 16 * ct, lane);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float acc = (r == cc) ? 1.f : 0.f;
-#pragma unroll
-          for (int m = 0; m < r; ++m) acc -= sA[(16 * b + r) * LDA + 16 * b + m] * x[m];
-          x[r] = acc;
-        }
-        if (lane < 16) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) sT[(16 * b + r) * LDA + 16 * b + cc] = x[r];
-        }
-        // zero the strictly-upper blocks of T in this block row
-        for (int e = lane; e < 16 * 64; e += 64) {
-          const int r = 16 * b + (e >> 6), col = e & 63;
-          if ((col >> 4) > b) sT[r * LDA + col] = 0.f;
-        }
-      }
-      __syncthreads();
-      // 2b: off-diagonal blocks by distance d: T_ij = -T_ii sum_{m=j}^{i-1} A_im T_mj
-      for (int d = 1; d < 4; ++d) {
-        const int nblk = 4 - d;
-        for (int e = tid; e < nblk * 256; e += NTHR) {
-          const int bj = e >> 8, r = (e >> 4) & 15, cc = e & 15;
-          const int bi = bj + d;
-          float acc = 0.f;
-          for (int m = bj; m < bi; ++m)
-#pragma unroll
-            for (int kk = 0; kk < 16; ++kk)
-              acc += sA[(16 * bi + r) * LDA + 16 * m + kk] * sT[(16 * m + kk) * LDA + 16 * bj + cc];
-          sX[e] = acc;
-        }
-        __syncthreads();
-        for (int e = tid; e < nblk * 256; e += NTHR) {
-          const int bj = e >> 8, r = (e >> 4) & 15, cc = e & 15;
-          const int bi = bj + d;
-          float acc = 0.f;
-#pragma unroll
-          for (int kk = 0; kk < 16; ++kk)
-            acc += sT[(16 * bi + r) * LDA + 16 * bi + kk] * sX[(bj << 8) + kk * 16 + cc];
-          sT[(16 * bi + r) * LDA + 16 * bj + cc] = -acc;
-        }
-        __syncthreads();
-      }
-      // 2c: Tk = T diag(beta e^G), Tv = T diag(beta), split into bf16 hi + lo
-      float tk[16], tv[16];
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int idx = tid + e * NTHR, r = idx >> 6, cc = idx & 63;
-        const float t = sT[r * LDA + cc];
-        tk[e] = t * sB[cc] * sEG[cc];
-        tv[e] = t * sB[cc];
-      }
-      __syncthreads();
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int idx = tid + e * NTHR, r = idx >> 6, cc = idx & 63;
-        const bf16 kh_ = (bf16)tk[e];
-        sTkh[r * LDT + cc] = kh_;
-        sTkl[r * LDT + cc] = (bf16)(tk[e] - (float)kh_);
-        if (MODE != MODE_PHI) {
-          const bf16 vh_ = (bf16)tv[e];
-          sTvh[r * LDT + cc] = vh_;
-          sTvl[r * LDT + cc] = (bf16)(tv[e] - (float)vh_);
-        }
-      }
-      __syncthreads();
-    }
-
-    // ---- phase 3: W = Tk K (to LDS, negated), U = Tv V (registers) -----------
-    f32x4 Vn[4][2];  // U, then V_new: rows 16mt.., cols 32w+16ct..
-    {
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
-          const int nt = 2 * wave + ct;
-          f32x4 w = {0.f, 0.f, 0.f, 0.f};
-          f32x4 u = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int ks = 0; ks < 2; ++ks) {
-            const bf16x8 bk = frag(sKt, LDT, 16 * nt, 32 * ks, lane);
-            w = mfma16(frag(sTkh, LDT, 16 * mt, 32 * ks, lane), bk, w);
-            w = mfma16(frag(sTkl, LDT, 16 * mt, 32 * ks, lane), bk, w);
-            if (MODE != MODE_PHI) {
-              const bf16x8 bv = frag(sVt, LDT, 16 * nt, 32 * ks, lane);
-              u = mfma16(frag(sTvh, LDT, 16 * mt, 32 * ks, lane), bv, u);
-              u = mfma16(frag(sTvl, LDT, 16 * mt, 32 * ks, lane), bv, u);
+            for (int j = 0; j < 8; ++j) {
+              const float x = (float)vr[j] * sv[ks][j];
+              const bf16 hx = (bf16)x;
+              bvh[ks][j] = hx;
+              bvl[ks][j] = (bf16)(x - (float)hx);
             }
           }
+        }
 #pragma unroll
-          for (int v = 0; v < 4; ++v)
-            sW[(16 * mt + 4 * q4 + v) * LDQ + 16 * nt + l16] = (bf16)(-w[v]);
+        for (int mt = 0; mt < MT; ++mt) {
+          f32x4 w = {0.f, 0.f, 0.f, 0.f}, u = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < KT; ++ks) {
+            if (32 * ks > 16 * mt + 15) continue;  // T is lower triangular
+            const bf16x8 th = frag(sTh, LDT, 16 * mt, 32 * ks, lane);
+            const bf16x8 tl = frag(sTl, LDT, 16 * mt, 32 * ks, lane);
+            w = mfma16(th, bkh[ks], w);
+            w = mfma16(th, bkl[ks], w);
+            w = mfma16(tl, bkh[ks], w);
+            if (MODE != MODE_PHI) {
+              u = mfma16(th, bvh[ks], u);
+              u = mfma16(th, bvl[ks], u);
+              u = mfma16(tl, bvh[ks], u);
+            }
+          }
+          {
+            // -W^T[feature][token]: this lane's 4 tokens are consecutive
+            bf16x4 wh, wl;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              wh[v] = (bf16)(-w[v]);
+              wl[v] = (bf16)(-w[v] - (float)wh[v]);
+            }
+            const int a = (32 * wave + 16 * ct + l16) * LDWT + 16 * mt + 4 * q4;
+            *reinterpret_cast<bf16x4*>(sW + a) = wh;
+            *reinterpret_cast<bf16x4*>(sWl + a) = wl;
+          }
           Vn[mt][ct] = u;
         }
-    }
-    __syncthreads();
-
-    // ---- phase 4: V_new = U - W S (state as bf16 B operand) -------------------
-    bf16x8 Sb[4][2];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) Sb[ks][ct] = pack_b(S[2 * ks][ct], S[2 * ks + 1][ct]);
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const bf16x8 a = frag_perm(sW, LDQ, 16 * mt, 32 * ks, lane);
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) Vn[mt][ct] = mfma16(a, Sb[ks][ct], Vn[mt][ct]);
       }
+    }
+    lds_barrier();
+
+    // ---- phase 4: V_new = U - W S, with W and S as bf16 hi+lo pairs ------------
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      bf16x8 Sh[2], Sl[2];
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) pack_b_hilo(S[2 * ks][ct], S[2 * ks + 1][ct], Sh[ct], Sl[ct]);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const bf16x8 a = frag_t_perm(sW, LDWT, 32 * ks, 16 * mt, lane);
+        const bf16x8 al = frag_t_perm(sWl, LDWT, 32 * ks, 16 * mt, lane);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+          Vn[mt][ct] = mfma16(a, Sh[ct], Vn[mt][ct]);
+          Vn[mt][ct] = mfma16(a, Sl[ct], Vn[mt][ct]);
+          Vn[mt][ct] = mfma16(al, Sh[ct], Vn[mt][ct]);
+        }
+      }
+    }
 
     // ---- phase 5: O = scale [e^G (Q S) + P V_new] ------------------------------
     if (out_chunk) {
-      f32x4 O[4][2];
+      f32x4 O[MT][2];
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) O[mt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+      for (int ks = 0; ks < 4; ++ks) {
+        bf16x8 Sh[2];
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
+        for (int ct = 0; ct < 2; ++ct) Sh[ct] = pack_b(S[2 * ks][ct], S[2 * ks + 1][ct]);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
           const bf16x8 a = frag_perm(sQ, LDQ, 16 * mt, 32 * ks, lane);
 #pragma unroll
-          for (int ct = 0; ct < 2; ++ct) O[mt][ct] = mfma16(a, Sb[ks][ct], O[mt][ct]);
+          for (int ct = 0; ct < 2; ++ct) O[mt][ct] = mfma16(a, Sh[ct], O[mt][ct]);
         }
+      }
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const float e = sEG[16 * mt + 4 * q4 + v];
           O[mt][0][v] *= e;
           O[mt][1][v] *= e;
         }
-      bf16x8 Vb[2][2];
+      bf16x8 Vb[KT][2];
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
+      for (int ks = 0; ks < KT; ++ks)
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) Vb[ks][ct] = pack_b(Vn[2 * ks][ct], Vn[2 * ks + 1][ct]);
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
+        for (int ks = 0; ks < KT; ++ks) {
           if (32 * ks > 16 * mt + 15) continue;  // P is lower triangular
           const bf16x8 a = frag_perm(sP, LDT, 16 * mt, 32 * ks, lane);
 #pragma unroll
           for (int ct = 0; ct < 2; ++ct) O[mt][ct] = mfma16(a, Vb[ks][ct], O[mt][ct]);
         }
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
@@ -520,24 +694,24 @@ __global__ __launch_bounds__(NTHR, 1) void gdn_chunk_kernel(Params p) {
 #pragma unroll
           for (int v = 0; v < 4; ++v) S[rt][ct][v] *= egl;
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const float e = sEDL[16 * mt + 4 * q4 + v];
           Vn[mt][0][v] *= e;
           Vn[mt][1][v] *= e;
         }
-      bf16x8 Vh[2][2], Vl[2][2];
+      bf16x8 Vh[KT][2], Vl[KT][2];
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
+      for (int ks = 0; ks < KT; ++ks)
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct)
           pack_b_hilo(Vn[2 * ks][ct], Vn[2 * ks + 1][ct], Vh[ks][ct], Vl[ks][ct]);
 #pragma unroll
       for (int rt = 0; rt < 8; ++rt)
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          const bf16x8 a = frag_perm(sKt, LDT, 16 * rt, 32 * ks, lane);
+        for (int ks = 0; ks < KT; ++ks) {
+          const bf16x8 a = frag_t_perm(sK, LDQ, 32 * ks, 16 * rt, lane);
 #pragma unroll
           for (int ct = 0; ct < 2; ++ct) {
             S[rt][ct] = mfma16(a, Vh[ks][ct], S[rt][ct]);
@@ -545,20 +719,20 @@ __global__ __launch_bounds__(NTHR, 1) void gdn_chunk_kernel(Params p) {
           }
         }
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---- store O (coalesced 16-byte rows) --------------------------------------
     if (out_chunk) {
       bf16* oh = p.o + (int64_t)h * D;
 #pragma unroll
-      for (int pass = 0; pass < 4; ++pass) {
+      for (int pass = 0; pass < MT; ++pass) {
         const int row = pass * 16 + (tid >> 4);
         const int f0 = (tid & 15) * 8;
         if (row < nval)
           *reinterpret_cast<bf16x8*>(oh + (int64_t)(tok0 + row) * q_rs + f0) =
               *reinterpret_cast<const bf16x8*>(sO + row * LDQ + f0);
       }
-      __syncthreads();
+      lds_barrier();
     }
   }
 
@@ -602,7 +776,7 @@ __global__ __launch_bounds__(64) void gdn_plan_kernel(Params p, int N) {
         for (int c = si.c_start - 1; c >= lo; --c) {
           const int t = si.bos + c * C + lane;
           float b = 0.f;
-          if (t < si.eos) {
+          if (lane < C && t < si.eos) {
             const int64_t gi = (int64_t)t * H + h;
             const float gv = ld_scalar(p.g, gi, p.g_dt);
             const float bv = ld_scalar(p.beta, gi, p.beta_dt);

@@ -154,14 +154,15 @@ def fused_recurrent_gated_delta_rule(q, k, v, g, beta=None, scale=None, initial_
     return o.reshape(B, T, H, V), (pool if output_final_state else None)
 
 
-# Segmented chunk-scan planning (host side).  A segment is a run of 64-token
+# Segmented chunk-scan planning (host side).  A segment is a run of CHUNK-token
 # chunks of one sequence that one workgroup walks serially; more segments give
 # more parallelism at the cost of a short warm-up (or the exact scan) per
-# segment boundary.
-CHUNK = 64
-MIN_SEGMENT_CHUNKS = 8
-MAX_WARM_CHUNKS = 8
+# segment boundary.  CHUNK matches the kernel's internal chunk length.
+CHUNK = 32
+MIN_SEGMENT_CHUNKS = 16
+MAX_WARM_CHUNKS = 16
 DECAY_THRESHOLD = 60.0   # warm-up drops history bounded by exp(-60)
+WORKGROUPS_PER_CU = 2
 _CU_COUNT: dict[int, int] = {}
 
 
@@ -244,7 +245,7 @@ def chunk_gated_delta_rule_gqa(
     if cu_seqlens is not None and bounds and bounds[-1][1] < T:
         o[:, bounds[-1][1]:].zero_()  # tokens past the last sequence are not computed
     ht = torch.empty(N, H, K, V, dtype=torch.float32, device=q.device) if output_final_state else None
-    rows = _segment_table(bounds, H, _cu_count(q.device), _segment_chunks)
+    rows = _segment_table(bounds, H, WORKGROUPS_PER_CU * _cu_count(q.device), _segment_chunks)
     seg = torch.tensor(rows, dtype=torch.int32).to(q.device, non_blocking=True)
     lib = _lib.load()
     ws_bytes = int(lib.hmx_gdn_chunk_workspace_bytes(len(rows), N, H))

@@ -91,7 +91,8 @@ int hmx_gdn_recurrent_fwd(const void* q, const void* k, const void* v, int32_t q
 
 
 /*
- * GDN chunked prefill forward (chunk 64), GQA-native, varlen via a segment table.
+ * GDN chunked prefill forward, GQA-native, varlen via a segment table (the kernel
+ * walks 32-token chunks; the result is the chunked recurrence at any chunk size).
  *  q [T_total, H, 128]; k, v [T_total, HKV, 128] (bf16, contiguous; T_total = B*T)
  *  g, beta [T_total, H] (f32/bf16/f16); o [T_total, H, 128] (bf16)
  *  h0 [N, H, 128, 128] fp32 or NULL; ht [N, H, 128, 128] fp32 or NULL
