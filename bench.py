@@ -106,6 +106,25 @@ def cpu_baseline(sample_tokens=4096):
                 f"chunked form in fp32 torch on CPU, {dt:.2f} s")
 
 
+def copy_calibration(dev, nbytes=1 << 30, reps=5):
+    """A plain device copy of known size: what FETCH_SIZE / WRITE_SIZE read for it
+    calibrates the counters (bytes moved per dispatch = nbytes each way)."""
+    import torch
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device=dev).uniform_()
+    dst = torch.empty_like(src)
+    ms = _timed(lambda: dst.copy_(src), reps, 1)
+    return dict(bytes_each_way=nbytes, ms=ms, GBps=2 * nbytes / (ms * 1e-3) / 1e9)
+
+
+def measured_traffic(key):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary (profiles/), if any."""
+    f = REPO / "profiles" / "traffic.json"
+    try:
+        return json.loads(f.read_text())[key]["hbm_bytes"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -113,6 +132,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", choices=["prefill", "decode"], default=None)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 1 GiB device copy (HBM counter calibration)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the mixer ops shard by head/sequence with no "
@@ -121,6 +142,9 @@ def main():
         sys.exit(2)
     import torch
     dev = torch.device("cuda:0")
+    if a.copy_calibration:
+        print(json.dumps({"copy_calibration": copy_calibration(dev)}), flush=True)
+        return
     out = {}
     if a.only in (None, "prefill"):
         pf = bench_prefill(dev, a.steps, a.warmup)
@@ -143,7 +167,8 @@ def main():
                        "qkv_dtype": "bf16", "state_dtype": "fp32"},
             "roofline": {"bound": "hbm", "achieved": round(pf["GBps"], 1),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(pf["GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
+                         "frac": round(pf["GBps"] / HBM_PEAK_GBS, 4),
+                         "traffic": measured_traffic("gdn_prefill_c1"),
                          "kernel": "all launches of one prefill op call",
                          "algorithmic_bytes": pf["bytes"],
                          "mfma_TFLOPs": round(pf["TFLOPs"], 1),
@@ -158,6 +183,7 @@ def main():
                        "d": 128, "steps": 512, "pool": "fp32 [256,32,128,128] randperm slots"},
             "roofline": {"bound": "hbm", "achieved": round(dc["GBps"], 1), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(dc["GBps"] / HBM_PEAK_GBS, 4),
+                         "traffic": measured_traffic("gdn_decode_c2"),
                          "algorithmic_bytes": dc["bytes"]},
         }
         if "value" not in line:

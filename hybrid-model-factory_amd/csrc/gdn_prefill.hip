@@ -50,7 +50,7 @@ constexpr int LDQ = D + 8;     // bf16 [C][128] row stride (q, k, v, W, O stagin
 constexpr int LDT = C + 8;     // bf16 [C][C] row stride (P, T hi/lo)
 constexpr int LDA = C + 8;     // fp32 [C][C] row stride (A, T)
 constexpr int LDWT = C + 8;    // bf16 [128][C] row stride (W^T hi/lo)
-static_assert(C == 32 || C == 64, "chunk length");
+static_assert(C == 32, "chunk length: the triangular solve is written for 32");
 
 enum Mode { MODE_OUT = 0, MODE_S0 = 1, MODE_PHI = 2 };
 
@@ -69,8 +69,7 @@ constexpr int SZ_WT = D * LDWT * 2;
 constexpr int OFF_W = OFF_TL + SZ_P;        // -W^T hi
 constexpr int OFF_WL = OFF_W + SZ_WT;       // -W^T lo
 constexpr int OFF_P = OFF_WL + SZ_WT;
-constexpr int OFF_X = OFF_P + SZ_P;         // fp32 32x32 scratch for the T merge
-constexpr int OFF_G = OFF_X + (C == 64 ? 32 * 33 * 4 : 0);  // fp32 G, beta, e^G, e^{Gl-G} [C]
+constexpr int OFF_G = OFF_P + SZ_P;         // fp32 G, beta, e^G, e^{Gl-G} [C]
 constexpr int SMEM = OFF_G + 4 * C * 4;
 static_assert(SMEM <= 80 * 1024, "LDS budget: two workgroups per CU");
 
@@ -86,8 +85,7 @@ struct Params {
   const float* h0;           // [N,H,K,V] or null
   float* ht;                 // [N,H,K,V] or null
   const int* seg;            // [nseg_total][8]
-  int* plan;                 // [nseg_total][H]: warm-up start chunk, or -1
-  int* exact;                // [N][H]
+  int* plan;                 // [nseg_total][H]: warm-up start chunk, or -1 (null: 1 seg/seq)
   float* ws_s0;              // [nseg_total][H][D][D]
   float* ws_phi;
   float* ws_init;
@@ -108,6 +106,15 @@ __device__ __forceinline__ float ld_scalar(const void* p, int64_t i, int dt) {
 __device__ __forceinline__ SegInfo load_seg(const int* seg, int s) {
   const int* r = seg + s * 8;
   return SegInfo{r[0], r[1], r[2], r[3], r[4], r[5], r[6], r[7]};
+}
+
+// A sequence/head pair needs the exact segment scan when any of its later
+// segments found no warm-up start (plan == -1).
+__device__ __forceinline__ bool seq_exact(const int* plan, const SegInfo& si, int H, int h) {
+  if (!plan) return false;
+  for (int s = si.first_seg + 1; s < si.first_seg + si.nseg; ++s)
+    if (plan[s * H + h] < 0) return true;
+  return false;
 }
 
 __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
@@ -277,6 +284,34 @@ __device__ __forceinline__ void stage_row(bf16* dst, const bf16x8& raw, bool nor
   *reinterpret_cast<bf16x8*>(dst) = b;
 }
 
+// (I + A)^-1 of a strictly-lower 16x16 block held in C layout (A) together
+// with its transpose (At), by the exact identity for nilpotent A (A^16 = 0):
+//   (I + A)^-1 = (I - A)(I + A^2)(I + A^4)(I + A^8),
+// on fp32 MFMA.  A product X.Y takes X^T and Y in C layout: with k = 4q + s,
+// lane (q, l) supplies X[l][4q+s] = (X^T)_C[s] and Y[4q+s][l] = Y_C[s].
+__device__ __forceinline__ f32x4 mm_ct(const f32x4& Xt, const f32x4& Y, f32x4 acc) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) acc = mfma16f(Xt[s], Y[s], acc);
+  return acc;
+}
+
+__device__ __forceinline__ f32x4 inv_unit_lower16(const f32x4& A, const f32x4& At, int q4, int l16) {
+  const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+  const f32x4 A2 = mm_ct(At, A, z), A2t = mm_ct(A, At, z);
+  const f32x4 A4 = mm_ct(A2t, A2, z), A4t = mm_ct(A2, A2t, z);
+  const f32x4 A8 = mm_ct(A4t, A4, z);
+  f32x4 P1, P1t;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const float d = (4 * q4 + v == l16) ? 1.f : 0.f;
+    P1[v] = d - A[v];
+    P1t[v] = d - At[v];
+  }
+  const f32x4 P2 = mm_ct(P1t, A2, P1), P2t = mm_ct(A2, P1t, P1t);
+  const f32x4 P3 = mm_ct(P2t, A4, P2), P3t = mm_ct(A4, P2t, P2t);
+  return mm_ct(P3t, A8, P3);
+}
+
 // ---------------------------------------------------------------------------
 // T = (I + A)^-1 for the strictly-lower 64x64 A in sA (fp32), into sT (fp32).
 // 16x16 diagonal blocks by forward substitution (one wave each, register
@@ -291,82 +326,23 @@ __device__ __forceinline__ void put_t(float* sT, bf16* sTh, bf16* sTl, int r, in
   sTl[r * LDT + c] = (bf16)(x - (float)h);
 }
 
-__device__ __forceinline__ void tri_inverse(const float* sA, float* sT, bf16* sTh, bf16* sTl,
-                                           float* sX, int wave, int lane) {
+__device__ __forceinline__ void tri_merge(const float* sA, float* sT, bf16* sTh, bf16* sTl,
+                                         int wave, int lane) {
+  static_assert(C == 32, "one 16x16 merge");
   const int q4 = lane >> 4, l16 = lane & 15;
-  if (wave < MT) {
-    // diagonal block b = wave: lane l16 solves column l16 of (I + A_bb) x = e
-    const int b = wave;
-    const float* Ab = sA + (16 * b) * LDA + 16 * b;
-    float x[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float arow[16];
-#pragma unroll
-      for (int m = 0; m < 16; m += 4) {
-        const float4 t = *reinterpret_cast<const float4*>(Ab + r * LDA + m);
-        arow[m] = t.x; arow[m + 1] = t.y; arow[m + 2] = t.z; arow[m + 3] = t.w;
-      }
-      float acc = (r == l16) ? 1.f : 0.f;
-#pragma unroll
-      for (int m = 0; m < r; ++m) acc -= arow[m] * x[m];
-      x[r] = acc;
-    }
-    // lanes 16..63 duplicate lanes 0..15.  Strictly-upper blocks of T are never
-    // read (hi/lo consumers skip them), so they are not written.
-    if (lane < 16) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) put_t(sT, sTh, sTl, 16 * b + r, 16 * b + l16, x[r]);
-    }
-  }
-  lds_barrier();
-  // 16x16 merges T_{2p+1,2p} = -T_{2p+1,2p+1} A_{2p+1,2p} T_{2p,2p}: wave p
-  if (wave < MT / 2) {
-    const int i = 2 * wave + 1, j = 2 * wave;
-    // X = A_ij T_jj  (A operand from sA, B operand from sT, k in natural order)
+  if (wave == 0) {
+    // T_10 = -T_11 A_10 T_00: X = A_10 T_00 (natural k), then Y = T_11 X (k = 4q + s)
     f32x4 X = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 4; ++s)
-      X = mfma16f(sA[(16 * i + l16) * LDA + 16 * j + 4 * s + q4],
-                  sT[(16 * j + 4 * s + q4) * LDA + 16 * j + l16], X);
-    // Y = T_ii X: X is in C layout, usable as B operand with k = 4q + s
+      X = mfma16f(sA[(16 + l16) * LDA + 4 * s + q4], sT[(4 * s + q4) * LDA + l16], X);
     f32x4 Y = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < 4; ++s) Y = mfma16f(sT[(16 * i + l16) * LDA + 16 * i + 4 * q4 + s], X[s], Y);
+    for (int s = 0; s < 4; ++s) Y = mfma16f(sT[(16 + l16) * LDA + 16 + 4 * q4 + s], X[s], Y);
 #pragma unroll
-    for (int v = 0; v < 4; ++v) put_t(sT, sTh, sTl, 16 * i + 4 * q4 + v, 16 * j + l16, -Y[v]);
+    for (int v = 0; v < 4; ++v) put_t(sT, sTh, sTl, 16 + 4 * q4 + v, l16, -Y[v]);
   }
   lds_barrier();
-  if constexpr (C == 64) {
-    // 32x32 merge: X = A_HL T_LL (wave w -> tile (a, b) = (w>>1, w&1))
-    {
-      const int a = wave >> 1, b = wave & 1;
-      f32x4 X = {0.f, 0.f, 0.f, 0.f};
-      for (int c = b; c < 2; ++c) {  // T_LL is block lower-triangular
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-          X = mfma16f(sA[(32 + 16 * a + l16) * LDA + 16 * c + 4 * s + q4],
-                      sT[(16 * c + 4 * s + q4) * LDA + 16 * b + l16], X);
-      }
-#pragma unroll
-      for (int v = 0; v < 4; ++v) sX[(16 * a + 4 * q4 + v) * 33 + 16 * b + l16] = X[v];
-    }
-    lds_barrier();
-    {
-      const int a = wave >> 1, b = wave & 1;
-      f32x4 Y = {0.f, 0.f, 0.f, 0.f};
-      for (int c = 0; c <= a; ++c) {  // T_HH is block lower-triangular
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-          Y = mfma16f(sT[(32 + 16 * a + l16) * LDA + 32 + 16 * c + 4 * s + q4],
-                      sX[(16 * c + 4 * s + q4) * 33 + 16 * b + l16], Y);
-      }
-#pragma unroll
-      for (int v = 0; v < 4; ++v)
-        put_t(sT, sTh, sTl, 32 + 16 * a + 4 * q4 + v, 16 * b + l16, -Y[v]);
-    }
-    lds_barrier();
-  }
 }
 
 // ---------------------------------------------------------------------------
@@ -386,7 +362,6 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
   bf16* sW = reinterpret_cast<bf16*>(smem + OFF_W);
   bf16* sWl = reinterpret_cast<bf16*>(smem + OFF_WL);
   bf16* sP = reinterpret_cast<bf16*>(smem + OFF_P);
-  float* sX = reinterpret_cast<float*>(smem + OFF_X);
   float* sG = reinterpret_cast<float*>(smem + OFF_G);
   float* sB = sG + C;
   float* sEG = sB + C;    // e^{G}
@@ -405,7 +380,7 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
   const int hk = h / (H / p.HKV);
 
   // ---- decide the chunk range and the initial state ------------------------
-  const bool exact = p.exact && p.exact[si.n * H + h];
+  const bool exact = seq_exact(p.plan, si, H, h);
   int c_begin = si.c_start;            // first chunk processed
   const int c_out = si.c_start;        // first chunk whose output is written
   int init_kind;                       // 0 zero, 1 h0, 2 ws_init, 3 identity
@@ -527,19 +502,39 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
         for (int ks = 0; ks < 4; ++ks) acc = mfma16(af[ks], frag(sK, LDQ, 16 * j, 32 * ks, lane), acc);
         const int col = 16 * j + l16;
         const float gc = sG[col];
+        if (isP) {
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int row = 16 * i + 4 * q4 + v;
-          const float dcy = (row >= col) ? fast_exp(gr[v] - gc) : 0.f;
-          if (isP) sP[row * LDT + col] = (bf16)(acc[v] * dcy);
-          else sA[row * LDA + col] = row > col ? br[v] * acc[v] * dcy : 0.f;
+          for (int v = 0; v < 4; ++v) {
+            const int row = 16 * i + 4 * q4 + v;
+            const float dcy = (row >= col) ? fast_exp(gr[v] - gc) : 0.f;
+            sP[row * LDT + col] = (bf16)(acc[v] * dcy);
+          }
+        } else if (j < i) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int row = 16 * i + 4 * q4 + v;
+            sA[row * LDA + col] = br[v] * acc[v] * fast_exp(gr[v] - gc);
+          }
+        } else {
+          // diagonal tile: A and A^T in C layout (k.k^T is symmetric), then T_ii
+          const float bc = sB[col];
+          f32x4 At_, Ad;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int row = 16 * i + 4 * q4 + v;
+            Ad[v] = row > col ? br[v] * acc[v] * fast_exp(gr[v] - gc) : 0.f;
+            At_[v] = col > row ? bc * acc[v] * fast_exp(gc - gr[v]) : 0.f;
+          }
+          const f32x4 Tii = inv_unit_lower16(Ad, At_, q4, l16);
+#pragma unroll
+          for (int v = 0; v < 4; ++v) put_t(sT, sTh, sTl, 16 * i + 4 * q4 + v, col, Tii[v]);
         }
       }
     }
     lds_barrier();
 
-    // ---- phase 2: T = (I + A)^-1 in fp32, also kept as bf16 hi + lo ------------
-    tri_inverse(sA, sT, sTh, sTl, sX, wave, lane);
+    // ---- phase 2: off-diagonal block of T = (I + A)^-1 (fp32, + bf16 hi/lo) ------
+    tri_merge(sA, sT, sTh, sTl, wave, lane);
 
     // ---- phase 3: W = T diag(beta e^G) K (to LDS, negated hi/lo), U = T diag(beta) V
     //      (registers).  The token scales are applied to the B fragments in fp32,
@@ -759,39 +754,32 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
 // ---------------------------------------------------------------------------
 // plan: warm-up start chunk per (segment, head); exact flag per (sequence, head)
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(64) void gdn_plan_kernel(Params p, int N) {
-  const int n = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+__global__ __launch_bounds__(64) void gdn_plan_kernel(Params p) {
+  const int s = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
   const int H = p.H;
-  int any_exact = 0;
-  // find this sequence's segments: the table is sorted by sequence
-  for (int s = 0; s < p.nseg_total; ++s) {
-    const SegInfo si = load_seg(p.seg, s);
-    if (si.n != n) continue;
-    int plan = 0;
-    if (si.seg_idx > 0) {
-      plan = -1;
-      if (p.l2norm) {
-        float acc = 0.f;
-        const int lo = max(0, si.c_start - p.max_warm);
-        for (int c = si.c_start - 1; c >= lo; --c) {
-          const int t = si.bos + c * C + lane;
-          float b = 0.f;
-          if (lane < C && t < si.eos) {
-            const int64_t gi = (int64_t)t * H + h;
-            const float gv = ld_scalar(p.g, gi, p.g_dt);
-            const float bv = ld_scalar(p.beta, gi, p.beta_dt);
-            b = gv + logf(fmaxf(1.f, fabsf(1.f - bv)));
-          }
-          acc += wave_sum(b);
-          if (acc < -p.decay_thresh) { plan = c; break; }
-          if (c == 0) { plan = 0; break; }  // reached the sequence start: exact from h0
+  const SegInfo si = load_seg(p.seg, s);
+  int plan = 0;
+  if (si.seg_idx > 0) {
+    plan = -1;
+    if (p.l2norm) {
+      float acc = 0.f;
+      const int lo = max(0, si.c_start - p.max_warm);
+      for (int c = si.c_start - 1; c >= lo; --c) {
+        const int t = si.bos + c * C + lane;
+        float b = 0.f;
+        if (lane < C && t < si.eos) {
+          const int64_t gi = (int64_t)t * H + h;
+          const float gv = ld_scalar(p.g, gi, p.g_dt);
+          const float bv = ld_scalar(p.beta, gi, p.beta_dt);
+          b = gv + logf(fmaxf(1.f, fabsf(1.f - bv)));
         }
+        acc += wave_sum(b);
+        if (acc < -p.decay_thresh) { plan = c; break; }
+        if (c == 0) { plan = 0; break; }  // reached the sequence start: exact from h0
       }
     }
-    if (plan < 0) any_exact = 1;
-    if (lane == 0) p.plan[s * H + h] = plan;
   }
-  if (lane == 0) p.exact[n * H + h] = any_exact;
+  if (lane == 0) p.plan[s * H + h] = plan;
 }
 
 // ---------------------------------------------------------------------------
@@ -802,13 +790,13 @@ __global__ __launch_bounds__(NTHR) void gdn_seg_combine_kernel(Params p, int N) 
   __shared__ float sS[D * 16];
   const int nh = blockIdx.x, cb = blockIdx.y, tid = threadIdx.x;
   const int H = p.H, n = nh / H, h = nh % H;
-  if (!p.exact[n * H + h]) return;
   int first = -1, nseg = 0;
+  SegInfo si{};
   for (int s = 0; s < p.nseg_total; ++s) {
-    const SegInfo si = load_seg(p.seg, s);
+    si = load_seg(p.seg, s);
     if (si.n == n) { first = si.first_seg; nseg = si.nseg; break; }
   }
-  if (first < 0 || nseg < 2) return;
+  if (first < 0 || nseg < 2 || !seq_exact(p.plan, si, H, h)) return;
   const int row = tid >> 1, c0 = (tid & 1) * 8;
   const int64_t hoff = (int64_t)h * D * D;
   // S_1
@@ -890,15 +878,14 @@ extern "C" int hmx_gdn_chunk_fwd(const void* q, const void* k, const void* v, in
   p.ws_init = multi ? reinterpret_cast<float*>(ws + 2 * st) : nullptr;
   char* tail = ws + (multi ? 3 * st : 0);
   p.plan = reinterpret_cast<int*>(tail);
-  p.exact = reinterpret_cast<int*>(tail + (size_t)nseg_total * H * sizeof(int));
   hipStream_t s = (hipStream_t)stream;
   if (multi) {
-    hipLaunchKernelGGL(gdn_plan_kernel, dim3(N, H), dim3(64), 0, s, p, N);
+    hipLaunchKernelGGL(gdn_plan_kernel, dim3(nseg_total, H), dim3(64), 0, s, p);
     hipLaunchKernelGGL(gdn_chunk_kernel<MODE_S0>, dim3(nseg_total, H), dim3(NTHR), 0, s, p);
     hipLaunchKernelGGL(gdn_chunk_kernel<MODE_PHI>, dim3(nseg_total, H), dim3(NTHR), 0, s, p);
     hipLaunchKernelGGL(gdn_seg_combine_kernel, dim3(N * H, D / 16), dim3(NTHR), 0, s, p, N);
   } else {
-    p.exact = nullptr;  // one segment per sequence: every segment starts from h0
+    p.plan = nullptr;  // one segment per sequence: every segment starts from h0
   }
   hipLaunchKernelGGL(gdn_chunk_kernel<MODE_OUT>, dim3(nseg_total, H), dim3(NTHR), 0, s, p);
   return check_launch("hmx_gdn_chunk_fwd");
@@ -907,6 +894,7 @@ extern "C" int hmx_gdn_chunk_fwd(const void* q, const void* k, const void* v, in
 extern "C" size_t hmx_gdn_chunk_workspace_bytes(int32_t nseg_total, int32_t N, int32_t H) {
   const bool multi = nseg_total > N;
   size_t b = multi ? 3 * (size_t)nseg_total * H * D * D * sizeof(float) : 0;
-  b += (size_t)nseg_total * H * sizeof(int) + (size_t)N * H * sizeof(int);
+  b += (size_t)nseg_total * H * sizeof(int);
+  (void)N;
   return b;
 }
