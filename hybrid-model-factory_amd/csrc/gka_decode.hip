@@ -1,0 +1,249 @@
+// GKA (Gated KalmaNet) decode step: fused h_kk update, Chebyshev ridge solve,
+// alpha blend, h_kv update and readout, in place on slot-indexed state pools.
+//
+// Per sequence n (first token only) and head h
+// (vllm-inference/src/primed_vllm/gka/ops/chebyshev_iteration_gqa.py:79-170):
+//   q, k <- q/|q|, k/|k|;  k~ = (beta+1e-6) k;  v~ = (beta+1e-6) v
+//   H <- e^{gk} H + k~ k~^T                       (stored)
+//   f = |H|_F, lam = r f, tau = 2/(2lam+f), c = (f/(2lam+f)/2)^2
+//   x = tau q, x_prev = 0, w = 2; num_iter x { w <- 1/(1-cw);
+//       x, x_prev <- w x - tau w (H x + lam x - q) - (w-1) x_prev, x }
+//   x <- q + alpha (x - q);  S <- e^{gk} S + k~ v~^T (stored);  o = scale S^T x
+//
+// Mapping: one 256-thread workgroup per (sequence, head); wave w owns state
+// columns [32w, 32w+32) of both H and S, lane l owns 4 columns (l&7) of 16
+// consecutive rows (l>>3), all in registers.  Column sums (H x, S^T x) are a
+// per-lane partial plus a 3-step xor butterfly; the iterate x is exchanged
+// through a double-buffered 128-float LDS vector, one barrier per iteration.
+// Roofline: HBM-bound read-modify-write of two fp32 128x128 states (256 KiB
+// per (sequence, head)) plus num_iter matvecs of 2*128^2 flops.
+#include "common.hpp"
+
+namespace hmx {
+namespace gkad {
+
+constexpr int D = 128;
+
+struct Params {
+  const void* q; const void* k; const void* v;
+  const void* alpha; int alpha_dt;
+  const void* gk; int gk_dt;          // may be null (no decay)
+  const void* beta; int beta_dt;      // may be null
+  void* o;
+  const float* hkk_in; float* hkk_out; int64_t hkk_in_rs, hkk_out_rs;
+  const void* hkv_in; void* hkv_out; int64_t hkv_in_rs, hkv_out_rs;
+  const int32_t* cu_seqlens;
+  const int32_t* idx; int64_t idx_stride;
+  int64_t T;
+  int H, HKV;
+  int num_iter;
+  float ridge_ratio, scale;
+};
+
+__device__ __forceinline__ float ld_scalar(const void* p, int64_t i, int dt) {
+  if (dt == HMX_F32) return static_cast<const float*>(p)[i];
+  if (dt == HMX_BF16) return (float)static_cast<const bf16*>(p)[i];
+  return (float)static_cast<const f16*>(p)[i];
+}
+
+__device__ __forceinline__ float rowgroup_sum(float x) {
+  x += shfl_xor(x, 8);
+  x += shfl_xor(x, 16);
+  x += shfl_xor(x, 32);
+  return x;
+}
+
+template <typename TQ, typename TKV>
+__global__ __launch_bounds__(256) void gka_decode_kernel(Params p) {
+  __shared__ float sx[2][D];
+  __shared__ float sred[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = lane & 7, r = lane >> 3;
+  const int n = blockIdx.x / p.H, h = blockIdx.x - n * p.H;
+  const int hk = h / (p.H / p.HKV);
+  const int col = wave * 32 + c * 4;   // this lane's 4 columns
+  const int row0 = r * 16;             // this lane's 16 rows
+
+  int64_t bos, len;
+  if (p.cu_seqlens) {
+    bos = p.cu_seqlens[n];
+    len = (int64_t)p.cu_seqlens[n + 1] - bos;
+  } else {
+    bos = (int64_t)n * p.T;
+    len = p.T;
+  }
+  if (len <= 0) return;
+  const int64_t slot = p.idx ? (int64_t)p.idx[(int64_t)n * p.idx_stride] : n;
+  if (slot < 0) return;
+
+  // ---- state loads (issued first: they dominate the traffic)
+  float Hs[16][4], Ss[16][4];
+  {
+    const float* hsrc = p.hkk_in + slot * p.hkk_in_rs + (int64_t)h * D * D + row0 * D + col;
+    const TKV* ssrc = static_cast<const TKV*>(p.hkv_in) + slot * p.hkv_in_rs +
+                      (int64_t)h * D * D + row0 * D + col;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      load_vec<4>(hsrc + i * D, Hs[i]);
+      load_vec<4>(ssrc + i * D, Ss[i]);
+    }
+  }
+  // ---- token inputs
+  const TQ* qp = static_cast<const TQ*>(p.q) + (bos * p.H + h) * D;
+  const TQ* kp = static_cast<const TQ*>(p.k) + (bos * p.HKV + hk) * D;
+  const TQ* vp = static_cast<const TQ*>(p.v) + (bos * p.HKV + hk) * D;
+  float kr[16], qr[16], kc[4], qc[4], vc[4];
+  load_vec<16>(kp + row0, kr);
+  load_vec<16>(qp + row0, qr);
+  load_vec<4>(kp + col, kc);
+  load_vec<4>(qp + col, qc);
+  load_vec<4>(vp + col, vc);
+  const int64_t si = bos * p.H + h;
+  const float alpha = ld_scalar(p.alpha, si, p.alpha_dt);
+  const float egk = p.gk ? expf(ld_scalar(p.gk, si, p.gk_dt)) : 1.0f;
+  const float bscale = p.beta ? ld_scalar(p.beta, si, p.beta_dt) + 1e-6f : 1.0f;
+
+  float sk = 0.f, sq = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) { sk += kr[i] * kr[i]; sq += qr[i] * qr[i]; }
+  sk = rowgroup_sum(sk);
+  sq = rowgroup_sum(sq);
+  const float ik = bscale / sqrtf(sk), iq = 1.0f / sqrtf(sq);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) { kr[i] *= ik; qr[i] *= iq; }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) { kc[j] *= ik; qc[j] *= iq; vc[j] *= bscale; }
+
+  // ---- H <- e^{gk} H + k~ k~^T, stored; |H|_F^2
+  float fro2 = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      Hs[i][j] = Hs[i][j] * egk + kr[i] * kc[j];
+      fro2 += Hs[i][j] * Hs[i][j];
+    }
+  {
+    float* hdst = p.hkk_out + slot * p.hkk_out_rs + (int64_t)h * D * D + row0 * D + col;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) store_vec<4>(hdst + i * D, Hs[i]);
+  }
+  fro2 = wave_sum(fro2);
+  if (lane == 0) sred[wave] = fro2;
+  if (tid < D) sx[0][tid] = 0.f;
+  __syncthreads();
+  const float fro = sqrtf(sred[0] + sred[1] + sred[2] + sred[3]);
+  const float lam = p.ridge_ratio * fro;
+  const float inv_den = 1.0f / (2.0f * lam + fro);
+  const float tau = 2.0f * inv_den;
+  const float cc = (fro * inv_den * 0.5f) * (fro * inv_den * 0.5f);
+
+  // ---- Chebyshev iteration; lanes keep x, x_prev for their 4 columns
+  float xc[4], xp[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) { xc[j] = tau * qc[j]; xp[j] = 0.f; }
+  float xr[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) xr[i] = tau * qr[i];
+  float w = 2.0f;
+  int buf = 0;
+  for (int it = 0; it < p.num_iter; ++it) {
+    w = 1.0f / (1.0f - cc * w);
+    float hx[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) hx[j] += xr[i] * Hs[i][j];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float hxj = rowgroup_sum(hx[j]);
+      const float grad = tau * w * (hxj + lam * xc[j] - qc[j]) + (w - 1.0f) * xp[j];
+      xp[j] = xc[j];
+      xc[j] = w * xc[j] - grad;
+    }
+    buf ^= 1;
+    if (r == 0) *reinterpret_cast<float4*>(&sx[buf][col]) = make_float4(xc[0], xc[1], xc[2], xc[3]);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 16; i += 4) {
+      const float4 t = *reinterpret_cast<const float4*>(&sx[buf][row0 + i]);
+      xr[i] = t.x; xr[i + 1] = t.y; xr[i + 2] = t.z; xr[i + 3] = t.w;
+    }
+  }
+  // ---- alpha blend (rows), S update, readout o = scale S^T x
+#pragma unroll
+  for (int i = 0; i < 16; ++i) xr[i] = (qr[i] + alpha * (xr[i] - qr[i])) * p.scale;
+  float ov[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      Ss[i][j] = Ss[i][j] * egk + kr[i] * vc[j];
+      ov[j] += Ss[i][j] * xr[i];
+    }
+  {
+    TKV* sdst = static_cast<TKV*>(p.hkv_out) + slot * p.hkv_out_rs + (int64_t)h * D * D +
+                row0 * D + col;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) store_vec<4>(sdst + i * D, Ss[i]);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) ov[j] = rowgroup_sum(ov[j]);
+  if (r == 0) store_vec<4>(static_cast<TQ*>(p.o) + (bos * p.H + h) * D + col, ov);
+}
+
+template <typename TQ>
+static int dispatch_kv(const Params& p, int64_t N, int kv_dt, hipStream_t s) {
+  if (kv_dt == HMX_F32)
+    hipLaunchKernelGGL((gka_decode_kernel<TQ, float>), dim3((unsigned)(N * p.H)), dim3(256), 0, s, p);
+  else if (kv_dt == HMX_BF16)
+    hipLaunchKernelGGL((gka_decode_kernel<TQ, bf16>), dim3((unsigned)(N * p.H)), dim3(256), 0, s, p);
+  else
+    return set_error(HMX_EUNSUPPORTED, "hmx_gka_decode_fwd: h_kv dtype %d", kv_dt);
+  return HMX_OK;
+}
+
+}  // namespace gkad
+}  // namespace hmx
+
+extern "C" int hmx_gka_decode_fwd(const void* q, const void* k, const void* v, int32_t qkv_dtype,
+                                  const void* alpha, int32_t alpha_dtype, const void* gk,
+                                  int32_t gk_dtype, const void* beta, int32_t beta_dtype, void* o,
+                                  const float* h_kk_in, int64_t h_kk_in_row_stride,
+                                  float* h_kk_out, int64_t h_kk_out_row_stride,
+                                  const void* h_kv_in, int64_t h_kv_in_row_stride, void* h_kv_out,
+                                  int64_t h_kv_out_row_stride, int32_t h_kv_dtype,
+                                  const int32_t* cu_seqlens, const int32_t* ssm_state_indices,
+                                  int64_t idx_stride, int64_t B, int64_t T, int64_t N, int32_t H,
+                                  int32_t HKV, int32_t D, int32_t V, int32_t num_iter,
+                                  float ridge_ratio, float scale, void* stream) {
+  using namespace hmx;
+  HMX_REQUIRE(D == gkad::D && V == gkad::D, HMX_EUNSUPPORTED,
+              "hmx_gka_decode_fwd: only D == V == 128 is supported (got D=%d V=%d)", D, V);
+  HMX_REQUIRE(H > 0 && HKV > 0 && H % HKV == 0, HMX_EINVAL,
+              "hmx_gka_decode_fwd: H=%d must be a positive multiple of HKV=%d", H, HKV);
+  HMX_REQUIRE(q && k && v && alpha && o && h_kk_in && h_kk_out && h_kv_in && h_kv_out, HMX_EINVAL,
+              "hmx_gka_decode_fwd: null tensor pointer");
+  HMX_REQUIRE(num_iter >= 0, HMX_EINVAL, "hmx_gka_decode_fwd: num_iter=%d", num_iter);
+  HMX_REQUIRE(cu_seqlens || N == B, HMX_EINVAL, "hmx_gka_decode_fwd: N != B without cu_seqlens");
+  if (N == 0) return HMX_OK;
+  gkad::Params p;
+  p.q = q; p.k = k; p.v = v;
+  p.alpha = alpha; p.alpha_dt = alpha_dtype; p.gk = gk; p.gk_dt = gk_dtype;
+  p.beta = beta; p.beta_dt = beta_dtype; p.o = o;
+  p.hkk_in = h_kk_in; p.hkk_out = h_kk_out; p.hkk_in_rs = h_kk_in_row_stride;
+  p.hkk_out_rs = h_kk_out_row_stride;
+  p.hkv_in = h_kv_in; p.hkv_out = h_kv_out; p.hkv_in_rs = h_kv_in_row_stride;
+  p.hkv_out_rs = h_kv_out_row_stride;
+  p.cu_seqlens = cu_seqlens; p.idx = ssm_state_indices; p.idx_stride = idx_stride;
+  p.T = T; p.H = H; p.HKV = HKV; p.num_iter = num_iter; p.ridge_ratio = ridge_ratio;
+  p.scale = scale;
+  hipStream_t s = (hipStream_t)stream;
+  int rc;
+  if (qkv_dtype == HMX_BF16) rc = gkad::dispatch_kv<bf16>(p, N, h_kv_dtype, s);
+  else if (qkv_dtype == HMX_F16) rc = gkad::dispatch_kv<f16>(p, N, h_kv_dtype, s);
+  else if (qkv_dtype == HMX_F32) rc = gkad::dispatch_kv<float>(p, N, h_kv_dtype, s);
+  else rc = set_error(HMX_EUNSUPPORTED, "hmx_gka_decode_fwd: qkv dtype %d", qkv_dtype);
+  if (rc != HMX_OK) return rc;
+  return check_launch("hmx_gka_decode_fwd");
+}

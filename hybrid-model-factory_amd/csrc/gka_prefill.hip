@@ -1,0 +1,784 @@
+// GKA (Gated KalmaNet) chunked prefill: per-token Chebyshev ridge solve against
+// the running key Gram matrix H (h_kk), alpha blend, and beta^2-weighted gated
+// linear attention over the value state S (h_kv); bf16 q/k/v, fp32 states.
+//
+// Semantics (per token t, head h; reference files under
+// vllm-inference/src/primed_vllm/gka/):
+//   q, k <- q/|q|, k/|k| (no eps)                          gka_forward.py:114-159
+//   k~ = (beta+1e-6) k
+//   H_t = e^{Gk_t} H_c + sum_{j<=t} e^{Gk_t-Gk_j} k~_j k~_j^T  chebyshev_prefill_gqa.py:28-106
+//   f_t = |H_t|_F (closed form, :227-235); lam = r f; tau = 2/(2lam+f);
+//   c = (f/(2lam+f)/2)^2; x = tau q; num_iter x { w <- 1/(1-cw);
+//   x, x_prev <- w x - tau w (H_t x + lam x - q) - (w-1) x_prev, x }  :243-263
+//   q <- q + alpha (x - q)                                  gka_forward.py:225
+//   o_t = scale [e^{G_t} q^T S_c + sum_{j<=t} e^{G_t-G_j} (q.k_j)(beta_j+1e-6)^2 v_j]
+//                                                           ops/chunk_o_gqa.py:25-114
+//   S_{c+1} = e^{G_last} S_c + K^T (e^{G_last-G} (beta+1e-6)^2 V)   chunk_simple_gla_gqa.py:33-101
+//   H_{c+1} = e^{Gk_last} H_c + K~^T (e^{Gk_last-Gk} K~)
+//
+// Decomposition.  One 256-thread workgroup per (segment, head) walks 32-token
+// chunks with H and S in MFMA accumulator registers (wave w owns columns
+// [32w, 32w+32) of both).  Both state recurrences are linear with a scalar
+// decay, so a segment's start state is exact from a scalar-decay combine of the
+// other segments' zero-start end states (pass LOCAL + combine), no transition
+// matrices needed.
+//
+// Numerics.  Raw k stays exact in bf16; the L2 normalisation and (beta+1e-6)
+// become fp32 per-token scales folded into fp32 epilogues or into B operands
+// that are then split into bf16 hi + lo.  The Chebyshev iterate and H are used
+// as hi/lo pairs in the solver's products; the GLA output uses bf16 operands.
+//
+// Roofline: MFMA-bound at num_iter >= 8 (2*num_iter*(C*d^2 + 2*C^2*d) flops per
+// chunk-head for the solver) plus the HBM minimum (q,k,v,o bf16 + gates +
+// states).
+#include "common.hpp"
+#include "mfma.hpp"
+
+namespace hmx {
+namespace gkap {
+
+constexpr int C = 32;           // tokens per chunk
+constexpr int MT = C / 16;
+constexpr int D = 128;
+constexpr int NTHR = 256;
+constexpr int LDQ = D + 8;      // bf16 [C][D] row stride (q, k, v, O)
+constexpr int LDX = C + 8;      // bf16 [D][C] row stride (X^T hi/lo, Q^T)
+constexpr int LDZ = C + 8;      // bf16 [C][C] row stride (Z, A2)
+constexpr int LDK = C + 1;      // fp32 [C][C] (scaled k.k Gram)
+constexpr float EPS = 1e-6f;
+
+enum Mode { MODE_OUT = 0, MODE_LOCAL = 1 };
+
+// LDS layout (bytes)
+constexpr int SZ_Q = C * LDQ * 2;   // 8704
+constexpr int SZ_XT = D * LDX * 2;  // 10240
+constexpr int SZ_Z = C * LDZ * 2;   // 2560
+constexpr int OFF_Q = 0;
+constexpr int OFF_K = OFF_Q + SZ_Q;
+constexpr int OFF_V = OFF_K + SZ_Q;
+constexpr int OFF_O = OFF_V + SZ_Q;
+constexpr int OFF_XH = OFF_O + SZ_Q;
+constexpr int OFF_XL = OFF_XH + SZ_XT;
+constexpr int OFF_ZH = OFF_XL + SZ_XT;
+constexpr int OFF_ZL = OFF_ZH + SZ_Z;
+constexpr int OFF_KK = OFF_ZL + SZ_Z;              // fp32 [C][LDK]
+constexpr int OFF_S = OFF_KK + C * LDK * 4;         // fp32 per-token scalars
+constexpr int NSC = 21;                             // scalar arrays of C floats
+constexpr int SMEM = OFF_S + NSC * C * 4;
+static_assert(SMEM <= 80 * 1024, "LDS budget");
+// per-token scalar array indices
+enum { S_G, S_GK, S_EG, S_EGK, S_EDL, S_EDLK, S_BE, S_SK, S_IQ, S_ALPHA, S_KN2, S_QN2,
+       S_U0, S_U1, S_U2, S_U3, S_F0, S_F1, S_TAU, S_LAM, S_CC };
+static_assert(S_CC < NSC, "scalar slots");
+
+struct SegInfo { int n, bos, eos, c_start, c_end, seg_idx, first_seg, nseg; };
+
+struct Params {
+  const bf16* q; const bf16* k; const bf16* v;
+  const void* alpha; int alpha_dt;
+  const void* g; int g_dt;
+  const void* gk; int gk_dt;       // null: no h_kk decay
+  const void* beta; int beta_dt;   // null: no beta
+  bf16* o;
+  const float* hkk0; const float* hkv0;   // [N,H,D,D] or null
+  float* hkk_t; float* hkv_t;             // [N,H,D,D] or null
+  const int* seg; int nseg_total;
+  float* ws_dh; float* ws_ds;             // [nseg][H][D][D] zero-start segment end states
+  float* ws_dec;                          // [nseg][H][2]: sum gk, sum g over the segment
+  float* ws_h0; float* ws_s0;             // [nseg][H][D][D] segment start states
+  int H, HKV, num_iter;
+  float ridge_ratio, scale;
+};
+
+__device__ __forceinline__ float ldsc(const void* p, int64_t i, int dt) {
+  if (dt == HMX_F32) return static_cast<const float*>(p)[i];
+  if (dt == HMX_BF16) return (float)static_cast<const bf16*>(p)[i];
+  return (float)static_cast<const f16*>(p)[i];
+}
+
+__device__ __forceinline__ SegInfo load_seg(const int* seg, int s) {
+  const int* r = seg + s * 8;
+  return SegInfo{r[0], r[1], r[2], r[3], r[4], r[5], r[6], r[7]};
+}
+
+struct Raw {
+  bf16x8 k[MT], v[MT], q[MT];
+  float g, gk, b, a;
+};
+
+template <int MODE>
+__device__ __forceinline__ void load_raw(Raw& r, const Params& p, const bf16* qh, const bf16* kh,
+                                         const bf16* vh, int64_t q_rs, int64_t kv_rs, int tok0,
+                                         int nval, int tid, int h) {
+#pragma unroll
+  for (int pass = 0; pass < MT; ++pass) {
+    const int row = pass * 16 + (tid >> 4), f0 = (tid & 15) * 8;
+    const bool ok = row < nval;
+    const int64_t tok = tok0 + row;
+    r.k[pass] = ok ? *reinterpret_cast<const bf16x8*>(kh + tok * kv_rs + f0) : bf16x8{};
+    r.v[pass] = ok ? *reinterpret_cast<const bf16x8*>(vh + tok * kv_rs + f0) : bf16x8{};
+    if (MODE == MODE_OUT)
+      r.q[pass] = ok ? *reinterpret_cast<const bf16x8*>(qh + tok * q_rs + f0) : bf16x8{};
+  }
+  if (tid < C) {
+    const bool ok = tid < nval;
+    const int64_t i = (int64_t)(tok0 + tid) * p.H + h;
+    r.g = ok ? ldsc(p.g, i, p.g_dt) : 0.f;
+    r.gk = (ok && p.gk) ? ldsc(p.gk, i, p.gk_dt) : 0.f;
+    r.b = (ok && p.beta) ? ldsc(p.beta, i, p.beta_dt) : 0.f;
+    r.a = (ok && MODE == MODE_OUT) ? ldsc(p.alpha, i, p.alpha_dt) : 0.f;
+  }
+}
+
+// Sum of squares of a staged 8-feature slice over its 16-lane row.
+__device__ __forceinline__ float row_sumsq(const bf16x8& x) {
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) s += (float)x[j] * (float)x[j];
+  return row16_sum(s);
+}
+
+// Writes a C-layout 16x16 register tile transposed (M^T[col][row]) as bf16 hi/lo,
+// 4 consecutive rows per lane -> one 8-byte store each.
+__device__ __forceinline__ void put_t_hilo(bf16* th, bf16* tl, int ld, int r0, int c0,
+                                           const f32x4& x, int q4, int l16) {
+  bf16x4 hi, lo;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    hi[v] = (bf16)x[v];
+    lo[v] = (bf16)(x[v] - (float)hi[v]);
+  }
+  const int a = (c0 + l16) * ld + r0 + 4 * q4;
+  *reinterpret_cast<bf16x4*>(th + a) = hi;
+  if (tl) *reinterpret_cast<bf16x4*>(tl + a) = lo;
+}
+
+template <int MODE>
+__global__ __launch_bounds__(NTHR, 1) void gka_chunk_kernel(Params p) {
+  __shared__ __align__(16) unsigned char smem[SMEM];
+  bf16* sQ = reinterpret_cast<bf16*>(smem + OFF_Q);
+  bf16* sK = reinterpret_cast<bf16*>(smem + OFF_K);
+  bf16* sV = reinterpret_cast<bf16*>(smem + OFF_V);
+  bf16* sO = reinterpret_cast<bf16*>(smem + OFF_O);
+  bf16* sXh = reinterpret_cast<bf16*>(smem + OFF_XH);
+  bf16* sXl = reinterpret_cast<bf16*>(smem + OFF_XL);
+  bf16* sZh = reinterpret_cast<bf16*>(smem + OFF_ZH);
+  bf16* sZl = reinterpret_cast<bf16*>(smem + OFF_ZL);
+  float* sKK = reinterpret_cast<float*>(smem + OFF_KK);
+  float* sc = reinterpret_cast<float*>(smem + OFF_S);
+  auto SC = [&](int slot, int t) -> float& { return sc[slot * C + t]; };
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int q4 = lane >> 4, l16 = lane & 15;
+  const int s_id = blockIdx.x, h = blockIdx.y;
+  const SegInfo si = load_seg(p.seg, s_id);
+  const int H = p.H, hk = h / (H / p.HKV);
+  const bool solve = (MODE == MODE_OUT) && p.num_iter > 0;
+  const bool track_h = p.num_iter > 0;
+
+  if (MODE == MODE_LOCAL && si.seg_idx == si.nseg - 1) return;
+
+  // ---- initial states ----------------------------------------------------
+  f32x4 Hs[8][2], Ss[8][2];
+  {
+    const float *hsrc = nullptr, *ssrc = nullptr;
+    if (MODE == MODE_OUT) {
+      if (si.seg_idx == 0) {
+        if (p.hkk0) hsrc = p.hkk0 + ((int64_t)si.n * H + h) * D * D;
+        if (p.hkv0) ssrc = p.hkv0 + ((int64_t)si.n * H + h) * D * D;
+      } else {
+        hsrc = p.ws_h0 + ((int64_t)s_id * H + h) * D * D;
+        ssrc = p.ws_s0 + ((int64_t)s_id * H + h) * D * D;
+      }
+    }
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int off = (16 * rt + 4 * q4 + v) * D + 32 * wave + 16 * ct + l16;
+          Hs[rt][ct][v] = (hsrc && track_h) ? hsrc[off] : 0.f;
+          Ss[rt][ct][v] = ssrc ? ssrc[off] : 0.f;
+        }
+  }
+
+  const int64_t q_rs = (int64_t)H * D, kv_rs = (int64_t)p.HKV * D;
+  const bf16* qh = p.q + (int64_t)h * D;
+  const bf16* kh = p.k + (int64_t)hk * D;
+  const bf16* vh = p.v + (int64_t)hk * D;
+  float seg_gk = 0.f, seg_g = 0.f;
+
+  Raw raw;
+  if (si.c_start < si.c_end)
+    load_raw<MODE>(raw, p, qh, kh, vh, q_rs, kv_rs, si.bos + si.c_start * C,
+                   min(C, si.eos - (si.bos + si.c_start * C)), tid, h);
+
+  for (int c = si.c_start; c < si.c_end; ++c) {
+    const int tok0 = si.bos + c * C;
+    const int nval = min(C, si.eos - tok0);
+
+    // ---- P0: stage raw rows, row norms, per-token gates ---------------------
+#pragma unroll
+    for (int pass = 0; pass < MT; ++pass) {
+      const int row = pass * 16 + (tid >> 4), f0 = (tid & 15) * 8;
+      *reinterpret_cast<bf16x8*>(sK + row * LDQ + f0) = raw.k[pass];
+      *reinterpret_cast<bf16x8*>(sV + row * LDQ + f0) = raw.v[pass];
+      const float kn2 = row_sumsq(raw.k[pass]);
+      if ((tid & 15) == 0) SC(S_KN2, row) = kn2;
+      if (MODE == MODE_OUT) {
+        *reinterpret_cast<bf16x8*>(sQ + row * LDQ + f0) = raw.q[pass];
+        const float qn2 = row_sumsq(raw.q[pass]);
+        if ((tid & 15) == 0) SC(S_QN2, row) = qn2;
+      }
+    }
+    if (wave == 0) {
+      const bool ok = lane < C;
+      const float G = scan32(ok ? raw.g : 0.f);
+      const float Gk = scan32(ok ? raw.gk : 0.f);
+      const float GL = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, G), C - 1));
+      const float GkL = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, Gk), C - 1));
+      if (ok) {
+        SC(S_G, lane) = G;
+        SC(S_GK, lane) = Gk;
+        SC(S_EG, lane) = fast_exp(G);
+        SC(S_EGK, lane) = fast_exp(Gk);
+        SC(S_EDL, lane) = fast_exp(GL - G);
+        SC(S_EDLK, lane) = fast_exp(GkL - Gk);
+        SC(S_BE, lane) = p.beta ? raw.b + EPS : 1.0f;
+        SC(S_ALPHA, lane) = raw.a;
+      }
+      seg_g += GL;
+      seg_gk += GkL;
+    }
+    if (c + 1 < si.c_end) {
+      const int t1 = tok0 + C;
+      load_raw<MODE>(raw, p, qh, kh, vh, q_rs, kv_rs, t1, min(C, si.eos - t1), tid, h);
+    }
+    lds_barrier();
+    // per-token scales: s_t = (beta_t+eps)/|k_t| (k~ = s k), iq_t = 1/|q_t|
+    if (tid < C) {
+      const float kn2 = SC(S_KN2, tid);
+      SC(S_SK, tid) = tid < nval ? SC(S_BE, tid) / sqrtf(kn2) : 0.f;
+      if (MODE == MODE_OUT) SC(S_IQ, tid) = tid < nval ? 1.0f / sqrtf(SC(S_QN2, tid)) : 0.f;
+    }
+
+    lds_barrier();
+    // q^ for this wave's columns (C layout), fp32
+    f32x4 qv[MT][2];
+    if (MODE == MODE_OUT) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int t = 16 * mt + 4 * q4 + v;
+            qv[mt][ct][v] = (float)sQ[t * LDQ + 32 * wave + 16 * ct + l16] * SC(S_IQ, t);
+          }
+    }
+
+    // ---- P1: the Chebyshev solve (OUT, num_iter > 0) -------------------------
+    f32x4 xq[MT][2];  // the query fed to the GLA (solved + alpha-blended, or q^)
+    if (MODE == MODE_OUT) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) xq[mt][ct] = qv[mt][ct];
+    }
+    if (solve) {
+      // P1a: u_j = k~_j H_c k~_j^T (per-wave partials), |H_c|^2, scaled Gram k~.k~
+      {
+        float u[MT][4];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) u[mt][v] = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          bf16x8 Hh[2], Hl[2];
+#pragma unroll
+          for (int ct = 0; ct < 2; ++ct) pack_b_hilo(Hs[2 * ks][ct], Hs[2 * ks + 1][ct], Hh[ct], Hl[ct]);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const bf16x8 a = frag_perm(sK, LDQ, 16 * mt, 32 * ks, lane);
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) {
+              f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+              acc = mfma16(a, Hh[ct], acc);
+              acc = mfma16(a, Hl[ct], acc);
+#pragma unroll
+              for (int v = 0; v < 4; ++v)
+                u[mt][v] += acc[v] *
+                            (float)sK[(16 * mt + 4 * q4 + v) * LDQ + 32 * wave + 16 * ct + l16];
+            }
+          }
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const float s = row16_sum(u[mt][v]);
+            if (l16 == 0) SC(S_U0 + wave, 16 * mt + 4 * q4 + v) = s;
+          }
+        float hn = 0.f;
+#pragma unroll
+        for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+          for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) hn += Hs[rt][ct][v] * Hs[rt][ct][v];
+        hn = wave_sum(hn);
+        if (lane == 0) SC(S_F0 + 0, C - 1 - wave) = hn;  // |H_c|^2 partials in the F0 tail
+        // Gram tiles (0,0), (1,0), (1,1) on waves 0..2: sKK[t][j] = s_t s_j k_t.k_j
+        if (wave < 3) {
+          const int a = (wave == 0) ? 0 : 1, b = (wave == 2) ? 1 : 0;
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks)
+            acc = mfma16(frag(sK, LDQ, 16 * a, 32 * ks, lane), frag(sK, LDQ, 16 * b, 32 * ks, lane), acc);
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int t = 16 * a + 4 * q4 + v, j = 16 * b + l16;
+            sKK[t * LDK + j] = acc[v] * SC(S_SK, t) * SC(S_SK, j);
+          }
+        }
+      }
+      lds_barrier();
+      // P1b: in-chunk part of |H_t|_F^2 = sum_l M_tl (M . KK^2)_tl, M_tj = e^{Gk_t-Gk_j} (t>=j)
+      float hc2 = SC(S_F0, C - 1) + SC(S_F0, C - 2) + SC(S_F0, C - 3) + SC(S_F0, C - 4);
+      lds_barrier();
+      if (wave < 3) {
+        const int a = (wave == 0) ? 0 : 1, b = (wave == 2) ? 1 : 0;
+        f32x4 R = {0.f, 0.f, 0.f, 0.f};
+        // R_tl = sum_j M_tj KK_jl^2 over j <= t (KK symmetric; only j >= l contributes via M? no:
+        // every j <= t contributes); k in natural order j = 4s + q (two 16-blocks)
+        for (int jb = 0; jb <= a; ++jb) {
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            const int t = 16 * a + l16, j = 16 * jb + 4 * s + q4, l = 16 * b + l16;
+            const float m = (t >= j) ? fast_exp(SC(S_GK, t) - SC(S_GK, j)) : 0.f;
+            const float kk = (j >= l) ? sKK[j * LDK + l] : sKK[l * LDK + j];
+            R = mfma16f(m, kk * kk, R);
+          }
+        }
+        float fp[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int t = 16 * a + 4 * q4 + v, l = 16 * b + l16;
+          const float m = (t >= l) ? fast_exp(SC(S_GK, t) - SC(S_GK, l)) : 0.f;
+          fp[v] = row16_sum(R[v] * m);
+        }
+        if (l16 == 0) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) SC(b == 0 ? S_F0 : S_F1, 16 * a + 4 * q4 + v) = fp[v];
+        }
+        if (a == 0 && l16 == 0) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) SC(S_F1, 4 * q4 + v) = 0.f;  // tile (0,1) is empty
+        }
+      }
+      lds_barrier();
+      // P1c: per-token f, lam, tau, c
+      if (tid < C) {
+        const int t = tid;
+        float cross = 0.f;
+        for (int j = 0; j <= t; ++j) {
+          const float uj = (SC(S_U0, j) + SC(S_U1, j) + SC(S_U2, j) + SC(S_U3, j)) *
+                           SC(S_SK, j) * SC(S_SK, j);
+          cross += fast_exp(SC(S_GK, t) - SC(S_GK, j)) * uj;
+        }
+        const float egk = SC(S_EGK, t);
+        const float f2 = egk * egk * hc2 + 2.f * egk * cross + SC(S_F0, t) + SC(S_F1, t);
+        const float f = sqrtf(f2);
+        const float lam = p.ridge_ratio * f;
+        const float inv = 1.0f / (2.f * lam + f);
+        SC(S_TAU, t) = 2.f * inv;
+        SC(S_LAM, t) = lam;
+        const float cc = f * inv * 0.5f;
+        SC(S_CC, t) = cc * cc;
+      }
+      lds_barrier();
+
+      // P1d: the iteration.  Each wave owns X[:, 32w..32w+32) in registers.
+      float tau[MT][4], lam[MT][4], ccv[MT][4], om[MT][4];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int t = 16 * mt + 4 * q4 + v;
+          tau[mt][v] = SC(S_TAU, t);
+          lam[mt][v] = SC(S_LAM, t);
+          ccv[mt][v] = SC(S_CC, t);
+          om[mt][v] = 2.0f;
+        }
+      f32x4 X[MT][2], Xp[MT][2];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            X[mt][ct][v] = tau[mt][v] * qv[mt][ct][v];
+            Xp[mt][ct][v] = 0.f;
+          }
+        }
+      for (int it = 0; it < p.num_iter; ++it) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int ct = 0; ct < 2; ++ct)
+            put_t_hilo(sXh, sXl, LDX, 16 * mt, 32 * wave + 16 * ct, X[mt][ct], q4, l16);
+        lds_barrier();
+        // Z~_tj = M_tj s_j^2 (x_t . k_j) for j <= t on waves 0..2
+        if (wave < 3) {
+          const int a = (wave == 0) ? 0 : 1, b = (wave == 2) ? 1 : 0;
+          f32x4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks) {
+            const bf16x8 bk = frag(sK, LDQ, 16 * b, 32 * ks, lane);
+            z = mfma16(frag_t(sXh, LDX, 32 * ks, 16 * a, lane), bk, z);
+            z = mfma16(frag_t(sXl, LDX, 32 * ks, 16 * a, lane), bk, z);
+          }
+          f32x4 zs;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int t = 16 * a + 4 * q4 + v, j = 16 * b + l16;
+            const float s = SC(S_SK, j);
+            zs[v] = (t >= j) ? z[v] * s * s * fast_exp(SC(S_GK, t) - SC(S_GK, j)) : 0.f;
+          }
+          // store Z~ row-major (t, j): 2-byte writes
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int t = 16 * a + 4 * q4 + v, j = 16 * b + l16;
+            const bf16 hi = (bf16)zs[v];
+            sZh[t * LDZ + j] = hi;
+            sZl[t * LDZ + j] = (bf16)(zs[v] - (float)hi);
+          }
+        } else {
+          // wave 3 zeroes the empty upper tile (0,1)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            sZh[(4 * q4 + v) * LDZ + 16 + l16] = (bf16)0.f;
+            sZl[(4 * q4 + v) * LDZ + 16 + l16] = (bf16)0.f;
+          }
+        }
+        // Y = e^{Gk} (X H_c) for this wave's columns (X, H as hi/lo)
+        f32x4 Y[MT][2];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int ct = 0; ct < 2; ++ct) Y[mt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          bf16x8 Hh[2], Hl[2];
+#pragma unroll
+          for (int ct = 0; ct < 2; ++ct) pack_b_hilo(Hs[2 * ks][ct], Hs[2 * ks + 1][ct], Hh[ct], Hl[ct]);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const bf16x8 ah = frag_t_perm(sXh, LDX, 32 * ks, 16 * mt, lane);
+            const bf16x8 al = frag_t_perm(sXl, LDX, 32 * ks, 16 * mt, lane);
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) {
+              Y[mt][ct] = mfma16(ah, Hh[ct], Y[mt][ct]);
+              Y[mt][ct] = mfma16(ah, Hl[ct], Y[mt][ct]);
+              Y[mt][ct] = mfma16(al, Hh[ct], Y[mt][ct]);
+            }
+          }
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const float e = SC(S_EGK, 16 * mt + 4 * q4 + v);
+            Y[mt][0][v] *= e;
+            Y[mt][1][v] *= e;
+          }
+        lds_barrier();
+        // Y += Z~ K (Z~ hi/lo, raw K exact)
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+          const bf16x8 bk = frag_t(sK, LDQ, 0, 32 * wave + 16 * ct, lane);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            Y[mt][ct] = mfma16(frag(sZh, LDZ, 16 * mt, 0, lane), bk, Y[mt][ct]);
+            Y[mt][ct] = mfma16(frag(sZl, LDZ, 16 * mt, 0, lane), bk, Y[mt][ct]);
+          }
+        }
+        // Chebyshev update
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const float w = 1.0f / (1.0f - ccv[mt][v] * om[mt][v]);
+            om[mt][v] = w;
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) {
+              const float x = X[mt][ct][v];
+              const float grad = tau[mt][v] * w * (Y[mt][ct][v] + lam[mt][v] * x - qv[mt][ct][v]) +
+                                 (w - 1.0f) * Xp[mt][ct][v];
+              Xp[mt][ct][v] = x;
+              X[mt][ct][v] = w * x - grad;
+            }
+          }
+      }
+      // alpha blend
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float al = SC(S_ALPHA, 16 * mt + 4 * q4 + v);
+#pragma unroll
+          for (int ct = 0; ct < 2; ++ct)
+            xq[mt][ct][v] = qv[mt][ct][v] + al * (X[mt][ct][v] - qv[mt][ct][v]);
+        }
+    }
+
+    // ---- P2: GLA output (OUT) ------------------------------------------------
+    if (MODE == MODE_OUT) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
+          put_t_hilo(sXh, sXl, LDX, 16 * mt, 32 * wave + 16 * ct, xq[mt][ct], q4, l16);
+      lds_barrier();
+      // A2_tj = e^{G_t-G_j} (xq_t . k_j) s_j (beta_j+eps)  (j <= t), waves 0..2
+      if (wave < 3) {
+        const int a = (wave == 0) ? 0 : 1, b = (wave == 2) ? 1 : 0;
+        f32x4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          const bf16x8 bk = frag(sK, LDQ, 16 * b, 32 * ks, lane);
+          z = mfma16(frag_t(sXh, LDX, 32 * ks, 16 * a, lane), bk, z);
+          z = mfma16(frag_t(sXl, LDX, 32 * ks, 16 * a, lane), bk, z);
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int t = 16 * a + 4 * q4 + v, j = 16 * b + l16;
+          const float w = (t >= j) ? fast_exp(SC(S_G, t) - SC(S_G, j)) * SC(S_SK, j) * SC(S_BE, j) : 0.f;
+          sZh[t * LDZ + j] = (bf16)(z[v] * w);
+        }
+      } else {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) sZh[(4 * q4 + v) * LDZ + 16 + l16] = (bf16)0.f;
+      }
+      f32x4 O[MT][2];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) O[mt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        // The solved query is large off the key span, so both operands carry a
+        // bf16 remainder: a single bf16 rounding of either costs ~3% of |o|.
+        bf16x8 Sh[2], Sl[2];
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) pack_b_hilo(Ss[2 * ks][ct], Ss[2 * ks + 1][ct], Sh[ct], Sl[ct]);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const bf16x8 ah = frag_t_perm(sXh, LDX, 32 * ks, 16 * mt, lane);
+          const bf16x8 al = frag_t_perm(sXl, LDX, 32 * ks, 16 * mt, lane);
+#pragma unroll
+          for (int ct = 0; ct < 2; ++ct) {
+            O[mt][ct] = mfma16(ah, Sh[ct], O[mt][ct]);
+            O[mt][ct] = mfma16(al, Sh[ct], O[mt][ct]);
+            O[mt][ct] = mfma16(ah, Sl[ct], O[mt][ct]);
+          }
+        }
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float e = SC(S_EG, 16 * mt + 4 * q4 + v);
+          O[mt][0][v] *= e;
+          O[mt][1][v] *= e;
+        }
+      lds_barrier();
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        const bf16x8 bv = frag_t(sV, LDQ, 0, 32 * wave + 16 * ct, lane);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) O[mt][ct] = mfma16(frag(sZh, LDZ, 16 * mt, 0, lane), bv, O[mt][ct]);
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            sO[(16 * mt + 4 * q4 + v) * LDQ + 32 * wave + 16 * ct + l16] = (bf16)(O[mt][ct][v] * p.scale);
+    }
+
+    // ---- P3: state updates (hi/lo B operands) ---------------------------------
+    {
+      const float egl = SC(S_EG, C - 1), egkl = SC(S_EGK, C - 1);
+#pragma unroll
+      for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            Ss[rt][ct][v] *= egl;
+            if (track_h) Hs[rt][ct][v] *= egkl;
+          }
+      float fs[8], fh[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int t = 8 * q4 + j;
+        const float s = SC(S_SK, t);
+        fs[j] = s * SC(S_BE, t) * SC(S_EDL, t);
+        fh[j] = s * s * SC(S_EDLK, t);
+      }
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        const bf16x8 vr = frag_t(sV, LDQ, 0, 32 * wave + 16 * ct, lane);
+        const bf16x8 kr = frag_t(sK, LDQ, 0, 32 * wave + 16 * ct, lane);
+        bf16x8 vh, vl, kh_, kl_;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float x = (float)vr[j] * fs[j];
+          vh[j] = (bf16)x;
+          vl[j] = (bf16)(x - (float)vh[j]);
+          const float y = (float)kr[j] * fh[j];
+          kh_[j] = (bf16)y;
+          kl_[j] = (bf16)(y - (float)kh_[j]);
+        }
+#pragma unroll
+        for (int rt = 0; rt < 8; ++rt) {
+          const bf16x8 a = frag_t(sK, LDQ, 0, 16 * rt, lane);
+          Ss[rt][ct] = mfma16(a, vh, Ss[rt][ct]);
+          Ss[rt][ct] = mfma16(a, vl, Ss[rt][ct]);
+          if (track_h) {
+            Hs[rt][ct] = mfma16(a, kh_, Hs[rt][ct]);
+            Hs[rt][ct] = mfma16(a, kl_, Hs[rt][ct]);
+          }
+        }
+      }
+    }
+    lds_barrier();
+
+    // ---- store O -------------------------------------------------------------
+    if (MODE == MODE_OUT) {
+      bf16* oh = p.o + (int64_t)h * D;
+#pragma unroll
+      for (int pass = 0; pass < MT; ++pass) {
+        const int row = pass * 16 + (tid >> 4), f0 = (tid & 15) * 8;
+        if (row < nval)
+          *reinterpret_cast<bf16x8*>(oh + (int64_t)(tok0 + row) * q_rs + f0) =
+              *reinterpret_cast<const bf16x8*>(sO + row * LDQ + f0);
+      }
+    }
+  }
+
+  // ---- end states ----------------------------------------------------------
+  float *hd = nullptr, *sd = nullptr;
+  if (MODE == MODE_OUT) {
+    if (si.seg_idx == si.nseg - 1) {
+      if (p.hkk_t && track_h) hd = p.hkk_t + ((int64_t)si.n * H + h) * D * D;
+      if (p.hkv_t) sd = p.hkv_t + ((int64_t)si.n * H + h) * D * D;
+    }
+  } else {
+    hd = track_h ? p.ws_dh + ((int64_t)s_id * H + h) * D * D : nullptr;
+    sd = p.ws_ds + ((int64_t)s_id * H + h) * D * D;
+    if (tid == 0) {
+      p.ws_dec[((int64_t)s_id * H + h) * 2 + 0] = seg_gk;
+      p.ws_dec[((int64_t)s_id * H + h) * 2 + 1] = seg_g;
+    }
+  }
+#pragma unroll
+  for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int off = (16 * rt + 4 * q4 + v) * D + 32 * wave + 16 * ct + l16;
+        if (hd) hd[off] = Hs[rt][ct][v];
+        if (sd) sd[off] = Ss[rt][ct][v];
+      }
+}
+
+// Segment start states: X_0 = initial, X_{s+1} = e^{D_s} X_s + dX_s (elementwise).
+__global__ __launch_bounds__(256) void gka_seg_combine_kernel(Params p) {
+  const int nh = blockIdx.x, H = p.H;
+  const int n = nh / H, h = nh % H;
+  int first = -1, nseg = 0;
+  for (int s = 0; s < p.nseg_total; ++s) {
+    const SegInfo si = load_seg(p.seg, s);
+    if (si.n == n) { first = si.first_seg; nseg = si.nseg; break; }
+  }
+  if (first < 0 || nseg < 2) return;
+  const bool track_h = p.num_iter > 0;
+  for (int e = blockIdx.y * 256 + threadIdx.x; e < D * D; e += gridDim.y * 256) {
+    float hx = (track_h && p.hkk0) ? p.hkk0[((int64_t)n * H + h) * D * D + e] : 0.f;
+    float sx = p.hkv0 ? p.hkv0[((int64_t)n * H + h) * D * D + e] : 0.f;
+    for (int s = 0; s < nseg - 1; ++s) {
+      const int64_t b = ((int64_t)(first + s) * H + h);
+      const float dk = expf(p.ws_dec[b * 2 + 0]), dg = expf(p.ws_dec[b * 2 + 1]);
+      if (track_h) hx = hx * dk + p.ws_dh[b * D * D + e];
+      sx = sx * dg + p.ws_ds[b * D * D + e];
+      const int64_t nb = ((int64_t)(first + s + 1) * H + h) * D * D + e;
+      if (track_h) p.ws_h0[nb] = hx;
+      p.ws_s0[nb] = sx;
+    }
+  }
+}
+
+}  // namespace gkap
+}  // namespace hmx
+
+using namespace hmx;
+using namespace hmx::gkap;
+
+extern "C" size_t hmx_gka_chunk_workspace_bytes(int32_t nseg_total, int32_t N, int32_t H) {
+  if (nseg_total <= N) return 16;
+  const size_t st = (size_t)nseg_total * H * D * D * sizeof(float);
+  return 4 * st + (size_t)nseg_total * H * 2 * sizeof(float);
+}
+
+extern "C" int hmx_gka_chunk_fwd(const void* q, const void* k, const void* v, int32_t qkv_dtype,
+                                 const void* alpha, int32_t alpha_dtype, const void* g,
+                                 int32_t g_dtype, const void* gk, int32_t gk_dtype,
+                                 const void* beta, int32_t beta_dtype, void* o,
+                                 const float* h_kk0, const float* h_kv0, float* h_kk_final,
+                                 float* h_kv_final, const int32_t* seg_table, int32_t nseg_total,
+                                 int32_t N, int32_t H, int32_t HKV, int32_t D_, int32_t V,
+                                 int32_t num_iter, float ridge_ratio, float scale,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  HMX_REQUIRE(qkv_dtype == HMX_BF16, HMX_EUNSUPPORTED,
+              "hmx_gka_chunk_fwd: q/k/v must be bfloat16 (got dtype code %d)", qkv_dtype);
+  HMX_REQUIRE(D_ == D && V == D, HMX_EUNSUPPORTED,
+              "hmx_gka_chunk_fwd: only D == V == 128 is supported (got D=%d V=%d)", D_, V);
+  HMX_REQUIRE(H > 0 && HKV > 0 && H % HKV == 0, HMX_EINVAL, "hmx_gka_chunk_fwd: H/HKV");
+  HMX_REQUIRE(q && k && v && alpha && g && o && seg_table, HMX_EINVAL,
+              "hmx_gka_chunk_fwd: null tensor pointer");
+  HMX_REQUIRE(num_iter >= 0, HMX_EINVAL, "hmx_gka_chunk_fwd: num_iter=%d", num_iter);
+  if (nseg_total == 0) return HMX_OK;
+  const size_t need = hmx_gka_chunk_workspace_bytes(nseg_total, N, H);
+  HMX_REQUIRE(workspace && workspace_bytes >= need, HMX_EINVAL,
+              "hmx_gka_chunk_fwd: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  Params p;
+  p.q = static_cast<const bf16*>(q); p.k = static_cast<const bf16*>(k);
+  p.v = static_cast<const bf16*>(v);
+  p.alpha = alpha; p.alpha_dt = alpha_dtype; p.g = g; p.g_dt = g_dtype;
+  p.gk = gk; p.gk_dt = gk_dtype; p.beta = beta; p.beta_dt = beta_dtype;
+  p.o = static_cast<bf16*>(o);
+  p.hkk0 = h_kk0; p.hkv0 = h_kv0; p.hkk_t = h_kk_final; p.hkv_t = h_kv_final;
+  p.seg = seg_table; p.nseg_total = nseg_total;
+  p.H = H; p.HKV = HKV; p.num_iter = num_iter; p.ridge_ratio = ridge_ratio; p.scale = scale;
+  const bool multi = nseg_total > N;
+  const size_t st = (size_t)nseg_total * H * D * D;
+  float* ws = static_cast<float*>(workspace);
+  p.ws_dh = multi ? ws : nullptr;
+  p.ws_ds = multi ? ws + st : nullptr;
+  p.ws_h0 = multi ? ws + 2 * st : nullptr;
+  p.ws_s0 = multi ? ws + 3 * st : nullptr;
+  p.ws_dec = multi ? ws + 4 * st : nullptr;
+  hipStream_t s = (hipStream_t)stream;
+  if (multi) {
+    hipLaunchKernelGGL(gka_chunk_kernel<MODE_LOCAL>, dim3(nseg_total, H), dim3(NTHR), 0, s, p);
+    hipLaunchKernelGGL(gka_seg_combine_kernel, dim3(N * H, 16), dim3(256), 0, s, p);
+  }
+  hipLaunchKernelGGL(gka_chunk_kernel<MODE_OUT>, dim3(nseg_total, H), dim3(NTHR), 0, s, p);
+  return check_launch("hmx_gka_chunk_fwd");
+}

@@ -1,0 +1,130 @@
+// MFMA fragment, LDS and lane-permute helpers shared by the chunked kernels
+// (gfx950: v_mfma_f32_16x16x32_bf16, v_mfma_f32_16x16x4_f32, ds_read_b64_tr_b16).
+//
+// Operand conventions for the 16x16 MFMAs (lane l, q = l>>4, l16 = l&15):
+//   A: row l16, 8 (bf16) or 1 (f32) k values of lane group q
+//   B: column l16, the same k values
+//   C/D: rows 4q+v (v = 0..3), column l16
+// Only the A/B k assignment has to agree between the two operands, which lets a
+// C-layout register tile serve directly as a B operand (see frag_perm/pack_b).
+#pragma once
+#include "common.hpp"
+
+namespace hmx {
+
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x4 mfma16f(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// A (or B^T) fragment in natural k order: lane holds row r0+(l&15), k0+8(l>>4)..+7.
+__device__ __forceinline__ bf16x8 frag(const bf16* base, int ld, int r0, int k0, int lane) {
+  return *reinterpret_cast<const bf16x8*>(base + (r0 + (lane & 15)) * ld + k0 + 8 * (lane >> 4));
+}
+
+// A fragment whose k order matches a B operand built from two C-layout tiles:
+// lane holds row r0+(l&15), k = k0+4q+{0..3} and k0+16+4q+{0..3}, q = l>>4.
+__device__ __forceinline__ bf16x8 frag_perm(const bf16* base, int ld, int r0, int k0, int lane) {
+  const bf16* p = base + (r0 + (lane & 15)) * ld + k0 + 4 * (lane >> 4);
+  const bf16x4 a = *reinterpret_cast<const bf16x4*>(p);
+  const bf16x4 b = *reinterpret_cast<const bf16x4*>(p + 16);
+  return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// Transposing LDS read (gfx950 ds_read_b64_tr_b16) of a row-major bf16 matrix
+// M[row][col]: within each 16-lane group, lane i receives M[t0+j][c0+i] for
+// j = 0..3 (4 consecutive rows of one column), where the group reads rows
+// t0..t0+3 and columns c0..c0+15.  Each source lane s supplies the address of
+// M[t0 + s/4][c0 + 4(s%4)].
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ bf16x4 ld_tr(const bf16* base, int ld, int t0, int c0, int lane) {
+  const int s = lane & 15;
+  const bf16* a = base + (t0 + (s >> 2)) * ld + c0 + 4 * (s & 3);
+  const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(a));
+  return __builtin_bit_cast(bf16x4, r);
+}
+
+// B fragment of M[k=row][n=col] in natural k order (k = t0 + 8q + 0..7) from a
+// row-major bf16 matrix: column c0 + (l&15).
+__device__ __forceinline__ bf16x8 frag_t(const bf16* base, int ld, int t0, int c0, int lane) {
+  const int tq = t0 + 8 * (lane >> 4);
+  const bf16x4 a = ld_tr(base, ld, tq, c0, lane);
+  const bf16x4 b = ld_tr(base, ld, tq + 4, c0, lane);
+  return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// A fragment of M^T (rows = columns of M, k = rows of M) in the permuted k
+// order of frag_perm: k = t0+4q+{0..3} and t0+16+4q+{0..3}.
+__device__ __forceinline__ bf16x8 frag_t_perm(const bf16* base, int ld, int t0, int c0, int lane) {
+  const int tq = t0 + 4 * (lane >> 4);
+  const bf16x4 a = ld_tr(base, ld, tq, c0, lane);
+  const bf16x4 b = ld_tr(base, ld, tq + 16, c0, lane);
+  return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// B fragment from two vertically stacked C-layout 16x16 tiles (rows 0-15 in t0,
+// rows 16-31 in t1); pairs with frag_perm.
+__device__ __forceinline__ bf16x8 pack_b(const f32x4& t0, const f32x4& t1) {
+  return bf16x8{(bf16)t0[0], (bf16)t0[1], (bf16)t0[2], (bf16)t0[3],
+                (bf16)t1[0], (bf16)t1[1], (bf16)t1[2], (bf16)t1[3]};
+}
+
+// hi/lo split of the same pair: x ~= hi + lo with both in bf16.
+__device__ __forceinline__ void pack_b_hilo(const f32x4& t0, const f32x4& t1, bf16x8& hi,
+                                            bf16x8& lo) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const bf16 h0 = (bf16)t0[j], h1 = (bf16)t1[j];
+    hi[j] = h0; hi[4 + j] = h1;
+    lo[j] = (bf16)(t0[j] - (float)h0);
+    lo[4 + j] = (bf16)(t1[j] - (float)h1);
+  }
+}
+
+// Sum over the 16 lanes of a DPP row (VALU lane permutes, no LDS traffic).
+__device__ __forceinline__ float row16_sum(float x) {
+  auto dpp = [](float v, int ctrl) -> float {
+    int r;
+    switch (ctrl) {
+      case 0: r = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false); break;
+      case 1: r = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false); break;
+      case 2: r = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false); break;
+      default: r = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false); break;
+    }
+    return __builtin_bit_cast(float, r);
+  };
+  x += dpp(x, 0);  // quad_perm [1,0,3,2]
+  x += dpp(x, 1);  // quad_perm [2,3,0,1]
+  x += dpp(x, 2);  // row_half_mirror
+  x += dpp(x, 3);  // row_mirror
+  return x;
+}
+
+// Inclusive prefix sum over lanes 0..31 (two DPP rows) with VALU lane shifts.
+#define HMX_DPP_F(v, ctrl, rmask) \
+  __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, (v)), (ctrl), \
+                                                        (rmask), 0xF, true))
+__device__ __forceinline__ float scan32(float x) {
+  x += HMX_DPP_F(x, 0x111, 0xF);  // row_shr:1
+  x += HMX_DPP_F(x, 0x112, 0xF);  // row_shr:2
+  x += HMX_DPP_F(x, 0x114, 0xF);  // row_shr:4
+  x += HMX_DPP_F(x, 0x118, 0xF);  // row_shr:8
+  x += HMX_DPP_F(x, 0x142, 0xA);  // row_bcast:15 into rows 1 and 3
+  return x;
+}
+#undef HMX_DPP_F
+
+// Workgroup barrier that orders LDS only: global loads issued before it stay in
+// flight (the next chunk's prefetch), unlike __syncthreads().
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+
+}  // namespace hmx

@@ -1,6 +1,8 @@
 """Mixer ops with the reference's names, argument order, defaults and returns."""
 from .gdn import (chunk_gated_delta_rule, chunk_gated_delta_rule_gqa, fused_gdn_gating,
                   fused_recurrent_gated_delta_rule, fused_recurrent_gated_delta_rule_gqa)
+from .gka import (chebyshev_iteration_gqa, fused_gka_gating, gka_chebyshev_gla_decode,
+                  gka_chebyshev_gla_prefill)
 
 __all__ = [
     "fused_gdn_gating",
@@ -8,4 +10,8 @@ __all__ = [
     "fused_recurrent_gated_delta_rule",
     "chunk_gated_delta_rule_gqa",
     "chunk_gated_delta_rule",
+    "fused_gka_gating",
+    "chebyshev_iteration_gqa",
+    "gka_chebyshev_gla_decode",
+    "gka_chebyshev_gla_prefill",
 ]

@@ -1,0 +1,197 @@
+"""Gated KalmaNet (GKA) ops — the reference's Python signatures over libhmx.
+
+Entry points (reference paths relative to the reference repository root):
+
+- ``fused_gka_gating`` — vllm-inference/src/primed_vllm/primed_gka_layer.py:303-358
+- ``chebyshev_iteration_gqa`` — .../gka/ops/chebyshev_iteration_gqa.py:173-238
+- ``gka_chebyshev_gla_decode`` — .../gka/gka_forward.py:248-326
+- ``gka_chebyshev_gla_prefill`` — .../gka/gka_forward.py:161-242
+
+Differences from the reference, by design: q and k are L2-normalised inside the
+kernels instead of in place on the caller's tensors (gka_forward.py:149-159
+mutates them); the results are the same.
+"""
+from __future__ import annotations
+
+import logging
+
+import torch
+
+from .. import _lib
+from .gdn import _cu_count, _i32, _segment_table
+
+GKA_WORKGROUPS_PER_CU = 1
+_warned_num_iter_zero = False
+
+
+def _check_sketching_constraints(gka, num_sketches_per_head, func_name):
+    """Sketching is unsupported, as in gka_forward.py:23-34."""
+    if gka is not None:
+        raise NotImplementedError(
+            f"{func_name}: gka projection is not supported. Set parallel_latent_sketch=False in config. ")
+    if num_sketches_per_head != 1:
+        raise NotImplementedError(
+            f"{func_name}: num_sketches_per_head={num_sketches_per_head} is not supported. "
+            "Must be 1 due to numerical instability in gating kernel. ")
+
+
+def fused_gka_gating(A_log: torch.Tensor, a: torch.Tensor, alpha_in: torch.Tensor,
+                     b: torch.Tensor | None, dt_bias: torch.Tensor, beta: float = 1.0,
+                     threshold: float = 20.0):
+    """g = -exp(A_log) softplus(a + dt_bias), alpha = sigmoid(alpha_in), beta = sigmoid(b).
+
+    Returns (g, alpha, beta or None), each [1, num_tokens, num_heads] in a.dtype
+    (primed_gka_layer.py:303-358).
+    """
+    _lib.require_gpu(A_log, a, alpha_in, b, dt_bias)
+    num_tokens, num_heads = a.shape
+    g = torch.empty(num_tokens, num_heads, dtype=a.dtype, device=a.device)
+    alpha = torch.empty_like(g)
+    beta_out = torch.empty_like(g) if b is not None else None
+    if alpha_in.dtype != a.dtype or (b is not None and b.dtype != a.dtype):
+        raise ValueError("a, alpha_in and b must share a dtype")
+    _lib.call("hmx_gka_gating",
+              _lib.ptr(A_log), _lib.dtype_code(A_log),
+              _lib.ptr(a), a.stride(0), a.stride(1),
+              _lib.ptr(alpha_in), alpha_in.stride(0), alpha_in.stride(1),
+              _lib.ptr(b), 0 if b is None else b.stride(0), 0 if b is None else b.stride(1),
+              _lib.dtype_code(a), _lib.ptr(dt_bias), _lib.dtype_code(dt_bias),
+              _lib.ptr(g), _lib.ptr(alpha), _lib.ptr(beta_out), _lib.dtype_code(g),
+              num_tokens, num_heads, float(beta), float(threshold), _lib.stream_of(a))
+    return (g.unsqueeze(0), alpha.unsqueeze(0),
+            beta_out.unsqueeze(0) if beta_out is not None else None)
+
+
+def chebyshev_iteration_gqa(k, q, v, alpha, gk=None, beta=None, num_iter: int = 15,
+                            scale: float | None = None, ridge_ratio: float = 0.1,
+                            initial_state_kk=None, initial_state_kv=None,
+                            output_final_state: bool = True, inplace_final_state: bool = True,
+                            cu_seqlens=None, ssm_state_indices=None):
+    """Fused GKA decode step (chebyshev_iteration_gqa.py:173-238).
+
+    k [B,T,HKV,D]; q [B,T,H,D]; v [B,T,HKV,V]; alpha, gk, beta [B,T,H].
+    States [N,H,D,D] / [N,H,D,V] (slot pools with ssm_state_indices), updated in
+    place when ``inplace_final_state``.  Only the first token of each sequence
+    is processed.  Returns (o, h_kk_out, h_kv_out).
+    """
+    if cu_seqlens is not None and q.shape[0] != 1:
+        raise ValueError(f"Batch size must be 1 when using cu_seqlens, got {q.shape[0]}.")
+    B, T, H, D = q.shape
+    HKV, V = k.shape[2], v.shape[-1]
+    N = B if cu_seqlens is None else len(cu_seqlens) - 1
+    if scale is None:
+        scale = D ** -0.5
+    if initial_state_kk is None:
+        initial_state_kk = q.new_zeros(N, H, D, D, dtype=torch.float32)
+    if initial_state_kv is None:
+        initial_state_kv = q.new_zeros(N, H, D, V, dtype=torch.float32)
+    _lib.require_gpu(q, k, v, alpha, gk, beta, initial_state_kk, initial_state_kv, cu_seqlens,
+                     ssm_state_indices)
+    if initial_state_kk.dtype != torch.float32:
+        raise NotImplementedError("h_kk state must be float32 (primed_gka_layer.py:424-430)")
+    for st, last in ((initial_state_kk, D), (initial_state_kv, V)):
+        if tuple(st.shape[1:]) != (H, D, last) or not st[0].is_contiguous():
+            raise ValueError(f"state must be [rows,{H},{D},{last}] with contiguous rows, "
+                             f"got {tuple(st.shape)}")
+    q, k, v, alpha = (x.contiguous() for x in (q, k, v, alpha))
+    gk = None if gk is None else gk.contiguous()
+    beta = None if beta is None else beta.contiguous()
+    if inplace_final_state:
+        hkk, hkv = initial_state_kk, initial_state_kv
+    else:
+        hkk, hkv = initial_state_kk.clone(), initial_state_kv.clone()
+    idx = _i32(ssm_state_indices)
+    o = q.new_empty(B, T, H, V)
+    _lib.call("hmx_gka_decode_fwd",
+              _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.dtype_code(q),
+              _lib.ptr(alpha), _lib.dtype_code(alpha),
+              _lib.ptr(gk), 0 if gk is None else _lib.dtype_code(gk),
+              _lib.ptr(beta), 0 if beta is None else _lib.dtype_code(beta),
+              _lib.ptr(o),
+              _lib.ptr(hkk), hkk.stride(0), _lib.ptr(hkk), hkk.stride(0),
+              _lib.ptr(hkv), hkv.stride(0), _lib.ptr(hkv), hkv.stride(0), _lib.dtype_code(hkv),
+              _lib.ptr(_i32(cu_seqlens)), _lib.ptr(idx), 0 if idx is None else idx.stride(0),
+              B, T, N, H, HKV, D, V, int(num_iter), float(ridge_ratio), float(scale),
+              _lib.stream_of(q))
+    if not output_final_state:
+        return o, None, None
+    if not inplace_final_state and idx is not None:
+        # the reference writes sequence n's new state to row n (chebyshev_iteration_gqa.py:106)
+        hkk, hkv = hkk[idx.long()], hkv[idx.long()]
+    return o, hkk, hkv
+
+
+def gka_chebyshev_gla_decode(q, k, v, alpha, g, gk, beta, gla_scale: float,
+                             ridge_ratio: float = 0.02, num_sketches_per_head: int = 1,
+                             num_iter: int = 30, gka=None, h_kk=None, h_kv=None,
+                             cu_seqlens=None, ssm_state_indices=None):
+    """Single-token GKA decode (gka_forward.py:248-326)."""
+    global _warned_num_iter_zero
+    _check_sketching_constraints(gka, num_sketches_per_head, "gka_chebyshev_gla_decode")
+    if num_iter == 0:
+        if not _warned_num_iter_zero:
+            logging.warning("gka_chebyshev_gla_decode: num_iter=0, running 1 Chebyshev iteration. "
+                            "Ensure alpha is zeroed out by the caller to skip query correction.")
+            _warned_num_iter_zero = True
+        num_iter = 1
+    assert g is gk, "GLA gate g not equal to GKA gate gk is not supported for decoding."
+    return chebyshev_iteration_gqa(k=k, q=q, v=v, alpha=alpha, gk=gk, beta=beta,
+                                   num_iter=num_iter, scale=gla_scale, ridge_ratio=ridge_ratio,
+                                   initial_state_kk=h_kk, initial_state_kv=h_kv,
+                                   output_final_state=True, inplace_final_state=True,
+                                   cu_seqlens=cu_seqlens, ssm_state_indices=ssm_state_indices)
+
+
+def gka_chebyshev_gla_prefill(q, k, v, alpha, g, gk, beta, gla_scale: float,
+                              ridge_ratio: float = 0.02, num_sketches_per_head: int = 1,
+                              num_iter: int = 30, gka=None, h_kk_initial=None, h_kv_initial=None,
+                              output_final_state: bool = True, cu_seqlens=None, *,
+                              _segment_chunks: int | None = None):
+    """Full GKA prefill: Chebyshev query refinement + beta^2 simple GLA
+    (gka_forward.py:161-242).  Returns (o, h_kk_final, h_kv_final); h_kk_final is
+    None when num_iter == 0 or not output_final_state."""
+    _check_sketching_constraints(gka, num_sketches_per_head, "gka_chebyshev_gla_prefill")
+    if cu_seqlens is not None and q.shape[0] != 1:
+        raise ValueError(f"Batch size must be 1 when using cu_seqlens, got {q.shape[0]}")
+    _lib.require_gpu(q, k, v, alpha, g, gk, beta, h_kk_initial, h_kv_initial, cu_seqlens)
+    B, T, H, D = q.shape
+    HKV, V = k.shape[2], v.shape[-1]
+    if cu_seqlens is None:
+        bounds = [(n * T, n * T + T) for n in range(B)]
+    else:
+        cs = [int(x) for x in cu_seqlens.tolist()]
+        bounds = [(cs[n], cs[n + 1]) for n in range(len(cs) - 1)]
+    N = len(bounds)
+    for st, last, name in ((h_kk_initial, D, "h_kk_initial"), (h_kv_initial, V, "h_kv_initial")):
+        if st is not None and tuple(st.shape) != (N, H, D, last):
+            raise ValueError(f"{name} must be [{N},{H},{D},{last}], got {tuple(st.shape)}")
+    q, k, v, alpha, g = (x.contiguous() for x in (q, k, v, alpha, g))
+    gk = None if gk is None else gk.contiguous()
+    beta = None if beta is None else beta.contiguous()
+    hkk0 = None if h_kk_initial is None else h_kk_initial.to(torch.float32).contiguous()
+    hkv0 = None if h_kv_initial is None else h_kv_initial.to(torch.float32).contiguous()
+    o = torch.empty(B, T, H, V, dtype=q.dtype, device=q.device)
+    if cu_seqlens is not None and bounds and bounds[-1][1] < T:
+        o[:, bounds[-1][1]:].zero_()
+    hkk_t = (torch.empty(N, H, D, D, dtype=torch.float32, device=q.device)
+             if output_final_state and num_iter > 0 else None)
+    hkv_t = (torch.empty(N, H, D, V, dtype=torch.float32, device=q.device)
+             if output_final_state else None)
+    rows = _segment_table(bounds, H, GKA_WORKGROUPS_PER_CU * _cu_count(q.device), _segment_chunks)
+    seg = torch.tensor(rows, dtype=torch.int32).to(q.device, non_blocking=True)
+    lib = _lib.load()
+    ws_bytes = int(lib.hmx_gka_chunk_workspace_bytes(len(rows), N, H))
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=q.device)
+    _lib.call("hmx_gka_chunk_fwd",
+              _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.dtype_code(q),
+              _lib.ptr(alpha), _lib.dtype_code(alpha), _lib.ptr(g), _lib.dtype_code(g),
+              _lib.ptr(gk), 0 if gk is None else _lib.dtype_code(gk),
+              _lib.ptr(beta), 0 if beta is None else _lib.dtype_code(beta),
+              _lib.ptr(o), _lib.ptr(hkk0), _lib.ptr(hkv0), _lib.ptr(hkk_t), _lib.ptr(hkv_t),
+              _lib.ptr(seg), len(rows), N, H, HKV, D, V, int(num_iter), float(ridge_ratio),
+              float(gla_scale), _lib.ptr(ws), ws.numel(), _lib.stream_of(q))
+    return o, hkk_t, hkv_t
+
+
+__all__ = ["fused_gka_gating", "chebyshev_iteration_gqa", "gka_chebyshev_gla_decode",
+           "gka_chebyshev_gla_prefill"]

@@ -78,6 +78,35 @@ def decode_inputs(n_seqs: int = 256, H: int = 32, HKV: int = 32, D: int = 128, s
     return {n: t.to(device) for n, t in out.items()}
 
 
+def gka_inputs(T: int, H: int, HKV: int, D: int, dtype=torch.bfloat16, config_id: int = 3,
+               B: int = 1, device="cpu", gen_device="cpu"):
+    """C3: q,k L2-normalised, v ~ N(0,1); alpha, beta = sigmoid(N(0,1));
+    g = gk = logsigmoid(N(0,1)) (one tensor passed as both gates)."""
+    gd = gen(config_id, gen_device)
+    q = _l2n(_randn(gd, (B, T, H, D), gen_device))
+    k = _l2n(_randn(gd, (B, T, HKV, D), gen_device))
+    v = _randn(gd, (B, T, HKV, D), gen_device)
+    alpha = torch.sigmoid(_randn(gd, (B, T, H), gen_device))
+    beta = torch.sigmoid(_randn(gd, (B, T, H), gen_device))
+    g = F.logsigmoid(_randn(gd, (B, T, H), gen_device))
+    out = dict(q=q.to(dtype), k=k.to(dtype), v=v.to(dtype), alpha=alpha, beta=beta, g=g)
+    out = {n: t.to(device) for n, t in out.items()}
+    out["gk"] = out["g"]
+    return out
+
+
+def gka_prefill_flops(T: int, H: int, num_iter: int, d: int = 128, C: int = 64) -> float:
+    """2*T*H*[(4+n) d^2 + (3+2n) C d + C^2] (h_kk update, exact-fro terms, n solver
+    iterations of x.H_c / x.K^T / .K, and the GLA)."""
+    n = num_iter
+    return 2.0 * T * H * ((4 + n) * d * d + (3 + 2 * n) * C * d + C * C)
+
+
+def gka_prefill_bytes(T: int, H: int, HKV: int, d: int = 128, n_seqs: int = 1) -> float:
+    """q,o [T,H,d] + k,v [T,HKV,d] bf16 + alpha,beta,g fp32 + two fp32 final states."""
+    return T * H * 2 * d * 2 + T * HKV * 2 * d * 2 + 3 * T * H * 4 + 2 * n_seqs * H * d * d * 4
+
+
 # ---------------------------------------------------------------------------
 # algorithmic work per unit (used for roofline.achieved)
 # ---------------------------------------------------------------------------
@@ -106,5 +135,5 @@ def ceil_div(a: int, b: int) -> int:
     return -(-a // b)
 
 
-__all__ = ["gen", "gdn_inputs", "varlen_lengths", "cu_from_lengths", "decode_inputs",
+__all__ = ["gen", "gdn_inputs", "gka_inputs", "gka_prefill_flops", "gka_prefill_bytes", "varlen_lengths", "cu_from_lengths", "decode_inputs",
            "gdn_prefill_flops", "gdn_prefill_bytes", "gdn_decode_bytes", "ceil_div", "math"]

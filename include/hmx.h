@@ -122,6 +122,76 @@ int hmx_gdn_chunk_fwd(const void* q, const void* k, const void* v, int32_t qkv_d
  * reference allocates its intermediates inside the op, chunk_gqa.py:63-81). */
 size_t hmx_gdn_chunk_workspace_bytes(int32_t nseg_total, int32_t N, int32_t H);
 
+/*
+ * GKA gating: g = -exp(A_log) * softplus(a + dt_bias), alpha = sigmoid(alpha_in),
+ * beta_out = sigmoid(b) when b is not NULL.  [num_tokens, num_heads] inputs with
+ * arbitrary strides; contiguous outputs in out_dtype.
+ * Replaces: fused_gka_gating
+ *   vllm-inference/src/primed_vllm/primed_gka_layer.py:303-358 (kernel :224-300).
+ */
+int hmx_gka_gating(const void* A_log, int32_t A_log_dtype,
+                   const void* a, int64_t a_stride0, int64_t a_stride1,
+                   const void* alpha_in, int64_t alpha_in_stride0, int64_t alpha_in_stride1,
+                   const void* b, int64_t b_stride0, int64_t b_stride1, int32_t in_dtype,
+                   const void* dt_bias, int32_t dt_bias_dtype,
+                   void* g, void* alpha, void* beta_out, int32_t out_dtype,
+                   int64_t num_tokens, int32_t num_heads, float sp_beta, float threshold,
+                   void* stream);
+
+/*
+ * GKA decode step (first token of each sequence), in place on slot-indexed pools.
+ *  q [B*T, H, 128]; k, v [B*T, HKV, 128] (qkv_dtype); alpha [B*T, H];
+ *  gk, beta [B*T, H] or NULL; o [B*T, H, 128] (qkv_dtype; first token per sequence)
+ *  h_kk_in/out fp32 rows of [H, 128, 128] (row strides in elements; in == out for
+ *  the in-place update); h_kv_in/out rows of [H, 128, 128] in h_kv_dtype (f32/bf16).
+ *  State row of sequence n: ssm_state_indices[n*idx_stride], or n without indices.
+ *  num_iter Chebyshev steps; ridge_ratio; scale (the GLA scale).
+ * Replaces: chebyshev_iteration_gqa / gka_chebyshev_gla_decode
+ *   vllm-inference/src/primed_vllm/gka/ops/chebyshev_iteration_gqa.py:173-238 (kernel :22-170),
+ *   vllm-inference/src/primed_vllm/gka/gka_forward.py:248-326.
+ */
+int hmx_gka_decode_fwd(const void* q, const void* k, const void* v, int32_t qkv_dtype,
+                       const void* alpha, int32_t alpha_dtype,
+                       const void* gk, int32_t gk_dtype, const void* beta, int32_t beta_dtype,
+                       void* o,
+                       const float* h_kk_in, int64_t h_kk_in_row_stride,
+                       float* h_kk_out, int64_t h_kk_out_row_stride,
+                       const void* h_kv_in, int64_t h_kv_in_row_stride,
+                       void* h_kv_out, int64_t h_kv_out_row_stride, int32_t h_kv_dtype,
+                       const int32_t* cu_seqlens, const int32_t* ssm_state_indices,
+                       int64_t idx_stride, int64_t B, int64_t T, int64_t N,
+                       int32_t H, int32_t HKV, int32_t D, int32_t V,
+                       int32_t num_iter, float ridge_ratio, float scale, void* stream);
+
+/*
+ * GKA chunked prefill forward (Chebyshev ridge solve + beta^2 GLA), GQA-native,
+ * varlen via the same segment table layout as hmx_gdn_chunk_fwd (chunks of 32
+ * tokens).  q [T_total, H, 128]; k, v [T_total, HKV, 128] bf16 (raw: q and k are
+ * L2-normalised inside, without eps); alpha, g [T_total, H]; gk, beta
+ * [T_total, H] or NULL; o [T_total, H, 128] bf16.  h_kk0 / h_kv0 fp32
+ * [N, H, 128, 128] or NULL; h_kk_final / h_kv_final fp32 [N, H, 128, 128] or
+ * NULL (h_kk_final is not written when num_iter == 0).
+ * workspace: hmx_gka_chunk_workspace_bytes(...) bytes of device scratch.
+ * Replaces: gka_chebyshev_gla_prefill
+ *   vllm-inference/src/primed_vllm/gka/gka_forward.py:161-242 (and its kernels
+ *   ops/chebyshev_prefill_gqa.py:28-316, ops/chunk_simple_gla_gqa.py:33-190,
+ *   ops/chunk_o_gqa.py:25-171).
+ */
+int hmx_gka_chunk_fwd(const void* q, const void* k, const void* v, int32_t qkv_dtype,
+                      const void* alpha, int32_t alpha_dtype, const void* g, int32_t g_dtype,
+                      const void* gk, int32_t gk_dtype, const void* beta, int32_t beta_dtype,
+                      void* o, const float* h_kk0, const float* h_kv0,
+                      float* h_kk_final, float* h_kv_final,
+                      const int32_t* seg_table, int32_t nseg_total, int32_t N,
+                      int32_t H, int32_t HKV, int32_t D, int32_t V,
+                      int32_t num_iter, float ridge_ratio, float scale,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes hmx_gka_chunk_fwd needs (host-only arithmetic).  Companion of
+ * hmx_gka_chunk_fwd; no reference counterpart (the reference allocates its
+ * chunk states inside the op, chebyshev_prefill_gqa.py:137). */
+size_t hmx_gka_chunk_workspace_bytes(int32_t nseg_total, int32_t N, int32_t H);
+
 #ifdef __cplusplus
 }
 #endif
