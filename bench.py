@@ -8,7 +8,10 @@ C2 (256 sequences x 1 token, H=32, fp32 state pool of 512 MiB through a random
 slot permutation, 512 consecutive steps) in steps/s, each with its roofline,
 and the CPU oracle timed on a bounded sample of the same workloads.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only prefill|decode]
+GKA prefill at C3 (the C1 shape, Chebyshev solve at 8 and 32 iterations) is
+reported under ``gka`` against the bf16 MFMA roofline.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only prefill|decode|gka]
 """
 from __future__ import annotations
 
@@ -86,6 +89,26 @@ def bench_decode(dev, steps_total=512, warmup=8):
     return dict(ms=ms, steps_per_s=1e3 / ms, tokens_per_s=N * 1e3 / ms, bytes=by, GBps=gbs)
 
 
+def bench_gka(dev, steps, warmup, num_iter):
+    """C3: gka_chebyshev_gla_prefill at the C1 shape, ridge 0.01, zero initial states."""
+    import hmx
+    from hmx import workloads as wl
+    T, H, D = 32768, 32, 128
+    d = wl.gka_inputs(T=T, H=H, HKV=H, D=D, config_id=3, device=dev, gen_device=dev)
+    args = [d[n] for n in ("q", "k", "v", "alpha", "g", "gk", "beta")]
+
+    def step():
+        hmx.gka_chebyshev_gla_prefill(*args, D ** -0.5, ridge_ratio=0.01, num_iter=num_iter,
+                                      output_final_state=True)
+
+    ms = _timed(step, steps, warmup)
+    fl = wl.gka_prefill_flops(T, H, num_iter)
+    by = wl.gka_prefill_bytes(T, H, H)
+    tfs = fl / (ms * 1e-3) / 1e12
+    return dict(ms=ms, tokens_per_s=T / (ms * 1e-3), flops=fl, bytes=by, TFLOPs=tfs,
+                GBps=by / (ms * 1e-3) / 1e9)
+
+
 def cpu_baseline(sample_tokens=4096):
     """The oracle's chunked fp32 restatement on the host (a bounded sample of C1)."""
     import torch
@@ -131,7 +154,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "decode"], default=None)
+    ap.add_argument("--only", choices=["prefill", "decode", "gka"], default=None)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (HBM counter calibration)")
     a = ap.parse_args()
@@ -151,6 +174,8 @@ def main():
         out["prefill"] = pf
     if a.only in (None, "decode"):
         out["decode"] = bench_decode(dev)
+    if a.only in (None, "gka"):
+        out["gka"] = {n: bench_gka(dev, max(2, a.steps // 4), 1, n) for n in (8, 32)}
     line = {
         "metric": "mixer prefill tokens/sec + decode steps/sec at 8B shape; % of roofline (1 GPU)",
         "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
@@ -191,6 +216,21 @@ def main():
                          "ms_per_step": line["decode"]["ms_per_step"],
                          "config": line["decode"]["config"],
                          "roofline": line["decode"]["roofline"]})
+    if "gka" in out:
+        line["gka"] = {}
+        for n, r in out["gka"].items():
+            line["gka"][f"num_iter_{n}"] = {
+                "value": round(r["tokens_per_s"], 1), "unit": "tokens/s",
+                "ms_per_step": round(r["ms"], 4),
+                "config": {"workload": "C3 GKA prefill (gka_chebyshev_gla_prefill)", "B": 1,
+                           "T": 32768, "H": 32, "d": 128, "num_iter": n, "ridge_ratio": 0.01},
+                "roofline": {"bound": "mfma", "achieved": round(r["TFLOPs"], 1),
+                             "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                             "frac": round(r["TFLOPs"] / BF16_PEAK_TFLOPS, 4),
+                             "traffic": measured_traffic(f"gka_prefill_c3_n{n}"),
+                             "algorithmic_flops": r["flops"],
+                             "hbm_GBps": round(r["GBps"], 1)},
+            }
     if not a.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line), flush=True)
