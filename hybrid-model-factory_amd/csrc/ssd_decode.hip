@@ -1,0 +1,194 @@
+// Mamba2 single-token state update (selective_state_update) for gfx950: an
+// in-place read-modify-write of one slot of the SSM state pool per (sequence,
+// head), HBM-bound on the state.
+//
+// Semantics (mamba_ssm / vLLM selective_state_update; reference calls at
+// training/.../layers/mamba/mamba2.py:776-800 and
+// vllm-inference/src/primed_vllm/primed_mamba2_layer.py:1000-1021):
+//   d      = dt[p] + dt_bias[p]; d = softplus_20(d) if dt_softplus
+//   S[p,n] = S[p,n] e^{A[p,n] d} + d x[p] B[n]
+//   out[p] = sum_n S[p,n] C[n] + D[p] x[p];  out *= z sigmoid(z) if z is given
+// The source slot is state_batch_indices[i] (or i); entries equal to
+// pad_slot_id are skipped; the result goes to dst_state_batch_indices[i] when
+// given, else back to the source slot.
+//
+// Layout: one 256-thread workgroup per (sequence, head).  Thread t owns the
+// 4 consecutive n of columns 4 (t mod N/4) for rows p = t / (N/4) + k (1024/N),
+// so every state load and store is a fully coalesced 16-byte (fp32) access.
+#include "common.hpp"
+
+namespace hmx {
+namespace ssdd {
+
+constexpr int NTHR = 256;
+
+struct Params {
+  void* state; int64_t slot_stride;          // [slots][H][P][N], inner contiguous
+  const void* x; int x_dt; int64_t x_bs, x_hs, x_ps;
+  const void* dt; int dt_dt; int64_t dt_bs, dt_hs, dt_ps;
+  const float* A; int64_t a_hs, a_ps, a_ns;  // fp32 [H][P][N] (any strides)
+  const void* B; int b_dt; int64_t b_bs, b_gs;
+  const void* C; int c_dt; int64_t c_bs, c_gs;
+  const float* D; int64_t d_hs, d_ps;        // or null
+  const float* dt_bias; int64_t db_hs, db_ps; // or null
+  const void* z; int z_dt; int64_t z_bs, z_hs, z_ps;  // or null
+  void* out; int out_dt; int64_t o_bs, o_hs, o_ps;
+  const int* src_idx; const int* dst_idx; int pad_slot;
+  int H, G, softplus;
+};
+
+__device__ __forceinline__ float ld_any(const void* p, int64_t i, int dt) {
+  if (dt == HMX_F32) return static_cast<const float*>(p)[i];
+  if (dt == HMX_BF16) return (float)static_cast<const bf16*>(p)[i];
+  return (float)static_cast<const f16*>(p)[i];
+}
+
+__device__ __forceinline__ void st_any(void* p, int64_t i, int dt, float v) {
+  if (dt == HMX_F32) static_cast<float*>(p)[i] = v;
+  else if (dt == HMX_BF16) static_cast<bf16*>(p)[i] = (bf16)v;
+  else static_cast<f16*>(p)[i] = (f16)v;
+}
+
+template <typename TS>
+__device__ __forceinline__ f32x4 ld4(const TS* p) {
+  if constexpr (sizeof(TS) == 4) {
+    return *reinterpret_cast<const f32x4*>(p);
+  } else {
+    const bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
+    return f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+  }
+}
+
+template <typename TS>
+__device__ __forceinline__ void st4(TS* p, const f32x4& v) {
+  if constexpr (sizeof(TS) == 4) {
+    *reinterpret_cast<f32x4*>(p) = v;
+  } else {
+    *reinterpret_cast<bf16x4*>(p) = bf16x4{(bf16)v[0], (bf16)v[1], (bf16)v[2], (bf16)v[3]};
+  }
+}
+
+template <typename TS, int P, int N, bool A_TIED>
+__global__ __launch_bounds__(NTHR) void ssd_state_update_kernel(Params p) {
+  constexpr int GN = N / 4;            // threads per row
+  constexpr int RPP = NTHR / GN;       // rows per pass
+  constexpr int PASSES = P / RPP;
+  const int i = blockIdx.x / p.H, h = blockIdx.x % p.H;
+  const int g = h / (p.H / p.G);
+  const int src = p.src_idx ? p.src_idx[i] : i;
+  if (src == p.pad_slot) return;
+  const int dst = p.dst_idx ? p.dst_idx[i] : src;
+  const int tid = threadIdx.x, n0 = 4 * (tid % GN), r0 = tid / GN;
+
+  float bv[4], cv[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    bv[j] = ld_any(p.B, (int64_t)i * p.b_bs + (int64_t)g * p.b_gs + n0 + j, p.b_dt);
+    cv[j] = ld_any(p.C, (int64_t)i * p.c_bs + (int64_t)g * p.c_gs + n0 + j, p.c_dt);
+  }
+  const TS* sin = static_cast<const TS*>(p.state) + (int64_t)src * p.slot_stride + (int64_t)h * P * N;
+  TS* sout = static_cast<TS*>(p.state) + (int64_t)dst * p.slot_stride + (int64_t)h * P * N;
+
+  f32x4 st[PASSES];
+#pragma unroll
+  for (int k = 0; k < PASSES; ++k) st[k] = ld4(sin + (int64_t)(r0 + k * RPP) * N + n0);
+
+#pragma unroll
+  for (int k = 0; k < PASSES; ++k) {
+    const int pr = r0 + k * RPP;
+    const float xv = ld_any(p.x, (int64_t)i * p.x_bs + (int64_t)h * p.x_hs + (int64_t)pr * p.x_ps, p.x_dt);
+    float d = ld_any(p.dt, (int64_t)i * p.dt_bs + (int64_t)h * p.dt_hs + (int64_t)pr * p.dt_ps, p.dt_dt);
+    if (p.dt_bias) d += p.dt_bias[(int64_t)h * p.db_hs + (int64_t)pr * p.db_ps];
+    if (p.softplus) d = d <= 20.f ? log1pf(expf(d)) : d;
+    const float dx = d * xv;
+    float acc = 0.f;
+    if constexpr (A_TIED) {
+      const float da = expf(p.A[(int64_t)h * p.a_hs] * d);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        st[k][j] = st[k][j] * da + dx * bv[j];
+        acc += st[k][j] * cv[j];
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float a = p.A[(int64_t)h * p.a_hs + (int64_t)pr * p.a_ps + (int64_t)(n0 + j) * p.a_ns];
+        st[k][j] = st[k][j] * expf(a * d) + dx * bv[j];
+        acc += st[k][j] * cv[j];
+      }
+    }
+#pragma unroll
+    for (int m = 1; m < GN; m <<= 1) acc += shfl_xor(acc, m);
+    if (tid % GN == 0) {
+      float o = acc;
+      if (p.D) o += p.D[(int64_t)h * p.d_hs + (int64_t)pr * p.d_ps] * xv;
+      if (p.z) {
+        const float zz = ld_any(p.z, (int64_t)i * p.z_bs + (int64_t)h * p.z_hs + (int64_t)pr * p.z_ps, p.z_dt);
+        o *= zz / (1.f + expf(-zz));
+      }
+      st_any(p.out, (int64_t)i * p.o_bs + (int64_t)h * p.o_hs + (int64_t)pr * p.o_ps, p.out_dt, o);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < PASSES; ++k) st4(sout + (int64_t)(r0 + k * RPP) * N + n0, st[k]);
+}
+
+template <typename TS, int P, int N>
+void launch(const Params& p, int batch, bool tied, hipStream_t s) {
+  if (tied)
+    hipLaunchKernelGGL((ssd_state_update_kernel<TS, P, N, true>), dim3(batch * p.H), dim3(NTHR), 0, s, p);
+  else
+    hipLaunchKernelGGL((ssd_state_update_kernel<TS, P, N, false>), dim3(batch * p.H), dim3(NTHR), 0, s, p);
+}
+
+}  // namespace ssdd
+}  // namespace hmx
+
+using namespace hmx;
+using namespace hmx::ssdd;
+
+extern "C" int hmx_ssd_state_update(
+    void* state, int32_t state_dtype, int64_t slot_stride, const void* x, int32_t x_dtype,
+    int64_t x_bs, int64_t x_hs, int64_t x_ps, const void* dt, int32_t dt_dtype, int64_t dt_bs,
+    int64_t dt_hs, int64_t dt_ps, const float* A, int64_t a_hs, int64_t a_ps, int64_t a_ns,
+    const void* B, int32_t b_dtype, int64_t b_bs, int64_t b_gs, const void* C, int32_t c_dtype,
+    int64_t c_bs, int64_t c_gs, const float* D, int64_t d_hs, int64_t d_ps, const float* dt_bias,
+    int64_t db_hs, int64_t db_ps, const void* z, int32_t z_dtype, int64_t z_bs, int64_t z_hs,
+    int64_t z_ps, void* out, int32_t out_dtype, int64_t o_bs, int64_t o_hs, int64_t o_ps,
+    const int32_t* state_batch_indices, const int32_t* dst_state_batch_indices,
+    int32_t pad_slot_id, int32_t batch, int32_t H, int32_t G, int32_t P, int32_t N,
+    int32_t dt_softplus, void* stream) {
+  HMX_REQUIRE(state_dtype == HMX_F32 || state_dtype == HMX_BF16, HMX_EUNSUPPORTED,
+              "hmx_ssd_state_update: state must be float32 or bfloat16 (dtype code %d)", state_dtype);
+  HMX_REQUIRE((P == 64 || P == 128) && (N == 64 || N == 128), HMX_EUNSUPPORTED,
+              "hmx_ssd_state_update: headdim in {64,128} and d_state in {64,128} (got %d, %d)", P, N);
+  HMX_REQUIRE(H > 0 && G > 0 && H % G == 0, HMX_EINVAL, "hmx_ssd_state_update: H=%d G=%d", H, G);
+  HMX_REQUIRE(state && x && dt && A && B && C && out, HMX_EINVAL,
+              "hmx_ssd_state_update: null tensor pointer");
+  HMX_REQUIRE(slot_stride % 4 == 0, HMX_EINVAL,
+              "hmx_ssd_state_update: the state slot stride must be a multiple of 4 elements");
+  if (batch == 0) return HMX_OK;
+  Params p;
+  p.state = state; p.slot_stride = slot_stride;
+  p.x = x; p.x_dt = x_dtype; p.x_bs = x_bs; p.x_hs = x_hs; p.x_ps = x_ps;
+  p.dt = dt; p.dt_dt = dt_dtype; p.dt_bs = dt_bs; p.dt_hs = dt_hs; p.dt_ps = dt_ps;
+  p.A = A; p.a_hs = a_hs; p.a_ps = a_ps; p.a_ns = a_ns;
+  p.B = B; p.b_dt = b_dtype; p.b_bs = b_bs; p.b_gs = b_gs;
+  p.C = C; p.c_dt = c_dtype; p.c_bs = c_bs; p.c_gs = c_gs;
+  p.D = D; p.d_hs = d_hs; p.d_ps = d_ps;
+  p.dt_bias = dt_bias; p.db_hs = db_hs; p.db_ps = db_ps;
+  p.z = z; p.z_dt = z_dtype; p.z_bs = z_bs; p.z_hs = z_hs; p.z_ps = z_ps;
+  p.out = out; p.out_dt = out_dtype; p.o_bs = o_bs; p.o_hs = o_hs; p.o_ps = o_ps;
+  p.src_idx = state_batch_indices; p.dst_idx = dst_state_batch_indices; p.pad_slot = pad_slot_id;
+  p.H = H; p.G = G; p.softplus = dt_softplus;
+  const bool tied = a_ps == 0 && a_ns == 0;
+  hipStream_t s = (hipStream_t)stream;
+#define HMX_SSDD(TS)                                          \
+  if (P == 64 && N == 128) launch<TS, 64, 128>(p, batch, tied, s);        \
+  else if (P == 128 && N == 128) launch<TS, 128, 128>(p, batch, tied, s); \
+  else if (P == 64 && N == 64) launch<TS, 64, 64>(p, batch, tied, s);     \
+  else launch<TS, 128, 64>(p, batch, tied, s);
+  if (state_dtype == HMX_F32) { HMX_SSDD(float) } else { HMX_SSDD(bf16) }
+#undef HMX_SSDD
+  return check_launch("hmx_ssd_state_update");
+}

@@ -1,0 +1,525 @@
+// Mamba2 SSD chunk scan (mamba_chunk_scan_combined / _varlen) for gfx950:
+// bf16 x/B/C/z/y, fp32 dt math and fp32 states.
+//
+// Semantics (per head h, group g = h / (H/G), state S in R^{P x N}; the
+// reference calls sit at training/.../layers/mamba/mamba2.py:555-580 and
+// vllm-inference/src/primed_vllm/primed_mamba2_layer.py:844-863; the kernels
+// there are mamba_ssm 2.3.0 / vLLM 0.15.1, not vendored):
+//   dt'_t = clamp(softplus_20(dt_t + dt_bias_h), dt_min, dt_max)
+//   S_t   = e^{dt'_t A_h} S_{t-1} + dt'_t x_t B_t^T
+//   y_t   = S_t C_t + D_hp x_t ;  y_t *= z_t sigmoid(z_t) if z is given
+//
+// Chunked form over L = 64 tokens with a_t = dt'_t A_h and A_t = sum_{s<=t} a_s
+// (inclusive, from the chunk start):
+//   M[t][j] = (C_t . B_j) e^{A_t - A_j} dt'_j        (j <= t)
+//   Y       = diag(e^{A}) C S^T + M X  (+ D x, z gate)
+//   S^T    <- e^{A_L} S^T + B^T diag(dt' e^{A_L - A}) X
+// The state lives transposed (S^T, rows n, columns p) in MFMA accumulator
+// registers: wave w owns p-columns [16 PB w, 16 PB (w+1)) for every n, so the
+// C S^T product and the state update never leave the wave.  The state is linear
+// with a scalar decay per chunk, so a segment's start state is exact from a
+// scalar-decay combine of the other segments' zero-start end states (pass
+// LOCAL + combine, the carry of mamba_mixer_cp_utils.py:44-65).
+//
+// Numerics: x, B, C enter the MFMAs exactly (bf16 inputs); the fp32 factors
+// M, S and w x are each split into bf16 hi + lo so no product rounds them to
+// 8 bits (one rounding of M alone costs ~6e-3 absolute at |y| ~ 7).
+//
+// Workgroup order: the 1-D grid maps block ids so that the heads sharing one
+// B/C group and segment have ids equal mod 8, i.e. land on one XCD and share
+// its L2 for the B/C chunk reads.
+//
+// Roofline: HBM-bound at the C4 shape (x, y, B, C, dt and the final state move
+// once; the LOCAL pass re-reads x, B and dt of all but the last segment).
+#include "common.hpp"
+#include "mfma.hpp"
+
+namespace hmx {
+namespace ssd {
+
+constexpr int L = 64;          // tokens per chunk
+constexpr int NTHR = 256;
+constexpr int LDM = L + 8;     // bf16 [L][L] row stride of M
+
+enum Mode { MODE_OUT = 0, MODE_LOCAL = 1 };
+
+struct SegInfo { int n, bos, eos, c_start, c_end, seg_idx, first_seg, nseg; };
+
+struct Params {
+  const bf16* x; int64_t x_ts, x_hs;
+  const bf16* B; int64_t b_ts, b_gs;
+  const bf16* C; int64_t c_ts, c_gs;
+  const void* dt; int dt_dt; int64_t dt_ts, dt_hs;
+  const float* A;          // [H]
+  const float* D;          // [H][P] or null
+  const float* dt_bias;    // [H] or null
+  const bf16* z; int64_t z_ts, z_hs;   // or null
+  bf16* y; int64_t y_ts, y_hs;
+  const float* h0;         // [nseq][H][P][N] or null
+  float* hT;               // [nseq][H][P][N] or null
+  const int* seg; int nseg_total;
+  float* ws_loc;           // [nseg][H][P][N] zero-start segment end states
+  float* ws_s0;            // [nseg][H][P][N] segment start states
+  float* ws_dec;           // [nseg][H] segment log-decay sum_t a_t
+  int H, G, softplus;
+  float dt_min, dt_max;
+};
+
+template <int P, int N>
+struct Cfg {
+  static constexpr int LDX = P + 8;   // bf16 [L][P] (x, y / z staging)
+  static constexpr int LDB = N + 8;   // bf16 [L][N] (B, C)
+  static constexpr int PB = P / 64;   // 16-wide p-blocks per wave
+  static constexpr int NB = N / 16;   // 16-row n-blocks of S^T
+  static constexpr int VX = L * P / 8 / NTHR;   // 16-byte x vectors per thread
+  static constexpr int VB = L * N / 8 / NTHR;   // 16-byte B (or C) vectors per thread
+  static constexpr int OFF_X = 0;
+  static constexpr int OFF_B = OFF_X + L * LDX * 2;
+  static constexpr int OFF_C = OFF_B + L * LDB * 2;
+  static constexpr int OFF_M = OFF_C + L * LDB * 2;
+  static constexpr int OFF_Y = OFF_M + L * LDM * 2;
+  static constexpr int OFF_S = OFF_Y + L * LDX * 2;
+  static constexpr int SMEM = OFF_S + 4 * L * 4;
+  static_assert(SMEM <= 80 * 1024, "LDS budget: two workgroups per CU");
+  static_assert(P % 64 == 0 && N % 32 == 0, "tile shape");
+};
+
+// per-token scalar arrays (fp32 [L] each)
+enum { S_DT, S_ACS, S_W, S_EA };
+
+__device__ __forceinline__ float ld_any(const void* p, int64_t i, int dt) {
+  if (dt == HMX_F32) return static_cast<const float*>(p)[i];
+  if (dt == HMX_BF16) return (float)static_cast<const bf16*>(p)[i];
+  return (float)static_cast<const f16*>(p)[i];
+}
+
+__device__ __forceinline__ SegInfo load_seg(const int* seg, int s) {
+  const int* r = seg + s * 8;
+  return SegInfo{r[0], r[1], r[2], r[3], r[4], r[5], r[6], r[7]};
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ float scan64(float x, int lane) {
+  x = scan32(x);
+  const float lo = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 31));
+  return lane >= 32 ? x + lo : x;
+}
+
+template <int P, int N>
+struct Raw {
+  bf16x8 x[Cfg<P, N>::VX], z[Cfg<P, N>::VX], b[Cfg<P, N>::VB], c[Cfg<P, N>::VB];
+  float dt;
+};
+
+template <int P, int N, int MODE>
+__device__ __forceinline__ void load_raw(Raw<P, N>& r, const Params& p, int tok0, int nval,
+                                         int h, int g, int tid) {
+  using K = Cfg<P, N>;
+#pragma unroll
+  for (int i = 0; i < K::VX; ++i) {
+    const int e = tid + NTHR * i, row = e / (P / 8), c8 = (e % (P / 8)) * 8;
+    const bool ok = row < nval;
+    const int64_t tok = tok0 + row;
+    r.x[i] = ok ? *reinterpret_cast<const bf16x8*>(p.x + tok * p.x_ts + h * p.x_hs + c8) : bf16x8{};
+    if (MODE == MODE_OUT)
+      r.z[i] = (ok && p.z) ? *reinterpret_cast<const bf16x8*>(p.z + tok * p.z_ts + h * p.z_hs + c8)
+                           : bf16x8{};
+  }
+#pragma unroll
+  for (int i = 0; i < K::VB; ++i) {
+    const int e = tid + NTHR * i, row = e / (N / 8), c8 = (e % (N / 8)) * 8;
+    const bool ok = row < nval;
+    const int64_t tok = tok0 + row;
+    r.b[i] = ok ? *reinterpret_cast<const bf16x8*>(p.B + tok * p.b_ts + g * p.b_gs + c8) : bf16x8{};
+    if (MODE == MODE_OUT)
+      r.c[i] = ok ? *reinterpret_cast<const bf16x8*>(p.C + tok * p.c_ts + g * p.c_gs + c8) : bf16x8{};
+  }
+  if (tid < L)
+    r.dt = tid < nval ? ld_any(p.dt, (int64_t)(tok0 + tid) * p.dt_ts + h * p.dt_hs, p.dt_dt) : 0.f;
+}
+
+template <int P, int N, int MODE>
+__global__ __launch_bounds__(NTHR, 2) void ssd_chunk_kernel(Params p) {
+  using K = Cfg<P, N>;
+  constexpr int LDX = K::LDX, LDB = K::LDB, PB = K::PB, NB = K::NB;
+  __shared__ __align__(16) unsigned char smem[K::SMEM];
+  bf16* sX = reinterpret_cast<bf16*>(smem + K::OFF_X);
+  bf16* sB = reinterpret_cast<bf16*>(smem + K::OFF_B);
+  bf16* sC = reinterpret_cast<bf16*>(smem + K::OFF_C);
+  bf16* sM = reinterpret_cast<bf16*>(smem + K::OFF_M);
+  bf16* sY = reinterpret_cast<bf16*>(smem + K::OFF_Y);
+  float* sc = reinterpret_cast<float*>(smem + K::OFF_S);
+  auto SC = [&](int slot, int t) -> float& { return sc[slot * L + t]; };
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int q4 = lane >> 4, l16 = lane & 15;
+  // XCD-aware block order: ids of the heads of one (segment, group) agree mod 8.
+  const int H = p.H, G = p.G, HG = H / G;
+  const int id = blockIdx.x, sg = id % (p.nseg_total * G);
+  const int s_id = sg / G, g = sg % G, h = g * HG + id / (p.nseg_total * G);
+  const SegInfo si = load_seg(p.seg, s_id);
+  if (MODE == MODE_LOCAL && si.seg_idx == si.nseg - 1) return;
+
+  const float A_h = p.A[h];
+  const float bias = p.dt_bias ? p.dt_bias[h] : 0.f;
+
+  // ---- initial state S^T: tile (nb, i) holds rows n = 16nb+4q4+v, column
+  // p = 16(PB wave + i) + l16 --------------------------------------------------
+  f32x4 ST[NB][PB];
+  {
+    const float* src = nullptr;
+    if (MODE == MODE_OUT) {
+      if (si.seg_idx == 0) {
+        if (p.h0) src = p.h0 + ((int64_t)si.n * H + h) * P * N;
+      } else {
+        src = p.ws_s0 + ((int64_t)s_id * H + h) * P * N;
+      }
+    }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int i = 0; i < PB; ++i) {
+        const int pc = 16 * (PB * wave + i) + l16;
+        ST[nb][i] = src ? *reinterpret_cast<const f32x4*>(src + (int64_t)pc * N + 16 * nb + 4 * q4)
+                        : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+  }
+  float dsum = 0.f;   // segment log-decay (LOCAL)
+
+  Raw<P, N> raw;
+  if (si.c_start < si.c_end) {
+    const int tok0 = si.bos + si.c_start * L;
+    load_raw<P, N, MODE>(raw, p, tok0, min(L, si.eos - tok0), h, g, tid);
+  }
+
+  for (int c = si.c_start; c < si.c_end; ++c) {
+    const int tok0 = si.bos + c * L;
+    const int nval = min(L, si.eos - tok0);
+    // ---- stage the prefetched chunk -----------------------------------------
+#pragma unroll
+    for (int i = 0; i < K::VX; ++i) {
+      const int e = tid + NTHR * i, row = e / (P / 8), c8 = (e % (P / 8)) * 8;
+      *reinterpret_cast<bf16x8*>(sX + row * LDX + c8) = raw.x[i];
+    }
+#pragma unroll
+    for (int i = 0; i < K::VB; ++i) {
+      const int e = tid + NTHR * i, row = e / (N / 8), c8 = (e % (N / 8)) * 8;
+      *reinterpret_cast<bf16x8*>(sB + row * LDB + c8) = raw.b[i];
+      if (MODE == MODE_OUT) *reinterpret_cast<bf16x8*>(sC + row * LDB + c8) = raw.c[i];
+    }
+    bf16x8 zst[K::VX];
+    if (MODE == MODE_OUT) {
+#pragma unroll
+      for (int i = 0; i < K::VX; ++i) zst[i] = raw.z[i];
+    }
+    if (wave == 0) {
+      float d = raw.dt + bias;
+      if (p.softplus) d = d <= 20.f ? log1pf(expf(d)) : d;
+      d = fminf(fmaxf(d, p.dt_min), p.dt_max);
+      if (lane >= nval) d = 0.f;
+      const float acs = scan64(d * A_h, lane);
+      const float al = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acs), 63));
+      SC(S_DT, lane) = d;
+      SC(S_ACS, lane) = acs;
+      SC(S_W, lane) = d * fast_exp(al - acs);
+      SC(S_EA, lane) = fast_exp(acs);
+    }
+    if (c + 1 < si.c_end) {
+      const int t1 = tok0 + L;
+      load_raw<P, N, MODE>(raw, p, t1, min(L, si.eos - t1), h, g, tid);
+    }
+    lds_barrier();
+    const float al = SC(S_ACS, L - 1);
+
+    if (MODE == MODE_OUT) {
+      // z into the y staging buffer (read back in C layout by the owner lanes)
+#pragma unroll
+      for (int i = 0; i < K::VX; ++i) {
+        const int e = tid + NTHR * i, row = e / (P / 8), c8 = (e % (P / 8)) * 8;
+        *reinterpret_cast<bf16x8*>(sY + row * LDX + c8) = zst[i];
+      }
+      // ---- Y = diag(e^A) C S^T (S as bf16 hi + lo) ------------------------------
+      f32x4 Y[4][PB];
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+        for (int i = 0; i < PB; ++i) Y[tb][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < N / 32; ++ks) {
+        bf16x8 bh[PB], bl[PB];
+#pragma unroll
+        for (int i = 0; i < PB; ++i) pack_b_hilo(ST[2 * ks][i], ST[2 * ks + 1][i], bh[i], bl[i]);
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) {
+          const bf16x8 a = frag_perm(sC, LDB, 16 * tb, 32 * ks, lane);
+#pragma unroll
+          for (int i = 0; i < PB; ++i) {
+            Y[tb][i] = mfma16(a, bh[i], Y[tb][i]);
+            Y[tb][i] = mfma16(a, bl[i], Y[tb][i]);
+          }
+        }
+      }
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float e = SC(S_EA, 16 * tb + 4 * q4 + v);
+#pragma unroll
+          for (int i = 0; i < PB; ++i) Y[tb][i][v] *= e;
+        }
+      // ---- M = (C B^T) o decay o dt as bf16 hi + lo (lower tiles; (0,1), (2,3)
+      // zeroed).  Tiles per wave: w0 (0,0)(1,0)(2,0)+zero(0,1);
+      // w1 (1,1)(2,1)(3,0)+zero(2,3); w2 (2,2)(3,1); w3 (3,2)(3,3) -------------
+      constexpr int TT[4][3][2] = {{{0, 0}, {1, 0}, {2, 0}}, {{1, 1}, {2, 1}, {3, 0}},
+                                   {{2, 2}, {3, 1}, {-1, -1}}, {{3, 2}, {3, 3}, {-1, -1}}};
+      bf16x4 mh[3], ml[3];
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        const int tb = TT[wave][k][0], jb = TT[wave][k][1];
+        if (tb < 0) continue;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < N / 32; ++ks)
+          acc = mfma16(frag(sC, LDB, 16 * tb, 32 * ks, lane), frag(sB, LDB, 16 * jb, 32 * ks, lane), acc);
+        const int j = 16 * jb + l16;
+        const float aj = SC(S_ACS, j), dj = SC(S_DT, j);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int t = 16 * tb + 4 * q4 + v;
+          const float m = (t >= j) ? acc[v] * fast_exp(SC(S_ACS, t) - aj) * dj : 0.f;
+          mh[k][v] = (bf16)m;
+          ml[k][v] = (bf16)(m - (float)mh[k][v]);
+        }
+      }
+      lds_barrier();   // every wave is done with sC: its space takes the M low parts
+      bf16* sML = sC;
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        const int tb = TT[wave][k][0], jb = TT[wave][k][1];
+        if (tb < 0) continue;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int a = (16 * tb + 4 * q4 + v) * LDM + 16 * jb + l16;
+          sM[a] = mh[k][v];
+          sML[a] = ml[k][v];
+        }
+      }
+      if (wave < 2) {
+        const int tb = wave == 0 ? 0 : 2;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int a = (16 * tb + 4 * q4 + v) * LDM + 16 * (tb + 1) + l16;
+          sM[a] = (bf16)0.f;
+          sML[a] = (bf16)0.f;
+        }
+      }
+      lds_barrier();
+
+      // ---- Y += M X (+ D x, z gate) ----------------------------------------------
+      bf16x8 bx[2][PB];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int i = 0; i < PB; ++i) bx[ks][i] = frag_t(sX, LDX, 32 * ks, 16 * (PB * wave + i), lane);
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+        for (int ks = 0; ks <= tb / 2; ++ks) {
+          const bf16x8 ah = frag(sM, LDM, 16 * tb, 32 * ks, lane);
+          const bf16x8 a_l = frag(sML, LDM, 16 * tb, 32 * ks, lane);
+#pragma unroll
+          for (int i = 0; i < PB; ++i) {
+            Y[tb][i] = mfma16(ah, bx[ks][i], Y[tb][i]);
+            Y[tb][i] = mfma16(a_l, bx[ks][i], Y[tb][i]);
+          }
+        }
+#pragma unroll
+      for (int i = 0; i < PB; ++i) {
+        const int pc = 16 * (PB * wave + i);
+        const float dv = p.D ? p.D[h * P + pc + l16] : 0.f;
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) {
+          const bf16x4 xv = ld_tr(sX, LDX, 16 * tb + 4 * q4, pc, lane);
+          bf16x4 zv;
+          if (p.z) zv = ld_tr(sY, LDX, 16 * tb + 4 * q4, pc, lane);
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            float yv = Y[tb][i][v] + dv * (float)xv[v];
+            if (p.z) {
+              const float zz = (float)zv[v];
+              yv *= zz / (1.f + fast_exp(-zz));
+            }
+            sY[(16 * tb + 4 * q4 + v) * LDX + pc + l16] = (bf16)yv;
+          }
+        }
+      }
+    }
+
+    // ---- S^T <- e^{A_L} S^T + B^T diag(w) X ------------------------------------
+    {
+      const float ea = fast_exp(al);
+      dsum += al;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int i = 0; i < PB; ++i)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) ST[nb][i][v] *= ea;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        float w[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) w[j] = SC(S_W, 32 * ks + 8 * q4 + j);
+        // w x as bf16 hi + lo: one rounding of it would cost ~1e-3 of |S|
+        bf16x8 bwh[PB], bwl[PB];
+#pragma unroll
+        for (int i = 0; i < PB; ++i) {
+          const bf16x8 xr = frag_t(sX, LDX, 32 * ks, 16 * (PB * wave + i), lane);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float f = (float)xr[j] * w[j];
+            bwh[i][j] = (bf16)f;
+            bwl[i][j] = (bf16)(f - (float)bwh[i][j]);
+          }
+        }
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          const bf16x8 a = frag_t(sB, LDB, 32 * ks, 16 * nb, lane);
+#pragma unroll
+          for (int i = 0; i < PB; ++i) {
+            ST[nb][i] = mfma16(a, bwh[i], ST[nb][i]);
+            ST[nb][i] = mfma16(a, bwl[i], ST[nb][i]);
+          }
+        }
+      }
+    }
+    lds_barrier();
+
+    if (MODE == MODE_OUT) {
+      // ---- coalesced y store ----------------------------------------------------
+#pragma unroll
+      for (int i = 0; i < K::VX; ++i) {
+        const int e = tid + NTHR * i, row = e / (P / 8), c8 = (e % (P / 8)) * 8;
+        if (row < nval)
+          *reinterpret_cast<bf16x8*>(p.y + (int64_t)(tok0 + row) * p.y_ts + h * p.y_hs + c8) =
+              *reinterpret_cast<const bf16x8*>(sY + row * LDX + c8);
+      }
+    }
+  }
+
+  // ---- segment end state --------------------------------------------------------
+  float* dst = nullptr;
+  if (MODE == MODE_LOCAL) {
+    dst = p.ws_loc + ((int64_t)s_id * H + h) * P * N;
+    if (tid == 0) p.ws_dec[(int64_t)s_id * H + h] = dsum;
+  } else if (si.seg_idx == si.nseg - 1 && p.hT) {
+    dst = p.hT + ((int64_t)si.n * H + h) * P * N;
+  }
+  if (dst) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int i = 0; i < PB; ++i) {
+        const int pc = 16 * (PB * wave + i) + l16;
+        *reinterpret_cast<f32x4*>(dst + (int64_t)pc * N + 16 * nb + 4 * q4) = ST[nb][i];
+      }
+  }
+}
+
+// Segment start states: S0[first] = h0 (or 0); S0[s+1] = e^{dec[s]} S0[s] + loc[s].
+__global__ __launch_bounds__(256) void ssd_seg_combine_kernel(Params p, int PN) {
+  const int nh = blockIdx.x, H = p.H;
+  const int n = nh / H, h = nh % H;
+  int first = -1, nseg = 0;
+  for (int s = 0; s < p.nseg_total; ++s) {
+    const SegInfo si = load_seg(p.seg, s);
+    if (si.n == n) { first = si.first_seg; nseg = si.nseg; break; }
+  }
+  if (first < 0 || nseg < 2) return;
+  for (int e = blockIdx.y * 256 + threadIdx.x; e < PN; e += gridDim.y * 256) {
+    float sx = p.h0 ? p.h0[((int64_t)n * H + h) * PN + e] : 0.f;
+    for (int s = 0; s < nseg - 1; ++s) {
+      const int64_t b = (int64_t)(first + s) * H + h;
+      sx = sx * expf(p.ws_dec[b]) + p.ws_loc[b * PN + e];
+      p.ws_s0[((int64_t)(first + s + 1) * H + h) * PN + e] = sx;
+    }
+  }
+}
+
+template <int P, int N>
+void launch(const Params& p, int nseq, hipStream_t s) {
+  const bool multi = p.nseg_total > nseq;
+  const dim3 grid(p.nseg_total * p.H);
+  if (multi) {
+    hipLaunchKernelGGL((ssd_chunk_kernel<P, N, MODE_LOCAL>), grid, dim3(NTHR), 0, s, p);
+    hipLaunchKernelGGL(ssd_seg_combine_kernel, dim3(nseq * p.H, (P * N + 1023) / 1024), dim3(256),
+                       0, s, p, P * N);
+  }
+  hipLaunchKernelGGL((ssd_chunk_kernel<P, N, MODE_OUT>), grid, dim3(NTHR), 0, s, p);
+}
+
+}  // namespace ssd
+}  // namespace hmx
+
+using namespace hmx;
+using namespace hmx::ssd;
+
+extern "C" size_t hmx_ssd_chunk_workspace_bytes(int32_t nseg_total, int32_t nseq, int32_t H,
+                                                int32_t P, int32_t N) {
+  if (nseg_total <= nseq) return 16;
+  const size_t st = (size_t)nseg_total * H * P * N * sizeof(float);
+  return 2 * st + (size_t)nseg_total * H * sizeof(float);
+}
+
+extern "C" int hmx_ssd_chunk_fwd(const void* x, int64_t x_ts, int64_t x_hs, const void* B,
+                                 int64_t b_ts, int64_t b_gs, const void* C, int64_t c_ts,
+                                 int64_t c_gs, int32_t xbc_dtype, const void* dt, int32_t dt_dtype,
+                                 int64_t dt_ts, int64_t dt_hs, const float* A, const float* D,
+                                 const float* dt_bias, const void* z, int64_t z_ts, int64_t z_hs,
+                                 void* y, int64_t y_ts, int64_t y_hs, const float* h0,
+                                 float* h_final, const int32_t* seg_table, int32_t nseg_total,
+                                 int32_t nseq, int32_t H, int32_t G, int32_t P, int32_t N,
+                                 int32_t dt_softplus, float dt_min, float dt_max, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+  HMX_REQUIRE(xbc_dtype == HMX_BF16, HMX_EUNSUPPORTED,
+              "hmx_ssd_chunk_fwd: x/B/C/z must be bfloat16 (got dtype code %d)", xbc_dtype);
+  HMX_REQUIRE((P == 64 || P == 128) && (N == 64 || N == 128), HMX_EUNSUPPORTED,
+              "hmx_ssd_chunk_fwd: headdim in {64,128} and d_state in {64,128} (got %d, %d)", P, N);
+  HMX_REQUIRE(H > 0 && G > 0 && H % G == 0, HMX_EINVAL, "hmx_ssd_chunk_fwd: H=%d G=%d", H, G);
+  HMX_REQUIRE(x && B && C && dt && A && y && seg_table, HMX_EINVAL,
+              "hmx_ssd_chunk_fwd: null tensor pointer");
+  HMX_REQUIRE(dt_dtype == HMX_F32 || dt_dtype == HMX_BF16 || dt_dtype == HMX_F16, HMX_EINVAL,
+              "hmx_ssd_chunk_fwd: dt dtype code %d", dt_dtype);
+  const int64_t strides[] = {x_ts, x_hs, b_ts, b_gs, c_ts, c_gs, y_ts, y_hs,
+                             z ? z_ts : 8, z ? z_hs : 8};
+  for (int64_t st : strides)
+    HMX_REQUIRE(st % 8 == 0, HMX_EINVAL,
+                "hmx_ssd_chunk_fwd: token/head strides must be multiples of 8 elements");
+  if (nseg_total == 0) return HMX_OK;
+  const size_t need = hmx_ssd_chunk_workspace_bytes(nseg_total, nseq, H, P, N);
+  HMX_REQUIRE(workspace && workspace_bytes >= need, HMX_EINVAL,
+              "hmx_ssd_chunk_fwd: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  Params p;
+  p.x = static_cast<const bf16*>(x); p.x_ts = x_ts; p.x_hs = x_hs;
+  p.B = static_cast<const bf16*>(B); p.b_ts = b_ts; p.b_gs = b_gs;
+  p.C = static_cast<const bf16*>(C); p.c_ts = c_ts; p.c_gs = c_gs;
+  p.dt = dt; p.dt_dt = dt_dtype; p.dt_ts = dt_ts; p.dt_hs = dt_hs;
+  p.A = A; p.D = D; p.dt_bias = dt_bias;
+  p.z = static_cast<const bf16*>(z); p.z_ts = z_ts; p.z_hs = z_hs;
+  p.y = static_cast<bf16*>(y); p.y_ts = y_ts; p.y_hs = y_hs;
+  p.h0 = h0; p.hT = h_final;
+  p.seg = seg_table; p.nseg_total = nseg_total;
+  const bool multi = nseg_total > nseq;
+  const size_t st = (size_t)nseg_total * H * P * N;
+  float* ws = static_cast<float*>(workspace);
+  p.ws_loc = multi ? ws : nullptr;
+  p.ws_s0 = multi ? ws + st : nullptr;
+  p.ws_dec = multi ? ws + 2 * st : nullptr;
+  p.H = H; p.G = G; p.softplus = dt_softplus; p.dt_min = dt_min; p.dt_max = dt_max;
+  hipStream_t s = (hipStream_t)stream;
+  if (P == 64 && N == 128) launch<64, 128>(p, nseq, s);
+  else if (P == 128 && N == 128) launch<128, 128>(p, nseq, s);
+  else if (P == 64 && N == 64) launch<64, 64>(p, nseq, s);
+  else launch<128, 64>(p, nseq, s);
+  return check_launch("hmx_ssd_chunk_fwd");
+}

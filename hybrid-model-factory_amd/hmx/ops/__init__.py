@@ -3,6 +3,8 @@ from .gdn import (chunk_gated_delta_rule, chunk_gated_delta_rule_gqa, fused_gdn_
                   fused_recurrent_gated_delta_rule, fused_recurrent_gated_delta_rule_gqa)
 from .gka import (chebyshev_iteration_gqa, fused_gka_gating, gka_chebyshev_gla_decode,
                   gka_chebyshev_gla_prefill)
+from .ssd import (mamba_chunk_scan_combined, mamba_chunk_scan_combined_varlen,
+                  selective_state_update)
 
 __all__ = [
     "fused_gdn_gating",
@@ -14,4 +16,7 @@ __all__ = [
     "chebyshev_iteration_gqa",
     "gka_chebyshev_gla_decode",
     "gka_chebyshev_gla_prefill",
+    "mamba_chunk_scan_combined",
+    "mamba_chunk_scan_combined_varlen",
+    "selective_state_update",
 ]

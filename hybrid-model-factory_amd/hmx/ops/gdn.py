@@ -174,9 +174,10 @@ def _cu_count(device: torch.device) -> int:
 
 
 def _segment_table(bounds: list[tuple[int, int]], H: int, workgroups: int,
-                   segment_chunks: int | None = None) -> list[list[int]]:
-    """Rows (n, bos, eos, c_start, c_end, seg_idx, first_seg, nseg) for every sequence."""
-    chunks = [-(-(eos - bos) // CHUNK) for bos, eos in bounds]
+                   segment_chunks: int | None = None, chunk: int = CHUNK) -> list[list[int]]:
+    """Rows (n, bos, eos, c_start, c_end, seg_idx, first_seg, nseg) for every sequence,
+    over ``chunk``-token chunks."""
+    chunks = [-(-(eos - bos) // chunk) for bos, eos in bounds]
     if segment_chunks is None:
         total = max(1, sum(chunks))
         segment_chunks = max(MIN_SEGMENT_CHUNKS, -(-total * H // max(1, workgroups)))

@@ -1,0 +1,274 @@
+"""Mamba2 SSD ops: chunk scan (mamba_ssm and vLLM-varlen signatures) and the
+single-token selective_state_update, on the HIP kernels in libhmx.so.
+
+The reference calls un-vendored kernels (mamba_ssm 2.3.0, vLLM 0.15.1) from
+  training/src/hmf/model/hybrid_zoo/layers/mamba/mamba2.py:555-580 (scan),
+  :776-800 (decode step), and
+  vllm-inference/src/primed_vllm/primed_mamba2_layer.py:844-863 (varlen scan),
+  :1000-1021 (decode step).
+These wrappers keep those names, argument orders, defaults and return shapes.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+from .gdn import _cu_count, _segment_table
+
+SSD_CHUNK = 64                 # the kernel's internal chunk length (tokens)
+SSD_WORKGROUPS_PER_CU = 2
+PAD_SLOT_ID = -1
+
+
+def _vec_ok(t: torch.Tensor, dims: tuple[int, ...]) -> bool:
+    """Last dim contiguous, the given dims' strides multiples of 8, 16-byte base."""
+    return (t.stride(-1) == 1 and all(t.stride(d) % 8 == 0 for d in dims)
+            and t.data_ptr() % 16 == 0)
+
+
+def _tokens_view(t: torch.Tensor) -> torch.Tensor:
+    """[b, l, ...] -> [b*l, ...] as a view when the batch dim steps over whole rows."""
+    b, l = t.shape[0], t.shape[1]
+    if b == 1 or t.stride(0) == l * t.stride(1):
+        return t.as_strided((b * l, *t.shape[2:]), (t.stride(1), *t.stride()[2:]),
+                            t.storage_offset())
+    return t.contiguous().view(b * l, *t.shape[2:])
+
+
+def _prep3(t: torch.Tensor) -> torch.Tensor:
+    """[tokens, heads, dim] with vector-friendly strides (copy only if needed)."""
+    return t if _vec_ok(t, (0, 1)) else t.contiguous()
+
+
+def _ssd_scan(x, dt, A, B, C, D, z, dt_bias, dt_softplus, dt_limit, bounds, h0, y,
+              want_final: bool, segment_chunks=None):
+    """Core launcher over flattened tokens.  x, z, y [T,H,P]; dt [T,H]; B, C [T,G,N];
+    bounds: list of (bos, eos); h0 fp32 [nseq,H,P,N] or None.  Returns the fp32 end
+    states [nseq,H,P,N] (or None)."""
+    T, H, P = x.shape
+    G, N = B.shape[1], B.shape[2]
+    if x.dtype != torch.bfloat16 or B.dtype != torch.bfloat16 or C.dtype != torch.bfloat16:
+        raise NotImplementedError("hmx SSD scan: x, B and C must be bfloat16 "
+                                  f"(got {x.dtype}, {B.dtype}, {C.dtype})")
+    if z is not None and z.dtype != torch.bfloat16:
+        z = z.to(torch.bfloat16)
+    if H % G != 0:
+        raise ValueError(f"nheads {H} must be a multiple of ngroups {G}")
+    x, B, C, y = _prep3(x), _prep3(B), _prep3(C), y
+    z = None if z is None else _prep3(z)
+    if not _vec_ok(y, (0, 1)):
+        raise ValueError("output tensor must have a contiguous last dim and 8-element strides")
+    A32 = A.to(torch.float32).contiguous()
+    Dm = None
+    if D is not None:
+        Dm = (D.to(torch.float32)[:, None].expand(H, P) if D.dim() == 1
+              else D.to(torch.float32)).contiguous()
+    bias = None if dt_bias is None else dt_bias.to(torch.float32).contiguous()
+    nseq = len(bounds)
+    hT = torch.empty(nseq, H, P, N, dtype=torch.float32, device=x.device) if want_final else None
+    rows = _segment_table(bounds, H, SSD_WORKGROUPS_PER_CU * _cu_count(x.device), segment_chunks,
+                          chunk=SSD_CHUNK)
+    seg = torch.tensor(rows, dtype=torch.int32).to(x.device, non_blocking=True)
+    lib = _lib.load()
+    ws_bytes = int(lib.hmx_ssd_chunk_workspace_bytes(len(rows), nseq, H, P, N))
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=x.device)
+    lo, hi = float(dt_limit[0]), float(dt_limit[1])
+    _lib.call("hmx_ssd_chunk_fwd",
+              _lib.ptr(x), x.stride(0), x.stride(1), _lib.ptr(B), B.stride(0), B.stride(1),
+              _lib.ptr(C), C.stride(0), C.stride(1), _lib.dtype_code(x),
+              _lib.ptr(dt), _lib.dtype_code(dt), dt.stride(0), dt.stride(1),
+              _lib.ptr(A32), _lib.ptr(Dm), _lib.ptr(bias),
+              _lib.ptr(z), 0 if z is None else z.stride(0), 0 if z is None else z.stride(1),
+              _lib.ptr(y), y.stride(0), y.stride(1), _lib.ptr(h0), _lib.ptr(hT),
+              _lib.ptr(seg), len(rows), nseq, H, G, P, N, int(bool(dt_softplus)), lo, hi,
+              _lib.ptr(ws), ws.numel(), _lib.stream_of(x))
+    return hT
+
+
+def _runs(row: list[int]) -> list[tuple[int, int]]:
+    out, a = [], 0
+    for i in range(1, len(row) + 1):
+        if i == len(row) or row[i] != row[a]:
+            out.append((a, i))
+            a = i
+    return out
+
+
+def mamba_chunk_scan_combined(x, dt, A, B, C, chunk_size, D=None, z=None, dt_bias=None,
+                              initial_states=None, seq_idx=None, cu_seqlens=None,
+                              dt_softplus=False, dt_limit=(0.0, float("inf")),
+                              return_final_states=False, return_varlen_states=False, *,
+                              _segment_chunks: int | None = None):
+    """mamba_ssm ``mamba_chunk_scan_combined`` (call site mamba2.py:555-580).
+
+    x [b,l,H,P] bf16; dt [b,l,H]; A [H]; B, C [b,l,G,N] bf16; D [H] or [H,P];
+    z [b,l,H,P]; dt_bias [H]; initial_states [b,H,P,N] (seeds the first sequence of
+    each row); seq_idx [b,l] (the state restarts where it changes; without it,
+    cu_seqlens boundaries restart it); cu_seqlens [n+1] with b == 1 selects the
+    varlen_states (state after each sequence's last token).  Returns y
+    [b,l,H,P] (x.dtype), then final_states [b,H,P,N] fp32 if return_final_states,
+    then varlen_states [n,H,P,N] fp32 if return_varlen_states.  chunk_size is
+    accepted for signature compatibility: the kernel tiles by 64 tokens and the
+    result does not depend on the chunking beyond fp32 rounding.
+    """
+    if return_varlen_states and cu_seqlens is None:
+        raise ValueError("return_varlen_states requires cu_seqlens")
+    if cu_seqlens is not None and x.shape[0] != 1:
+        raise ValueError(f"cu_seqlens needs batch size 1, got {x.shape[0]}")
+    _lib.require_gpu(x, dt, A, B, C, D, z, dt_bias, initial_states, seq_idx, cu_seqlens)
+    b, l, H, P = x.shape
+    G, N = B.shape[2], B.shape[3]
+    if initial_states is not None and tuple(initial_states.shape) != (b, H, P, N):
+        raise ValueError(f"initial_states must be {(b, H, P, N)}, got {tuple(initial_states.shape)}")
+    # sequences over the flattened token axis
+    runs_per_row: list[list[tuple[int, int]]] = []
+    if seq_idx is not None:
+        rows = seq_idx.to(torch.int64).cpu().tolist()
+        runs_per_row = [_runs(r) for r in rows]
+    elif cu_seqlens is not None:
+        cs = [int(v) for v in cu_seqlens.tolist()]
+        runs_per_row = [[(cs[i], cs[i + 1]) for i in range(len(cs) - 1) if cs[i + 1] > cs[i]]]
+    else:
+        runs_per_row = [[(0, l)] for _ in range(b)]
+    bounds, first_of_row, last_of_row, end_at = [], [], [], {}
+    for r, runs in enumerate(runs_per_row):
+        first_of_row.append(len(bounds) if runs and runs[0][0] == 0 else -1)
+        for s0, s1 in runs:
+            end_at[(r, s1)] = len(bounds)
+            bounds.append((r * l + s0, r * l + s1))
+        last_of_row.append(len(bounds) - 1 if runs else -1)
+    h0 = None
+    if initial_states is not None:
+        h0 = torch.zeros(len(bounds), H, P, N, dtype=torch.float32, device=x.device)
+        for r, f in enumerate(first_of_row):
+            if f >= 0:
+                h0[f] = initial_states[r].to(torch.float32)
+    xf, zf = _tokens_view(x), (None if z is None else _tokens_view(z))
+    y = torch.empty(b, l, H, P, dtype=x.dtype, device=x.device)
+    want = return_final_states or return_varlen_states
+    hT = _ssd_scan(xf, _tokens_view(dt), A, _tokens_view(B), _tokens_view(C), D, zf, dt_bias,
+                   dt_softplus, dt_limit, bounds, h0, y.view(b * l, H, P), want, _segment_chunks)
+    out = [y]
+    if return_final_states:
+        fin = torch.zeros(b, H, P, N, dtype=torch.float32, device=x.device)
+        for r, i in enumerate(last_of_row):
+            if i >= 0:
+                fin[r] = hT[i]
+            elif initial_states is not None:
+                fin[r] = initial_states[r].to(torch.float32)
+        out.append(fin)
+    if return_varlen_states:
+        cs = [int(v) for v in cu_seqlens.tolist()]
+        idx = []
+        for i in range(len(cs) - 1):
+            if (0, cs[i + 1]) not in end_at or cs[i + 1] == cs[i]:
+                raise ValueError("cu_seqlens boundaries must coincide with the scan's sequences")
+            idx.append(end_at[(0, cs[i + 1])])
+        out.append(hT[torch.tensor(idx, device=x.device)])
+    return out[0] if len(out) == 1 else tuple(out)
+
+
+def mamba_chunk_scan_combined_varlen(x, dt, A, B, C, chunk_size, cu_seqlens, cu_chunk_seqlens=None,
+                                     last_chunk_indices=None, seq_idx=None, out=None, D=None,
+                                     z=None, dt_bias=None, initial_states=None, dt_softplus=False,
+                                     dt_limit=(0.0, float("inf")),
+                                     return_intermediate_states=False, state_dtype=None, *,
+                                     _segment_chunks: int | None = None):
+    """vLLM ``mamba_chunk_scan_combined_varlen`` (call site primed_mamba2_layer.py:844-863).
+
+    x [T,H,P] bf16; dt [T,H]; A [H]; B, C [T,G,N] bf16; cu_seqlens [n+1];
+    initial_states [n,H,P,N] or None (each sequence starts from its own state);
+    ``out`` [T,H,P] is written in place (allocated when None).  Returns
+    varlen_states [n,H,P,N] in state_dtype (fp32 when None).  cu_chunk_seqlens,
+    last_chunk_indices and seq_idx are chunking metadata derived from
+    cu_seqlens; the kernel uses its own 64-token chunks.  Per-chunk
+    (return_intermediate_states) output is not supported.
+    """
+    if return_intermediate_states:
+        raise NotImplementedError("return_intermediate_states (prefix-cache chunk states) is "
+                                  "not supported by the hmx SSD scan")
+    _lib.require_gpu(x, dt, A, B, C, D, z, dt_bias, initial_states, cu_seqlens, out)
+    T, H, P = x.shape
+    N = B.shape[-1]
+    cs = [int(v) for v in cu_seqlens.tolist()]
+    bounds = [(cs[i], cs[i + 1]) for i in range(len(cs) - 1)]
+    if initial_states is not None and tuple(initial_states.shape) != (len(bounds), H, P, N):
+        raise ValueError(f"initial_states must be {(len(bounds), H, P, N)}, "
+                         f"got {tuple(initial_states.shape)}")
+    h0 = None if initial_states is None else initial_states.to(torch.float32).contiguous()
+    if out is None:
+        out = torch.empty(T, H, P, dtype=x.dtype, device=x.device)
+    if out.dtype != x.dtype:
+        raise ValueError(f"out dtype {out.dtype} must match x dtype {x.dtype}")
+    hT = _ssd_scan(x, dt, A, B, C, D, z, dt_bias, dt_softplus, dt_limit, bounds, h0, out, True,
+                   _segment_chunks)
+    return hT if state_dtype in (None, torch.float32) else hT.to(state_dtype)
+
+
+def selective_state_update(state, x, dt, A, B, C, D=None, z=None, dt_bias=None,
+                           dt_softplus=False, state_batch_indices=None,
+                           dst_state_batch_indices=None, pad_slot_id=PAD_SLOT_ID, out=None,
+                           num_accepted_tokens=None, cu_seqlens=None):
+    """mamba_ssm / vLLM ``selective_state_update``: one decode step, in place on
+    ``state`` (calls mamba2.py:789-800, primed_mamba2_layer.py:1007-1021).
+
+    state [slots,H,P,N] (or [slots,P,N]); x, dt [b,H,P] (or [b,P]); A [H,P,N];
+    B, C [b,G,N] (or [b,N]); D, dt_bias [H,P]; z [b,H,P]; state_batch_indices
+    [b] (entries equal to pad_slot_id are skipped); dst_state_batch_indices [b]
+    (write target, default the source slot).  ``out`` is written in place
+    (allocated like x when None) and returned.
+    """
+    if num_accepted_tokens is not None or cu_seqlens is not None:
+        raise NotImplementedError("multi-token (speculative) selective_state_update is not "
+                                  "supported by hmx")
+    _lib.require_gpu(state, x, dt, A, B, C, D, z, dt_bias, state_batch_indices,
+                     dst_state_batch_indices, out)
+    if state.dim() == 3:   # no head dim
+        state, x, dt, A = state.unsqueeze(1), x.unsqueeze(1), dt.unsqueeze(1), A.unsqueeze(0)
+        B, C = B.unsqueeze(1), C.unsqueeze(1)
+        D = None if D is None else D.unsqueeze(0)
+        z = None if z is None else z.unsqueeze(1)
+        dt_bias = None if dt_bias is None else dt_bias.unsqueeze(0)
+        if out is not None:
+            out = out.unsqueeze(1)
+    slots, H, P, N = state.shape
+    bsz = x.shape[0]
+    G = B.shape[1]
+    if tuple(x.shape) != (bsz, H, P) or tuple(dt.shape) != (bsz, H, P):
+        raise ValueError(f"x and dt must be {(bsz, H, P)}, got {tuple(x.shape)}, {tuple(dt.shape)}")
+    if tuple(A.shape) != (H, P, N):
+        raise ValueError(f"A must be {(H, P, N)}, got {tuple(A.shape)}")
+    if H % G != 0 or tuple(B.shape) != (bsz, G, N) or tuple(C.shape) != (bsz, G, N):
+        raise ValueError(f"B, C must be [{bsz}, G, {N}] with G dividing {H}")
+    if state.stride(3) != 1 or state.stride(2) != N or state.stride(1) != P * N:
+        raise ValueError("state must be contiguous within a slot ([H,P,N] row-major)")
+    if out is None:
+        out = torch.empty_like(x)
+    A = A if A.dtype == torch.float32 else A.to(torch.float32)
+    B = B if B.stride(-1) == 1 else B.contiguous()
+    C = C if C.stride(-1) == 1 else C.contiguous()
+    D = None if D is None else D.to(torch.float32)
+    dt_bias = None if dt_bias is None else dt_bias.to(torch.float32)
+
+    def i32(t):
+        return None if t is None else t.to(torch.int32).contiguous()
+
+    src, dst = i32(state_batch_indices), i32(dst_state_batch_indices)
+    st = lambda t, i: 0 if t is None else t.stride(i)
+    _lib.call("hmx_ssd_state_update",
+              _lib.ptr(state), _lib.dtype_code(state), state.stride(0),
+              _lib.ptr(x), _lib.dtype_code(x), x.stride(0), x.stride(1), x.stride(2),
+              _lib.ptr(dt), _lib.dtype_code(dt), dt.stride(0), dt.stride(1), dt.stride(2),
+              _lib.ptr(A), A.stride(0), A.stride(1), A.stride(2),
+              _lib.ptr(B), _lib.dtype_code(B), B.stride(0), B.stride(1),
+              _lib.ptr(C), _lib.dtype_code(C), C.stride(0), C.stride(1),
+              _lib.ptr(D), st(D, 0), st(D, 1), _lib.ptr(dt_bias), st(dt_bias, 0), st(dt_bias, 1),
+              _lib.ptr(z), 0 if z is None else _lib.dtype_code(z), st(z, 0), st(z, 1), st(z, 2),
+              _lib.ptr(out), _lib.dtype_code(out), out.stride(0), out.stride(1), out.stride(2),
+              _lib.ptr(src), _lib.ptr(dst), int(pad_slot_id), bsz, H, G, P, N,
+              int(bool(dt_softplus)), _lib.stream_of(x))
+    return out
+
+
+__all__ = ["mamba_chunk_scan_combined", "mamba_chunk_scan_combined_varlen",
+           "selective_state_update"]

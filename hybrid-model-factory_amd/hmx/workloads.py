@@ -107,6 +107,44 @@ def gka_prefill_bytes(T: int, H: int, HKV: int, d: int = 128, n_seqs: int = 1) -
     return T * H * 2 * d * 2 + T * HKV * 2 * d * 2 + 3 * T * H * 4 + 2 * n_seqs * H * d * d * 4
 
 
+def ssd_inputs(b: int = 2, T: int = 16384, H: int = 64, P: int = 64, N: int = 128, G: int = 8,
+               config_id: int = 4, device="cpu", gen_device="cpu"):
+    """C4: x [b,T,H,P], B, C [b,T,G,N] bf16 ~ N(0,1); dt_raw [b,T,H] ~ N(-2, 0.5) fp32
+    (passed with dt_softplus=True); dt_bias [H] = softplus^-1(exp(U(ln 1e-3, ln 1e-1)));
+    A [H] = -exp(U(ln 1, ln 16)); D [H] ~ N(1, 0.1); drawn in that order."""
+    gd = gen(config_id, gen_device)
+    x = _randn(gd, (b, T, H, P), gen_device)
+    Bm = _randn(gd, (b, T, G, N), gen_device)
+    Cm = _randn(gd, (b, T, G, N), gen_device)
+    dt = _randn(gd, (b, T, H), gen_device) * 0.5 - 2.0
+    u = torch.rand(H, generator=gd, device=gen_device)
+    dtv = torch.exp(u * (math.log(0.1) - math.log(1e-3)) + math.log(1e-3))
+    dt_bias = dtv + torch.log(-torch.expm1(-dtv))
+    A = -torch.exp(torch.rand(H, generator=gd, device=gen_device) * math.log(16.0))
+    D = _randn(gd, (H,), gen_device) * 0.1 + 1.0
+    out = dict(x=x.to(torch.bfloat16), B=Bm.to(torch.bfloat16), C=Cm.to(torch.bfloat16), dt=dt,
+               dt_bias=dt_bias, A=A, D=D)
+    return {n: t.to(device) for n, t in out.items()}
+
+
+def ssd_flops(tokens: int, H: int, G: int, P: int = 64, N: int = 128, L: int = 256) -> float:
+    """2*tokens*[H(L*P + 2*N*P) + G*L*N]: per chunk-head the intra-chunk (CB^T)X,
+    the state-to-output C S^T and the state update X^T B, plus CB^T once per group."""
+    return 2.0 * tokens * (H * (L * P + 2 * N * P) + G * L * N)
+
+
+def ssd_bytes(tokens: int, H: int, G: int, P: int = 64, N: int = 128, n_seqs: int = 2) -> float:
+    """x, y bf16 [tokens,H,P] + B, C bf16 [tokens,G,N] + dt fp32 + final fp32 states."""
+    return 2 * tokens * H * P * 2 + 2 * tokens * G * N * 2 + tokens * H * 4 + n_seqs * H * P * N * 4
+
+
+def ssd_decode_bytes(batch: int, H: int, G: int, P: int = 64, N: int = 128,
+                     state_bytes: int = 4) -> float:
+    """State read + write per (sequence, head), x/out bf16, dt, B, C."""
+    return (2 * batch * H * P * N * state_bytes + 2 * batch * H * P * 2 + batch * H * P * 4
+            + 2 * batch * G * N * 2)
+
+
 # ---------------------------------------------------------------------------
 # algorithmic work per unit (used for roofline.achieved)
 # ---------------------------------------------------------------------------
@@ -135,5 +173,7 @@ def ceil_div(a: int, b: int) -> int:
     return -(-a // b)
 
 
-__all__ = ["gen", "gdn_inputs", "gka_inputs", "gka_prefill_flops", "gka_prefill_bytes", "varlen_lengths", "cu_from_lengths", "decode_inputs",
-           "gdn_prefill_flops", "gdn_prefill_bytes", "gdn_decode_bytes", "ceil_div", "math"]
+__all__ = ["gen", "gdn_inputs", "gka_inputs", "gka_prefill_flops", "gka_prefill_bytes",
+           "varlen_lengths", "cu_from_lengths", "decode_inputs", "ssd_inputs", "ssd_flops",
+           "ssd_bytes", "ssd_decode_bytes", "gdn_prefill_flops", "gdn_prefill_bytes",
+           "gdn_decode_bytes", "ceil_div"]

@@ -192,6 +192,71 @@ int hmx_gka_chunk_fwd(const void* q, const void* k, const void* v, int32_t qkv_d
  * chunk states inside the op, chebyshev_prefill_gqa.py:137). */
 size_t hmx_gka_chunk_workspace_bytes(int32_t nseg_total, int32_t N, int32_t H);
 
+/*
+ * Mamba2 SSD chunk scan forward, bf16 x/B/C/z/y, fp32 states, varlen via a
+ * segment table of rows (n, bos, eos, c_start, c_end, seg_idx, first_seg, nseg)
+ * over 64-token chunks (bos/eos index the flattened token axis; sequence n
+ * starts from h0[n] or zero and its end state goes to h_final[n]).
+ *  x, z, y [tokens, H, P]: element strides x_ts/x_hs (token, head), last dim
+ *  contiguous; B, C [tokens, G, N] with strides (token, group); dt [tokens, H]
+ *  (f32/bf16/f16) with strides; A [H] fp32 (= -exp(A_log)); D [H, P] fp32 or
+ *  NULL; dt_bias [H] fp32 or NULL; z NULL for no gate.  dt' =
+ *  clamp(softplus(dt + dt_bias) if dt_softplus else dt + dt_bias, dt_min, dt_max).
+ *  h0, h_final fp32 [nseq, H, P, N] or NULL.  P, N in {64, 128}; token/head
+ *  strides multiples of 8 elements.
+ * workspace: hmx_ssd_chunk_workspace_bytes(...) bytes of device scratch.
+ * Replaces: mamba_chunk_scan_combined (mamba_ssm 2.3.0; call site
+ *   training/src/hmf/model/hybrid_zoo/layers/mamba/mamba2.py:555-580) and
+ *   mamba_chunk_scan_combined_varlen (vLLM 0.15.1; call site
+ *   vllm-inference/src/primed_vllm/primed_mamba2_layer.py:844-863).
+ */
+int hmx_ssd_chunk_fwd(const void* x, int64_t x_ts, int64_t x_hs,
+                      const void* B, int64_t b_ts, int64_t b_gs,
+                      const void* C, int64_t c_ts, int64_t c_gs, int32_t xbc_dtype,
+                      const void* dt, int32_t dt_dtype, int64_t dt_ts, int64_t dt_hs,
+                      const float* A, const float* D, const float* dt_bias,
+                      const void* z, int64_t z_ts, int64_t z_hs,
+                      void* y, int64_t y_ts, int64_t y_hs,
+                      const float* h0, float* h_final,
+                      const int32_t* seg_table, int32_t nseg_total, int32_t nseq,
+                      int32_t H, int32_t G, int32_t P, int32_t N,
+                      int32_t dt_softplus, float dt_min, float dt_max,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes hmx_ssd_chunk_fwd needs (host-only arithmetic).  Companion of
+ * hmx_ssd_chunk_fwd; no reference counterpart (mamba_ssm allocates its chunk
+ * states inside the op). */
+size_t hmx_ssd_chunk_workspace_bytes(int32_t nseg_total, int32_t nseq, int32_t H,
+                                     int32_t P, int32_t N);
+
+/*
+ * Mamba2 single-token state update, in place on a slot-indexed state pool.
+ *  state [slots, H, P, N] (f32 or bf16; slot_stride in elements, the rest
+ *  contiguous); x, dt, z, out [batch, H, P] with element strides (batch, head, p);
+ *  A fp32 [H, P, N] with strides (a_ps == a_ns == 0: one value per head);
+ *  B, C [batch, G, N] with strides (batch, group), N contiguous; D, dt_bias fp32
+ *  [H, P] with strides, or NULL.  Source slot state_batch_indices[i] (or i),
+ *  skipped when equal to pad_slot_id; written to dst_state_batch_indices[i] when
+ *  given.  P, N in {64, 128}.
+ * Replaces: selective_state_update (mamba_ssm / vLLM; call sites
+ *   training/src/hmf/model/hybrid_zoo/layers/mamba/mamba2.py:776-800,
+ *   vllm-inference/src/primed_vllm/primed_mamba2_layer.py:1000-1021).
+ */
+int hmx_ssd_state_update(void* state, int32_t state_dtype, int64_t slot_stride,
+                         const void* x, int32_t x_dtype, int64_t x_bs, int64_t x_hs, int64_t x_ps,
+                         const void* dt, int32_t dt_dtype, int64_t dt_bs, int64_t dt_hs,
+                         int64_t dt_ps, const float* A, int64_t a_hs, int64_t a_ps, int64_t a_ns,
+                         const void* B, int32_t b_dtype, int64_t b_bs, int64_t b_gs,
+                         const void* C, int32_t c_dtype, int64_t c_bs, int64_t c_gs,
+                         const float* D, int64_t d_hs, int64_t d_ps,
+                         const float* dt_bias, int64_t db_hs, int64_t db_ps,
+                         const void* z, int32_t z_dtype, int64_t z_bs, int64_t z_hs, int64_t z_ps,
+                         void* out, int32_t out_dtype, int64_t o_bs, int64_t o_hs, int64_t o_ps,
+                         const int32_t* state_batch_indices,
+                         const int32_t* dst_state_batch_indices, int32_t pad_slot_id,
+                         int32_t batch, int32_t H, int32_t G, int32_t P, int32_t N,
+                         int32_t dt_softplus, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
