@@ -9,9 +9,11 @@ slot permutation, 512 consecutive steps) in steps/s, each with its roofline,
 and the CPU oracle timed on a bounded sample of the same workloads.
 
 GKA prefill at C3 (the C1 shape, Chebyshev solve at 8 and 32 iterations) is
-reported under ``gka`` against the bf16 MFMA roofline.
+reported under ``gka`` against the bf16 MFMA roofline; the Mamba2 SSD chunk scan
+at C4 under ``ssd`` and its single-token state update under ``ssd_decode``, both
+against HBM.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only prefill|decode|gka]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only prefill|decode|gka|ssd]
 """
 from __future__ import annotations
 
@@ -109,6 +111,57 @@ def bench_gka(dev, steps, warmup, num_iter):
                 GBps=by / (ms * 1e-3) / 1e9)
 
 
+def bench_ssd(dev, steps, warmup):
+    """C4: mamba_chunk_scan_combined, b=2, T=16384, H=64, P=64, N=128, G=8, fp32 final state."""
+    import hmx
+    from hmx import workloads as wl
+    b, T, H, P, N, G = 2, 16384, 64, 64, 128, 8
+    d = wl.ssd_inputs(b=b, T=T, H=H, P=P, N=N, G=G, config_id=4, device=dev, gen_device=dev)
+
+    def step():
+        hmx.mamba_chunk_scan_combined(d["x"], d["dt"], d["A"], d["B"], d["C"], 256, D=d["D"],
+                                      dt_bias=d["dt_bias"], dt_softplus=True,
+                                      return_final_states=True)
+
+    ms = _timed(step, steps, warmup)
+    by = wl.ssd_bytes(b * T, H, G, P, N, n_seqs=b)
+    fl = wl.ssd_flops(b * T, H, G, P, N)
+    return dict(ms=ms, tokens_per_s=b * T / (ms * 1e-3), bytes=by, flops=fl,
+                GBps=by / (ms * 1e-3) / 1e9, TFLOPs=fl / (ms * 1e-3) / 1e12)
+
+
+def bench_ssd_decode(dev, steps=64, warmup=4):
+    """selective_state_update over a 256-slot fp32 pool (H=64, P=64, N=128, G=8; vLLM's
+    expanded A/dt/D views), randperm slots -- the C2 batch shape on the C4 layer."""
+    import torch
+    import hmx
+    from hmx import workloads as wl
+    bsz, H, P, N, G = 256, 64, 64, 128, 8
+    g = torch.Generator(device=dev).manual_seed(wl.SEED_BASE + 5)
+    pool = torch.randn(bsz, H, P, N, generator=g, device=dev) * 0.02
+    idx = torch.randperm(bsz, generator=g, device=dev).to(torch.int32)
+    x = torch.randn(steps, bsz, H, P, generator=g, device=dev).bfloat16()
+    dt = torch.randn(steps, bsz, H, generator=g, device=dev) * 0.5 - 2.0
+    B = torch.randn(steps, bsz, G, N, generator=g, device=dev).bfloat16()
+    C = torch.randn(steps, bsz, G, N, generator=g, device=dev).bfloat16()
+    A = -torch.exp(torch.rand(H, generator=g, device=dev) * 2.77)
+    Ae = A[:, None, None].expand(H, P, N)
+    De = torch.ones(H, device=dev)[:, None].expand(H, P)
+    be = torch.full((H,), -4.0, device=dev)[:, None].expand(H, P)
+    out = torch.empty(bsz, H, P, dtype=torch.bfloat16, device=dev)
+    it = {"s": 0}
+
+    def step():
+        s = it["s"] % steps
+        it["s"] += 1
+        hmx.selective_state_update(pool, x[s], dt[s][:, :, None].expand(bsz, H, P), Ae, B[s], C[s],
+                                   De, None, be, True, state_batch_indices=idx, out=out)
+
+    ms = _timed(step, steps, warmup)
+    by = wl.ssd_decode_bytes(bsz, H, G, P, N)
+    return dict(ms=ms, steps_per_s=1e3 / ms, bytes=by, GBps=by / (ms * 1e-3) / 1e9)
+
+
 def cpu_baseline(sample_tokens=4096):
     """The oracle's chunked fp32 restatement on the host (a bounded sample of C1)."""
     import torch
@@ -154,7 +207,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "decode", "gka"], default=None)
+    ap.add_argument("--only", choices=["prefill", "decode", "gka", "ssd"], default=None)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (HBM counter calibration)")
     a = ap.parse_args()
@@ -176,6 +229,9 @@ def main():
         out["decode"] = bench_decode(dev)
     if a.only in (None, "gka"):
         out["gka"] = {n: bench_gka(dev, max(2, a.steps // 4), 1, n) for n in (8, 32)}
+    if a.only in (None, "ssd"):
+        out["ssd"] = bench_ssd(dev, a.steps, a.warmup)
+        out["ssd_decode"] = bench_ssd_decode(dev)
     line = {
         "metric": "mixer prefill tokens/sec + decode steps/sec at 8B shape; % of roofline (1 GPU)",
         "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
@@ -231,6 +287,27 @@ def main():
                              "algorithmic_flops": r["flops"],
                              "hbm_GBps": round(r["GBps"], 1)},
             }
+    if "ssd" in out:
+        r = out["ssd"]
+        line["ssd"] = {
+            "value": round(r["tokens_per_s"], 1), "unit": "tokens/s", "ms_per_step": round(r["ms"], 4),
+            "config": {"workload": "C4 Mamba2 SSD chunk scan (mamba_chunk_scan_combined)", "B": 2,
+                       "T": 16384, "H": 64, "P": 64, "N": 128, "G": 8, "chunk": 256},
+            "roofline": {"bound": "hbm", "achieved": round(r["GBps"], 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(r["GBps"] / HBM_PEAK_GBS, 4),
+                         "traffic": measured_traffic("ssd_c4"), "algorithmic_bytes": r["bytes"],
+                         "mfma_TFLOPs": round(r["TFLOPs"], 1),
+                         "mfma_frac": round(r["TFLOPs"] / BF16_PEAK_TFLOPS, 4)},
+        }
+        r = out["ssd_decode"]
+        line["ssd_decode"] = {
+            "value": round(r["steps_per_s"], 1), "unit": "steps/s", "ms_per_step": round(r["ms"], 4),
+            "config": {"workload": "Mamba2 selective_state_update, 256 seqs x 1 token",
+                       "H": 64, "P": 64, "N": 128, "G": 8, "pool": "fp32 [256,64,64,128]"},
+            "roofline": {"bound": "hbm", "achieved": round(r["GBps"], 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(r["GBps"] / HBM_PEAK_GBS, 4),
+                         "algorithmic_bytes": r["bytes"]},
+        }
     if not a.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line), flush=True)
