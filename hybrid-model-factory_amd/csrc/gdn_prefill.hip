@@ -29,15 +29,14 @@
 //     (weak decay): per-segment zero-start end states S0_s and transitions
 //     Phi_s (chain started from I with V = 0), then S_{s+1} = Phi_s S_s + S0_s.
 //
-// Numerics: MFMA operands are bf16 with fp32 accumulation.  q and k enter raw
-// (exact bf16); the L2 normalisation is a pair of fp32 per-token factors
-// 1/|q|, 1/|k| folded into A, P, T's column scales, O's row scale and the state
-// update's token scale.  T's columns carry beta e^G / |k| (for W) or beta (for
-// U) and are split into bf16 hi + lo, so K and V enter exactly; the decayed
-// V_new of the state update and the W.S pair are hi/lo as well, giving ~fp32
-// accuracy where the state is sensitive; Q, P and S as the B operand of Q.S are
-// bf16.  Waves raise their priority through the MFMA-dense phases so the two
-// workgroups sharing a CU overlap one's VALU/LDS work with the other's MFMAs.
+// Numerics: MFMA operands are bf16 with fp32 accumulation.  T (with beta and
+// beta e^G folded in, so K and V enter exactly) and the decayed V_new of the
+// state update are split into bf16 hi + lo pairs, giving ~fp32 accuracy where
+// the state is sensitive; W, Q, P and the state as a B operand are bf16.
+//
+// Waves raise their priority through the MFMA-dense phases (W/U, V_new, O, state
+// update) so the two workgroups sharing a CU overlap one's VALU/LDS work with the
+// other's MFMAs (7% at C1).
 //
 // Roofline: HBM-bound at the algorithmic minimum (q,k,v,o bf16 + g,beta +
 // final state); FLOPs 2*T*H*(5*C*d + 3*d^2).
@@ -69,16 +68,14 @@ constexpr int OFF_K = OFF_Q + SZ_Q;
 constexpr int OFF_V = OFF_K + SZ_Q;         // also the O staging buffer
 constexpr int OFF_A = OFF_V + SZ_Q;         // fp32 A
 constexpr int OFF_T = OFF_A + SZ_F32;       // fp32 T
-constexpr int OFF_TWH = OFF_T + SZ_F32;     // bf16 hi/lo of T diag(beta e^G r_k)  (for W)
-constexpr int OFF_TWL = OFF_TWH + SZ_P;
-constexpr int OFF_TUH = OFF_TWL + SZ_P;     // bf16 hi/lo of T diag(beta)          (for U)
-constexpr int OFF_TUL = OFF_TUH + SZ_P;
+constexpr int OFF_TH = OFF_T + SZ_F32;      // bf16 T hi
+constexpr int OFF_TL = OFF_TH + SZ_P;       // bf16 T lo
 constexpr int SZ_WT = D * LDWT * 2;
-constexpr int OFF_W = OFF_TUL + SZ_P;       // -W^T hi
+constexpr int OFF_W = OFF_TL + SZ_P;        // -W^T hi
 constexpr int OFF_WL = OFF_W + SZ_WT;       // -W^T lo
 constexpr int OFF_P = OFF_WL + SZ_WT;
-constexpr int OFF_G = OFF_P + SZ_P;         // fp32 G, beta, e^G, e^{Gl-G}, 1/|k|, 1/|q| [C]
-constexpr int SMEM = OFF_G + 6 * C * 4;
+constexpr int OFF_G = OFF_P + SZ_P;         // fp32 G, beta, e^G, e^{Gl-G} [C]
+constexpr int SMEM = OFF_G + 4 * C * 4;
 static_assert(SMEM <= 80 * 1024, "LDS budget: two workgroups per CU");
 
 struct SegInfo {     // one row of the host-built segment table (int32 x 8)
@@ -158,14 +155,24 @@ __device__ __forceinline__ void load_raw(RawChunk& r, const Params& p, const bf1
   }
 }
 
-// 1/sqrt(|x|^2 + 1e-6) of a row whose 128 features are spread 8 per lane over
-// the 16 lanes of a DPP row.  The vectors themselves stay raw (exact bf16): the
-// normalisation enters every product as an fp32 per-token factor.
-__device__ __forceinline__ float row_rnorm(const bf16x8& raw) {
-  float ss = 0.f;
+// Stage one 8-feature row slice: optionally L2-normalise across the 16 lanes
+// holding the row, round to bf16, write to LDS.
+__device__ __forceinline__ void stage_row(bf16* dst, const bf16x8& raw, bool norm) {
+  float f[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) ss += (float)raw[j] * (float)raw[j];
-  return 1.0f / sqrtf(row16_sum(ss) + 1e-6f);
+  for (int j = 0; j < 8; ++j) f[j] = (float)raw[j];
+  if (norm) {
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss += f[j] * f[j];
+    const float inv = 1.0f / sqrtf(row16_sum(ss) + 1e-6f);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) f[j] *= inv;
+  }
+  bf16x8 b;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) b[j] = (bf16)f[j];
+  *reinterpret_cast<bf16x8*>(dst) = b;
 }
 
 // (I + A)^-1 of a strictly-lower 16x16 block held in C layout (A) together
@@ -203,24 +210,15 @@ __device__ __forceinline__ f32x4 inv_unit_lower16(const f32x4& A, const f32x4& A
 //   T_10 = -T_11 A_10 T_00,  T_32 = -T_33 A_32 T_22            (16x16)
 //   T[32:,:32] = -T_HH A_HL T_LL                                (32x32)
 // ---------------------------------------------------------------------------
-// T[r][c] in fp32 (for the block merges) and as bf16 hi/lo of T diag(sw) and
-// T diag(su): the token scales of W = T diag(beta e^G r_k) K and U = T diag(beta) V
-// are folded into T's columns so K and V enter the MFMAs exactly.
-struct TOut { float* T; bf16* wh; bf16* wl; bf16* uh; bf16* ul; };
-
-__device__ __forceinline__ void put_t(const TOut& t, int r, int c, float x, float sw, float su) {
-  t.T[r * LDA + c] = x;
-  const float xw = x * sw, xu = x * su;
-  const bf16 hw = (bf16)xw, hu = (bf16)xu;
-  t.wh[r * LDT + c] = hw;
-  t.wl[r * LDT + c] = (bf16)(xw - (float)hw);
-  t.uh[r * LDT + c] = hu;
-  t.ul[r * LDT + c] = (bf16)(xu - (float)hu);
+__device__ __forceinline__ void put_t(float* sT, bf16* sTh, bf16* sTl, int r, int c, float x) {
+  sT[r * LDA + c] = x;
+  const bf16 h = (bf16)x;
+  sTh[r * LDT + c] = h;
+  sTl[r * LDT + c] = (bf16)(x - (float)h);
 }
 
-__device__ __forceinline__ void tri_merge(const float* sA, const TOut& t, const float* sB,
-                                         const float* sEG, const float* sRK, int wave, int lane) {
-  float* sT = t.T;
+__device__ __forceinline__ void tri_merge(const float* sA, float* sT, bf16* sTh, bf16* sTl,
+                                         int wave, int lane) {
   static_assert(C == 32, "one 16x16 merge");
   const int q4 = lane >> 4, l16 = lane & 15;
   if (wave == 0) {
@@ -232,9 +230,8 @@ __device__ __forceinline__ void tri_merge(const float* sA, const TOut& t, const 
     f32x4 Y = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 4; ++s) Y = mfma16f(sT[(16 + l16) * LDA + 16 + 4 * q4 + s], X[s], Y);
-    const float su = sB[l16], sw = su * sEG[l16] * sRK[l16];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) put_t(t, 16 + 4 * q4 + v, l16, -Y[v], sw, su);
+    for (int v = 0; v < 4; ++v) put_t(sT, sTh, sTl, 16 + 4 * q4 + v, l16, -Y[v]);
   }
   lds_barrier();
 }
@@ -251,8 +248,8 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
   bf16* sO = sV;  // O staging reuses V after U is formed
   float* sA = reinterpret_cast<float*>(smem + OFF_A);
   float* sT = reinterpret_cast<float*>(smem + OFF_T);
-  const TOut tout{sT, reinterpret_cast<bf16*>(smem + OFF_TWH), reinterpret_cast<bf16*>(smem + OFF_TWL),
-                  reinterpret_cast<bf16*>(smem + OFF_TUH), reinterpret_cast<bf16*>(smem + OFF_TUL)};
+  bf16* sTh = reinterpret_cast<bf16*>(smem + OFF_TH);
+  bf16* sTl = reinterpret_cast<bf16*>(smem + OFF_TL);
   bf16* sW = reinterpret_cast<bf16*>(smem + OFF_W);
   bf16* sWl = reinterpret_cast<bf16*>(smem + OFF_WL);
   bf16* sP = reinterpret_cast<bf16*>(smem + OFF_P);
@@ -260,17 +257,12 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
   float* sB = sG + C;
   float* sEG = sB + C;    // e^{G}
   float* sEDL = sEG + C;  // e^{G_last - G}
-  float* sRK = sEDL + C;  // 1/|k| (1 without in-kernel l2norm)
-  float* sRQ = sRK + C;   // 1/|q|
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  // the scaled T hi/lo upper-triangular 16x16 blocks are never written: zero them once
+  // T hi/lo upper-triangular 16x16 blocks are never written: zero them once
   for (int i = tid; i < C * C; i += NTHR) {
     const int r = i / C, c = i % C;
-    if ((c >> 4) > (r >> 4)) {
-      tout.wh[r * LDT + c] = (bf16)0.f; tout.wl[r * LDT + c] = (bf16)0.f;
-      tout.uh[r * LDT + c] = (bf16)0.f; tout.ul[r * LDT + c] = (bf16)0.f;
-    }
+    if ((c >> 4) > (r >> 4)) { sTh[r * LDT + c] = (bf16)0.f; sTl[r * LDT + c] = (bf16)0.f; }
   }
   const int q4 = lane >> 4, l16 = lane & 15;
   const int s_id = blockIdx.x, h = blockIdx.y;
@@ -354,15 +346,9 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
       for (int pass = 0; pass < MT; ++pass) {
         const int row = pass * 16 + (tid >> 4);
         const int f0 = (tid & 15) * 8;
-        *reinterpret_cast<bf16x8*>(sK + row * LDQ + f0) = raw.k[pass];
+        stage_row(sK + row * LDQ + f0, raw.k[pass], p.l2norm);
         if (MODE != MODE_PHI) *reinterpret_cast<bf16x8*>(sV + row * LDQ + f0) = raw.v[pass];
-        if (out_chunk) *reinterpret_cast<bf16x8*>(sQ + row * LDQ + f0) = raw.q[pass];
-        const float rk = p.l2norm ? row_rnorm(raw.k[pass]) : 1.f;
-        const float rq = (p.l2norm && out_chunk) ? row_rnorm(raw.q[pass]) : 1.f;
-        if ((tid & 15) == 0) {
-          sRK[row] = rk;
-          sRQ[row] = rq;
-        }
+        if (out_chunk) stage_row(sQ + row * LDQ + f0, raw.q[pass], p.l2norm);
       }
       if (wave == 0) {
         static_assert(C == 32, "the DPP scan covers 32 lanes");
@@ -393,12 +379,11 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
       bf16x8 af[4];
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) af[ks] = frag(Am, LDQ, 16 * i, 32 * ks, lane);
-      float gr[4], br[4], rr[4];
+      float gr[4], br[4];
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         gr[v] = sG[16 * i + 4 * q4 + v];
         br[v] = sB[16 * i + 4 * q4 + v];
-        rr[v] = isP ? sRQ[16 * i + 4 * q4 + v] : sRK[16 * i + 4 * q4 + v];
       }
 #pragma unroll
       for (int j = 0; j < MT; ++j) {
@@ -407,19 +392,19 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) acc = mfma16(af[ks], frag(sK, LDQ, 16 * j, 32 * ks, lane), acc);
         const int col = 16 * j + l16;
-        const float gc = sG[col], rc = sRK[col];
+        const float gc = sG[col];
         if (isP) {
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
             const int row = 16 * i + 4 * q4 + v;
-            const float dcy = (row >= col) ? fast_exp(gr[v] - gc) * rr[v] * rc : 0.f;
+            const float dcy = (row >= col) ? fast_exp(gr[v] - gc) : 0.f;
             sP[row * LDT + col] = (bf16)(acc[v] * dcy);
           }
         } else if (j < i) {
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
             const int row = 16 * i + 4 * q4 + v;
-            sA[row * LDA + col] = br[v] * rr[v] * rc * acc[v] * fast_exp(gr[v] - gc);
+            sA[row * LDA + col] = br[v] * acc[v] * fast_exp(gr[v] - gc);
           }
         } else {
           // diagonal tile: A and A^T in C layout (k.k^T is symmetric), then T_ii
@@ -428,35 +413,58 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
             const int row = 16 * i + 4 * q4 + v;
-            const float kk = acc[v] * rr[v] * rc;
-            Ad[v] = row > col ? br[v] * kk * fast_exp(gr[v] - gc) : 0.f;
-            At_[v] = col > row ? bc * kk * fast_exp(gc - gr[v]) : 0.f;
+            Ad[v] = row > col ? br[v] * acc[v] * fast_exp(gr[v] - gc) : 0.f;
+            At_[v] = col > row ? bc * acc[v] * fast_exp(gc - gr[v]) : 0.f;
           }
           const f32x4 Tii = inv_unit_lower16(Ad, At_, q4, l16);
-          const float su = bc, sw = bc * sEG[col] * rc;
 #pragma unroll
-          for (int v = 0; v < 4; ++v) put_t(tout, 16 * i + 4 * q4 + v, col, Tii[v], sw, su);
+          for (int v = 0; v < 4; ++v) put_t(sT, sTh, sTl, 16 * i + 4 * q4 + v, col, Tii[v]);
         }
       }
     }
     lds_barrier();
 
     // ---- phase 2: off-diagonal block of T = (I + A)^-1 (fp32, + bf16 hi/lo) ------
-    tri_merge(sA, tout, sB, sEG, sRK, wave, lane);
+    tri_merge(sA, sT, sTh, sTl, wave, lane);
 
-    // ---- phase 3: W = [T diag(beta e^G r_k)] K (to LDS, negated hi/lo) and
-    //      U = [T diag(beta)] V (registers): the scaled T arrives as bf16 hi + lo,
-    //      K and V enter exactly (2 products each).
     __builtin_amdgcn_s_setprio(1);
+    // ---- phase 3: W = T diag(beta e^G) K (to LDS, negated hi/lo), U = T diag(beta) V
+    //      (registers).  The token scales are applied to the B fragments in fp32,
+    //      split into hi/lo, and multiplied by T hi/lo (3 products each).
     f32x4 Vn[MT][2];  // U, then V_new: rows 16mt.., cols 32w+16ct..
     {
+      float sk[KT][8], sv[KT][8];
+#pragma unroll
+      for (int ks = 0; ks < KT; ++ks)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int t = 32 * ks + 8 * q4 + j;
+          sv[ks][j] = sB[t];
+          sk[ks][j] = sv[ks][j] * sEG[t];
+        }
 #pragma unroll
       for (int ct = 0; ct < 2; ++ct) {
-        bf16x8 bk[KT], bv[KT];
+        bf16x8 bkh[KT], bkl[KT], bvh[KT], bvl[KT];
 #pragma unroll
         for (int ks = 0; ks < KT; ++ks) {
-          bk[ks] = frag_t(sK, LDQ, 32 * ks, 32 * wave + 16 * ct, lane);
-          if (MODE != MODE_PHI) bv[ks] = frag_t(sV, LDQ, 32 * ks, 32 * wave + 16 * ct, lane);
+          const bf16x8 kr = frag_t(sK, LDQ, 32 * ks, 32 * wave + 16 * ct, lane);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float x = (float)kr[j] * sk[ks][j];
+            const bf16 hx = (bf16)x;
+            bkh[ks][j] = hx;
+            bkl[ks][j] = (bf16)(x - (float)hx);
+          }
+          if (MODE != MODE_PHI) {
+            const bf16x8 vr = frag_t(sV, LDQ, 32 * ks, 32 * wave + 16 * ct, lane);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              const float x = (float)vr[j] * sv[ks][j];
+              const bf16 hx = (bf16)x;
+              bvh[ks][j] = hx;
+              bvl[ks][j] = (bf16)(x - (float)hx);
+            }
+          }
         }
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
@@ -464,11 +472,15 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
 #pragma unroll
           for (int ks = 0; ks < KT; ++ks) {
             if (32 * ks > 16 * mt + 15) continue;  // T is lower triangular
-            w = mfma16(frag(tout.wh, LDT, 16 * mt, 32 * ks, lane), bk[ks], w);
-            w = mfma16(frag(tout.wl, LDT, 16 * mt, 32 * ks, lane), bk[ks], w);
+            const bf16x8 th = frag(sTh, LDT, 16 * mt, 32 * ks, lane);
+            const bf16x8 tl = frag(sTl, LDT, 16 * mt, 32 * ks, lane);
+            w = mfma16(th, bkh[ks], w);
+            w = mfma16(th, bkl[ks], w);
+            w = mfma16(tl, bkh[ks], w);
             if (MODE != MODE_PHI) {
-              u = mfma16(frag(tout.uh, LDT, 16 * mt, 32 * ks, lane), bv[ks], u);
-              u = mfma16(frag(tout.ul, LDT, 16 * mt, 32 * ks, lane), bv[ks], u);
+              u = mfma16(th, bvh[ks], u);
+              u = mfma16(th, bvl[ks], u);
+              u = mfma16(tl, bvh[ks], u);
             }
           }
           {
@@ -489,14 +501,8 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
     }
     lds_barrier();
 
-    // ---- phase 4: V_new = U - W S with W and S as bf16 hi+lo pairs, and the
-    //      inter-chunk part of the output, Q S, from the same S hi operand ------
     __builtin_amdgcn_s_setprio(2);
-    f32x4 O[MT][2];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) O[mt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // ---- phase 4: V_new = U - W S, with W and S as bf16 hi+lo pairs ------------
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       bf16x8 Sh[2], Sl[2];
@@ -512,22 +518,33 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
           Vn[mt][ct] = mfma16(a, Sl[ct], Vn[mt][ct]);
           Vn[mt][ct] = mfma16(al, Sh[ct], Vn[mt][ct]);
         }
-        if (out_chunk) {
-          const bf16x8 aq = frag_perm(sQ, LDQ, 16 * mt, 32 * ks, lane);
-#pragma unroll
-          for (int ct = 0; ct < 2; ++ct) O[mt][ct] = mfma16(aq, Sh[ct], O[mt][ct]);
-        }
       }
     }
 
-    // ---- phase 5: O = scale [e^G r_q (Q S) + P V_new] ---------------------------
+    // ---- phase 5: O = scale [e^G (Q S) + P V_new] ------------------------------
     if (out_chunk) {
+      f32x4 O[MT][2];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) O[mt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        bf16x8 Sh[2];
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) Sh[ct] = pack_b(S[2 * ks][ct], S[2 * ks + 1][ct]);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const bf16x8 a = frag_perm(sQ, LDQ, 16 * mt, 32 * ks, lane);
+#pragma unroll
+          for (int ct = 0; ct < 2; ++ct) O[mt][ct] = mfma16(a, Sh[ct], O[mt][ct]);
+        }
+      }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          const int t = 16 * mt + 4 * q4 + v;
-          const float e = sEG[t] * sRQ[t];
+          const float e = sEG[16 * mt + 4 * q4 + v];
           O[mt][0][v] *= e;
           O[mt][1][v] *= e;
         }
@@ -555,7 +572,7 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
                 (bf16)(O[mt][ct][v] * p.scale);
     }
 
-    // ---- phase 6: S <- e^{G_last} S + K^T (r_k e^{G_last-G} V_new), hi/lo -------
+    // ---- phase 6: S <- e^{G_last} S + K^T (e^{G_last-G} V_new), hi/lo ---------
     {
       const float egl = sEG[C - 1];
 #pragma unroll
@@ -568,8 +585,7 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          const int t = 16 * mt + 4 * q4 + v;
-          const float e = sEDL[t] * sRK[t];
+          const float e = sEDL[16 * mt + 4 * q4 + v];
           Vn[mt][0][v] *= e;
           Vn[mt][1][v] *= e;
         }
