@@ -79,7 +79,7 @@ struct Cfg {
   static constexpr int OFF_M = OFF_C + L * LDB * 2;
   static constexpr int OFF_Y = OFF_M + L * LDM * 2;
   static constexpr int OFF_S = OFF_Y + L * LDX * 2;
-  static constexpr int SMEM = OFF_S + 4 * L * 4;
+  static constexpr int SMEM = OFF_S + 2 * 4 * L * 4;   // two buffers of 4 scalar arrays
   static_assert(SMEM <= 80 * 1024, "LDS budget: two workgroups per CU");
   static_assert(P % 64 == 0 && N % 32 == 0, "tile shape");
 };
@@ -96,6 +96,17 @@ __device__ __forceinline__ float ld_any(const void* p, int64_t i, int dt) {
 __device__ __forceinline__ SegInfo load_seg(const int* seg, int s) {
   const int* r = seg + s * 8;
   return SegInfo{r[0], r[1], r[2], r[3], r[4], r[5], r[6], r[7]};
+}
+
+// softplus with mamba's threshold (x for x > 20): max(x, 0) + log1p(e^{-|x|}),
+// log1p by Goldberg's correction log(w) u / (w - 1), w = 1 + u (exact for u
+// below w's rounding), on the hardware exp/log.
+__device__ __forceinline__ float softplus20(float x) {
+  if (x > 20.f) return x;
+  const float u = fast_exp(-fabsf(x));
+  const float w = 1.f + u;
+  const float l1p = (w == 1.f) ? u : __logf(w) * (u / (w - 1.f));
+  return fmaxf(x, 0.f) + l1p;
 }
 
 // Inclusive prefix sum over the 64 lanes of a wave.
@@ -134,8 +145,9 @@ __device__ __forceinline__ void load_raw(Raw<P, N>& r, const Params& p, int tok0
     if (MODE == MODE_OUT)
       r.c[i] = ok ? *reinterpret_cast<const bf16x8*>(p.C + tok * p.c_ts + g * p.c_gs + c8) : bf16x8{};
   }
-  if (tid < L)
-    r.dt = tid < nval ? ld_any(p.dt, (int64_t)(tok0 + tid) * p.dt_ts + h * p.dt_hs, p.dt_dt) : 0.f;
+  const int t = tid - (NTHR - L);   // the last wave loads dt (lane t = token t)
+  if (t >= 0)
+    r.dt = t < nval ? ld_any(p.dt, (int64_t)(tok0 + t) * p.dt_ts + h * p.dt_hs, p.dt_dt) : 0.f;
 }
 
 template <int P, int N, int MODE>
@@ -149,7 +161,11 @@ __global__ __launch_bounds__(NTHR, 2) void ssd_chunk_kernel(Params p) {
   bf16* sM = reinterpret_cast<bf16*>(smem + K::OFF_M);
   bf16* sY = reinterpret_cast<bf16*>(smem + K::OFF_Y);
   float* sc = reinterpret_cast<float*>(smem + K::OFF_S);
-  auto SC = [&](int slot, int t) -> float& { return sc[slot * L + t]; };
+  // per-token scalars, double-buffered by chunk parity: SC(buf, slot, t)
+  auto SC = [&](int buf, int slot, int t) -> float& { return sc[(buf * 4 + slot) * L + t]; };
+  auto SC4 = [&](int buf, int slot, int t) -> f32x4 {
+    return *reinterpret_cast<const f32x4*>(&sc[(buf * 4 + slot) * L + t]);
+  };
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int q4 = lane >> 4, l16 = lane & 15;
@@ -186,50 +202,59 @@ __global__ __launch_bounds__(NTHR, 2) void ssd_chunk_kernel(Params p) {
   }
   float dsum = 0.f;   // segment log-decay (LOCAL)
 
-  Raw<P, N> raw;
-  if (si.c_start < si.c_end) {
-    const int tok0 = si.bos + si.c_start * L;
-    load_raw<P, N, MODE>(raw, p, tok0, min(L, si.eos - tok0), h, g, tid);
-  }
+  // Raw chunks in flight: the light LOCAL pass keeps two (the loop is unrolled by
+  // two so the register sets alternate statically: chunk c in `cur`, chunk c+1
+  // arriving in `nxt`); the OUT pass, whose chunk work covers the load latency,
+  // keeps one (cur == nxt, refilled with chunk c+1 after staging).
+  constexpr int AHEAD = (MODE == MODE_LOCAL) ? 2 : 1;
+  Raw<P, N> ra, rb;
+  const auto nval_of = [&](int c) { return min(L, si.eos - (si.bos + c * L)); };
+  if (si.c_start < si.c_end)
+    load_raw<P, N, MODE>(ra, p, si.bos + si.c_start * L, nval_of(si.c_start), h, g, tid);
+  if (AHEAD == 2 && si.c_start + 1 < si.c_end)
+    load_raw<P, N, MODE>(rb, p, si.bos + (si.c_start + 1) * L, nval_of(si.c_start + 1), h, g, tid);
 
-  for (int c = si.c_start; c < si.c_end; ++c) {
+  // dt' = clamp(softplus(dt + bias)), A_t = cumsum(dt' A), w_t = dt' e^{A_L - A_t},
+  // e^{A_t} of chunk c into scalar buffer `buf` (the last wave; lane = token)
+  const auto make_scalars = [&](float dt_raw, int c, int buf) {
+    float d = dt_raw + bias;
+    if (p.softplus) d = softplus20(d);
+    d = fminf(fmaxf(d, p.dt_min), p.dt_max);
+    if (lane >= nval_of(c)) d = 0.f;
+    const float acs = scan64(d * A_h, lane);
+    const float alast = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acs), 63));
+    SC(buf, S_DT, lane) = d;
+    SC(buf, S_ACS, lane) = acs;
+    SC(buf, S_W, lane) = d * fast_exp(alast - acs);
+    SC(buf, S_EA, lane) = fast_exp(acs);
+  };
+  if (si.c_start < si.c_end && wave == NTHR / 64 - 1) make_scalars(ra.dt, si.c_start, 0);
+
+  const auto chunk = [&](Raw<P, N>& cur, Raw<P, N>& nxt, int c) {
     const int tok0 = si.bos + c * L;
-    const int nval = min(L, si.eos - tok0);
-    // ---- stage the prefetched chunk -----------------------------------------
+    const int nval = nval_of(c);
+    const int cb = (c - si.c_start) & 1;
+    // ---- stage chunk c, then refill `cur` with chunk c + AHEAD -------------------
 #pragma unroll
     for (int i = 0; i < K::VX; ++i) {
       const int e = tid + NTHR * i, row = e / (P / 8), c8 = (e % (P / 8)) * 8;
-      *reinterpret_cast<bf16x8*>(sX + row * LDX + c8) = raw.x[i];
+      *reinterpret_cast<bf16x8*>(sX + row * LDX + c8) = cur.x[i];
     }
 #pragma unroll
     for (int i = 0; i < K::VB; ++i) {
       const int e = tid + NTHR * i, row = e / (N / 8), c8 = (e % (N / 8)) * 8;
-      *reinterpret_cast<bf16x8*>(sB + row * LDB + c8) = raw.b[i];
-      if (MODE == MODE_OUT) *reinterpret_cast<bf16x8*>(sC + row * LDB + c8) = raw.c[i];
+      *reinterpret_cast<bf16x8*>(sB + row * LDB + c8) = cur.b[i];
+      if (MODE == MODE_OUT) *reinterpret_cast<bf16x8*>(sC + row * LDB + c8) = cur.c[i];
     }
     bf16x8 zst[K::VX];
     if (MODE == MODE_OUT) {
 #pragma unroll
-      for (int i = 0; i < K::VX; ++i) zst[i] = raw.z[i];
+      for (int i = 0; i < K::VX; ++i) zst[i] = cur.z[i];
     }
-    if (wave == 0) {
-      float d = raw.dt + bias;
-      if (p.softplus) d = d <= 20.f ? log1pf(expf(d)) : d;
-      d = fminf(fmaxf(d, p.dt_min), p.dt_max);
-      if (lane >= nval) d = 0.f;
-      const float acs = scan64(d * A_h, lane);
-      const float al = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acs), 63));
-      SC(S_DT, lane) = d;
-      SC(S_ACS, lane) = acs;
-      SC(S_W, lane) = d * fast_exp(al - acs);
-      SC(S_EA, lane) = fast_exp(acs);
-    }
-    if (c + 1 < si.c_end) {
-      const int t1 = tok0 + L;
-      load_raw<P, N, MODE>(raw, p, t1, min(L, si.eos - t1), h, g, tid);
-    }
+    if (c + AHEAD < si.c_end)
+      load_raw<P, N, MODE>(cur, p, tok0 + AHEAD * L, nval_of(c + AHEAD), h, g, tid);
     lds_barrier();
-    const float al = SC(S_ACS, L - 1);
+    const float al = SC(cb, S_ACS, L - 1);
 
     if (MODE == MODE_OUT) {
       // z into the y staging buffer (read back in C layout by the owner lanes)
@@ -260,13 +285,15 @@ __global__ __launch_bounds__(NTHR, 2) void ssd_chunk_kernel(Params p) {
         }
       }
 #pragma unroll
-      for (int tb = 0; tb < 4; ++tb)
+      for (int tb = 0; tb < 4; ++tb) {
+        const f32x4 ea4 = SC4(cb, S_EA, 16 * tb + 4 * q4);
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          const float e = SC(S_EA, 16 * tb + 4 * q4 + v);
+          const float e = ea4[v];
 #pragma unroll
           for (int i = 0; i < PB; ++i) Y[tb][i][v] *= e;
         }
+      }
       // ---- M = (C B^T) o decay o dt as bf16 hi + lo (lower tiles; (0,1), (2,3)
       // zeroed).  Tiles per wave: w0 (0,0)(1,0)(2,0)+zero(0,1);
       // w1 (1,1)(2,1)(3,0)+zero(2,3); w2 (2,2)(3,1); w3 (3,2)(3,3) -------------
@@ -282,15 +309,18 @@ __global__ __launch_bounds__(NTHR, 2) void ssd_chunk_kernel(Params p) {
         for (int ks = 0; ks < N / 32; ++ks)
           acc = mfma16(frag(sC, LDB, 16 * tb, 32 * ks, lane), frag(sB, LDB, 16 * jb, 32 * ks, lane), acc);
         const int j = 16 * jb + l16;
-        const float aj = SC(S_ACS, j), dj = SC(S_DT, j);
+        const float aj = SC(cb, S_ACS, j), dj = SC(cb, S_DT, j);
+        const f32x4 at4 = SC4(cb, S_ACS, 16 * tb + 4 * q4);
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int t = 16 * tb + 4 * q4 + v;
-          const float m = (t >= j) ? acc[v] * fast_exp(SC(S_ACS, t) - aj) * dj : 0.f;
+          const float m = (t >= j) ? acc[v] * fast_exp(at4[v] - aj) * dj : 0.f;
           mh[k][v] = (bf16)m;
           ml[k][v] = (bf16)(m - (float)mh[k][v]);
         }
       }
+      // the last wave (fewest tiles) turns the next chunk's dt into its scalars
+      if (wave == NTHR / 64 - 1 && c + 1 < si.c_end) make_scalars(nxt.dt, c + 1, cb ^ 1);
       lds_barrier();   // every wave is done with sC: its space takes the M low parts
       bf16* sML = sC;
 #pragma unroll
@@ -353,6 +383,8 @@ __global__ __launch_bounds__(NTHR, 2) void ssd_chunk_kernel(Params p) {
           }
         }
       }
+    } else if (wave == NTHR / 64 - 1 && c + 1 < si.c_end) {
+      make_scalars(nxt.dt, c + 1, cb ^ 1);
     }
 
     // ---- S^T <- e^{A_L} S^T + B^T diag(w) X ------------------------------------
@@ -367,9 +399,8 @@ __global__ __launch_bounds__(NTHR, 2) void ssd_chunk_kernel(Params p) {
           for (int v = 0; v < 4; ++v) ST[nb][i][v] *= ea;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        float w[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) w[j] = SC(S_W, 32 * ks + 8 * q4 + j);
+        const f32x4 w0 = SC4(cb, S_W, 32 * ks + 8 * q4), w1 = SC4(cb, S_W, 32 * ks + 8 * q4 + 4);
+        const float w[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
         // w x as bf16 hi + lo: one rounding of it would cost ~1e-3 of |S|
         bf16x8 bwh[PB], bwl[PB];
 #pragma unroll
@@ -405,6 +436,15 @@ __global__ __launch_bounds__(NTHR, 2) void ssd_chunk_kernel(Params p) {
               *reinterpret_cast<const bf16x8*>(sY + row * LDX + c8);
       }
     }
+  };
+
+  if (AHEAD == 2) {
+    for (int c = si.c_start; c < si.c_end; c += 2) {
+      chunk(ra, rb, c);
+      if (c + 1 < si.c_end) chunk(rb, ra, c + 1);
+    }
+  } else {
+    for (int c = si.c_start; c < si.c_end; ++c) chunk(ra, ra, c);
   }
 
   // ---- segment end state --------------------------------------------------------
