@@ -88,6 +88,7 @@ struct Params {
   float* ws_h0; float* ws_s0;             // [nseg][H][D][D] segment start states
   int H, HKV, num_iter;
   float ridge_ratio, scale;
+  int l2norm;                             // 0: q, k are used as given
 };
 
 __device__ __forceinline__ float ldsc(const void* p, int64_t i, int dt) {
@@ -257,10 +258,12 @@ __global__ __launch_bounds__(NTHR, 1) void gka_chunk_kernel(Params p) {
     }
     lds_barrier();
     // per-token scales: s_t = (beta_t+eps)/|k_t| (k~ = s k), iq_t = 1/|q_t|
+    // (without in-kernel normalisation: s_t = beta_t+eps or 1, iq_t = 1)
     if (tid < C) {
       const float kn2 = SC(S_KN2, tid);
-      SC(S_SK, tid) = tid < nval ? SC(S_BE, tid) / sqrtf(kn2) : 0.f;
-      if (MODE == MODE_OUT) SC(S_IQ, tid) = tid < nval ? 1.0f / sqrtf(SC(S_QN2, tid)) : 0.f;
+      SC(S_SK, tid) = tid < nval ? SC(S_BE, tid) * (p.l2norm ? 1.0f / sqrtf(kn2) : 1.f) : 0.f;
+      if (MODE == MODE_OUT)
+        SC(S_IQ, tid) = tid < nval ? (p.l2norm ? 1.0f / sqrtf(SC(S_QN2, tid)) : 1.f) : 0.f;
     }
 
     lds_barrier();
@@ -744,7 +747,8 @@ extern "C" int hmx_gka_chunk_fwd(const void* q, const void* k, const void* v, in
                                  float* h_kv_final, const int32_t* seg_table, int32_t nseg_total,
                                  int32_t N, int32_t H, int32_t HKV, int32_t D_, int32_t V,
                                  int32_t num_iter, float ridge_ratio, float scale,
-                                 void* workspace, size_t workspace_bytes, void* stream) {
+                                 int32_t use_qk_l2norm, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
   HMX_REQUIRE(qkv_dtype == HMX_BF16, HMX_EUNSUPPORTED,
               "hmx_gka_chunk_fwd: q/k/v must be bfloat16 (got dtype code %d)", qkv_dtype);
   HMX_REQUIRE(D_ == D && V == D, HMX_EUNSUPPORTED,
@@ -766,6 +770,7 @@ extern "C" int hmx_gka_chunk_fwd(const void* q, const void* k, const void* v, in
   p.hkk0 = h_kk0; p.hkv0 = h_kv0; p.hkk_t = h_kk_final; p.hkv_t = h_kv_final;
   p.seg = seg_table; p.nseg_total = nseg_total;
   p.H = H; p.HKV = HKV; p.num_iter = num_iter; p.ridge_ratio = ridge_ratio; p.scale = scale;
+  p.l2norm = use_qk_l2norm;
   const bool multi = nseg_total > N;
   const size_t st = (size_t)nseg_total * H * D * D;
   float* ws = static_cast<float*>(workspace);

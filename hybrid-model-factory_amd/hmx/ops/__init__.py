@@ -1,8 +1,8 @@
 """Mixer ops with the reference's names, argument order, defaults and returns."""
 from .gdn import (chunk_gated_delta_rule, chunk_gated_delta_rule_gqa, fused_gdn_gating,
                   fused_recurrent_gated_delta_rule, fused_recurrent_gated_delta_rule_gqa)
-from .gka import (chebyshev_iteration_gqa, fused_gka_gating, gka_chebyshev_gla_decode,
-                  gka_chebyshev_gla_prefill)
+from .gka import (chebyshev_iteration_gqa, fused_gka_gating, gka_chebyshev_gla,
+                  gka_chebyshev_gla_decode, gka_chebyshev_gla_prefill, torch_decoding_one_step)
 from .ssd import (mamba_chunk_scan_combined, mamba_chunk_scan_combined_varlen,
                   selective_state_update)
 
@@ -16,6 +16,8 @@ __all__ = [
     "chebyshev_iteration_gqa",
     "gka_chebyshev_gla_decode",
     "gka_chebyshev_gla_prefill",
+    "gka_chebyshev_gla",
+    "torch_decoding_one_step",
     "mamba_chunk_scan_combined",
     "mamba_chunk_scan_combined_varlen",
     "selective_state_update",

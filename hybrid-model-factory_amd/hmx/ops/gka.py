@@ -153,6 +153,13 @@ def gka_chebyshev_gla_prefill(q, k, v, alpha, g, gk, beta, gla_scale: float,
     _check_sketching_constraints(gka, num_sketches_per_head, "gka_chebyshev_gla_prefill")
     if cu_seqlens is not None and q.shape[0] != 1:
         raise ValueError(f"Batch size must be 1 when using cu_seqlens, got {q.shape[0]}")
+    return _gka_prefill(q, k, v, alpha, g, gk, beta, gla_scale, ridge_ratio, num_iter,
+                        h_kk_initial, h_kv_initial, output_final_state, cu_seqlens, True,
+                        _segment_chunks)
+
+
+def _gka_prefill(q, k, v, alpha, g, gk, beta, gla_scale, ridge_ratio, num_iter, h_kk_initial,
+                 h_kv_initial, output_final_state, cu_seqlens, l2norm, segment_chunks=None):
     _lib.require_gpu(q, k, v, alpha, g, gk, beta, h_kk_initial, h_kv_initial, cu_seqlens)
     B, T, H, D = q.shape
     HKV, V = k.shape[2], v.shape[-1]
@@ -177,7 +184,7 @@ def gka_chebyshev_gla_prefill(q, k, v, alpha, g, gk, beta, gla_scale: float,
              if output_final_state and num_iter > 0 else None)
     hkv_t = (torch.empty(N, H, D, V, dtype=torch.float32, device=q.device)
              if output_final_state else None)
-    rows = _segment_table(bounds, H, GKA_WORKGROUPS_PER_CU * _cu_count(q.device), _segment_chunks)
+    rows = _segment_table(bounds, H, GKA_WORKGROUPS_PER_CU * _cu_count(q.device), segment_chunks)
     seg = torch.tensor(rows, dtype=torch.int32).to(q.device, non_blocking=True)
     lib = _lib.load()
     ws_bytes = int(lib.hmx_gka_chunk_workspace_bytes(len(rows), N, H))
@@ -189,9 +196,50 @@ def gka_chebyshev_gla_prefill(q, k, v, alpha, g, gk, beta, gla_scale: float,
               _lib.ptr(beta), 0 if beta is None else _lib.dtype_code(beta),
               _lib.ptr(o), _lib.ptr(hkk0), _lib.ptr(hkv0), _lib.ptr(hkk_t), _lib.ptr(hkv_t),
               _lib.ptr(seg), len(rows), N, H, HKV, D, V, int(num_iter), float(ridge_ratio),
-              float(gla_scale), _lib.ptr(ws), ws.numel(), _lib.stream_of(q))
+              float(gla_scale), int(bool(l2norm)), _lib.ptr(ws), ws.numel(), _lib.stream_of(q))
     return o, hkk_t, hkv_t
 
 
+def gka_chebyshev_gla(q, k, v, alpha, g, gk, gla_scale, ridge_strength: float = 0.02,
+                      solver_type: str = "chebyshev", num_iter: int = 30, bp_lambda: bool = True,
+                      chunk_size: int = 64):
+    """Training-form GKA forward (layers/gated_kalmanet/ops/chebyshev/
+    gka_chebyshev_solve.py:107-164): q, k, v [B,L,H,D] with heads expanded, q and k
+    already normalised and beta already applied to k and v by the layer
+    (gka.py:477-490), no initial state.  ridge_strength is the ratio to |H_t|_F.
+    Returns (o, kk_final [B,H,D,D] fp32 or None when num_iter == 0, kv_final).
+    Forward only: bp_lambda and chunk_size only concern the reference's backward
+    and its tiling."""
+    if solver_type != "chebyshev":
+        raise ValueError(f"Unknown GKA solver type: {solver_type}")
+    if g is None:
+        g = torch.zeros(q.shape[:3], dtype=torch.float32, device=q.device)
+    return _gka_prefill(q, k, v, alpha, g, gk, None, gla_scale, ridge_strength, num_iter,
+                        None, None, True, None, False)
+
+
+def torch_decoding_one_step(q, k, v, alpha, g, gk, gla_scale: float, ridge_strength: float,
+                            solver_type: str, num_iter: int, prev_h_kk, prev_h_kv):
+    """Training-form single-token GKA step (gka_chebyshev_solve.py:324-397): q, k, v
+    [B,1,H,D] or [1,H,D] (normalised, beta applied by the layer); separate gates g
+    (h_kv) and gk (h_kk); prev_h_kk / prev_h_kv [B,H,D,D] or None.  Returns
+    (o [B,1,H,D], h_kk or None when num_iter == 0, h_kv)."""
+    if solver_type != "chebyshev":
+        raise ValueError(f"Unknown GKA solver type: {solver_type}")
+    if q.dim() < 4:
+        q, k, v = q[None], k[None], v[None]
+        alpha = alpha[None]
+        g = None if g is None else g[None]
+        gk = None if gk is None else gk[None]
+    if g is None:
+        g = torch.zeros(q.shape[:3], dtype=torch.float32, device=q.device)
+    if num_iter > 0 and prev_h_kk is None:
+        prev_h_kk = torch.zeros(q.shape[0], q.shape[2], q.shape[3], q.shape[3],
+                                dtype=torch.float32, device=q.device)
+    o, hkk, hkv = _gka_prefill(q, k, v, alpha, g, gk, None, gla_scale, ridge_strength, num_iter,
+                               prev_h_kk if num_iter > 0 else None, prev_h_kv, True, None, False)
+    return o, hkk, hkv
+
+
 __all__ = ["fused_gka_gating", "chebyshev_iteration_gqa", "gka_chebyshev_gla_decode",
-           "gka_chebyshev_gla_prefill"]
+           "gka_chebyshev_gla_prefill", "gka_chebyshev_gla", "torch_decoding_one_step"]

@@ -168,14 +168,19 @@ int hmx_gka_decode_fwd(const void* q, const void* k, const void* v, int32_t qkv_
  * varlen via the same segment table layout as hmx_gdn_chunk_fwd (chunks of 32
  * tokens).  q [T_total, H, 128]; k, v [T_total, HKV, 128] bf16 (raw: q and k are
  * L2-normalised inside, without eps); alpha, g [T_total, H]; gk, beta
- * [T_total, H] or NULL; o [T_total, H, 128] bf16.  h_kk0 / h_kv0 fp32
+ * [T_total, H] or NULL; o [T_total, H, 128] bf16.  use_qk_l2norm = 0 uses q and k
+ * as given (the training form, whose layer normalises them and applies beta to
+ * k and v).  h_kk0 / h_kv0 fp32
  * [N, H, 128, 128] or NULL; h_kk_final / h_kv_final fp32 [N, H, 128, 128] or
  * NULL (h_kk_final is not written when num_iter == 0).
  * workspace: hmx_gka_chunk_workspace_bytes(...) bytes of device scratch.
  * Replaces: gka_chebyshev_gla_prefill
  *   vllm-inference/src/primed_vllm/gka/gka_forward.py:161-242 (and its kernels
  *   ops/chebyshev_prefill_gqa.py:28-316, ops/chunk_simple_gla_gqa.py:33-190,
- *   ops/chunk_o_gqa.py:25-171).
+ *   ops/chunk_o_gqa.py:25-171) and, with use_qk_l2norm = 0 and beta = NULL, the
+ *   training forms gka_chebyshev_gla / torch_decoding_one_step
+ *   (training/src/hmf/model/hybrid_zoo/layers/gated_kalmanet/ops/chebyshev/
+ *   gka_chebyshev_solve.py:107-164, :324-397).
  */
 int hmx_gka_chunk_fwd(const void* q, const void* k, const void* v, int32_t qkv_dtype,
                       const void* alpha, int32_t alpha_dtype, const void* g, int32_t g_dtype,
@@ -184,7 +189,7 @@ int hmx_gka_chunk_fwd(const void* q, const void* k, const void* v, int32_t qkv_d
                       float* h_kk_final, float* h_kv_final,
                       const int32_t* seg_table, int32_t nseg_total, int32_t N,
                       int32_t H, int32_t HKV, int32_t D, int32_t V,
-                      int32_t num_iter, float ridge_ratio, float scale,
+                      int32_t num_iter, float ridge_ratio, float scale, int32_t use_qk_l2norm,
                       void* workspace, size_t workspace_bytes, void* stream);
 
 /* Workspace bytes hmx_gka_chunk_fwd needs (host-only arithmetic).  Companion of

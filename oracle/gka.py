@@ -73,16 +73,18 @@ def _expand(x, H):
 
 
 def gka_seq(q, k, v, alpha, g, gk, beta, scale, ridge_ratio, num_iter, h_kk0=None, h_kv0=None,
-            dtype=DEFAULT):
+            dtype=DEFAULT, normalize=True):
     """Per-token GKA over ONE sequence (prefill semantics).
 
     q [T,H,D]; k [T,HKV,D]; v [T,HKV,V]; alpha, g [T,H]; gk, beta [T,H] or None.
-    Returns (o [T,H,V], h_kk [H,D,D] or None, h_kv [H,D,V]).
+    ``normalize=False`` uses q and k as given (the training form, whose layer has
+    normalised them).  Returns (o [T,H,V], h_kk [H,D,D] or None, h_kv [H,D,V]).
     """
     T, H, D = q.shape
     V = v.shape[-1]
-    q = l2n(q.to(dtype))
-    k = _expand(l2n(k.to(dtype)), H)
+    nz = l2n if normalize else (lambda x: x)
+    q = nz(q.to(dtype))
+    k = _expand(nz(k.to(dtype)), H)
     v = _expand(v.to(dtype), H)
     be = None if beta is None else beta.to(dtype) + EPS
     Hs = torch.zeros(H, D, D, dtype=dtype) if h_kk0 is None else h_kk0.to(dtype).clone()
@@ -137,6 +139,51 @@ def gka_chebyshev_gla_prefill(q, k, v, alpha, g, gk, beta, gla_scale, ridge_rati
     if not output_final_state:
         return o, None, None
     return o, (hkk if num_iter > 0 else None), hkv
+
+
+def gka_chebyshev_gla(q, k, v, alpha, g, gk, gla_scale, ridge_strength=0.02, num_iter=30,
+                      dtype=DEFAULT):
+    """Training-form GKA forward (layers/gated_kalmanet/ops/chebyshev/
+    gka_chebyshev_solve.py:107-164): q, k, v [B,L,H,D] used as given (the layer
+    normalised q, k with /(|x|+1e-6) and applied (beta+1e-6) to k and v,
+    gka.py:477-490); H_t = e^{gk} H + k k^T from zero (ChebyshevIteration with
+    h0=None, chebyshev_iteration.py:569-604); GLA with gate g from zero.
+    Returns (o, kk_final or None, kv_final)."""
+    B, T, H, D = q.shape
+    V = v.shape[-1]
+    o = torch.zeros(B, T, H, V, dtype=dtype)
+    kk = torch.zeros(B, H, D, D, dtype=dtype)
+    kv = torch.zeros(B, H, D, V, dtype=dtype)
+    for b in range(B):
+        gb = torch.zeros(T, H, dtype=dtype) if g is None else g[b]
+        o[b], hk, kv[b] = gka_seq(q[b], k[b], v[b], alpha[b], gb, None if gk is None else gk[b],
+                                  None, gla_scale, ridge_strength, num_iter, dtype=dtype,
+                                  normalize=False)
+        if hk is not None:
+            kk[b] = hk
+    return o, (kk if num_iter > 0 else None), kv
+
+
+def torch_decoding_one_step(q, k, v, alpha, g, gk, gla_scale, ridge_strength, num_iter,
+                            prev_h_kk=None, prev_h_kv=None, dtype=DEFAULT):
+    """Training-form single-token step (gka_chebyshev_solve.py:324-397; the h_kk
+    update and solve of its inference kernel :167-266): q, k, v [B,1,H,D].
+    Returns (o [B,1,H,D], h_kk or None, h_kv)."""
+    B, _, H, D = q.shape
+    V = v.shape[-1]
+    o = torch.zeros(B, 1, H, V, dtype=dtype)
+    kk = torch.zeros(B, H, D, D, dtype=dtype)
+    kv = torch.zeros(B, H, D, V, dtype=dtype)
+    for b in range(B):
+        gb = torch.zeros(1, H, dtype=dtype) if g is None else g[b]
+        o[b], hk, kv[b] = gka_seq(q[b], k[b], v[b], alpha[b], gb, None if gk is None else gk[b],
+                                  None, gla_scale, ridge_strength, num_iter,
+                                  None if prev_h_kk is None else prev_h_kk[b],
+                                  None if prev_h_kv is None else prev_h_kv[b], dtype=dtype,
+                                  normalize=False)
+        if hk is not None:
+            kk[b] = hk
+    return o, (kk if num_iter > 0 else None), kv
 
 
 def gka_chebyshev_gla_decode(q, k, v, alpha, g, gk, beta, gla_scale, ridge_ratio=0.02,

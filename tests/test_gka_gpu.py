@@ -168,3 +168,60 @@ def test_gka_prefill_c3_subset(dev):
     sub = [a[:, :512, :2] for a in args]
     o_r, _, _ = ref.gka_chebyshev_gla_prefill(*sub, 128 ** -0.5, ridge_ratio=0.01, num_iter=8)
     assert_out_close(o[:, :512, :2], o_r)
+
+
+def _layer_prepared(B, T, H, seed):
+    """Inputs as the training layer hands them over (gka.py:477-490): q, k divided by
+    (|x| + 1e-6), (beta + 1e-6) applied to k and v, all cast back to bf16."""
+    g0 = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, T, H, 128, generator=g0)
+    k = torch.randn(B, T, H, 128, generator=g0)
+    v = torch.randn(B, T, H, 128, generator=g0)
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=g0))
+    q = (q / (q.norm(dim=-1, keepdim=True) + 1e-6)).bfloat16()
+    k = (k / (k.norm(dim=-1, keepdim=True) + 1e-6) * (beta[..., None] + 1e-6)).bfloat16()
+    v = (v * (beta[..., None] + 1e-6)).bfloat16()
+    alpha = torch.sigmoid(torch.randn(B, T, H, generator=g0))
+    g = F.logsigmoid(torch.randn(B, T, H, generator=g0))
+    gk = F.logsigmoid(torch.randn(B, T, H, generator=g0) + 1.0)
+    return q, k, v, alpha, g, gk
+
+
+@pytest.mark.parametrize("num_iter", [8, 0])
+def test_gka_training_form(dev, num_iter):
+    q, k, v, alpha, g, gk = _layer_prepared(2, 70, 2, 50 + num_iter)
+    o_r, hk_r, hv_r = ref.gka_chebyshev_gla(q, k, v, alpha, g, gk, 128 ** -0.5,
+                                           ridge_strength=0.02, num_iter=num_iter)
+    d = [x.to(dev) for x in (q, k, v, alpha, g, gk)]
+    o, hk, hv = hmx.gka_chebyshev_gla(*d, 128 ** -0.5, ridge_strength=0.02, num_iter=num_iter)
+    torch.cuda.synchronize()
+    assert_out_close(o, o_r)
+    assert_state_close(hv, hv_r, what="kv_final")
+    if num_iter:
+        assert_state_close(hk, hk_r, what="kk_final")
+    else:
+        assert hk is None
+
+
+def test_gka_training_decode_steps(dev):
+    q, k, v, alpha, g, gk = _layer_prepared(3, 6, 2, 60)
+    g0 = torch.Generator().manual_seed(61)
+    hk0 = _psd_pool(3, 2, g0)
+    hv0 = torch.randn(3, 2, 128, 128, generator=g0) * 0.02
+    hk_r, hv_r, hk, hv = hk0, hv0, hk0.to(dev), hv0.to(dev)
+    for t in range(q.shape[1]):
+        sl = slice(t, t + 1)
+        o_r, hk_r, hv_r = ref.torch_decoding_one_step(q[:, sl], k[:, sl], v[:, sl], alpha[:, sl],
+                                                      g[:, sl], gk[:, sl], 0.1, 0.02, 8, hk_r, hv_r)
+        o, hk, hv = hmx.torch_decoding_one_step(*(x[:, sl].to(dev) for x in (q, k, v, alpha, g, gk)),
+                                                0.1, 0.02, "chebyshev", 8, hk, hv)
+        torch.cuda.synchronize()
+        assert o.shape == (3, 1, 2, 128)
+        assert_out_close(o, o_r)
+    assert_state_close(hk, hk_r, what="h_kk")
+    assert_state_close(hv, hv_r, what="h_kv")
+    # unbatched [1, H, D] inputs and no h_kk (num_iter = 0)
+    o, hk1, hv1 = hmx.torch_decoding_one_step(*(x[0, 0:1].to(dev) for x in (q, k, v, alpha, g, gk)),
+                                              0.1, 0.02, "chebyshev", 0, None, None)
+    torch.cuda.synchronize()
+    assert hk1 is None and o.shape == (1, 1, 2, 128)

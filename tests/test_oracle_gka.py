@@ -149,3 +149,33 @@ def test_gka_gating_matches_library():
     g, al, be = ref.gka_gating(A_log, a, ai, b, dt)
     assert torch.allclose(g[0], -A_log.exp() * F.softplus(a + dt))
     assert torch.allclose(al[0], torch.sigmoid(ai)) and torch.allclose(be[0], torch.sigmoid(b))
+
+
+def test_training_form_equals_serving_form_on_layer_normalised_inputs():
+    """gka_chebyshev_gla on inputs the layer prepared (unit q, k~ = (beta+eps) k^,
+    v~ = (beta+eps) v) equals gka_chebyshev_gla_prefill on the raw inputs."""
+    T, H, D = 24, 2, 8
+    q, k, v, alpha, g, gk, be = _inputs(T, H, H, D, 30)
+    o_s, hk_s, hv_s = ref.gka_chebyshev_gla_prefill(q[None], k[None], v[None], alpha[None], g[None],
+                                                   gk[None], be[None], 0.3, ridge_ratio=0.05,
+                                                   num_iter=6)
+    s = (be + 1e-6)[..., None]
+    qn, kn = ref.l2n(q), ref.l2n(k) * s
+    o_t, hk_t, hv_t = ref.gka_chebyshev_gla(qn[None], kn[None], (v * s)[None], alpha[None], g[None],
+                                           gk[None], 0.3, ridge_strength=0.05, num_iter=6)
+    assert torch.allclose(o_t, o_s, rtol=1e-10, atol=1e-12)
+    assert torch.allclose(hk_t, hk_s) and torch.allclose(hv_t, hv_s)
+
+
+def test_training_decode_steps_equal_training_prefill():
+    T, H, D = 9, 2, 8
+    q, k, v, alpha, g, gk, _ = _inputs(T, H, H, D, 31)
+    o_p, hk_p, hv_p = ref.gka_chebyshev_gla(q[None], k[None], v[None], alpha[None], g[None],
+                                           gk[None], 0.2, ridge_strength=0.02, num_iter=5)
+    hk = hv = None
+    for t in range(T):
+        o, hk, hv = ref.torch_decoding_one_step(q[None, t:t + 1], k[None, t:t + 1], v[None, t:t + 1],
+                                                alpha[None, t:t + 1], g[None, t:t + 1],
+                                                gk[None, t:t + 1], 0.2, 0.02, 5, hk, hv)
+        assert torch.allclose(o[0, 0], o_p[0, t])
+    assert torch.allclose(hk, hk_p) and torch.allclose(hv, hv_p)
