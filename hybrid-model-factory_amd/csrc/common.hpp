@@ -63,6 +63,27 @@ __device__ __forceinline__ void load_vec(const T* __restrict__ p, float* out) {
   }
 }
 
+// store_vec with non-temporal stores: for streams written once and not re-read
+// by the same kernel (a recurrent state's write-back).
+template <int N, typename T>
+__device__ __forceinline__ void store_vec_nt(T* __restrict__ p, const float* in) {
+  if constexpr (sizeof(T) == 4) {
+#pragma unroll
+    for (int i = 0; i < N; i += 4)
+      __builtin_nontemporal_store(f32x4{in[i], in[i + 1], in[i + 2], in[i + 3]},
+                                  reinterpret_cast<f32x4*>(p + i));
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; i += 4) {
+      typedef T T4 __attribute__((ext_vector_type(4)));
+      T4 t;
+      t[0] = from_f32<T>(in[i]); t[1] = from_f32<T>(in[i + 1]);
+      t[2] = from_f32<T>(in[i + 2]); t[3] = from_f32<T>(in[i + 3]);
+      __builtin_nontemporal_store(t, reinterpret_cast<T4*>(p + i));
+    }
+  }
+}
+
 template <int N, typename T>
 __device__ __forceinline__ void store_vec(T* __restrict__ p, const float* in) {
   if constexpr (sizeof(T) == 4) {

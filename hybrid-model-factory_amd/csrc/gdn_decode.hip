@@ -163,7 +163,7 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(RecurrentParams p) {
   TS* dst = static_cast<TS*>(p.ht) + write_row * p.ht_rs + (int64_t)h * K * V +
             (int64_t)(r * R) * V + col;
 #pragma unroll
-  for (int i = 0; i < R; ++i) store_vec<4>(dst + (int64_t)i * V, S[i]);
+  for (int i = 0; i < R; ++i) store_vec_nt<4>(dst + (int64_t)i * V, S[i]);
 }
 
 template <int K, typename TQ, typename TS>

@@ -16,9 +16,21 @@
 // 4 consecutive n of columns 4 (t mod N/4) for rows p = t / (N/4) + k (1024/N),
 // so every state load and store is a fully coalesced 16-byte (fp32) access.
 #include "common.hpp"
+#include "mfma.hpp"
 
 namespace hmx {
 namespace ssdd {
+
+// Sum over the GN lanes that share a state row (GN = 16: one DPP row; GN = 32:
+// two rows combined by row_bcast:15 into the odd rows).  Valid in the row's
+// leader lane: lane 16 of each 32 (GN = 32) or lane 0 of each 16.
+template <int GN>
+__device__ __forceinline__ float row_total(float x) {
+  x = row16_sum(x);
+  if constexpr (GN == 32)
+    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x142, 0xA, 0xF, false));
+  return x;
+}
 
 constexpr int NTHR = 256;
 
@@ -59,10 +71,12 @@ __device__ __forceinline__ f32x4 ld4(const TS* p) {
   }
 }
 
+// The updated state is written once and not read again in this step:
+// non-temporal stores keep it from displacing the state still being read.
 template <typename TS>
 __device__ __forceinline__ void st4(TS* p, const f32x4& v) {
   if constexpr (sizeof(TS) == 4) {
-    *reinterpret_cast<f32x4*>(p) = v;
+    __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(p));
   } else {
     *reinterpret_cast<bf16x4*>(p) = bf16x4{(bf16)v[0], (bf16)v[1], (bf16)v[2], (bf16)v[3]};
   }
@@ -117,9 +131,8 @@ __global__ __launch_bounds__(NTHR) void ssd_state_update_kernel(Params p) {
         acc += st[k][j] * cv[j];
       }
     }
-#pragma unroll
-    for (int m = 1; m < GN; m <<= 1) acc += shfl_xor(acc, m);
-    if (tid % GN == 0) {
+    acc = row_total<GN>(acc);
+    if (GN == 32 ? (tid & 31) == 16 : (tid & 15) == 0) {   // the row's leader lane
       float o = acc;
       if (p.D) o += p.D[(int64_t)h * p.d_hs + (int64_t)pr * p.d_ps] * xv;
       if (p.z) {
