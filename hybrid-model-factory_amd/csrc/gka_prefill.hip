@@ -40,7 +40,16 @@ namespace gkap {
 constexpr int C = 32;           // tokens per chunk
 constexpr int MT = C / 16;
 constexpr int D = 128;
-constexpr int NTHR = 256;
+#ifndef HMX_GKA_WAVES
+#define HMX_GKA_WAVES 8
+#endif
+constexpr int NW = HMX_GKA_WAVES;   // waves per workgroup (one workgroup per CU)
+constexpr int NTHR = 64 * NW;
+constexpr int CW = D / NW;          // state columns owned by one wave
+constexpr int NCT = CW / 16;        // 16-column tiles per wave
+constexpr int RPP = NTHR / 16;      // chunk rows staged per pass (16 lanes per row)
+constexpr int NPASS = C / RPP;      // staging passes per chunk
+static_assert(NW == 4 || NW == 8, "4 or 8 waves");
 constexpr int LDQ = D + 8;      // bf16 [C][D] row stride (q, k, v, O)
 constexpr int LDX = C + 8;      // bf16 [D][C] row stride (X^T hi/lo, Q^T)
 constexpr int LDZ = C + 8;      // bf16 [C][C] row stride (Z, A2)
@@ -63,12 +72,14 @@ constexpr int OFF_ZH = OFF_XL + SZ_XT;
 constexpr int OFF_ZL = OFF_ZH + SZ_Z;
 constexpr int OFF_KK = OFF_ZL + SZ_Z;              // fp32 [C][LDK]
 constexpr int OFF_S = OFF_KK + C * LDK * 4;         // fp32 per-token scalars
-constexpr int NSC = 21;                             // scalar arrays of C floats
+constexpr int NSC = 25;                             // scalar arrays of C floats
 constexpr int SMEM = OFF_S + NSC * C * 4;
 static_assert(SMEM <= 80 * 1024, "LDS budget");
 // per-token scalar array indices
 enum { S_G, S_GK, S_EG, S_EGK, S_EDL, S_EDLK, S_BE, S_SK, S_IQ, S_ALPHA, S_KN2, S_QN2,
-       S_U0, S_U1, S_U2, S_U3, S_F0, S_F1, S_TAU, S_LAM, S_CC };
+       S_U0 };                                        // S_U0 .. S_U0 + NW - 1: per-wave u partials
+constexpr int S_F0 = S_U0 + NW, S_F1 = S_F0 + 1, S_TAU = S_F1 + 1, S_LAM = S_TAU + 1,
+              S_CC = S_LAM + 1;
 static_assert(S_CC < NSC, "scalar slots");
 
 struct SegInfo { int n, bos, eos, c_start, c_end, seg_idx, first_seg, nseg; };
@@ -103,7 +114,7 @@ __device__ __forceinline__ SegInfo load_seg(const int* seg, int s) {
 }
 
 struct Raw {
-  bf16x8 k[MT], v[MT], q[MT];
+  bf16x8 k[NPASS], v[NPASS], q[NPASS];
   float g, gk, b, a;
 };
 
@@ -112,8 +123,8 @@ __device__ __forceinline__ void load_raw(Raw& r, const Params& p, const bf16* qh
                                          const bf16* vh, int64_t q_rs, int64_t kv_rs, int tok0,
                                          int nval, int tid, int h) {
 #pragma unroll
-  for (int pass = 0; pass < MT; ++pass) {
-    const int row = pass * 16 + (tid >> 4), f0 = (tid & 15) * 8;
+  for (int pass = 0; pass < NPASS; ++pass) {
+    const int row = pass * RPP + (tid >> 4), f0 = (tid & 15) * 8;
     const bool ok = row < nval;
     const int64_t tok = tok0 + row;
     r.k[pass] = ok ? *reinterpret_cast<const bf16x8*>(kh + tok * kv_rs + f0) : bf16x8{};
@@ -155,7 +166,8 @@ __device__ __forceinline__ void put_t_hilo(bf16* th, bf16* tl, int ld, int r0, i
 }
 
 template <int MODE>
-__global__ __launch_bounds__(NTHR, 1) void gka_chunk_kernel(Params p) {
+// One workgroup per CU: NW / 4 waves per SIMD (the second bound is waves per SIMD).
+__global__ __launch_bounds__(NTHR, NW / 4) void gka_chunk_kernel(Params p) {
   __shared__ __align__(16) unsigned char smem[SMEM];
   bf16* sQ = reinterpret_cast<bf16*>(smem + OFF_Q);
   bf16* sK = reinterpret_cast<bf16*>(smem + OFF_K);
@@ -180,7 +192,7 @@ __global__ __launch_bounds__(NTHR, 1) void gka_chunk_kernel(Params p) {
   if (MODE == MODE_LOCAL && si.seg_idx == si.nseg - 1) return;
 
   // ---- initial states ----------------------------------------------------
-  f32x4 Hs[8][2], Ss[8][2];
+  f32x4 Hs[8][NCT], Ss[8][NCT];
   {
     const float *hsrc = nullptr, *ssrc = nullptr;
     if (MODE == MODE_OUT) {
@@ -195,10 +207,10 @@ __global__ __launch_bounds__(NTHR, 1) void gka_chunk_kernel(Params p) {
 #pragma unroll
     for (int rt = 0; rt < 8; ++rt)
 #pragma unroll
-      for (int ct = 0; ct < 2; ++ct)
+      for (int ct = 0; ct < NCT; ++ct)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          const int off = (16 * rt + 4 * q4 + v) * D + 32 * wave + 16 * ct + l16;
+          const int off = (16 * rt + 4 * q4 + v) * D + CW * wave + 16 * ct + l16;
           Hs[rt][ct][v] = (hsrc && track_h) ? hsrc[off] : 0.f;
           Ss[rt][ct][v] = ssrc ? ssrc[off] : 0.f;
         }
@@ -221,8 +233,8 @@ __global__ __launch_bounds__(NTHR, 1) void gka_chunk_kernel(Params p) {
 
     // ---- P0: stage raw rows, row norms, per-token gates ---------------------
 #pragma unroll
-    for (int pass = 0; pass < MT; ++pass) {
-      const int row = pass * 16 + (tid >> 4), f0 = (tid & 15) * 8;
+    for (int pass = 0; pass < NPASS; ++pass) {
+      const int row = pass * RPP + (tid >> 4), f0 = (tid & 15) * 8;
       *reinterpret_cast<bf16x8*>(sK + row * LDQ + f0) = raw.k[pass];
       *reinterpret_cast<bf16x8*>(sV + row * LDQ + f0) = raw.v[pass];
       const float kn2 = row_sumsq(raw.k[pass]);
@@ -268,26 +280,26 @@ __global__ __launch_bounds__(NTHR, 1) void gka_chunk_kernel(Params p) {
 
     lds_barrier();
     // q^ for this wave's columns (C layout), fp32
-    f32x4 qv[MT][2];
+    f32x4 qv[MT][NCT];
     if (MODE == MODE_OUT) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct)
+        for (int ct = 0; ct < NCT; ++ct)
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
             const int t = 16 * mt + 4 * q4 + v;
-            qv[mt][ct][v] = (float)sQ[t * LDQ + 32 * wave + 16 * ct + l16] * SC(S_IQ, t);
+            qv[mt][ct][v] = (float)sQ[t * LDQ + CW * wave + 16 * ct + l16] * SC(S_IQ, t);
           }
     }
 
     // ---- P1: the Chebyshev solve (OUT, num_iter > 0) -------------------------
-    f32x4 xq[MT][2];  // the query fed to the GLA (solved + alpha-blended, or q^)
+    f32x4 xq[MT][NCT];  // the query fed to the GLA (solved + alpha-blended, or q^)
     if (MODE == MODE_OUT) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct) xq[mt][ct] = qv[mt][ct];
+        for (int ct = 0; ct < NCT; ++ct) xq[mt][ct] = qv[mt][ct];
     }
     if (solve) {
       // P1a: u_j = k~_j H_c k~_j^T (per-wave partials), |H_c|^2, scaled Gram k~.k~
@@ -299,21 +311,21 @@ __global__ __launch_bounds__(NTHR, 1) void gka_chunk_kernel(Params p) {
           for (int v = 0; v < 4; ++v) u[mt][v] = 0.f;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-          bf16x8 Hh[2], Hl[2];
+          bf16x8 Hh[NCT], Hl[NCT];
 #pragma unroll
-          for (int ct = 0; ct < 2; ++ct) pack_b_hilo(Hs[2 * ks][ct], Hs[2 * ks + 1][ct], Hh[ct], Hl[ct]);
+          for (int ct = 0; ct < NCT; ++ct) pack_b_hilo(Hs[2 * ks][ct], Hs[2 * ks + 1][ct], Hh[ct], Hl[ct]);
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) {
             const bf16x8 a = frag_perm(sK, LDQ, 16 * mt, 32 * ks, lane);
 #pragma unroll
-            for (int ct = 0; ct < 2; ++ct) {
+            for (int ct = 0; ct < NCT; ++ct) {
               f32x4 acc = {0.f, 0.f, 0.f, 0.f};
               acc = mfma16(a, Hh[ct], acc);
               acc = mfma16(a, Hl[ct], acc);
 #pragma unroll
               for (int v = 0; v < 4; ++v)
                 u[mt][v] += acc[v] *
-                            (float)sK[(16 * mt + 4 * q4 + v) * LDQ + 32 * wave + 16 * ct + l16];
+                            (float)sK[(16 * mt + 4 * q4 + v) * LDQ + CW * wave + 16 * ct + l16];
             }
           }
         }
@@ -328,11 +340,11 @@ __global__ __launch_bounds__(NTHR, 1) void gka_chunk_kernel(Params p) {
 #pragma unroll
         for (int rt = 0; rt < 8; ++rt)
 #pragma unroll
-          for (int ct = 0; ct < 2; ++ct)
+          for (int ct = 0; ct < NCT; ++ct)
 #pragma unroll
             for (int v = 0; v < 4; ++v) hn += Hs[rt][ct][v] * Hs[rt][ct][v];
         hn = wave_sum(hn);
-        if (lane == 0) SC(S_F0 + 0, C - 1 - wave) = hn;  // |H_c|^2 partials in the F0 tail
+        if (lane == 0) SC(S_F0, C - 1 - wave) = hn;  // |H_c|^2 partials in the F0 tail
         // Gram tiles (0,0), (1,0), (1,1) on waves 0..2: sKK[t][j] = s_t s_j k_t.k_j
         if (wave < 3) {
           const int a = (wave == 0) ? 0 : 1, b = (wave == 2) ? 1 : 0;
@@ -349,7 +361,9 @@ __global__ __launch_bounds__(NTHR, 1) void gka_chunk_kernel(Params p) {
       }
       lds_barrier();
       // P1b: in-chunk part of |H_t|_F^2 = sum_l M_tl (M . KK^2)_tl, M_tj = e^{Gk_t-Gk_j} (t>=j)
-      float hc2 = SC(S_F0, C - 1) + SC(S_F0, C - 2) + SC(S_F0, C - 3) + SC(S_F0, C - 4);
+      float hc2 = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) hc2 += SC(S_F0, C - 1 - w);
       lds_barrier();
       if (wave < 3) {
         const int a = (wave == 0) ? 0 : 1, b = (wave == 2) ? 1 : 0;
@@ -387,8 +401,10 @@ __global__ __launch_bounds__(NTHR, 1) void gka_chunk_kernel(Params p) {
         const int t = tid;
         float cross = 0.f;
         for (int j = 0; j <= t; ++j) {
-          const float uj = (SC(S_U0, j) + SC(S_U1, j) + SC(S_U2, j) + SC(S_U3, j)) *
-                           SC(S_SK, j) * SC(S_SK, j);
+          float usum = 0.f;
+#pragma unroll
+          for (int w = 0; w < NW; ++w) usum += SC(S_U0 + w, j);
+          const float uj = usum * SC(S_SK, j) * SC(S_SK, j);
           cross += fast_exp(SC(S_GK, t) - SC(S_GK, j)) * uj;
         }
         const float egk = SC(S_EGK, t);
@@ -415,11 +431,11 @@ __global__ __launch_bounds__(NTHR, 1) void gka_chunk_kernel(Params p) {
           ccv[mt][v] = SC(S_CC, t);
           om[mt][v] = 2.0f;
         }
-      f32x4 X[MT][2], Xp[MT][2];
+      f32x4 X[MT][NCT], Xp[MT][NCT];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
+        for (int ct = 0; ct < NCT; ++ct) {
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
             X[mt][ct][v] = tau[mt][v] * qv[mt][ct][v];
@@ -430,8 +446,8 @@ __global__ __launch_bounds__(NTHR, 1) void gka_chunk_kernel(Params p) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-          for (int ct = 0; ct < 2; ++ct)
-            put_t_hilo(sXh, sXl, LDX, 16 * mt, 32 * wave + 16 * ct, X[mt][ct], q4, l16);
+          for (int ct = 0; ct < NCT; ++ct)
+            put_t_hilo(sXh, sXl, LDX, 16 * mt, CW * wave + 16 * ct, X[mt][ct], q4, l16);
         lds_barrier();
         // Z~_tj = M_tj s_j^2 (x_t . k_j) for j <= t on waves 0..2
         if (wave < 3) {
@@ -458,7 +474,7 @@ __global__ __launch_bounds__(NTHR, 1) void gka_chunk_kernel(Params p) {
             sZh[t * LDZ + j] = hi;
             sZl[t * LDZ + j] = (bf16)(zs[v] - (float)hi);
           }
-        } else {
+        } else if (wave == 3) {
           // wave 3 zeroes the empty upper tile (0,1)
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
@@ -467,22 +483,22 @@ __global__ __launch_bounds__(NTHR, 1) void gka_chunk_kernel(Params p) {
           }
         }
         // Y = e^{Gk} (X H_c) for this wave's columns (X, H as hi/lo)
-        f32x4 Y[MT][2];
+        f32x4 Y[MT][NCT];
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-          for (int ct = 0; ct < 2; ++ct) Y[mt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+          for (int ct = 0; ct < NCT; ++ct) Y[mt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-          bf16x8 Hh[2], Hl[2];
+          bf16x8 Hh[NCT], Hl[NCT];
 #pragma unroll
-          for (int ct = 0; ct < 2; ++ct) pack_b_hilo(Hs[2 * ks][ct], Hs[2 * ks + 1][ct], Hh[ct], Hl[ct]);
+          for (int ct = 0; ct < NCT; ++ct) pack_b_hilo(Hs[2 * ks][ct], Hs[2 * ks + 1][ct], Hh[ct], Hl[ct]);
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) {
             const bf16x8 ah = frag_t_perm(sXh, LDX, 32 * ks, 16 * mt, lane);
             const bf16x8 al = frag_t_perm(sXl, LDX, 32 * ks, 16 * mt, lane);
 #pragma unroll
-            for (int ct = 0; ct < 2; ++ct) {
+            for (int ct = 0; ct < NCT; ++ct) {
               Y[mt][ct] = mfma16(ah, Hh[ct], Y[mt][ct]);
               Y[mt][ct] = mfma16(ah, Hl[ct], Y[mt][ct]);
               Y[mt][ct] = mfma16(al, Hh[ct], Y[mt][ct]);
@@ -494,14 +510,14 @@ __global__ __launch_bounds__(NTHR, 1) void gka_chunk_kernel(Params p) {
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
             const float e = SC(S_EGK, 16 * mt + 4 * q4 + v);
-            Y[mt][0][v] *= e;
-            Y[mt][1][v] *= e;
+#pragma unroll
+            for (int ct = 0; ct < NCT; ++ct) Y[mt][ct][v] *= e;
           }
         lds_barrier();
         // Y += Z~ K (Z~ hi/lo, raw K exact)
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
-          const bf16x8 bk = frag_t(sK, LDQ, 0, 32 * wave + 16 * ct, lane);
+        for (int ct = 0; ct < NCT; ++ct) {
+          const bf16x8 bk = frag_t(sK, LDQ, 0, CW * wave + 16 * ct, lane);
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) {
             Y[mt][ct] = mfma16(frag(sZh, LDZ, 16 * mt, 0, lane), bk, Y[mt][ct]);
@@ -516,7 +532,7 @@ __global__ __launch_bounds__(NTHR, 1) void gka_chunk_kernel(Params p) {
             const float w = 1.0f / (1.0f - ccv[mt][v] * om[mt][v]);
             om[mt][v] = w;
 #pragma unroll
-            for (int ct = 0; ct < 2; ++ct) {
+            for (int ct = 0; ct < NCT; ++ct) {
               const float x = X[mt][ct][v];
               const float grad = tau[mt][v] * w * (Y[mt][ct][v] + lam[mt][v] * x - qv[mt][ct][v]) +
                                  (w - 1.0f) * Xp[mt][ct][v];
@@ -532,7 +548,7 @@ __global__ __launch_bounds__(NTHR, 1) void gka_chunk_kernel(Params p) {
         for (int v = 0; v < 4; ++v) {
           const float al = SC(S_ALPHA, 16 * mt + 4 * q4 + v);
 #pragma unroll
-          for (int ct = 0; ct < 2; ++ct)
+          for (int ct = 0; ct < NCT; ++ct)
             xq[mt][ct][v] = qv[mt][ct][v] + al * (X[mt][ct][v] - qv[mt][ct][v]);
         }
     }
@@ -542,8 +558,8 @@ __global__ __launch_bounds__(NTHR, 1) void gka_chunk_kernel(Params p) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct)
-          put_t_hilo(sXh, sXl, LDX, 16 * mt, 32 * wave + 16 * ct, xq[mt][ct], q4, l16);
+        for (int ct = 0; ct < NCT; ++ct)
+          put_t_hilo(sXh, sXl, LDX, 16 * mt, CW * wave + 16 * ct, xq[mt][ct], q4, l16);
       lds_barrier();
       // A2_tj = e^{G_t-G_j} (xq_t . k_j) s_j (beta_j+eps)  (j <= t), waves 0..2
       if (wave < 3) {
@@ -561,28 +577,28 @@ __global__ __launch_bounds__(NTHR, 1) void gka_chunk_kernel(Params p) {
           const float w = (t >= j) ? fast_exp(SC(S_G, t) - SC(S_G, j)) * SC(S_SK, j) * SC(S_BE, j) : 0.f;
           sZh[t * LDZ + j] = (bf16)(z[v] * w);
         }
-      } else {
+      } else if (wave == 3) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) sZh[(4 * q4 + v) * LDZ + 16 + l16] = (bf16)0.f;
       }
-      f32x4 O[MT][2];
+      f32x4 O[MT][NCT];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct) O[mt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int ct = 0; ct < NCT; ++ct) O[mt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         // The solved query is large off the key span, so both operands carry a
         // bf16 remainder: a single bf16 rounding of either costs ~3% of |o|.
-        bf16x8 Sh[2], Sl[2];
+        bf16x8 Sh[NCT], Sl[NCT];
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct) pack_b_hilo(Ss[2 * ks][ct], Ss[2 * ks + 1][ct], Sh[ct], Sl[ct]);
+        for (int ct = 0; ct < NCT; ++ct) pack_b_hilo(Ss[2 * ks][ct], Ss[2 * ks + 1][ct], Sh[ct], Sl[ct]);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
           const bf16x8 ah = frag_t_perm(sXh, LDX, 32 * ks, 16 * mt, lane);
           const bf16x8 al = frag_t_perm(sXl, LDX, 32 * ks, 16 * mt, lane);
 #pragma unroll
-          for (int ct = 0; ct < 2; ++ct) {
+          for (int ct = 0; ct < NCT; ++ct) {
             O[mt][ct] = mfma16(ah, Sh[ct], O[mt][ct]);
             O[mt][ct] = mfma16(al, Sh[ct], O[mt][ct]);
             O[mt][ct] = mfma16(ah, Sl[ct], O[mt][ct]);
@@ -594,23 +610,23 @@ __global__ __launch_bounds__(NTHR, 1) void gka_chunk_kernel(Params p) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const float e = SC(S_EG, 16 * mt + 4 * q4 + v);
-          O[mt][0][v] *= e;
-          O[mt][1][v] *= e;
+#pragma unroll
+          for (int ct = 0; ct < NCT; ++ct) O[mt][ct][v] *= e;
         }
       lds_barrier();
 #pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        const bf16x8 bv = frag_t(sV, LDQ, 0, 32 * wave + 16 * ct, lane);
+      for (int ct = 0; ct < NCT; ++ct) {
+        const bf16x8 bv = frag_t(sV, LDQ, 0, CW * wave + 16 * ct, lane);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) O[mt][ct] = mfma16(frag(sZh, LDZ, 16 * mt, 0, lane), bv, O[mt][ct]);
       }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct)
+        for (int ct = 0; ct < NCT; ++ct)
 #pragma unroll
           for (int v = 0; v < 4; ++v)
-            sO[(16 * mt + 4 * q4 + v) * LDQ + 32 * wave + 16 * ct + l16] = (bf16)(O[mt][ct][v] * p.scale);
+            sO[(16 * mt + 4 * q4 + v) * LDQ + CW * wave + 16 * ct + l16] = (bf16)(O[mt][ct][v] * p.scale);
     }
 
     // ---- P3: state updates (hi/lo B operands) ---------------------------------
@@ -619,7 +635,7 @@ __global__ __launch_bounds__(NTHR, 1) void gka_chunk_kernel(Params p) {
 #pragma unroll
       for (int rt = 0; rt < 8; ++rt)
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct)
+        for (int ct = 0; ct < NCT; ++ct)
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
             Ss[rt][ct][v] *= egl;
@@ -634,9 +650,9 @@ __global__ __launch_bounds__(NTHR, 1) void gka_chunk_kernel(Params p) {
         fh[j] = s * s * SC(S_EDLK, t);
       }
 #pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        const bf16x8 vr = frag_t(sV, LDQ, 0, 32 * wave + 16 * ct, lane);
-        const bf16x8 kr = frag_t(sK, LDQ, 0, 32 * wave + 16 * ct, lane);
+      for (int ct = 0; ct < NCT; ++ct) {
+        const bf16x8 vr = frag_t(sV, LDQ, 0, CW * wave + 16 * ct, lane);
+        const bf16x8 kr = frag_t(sK, LDQ, 0, CW * wave + 16 * ct, lane);
         bf16x8 vh, vl, kh_, kl_;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -665,8 +681,8 @@ __global__ __launch_bounds__(NTHR, 1) void gka_chunk_kernel(Params p) {
     if (MODE == MODE_OUT) {
       bf16* oh = p.o + (int64_t)h * D;
 #pragma unroll
-      for (int pass = 0; pass < MT; ++pass) {
-        const int row = pass * 16 + (tid >> 4), f0 = (tid & 15) * 8;
+      for (int pass = 0; pass < NPASS; ++pass) {
+        const int row = pass * RPP + (tid >> 4), f0 = (tid & 15) * 8;
         if (row < nval)
           *reinterpret_cast<bf16x8*>(oh + (int64_t)(tok0 + row) * q_rs + f0) =
               *reinterpret_cast<const bf16x8*>(sO + row * LDQ + f0);
@@ -692,10 +708,10 @@ __global__ __launch_bounds__(NTHR, 1) void gka_chunk_kernel(Params p) {
 #pragma unroll
   for (int rt = 0; rt < 8; ++rt)
 #pragma unroll
-    for (int ct = 0; ct < 2; ++ct)
+    for (int ct = 0; ct < NCT; ++ct)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const int off = (16 * rt + 4 * q4 + v) * D + 32 * wave + 16 * ct + l16;
+        const int off = (16 * rt + 4 * q4 + v) * D + CW * wave + 16 * ct + l16;
         if (hd) hd[off] = Hs[rt][ct][v];
         if (sd) sd[off] = Ss[rt][ct][v];
       }
