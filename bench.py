@@ -307,6 +307,7 @@ def main():
                        "H": 64, "P": 64, "N": 128, "G": 8, "pool": "fp32 [256,64,64,128]"},
             "roofline": {"bound": "hbm", "achieved": round(r["GBps"], 1), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(r["GBps"] / HBM_PEAK_GBS, 4),
+                         "traffic": measured_traffic("ssd_decode"),
                          "algorithmic_bytes": r["bytes"]},
         }
     if not a.no_cpu:
