@@ -5,14 +5,18 @@
 // chain l2norm -> chunk cumsum -> KK^T -> (I+A)^-1 -> w,u -> h,v_new -> o), with
 // per-chunk maths (C tokens per chunk, G = in-chunk cumsum of g):
 //   A_ij = beta_i (k_i.k_j) e^{G_i-G_j} (j<i);  T = (I+A)^-1
-//   U = T diag(beta) V;   W = T diag(beta e^G) K
-//   V_new = U - W S;      O = scale [e^G (Q S) + tril(Q K^T e^{G_i-G_j}) V_new]
+//   V_new = T diag(beta) (V - diag(e^G) K S)
+//         (= U - W S with U = T diag(beta) V, W = T diag(beta e^G) K)
+//   O = scale [e^G (Q S) + tril(Q K^T e^{G_i-G_j}) V_new]
 //   S <- e^{G_last} S + K^T (e^{G_last-G} V_new)
+// Forming V_new from K S instead of W S needs no W: T is applied to the 32 x 32
+// right-hand side in registers, by blockwise substitution over its two 16-row
+// blocks (T_00, T_11 and -A_10; no merged T_10):
+//   V_new_0 = T_00 Y_0,  V_new_1 = T_11 (Y_1 - A_10 V_new_0),  Y = beta (V - e^G K S).
 //
 // The chunk length is an internal choice (the result is the same recurrence at
 // any chunk length, up to fp32 rounding): C = 32 keeps a workgroup's LDS under
-// 80 KB so two workgroups share a CU and overlap each other's latency-bound
-// phases (triangular solve, barriers) with MFMA work.
+// 80 KB so two workgroups share a CU.
 //
 // Parallel decomposition (segmented chunk scan).  Each sequence's chunks are
 // split into segments; one 256-thread workgroup owns one (segment, head) and
@@ -29,53 +33,48 @@
 //     (weak decay): per-segment zero-start end states S0_s and transitions
 //     Phi_s (chain started from I with V = 0), then S_{s+1} = Phi_s S_s + S0_s.
 //
-// Numerics: MFMA operands are bf16 with fp32 accumulation.  T (with beta and
-// beta e^G folded in, so K and V enter exactly) and the decayed V_new of the
-// state update are split into bf16 hi + lo pairs, giving ~fp32 accuracy where
-// the state is sensitive; W, Q, P and the state as a B operand are bf16.
+// Chunk pipeline: two barriers per chunk.  Phase 1 forms the chunk's T blocks
+// (waves 0-1) and P (waves 2-3) while every wave computes K S and Q S for its
+// state columns and stores the previous chunk's O; phase 2 forms V_new, O and
+// the state update, then stages the next chunk (prefetched one chunk ahead
+// into registers) into the other of two LDS buffers.
 //
-// Waves raise their priority through the MFMA-dense phases (W/U, V_new, O, state
-// update) so the two workgroups sharing a CU overlap one's VALU/LDS work with the
-// other's MFMAs (7% at C1).
+// Numerics: MFMA operands are bf16 with fp32 accumulation.  The state enters
+// K S as a bf16 hi + lo pair, and T, A_10 and the right-hand sides of the
+// substitution as hi/lo pairs (two MFMAs per product, see mm_hl), giving ~fp32
+// accuracy where the state is sensitive; Q, P and the state in Q S are bf16.
 //
 // Roofline: HBM-bound at the algorithmic minimum (q,k,v,o bf16 + g,beta +
 // final state); FLOPs 2*T*H*(5*C*d + 3*d^2).
+#include <type_traits>
+
 #include "common.hpp"
 #include "mfma.hpp"
 
 namespace hmx {
 namespace gdnp {
 
-constexpr int C = 32;          // chunk length (tokens); 32 keeps LDS at 2 workgroups/CU
+constexpr int C = 32;          // chunk length (tokens)
 constexpr int MT = C / 16;     // 16-row tiles per chunk
-constexpr int KT = C / 32;     // 32-token MFMA k-steps per chunk
 constexpr int D = 128;         // head dim (K == V == 128)
 constexpr int NTHR = 256;      // 4 waves
-constexpr int LDQ = D + 8;     // bf16 [C][128] row stride (q, k, v, W, O staging)
-constexpr int LDT = C + 8;     // bf16 [C][C] row stride (P, T hi/lo)
-constexpr int LDA = C + 8;     // fp32 [C][C] row stride (A, T)
-constexpr int LDWT = C + 8;    // bf16 [128][C] row stride (W^T hi/lo)
-static_assert(C == 32, "chunk length: the triangular solve is written for 32");
+constexpr int LDQ = D + 8;     // bf16 [C][128] row stride (q, k, v, O staging)
+constexpr int LDT = C + 8;     // bf16 [C][C] row stride (P, T/A hi/lo)
+static_assert(C == 32, "chunk length: the substitution and the g scan are written for 32");
 
 enum Mode { MODE_OUT = 0, MODE_S0 = 1, MODE_PHI = 2 };
 
-// shared-memory layout (bytes)
+// shared-memory layout (bytes): two staging buffers (K, Q, V, per-token
+// scalars), the O staging tile, T/A hi and lo, P
 constexpr int SZ_Q = C * LDQ * 2;
-constexpr int SZ_F32 = C * LDA * 4;
+constexpr int SZ_SC = 4 * C * 4;                 // G, beta, e^G, e^{G_last-G}
+constexpr int SZ_BUF = 3 * SZ_Q + SZ_SC;
 constexpr int SZ_P = C * LDT * 2;
-constexpr int OFF_Q = 0;
-constexpr int OFF_K = OFF_Q + SZ_Q;
-constexpr int OFF_V = OFF_K + SZ_Q;         // also the O staging buffer
-constexpr int OFF_A = OFF_V + SZ_Q;         // fp32 A
-constexpr int OFF_T = OFF_A + SZ_F32;       // fp32 T
-constexpr int OFF_TH = OFF_T + SZ_F32;      // bf16 T hi
-constexpr int OFF_TL = OFF_TH + SZ_P;       // bf16 T lo
-constexpr int SZ_WT = D * LDWT * 2;
-constexpr int OFF_W = OFF_TL + SZ_P;        // -W^T hi
-constexpr int OFF_WL = OFF_W + SZ_WT;       // -W^T lo
-constexpr int OFF_P = OFF_WL + SZ_WT;
-constexpr int OFF_G = OFF_P + SZ_P;         // fp32 G, beta, e^G, e^{Gl-G} [C]
-constexpr int SMEM = OFF_G + 4 * C * 4;
+constexpr int OFF_O = 2 * SZ_BUF;
+constexpr int OFF_TH = OFF_O + SZ_Q;   // rows 0-15: T_00 | rows 16-31: -A_10, T_11
+constexpr int OFF_TL = OFF_TH + SZ_P;
+constexpr int OFF_P = OFF_TL + SZ_P;
+constexpr int SMEM = OFF_P + SZ_P;
 static_assert(SMEM <= 80 * 1024, "LDS budget: two workgroups per CU");
 
 struct SegInfo {     // one row of the host-built segment table (int32 x 8)
@@ -122,8 +121,8 @@ __device__ __forceinline__ bool seq_exact(const int* plan, const SegInfo& si, in
   return false;
 }
 
-// One chunk's raw inputs for this thread: 4 rows x 8 features of k, v, q and
-// (wave 0) one token's g and beta.  Loaded one chunk ahead.
+// One chunk's raw inputs for this thread: 2 rows x 8 features of k, v, q and
+// (lanes 0-31 of wave 0) one token's g and beta.  Loaded one chunk ahead.
 struct RawChunk {
   bf16x8 k[MT], v[MT], q[MT];
   float g, b;
@@ -155,6 +154,25 @@ __device__ __forceinline__ void load_raw(RawChunk& r, const Params& p, const bf1
   }
 }
 
+// One staged chunk in LDS.
+struct Stage {
+  bf16* K; bf16* Q; bf16* V;
+  float* G; float* B; float* EG; float* EDL;   // G, beta, e^G, e^{G_last-G} per token
+};
+
+__device__ __forceinline__ Stage stage_at(unsigned char* smem, int bi) {
+  unsigned char* b = smem + bi * SZ_BUF;
+  Stage s;
+  s.K = reinterpret_cast<bf16*>(b);
+  s.Q = reinterpret_cast<bf16*>(b + SZ_Q);
+  s.V = reinterpret_cast<bf16*>(b + 2 * SZ_Q);
+  s.G = reinterpret_cast<float*>(b + 3 * SZ_Q);
+  s.B = s.G + C;
+  s.EG = s.B + C;
+  s.EDL = s.EG + C;
+  return s;
+}
+
 // Stage one 8-feature row slice: optionally L2-normalise across the 16 lanes
 // holding the row, round to bf16, write to LDS.
 __device__ __forceinline__ void stage_row(bf16* dst, const bf16x8& raw, bool norm) {
@@ -175,65 +193,110 @@ __device__ __forceinline__ void stage_row(bf16* dst, const bf16x8& raw, bool nor
   *reinterpret_cast<bf16x8*>(dst) = b;
 }
 
-// (I + A)^-1 of a strictly-lower 16x16 block held in C layout (A) together
-// with its transpose (At), by the exact identity for nilpotent A (A^16 = 0):
-//   (I + A)^-1 = (I - A)(I + A^2)(I + A^4)(I + A^8),
-// on fp32 MFMA.  A product X.Y takes X^T and Y in C layout: with k = 4q + s,
-// lane (q, l) supplies X[l][4q+s] = (X^T)_C[s] and Y[4q+s][l] = Y_C[s].
-__device__ __forceinline__ f32x4 mm_ct(const f32x4& Xt, const f32x4& Y, f32x4 acc) {
+// Write a prefetched chunk into staging buffer st: k (and q) rows L2-normalised,
+// v as is, and the per-token scalars from the in-chunk cumsum of g (wave 0).
+template <int MODE>
+__device__ __forceinline__ void stage_chunk(const Stage& st, const RawChunk& r, bool with_q,
+                                            bool norm, int tid, int wave, int lane) {
 #pragma unroll
-  for (int s = 0; s < 4; ++s) acc = mfma16f(Xt[s], Y[s], acc);
-  return acc;
+  for (int pass = 0; pass < MT; ++pass) {
+    const int row = pass * 16 + (tid >> 4);
+    const int f0 = (tid & 15) * 8;
+    stage_row(st.K + row * LDQ + f0, r.k[pass], norm);
+    if (MODE != MODE_PHI) *reinterpret_cast<bf16x8*>(st.V + row * LDQ + f0) = r.v[pass];
+    if (MODE == MODE_OUT && with_q) stage_row(st.Q + row * LDQ + f0, r.q[pass], norm);
+  }
+  if (wave == 0) {
+    const float gv = scan32(lane < C ? r.g : 0.f);
+    const float glast = __builtin_bit_cast(
+        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gv), C - 1));
+    if (lane < C) {
+      st.G[lane] = gv;
+      st.B[lane] = r.b;
+      st.EG[lane] = fast_exp(gv);
+      st.EDL[lane] = fast_exp(glast - gv);
+    }
+  }
 }
 
-__device__ __forceinline__ f32x4 inv_unit_lower16(const f32x4& A, const f32x4& At, int q4, int l16) {
-  const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-  const f32x4 A2 = mm_ct(At, A, z), A2t = mm_ct(A, At, z);
-  const f32x4 A4 = mm_ct(A2t, A2, z), A4t = mm_ct(A2, A2t, z);
-  const f32x4 A8 = mm_ct(A4t, A4, z);
-  f32x4 P1, P1t;
+// ---------------------------------------------------------------------------
+// 16x16 products on bf16 hi + lo pairs (x ~= hi + lo, ~16 significant bits)
+// ---------------------------------------------------------------------------
+struct HL {
+  bf16x4 h, l;
+};
+
+__device__ __forceinline__ HL split_hl(const f32x4& x) {
+  HL r;
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
-    const float d = (4 * q4 + v == l16) ? 1.f : 0.f;
-    P1[v] = d - A[v];
-    P1t[v] = d - At[v];
+    r.h[v] = (bf16)x[v];
+    r.l[v] = (bf16)(x[v] - (float)r.h[v]);
   }
-  const f32x4 P2 = mm_ct(P1t, A2, P1), P2t = mm_ct(A2, P1t, P1t);
-  const f32x4 P3 = mm_ct(P2t, A4, P2), P3t = mm_ct(A4, P2t, P2t);
-  return mm_ct(P3t, A8, P3);
+  return r;
 }
 
-// ---------------------------------------------------------------------------
-// T = (I + A)^-1 for the strictly-lower 64x64 A in sA (fp32), into sT (fp32).
-// 16x16 diagonal blocks by forward substitution (one wave each, register
-// resident), then the block merges with fp32 MFMA:
-//   T_10 = -T_11 A_10 T_00,  T_32 = -T_33 A_32 T_22            (16x16)
-//   T[32:,:32] = -T_HH A_HL T_LL                                (32x32)
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ void put_t(float* sT, bf16* sTh, bf16* sTl, int r, int c, float x) {
-  sT[r * LDA + c] = x;
+// acc + X.Y from X^T and Y in C layout: lane (q, l16) holds X[l16][4q..4q+3]
+// (= its X^T values) and Y[4q..4q+3][l16], so the A operand {Xh, Xl} and the B
+// operands {Yh, Yh}, {Yl, Yl} agree on k; two MFMAs give (Xh + Xl)(Yh + Yl).
+__device__ __forceinline__ f32x4 mm_ct(const HL& xt, const HL& y, f32x4 acc) {
+  const bf16x8 a = {xt.h[0], xt.h[1], xt.h[2], xt.h[3], xt.l[0], xt.l[1], xt.l[2], xt.l[3]};
+  acc = mfma16(a, bf16x8{y.h[0], y.h[1], y.h[2], y.h[3], y.h[0], y.h[1], y.h[2], y.h[3]}, acc);
+  return mfma16(a, bf16x8{y.l[0], y.l[1], y.l[2], y.l[3], y.l[0], y.l[1], y.l[2], y.l[3]}, acc);
+}
+
+// (I + A)^-1 of a strictly-lower 16x16 block held in C layout (A) together
+// with its transpose (At), by the exact identity for nilpotent A (A^16 = 0):
+//   (I + A)^-1 = (I + A^8)(I + A^4)(I + A^2)(I - A)
+// (the factors commute).  Left operands enter transposed, so the chain forms
+// A^2, A^4 and their transposes, then (A^8)^T = (A^4)^T (A^4)^T.
+__device__ __forceinline__ f32x4 inv_unit_lower16(const f32x4& A, const f32x4& At, int q4, int l16) {
+  const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+  const HL a = split_hl(A), at = split_hl(At);
+  const f32x4 A2 = mm_ct(at, a, z), A2t = mm_ct(a, at, z);
+  const HL a2 = split_hl(A2), a2t = split_hl(A2t);
+  const f32x4 A4 = mm_ct(a2t, a2, z), A4t = mm_ct(a2, a2t, z);
+  const HL a4 = split_hl(A4), a4t = split_hl(A4t);
+  const HL a8t = split_hl(mm_ct(a4, a4t, z));
+  f32x4 R;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) R[v] = ((4 * q4 + v == l16) ? 1.f : 0.f) - A[v];
+  R = mm_ct(a2t, split_hl(R), R);
+  R = mm_ct(a4t, split_hl(R), R);
+  return mm_ct(a8t, split_hl(R), R);
+}
+
+// 16x16 blocks kept in LDS as hi/lo pairs
+__device__ __forceinline__ void put_hl(bf16* hi, bf16* lo, int r, int c, float x) {
   const bf16 h = (bf16)x;
-  sTh[r * LDT + c] = h;
-  sTl[r * LDT + c] = (bf16)(x - (float)h);
+  hi[r * LDT + c] = h;
+  lo[r * LDT + c] = (bf16)(x - (float)h);
 }
 
-__device__ __forceinline__ void tri_merge(const float* sA, float* sT, bf16* sTh, bf16* sTl,
-                                         int wave, int lane) {
-  static_assert(C == 32, "one 16x16 merge");
-  const int q4 = lane >> 4, l16 = lane & 15;
-  if (wave == 0) {
-    // T_10 = -T_11 A_10 T_00: X = A_10 T_00 (natural k), then Y = T_11 X (k = 4q + s)
-    f32x4 X = {0.f, 0.f, 0.f, 0.f};
+// A operand of the 16x16 block at (r0, c0) of a hi/lo pair: lane (q, l16) holds
+// row r0+l16, columns c0+4q..c0+4q+3 of hi, then the same of lo.  Paired with a
+// B operand {y[0..3], y[0..3]} built from a C-layout tile (rows 4q..4q+3), one
+// 16x16x32 MFMA forms hi.Y + lo.Y.
+__device__ __forceinline__ bf16x8 ld_hl(const bf16* hi, const bf16* lo, int r0, int c0, int lane) {
+  const int off = (r0 + (lane & 15)) * LDT + c0 + 4 * (lane >> 4);
+  const bf16x4 a = *reinterpret_cast<const bf16x4*>(hi + off);
+  const bf16x4 b = *reinterpret_cast<const bf16x4*>(lo + off);
+  return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// acc + X.Y for a hi/lo block X (from ld_hl) and a C-layout fp32 tile Y split
+// into hi/lo: two MFMAs, (Xh + Xl)(Yh + Yl).
+__device__ __forceinline__ f32x4 mm_hl(const bf16x8& xa, const f32x4& y, f32x4 acc) {
+  bf16x8 bh, bl;
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
-      X = mfma16f(sA[(16 + l16) * LDA + 4 * s + q4], sT[(4 * s + q4) * LDA + l16], X);
-    f32x4 Y = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < 4; ++s) Y = mfma16f(sT[(16 + l16) * LDA + 16 + 4 * q4 + s], X[s], Y);
-#pragma unroll
-    for (int v = 0; v < 4; ++v) put_t(sT, sTh, sTl, 16 + 4 * q4 + v, l16, -Y[v]);
+  for (int v = 0; v < 4; ++v) {
+    const bf16 h = (bf16)y[v];
+    const bf16 l = (bf16)(y[v] - (float)h);
+    bh[v] = h; bh[4 + v] = h;
+    bl[v] = l; bl[4 + v] = l;
   }
-  lds_barrier();
+  acc = mfma16(xa, bh, acc);
+  return mfma16(xa, bl, acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -242,28 +305,12 @@ __device__ __forceinline__ void tri_merge(const float* sA, float* sT, bf16* sTh,
 template <int MODE>
 __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
   __shared__ __align__(16) unsigned char smem[SMEM];
-  bf16* sQ = reinterpret_cast<bf16*>(smem + OFF_Q);
-  bf16* sK = reinterpret_cast<bf16*>(smem + OFF_K);
-  bf16* sV = reinterpret_cast<bf16*>(smem + OFF_V);
-  bf16* sO = sV;  // O staging reuses V after U is formed
-  float* sA = reinterpret_cast<float*>(smem + OFF_A);
-  float* sT = reinterpret_cast<float*>(smem + OFF_T);
+  bf16* sO = reinterpret_cast<bf16*>(smem + OFF_O);
   bf16* sTh = reinterpret_cast<bf16*>(smem + OFF_TH);
   bf16* sTl = reinterpret_cast<bf16*>(smem + OFF_TL);
-  bf16* sW = reinterpret_cast<bf16*>(smem + OFF_W);
-  bf16* sWl = reinterpret_cast<bf16*>(smem + OFF_WL);
   bf16* sP = reinterpret_cast<bf16*>(smem + OFF_P);
-  float* sG = reinterpret_cast<float*>(smem + OFF_G);
-  float* sB = sG + C;
-  float* sEG = sB + C;    // e^{G}
-  float* sEDL = sEG + C;  // e^{G_last - G}
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  // T hi/lo upper-triangular 16x16 blocks are never written: zero them once
-  for (int i = tid; i < C * C; i += NTHR) {
-    const int r = i / C, c = i % C;
-    if ((c >> 4) > (r >> 4)) { sTh[r * LDT + c] = (bf16)0.f; sTl[r * LDT + c] = (bf16)0.f; }
-  }
   const int q4 = lane >> 4, l16 = lane & 15;
   const int s_id = blockIdx.x, h = blockIdx.y;
   const SegInfo si = load_seg(p.seg, s_id);
@@ -316,312 +363,269 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
         }
   }
 
-  // P's strictly-upper 16x16 tiles are never written by phase 1: zero them once.
+  // P's strictly-upper 16x16 tile is never written by phase 1: zero it once.
   if (MODE == MODE_OUT) {
-    for (int i = tid; i < C * C; i += NTHR) {
-      const int r = i / C, c = i % C;
-      if ((c >> 4) > (r >> 4)) sP[r * LDT + c] = (bf16)0.f;
-    }
+    for (int i = tid; i < 16 * 16; i += NTHR) sP[(i >> 4) * LDT + 16 + (i & 15)] = (bf16)0.f;
   }
 
   const int64_t q_rs = (int64_t)H * D, kv_rs = (int64_t)p.HKV * D;
   const bf16* qh = p.q + (int64_t)h * D;
   const bf16* kh = p.k + (int64_t)hk * D;
   const bf16* vh = p.v + (int64_t)hk * D;
+  bf16* oh = p.o + (int64_t)h * D;
 
-  RawChunk raw;
-  if (c_begin < si.c_end)
-    load_raw<MODE>(raw, p, qh, kh, vh, q_rs, kv_rs, si.bos + c_begin * C,
-                   min(C, si.eos - (si.bos + c_begin * C)), c_begin >= c_out, tid, h);
-
-  for (int c = c_begin; c < si.c_end; ++c) {
-    const int tok0 = si.bos + c * C;
-    const int nval = min(C, si.eos - tok0);
-    const bool out_chunk = (MODE == MODE_OUT) && (c >= c_out);
-
-    // ---- phase 0: stage the prefetched chunk in LDS (L2-normalise q,k rows),
-    //      g cumsum; then prefetch the next chunk into registers --------------
-    {
+  // Coalesced 16-byte store of the O tile staged in sO (chunk starting at tok0).
+  auto store_o = [&](int tok0, int nval) {
 #pragma unroll
-      for (int pass = 0; pass < MT; ++pass) {
-        const int row = pass * 16 + (tid >> 4);
-        const int f0 = (tid & 15) * 8;
-        stage_row(sK + row * LDQ + f0, raw.k[pass], p.l2norm);
-        if (MODE != MODE_PHI) *reinterpret_cast<bf16x8*>(sV + row * LDQ + f0) = raw.v[pass];
-        if (out_chunk) stage_row(sQ + row * LDQ + f0, raw.q[pass], p.l2norm);
-      }
-      if (wave == 0) {
-        static_assert(C == 32, "the DPP scan covers 32 lanes");
-        const float gv = scan32(lane < C ? raw.g : 0.f);
-        const float glast = __builtin_bit_cast(
-            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gv), C - 1));
-        if (lane < C) {
-          sG[lane] = gv;
-          sB[lane] = raw.b;
-          sEG[lane] = fast_exp(gv);
-          sEDL[lane] = fast_exp(glast - gv);
-        }
-      }
-      if (c + 1 < si.c_end) {
-        const int t1 = tok0 + C;
-        load_raw<MODE>(raw, p, qh, kh, vh, q_rs, kv_rs, t1, min(C, si.eos - t1), c + 1 >= c_out,
-                       tid, h);
+    for (int pass = 0; pass < MT; ++pass) {
+      const int row = pass * 16 + (tid >> 4);
+      const int f0 = (tid & 15) * 8;
+      if (row < nval)
+        *reinterpret_cast<bf16x8*>(oh + (int64_t)(tok0 + row) * q_rs + f0) =
+            *reinterpret_cast<const bf16x8*>(sO + row * LDQ + f0);
+    }
+  };
+
+  if (c_begin >= si.c_end) {
+    // nothing to scan (empty segment): only the end state below
+  } else {
+    RawChunk raw;
+    {
+      const int t0 = si.bos + c_begin * C;
+      load_raw<MODE>(raw, p, qh, kh, vh, q_rs, kv_rs, t0, min(C, si.eos - t0), c_begin >= c_out,
+                     tid, h);
+      stage_chunk<MODE>(stage_at(smem, 0), raw, c_begin >= c_out, p.l2norm, tid, wave, lane);
+      if (c_begin + 1 < si.c_end) {
+        const int t1 = t0 + C;
+        load_raw<MODE>(raw, p, qh, kh, vh, q_rs, kv_rs, t1, min(C, si.eos - t1),
+                       c_begin + 1 >= c_out, tid, h);
       }
     }
     lds_barrier();
 
-    // ---- phase 1: A = beta_i (k_i.k_j) e^{G_i-G_j} (j<i), P = q_i.k_j e^{G_i-G_j} (j<=i)
-    //      wave w < MT owns A's 16-row strip w; wave MT + w owns P's strip w
-    if (wave < MT || (out_chunk && wave < 2 * MT)) {
-      const bool isP = wave >= MT;
-      const int i = isP ? wave - MT : wave;
-      const bf16* Am = isP ? sQ : sK;
-      bf16x8 af[4];
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) af[ks] = frag(Am, LDQ, 16 * i, 32 * ks, lane);
-      float gr[4], br[4];
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        gr[v] = sG[16 * i + 4 * q4 + v];
-        br[v] = sB[16 * i + 4 * q4 + v];
-      }
-#pragma unroll
-      for (int j = 0; j < MT; ++j) {
-        if (j > i) break;
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) acc = mfma16(af[ks], frag(sK, LDQ, 16 * j, 32 * ks, lane), acc);
-        const int col = 16 * j + l16;
-        const float gc = sG[col];
-        if (isP) {
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const int row = 16 * i + 4 * q4 + v;
-            const float dcy = (row >= col) ? fast_exp(gr[v] - gc) : 0.f;
-            sP[row * LDT + col] = (bf16)(acc[v] * dcy);
-          }
-        } else if (j < i) {
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const int row = 16 * i + 4 * q4 + v;
-            sA[row * LDA + col] = br[v] * acc[v] * fast_exp(gr[v] - gc);
-          }
-        } else {
-          // diagonal tile: A and A^T in C layout (k.k^T is symmetric), then T_ii
-          const float bc = sB[col];
-          f32x4 At_, Ad;
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const int row = 16 * i + 4 * q4 + v;
-            Ad[v] = row > col ? br[v] * acc[v] * fast_exp(gr[v] - gc) : 0.f;
-            At_[v] = col > row ? bc * acc[v] * fast_exp(gc - gr[v]) : 0.f;
-          }
-          const f32x4 Tii = inv_unit_lower16(Ad, At_, q4, l16);
-#pragma unroll
-          for (int v = 0; v < 4; ++v) put_t(sT, sTh, sTl, 16 * i + 4 * q4 + v, col, Tii[v]);
-        }
-      }
-    }
-    lds_barrier();
+    for (int c = c_begin; c < si.c_end; ++c) {
+      const int bi = (c - c_begin) & 1;
+      const Stage cur = stage_at(smem, bi);
+      const int tok0 = si.bos + c * C;
+      const bool out_chunk = (MODE == MODE_OUT) && (c >= c_out);
 
-    // ---- phase 2: off-diagonal block of T = (I + A)^-1 (fp32, + bf16 hi/lo) ------
-    tri_merge(sA, sT, sTh, sTl, wave, lane);
+      // ---- phase 1: T blocks / P; K S and Q S; store the previous chunk's O ----
+      if (MODE == MODE_OUT && c > c_out) store_o(tok0 - C, C);
 
-    __builtin_amdgcn_s_setprio(1);
-    // ---- phase 3: W = T diag(beta e^G) K (to LDS, negated hi/lo), U = T diag(beta) V
-    //      (registers).  The token scales are applied to the B fragments in fp32,
-    //      split into hi/lo, and multiplied by T hi/lo (3 products each).
-    f32x4 Vn[MT][2];  // U, then V_new: rows 16mt.., cols 32w+16ct..
-    {
-      float sk[KT][8], sv[KT][8];
+      f32x4 X[MT][2], QS[MT][2];
+      auto phase1 = [&](auto role_c, auto outq_c) {
+        constexpr int R = decltype(role_c)::value;
+        constexpr bool OQ = decltype(outq_c)::value;
+        if constexpr (R < MT) {
+          // A strip R: off-diagonal tile -> -A_10 (hi/lo), diagonal tile -> T_RR (hi/lo)
+          bf16x8 af[4];
 #pragma unroll
-      for (int ks = 0; ks < KT; ++ks)
+          for (int ks = 0; ks < 4; ++ks) af[ks] = frag(cur.K, LDQ, 16 * R, 32 * ks, lane);
+          float gr[4], br[4];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int t = 32 * ks + 8 * q4 + j;
-          sv[ks][j] = sB[t];
-          sk[ks][j] = sv[ks][j] * sEG[t];
-        }
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        bf16x8 bkh[KT], bkl[KT], bvh[KT], bvl[KT];
-#pragma unroll
-        for (int ks = 0; ks < KT; ++ks) {
-          const bf16x8 kr = frag_t(sK, LDQ, 32 * ks, 32 * wave + 16 * ct, lane);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const float x = (float)kr[j] * sk[ks][j];
-            const bf16 hx = (bf16)x;
-            bkh[ks][j] = hx;
-            bkl[ks][j] = (bf16)(x - (float)hx);
+          for (int v = 0; v < 4; ++v) {
+            gr[v] = cur.G[16 * R + 4 * q4 + v];
+            br[v] = cur.B[16 * R + 4 * q4 + v];
           }
-          if (MODE != MODE_PHI) {
-            const bf16x8 vr = frag_t(sV, LDQ, 32 * ks, 32 * wave + 16 * ct, lane);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-              const float x = (float)vr[j] * sv[ks][j];
-              const bf16 hx = (bf16)x;
-              bvh[ks][j] = hx;
-              bvl[ks][j] = (bf16)(x - (float)hx);
+          for (int j = 0; j <= R; ++j) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+              acc = mfma16(af[ks], frag(cur.K, LDQ, 16 * j, 32 * ks, lane), acc);
+            const int col = 16 * j + l16;
+            const float gc = cur.G[col];
+            if (j < R) {
+#pragma unroll
+              for (int v = 0; v < 4; ++v)
+                put_hl(sTh, sTl, 16 * R + 4 * q4 + v, col,
+                       -br[v] * acc[v] * fast_exp(gr[v] - gc));
+            } else {
+              // A and A^T of the diagonal tile in C layout (k.k^T is symmetric)
+              const float bc = cur.B[col];
+              f32x4 At_, Ad;
+#pragma unroll
+              for (int v = 0; v < 4; ++v) {
+                const int row = 16 * R + 4 * q4 + v;
+                Ad[v] = row > col ? br[v] * acc[v] * fast_exp(gr[v] - gc) : 0.f;
+                At_[v] = col > row ? bc * acc[v] * fast_exp(gc - gr[v]) : 0.f;
+              }
+              const f32x4 Tii = inv_unit_lower16(Ad, At_, q4, l16);
+#pragma unroll
+              for (int v = 0; v < 4; ++v) put_hl(sTh, sTl, 16 * R + 4 * q4 + v, col, Tii[v]);
             }
           }
-        }
+        } else if constexpr (OQ) {
+          // P strip i = R - MT: q_r.k_c e^{G_r-G_c} for c <= r
+          constexpr int i = R - MT;
+          bf16x8 af[4];
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          f32x4 w = {0.f, 0.f, 0.f, 0.f}, u = {0.f, 0.f, 0.f, 0.f};
+          for (int ks = 0; ks < 4; ++ks) af[ks] = frag(cur.Q, LDQ, 16 * i, 32 * ks, lane);
+          float gr[4];
 #pragma unroll
-          for (int ks = 0; ks < KT; ++ks) {
-            if (32 * ks > 16 * mt + 15) continue;  // T is lower triangular
-            const bf16x8 th = frag(sTh, LDT, 16 * mt, 32 * ks, lane);
-            const bf16x8 tl = frag(sTl, LDT, 16 * mt, 32 * ks, lane);
-            w = mfma16(th, bkh[ks], w);
-            w = mfma16(th, bkl[ks], w);
-            w = mfma16(tl, bkh[ks], w);
-            if (MODE != MODE_PHI) {
-              u = mfma16(th, bvh[ks], u);
-              u = mfma16(th, bvl[ks], u);
-              u = mfma16(tl, bvh[ks], u);
-            }
-          }
-          {
-            // -W^T[feature][token]: this lane's 4 tokens are consecutive
-            bf16x4 wh, wl;
+          for (int v = 0; v < 4; ++v) gr[v] = cur.G[16 * i + 4 * q4 + v];
+#pragma unroll
+          for (int j = 0; j <= i; ++j) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+              acc = mfma16(af[ks], frag(cur.K, LDQ, 16 * j, 32 * ks, lane), acc);
+            const int col = 16 * j + l16;
+            const float gc = cur.G[col];
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-              wh[v] = (bf16)(-w[v]);
-              wl[v] = (bf16)(-w[v] - (float)wh[v]);
+              const int row = 16 * i + 4 * q4 + v;
+              const float dcy = (row >= col) ? fast_exp(gr[v] - gc) : 0.f;
+              sP[row * LDT + col] = (bf16)(acc[v] * dcy);
             }
-            const int a = (32 * wave + 16 * ct + l16) * LDWT + 16 * mt + 4 * q4;
-            *reinterpret_cast<bf16x4*>(sW + a) = wh;
-            *reinterpret_cast<bf16x4*>(sWl + a) = wl;
           }
-          Vn[mt][ct] = u;
         }
-      }
-    }
-    lds_barrier();
-
-    __builtin_amdgcn_s_setprio(2);
-    // ---- phase 4: V_new = U - W S, with W and S as bf16 hi+lo pairs ------------
+        // K S (state as hi + lo) and Q S (state as bf16) for this wave's columns
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      bf16x8 Sh[2], Sl[2];
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) pack_b_hilo(S[2 * ks][ct], S[2 * ks + 1][ct], Sh[ct], Sl[ct]);
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const bf16x8 a = frag_t_perm(sW, LDWT, 32 * ks, 16 * mt, lane);
-        const bf16x8 al = frag_t_perm(sWl, LDWT, 32 * ks, 16 * mt, lane);
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
-          Vn[mt][ct] = mfma16(a, Sh[ct], Vn[mt][ct]);
-          Vn[mt][ct] = mfma16(a, Sl[ct], Vn[mt][ct]);
-          Vn[mt][ct] = mfma16(al, Sh[ct], Vn[mt][ct]);
-        }
-      }
-    }
-
-    // ---- phase 5: O = scale [e^G (Q S) + P V_new] ------------------------------
-    if (out_chunk) {
-      f32x4 O[MT][2];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) O[mt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        bf16x8 Sh[2];
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) Sh[ct] = pack_b(S[2 * ks][ct], S[2 * ks + 1][ct]);
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const bf16x8 a = frag_perm(sQ, LDQ, 16 * mt, 32 * ks, lane);
-#pragma unroll
-          for (int ct = 0; ct < 2; ++ct) O[mt][ct] = mfma16(a, Sh[ct], O[mt][ct]);
-        }
-      }
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const float e = sEG[16 * mt + 4 * q4 + v];
-          O[mt][0][v] *= e;
-          O[mt][1][v] *= e;
-        }
-      bf16x8 Vb[KT][2];
-#pragma unroll
-      for (int ks = 0; ks < KT; ++ks)
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) Vb[ks][ct] = pack_b(Vn[2 * ks][ct], Vn[2 * ks + 1][ct]);
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int ks = 0; ks < KT; ++ks) {
-          if (32 * ks > 16 * mt + 15) continue;  // P is lower triangular
-          const bf16x8 a = frag_perm(sP, LDT, 16 * mt, 32 * ks, lane);
-#pragma unroll
-          for (int ct = 0; ct < 2; ++ct) O[mt][ct] = mfma16(a, Vb[ks][ct], O[mt][ct]);
-        }
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-          for (int v = 0; v < 4; ++v)
-            sO[(16 * mt + 4 * q4 + v) * LDQ + 32 * wave + 16 * ct + l16] =
-                (bf16)(O[mt][ct][v] * p.scale);
-    }
-
-    // ---- phase 6: S <- e^{G_last} S + K^T (e^{G_last-G} V_new), hi/lo ---------
-    {
-      const float egl = sEG[C - 1];
-#pragma unroll
-      for (int rt = 0; rt < 8; ++rt)
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) S[rt][ct][v] *= egl;
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const float e = sEDL[16 * mt + 4 * q4 + v];
-          Vn[mt][0][v] *= e;
-          Vn[mt][1][v] *= e;
-        }
-      bf16x8 Vh[KT][2], Vl[KT][2];
-#pragma unroll
-      for (int ks = 0; ks < KT; ++ks)
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct)
-          pack_b_hilo(Vn[2 * ks][ct], Vn[2 * ks + 1][ct], Vh[ks][ct], Vl[ks][ct]);
-#pragma unroll
-      for (int rt = 0; rt < 8; ++rt)
-#pragma unroll
-        for (int ks = 0; ks < KT; ++ks) {
-          const bf16x8 a = frag_t_perm(sK, LDQ, 32 * ks, 16 * rt, lane);
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
           for (int ct = 0; ct < 2; ++ct) {
-            S[rt][ct] = mfma16(a, Vh[ks][ct], S[rt][ct]);
-            S[rt][ct] = mfma16(a, Vl[ks][ct], S[rt][ct]);
+            X[mt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+            QS[mt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+          }
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          bf16x8 Sh[2], Sl[2];
+#pragma unroll
+          for (int ct = 0; ct < 2; ++ct) pack_b_hilo(S[2 * ks][ct], S[2 * ks + 1][ct], Sh[ct], Sl[ct]);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const bf16x8 a = frag_perm(cur.K, LDQ, 16 * mt, 32 * ks, lane);
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) {
+              X[mt][ct] = mfma16(a, Sh[ct], X[mt][ct]);
+              X[mt][ct] = mfma16(a, Sl[ct], X[mt][ct]);
+            }
+            if constexpr (OQ) {
+              const bf16x8 aq = frag_perm(cur.Q, LDQ, 16 * mt, 32 * ks, lane);
+#pragma unroll
+              for (int ct = 0; ct < 2; ++ct) QS[mt][ct] = mfma16(aq, Sh[ct], QS[mt][ct]);
+            }
           }
         }
-    }
-    __builtin_amdgcn_s_setprio(0);
-    lds_barrier();
-
-    // ---- store O (coalesced 16-byte rows) --------------------------------------
-    if (out_chunk) {
-      bf16* oh = p.o + (int64_t)h * D;
-#pragma unroll
-      for (int pass = 0; pass < MT; ++pass) {
-        const int row = pass * 16 + (tid >> 4);
-        const int f0 = (tid & 15) * 8;
-        if (row < nval)
-          *reinterpret_cast<bf16x8*>(oh + (int64_t)(tok0 + row) * q_rs + f0) =
-              *reinterpret_cast<const bf16x8*>(sO + row * LDQ + f0);
+      };
+      using I0 = std::integral_constant<int, 0>;
+      using I1 = std::integral_constant<int, 1>;
+      using I2 = std::integral_constant<int, 2>;
+      using I3 = std::integral_constant<int, 3>;
+      using BT = std::true_type;
+      using BF = std::false_type;
+      if (MODE == MODE_OUT && out_chunk) {
+        if (wave == 0) phase1(I0{}, BT{});
+        else if (wave == 1) phase1(I1{}, BT{});
+        else if (wave == 2) phase1(I2{}, BT{});
+        else phase1(I3{}, BT{});
+      } else {
+        if (wave == 0) phase1(I0{}, BF{});
+        else if (wave == 1) phase1(I1{}, BF{});
+        else phase1(I2{}, BF{});
       }
       lds_barrier();
+
+      __builtin_amdgcn_s_setprio(1);
+      // ---- phase 2: Y = beta (V - e^G K S); V_new by blockwise substitution --------
+      f32x4 Vn[MT][2];
+      {
+        f32x4 Y[MT][2];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int ct = 0; ct < 2; ++ct) {
+            bf16x4 vt = {};
+            if (MODE != MODE_PHI) vt = ld_tr(cur.V, LDQ, 16 * mt + 4 * q4, 32 * wave + 16 * ct, lane);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              const int r = 16 * mt + 4 * q4 + v;
+              Y[mt][ct][v] = cur.B[r] * ((float)vt[v] - cur.EG[r] * X[mt][ct][v]);
+            }
+          }
+        const bf16x8 t00 = ld_hl(sTh, sTl, 0, 0, lane);
+        const bf16x8 na10 = ld_hl(sTh, sTl, 16, 0, lane);
+        const bf16x8 t11 = ld_hl(sTh, sTl, 16, 16, lane);
+        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+          Vn[0][ct] = mm_hl(t00, Y[0][ct], z);
+          const f32x4 r1 = mm_hl(na10, Vn[0][ct], Y[1][ct]);
+          Vn[1][ct] = mm_hl(t11, r1, z);
+        }
+      }
+
+      // ---- O = scale [e^G (Q S) + P V_new] -> sO ----------------------------------
+      if (out_chunk) {
+        bf16x8 Vb[2];
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) Vb[ct] = pack_b(Vn[0][ct], Vn[1][ct]);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          f32x4 O[2];
+#pragma unroll
+          for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) O[ct][v] = QS[mt][ct][v] * cur.EG[16 * mt + 4 * q4 + v];
+          const bf16x8 a = frag_perm(sP, LDT, 16 * mt, 0, lane);
+#pragma unroll
+          for (int ct = 0; ct < 2; ++ct) {
+            O[ct] = mfma16(a, Vb[ct], O[ct]);
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+              sO[(16 * mt + 4 * q4 + v) * LDQ + 32 * wave + 16 * ct + l16] =
+                  (bf16)(O[ct][v] * p.scale);
+          }
+        }
+      }
+
+      // ---- S <- e^{G_last} S + K^T (e^{G_last-G} V_new), V_new as hi/lo ----------
+      {
+        const float egl = cur.EG[C - 1];
+#pragma unroll
+        for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+          for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) S[rt][ct][v] *= egl;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const float e = cur.EDL[16 * mt + 4 * q4 + v];
+            Vn[mt][0][v] *= e;
+            Vn[mt][1][v] *= e;
+          }
+        bf16x8 Vh[2], Vl[2];
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) pack_b_hilo(Vn[0][ct], Vn[1][ct], Vh[ct], Vl[ct]);
+#pragma unroll
+        for (int rt = 0; rt < 8; ++rt) {
+          const bf16x8 a = frag_t_perm(cur.K, LDQ, 0, 16 * rt, lane);
+#pragma unroll
+          for (int ct = 0; ct < 2; ++ct) {
+            S[rt][ct] = mfma16(a, Vh[ct], S[rt][ct]);
+            S[rt][ct] = mfma16(a, Vl[ct], S[rt][ct]);
+          }
+        }
+      }
+      __builtin_amdgcn_s_setprio(0);
+
+      // ---- stage the next chunk into the other buffer; prefetch the one after -------
+      if (c + 1 < si.c_end) {
+        stage_chunk<MODE>(stage_at(smem, bi ^ 1), raw, c + 1 >= c_out, p.l2norm, tid, wave, lane);
+        if (c + 2 < si.c_end) {
+          const int t2 = tok0 + 2 * C;
+          load_raw<MODE>(raw, p, qh, kh, vh, q_rs, kv_rs, t2, min(C, si.eos - t2),
+                         c + 2 >= c_out, tid, h);
+        }
+      }
+      lds_barrier();
+    }
+    if (MODE == MODE_OUT && si.c_end > c_out) {
+      const int tl = si.bos + (si.c_end - 1) * C;
+      store_o(tl, min(C, si.eos - tl));
     }
   }
 
