@@ -35,14 +35,18 @@
 //
 // Chunk pipeline: two barriers per chunk.  Phase 1 forms the chunk's T blocks
 // (waves 0-1) and P (waves 2-3) while every wave computes K S and Q S for its
-// state columns and stores the previous chunk's O; phase 2 forms V_new, O and
-// the state update, then stages the next chunk (prefetched one chunk ahead
-// into registers) into the other of two LDS buffers.
+// state columns, stores the previous chunk's O, and prepares the next chunk
+// (prefetched one chunk ahead into registers): its row norms and g cumsum.
+// Phase 2 forms V_new, O and the state update, then stages the next chunk into
+// the other of two LDS buffers.
 //
-// Numerics: MFMA operands are bf16 with fp32 accumulation.  The state enters
-// K S as a bf16 hi + lo pair, and T, A_10 and the right-hand sides of the
-// substitution as hi/lo pairs (two MFMAs per product, see mm_hl), giving ~fp32
-// accuracy where the state is sensitive; Q, P and the state in Q S are bf16.
+// Numerics: MFMA operands are bf16 with fp32 accumulation.  k and q enter the
+// products raw (exact bf16 inputs); the L2 normalisation is applied as fp32 row
+// and column factors (A, P) and row factors (K S, Q S, the state update).  The
+// state enters K S as a bf16 hi + lo pair, and T, A_10 and the right-hand sides
+// of the substitution as hi/lo pairs (two MFMAs per product, see mm_hl), giving
+// ~fp32 accuracy where the state is sensitive; P, V_new in P V_new and the
+// state in Q S are bf16.
 //
 // Roofline: HBM-bound at the algorithmic minimum (q,k,v,o bf16 + g,beta +
 // final state); FLOPs 2*T*H*(5*C*d + 3*d^2).
@@ -67,7 +71,7 @@ enum Mode { MODE_OUT = 0, MODE_S0 = 1, MODE_PHI = 2 };
 // shared-memory layout (bytes): two staging buffers (K, Q, V, per-token
 // scalars), the O staging tile, T/A hi and lo, P
 constexpr int SZ_Q = C * LDQ * 2;
-constexpr int SZ_SC = 4 * C * 4;                 // G, beta, e^G, e^{G_last-G}
+constexpr int SZ_SC = 9 * C * 4;                 // per-token scalars (see Stage)
 constexpr int SZ_BUF = 3 * SZ_Q + SZ_SC;
 constexpr int SZ_P = C * LDT * 2;
 constexpr int OFF_O = 2 * SZ_BUF;
@@ -122,10 +126,14 @@ __device__ __forceinline__ bool seq_exact(const int* plan, const SegInfo& si, in
 }
 
 // One chunk's raw inputs for this thread: 2 rows x 8 features of k, v, q and
-// (lanes 0-31 of wave 0) one token's g and beta.  Loaded one chunk ahead.
+// (lanes 0-31 of wave 0) one token's g and beta, loaded one chunk ahead; then
+// the row factors of those rows and (wave 0) the token's g cumsum, e^G and
+// e^{G_last-G}, formed while the current chunk's MFMA work runs (prep_*).
 struct RawChunk {
   bf16x8 k[MT], v[MT], q[MT];
   float g, b;
+  float rk[MT], rq[MT];
+  float gs, eg, edl;
 };
 
 template <int MODE>
@@ -151,13 +159,20 @@ __device__ __forceinline__ void load_raw(RawChunk& r, const Params& p, const bf1
     const int64_t gi = (int64_t)(tok0 + tid) * p.H + h;
     r.g = ok ? ld_scalar(p.g, gi, p.g_dt) : 0.f;
     r.b = ok ? ld_scalar(p.beta, gi, p.beta_dt) : 0.f;
+  } else {
+    r.g = 0.f;
+    r.b = 0.f;
   }
 }
 
-// One staged chunk in LDS.
+// One staged chunk in LDS: raw k, q, v rows and per-token scalars.  With
+// in-kernel L2 normalisation k_n = rk k and q_n = rq q; the row factors rk, rq
+// are applied to the products (A, P, K S, Q S, the state update) in fp32.
 struct Stage {
   bf16* K; bf16* Q; bf16* V;
-  float* G; float* B; float* EG; float* EDL;   // G, beta, e^G, e^{G_last-G} per token
+  float* G; float* B; float* EG; float* EDL;   // G, beta, e^G, e^{G_last-G}
+  float* RK; float* RQ;                        // rk, rq (1 without normalisation)
+  float* EGK; float* EGQ; float* EDLK;         // e^G rk, scale e^G rq, e^{G_last-G} rk
 };
 
 __device__ __forceinline__ Stage stage_at(unsigned char* smem, int bi) {
@@ -170,52 +185,65 @@ __device__ __forceinline__ Stage stage_at(unsigned char* smem, int bi) {
   s.B = s.G + C;
   s.EG = s.B + C;
   s.EDL = s.EG + C;
+  s.RK = s.EDL + C;
+  s.RQ = s.RK + C;
+  s.EGK = s.RQ + C;
+  s.EGQ = s.EGK + C;
+  s.EDLK = s.EGQ + C;
   return s;
 }
 
-// Stage one 8-feature row slice: optionally L2-normalise across the 16 lanes
-// holding the row, round to bf16, write to LDS.
-__device__ __forceinline__ void stage_row(bf16* dst, const bf16x8& raw, bool norm) {
-  float f[8];
+// 1 / ||row|| of the row whose 8-feature slices the 16 lanes of a DPP row hold.
+__device__ __forceinline__ float row_inv_norm(const bf16x8& raw) {
+  float ss = 0.f;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) f[j] = (float)raw[j];
-  if (norm) {
-    float ss = 0.f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) ss += f[j] * f[j];
-    const float inv = 1.0f / sqrtf(row16_sum(ss) + 1e-6f);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) f[j] *= inv;
-  }
-  bf16x8 b;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) b[j] = (bf16)f[j];
-  *reinterpret_cast<bf16x8*>(dst) = b;
+  for (int j = 0; j < 8; j += 2)
+    ss = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{raw[j], raw[j + 1]}, bf16x2{raw[j], raw[j + 1]},
+                                         ss, false);
+  return __builtin_amdgcn_rsqf(row16_sum(ss) + 1e-6f);
 }
 
-// Write a prefetched chunk into staging buffer st: k (and q) rows L2-normalised,
-// v as is, and the per-token scalars from the in-chunk cumsum of g (wave 0).
+// Row factors of the prefetched rows (1 without in-kernel normalisation).
+template <int MODE>
+__device__ __forceinline__ void prep_rows(RawChunk& r, bool norm) {
+#pragma unroll
+  for (int pass = 0; pass < MT; ++pass) {
+    r.rk[pass] = norm ? row_inv_norm(r.k[pass]) : 1.f;
+    if (MODE == MODE_OUT) r.rq[pass] = norm ? row_inv_norm(r.q[pass]) : 1.f;
+  }
+}
+
+// In-chunk cumsum of g and the decay factors (wave 0; lanes 0-31 = tokens).
+__device__ __forceinline__ void prep_scan(RawChunk& r, int lane) {
+  const float gv = scan32(lane < C ? r.g : 0.f);
+  const float glast = __builtin_bit_cast(
+      float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gv), C - 1));
+  r.gs = gv;
+  r.eg = fast_exp(gv);
+  r.edl = fast_exp(glast - gv);
+}
+
+// Write a prefetched, prepared chunk into staging buffer st.
 template <int MODE>
 __device__ __forceinline__ void stage_chunk(const Stage& st, const RawChunk& r, bool with_q,
-                                            bool norm, int tid, int wave, int lane) {
+                                            int tid, int wave, int lane) {
 #pragma unroll
   for (int pass = 0; pass < MT; ++pass) {
     const int row = pass * 16 + (tid >> 4);
     const int f0 = (tid & 15) * 8;
-    stage_row(st.K + row * LDQ + f0, r.k[pass], norm);
+    *reinterpret_cast<bf16x8*>(st.K + row * LDQ + f0) = r.k[pass];
+    if ((tid & 15) == 0) st.RK[row] = r.rk[pass];
     if (MODE != MODE_PHI) *reinterpret_cast<bf16x8*>(st.V + row * LDQ + f0) = r.v[pass];
-    if (MODE == MODE_OUT && with_q) stage_row(st.Q + row * LDQ + f0, r.q[pass], norm);
-  }
-  if (wave == 0) {
-    const float gv = scan32(lane < C ? r.g : 0.f);
-    const float glast = __builtin_bit_cast(
-        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gv), C - 1));
-    if (lane < C) {
-      st.G[lane] = gv;
-      st.B[lane] = r.b;
-      st.EG[lane] = fast_exp(gv);
-      st.EDL[lane] = fast_exp(glast - gv);
+    if (MODE == MODE_OUT && with_q) {
+      *reinterpret_cast<bf16x8*>(st.Q + row * LDQ + f0) = r.q[pass];
+      if ((tid & 15) == 0) st.RQ[row] = r.rq[pass];
     }
+  }
+  if (wave == 0 && lane < C) {
+    st.G[lane] = r.gs;
+    st.B[lane] = r.b;
+    st.EG[lane] = r.eg;
+    st.EDL[lane] = r.edl;
   }
 }
 
@@ -227,13 +255,10 @@ struct HL {
 };
 
 __device__ __forceinline__ HL split_hl(const f32x4& x) {
-  HL r;
-#pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    r.h[v] = (bf16)x[v];
-    r.l[v] = (bf16)(x[v] - (float)r.h[v]);
-  }
-  return r;
+  bf16x2 h0, h1, l0, l1;
+  split2(x[0], x[1], h0, l0);
+  split2(x[2], x[3], h1, l1);
+  return HL{bf16x4{h0[0], h0[1], h1[0], h1[1]}, bf16x4{l0[0], l0[1], l1[0], l1[1]}};
 }
 
 // acc + X.Y from X^T and Y in C layout: lane (q, l16) holds X[l16][4q..4q+3]
@@ -287,16 +312,9 @@ __device__ __forceinline__ bf16x8 ld_hl(const bf16* hi, const bf16* lo, int r0, 
 // acc + X.Y for a hi/lo block X (from ld_hl) and a C-layout fp32 tile Y split
 // into hi/lo: two MFMAs, (Xh + Xl)(Yh + Yl).
 __device__ __forceinline__ f32x4 mm_hl(const bf16x8& xa, const f32x4& y, f32x4 acc) {
-  bf16x8 bh, bl;
-#pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const bf16 h = (bf16)y[v];
-    const bf16 l = (bf16)(y[v] - (float)h);
-    bh[v] = h; bh[4 + v] = h;
-    bl[v] = l; bl[4 + v] = l;
-  }
-  acc = mfma16(xa, bh, acc);
-  return mfma16(xa, bl, acc);
+  const HL s = split_hl(y);
+  acc = mfma16(xa, bf16x8{s.h[0], s.h[1], s.h[2], s.h[3], s.h[0], s.h[1], s.h[2], s.h[3]}, acc);
+  return mfma16(xa, bf16x8{s.l[0], s.l[1], s.l[2], s.l[3], s.l[0], s.l[1], s.l[2], s.l[3]}, acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -394,7 +412,9 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
       const int t0 = si.bos + c_begin * C;
       load_raw<MODE>(raw, p, qh, kh, vh, q_rs, kv_rs, t0, min(C, si.eos - t0), c_begin >= c_out,
                      tid, h);
-      stage_chunk<MODE>(stage_at(smem, 0), raw, c_begin >= c_out, p.l2norm, tid, wave, lane);
+      prep_rows<MODE>(raw, p.l2norm);
+      if (wave == 0) prep_scan(raw, lane);
+      stage_chunk<MODE>(stage_at(smem, 0), raw, c_begin >= c_out, tid, wave, lane);
       if (c_begin + 1 < si.c_end) {
         const int t1 = t0 + C;
         load_raw<MODE>(raw, p, qh, kh, vh, q_rs, kv_rs, t1, min(C, si.eos - t1),
@@ -421,11 +441,12 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
           bf16x8 af[4];
 #pragma unroll
           for (int ks = 0; ks < 4; ++ks) af[ks] = frag(cur.K, LDQ, 16 * R, 32 * ks, lane);
-          float gr[4], br[4];
+          float gr[4], br[4], kr[4];
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
             gr[v] = cur.G[16 * R + 4 * q4 + v];
-            br[v] = cur.B[16 * R + 4 * q4 + v];
+            kr[v] = cur.RK[16 * R + 4 * q4 + v];
+            br[v] = cur.B[16 * R + 4 * q4 + v] * kr[v];
           }
 #pragma unroll
           for (int j = 0; j <= R; ++j) {
@@ -435,6 +456,9 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
               acc = mfma16(af[ks], frag(cur.K, LDQ, 16 * j, 32 * ks, lane), acc);
             const int col = 16 * j + l16;
             const float gc = cur.G[col];
+            const float kc = cur.RK[col];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[v] *= kc;   // normalised k_r.k_c = kr kc (k_r.k_c)
             if (j < R) {
 #pragma unroll
               for (int v = 0; v < 4; ++v)
@@ -448,7 +472,7 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
               for (int v = 0; v < 4; ++v) {
                 const int row = 16 * R + 4 * q4 + v;
                 Ad[v] = row > col ? br[v] * acc[v] * fast_exp(gr[v] - gc) : 0.f;
-                At_[v] = col > row ? bc * acc[v] * fast_exp(gc - gr[v]) : 0.f;
+                At_[v] = col > row ? bc * kr[v] * acc[v] * fast_exp(gc - gr[v]) : 0.f;
               }
               const f32x4 Tii = inv_unit_lower16(Ad, At_, q4, l16);
 #pragma unroll
@@ -461,9 +485,12 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
           bf16x8 af[4];
 #pragma unroll
           for (int ks = 0; ks < 4; ++ks) af[ks] = frag(cur.Q, LDQ, 16 * i, 32 * ks, lane);
-          float gr[4];
+          float gr[4], qr[4];
 #pragma unroll
-          for (int v = 0; v < 4; ++v) gr[v] = cur.G[16 * i + 4 * q4 + v];
+          for (int v = 0; v < 4; ++v) {
+            gr[v] = cur.G[16 * i + 4 * q4 + v];
+            qr[v] = cur.RQ[16 * i + 4 * q4 + v] * p.scale;
+          }
 #pragma unroll
           for (int j = 0; j <= i; ++j) {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -472,12 +499,22 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
               acc = mfma16(af[ks], frag(cur.K, LDQ, 16 * j, 32 * ks, lane), acc);
             const int col = 16 * j + l16;
             const float gc = cur.G[col];
+            const float kc = cur.RK[col];
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
               const int row = 16 * i + 4 * q4 + v;
-              const float dcy = (row >= col) ? fast_exp(gr[v] - gc) : 0.f;
+              const float dcy = (row >= col) ? qr[v] * kc * fast_exp(gr[v] - gc) : 0.f;
               sP[row * LDT + col] = (bf16)(acc[v] * dcy);
             }
+          }
+        }
+        if constexpr (R == MT) {
+          // per-token factors of phase 2 (k and q row norms folded in)
+          if (lane < C) {
+            const float eg = cur.EG[lane], rk = cur.RK[lane];
+            cur.EGK[lane] = eg * rk;
+            cur.EDLK[lane] = cur.EDL[lane] * rk;
+            if constexpr (OQ) cur.EGQ[lane] = eg * cur.RQ[lane] * p.scale;
           }
         }
         // K S (state as hi + lo) and Q S (state as bf16) for this wave's columns
@@ -508,6 +545,10 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
             }
           }
         }
+        // the next chunk's row factors and g scan (its rows are in registers;
+        // unused values when this is the segment's last chunk)
+        prep_rows<MODE>(raw, p.l2norm);
+        if constexpr (R == 0) prep_scan(raw, lane);
       };
       using I0 = std::integral_constant<int, 0>;
       using I1 = std::integral_constant<int, 1>;
@@ -523,7 +564,8 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
       } else {
         if (wave == 0) phase1(I0{}, BF{});
         else if (wave == 1) phase1(I1{}, BF{});
-        else phase1(I2{}, BF{});
+        else if (wave == 2) phase1(I2{}, BF{});
+        else phase1(I3{}, BF{});
       }
       lds_barrier();
 
@@ -541,7 +583,7 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
               const int r = 16 * mt + 4 * q4 + v;
-              Y[mt][ct][v] = cur.B[r] * ((float)vt[v] - cur.EG[r] * X[mt][ct][v]);
+              Y[mt][ct][v] = cur.B[r] * ((float)vt[v] - cur.EGK[r] * X[mt][ct][v]);
             }
           }
         const bf16x8 t00 = ld_hl(sTh, sTl, 0, 0, lane);
@@ -567,7 +609,7 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
 #pragma unroll
           for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) O[ct][v] = QS[mt][ct][v] * cur.EG[16 * mt + 4 * q4 + v];
+            for (int v = 0; v < 4; ++v) O[ct][v] = QS[mt][ct][v] * cur.EGQ[16 * mt + 4 * q4 + v];
           const bf16x8 a = frag_perm(sP, LDT, 16 * mt, 0, lane);
 #pragma unroll
           for (int ct = 0; ct < 2; ++ct) {
@@ -575,7 +617,7 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
 #pragma unroll
             for (int v = 0; v < 4; ++v)
               sO[(16 * mt + 4 * q4 + v) * LDQ + 32 * wave + 16 * ct + l16] =
-                  (bf16)(O[ct][v] * p.scale);
+                  (bf16)O[ct][v];
           }
         }
       }
@@ -593,7 +635,7 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
-            const float e = cur.EDL[16 * mt + 4 * q4 + v];
+            const float e = cur.EDLK[16 * mt + 4 * q4 + v];
             Vn[mt][0][v] *= e;
             Vn[mt][1][v] *= e;
           }
@@ -614,7 +656,7 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
 
       // ---- stage the next chunk into the other buffer; prefetch the one after -------
       if (c + 1 < si.c_end) {
-        stage_chunk<MODE>(stage_at(smem, bi ^ 1), raw, c + 1 >= c_out, p.l2norm, tid, wave, lane);
+        stage_chunk<MODE>(stage_at(smem, bi ^ 1), raw, c + 1 >= c_out, tid, wave, lane);
         if (c + 2 < si.c_end) {
           const int t2 = tok0 + 2 * C;
           load_raw<MODE>(raw, p, qh, kh, vh, q_rs, kv_rs, t2, min(C, si.eos - t2),

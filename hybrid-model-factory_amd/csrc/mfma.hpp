@@ -73,16 +73,28 @@ __device__ __forceinline__ bf16x8 pack_b(const f32x4& t0, const f32x4& t1) {
                 (bf16)t1[0], (bf16)t1[1], (bf16)t1[2], (bf16)t1[3]};
 }
 
+// hi/lo split of two floats: hi = bf16(x) (one v_cvt_pk_bf16_f32), lo =
+// bf16(x - hi), with hi widened back to fp32 exactly by a shift (low half) and
+// a mask (high half) of the packed pair.  x ~= hi + lo to ~16 significant bits.
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void split2(float x0, float x1, bf16x2& hi, bf16x2& lo) {
+  hi = bf16x2{(bf16)x0, (bf16)x1};
+  const unsigned hb = __builtin_bit_cast(unsigned, hi);
+  const float h0 = __builtin_bit_cast(float, hb << 16);
+  const float h1 = __builtin_bit_cast(float, hb & 0xffff0000u);
+  lo = bf16x2{(bf16)(x0 - h0), (bf16)(x1 - h1)};
+}
+
 // hi/lo split of the same pair: x ~= hi + lo with both in bf16.
 __device__ __forceinline__ void pack_b_hilo(const f32x4& t0, const f32x4& t1, bf16x8& hi,
                                             bf16x8& lo) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const bf16 h0 = (bf16)t0[j], h1 = (bf16)t1[j];
-    hi[j] = h0; hi[4 + j] = h1;
-    lo[j] = (bf16)(t0[j] - (float)h0);
-    lo[4 + j] = (bf16)(t1[j] - (float)h1);
-  }
+  bf16x2 h[4], l[4];
+  split2(t0[0], t0[1], h[0], l[0]);
+  split2(t0[2], t0[3], h[1], l[1]);
+  split2(t1[0], t1[1], h[2], l[2]);
+  split2(t1[2], t1[3], h[3], l[3]);
+  hi = bf16x8{h[0][0], h[0][1], h[1][0], h[1][1], h[2][0], h[2][1], h[3][0], h[3][1]};
+  lo = bf16x8{l[0][0], l[0][1], l[1][0], l[1][1], l[2][0], l[2][1], l[3][0], l[3][1]};
 }
 
 // Sum over the 16 lanes of a DPP row (VALU lane permutes, no LDS traffic).
