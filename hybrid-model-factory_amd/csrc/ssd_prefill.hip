@@ -79,7 +79,11 @@ struct Cfg {
   static constexpr int OFF_M = OFF_C + L * LDB * 2;
   static constexpr int OFF_Y = OFF_M + L * LDM * 2;
   static constexpr int OFF_S = OFF_Y + L * LDX * 2;
-  static constexpr int SMEM = OFF_S + 2 * 4 * L * 4;   // two buffers of 4 scalar arrays
+  static constexpr int OFF_ML = OFF_S + 2 * 4 * L * 4;   // two buffers of 4 scalar arrays
+  // M's low half gets its own region when it fits (no barrier before writing M);
+  // otherwise it reuses C's space once every wave is done with C.
+  static constexpr bool SEP_ML = OFF_ML + L * LDM * 2 <= 80 * 1024;
+  static constexpr int SMEM = SEP_ML ? OFF_ML + L * LDM * 2 : OFF_ML;
   static_assert(SMEM <= 80 * 1024, "LDS budget: two workgroups per CU");
   static_assert(P % 64 == 0 && N % 32 == 0, "tile shape");
 };
@@ -230,9 +234,21 @@ __global__ __launch_bounds__(NTHR, 2) void ssd_chunk_kernel(Params p) {
   };
   if (si.c_start < si.c_end && wave == NTHR / 64 - 1) make_scalars(ra.dt, si.c_start, 0);
 
+  // coalesced store of the y tile staged in sY (chunk starting at tok0)
+  const auto store_y = [&](int tok0, int nval) {
+#pragma unroll
+    for (int i = 0; i < K::VX; ++i) {
+      const int e = tid + NTHR * i, row = e / (P / 8), c8 = (e % (P / 8)) * 8;
+      if (row < nval)
+        *reinterpret_cast<bf16x8*>(p.y + (int64_t)(tok0 + row) * p.y_ts + h * p.y_hs + c8) =
+            *reinterpret_cast<const bf16x8*>(sY + row * LDX + c8);
+    }
+  };
+
+  // Per chunk (OUT): stage | C S^T, M, state update | M X + epilogue, with the
+  // previous chunk's y stored while this one is staged.
   const auto chunk = [&](Raw<P, N>& cur, Raw<P, N>& nxt, int c) {
     const int tok0 = si.bos + c * L;
-    const int nval = nval_of(c);
     const int cb = (c - si.c_start) & 1;
     // ---- stage chunk c, then refill `cur` with chunk c + AHEAD -------------------
 #pragma unroll
@@ -246,6 +262,7 @@ __global__ __launch_bounds__(NTHR, 2) void ssd_chunk_kernel(Params p) {
       *reinterpret_cast<bf16x8*>(sB + row * LDB + c8) = cur.b[i];
       if (MODE == MODE_OUT) *reinterpret_cast<bf16x8*>(sC + row * LDB + c8) = cur.c[i];
     }
+    if (MODE == MODE_OUT && c > si.c_start) store_y(tok0 - L, L);
     bf16x8 zst[K::VX];
     if (MODE == MODE_OUT) {
 #pragma unroll
@@ -256,15 +273,17 @@ __global__ __launch_bounds__(NTHR, 2) void ssd_chunk_kernel(Params p) {
     lds_barrier();
     const float al = SC(cb, S_ACS, L - 1);
 
+    f32x4 Y[4][PB];
     if (MODE == MODE_OUT) {
       // z into the y staging buffer (read back in C layout by the owner lanes)
+      if (p.z) {
 #pragma unroll
-      for (int i = 0; i < K::VX; ++i) {
-        const int e = tid + NTHR * i, row = e / (P / 8), c8 = (e % (P / 8)) * 8;
-        *reinterpret_cast<bf16x8*>(sY + row * LDX + c8) = zst[i];
+        for (int i = 0; i < K::VX; ++i) {
+          const int e = tid + NTHR * i, row = e / (P / 8), c8 = (e % (P / 8)) * 8;
+          *reinterpret_cast<bf16x8*>(sY + row * LDX + c8) = zst[i];
+        }
       }
       // ---- Y = diag(e^A) C S^T (S as bf16 hi + lo) ------------------------------
-      f32x4 Y[4][PB];
 #pragma unroll
       for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
@@ -311,18 +330,22 @@ __global__ __launch_bounds__(NTHR, 2) void ssd_chunk_kernel(Params p) {
         const int j = 16 * jb + l16;
         const float aj = SC(cb, S_ACS, j), dj = SC(cb, S_DT, j);
         const f32x4 at4 = SC4(cb, S_ACS, 16 * tb + 4 * q4);
+        f32x4 m;
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int t = 16 * tb + 4 * q4 + v;
-          const float m = (t >= j) ? acc[v] * fast_exp(at4[v] - aj) * dj : 0.f;
-          mh[k][v] = (bf16)m;
-          ml[k][v] = (bf16)(m - (float)mh[k][v]);
+          m[v] = (t >= j) ? acc[v] * fast_exp(at4[v] - aj) * dj : 0.f;
         }
+        bf16x2 h0, h1, l0, l1;
+        split2(m[0], m[1], h0, l0);
+        split2(m[2], m[3], h1, l1);
+        mh[k] = bf16x4{h0[0], h0[1], h1[0], h1[1]};
+        ml[k] = bf16x4{l0[0], l0[1], l1[0], l1[1]};
       }
       // the last wave (fewest tiles) turns the next chunk's dt into its scalars
       if (wave == NTHR / 64 - 1 && c + 1 < si.c_end) make_scalars(nxt.dt, c + 1, cb ^ 1);
-      lds_barrier();   // every wave is done with sC: its space takes the M low parts
-      bf16* sML = sC;
+      if constexpr (!K::SEP_ML) lds_barrier();   // every wave is done with sC: M's low half goes there
+      bf16* sML = K::SEP_ML ? reinterpret_cast<bf16*>(smem + K::OFF_ML) : sC;
 #pragma unroll
       for (int k = 0; k < 3; ++k) {
         const int tb = TT[wave][k][0], jb = TT[wave][k][1];
@@ -343,9 +366,57 @@ __global__ __launch_bounds__(NTHR, 2) void ssd_chunk_kernel(Params p) {
           sML[a] = (bf16)0.f;
         }
       }
-      lds_barrier();
+    } else if (wave == NTHR / 64 - 1 && c + 1 < si.c_end) {
+      make_scalars(nxt.dt, c + 1, cb ^ 1);
+    }
 
-      // ---- Y += M X (+ D x, z gate) ----------------------------------------------
+    // ---- S^T <- e^{A_L} S^T + B^T diag(w) X (after C S^T used the chunk's start
+    // state).  With one p-block per wave it runs before the M X phase; with two,
+    // after it, where the Y accumulators of C S^T are no longer live next to it.
+    const auto state_update = [&]() {
+      const float ea = fast_exp(al);
+      dsum += al;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int i = 0; i < PB; ++i)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) ST[nb][i][v] *= ea;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const f32x4 w0 = SC4(cb, S_W, 32 * ks + 8 * q4), w1 = SC4(cb, S_W, 32 * ks + 8 * q4 + 4);
+        const float w[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
+        // w x as bf16 hi + lo: one rounding of it would cost ~1e-3 of |S|
+        bf16x8 bwh[PB], bwl[PB];
+#pragma unroll
+        for (int i = 0; i < PB; ++i) {
+          const bf16x8 xr = frag_t(sX, LDX, 32 * ks, 16 * (PB * wave + i), lane);
+#pragma unroll
+          for (int j = 0; j < 8; j += 2) {
+            bf16x2 hh, ll;
+            split2((float)xr[j] * w[j], (float)xr[j + 1] * w[j + 1], hh, ll);
+            bwh[i][j] = hh[0]; bwh[i][j + 1] = hh[1];
+            bwl[i][j] = ll[0]; bwl[i][j + 1] = ll[1];
+          }
+        }
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          const bf16x8 a = frag_t(sB, LDB, 32 * ks, 16 * nb, lane);
+#pragma unroll
+          for (int i = 0; i < PB; ++i) {
+            ST[nb][i] = mfma16(a, bwh[i], ST[nb][i]);
+            ST[nb][i] = mfma16(a, bwl[i], ST[nb][i]);
+          }
+        }
+      }
+    };
+    constexpr bool EARLY_UPDATE = (PB == 1) || (MODE == MODE_LOCAL);
+    if (EARLY_UPDATE) state_update();
+
+    if (MODE == MODE_OUT) {
+      lds_barrier();   // M complete
+      // ---- Y += M X (+ D x, z gate) -> sY -----------------------------------------
+      const bf16* sML = K::SEP_ML ? reinterpret_cast<const bf16*>(smem + K::OFF_ML) : sC;
       bf16x8 bx[2][PB];
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
@@ -383,59 +454,9 @@ __global__ __launch_bounds__(NTHR, 2) void ssd_chunk_kernel(Params p) {
           }
         }
       }
-    } else if (wave == NTHR / 64 - 1 && c + 1 < si.c_end) {
-      make_scalars(nxt.dt, c + 1, cb ^ 1);
     }
-
-    // ---- S^T <- e^{A_L} S^T + B^T diag(w) X ------------------------------------
-    {
-      const float ea = fast_exp(al);
-      dsum += al;
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-        for (int i = 0; i < PB; ++i)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) ST[nb][i][v] *= ea;
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const f32x4 w0 = SC4(cb, S_W, 32 * ks + 8 * q4), w1 = SC4(cb, S_W, 32 * ks + 8 * q4 + 4);
-        const float w[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
-        // w x as bf16 hi + lo: one rounding of it would cost ~1e-3 of |S|
-        bf16x8 bwh[PB], bwl[PB];
-#pragma unroll
-        for (int i = 0; i < PB; ++i) {
-          const bf16x8 xr = frag_t(sX, LDX, 32 * ks, 16 * (PB * wave + i), lane);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const float f = (float)xr[j] * w[j];
-            bwh[i][j] = (bf16)f;
-            bwl[i][j] = (bf16)(f - (float)bwh[i][j]);
-          }
-        }
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-          const bf16x8 a = frag_t(sB, LDB, 32 * ks, 16 * nb, lane);
-#pragma unroll
-          for (int i = 0; i < PB; ++i) {
-            ST[nb][i] = mfma16(a, bwh[i], ST[nb][i]);
-            ST[nb][i] = mfma16(a, bwl[i], ST[nb][i]);
-          }
-        }
-      }
-    }
+    if (!EARLY_UPDATE) state_update();
     lds_barrier();
-
-    if (MODE == MODE_OUT) {
-      // ---- coalesced y store ----------------------------------------------------
-#pragma unroll
-      for (int i = 0; i < K::VX; ++i) {
-        const int e = tid + NTHR * i, row = e / (P / 8), c8 = (e % (P / 8)) * 8;
-        if (row < nval)
-          *reinterpret_cast<bf16x8*>(p.y + (int64_t)(tok0 + row) * p.y_ts + h * p.y_hs + c8) =
-              *reinterpret_cast<const bf16x8*>(sY + row * LDX + c8);
-      }
-    }
   };
 
   if (AHEAD == 2) {
@@ -446,6 +467,7 @@ __global__ __launch_bounds__(NTHR, 2) void ssd_chunk_kernel(Params p) {
   } else {
     for (int c = si.c_start; c < si.c_end; ++c) chunk(ra, ra, c);
   }
+  if (MODE == MODE_OUT && si.c_start < si.c_end) store_y(si.bos + (si.c_end - 1) * L, nval_of(si.c_end - 1));
 
   // ---- segment end state --------------------------------------------------------
   float* dst = nullptr;
