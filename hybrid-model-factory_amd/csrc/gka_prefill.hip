@@ -442,6 +442,17 @@ __global__ __launch_bounds__(NTHR, NW / 4) void gka_chunk_kernel(Params p) {
             Xp[mt][ct][v] = 0.f;
           }
         }
+      // Z~ weights M_tj s_j^2 (j <= t) of this wave's tile, fixed over the iterations
+      f32x4 zw = {0.f, 0.f, 0.f, 0.f};
+      if (wave < 3) {
+        const int a = (wave == 0) ? 0 : 1, b = (wave == 2) ? 1 : 0;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int t = 16 * a + 4 * q4 + v, j = 16 * b + l16;
+          const float sj = SC(S_SK, j);
+          zw[v] = (t >= j) ? sj * sj * fast_exp(SC(S_GK, t) - SC(S_GK, j)) : 0.f;
+        }
+      }
       for (int it = 0; it < p.num_iter; ++it) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
@@ -461,11 +472,7 @@ __global__ __launch_bounds__(NTHR, NW / 4) void gka_chunk_kernel(Params p) {
           }
           f32x4 zs;
 #pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const int t = 16 * a + 4 * q4 + v, j = 16 * b + l16;
-            const float s = SC(S_SK, j);
-            zs[v] = (t >= j) ? z[v] * s * s * fast_exp(SC(S_GK, t) - SC(S_GK, j)) : 0.f;
-          }
+          for (int v = 0; v < 4; ++v) zs[v] = z[v] * zw[v];
           // store Z~ row-major (t, j): 2-byte writes
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
@@ -529,7 +536,8 @@ __global__ __launch_bounds__(NTHR, NW / 4) void gka_chunk_kernel(Params p) {
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
-            const float w = 1.0f / (1.0f - ccv[mt][v] * om[mt][v]);
+            // w <= 2 (c <= 1/4, omega <= 2): the hardware reciprocal (1 ulp) suffices
+            const float w = __builtin_amdgcn_rcpf(1.0f - ccv[mt][v] * om[mt][v]);
             om[mt][v] = w;
 #pragma unroll
             for (int ct = 0; ct < NCT; ++ct) {
