@@ -11,8 +11,9 @@
 //   S <- e^{G_last} S + K^T (e^{G_last-G} V_new)
 // Forming V_new from K S instead of W S needs no W: T is applied to the 32 x 32
 // right-hand side in registers, by blockwise substitution over its two 16-row
-// blocks (T_00, T_11 and -A_10; no merged T_10):
-//   V_new_0 = T_00 Y_0,  V_new_1 = T_11 (Y_1 - A_10 V_new_0),  Y = beta (V - e^G K S).
+// blocks (no merged T_10), with beta folded into T's columns (T' = T diag(beta))
+// and A_10 = diag(beta_1) M_10:
+//   V_new_0 = T'_00 Y_0,  V_new_1 = T'_11 (Y_1 - M_10 V_new_0),  Y = V - e^G K S.
 //
 // The chunk length is an internal choice (the result is the same recurrence at
 // any chunk length, up to fp32 rounding): C = 32 keeps a workgroup's LDS under
@@ -404,6 +405,10 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
     }
   };
 
+  // The state is kept as S / gam with a running scalar gam (the product of the
+  // chunk decays e^{G_last} since the last renormalisation): the decay then costs
+  // per-token factors instead of a multiply of every state element per chunk.
+  float gam = 1.f;
   if (c_begin >= si.c_end) {
     // nothing to scan (empty segment): only the end state below
   } else {
@@ -428,6 +433,11 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
       const Stage cur = stage_at(smem, bi);
       const int tok0 = si.bos + c * C;
       const bool out_chunk = (MODE == MODE_OUT) && (c >= c_out);
+      // gam after this chunk; renormalise (fold gam into the state) before 1/gam
+      // could overflow the update weights
+      const float graw = gam * cur.EG[C - 1];
+      const bool renorm = graw < 0x1p-60f;
+      const float gnext = renorm ? 1.f : graw;
 
       // ---- phase 1: T blocks / P; K S and Q S; store the previous chunk's O ----
       if (MODE == MODE_OUT && c > c_out) store_o(tok0 - C, C);
@@ -463,7 +473,7 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
 #pragma unroll
               for (int v = 0; v < 4; ++v)
                 put_hl(sTh, sTl, 16 * R + 4 * q4 + v, col,
-                       -br[v] * acc[v] * fast_exp(gr[v] - gc));
+                       -kr[v] * acc[v] * fast_exp(gr[v] - gc));
             } else {
               // A and A^T of the diagonal tile in C layout (k.k^T is symmetric)
               const float bc = cur.B[col];
@@ -476,7 +486,7 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
               }
               const f32x4 Tii = inv_unit_lower16(Ad, At_, q4, l16);
 #pragma unroll
-              for (int v = 0; v < 4; ++v) put_hl(sTh, sTl, 16 * R + 4 * q4 + v, col, Tii[v]);
+              for (int v = 0; v < 4; ++v) put_hl(sTh, sTl, 16 * R + 4 * q4 + v, col, Tii[v] * bc);
             }
           }
         } else if constexpr (OQ) {
@@ -511,9 +521,9 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
         if constexpr (R == MT) {
           // per-token factors of phase 2 (k and q row norms folded in)
           if (lane < C) {
-            const float eg = cur.EG[lane], rk = cur.RK[lane];
+            const float eg = cur.EG[lane] * gam, rk = cur.RK[lane];
             cur.EGK[lane] = eg * rk;
-            cur.EDLK[lane] = cur.EDL[lane] * rk;
+            cur.EDLK[lane] = cur.EDL[lane] * rk / gnext;
             if constexpr (OQ) cur.EGQ[lane] = eg * cur.RQ[lane] * p.scale;
           }
         }
@@ -583,7 +593,7 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
               const int r = 16 * mt + 4 * q4 + v;
-              Y[mt][ct][v] = cur.B[r] * ((float)vt[v] - cur.EGK[r] * X[mt][ct][v]);
+              Y[mt][ct][v] = (float)vt[v] - cur.EGK[r] * X[mt][ct][v];
             }
           }
         const bf16x8 t00 = ld_hl(sTh, sTl, 0, 0, lane);
@@ -624,13 +634,14 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
 
       // ---- S <- e^{G_last} S + K^T (e^{G_last-G} V_new), V_new as hi/lo ----------
       {
-        const float egl = cur.EG[C - 1];
+        if (renorm) {
 #pragma unroll
-        for (int rt = 0; rt < 8; ++rt)
+          for (int rt = 0; rt < 8; ++rt)
 #pragma unroll
-          for (int ct = 0; ct < 2; ++ct)
+            for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) S[rt][ct][v] *= egl;
+              for (int v = 0; v < 4; ++v) S[rt][ct][v] *= graw;
+        }
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -663,6 +674,7 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
                          c + 2 >= c_out, tid, h);
         }
       }
+      gam = gnext;
       lds_barrier();
     }
     if (MODE == MODE_OUT && si.c_end > c_out) {
@@ -687,7 +699,7 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
       for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
         for (int v = 0; v < 4; ++v)
-          dst[(16 * rt + 4 * q4 + v) * D + 32 * wave + 16 * ct + l16] = S[rt][ct][v];
+          dst[(16 * rt + 4 * q4 + v) * D + 32 * wave + 16 * ct + l16] = S[rt][ct][v] * gam;
   }
 }
 
