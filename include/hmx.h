@@ -262,6 +262,25 @@ int hmx_ssd_state_update(void* state, int32_t state_dtype, int64_t slot_stride,
                          int32_t batch, int32_t H, int32_t G, int32_t P, int32_t N,
                          int32_t dt_softplus, void* stream);
 
+/*
+ * Gated RMSNorm over rows of D elements (the GDN / GKA output norm):
+ *   norm_before_gate != 0:  out = x / sqrt(mean(x^2) + eps) * weight * silu(z)
+ *   norm_before_gate == 0:  u = x * silu(z); out = u / sqrt(mean(u^2) + eps) * weight
+ * z may be NULL (plain RMSNorm).  x, z, out share `dtype` (16-byte aligned rows,
+ * element row strides); weight [D] in weight_dtype.  fp32 arithmetic, one rounding
+ * to dtype.  D in {64, 128, 256}.
+ * Replaces: RMSNormGated(head_v_dim, group_size=None, norm_before_gate=True)
+ *   (vLLM, un-vendored), constructed at
+ *   vllm-inference/src/primed_vllm/primed_gdn_layer.py:443-450 and
+ *   primed_gka_layer.py:736-743, called at primed_gdn_layer.py:626 and
+ *   primed_gka_layer.py:949; fla FusedRMSNormGated in the training layers
+ *   (training/.../layers/gated_deltanet/gdn.py:201, layers/gated_kalmanet/gka.py:233).
+ */
+int hmx_rms_norm_gated(const void* x, int64_t x_row_stride, const void* z,
+                       int64_t z_row_stride, int32_t dtype, const void* weight,
+                       int32_t weight_dtype, void* out, int64_t out_row_stride, int64_t rows,
+                       int32_t D, float eps, int32_t norm_before_gate, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
