@@ -79,7 +79,8 @@ constexpr int OFF_O = 2 * SZ_BUF;
 constexpr int OFF_TH = OFF_O + SZ_Q;   // rows 0-15: T_00 | rows 16-31: -A_10, T_11
 constexpr int OFF_TL = OFF_TH + SZ_P;
 constexpr int OFF_P = OFF_TL + SZ_P;
-constexpr int SMEM = OFF_P + SZ_P;
+constexpr int OFF_NW = OFF_P + SZ_P;        // fp32 [D] output-norm weight (NORM)
+constexpr int SMEM = OFF_NW + D * 4;
 static_assert(SMEM <= 80 * 1024, "LDS budget: two workgroups per CU");
 
 struct SegInfo {     // one row of the host-built segment table (int32 x 8)
@@ -104,6 +105,10 @@ struct Params {
   int l2norm;
   int max_warm;
   float decay_thresh;
+  // optional gated RMSNorm of each output row (NORM kernels)
+  const bf16* zg; int64_t zg_ts, zg_hs;   // gate rows, or null (plain RMSNorm)
+  const void* onw; int onw_dt;            // weight [D]
+  float on_eps;
 };
 
 __device__ __forceinline__ float ld_scalar(const void* p, int64_t i, int dt) {
@@ -321,7 +326,9 @@ __device__ __forceinline__ f32x4 mm_hl(const bf16x8& xa, const f32x4& y, f32x4 a
 // ---------------------------------------------------------------------------
 // the chunk-scan workgroup
 // ---------------------------------------------------------------------------
-template <int MODE>
+// NORM: the output rows pass through the gated RMSNorm of hmx_rms_norm_gated
+// (norm before gate) on their way out of sO.
+template <int MODE, bool NORM = false>
 __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
   __shared__ __align__(16) unsigned char smem[SMEM];
   bf16* sO = reinterpret_cast<bf16*>(smem + OFF_O);
@@ -404,6 +411,58 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
             *reinterpret_cast<const bf16x8*>(sO + row * LDQ + f0);
     }
   };
+  // NORM: the gate slices of this thread's two output rows (loaded a phase ahead),
+  // then out = o / sqrt(mean(o^2) + eps) * w * silu(z) over each 128-wide row
+  // (16 lanes x 8), o as rounded into sO.
+  const float* sNW = reinterpret_cast<const float*>(smem + OFF_NW);
+  const bf16* zh = NORM && p.zg ? p.zg + (int64_t)h * p.zg_hs : nullptr;
+  auto load_gate = [&](bf16x8* zr, int tok0, int nval) {
+#pragma unroll
+    for (int pass = 0; pass < MT; ++pass) {
+      const int row = pass * 16 + (tid >> 4);
+      zr[pass] = (zh && row < nval)
+                     ? *reinterpret_cast<const bf16x8*>(zh + (int64_t)(tok0 + row) * p.zg_ts +
+                                                        (tid & 15) * 8)
+                     : bf16x8{};
+    }
+  };
+  auto store_o_norm = [&](int tok0, int nval, const bf16x8* zr) {
+#pragma unroll
+    for (int pass = 0; pass < MT; ++pass) {
+      const int row = pass * 16 + (tid >> 4);
+      const int f0 = (tid & 15) * 8;
+      const bf16x8 ov = *reinterpret_cast<const bf16x8*>(sO + row * LDQ + f0);
+      float f[8], ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        f[j] = (float)ov[j];
+        ss += f[j] * f[j];
+      }
+      const float rstd = 1.0f / sqrtf(row16_sum(ss) * (1.0f / D) + p.on_eps);
+      const f32x4 w0 = *reinterpret_cast<const f32x4*>(sNW + f0);
+      const f32x4 w1 = *reinterpret_cast<const f32x4*>(sNW + f0 + 4);
+      const float w[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
+      bf16x8 out;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float y = f[j] * rstd * w[j];
+        if (zh) {
+          const float z = (float)zr[pass][j];
+          y *= z * __builtin_amdgcn_rcpf(1.0f + fast_exp(-z));
+        }
+        out[j] = (bf16)y;
+      }
+      if (row < nval)
+        *reinterpret_cast<bf16x8*>(oh + (int64_t)(tok0 + row) * q_rs + f0) = out;
+    }
+  };
+  if (NORM && tid < D) {
+    float wv;
+    if (p.onw_dt == HMX_F32) wv = static_cast<const float*>(p.onw)[tid];
+    else if (p.onw_dt == HMX_BF16) wv = (float)static_cast<const bf16*>(p.onw)[tid];
+    else wv = (float)static_cast<const f16*>(p.onw)[tid];
+    reinterpret_cast<float*>(smem + OFF_NW)[tid] = wv;
+  }
 
   // The state is kept as S / gam with a running scalar gam (the product of the
   // chunk decays e^{G_last} since the last renormalisation): the decay then costs
@@ -440,7 +499,11 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
       const float gnext = renorm ? 1.f : graw;
 
       // ---- phase 1: T blocks / P; K S and Q S; store the previous chunk's O ----
-      if (MODE == MODE_OUT && c > c_out) store_o(tok0 - C, C);
+      bf16x8 zr[MT];
+      if (MODE == MODE_OUT && c > c_out) {
+        if constexpr (NORM) load_gate(zr, tok0 - C, C);   // stored at the end of phase 1
+        else store_o(tok0 - C, C);
+      }
 
       f32x4 X[MT][2], QS[MT][2];
       auto phase1 = [&](auto role_c, auto outq_c) {
@@ -577,6 +640,9 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
         else if (wave == 2) phase1(I2{}, BF{});
         else phase1(I3{}, BF{});
       }
+      if constexpr (NORM) {
+        if (c > c_out) store_o_norm(tok0 - C, C, zr);
+      }
       lds_barrier();
 
       __builtin_amdgcn_s_setprio(1);
@@ -679,7 +745,13 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
     }
     if (MODE == MODE_OUT && si.c_end > c_out) {
       const int tl = si.bos + (si.c_end - 1) * C;
-      store_o(tl, min(C, si.eos - tl));
+      if constexpr (NORM) {
+        bf16x8 zl[MT];
+        load_gate(zl, tl, min(C, si.eos - tl));
+        store_o_norm(tl, min(C, si.eos - tl), zl);
+      } else {
+        store_o(tl, min(C, si.eos - tl));
+      }
     }
   }
 
@@ -798,7 +870,7 @@ extern "C" int hmx_gdn_chunk_fwd(const void* q, const void* k, const void* v, in
                                  int32_t H, int32_t HKV, int32_t K, int32_t V, float scale,
                                  int32_t use_qk_l2norm, int32_t max_warm_chunks,
                                  float decay_threshold, void* workspace, size_t workspace_bytes,
-                                 void* stream) {
+                                 const hmx_gated_norm* o_norm, void* stream) {
   HMX_REQUIRE(qkv_dtype == HMX_BF16, HMX_EUNSUPPORTED,
               "hmx_gdn_chunk_fwd: q/k/v must be bfloat16 (got dtype code %d)", qkv_dtype);
   HMX_REQUIRE(K == D && V == D, HMX_EUNSUPPORTED,
@@ -821,6 +893,18 @@ extern "C" int hmx_gdn_chunk_fwd(const void* q, const void* k, const void* v, in
   p.o = static_cast<bf16*>(o); p.h0 = h0; p.ht = ht;
   p.seg = seg_table; p.nseg_total = nseg_total; p.H = H; p.HKV = HKV; p.scale = scale;
   p.l2norm = use_qk_l2norm; p.max_warm = max_warm_chunks; p.decay_thresh = decay_threshold;
+  p.zg = nullptr; p.zg_ts = p.zg_hs = 0; p.onw = nullptr; p.onw_dt = HMX_F32; p.on_eps = 0.f;
+  if (o_norm) {
+    HMX_REQUIRE(o_norm->weight && o_norm->weight_dtype >= 0 && o_norm->weight_dtype <= 2,
+                HMX_EINVAL, "hmx_gdn_chunk_fwd: o_norm needs a weight (dtype code 0-2)");
+    HMX_REQUIRE(!o_norm->gate || ((uintptr_t)o_norm->gate % 16 == 0 &&
+                                  o_norm->gate_token_stride % 8 == 0 &&
+                                  o_norm->gate_head_stride % 8 == 0),
+                HMX_EINVAL, "hmx_gdn_chunk_fwd: o_norm gate rows must be 16-byte aligned");
+    p.zg = static_cast<const bf16*>(o_norm->gate);
+    p.zg_ts = o_norm->gate_token_stride; p.zg_hs = o_norm->gate_head_stride;
+    p.onw = o_norm->weight; p.onw_dt = o_norm->weight_dtype; p.on_eps = o_norm->eps;
+  }
   // workspace carve-up: state buffers first (256-byte aligned), then plan/exact
   const size_t st = (size_t)nseg_total * H * D * D * sizeof(float);
   char* ws = static_cast<char*>(workspace);
@@ -839,7 +923,10 @@ extern "C" int hmx_gdn_chunk_fwd(const void* q, const void* k, const void* v, in
   } else {
     p.plan = nullptr;  // one segment per sequence: every segment starts from h0
   }
-  hipLaunchKernelGGL(gdn_chunk_kernel<MODE_OUT>, dim3(nseg_total, H), dim3(NTHR), 0, s, p);
+  if (o_norm)
+    hipLaunchKernelGGL((gdn_chunk_kernel<MODE_OUT, true>), dim3(nseg_total, H), dim3(NTHR), 0, s, p);
+  else
+    hipLaunchKernelGGL(gdn_chunk_kernel<MODE_OUT>, dim3(nseg_total, H), dim3(NTHR), 0, s, p);
   return check_launch("hmx_gdn_chunk_fwd");
 }
 

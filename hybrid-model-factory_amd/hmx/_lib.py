@@ -38,7 +38,7 @@ SIGNATURES: dict[str, list] = {
                               _F32, _I32, _I32, _P],
     "hmx_gdn_chunk_fwd": [_P, _P, _P, _I32, _P, _I32, _P, _I32, _P, _P, _P,
                           _P, _I32, _I32, _I32, _I32, _I32, _I32, _F32,
-                          _I32, _I32, _F32, _P, ctypes.c_size_t, _P],
+                          _I32, _I32, _F32, _P, ctypes.c_size_t, _P, _P],
     "hmx_gdn_chunk_workspace_bytes": [_I32, _I32, _I32],
     "hmx_gka_gating": [_P, _I32, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I32, _P, _I32,
                        _P, _P, _P, _I32, _I64, _I32, _F32, _F32, _P],
@@ -66,6 +66,27 @@ SIGNATURES: dict[str, list] = {
 _RESTYPES = {"hmx_last_error": ctypes.c_char_p, "hmx_gdn_chunk_workspace_bytes": ctypes.c_size_t,
              "hmx_gka_chunk_workspace_bytes": ctypes.c_size_t,
              "hmx_ssd_chunk_workspace_bytes": ctypes.c_size_t}
+
+
+
+class GatedNorm(ctypes.Structure):
+    """hmx_gated_norm (include/hmx.h): the optional output-norm epilogue."""
+    _fields_ = [("gate", _P), ("gate_token_stride", _I64), ("gate_head_stride", _I64),
+                ("weight", _P), ("weight_dtype", _I32), ("eps", _F32)]
+
+
+def gated_norm(gate: torch.Tensor | None, weight: torch.Tensor, eps: float, V: int):
+    """ctypes pointer to an hmx_gated_norm for a gate viewed as [tokens, H, V]
+    (None: no epilogue requested -> returns None, i.e. NULL)."""
+    w = weight.contiguous()
+    if w.numel() != V:
+        raise ValueError(f"o_norm weight has {w.numel()} elements, expected {V}")
+    s = GatedNorm(None if gate is None else ctypes.c_void_p(gate.data_ptr()),
+                  0 if gate is None else gate.stride(0), 0 if gate is None else gate.stride(1),
+                  ctypes.c_void_p(w.data_ptr()), dtype_code(w), float(eps))
+    s._keep = (gate, w)   # the tensors outlive the call
+    return ctypes.pointer(s)
+
 
 _lib = None
 

@@ -202,6 +202,9 @@ def chunk_gated_delta_rule_gqa(
     cu_seqlens: torch.Tensor | None = None,
     use_qk_l2norm_in_kernel: bool = False,
     *,
+    o_norm_weight: torch.Tensor | None = None,
+    o_norm_gate: torch.Tensor | None = None,
+    o_norm_eps: float = 1e-5,
     _segment_chunks: int | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor | None]:
     """GQA-native chunked gated delta rule (prefill).
@@ -211,6 +214,12 @@ def chunk_gated_delta_rule_gqa(
     (o [B,T,H,V] in q.dtype, final_state [N,H,K,V] fp32 or None)
     (chunk_gqa.py:15-83).  ``_segment_chunks`` overrides the parallel
     decomposition (tests); results do not depend on it beyond fp32 rounding.
+    
+    Keyword-only extension (no reference counterpart): ``o_norm_weight`` [V] (and
+    optionally ``o_norm_gate`` [B,T,H,V], q.dtype) returns the layer's
+    ``o_norm(o, z)`` (gated RMSNorm, norm before gate, eps ``o_norm_eps``;
+    primed_gdn_layer.py:621-626) computed in the kernel's output epilogue instead
+    of o.
     """
     assert q.dtype == k.dtype == v.dtype
     assert q.dtype != torch.float32, "Does not support float32. Use bfloat16."
@@ -251,14 +260,32 @@ def chunk_gated_delta_rule_gqa(
     lib = _lib.load()
     ws_bytes = int(lib.hmx_gdn_chunk_workspace_bytes(len(rows), N, H))
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
+    onorm = None
+    if o_norm_weight is not None:
+        _lib.require_gpu(o_norm_weight, o_norm_gate)
+        z = None if o_norm_gate is None else _gate_rows(o_norm_gate, (B, T, H, V), q.dtype)
+        onorm = _lib.gated_norm(z, o_norm_weight, o_norm_eps, V)
+    elif o_norm_gate is not None:
+        raise ValueError("o_norm_gate needs o_norm_weight")
     _lib.call("hmx_gdn_chunk_fwd",
               _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.dtype_code(q),
               _lib.ptr(g), _lib.dtype_code(g), _lib.ptr(beta), _lib.dtype_code(beta),
               _lib.ptr(o), _lib.ptr(h0), _lib.ptr(ht),
               _lib.ptr(seg), len(rows), N, H, HKV, K, V, float(scale),
               int(bool(use_qk_l2norm_in_kernel)), MAX_WARM_CHUNKS, DECAY_THRESHOLD,
-              _lib.ptr(ws), ws.numel(), _lib.stream_of(q))
+              _lib.ptr(ws), ws.numel(), onorm, _lib.stream_of(q))
     return o, ht
+
+
+def _gate_rows(z: torch.Tensor, shape: tuple, dtype: torch.dtype) -> torch.Tensor:
+    """The output-norm gate as a [tokens, H, V] view with V contiguous and 16-byte
+    aligned rows (copied only when no such view exists)."""
+    if tuple(z.shape) != tuple(shape) or z.dtype != dtype:
+        raise ValueError(f"o_norm_gate must be {tuple(shape)} {dtype}, got {tuple(z.shape)} {z.dtype}")
+    zz = z.reshape(-1, shape[-2], shape[-1]) if z.dim() == 4 else z
+    if (zz.stride(-1) != 1 or zz.stride(0) % 8 or zz.stride(1) % 8 or zz.data_ptr() % 16):
+        zz = zz.contiguous()
+    return zz
 
 
 def chunk_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None,

@@ -38,6 +38,21 @@ enum hmx_status {
 enum hmx_dtype { HMX_F32 = 0, HMX_BF16 = 1, HMX_F16 = 2 };
 
 int hmx_abi_version(void);
+
+/* Optional output epilogue of the mixer ops: the gated RMSNorm of
+ * hmx_rms_norm_gated (norm before gate) applied to every output row (one head's V
+ * values) before it is stored, so out = o / sqrt(mean(o^2) + eps) * weight *
+ * silu(gate), with o as the op would have returned it.  It fuses the layers'
+ * o_norm(core_attn_out, z) (vllm-inference/src/primed_vllm/primed_gdn_layer.py:626,
+ * primed_gka_layer.py:949) into the op; no reference counterpart as one call. */
+typedef struct hmx_gated_norm {
+  const void* gate;           /* [tokens, H, V] in the op's q/k/v dtype, or NULL */
+  int64_t gate_token_stride;  /* elements between tokens (multiple of 8) */
+  int64_t gate_head_stride;   /* elements between heads (multiple of 8); V contiguous */
+  const void* weight;         /* [V] */
+  int32_t weight_dtype;
+  float eps;
+} hmx_gated_norm;
 const char* hmx_last_error(void);
 
 /*
@@ -105,6 +120,7 @@ int hmx_gdn_recurrent_fwd(const void* q, const void* k, const void* v, int32_t q
  *    history is bounded below exp(-decay_threshold); otherwise the exact
  *    segment scan runs.
  *  workspace: device scratch of hmx_gdn_chunk_workspace_bytes(...) bytes.
+ *  o_norm: NULL, or the output gated RMSNorm applied in the op's epilogue.
  * Replaces: chunk_gated_delta_rule_gqa
  *   vllm-inference/src/primed_vllm/gdn/ops/chunk_gqa.py:15-83 (and its kernels
  *   wy_fast_gqa.py:19-112, chunk_delta_h_gqa.py:29-215, chunk_o_gqa.py:30-114).
@@ -115,7 +131,8 @@ int hmx_gdn_chunk_fwd(const void* q, const void* k, const void* v, int32_t qkv_d
                       const int32_t* seg_table, int32_t nseg_total, int32_t N,
                       int32_t H, int32_t HKV, int32_t K, int32_t V, float scale,
                       int32_t use_qk_l2norm, int32_t max_warm_chunks, float decay_threshold,
-                      void* workspace, size_t workspace_bytes, void* stream);
+                      void* workspace, size_t workspace_bytes, const hmx_gated_norm* o_norm,
+                      void* stream);
 
 /* Workspace bytes hmx_gdn_chunk_fwd needs for a given segment table (host-only
  * arithmetic).  Companion of hmx_gdn_chunk_fwd; no reference counterpart (the
