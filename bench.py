@@ -68,6 +68,37 @@ def bench_prefill(dev, steps, warmup, HKV=32):
     return dict(ms=ms, tokens_per_s=T / (ms * 1e-3), bytes=by, flops=fl, GBps=gbs, TFLOPs=tfs)
 
 
+def bench_onorm(dev, steps, warmup):
+    """The layer's output norm o_norm(o, z) at C1: the standalone gated RMSNorm kernel,
+    prefill + norm as two ops, and the prefill with the norm fused into its epilogue."""
+    import torch
+    import hmx
+    from hmx import workloads as wl
+    T, H, D = 32768, 32, 128
+    d = wl.gdn_inputs(T=T, H=H, HKV=H, D=D, config_id=1, device=dev, gen_device=dev)
+    args = [d[n] for n in ("q", "k", "v", "g", "beta")]
+    g = torch.Generator(device=dev).manual_seed(wl.SEED_BASE + 6)
+    z = torch.randn(1, T, H, D, generator=g, device=dev).bfloat16()
+    w = torch.rand(D, generator=g, device=dev) + 0.5
+    o, _ = hmx.chunk_gated_delta_rule_gqa(*args, use_qk_l2norm_in_kernel=True)
+    ms_norm = _timed(lambda: hmx.rms_norm_gated(o, z, w), steps, warmup)
+
+    def unfused():
+        oo, _ = hmx.chunk_gated_delta_rule_gqa(*args, output_final_state=True,
+                                               use_qk_l2norm_in_kernel=True)
+        hmx.rms_norm_gated(oo, z, w)
+
+    def fused():
+        hmx.chunk_gated_delta_rule_gqa(*args, output_final_state=True, use_qk_l2norm_in_kernel=True,
+                                       o_norm_weight=w, o_norm_gate=z)
+
+    ms_unf = _timed(unfused, steps, warmup)
+    ms_fus = _timed(fused, steps, warmup)
+    norm_bytes = 3 * T * H * D * 2   # o, z read; out written (bf16)
+    return dict(ms_norm=ms_norm, ms_unfused=ms_unf, ms_fused=ms_fus, norm_bytes=norm_bytes,
+                norm_GBps=norm_bytes / (ms_norm * 1e-3) / 1e9)
+
+
 def bench_decode(dev, steps_total=512, warmup=8):
     import torch
     import hmx
@@ -208,7 +239,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "decode", "gka", "ssd"], default=None)
+    ap.add_argument("--only", choices=["prefill", "decode", "gka", "ssd", "onorm"], default=None)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (HBM counter calibration)")
     a = ap.parse_args()
@@ -226,6 +257,8 @@ def main():
     if a.only in (None, "prefill"):
         pf = bench_prefill(dev, a.steps, a.warmup)
         out["prefill"] = pf
+    if a.only in (None, "onorm"):
+        out["onorm"] = bench_onorm(dev, a.steps, a.warmup)
     if a.only in (None, "decode"):
         out["decode"] = bench_decode(dev)
     if a.only in (None, "gka"):
@@ -273,6 +306,19 @@ def main():
                          "ms_per_step": line["decode"]["ms_per_step"],
                          "config": line["decode"]["config"],
                          "roofline": line["decode"]["roofline"]})
+    if "onorm" in out:
+        r = out["onorm"]
+        line["o_norm"] = {
+            "config": {"workload": "C1 GDN prefill output norm o_norm(o, z) (gated RMSNorm, "
+                                   "norm before gate)", "T": 32768, "H": 32, "d": 128},
+            "prefill_then_norm_ms": round(r["ms_unfused"], 4),
+            "prefill_fused_norm_ms": round(r["ms_fused"], 4),
+            "norm_kernel_ms": round(r["ms_norm"], 4),
+            "norm_roofline": {"bound": "hbm", "achieved": round(r["norm_GBps"], 1),
+                              "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                              "frac": round(r["norm_GBps"] / HBM_PEAK_GBS, 4),
+                              "algorithmic_bytes": r["norm_bytes"], "traffic": None},
+        }
     if "gka" in out:
         line["gka"] = {}
         for n, r in out["gka"].items():
