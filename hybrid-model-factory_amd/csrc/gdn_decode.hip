@@ -35,6 +35,10 @@ struct RecurrentParams {
   int H, HKV, V;
   float scale;
   int l2norm, inplace;
+  // optional gated RMSNorm of each output row (NORM kernels; V <= 128)
+  const void* zg; int64_t zg_ts, zg_hs;   // gate rows in q's dtype, or null
+  const void* onw; int onw_dt;            // weight [V]
+  float on_eps;
 };
 
 __device__ __forceinline__ float load_scalar(const void* p, int64_t i, int dtype) {
@@ -51,7 +55,10 @@ __device__ __forceinline__ float rowgroup_sum(float x) {
   return x;
 }
 
-template <int K, typename TQ, typename TS>
+// NORM: each output row (one workgroup holds all V <= 128 columns) passes through
+// the gated RMSNorm of hmx_rms_norm_gated (norm before gate) on its way out, from
+// o as rounded to q's dtype; the sum of squares crosses the waves through LDS.
+template <int K, typename TQ, typename TS, bool NORM>
 __global__ __launch_bounds__(256) void gdn_recurrent_kernel(RecurrentParams p) {
   constexpr int R = K / 8;  // rows per lane
   const int lane = threadIdx.x & 63;
@@ -90,6 +97,13 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(RecurrentParams p) {
     if (write_row < 0) return;
   } else {
     write_row = n;
+  }
+
+  __shared__ float part[2][4];   // NORM: per-wave sums of squares, by token parity
+  float wn[4] = {0.f, 0.f, 0.f, 0.f};
+  if (NORM) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) wn[j] = load_scalar(p.onw, col + j, p.onw_dt);
   }
 
   float S[R][4];
@@ -157,6 +171,29 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(RecurrentParams p) {
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) ov[j] = rowgroup_sum(ov[j]);
+    if constexpr (NORM) {
+      float zz[4] = {0.f, 0.f, 0.f, 0.f};
+      if (p.zg) load_vec<4>(static_cast<const TQ*>(p.zg) + tok * p.zg_ts + h * p.zg_hs + col, zz);
+      float ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        ov[j] = to_f32(from_f32<TQ>(ov[j]));   // o as the op returns it
+        ss += ov[j] * ov[j];
+      }
+      ss += shfl_xor(ss, 1);
+      ss += shfl_xor(ss, 2);
+      ss += shfl_xor(ss, 4);
+      if (lane == 0) part[t & 1][wave] = ss;
+      __syncthreads();
+      float tot = 0.f;
+      for (int w = 0; w < (int)(blockDim.x >> 6); ++w) tot += part[t & 1][w];
+      const float rstd = 1.0f / sqrtf(tot / V + p.on_eps);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        ov[j] *= rstd * wn[j];
+        if (p.zg) ov[j] *= zz[j] / (1.0f + expf(-zz[j]));
+      }
+    }
     if (r == 0) store_vec<4>(static_cast<TQ*>(p.o) + (tok * p.H + h) * V + col, ov);
   }
 
@@ -170,9 +207,12 @@ template <int K, typename TQ, typename TS>
 static void launch(const RecurrentParams& p, int64_t N, hipStream_t s) {
   // at most 4 waves (128 state columns) per workgroup; wider V spans grid.y
   const int waves = p.V / 32;
-  hipLaunchKernelGGL((gdn_recurrent_kernel<K, TQ, TS>),
-                     dim3((unsigned)(N * p.H), (unsigned)((waves + 3) / 4)),
-                     dim3(64 * (waves < 4 ? waves : 4)), 0, s, p);
+  const dim3 grid((unsigned)(N * p.H), (unsigned)((waves + 3) / 4)),
+      block(64 * (waves < 4 ? waves : 4));
+  if (p.onw)
+    hipLaunchKernelGGL((gdn_recurrent_kernel<K, TQ, TS, true>), grid, block, 0, s, p);
+  else
+    hipLaunchKernelGGL((gdn_recurrent_kernel<K, TQ, TS, false>), grid, block, 0, s, p);
 }
 
 template <int K, typename TQ>
@@ -201,7 +241,7 @@ extern "C" int hmx_gdn_recurrent_fwd(
     const int32_t* cu_seqlens, const int32_t* ssm_state_indices, int64_t idx_stride,
     const int32_t* num_accepted_tokens, int64_t B, int64_t T, int64_t N, int32_t H, int32_t HKV,
     int32_t K, int32_t V, float scale, int32_t use_qk_l2norm, int32_t inplace_final_state,
-    void* stream) {
+    const hmx_gated_norm* o_norm, void* stream) {
   using namespace hmx;
   HMX_REQUIRE(H > 0 && HKV > 0 && H % HKV == 0, HMX_EINVAL,
               "hmx_gdn_recurrent_fwd: H=%d must be a positive multiple of HKV=%d", H, HKV);
@@ -228,6 +268,20 @@ extern "C" int hmx_gdn_recurrent_fwd(
   p.cu_seqlens = cu_seqlens; p.idx = ssm_state_indices; p.idx_stride = idx_stride;
   p.num_accepted = num_accepted_tokens; p.T = T; p.H = H; p.HKV = HKV; p.V = V;
   p.scale = scale; p.l2norm = use_qk_l2norm; p.inplace = inplace_final_state;
+  p.zg = nullptr; p.zg_ts = p.zg_hs = 0; p.onw = nullptr; p.onw_dt = HMX_F32; p.on_eps = 0.f;
+  if (o_norm) {
+    HMX_REQUIRE(V <= 128, HMX_EUNSUPPORTED,
+                "hmx_gdn_recurrent_fwd: the fused output norm needs V <= 128 (got %d)", V);
+    HMX_REQUIRE(o_norm->weight && o_norm->weight_dtype >= 0 && o_norm->weight_dtype <= 2,
+                HMX_EINVAL, "hmx_gdn_recurrent_fwd: o_norm needs a weight (dtype code 0-2)");
+    const int64_t vec = qkv_dtype == HMX_F32 ? 4 : 8;
+    HMX_REQUIRE(!o_norm->gate || ((uintptr_t)o_norm->gate % 8 == 0 &&
+                                  o_norm->gate_token_stride % vec == 0 &&
+                                  o_norm->gate_head_stride % vec == 0),
+                HMX_EINVAL, "hmx_gdn_recurrent_fwd: o_norm gate rows must be aligned");
+    p.zg = o_norm->gate; p.zg_ts = o_norm->gate_token_stride; p.zg_hs = o_norm->gate_head_stride;
+    p.onw = o_norm->weight; p.onw_dt = o_norm->weight_dtype; p.on_eps = o_norm->eps;
+  }
   hipStream_t s = (hipStream_t)stream;
   int rc;
   if (K == 64) rc = dispatch_qkv<64>(p, N, qkv_dtype, state_dtype, s);

@@ -35,7 +35,7 @@ SIGNATURES: dict[str, list] = {
                               _P, _I64, _P, _I64, _I32,
                               _P, _P, _I64, _P,
                               _I64, _I64, _I64, _I32, _I32, _I32, _I32,
-                              _F32, _I32, _I32, _P],
+                              _F32, _I32, _I32, _P, _P],
     "hmx_gdn_chunk_fwd": [_P, _P, _P, _I32, _P, _I32, _P, _I32, _P, _P, _P,
                           _P, _I32, _I32, _I32, _I32, _I32, _I32, _F32,
                           _I32, _I32, _F32, _P, ctypes.c_size_t, _P, _P],

@@ -65,6 +65,10 @@ def fused_recurrent_gated_delta_rule_gqa(
     ssm_state_indices: torch.Tensor | None = None,
     num_accepted_tokens: torch.Tensor | None = None,
     use_qk_l2norm_in_kernel: bool = False,
+    *,
+    o_norm_weight: torch.Tensor | None = None,
+    o_norm_gate: torch.Tensor | None = None,
+    o_norm_eps: float = 1e-5,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """GQA-native fused recurrent gated delta rule (decode).
 
@@ -73,6 +77,11 @@ def fused_recurrent_gated_delta_rule_gqa(
     [slots,H,K,V] is updated in place at ``ssm_state_indices`` and returned;
     otherwise a new [B,T,H,K,V] tensor holds sequence n's final state in flat
     row n.  Returns (o [B,T,H,V], final_state)  (fused_recurrent_gqa.py:227-277).
+
+    Keyword-only extension (no reference counterpart): ``o_norm_weight`` [V] (and
+    optionally ``o_norm_gate`` [B,T,H,V], q.dtype) returns the layer's gated
+    RMSNorm ``o_norm(o, z)`` (primed_gdn_layer.py:621-626) instead of o, fused into
+    the kernel's output for V <= 128 (a separate hmx.rms_norm_gated call otherwise).
     """
     if cu_seqlens is not None and q.shape[0] != 1:
         raise ValueError(f"Batch size expected to be 1 with cu_seqlens, got {q.shape[0]}")
@@ -109,6 +118,16 @@ def fused_recurrent_gated_delta_rule_gqa(
     idx_stride = 0 if idx is None else idx.stride(0)
     o = q.new_empty(B, T, H, V)
     state_dt = _lib.dtype_code(final_state)
+    onorm, norm_after = None, False
+    if o_norm_weight is not None:
+        _lib.require_gpu(o_norm_weight, o_norm_gate)
+        z = None if o_norm_gate is None else _gate_rows(o_norm_gate, (B, T, H, V), q.dtype)
+        if V <= 128:
+            onorm = _lib.gated_norm(z, o_norm_weight, o_norm_eps, V)
+        else:
+            norm_after = True
+    elif o_norm_gate is not None:
+        raise ValueError("o_norm_gate needs o_norm_weight")
     _lib.call("hmx_gdn_recurrent_fwd",
               _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.dtype_code(q),
               _lib.ptr(g), _lib.dtype_code(g),
@@ -120,7 +139,10 @@ def fused_recurrent_gated_delta_rule_gqa(
               _lib.ptr(_i32(cu_seqlens)), _lib.ptr(idx), idx_stride,
               _lib.ptr(_i32(num_accepted_tokens)),
               B, T, N, H, HKV, K, V, float(scale), int(bool(use_qk_l2norm_in_kernel)),
-              int(bool(inplace_final_state)), _lib.stream_of(q))
+              int(bool(inplace_final_state)), onorm, _lib.stream_of(q))
+    if norm_after:
+        from .norm import rms_norm_gated
+        o = rms_norm_gated(o, o_norm_gate, o_norm_weight, eps=o_norm_eps)
     return o, final_state
 
 

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define HMX_ABI_VERSION 1
+#define HMX_ABI_VERSION 2  /* 2: optional hmx_gated_norm output epilogue in the GDN ops */
 
 enum hmx_status {
   HMX_OK = 0,
@@ -102,7 +102,7 @@ int hmx_gdn_recurrent_fwd(const void* q, const void* k, const void* v, int32_t q
                           int64_t B, int64_t T, int64_t N,
                           int32_t H, int32_t HKV, int32_t K, int32_t V,
                           float scale, int32_t use_qk_l2norm, int32_t inplace_final_state,
-                          void* stream);
+                          const hmx_gated_norm* o_norm, void* stream);
 
 
 /*

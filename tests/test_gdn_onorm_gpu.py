@@ -98,3 +98,35 @@ def test_fused_norm_strided_gate_bf16_weight(dev):
     unf = hmx.rms_norm_gated(o, z, wb.to(dev))
     torch.cuda.synchronize()
     _close_ulp(on, unf)
+
+
+@pytest.mark.parametrize("K,V,lens", [(128, 128, [1] * 9), (128, 128, [3, 0, 5, 1, 4]),
+                                      (64, 64, [2, 1, 3]), (128, 256, [1, 2])])
+def test_decode_fused_norm(dev, K, V, lens):
+    """The decode op with o_norm: fused in the kernel for V <= 128 (per-token
+    cross-wave sums, multi-token sequences), a separate norm call for V = 256; both
+    against decode-then-norm, with the pool updated identically."""
+    H, HKV, slots = 4, 2, 16
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0)), dtype=torch.int32)
+    n_tok, N = int(cu[-1]), len(lens)
+    g0 = torch.Generator().manual_seed(K + V + n_tok)
+    q = F.normalize(torch.randn(1, n_tok, H, K, generator=g0), dim=-1).bfloat16()
+    k = F.normalize(torch.randn(1, n_tok, HKV, K, generator=g0), dim=-1).bfloat16()
+    v = torch.randn(1, n_tok, HKV, V, generator=g0).bfloat16()
+    g = F.logsigmoid(torch.randn(1, n_tok, H, generator=g0))
+    beta = torch.sigmoid(torch.randn(1, n_tok, H, generator=g0))
+    z = (torch.randn(1, n_tok, H, V, generator=g0) * 1.5).bfloat16()
+    w = torch.rand(V, generator=g0) + 0.5
+    pool = torch.randn(slots, H, K, V, generator=g0) * 0.02
+    idx = torch.randperm(slots, generator=g0)[:N].to(torch.int32)
+    d = [x.to(dev) for x in (q, k, v, g, beta)]
+    kw = dict(inplace_final_state=True, cu_seqlens=cu.to(dev), ssm_state_indices=idx.to(dev),
+              use_qk_l2norm_in_kernel=True)
+    p1, p2 = pool.to(dev), pool.to(dev)
+    o, _ = hmx.fused_recurrent_gated_delta_rule_gqa(*d, initial_state=p1, **kw)
+    on, _ = hmx.fused_recurrent_gated_delta_rule_gqa(*d, initial_state=p2, **kw,
+                                                     o_norm_weight=w.to(dev), o_norm_gate=z.to(dev))
+    unf = hmx.rms_norm_gated(o, z.to(dev), w.to(dev))
+    torch.cuda.synchronize()
+    assert torch.equal(p1, p2)
+    _close_ulp(on, unf)
