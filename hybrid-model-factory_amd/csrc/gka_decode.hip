@@ -38,6 +38,10 @@ struct Params {
   int H, HKV;
   int num_iter;
   float ridge_ratio, scale;
+  // optional gated RMSNorm of the output row (NORM kernels)
+  const void* zg; int64_t zg_ts, zg_hs;   // gate rows in q's dtype, or null
+  const void* onw; int onw_dt;            // weight [D]
+  float on_eps;
 };
 
 __device__ __forceinline__ float ld_scalar(const void* p, int64_t i, int dt) {
@@ -53,10 +57,13 @@ __device__ __forceinline__ float rowgroup_sum(float x) {
   return x;
 }
 
-template <typename TQ, typename TKV>
+// NORM: the output row passes through the gated RMSNorm of hmx_rms_norm_gated
+// (norm before gate), from o as rounded to q's dtype.
+template <typename TQ, typename TKV, bool NORM>
 __global__ __launch_bounds__(256) void gka_decode_kernel(Params p) {
   __shared__ float sx[2][D];
   __shared__ float sred[4];
+  __shared__ float spart[4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = lane & 7, r = lane >> 3;
   const int n = blockIdx.x / p.H, h = blockIdx.x - n * p.H;
@@ -148,7 +155,8 @@ __global__ __launch_bounds__(256) void gka_decode_kernel(Params p) {
   float w = 2.0f;
   int buf = 0;
   for (int it = 0; it < p.num_iter; ++it) {
-    w = 1.0f / (1.0f - cc * w);
+    // w <= 2 (c <= 1/4, omega <= 2): the hardware reciprocal (1 ulp) suffices
+    w = __builtin_amdgcn_rcpf(1.0f - cc * w);
     float hx[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < 16; ++i)
@@ -189,15 +197,46 @@ __global__ __launch_bounds__(256) void gka_decode_kernel(Params p) {
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j) ov[j] = rowgroup_sum(ov[j]);
+  if constexpr (NORM) {
+    float zz[4] = {0.f, 0.f, 0.f, 0.f};
+    if (p.zg) load_vec<4>(static_cast<const TQ*>(p.zg) + bos * p.zg_ts + h * p.zg_hs + col, zz);
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      ov[j] = to_f32(from_f32<TQ>(ov[j]));   // o as the op returns it
+      ss += ov[j] * ov[j];
+    }
+    ss += shfl_xor(ss, 1);
+    ss += shfl_xor(ss, 2);
+    ss += shfl_xor(ss, 4);
+    if (lane == 0) spart[wave] = ss;
+    __syncthreads();
+    const float rstd = 1.0f / sqrtf((spart[0] + spart[1] + spart[2] + spart[3]) / D + p.on_eps);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      ov[j] *= rstd * ld_scalar(p.onw, col + j, p.onw_dt);
+      if (p.zg) ov[j] *= zz[j] / (1.0f + expf(-zz[j]));
+    }
+  }
   if (r == 0) store_vec<4>(static_cast<TQ*>(p.o) + (bos * p.H + h) * D + col, ov);
+}
+
+template <typename TQ, typename TKV>
+static void launch(const Params& p, int64_t N, hipStream_t s) {
+  if (p.onw)
+    hipLaunchKernelGGL((gka_decode_kernel<TQ, TKV, true>), dim3((unsigned)(N * p.H)), dim3(256), 0,
+                       s, p);
+  else
+    hipLaunchKernelGGL((gka_decode_kernel<TQ, TKV, false>), dim3((unsigned)(N * p.H)), dim3(256), 0,
+                       s, p);
 }
 
 template <typename TQ>
 static int dispatch_kv(const Params& p, int64_t N, int kv_dt, hipStream_t s) {
   if (kv_dt == HMX_F32)
-    hipLaunchKernelGGL((gka_decode_kernel<TQ, float>), dim3((unsigned)(N * p.H)), dim3(256), 0, s, p);
+    launch<TQ, float>(p, N, s);
   else if (kv_dt == HMX_BF16)
-    hipLaunchKernelGGL((gka_decode_kernel<TQ, bf16>), dim3((unsigned)(N * p.H)), dim3(256), 0, s, p);
+    launch<TQ, bf16>(p, N, s);
   else
     return set_error(HMX_EUNSUPPORTED, "hmx_gka_decode_fwd: h_kv dtype %d", kv_dt);
   return HMX_OK;
@@ -216,7 +255,8 @@ extern "C" int hmx_gka_decode_fwd(const void* q, const void* k, const void* v, i
                                   const int32_t* cu_seqlens, const int32_t* ssm_state_indices,
                                   int64_t idx_stride, int64_t B, int64_t T, int64_t N, int32_t H,
                                   int32_t HKV, int32_t D, int32_t V, int32_t num_iter,
-                                  float ridge_ratio, float scale, void* stream) {
+                                  float ridge_ratio, float scale, const hmx_gated_norm* o_norm,
+                                  void* stream) {
   using namespace hmx;
   HMX_REQUIRE(D == gkad::D && V == gkad::D, HMX_EUNSUPPORTED,
               "hmx_gka_decode_fwd: only D == V == 128 is supported (got D=%d V=%d)", D, V);
@@ -238,6 +278,18 @@ extern "C" int hmx_gka_decode_fwd(const void* q, const void* k, const void* v, i
   p.cu_seqlens = cu_seqlens; p.idx = ssm_state_indices; p.idx_stride = idx_stride;
   p.T = T; p.H = H; p.HKV = HKV; p.num_iter = num_iter; p.ridge_ratio = ridge_ratio;
   p.scale = scale;
+  p.zg = nullptr; p.zg_ts = p.zg_hs = 0; p.onw = nullptr; p.onw_dt = HMX_F32; p.on_eps = 0.f;
+  if (o_norm) {
+    HMX_REQUIRE(o_norm->weight && o_norm->weight_dtype >= 0 && o_norm->weight_dtype <= 2,
+                HMX_EINVAL, "hmx_gka_decode_fwd: o_norm needs a weight (dtype code 0-2)");
+    const int64_t vec = qkv_dtype == HMX_F32 ? 4 : 8;
+    HMX_REQUIRE(!o_norm->gate || ((uintptr_t)o_norm->gate % 8 == 0 &&
+                                  o_norm->gate_token_stride % vec == 0 &&
+                                  o_norm->gate_head_stride % vec == 0),
+                HMX_EINVAL, "hmx_gka_decode_fwd: o_norm gate rows must be aligned");
+    p.zg = o_norm->gate; p.zg_ts = o_norm->gate_token_stride; p.zg_hs = o_norm->gate_head_stride;
+    p.onw = o_norm->weight; p.onw_dt = o_norm->weight_dtype; p.on_eps = o_norm->eps;
+  }
   hipStream_t s = (hipStream_t)stream;
   int rc;
   if (qkv_dtype == HMX_BF16) rc = gkad::dispatch_kv<bf16>(p, N, h_kv_dtype, s);

@@ -73,7 +73,8 @@ constexpr int OFF_ZL = OFF_ZH + SZ_Z;
 constexpr int OFF_KK = OFF_ZL + SZ_Z;              // fp32 [C][LDK]
 constexpr int OFF_S = OFF_KK + C * LDK * 4;         // fp32 per-token scalars
 constexpr int NSC = 25;                             // scalar arrays of C floats
-constexpr int SMEM = OFF_S + NSC * C * 4;
+constexpr int OFF_NW = OFF_S + NSC * C * 4;        // fp32 [D] output-norm weight (NORM)
+constexpr int SMEM = OFF_NW + D * 4;
 static_assert(SMEM <= 80 * 1024, "LDS budget");
 // per-token scalar array indices
 enum { S_G, S_GK, S_EG, S_EGK, S_EDL, S_EDLK, S_BE, S_SK, S_IQ, S_ALPHA, S_KN2, S_QN2,
@@ -100,6 +101,10 @@ struct Params {
   int H, HKV, num_iter;
   float ridge_ratio, scale;
   int l2norm;                             // 0: q, k are used as given
+  // optional gated RMSNorm of each output row (NORM kernels)
+  const bf16* zg; int64_t zg_ts, zg_hs;   // gate rows, or null (plain RMSNorm)
+  const void* onw; int onw_dt;            // weight [D]
+  float on_eps;
 };
 
 __device__ __forceinline__ float ldsc(const void* p, int64_t i, int dt) {
@@ -165,8 +170,10 @@ __device__ __forceinline__ void put_t_hilo(bf16* th, bf16* tl, int ld, int r0, i
   if (tl) *reinterpret_cast<bf16x4*>(tl + a) = lo;
 }
 
-template <int MODE>
 // One workgroup per CU: NW / 4 waves per SIMD (the second bound is waves per SIMD).
+// NORM: the output rows pass through the gated RMSNorm of hmx_rms_norm_gated (norm
+// before gate) on their way out of sO.
+template <int MODE, bool NORM = false>
 __global__ __launch_bounds__(NTHR, NW / 4) void gka_chunk_kernel(Params p) {
   __shared__ __align__(16) unsigned char smem[SMEM];
   bf16* sQ = reinterpret_cast<bf16*>(smem + OFF_Q);
@@ -190,6 +197,13 @@ __global__ __launch_bounds__(NTHR, NW / 4) void gka_chunk_kernel(Params p) {
   const bool track_h = p.num_iter > 0;
 
   if (MODE == MODE_LOCAL && si.seg_idx == si.nseg - 1) return;
+  if (NORM && tid < D) {
+    float wv;
+    if (p.onw_dt == HMX_F32) wv = static_cast<const float*>(p.onw)[tid];
+    else if (p.onw_dt == HMX_BF16) wv = (float)static_cast<const bf16*>(p.onw)[tid];
+    else wv = (float)static_cast<const f16*>(p.onw)[tid];
+    reinterpret_cast<float*>(smem + OFF_NW)[tid] = wv;   // read after the chunk's barriers
+  }
 
   // ---- initial states ----------------------------------------------------
   f32x4 Hs[8][NCT], Ss[8][NCT];
@@ -637,7 +651,19 @@ __global__ __launch_bounds__(NTHR, NW / 4) void gka_chunk_kernel(Params p) {
             sO[(16 * mt + 4 * q4 + v) * LDQ + CW * wave + 16 * ct + l16] = (bf16)(O[mt][ct][v] * p.scale);
     }
 
-    // ---- P3: state updates (hi/lo B operands) ---------------------------------
+    // ---- P3: state updates (hi/lo B operands); the output-norm gate is loaded
+    // here, a phase before the O store uses it ---------------------------------
+    bf16x8 zr[NPASS];
+    if constexpr (NORM) {
+#pragma unroll
+      for (int pass = 0; pass < NPASS; ++pass) {
+        const int row = pass * RPP + (tid >> 4);
+        zr[pass] = (p.zg && row < nval)
+                       ? *reinterpret_cast<const bf16x8*>(p.zg + (int64_t)(tok0 + row) * p.zg_ts +
+                                                          (int64_t)h * p.zg_hs + (tid & 15) * 8)
+                       : bf16x8{};
+      }
+    }
     {
       const float egl = SC(S_EG, C - 1), egkl = SC(S_EGK, C - 1);
 #pragma unroll
@@ -685,15 +711,33 @@ __global__ __launch_bounds__(NTHR, NW / 4) void gka_chunk_kernel(Params p) {
     }
     lds_barrier();
 
-    // ---- store O -------------------------------------------------------------
+    // ---- store O (NORM: out = o / sqrt(mean(o^2) + eps) * w * silu(z) per row) -
     if (MODE == MODE_OUT) {
       bf16* oh = p.o + (int64_t)h * D;
 #pragma unroll
       for (int pass = 0; pass < NPASS; ++pass) {
         const int row = pass * RPP + (tid >> 4), f0 = (tid & 15) * 8;
-        if (row < nval)
-          *reinterpret_cast<bf16x8*>(oh + (int64_t)(tok0 + row) * q_rs + f0) =
-              *reinterpret_cast<const bf16x8*>(sO + row * LDQ + f0);
+        bf16x8 ov = *reinterpret_cast<const bf16x8*>(sO + row * LDQ + f0);
+        if constexpr (NORM) {
+          const float* sNW = reinterpret_cast<const float*>(smem + OFF_NW);
+          float f[8], ss = 0.f;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            f[j] = (float)ov[j];
+            ss += f[j] * f[j];
+          }
+          const float rstd = 1.0f / sqrtf(row16_sum(ss) * (1.0f / D) + p.on_eps);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            float y = f[j] * rstd * sNW[f0 + j];
+            if (p.zg) {
+              const float z = (float)zr[pass][j];
+              y *= z * __builtin_amdgcn_rcpf(1.0f + fast_exp(-z));
+            }
+            ov[j] = (bf16)y;
+          }
+        }
+        if (row < nval) *reinterpret_cast<bf16x8*>(oh + (int64_t)(tok0 + row) * q_rs + f0) = ov;
       }
     }
   }
@@ -772,7 +816,7 @@ extern "C" int hmx_gka_chunk_fwd(const void* q, const void* k, const void* v, in
                                  int32_t N, int32_t H, int32_t HKV, int32_t D_, int32_t V,
                                  int32_t num_iter, float ridge_ratio, float scale,
                                  int32_t use_qk_l2norm, void* workspace, size_t workspace_bytes,
-                                 void* stream) {
+                                 const hmx_gated_norm* o_norm, void* stream) {
   HMX_REQUIRE(qkv_dtype == HMX_BF16, HMX_EUNSUPPORTED,
               "hmx_gka_chunk_fwd: q/k/v must be bfloat16 (got dtype code %d)", qkv_dtype);
   HMX_REQUIRE(D_ == D && V == D, HMX_EUNSUPPORTED,
@@ -790,6 +834,18 @@ extern "C" int hmx_gka_chunk_fwd(const void* q, const void* k, const void* v, in
   p.v = static_cast<const bf16*>(v);
   p.alpha = alpha; p.alpha_dt = alpha_dtype; p.g = g; p.g_dt = g_dtype;
   p.gk = gk; p.gk_dt = gk_dtype; p.beta = beta; p.beta_dt = beta_dtype;
+  p.zg = nullptr; p.zg_ts = p.zg_hs = 0; p.onw = nullptr; p.onw_dt = HMX_F32; p.on_eps = 0.f;
+  if (o_norm) {
+    HMX_REQUIRE(o_norm->weight && o_norm->weight_dtype >= 0 && o_norm->weight_dtype <= 2,
+                HMX_EINVAL, "hmx_gka_chunk_fwd: o_norm needs a weight (dtype code 0-2)");
+    HMX_REQUIRE(!o_norm->gate || ((uintptr_t)o_norm->gate % 16 == 0 &&
+                                  o_norm->gate_token_stride % 8 == 0 &&
+                                  o_norm->gate_head_stride % 8 == 0),
+                HMX_EINVAL, "hmx_gka_chunk_fwd: o_norm gate rows must be 16-byte aligned");
+    p.zg = static_cast<const bf16*>(o_norm->gate);
+    p.zg_ts = o_norm->gate_token_stride; p.zg_hs = o_norm->gate_head_stride;
+    p.onw = o_norm->weight; p.onw_dt = o_norm->weight_dtype; p.on_eps = o_norm->eps;
+  }
   p.o = static_cast<bf16*>(o);
   p.hkk0 = h_kk0; p.hkv0 = h_kv0; p.hkk_t = h_kk_final; p.hkv_t = h_kv_final;
   p.seg = seg_table; p.nseg_total = nseg_total;
@@ -808,6 +864,9 @@ extern "C" int hmx_gka_chunk_fwd(const void* q, const void* k, const void* v, in
     hipLaunchKernelGGL(gka_chunk_kernel<MODE_LOCAL>, dim3(nseg_total, H), dim3(NTHR), 0, s, p);
     hipLaunchKernelGGL(gka_seg_combine_kernel, dim3(N * H, 16), dim3(256), 0, s, p);
   }
-  hipLaunchKernelGGL(gka_chunk_kernel<MODE_OUT>, dim3(nseg_total, H), dim3(NTHR), 0, s, p);
+  if (o_norm)
+    hipLaunchKernelGGL((gka_chunk_kernel<MODE_OUT, true>), dim3(nseg_total, H), dim3(NTHR), 0, s, p);
+  else
+    hipLaunchKernelGGL(gka_chunk_kernel<MODE_OUT>, dim3(nseg_total, H), dim3(NTHR), 0, s, p);
   return check_launch("hmx_gka_chunk_fwd");
 }

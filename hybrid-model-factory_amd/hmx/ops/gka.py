@@ -18,7 +18,7 @@ import logging
 import torch
 
 from .. import _lib
-from .gdn import _cu_count, _i32, _segment_table
+from .gdn import _cu_count, _gate_rows, _i32, _segment_table
 
 GKA_WORKGROUPS_PER_CU = 1
 _warned_num_iter_zero = False
@@ -66,13 +66,19 @@ def chebyshev_iteration_gqa(k, q, v, alpha, gk=None, beta=None, num_iter: int = 
                             scale: float | None = None, ridge_ratio: float = 0.1,
                             initial_state_kk=None, initial_state_kv=None,
                             output_final_state: bool = True, inplace_final_state: bool = True,
-                            cu_seqlens=None, ssm_state_indices=None):
+                            cu_seqlens=None, ssm_state_indices=None, *,
+                            o_norm_weight=None, o_norm_gate=None, o_norm_eps: float = 1e-6):
     """Fused GKA decode step (chebyshev_iteration_gqa.py:173-238).
 
     k [B,T,HKV,D]; q [B,T,H,D]; v [B,T,HKV,V]; alpha, gk, beta [B,T,H].
     States [N,H,D,D] / [N,H,D,V] (slot pools with ssm_state_indices), updated in
     place when ``inplace_final_state``.  Only the first token of each sequence
     is processed.  Returns (o, h_kk_out, h_kv_out).
+
+    Keyword-only extension (no reference counterpart): ``o_norm_weight`` [V] (and
+    optionally ``o_norm_gate`` [B,T,H,V], q.dtype) returns the layer's gated
+    RMSNorm ``o_norm(o, z)`` (primed_gka_layer.py:944-949) fused into the kernel's
+    output instead of o.
     """
     if cu_seqlens is not None and q.shape[0] != 1:
         raise ValueError(f"Batch size must be 1 when using cu_seqlens, got {q.shape[0]}.")
@@ -102,6 +108,7 @@ def chebyshev_iteration_gqa(k, q, v, alpha, gk=None, beta=None, num_iter: int = 
         hkk, hkv = initial_state_kk.clone(), initial_state_kv.clone()
     idx = _i32(ssm_state_indices)
     o = q.new_empty(B, T, H, V)
+    onorm = _onorm(o_norm_weight, o_norm_gate, o_norm_eps, (B, T, H, V), q.dtype)
     _lib.call("hmx_gka_decode_fwd",
               _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.dtype_code(q),
               _lib.ptr(alpha), _lib.dtype_code(alpha),
@@ -112,7 +119,7 @@ def chebyshev_iteration_gqa(k, q, v, alpha, gk=None, beta=None, num_iter: int = 
               _lib.ptr(hkv), hkv.stride(0), _lib.ptr(hkv), hkv.stride(0), _lib.dtype_code(hkv),
               _lib.ptr(_i32(cu_seqlens)), _lib.ptr(idx), 0 if idx is None else idx.stride(0),
               B, T, N, H, HKV, D, V, int(num_iter), float(ridge_ratio), float(scale),
-              _lib.stream_of(q))
+              onorm, _lib.stream_of(q))
     if not output_final_state:
         return o, None, None
     if not inplace_final_state and idx is not None:
@@ -124,8 +131,10 @@ def chebyshev_iteration_gqa(k, q, v, alpha, gk=None, beta=None, num_iter: int = 
 def gka_chebyshev_gla_decode(q, k, v, alpha, g, gk, beta, gla_scale: float,
                              ridge_ratio: float = 0.02, num_sketches_per_head: int = 1,
                              num_iter: int = 30, gka=None, h_kk=None, h_kv=None,
-                             cu_seqlens=None, ssm_state_indices=None):
-    """Single-token GKA decode (gka_forward.py:248-326)."""
+                             cu_seqlens=None, ssm_state_indices=None, *,
+                             o_norm_weight=None, o_norm_gate=None, o_norm_eps: float = 1e-6):
+    """Single-token GKA decode (gka_forward.py:248-326).  ``o_norm_*``: see
+    chebyshev_iteration_gqa."""
     global _warned_num_iter_zero
     _check_sketching_constraints(gka, num_sketches_per_head, "gka_chebyshev_gla_decode")
     if num_iter == 0:
@@ -139,27 +148,47 @@ def gka_chebyshev_gla_decode(q, k, v, alpha, g, gk, beta, gla_scale: float,
                                    num_iter=num_iter, scale=gla_scale, ridge_ratio=ridge_ratio,
                                    initial_state_kk=h_kk, initial_state_kv=h_kv,
                                    output_final_state=True, inplace_final_state=True,
-                                   cu_seqlens=cu_seqlens, ssm_state_indices=ssm_state_indices)
+                                   cu_seqlens=cu_seqlens, ssm_state_indices=ssm_state_indices,
+                                   o_norm_weight=o_norm_weight, o_norm_gate=o_norm_gate,
+                                   o_norm_eps=o_norm_eps)
 
 
 def gka_chebyshev_gla_prefill(q, k, v, alpha, g, gk, beta, gla_scale: float,
                               ridge_ratio: float = 0.02, num_sketches_per_head: int = 1,
                               num_iter: int = 30, gka=None, h_kk_initial=None, h_kv_initial=None,
                               output_final_state: bool = True, cu_seqlens=None, *,
+                              o_norm_weight=None, o_norm_gate=None, o_norm_eps: float = 1e-6,
                               _segment_chunks: int | None = None):
     """Full GKA prefill: Chebyshev query refinement + beta^2 simple GLA
     (gka_forward.py:161-242).  Returns (o, h_kk_final, h_kv_final); h_kk_final is
-    None when num_iter == 0 or not output_final_state."""
+    None when num_iter == 0 or not output_final_state.
+
+    Keyword-only extension (no reference counterpart): ``o_norm_weight`` [V] (and
+    optionally ``o_norm_gate`` [B,T,H,V], q.dtype) returns the layer's gated
+    RMSNorm ``o_norm(o, z)`` (primed_gka_layer.py:944-949) computed in the
+    kernel's output epilogue instead of o."""
     _check_sketching_constraints(gka, num_sketches_per_head, "gka_chebyshev_gla_prefill")
     if cu_seqlens is not None and q.shape[0] != 1:
         raise ValueError(f"Batch size must be 1 when using cu_seqlens, got {q.shape[0]}")
     return _gka_prefill(q, k, v, alpha, g, gk, beta, gla_scale, ridge_ratio, num_iter,
                         h_kk_initial, h_kv_initial, output_final_state, cu_seqlens, True,
-                        _segment_chunks)
+                        _segment_chunks, (o_norm_weight, o_norm_gate, o_norm_eps))
+
+
+def _onorm(weight, gate, eps, shape, dtype):
+    """hmx_gated_norm pointer for the optional output norm (None: not requested)."""
+    if weight is None:
+        if gate is not None:
+            raise ValueError("o_norm_gate needs o_norm_weight")
+        return None
+    _lib.require_gpu(weight, gate)
+    z = None if gate is None else _gate_rows(gate, shape, dtype)
+    return _lib.gated_norm(z, weight, eps, shape[-1])
 
 
 def _gka_prefill(q, k, v, alpha, g, gk, beta, gla_scale, ridge_ratio, num_iter, h_kk_initial,
-                 h_kv_initial, output_final_state, cu_seqlens, l2norm, segment_chunks=None):
+                 h_kv_initial, output_final_state, cu_seqlens, l2norm, segment_chunks=None,
+                 o_norm=(None, None, 1e-6)):
     _lib.require_gpu(q, k, v, alpha, g, gk, beta, h_kk_initial, h_kv_initial, cu_seqlens)
     B, T, H, D = q.shape
     HKV, V = k.shape[2], v.shape[-1]
@@ -196,7 +225,8 @@ def _gka_prefill(q, k, v, alpha, g, gk, beta, gla_scale, ridge_ratio, num_iter, 
               _lib.ptr(beta), 0 if beta is None else _lib.dtype_code(beta),
               _lib.ptr(o), _lib.ptr(hkk0), _lib.ptr(hkv0), _lib.ptr(hkk_t), _lib.ptr(hkv_t),
               _lib.ptr(seg), len(rows), N, H, HKV, D, V, int(num_iter), float(ridge_ratio),
-              float(gla_scale), int(bool(l2norm)), _lib.ptr(ws), ws.numel(), _lib.stream_of(q))
+              float(gla_scale), int(bool(l2norm)), _lib.ptr(ws), ws.numel(),
+              _onorm(*o_norm, tuple(o.shape), q.dtype), _lib.stream_of(q))
     return o, hkk_t, hkv_t
 
 

@@ -178,7 +178,8 @@ int hmx_gka_decode_fwd(const void* q, const void* k, const void* v, int32_t qkv_
                        const int32_t* cu_seqlens, const int32_t* ssm_state_indices,
                        int64_t idx_stride, int64_t B, int64_t T, int64_t N,
                        int32_t H, int32_t HKV, int32_t D, int32_t V,
-                       int32_t num_iter, float ridge_ratio, float scale, void* stream);
+                       int32_t num_iter, float ridge_ratio, float scale,
+                       const hmx_gated_norm* o_norm, void* stream);
 
 /*
  * GKA chunked prefill forward (Chebyshev ridge solve + beta^2 GLA), GQA-native,
@@ -207,7 +208,8 @@ int hmx_gka_chunk_fwd(const void* q, const void* k, const void* v, int32_t qkv_d
                       const int32_t* seg_table, int32_t nseg_total, int32_t N,
                       int32_t H, int32_t HKV, int32_t D, int32_t V,
                       int32_t num_iter, float ridge_ratio, float scale, int32_t use_qk_l2norm,
-                      void* workspace, size_t workspace_bytes, void* stream);
+                      void* workspace, size_t workspace_bytes,
+                      const hmx_gated_norm* o_norm, void* stream);
 
 /* Workspace bytes hmx_gka_chunk_fwd needs (host-only arithmetic).  Companion of
  * hmx_gka_chunk_fwd; no reference counterpart (the reference allocates its
