@@ -3,6 +3,7 @@ from .gdn import (chunk_gated_delta_rule, chunk_gated_delta_rule_gqa, fused_gdn_
                   fused_recurrent_gated_delta_rule, fused_recurrent_gated_delta_rule_gqa)
 from .gka import (chebyshev_iteration_gqa, fused_gka_gating, gka_chebyshev_gla,
                   gka_chebyshev_gla_decode, gka_chebyshev_gla_prefill, torch_decoding_one_step)
+from .conv import causal_conv1d_fn, causal_conv1d_update
 from .norm import rms_norm_gated
 from .ssd import (mamba_chunk_scan_combined, mamba_chunk_scan_combined_varlen,
                   selective_state_update)
@@ -23,4 +24,6 @@ __all__ = [
     "mamba_chunk_scan_combined_varlen",
     "selective_state_update",
     "rms_norm_gated",
+    "causal_conv1d_fn",
+    "causal_conv1d_update",
 ]

@@ -1,0 +1,123 @@
+"""Short causal depthwise conv1d: the mixers' input convolution.
+
+vLLM's ``causal_conv1d_fn`` (prefill) and ``causal_conv1d_update`` (decode), as the
+layers call them (vllm-inference/src/primed_vllm/primed_gdn_layer.py:700-780): x is
+the [dim, tokens] transposed view of the [tokens, dim] projection output, the
+weight [dim, width], and the conv state pool [slots, state_len, dim] with
+channels contiguous (primed_utils.py:174-177).  Per channel,
+
+    out[t] = act(bias + sum_i w[i] x[t - (width-1) + i]),  act = silu ("silu"/"swish") or none,
+
+with positions before a sequence's first token taken from its state (zeros
+without an initial state); the state then holds the sequence's last state_len
+inputs.  Speculative decoding (``num_accepted_tokens``) and prefix-cache block
+arguments are not supported (NotImplementedError).
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+
+PAD_SLOT_ID = -1
+
+
+def _act(activation) -> int:
+    if activation in (None, False):
+        return 0
+    if activation is True or activation in ("silu", "swish"):
+        return 1
+    raise NotImplementedError(f"activation {activation!r} (silu, swish or None)")
+
+
+def _rows(t: torch.Tensor) -> torch.Tensor:
+    """[tokens, dim] rows with channels contiguous and 16-byte aligned rows."""
+    if t.stride(-1) != 1 or t.stride(0) % (16 // t.element_size()) or t.data_ptr() % 16:
+        t = t.contiguous()
+    return t
+
+
+def _i32(t):
+    return None if t is None else t.to(torch.int32).contiguous()
+
+
+def causal_conv1d_fn(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None,
+                     conv_states: torch.Tensor | None = None,
+                     query_start_loc: torch.Tensor | None = None,
+                     cache_indices: torch.Tensor | None = None,
+                     has_initial_state: torch.Tensor | None = None,
+                     activation: str | None = "silu", pad_slot_id: int = PAD_SLOT_ID,
+                     metadata=None, validate_data: bool = False, **block_args) -> torch.Tensor:
+    """Prefill conv over concatenated sequences.  x [dim, total] (the transposed
+    view of [total, dim]); returns the same layout.  ``conv_states`` is updated in
+    place at ``cache_indices`` (default: sequence b uses slot b)."""
+    if any(v is not None for v in block_args.values()):
+        raise NotImplementedError("prefix-cache block arguments of causal_conv1d_fn: "
+                                  f"{sorted(k for k, v in block_args.items() if v is not None)}")
+    _lib.require_gpu(x, weight, bias, conv_states, query_start_loc, cache_indices,
+                     has_initial_state)
+    dim, total = x.shape
+    W = weight.shape[-1]
+    if weight.shape != (dim, W):
+        raise ValueError(f"weight must be [{dim}, width], got {tuple(weight.shape)}")
+    xr = _rows(x.t())
+    if query_start_loc is None:
+        query_start_loc = torch.tensor([0, total], dtype=torch.int32, device=x.device)
+    qs = _i32(query_start_loc)
+    bounds = [int(v) for v in qs.tolist()]
+    batch = len(bounds) - 1
+    if bounds[0] != 0 or any(b < a for a, b in zip(bounds, bounds[1:])) or bounds[-1] > total:
+        raise ValueError(f"query_start_loc must be non-decreasing from 0 to <= {total}: {bounds}")
+    out = torch.empty(total, dim, dtype=x.dtype, device=x.device)
+    if bounds[-1] < total:
+        out[bounds[-1]:].zero_()      # tokens past the last sequence are not computed
+    st_len, sst, srs = 0, 0, 0
+    if conv_states is not None:
+        if conv_states.dtype != x.dtype or conv_states.shape[-1] != dim or \
+                conv_states.stride(-1) != 1:
+            raise ValueError(f"conv_states must be [slots, state_len, {dim}] {x.dtype} with "
+                             f"channels contiguous, got {tuple(conv_states.shape)} {conv_states.dtype}")
+        st_len, sst, srs = conv_states.shape[1], conv_states.stride(0), conv_states.stride(1)
+    hinit = None if has_initial_state is None else has_initial_state.to(torch.uint8).contiguous()
+    w = weight.contiguous()
+    b = None if bias is None else bias.contiguous()
+    _lib.call("hmx_causal_conv1d_fwd", _lib.ptr(xr), xr.stride(0), _lib.ptr(out), out.stride(0),
+              _lib.dtype_code(x), _lib.ptr(w), _lib.dtype_code(w), W, _lib.ptr(b),
+              0 if b is None else _lib.dtype_code(b), _lib.ptr(conv_states), sst, srs, st_len,
+              _lib.ptr(qs), batch, bounds[-1], _lib.ptr(_i32(cache_indices)), _lib.ptr(hinit),
+              dim, _act(activation), int(pad_slot_id), _lib.stream_of(x))
+    return out.t()
+
+
+def causal_conv1d_update(x: torch.Tensor, conv_state: torch.Tensor, weight: torch.Tensor,
+                         bias: torch.Tensor | None = None, activation=None,
+                         conv_state_indices: torch.Tensor | None = None,
+                         num_accepted_tokens: torch.Tensor | None = None,
+                         query_start_loc: torch.Tensor | None = None, max_query_len: int = -1,
+                         pad_slot_id: int = PAD_SLOT_ID, validate_data: bool = False
+                         ) -> torch.Tensor:
+    """Decode conv: x [batch, dim], one token per sequence, against the slot pool
+    ``conv_state`` [slots, state_len, dim] (updated in place: the state shifts by
+    one row).  Returns [batch, dim]; padded entries (slot == pad_slot_id) give 0."""
+    if num_accepted_tokens is not None or query_start_loc is not None:
+        raise NotImplementedError("speculative multi-token causal_conv1d_update")
+    _lib.require_gpu(x, conv_state, weight, bias, conv_state_indices)
+    if x.dim() != 2:
+        raise NotImplementedError(f"x must be [batch, dim], got {tuple(x.shape)}")
+    batch, dim = x.shape
+    W = weight.shape[-1]
+    if weight.shape != (dim, W):
+        raise ValueError(f"weight must be [{dim}, width], got {tuple(weight.shape)}")
+    if conv_state.dtype != x.dtype or conv_state.shape[-1] != dim or conv_state.stride(-1) != 1:
+        raise ValueError(f"conv_state must be [slots, state_len, {dim}] {x.dtype} with channels "
+                         f"contiguous, got {tuple(conv_state.shape)} {conv_state.dtype}")
+    xr = _rows(x)
+    out = torch.empty(batch, dim, dtype=x.dtype, device=x.device)
+    w = weight.contiguous()
+    b = None if bias is None else bias.contiguous()
+    _lib.call("hmx_causal_conv1d_update", _lib.ptr(xr), xr.stride(0), _lib.ptr(out), out.stride(0),
+              _lib.dtype_code(x), _lib.ptr(w), _lib.dtype_code(w), W, _lib.ptr(b),
+              0 if b is None else _lib.dtype_code(b), _lib.ptr(conv_state), conv_state.stride(0),
+              conv_state.stride(1), conv_state.shape[1], _lib.ptr(_i32(conv_state_indices)),
+              batch, dim, _act(activation), int(pad_slot_id), _lib.stream_of(x))
+    return out

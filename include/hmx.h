@@ -300,6 +300,49 @@ int hmx_rms_norm_gated(const void* x, int64_t x_row_stride, const void* z,
                        int32_t weight_dtype, void* out, int64_t out_row_stride, int64_t rows,
                        int32_t D, float eps, int32_t norm_before_gate, void* stream);
 
+/*
+ * Short causal depthwise conv1d, prefill over concatenated sequences:
+ *   out[t, c] = act(bias[c] + sum_i weight[c, i] x[t - (width-1) + i, c])
+ * act = silu (activation 1) or none (0); width in 2..4.  x / out [total_tokens, dim]
+ * rows (element token strides, channels contiguous, 16-byte aligned), sequence b =
+ * tokens [query_start_loc[b], query_start_loc[b+1]), total_tokens ==
+ * query_start_loc[batch].  Positions before a sequence's first token read its conv
+ * state (when conv_states is not NULL and has_initial_state[b] != 0, or
+ * has_initial_state is NULL), zeros otherwise; afterwards the state holds the
+ * sequence's last state_len inputs.  conv_states [slots, state_len, dim] in x's dtype
+ * (element slot / row strides), slot cache_indices[b] (or b), skipped (output 0)
+ * when equal to pad_slot_id; state_len in [width-1, 8].  weight [dim, width] and bias
+ * [dim] (or NULL) in their dtypes.
+ * Replaces: causal_conv1d_fn (vLLM, un-vendored; called at
+ *   vllm-inference/src/primed_vllm/primed_gdn_layer.py:747-757, :763-773; torch form
+ *   training/.../qwen3_5_moe_hmf/modeling_qwen3_5_moe_hmf.py:306-321).
+ */
+int hmx_causal_conv1d_fwd(const void* x, int64_t x_token_stride, void* out,
+                          int64_t out_token_stride, int32_t dtype, const void* weight,
+                          int32_t weight_dtype, int32_t width, const void* bias,
+                          int32_t bias_dtype, void* conv_states, int64_t state_slot_stride,
+                          int64_t state_row_stride, int32_t state_len,
+                          const int32_t* query_start_loc, int32_t batch, int64_t total_tokens,
+                          const int32_t* cache_indices, const uint8_t* has_initial_state,
+                          int32_t dim, int32_t activation, int32_t pad_slot_id, void* stream);
+
+/*
+ * Short causal depthwise conv1d, one decode token per sequence: x / out [batch, dim]
+ * rows; the window is the last width-1 rows of conv_state[conv_state_indices[b]]
+ * (or b) followed by x[b]; the state then shifts by one row with x[b] appended.
+ * Padded entries (slot == pad_slot_id) write 0 and leave the pool alone.
+ * Replaces: causal_conv1d_update (vLLM, un-vendored; called at
+ *   vllm-inference/src/primed_vllm/primed_gdn_layer.py:735-743, :775-785), without
+ *   its speculative multi-token form.
+ */
+int hmx_causal_conv1d_update(const void* x, int64_t x_token_stride, void* out,
+                             int64_t out_token_stride, int32_t dtype, const void* weight,
+                             int32_t weight_dtype, int32_t width, const void* bias,
+                             int32_t bias_dtype, void* conv_state, int64_t state_slot_stride,
+                             int64_t state_row_stride, int32_t state_len,
+                             const int32_t* conv_state_indices, int32_t batch, int32_t dim,
+                             int32_t activation, int32_t pad_slot_id, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

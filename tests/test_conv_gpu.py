@@ -1,0 +1,118 @@
+"""GPU parity: hmx.causal_conv1d_fn / causal_conv1d_update (the mixers' short
+causal conv1d) against the CPU oracle.
+
+Covers widths 2-4, bias and none, silu and none, varlen with empty and 1-token
+sequences crossing the 64-token tiles, has_initial_state mixes, pad slots, a
+state with speculative slack rows (state_len > width - 1), a strided x (the
+transposed slice of a fused projection, as the layers pass it), fp32 rows, and T
+decode steps against one prefill.  States hold raw inputs, so they must match
+bit for bit; outputs within the output rounding.
+"""
+import pytest
+import torch
+
+import hmx
+from oracle import conv as ref
+from util import assert_out_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _setup(lens, dim, W, slots, st_len, seed, dt=torch.bfloat16, bias=True):
+    g = torch.Generator().manual_seed(seed)
+    qs = torch.tensor([0] + list(torch.tensor(lens).cumsum(0)), dtype=torch.int32)
+    total = int(qs[-1])
+    x = torch.randn(total, dim, generator=g).to(dt)
+    w = torch.randn(dim, W, generator=g) * 0.5
+    b = torch.randn(dim, generator=g) * 0.1 if bias else None
+    pool = torch.randn(slots, st_len, dim, generator=g).to(dt)
+    return qs, x, w, b, pool, g
+
+
+def _close(out, expect):
+    """fp32 accumulation, one rounding to bf16: the error beyond half an ulp stays
+    at fp32 level; the norm-wise error is bf16 rounding alone (about 1.7e-3)."""
+    assert_out_close(out.cpu(), expect, max_abs_tol=1e-4, rel_tol=4e-3)
+
+
+@pytest.mark.parametrize("W,bias,act", [(4, True, "silu"), (3, False, "silu"), (2, True, None)])
+def test_prefill_varlen(dev, W, bias, act):
+    lens = [130, 0, 1, 64, 7, 200]
+    qs, x, w, b, pool, g = _setup(lens, 1024, W, 9, W - 1, W, bias=bias)
+    idx = torch.tensor([3, 0, 8, 5, -1, 1], dtype=torch.int32)
+    init = torch.tensor([True, True, False, True, True, False])
+    out_r, pool_r = ref.causal_conv1d_varlen(x, w, b, pool, qs, idx, init, act)
+    pool_d = pool.to(dev)
+    d = lambda t: None if t is None else t.to(dev)
+    out = hmx.causal_conv1d_fn(x.to(dev).t(), d(w), d(b), conv_states=pool_d,
+                               query_start_loc=d(qs), cache_indices=d(idx),
+                               has_initial_state=d(init), activation=act)
+    torch.cuda.synchronize()
+    assert out.shape == (1024, x.shape[0])
+    _close(out.t(), out_r)
+    assert torch.equal(pool_d.cpu(), pool_r.to(pool.dtype))
+
+
+def test_prefill_no_state_strided_and_fp32(dev):
+    g = torch.Generator().manual_seed(11)
+    proj = torch.randn(300, 3 * 512, generator=g).bfloat16().to(dev)
+    x = proj[:, 512:1536]                 # a slice of a fused projection
+    w = (torch.randn(1024, 4, generator=g) * 0.5).to(dev)
+    out = hmx.causal_conv1d_fn(x.t(), w, None)
+    torch.cuda.synchronize()
+    o_r, _ = ref.conv_sequence(x.cpu(), None, w.cpu(), None, "silu")
+    _close(out.t(), o_r)
+    xf = torch.randn(90, 256, generator=g)
+    wf = torch.randn(256, 3, generator=g)
+    outf = hmx.causal_conv1d_fn(xf.to(dev).t(), wf.to(dev), None, activation=None)
+    torch.cuda.synchronize()
+    o_r, _ = ref.conv_sequence(xf, None, wf, None, None)
+    assert_out_close(outf.t().cpu(), o_r, max_abs_tol=1e-5, rel_tol=1e-6)
+
+
+@pytest.mark.parametrize("st_len", [3, 5])
+def test_decode_steps_equal_prefill(dev, st_len):
+    """T single-token updates == one prefill (outputs and final state), with a pad
+    entry in the batch and state_len slack rows."""
+    dim, W, T = 512, 4, 9
+    qs, x, w, b, pool, g = _setup([T] * 3, dim, W, 4, st_len, 20 + st_len)
+    xs = x.view(3, T, dim)
+    idx = torch.tensor([2, 0, 3], dtype=torch.int32)
+    pool_d = pool.to(dev)
+    outs = []
+    for t in range(T):
+        bidx = idx.clone()
+        if t == 4:
+            bidx[1] = -1      # a padded entry in one step
+        o = hmx.causal_conv1d_update(xs[:, t].contiguous().to(dev), pool_d, w.to(dev), b.to(dev),
+                                     "silu", conv_state_indices=bidx.to(dev))
+        outs.append(o.cpu())
+        if t == 4:
+            assert torch.equal(o[1].cpu(), torch.zeros(dim, dtype=x.dtype))
+    torch.cuda.synchronize()
+    # sequences 0 and 2 never padded: equal the oracle's prefill from their slots
+    for n in (0, 2):
+        o_r, s_r = ref.conv_sequence(xs[n], pool[idx[n]], w, b, "silu")
+        _close(torch.stack([outs[t][n] for t in range(T)]), o_r)
+        assert torch.equal(pool_d[idx[n]].cpu(), s_r.to(pool.dtype))
+    # the oracle's decode agrees step by step as well (pad skipped at step 4)
+    pool_r = pool.clone().double()
+    for t in range(T):
+        bidx = idx.clone()
+        if t == 4:
+            bidx[1] = -1
+        o_r, pool_r = ref.causal_conv1d_update(xs[:, t], pool_r, w, b, "silu", bidx)
+        _close(outs[t], o_r)
+    assert torch.equal(pool_d.cpu(), pool_r.to(pool.dtype))
+
+
+def test_errors(dev):
+    x = torch.zeros(8, 64, dtype=torch.bfloat16, device=dev)
+    w = torch.zeros(64, 4, device=dev)
+    pool = torch.zeros(2, 3, 64, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(NotImplementedError):
+        hmx.causal_conv1d_update(x, pool, w, num_accepted_tokens=torch.ones(8, device=dev))
+    with pytest.raises(NotImplementedError):
+        hmx.causal_conv1d_fn(x.t(), torch.zeros(64, 5, device=dev))    # width 5
+    with pytest.raises(ValueError):
+        hmx.causal_conv1d_fn(x.t(), torch.zeros(32, 4, device=dev))    # weight/dim mismatch
