@@ -13,7 +13,7 @@ reported under ``gka`` against the bf16 MFMA roofline; the Mamba2 SSD chunk scan
 at C4 under ``ssd`` and its single-token state update under ``ssd_decode``, both
 against HBM.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only prefill|decode|gka|ssd]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only prefill|decode|gka|ssd|onorm|conv]
 """
 from __future__ import annotations
 
@@ -97,6 +97,35 @@ def bench_onorm(dev, steps, warmup):
     norm_bytes = 3 * T * H * D * 2   # o, z read; out written (bf16)
     return dict(ms_norm=ms_norm, ms_unfused=ms_unf, ms_fused=ms_fus, norm_bytes=norm_bytes,
                 norm_GBps=norm_bytes / (ms_norm * 1e-3) / 1e9)
+
+
+def bench_conv(dev, steps, warmup):
+    """The GDN layer's input conv at the C1 shape: causal_conv1d_fn over q|k|v
+    (dim 3*32*128 = 12288, width 4, silu) for 8 sequences x 4096 tokens with a
+    state pool, and causal_conv1d_update for 256 sequences x 1 token."""
+    import torch
+    import hmx
+    from hmx import workloads as wl
+    T, dim, W, nseq, st_len = 32768, 3 * 32 * 128, 4, 8, 3
+    g = torch.Generator(device=dev).manual_seed(wl.SEED_BASE + 7)
+    x = torch.randn(T, dim, generator=g, device=dev).bfloat16()
+    w = torch.randn(dim, W, generator=g, device=dev) * 0.5
+    b = torch.randn(dim, generator=g, device=dev) * 0.1
+    pool = torch.randn(nseq, st_len, dim, generator=g, device=dev).bfloat16()
+    qs = torch.arange(0, T + 1, T // nseq, dtype=torch.int32, device=dev)
+    init = torch.ones(nseq, dtype=torch.bool, device=dev)
+    ms_fwd = _timed(lambda: hmx.causal_conv1d_fn(x.t(), w, b, conv_states=pool, query_start_loc=qs,
+                                                 has_initial_state=init), steps, warmup)
+    fwd_bytes = 2 * T * dim * 2 + 2 * nseq * st_len * dim * 2   # x read, out written; states
+    N = 256
+    xd = torch.randn(N, dim, generator=g, device=dev).bfloat16()
+    dpool = torch.randn(N, st_len, dim, generator=g, device=dev).bfloat16()
+    idx = torch.randperm(N, device=dev, generator=g).to(torch.int32)
+    ms_dec = _timed(lambda: hmx.causal_conv1d_update(xd, dpool, w, b, "silu",
+                                                     conv_state_indices=idx), 200, 10)
+    dec_bytes = N * dim * 2 * (2 + 2 * st_len)                  # x, out; state read + written
+    return dict(ms_fwd=ms_fwd, fwd_bytes=fwd_bytes, fwd_GBps=fwd_bytes / (ms_fwd * 1e-3) / 1e9,
+                ms_dec=ms_dec, dec_bytes=dec_bytes, dec_GBps=dec_bytes / (ms_dec * 1e-3) / 1e9)
 
 
 def bench_decode(dev, steps_total=512, warmup=8):
@@ -239,7 +268,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "decode", "gka", "ssd", "onorm"], default=None)
+    ap.add_argument("--only", choices=["prefill", "decode", "gka", "ssd", "onorm", "conv"], default=None)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (HBM counter calibration)")
     a = ap.parse_args()
@@ -259,6 +288,8 @@ def main():
         out["prefill"] = pf
     if a.only in (None, "onorm"):
         out["onorm"] = bench_onorm(dev, a.steps, a.warmup)
+    if a.only in (None, "conv"):
+        out["conv"] = bench_conv(dev, a.steps, a.warmup)
     if a.only in (None, "decode"):
         out["decode"] = bench_decode(dev)
     if a.only in (None, "gka"):
@@ -318,6 +349,24 @@ def main():
                               "peak": HBM_PEAK_GBS, "unit": "GB/s",
                               "frac": round(r["norm_GBps"] / HBM_PEAK_GBS, 4),
                               "algorithmic_bytes": r["norm_bytes"], "traffic": None},
+        }
+    if "conv" in out:
+        r = out["conv"]
+        line["conv1d"] = {
+            "config": {"workload": "GDN input conv (causal_conv1d_fn / causal_conv1d_update), "
+                                   "q|k|v dim 12288, width 4, silu, bf16",
+                       "prefill": "8 seqs x 4096 tokens, state pool [8,3,12288]",
+                       "decode": "256 seqs x 1 token, pool [256,3,12288] randperm slots"},
+            "prefill_ms": round(r["ms_fwd"], 4),
+            "prefill_roofline": {"bound": "hbm", "achieved": round(r["fwd_GBps"], 1),
+                                 "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                 "frac": round(r["fwd_GBps"] / HBM_PEAK_GBS, 4),
+                                 "algorithmic_bytes": r["fwd_bytes"], "traffic": None},
+            "decode_ms": round(r["ms_dec"], 4),
+            "decode_roofline": {"bound": "hbm", "achieved": round(r["dec_GBps"], 1),
+                                "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                "frac": round(r["dec_GBps"] / HBM_PEAK_GBS, 4),
+                                "algorithmic_bytes": r["dec_bytes"], "traffic": None},
         }
     if "gka" in out:
         line["gka"] = {}

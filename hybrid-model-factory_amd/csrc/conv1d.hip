@@ -13,7 +13,8 @@
 //
 // Layout: a thread owns 8 consecutive channels (one 16-byte vector of a bf16 row)
 // and walks a tile of tokens with the last W-1 inputs in registers; rows of x are
-// read once.  The prefill writes the new states in a second launch, after every
+// read once.  Width and activation are template parameters so every register
+// array is indexed at compile time (no scratch).  The prefill writes the new states in a second launch, after every
 // tile has read the old ones (a sequence's first tile reads its slot while its last
 // tile would write it).  HBM-bound: x read once, out written once.
 #include "common.hpp"
@@ -22,54 +23,107 @@ namespace hmx {
 namespace conv {
 
 constexpr int TT = 64;         // tokens per prefill tile
+constexpr int U = 8;           // rows loaded ahead per thread (memory-level parallelism)
 constexpr int NT = 256;        // threads per workgroup (2048 channels)
 
-__device__ __forceinline__ float ld_any(const void* p, int64_t i, int dt) {
-  if (dt == HMX_F32) return static_cast<const float*>(p)[i];
-  if (dt == HMX_BF16) return (float)static_cast<const bf16*>(p)[i];
-  return (float)static_cast<const f16*>(p)[i];
+// 8 consecutive channels: one 16-byte load for 16-bit rows, two for fp32
+template <typename T>
+__device__ __forceinline__ void ld8(const T* __restrict__ p, float (&o)[8]) {
+  if constexpr (sizeof(T) == 4) {
+    load_vec<8>(p, o);
+  } else {
+    typedef T T8 __attribute__((ext_vector_type(8)));
+    const T8 v = *reinterpret_cast<const T8*>(p);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = to_f32(v[j]);
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void st8(T* __restrict__ p, const float (&y)[8]) {
+  if constexpr (sizeof(T) == 4) {
+    store_vec<8>(p, y);
+  } else {
+    typedef T T8 __attribute__((ext_vector_type(8)));
+    T8 v;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = from_f32<T>(y[j]);
+    *reinterpret_cast<T8*>(p) = v;
+  }
 }
 
 struct Params {
   const void* x; int64_t xs;          // [tokens, dim] rows
   void* out; int64_t os;
-  const void* w; int w_dt; int W;     // [dim, W]
+  const void* w; int w_dt;            // [dim, W]
   const void* bias; int b_dt;         // [dim] or null
   void* st; int64_t st_slot, st_row; int st_len;   // [slots, st_len, dim] or null
   const int32_t* qs; int batch; int64_t total;
   const int32_t* idx;                 // slot per sequence, or null (slot = sequence)
   const uint8_t* has_init;            // per sequence, or null (all true)
-  int dim, act, pad;
+  int dim, pad;
 };
 
-template <typename T>
+// Taps of 8 channels; the window holds the W-1 inputs before the current one
+// (win[0] oldest), so tap i < W-1 reads win[i] and tap W-1 the current input.
+template <int W, bool ACT>
 struct Taps {
-  float w[4][8], b[8];
-  __device__ __forceinline__ void load(const Params& p, int c0) {
+  float w[W][8], b[8];
+  // The 8W weights of channels c0..c0+7 are contiguous ([dim, W] rows): vector
+  // loads of one dtype branch, all in flight together.
+  template <typename WT>
+  __device__ __forceinline__ void load_t(const Params& p, int c0) {
+    float f[8 * W];
+    const WT* wp = static_cast<const WT*>(p.w) + (int64_t)c0 * W;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int k = 0; k < W; ++k) {
+      float v[8];
+      ld8(wp + 8 * k, v);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) w[i][j] = i < p.W ? ld_any(p.w, (int64_t)(c0 + j) * p.W + i, p.w_dt) : 0.f;
-      b[j] = p.bias ? ld_any(p.bias, c0 + j, p.b_dt) : 0.f;
+      for (int j = 0; j < 8; ++j) f[8 * k + j] = v[j];
     }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int i = 0; i < W; ++i) w[i][j] = f[j * W + i];
   }
-  // window[0..2] = inputs at t-3..t-1 (taps shifted so tap W-1 is the current input)
-  __device__ __forceinline__ void apply(const float (&win)[3][8], const float (&xt)[8], int W,
-                                        int act, float (&y)[8]) const {
+  template <typename BT>
+  __device__ __forceinline__ void load_b(const Params& p, int c0) {
+    ld8(static_cast<const BT*>(p.bias) + c0, b);
+  }
+  __device__ __forceinline__ void load(const Params& p, int c0) {
+    if (p.w_dt == HMX_F32) load_t<float>(p, c0);
+    else if (p.w_dt == HMX_BF16) load_t<bf16>(p, c0);
+    else load_t<f16>(p, c0);
+    if (!p.bias) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) b[j] = 0.f;
+    } else if (p.b_dt == HMX_F32) load_b<float>(p, c0);
+    else if (p.b_dt == HMX_BF16) load_b<bf16>(p, c0);
+    else load_b<f16>(p, c0);
+  }
+  __device__ __forceinline__ void apply(const float (&win)[W - 1][8], const float (&xt)[8],
+                                        float (&y)[8]) const {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       float a = b[j];
-      // tap i reads t - (W-1) + i: the window row 3 - (W-1) + i for i < W-1, x_t for i = W-1
 #pragma unroll
-      for (int i = 0; i < 3; ++i) {
-        const int r = 3 - (W - 1) + i;
-        if (i < W - 1) a += w[i][j] * win[r][j];
-      }
+      for (int i = 0; i < W - 1; ++i) a += w[i][j] * win[i][j];
       a += w[W - 1][j] * xt[j];
-      y[j] = act ? a / (1.0f + fast_exp(-a)) : a;
+      y[j] = ACT ? a * __builtin_amdgcn_rcpf(1.0f + fast_exp(-a)) : a;
     }
   }
 };
+
+template <int W>
+__device__ __forceinline__ void shift_in(float (&win)[W - 1][8], const float (&xt)[8]) {
+#pragma unroll
+  for (int i = 0; i + 1 < W - 1; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) win[i][j] = win[i + 1][j];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) win[W - 2][j] = xt[j];
+}
 
 // sequence of token t: largest b with qs[b] <= t (non-empty sequences only)
 __device__ __forceinline__ int seq_of(const int32_t* qs, int batch, int64_t t) {
@@ -81,7 +135,6 @@ __device__ __forceinline__ int seq_of(const int32_t* qs, int batch, int64_t t) {
   return lo;
 }
 
-template <typename T>
 __device__ __forceinline__ bool seq_slot(const Params& p, int b, int64_t& slot, bool& init) {
   slot = p.idx ? p.idx[b] : b;
   const bool ok = slot != p.pad;
@@ -91,60 +144,70 @@ __device__ __forceinline__ bool seq_slot(const Params& p, int b, int64_t& slot, 
 
 // The W-1 inputs before token t of sequence b (starting at token s): from x, or
 // from the state rows (init), or zeros.
-template <typename T>
+template <typename T, int W>
 __device__ __forceinline__ void load_window(const Params& p, int64_t t, int64_t s, int64_t slot,
-                                            bool init, int c0, float (&win)[3][8]) {
+                                            bool init, int c0, float (&win)[W - 1][8]) {
 #pragma unroll
-  for (int r = 0; r < 3; ++r) {
-    const int64_t pos = t - 3 + r;   // window row r holds position t - 3 + r
+  for (int r = 0; r < W - 1; ++r) {
+    const int64_t pos = t - (W - 1) + r;   // window row r holds position t - (W-1) + r
 #pragma unroll
     for (int j = 0; j < 8; ++j) win[r][j] = 0.f;
     if (pos >= s) {
-      load_vec<8>(static_cast<const T*>(p.x) + pos * p.xs + c0, win[r]);
+      ld8(static_cast<const T*>(p.x) + pos * p.xs + c0, win[r]);
     } else if (init) {
       const int64_t row = p.st_len + (pos - s);   // state row of position pos (< 0 -> none)
-      if (row >= 0)
-        load_vec<8>(static_cast<const T*>(p.st) + slot * p.st_slot + row * p.st_row + c0, win[r]);
+      if (row >= 0) ld8(static_cast<const T*>(p.st) + slot * p.st_slot + row * p.st_row + c0, win[r]);
     }
   }
 }
 
-template <typename T>
+// Prefill: a workgroup owns TT tokens x 2048 channels; each thread walks its 8
+// channels through the tile, loading U rows ahead before computing them.  Token
+// and sequence indices are uniform across the workgroup, so the sequence-boundary
+// branch is scalar.
+template <typename T, int W, bool ACT>
 __global__ __launch_bounds__(NT) void conv_fwd_kernel(Params p) {
   const int c0 = (blockIdx.y * NT + threadIdx.x) * 8;
   if (c0 >= p.dim) return;
   const int64_t t0 = (int64_t)blockIdx.x * TT;
   const int64_t t1 = min(t0 + TT, p.total);
-  Taps<T> tp;
+  Taps<W, ACT> tp;
   tp.load(p, c0);
   int b = seq_of(p.qs, p.batch, t0);
   int64_t s = p.qs[b], e = p.qs[b + 1];
   int64_t slot;
   bool init;
-  bool ok = seq_slot<T>(p, b, slot, init);
-  float win[3][8];
-  load_window<T>(p, t0, s, slot, init, c0, win);
-  for (int64_t t = t0; t < t1; ++t) {
-    if (t >= e) {   // next non-empty sequence starts at t
-      while (p.qs[b + 1] <= t) ++b;
-      s = p.qs[b];
-      e = p.qs[b + 1];
-      ok = seq_slot<T>(p, b, slot, init);
-      load_window<T>(p, t, s, slot, init, c0, win);
-    }
-    float xt[8], y[8];
-    load_vec<8>(static_cast<const T*>(p.x) + t * p.xs + c0, xt);
-    tp.apply(win, xt, p.W, p.act, y);
-    if (!ok) {
+  bool ok = seq_slot(p, b, slot, init);
+  float win[W - 1][8];
+  load_window<T, W>(p, t0, s, slot, init, c0, win);
+  const T* __restrict__ xp = static_cast<const T*>(p.x) + c0;
+  T* __restrict__ op = static_cast<T*>(p.out) + c0;
+  for (int64_t tb = t0; tb < t1; tb += U) {
+    // unconditional loads (rows past the tile end re-read its last row, unused) so
+    // all U are in flight before the first is converted
+    float xt[U][8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) y[j] = 0.f;
-    }
-    store_vec<8>(static_cast<T*>(p.out) + t * p.os + c0, y);
+    for (int u = 0; u < U; ++u) ld8(xp + min(tb + u, t1 - 1) * p.xs, xt[u]);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      win[0][j] = win[1][j];
-      win[1][j] = win[2][j];
-      win[2][j] = xt[j];
+    for (int u = 0; u < U; ++u) {
+      const int64_t t = tb + u;
+      if (t < t1) {
+        if (t >= e) {   // next non-empty sequence starts at t
+          while (p.qs[b + 1] <= t) ++b;
+          s = p.qs[b];
+          e = p.qs[b + 1];
+          ok = seq_slot(p, b, slot, init);
+          load_window<T, W>(p, t, s, slot, init, c0, win);
+        }
+        float y[8];
+        tp.apply(win, xt[u], y);
+        if (!ok) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) y[j] = 0.f;
+        }
+        st8(op + t * p.os, y);
+        shift_in<W>(win, xt[u]);
+      }
     }
   }
 }
@@ -159,28 +222,32 @@ __global__ __launch_bounds__(NT) void conv_state_kernel(Params p) {
   if (c0 >= p.dim) return;
   int64_t slot;
   bool init;
-  if (!seq_slot<T>(p, b, slot, init)) return;
-  const int64_t s = p.qs[b], e = p.qs[b + 1], len = e - s;
-  if (len == 0) return;   // an empty sequence keeps its state
+  if (!seq_slot(p, b, slot, init)) return;
+  const int64_t s = p.qs[b], e = p.qs[b + 1];
+  if (e == s) return;     // an empty sequence keeps its state
   float rows[8][8];       // st_len <= 8
-  for (int r = 0; r < p.st_len; ++r) {
-    const int64_t pos = e - p.st_len + r;   // sequence position of new state row r
 #pragma unroll
-    for (int j = 0; j < 8; ++j) rows[r & 7][j] = 0.f;
-    if (pos >= s) {
-      load_vec<8>(static_cast<const T*>(p.x) + pos * p.xs + c0, rows[r & 7]);
-    } else if (init) {
-      const int64_t row = p.st_len + (pos - s);
-      if (row >= 0)
-        load_vec<8>(static_cast<const T*>(p.st) + slot * p.st_slot + row * p.st_row + c0, rows[r & 7]);
+  for (int r = 0; r < 8; ++r) {
+    if (r < p.st_len) {
+      const int64_t pos = e - p.st_len + r;   // sequence position of new state row r
+#pragma unroll
+      for (int j = 0; j < 8; ++j) rows[r][j] = 0.f;
+      if (pos >= s) {
+        ld8(static_cast<const T*>(p.x) + pos * p.xs + c0, rows[r]);
+      } else if (init) {
+        const int64_t row = p.st_len + (pos - s);
+        if (row >= 0) ld8(static_cast<const T*>(p.st) + slot * p.st_slot + row * p.st_row + c0, rows[r]);
+      }
     }
   }
-  for (int r = 0; r < p.st_len; ++r)
-    store_vec<8>(static_cast<T*>(p.st) + slot * p.st_slot + r * p.st_row + c0, rows[r & 7]);
+  T* srow = static_cast<T*>(p.st) + slot * p.st_slot + c0;
+#pragma unroll
+  for (int r = 0; r < 8; ++r)
+    if (r < p.st_len) st8(srow + r * p.st_row, rows[r]);
 }
 
 // Decode: one token per sequence against its slot; the state shifts by one row.
-template <typename T>
+template <typename T, int W, bool ACT>
 __global__ __launch_bounds__(NT) void conv_update_kernel(Params p) {
   const int c0 = (blockIdx.y * NT + threadIdx.x) * 8;
   const int b = blockIdx.x;
@@ -189,45 +256,71 @@ __global__ __launch_bounds__(NT) void conv_update_kernel(Params p) {
   T* orow = static_cast<T*>(p.out) + (int64_t)b * p.os + c0;
   if (slot == p.pad) {   // padded entry: zero output, no state access
     const float zero[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    store_vec<8>(orow, zero);
+    st8(orow, zero);
     return;
   }
-  Taps<T> tp;
-  tp.load(p, c0);
   T* srow = static_cast<T*>(p.st) + slot * p.st_slot + c0;
-  float rows[8][8];   // st_len <= 8
-  for (int r = 0; r < p.st_len; ++r) load_vec<8>(srow + r * p.st_row, rows[r & 7]);
-  float win[3][8], xt[8], y[8];
+  const int L = p.st_len;
+  float xt[8], win[W - 1][8], y[8];
+  ld8(static_cast<const T*>(p.x) + (int64_t)b * p.xs + c0, xt);
 #pragma unroll
-  for (int r = 0; r < 3; ++r) {
-    const int sr = p.st_len - 3 + r;   // window row r = state row st_len - 3 + r
+  for (int i = 0; i < W - 1; ++i) ld8(srow + (int64_t)(L - (W - 1) + i) * p.st_row, win[i]);
+  float rows[8][8];      // rows 1 .. L-1 of a state longer than the window
+  const bool slack = L > W - 1;
+  if (slack) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) win[r][j] = sr >= 0 ? rows[sr & 7][j] : 0.f;
+    for (int r = 1; r < 8; ++r)
+      if (r < L - (W - 1)) ld8(srow + r * p.st_row, rows[r]);
   }
-  load_vec<8>(static_cast<const T*>(p.x) + (int64_t)b * p.xs + c0, xt);
-  tp.apply(win, xt, p.W, p.act, y);
-  store_vec<8>(orow, y);
-  for (int r = 0; r + 1 < p.st_len; ++r) store_vec<8>(srow + r * p.st_row, rows[(r + 1) & 7]);
-  store_vec<8>(srow + (int64_t)(p.st_len - 1) * p.st_row, xt);
+  Taps<W, ACT> tp;
+  tp.load(p, c0);
+  tp.apply(win, xt, y);
+  st8(orow, y);
+  // shift: row r <- row r+1; the window rows are the last W-1 rows
+  if (slack) {
+#pragma unroll
+    for (int r = 0; r + 1 < 8; ++r)
+      if (r + 1 < L - (W - 1)) st8(srow + r * p.st_row, rows[r + 1]);
+  }
+#pragma unroll
+  for (int i = 0; i < W - 1; ++i) {
+    const int r = L - (W - 1) + i - 1;       // destination of window row i
+    if (r >= 0) st8(srow + (int64_t)r * p.st_row, win[i]);
+  }
+  st8(srow + (int64_t)(L - 1) * p.st_row, xt);
 }
 
-template <typename T>
-void launch_fwd(const Params& p, hipStream_t s) {
+template <typename T, int W, bool ACT>
+void launch_fwd_w(const Params& p, hipStream_t s) {
   const unsigned cg = (unsigned)((p.dim / 8 + NT - 1) / NT);
   if (p.total > 0)
-    hipLaunchKernelGGL(conv_fwd_kernel<T>, dim3((unsigned)((p.total + TT - 1) / TT), cg),
+    hipLaunchKernelGGL((conv_fwd_kernel<T, W, ACT>), dim3((unsigned)((p.total + TT - 1) / TT), cg),
                        dim3(NT), 0, s, p);
   if (p.st && p.batch > 0)
     hipLaunchKernelGGL(conv_state_kernel<T>, dim3((unsigned)p.batch, cg), dim3(NT), 0, s, p);
 }
 
-template <typename T>
-void launch_update(const Params& p, hipStream_t s) {
+template <typename T, int W, bool ACT>
+void launch_update_w(const Params& p, hipStream_t s) {
   const unsigned cg = (unsigned)((p.dim / 8 + NT - 1) / NT);
-  hipLaunchKernelGGL(conv_update_kernel<T>, dim3((unsigned)p.batch, cg), dim3(NT), 0, s, p);
+  hipLaunchKernelGGL((conv_update_kernel<T, W, ACT>), dim3((unsigned)p.batch, cg), dim3(NT), 0, s,
+                     p);
 }
 
-int check_common(const char* fn, int32_t dtype, int32_t width, int32_t dim, int32_t state_len,
+template <typename T, bool UPDATE>
+void dispatch(const Params& p, int W, int act, hipStream_t s) {
+#define HMX_CONV_CASE(WW, AA)                                            \
+  if (W == WW && (act != 0) == AA) {                                      \
+    if (UPDATE) launch_update_w<T, WW, AA>(p, s); else launch_fwd_w<T, WW, AA>(p, s); \
+    return;                                                               \
+  }
+  HMX_CONV_CASE(2, false) HMX_CONV_CASE(2, true) HMX_CONV_CASE(3, false)
+  HMX_CONV_CASE(3, true) HMX_CONV_CASE(4, false) HMX_CONV_CASE(4, true)
+#undef HMX_CONV_CASE
+}
+
+int check_common(const char* fn, const void* x, const void* out, const void* weight,
+                 int32_t dtype, int32_t width, int32_t dim, int32_t state_len,
                  int32_t weight_dtype, const void* bias, int32_t bias_dtype, int64_t xs,
                  int64_t os, int64_t st_row, int64_t st_slot, const void* st) {
   HMX_REQUIRE(dtype >= 0 && dtype <= 2, HMX_EUNSUPPORTED, "%s: dtype code %d", fn, dtype);
@@ -242,6 +335,10 @@ int check_common(const char* fn, int32_t dtype, int32_t width, int32_t dim, int3
               HMX_EINVAL, "%s: token / state strides must be multiples of 16 bytes", fn);
   HMX_REQUIRE(!st || (state_len >= width - 1 && state_len <= 8), HMX_EUNSUPPORTED,
               "%s: state_len %d must be in [width-1, 8]", fn, state_len);
+  const uintptr_t any = (uintptr_t)x | (uintptr_t)out | (uintptr_t)weight | (uintptr_t)bias |
+                        (uintptr_t)st;
+  HMX_REQUIRE(any % 16 == 0, HMX_EINVAL,
+              "%s: x, out, weight, bias and state pointers must be 16-byte aligned", fn);
   return HMX_OK;
 }
 
@@ -262,22 +359,22 @@ extern "C" int hmx_causal_conv1d_fwd(const void* x, int64_t x_token_stride, void
                                      const uint8_t* has_initial_state, int32_t dim,
                                      int32_t activation, int32_t pad_slot_id, void* stream) {
   // total_tokens must equal query_start_loc[batch] (the kernels walk sequences up to it)
-  const int rc = check_common("hmx_causal_conv1d_fwd", dtype, width, dim, state_len, weight_dtype,
-                              bias, bias_dtype, x_token_stride, out_token_stride, state_row_stride,
-                              state_slot_stride, conv_states);
+  const int rc = check_common("hmx_causal_conv1d_fwd", x, out, weight, dtype, width, dim,
+                              state_len, weight_dtype, bias, bias_dtype, x_token_stride,
+                              out_token_stride, state_row_stride, state_slot_stride, conv_states);
   if (rc != HMX_OK) return rc;
   HMX_REQUIRE(batch >= 0 && total_tokens >= 0, HMX_EINVAL, "hmx_causal_conv1d_fwd: sizes");
   if (batch == 0 || total_tokens == 0) return HMX_OK;
   HMX_REQUIRE(x && out && weight && query_start_loc, HMX_EINVAL,
               "hmx_causal_conv1d_fwd: null pointer");
-  Params p{x, x_token_stride, out, out_token_stride, weight, weight_dtype, width, bias,
-           bias_dtype, conv_states, state_slot_stride, state_row_stride,
+  Params p{x, x_token_stride, out, out_token_stride, weight, weight_dtype, bias, bias_dtype,
+           conv_states, state_slot_stride, state_row_stride,
            conv_states ? state_len : width - 1, query_start_loc, batch, total_tokens,
-           cache_indices, has_initial_state, dim, activation, pad_slot_id};
+           cache_indices, has_initial_state, dim, pad_slot_id};
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == HMX_BF16) launch_fwd<bf16>(p, s);
-  else if (dtype == HMX_F16) launch_fwd<f16>(p, s);
-  else launch_fwd<float>(p, s);
+  if (dtype == HMX_BF16) dispatch<bf16, false>(p, width, activation, s);
+  else if (dtype == HMX_F16) dispatch<f16, false>(p, width, activation, s);
+  else dispatch<float, false>(p, width, activation, s);
   return check_launch("hmx_causal_conv1d_fwd");
 }
 
@@ -289,20 +386,20 @@ extern "C" int hmx_causal_conv1d_update(const void* x, int64_t x_token_stride, v
                                         int32_t state_len, const int32_t* conv_state_indices,
                                         int32_t batch, int32_t dim, int32_t activation,
                                         int32_t pad_slot_id, void* stream) {
-  const int rc = check_common("hmx_causal_conv1d_update", dtype, width, dim, state_len,
-                              weight_dtype, bias, bias_dtype, x_token_stride, out_token_stride,
-                              state_row_stride, state_slot_stride, conv_state);
+  const int rc = check_common("hmx_causal_conv1d_update", x, out, weight, dtype, width, dim,
+                              state_len, weight_dtype, bias, bias_dtype, x_token_stride,
+                              out_token_stride, state_row_stride, state_slot_stride, conv_state);
   if (rc != HMX_OK) return rc;
   HMX_REQUIRE(batch >= 0, HMX_EINVAL, "hmx_causal_conv1d_update: batch %d", batch);
   if (batch == 0) return HMX_OK;
   HMX_REQUIRE(x && out && weight && conv_state, HMX_EINVAL,
               "hmx_causal_conv1d_update: null pointer");
-  Params p{x, x_token_stride, out, out_token_stride, weight, weight_dtype, width, bias,
-           bias_dtype, conv_state, state_slot_stride, state_row_stride, state_len, nullptr,
-           batch, batch, conv_state_indices, nullptr, dim, activation, pad_slot_id};
+  Params p{x, x_token_stride, out, out_token_stride, weight, weight_dtype, bias, bias_dtype,
+           conv_state, state_slot_stride, state_row_stride, state_len, nullptr, batch, batch,
+           conv_state_indices, nullptr, dim, pad_slot_id};
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == HMX_BF16) launch_update<bf16>(p, s);
-  else if (dtype == HMX_F16) launch_update<f16>(p, s);
-  else launch_update<float>(p, s);
+  if (dtype == HMX_BF16) dispatch<bf16, true>(p, width, activation, s);
+  else if (dtype == HMX_F16) dispatch<f16, true>(p, width, activation, s);
+  else dispatch<float, true>(p, width, activation, s);
   return check_launch("hmx_causal_conv1d_update");
 }

@@ -37,6 +37,14 @@ def _rows(t: torch.Tensor) -> torch.Tensor:
     return t
 
 
+def _aligned(t):
+    """Contiguous with a 16-byte aligned start (the kernels load 16-byte vectors)."""
+    if t is None:
+        return None
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
 def _i32(t):
     return None if t is None else t.to(torch.int32).contiguous()
 
@@ -79,8 +87,7 @@ def causal_conv1d_fn(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor |
                              f"channels contiguous, got {tuple(conv_states.shape)} {conv_states.dtype}")
         st_len, sst, srs = conv_states.shape[1], conv_states.stride(0), conv_states.stride(1)
     hinit = None if has_initial_state is None else has_initial_state.to(torch.uint8).contiguous()
-    w = weight.contiguous()
-    b = None if bias is None else bias.contiguous()
+    w, b = _aligned(weight), _aligned(bias)
     _lib.call("hmx_causal_conv1d_fwd", _lib.ptr(xr), xr.stride(0), _lib.ptr(out), out.stride(0),
               _lib.dtype_code(x), _lib.ptr(w), _lib.dtype_code(w), W, _lib.ptr(b),
               0 if b is None else _lib.dtype_code(b), _lib.ptr(conv_states), sst, srs, st_len,
@@ -113,8 +120,7 @@ def causal_conv1d_update(x: torch.Tensor, conv_state: torch.Tensor, weight: torc
                          f"contiguous, got {tuple(conv_state.shape)} {conv_state.dtype}")
     xr = _rows(x)
     out = torch.empty(batch, dim, dtype=x.dtype, device=x.device)
-    w = weight.contiguous()
-    b = None if bias is None else bias.contiguous()
+    w, b = _aligned(weight), _aligned(bias)
     _lib.call("hmx_causal_conv1d_update", _lib.ptr(xr), xr.stride(0), _lib.ptr(out), out.stride(0),
               _lib.dtype_code(x), _lib.ptr(w), _lib.dtype_code(w), W, _lib.ptr(b),
               0 if b is None else _lib.dtype_code(b), _lib.ptr(conv_state), conv_state.stride(0),
