@@ -114,12 +114,13 @@ def bench_conv(dev, steps, warmup):
     pool = torch.randn(nseq, st_len, dim, generator=g, device=dev).bfloat16()
     qs = torch.arange(0, T + 1, T // nseq, dtype=torch.int32, device=dev)
     init = torch.ones(nseq, dtype=torch.bool, device=dev)
+    pool = pool.transpose(1, 2)        # the layers pass the [slots, dim, state_len] view
     ms_fwd = _timed(lambda: hmx.causal_conv1d_fn(x.t(), w, b, conv_states=pool, query_start_loc=qs,
                                                  has_initial_state=init), steps, warmup)
     fwd_bytes = 2 * T * dim * 2 + 2 * nseq * st_len * dim * 2   # x read, out written; states
     N = 256
     xd = torch.randn(N, dim, generator=g, device=dev).bfloat16()
-    dpool = torch.randn(N, st_len, dim, generator=g, device=dev).bfloat16()
+    dpool = torch.randn(N, st_len, dim, generator=g, device=dev).bfloat16().transpose(1, 2)
     idx = torch.randperm(N, device=dev, generator=g).to(torch.int32)
     ms_dec = _timed(lambda: hmx.causal_conv1d_update(xd, dpool, w, b, "silu",
                                                      conv_state_indices=idx), 200, 10)
@@ -355,8 +356,9 @@ def main():
         line["conv1d"] = {
             "config": {"workload": "GDN input conv (causal_conv1d_fn / causal_conv1d_update), "
                                    "q|k|v dim 12288, width 4, silu, bf16",
-                       "prefill": "8 seqs x 4096 tokens, state pool [8,3,12288]",
-                       "decode": "256 seqs x 1 token, pool [256,3,12288] randperm slots"},
+                       "prefill": "8 seqs x 4096 tokens, state cache [8,3,12288] "
+                                  "(passed as its [8,12288,3] view)",
+                       "decode": "256 seqs x 1 token, cache [256,3,12288] randperm slots"},
             "prefill_ms": round(r["ms_fwd"], 4),
             "prefill_roofline": {"bound": "hbm", "achieved": round(r["fwd_GBps"], 1),
                                  "peak": HBM_PEAK_GBS, "unit": "GB/s",

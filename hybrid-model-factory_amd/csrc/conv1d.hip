@@ -125,6 +125,14 @@ __device__ __forceinline__ void shift_in(float (&win)[W - 1][8], const float (&x
   for (int j = 0; j < 8; ++j) win[W - 2][j] = xt[j];
 }
 
+// Token range [s, e) of sequence b, clamped to [0, total) so that a malformed
+// query_start_loc (not checked on the host, which would need a device sync) cannot
+// move an access outside x; identity for a well-formed one.
+__device__ __forceinline__ void seq_range(const Params& p, int b, int64_t& s, int64_t& e) {
+  s = min(max((int64_t)p.qs[b], (int64_t)0), p.total);
+  e = min(max((int64_t)p.qs[b + 1], s), p.total);
+}
+
 // sequence of token t: largest b with qs[b] <= t (non-empty sequences only)
 __device__ __forceinline__ int seq_of(const int32_t* qs, int batch, int64_t t) {
   int lo = 0, hi = batch - 1;
@@ -173,13 +181,23 @@ __global__ __launch_bounds__(NT) void conv_fwd_kernel(Params p) {
   const int64_t t1 = min(t0 + TT, p.total);
   Taps<W, ACT> tp;
   tp.load(p, c0);
-  int b = seq_of(p.qs, p.batch, t0);
-  int64_t s = p.qs[b], e = p.qs[b + 1];
-  int64_t slot;
-  bool init;
-  bool ok = seq_slot(p, b, slot, init);
+  // tokens from qs[batch] on belong to no sequence: zero output
+  const int64_t tend = min(max((int64_t)p.qs[p.batch], (int64_t)0), p.total);
+  int b = 0;
+  int64_t s = 0, e = p.total, slot = 0;
+  bool init = false, ok = false;
   float win[W - 1][8];
-  load_window<T, W>(p, t0, s, slot, init, c0, win);
+  if (t0 < tend) {
+    b = seq_of(p.qs, p.batch, t0);
+    seq_range(p, b, s, e);
+    ok = seq_slot(p, b, slot, init);
+    load_window<T, W>(p, t0, s, slot, init, c0, win);
+  } else {
+#pragma unroll
+    for (int r = 0; r < W - 1; ++r)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) win[r][j] = 0.f;
+  }
   const T* __restrict__ xp = static_cast<const T*>(p.x) + c0;
   T* __restrict__ op = static_cast<T*>(p.out) + c0;
   for (int64_t tb = t0; tb < t1; tb += U) {
@@ -192,12 +210,16 @@ __global__ __launch_bounds__(NT) void conv_fwd_kernel(Params p) {
     for (int u = 0; u < U; ++u) {
       const int64_t t = tb + u;
       if (t < t1) {
-        if (t >= e) {   // next non-empty sequence starts at t
-          while (p.qs[b + 1] <= t) ++b;
-          s = p.qs[b];
-          e = p.qs[b + 1];
-          ok = seq_slot(p, b, slot, init);
-          load_window<T, W>(p, t, s, slot, init, c0, win);
+        if (t >= e) {
+          if (t >= tend) {   // past the last sequence
+            ok = false;
+            e = p.total;
+          } else {           // next non-empty sequence starts at t
+            while (b + 1 < p.batch && p.qs[b + 1] <= t) ++b;
+            seq_range(p, b, s, e);
+            ok = seq_slot(p, b, slot, init);
+            load_window<T, W>(p, t, s, slot, init, c0, win);
+          }
         }
         float y[8];
         tp.apply(win, xt[u], y);
@@ -223,7 +245,8 @@ __global__ __launch_bounds__(NT) void conv_state_kernel(Params p) {
   int64_t slot;
   bool init;
   if (!seq_slot(p, b, slot, init)) return;
-  const int64_t s = p.qs[b], e = p.qs[b + 1];
+  int64_t s, e;
+  seq_range(p, b, s, e);
   if (e == s) return;     // an empty sequence keeps its state
   float rows[8][8];       // st_len <= 8
 #pragma unroll
@@ -358,13 +381,12 @@ extern "C" int hmx_causal_conv1d_fwd(const void* x, int64_t x_token_stride, void
                                      const int32_t* cache_indices,
                                      const uint8_t* has_initial_state, int32_t dim,
                                      int32_t activation, int32_t pad_slot_id, void* stream) {
-  // total_tokens must equal query_start_loc[batch] (the kernels walk sequences up to it)
   const int rc = check_common("hmx_causal_conv1d_fwd", x, out, weight, dtype, width, dim,
                               state_len, weight_dtype, bias, bias_dtype, x_token_stride,
                               out_token_stride, state_row_stride, state_slot_stride, conv_states);
   if (rc != HMX_OK) return rc;
   HMX_REQUIRE(batch >= 0 && total_tokens >= 0, HMX_EINVAL, "hmx_causal_conv1d_fwd: sizes");
-  if (batch == 0 || total_tokens == 0) return HMX_OK;
+  if (total_tokens == 0) return HMX_OK;   // batch 0: every token gets output 0
   HMX_REQUIRE(x && out && weight && query_start_loc, HMX_EINVAL,
               "hmx_causal_conv1d_fwd: null pointer");
   Params p{x, x_token_stride, out, out_token_stride, weight, weight_dtype, bias, bias_dtype,

@@ -218,6 +218,49 @@ def _(state, x, dt, A, B, C, D, z, dt_bias, dt_softplus, state_batch_indices,
 
 
 
+# ------------------------------------------------------- conv1d and the output norm
+@torch.library.custom_op("hmx::causal_conv1d_fn", mutates_args=("conv_states",))
+def _conv_fwd(x: Tensor, weight: Tensor, bias: Optional[Tensor], conv_states: Optional[Tensor],
+              query_start_loc: Optional[Tensor], cache_indices: Optional[Tensor],
+              has_initial_state: Optional[Tensor], activation: Optional[str],
+              pad_slot_id: int) -> Tensor:
+    return ops.conv.conv_fwd_rows(x, weight, bias, conv_states, query_start_loc, cache_indices,
+                                  has_initial_state, activation, pad_slot_id)
+
+
+@_conv_fwd.register_fake
+def _(x, weight, bias, conv_states, query_start_loc, cache_indices, has_initial_state, activation,
+      pad_slot_id):
+    return x.new_empty(x.shape[1], x.shape[0])
+
+
+@torch.library.custom_op("hmx::causal_conv1d_update", mutates_args=("conv_state",))
+def _conv_update(x: Tensor, conv_state: Tensor, weight: Tensor, bias: Optional[Tensor],
+                 activation: Optional[str], conv_state_indices: Optional[Tensor],
+                 pad_slot_id: int) -> Tensor:
+    return ops.causal_conv1d_update(x, conv_state, weight, bias, activation, conv_state_indices,
+                                    pad_slot_id=pad_slot_id)
+
+
+@_conv_update.register_fake
+def _(x, conv_state, weight, bias, activation, conv_state_indices, pad_slot_id):
+    return x.new_empty(x.shape)
+
+
+@torch.library.custom_op("hmx::rms_norm_gated", mutates_args=())
+def _norm(x: Tensor, z: Optional[Tensor], weight: Tensor, eps: float,
+          norm_before_gate: bool) -> Tensor:
+    return ops.rms_norm_gated(x, z, weight, eps, norm_before_gate)
+
+
+@_norm.register_fake
+def _(x, z, weight, eps, norm_before_gate):
+    return torch.empty_like(x)
+
+
+_forward_only(_norm, "rms_norm_gated")
+
+
 # ------------------------------------------------------- reference-signature wrappers
 def chunk_gated_delta_rule_gqa(q, k, v, g, beta, scale=None, initial_state=None,
                                output_final_state=False, cu_seqlens=None,
@@ -298,6 +341,44 @@ def selective_state_update(state, x, dt, A, B, C, D=None, z=None, dt_bias=None,
     return out
 
 
+def _act_name(activation):
+    if activation is True:
+        return "silu"
+    return None if activation in (None, False) else activation
+
+
+def causal_conv1d_fn(x, weight, bias=None, conv_states=None, query_start_loc=None,
+                     cache_indices=None, has_initial_state=None, activation="silu",
+                     pad_slot_id=-1, metadata=None, validate_data=False, **block_args):
+    """``torch.ops.hmx.causal_conv1d_fn`` with vLLM's signature (called at
+    primed_gdn_layer.py:747-757); returns the [dim, total] view."""
+    if any(v is not None for v in block_args.values()):
+        raise NotImplementedError("prefix-cache block arguments of causal_conv1d_fn")
+    return torch.ops.hmx.causal_conv1d_fn(x, weight, bias, conv_states, query_start_loc,
+                                          cache_indices, has_initial_state,
+                                          _act_name(activation), int(pad_slot_id)).t()
+
+
+def causal_conv1d_update(x, conv_state, weight, bias=None, activation=None,
+                         conv_state_indices=None, num_accepted_tokens=None, query_start_loc=None,
+                         max_query_len=-1, pad_slot_id=-1, validate_data=False,
+                         block_idx_last_scheduled_token=None, initial_state_idx=None):
+    """``torch.ops.hmx.causal_conv1d_update`` with vLLM's signature (called at
+    primed_gdn_layer.py:775-785); the state pool is updated in place."""
+    if num_accepted_tokens is not None or query_start_loc is not None:
+        raise NotImplementedError("speculative multi-token causal_conv1d_update")
+    if block_idx_last_scheduled_token is not None or initial_state_idx is not None:
+        raise NotImplementedError("prefix-cache block arguments of causal_conv1d_update")
+    return torch.ops.hmx.causal_conv1d_update(x, conv_state, weight, bias, _act_name(activation),
+                                              conv_state_indices, int(pad_slot_id))
+
+
+def rms_norm_gated(x, z, weight, eps=1e-5, norm_before_gate=True):
+    """``torch.ops.hmx.rms_norm_gated``: the layers' output norm ``o_norm(o, z)``."""
+    return torch.ops.hmx.rms_norm_gated(x, z, weight, float(eps), bool(norm_before_gate))
+
+
 __all__ = ["chunk_gated_delta_rule_gqa", "fused_recurrent_gated_delta_rule_gqa",
            "gka_chebyshev_gla_prefill", "gka_chebyshev_gla_decode",
-           "mamba_chunk_scan_combined_varlen", "selective_state_update"]
+           "mamba_chunk_scan_combined_varlen", "selective_state_update", "causal_conv1d_fn",
+           "causal_conv1d_update", "rms_norm_gated"]

@@ -3,8 +3,10 @@
 vLLM's ``causal_conv1d_fn`` (prefill) and ``causal_conv1d_update`` (decode), as the
 layers call them (vllm-inference/src/primed_vllm/primed_gdn_layer.py:700-780): x is
 the [dim, tokens] transposed view of the [tokens, dim] projection output, the
-weight [dim, width], and the conv state pool [slots, state_len, dim] with
-channels contiguous (primed_utils.py:174-177).  Per channel,
+weight [dim, width], and the conv state pool the [slots, dim, state_len] view
+``self_kv_cache[0].transpose(-1, -2)`` (primed_gdn_layer.py:669) of the cache
+tensor [slots, state_len, dim] with channels contiguous (primed_utils.py:174-177).
+Per channel,
 
     out[t] = act(bias + sum_i w[i] x[t - (width-1) + i]),  act = silu ("silu"/"swish") or none,
 
@@ -45,6 +47,16 @@ def _aligned(t):
     return t if t.data_ptr() % 16 == 0 else t.clone()
 
 
+def _pool(st: torch.Tensor, dim: int, dtype, name: str):
+    """(state_len, slot stride, row stride) of a [slots, dim, state_len] pool view
+    whose channel axis is contiguous."""
+    if st.dim() != 3 or st.shape[1] != dim or st.dtype != dtype or st.stride(1) != 1:
+        raise ValueError(f"{name} must be the [slots, {dim}, state_len] {dtype} view of a "
+                         f"[slots, state_len, {dim}] cache (channels contiguous), got "
+                         f"{tuple(st.shape)} strides {st.stride()} {st.dtype}")
+    return st.shape[2], st.stride(0), st.stride(2)
+
+
 def _i32(t):
     return None if t is None else t.to(torch.int32).contiguous()
 
@@ -57,11 +69,26 @@ def causal_conv1d_fn(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor |
                      activation: str | None = "silu", pad_slot_id: int = PAD_SLOT_ID,
                      metadata=None, validate_data: bool = False, **block_args) -> torch.Tensor:
     """Prefill conv over concatenated sequences.  x [dim, total] (the transposed
-    view of [total, dim]); returns the same layout.  ``conv_states`` is updated in
-    place at ``cache_indices`` (default: sequence b uses slot b)."""
+    view of [total, dim]); returns the same layout.  ``conv_states`` [slots, dim,
+    state_len] (channels contiguous) is updated in place at ``cache_indices``
+    (default: sequence b uses slot b)."""
     if any(v is not None for v in block_args.values()):
         raise NotImplementedError("prefix-cache block arguments of causal_conv1d_fn: "
                                   f"{sorted(k for k, v in block_args.items() if v is not None)}")
+    return conv_fwd_rows(x, weight, bias, conv_states, query_start_loc, cache_indices,
+                         has_initial_state, activation, pad_slot_id, validate_data).t()
+
+
+def conv_fwd_rows(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None,
+                  conv_states: torch.Tensor | None, query_start_loc: torch.Tensor | None,
+                  cache_indices: torch.Tensor | None, has_initial_state: torch.Tensor | None,
+                  activation, pad_slot_id: int = PAD_SLOT_ID,
+                  validate_data: bool = False) -> torch.Tensor:
+    """``causal_conv1d_fn`` returning the output as contiguous [total, dim] rows.
+    Tokens from ``query_start_loc[-1]`` on belong to no sequence and give 0.  No
+    device value is read back unless ``validate_data`` (the kernels clamp sequence
+    bounds to the token count, so a malformed ``query_start_loc`` cannot move an
+    access outside x)."""
     _lib.require_gpu(x, weight, bias, conv_states, query_start_loc, cache_indices,
                      has_initial_state)
     dim, total = x.shape
@@ -72,28 +99,25 @@ def causal_conv1d_fn(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor |
     if query_start_loc is None:
         query_start_loc = torch.tensor([0, total], dtype=torch.int32, device=x.device)
     qs = _i32(query_start_loc)
-    bounds = [int(v) for v in qs.tolist()]
-    batch = len(bounds) - 1
-    if bounds[0] != 0 or any(b < a for a, b in zip(bounds, bounds[1:])) or bounds[-1] > total:
-        raise ValueError(f"query_start_loc must be non-decreasing from 0 to <= {total}: {bounds}")
+    batch = qs.shape[0] - 1
+    if validate_data:
+        bounds = [int(v) for v in qs.tolist()]
+        if bounds[0] != 0 or any(b < a for a, b in zip(bounds, bounds[1:])) or \
+                bounds[-1] > total:
+            raise ValueError(f"query_start_loc must be non-decreasing from 0 to <= {total}: "
+                             f"{bounds}")
     out = torch.empty(total, dim, dtype=x.dtype, device=x.device)
-    if bounds[-1] < total:
-        out[bounds[-1]:].zero_()      # tokens past the last sequence are not computed
     st_len, sst, srs = 0, 0, 0
     if conv_states is not None:
-        if conv_states.dtype != x.dtype or conv_states.shape[-1] != dim or \
-                conv_states.stride(-1) != 1:
-            raise ValueError(f"conv_states must be [slots, state_len, {dim}] {x.dtype} with "
-                             f"channels contiguous, got {tuple(conv_states.shape)} {conv_states.dtype}")
-        st_len, sst, srs = conv_states.shape[1], conv_states.stride(0), conv_states.stride(1)
+        st_len, sst, srs = _pool(conv_states, dim, x.dtype, "conv_states")
     hinit = None if has_initial_state is None else has_initial_state.to(torch.uint8).contiguous()
     w, b = _aligned(weight), _aligned(bias)
     _lib.call("hmx_causal_conv1d_fwd", _lib.ptr(xr), xr.stride(0), _lib.ptr(out), out.stride(0),
               _lib.dtype_code(x), _lib.ptr(w), _lib.dtype_code(w), W, _lib.ptr(b),
               0 if b is None else _lib.dtype_code(b), _lib.ptr(conv_states), sst, srs, st_len,
-              _lib.ptr(qs), batch, bounds[-1], _lib.ptr(_i32(cache_indices)), _lib.ptr(hinit),
+              _lib.ptr(qs), batch, total, _lib.ptr(_i32(cache_indices)), _lib.ptr(hinit),
               dim, _act(activation), int(pad_slot_id), _lib.stream_of(x))
-    return out.t()
+    return out
 
 
 def causal_conv1d_update(x: torch.Tensor, conv_state: torch.Tensor, weight: torch.Tensor,
@@ -101,13 +125,17 @@ def causal_conv1d_update(x: torch.Tensor, conv_state: torch.Tensor, weight: torc
                          conv_state_indices: torch.Tensor | None = None,
                          num_accepted_tokens: torch.Tensor | None = None,
                          query_start_loc: torch.Tensor | None = None, max_query_len: int = -1,
-                         pad_slot_id: int = PAD_SLOT_ID, validate_data: bool = False
-                         ) -> torch.Tensor:
+                         pad_slot_id: int = PAD_SLOT_ID, validate_data: bool = False,
+                         block_idx_last_scheduled_token: torch.Tensor | None = None,
+                         initial_state_idx: torch.Tensor | None = None) -> torch.Tensor:
     """Decode conv: x [batch, dim], one token per sequence, against the slot pool
-    ``conv_state`` [slots, state_len, dim] (updated in place: the state shifts by
-    one row).  Returns [batch, dim]; padded entries (slot == pad_slot_id) give 0."""
+    ``conv_state`` [slots, dim, state_len] (channels contiguous; updated in place:
+    the state shifts by one position).  Returns [batch, dim]; padded entries (slot ==
+    pad_slot_id) give 0."""
     if num_accepted_tokens is not None or query_start_loc is not None:
         raise NotImplementedError("speculative multi-token causal_conv1d_update")
+    if block_idx_last_scheduled_token is not None or initial_state_idx is not None:
+        raise NotImplementedError("prefix-cache block arguments of causal_conv1d_update")
     _lib.require_gpu(x, conv_state, weight, bias, conv_state_indices)
     if x.dim() != 2:
         raise NotImplementedError(f"x must be [batch, dim], got {tuple(x.shape)}")
@@ -115,15 +143,13 @@ def causal_conv1d_update(x: torch.Tensor, conv_state: torch.Tensor, weight: torc
     W = weight.shape[-1]
     if weight.shape != (dim, W):
         raise ValueError(f"weight must be [{dim}, width], got {tuple(weight.shape)}")
-    if conv_state.dtype != x.dtype or conv_state.shape[-1] != dim or conv_state.stride(-1) != 1:
-        raise ValueError(f"conv_state must be [slots, state_len, {dim}] {x.dtype} with channels "
-                         f"contiguous, got {tuple(conv_state.shape)} {conv_state.dtype}")
+    st_len, sst, srs = _pool(conv_state, dim, x.dtype, "conv_state")
     xr = _rows(x)
     out = torch.empty(batch, dim, dtype=x.dtype, device=x.device)
     w, b = _aligned(weight), _aligned(bias)
     _lib.call("hmx_causal_conv1d_update", _lib.ptr(xr), xr.stride(0), _lib.ptr(out), out.stride(0),
               _lib.dtype_code(x), _lib.ptr(w), _lib.dtype_code(w), W, _lib.ptr(b),
-              0 if b is None else _lib.dtype_code(b), _lib.ptr(conv_state), conv_state.stride(0),
-              conv_state.stride(1), conv_state.shape[1], _lib.ptr(_i32(conv_state_indices)),
+              0 if b is None else _lib.dtype_code(b), _lib.ptr(conv_state), sst, srs, st_len,
+              _lib.ptr(_i32(conv_state_indices)),
               batch, dim, _act(activation), int(pad_slot_id), _lib.stream_of(x))
     return out

@@ -305,12 +305,15 @@ int hmx_rms_norm_gated(const void* x, int64_t x_row_stride, const void* z,
  *   out[t, c] = act(bias[c] + sum_i weight[c, i] x[t - (width-1) + i, c])
  * act = silu (activation 1) or none (0); width in 2..4.  x / out [total_tokens, dim]
  * rows (element token strides, channels contiguous, 16-byte aligned), sequence b =
- * tokens [query_start_loc[b], query_start_loc[b+1]), total_tokens ==
- * query_start_loc[batch].  Positions before a sequence's first token read its conv
+ * tokens [query_start_loc[b], query_start_loc[b+1]) (non-decreasing from 0; the
+ * kernels clamp them to [0, total_tokens]); tokens from query_start_loc[batch] to
+ * total_tokens get output 0.  Positions before a sequence's first token read its conv
  * state (when conv_states is not NULL and has_initial_state[b] != 0, or
  * has_initial_state is NULL), zeros otherwise; afterwards the state holds the
- * sequence's last state_len inputs.  conv_states [slots, state_len, dim] in x's dtype
- * (element slot / row strides), slot cache_indices[b] (or b), skipped (output 0)
+ * sequence's last state_len inputs.  conv_states: rows [slots, state_len, dim] in x's
+ * dtype, channels contiguous (element slot / row strides; the layers' cache tensor
+ * self_kv_cache[0], primed_gdn_layer.py:669, which they hand to vLLM as its
+ * [slots, dim, state_len] transpose), slot cache_indices[b] (or b), skipped (output 0)
  * when equal to pad_slot_id; state_len in [width-1, 8].  weight [dim, width] and bias
  * [dim] (or NULL) in their dtypes.
  * Replaces: causal_conv1d_fn (vLLM, un-vendored; called at

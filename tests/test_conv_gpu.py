@@ -5,8 +5,10 @@ Covers widths 2-4, bias and none, silu and none, varlen with empty and 1-token
 sequences crossing the 64-token tiles, has_initial_state mixes, pad slots, a
 state with speculative slack rows (state_len > width - 1), a strided x (the
 transposed slice of a fused projection, as the layers pass it), fp32 rows, and T
-decode steps against one prefill.  States hold raw inputs, so they must match
-bit for bit; outputs within the output rounding.
+decode steps against one prefill.  The pool is passed as the layers pass it: the
+[slots, dim, state_len] transpose of the [slots, state_len, dim] cache.  States
+hold raw inputs, so they must match bit for bit; outputs within the output
+rounding.
 """
 import pytest
 import torch
@@ -44,13 +46,36 @@ def test_prefill_varlen(dev, W, bias, act):
     out_r, pool_r = ref.causal_conv1d_varlen(x, w, b, pool, qs, idx, init, act)
     pool_d = pool.to(dev)
     d = lambda t: None if t is None else t.to(dev)
-    out = hmx.causal_conv1d_fn(x.to(dev).t(), d(w), d(b), conv_states=pool_d,
+    out = hmx.causal_conv1d_fn(x.to(dev).t(), d(w), d(b), conv_states=pool_d.transpose(1, 2),
                                query_start_loc=d(qs), cache_indices=d(idx),
                                has_initial_state=d(init), activation=act)
     torch.cuda.synchronize()
     assert out.shape == (1024, x.shape[0])
     _close(out.t(), out_r)
     assert torch.equal(pool_d.cpu(), pool_r.to(pool.dtype))
+
+
+def test_tokens_past_last_sequence_are_zero(dev):
+    """x longer than query_start_loc[-1] (a padded batch): the tail gives 0, and a
+    batch of no sequences gives all zeros; validate_data rejects malformed bounds."""
+    qs, x, w, b, pool, g = _setup([50, 70], 256, 4, 2, 3, 31)
+    xp = torch.cat([x, torch.randn(90, 256, generator=g).bfloat16()])   # 90 padding tokens
+    out_r, pool_r = ref.causal_conv1d_varlen(x, w, b, pool, qs, None, None, "silu")
+    pool_d = pool.to(dev)
+    out = hmx.causal_conv1d_fn(xp.to(dev).t(), w.to(dev), b.to(dev),
+                               conv_states=pool_d.transpose(1, 2), query_start_loc=qs.to(dev))
+    torch.cuda.synchronize()
+    _close(out.t()[:120], out_r)
+    assert torch.equal(out.t()[120:].cpu(), torch.zeros(90, 256, dtype=x.dtype))
+    assert torch.equal(pool_d.cpu(), pool_r.to(pool.dtype))
+    none = hmx.causal_conv1d_fn(xp[:40].to(dev).t(), w.to(dev), None,
+                                query_start_loc=torch.zeros(1, dtype=torch.int32, device=dev))
+    torch.cuda.synchronize()
+    assert torch.equal(none.cpu(), torch.zeros(256, 40, dtype=x.dtype))
+    with pytest.raises(ValueError):
+        hmx.causal_conv1d_fn(xp[:40].to(dev).t(), w.to(dev), None, validate_data=True,
+                             query_start_loc=torch.tensor([0, 30, 20], dtype=torch.int32,
+                                                          device=dev))
 
 
 def test_prefill_no_state_strided_and_fp32(dev):
@@ -84,8 +109,9 @@ def test_decode_steps_equal_prefill(dev, st_len):
         bidx = idx.clone()
         if t == 4:
             bidx[1] = -1      # a padded entry in one step
-        o = hmx.causal_conv1d_update(xs[:, t].contiguous().to(dev), pool_d, w.to(dev), b.to(dev),
-                                     "silu", conv_state_indices=bidx.to(dev))
+        o = hmx.causal_conv1d_update(xs[:, t].contiguous().to(dev), pool_d.transpose(1, 2),
+                                     w.to(dev), b.to(dev), "silu",
+                                     conv_state_indices=bidx.to(dev))
         outs.append(o.cpu())
         if t == 4:
             assert torch.equal(o[1].cpu(), torch.zeros(dim, dtype=x.dtype))
@@ -109,10 +135,14 @@ def test_decode_steps_equal_prefill(dev, st_len):
 def test_errors(dev):
     x = torch.zeros(8, 64, dtype=torch.bfloat16, device=dev)
     w = torch.zeros(64, 4, device=dev)
-    pool = torch.zeros(2, 3, 64, dtype=torch.bfloat16, device=dev)
+    pool = torch.zeros(2, 3, 64, dtype=torch.bfloat16, device=dev).transpose(1, 2)
     with pytest.raises(NotImplementedError):
         hmx.causal_conv1d_update(x, pool, w, num_accepted_tokens=torch.ones(8, device=dev))
     with pytest.raises(NotImplementedError):
         hmx.causal_conv1d_fn(x.t(), torch.zeros(64, 5, device=dev))    # width 5
     with pytest.raises(ValueError):
         hmx.causal_conv1d_fn(x.t(), torch.zeros(32, 4, device=dev))    # weight/dim mismatch
+    with pytest.raises(ValueError):    # the cache rows themselves, not the [slots, dim, len] view
+        hmx.causal_conv1d_update(x, pool.transpose(1, 2).contiguous(), w)
+    with pytest.raises(NotImplementedError):
+        hmx.causal_conv1d_update(x, pool, w, initial_state_idx=torch.zeros(8, device=dev))

@@ -12,7 +12,8 @@ def test_ops_registered_with_mutations():
     for name in ("fused_gdn_gating", "chunk_gated_delta_rule_gqa",
                  "fused_recurrent_gated_delta_rule_gqa", "gka_chebyshev_gla_prefill",
                  "gka_chebyshev_gla_decode", "mamba_chunk_scan_combined",
-                 "mamba_chunk_scan_combined_varlen", "selective_state_update"):
+                 "mamba_chunk_scan_combined_varlen", "selective_state_update",
+                 "causal_conv1d_fn", "causal_conv1d_update", "rms_norm_gated"):
         assert hasattr(torch.ops.hmx, name), name
     def mutated(op):
         return {a.name for a in op.default._schema.arguments
@@ -22,6 +23,9 @@ def test_ops_registered_with_mutations():
     assert mutated(torch.ops.hmx.gka_chebyshev_gla_decode) == {"h_kk", "h_kv"}
     assert mutated(torch.ops.hmx.mamba_chunk_scan_combined_varlen) == {"out"}
     assert mutated(torch.ops.hmx.chunk_gated_delta_rule_gqa) == set()
+    assert mutated(torch.ops.hmx.causal_conv1d_fn) == {"conv_states"}
+    assert mutated(torch.ops.hmx.causal_conv1d_update) == {"conv_state"}
+    assert mutated(torch.ops.hmx.rms_norm_gated) == set()
 
 
 def test_fake_shapes_gdn_gka():
@@ -61,3 +65,16 @@ def test_backward_is_refused():
     o, _ = torch.ops.hmx.chunk_gated_delta_rule_gqa(q, q, q, g, g, 0.1, None, False, None, True)
     with pytest.raises(NotImplementedError, match="forward-only"):
         o.sum().backward()
+
+
+def test_fake_shapes_conv_norm():
+    x = torch.empty(300, 96, device=M, dtype=torch.bfloat16)
+    w = torch.empty(96, 4, device=M)
+    pool = torch.empty(3, 3, 96, device=M, dtype=torch.bfloat16).transpose(1, 2)
+    out = torch.ops.hmx.causal_conv1d_fn(x.t(), w, None, pool, None, None, None, "silu", -1)
+    assert out.shape == (300, 96)                  # [total, dim] rows; the wrapper transposes
+    o = torch.ops.hmx.causal_conv1d_update(x[:5], pool, w, None, "silu", None, -1)
+    assert o.shape == (5, 96)
+    z = torch.empty(2, 7, 4, 128, device=M, dtype=torch.bfloat16)
+    assert torch.ops.hmx.rms_norm_gated(z, z, torch.empty(128, device=M), 1e-6, True).shape == \
+        z.shape

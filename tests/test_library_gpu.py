@@ -82,3 +82,33 @@ def test_opcheck_functional_ops(dev):
                            float("inf")),
                           test_utils=("test_schema", "test_faketensor",
                                       "test_autograd_registration"))
+
+
+def test_conv_and_norm_registered_equal_direct(dev):
+    g0 = torch.Generator().manual_seed(4)
+    x = torch.randn(150, 256, generator=g0).bfloat16().to(dev)
+    w = torch.randn(256, 4, generator=g0).to(dev)
+    b = torch.randn(256, generator=g0).to(dev)
+    pool = torch.randn(4, 3, 256, generator=g0).bfloat16().to(dev).transpose(1, 2)
+    pool2 = pool.clone(memory_format=torch.preserve_format)
+    qs = torch.tensor([0, 60, 150], dtype=torch.int32, device=dev)
+    idx = torch.tensor([3, 1], dtype=torch.int32, device=dev)
+    o1 = hmx.causal_conv1d_fn(x.t(), w, b, conv_states=pool, query_start_loc=qs, cache_indices=idx)
+    o2 = hl.causal_conv1d_fn(x.t(), w, b, conv_states=pool2, query_start_loc=qs, cache_indices=idx)
+    torch.cuda.synchronize()
+    assert o2.shape == (256, 150) and torch.equal(o1, o2) and torch.equal(pool, pool2)
+    u1 = hmx.causal_conv1d_update(x[:2], pool, w, b, "silu", conv_state_indices=idx)
+    u2 = hl.causal_conv1d_update(x[:2], pool2, w, b, True, conv_state_indices=idx)
+    torch.cuda.synchronize()
+    assert torch.equal(u1, u2) and torch.equal(pool, pool2)
+    z = torch.randn(2, 9, 4, 128, generator=g0).bfloat16().to(dev)
+    wn = torch.rand(128, generator=g0).to(dev)
+    assert torch.equal(hmx.rms_norm_gated(z, z.flip(0), wn, 1e-6),
+                       hl.rms_norm_gated(z, z.flip(0), wn, 1e-6))
+    torch.library.opcheck(torch.ops.hmx.rms_norm_gated.default, (z, z.flip(0), wn, 1e-6, True),
+                          test_utils=("test_schema", "test_faketensor",
+                                      "test_autograd_registration"))
+    torch.library.opcheck(torch.ops.hmx.causal_conv1d_update.default,
+                          (x[:2], pool.clone(memory_format=torch.preserve_format), w, b, "silu",
+                           idx, -1),
+                          test_utils=("test_schema", "test_faketensor"))
