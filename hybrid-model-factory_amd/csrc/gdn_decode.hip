@@ -23,6 +23,7 @@ namespace hmx {
 
 struct RecurrentParams {
   const void* q; const void* k; const void* v;
+  int64_t q_ts, k_ts, v_ts;   // token strides (elements); heads are K (V for v) apart
   const void* g; int g_dt;
   const void* beta; int beta_dt; int beta_headwise;
   void* o;
@@ -120,9 +121,9 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(RecurrentParams p) {
   for (int64_t t = 0; t < T; ++t) {
     const int64_t tok = bos + t;
     float kr[R], qr[R], vv[4], bb[4];
-    load_vec<R>(static_cast<const TQ*>(p.k) + (tok * p.HKV + hk) * K + r * R, kr);
-    load_vec<R>(static_cast<const TQ*>(p.q) + (tok * p.H + h) * K + r * R, qr);
-    load_vec<4>(static_cast<const TQ*>(p.v) + (tok * p.HKV + hk) * V + col, vv);
+    load_vec<R>(static_cast<const TQ*>(p.k) + tok * p.k_ts + (int64_t)hk * K + r * R, kr);
+    load_vec<R>(static_cast<const TQ*>(p.q) + tok * p.q_ts + (int64_t)h * K + r * R, qr);
+    load_vec<4>(static_cast<const TQ*>(p.v) + tok * p.v_ts + (int64_t)hk * V + col, vv);
     const float gt = load_scalar(p.g, tok * p.H + h, p.g_dt);
     if (p.beta_headwise) {
 #pragma unroll
@@ -235,7 +236,8 @@ static int dispatch_qkv(const RecurrentParams& p, int64_t N, int qkv_dt, int sta
 }  // namespace hmx
 
 extern "C" int hmx_gdn_recurrent_fwd(
-    const void* q, const void* k, const void* v, int32_t qkv_dtype, const void* g,
+    const void* q, int64_t q_token_stride, const void* k, int64_t k_token_stride, const void* v,
+    int64_t v_token_stride, int32_t qkv_dtype, const void* g,
     int32_t g_dtype, const void* beta, int32_t beta_dtype, int32_t beta_headwise, void* o,
     const void* h0, int64_t h0_row_stride, void* ht, int64_t ht_row_stride, int32_t state_dtype,
     const int32_t* cu_seqlens, const int32_t* ssm_state_indices, int64_t idx_stride,
@@ -260,9 +262,14 @@ extern "C" int hmx_gdn_recurrent_fwd(
               (long long)N, (long long)B);
   HMX_REQUIRE(g_dtype >= 0 && g_dtype <= 2 && beta_dtype >= 0 && beta_dtype <= 2, HMX_EUNSUPPORTED,
               "hmx_gdn_recurrent_fwd: g/beta dtype");
+  HMX_REQUIRE(q_token_stride % 4 == 0 && k_token_stride % 4 == 0 && v_token_stride % 4 == 0 &&
+                  ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) % 16 == 0,
+              HMX_EINVAL, "hmx_gdn_recurrent_fwd: q/k/v token strides must be multiples of 4 "
+              "elements and the bases 16-byte aligned");
   if (N == 0) return HMX_OK;
   RecurrentParams p;
   p.q = q; p.k = k; p.v = v; p.g = g; p.g_dt = g_dtype;
+  p.q_ts = q_token_stride; p.k_ts = k_token_stride; p.v_ts = v_token_stride;
   p.beta = beta; p.beta_dt = beta_dtype; p.beta_headwise = beta_headwise;
   p.o = o; p.h0 = h0; p.h0_rs = h0_row_stride; p.ht = ht; p.ht_rs = ht_row_stride;
   p.cu_seqlens = cu_seqlens; p.idx = ssm_state_indices; p.idx_stride = idx_stride;

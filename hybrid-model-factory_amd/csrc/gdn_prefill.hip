@@ -89,11 +89,21 @@ struct SegInfo {     // one row of the host-built segment table (int32 x 8)
 
 struct Params {
   const bf16* q; const bf16* k; const bf16* v;
+  int64_t q_ts, k_ts, v_ts;  // token strides (elements); heads are D apart
   const void* g; int g_dt;
   const void* beta; int beta_dt;
   bf16* o;
-  const float* h0;           // [N,H,K,V] or null
-  float* ht;                 // [N,H,K,V] or null
+  // States: slot sidx[n] (or n) of the h0 / ht bases, st_ss elements apart, in
+  // st_dt (f32 or bf16); a negative slot or hinit[n] == 0 starts from zero, and a
+  // negative slot writes no end state.  With sidx the two may alias (one pool):
+  // the end states of split sequences then go through ws_ht (copied after the
+  // launch that may still read the pool).
+  const void* h0;            // or null (zero start)
+  void* ht;                  // or null (no end state)
+  int64_t st_ss; int st_dt;
+  const int* sidx;           // [N] or null
+  const uint8_t* hinit;      // [N] or null
+  float* ws_ht;              // [N][H][D][D] or null
   const int* seg;            // [nseg_total][8]
   int* plan;                 // [nseg_total][H]: warm-up start chunk, or -1 (null: 1 seg/seq)
   float* ws_s0;              // [nseg_total][H][D][D]
@@ -144,20 +154,19 @@ struct RawChunk {
 
 template <int MODE>
 __device__ __forceinline__ void load_raw(RawChunk& r, const Params& p, const bf16* qh,
-                                         const bf16* kh, const bf16* vh, int64_t q_rs,
-                                         int64_t kv_rs, int tok0, int nval, bool need_q,
-                                         int tid, int h) {
+                                         const bf16* kh, const bf16* vh, int tok0, int nval,
+                                         bool need_q, int tid, int h) {
 #pragma unroll
   for (int pass = 0; pass < MT; ++pass) {
     const int row = pass * 16 + (tid >> 4);
     const int f0 = (tid & 15) * 8;
     const bool ok = row < nval;
     const int64_t tok = tok0 + row;
-    r.k[pass] = ok ? *reinterpret_cast<const bf16x8*>(kh + tok * kv_rs + f0) : bf16x8{};
+    r.k[pass] = ok ? *reinterpret_cast<const bf16x8*>(kh + tok * p.k_ts + f0) : bf16x8{};
     if (MODE != MODE_PHI)
-      r.v[pass] = ok ? *reinterpret_cast<const bf16x8*>(vh + tok * kv_rs + f0) : bf16x8{};
+      r.v[pass] = ok ? *reinterpret_cast<const bf16x8*>(vh + tok * p.v_ts + f0) : bf16x8{};
     if (MODE == MODE_OUT)
-      r.q[pass] = (ok && need_q) ? *reinterpret_cast<const bf16x8*>(qh + tok * q_rs + f0)
+      r.q[pass] = (ok && need_q) ? *reinterpret_cast<const bf16x8*>(qh + tok * p.q_ts + f0)
                                  : bf16x8{};
   }
   if (tid < C) {
@@ -367,13 +376,19 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
       init_kind = (si.seg_idx == 0) ? 1 : 0;
     }
   }
-  if (init_kind == 1 && !p.h0) init_kind = 0;
+  const int64_t slot = p.sidx ? (int64_t)p.sidx[si.n] : si.n;
+  if (init_kind == 1 && (!p.h0 || slot < 0 || (p.hinit && !p.hinit[si.n]))) init_kind = 0;
 
   // ---- state registers: S[rt][ct] is the 16x16 tile (rows 16rt.., cols 32w+16ct..)
   f32x4 S[8][2];
   {
     const float* src = nullptr;
-    if (init_kind == 1) src = p.h0 + ((int64_t)si.n * H + h) * D * D;
+    const bf16* src16 = nullptr;
+    if (init_kind == 1) {
+      const int64_t off = slot * p.st_ss + (int64_t)h * D * D;
+      if (p.st_dt == HMX_BF16) src16 = static_cast<const bf16*>(p.h0) + off;
+      else src = static_cast<const float*>(p.h0) + off;
+    }
     if (init_kind == 2) src = p.ws_init + ((int64_t)s_id * H + h) * D * D;
 #pragma unroll
     for (int rt = 0; rt < 8; ++rt)
@@ -384,6 +399,7 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
           const int row = 16 * rt + 4 * q4 + v, col = 32 * wave + 16 * ct + l16;
           float x = 0.f;
           if (src) x = src[row * D + col];
+          if (src16) x = (float)src16[row * D + col];
           if (init_kind == 3) x = (row == col) ? 1.f : 0.f;
           S[rt][ct][v] = x;
         }
@@ -394,7 +410,7 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
     for (int i = tid; i < 16 * 16; i += NTHR) sP[(i >> 4) * LDT + 16 + (i & 15)] = (bf16)0.f;
   }
 
-  const int64_t q_rs = (int64_t)H * D, kv_rs = (int64_t)p.HKV * D;
+  const int64_t o_rs = (int64_t)H * D;
   const bf16* qh = p.q + (int64_t)h * D;
   const bf16* kh = p.k + (int64_t)hk * D;
   const bf16* vh = p.v + (int64_t)hk * D;
@@ -407,7 +423,7 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
       const int row = pass * 16 + (tid >> 4);
       const int f0 = (tid & 15) * 8;
       if (row < nval)
-        *reinterpret_cast<bf16x8*>(oh + (int64_t)(tok0 + row) * q_rs + f0) =
+        *reinterpret_cast<bf16x8*>(oh + (int64_t)(tok0 + row) * o_rs + f0) =
             *reinterpret_cast<const bf16x8*>(sO + row * LDQ + f0);
     }
   };
@@ -453,7 +469,7 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
         out[j] = (bf16)y;
       }
       if (row < nval)
-        *reinterpret_cast<bf16x8*>(oh + (int64_t)(tok0 + row) * q_rs + f0) = out;
+        *reinterpret_cast<bf16x8*>(oh + (int64_t)(tok0 + row) * o_rs + f0) = out;
     }
   };
   if (NORM && tid < D) {
@@ -474,14 +490,14 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
     RawChunk raw;
     {
       const int t0 = si.bos + c_begin * C;
-      load_raw<MODE>(raw, p, qh, kh, vh, q_rs, kv_rs, t0, min(C, si.eos - t0), c_begin >= c_out,
+      load_raw<MODE>(raw, p, qh, kh, vh, t0, min(C, si.eos - t0), c_begin >= c_out,
                      tid, h);
       prep_rows<MODE>(raw, p.l2norm);
       if (wave == 0) prep_scan(raw, lane);
       stage_chunk<MODE>(stage_at(smem, 0), raw, c_begin >= c_out, tid, wave, lane);
       if (c_begin + 1 < si.c_end) {
         const int t1 = t0 + C;
-        load_raw<MODE>(raw, p, qh, kh, vh, q_rs, kv_rs, t1, min(C, si.eos - t1),
+        load_raw<MODE>(raw, p, qh, kh, vh, t1, min(C, si.eos - t1),
                        c_begin + 1 >= c_out, tid, h);
       }
     }
@@ -736,7 +752,7 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
         stage_chunk<MODE>(stage_at(smem, bi ^ 1), raw, c + 1 >= c_out, tid, wave, lane);
         if (c + 2 < si.c_end) {
           const int t2 = tok0 + 2 * C;
-          load_raw<MODE>(raw, p, qh, kh, vh, q_rs, kv_rs, t2, min(C, si.eos - t2),
+          load_raw<MODE>(raw, p, qh, kh, vh, t2, min(C, si.eos - t2),
                          c + 2 >= c_out, tid, h);
         }
       }
@@ -757,21 +773,33 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
 
   // ---- write the end state ---------------------------------------------------
   float* dst = nullptr;
+  bf16* dst16 = nullptr;
   if (MODE == MODE_OUT) {
-    if (si.seg_idx == si.nseg - 1 && p.ht) dst = p.ht + ((int64_t)si.n * H + h) * D * D;
+    if (si.seg_idx == si.nseg - 1 && p.ht && slot >= 0) {
+      if (p.ws_ht && si.nseg > 1) {
+        dst = p.ws_ht + ((int64_t)si.n * H + h) * D * D;
+      } else {
+        const int64_t off = slot * p.st_ss + (int64_t)h * D * D;
+        if (p.st_dt == HMX_BF16) dst16 = static_cast<bf16*>(p.ht) + off;
+        else dst = static_cast<float*>(p.ht) + off;
+      }
+    }
   } else if (MODE == MODE_S0) {
     dst = p.ws_s0 + ((int64_t)s_id * H + h) * D * D;
   } else {
     dst = p.ws_phi + ((int64_t)s_id * H + h) * D * D;
   }
-  if (dst) {
+  if (dst || dst16) {
 #pragma unroll
     for (int rt = 0; rt < 8; ++rt)
 #pragma unroll
       for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-        for (int v = 0; v < 4; ++v)
-          dst[(16 * rt + 4 * q4 + v) * D + 32 * wave + 16 * ct + l16] = S[rt][ct][v] * gam;
+        for (int v = 0; v < 4; ++v) {
+          const int i = (16 * rt + 4 * q4 + v) * D + 32 * wave + 16 * ct + l16;
+          if (dst) dst[i] = S[rt][ct][v] * gam;
+          else dst16[i] = (bf16)(S[rt][ct][v] * gam);
+        }
   }
 }
 
@@ -857,15 +885,44 @@ __global__ __launch_bounds__(NTHR) void gdn_seg_combine_kernel(Params p, int N) 
   }
 }
 
+// ---------------------------------------------------------------------------
+// pooled end states of split sequences: ws_ht -> the pool slot, after every launch
+// that may still read the pool.  One workgroup per (sequence, head).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(NTHR) void gdn_state_copy_kernel(Params p) {
+  const int n = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+  int nseg = 0;
+  for (int s = 0; s < p.nseg_total; ++s) {
+    const SegInfo si = load_seg(p.seg, s);
+    if (si.n == n) { nseg = si.nseg; break; }
+  }
+  const int64_t slot = p.sidx[n];
+  if (nseg < 2 || slot < 0) return;
+  const float* src = p.ws_ht + ((int64_t)n * p.H + h) * D * D;
+  const int64_t off = slot * p.st_ss + (int64_t)h * D * D;
+  for (int i = tid * 4; i < D * D; i += NTHR * 4) {
+    const f32x4 x = *reinterpret_cast<const f32x4*>(src + i);
+    if (p.st_dt == HMX_BF16) {
+      bf16x4 y{(bf16)x[0], (bf16)x[1], (bf16)x[2], (bf16)x[3]};
+      *reinterpret_cast<bf16x4*>(static_cast<bf16*>(p.ht) + off + i) = y;
+    } else {
+      *reinterpret_cast<f32x4*>(static_cast<float*>(p.ht) + off + i) = x;
+    }
+  }
+}
+
 }  // namespace gdnp
 }  // namespace hmx
 
 using namespace hmx;
 using namespace hmx::gdnp;
 
-extern "C" int hmx_gdn_chunk_fwd(const void* q, const void* k, const void* v, int32_t qkv_dtype,
-                                 const void* g, int32_t g_dtype, const void* beta,
-                                 int32_t beta_dtype, void* o, const float* h0, float* ht,
+extern "C" int hmx_gdn_chunk_fwd(const void* q, int64_t q_token_stride, const void* k,
+                                 int64_t k_token_stride, const void* v, int64_t v_token_stride,
+                                 int32_t qkv_dtype, const void* g, int32_t g_dtype,
+                                 const void* beta, int32_t beta_dtype, void* o, const void* h0,
+                                 void* ht, int64_t state_slot_stride, int32_t state_dtype,
+                                 const int32_t* state_indices, const uint8_t* has_initial_state,
                                  const int32_t* seg_table, int32_t nseg_total, int32_t N,
                                  int32_t H, int32_t HKV, int32_t K, int32_t V, float scale,
                                  int32_t use_qk_l2norm, int32_t max_warm_chunks,
@@ -881,16 +938,28 @@ extern "C" int hmx_gdn_chunk_fwd(const void* q, const void* k, const void* v, in
               "hmx_gdn_chunk_fwd: null tensor pointer");
   HMX_REQUIRE(g_dtype >= 0 && g_dtype <= 2 && beta_dtype >= 0 && beta_dtype <= 2,
               HMX_EUNSUPPORTED, "hmx_gdn_chunk_fwd: g/beta dtype");
+  HMX_REQUIRE(q_token_stride % 8 == 0 && k_token_stride % 8 == 0 && v_token_stride % 8 == 0 &&
+                  ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)o) % 16 == 0,
+              HMX_EINVAL, "hmx_gdn_chunk_fwd: q/k/v/o rows must be 16-byte aligned");
+  HMX_REQUIRE(!(h0 || ht) || ((state_dtype == HMX_F32 || state_dtype == HMX_BF16) &&
+                              state_slot_stride % 4 == 0 &&
+                              ((uintptr_t)h0 | (uintptr_t)ht) % 16 == 0),
+              HMX_EINVAL, "hmx_gdn_chunk_fwd: states must be f32/bf16 with 16-byte aligned "
+              "slots (slot stride %lld)", (long long)state_slot_stride);
   if (nseg_total == 0) return HMX_OK;
-  const size_t need = hmx_gdn_chunk_workspace_bytes(nseg_total, N, H);
+  const int32_t pooled = state_indices != nullptr;
+  const size_t need = hmx_gdn_chunk_workspace_bytes(nseg_total, N, H, pooled);
   HMX_REQUIRE(workspace && workspace_bytes >= need, HMX_EINVAL,
               "hmx_gdn_chunk_fwd: workspace of %zu bytes needed, %zu given", need,
               workspace_bytes);
   Params p;
   p.q = static_cast<const bf16*>(q); p.k = static_cast<const bf16*>(k);
   p.v = static_cast<const bf16*>(v);
+  p.q_ts = q_token_stride; p.k_ts = k_token_stride; p.v_ts = v_token_stride;
   p.g = g; p.g_dt = g_dtype; p.beta = beta; p.beta_dt = beta_dtype;
   p.o = static_cast<bf16*>(o); p.h0 = h0; p.ht = ht;
+  p.st_ss = state_slot_stride; p.st_dt = state_dtype;
+  p.sidx = state_indices; p.hinit = has_initial_state;
   p.seg = seg_table; p.nseg_total = nseg_total; p.H = H; p.HKV = HKV; p.scale = scale;
   p.l2norm = use_qk_l2norm; p.max_warm = max_warm_chunks; p.decay_thresh = decay_threshold;
   p.zg = nullptr; p.zg_ts = p.zg_hs = 0; p.onw = nullptr; p.onw_dt = HMX_F32; p.on_eps = 0.f;
@@ -912,7 +981,9 @@ extern "C" int hmx_gdn_chunk_fwd(const void* q, const void* k, const void* v, in
   p.ws_s0 = multi ? reinterpret_cast<float*>(ws) : nullptr;
   p.ws_phi = multi ? reinterpret_cast<float*>(ws + st) : nullptr;
   p.ws_init = multi ? reinterpret_cast<float*>(ws + 2 * st) : nullptr;
-  char* tail = ws + (multi ? 3 * st : 0);
+  const bool staged = multi && pooled && ht;
+  p.ws_ht = staged ? reinterpret_cast<float*>(ws + 3 * st) : nullptr;
+  char* tail = ws + (multi ? 3 * st : 0) + (multi && pooled ? (size_t)N * H * D * D * 4 : 0);
   p.plan = reinterpret_cast<int*>(tail);
   hipStream_t s = (hipStream_t)stream;
   if (multi) {
@@ -927,13 +998,15 @@ extern "C" int hmx_gdn_chunk_fwd(const void* q, const void* k, const void* v, in
     hipLaunchKernelGGL((gdn_chunk_kernel<MODE_OUT, true>), dim3(nseg_total, H), dim3(NTHR), 0, s, p);
   else
     hipLaunchKernelGGL(gdn_chunk_kernel<MODE_OUT>, dim3(nseg_total, H), dim3(NTHR), 0, s, p);
+  if (staged) hipLaunchKernelGGL(gdn_state_copy_kernel, dim3(N, H), dim3(NTHR), 0, s, p);
   return check_launch("hmx_gdn_chunk_fwd");
 }
 
-extern "C" size_t hmx_gdn_chunk_workspace_bytes(int32_t nseg_total, int32_t N, int32_t H) {
+extern "C" size_t hmx_gdn_chunk_workspace_bytes(int32_t nseg_total, int32_t N, int32_t H,
+                                                int32_t pooled) {
   const bool multi = nseg_total > N;
   size_t b = multi ? 3 * (size_t)nseg_total * H * D * D * sizeof(float) : 0;
+  if (multi && pooled) b += (size_t)N * H * D * D * sizeof(float);   // staged end states
   b += (size_t)nseg_total * H * sizeof(int);
-  (void)N;
   return b;
 }

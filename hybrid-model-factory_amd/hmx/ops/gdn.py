@@ -28,6 +28,25 @@ def _i32(t: torch.Tensor | None) -> torch.Tensor | None:
     return t.contiguous()
 
 
+def _token_rows(t: torch.Tensor, mult: int) -> tuple[torch.Tensor, int]:
+    """(t, token stride) for a [B, T, heads, dim] tensor whose B*T tokens sit at one
+    stride with each token's heads contiguous -- the column slices of a fused
+    projection, as the layers pass q/k/v -- so the kernels read it in place; a
+    contiguous copy otherwise.  The stride must be a multiple of ``mult`` elements
+    and the base 16-byte aligned."""
+    B, T, Hh, Dd = t.shape
+    if B * T <= 1:
+        ts = Hh * Dd          # one token: the stride is never used
+    else:
+        ts = t.stride(1) if T > 1 else t.stride(0)
+    ok = (t.stride(-1) == 1 and (t.stride(2) == Dd or Hh == 1) and ts % mult == 0
+          and ts >= Hh * Dd and (B == 1 or t.stride(0) == T * ts) and t.data_ptr() % 16 == 0)
+    if not ok:
+        t = t.contiguous()
+        ts = Hh * Dd
+    return t, ts
+
+
 def fused_gdn_gating(A_log: torch.Tensor, a: torch.Tensor, b: torch.Tensor,
                      dt_bias: torch.Tensor, beta: float = 1.0,
                      threshold: float = 20.0) -> tuple[torch.Tensor, torch.Tensor]:
@@ -91,7 +110,8 @@ def fused_recurrent_gated_delta_rule_gqa(
         beta = torch.ones_like(g)
     _lib.require_gpu(q, k, v, g, beta, initial_state, cu_seqlens, ssm_state_indices,
                      num_accepted_tokens)
-    q, k, v, g, beta = (x.contiguous() for x in (q, k, v, g, beta))
+    g, beta = g.contiguous(), beta.contiguous()
+    (q, q_ts), (k, k_ts), (v, v_ts) = (_token_rows(x, 4) for x in (q, k, v))
     if not (q.dtype == k.dtype == v.dtype):
         raise AssertionError("q, k, v must share a dtype")
     B, T, H, K = q.shape
@@ -129,7 +149,7 @@ def fused_recurrent_gated_delta_rule_gqa(
     elif o_norm_gate is not None:
         raise ValueError("o_norm_gate needs o_norm_weight")
     _lib.call("hmx_gdn_recurrent_fwd",
-              _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.dtype_code(q),
+              _lib.ptr(q), q_ts, _lib.ptr(k), k_ts, _lib.ptr(v), v_ts, _lib.dtype_code(q),
               _lib.ptr(g), _lib.dtype_code(g),
               _lib.ptr(beta), _lib.dtype_code(beta), int(beta_headwise),
               _lib.ptr(o),
@@ -227,6 +247,9 @@ def chunk_gated_delta_rule_gqa(
     o_norm_weight: torch.Tensor | None = None,
     o_norm_gate: torch.Tensor | None = None,
     o_norm_eps: float = 1e-5,
+    ssm_state_indices: torch.Tensor | None = None,
+    has_initial_state: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
     _segment_chunks: int | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor | None]:
     """GQA-native chunked gated delta rule (prefill).
@@ -237,18 +260,31 @@ def chunk_gated_delta_rule_gqa(
     (chunk_gqa.py:15-83).  ``_segment_chunks`` overrides the parallel
     decomposition (tests); results do not depend on it beyond fp32 rounding.
     
-    Keyword-only extension (no reference counterpart): ``o_norm_weight`` [V] (and
-    optionally ``o_norm_gate`` [B,T,H,V], q.dtype) returns the layer's
-    ``o_norm(o, z)`` (gated RMSNorm, norm before gate, eps ``o_norm_eps``;
-    primed_gdn_layer.py:621-626) computed in the kernel's output epilogue instead
-    of o.
+    Keyword-only extensions (no reference counterpart):
+
+    - ``o_norm_weight`` [V] (and optionally ``o_norm_gate`` [B,T,H,V], q.dtype)
+      returns the layer's ``o_norm(o, z)`` (gated RMSNorm, norm before gate, eps
+      ``o_norm_eps``; primed_gdn_layer.py:621-626) computed in the kernel's output
+      epilogue instead of o.
+    - ``ssm_state_indices`` [N]: ``initial_state`` is the layer's state pool
+      [slots,H,K,V] (fp32 or bf16); sequence n starts from slot
+      ``ssm_state_indices[n]`` and, with ``output_final_state``, its end state is
+      written back into that slot in place; the pool is returned as the final
+      state.  This replaces the layer's gather / zero / scatter around the op
+      (primed_gdn_layer.py:868-879).  A negative slot starts from zero and writes
+      nothing.
+    - ``has_initial_state`` [N] bool: sequences with False start from zero.
+    - ``out`` [B,T,H,V] (q.dtype, contiguous): o is written there.
+
+    q, k and v may be the column slices of one fused projection (token stride
+    larger than heads x dim): they are read in place.
     """
     assert q.dtype == k.dtype == v.dtype
     assert q.dtype != torch.float32, "Does not support float32. Use bfloat16."
     assert len(beta.shape) == 3, "beta must be [B, T, H]"
     if cu_seqlens is not None and q.shape[0] != 1:
         raise ValueError(f"Batch size expected to be 1 with cu_seqlens, got {q.shape[0]}")
-    if cu_seqlens is not None and initial_state is not None:
+    if cu_seqlens is not None and initial_state is not None and ssm_state_indices is None:
         if initial_state.shape[0] != len(cu_seqlens) - 1:
             raise ValueError(f"Initial states count mismatch: {initial_state.shape[0]} vs "
                              f"{len(cu_seqlens) - 1}")
@@ -269,18 +305,49 @@ def chunk_gated_delta_rule_gqa(
         if cs[0] != 0 or cs[-1] > T or any(b < a for a, b in bounds):
             raise ValueError(f"cu_seqlens must be non-decreasing from 0 to <= {T}: {cs}")
     N = len(bounds)
-    if initial_state is not None and tuple(initial_state.shape) != (N, H, K, V):
-        raise ValueError(f"initial_state must be [{N},{H},{K},{V}], got {tuple(initial_state.shape)}")
-    q, k, v, g, beta = (x.contiguous() for x in (q, k, v, g, beta))
-    h0 = None if initial_state is None else initial_state.to(torch.float32).contiguous()
-    o = torch.empty(B, T, H, V, dtype=q.dtype, device=q.device)
+    _lib.require_gpu(ssm_state_indices, has_initial_state, out)
+    idx = None
+    if ssm_state_indices is not None:
+        if initial_state is None:
+            raise ValueError("ssm_state_indices needs initial_state (the state pool)")
+        idx = _i32(ssm_state_indices)
+        if idx.shape != (N,):
+            raise ValueError(f"ssm_state_indices must hold {N} slots, got {tuple(idx.shape)}")
+        pool = initial_state
+        if (pool.dim() != 4 or tuple(pool.shape[1:]) != (H, K, V) or not pool[0].is_contiguous()
+                or pool.dtype not in (torch.float32, torch.bfloat16)):
+            raise ValueError(f"the state pool must be [slots,{H},{K},{V}] fp32/bf16 with "
+                             f"contiguous slots, got {tuple(pool.shape)} {pool.dtype}")
+        h0, ht = pool, (pool if output_final_state else None)
+        st_ss, st_dt = pool.stride(0), _lib.dtype_code(pool)
+    else:
+        if initial_state is not None and tuple(initial_state.shape) != (N, H, K, V):
+            raise ValueError(f"initial_state must be [{N},{H},{K},{V}], "
+                             f"got {tuple(initial_state.shape)}")
+        h0 = None if initial_state is None else initial_state.to(torch.float32).contiguous()
+        ht = (torch.empty(N, H, K, V, dtype=torch.float32, device=q.device)
+              if output_final_state else None)
+        st_ss, st_dt = H * K * V, _lib.HMX_F32
+    hinit = None
+    if has_initial_state is not None:
+        if has_initial_state.shape != (N,):
+            raise ValueError(f"has_initial_state must be [{N}], got {tuple(has_initial_state.shape)}")
+        hinit = has_initial_state.to(torch.uint8).contiguous()
+    g, beta = g.contiguous(), beta.contiguous()
+    (q, q_ts), (k, k_ts), (v, v_ts) = (_token_rows(x, 8) for x in (q, k, v))
+    if out is not None:
+        if (tuple(out.shape) != (B, T, H, V) or out.dtype != q.dtype or not out.is_contiguous()
+                or out.data_ptr() % 16):
+            raise ValueError(f"out must be a contiguous [{B},{T},{H},{V}] {q.dtype} tensor")
+        o = out
+    else:
+        o = torch.empty(B, T, H, V, dtype=q.dtype, device=q.device)
     if cu_seqlens is not None and bounds and bounds[-1][1] < T:
         o[:, bounds[-1][1]:].zero_()  # tokens past the last sequence are not computed
-    ht = torch.empty(N, H, K, V, dtype=torch.float32, device=q.device) if output_final_state else None
     rows = _segment_table(bounds, H, WORKGROUPS_PER_CU * _cu_count(q.device), _segment_chunks)
     seg = torch.tensor(rows, dtype=torch.int32).to(q.device, non_blocking=True)
     lib = _lib.load()
-    ws_bytes = int(lib.hmx_gdn_chunk_workspace_bytes(len(rows), N, H))
+    ws_bytes = int(lib.hmx_gdn_chunk_workspace_bytes(len(rows), N, H, int(idx is not None)))
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
     onorm = None
     if o_norm_weight is not None:
@@ -290,10 +357,10 @@ def chunk_gated_delta_rule_gqa(
     elif o_norm_gate is not None:
         raise ValueError("o_norm_gate needs o_norm_weight")
     _lib.call("hmx_gdn_chunk_fwd",
-              _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.dtype_code(q),
+              _lib.ptr(q), q_ts, _lib.ptr(k), k_ts, _lib.ptr(v), v_ts, _lib.dtype_code(q),
               _lib.ptr(g), _lib.dtype_code(g), _lib.ptr(beta), _lib.dtype_code(beta),
-              _lib.ptr(o), _lib.ptr(h0), _lib.ptr(ht),
-              _lib.ptr(seg), len(rows), N, H, HKV, K, V, float(scale),
+              _lib.ptr(o), _lib.ptr(h0), _lib.ptr(ht), st_ss, st_dt, _lib.ptr(idx),
+              _lib.ptr(hinit), _lib.ptr(seg), len(rows), N, H, HKV, K, V, float(scale),
               int(bool(use_qk_l2norm_in_kernel)), MAX_WARM_CHUNKS, DECAY_THRESHOLD,
               _lib.ptr(ws), ws.numel(), onorm, _lib.stream_of(q))
     return o, ht

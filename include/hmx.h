@@ -26,7 +26,9 @@
 extern "C" {
 #endif
 
-#define HMX_ABI_VERSION 2  /* 2: optional hmx_gated_norm output epilogue in the GDN ops */
+#define HMX_ABI_VERSION 3  /* 2: optional hmx_gated_norm output epilogue in the GDN ops;
+                              3: q/k/v token strides in the GDN ops; slot-indexed state
+                              pools and has_initial_state in the GDN prefill */
 
 enum hmx_status {
   HMX_OK = 0,
@@ -75,7 +77,9 @@ int hmx_gdn_gating(const void* A_log, int32_t A_log_dtype,
 
 /*
  * GDN fused recurrent (decode) forward, GQA-native, slot-indexed state pool.
- *  q [B*T, H, K]; k [B*T, HKV, K]; v [B*T, HKV, V] (qkv_dtype, contiguous)
+ *  q [B*T, H, K]; k [B*T, HKV, K]; v [B*T, HKV, V] (qkv_dtype): rows *_token_stride
+ *    elements apart (multiples of 4; 16-byte aligned bases), heads contiguous in a
+ *    row - the column slices of a fused projection pass without a copy
  *  g [B*T, H] (g_dtype); beta [B*T, H] or [B*T, H, V] when beta_headwise
  *  o [B*T, H, V] (qkv_dtype)
  *  h0, ht: state tensors of state_dtype, rows of [H, K, V] with row strides
@@ -90,7 +94,9 @@ int hmx_gdn_gating(const void* A_log, int32_t A_log_dtype,
  *   vllm-inference/src/primed_vllm/gdn/ops/fused_recurrent_gqa.py:227-277
  *   (wrapper :157-224, kernel :25-154).
  */
-int hmx_gdn_recurrent_fwd(const void* q, const void* k, const void* v, int32_t qkv_dtype,
+int hmx_gdn_recurrent_fwd(const void* q, int64_t q_token_stride, const void* k,
+                          int64_t k_token_stride, const void* v, int64_t v_token_stride,
+                          int32_t qkv_dtype,
                           const void* g, int32_t g_dtype,
                           const void* beta, int32_t beta_dtype, int32_t beta_headwise,
                           void* o,
@@ -108,9 +114,18 @@ int hmx_gdn_recurrent_fwd(const void* q, const void* k, const void* v, int32_t q
 /*
  * GDN chunked prefill forward, GQA-native, varlen via a segment table (the kernel
  * walks 32-token chunks; the result is the chunked recurrence at any chunk size).
- *  q [T_total, H, 128]; k, v [T_total, HKV, 128] (bf16, contiguous; T_total = B*T)
- *  g, beta [T_total, H] (f32/bf16/f16); o [T_total, H, 128] (bf16)
- *  h0 [N, H, 128, 128] fp32 or NULL; ht [N, H, 128, 128] fp32 or NULL
+ *  q [T_total, H, 128]; k, v [T_total, HKV, 128] (bf16; T_total = B*T): rows
+ *    *_token_stride elements apart (multiples of 8; 16-byte aligned bases), heads
+ *    contiguous in a row - the column slices of a fused projection pass as views
+ *  g, beta [T_total, H] (f32/bf16/f16); o [T_total, H, 128] (bf16, contiguous)
+ *  h0 / ht: the initial / end states, each a base of [H, 128, 128] slots
+ *    state_slot_stride elements apart in state_dtype (f32 or bf16), or NULL (zero
+ *    start / no end state).  Sequence n uses slot state_indices[n] (n when
+ *    state_indices is NULL); a negative slot starts from zero and writes no end
+ *    state; has_initial_state[n] == 0 (when not NULL) starts from zero.  With
+ *    state_indices h0 and ht may be the same pool (read and written in place:
+ *    the end states of sequences split into segments are staged in the workspace
+ *    and copied into their slots by a last launch).
  *  seg_table: int32 [nseg_total][8] rows (n, bos, eos, c_start, c_end, seg_idx,
  *    first_seg, nseg) - the chunks [c_start, c_end) of sequence n (tokens
  *    [bos, eos)) form segment seg_idx of nseg; rows sorted by sequence, every
@@ -125,9 +140,12 @@ int hmx_gdn_recurrent_fwd(const void* q, const void* k, const void* v, int32_t q
  *   vllm-inference/src/primed_vllm/gdn/ops/chunk_gqa.py:15-83 (and its kernels
  *   wy_fast_gqa.py:19-112, chunk_delta_h_gqa.py:29-215, chunk_o_gqa.py:30-114).
  */
-int hmx_gdn_chunk_fwd(const void* q, const void* k, const void* v, int32_t qkv_dtype,
-                      const void* g, int32_t g_dtype, const void* beta, int32_t beta_dtype,
-                      void* o, const float* h0, float* ht,
+int hmx_gdn_chunk_fwd(const void* q, int64_t q_token_stride, const void* k,
+                      int64_t k_token_stride, const void* v, int64_t v_token_stride,
+                      int32_t qkv_dtype, const void* g, int32_t g_dtype, const void* beta,
+                      int32_t beta_dtype, void* o, const void* h0, void* ht,
+                      int64_t state_slot_stride, int32_t state_dtype,
+                      const int32_t* state_indices, const uint8_t* has_initial_state,
                       const int32_t* seg_table, int32_t nseg_total, int32_t N,
                       int32_t H, int32_t HKV, int32_t K, int32_t V, float scale,
                       int32_t use_qk_l2norm, int32_t max_warm_chunks, float decay_threshold,
@@ -135,9 +153,10 @@ int hmx_gdn_chunk_fwd(const void* q, const void* k, const void* v, int32_t qkv_d
                       void* stream);
 
 /* Workspace bytes hmx_gdn_chunk_fwd needs for a given segment table (host-only
- * arithmetic).  Companion of hmx_gdn_chunk_fwd; no reference counterpart (the
- * reference allocates its intermediates inside the op, chunk_gqa.py:63-81). */
-size_t hmx_gdn_chunk_workspace_bytes(int32_t nseg_total, int32_t N, int32_t H);
+ * arithmetic); pooled != 0 when the call passes state_indices.  Companion of
+ * hmx_gdn_chunk_fwd; no reference counterpart (the reference allocates its
+ * intermediates inside the op, chunk_gqa.py:63-81). */
+size_t hmx_gdn_chunk_workspace_bytes(int32_t nseg_total, int32_t N, int32_t H, int32_t pooled);
 
 /*
  * GKA gating: g = -exp(A_log) * softplus(a + dt_bias), alpha = sigmoid(alpha_in),

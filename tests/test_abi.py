@@ -34,21 +34,22 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_string():
     lib = _lib.load()
-    assert lib.hmx_abi_version() == 2
+    assert lib.hmx_abi_version() == 3
     assert isinstance(lib.hmx_last_error(), bytes)
 
 
 def test_invalid_args_map_to_status_codes():
     """A bad shape is rejected by the C side before any launch (no GPU touched)."""
     lib = _lib.load()
-    rc = lib.hmx_gdn_recurrent_fwd(None, None, None, 1, None, 0, None, 0, 0, None, None, 0, None, 0,
-                                   0, None, None, 0, None, 1, 1, 1, 4, 4, 96, 128, 1.0, 1, 0, None,
-                                   None)
+    rc = lib.hmx_gdn_recurrent_fwd(None, 0, None, 0, None, 0, 1, None, 0, None, 0, 0, None, None,
+                                   0, None, 0, 0, None, None, 0, None, 1, 1, 1, 4, 4, 96, 128, 1.0,
+                                   1, 0, None, None)
     assert rc == _lib.HMX_EUNSUPPORTED
     assert b"K=96" in lib.hmx_last_error()
     with pytest.raises(NotImplementedError):
-        _lib.call("hmx_gdn_recurrent_fwd", None, None, None, 1, None, 0, None, 0, 0, None, None, 0,
-                  None, 0, 0, None, None, 0, None, 1, 1, 1, 4, 4, 96, 128, 1.0, 1, 0, None, None)
+        _lib.call("hmx_gdn_recurrent_fwd", None, 0, None, 0, None, 0, 1, None, 0, None, 0, 0, None,
+                  None, 0, None, 0, 0, None, None, 0, None, 1, 1, 1, 4, 4, 96, 128, 1.0, 1, 0, None,
+                  None)
     with pytest.raises(ValueError):
         _lib.call("hmx_gdn_gating", None, 0, None, 0, 0, None, 0, 0, 1, None, 0, None, None, 1,
                   -1, 4, 1.0, 20.0, None)
