@@ -26,6 +26,7 @@ constexpr int D = 128;
 
 struct Params {
   const void* q; const void* k; const void* v;
+  int64_t q_ts, k_ts, v_ts;           // token strides (elements); heads are D apart
   const void* alpha; int alpha_dt;
   const void* gk; int gk_dt;          // may be null (no decay)
   const void* beta; int beta_dt;      // may be null
@@ -96,9 +97,9 @@ __global__ __launch_bounds__(256) void gka_decode_kernel(Params p) {
     }
   }
   // ---- token inputs
-  const TQ* qp = static_cast<const TQ*>(p.q) + (bos * p.H + h) * D;
-  const TQ* kp = static_cast<const TQ*>(p.k) + (bos * p.HKV + hk) * D;
-  const TQ* vp = static_cast<const TQ*>(p.v) + (bos * p.HKV + hk) * D;
+  const TQ* qp = static_cast<const TQ*>(p.q) + bos * p.q_ts + (int64_t)h * D;
+  const TQ* kp = static_cast<const TQ*>(p.k) + bos * p.k_ts + (int64_t)hk * D;
+  const TQ* vp = static_cast<const TQ*>(p.v) + bos * p.v_ts + (int64_t)hk * D;
   float kr[16], qr[16], kc[4], qc[4], vc[4];
   load_vec<16>(kp + row0, kr);
   load_vec<16>(qp + row0, qr);
@@ -245,7 +246,9 @@ static int dispatch_kv(const Params& p, int64_t N, int kv_dt, hipStream_t s) {
 }  // namespace gkad
 }  // namespace hmx
 
-extern "C" int hmx_gka_decode_fwd(const void* q, const void* k, const void* v, int32_t qkv_dtype,
+extern "C" int hmx_gka_decode_fwd(const void* q, int64_t q_token_stride, const void* k,
+                                  int64_t k_token_stride, const void* v, int64_t v_token_stride,
+                                  int32_t qkv_dtype,
                                   const void* alpha, int32_t alpha_dtype, const void* gk,
                                   int32_t gk_dtype, const void* beta, int32_t beta_dtype, void* o,
                                   const float* h_kk_in, int64_t h_kk_in_row_stride,
@@ -268,7 +271,12 @@ extern "C" int hmx_gka_decode_fwd(const void* q, const void* k, const void* v, i
   HMX_REQUIRE(cu_seqlens || N == B, HMX_EINVAL, "hmx_gka_decode_fwd: N != B without cu_seqlens");
   if (N == 0) return HMX_OK;
   gkad::Params p;
+  HMX_REQUIRE(q_token_stride % 4 == 0 && k_token_stride % 4 == 0 && v_token_stride % 4 == 0 &&
+                  ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) % 16 == 0,
+              HMX_EINVAL, "hmx_gka_decode_fwd: q/k/v token strides must be multiples of 4 "
+              "elements and the bases 16-byte aligned");
   p.q = q; p.k = k; p.v = v;
+  p.q_ts = q_token_stride; p.k_ts = k_token_stride; p.v_ts = v_token_stride;
   p.alpha = alpha; p.alpha_dt = alpha_dtype; p.gk = gk; p.gk_dt = gk_dtype;
   p.beta = beta; p.beta_dt = beta_dtype; p.o = o;
   p.hkk_in = h_kk_in; p.hkk_out = h_kk_out; p.hkk_in_rs = h_kk_in_row_stride;

@@ -85,15 +85,37 @@ static_assert(S_CC < NSC, "scalar slots");
 
 struct SegInfo { int n, bos, eos, c_start, c_end, seg_idx, first_seg, nseg; };
 
+// A state pool: slots of [H, D, D] states, ss elements apart, f32 or bf16; `in`
+// and `out` may be the same pool (read at the start, written at the end).
+struct Pool {
+  const void* in; void* out; int64_t ss; int dt;
+};
+
+__device__ __forceinline__ float pool_ld(const Pool& pl, int64_t i) {
+  return pl.dt == HMX_BF16 ? (float)static_cast<const bf16*>(pl.in)[i]
+                           : static_cast<const float*>(pl.in)[i];
+}
+
+__device__ __forceinline__ void pool_st(const Pool& pl, int64_t i, float x) {
+  if (pl.dt == HMX_BF16) static_cast<bf16*>(pl.out)[i] = (bf16)x;
+  else static_cast<float*>(pl.out)[i] = x;
+}
+
 struct Params {
   const bf16* q; const bf16* k; const bf16* v;
+  int64_t q_ts, k_ts, v_ts;               // token strides (elements); heads are D apart
   const void* alpha; int alpha_dt;
   const void* g; int g_dt;
   const void* gk; int gk_dt;       // null: no h_kk decay
   const void* beta; int beta_dt;   // null: no beta
   bf16* o;
-  const float* hkk0; const float* hkv0;   // [N,H,D,D] or null
-  float* hkk_t; float* hkv_t;             // [N,H,D,D] or null
+  // Sequence n's states: slot sidx[n] (or n) of the h_kk / h_kv pools; a negative
+  // slot or hinit[n] == 0 starts from zero, and a negative slot writes nothing.
+  // Only the combine launch and single-segment workgroups read the pools, so the
+  // last segment may write its end state straight into the slot.
+  Pool hkk, hkv;
+  const int* sidx;                        // [N] or null
+  const uint8_t* hinit;                   // [N] or null
   const int* seg; int nseg_total;
   float* ws_dh; float* ws_ds;             // [nseg][H][D][D] zero-start segment end states
   float* ws_dec;                          // [nseg][H][2]: sum gk, sum g over the segment
@@ -125,17 +147,16 @@ struct Raw {
 
 template <int MODE>
 __device__ __forceinline__ void load_raw(Raw& r, const Params& p, const bf16* qh, const bf16* kh,
-                                         const bf16* vh, int64_t q_rs, int64_t kv_rs, int tok0,
-                                         int nval, int tid, int h) {
+                                         const bf16* vh, int tok0, int nval, int tid, int h) {
 #pragma unroll
   for (int pass = 0; pass < NPASS; ++pass) {
     const int row = pass * RPP + (tid >> 4), f0 = (tid & 15) * 8;
     const bool ok = row < nval;
     const int64_t tok = tok0 + row;
-    r.k[pass] = ok ? *reinterpret_cast<const bf16x8*>(kh + tok * kv_rs + f0) : bf16x8{};
-    r.v[pass] = ok ? *reinterpret_cast<const bf16x8*>(vh + tok * kv_rs + f0) : bf16x8{};
+    r.k[pass] = ok ? *reinterpret_cast<const bf16x8*>(kh + tok * p.k_ts + f0) : bf16x8{};
+    r.v[pass] = ok ? *reinterpret_cast<const bf16x8*>(vh + tok * p.v_ts + f0) : bf16x8{};
     if (MODE == MODE_OUT)
-      r.q[pass] = ok ? *reinterpret_cast<const bf16x8*>(qh + tok * q_rs + f0) : bf16x8{};
+      r.q[pass] = ok ? *reinterpret_cast<const bf16x8*>(qh + tok * p.q_ts + f0) : bf16x8{};
   }
   if (tid < C) {
     const bool ok = tid < nval;
@@ -206,18 +227,23 @@ __global__ __launch_bounds__(NTHR, NW / 4) void gka_chunk_kernel(Params p) {
   }
 
   // ---- initial states ----------------------------------------------------
+  // A split sequence's segments (its first included) start from the workspace
+  // the combine launch filled; a single-segment sequence reads its pool slot.
+  const int64_t slot = p.sidx ? (int64_t)p.sidx[si.n] : si.n;
+  const int64_t hoff = (int64_t)h * D * D;
   f32x4 Hs[8][NCT], Ss[8][NCT];
   {
     const float *hsrc = nullptr, *ssrc = nullptr;
+    bool pooled = false;
     if (MODE == MODE_OUT) {
-      if (si.seg_idx == 0) {
-        if (p.hkk0) hsrc = p.hkk0 + ((int64_t)si.n * H + h) * D * D;
-        if (p.hkv0) ssrc = p.hkv0 + ((int64_t)si.n * H + h) * D * D;
+      if (si.nseg == 1) {
+        pooled = slot >= 0 && (!p.hinit || p.hinit[si.n]);
       } else {
         hsrc = p.ws_h0 + ((int64_t)s_id * H + h) * D * D;
         ssrc = p.ws_s0 + ((int64_t)s_id * H + h) * D * D;
       }
     }
+    const bool ph = pooled && track_h && p.hkk.in, ps = pooled && p.hkv.in;
 #pragma unroll
     for (int rt = 0; rt < 8; ++rt)
 #pragma unroll
@@ -225,12 +251,19 @@ __global__ __launch_bounds__(NTHR, NW / 4) void gka_chunk_kernel(Params p) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int off = (16 * rt + 4 * q4 + v) * D + CW * wave + 16 * ct + l16;
-          Hs[rt][ct][v] = (hsrc && track_h) ? hsrc[off] : 0.f;
-          Ss[rt][ct][v] = ssrc ? ssrc[off] : 0.f;
+          float hx = 0.f, sx = 0.f;
+          if (hsrc) {
+            hx = track_h ? hsrc[off] : 0.f;
+            sx = ssrc[off];
+          }
+          if (ph) hx = pool_ld(p.hkk, slot * p.hkk.ss + hoff + off);
+          if (ps) sx = pool_ld(p.hkv, slot * p.hkv.ss + hoff + off);
+          Hs[rt][ct][v] = hx;
+          Ss[rt][ct][v] = sx;
         }
   }
 
-  const int64_t q_rs = (int64_t)H * D, kv_rs = (int64_t)p.HKV * D;
+  const int64_t o_rs = (int64_t)H * D;
   const bf16* qh = p.q + (int64_t)h * D;
   const bf16* kh = p.k + (int64_t)hk * D;
   const bf16* vh = p.v + (int64_t)hk * D;
@@ -238,7 +271,7 @@ __global__ __launch_bounds__(NTHR, NW / 4) void gka_chunk_kernel(Params p) {
 
   Raw raw;
   if (si.c_start < si.c_end)
-    load_raw<MODE>(raw, p, qh, kh, vh, q_rs, kv_rs, si.bos + si.c_start * C,
+    load_raw<MODE>(raw, p, qh, kh, vh, si.bos + si.c_start * C,
                    min(C, si.eos - (si.bos + si.c_start * C)), tid, h);
 
   for (int c = si.c_start; c < si.c_end; ++c) {
@@ -280,7 +313,7 @@ __global__ __launch_bounds__(NTHR, NW / 4) void gka_chunk_kernel(Params p) {
     }
     if (c + 1 < si.c_end) {
       const int t1 = tok0 + C;
-      load_raw<MODE>(raw, p, qh, kh, vh, q_rs, kv_rs, t1, min(C, si.eos - t1), tid, h);
+      load_raw<MODE>(raw, p, qh, kh, vh, t1, min(C, si.eos - t1), tid, h);
     }
     lds_barrier();
     // per-token scales: s_t = (beta_t+eps)/|k_t| (k~ = s k), iq_t = 1/|q_t|
@@ -737,7 +770,7 @@ __global__ __launch_bounds__(NTHR, NW / 4) void gka_chunk_kernel(Params p) {
             ov[j] = (bf16)y;
           }
         }
-        if (row < nval) *reinterpret_cast<bf16x8*>(oh + (int64_t)(tok0 + row) * q_rs + f0) = ov;
+        if (row < nval) *reinterpret_cast<bf16x8*>(oh + (int64_t)(tok0 + row) * o_rs + f0) = ov;
       }
     }
   }
@@ -745,9 +778,21 @@ __global__ __launch_bounds__(NTHR, NW / 4) void gka_chunk_kernel(Params p) {
   // ---- end states ----------------------------------------------------------
   float *hd = nullptr, *sd = nullptr;
   if (MODE == MODE_OUT) {
-    if (si.seg_idx == si.nseg - 1) {
-      if (p.hkk_t && track_h) hd = p.hkk_t + ((int64_t)si.n * H + h) * D * D;
-      if (p.hkv_t) sd = p.hkv_t + ((int64_t)si.n * H + h) * D * D;
+    if (si.seg_idx == si.nseg - 1 && slot >= 0) {
+      // without the solver (num_iter 0) h_kk is not tracked: a pooled h_kk slot of a
+      // sequence without an initial state is cleared, the others keep their value
+      const bool wh = p.hkk.out && (track_h || (p.hinit && !p.hinit[si.n]));
+      const bool ws_ = p.hkv.out != nullptr;
+#pragma unroll
+      for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int off = (16 * rt + 4 * q4 + v) * D + CW * wave + 16 * ct + l16;
+            if (wh) pool_st(p.hkk, slot * p.hkk.ss + hoff + off, track_h ? Hs[rt][ct][v] : 0.f);
+            if (ws_) pool_st(p.hkv, slot * p.hkv.ss + hoff + off, Ss[rt][ct][v]);
+          }
     }
   } else {
     hd = track_h ? p.ws_dh + ((int64_t)s_id * H + h) * D * D : nullptr;
@@ -780,9 +825,17 @@ __global__ __launch_bounds__(256) void gka_seg_combine_kernel(Params p) {
   }
   if (first < 0 || nseg < 2) return;
   const bool track_h = p.num_iter > 0;
+  const int64_t slot = p.sidx ? (int64_t)p.sidx[n] : n;
+  const bool init = slot >= 0 && (!p.hinit || p.hinit[n]);
+  const int64_t hoff = (int64_t)h * D * D;
   for (int e = blockIdx.y * 256 + threadIdx.x; e < D * D; e += gridDim.y * 256) {
-    float hx = (track_h && p.hkk0) ? p.hkk0[((int64_t)n * H + h) * D * D + e] : 0.f;
-    float sx = p.hkv0 ? p.hkv0[((int64_t)n * H + h) * D * D + e] : 0.f;
+    float hx = (track_h && init && p.hkk.in) ? pool_ld(p.hkk, slot * p.hkk.ss + hoff + e) : 0.f;
+    float sx = (init && p.hkv.in) ? pool_ld(p.hkv, slot * p.hkv.ss + hoff + e) : 0.f;
+    {   // the first segment's start state, so that no OUT workgroup reads the pool
+      const int64_t fb = ((int64_t)first * H + h) * D * D + e;
+      if (track_h) p.ws_h0[fb] = hx;
+      p.ws_s0[fb] = sx;
+    }
     for (int s = 0; s < nseg - 1; ++s) {
       const int64_t b = ((int64_t)(first + s) * H + h);
       const float dk = expf(p.ws_dec[b * 2 + 0]), dg = expf(p.ws_dec[b * 2 + 1]);
@@ -807,12 +860,16 @@ extern "C" size_t hmx_gka_chunk_workspace_bytes(int32_t nseg_total, int32_t N, i
   return 4 * st + (size_t)nseg_total * H * 2 * sizeof(float);
 }
 
-extern "C" int hmx_gka_chunk_fwd(const void* q, const void* k, const void* v, int32_t qkv_dtype,
-                                 const void* alpha, int32_t alpha_dtype, const void* g,
-                                 int32_t g_dtype, const void* gk, int32_t gk_dtype,
+extern "C" int hmx_gka_chunk_fwd(const void* q, int64_t q_token_stride, const void* k,
+                                 int64_t k_token_stride, const void* v, int64_t v_token_stride,
+                                 int32_t qkv_dtype, const void* alpha, int32_t alpha_dtype,
+                                 const void* g, int32_t g_dtype, const void* gk, int32_t gk_dtype,
                                  const void* beta, int32_t beta_dtype, void* o,
-                                 const float* h_kk0, const float* h_kv0, float* h_kk_final,
-                                 float* h_kv_final, const int32_t* seg_table, int32_t nseg_total,
+                                 const void* h_kk0, void* h_kk_final, int64_t h_kk_slot_stride,
+                                 int32_t h_kk_dtype, const void* h_kv0, void* h_kv_final,
+                                 int64_t h_kv_slot_stride, int32_t h_kv_dtype,
+                                 const int32_t* state_indices, const uint8_t* has_initial_state,
+                                 const int32_t* seg_table, int32_t nseg_total,
                                  int32_t N, int32_t H, int32_t HKV, int32_t D_, int32_t V,
                                  int32_t num_iter, float ridge_ratio, float scale,
                                  int32_t use_qk_l2norm, void* workspace, size_t workspace_bytes,
@@ -825,6 +882,12 @@ extern "C" int hmx_gka_chunk_fwd(const void* q, const void* k, const void* v, in
   HMX_REQUIRE(q && k && v && alpha && g && o && seg_table, HMX_EINVAL,
               "hmx_gka_chunk_fwd: null tensor pointer");
   HMX_REQUIRE(num_iter >= 0, HMX_EINVAL, "hmx_gka_chunk_fwd: num_iter=%d", num_iter);
+  HMX_REQUIRE(q_token_stride % 8 == 0 && k_token_stride % 8 == 0 && v_token_stride % 8 == 0 &&
+                  ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)o) % 16 == 0,
+              HMX_EINVAL, "hmx_gka_chunk_fwd: q/k/v/o rows must be 16-byte aligned");
+  HMX_REQUIRE((h_kk_dtype == HMX_F32 || h_kk_dtype == HMX_BF16) &&
+                  (h_kv_dtype == HMX_F32 || h_kv_dtype == HMX_BF16),
+              HMX_EUNSUPPORTED, "hmx_gka_chunk_fwd: state dtypes must be f32 or bf16");
   if (nseg_total == 0) return HMX_OK;
   const size_t need = hmx_gka_chunk_workspace_bytes(nseg_total, N, H);
   HMX_REQUIRE(workspace && workspace_bytes >= need, HMX_EINVAL,
@@ -847,7 +910,10 @@ extern "C" int hmx_gka_chunk_fwd(const void* q, const void* k, const void* v, in
     p.onw = o_norm->weight; p.onw_dt = o_norm->weight_dtype; p.on_eps = o_norm->eps;
   }
   p.o = static_cast<bf16*>(o);
-  p.hkk0 = h_kk0; p.hkv0 = h_kv0; p.hkk_t = h_kk_final; p.hkv_t = h_kv_final;
+  p.q_ts = q_token_stride; p.k_ts = k_token_stride; p.v_ts = v_token_stride;
+  p.hkk = Pool{h_kk0, h_kk_final, h_kk_slot_stride, h_kk_dtype};
+  p.hkv = Pool{h_kv0, h_kv_final, h_kv_slot_stride, h_kv_dtype};
+  p.sidx = state_indices; p.hinit = has_initial_state;
   p.seg = seg_table; p.nseg_total = nseg_total;
   p.H = H; p.HKV = HKV; p.num_iter = num_iter; p.ridge_ratio = ridge_ratio; p.scale = scale;
   p.l2norm = use_qk_l2norm;

@@ -18,7 +18,7 @@ import logging
 import torch
 
 from .. import _lib
-from .gdn import _cu_count, _gate_rows, _i32, _segment_table
+from .gdn import _cu_count, _gate_rows, _i32, _segment_table, _token_rows
 
 GKA_WORKGROUPS_PER_CU = 1
 _warned_num_iter_zero = False
@@ -99,7 +99,8 @@ def chebyshev_iteration_gqa(k, q, v, alpha, gk=None, beta=None, num_iter: int = 
         if tuple(st.shape[1:]) != (H, D, last) or not st[0].is_contiguous():
             raise ValueError(f"state must be [rows,{H},{D},{last}] with contiguous rows, "
                              f"got {tuple(st.shape)}")
-    q, k, v, alpha = (x.contiguous() for x in (q, k, v, alpha))
+    alpha = alpha.contiguous()
+    (q, q_ts), (k, k_ts), (v, v_ts) = (_token_rows(x, 4) for x in (q, k, v))
     gk = None if gk is None else gk.contiguous()
     beta = None if beta is None else beta.contiguous()
     if inplace_final_state:
@@ -110,7 +111,7 @@ def chebyshev_iteration_gqa(k, q, v, alpha, gk=None, beta=None, num_iter: int = 
     o = q.new_empty(B, T, H, V)
     onorm = _onorm(o_norm_weight, o_norm_gate, o_norm_eps, (B, T, H, V), q.dtype)
     _lib.call("hmx_gka_decode_fwd",
-              _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.dtype_code(q),
+              _lib.ptr(q), q_ts, _lib.ptr(k), k_ts, _lib.ptr(v), v_ts, _lib.dtype_code(q),
               _lib.ptr(alpha), _lib.dtype_code(alpha),
               _lib.ptr(gk), 0 if gk is None else _lib.dtype_code(gk),
               _lib.ptr(beta), 0 if beta is None else _lib.dtype_code(beta),
@@ -158,21 +159,36 @@ def gka_chebyshev_gla_prefill(q, k, v, alpha, g, gk, beta, gla_scale: float,
                               num_iter: int = 30, gka=None, h_kk_initial=None, h_kv_initial=None,
                               output_final_state: bool = True, cu_seqlens=None, *,
                               o_norm_weight=None, o_norm_gate=None, o_norm_eps: float = 1e-6,
+                              ssm_state_indices=None, has_initial_state=None, out=None,
                               _segment_chunks: int | None = None):
     """Full GKA prefill: Chebyshev query refinement + beta^2 simple GLA
     (gka_forward.py:161-242).  Returns (o, h_kk_final, h_kv_final); h_kk_final is
     None when num_iter == 0 or not output_final_state.
 
-    Keyword-only extension (no reference counterpart): ``o_norm_weight`` [V] (and
-    optionally ``o_norm_gate`` [B,T,H,V], q.dtype) returns the layer's gated
-    RMSNorm ``o_norm(o, z)`` (primed_gka_layer.py:944-949) computed in the
-    kernel's output epilogue instead of o."""
+    Keyword-only extensions (no reference counterpart):
+
+    - ``o_norm_weight`` [V] (and optionally ``o_norm_gate`` [B,T,H,V], q.dtype)
+      returns the layer's gated RMSNorm ``o_norm(o, z)`` (primed_gka_layer.py:944-949)
+      computed in the kernel's output epilogue instead of o.
+    - ``ssm_state_indices`` [N]: ``h_kk_initial`` / ``h_kv_initial`` are the layer's
+      state pools [slots,H,D,D] (fp32 or bf16); sequence n starts from slot
+      ``ssm_state_indices[n]`` and, with ``output_final_state``, its end states are
+      written back into that slot in place (the pools are returned).  This replaces
+      the layer's gather / zero / scatter (primed_gka_layer.py:1245-1266); with
+      num_iter == 0 a sequence without an initial state clears its h_kk slot, as
+      that update does.  A negative slot starts from zero and writes nothing.
+    - ``has_initial_state`` [N] bool: sequences with False start from zero.
+    - ``out`` [B,T,H,V] (q.dtype, contiguous): o is written there.
+
+    q, k and v may be the column slices of one fused projection: they are read in
+    place."""
     _check_sketching_constraints(gka, num_sketches_per_head, "gka_chebyshev_gla_prefill")
     if cu_seqlens is not None and q.shape[0] != 1:
         raise ValueError(f"Batch size must be 1 when using cu_seqlens, got {q.shape[0]}")
     return _gka_prefill(q, k, v, alpha, g, gk, beta, gla_scale, ridge_ratio, num_iter,
                         h_kk_initial, h_kv_initial, output_final_state, cu_seqlens, True,
-                        _segment_chunks, (o_norm_weight, o_norm_gate, o_norm_eps))
+                        _segment_chunks, (o_norm_weight, o_norm_gate, o_norm_eps),
+                        ssm_state_indices, has_initial_state, out)
 
 
 def _onorm(weight, gate, eps, shape, dtype):
@@ -188,8 +204,9 @@ def _onorm(weight, gate, eps, shape, dtype):
 
 def _gka_prefill(q, k, v, alpha, g, gk, beta, gla_scale, ridge_ratio, num_iter, h_kk_initial,
                  h_kv_initial, output_final_state, cu_seqlens, l2norm, segment_chunks=None,
-                 o_norm=(None, None, 1e-6)):
-    _lib.require_gpu(q, k, v, alpha, g, gk, beta, h_kk_initial, h_kv_initial, cu_seqlens)
+                 o_norm=(None, None, 1e-6), state_indices=None, has_initial_state=None, out=None):
+    _lib.require_gpu(q, k, v, alpha, g, gk, beta, h_kk_initial, h_kv_initial, cu_seqlens,
+                     state_indices, has_initial_state, out)
     B, T, H, D = q.shape
     HKV, V = k.shape[2], v.shape[-1]
     if cu_seqlens is None:
@@ -198,35 +215,71 @@ def _gka_prefill(q, k, v, alpha, g, gk, beta, gla_scale, ridge_ratio, num_iter, 
         cs = [int(x) for x in cu_seqlens.tolist()]
         bounds = [(cs[n], cs[n + 1]) for n in range(len(cs) - 1)]
     N = len(bounds)
-    for st, last, name in ((h_kk_initial, D, "h_kk_initial"), (h_kv_initial, V, "h_kv_initial")):
-        if st is not None and tuple(st.shape) != (N, H, D, last):
-            raise ValueError(f"{name} must be [{N},{H},{D},{last}], got {tuple(st.shape)}")
-    q, k, v, alpha, g = (x.contiguous() for x in (q, k, v, alpha, g))
+    idx = None
+    if state_indices is not None:
+        idx = _i32(state_indices)
+        if idx.shape != (N,):
+            raise ValueError(f"ssm_state_indices must hold {N} slots, got {tuple(idx.shape)}")
+        pools = []
+        for st, last, name in ((h_kk_initial, D, "h_kk_initial"),
+                               (h_kv_initial, V, "h_kv_initial")):
+            if (st is None or st.dim() != 4 or tuple(st.shape[1:]) != (H, D, last)
+                    or not st[0].is_contiguous() or st.dtype not in (torch.float32, torch.bfloat16)):
+                raise ValueError(f"{name} must be the state pool [slots,{H},{D},{last}] fp32/bf16 "
+                                 f"with contiguous slots")
+            pools.append(st)
+        hkk0, hkv0 = pools
+        hkk_t = hkk0 if output_final_state else None
+        hkv_t = hkv0 if output_final_state else None
+        ss_kk, dt_kk = hkk0.stride(0), _lib.dtype_code(hkk0)
+        ss_kv, dt_kv = hkv0.stride(0), _lib.dtype_code(hkv0)
+    else:
+        for st, last, name in ((h_kk_initial, D, "h_kk_initial"),
+                               (h_kv_initial, V, "h_kv_initial")):
+            if st is not None and tuple(st.shape) != (N, H, D, last):
+                raise ValueError(f"{name} must be [{N},{H},{D},{last}], got {tuple(st.shape)}")
+        hkk0 = None if h_kk_initial is None else h_kk_initial.to(torch.float32).contiguous()
+        hkv0 = None if h_kv_initial is None else h_kv_initial.to(torch.float32).contiguous()
+        hkk_t = (torch.empty(N, H, D, D, dtype=torch.float32, device=q.device)
+                 if output_final_state and num_iter > 0 else None)
+        hkv_t = (torch.empty(N, H, D, V, dtype=torch.float32, device=q.device)
+                 if output_final_state else None)
+        ss_kk, dt_kk, ss_kv, dt_kv = H * D * D, _lib.HMX_F32, H * D * V, _lib.HMX_F32
+    hinit = None
+    if has_initial_state is not None:
+        if has_initial_state.shape != (N,):
+            raise ValueError(f"has_initial_state must be [{N}], got {tuple(has_initial_state.shape)}")
+        hinit = has_initial_state.to(torch.uint8).contiguous()
+    alpha, g = alpha.contiguous(), g.contiguous()
+    (q, q_ts), (k, k_ts), (v, v_ts) = (_token_rows(x, 8) for x in (q, k, v))
     gk = None if gk is None else gk.contiguous()
     beta = None if beta is None else beta.contiguous()
-    hkk0 = None if h_kk_initial is None else h_kk_initial.to(torch.float32).contiguous()
-    hkv0 = None if h_kv_initial is None else h_kv_initial.to(torch.float32).contiguous()
-    o = torch.empty(B, T, H, V, dtype=q.dtype, device=q.device)
+    if out is not None:
+        if (tuple(out.shape) != (B, T, H, V) or out.dtype != q.dtype or not out.is_contiguous()
+                or out.data_ptr() % 16):
+            raise ValueError(f"out must be a contiguous [{B},{T},{H},{V}] {q.dtype} tensor")
+        o = out
+    else:
+        o = torch.empty(B, T, H, V, dtype=q.dtype, device=q.device)
     if cu_seqlens is not None and bounds and bounds[-1][1] < T:
         o[:, bounds[-1][1]:].zero_()
-    hkk_t = (torch.empty(N, H, D, D, dtype=torch.float32, device=q.device)
-             if output_final_state and num_iter > 0 else None)
-    hkv_t = (torch.empty(N, H, D, V, dtype=torch.float32, device=q.device)
-             if output_final_state else None)
     rows = _segment_table(bounds, H, GKA_WORKGROUPS_PER_CU * _cu_count(q.device), segment_chunks)
     seg = torch.tensor(rows, dtype=torch.int32).to(q.device, non_blocking=True)
     lib = _lib.load()
     ws_bytes = int(lib.hmx_gka_chunk_workspace_bytes(len(rows), N, H))
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=q.device)
     _lib.call("hmx_gka_chunk_fwd",
-              _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.dtype_code(q),
+              _lib.ptr(q), q_ts, _lib.ptr(k), k_ts, _lib.ptr(v), v_ts, _lib.dtype_code(q),
               _lib.ptr(alpha), _lib.dtype_code(alpha), _lib.ptr(g), _lib.dtype_code(g),
               _lib.ptr(gk), 0 if gk is None else _lib.dtype_code(gk),
               _lib.ptr(beta), 0 if beta is None else _lib.dtype_code(beta),
-              _lib.ptr(o), _lib.ptr(hkk0), _lib.ptr(hkv0), _lib.ptr(hkk_t), _lib.ptr(hkv_t),
+              _lib.ptr(o), _lib.ptr(hkk0), _lib.ptr(hkk_t), ss_kk, dt_kk,
+              _lib.ptr(hkv0), _lib.ptr(hkv_t), ss_kv, dt_kv, _lib.ptr(idx), _lib.ptr(hinit),
               _lib.ptr(seg), len(rows), N, H, HKV, D, V, int(num_iter), float(ridge_ratio),
               float(gla_scale), int(bool(l2norm)), _lib.ptr(ws), ws.numel(),
               _onorm(*o_norm, tuple(o.shape), q.dtype), _lib.stream_of(q))
+    if idx is not None and num_iter == 0:
+        return o, None, hkv_t
     return o, hkk_t, hkv_t
 
 

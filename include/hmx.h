@@ -27,8 +27,9 @@ extern "C" {
 #endif
 
 #define HMX_ABI_VERSION 3  /* 2: optional hmx_gated_norm output epilogue in the GDN ops;
-                              3: q/k/v token strides in the GDN ops; slot-indexed state
-                              pools and has_initial_state in the GDN prefill */
+                              3: q/k/v token strides in the GDN and GKA ops; slot-indexed
+                              state pools and has_initial_state in the GDN and GKA
+                              prefills */
 
 enum hmx_status {
   HMX_OK = 0,
@@ -177,6 +178,8 @@ int hmx_gka_gating(const void* A_log, int32_t A_log_dtype,
 /*
  * GKA decode step (first token of each sequence), in place on slot-indexed pools.
  *  q [B*T, H, 128]; k, v [B*T, HKV, 128] (qkv_dtype); alpha [B*T, H];
+ *  q/k/v rows *_token_stride elements apart (multiples of 4; 16-byte aligned bases),
+ *  heads contiguous in a row (column slices of a fused projection pass as views)
  *  gk, beta [B*T, H] or NULL; o [B*T, H, 128] (qkv_dtype; first token per sequence)
  *  h_kk_in/out fp32 rows of [H, 128, 128] (row strides in elements; in == out for
  *  the in-place update); h_kv_in/out rows of [H, 128, 128] in h_kv_dtype (f32/bf16).
@@ -186,7 +189,9 @@ int hmx_gka_gating(const void* A_log, int32_t A_log_dtype,
  *   vllm-inference/src/primed_vllm/gka/ops/chebyshev_iteration_gqa.py:173-238 (kernel :22-170),
  *   vllm-inference/src/primed_vllm/gka/gka_forward.py:248-326.
  */
-int hmx_gka_decode_fwd(const void* q, const void* k, const void* v, int32_t qkv_dtype,
+int hmx_gka_decode_fwd(const void* q, int64_t q_token_stride, const void* k,
+                       int64_t k_token_stride, const void* v, int64_t v_token_stride,
+                       int32_t qkv_dtype,
                        const void* alpha, int32_t alpha_dtype,
                        const void* gk, int32_t gk_dtype, const void* beta, int32_t beta_dtype,
                        void* o,
@@ -204,12 +209,20 @@ int hmx_gka_decode_fwd(const void* q, const void* k, const void* v, int32_t qkv_
  * GKA chunked prefill forward (Chebyshev ridge solve + beta^2 GLA), GQA-native,
  * varlen via the same segment table layout as hmx_gdn_chunk_fwd (chunks of 32
  * tokens).  q [T_total, H, 128]; k, v [T_total, HKV, 128] bf16 (raw: q and k are
- * L2-normalised inside, without eps); alpha, g [T_total, H]; gk, beta
- * [T_total, H] or NULL; o [T_total, H, 128] bf16.  use_qk_l2norm = 0 uses q and k
- * as given (the training form, whose layer normalises them and applies beta to
- * k and v).  h_kk0 / h_kv0 fp32
- * [N, H, 128, 128] or NULL; h_kk_final / h_kv_final fp32 [N, H, 128, 128] or
- * NULL (h_kk_final is not written when num_iter == 0).
+ * L2-normalised inside, without eps), rows *_token_stride elements apart
+ * (multiples of 8; 16-byte aligned bases), heads contiguous in a row; alpha, g
+ * [T_total, H]; gk, beta [T_total, H] or NULL; o [T_total, H, 128] bf16
+ * (contiguous).  use_qk_l2norm = 0 uses q and k as given (the training form, whose
+ * layer normalises them and applies beta to k and v).
+ * States: h_kk0 / h_kk_final (and h_kv0 / h_kv_final) are bases of [H, 128, 128]
+ * slots h_kk_slot_stride (h_kv_slot_stride) elements apart in h_kk_dtype
+ * (h_kv_dtype), f32 or bf16, or NULL (zero start / no end state).  Sequence n
+ * uses slot state_indices[n] (n when NULL); a negative slot starts from zero and
+ * writes nothing; has_initial_state[n] == 0 (when not NULL) starts from zero.
+ * Initial and final bases may be the same pool (updated in place).  h_kk is not
+ * tracked when num_iter == 0: its end state is then not written, except that a
+ * sequence with has_initial_state[n] == 0 clears its h_kk slot (as the layer's
+ * update does, primed_gka_layer.py:1262-1265, :1296-1299).
  * workspace: hmx_gka_chunk_workspace_bytes(...) bytes of device scratch.
  * Replaces: gka_chebyshev_gla_prefill
  *   vllm-inference/src/primed_vllm/gka/gka_forward.py:161-242 (and its kernels
@@ -219,11 +232,15 @@ int hmx_gka_decode_fwd(const void* q, const void* k, const void* v, int32_t qkv_
  *   (training/src/hmf/model/hybrid_zoo/layers/gated_kalmanet/ops/chebyshev/
  *   gka_chebyshev_solve.py:107-164, :324-397).
  */
-int hmx_gka_chunk_fwd(const void* q, const void* k, const void* v, int32_t qkv_dtype,
-                      const void* alpha, int32_t alpha_dtype, const void* g, int32_t g_dtype,
-                      const void* gk, int32_t gk_dtype, const void* beta, int32_t beta_dtype,
-                      void* o, const float* h_kk0, const float* h_kv0,
-                      float* h_kk_final, float* h_kv_final,
+int hmx_gka_chunk_fwd(const void* q, int64_t q_token_stride, const void* k,
+                      int64_t k_token_stride, const void* v, int64_t v_token_stride,
+                      int32_t qkv_dtype, const void* alpha, int32_t alpha_dtype, const void* g,
+                      int32_t g_dtype, const void* gk, int32_t gk_dtype, const void* beta,
+                      int32_t beta_dtype, void* o,
+                      const void* h_kk0, void* h_kk_final, int64_t h_kk_slot_stride,
+                      int32_t h_kk_dtype, const void* h_kv0, void* h_kv_final,
+                      int64_t h_kv_slot_stride, int32_t h_kv_dtype,
+                      const int32_t* state_indices, const uint8_t* has_initial_state,
                       const int32_t* seg_table, int32_t nseg_total, int32_t N,
                       int32_t H, int32_t HKV, int32_t D, int32_t V,
                       int32_t num_iter, float ridge_ratio, float scale, int32_t use_qk_l2norm,
