@@ -55,8 +55,16 @@ struct Params {
   const float* dt_bias;    // [H] or null
   const bf16* z; int64_t z_ts, z_hs;   // or null
   bf16* y; int64_t y_ts, y_hs;
-  const float* h0;         // [nseq][H][P][N] or null
-  float* hT;               // [nseq][H][P][N] or null
+  // Sequence n's state: slot sidx[n] (or n) of the h0 / hT bases ([H][P][N] slots
+  // st_ss elements apart, f32 or bf16; they may be one pool).  A negative slot or
+  // hinit[n] == 0 starts from zero; a negative slot writes nothing.  Only the
+  // combine launch and single-segment workgroups read h0, so the last segment
+  // writes its end state straight into the slot.
+  const void* h0;          // or null
+  void* hT;                // or null
+  int64_t st_ss; int st_dt;
+  const int* sidx;         // [nseq] or null
+  const uint8_t* hinit;    // [nseq] or null
   const int* seg; int nseg_total;
   float* ws_loc;           // [nseg][H][P][N] zero-start segment end states
   float* ws_s0;            // [nseg][H][P][N] segment start states
@@ -185,13 +193,19 @@ __global__ __launch_bounds__(NTHR, 2) void ssd_chunk_kernel(Params p) {
 
   // ---- initial state S^T: tile (nb, i) holds rows n = 16nb+4q4+v, column
   // p = 16(PB wave + i) + l16 --------------------------------------------------
+  const int64_t slot = p.sidx ? (int64_t)p.sidx[si.n] : si.n;
+  const int64_t soff = slot * p.st_ss + (int64_t)h * P * N;
   f32x4 ST[NB][PB];
   {
     const float* src = nullptr;
+    const bf16* src16 = nullptr;
     if (MODE == MODE_OUT) {
-      if (si.seg_idx == 0) {
-        if (p.h0) src = p.h0 + ((int64_t)si.n * H + h) * P * N;
-      } else {
+      if (si.nseg == 1) {
+        if (p.h0 && slot >= 0 && (!p.hinit || p.hinit[si.n])) {
+          if (p.st_dt == HMX_BF16) src16 = static_cast<const bf16*>(p.h0) + soff;
+          else src = static_cast<const float*>(p.h0) + soff;
+        }
+      } else {   // split: every segment's start state comes from the combine launch
         src = p.ws_s0 + ((int64_t)s_id * H + h) * P * N;
       }
     }
@@ -200,8 +214,14 @@ __global__ __launch_bounds__(NTHR, 2) void ssd_chunk_kernel(Params p) {
 #pragma unroll
       for (int i = 0; i < PB; ++i) {
         const int pc = 16 * (PB * wave + i) + l16;
-        ST[nb][i] = src ? *reinterpret_cast<const f32x4*>(src + (int64_t)pc * N + 16 * nb + 4 * q4)
-                        : f32x4{0.f, 0.f, 0.f, 0.f};
+        const int64_t e = (int64_t)pc * N + 16 * nb + 4 * q4;
+        f32x4 x = {0.f, 0.f, 0.f, 0.f};
+        if (src) x = *reinterpret_cast<const f32x4*>(src + e);
+        if (src16) {
+          const bf16x4 b = *reinterpret_cast<const bf16x4*>(src16 + e);
+          x = f32x4{(float)b[0], (float)b[1], (float)b[2], (float)b[3]};
+        }
+        ST[nb][i] = x;
       }
   }
   float dsum = 0.f;   // segment log-decay (LOCAL)
@@ -471,24 +491,31 @@ __global__ __launch_bounds__(NTHR, 2) void ssd_chunk_kernel(Params p) {
 
   // ---- segment end state --------------------------------------------------------
   float* dst = nullptr;
+  bf16* dst16 = nullptr;
   if (MODE == MODE_LOCAL) {
     dst = p.ws_loc + ((int64_t)s_id * H + h) * P * N;
     if (tid == 0) p.ws_dec[(int64_t)s_id * H + h] = dsum;
-  } else if (si.seg_idx == si.nseg - 1 && p.hT) {
-    dst = p.hT + ((int64_t)si.n * H + h) * P * N;
+  } else if (si.seg_idx == si.nseg - 1 && p.hT && slot >= 0) {
+    if (p.st_dt == HMX_BF16) dst16 = static_cast<bf16*>(p.hT) + soff;
+    else dst = static_cast<float*>(p.hT) + soff;
   }
-  if (dst) {
+  if (dst || dst16) {
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
       for (int i = 0; i < PB; ++i) {
         const int pc = 16 * (PB * wave + i) + l16;
-        *reinterpret_cast<f32x4*>(dst + (int64_t)pc * N + 16 * nb + 4 * q4) = ST[nb][i];
+        const int64_t e = (int64_t)pc * N + 16 * nb + 4 * q4;
+        const f32x4 x = ST[nb][i];
+        if (dst) *reinterpret_cast<f32x4*>(dst + e) = x;
+        else *reinterpret_cast<bf16x4*>(dst16 + e) = bf16x4{(bf16)x[0], (bf16)x[1], (bf16)x[2],
+                                                             (bf16)x[3]};
       }
   }
 }
 
 // Segment start states: S0[first] = h0 (or 0); S0[s+1] = e^{dec[s]} S0[s] + loc[s].
+// One workgroup row per split (sequence, head); single-segment sequences return.
 __global__ __launch_bounds__(256) void ssd_seg_combine_kernel(Params p, int PN) {
   const int nh = blockIdx.x, H = p.H;
   const int n = nh / H, h = nh % H;
@@ -498,8 +525,15 @@ __global__ __launch_bounds__(256) void ssd_seg_combine_kernel(Params p, int PN) 
     if (si.n == n) { first = si.first_seg; nseg = si.nseg; break; }
   }
   if (first < 0 || nseg < 2) return;
+  const int64_t slot = p.sidx ? (int64_t)p.sidx[n] : n;
+  const bool init = p.h0 && slot >= 0 && (!p.hinit || p.hinit[n]);
+  const int64_t soff = slot * p.st_ss + (int64_t)h * PN;
   for (int e = blockIdx.y * 256 + threadIdx.x; e < PN; e += gridDim.y * 256) {
-    float sx = p.h0 ? p.h0[((int64_t)n * H + h) * PN + e] : 0.f;
+    float sx = 0.f;
+    if (init)
+      sx = p.st_dt == HMX_BF16 ? (float)static_cast<const bf16*>(p.h0)[soff + e]
+                               : static_cast<const float*>(p.h0)[soff + e];
+    p.ws_s0[((int64_t)first * H + h) * PN + e] = sx;   // no OUT workgroup reads h0
     for (int s = 0; s < nseg - 1; ++s) {
       const int64_t b = (int64_t)(first + s) * H + h;
       sx = sx * expf(p.ws_dec[b]) + p.ws_loc[b * PN + e];
@@ -538,8 +572,10 @@ extern "C" int hmx_ssd_chunk_fwd(const void* x, int64_t x_ts, int64_t x_hs, cons
                                  int64_t c_gs, int32_t xbc_dtype, const void* dt, int32_t dt_dtype,
                                  int64_t dt_ts, int64_t dt_hs, const float* A, const float* D,
                                  const float* dt_bias, const void* z, int64_t z_ts, int64_t z_hs,
-                                 void* y, int64_t y_ts, int64_t y_hs, const float* h0,
-                                 float* h_final, const int32_t* seg_table, int32_t nseg_total,
+                                 void* y, int64_t y_ts, int64_t y_hs, const void* h0,
+                                 void* h_final, int64_t state_slot_stride, int32_t state_dtype,
+                                 const int32_t* state_indices, const uint8_t* has_initial_state,
+                                 const int32_t* seg_table, int32_t nseg_total,
                                  int32_t nseq, int32_t H, int32_t G, int32_t P, int32_t N,
                                  int32_t dt_softplus, float dt_min, float dt_max, void* workspace,
                                  size_t workspace_bytes, void* stream) {
@@ -557,6 +593,10 @@ extern "C" int hmx_ssd_chunk_fwd(const void* x, int64_t x_ts, int64_t x_hs, cons
   for (int64_t st : strides)
     HMX_REQUIRE(st % 8 == 0, HMX_EINVAL,
                 "hmx_ssd_chunk_fwd: token/head strides must be multiples of 8 elements");
+  HMX_REQUIRE(!(h0 || h_final) || ((state_dtype == HMX_F32 || state_dtype == HMX_BF16) &&
+                                    state_slot_stride % 4 == 0 &&
+                                    ((uintptr_t)h0 | (uintptr_t)h_final) % 16 == 0),
+              HMX_EINVAL, "hmx_ssd_chunk_fwd: states must be f32/bf16 with 16-byte aligned slots");
   if (nseg_total == 0) return HMX_OK;
   const size_t need = hmx_ssd_chunk_workspace_bytes(nseg_total, nseq, H, P, N);
   HMX_REQUIRE(workspace && workspace_bytes >= need, HMX_EINVAL,
@@ -569,7 +609,8 @@ extern "C" int hmx_ssd_chunk_fwd(const void* x, int64_t x_ts, int64_t x_hs, cons
   p.A = A; p.D = D; p.dt_bias = dt_bias;
   p.z = static_cast<const bf16*>(z); p.z_ts = z_ts; p.z_hs = z_hs;
   p.y = static_cast<bf16*>(y); p.y_ts = y_ts; p.y_hs = y_hs;
-  p.h0 = h0; p.hT = h_final;
+  p.h0 = h0; p.hT = h_final; p.st_ss = state_slot_stride; p.st_dt = state_dtype;
+  p.sidx = state_indices; p.hinit = has_initial_state;
   p.seg = seg_table; p.nseg_total = nseg_total;
   const bool multi = nseg_total > nseq;
   const size_t st = (size_t)nseg_total * H * P * N;

@@ -41,10 +41,12 @@ def _prep3(t: torch.Tensor) -> torch.Tensor:
 
 
 def _ssd_scan(x, dt, A, B, C, D, z, dt_bias, dt_softplus, dt_limit, bounds, h0, y,
-              want_final: bool, segment_chunks=None):
+              want_final: bool, segment_chunks=None, pooled=None):
     """Core launcher over flattened tokens.  x, z, y [T,H,P]; dt [T,H]; B, C [T,G,N];
     bounds: list of (bos, eos); h0 fp32 [nseq,H,P,N] or None.  Returns the fp32 end
-    states [nseq,H,P,N] (or None)."""
+    states [nseq,H,P,N] (or None).  ``pooled`` = (pool, slot indices, has_initial_state
+    or None): sequences read and (with want_final) write the pool's slots in place
+    instead, and the pool is returned."""
     T, H, P = x.shape
     G, N = B.shape[1], B.shape[2]
     if x.dtype != torch.bfloat16 or B.dtype != torch.bfloat16 or C.dtype != torch.bfloat16:
@@ -65,7 +67,15 @@ def _ssd_scan(x, dt, A, B, C, D, z, dt_bias, dt_softplus, dt_limit, bounds, h0, 
               else D.to(torch.float32)).contiguous()
     bias = None if dt_bias is None else dt_bias.to(torch.float32).contiguous()
     nseq = len(bounds)
-    hT = torch.empty(nseq, H, P, N, dtype=torch.float32, device=x.device) if want_final else None
+    idx = hinit = None
+    if pooled is not None:
+        pool, idx, hinit = pooled
+        h0, hT = pool, (pool if want_final else None)
+        st_ss, st_dt = pool.stride(0), _lib.dtype_code(pool)
+    else:
+        hT = (torch.empty(nseq, H, P, N, dtype=torch.float32, device=x.device)
+              if want_final else None)
+        st_ss, st_dt = H * P * N, _lib.HMX_F32
     rows = _segment_table(bounds, H, SSD_WORKGROUPS_PER_CU * _cu_count(x.device), segment_chunks,
                           chunk=SSD_CHUNK)
     seg = torch.tensor(rows, dtype=torch.int32).to(x.device, non_blocking=True)
@@ -79,7 +89,8 @@ def _ssd_scan(x, dt, A, B, C, D, z, dt_bias, dt_softplus, dt_limit, bounds, h0, 
               _lib.ptr(dt), _lib.dtype_code(dt), dt.stride(0), dt.stride(1),
               _lib.ptr(A32), _lib.ptr(Dm), _lib.ptr(bias),
               _lib.ptr(z), 0 if z is None else z.stride(0), 0 if z is None else z.stride(1),
-              _lib.ptr(y), y.stride(0), y.stride(1), _lib.ptr(h0), _lib.ptr(hT),
+              _lib.ptr(y), y.stride(0), y.stride(1), _lib.ptr(h0), _lib.ptr(hT), st_ss, st_dt,
+              _lib.ptr(idx), _lib.ptr(hinit),
               _lib.ptr(seg), len(rows), nseq, H, G, P, N, int(bool(dt_softplus)), lo, hi,
               _lib.ptr(ws), ws.numel(), _lib.stream_of(x))
     return hT
@@ -173,6 +184,7 @@ def mamba_chunk_scan_combined_varlen(x, dt, A, B, C, chunk_size, cu_seqlens, cu_
                                      z=None, dt_bias=None, initial_states=None, dt_softplus=False,
                                      dt_limit=(0.0, float("inf")),
                                      return_intermediate_states=False, state_dtype=None, *,
+                                     ssm_state_indices=None, has_initial_state=None,
                                      _segment_chunks: int | None = None):
     """vLLM ``mamba_chunk_scan_combined_varlen`` (call site primed_mamba2_layer.py:844-863).
 
@@ -183,6 +195,14 @@ def mamba_chunk_scan_combined_varlen(x, dt, A, B, C, chunk_size, cu_seqlens, cu_
     last_chunk_indices and seq_idx are chunking metadata derived from
     cu_seqlens; the kernel uses its own 64-token chunks.  Per-chunk
     (return_intermediate_states) output is not supported.
+
+    Keyword-only extension (no reference counterpart): with ``ssm_state_indices``
+    [n], ``initial_states`` is the layer's state pool [slots,H,P,N] (fp32 or bf16):
+    sequence i starts from slot ``ssm_state_indices[i]`` (zero where
+    ``has_initial_state`` [n] is False or the slot is negative) and its end state
+    is written back into that slot in place; the pool is returned.  This replaces
+    the layer's gather and scatter around the op (primed_mamba2_layer.py:812-824,
+    :941).
     """
     if return_intermediate_states:
         raise NotImplementedError("return_intermediate_states (prefix-cache chunk states) is "
@@ -192,16 +212,38 @@ def mamba_chunk_scan_combined_varlen(x, dt, A, B, C, chunk_size, cu_seqlens, cu_
     N = B.shape[-1]
     cs = [int(v) for v in cu_seqlens.tolist()]
     bounds = [(cs[i], cs[i + 1]) for i in range(len(cs) - 1)]
-    if initial_states is not None and tuple(initial_states.shape) != (len(bounds), H, P, N):
-        raise ValueError(f"initial_states must be {(len(bounds), H, P, N)}, "
-                         f"got {tuple(initial_states.shape)}")
-    h0 = None if initial_states is None else initial_states.to(torch.float32).contiguous()
+    pooled = h0 = None
+    if ssm_state_indices is not None:
+        _lib.require_gpu(ssm_state_indices, has_initial_state)
+        pool = initial_states
+        if (pool is None or pool.dim() != 4 or tuple(pool.shape[1:]) != (H, P, N)
+                or not pool[0].is_contiguous() or pool.dtype not in (torch.float32, torch.bfloat16)):
+            raise ValueError(f"with ssm_state_indices, initial_states must be the state pool "
+                             f"[slots,{H},{P},{N}] fp32/bf16 with contiguous slots")
+        idx = ssm_state_indices.to(torch.int32).contiguous()
+        if idx.shape != (len(bounds),):
+            raise ValueError(f"ssm_state_indices must hold {len(bounds)} slots")
+        hinit = None
+        if has_initial_state is not None:
+            if has_initial_state.shape != (len(bounds),):
+                raise ValueError(f"has_initial_state must be [{len(bounds)}]")
+            hinit = has_initial_state.to(torch.uint8).contiguous()
+        pooled = (pool, idx, hinit)
+    else:
+        if initial_states is not None and tuple(initial_states.shape) != (len(bounds), H, P, N):
+            raise ValueError(f"initial_states must be {(len(bounds), H, P, N)}, "
+                             f"got {tuple(initial_states.shape)}")
+        if has_initial_state is not None:
+            raise ValueError("has_initial_state needs ssm_state_indices")
+        h0 = None if initial_states is None else initial_states.to(torch.float32).contiguous()
     if out is None:
         out = torch.empty(T, H, P, dtype=x.dtype, device=x.device)
     if out.dtype != x.dtype:
         raise ValueError(f"out dtype {out.dtype} must match x dtype {x.dtype}")
     hT = _ssd_scan(x, dt, A, B, C, D, z, dt_bias, dt_softplus, dt_limit, bounds, h0, out, True,
-                   _segment_chunks)
+                   _segment_chunks, pooled)
+    if pooled is not None:
+        return hT
     return hT if state_dtype in (None, torch.float32) else hT.to(state_dtype)
 
 

@@ -28,7 +28,7 @@ extern "C" {
 
 #define HMX_ABI_VERSION 3  /* 2: optional hmx_gated_norm output epilogue in the GDN ops;
                               3: q/k/v token strides in the GDN and GKA ops; slot-indexed
-                              state pools and has_initial_state in the GDN and GKA
+                              state pools and has_initial_state in the GDN, GKA and SSD
                               prefills */
 
 enum hmx_status {
@@ -255,15 +255,19 @@ size_t hmx_gka_chunk_workspace_bytes(int32_t nseg_total, int32_t N, int32_t H);
 /*
  * Mamba2 SSD chunk scan forward, bf16 x/B/C/z/y, fp32 states, varlen via a
  * segment table of rows (n, bos, eos, c_start, c_end, seg_idx, first_seg, nseg)
- * over 64-token chunks (bos/eos index the flattened token axis; sequence n
- * starts from h0[n] or zero and its end state goes to h_final[n]).
+ * over 64-token chunks (bos/eos index the flattened token axis).
  *  x, z, y [tokens, H, P]: element strides x_ts/x_hs (token, head), last dim
  *  contiguous; B, C [tokens, G, N] with strides (token, group); dt [tokens, H]
  *  (f32/bf16/f16) with strides; A [H] fp32 (= -exp(A_log)); D [H, P] fp32 or
  *  NULL; dt_bias [H] fp32 or NULL; z NULL for no gate.  dt' =
  *  clamp(softplus(dt + dt_bias) if dt_softplus else dt + dt_bias, dt_min, dt_max).
- *  h0, h_final fp32 [nseq, H, P, N] or NULL.  P, N in {64, 128}; token/head
- *  strides multiples of 8 elements.
+ *  h0 / h_final: the initial / end states, each a base of [H, P, N] slots
+ *  state_slot_stride elements apart in state_dtype (f32 or bf16), or NULL (zero
+ *  start / no end state).  Sequence n uses slot state_indices[n] (n when NULL);
+ *  a negative slot starts from zero and writes nothing; has_initial_state[n] == 0
+ *  (when not NULL) starts from zero.  h0 and h_final may be the same pool
+ *  (updated in place).  P, N in {64, 128}; token/head strides multiples of 8
+ *  elements.
  * workspace: hmx_ssd_chunk_workspace_bytes(...) bytes of device scratch.
  * Replaces: mamba_chunk_scan_combined (mamba_ssm 2.3.0; call site
  *   training/src/hmf/model/hybrid_zoo/layers/mamba/mamba2.py:555-580) and
@@ -277,7 +281,9 @@ int hmx_ssd_chunk_fwd(const void* x, int64_t x_ts, int64_t x_hs,
                       const float* A, const float* D, const float* dt_bias,
                       const void* z, int64_t z_ts, int64_t z_hs,
                       void* y, int64_t y_ts, int64_t y_hs,
-                      const float* h0, float* h_final,
+                      const void* h0, void* h_final, int64_t state_slot_stride,
+                      int32_t state_dtype, const int32_t* state_indices,
+                      const uint8_t* has_initial_state,
                       const int32_t* seg_table, int32_t nseg_total, int32_t nseq,
                       int32_t H, int32_t G, int32_t P, int32_t N,
                       int32_t dt_softplus, float dt_min, float dt_max,
