@@ -57,6 +57,17 @@ def _pool(st: torch.Tensor, dim: int, dtype, name: str):
     return st.shape[2], st.stride(0), st.stride(2)
 
 
+def _out_rows(out, rows: int, dim: int, x: torch.Tensor) -> torch.Tensor:
+    if out is None:
+        return torch.empty(rows, dim, dtype=x.dtype, device=x.device)
+    vec = 16 // x.element_size()
+    if (tuple(out.shape) != (rows, dim) or out.dtype != x.dtype or out.stride(-1) != 1
+            or (rows > 1 and out.stride(0) % vec) or out.data_ptr() % 16):
+        raise ValueError(f"out must be [{rows}, {dim}] {x.dtype} with contiguous, 16-byte "
+                         f"aligned rows, got {tuple(out.shape)} {out.dtype}")
+    return out
+
+
 def _i32(t):
     return None if t is None else t.to(torch.int32).contiguous()
 
@@ -83,12 +94,13 @@ def conv_fwd_rows(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | No
                   conv_states: torch.Tensor | None, query_start_loc: torch.Tensor | None,
                   cache_indices: torch.Tensor | None, has_initial_state: torch.Tensor | None,
                   activation, pad_slot_id: int = PAD_SLOT_ID,
-                  validate_data: bool = False) -> torch.Tensor:
+                  validate_data: bool = False, out: torch.Tensor | None = None) -> torch.Tensor:
     """``causal_conv1d_fn`` returning the output as contiguous [total, dim] rows.
     Tokens from ``query_start_loc[-1]`` on belong to no sequence and give 0.  No
     device value is read back unless ``validate_data`` (the kernels clamp sequence
     bounds to the token count, so a malformed ``query_start_loc`` cannot move an
-    access outside x)."""
+    access outside x).  ``out`` [total, dim] (x's dtype, channels contiguous) receives
+    the rows when given."""
     _lib.require_gpu(x, weight, bias, conv_states, query_start_loc, cache_indices,
                      has_initial_state)
     dim, total = x.shape
@@ -106,7 +118,7 @@ def conv_fwd_rows(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | No
                 bounds[-1] > total:
             raise ValueError(f"query_start_loc must be non-decreasing from 0 to <= {total}: "
                              f"{bounds}")
-    out = torch.empty(total, dim, dtype=x.dtype, device=x.device)
+    out = _out_rows(out, total, dim, x)
     st_len, sst, srs = 0, 0, 0
     if conv_states is not None:
         st_len, sst, srs = _pool(conv_states, dim, x.dtype, "conv_states")
@@ -127,11 +139,13 @@ def causal_conv1d_update(x: torch.Tensor, conv_state: torch.Tensor, weight: torc
                          query_start_loc: torch.Tensor | None = None, max_query_len: int = -1,
                          pad_slot_id: int = PAD_SLOT_ID, validate_data: bool = False,
                          block_idx_last_scheduled_token: torch.Tensor | None = None,
-                         initial_state_idx: torch.Tensor | None = None) -> torch.Tensor:
+                         initial_state_idx: torch.Tensor | None = None, *,
+                         out: torch.Tensor | None = None) -> torch.Tensor:
     """Decode conv: x [batch, dim], one token per sequence, against the slot pool
     ``conv_state`` [slots, dim, state_len] (channels contiguous; updated in place:
     the state shifts by one position).  Returns [batch, dim]; padded entries (slot ==
-    pad_slot_id) give 0."""
+    pad_slot_id) give 0.  ``out`` [batch, dim] (keyword-only, no reference
+    counterpart) receives the rows when given."""
     if num_accepted_tokens is not None or query_start_loc is not None:
         raise NotImplementedError("speculative multi-token causal_conv1d_update")
     if block_idx_last_scheduled_token is not None or initial_state_idx is not None:
@@ -145,7 +159,7 @@ def causal_conv1d_update(x: torch.Tensor, conv_state: torch.Tensor, weight: torc
         raise ValueError(f"weight must be [{dim}, width], got {tuple(weight.shape)}")
     st_len, sst, srs = _pool(conv_state, dim, x.dtype, "conv_state")
     xr = _rows(x)
-    out = torch.empty(batch, dim, dtype=x.dtype, device=x.device)
+    out = _out_rows(out, batch, dim, x)
     w, b = _aligned(weight), _aligned(bias)
     _lib.call("hmx_causal_conv1d_update", _lib.ptr(xr), xr.stride(0), _lib.ptr(out), out.stride(0),
               _lib.dtype_code(x), _lib.ptr(w), _lib.dtype_code(w), W, _lib.ptr(b),

@@ -88,6 +88,7 @@ def fused_recurrent_gated_delta_rule_gqa(
     o_norm_weight: torch.Tensor | None = None,
     o_norm_gate: torch.Tensor | None = None,
     o_norm_eps: float = 1e-5,
+    out: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """GQA-native fused recurrent gated delta rule (decode).
 
@@ -101,6 +102,7 @@ def fused_recurrent_gated_delta_rule_gqa(
     optionally ``o_norm_gate`` [B,T,H,V], q.dtype) returns the layer's gated
     RMSNorm ``o_norm(o, z)`` (primed_gdn_layer.py:621-626) instead of o, fused into
     the kernel's output for V <= 128 (a separate hmx.rms_norm_gated call otherwise).
+    ``out`` [B,T,H,V] (q.dtype, contiguous) receives o when given.
     """
     if cu_seqlens is not None and q.shape[0] != 1:
         raise ValueError(f"Batch size expected to be 1 with cu_seqlens, got {q.shape[0]}")
@@ -136,7 +138,14 @@ def fused_recurrent_gated_delta_rule_gqa(
             raise AssertionError("state dtypes differ")
     idx = _i32(ssm_state_indices)
     idx_stride = 0 if idx is None else idx.stride(0)
-    o = q.new_empty(B, T, H, V)
+    if out is not None:
+        _lib.require_gpu(out)
+        if (tuple(out.shape) != (B, T, H, V) or out.dtype != q.dtype or not out.is_contiguous()
+                or out.data_ptr() % 16):
+            raise ValueError(f"out must be a contiguous [{B},{T},{H},{V}] {q.dtype} tensor")
+        o = out
+    else:
+        o = q.new_empty(B, T, H, V)
     state_dt = _lib.dtype_code(final_state)
     onorm, norm_after = None, False
     if o_norm_weight is not None:
@@ -162,7 +171,11 @@ def fused_recurrent_gated_delta_rule_gqa(
               int(bool(inplace_final_state)), onorm, _lib.stream_of(q))
     if norm_after:
         from .norm import rms_norm_gated
-        o = rms_norm_gated(o, o_norm_gate, o_norm_weight, eps=o_norm_eps)
+        normed = rms_norm_gated(o, o_norm_gate, o_norm_weight, eps=o_norm_eps)
+        if out is None:
+            o = normed
+        else:
+            o.copy_(normed)
     return o, final_state
 
 

@@ -67,7 +67,8 @@ def chebyshev_iteration_gqa(k, q, v, alpha, gk=None, beta=None, num_iter: int = 
                             initial_state_kk=None, initial_state_kv=None,
                             output_final_state: bool = True, inplace_final_state: bool = True,
                             cu_seqlens=None, ssm_state_indices=None, *,
-                            o_norm_weight=None, o_norm_gate=None, o_norm_eps: float = 1e-6):
+                            o_norm_weight=None, o_norm_gate=None, o_norm_eps: float = 1e-6,
+                            out=None):
     """Fused GKA decode step (chebyshev_iteration_gqa.py:173-238).
 
     k [B,T,HKV,D]; q [B,T,H,D]; v [B,T,HKV,V]; alpha, gk, beta [B,T,H].
@@ -78,7 +79,7 @@ def chebyshev_iteration_gqa(k, q, v, alpha, gk=None, beta=None, num_iter: int = 
     Keyword-only extension (no reference counterpart): ``o_norm_weight`` [V] (and
     optionally ``o_norm_gate`` [B,T,H,V], q.dtype) returns the layer's gated
     RMSNorm ``o_norm(o, z)`` (primed_gka_layer.py:944-949) fused into the kernel's
-    output instead of o.
+    output instead of o; ``out`` [B,T,H,V] (q.dtype, contiguous) receives o.
     """
     if cu_seqlens is not None and q.shape[0] != 1:
         raise ValueError(f"Batch size must be 1 when using cu_seqlens, got {q.shape[0]}.")
@@ -108,7 +109,14 @@ def chebyshev_iteration_gqa(k, q, v, alpha, gk=None, beta=None, num_iter: int = 
     else:
         hkk, hkv = initial_state_kk.clone(), initial_state_kv.clone()
     idx = _i32(ssm_state_indices)
-    o = q.new_empty(B, T, H, V)
+    if out is not None:
+        _lib.require_gpu(out)
+        if (tuple(out.shape) != (B, T, H, V) or out.dtype != q.dtype or not out.is_contiguous()
+                or out.data_ptr() % 16):
+            raise ValueError(f"out must be a contiguous [{B},{T},{H},{V}] {q.dtype} tensor")
+        o = out
+    else:
+        o = q.new_empty(B, T, H, V)
     onorm = _onorm(o_norm_weight, o_norm_gate, o_norm_eps, (B, T, H, V), q.dtype)
     _lib.call("hmx_gka_decode_fwd",
               _lib.ptr(q), q_ts, _lib.ptr(k), k_ts, _lib.ptr(v), v_ts, _lib.dtype_code(q),
@@ -133,9 +141,10 @@ def gka_chebyshev_gla_decode(q, k, v, alpha, g, gk, beta, gla_scale: float,
                              ridge_ratio: float = 0.02, num_sketches_per_head: int = 1,
                              num_iter: int = 30, gka=None, h_kk=None, h_kv=None,
                              cu_seqlens=None, ssm_state_indices=None, *,
-                             o_norm_weight=None, o_norm_gate=None, o_norm_eps: float = 1e-6):
-    """Single-token GKA decode (gka_forward.py:248-326).  ``o_norm_*``: see
-    chebyshev_iteration_gqa."""
+                             o_norm_weight=None, o_norm_gate=None, o_norm_eps: float = 1e-6,
+                             out=None):
+    """Single-token GKA decode (gka_forward.py:248-326).  ``o_norm_*`` and ``out``:
+    see chebyshev_iteration_gqa."""
     global _warned_num_iter_zero
     _check_sketching_constraints(gka, num_sketches_per_head, "gka_chebyshev_gla_decode")
     if num_iter == 0:
@@ -151,7 +160,7 @@ def gka_chebyshev_gla_decode(q, k, v, alpha, g, gk, beta, gla_scale: float,
                                    output_final_state=True, inplace_final_state=True,
                                    cu_seqlens=cu_seqlens, ssm_state_indices=ssm_state_indices,
                                    o_norm_weight=o_norm_weight, o_norm_gate=o_norm_gate,
-                                   o_norm_eps=o_norm_eps)
+                                   o_norm_eps=o_norm_eps, out=out)
 
 
 def gka_chebyshev_gla_prefill(q, k, v, alpha, g, gk, beta, gla_scale: float,

@@ -1,0 +1,197 @@
+"""The vLLM layers' mixer cores over hmx ops: ``gdn_forward_core`` and
+``gka_forward_core``.
+
+These restate ``PrimedGatedDeltaNetAttention._forward_core``
+(vllm-inference/src/primed_vllm/primed_gdn_layer.py:635-936) and
+``PrimedGKAAttention._forward_core`` (primed_gka_layer.py:962-1338) for the
+non-speculative batches (pure decode, pure prefill, and mixed batches with the
+decodes first), with the same inputs and the same effect: ``core_attn_out`` rows
+written, the conv and recurrent state pools updated in place.  Compared with the
+reference sequence of calls they drop every copy around the ops:
+
+- the decode and prefill convs write one buffer (no ``torch.cat``);
+- q, k and v are column views of that buffer (the reference's
+  ``rearrange_mixed_qkv`` makes them contiguous, :485-560);
+- the prefill reads and writes the state pool by slot with ``has_initial_state``
+  (no gather, zeroing and scatter, :868-879 / primed_gka_layer.py:1245-1266);
+- the ops write into ``core_attn_out`` directly (no ``torch.cat`` and no final
+  copy, :925-936);
+- optionally (``o_norm=(weight, z, eps)``) the layer's output norm runs in the
+  ops' epilogue, so ``forward`` skips ``self.o_norm`` (:621-626).
+
+``layer`` is the vLLM layer object (or anything with the attributes the
+reference reads: conv1d.weight, activation, A, dt_bias, key_dim, kv_k_dim,
+kv_v_dim, num_heads, num_kv_heads, head_k_dim, head_v_dim, tp_size, proj_k, and
+allow_neg_eigval for GDN / the gka_config attributes for GKA);
+``attn_metadata`` is the layer's GDNAttentionMetadata (the fields the reference
+reads, with the primed builder's ``non_spec_query_start_loc_d/_p`` in mixed
+batches, primed_gdn_attn.py:40-113); ``conv_state`` is
+``self_kv_cache[0].transpose(-1, -2)`` and the recurrent pools the other cache
+entries, as the reference takes them from the forward context (:667-670).
+
+One deliberate difference: in mixed batches the reference hands the prefill conv
+the whole batch's ``has_initial_state`` (primed_gdn_layer.py:753,
+primed_gka_layer.py:1083) while its recurrent prefill uses the prefill slice
+(primed_gdn_layer.py:870, primed_gka_layer.py:1247); here both use the prefill
+slice.
+
+Speculative decoding (``spec_sequence_masks``) and the low-rank k/v projection
+(``proj_k``) raise NotImplementedError.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import ops
+
+
+def _check(layer, md):
+    if md.spec_sequence_masks is not None:
+        raise NotImplementedError("speculative decoding batches (spec_sequence_masks) are not "
+                                  "supported by the hmx mixer cores")
+    if getattr(layer, "proj_k", None) is not None:
+        raise NotImplementedError("the low-rank k/v projection (kv_proj_rank) is not supported "
+                                  "by the hmx mixer cores")
+
+
+def _conv(layer, md, mixed_qkv, cs):
+    """(conv output [n, conv_dim], decode / prefill split) of the non-spec tokens,
+    decodes first, in one buffer; updates the conv state pool in place."""
+    w = layer.conv1d.weight
+    w = w.view(w.size(0), w.size(2))
+    x = torch.empty_like(mixed_qkv)
+    nd, ndt, npf = md.num_decodes, md.num_decode_tokens, md.num_prefills
+    idx, has = md.non_spec_state_indices_tensor, md.has_initial_state
+    act = layer.activation
+    if nd > 0 and npf > 0:
+        ops.causal_conv1d_update(mixed_qkv[:ndt], cs, w, None, act,
+                                 conv_state_indices=idx[:nd], out=x[:ndt])
+        ops.conv.conv_fwd_rows(mixed_qkv[ndt:].t(), w, None, cs, md.non_spec_query_start_loc_p,
+                               idx[nd:], None if has is None else has[nd:], act, out=x[ndt:])
+    elif npf > 0:
+        ops.conv.conv_fwd_rows(mixed_qkv.t(), w, None, cs, md.non_spec_query_start_loc, idx, has,
+                               act, out=x)
+    elif nd > 0:
+        ops.causal_conv1d_update(mixed_qkv, cs, w, None, act,
+                                 conv_state_indices=idx[:mixed_qkv.shape[0]], out=x)
+    return x
+
+
+def _qkv(layer, x):
+    """q [1,n,H,Dk], k [1,n,HKV,Dk], v [1,n,HKV,Dv] as column views of x."""
+    tp = layer.tp_size
+    kd, kk = layer.key_dim // tp, layer.kv_k_dim // tp
+    H, HKV = layer.num_heads // tp, layer.num_kv_heads // tp
+    n = x.shape[0]
+    q = x[:, :kd].view(1, n, H, layer.head_k_dim)
+    k = x[:, kd:kd + kk].view(1, n, HKV, layer.head_k_dim)
+    v = x[:, kd + kk:].view(1, n, HKV, layer.head_v_dim)
+    return q, k, v
+
+
+def _split(md):
+    nd, ndt, npf = md.num_decodes, md.num_decode_tokens, md.num_prefills
+    idx, has = md.non_spec_state_indices_tensor, md.has_initial_state
+    mixed = nd > 0 and npf > 0
+    dec = None
+    if nd > 0:
+        cu_d = md.non_spec_query_start_loc_d if mixed else md.non_spec_query_start_loc[:nd + 1]
+        dec = (cu_d, idx[:nd] if mixed else idx)
+    pre = None
+    if npf > 0:
+        cu_p = md.non_spec_query_start_loc_p if mixed else md.non_spec_query_start_loc
+        pre = (cu_p, idx[nd:] if mixed else idx,
+               None if has is None else (has[nd:] if mixed else has))
+    return ndt, dec, pre
+
+
+def _norm_args(o_norm, lo, hi):
+    if o_norm is None:
+        return {}
+    w, z, eps = o_norm
+    return dict(o_norm_weight=w, o_norm_gate=None if z is None else z[lo:hi].unsqueeze(0),
+                o_norm_eps=eps)
+
+
+def gdn_forward_core(layer, mixed_qkv: torch.Tensor, b: torch.Tensor, a: torch.Tensor,
+                     core_attn_out: torch.Tensor, attn_metadata, conv_state: torch.Tensor,
+                     ssm_state: torch.Tensor, *, o_norm=None) -> None:
+    """primed_gdn_layer.py:635-936 over hmx ops (see the module docstring).
+    ``o_norm=(weight, z [tokens, H, V], eps)`` fuses the layer's output norm."""
+    md = attn_metadata
+    if md is None:
+        return
+    _check(layer, md)
+    n = md.num_actual_tokens
+    mixed_qkv, b, a = mixed_qkv[:n], b[:n], a[:n]
+    x = _conv(layer, md, mixed_qkv, conv_state)
+    q, k, v = _qkv(layer, x)
+    g, beta = ops.fused_gdn_gating(layer.A, a, b, layer.dt_bias)
+    if getattr(layer, "allow_neg_eigval", False):
+        beta = beta * 2.0
+    out = core_attn_out[:n].unsqueeze(0)
+    ndt, dec, pre = _split(md)
+    if dec is not None:
+        cu_d, idx_d = dec
+        ops.fused_recurrent_gated_delta_rule_gqa(
+            q[:, :ndt], k[:, :ndt], v[:, :ndt], g[:, :ndt], beta[:, :ndt],
+            initial_state=ssm_state, inplace_final_state=True, cu_seqlens=cu_d,
+            ssm_state_indices=idx_d, use_qk_l2norm_in_kernel=True, out=out[:, :ndt],
+            **_norm_args(o_norm, 0, ndt))
+    if pre is not None:
+        cu_p, idx_p, has_p = pre
+        ops.chunk_gated_delta_rule_gqa(
+            q[:, ndt:], k[:, ndt:], v[:, ndt:], g[:, ndt:], beta[:, ndt:],
+            initial_state=ssm_state, output_final_state=True, cu_seqlens=cu_p,
+            use_qk_l2norm_in_kernel=True, ssm_state_indices=idx_p, has_initial_state=has_p,
+            out=out[:, ndt:], **_norm_args(o_norm, ndt, n))
+
+
+def gka_forward_core(layer, mixed_qkv: torch.Tensor, a: torch.Tensor, alpha_in: torch.Tensor,
+                     b: torch.Tensor | None, core_attn_out: torch.Tensor, attn_metadata,
+                     conv_state: torch.Tensor, h_kk_state: torch.Tensor,
+                     h_kv_state: torch.Tensor, *, o_norm=None) -> None:
+    """primed_gka_layer.py:962-1338 over hmx ops (see the module docstring).
+    ``o_norm=(weight, z [tokens, H, V], eps)`` fuses the layer's output norm."""
+    md = attn_metadata
+    if md is None:
+        return
+    _check(layer, md)
+    if not layer.use_forgetting_gate:
+        raise NotImplementedError("GKA without the forgetting gate (g = None) is not supported "
+                                  "by the hmx mixer core")
+    n = md.num_actual_tokens
+    mixed_qkv, a, alpha_in = mixed_qkv[:n], a[:n], alpha_in[:n]
+    use_beta = layer.use_beta_gate
+    if use_beta:
+        b = b[:n]
+    x = _conv(layer, md, mixed_qkv, conv_state)
+    q, k, v = _qkv(layer, x)
+    # gating as primed_gka_layer.py:1138-1153
+    g, alpha, beta = ops.fused_gka_gating(layer.A, a, alpha_in, b if use_beta else None,
+                                          layer.dt_bias)
+    if layer.num_iter == 0:
+        alpha = torch.zeros_like(alpha)
+    elif layer._alpha_idx is None:
+        alpha = alpha + 0.5
+    kk_gate = layer.use_forgetting_gate_kk
+    out = core_attn_out[:n].unsqueeze(0)
+    ndt, dec, pre = _split(md)
+    sl = lambda t, lo, hi: None if t is None else t[:, lo:hi]
+    common = dict(gla_scale=layer.gla_scale, ridge_ratio=layer.ridge_strength,
+                  num_iter=layer.num_iter)
+    if dec is not None:
+        cu_d, idx_d = dec
+        g_d = g[:, :ndt]
+        ops.gka_chebyshev_gla_decode(
+            q[:, :ndt], k[:, :ndt], v[:, :ndt], alpha[:, :ndt], g_d, g_d if kk_gate else None,
+            sl(beta, 0, ndt), h_kk=h_kk_state, h_kv=h_kv_state, cu_seqlens=cu_d,
+            ssm_state_indices=idx_d, out=out[:, :ndt], **common, **_norm_args(o_norm, 0, ndt))
+    if pre is not None:
+        cu_p, idx_p, has_p = pre
+        g_p = g[:, ndt:]
+        ops.gka_chebyshev_gla_prefill(
+            q[:, ndt:], k[:, ndt:], v[:, ndt:], alpha[:, ndt:], g_p, g_p if kk_gate else None,
+            sl(beta, ndt, n), h_kk_initial=h_kk_state, h_kv_initial=h_kv_state,
+            output_final_state=True, cu_seqlens=cu_p, ssm_state_indices=idx_p,
+            has_initial_state=has_p, out=out[:, ndt:], **common, **_norm_args(o_norm, ndt, n))
