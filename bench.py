@@ -13,7 +13,7 @@ reported under ``gka`` against the bf16 MFMA roofline; the Mamba2 SSD chunk scan
 at C4 under ``ssd`` and its single-token state update under ``ssd_decode``, both
 against HBM.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only prefill|decode|gka|ssd|onorm|conv]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only prefill|decode|gka|ssd|onorm|conv|core]
 """
 from __future__ import annotations
 
@@ -127,6 +127,70 @@ def bench_conv(dev, steps, warmup):
     dec_bytes = N * dim * 2 * (2 + 2 * st_len)                  # x, out; state read + written
     return dict(ms_fwd=ms_fwd, fwd_bytes=fwd_bytes, fwd_GBps=fwd_bytes / (ms_fwd * 1e-3) / 1e9,
                 ms_dec=ms_dec, dec_bytes=dec_bytes, dec_GBps=dec_bytes / (ms_dec * 1e-3) / 1e9)
+
+
+def bench_core(dev, steps, warmup):
+    """The GDN layer's core at the C1 shape (8 sequences x 4096 tokens, H = HKV = 32,
+    d = 128, conv width 4, state pools of 8 slots): the reference layer's call
+    sequence over hmx ops (primed_gdn_layer.py:747-936 then o_norm, :621-626: conv
+    to a new tensor, contiguous q/k/v, gating, state gather and zeroing, prefill,
+    scatter, copy into core_attn_out, separate norm) against
+    hmx.serving.gdn_forward_core with the norm fused."""
+    from types import SimpleNamespace
+    import torch
+    import hmx
+    import hmx.serving as srv
+    from hmx import workloads as wl
+    T, H, D, nseq = 32768, 32, 128, 8
+    cd = 3 * H * D
+    g = torch.Generator(device=dev).manual_seed(wl.SEED_BASE + 8)
+    lay = SimpleNamespace(
+        conv1d=SimpleNamespace(weight=(torch.randn(cd, 1, 4, generator=g, device=dev) * 0.4)
+                               .bfloat16()),
+        activation="silu", A=torch.rand(H, generator=g, device=dev),
+        dt_bias=torch.randn(H, generator=g, device=dev), key_dim=H * D, kv_k_dim=H * D,
+        kv_v_dim=H * D, num_heads=H, num_kv_heads=H, head_k_dim=D, head_v_dim=D, tp_size=1,
+        proj_k=None, allow_neg_eigval=False)
+    mixed = torch.randn(T, cd, generator=g, device=dev).bfloat16()
+    a = torch.randn(T, H, generator=g, device=dev).bfloat16()
+    b = torch.randn(T, H, generator=g, device=dev).bfloat16()
+    z = torch.randn(T, H, D, generator=g, device=dev).bfloat16()
+    wn = torch.rand(D, generator=g, device=dev) + 0.5
+    conv_cache = torch.randn(nseq, 3, cd, generator=g, device=dev).bfloat16()
+    ssm = torch.randn(nseq, H, D, D, generator=g, device=dev) * 0.02
+    qs = torch.arange(0, T + 1, T // nseq, dtype=torch.int32, device=dev)
+    idx = torch.randperm(nseq, generator=g, device=dev).to(torch.int32)
+    has = torch.ones(nseq, dtype=torch.bool, device=dev)
+    md = SimpleNamespace(spec_sequence_masks=None, num_actual_tokens=T, num_decodes=0,
+                         num_decode_tokens=0, num_prefills=nseq, non_spec_query_start_loc=qs,
+                         non_spec_state_indices_tensor=idx, has_initial_state=has,
+                         non_spec_query_start_loc_d=None, non_spec_query_start_loc_p=None)
+    core = torch.zeros(T, H, D, dtype=torch.bfloat16, device=dev)
+    cs = conv_cache.transpose(1, 2)
+    w2 = lay.conv1d.weight.view(cd, 4)
+
+    def reference_sequence():
+        x = hmx.causal_conv1d_fn(mixed.t(), w2, None, conv_states=cs, query_start_loc=qs,
+                                 cache_indices=idx, has_initial_state=has).t()
+        q = x[:, :H * D].reshape(1, T, H, D).contiguous()
+        k = x[:, H * D:2 * H * D].reshape(1, T, H, D).contiguous()
+        v = x[:, 2 * H * D:].reshape(1, T, H, D).contiguous()
+        gg, beta = hmx.fused_gdn_gating(lay.A, a, b, lay.dt_bias)
+        init = ssm[idx.long()].contiguous()
+        init[~has] = 0
+        o, st = hmx.chunk_gated_delta_rule_gqa(q, k, v, gg, beta, initial_state=init,
+                                               output_final_state=True, cu_seqlens=qs,
+                                               use_qk_l2norm_in_kernel=True)
+        ssm[idx.long()] = st
+        core[:T] = o.squeeze(0)
+        return hmx.rms_norm_gated(core, z, wn, 1e-6)
+
+    def hmx_core():
+        srv.gdn_forward_core(lay, mixed, b, a, core, md, cs, ssm, o_norm=(wn, z, 1e-6))
+
+    ms_ref = _timed(reference_sequence, steps, warmup)
+    ms_core = _timed(hmx_core, steps, warmup)
+    return dict(ms_ref=ms_ref, ms_core=ms_core, tokens=T)
 
 
 def bench_decode(dev, steps_total=512, warmup=8):
@@ -269,7 +333,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "decode", "gka", "ssd", "onorm", "conv"], default=None)
+    ap.add_argument("--only", choices=["prefill", "decode", "gka", "ssd", "onorm", "conv", "core"], default=None)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (HBM counter calibration)")
     a = ap.parse_args()
@@ -291,6 +355,8 @@ def main():
         out["onorm"] = bench_onorm(dev, a.steps, a.warmup)
     if a.only in (None, "conv"):
         out["conv"] = bench_conv(dev, a.steps, a.warmup)
+    if a.only in (None, "core"):
+        out["core"] = bench_core(dev, max(2, a.steps // 2), a.warmup)
     if a.only in (None, "decode"):
         out["decode"] = bench_decode(dev)
     if a.only in (None, "gka"):
@@ -369,6 +435,15 @@ def main():
                                 "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                 "frac": round(r["dec_GBps"] / HBM_PEAK_GBS, 4),
                                 "algorithmic_bytes": r["dec_bytes"], "traffic": None},
+        }
+    if "core" in out:
+        r = out["core"]
+        line["gdn_layer_core"] = {
+            "config": {"workload": "GDN layer core + output norm at C1 (8 seqs x 4096 tokens, "
+                                   "H=HKV=32, d=128, conv width 4, pooled states)"},
+            "reference_call_sequence_ms": round(r["ms_ref"], 4),
+            "hmx_serving_core_ms": round(r["ms_core"], 4),
+            "tokens_per_s": round(r["tokens"] / (r["ms_core"] * 1e-3), 1),
         }
     if "gka" in out:
         line["gka"] = {}
