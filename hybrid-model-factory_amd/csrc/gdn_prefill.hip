@@ -89,7 +89,7 @@ struct SegInfo {     // one row of the host-built segment table (int32 x 8)
 
 struct Params {
   const bf16* q; const bf16* k; const bf16* v;
-  int64_t q_ts, k_ts, v_ts;  // token strides (elements); heads are D apart
+  int64_t q_ts, kv_ts;       // token strides (elements; k and v share one); heads are D apart
   const void* g; int g_dt;
   const void* beta; int beta_dt;
   bf16* o;
@@ -162,9 +162,9 @@ __device__ __forceinline__ void load_raw(RawChunk& r, const Params& p, const bf1
     const int f0 = (tid & 15) * 8;
     const bool ok = row < nval;
     const int64_t tok = tok0 + row;
-    r.k[pass] = ok ? *reinterpret_cast<const bf16x8*>(kh + tok * p.k_ts + f0) : bf16x8{};
+    r.k[pass] = ok ? *reinterpret_cast<const bf16x8*>(kh + tok * p.kv_ts + f0) : bf16x8{};
     if (MODE != MODE_PHI)
-      r.v[pass] = ok ? *reinterpret_cast<const bf16x8*>(vh + tok * p.v_ts + f0) : bf16x8{};
+      r.v[pass] = ok ? *reinterpret_cast<const bf16x8*>(vh + tok * p.kv_ts + f0) : bf16x8{};
     if (MODE == MODE_OUT)
       r.q[pass] = (ok && need_q) ? *reinterpret_cast<const bf16x8*>(qh + tok * p.q_ts + f0)
                                  : bf16x8{};
@@ -390,19 +390,34 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
       else src = static_cast<const float*>(p.h0) + off;
     }
     if (init_kind == 2) src = p.ws_init + ((int64_t)s_id * H + h) * D * D;
+    // one uniform branch per source type (a per-element choice costs registers)
+    if (src) {
 #pragma unroll
-    for (int rt = 0; rt < 8; ++rt)
+      for (int rt = 0; rt < 8; ++rt)
 #pragma unroll
-      for (int ct = 0; ct < 2; ++ct)
+        for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int row = 16 * rt + 4 * q4 + v, col = 32 * wave + 16 * ct + l16;
-          float x = 0.f;
-          if (src) x = src[row * D + col];
-          if (src16) x = (float)src16[row * D + col];
-          if (init_kind == 3) x = (row == col) ? 1.f : 0.f;
-          S[rt][ct][v] = x;
-        }
+          for (int v = 0; v < 4; ++v)
+            S[rt][ct][v] = src[(16 * rt + 4 * q4 + v) * D + 32 * wave + 16 * ct + l16];
+    } else if (src16) {
+#pragma unroll
+      for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            S[rt][ct][v] = (float)src16[(16 * rt + 4 * q4 + v) * D + 32 * wave + 16 * ct + l16];
+    } else {
+#pragma unroll
+      for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int row = 16 * rt + 4 * q4 + v, col = 32 * wave + 16 * ct + l16;
+            S[rt][ct][v] = (init_kind == 3 && row == col) ? 1.f : 0.f;
+          }
+    }
   }
 
   // P's strictly-upper 16x16 tile is never written by phase 1: zero it once.
@@ -941,6 +956,9 @@ extern "C" int hmx_gdn_chunk_fwd(const void* q, int64_t q_token_stride, const vo
   HMX_REQUIRE(q_token_stride % 8 == 0 && k_token_stride % 8 == 0 && v_token_stride % 8 == 0 &&
                   ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)o) % 16 == 0,
               HMX_EINVAL, "hmx_gdn_chunk_fwd: q/k/v/o rows must be 16-byte aligned");
+  HMX_REQUIRE(k_token_stride == v_token_stride, HMX_EINVAL,
+              "hmx_gdn_chunk_fwd: k and v must share a token stride (%lld vs %lld)",
+              (long long)k_token_stride, (long long)v_token_stride);
   HMX_REQUIRE(!(h0 || ht) || ((state_dtype == HMX_F32 || state_dtype == HMX_BF16) &&
                               state_slot_stride % 4 == 0 &&
                               ((uintptr_t)h0 | (uintptr_t)ht) % 16 == 0),
@@ -955,7 +973,7 @@ extern "C" int hmx_gdn_chunk_fwd(const void* q, int64_t q_token_stride, const vo
   Params p;
   p.q = static_cast<const bf16*>(q); p.k = static_cast<const bf16*>(k);
   p.v = static_cast<const bf16*>(v);
-  p.q_ts = q_token_stride; p.k_ts = k_token_stride; p.v_ts = v_token_stride;
+  p.q_ts = q_token_stride; p.kv_ts = k_token_stride;
   p.g = g; p.g_dt = g_dtype; p.beta = beta; p.beta_dt = beta_dtype;
   p.o = static_cast<bf16*>(o); p.h0 = h0; p.ht = ht;
   p.st_ss = state_slot_stride; p.st_dt = state_dtype;

@@ -103,7 +103,7 @@ __device__ __forceinline__ void pool_st(const Pool& pl, int64_t i, float x) {
 
 struct Params {
   const bf16* q; const bf16* k; const bf16* v;
-  int64_t q_ts, k_ts, v_ts;               // token strides (elements); heads are D apart
+  int64_t q_ts, kv_ts;                    // token strides (elements; k and v share one)
   const void* alpha; int alpha_dt;
   const void* g; int g_dt;
   const void* gk; int gk_dt;       // null: no h_kk decay
@@ -140,6 +140,56 @@ __device__ __forceinline__ SegInfo load_seg(const int* seg, int s) {
   return SegInfo{r[0], r[1], r[2], r[3], r[4], r[5], r[6], r[7]};
 }
 
+// One [D][D] state into accumulator tiles (rows 16rt+4q4+v, columns CW wave +
+// 16ct + l16): from fp32 workspace, or from a pool slot (f32 or bf16), or zeros.
+// (The pool comes by value: a pointer into the kernel's argument struct would move
+// the whole struct to scratch.)
+__device__ __forceinline__ void load_state(f32x4 (&X)[8][NCT], const float* ws, bool use_pool,
+                                           Pool pl, int64_t slot, int64_t hoff, int wave, int q4,
+                                           int l16) {
+#define HMX_GKA_STATE_LOOP(EXPR)                                                   \
+  _Pragma("unroll") for (int rt = 0; rt < 8; ++rt)                                \
+  _Pragma("unroll") for (int ct = 0; ct < NCT; ++ct)                              \
+  _Pragma("unroll") for (int v = 0; v < 4; ++v) {                                 \
+    const int off = (16 * rt + 4 * q4 + v) * D + CW * wave + 16 * ct + l16;      \
+    X[rt][ct][v] = (EXPR);                                                        \
+  }
+  if (ws) {
+    HMX_GKA_STATE_LOOP(ws[off])
+  } else if (use_pool && pl.dt == HMX_BF16) {
+    const bf16* b = static_cast<const bf16*>(pl.in) + slot * pl.ss + hoff;
+    HMX_GKA_STATE_LOOP((float)b[off])
+  } else if (use_pool) {
+    const float* f = static_cast<const float*>(pl.in) + slot * pl.ss + hoff;
+    HMX_GKA_STATE_LOOP(f[off])
+  } else {
+    HMX_GKA_STATE_LOOP(0.f)
+  }
+#undef HMX_GKA_STATE_LOOP
+}
+
+// One [D][D] state from accumulator tiles into a pool slot (f32 or bf16), or
+// zeros into it (clear).
+__device__ __forceinline__ void store_state(const f32x4 (&X)[8][NCT], Pool pl, int64_t slot,
+                                            int64_t hoff, int wave, int q4, int l16, bool clear) {
+#define HMX_GKA_STORE_LOOP(STMT)                                                   \
+  _Pragma("unroll") for (int rt = 0; rt < 8; ++rt)                                \
+  _Pragma("unroll") for (int ct = 0; ct < NCT; ++ct)                              \
+  _Pragma("unroll") for (int v = 0; v < 4; ++v) {                                 \
+    const int off = (16 * rt + 4 * q4 + v) * D + CW * wave + 16 * ct + l16;      \
+    const float x = clear ? 0.f : X[rt][ct][v];                                   \
+    STMT;                                                                         \
+  }
+  if (pl.dt == HMX_BF16) {
+    bf16* b = static_cast<bf16*>(pl.out) + slot * pl.ss + hoff;
+    HMX_GKA_STORE_LOOP(b[off] = (bf16)x)
+  } else {
+    float* f = static_cast<float*>(pl.out) + slot * pl.ss + hoff;
+    HMX_GKA_STORE_LOOP(f[off] = x)
+  }
+#undef HMX_GKA_STORE_LOOP
+}
+
 struct Raw {
   bf16x8 k[NPASS], v[NPASS], q[NPASS];
   float g, gk, b, a;
@@ -153,8 +203,8 @@ __device__ __forceinline__ void load_raw(Raw& r, const Params& p, const bf16* qh
     const int row = pass * RPP + (tid >> 4), f0 = (tid & 15) * 8;
     const bool ok = row < nval;
     const int64_t tok = tok0 + row;
-    r.k[pass] = ok ? *reinterpret_cast<const bf16x8*>(kh + tok * p.k_ts + f0) : bf16x8{};
-    r.v[pass] = ok ? *reinterpret_cast<const bf16x8*>(vh + tok * p.v_ts + f0) : bf16x8{};
+    r.k[pass] = ok ? *reinterpret_cast<const bf16x8*>(kh + tok * p.kv_ts + f0) : bf16x8{};
+    r.v[pass] = ok ? *reinterpret_cast<const bf16x8*>(vh + tok * p.kv_ts + f0) : bf16x8{};
     if (MODE == MODE_OUT)
       r.q[pass] = ok ? *reinterpret_cast<const bf16x8*>(qh + tok * p.q_ts + f0) : bf16x8{};
   }
@@ -243,24 +293,11 @@ __global__ __launch_bounds__(NTHR, NW / 4) void gka_chunk_kernel(Params p) {
         ssrc = p.ws_s0 + ((int64_t)s_id * H + h) * D * D;
       }
     }
-    const bool ph = pooled && track_h && p.hkk.in, ps = pooled && p.hkv.in;
-#pragma unroll
-    for (int rt = 0; rt < 8; ++rt)
-#pragma unroll
-      for (int ct = 0; ct < NCT; ++ct)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int off = (16 * rt + 4 * q4 + v) * D + CW * wave + 16 * ct + l16;
-          float hx = 0.f, sx = 0.f;
-          if (hsrc) {
-            hx = track_h ? hsrc[off] : 0.f;
-            sx = ssrc[off];
-          }
-          if (ph) hx = pool_ld(p.hkk, slot * p.hkk.ss + hoff + off);
-          if (ps) sx = pool_ld(p.hkv, slot * p.hkv.ss + hoff + off);
-          Hs[rt][ct][v] = hx;
-          Ss[rt][ct][v] = sx;
-        }
+    // h_kk then h_kv, each from one source chosen by a uniform branch (a per-element
+    // choice costs registers)
+    load_state(Hs, hsrc && track_h ? hsrc : nullptr, pooled && track_h && p.hkk.in, p.hkk, slot,
+               hoff, wave, q4, l16);
+    load_state(Ss, ssrc, pooled && p.hkv.in, p.hkv, slot, hoff, wave, q4, l16);
   }
 
   const int64_t o_rs = (int64_t)H * D;
@@ -781,18 +818,9 @@ __global__ __launch_bounds__(NTHR, NW / 4) void gka_chunk_kernel(Params p) {
     if (si.seg_idx == si.nseg - 1 && slot >= 0) {
       // without the solver (num_iter 0) h_kk is not tracked: a pooled h_kk slot of a
       // sequence without an initial state is cleared, the others keep their value
-      const bool wh = p.hkk.out && (track_h || (p.hinit && !p.hinit[si.n]));
-      const bool ws_ = p.hkv.out != nullptr;
-#pragma unroll
-      for (int rt = 0; rt < 8; ++rt)
-#pragma unroll
-        for (int ct = 0; ct < NCT; ++ct)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const int off = (16 * rt + 4 * q4 + v) * D + CW * wave + 16 * ct + l16;
-            if (wh) pool_st(p.hkk, slot * p.hkk.ss + hoff + off, track_h ? Hs[rt][ct][v] : 0.f);
-            if (ws_) pool_st(p.hkv, slot * p.hkv.ss + hoff + off, Ss[rt][ct][v]);
-          }
+      if (p.hkk.out && (track_h || (p.hinit && !p.hinit[si.n])))
+        store_state(Hs, p.hkk, slot, hoff, wave, q4, l16, !track_h);
+      if (p.hkv.out) store_state(Ss, p.hkv, slot, hoff, wave, q4, l16, false);
     }
   } else {
     hd = track_h ? p.ws_dh + ((int64_t)s_id * H + h) * D * D : nullptr;
@@ -885,6 +913,9 @@ extern "C" int hmx_gka_chunk_fwd(const void* q, int64_t q_token_stride, const vo
   HMX_REQUIRE(q_token_stride % 8 == 0 && k_token_stride % 8 == 0 && v_token_stride % 8 == 0 &&
                   ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)o) % 16 == 0,
               HMX_EINVAL, "hmx_gka_chunk_fwd: q/k/v/o rows must be 16-byte aligned");
+  HMX_REQUIRE(k_token_stride == v_token_stride, HMX_EINVAL,
+              "hmx_gka_chunk_fwd: k and v must share a token stride (%lld vs %lld)",
+              (long long)k_token_stride, (long long)v_token_stride);
   HMX_REQUIRE((h_kk_dtype == HMX_F32 || h_kk_dtype == HMX_BF16) &&
                   (h_kv_dtype == HMX_F32 || h_kv_dtype == HMX_BF16),
               HMX_EUNSUPPORTED, "hmx_gka_chunk_fwd: state dtypes must be f32 or bf16");
@@ -910,7 +941,7 @@ extern "C" int hmx_gka_chunk_fwd(const void* q, int64_t q_token_stride, const vo
     p.onw = o_norm->weight; p.onw_dt = o_norm->weight_dtype; p.on_eps = o_norm->eps;
   }
   p.o = static_cast<bf16*>(o);
-  p.q_ts = q_token_stride; p.k_ts = k_token_stride; p.v_ts = v_token_stride;
+  p.q_ts = q_token_stride; p.kv_ts = k_token_stride;
   p.hkk = Pool{h_kk0, h_kk_final, h_kk_slot_stride, h_kk_dtype};
   p.hkv = Pool{h_kv0, h_kv_final, h_kv_slot_stride, h_kv_dtype};
   p.sidx = state_indices; p.hinit = has_initial_state;

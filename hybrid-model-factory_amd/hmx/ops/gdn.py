@@ -348,6 +348,8 @@ def chunk_gated_delta_rule_gqa(
         hinit = has_initial_state.to(torch.uint8).contiguous()
     g, beta = g.contiguous(), beta.contiguous()
     (q, q_ts), (k, k_ts), (v, v_ts) = (_token_rows(x, 8) for x in (q, k, v))
+    if k_ts != v_ts:    # the prefill kernels read k and v at one token stride
+        (k, k_ts), (v, v_ts) = _token_rows(k.contiguous(), 8), _token_rows(v.contiguous(), 8)
     if out is not None:
         if (tuple(out.shape) != (B, T, H, V) or out.dtype != q.dtype or not out.is_contiguous()
                 or out.data_ptr() % 16):

@@ -261,6 +261,8 @@ def _gka_prefill(q, k, v, alpha, g, gk, beta, gla_scale, ridge_ratio, num_iter, 
         hinit = has_initial_state.to(torch.uint8).contiguous()
     alpha, g = alpha.contiguous(), g.contiguous()
     (q, q_ts), (k, k_ts), (v, v_ts) = (_token_rows(x, 8) for x in (q, k, v))
+    if k_ts != v_ts:    # the prefill kernels read k and v at one token stride
+        (k, k_ts), (v, v_ts) = _token_rows(k.contiguous(), 8), _token_rows(v.contiguous(), 8)
     gk = None if gk is None else gk.contiguous()
     beta = None if beta is None else beta.contiguous()
     if out is not None:
