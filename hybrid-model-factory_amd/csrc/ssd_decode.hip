@@ -15,6 +15,8 @@
 // Layout: one 256-thread workgroup per (sequence, head).  Thread t owns the
 // 4 consecutive n of columns 4 (t mod N/4) for rows p = t / (N/4) + k (1024/N),
 // so every state load and store is a fully coalesced 16-byte (fp32) access.
+#include <type_traits>
+
 #include "common.hpp"
 #include "mfma.hpp"
 
@@ -61,6 +63,22 @@ __device__ __forceinline__ void st_any(void* p, int64_t i, int dt, float v) {
   else static_cast<f16*>(p)[i] = (f16)v;
 }
 
+// Element loads of the per-token operands: a fixed type (one code path, so every
+// load of a thread is in flight at once), or Any (the dtype code decides).
+struct Any {};
+
+template <typename T>
+__device__ __forceinline__ float ld_t(const void* p, int64_t i, int dt) {
+  if constexpr (std::is_same_v<T, Any>) return ld_any(p, i, dt);
+  else return (float)static_cast<const T*>(p)[i];
+}
+
+template <typename T>
+__device__ __forceinline__ void st_t(void* p, int64_t i, int dt, float v) {
+  if constexpr (std::is_same_v<T, Any>) st_any(p, i, dt, v);
+  else static_cast<T*>(p)[i] = (T)v;
+}
+
 template <typename TS>
 __device__ __forceinline__ f32x4 ld4(const TS* p) {
   if constexpr (sizeof(TS) == 4) {
@@ -82,7 +100,8 @@ __device__ __forceinline__ void st4(TS* p, const f32x4& v) {
   }
 }
 
-template <typename TS, int P, int N, bool A_TIED>
+// TIO: the type of x, B, C, z and out (Any: per-tensor dtype codes); TDT: dt's.
+template <typename TS, int P, int N, bool A_TIED, typename TIO, typename TDT>
 __global__ __launch_bounds__(NTHR) void ssd_state_update_kernel(Params p) {
   constexpr int GN = N / 4;            // threads per row
   constexpr int RPP = NTHR / GN;       // rows per pass
@@ -97,8 +116,8 @@ __global__ __launch_bounds__(NTHR) void ssd_state_update_kernel(Params p) {
   float bv[4], cv[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    bv[j] = ld_any(p.B, (int64_t)i * p.b_bs + (int64_t)g * p.b_gs + n0 + j, p.b_dt);
-    cv[j] = ld_any(p.C, (int64_t)i * p.c_bs + (int64_t)g * p.c_gs + n0 + j, p.c_dt);
+    bv[j] = ld_t<TIO>(p.B, (int64_t)i * p.b_bs + (int64_t)g * p.b_gs + n0 + j, p.b_dt);
+    cv[j] = ld_t<TIO>(p.C, (int64_t)i * p.c_bs + (int64_t)g * p.c_gs + n0 + j, p.c_dt);
   }
   const TS* sin = static_cast<const TS*>(p.state) + (int64_t)src * p.slot_stride + (int64_t)h * P * N;
   TS* sout = static_cast<TS*>(p.state) + (int64_t)dst * p.slot_stride + (int64_t)h * P * N;
@@ -106,12 +125,19 @@ __global__ __launch_bounds__(NTHR) void ssd_state_update_kernel(Params p) {
   f32x4 st[PASSES];
 #pragma unroll
   for (int k = 0; k < PASSES; ++k) st[k] = ld4(sin + (int64_t)(r0 + k * RPP) * N + n0);
+  float xs[PASSES], ds[PASSES];
+#pragma unroll
+  for (int k = 0; k < PASSES; ++k) {
+    const int pr = r0 + k * RPP;
+    xs[k] = ld_t<TIO>(p.x, (int64_t)i * p.x_bs + (int64_t)h * p.x_hs + (int64_t)pr * p.x_ps, p.x_dt);
+    ds[k] = ld_t<TDT>(p.dt, (int64_t)i * p.dt_bs + (int64_t)h * p.dt_hs + (int64_t)pr * p.dt_ps, p.dt_dt);
+  }
 
 #pragma unroll
   for (int k = 0; k < PASSES; ++k) {
     const int pr = r0 + k * RPP;
-    const float xv = ld_any(p.x, (int64_t)i * p.x_bs + (int64_t)h * p.x_hs + (int64_t)pr * p.x_ps, p.x_dt);
-    float d = ld_any(p.dt, (int64_t)i * p.dt_bs + (int64_t)h * p.dt_hs + (int64_t)pr * p.dt_ps, p.dt_dt);
+    const float xv = xs[k];
+    float d = ds[k];
     if (p.dt_bias) d += p.dt_bias[(int64_t)h * p.db_hs + (int64_t)pr * p.db_ps];
     if (p.softplus) d = d <= 20.f ? log1pf(expf(d)) : d;
     const float dx = d * xv;
@@ -136,22 +162,36 @@ __global__ __launch_bounds__(NTHR) void ssd_state_update_kernel(Params p) {
       float o = acc;
       if (p.D) o += p.D[(int64_t)h * p.d_hs + (int64_t)pr * p.d_ps] * xv;
       if (p.z) {
-        const float zz = ld_any(p.z, (int64_t)i * p.z_bs + (int64_t)h * p.z_hs + (int64_t)pr * p.z_ps, p.z_dt);
+        const float zz = ld_t<TIO>(p.z, (int64_t)i * p.z_bs + (int64_t)h * p.z_hs + (int64_t)pr * p.z_ps, p.z_dt);
         o *= zz / (1.f + expf(-zz));
       }
-      st_any(p.out, (int64_t)i * p.o_bs + (int64_t)h * p.o_hs + (int64_t)pr * p.o_ps, p.out_dt, o);
+      st_t<TIO>(p.out, (int64_t)i * p.o_bs + (int64_t)h * p.o_hs + (int64_t)pr * p.o_ps, p.out_dt, o);
     }
   }
 #pragma unroll
   for (int k = 0; k < PASSES; ++k) st4(sout + (int64_t)(r0 + k * RPP) * N + n0, st[k]);
 }
 
+template <typename TS, int P, int N, typename TIO, typename TDT>
+void launch_t(const Params& p, int batch, bool tied, hipStream_t s) {
+  if (tied)
+    hipLaunchKernelGGL((ssd_state_update_kernel<TS, P, N, true, TIO, TDT>), dim3(batch * p.H),
+                       dim3(NTHR), 0, s, p);
+  else
+    hipLaunchKernelGGL((ssd_state_update_kernel<TS, P, N, false, TIO, TDT>), dim3(batch * p.H),
+                       dim3(NTHR), 0, s, p);
+}
+
+// The layers' dtypes get fixed-type kernels: x, B, C, z and out all bf16 (or all
+// fp32), dt bf16 or fp32; anything else takes the per-tensor dtype codes.
 template <typename TS, int P, int N>
 void launch(const Params& p, int batch, bool tied, hipStream_t s) {
-  if (tied)
-    hipLaunchKernelGGL((ssd_state_update_kernel<TS, P, N, true>), dim3(batch * p.H), dim3(NTHR), 0, s, p);
-  else
-    hipLaunchKernelGGL((ssd_state_update_kernel<TS, P, N, false>), dim3(batch * p.H), dim3(NTHR), 0, s, p);
+  const int io = p.x_dt;
+  const bool same = p.b_dt == io && p.c_dt == io && p.out_dt == io && (!p.z || p.z_dt == io);
+  if (same && io == HMX_BF16 && p.dt_dt == HMX_BF16) launch_t<TS, P, N, bf16, bf16>(p, batch, tied, s);
+  else if (same && io == HMX_BF16 && p.dt_dt == HMX_F32) launch_t<TS, P, N, bf16, float>(p, batch, tied, s);
+  else if (same && io == HMX_F32 && p.dt_dt == HMX_F32) launch_t<TS, P, N, float, float>(p, batch, tied, s);
+  else launch_t<TS, P, N, Any, Any>(p, batch, tied, s);
 }
 
 }  // namespace ssdd
