@@ -68,6 +68,30 @@ def bench_prefill(dev, steps, warmup, HKV=32):
     return dict(ms=ms, tokens_per_s=T / (ms * 1e-3), bytes=by, flops=fl, GBps=gbs, TFLOPs=tfs)
 
 
+def bench_prefill_varlen(dev, steps, warmup):
+    """C1 varlen: 8 sequences with randint(1024, 8193) tokens (the config generator's
+    first draw), zero fp32 initial states, final states out."""
+    import torch
+    import hmx
+    from hmx import workloads as wl
+    H, D = 32, 128
+    lens = wl.varlen_lengths()
+    cu = wl.cu_from_lengths(lens).to(dev)
+    T = int(lens.sum())
+    d = wl.gdn_inputs(T=T, H=H, HKV=H, D=D, config_id=1, device=dev, gen_device=dev)
+    args = [d[n] for n in ("q", "k", "v", "g", "beta")]
+    h0 = torch.zeros(len(lens), H, D, D, device=dev)
+
+    def step():
+        hmx.chunk_gated_delta_rule_gqa(*args, initial_state=h0, output_final_state=True,
+                                       cu_seqlens=cu, use_qk_l2norm_in_kernel=True)
+
+    ms = _timed(step, steps, warmup)
+    by = wl.gdn_prefill_bytes(T, H, H, n_seqs=len(lens))
+    return dict(ms=ms, tokens=T, lengths=[int(x) for x in lens], tokens_per_s=T / (ms * 1e-3),
+                bytes=by, GBps=by / (ms * 1e-3) / 1e9)
+
+
 def bench_onorm(dev, steps, warmup):
     """The layer's output norm o_norm(o, z) at C1: the standalone gated RMSNorm kernel,
     prefill + norm as two ops, and the prefill with the norm fused into its epilogue."""
@@ -308,6 +332,53 @@ def cpu_baseline(sample_tokens=32768):
                 f"oracle chunked form (chunk 64) in fp32 torch on CPU, {dt:.2f} s")
 
 
+def cpu_baselines_more():
+    """The oracle on bounded samples of C2-C4, same host, fp32 torch on all cores:
+    C2 8 of the 512 decode steps (256 sequences x 32 heads, the 512 MiB pool), C3 the
+    first 1024 tokens at num_iter 8 (the per-token restatement), C4 the whole
+    workload (chunked form)."""
+    import torch
+    from hmx import workloads as wl
+    from oracle import gdn as gref, gka as kref, ssd as sref
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    f32 = torch.float32
+    out = {}
+    steps = 8
+    d = wl.decode_inputs(n_seqs=256, H=32, HKV=32, D=128, steps=steps)
+    pool = d["pool"].clone()
+    t0 = time.perf_counter()
+    for s in range(steps):
+        gref.fused_recurrent_gated_delta_rule_gqa(
+            d["q"][s], d["k"][s], d["v"][s], d["g"][s], d["beta"][s], initial_state=pool,
+            inplace_final_state=True, cu_seqlens=d["cu_seqlens"], ssm_state_indices=d["idx"],
+            use_qk_l2norm_in_kernel=True, dtype=f32)
+    dt = time.perf_counter() - t0
+    out["decode"] = dict(value=steps / dt, unit="steps/s", cores=cores, kind="port",
+                         sample=f"C2 {steps} of 512 steps (256 seqs x 32 heads), oracle "
+                                f"recurrence in fp32 torch on CPU, {dt:.2f} s")
+    T = 1024
+    g = wl.gka_inputs(T=T, H=32, HKV=32, D=128)
+    t0 = time.perf_counter()
+    kref.gka_chebyshev_gla_prefill(g["q"], g["k"], g["v"], g["alpha"], g["g"], g["gk"],
+                                   g["beta"], 128 ** -0.5, ridge_ratio=0.01, num_iter=8,
+                                   dtype=f32)
+    dt = time.perf_counter() - t0
+    out["gka_num_iter_8"] = dict(value=T / dt, unit="tokens/s", cores=cores, kind="port",
+                                 sample=f"C3 first {T} tokens x 32 heads, num_iter 8, oracle "
+                                        f"per-token form in fp32 torch on CPU, {dt:.2f} s")
+    x = wl.ssd_inputs()
+    t0 = time.perf_counter()
+    sref.mamba_chunk_scan_combined(x["x"], x["dt"], x["A"], x["B"], x["C"], 256, D=x["D"],
+                                   dt_bias=x["dt_bias"], dt_softplus=True,
+                                   return_final_states=True, dtype=f32)
+    dt = time.perf_counter() - t0
+    out["ssd"] = dict(value=2 * 16384 / dt, unit="tokens/s", cores=cores, kind="port",
+                      sample=f"C4 whole workload (2 x 16384 tokens x 64 heads), oracle chunked "
+                             f"form in fp32 torch on CPU, {dt:.2f} s")
+    return out
+
+
 def copy_calibration(dev, nbytes=1 << 30, reps=5):
     """A plain device copy of known size: what FETCH_SIZE / WRITE_SIZE read for it
     calibrates the counters (bytes moved per dispatch = nbytes each way)."""
@@ -351,6 +422,8 @@ def main():
     if a.only in (None, "prefill"):
         pf = bench_prefill(dev, a.steps, a.warmup)
         out["prefill"] = pf
+        out["prefill_gqa"] = bench_prefill(dev, a.steps, a.warmup, HKV=8)
+        out["prefill_varlen"] = bench_prefill_varlen(dev, a.steps, a.warmup)
     if a.only in (None, "onorm"):
         out["onorm"] = bench_onorm(dev, a.steps, a.warmup)
     if a.only in (None, "conv"):
@@ -387,6 +460,27 @@ def main():
                          "mfma_TFLOPs": round(pf["TFLOPs"], 1),
                          "mfma_frac": round(pf["TFLOPs"] / BF16_PEAK_TFLOPS, 4)},
         })
+    if "prefill_gqa" in out:
+        r = out["prefill_gqa"]
+        line["prefill_gqa"] = {
+            "value": round(r["tokens_per_s"], 1), "unit": "tokens/s", "ms_per_step": round(r["ms"], 4),
+            "config": {"workload": "C1 with HKV=8 (Qwen3-8B GQA layout)", "T": 32768, "H": 32,
+                       "HKV": 8, "d": 128},
+            "roofline": {"bound": "hbm", "achieved": round(r["GBps"], 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(r["GBps"] / HBM_PEAK_GBS, 4),
+                         "algorithmic_bytes": r["bytes"], "traffic": None,
+                         "mfma_TFLOPs": round(r["TFLOPs"], 1)},
+        }
+        r = out["prefill_varlen"]
+        line["prefill_varlen"] = {
+            "value": round(r["tokens_per_s"], 1), "unit": "tokens/s", "ms_per_step": round(r["ms"], 4),
+            "config": {"workload": "C1 varlen: 8 sequences, randint(1024, 8193) tokens",
+                       "lengths": r["lengths"], "tokens": r["tokens"], "H": 32, "d": 128,
+                       "initial_state": "zeros fp32 [8,32,128,128]"},
+            "roofline": {"bound": "hbm", "achieved": round(r["GBps"], 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(r["GBps"] / HBM_PEAK_GBS, 4),
+                         "algorithmic_bytes": r["bytes"], "traffic": None},
+        }
     if "decode" in out:
         dc = out["decode"]
         line["decode"] = {
@@ -484,6 +578,8 @@ def main():
         }
     if not a.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
+        if a.only is None:
+            line["cpu_baselines_more"] = cpu_baselines_more()
     print(json.dumps(line), flush=True)
 
 
