@@ -55,6 +55,29 @@ def test_prefill_varlen(dev, W, bias, act):
     assert torch.equal(pool_d.cpu(), pool_r.to(pool.dtype))
 
 
+def test_several_channel_groups(dev):
+    """4608 channels: two full 2048-channel workgroups and a partial third, for the
+    prefill (with states) and the decode update."""
+    dim = 4608
+    qs, x, w, b, pool, g = _setup([300, 45], dim, 4, 3, 3, 41)
+    idx = torch.tensor([2, 0], dtype=torch.int32)
+    out_r, pool_r = ref.causal_conv1d_varlen(x, w, b, pool, qs, idx, None, "silu")
+    pool_d = pool.to(dev)
+    out = hmx.causal_conv1d_fn(x.to(dev).t(), w.to(dev), b.to(dev),
+                               conv_states=pool_d.transpose(1, 2), query_start_loc=qs.to(dev),
+                               cache_indices=idx.to(dev))
+    torch.cuda.synchronize()
+    _close(out.t(), out_r)
+    assert torch.equal(pool_d.cpu(), pool_r.to(pool.dtype))
+    xd = torch.randn(2, dim, generator=g).bfloat16()
+    o_r, pool_r2 = ref.causal_conv1d_update(xd, pool_r, w, b, "silu", idx)
+    o = hmx.causal_conv1d_update(xd.to(dev), pool_d.transpose(1, 2), w.to(dev), b.to(dev),
+                                 "silu", conv_state_indices=idx.to(dev))
+    torch.cuda.synchronize()
+    _close(o, o_r)
+    assert torch.equal(pool_d.cpu(), pool_r2.to(pool.dtype))
+
+
 def test_tokens_past_last_sequence_are_zero(dev):
     """x longer than query_start_loc[-1] (a padded batch): the tail gives 0, and a
     batch of no sequences gives all zeros; validate_data rejects malformed bounds."""
