@@ -260,11 +260,11 @@ def bench_gka(dev, steps, warmup, num_iter):
                 GBps=by / (ms * 1e-3) / 1e9)
 
 
-def bench_ssd(dev, steps, warmup):
-    """C4: mamba_chunk_scan_combined, b=2, T=16384, H=64, P=64, N=128, G=8, fp32 final state."""
+def bench_ssd(dev, steps, warmup, b=2, T=16384, H=64, P=64, N=128, G=8):
+    """C4: mamba_chunk_scan_combined, b=2, T=16384, H=64, P=64, N=128, G=8, fp32 final
+    state (other shapes through the keywords: the primed layout is P = N = 128, G = H)."""
     import hmx
     from hmx import workloads as wl
-    b, T, H, P, N, G = 2, 16384, 64, 64, 128, 8
     d = wl.ssd_inputs(b=b, T=T, H=H, P=P, N=N, G=G, config_id=4, device=dev, gen_device=dev)
 
     def step():
@@ -436,6 +436,7 @@ def main():
         out["gka"] = {n: bench_gka(dev, max(2, a.steps // 4), 1, n) for n in (8, 32)}
     if a.only in (None, "ssd"):
         out["ssd"] = bench_ssd(dev, a.steps, a.warmup)
+        out["ssd_primed"] = bench_ssd(dev, max(2, a.steps // 2), a.warmup, P=128, N=128, G=64)
         out["ssd_decode"] = bench_ssd_decode(dev)
     line = {
         "metric": "mixer prefill tokens/sec + decode steps/sec at 8B shape; % of roofline (1 GPU)",
@@ -565,6 +566,15 @@ def main():
                          "traffic": measured_traffic("ssd_c4"), "algorithmic_bytes": r["bytes"],
                          "mfma_TFLOPs": round(r["TFLOPs"], 1),
                          "mfma_frac": round(r["TFLOPs"] / BF16_PEAK_TFLOPS, 4)},
+        }
+        r = out["ssd_primed"]
+        line["ssd_primed"] = {
+            "value": round(r["tokens_per_s"], 1), "unit": "tokens/s", "ms_per_step": round(r["ms"], 4),
+            "config": {"workload": "Mamba2 SSD scan, primed layout (secondary shape)", "B": 2,
+                       "T": 16384, "H": 64, "P": 128, "N": 128, "G": 64},
+            "roofline": {"bound": "hbm", "achieved": round(r["GBps"], 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(r["GBps"] / HBM_PEAK_GBS, 4),
+                         "algorithmic_bytes": r["bytes"], "traffic": None},
         }
         r = out["ssd_decode"]
         line["ssd_decode"] = {
