@@ -152,3 +152,31 @@ def test_pool_argument_errors(dev):
     with pytest.raises(ValueError, match="out must be"):
         hmx.chunk_gated_delta_rule_gqa(q, k, v, g, beta,
                                        out=torch.empty(1, 10, 2, D, device=dev))
+
+
+def test_prefill_pool_in_place_c1_varlen(dev):
+    """C1's varlen case (8 sequences, 36-42K tokens, H = 32) with the pool read and
+    written in place: the planner splits the long sequences into segments (staged
+    end states) exactly as at full scale; bit-identical to gather -> op -> scatter."""
+    from hmx import workloads as wl
+    lens = wl.varlen_lengths()
+    cu = wl.cu_from_lengths(lens).to(dev)
+    T = int(lens.sum())
+    d = wl.gdn_inputs(T=T, H=32, HKV=32, D=D, config_id=1, device=dev, gen_device=dev)
+    args = [d[n] for n in ("q", "k", "v", "g", "beta")]
+    g0 = torch.Generator(device=dev).manual_seed(9)
+    pool = torch.randn(12, 32, D, D, generator=g0, device=dev) * 0.02
+    idx = torch.tensor([7, 2, 11, 0, 5, 9, 1, 4], dtype=torch.int32, device=dev)
+    has = torch.tensor([True, False, True, True, False, True, True, True], device=dev)
+    init = pool[idx.long()].contiguous()
+    init[~has] = 0
+    o_ref, s_ref = hmx.chunk_gated_delta_rule_gqa(*args, initial_state=init, output_final_state=True,
+                                                  cu_seqlens=cu, use_qk_l2norm_in_kernel=True)
+    pool_ref = pool.clone()
+    pool_ref[idx.long()] = s_ref
+    pool2 = pool.clone()
+    o, _ = hmx.chunk_gated_delta_rule_gqa(*args, initial_state=pool2, output_final_state=True,
+                                          cu_seqlens=cu, use_qk_l2norm_in_kernel=True,
+                                          ssm_state_indices=idx, has_initial_state=has)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o_ref) and torch.equal(pool2, pool_ref)
