@@ -15,6 +15,8 @@ stream.  There is no CPU fallback.
 """
 from __future__ import annotations
 
+import heapq
+
 import torch
 
 from .. import _lib
@@ -228,17 +230,53 @@ def _cu_count(device: torch.device) -> int:
     return _CU_COUNT[idx]
 
 
+def _balanced_counts(chunks: list[int], budget: int, min_seg: int) -> list[int]:
+    """Segments per sequence, at most ``budget`` in all, given one at a time to the
+    sequence whose segments are currently the longest (the longest segment bounds
+    the runtime when all segments run at once), down to ``min_seg`` chunks."""
+    ns = [1] * len(chunks)
+    heap = [(-c, n) for n, c in enumerate(chunks)]
+    heapq.heapify(heap)
+    total = len(chunks)
+    while total < budget and heap:
+        neg, n = heapq.heappop(heap)
+        if -neg < 2 * min_seg or chunks[n] / (ns[n] + 1) < min_seg:
+            continue          # too short to split further
+        ns[n] += 1
+        total += 1
+        heapq.heappush(heap, (-chunks[n] / ns[n], n))
+    return ns
+
+
 def _segment_table(bounds: list[tuple[int, int]], H: int, workgroups: int,
-                   segment_chunks: int | None = None, chunk: int = CHUNK) -> list[list[int]]:
+                   segment_chunks: int | None = None, chunk: int = CHUNK,
+                   warm_chunks: int = 3) -> list[list[int]]:
     """Rows (n, bos, eos, c_start, c_end, seg_idx, first_seg, nseg) for every sequence,
-    over ``chunk``-token chunks."""
+    over ``chunk``-token chunks.
+
+    With ``segment_chunks`` every sequence is cut into equal segments of at most
+    that many chunks (tests).  Otherwise the segment counts are balanced for
+    ``workgroups`` concurrent workgroups (``H`` per segment): one wave of segments
+    (at most workgroups / H per head) or two waves of shorter ones, whichever has
+    the smaller estimated makespan (the longest segment, plus ``warm_chunks`` of
+    warm-up for a split one, times the waves)."""
     chunks = [-(-(eos - bos) // chunk) for bos, eos in bounds]
-    if segment_chunks is None:
-        total = max(1, sum(chunks))
-        segment_chunks = max(MIN_SEGMENT_CHUNKS, -(-total * H // max(1, workgroups)))
+    if segment_chunks is not None:
+        counts = [max(1, -(-nc // segment_chunks)) for nc in chunks]
+    else:
+        slots = max(1, workgroups // max(1, H))
+        best = None
+        for waves in (1, 2):
+            cnt = _balanced_counts(chunks, waves * slots, MIN_SEGMENT_CHUNKS)
+            longest = max((-(-nc // ns) + (warm_chunks if ns > 1 else 0)
+                           for nc, ns in zip(chunks, cnt)), default=0)
+            # segments beyond one wave of slots queue behind the first wave
+            est = longest * min(waves, -(-sum(cnt) // slots))
+            if best is None or est < best[0]:
+                best = (est, cnt)
+        counts = best[1]
     rows: list[list[int]] = []
-    for n, ((bos, eos), nc) in enumerate(zip(bounds, chunks)):
-        ns = max(1, -(-nc // segment_chunks))
+    for n, ((bos, eos), nc, ns) in enumerate(zip(bounds, chunks, counts)):
         first = len(rows)
         for i in range(ns):
             rows.append([n, bos, eos, i * nc // ns, (i + 1) * nc // ns, i, first, ns])
