@@ -120,4 +120,15 @@ __device__ __forceinline__ float fast_exp(float x) {
   return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
 }
 
+// softplus with mamba's threshold (x for x > 20): max(x, 0) + log1p(e^{-|x|}),
+// log1p by Goldberg's correction log(w) u / (w - 1), w = 1 + u (exact for u
+// below w's rounding), on the hardware exp/log.
+__device__ __forceinline__ float softplus20(float x) {
+  if (x > 20.f) return x;
+  const float u = fast_exp(-fabsf(x));
+  const float w = 1.f + u;
+  const float l1p = (w == 1.f) ? u : __logf(w) * (u / (w - 1.f));
+  return fmaxf(x, 0.f) + l1p;
+}
+
 }  // namespace hmx

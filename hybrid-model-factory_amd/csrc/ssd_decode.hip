@@ -139,11 +139,11 @@ __global__ __launch_bounds__(NTHR) void ssd_state_update_kernel(Params p) {
     const float xv = xs[k];
     float d = ds[k];
     if (p.dt_bias) d += p.dt_bias[(int64_t)h * p.db_hs + (int64_t)pr * p.db_ps];
-    if (p.softplus) d = d <= 20.f ? log1pf(expf(d)) : d;
+    if (p.softplus) d = softplus20(d);
     const float dx = d * xv;
     float acc = 0.f;
     if constexpr (A_TIED) {
-      const float da = expf(p.A[(int64_t)h * p.a_hs] * d);
+      const float da = fast_exp(p.A[(int64_t)h * p.a_hs] * d);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         st[k][j] = st[k][j] * da + dx * bv[j];
@@ -153,7 +153,7 @@ __global__ __launch_bounds__(NTHR) void ssd_state_update_kernel(Params p) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const float a = p.A[(int64_t)h * p.a_hs + (int64_t)pr * p.a_ps + (int64_t)(n0 + j) * p.a_ns];
-        st[k][j] = st[k][j] * expf(a * d) + dx * bv[j];
+        st[k][j] = st[k][j] * fast_exp(a * d) + dx * bv[j];
         acc += st[k][j] * cv[j];
       }
     }
@@ -163,7 +163,7 @@ __global__ __launch_bounds__(NTHR) void ssd_state_update_kernel(Params p) {
       if (p.D) o += p.D[(int64_t)h * p.d_hs + (int64_t)pr * p.d_ps] * xv;
       if (p.z) {
         const float zz = ld_t<TIO>(p.z, (int64_t)i * p.z_bs + (int64_t)h * p.z_hs + (int64_t)pr * p.z_ps, p.z_dt);
-        o *= zz / (1.f + expf(-zz));
+        o *= zz * __builtin_amdgcn_rcpf(1.f + fast_exp(-zz));
       }
       st_t<TIO>(p.out, (int64_t)i * p.o_bs + (int64_t)h * p.o_hs + (int64_t)pr * p.o_ps, p.out_dt, o);
     }

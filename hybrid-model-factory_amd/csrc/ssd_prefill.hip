@@ -110,17 +110,6 @@ __device__ __forceinline__ SegInfo load_seg(const int* seg, int s) {
   return SegInfo{r[0], r[1], r[2], r[3], r[4], r[5], r[6], r[7]};
 }
 
-// softplus with mamba's threshold (x for x > 20): max(x, 0) + log1p(e^{-|x|}),
-// log1p by Goldberg's correction log(w) u / (w - 1), w = 1 + u (exact for u
-// below w's rounding), on the hardware exp/log.
-__device__ __forceinline__ float softplus20(float x) {
-  if (x > 20.f) return x;
-  const float u = fast_exp(-fabsf(x));
-  const float w = 1.f + u;
-  const float l1p = (w == 1.f) ? u : __logf(w) * (u / (w - 1.f));
-  return fmaxf(x, 0.f) + l1p;
-}
-
 // Inclusive prefix sum over the 64 lanes of a wave.
 __device__ __forceinline__ float scan64(float x, int lane) {
   x = scan32(x);
