@@ -48,7 +48,9 @@ struct Params {
   const void* z; int z_dt; int64_t z_bs, z_hs, z_ps;  // or null
   void* out; int out_dt; int64_t o_bs, o_hs, o_ps;
   const int* src_idx; const int* dst_idx; int pad_slot;
-  int H, G, softplus;
+  // x has HX heads, B G groups and C GC groups (each divides H): head h reads
+  // x head h / (H/HX), B group h / (H/G) and C group h / (H/GC).
+  int H, HX, G, GC, softplus;
 };
 
 __device__ __forceinline__ float ld_any(const void* p, int64_t i, int dt) {
@@ -107,7 +109,7 @@ __global__ __launch_bounds__(NTHR) void ssd_state_update_kernel(Params p) {
   constexpr int RPP = NTHR / GN;       // rows per pass
   constexpr int PASSES = P / RPP;
   const int i = blockIdx.x / p.H, h = blockIdx.x % p.H;
-  const int g = h / (p.H / p.G);
+  const int g = h / (p.H / p.G), gc = h / (p.H / p.GC), hx = h / (p.H / p.HX);
   const int src = p.src_idx ? p.src_idx[i] : i;
   if (src == p.pad_slot) return;
   const int dst = p.dst_idx ? p.dst_idx[i] : src;
@@ -117,7 +119,7 @@ __global__ __launch_bounds__(NTHR) void ssd_state_update_kernel(Params p) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     bv[j] = ld_t<TIO>(p.B, (int64_t)i * p.b_bs + (int64_t)g * p.b_gs + n0 + j, p.b_dt);
-    cv[j] = ld_t<TIO>(p.C, (int64_t)i * p.c_bs + (int64_t)g * p.c_gs + n0 + j, p.c_dt);
+    cv[j] = ld_t<TIO>(p.C, (int64_t)i * p.c_bs + (int64_t)gc * p.c_gs + n0 + j, p.c_dt);
   }
   const TS* sin = static_cast<const TS*>(p.state) + (int64_t)src * p.slot_stride + (int64_t)h * P * N;
   TS* sout = static_cast<TS*>(p.state) + (int64_t)dst * p.slot_stride + (int64_t)h * P * N;
@@ -129,7 +131,7 @@ __global__ __launch_bounds__(NTHR) void ssd_state_update_kernel(Params p) {
 #pragma unroll
   for (int k = 0; k < PASSES; ++k) {
     const int pr = r0 + k * RPP;
-    xs[k] = ld_t<TIO>(p.x, (int64_t)i * p.x_bs + (int64_t)h * p.x_hs + (int64_t)pr * p.x_ps, p.x_dt);
+    xs[k] = ld_t<TIO>(p.x, (int64_t)i * p.x_bs + (int64_t)hx * p.x_hs + (int64_t)pr * p.x_ps, p.x_dt);
     ds[k] = ld_t<TDT>(p.dt, (int64_t)i * p.dt_bs + (int64_t)h * p.dt_hs + (int64_t)pr * p.dt_ps, p.dt_dt);
   }
 
@@ -209,13 +211,16 @@ extern "C" int hmx_ssd_state_update(
     int64_t db_hs, int64_t db_ps, const void* z, int32_t z_dtype, int64_t z_bs, int64_t z_hs,
     int64_t z_ps, void* out, int32_t out_dtype, int64_t o_bs, int64_t o_hs, int64_t o_ps,
     const int32_t* state_batch_indices, const int32_t* dst_state_batch_indices,
-    int32_t pad_slot_id, int32_t batch, int32_t H, int32_t G, int32_t P, int32_t N,
+    int32_t pad_slot_id, int32_t batch, int32_t H, int32_t HX, int32_t G, int32_t GC, int32_t P,
+    int32_t N,
     int32_t dt_softplus, void* stream) {
   HMX_REQUIRE(state_dtype == HMX_F32 || state_dtype == HMX_BF16, HMX_EUNSUPPORTED,
               "hmx_ssd_state_update: state must be float32 or bfloat16 (dtype code %d)", state_dtype);
   HMX_REQUIRE((P == 64 || P == 128) && (N == 64 || N == 128), HMX_EUNSUPPORTED,
               "hmx_ssd_state_update: headdim in {64,128} and d_state in {64,128} (got %d, %d)", P, N);
-  HMX_REQUIRE(H > 0 && G > 0 && H % G == 0, HMX_EINVAL, "hmx_ssd_state_update: H=%d G=%d", H, G);
+  HMX_REQUIRE(H > 0 && HX > 0 && G > 0 && GC > 0 && H % HX == 0 && H % G == 0 && H % GC == 0,
+              HMX_EINVAL, "hmx_ssd_state_update: H=%d must be a multiple of HX=%d, G=%d and GC=%d",
+              H, HX, G, GC);
   HMX_REQUIRE(state && x && dt && A && B && C && out, HMX_EINVAL,
               "hmx_ssd_state_update: null tensor pointer");
   HMX_REQUIRE(slot_stride % 4 == 0, HMX_EINVAL,
@@ -233,7 +238,7 @@ extern "C" int hmx_ssd_state_update(
   p.z = z; p.z_dt = z_dtype; p.z_bs = z_bs; p.z_hs = z_hs; p.z_ps = z_ps;
   p.out = out; p.out_dt = out_dtype; p.o_bs = o_bs; p.o_hs = o_hs; p.o_ps = o_ps;
   p.src_idx = state_batch_indices; p.dst_idx = dst_state_batch_indices; p.pad_slot = pad_slot_id;
-  p.H = H; p.G = G; p.softplus = dt_softplus;
+  p.H = H; p.HX = HX; p.G = G; p.GC = GC; p.softplus = dt_softplus;
   const bool tied = a_ps == 0 && a_ns == 0;
   hipStream_t s = (hipStream_t)stream;
 #define HMX_SSDD(TS)                                          \

@@ -69,7 +69,9 @@ struct Params {
   float* ws_loc;           // [nseg][H][P][N] zero-start segment end states
   float* ws_s0;            // [nseg][H][P][N] segment start states
   float* ws_dec;           // [nseg][H] segment log-decay sum_t a_t
-  int H, G, softplus;
+  // x has HX heads and C has GC groups, B has G groups (each divides H): head h
+  // reads x head h / (H/HX), B group h / (H/G) and C group h / (H/GC).
+  int H, HX, G, GC, softplus;
   float dt_min, dt_max;
 };
 
@@ -125,14 +127,14 @@ struct Raw {
 
 template <int P, int N, int MODE>
 __device__ __forceinline__ void load_raw(Raw<P, N>& r, const Params& p, int tok0, int nval,
-                                         int h, int g, int tid) {
+                                         int h, int hx, int g, int gc, int tid) {
   using K = Cfg<P, N>;
 #pragma unroll
   for (int i = 0; i < K::VX; ++i) {
     const int e = tid + NTHR * i, row = e / (P / 8), c8 = (e % (P / 8)) * 8;
     const bool ok = row < nval;
     const int64_t tok = tok0 + row;
-    r.x[i] = ok ? *reinterpret_cast<const bf16x8*>(p.x + tok * p.x_ts + h * p.x_hs + c8) : bf16x8{};
+    r.x[i] = ok ? *reinterpret_cast<const bf16x8*>(p.x + tok * p.x_ts + hx * p.x_hs + c8) : bf16x8{};
     if (MODE == MODE_OUT)
       r.z[i] = (ok && p.z) ? *reinterpret_cast<const bf16x8*>(p.z + tok * p.z_ts + h * p.z_hs + c8)
                            : bf16x8{};
@@ -144,7 +146,7 @@ __device__ __forceinline__ void load_raw(Raw<P, N>& r, const Params& p, int tok0
     const int64_t tok = tok0 + row;
     r.b[i] = ok ? *reinterpret_cast<const bf16x8*>(p.B + tok * p.b_ts + g * p.b_gs + c8) : bf16x8{};
     if (MODE == MODE_OUT)
-      r.c[i] = ok ? *reinterpret_cast<const bf16x8*>(p.C + tok * p.c_ts + g * p.c_gs + c8) : bf16x8{};
+      r.c[i] = ok ? *reinterpret_cast<const bf16x8*>(p.C + tok * p.c_ts + gc * p.c_gs + c8) : bf16x8{};
   }
   const int t = tid - (NTHR - L);   // the last wave loads dt (lane t = token t)
   if (t >= 0)
@@ -174,6 +176,7 @@ __global__ __launch_bounds__(NTHR, 2) void ssd_chunk_kernel(Params p) {
   const int H = p.H, G = p.G, HG = H / G;
   const int id = blockIdx.x, sg = id % (p.nseg_total * G);
   const int s_id = sg / G, g = sg % G, h = g * HG + id / (p.nseg_total * G);
+  const int hx = h / (H / p.HX), gc = h / (H / p.GC);
   const SegInfo si = load_seg(p.seg, s_id);
   if (MODE == MODE_LOCAL && si.seg_idx == si.nseg - 1) return;
 
@@ -223,9 +226,9 @@ __global__ __launch_bounds__(NTHR, 2) void ssd_chunk_kernel(Params p) {
   Raw<P, N> ra, rb;
   const auto nval_of = [&](int c) { return min(L, si.eos - (si.bos + c * L)); };
   if (si.c_start < si.c_end)
-    load_raw<P, N, MODE>(ra, p, si.bos + si.c_start * L, nval_of(si.c_start), h, g, tid);
+    load_raw<P, N, MODE>(ra, p, si.bos + si.c_start * L, nval_of(si.c_start), h, hx, g, gc, tid);
   if (AHEAD == 2 && si.c_start + 1 < si.c_end)
-    load_raw<P, N, MODE>(rb, p, si.bos + (si.c_start + 1) * L, nval_of(si.c_start + 1), h, g, tid);
+    load_raw<P, N, MODE>(rb, p, si.bos + (si.c_start + 1) * L, nval_of(si.c_start + 1), h, hx, g, gc, tid);
 
   // dt' = clamp(softplus(dt + bias)), A_t = cumsum(dt' A), w_t = dt' e^{A_L - A_t},
   // e^{A_t} of chunk c into scalar buffer `buf` (the last wave; lane = token)
@@ -278,7 +281,7 @@ __global__ __launch_bounds__(NTHR, 2) void ssd_chunk_kernel(Params p) {
       for (int i = 0; i < K::VX; ++i) zst[i] = cur.z[i];
     }
     if (c + AHEAD < si.c_end)
-      load_raw<P, N, MODE>(cur, p, tok0 + AHEAD * L, nval_of(c + AHEAD), h, g, tid);
+      load_raw<P, N, MODE>(cur, p, tok0 + AHEAD * L, nval_of(c + AHEAD), h, hx, g, gc, tid);
     lds_barrier();
     const float al = SC(cb, S_ACS, L - 1);
 
@@ -565,14 +568,16 @@ extern "C" int hmx_ssd_chunk_fwd(const void* x, int64_t x_ts, int64_t x_hs, cons
                                  void* h_final, int64_t state_slot_stride, int32_t state_dtype,
                                  const int32_t* state_indices, const uint8_t* has_initial_state,
                                  const int32_t* seg_table, int32_t nseg_total,
-                                 int32_t nseq, int32_t H, int32_t G, int32_t P, int32_t N,
-                                 int32_t dt_softplus, float dt_min, float dt_max, void* workspace,
+                                 int32_t nseq, int32_t H, int32_t HX, int32_t G, int32_t GC,
+                                 int32_t P, int32_t N, int32_t dt_softplus, float dt_min, float dt_max, void* workspace,
                                  size_t workspace_bytes, void* stream) {
   HMX_REQUIRE(xbc_dtype == HMX_BF16, HMX_EUNSUPPORTED,
               "hmx_ssd_chunk_fwd: x/B/C/z must be bfloat16 (got dtype code %d)", xbc_dtype);
   HMX_REQUIRE((P == 64 || P == 128) && (N == 64 || N == 128), HMX_EUNSUPPORTED,
               "hmx_ssd_chunk_fwd: headdim in {64,128} and d_state in {64,128} (got %d, %d)", P, N);
-  HMX_REQUIRE(H > 0 && G > 0 && H % G == 0, HMX_EINVAL, "hmx_ssd_chunk_fwd: H=%d G=%d", H, G);
+  HMX_REQUIRE(H > 0 && HX > 0 && G > 0 && GC > 0 && H % HX == 0 && H % G == 0 && H % GC == 0,
+              HMX_EINVAL, "hmx_ssd_chunk_fwd: H=%d must be a multiple of HX=%d, G=%d and GC=%d",
+              H, HX, G, GC);
   HMX_REQUIRE(x && B && C && dt && A && y && seg_table, HMX_EINVAL,
               "hmx_ssd_chunk_fwd: null tensor pointer");
   HMX_REQUIRE(dt_dtype == HMX_F32 || dt_dtype == HMX_BF16 || dt_dtype == HMX_F16, HMX_EINVAL,
@@ -607,7 +612,7 @@ extern "C" int hmx_ssd_chunk_fwd(const void* x, int64_t x_ts, int64_t x_hs, cons
   p.ws_loc = multi ? ws : nullptr;
   p.ws_s0 = multi ? ws + st : nullptr;
   p.ws_dec = multi ? ws + 2 * st : nullptr;
-  p.H = H; p.G = G; p.softplus = dt_softplus; p.dt_min = dt_min; p.dt_max = dt_max;
+  p.H = H; p.HX = HX; p.G = G; p.GC = GC; p.softplus = dt_softplus; p.dt_min = dt_min; p.dt_max = dt_max;
   hipStream_t s = (hipStream_t)stream;
   if (P == 64 && N == 128) launch<64, 128>(p, nseq, s);
   else if (P == 128 && N == 128) launch<128, 128>(p, nseq, s);

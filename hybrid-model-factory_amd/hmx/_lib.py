@@ -56,7 +56,8 @@ SIGNATURES: dict[str, list] = {
     "hmx_ssd_chunk_fwd": [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I32,
                           _P, _I32, _I64, _I64, _P, _P, _P, _P, _I64, _I64,
                           _P, _I64, _I64, _P, _P, _I64, _I32, _P, _P, _P, _I32, _I32,
-                          _I32, _I32, _I32, _I32, _I32, _F32, _F32, _P, ctypes.c_size_t, _P],
+                          _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _F32, _P, ctypes.c_size_t,
+                          _P],
     "hmx_ssd_chunk_workspace_bytes": [_I32, _I32, _I32, _I32, _I32],
     "hmx_causal_conv1d_fwd": [_P, _I64, _P, _I64, _I32, _P, _I32, _I32, _P, _I32, _P, _I64, _I64,
                               _I32, _P, _I32, _I64, _P, _P, _I32, _I32, _I32, _P],
@@ -68,7 +69,7 @@ SIGNATURES: dict[str, list] = {
                              _P, _I32, _I64, _I64, _P, _I32, _I64, _I64,
                              _P, _I64, _I64, _P, _I64, _I64,
                              _P, _I32, _I64, _I64, _I64, _P, _I32, _I64, _I64, _I64,
-                             _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _P],
+                             _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _P],
 }
 _RESTYPES = {"hmx_last_error": ctypes.c_char_p, "hmx_gdn_chunk_workspace_bytes": ctypes.c_size_t,
              "hmx_gka_chunk_workspace_bytes": ctypes.c_size_t,

@@ -195,7 +195,7 @@ def _ssd_varlen(x: Tensor, dt: Tensor, A: Tensor, B: Tensor, C: Tensor, chunk_si
 @_ssd_varlen.register_fake
 def _(x, dt, A, B, C, chunk_size, cu_seqlens, out, D, z, dt_bias, initial_states, dt_softplus,
       dt_min, dt_max):
-    T, H, P = x.shape
+    H, P = dt.shape[1], x.shape[2]
     return x.new_empty(cu_seqlens.shape[0] - 1, H, P, B.shape[-1], dtype=torch.float32)
 
 
@@ -322,7 +322,7 @@ def mamba_chunk_scan_combined_varlen(x, dt, A, B, C, chunk_size, cu_seqlens, cu_
     if return_intermediate_states:
         raise NotImplementedError("return_intermediate_states is not supported by hmx")
     if out is None:
-        out = x.new_empty(x.shape)
+        out = x.new_empty(x.shape[0], dt.shape[1], x.shape[2])
     st = torch.ops.hmx.mamba_chunk_scan_combined_varlen(
         x, dt, A, B, C, int(chunk_size), cu_seqlens, out, D, z, dt_bias, initial_states,
         bool(dt_softplus), float(dt_limit[0]), float(dt_limit[1]))
@@ -334,7 +334,7 @@ def selective_state_update(state, x, dt, A, B, C, D=None, z=None, dt_bias=None,
                            dst_state_batch_indices=None, pad_slot_id=-1, out=None):
     """``torch.ops.hmx.selective_state_update``; returns ``out``."""
     if out is None:
-        out = torch.empty_like(x)
+        out = x.new_empty(dt.shape)
     torch.ops.hmx.selective_state_update(state, x, dt, A, B, C, D, z, dt_bias, bool(dt_softplus),
                                          state_batch_indices, dst_state_batch_indices,
                                          int(pad_slot_id), out)

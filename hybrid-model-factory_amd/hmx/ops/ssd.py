@@ -42,20 +42,26 @@ def _prep3(t: torch.Tensor) -> torch.Tensor:
 
 def _ssd_scan(x, dt, A, B, C, D, z, dt_bias, dt_softplus, dt_limit, bounds, h0, y,
               want_final: bool, segment_chunks=None, pooled=None):
-    """Core launcher over flattened tokens.  x, z, y [T,H,P]; dt [T,H]; B, C [T,G,N];
+    """Core launcher over flattened tokens.  z, y [T,H,P]; dt [T,H]; x [T,HX,P],
+    B [T,G,N], C [T,GC,N] with HX, G, GC dividing H (head h reads x head
+    h // (H // HX), B group h // (H // G), C group h // (H // GC));
     bounds: list of (bos, eos); h0 fp32 [nseq,H,P,N] or None.  Returns the fp32 end
     states [nseq,H,P,N] (or None).  ``pooled`` = (pool, slot indices, has_initial_state
     or None): sequences read and (with want_final) write the pool's slots in place
     instead, and the pool is returned."""
-    T, H, P = x.shape
-    G, N = B.shape[1], B.shape[2]
+    T, HX, P = x.shape
+    H = dt.shape[1]
+    G, N, GC = B.shape[1], B.shape[2], C.shape[1]
     if x.dtype != torch.bfloat16 or B.dtype != torch.bfloat16 or C.dtype != torch.bfloat16:
         raise NotImplementedError("hmx SSD scan: x, B and C must be bfloat16 "
                                   f"(got {x.dtype}, {B.dtype}, {C.dtype})")
     if z is not None and z.dtype != torch.bfloat16:
         z = z.to(torch.bfloat16)
-    if H % G != 0:
-        raise ValueError(f"nheads {H} must be a multiple of ngroups {G}")
+    if H % G != 0 or H % GC != 0 or H % HX != 0:
+        raise ValueError(f"nheads {H} must be a multiple of ngroups {G} (B), {GC} (C) and of "
+                         f"x's heads {HX}")
+    if tuple(C.shape) != (T, GC, N) or tuple(y.shape) != (T, H, P):
+        raise ValueError(f"C must be [{T}, groups, {N}] and out [{T}, {H}, {P}]")
     x, B, C, y = _prep3(x), _prep3(B), _prep3(C), y
     z = None if z is None else _prep3(z)
     if not _vec_ok(y, (0, 1)):
@@ -91,7 +97,7 @@ def _ssd_scan(x, dt, A, B, C, D, z, dt_bias, dt_softplus, dt_limit, bounds, h0, 
               _lib.ptr(z), 0 if z is None else z.stride(0), 0 if z is None else z.stride(1),
               _lib.ptr(y), y.stride(0), y.stride(1), _lib.ptr(h0), _lib.ptr(hT), st_ss, st_dt,
               _lib.ptr(idx), _lib.ptr(hinit),
-              _lib.ptr(seg), len(rows), nseq, H, G, P, N, int(bool(dt_softplus)), lo, hi,
+              _lib.ptr(seg), len(rows), nseq, H, HX, G, GC, P, N, int(bool(dt_softplus)), lo, hi,
               _lib.ptr(ws), ws.numel(), _lib.stream_of(x))
     return hT
 
@@ -203,12 +209,19 @@ def mamba_chunk_scan_combined_varlen(x, dt, A, B, C, chunk_size, cu_seqlens, cu_
     is written back into that slot in place; the pool is returned.  This replaces
     the layer's gather and scatter around the op (primed_mamba2_layer.py:812-824,
     :941).
+
+    Grouped operands (no reference counterpart): the heads H are dt's; x may hold
+    HX heads and C its own GC groups (each dividing H), head h reading x head
+    h // (H // HX) and C group h // (H // GC), as B's groups already work.  The
+    primed layer's repeat_kv'd x and B (primed_mamba2_layer.py:800-835) are read
+    in place this way.
     """
     if return_intermediate_states:
         raise NotImplementedError("return_intermediate_states (prefix-cache chunk states) is "
                                   "not supported by the hmx SSD scan")
     _lib.require_gpu(x, dt, A, B, C, D, z, dt_bias, initial_states, cu_seqlens, out)
-    T, H, P = x.shape
+    T, P = x.shape[0], x.shape[2]
+    H = dt.shape[1]
     N = B.shape[-1]
     cs = [int(v) for v in cu_seqlens.tolist()]
     bounds = [(cs[i], cs[i + 1]) for i in range(len(cs) - 1)]
@@ -258,14 +271,20 @@ def selective_state_update(state, x, dt, A, B, C, D=None, z=None, dt_bias=None,
     B, C [b,G,N] (or [b,N]); D, dt_bias [H,P]; z [b,H,P]; state_batch_indices
     [b] (entries equal to pad_slot_id are skipped); dst_state_batch_indices [b]
     (write target, default the source slot).  ``out`` is written in place
-    (allocated like x when None) and returned.
+    (allocated like dt when None, in x's dtype) and returned.
+
+    Grouped operands (no reference counterpart): x may hold HX heads and C its
+    own GC groups (each dividing H), head h reading x head h // (H // HX) and C
+    group h // (H // GC), so the primed layer's repeat_kv'd x and B
+    (primed_mamba2_layer.py:972-985) are read in place.
     """
     if num_accepted_tokens is not None or cu_seqlens is not None:
         raise NotImplementedError("multi-token (speculative) selective_state_update is not "
                                   "supported by hmx")
     _lib.require_gpu(state, x, dt, A, B, C, D, z, dt_bias, state_batch_indices,
                      dst_state_batch_indices, out)
-    if state.dim() == 3:   # no head dim
+    headless = state.dim() == 3
+    if headless:   # no head dim
         state, x, dt, A = state.unsqueeze(1), x.unsqueeze(1), dt.unsqueeze(1), A.unsqueeze(0)
         B, C = B.unsqueeze(1), C.unsqueeze(1)
         D = None if D is None else D.unsqueeze(0)
@@ -275,17 +294,21 @@ def selective_state_update(state, x, dt, A, B, C, D=None, z=None, dt_bias=None,
             out = out.unsqueeze(1)
     slots, H, P, N = state.shape
     bsz = x.shape[0]
-    G = B.shape[1]
-    if tuple(x.shape) != (bsz, H, P) or tuple(dt.shape) != (bsz, H, P):
-        raise ValueError(f"x and dt must be {(bsz, H, P)}, got {tuple(x.shape)}, {tuple(dt.shape)}")
+    G, GC, HX = B.shape[1], C.shape[1], x.shape[1]
+    if (x.dim() != 3 or x.shape[0] != bsz or x.shape[2] != P or H % HX != 0
+            or tuple(dt.shape) != (bsz, H, P)):
+        raise ValueError(f"x must be [{bsz}, heads dividing {H}, {P}] and dt {(bsz, H, P)}, got "
+                         f"{tuple(x.shape)}, {tuple(dt.shape)}")
     if tuple(A.shape) != (H, P, N):
         raise ValueError(f"A must be {(H, P, N)}, got {tuple(A.shape)}")
-    if H % G != 0 or tuple(B.shape) != (bsz, G, N) or tuple(C.shape) != (bsz, G, N):
-        raise ValueError(f"B, C must be [{bsz}, G, {N}] with G dividing {H}")
+    if H % G != 0 or H % GC != 0 or tuple(B.shape) != (bsz, G, N) or tuple(C.shape) != (bsz, GC, N):
+        raise ValueError(f"B, C must be [{bsz}, groups, {N}] with groups dividing {H}")
     if state.stride(3) != 1 or state.stride(2) != N or state.stride(1) != P * N:
         raise ValueError("state must be contiguous within a slot ([H,P,N] row-major)")
     if out is None:
-        out = torch.empty_like(x)
+        out = torch.empty(bsz, H, P, dtype=x.dtype, device=x.device)
+    if tuple(out.shape) != (bsz, H, P):
+        raise ValueError(f"out must be {(bsz, H, P)}, got {tuple(out.shape)}")
     A = A if A.dtype == torch.float32 else A.to(torch.float32)
     B = B if B.stride(-1) == 1 else B.contiguous()
     C = C if C.stride(-1) == 1 else C.contiguous()
@@ -307,9 +330,9 @@ def selective_state_update(state, x, dt, A, B, C, D=None, z=None, dt_bias=None,
               _lib.ptr(D), st(D, 0), st(D, 1), _lib.ptr(dt_bias), st(dt_bias, 0), st(dt_bias, 1),
               _lib.ptr(z), 0 if z is None else _lib.dtype_code(z), st(z, 0), st(z, 1), st(z, 2),
               _lib.ptr(out), _lib.dtype_code(out), out.stride(0), out.stride(1), out.stride(2),
-              _lib.ptr(src), _lib.ptr(dst), int(pad_slot_id), bsz, H, G, P, N,
+              _lib.ptr(src), _lib.ptr(dst), int(pad_slot_id), bsz, H, HX, G, GC, P, N,
               int(bool(dt_softplus)), _lib.stream_of(x))
-    return out
+    return out.squeeze(1) if headless else out
 
 
 __all__ = ["mamba_chunk_scan_combined", "mamba_chunk_scan_combined_varlen",

@@ -1,5 +1,5 @@
-"""The vLLM layers' mixer cores over hmx ops: ``gdn_forward_core`` and
-``gka_forward_core``.
+"""The vLLM layers' mixer cores over hmx ops: ``gdn_forward_core``,
+``gka_forward_core`` and ``mamba2_conv_ssm_forward``.
 
 These restate ``PrimedGatedDeltaNetAttention._forward_core``
 (vllm-inference/src/primed_vllm/primed_gdn_layer.py:635-936) and
@@ -37,6 +37,16 @@ slice.
 
 Speculative decoding (``spec_sequence_masks``) and the low-rank k/v projection
 (``proj_k``) raise NotImplementedError.
+
+``mamba2_conv_ssm_forward`` restates ``PrimedMamba2Layer.conv_ssm_forward``
+(primed_mamba2_layer.py:615-1021) the same way: the decode and prefill convs write
+one buffer, the repeat_kv'd x and B and the per-head C are read in place from it
+by the SSD ops' grouped operands (no rearrange / repeat_kv / permute copies,
+:800-835, :972-985), the prefill scan reads and writes the state pool by slot (no
+gather and scatter, :812-824, :941), and both scans write ``output`` directly.
+The B/C RMSNorms run through the layer's own modules, as the reference calls
+them (:663-669).  Prefix caching (``mamba_cache_mode == "all"``) and the rotary
+position embedding (``use_pos_embed``) raise NotImplementedError.
 """
 from __future__ import annotations
 
@@ -195,3 +205,81 @@ def gka_forward_core(layer, mixed_qkv: torch.Tensor, a: torch.Tensor, alpha_in: 
             sl(beta, ndt, n), h_kk_initial=h_kk_state, h_kv_initial=h_kv_state,
             output_final_state=True, cu_seqlens=cu_p, ssm_state_indices=idx_p,
             has_initial_state=has_p, out=out[:, ndt:], **common, **_norm_args(o_norm, ndt, n))
+
+
+def mamba2_conv_ssm_forward(layer, projected_states: torch.Tensor, output: torch.Tensor,
+                            attn_metadata, conv_state: torch.Tensor,
+                            ssm_state: torch.Tensor) -> None:
+    """primed_mamba2_layer.py:615-1021 over hmx ops (see the module docstring).
+
+    ``layer`` carries the reference's attributes (tped_intermediate_size,
+    tped_conv_size, dt_pad, num_heads, tp_size, xb_size, ssm_state_size, head_dim,
+    n_groups, conv_weights [conv_dim, W], conv1d.bias, activation, A, D, dt_bias,
+    B_norm / C_norm (or None), use_pos_embed, cache_config); ``attn_metadata`` is
+    the layer's Mamba2AttentionMetadata (num_prefills, num_decode_tokens,
+    num_prefill_tokens, state_indices_tensor, has_initial_states_p,
+    prep_initial_states, query_start_loc_p); ``conv_state`` is
+    ``kv_cache[0].transpose(-1, -2)`` and ``ssm_state`` ``kv_cache[1]``
+    (:650-653).  Writes ``output[:num_actual_tokens]`` ([tokens, intermediate],
+    decodes first) and updates both pools in place."""
+    md = attn_metadata
+    if md is None:
+        raise NotImplementedError("the profile run (attn_metadata None) is not handled by the "
+                                  "hmx Mamba2 core")
+    cc = getattr(layer, "cache_config", None)
+    if cc is not None and getattr(cc, "mamba_cache_mode", None) == "all":
+        raise NotImplementedError("prefix caching (mamba_cache_mode 'all') is not supported by "
+                                  "the hmx Mamba2 core")
+    if getattr(layer, "use_pos_embed", False):
+        raise NotImplementedError("the rotary position embedding (use_pos_embed) is not "
+                                  "supported by the hmx Mamba2 core")
+    tp = layer.tp_size
+    I, CD = layer.tped_intermediate_size, layer.tped_conv_size
+    H = layer.num_heads // tp
+    P, N = layer.head_dim, layer.ssm_state_size
+    xb = layer.xb_size // tp
+    HX = xb // N                                         # x and B heads before repeat_kv
+    if HX * N != xb or P != N or H % HX != 0:
+        raise NotImplementedError(f"hmx Mamba2 core needs head_dim == d_state and xb_size a "
+                                  f"multiple of d_state dividing the heads (P={P}, N={N}, "
+                                  f"xb={xb}, H={H})")
+    hbc = projected_states[:, I:I + CD]                  # :622-631
+    dt = projected_states[:, I + CD:I + CD + H]          # dt_pad columns dropped (:633-634)
+    if layer.B_norm is not None:                         # :663-669
+        hs, B, C = torch.split(hbc, [xb, xb, CD - 2 * xb], dim=-1)
+        B = layer.B_norm(B.reshape(-1, layer.head_dim)).view(B.shape)
+        C = layer.C_norm(C.reshape(-1, layer.head_dim)).view(C.shape)
+        hbc = torch.cat([hs, B, C], dim=-1)
+    nd, npf = md.num_decode_tokens, md.num_prefills
+    n = nd + md.num_prefill_tokens
+    idx = md.state_indices_tensor
+    w = layer.conv_weights
+    bias = getattr(layer.conv1d, "bias", None)
+    act = layer.activation
+    x = torch.empty(n, CD, dtype=hbc.dtype, device=hbc.device)
+    out = output[:n].view(n, H, P)
+    if npf > 0:
+        idx_p = idx[nd:nd + npf]
+        has = md.has_initial_states_p
+        if has is None or not md.prep_initial_states:    # :811-824: no initial states
+            has = torch.zeros(npf, dtype=torch.bool, device=hbc.device)
+        qsl = md.query_start_loc_p
+        ops.conv.conv_fwd_rows(hbc[nd:n].t(), w, bias, conv_state, qsl, idx_p, has, act,
+                               out=x[nd:])
+        xp = x[nd:]
+        ops.mamba_chunk_scan_combined_varlen(
+            xp[:, :xb].view(-1, HX, P), dt[nd:n], layer.A, xp[:, xb:2 * xb].view(-1, HX, N),
+            xp[:, 2 * xb:].view(-1, H, N), layer.chunk_size, cu_seqlens=qsl, out=out[nd:],
+            D=layer.D, dt_bias=layer.dt_bias, initial_states=ssm_state, dt_softplus=True,
+            dt_limit=(0.0, float("inf")), ssm_state_indices=idx_p, has_initial_state=has)
+    if nd > 0:
+        idx_d = idx[:nd]
+        ops.causal_conv1d_update(hbc[:nd], conv_state, w, bias, act, conv_state_indices=idx_d,
+                                 out=x[:nd])
+        xd = x[:nd]
+        ops.selective_state_update(
+            ssm_state, xd[:, :xb].view(nd, HX, P), dt[:nd, :, None].expand(nd, H, P),
+            layer.A[:, None, None].expand(H, P, N), xd[:, xb:2 * xb].view(nd, HX, N),
+            xd[:, 2 * xb:].view(nd, H, N), layer.D[:, None].expand(H, P), z=None,
+            dt_bias=layer.dt_bias[:, None].expand(H, P), dt_softplus=True,
+            state_batch_indices=idx_d, dst_state_batch_indices=idx_d, out=out[:nd])

@@ -26,10 +26,11 @@
 extern "C" {
 #endif
 
-#define HMX_ABI_VERSION 3  /* 2: optional hmx_gated_norm output epilogue in the GDN ops;
+#define HMX_ABI_VERSION 4  /* 2: optional hmx_gated_norm output epilogue in the GDN ops;
                               3: q/k/v token strides in the GDN and GKA ops; slot-indexed
                               state pools and has_initial_state in the GDN, GKA and SSD
-                              prefills */
+                              prefills;
+                              4: grouped x heads (HX) and C groups (GC) in the SSD ops */
 
 enum hmx_status {
   HMX_OK = 0,
@@ -256,8 +257,12 @@ size_t hmx_gka_chunk_workspace_bytes(int32_t nseg_total, int32_t N, int32_t H);
  * Mamba2 SSD chunk scan forward, bf16 x/B/C/z/y, fp32 states, varlen via a
  * segment table of rows (n, bos, eos, c_start, c_end, seg_idx, first_seg, nseg)
  * over 64-token chunks (bos/eos index the flattened token axis).
- *  x, z, y [tokens, H, P]: element strides x_ts/x_hs (token, head), last dim
- *  contiguous; B, C [tokens, G, N] with strides (token, group); dt [tokens, H]
+ *  z, y [tokens, H, P], x [tokens, HX, P]: element strides (token, head), last
+ *  dim contiguous; B [tokens, G, N], C [tokens, GC, N] with strides (token,
+ *  group); head h reads x head h/(H/HX), B group h/(H/G), C group h/(H/GC) (HX,
+ *  G, GC divide H; HX = GC = H with G = ngroups is the reference's layout, the
+ *  primed Mamba2 layer's repeat_kv'd x and B are HX = G = d_xb/headdim read in
+ *  place, primed_mamba2_layer.py:800-835); dt [tokens, H]
  *  (f32/bf16/f16) with strides; A [H] fp32 (= -exp(A_log)); D [H, P] fp32 or
  *  NULL; dt_bias [H] fp32 or NULL; z NULL for no gate.  dt' =
  *  clamp(softplus(dt + dt_bias) if dt_softplus else dt + dt_bias, dt_min, dt_max).
@@ -285,7 +290,7 @@ int hmx_ssd_chunk_fwd(const void* x, int64_t x_ts, int64_t x_hs,
                       int32_t state_dtype, const int32_t* state_indices,
                       const uint8_t* has_initial_state,
                       const int32_t* seg_table, int32_t nseg_total, int32_t nseq,
-                      int32_t H, int32_t G, int32_t P, int32_t N,
+                      int32_t H, int32_t HX, int32_t G, int32_t GC, int32_t P, int32_t N,
                       int32_t dt_softplus, float dt_min, float dt_max,
                       void* workspace, size_t workspace_bytes, void* stream);
 
@@ -298,9 +303,11 @@ size_t hmx_ssd_chunk_workspace_bytes(int32_t nseg_total, int32_t nseq, int32_t H
 /*
  * Mamba2 single-token state update, in place on a slot-indexed state pool.
  *  state [slots, H, P, N] (f32 or bf16; slot_stride in elements, the rest
- *  contiguous); x, dt, z, out [batch, H, P] with element strides (batch, head, p);
- *  A fp32 [H, P, N] with strides (a_ps == a_ns == 0: one value per head);
- *  B, C [batch, G, N] with strides (batch, group), N contiguous; D, dt_bias fp32
+ *  contiguous); dt, z, out [batch, H, P], x [batch, HX, P] with element strides
+ *  (batch, head, p); A fp32 [H, P, N] with strides (a_ps == a_ns == 0: one value
+ *  per head); B [batch, G, N], C [batch, GC, N] with strides (batch, group), N
+ *  contiguous; head h reads x head h/(H/HX), B group h/(H/G), C group h/(H/GC)
+ *  (HX, G, GC divide H; HX = GC = H is the reference's layout); D, dt_bias fp32
  *  [H, P] with strides, or NULL.  Source slot state_batch_indices[i] (or i),
  *  skipped when equal to pad_slot_id; written to dst_state_batch_indices[i] when
  *  given.  P, N in {64, 128}.
@@ -320,8 +327,8 @@ int hmx_ssd_state_update(void* state, int32_t state_dtype, int64_t slot_stride,
                          void* out, int32_t out_dtype, int64_t o_bs, int64_t o_hs, int64_t o_ps,
                          const int32_t* state_batch_indices,
                          const int32_t* dst_state_batch_indices, int32_t pad_slot_id,
-                         int32_t batch, int32_t H, int32_t G, int32_t P, int32_t N,
-                         int32_t dt_softplus, void* stream);
+                         int32_t batch, int32_t H, int32_t HX, int32_t G, int32_t GC,
+                         int32_t P, int32_t N, int32_t dt_softplus, void* stream);
 
 /*
  * Gated RMSNorm over rows of D elements (the GDN / GKA output norm):
