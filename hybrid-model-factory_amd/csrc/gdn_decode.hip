@@ -9,14 +9,16 @@
 // Layout & mapping.  One workgroup per (sequence, head, 128 state columns) with
 // up to 4 waves; wave w owns 32 state columns for all K rows, kept in registers for
 // the whole token loop.  Lane l owns 4 consecutive columns (c = l&7) of
-// R = K/8 consecutive rows (r = l>>3).  One load instruction of the wave
-// touches 8 rows x 128 contiguous bytes, so the four waves of a workgroup
-// stream the head's K*V*4-byte state as full 512-byte rows.  Column sums over
+// R = K/8 rows r, r+8, ..., r+8(R-1) (r = l>>3).  One load instruction of the
+// wave touches 8 consecutive rows x 128 contiguous bytes, so the four waves of a
+// workgroup stream the head's K*V*4-byte state in contiguous 8-row blocks.  Column sums over
 // k (S^T k, S^T q) are a per-lane partial over R rows plus a 3-step xor
 // butterfly over the row-group lane bits — no LDS, no barriers.
 //
 // Roofline: HBM-bound read-modify-write of the state, 2*K*V*sizeof(state)
 // bytes per (sequence, head) per call (q/k/v/o add 6*K*2 bytes).
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace hmx {
@@ -48,6 +50,17 @@ __device__ __forceinline__ float load_scalar(const void* p, int64_t i, int dtype
   return (float)static_cast<const f16*>(p)[i];
 }
 
+// Loads of g and beta: a fixed element type (one code path, so the state and
+// per-token loads of a thread are all in flight together) or DynG (the dtype
+// code decides at run time).
+struct DynG {};
+
+template <typename TG>
+__device__ __forceinline__ float load_gate(const void* p, int64_t i, int dtype) {
+  if constexpr (std::is_same_v<TG, DynG>) return load_scalar(p, i, dtype);
+  else return (float)static_cast<const TG*>(p)[i];
+}
+
 // Sum a value over the 8 row-group lanes (lane bits 3..5) of a wave.
 __device__ __forceinline__ float rowgroup_sum(float x) {
   x += shfl_xor(x, 8);
@@ -59,7 +72,7 @@ __device__ __forceinline__ float rowgroup_sum(float x) {
 // NORM: each output row (one workgroup holds all V <= 128 columns) passes through
 // the gated RMSNorm of hmx_rms_norm_gated (norm before gate) on its way out, from
 // o as rounded to q's dtype; the sum of squares crosses the waves through LDS.
-template <int K, typename TQ, typename TS, bool NORM>
+template <int K, typename TQ, typename TS, bool NORM, typename TG>
 __global__ __launch_bounds__(256) void gdn_recurrent_kernel(RecurrentParams p) {
   constexpr int R = K / 8;  // rows per lane
   const int lane = threadIdx.x & 63;
@@ -110,9 +123,9 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(RecurrentParams p) {
   float S[R][4];
   if (read_row >= 0) {
     const TS* src = static_cast<const TS*>(p.h0) + read_row * p.h0_rs + (int64_t)h * K * V +
-                    (int64_t)(r * R) * V + col;
+                    (int64_t)r * V + col;
 #pragma unroll
-    for (int i = 0; i < R; ++i) load_vec<4>(src + (int64_t)i * V, S[i]);
+    for (int i = 0; i < R; ++i) load_vec<4>(src + (int64_t)(8 * i) * V, S[i]);
   } else {
 #pragma unroll
     for (int i = 0; i < R; ++i) S[i][0] = S[i][1] = S[i][2] = S[i][3] = 0.f;
@@ -121,16 +134,23 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(RecurrentParams p) {
   for (int64_t t = 0; t < T; ++t) {
     const int64_t tok = bos + t;
     float kr[R], qr[R], vv[4], bb[4];
-    load_vec<R>(static_cast<const TQ*>(p.k) + tok * p.k_ts + (int64_t)hk * K + r * R, kr);
-    load_vec<R>(static_cast<const TQ*>(p.q) + tok * p.q_ts + (int64_t)h * K + r * R, qr);
+    {
+      const TQ* kp = static_cast<const TQ*>(p.k) + tok * p.k_ts + (int64_t)hk * K + r;
+      const TQ* qp = static_cast<const TQ*>(p.q) + tok * p.q_ts + (int64_t)h * K + r;
+#pragma unroll
+      for (int i = 0; i < R; ++i) {
+        kr[i] = to_f32(kp[8 * i]);
+        qr[i] = to_f32(qp[8 * i]);
+      }
+    }
     load_vec<4>(static_cast<const TQ*>(p.v) + tok * p.v_ts + (int64_t)hk * V + col, vv);
-    const float gt = load_scalar(p.g, tok * p.H + h, p.g_dt);
+    const float gt = load_gate<TG>(p.g, tok * p.H + h, p.g_dt);
     if (p.beta_headwise) {
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        bb[j] = load_scalar(p.beta, (tok * p.H + h) * V + col + j, p.beta_dt);
+        bb[j] = load_gate<TG>(p.beta, (tok * p.H + h) * V + col + j, p.beta_dt);
     } else {
-      const float bs = load_scalar(p.beta, tok * p.H + h, p.beta_dt);
+      const float bs = load_gate<TG>(p.beta, tok * p.H + h, p.beta_dt);
       bb[0] = bb[1] = bb[2] = bb[3] = bs;
     }
 
@@ -149,7 +169,7 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(RecurrentParams p) {
 #pragma unroll
     for (int i = 0; i < R; ++i) qr[i] *= qs;
 
-    const float eg = expf(gt);
+    const float eg = fast_exp(gt);
     float kv[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < R; ++i) {
@@ -199,9 +219,17 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(RecurrentParams p) {
   }
 
   TS* dst = static_cast<TS*>(p.ht) + write_row * p.ht_rs + (int64_t)h * K * V +
-            (int64_t)(r * R) * V + col;
+            (int64_t)r * V + col;
 #pragma unroll
-  for (int i = 0; i < R; ++i) store_vec_nt<4>(dst + (int64_t)i * V, S[i]);
+  for (int i = 0; i < R; ++i) store_vec_nt<4>(dst + (int64_t)(8 * i) * V, S[i]);
+}
+
+template <int K, typename TQ, typename TS, typename TG>
+static void launch_g(const RecurrentParams& p, const dim3& grid, const dim3& block, hipStream_t s) {
+  if (p.onw)
+    hipLaunchKernelGGL((gdn_recurrent_kernel<K, TQ, TS, true, TG>), grid, block, 0, s, p);
+  else
+    hipLaunchKernelGGL((gdn_recurrent_kernel<K, TQ, TS, false, TG>), grid, block, 0, s, p);
 }
 
 template <int K, typename TQ, typename TS>
@@ -210,10 +238,13 @@ static void launch(const RecurrentParams& p, int64_t N, hipStream_t s) {
   const int waves = p.V / 32;
   const dim3 grid((unsigned)(N * p.H), (unsigned)((waves + 3) / 4)),
       block(64 * (waves < 4 ? waves : 4));
-  if (p.onw)
-    hipLaunchKernelGGL((gdn_recurrent_kernel<K, TQ, TS, true>), grid, block, 0, s, p);
+  // typed g/beta paths for bf16 q/k/v with g and beta both fp32 or both bf16
+  if (std::is_same_v<TQ, bf16> && p.g_dt == p.beta_dt && p.g_dt == HMX_F32)
+    launch_g<K, TQ, TS, float>(p, grid, block, s);
+  else if (std::is_same_v<TQ, bf16> && p.g_dt == p.beta_dt && p.g_dt == HMX_BF16)
+    launch_g<K, TQ, TS, bf16>(p, grid, block, s);
   else
-    hipLaunchKernelGGL((gdn_recurrent_kernel<K, TQ, TS, false>), grid, block, 0, s, p);
+    launch_g<K, TQ, TS, DynG>(p, grid, block, s);
 }
 
 template <int K, typename TQ>
