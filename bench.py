@@ -257,6 +257,42 @@ def bench_decode(dev, steps_total=512, warmup=8):
     return dict(ms=ms, steps_per_s=1e3 / ms, tokens_per_s=N * 1e3 / ms, bytes=by, GBps=gbs)
 
 
+def bench_gka_decode(dev, num_iter=8, steps_total=128, warmup=4):
+    """K7: gka_chebyshev_gla_decode over 256 sequences x 1 token, H = 32, d = 128, in
+    place on fp32 h_kk / h_kv pools (randperm slots), the C2 batch shape."""
+    import torch
+    import torch.nn.functional as F
+    import hmx
+    from hmx import workloads as wl
+    N, H, D = 256, 32, 128
+    g = torch.Generator(device=dev).manual_seed(wl.SEED_BASE + 6)
+    q = torch.randn(steps_total, 1, N, H, D, generator=g, device=dev).bfloat16()
+    k = torch.randn(steps_total, 1, N, H, D, generator=g, device=dev).bfloat16()
+    v = torch.randn(steps_total, 1, N, H, D, generator=g, device=dev).bfloat16()
+    alpha = torch.sigmoid(torch.randn(steps_total, 1, N, H, generator=g, device=dev))
+    gk = F.logsigmoid(torch.randn(steps_total, 1, N, H, generator=g, device=dev))
+    beta = torch.sigmoid(torch.randn(steps_total, 1, N, H, generator=g, device=dev))
+    x = torch.randn(N, H, D, 16, generator=g, device=dev) * 0.05
+    hkk = x @ x.transpose(-1, -2)
+    hkv = torch.randn(N, H, D, D, generator=g, device=dev) * 0.02
+    idx = torch.randperm(N, generator=g, device=dev).to(torch.int32)
+    cu = torch.arange(N + 1, dtype=torch.int32, device=dev)
+    out = torch.empty(1, N, H, D, dtype=torch.bfloat16, device=dev)
+    it = {"s": 0}
+
+    def step():
+        s = it["s"] % steps_total
+        it["s"] += 1
+        gs = gk[s]                                   # the op requires g is gk
+        hmx.gka_chebyshev_gla_decode(q[s], k[s], v[s], alpha[s], gs, gs, beta[s],
+                                     D ** -0.5, num_iter=num_iter, h_kk=hkk, h_kv=hkv,
+                                     cu_seqlens=cu, ssm_state_indices=idx, out=out)
+
+    ms = _timed(step, steps_total, warmup)
+    by = wl.gka_decode_bytes(N, H, H, D)
+    return dict(ms=ms, steps_per_s=1e3 / ms, bytes=by, GBps=by / (ms * 1e-3) / 1e9)
+
+
 def bench_gka(dev, steps, warmup, num_iter):
     """C3: gka_chebyshev_gla_prefill at the C1 shape, ridge 0.01, zero initial states."""
     import hmx
@@ -450,6 +486,7 @@ def main():
         out["core"] = bench_core(dev, max(2, a.steps // 2), a.warmup)
     if a.only in (None, "decode"):
         out["decode"] = bench_decode(dev)
+        out["gka_decode"] = bench_gka_decode(dev)
     if a.only in (None, "ssd"):
         out["ssd"] = bench_ssd(dev, a.steps, a.warmup)
         out["ssd_primed"] = bench_ssd(dev, max(2, a.steps // 2), a.warmup, P=128, N=128, G=64)
@@ -605,6 +642,16 @@ def main():
                          "unit": "GB/s", "frac": round(r["GBps"] / HBM_PEAK_GBS, 4),
                          "traffic": measured_traffic("ssd_decode"),
                          "algorithmic_bytes": r["bytes"]},
+        }
+    if "gka_decode" in out:
+        r = out["gka_decode"]
+        line["gka_decode"] = {
+            "value": round(r["steps_per_s"], 1), "unit": "steps/s", "ms_per_step": round(r["ms"], 4),
+            "config": {"workload": "GKA decode (gka_chebyshev_gla_decode), 256 seqs x 1 token",
+                       "H": 32, "d": 128, "num_iter": 8, "pools": "fp32 h_kk, h_kv [256,32,128,128]"},
+            "roofline": {"bound": "hbm", "achieved": round(r["GBps"], 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(r["GBps"] / HBM_PEAK_GBS, 4),
+                         "traffic": None, "algorithmic_bytes": r["bytes"]},
         }
     if not a.no_cpu:
         line["cpu_baseline"] = cpu_baseline()

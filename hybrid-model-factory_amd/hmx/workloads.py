@@ -169,6 +169,13 @@ def gdn_decode_bytes(n_seqs: int, H: int, HKV: int, K: int = 128, V: int = 128,
             + n_seqs * HKV * (K + V) * in_bytes + 2 * n_seqs * H * 4)
 
 
+def gka_decode_bytes(n_seqs: int, H: int, HKV: int, D: int = 128, in_bytes: int = 2) -> float:
+    """h_kk and h_kv (fp32) read + write per (seq, head) plus q,o [n,H,D], k,v
+    [n,HKV,D] and alpha, g, beta fp32."""
+    return (4 * n_seqs * H * D * D * 4 + 2 * n_seqs * H * D * in_bytes
+            + 2 * n_seqs * HKV * D * in_bytes + 3 * n_seqs * H * 4)
+
+
 def ceil_div(a: int, b: int) -> int:
     return -(-a // b)
 
