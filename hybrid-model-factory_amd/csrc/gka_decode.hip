@@ -84,17 +84,14 @@ __global__ __launch_bounds__(256) void gka_decode_kernel(Params p) {
   const int64_t slot = p.idx ? (int64_t)p.idx[(int64_t)n * p.idx_stride] : n;
   if (slot < 0) return;
 
-  // ---- state loads (issued first: they dominate the traffic)
-  float Hs[16][4], Ss[16][4];
+  // ---- h_kk loads (issued first).  h_kv is loaded after the iteration, once
+  // h_kk's registers are free: the iteration phase then holds one state, which
+  // doubles the workgroups a CU keeps in flight.
+  float Hs[16][4];
   {
     const float* hsrc = p.hkk_in + slot * p.hkk_in_rs + (int64_t)h * D * D + row0 * D + col;
-    const TKV* ssrc = static_cast<const TKV*>(p.hkv_in) + slot * p.hkv_in_rs +
-                      (int64_t)h * D * D + row0 * D + col;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      load_vec<4>(hsrc + i * D, Hs[i]);
-      load_vec<4>(ssrc + i * D, Ss[i]);
-    }
+    for (int i = 0; i < 16; ++i) load_vec<4>(hsrc + i * D, Hs[i]);
   }
   // ---- token inputs
   const TQ* qp = static_cast<const TQ*>(p.q) + bos * p.q_ts + (int64_t)h * D;
@@ -179,6 +176,18 @@ __global__ __launch_bounds__(256) void gka_decode_kernel(Params p) {
       xr[i] = t.x; xr[i + 1] = t.y; xr[i + 2] = t.z; xr[i + 3] = t.w;
     }
   }
+  // ---- h_kv loads; k and q rows again (L2 hits) instead of keeping them live
+  float Ss[16][4];
+  {
+    const TKV* ssrc = static_cast<const TKV*>(p.hkv_in) + slot * p.hkv_in_rs +
+                      (int64_t)h * D * D + row0 * D + col;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) load_vec<4>(ssrc + i * D, Ss[i]);
+  }
+  load_vec<16>(kp + row0, kr);
+  load_vec<16>(qp + row0, qr);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) { kr[i] *= ik; qr[i] *= iq; }
   // ---- alpha blend (rows), S update, readout o = scale S^T x
 #pragma unroll
   for (int i = 0; i < 16; ++i) xr[i] = (qr[i] + alpha * (xr[i] - qr[i])) * p.scale;
