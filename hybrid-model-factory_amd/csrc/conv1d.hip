@@ -62,6 +62,7 @@ struct Params {
   const int32_t* idx;                 // slot per sequence, or null (slot = sequence)
   const uint8_t* has_init;            // per sequence, or null (all true)
   int dim, pad;
+  int64_t tile0;                      // prefill: first token tile of this launch
 };
 
 // Taps of 8 channels; the window holds the W-1 inputs before the current one
@@ -175,9 +176,9 @@ __device__ __forceinline__ void load_window(const Params& p, int64_t t, int64_t 
 // branch is scalar.
 template <typename T, int W, bool ACT>
 __global__ __launch_bounds__(NT) void conv_fwd_kernel(Params p) {
-  const int c0 = (blockIdx.y * NT + threadIdx.x) * 8;
+  const int c0 = (blockIdx.x * NT + threadIdx.x) * 8;
   if (c0 >= p.dim) return;
-  const int64_t t0 = (int64_t)blockIdx.x * TT;
+  const int64_t t0 = (p.tile0 + blockIdx.y) * TT;
   const int64_t t1 = min(t0 + TT, p.total);
   Taps<W, ACT> tp;
   tp.load(p, c0);
@@ -316,9 +317,15 @@ __global__ __launch_bounds__(NT) void conv_update_kernel(Params p) {
 template <typename T, int W, bool ACT>
 void launch_fwd_w(const Params& p, hipStream_t s) {
   const unsigned cg = (unsigned)((p.dim / 8 + NT - 1) / NT);
-  if (p.total > 0)
-    hipLaunchKernelGGL((conv_fwd_kernel<T, W, ACT>), dim3((unsigned)((p.total + TT - 1) / TT), cg),
-                       dim3(NT), 0, s, p);
+  // channel groups on x, so the groups of one token tile run together and read
+  // whole rows; token tiles on y, in launches of at most 65535 (grid y's limit)
+  const int64_t tiles = (p.total + TT - 1) / TT;
+  for (int64_t t = 0; t < tiles; t += 65535) {
+    Params q = p;
+    q.tile0 = t;
+    hipLaunchKernelGGL((conv_fwd_kernel<T, W, ACT>), dim3(cg, (unsigned)min(tiles - t, (int64_t)65535)),
+                       dim3(NT), 0, s, q);
+  }
   if (p.st && p.batch > 0)
     hipLaunchKernelGGL(conv_state_kernel<T>, dim3((unsigned)p.batch, cg), dim3(NT), 0, s, p);
 }

@@ -169,3 +169,23 @@ def test_errors(dev):
         hmx.causal_conv1d_update(x, pool.transpose(1, 2).contiguous(), w)
     with pytest.raises(NotImplementedError):
         hmx.causal_conv1d_update(x, pool, w, initial_state_idx=torch.zeros(8, device=dev))
+
+
+def test_prefill_more_tiles_than_one_launch(dev):
+    """65535 * 64 + 200 tokens: the token tiles exceed one launch's grid (65535 in
+    y), so the prefill runs as two launches; a sequence boundary falls inside the
+    second.  8 channels keep it at 67 MB."""
+    T = 65535 * 64 + 200
+    lens = [T - 150, 150]
+    qs, x, w, b, pool, g = _setup(lens, 8, 4, 3, 3, 11)
+    idx = torch.tensor([2, 0], dtype=torch.int32)
+    init = torch.tensor([True, False])
+    out_r, pool_r = ref.causal_conv1d_varlen(x, w, b, pool, qs, idx, init, "silu")
+    pool_d = pool.to(dev)
+    d = lambda t: t.to(dev)
+    out = hmx.causal_conv1d_fn(x.to(dev).t(), d(w), d(b), conv_states=pool_d.transpose(1, 2),
+                               query_start_loc=d(qs), cache_indices=d(idx),
+                               has_initial_state=d(init), activation="silu")
+    torch.cuda.synchronize()
+    _close(out.t(), out_r)
+    assert torch.equal(pool_d.cpu(), pool_r.to(pool.dtype))
