@@ -35,8 +35,13 @@ BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 
 def _device_warmup(dev, seconds=0.5):
     """Untimed: keep the GPU busy (matrix products and a 512 MiB copy) for about
-    ``seconds`` so its clocks have ramped up before the first timed leg; without it
-    the first leg measured ~15% slow against the same leg later in the run."""
+    ``seconds``, so it is in its loaded power state when a leg's warm-up steps
+    start.  The chip leaves that state within about a second of light load (input
+    generation is enough): a kernel trace of 20-call blocks of the C1 prefill
+    after input generation shows its main kernel at 474 us in the first block,
+    415 us in the second and 381-388 us from the fourth on, and the same again
+    after 2 s idle; with this warm-up right before the leg, the first block is
+    already within 3% of the later ones."""
     import torch
     a = torch.randn(4096, 4096, device=dev, dtype=torch.bfloat16)
     src = torch.empty(256 << 20, device=dev, dtype=torch.bfloat16)
@@ -52,6 +57,7 @@ def _device_warmup(dev, seconds=0.5):
 
 def _timed(fn, steps, warmup, stream=None):
     import torch
+    _device_warmup(torch.device("cuda", torch.cuda.current_device()))
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -471,7 +477,6 @@ def main():
     if a.copy_calibration:
         print(json.dumps({"copy_calibration": copy_calibration(dev)}), flush=True)
         return
-    _device_warmup(dev)
     out = {}
     if a.only in (None, "prefill"):
         pf = bench_prefill(dev, a.steps, a.warmup)
@@ -491,8 +496,7 @@ def main():
         out["ssd"] = bench_ssd(dev, a.steps, a.warmup)
         out["ssd_primed"] = bench_ssd(dev, max(2, a.steps // 2), a.warmup, P=128, N=128, G=64)
         out["ssd_decode"] = bench_ssd_decode(dev)
-    # last: the GKA legs are long and compute-bound, and the legs after them measured
-    # ~10% slower (the chip's power state), so nothing follows them
+    # last: the GKA legs are long and compute-bound
     if a.only in (None, "gka"):
         out["gka"] = {n: bench_gka(dev, max(2, a.steps // 4), 1, n) for n in (8, 32)}
     line = {

@@ -20,6 +20,7 @@ from __future__ import annotations
 import torch
 
 from .. import _lib
+from .gdn import _device_table
 
 PAD_SLOT_ID = -1
 
@@ -109,7 +110,7 @@ def conv_fwd_rows(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | No
         raise ValueError(f"weight must be [{dim}, width], got {tuple(weight.shape)}")
     xr = _rows(x.t())
     if query_start_loc is None:
-        query_start_loc = torch.tensor([0, total], dtype=torch.int32, device=x.device)
+        query_start_loc = _device_table([[0, total]], x.device)[0]
     qs = _i32(query_start_loc)
     batch = qs.shape[0] - 1
     if validate_data:

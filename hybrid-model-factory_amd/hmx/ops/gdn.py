@@ -15,6 +15,7 @@ stream.  There is no CPU fallback.
 """
 from __future__ import annotations
 
+import collections
 import heapq
 
 import torch
@@ -230,6 +231,31 @@ def _cu_count(device: torch.device) -> int:
     return _CU_COUNT[idx]
 
 
+_SEG_CACHE: "collections.OrderedDict[tuple, torch.Tensor]" = collections.OrderedDict()
+_SEG_CACHE_SIZE = 64
+
+
+def _device_table(rows: list[list[int]], device) -> torch.Tensor:
+    """The segment table as an int32 device tensor, without blocking the host.
+
+    A copy from pageable memory waits for the stream to drain, which leaves the
+    GPU idle for the host's per-call work; the table is therefore staged in
+    pinned memory (the copy is then asynchronous), and the device copies of the
+    last few distinct tables are kept, so a repeated batch shape uploads nothing.
+    Kernels only read the table."""
+    key = (str(device), tuple(map(tuple, rows)))
+    t = _SEG_CACHE.get(key)
+    if t is not None:
+        _SEG_CACHE.move_to_end(key)
+        return t
+    host = torch.tensor(rows, dtype=torch.int32).pin_memory()
+    t = host.to(device, non_blocking=True)
+    _SEG_CACHE[key] = t
+    if len(_SEG_CACHE) > _SEG_CACHE_SIZE:
+        _SEG_CACHE.popitem(last=False)
+    return t
+
+
 def _balanced_counts(chunks: list[int], budget: int, min_seg: int) -> list[int]:
     """Segments per sequence, at most ``budget`` in all, given one at a time to the
     sequence whose segments are currently the longest (the longest segment bounds
@@ -398,7 +424,7 @@ def chunk_gated_delta_rule_gqa(
     if cu_seqlens is not None and bounds and bounds[-1][1] < T:
         o[:, bounds[-1][1]:].zero_()  # tokens past the last sequence are not computed
     rows = _segment_table(bounds, H, WORKGROUPS_PER_CU * _cu_count(q.device), _segment_chunks)
-    seg = torch.tensor(rows, dtype=torch.int32).to(q.device, non_blocking=True)
+    seg = _device_table(rows, q.device)
     lib = _lib.load()
     ws_bytes = int(lib.hmx_gdn_chunk_workspace_bytes(len(rows), N, H, int(idx is not None)))
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)

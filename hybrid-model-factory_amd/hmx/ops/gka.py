@@ -18,7 +18,7 @@ import logging
 import torch
 
 from .. import _lib
-from .gdn import _cu_count, _gate_rows, _i32, _segment_table, _token_rows
+from .gdn import _cu_count, _device_table, _gate_rows, _i32, _segment_table, _token_rows
 
 GKA_WORKGROUPS_PER_CU = 1
 _warned_num_iter_zero = False
@@ -275,7 +275,7 @@ def _gka_prefill(q, k, v, alpha, g, gk, beta, gla_scale, ridge_ratio, num_iter, 
     if cu_seqlens is not None and bounds and bounds[-1][1] < T:
         o[:, bounds[-1][1]:].zero_()
     rows = _segment_table(bounds, H, GKA_WORKGROUPS_PER_CU * _cu_count(q.device), segment_chunks)
-    seg = torch.tensor(rows, dtype=torch.int32).to(q.device, non_blocking=True)
+    seg = _device_table(rows, q.device)
     lib = _lib.load()
     ws_bytes = int(lib.hmx_gka_chunk_workspace_bytes(len(rows), N, H))
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=q.device)

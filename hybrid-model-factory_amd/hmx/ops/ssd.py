@@ -13,7 +13,7 @@ from __future__ import annotations
 import torch
 
 from .. import _lib
-from .gdn import _cu_count, _segment_table
+from .gdn import _cu_count, _device_table, _segment_table
 
 SSD_CHUNK = 64                 # the kernel's internal chunk length (tokens)
 SSD_WORKGROUPS_PER_CU = 2
@@ -84,7 +84,7 @@ def _ssd_scan(x, dt, A, B, C, D, z, dt_bias, dt_softplus, dt_limit, bounds, h0, 
         st_ss, st_dt = H * P * N, _lib.HMX_F32
     rows = _segment_table(bounds, H, SSD_WORKGROUPS_PER_CU * _cu_count(x.device), segment_chunks,
                           chunk=SSD_CHUNK)
-    seg = torch.tensor(rows, dtype=torch.int32).to(x.device, non_blocking=True)
+    seg = _device_table(rows, x.device)
     lib = _lib.load()
     ws_bytes = int(lib.hmx_ssd_chunk_workspace_bytes(len(rows), nseq, H, P, N))
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=x.device)
