@@ -55,9 +55,9 @@ def test_scan_batch_initial_and_final_states(dev, P, N):
     assert_state_close(f, f_r, what="final_states")
 
 
-@pytest.mark.parametrize("seg", [None, 2])
-def test_scan_seq_idx_z_dhdim_varlen_states(dev, seg):
-    l, H, G, P, N = 1000, 4, 1, 64, 128
+@pytest.mark.parametrize("seg,P", [(None, 64), (2, 64), (2, 128)])
+def test_scan_seq_idx_z_dhdim_varlen_states(dev, seg, P):
+    l, H, G, N = 1000, 4, 1, 128
     x, dt, A, B, C, D, bias, z, g0 = _inputs(1, l, H, G, P, N, 7, z=True)
     Dh = torch.randn(H, P, generator=g0) * 0.1 + 1.0
     h0 = torch.randn(1, H, P, N, generator=g0) * 0.1
