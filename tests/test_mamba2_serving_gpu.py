@@ -105,7 +105,7 @@ class _RMSNorm:
     def __call__(self, x):
         xf = x.float()
         y = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)).to(x.dtype)
-        return y * self.weight.to(y.device)
+        return y * self.weight
 
 
 def _layer(seed, dev):
@@ -118,8 +118,8 @@ def _layer(seed, dev):
         conv1d=SimpleNamespace(bias=(torch.randn(CD, generator=g0) * 0.1).bfloat16().to(dev)),
         activation="silu", A=(-torch.exp(torch.rand(H, generator=g0) * 2)).to(dev),
         D=torch.randn(H, generator=g0).to(dev), dt_bias=(torch.randn(H, generator=g0) * 0.5).to(dev),
-        B_norm=_RMSNorm((torch.rand(P, generator=g0) + 0.5).bfloat16()),
-        C_norm=_RMSNorm((torch.rand(P, generator=g0) + 0.5).bfloat16()),
+        B_norm=_RMSNorm((torch.rand(P, generator=g0) + 0.5).bfloat16().to(dev)),
+        C_norm=_RMSNorm((torch.rand(P, generator=g0) + 0.5).bfloat16().to(dev)),
         use_pos_embed=False, cache_config=SimpleNamespace(mamba_cache_mode="none"))
     return lay, 2 * I + 2 * XB + H + pad
 
@@ -215,3 +215,38 @@ def test_conv_ssm_forward_rejects_prefix_caching(dev):
     md, *_ = _meta("decode", dev)
     with pytest.raises(NotImplementedError):
         srv.mamba2_conv_ssm_forward(lay, None, None, md, None, None)
+
+
+def test_conv_ssm_forward_decode_graph_replays_match_eager(dev):
+    """The decode-only core captured in a HIP graph (vLLM captures decode batches)
+    and replayed with eager work between replays: every replay equals an eager run
+    of the same step from the same pools, bit for bit."""
+    lay, dproj = _layer(3, dev)
+    md, nd, _, idx, _ = _meta("decode", dev)
+    g0 = torch.Generator().manual_seed(30)
+    conv = torch.randn(SLOTS, W - 1, CD, generator=g0).bfloat16().to(dev)
+    pool = (torch.randn(SLOTS, H, P, N, generator=g0) * 0.1).to(dev)
+    proj = torch.randn(nd, dproj, generator=g0).bfloat16().to(dev)
+    output = torch.zeros(nd, I, dtype=torch.bfloat16, device=dev)
+    step = lambda pr, o, c, s: srv.mamba2_conv_ssm_forward(lay, pr, o, md, c.transpose(1, 2), s)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step(proj.clone(), output.clone(), conv.clone(), pool.clone())
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    snap = (conv.clone(), pool.clone())
+    with torch.cuda.graph(graph):
+        step(proj, output, conv, pool)
+    conv.copy_(snap[0])
+    pool.copy_(snap[1])
+    for r in range(4):
+        proj.copy_(torch.randn(nd, dproj, generator=g0).bfloat16().to(dev))
+        ref_c, ref_s, ref_o = conv.clone(), pool.clone(), torch.zeros_like(output)
+        step(proj.clone(), ref_o, ref_c, ref_s)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(output, ref_o), f"replay {r}: output"
+        assert torch.equal(conv, ref_c) and torch.equal(pool, ref_s), f"replay {r}: pools"
+        _ = torch.randn(1000, device=dev).sum().item()
