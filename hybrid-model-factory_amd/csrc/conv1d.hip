@@ -60,7 +60,7 @@ struct Params {
   void* st; int64_t st_slot, st_row; int st_len;   // [slots, st_len, dim] or null
   const int32_t* qs; int batch; int64_t total;
   const int32_t* idx;                 // slot per sequence, or null (slot = sequence)
-  const uint8_t* has_init;            // per sequence, or null (all true)
+  const uint8_t* has_init;            // per sequence, or null (none: every sequence starts from zeros)
   int dim, pad;
   int64_t tile0;                      // prefill: first token tile of this launch
 };
@@ -147,7 +147,7 @@ __device__ __forceinline__ int seq_of(const int32_t* qs, int batch, int64_t t) {
 __device__ __forceinline__ bool seq_slot(const Params& p, int b, int64_t& slot, bool& init) {
   slot = p.idx ? p.idx[b] : b;
   const bool ok = slot != p.pad;
-  init = ok && p.st && (p.has_init ? p.has_init[b] != 0 : true);   // never read a pad slot
+  init = ok && p.st && p.has_init && p.has_init[b] != 0;   // never read a pad slot
   return ok;
 }
 

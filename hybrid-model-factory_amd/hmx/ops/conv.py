@@ -83,7 +83,9 @@ def causal_conv1d_fn(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor |
     """Prefill conv over concatenated sequences.  x [dim, total] (the transposed
     view of [total, dim]); returns the same layout.  ``conv_states`` [slots, dim,
     state_len] (channels contiguous) is updated in place at ``cache_indices``
-    (default: sequence b uses slot b)."""
+    (default: sequence b uses slot b).  A sequence starts from its slot's state
+    where ``has_initial_state`` [batch] is True, and from zeros elsewhere and when
+    it is None (as vLLM's kernel loads initial states only given the flags)."""
     if any(v is not None for v in block_args.values()):
         raise NotImplementedError("prefix-cache block arguments of causal_conv1d_fn: "
                                   f"{sorted(k for k, v in block_args.items() if v is not None)}")

@@ -260,11 +260,12 @@ def mamba2_conv_ssm_forward(layer, projected_states: torch.Tensor, output: torch
     out = output[:n].view(n, H, P)
     if npf > 0:
         idx_p = idx[nd:nd + npf]
-        has = md.has_initial_states_p
-        if has is None or not md.prep_initial_states:    # :811-824: no initial states
+        has_c = md.has_initial_states_p                  # the conv takes the flags as given (:782)
+        has = has_c
+        if has is None or not md.prep_initial_states:    # the scan starts from zeros (:811-824)
             has = torch.zeros(npf, dtype=torch.bool, device=hbc.device)
         qsl = md.query_start_loc_p
-        ops.conv.conv_fwd_rows(hbc[nd:n].t(), w, bias, conv_state, qsl, idx_p, has, act,
+        ops.conv.conv_fwd_rows(hbc[nd:n].t(), w, bias, conv_state, qsl, idx_p, has_c, act,
                                out=x[nd:])
         xp = x[nd:]
         ops.mamba_chunk_scan_combined_varlen(

@@ -59,7 +59,9 @@ def causal_conv1d_varlen(x, weight, bias, conv_states, query_start_loc, cache_in
         slot = int(cache_indices[b]) if cache_indices is not None else b
         if slot == pad_slot_id:
             continue
-        init = bool(has_initial_state[b]) if has_initial_state is not None else True
+        # no flags: no initial states (vLLM's causal_conv1d_fn loads the cached state
+        # only where a has_initial_state tensor says so)
+        init = bool(has_initial_state[b]) if has_initial_state is not None else False
         st = states[slot] if init else torch.zeros_like(states[slot])
         o, ns = conv_sequence(x[qs[b]:qs[b + 1]], st, weight, bias, activation, dtype)
         out[qs[b]:qs[b + 1]] = o

@@ -61,11 +61,12 @@ def test_several_channel_groups(dev):
     dim = 4608
     qs, x, w, b, pool, g = _setup([300, 45], dim, 4, 3, 3, 41)
     idx = torch.tensor([2, 0], dtype=torch.int32)
-    out_r, pool_r = ref.causal_conv1d_varlen(x, w, b, pool, qs, idx, None, "silu")
+    init = torch.tensor([True, True])
+    out_r, pool_r = ref.causal_conv1d_varlen(x, w, b, pool, qs, idx, init, "silu")
     pool_d = pool.to(dev)
     out = hmx.causal_conv1d_fn(x.to(dev).t(), w.to(dev), b.to(dev),
                                conv_states=pool_d.transpose(1, 2), query_start_loc=qs.to(dev),
-                               cache_indices=idx.to(dev))
+                               cache_indices=idx.to(dev), has_initial_state=init.to(dev))
     torch.cuda.synchronize()
     _close(out.t(), out_r)
     assert torch.equal(pool_d.cpu(), pool_r.to(pool.dtype))

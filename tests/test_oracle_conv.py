@@ -85,6 +85,12 @@ def test_varlen_pad_and_initial_flags():
     assert torch.equal(out[8:15], o3) and torch.equal(new[0], s3)
     assert torch.equal(out[5:8], torch.zeros(3, 8, dtype=D64))   # pad slot: untouched
     assert torch.equal(new[1], pool[1])                           # empty sequence: state kept
+    # no flags: no initial states (vLLM's causal_conv1d_fn reads the cache only where a
+    # has_initial_state tensor says so)
+    out_n, new_n = ref.causal_conv1d_varlen(x, w, None, pool, qs, idx, None, "silu")
+    out_f, new_f = ref.causal_conv1d_varlen(x, w, None, pool, qs, idx,
+                                            torch.zeros(4, dtype=torch.bool), "silu")
+    assert torch.equal(out_n, out_f) and torch.equal(new_n, new_f)
 
 
 def test_state_slack_rows():
