@@ -194,6 +194,8 @@ def gka_chebyshev_gla_prefill(q, k, v, alpha, g, gk, beta, gla_scale: float,
     _check_sketching_constraints(gka, num_sketches_per_head, "gka_chebyshev_gla_prefill")
     if cu_seqlens is not None and q.shape[0] != 1:
         raise ValueError(f"Batch size must be 1 when using cu_seqlens, got {q.shape[0]}")
+    if g is None:     # no GLA decay (the layer without a forgetting gate): e^0 = 1
+        g = torch.zeros(q.shape[:3], dtype=torch.float32, device=q.device)
     return _gka_prefill(q, k, v, alpha, g, gk, beta, gla_scale, ridge_ratio, num_iter,
                         h_kk_initial, h_kv_initial, output_final_state, cu_seqlens, True,
                         _segment_chunks, (o_norm_weight, o_norm_gate, o_norm_eps),

@@ -167,9 +167,6 @@ def gka_forward_core(layer, mixed_qkv: torch.Tensor, a: torch.Tensor, alpha_in: 
     if md is None:
         return
     _check(layer, md)
-    if not layer.use_forgetting_gate:
-        raise NotImplementedError("GKA without the forgetting gate (g = None) is not supported "
-                                  "by the hmx mixer core")
     n = md.num_actual_tokens
     mixed_qkv, a, alpha_in = mixed_qkv[:n], a[:n], alpha_in[:n]
     use_beta = layer.use_beta_gate
@@ -178,8 +175,13 @@ def gka_forward_core(layer, mixed_qkv: torch.Tensor, a: torch.Tensor, alpha_in: 
     x = _conv(layer, md, mixed_qkv, conv_state)
     q, k, v = _qkv(layer, x)
     # gating as primed_gka_layer.py:1138-1153
-    g, alpha, beta = ops.fused_gka_gating(layer.A, a, alpha_in, b if use_beta else None,
-                                          layer.dt_bias)
+    if layer.use_forgetting_gate:
+        g, alpha, beta = ops.fused_gka_gating(layer.A, a, alpha_in, b if use_beta else None,
+                                              layer.dt_bias)
+    else:                                  # no decay: g = None (:1144-1148)
+        g = None
+        alpha = alpha_in.sigmoid().unsqueeze(0)
+        beta = b.sigmoid().unsqueeze(0) if use_beta else None
     if layer.num_iter == 0:
         alpha = torch.zeros_like(alpha)
     elif layer._alpha_idx is None:
@@ -192,14 +194,14 @@ def gka_forward_core(layer, mixed_qkv: torch.Tensor, a: torch.Tensor, alpha_in: 
                   num_iter=layer.num_iter)
     if dec is not None:
         cu_d, idx_d = dec
-        g_d = g[:, :ndt]
+        g_d = sl(g, 0, ndt)
         ops.gka_chebyshev_gla_decode(
             q[:, :ndt], k[:, :ndt], v[:, :ndt], alpha[:, :ndt], g_d, g_d if kk_gate else None,
             sl(beta, 0, ndt), h_kk=h_kk_state, h_kv=h_kv_state, cu_seqlens=cu_d,
             ssm_state_indices=idx_d, out=out[:, :ndt], **common, **_norm_args(o_norm, 0, ndt))
     if pre is not None:
         cu_p, idx_p, has_p = pre
-        g_p = g[:, ndt:]
+        g_p = sl(g, ndt, n)
         ops.gka_chebyshev_gla_prefill(
             q[:, ndt:], k[:, ndt:], v[:, ndt:], alpha[:, ndt:], g_p, g_p if kk_gate else None,
             sl(beta, ndt, n), h_kk_initial=h_kk_state, h_kv_initial=h_kv_state,

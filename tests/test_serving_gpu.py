@@ -117,9 +117,14 @@ def _expected(kind, lay, md_lens, idx, has, nd, mixed_qkv, gates, conv_cache, st
             st_new[0][slot] = S
         else:
             a, alpha_in, b = gates
-            g, alpha, beta = kref.gka_gating(lay.A.cpu(), a[sl], alpha_in[sl], b[sl],
-                                             lay.dt_bias.cpu())
-            g, alpha, beta = g.to(a.dtype), alpha.to(a.dtype), beta.to(a.dtype)
+            if lay.use_forgetting_gate:
+                g, alpha, beta = kref.gka_gating(lay.A.cpu(), a[sl], alpha_in[sl], b[sl],
+                                                 lay.dt_bias.cpu())
+                g, alpha, beta = g.to(a.dtype), alpha.to(a.dtype), beta.to(a.dtype)
+            else:    # no forgetting gate: no decay, sigmoid gates in a.dtype (:1144-1148)
+                g = torch.zeros(1, L, H, dtype=a.dtype)
+                alpha = torch.sigmoid(alpha_in[sl].float()).to(a.dtype)[None]
+                beta = torch.sigmoid(b[sl].float()).to(a.dtype)[None]
             alpha = alpha + 0.5                         # in a.dtype, as the layer adds it
             hkv0 = states[0][slot] if init else None
             hkk0 = states[1][slot] if init else None
@@ -130,8 +135,8 @@ def _expected(kind, lay, md_lens, idx, has, nd, mixed_qkv, gates, conv_cache, st
     return torch.cat(outs), conv_new, st_new
 
 
-def _run(kind, batch, dev, o_norm=False, seed=1):
-    lay = _layer(kind, seed)
+def _run(kind, batch, dev, o_norm=False, seed=1, **extra):
+    lay = _layer(kind, seed, **extra)
     md, lens, idx, has = _meta(batch, dev)
     nd = BATCHES[batch][0]
     n = md.num_actual_tokens
@@ -195,6 +200,21 @@ def test_forward_core_fused_o_norm(dev, kind):
     assert (got == expect).double().mean().item() >= 0.98
     for a, b in zip(plain["states_d"], fused["states_d"]):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("batch", ["mixed", "decode"])
+def test_gka_core_without_forgetting_gate(dev, batch):
+    """use_forgetting_gate = False: g = None (no decay) and sigmoid alpha / beta in
+    the gate dtype (primed_gka_layer.py:1144-1148)."""
+    r = _run("gka", batch, dev, use_forgetting_gate=False, use_forgetting_gate_kk=False)
+    o_r, conv_r, st_r = _expected("gka", r["lay"], r["lens"], r["idx"], r["has"], r["nd"],
+                                  r["mixed_qkv"], r["gates"], r["conv_cache"], r["states"])
+    n = r["n"]
+    assert_out_close(r["core"][:n], o_r)
+    assert torch.equal(r["cc"], conv_r)
+    for got, exp in zip(r["states_d"], st_r):
+        for s in set(int(i) for i in r["idx"]):
+            assert_state_close(got[s], exp[s], what=f"slot {s}")
 
 
 def test_forward_core_rejects_spec_decode(dev):
