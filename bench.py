@@ -176,6 +176,81 @@ def bench_conv(dev, steps, warmup):
                 ms_dec=ms_dec, dec_bytes=dec_bytes, dec_GBps=dec_bytes / (ms_dec * 1e-3) / 1e9)
 
 
+def bench_mamba2_core(dev, steps, warmup):
+    """The primed Mamba2 layer's conv_ssm_forward on a prefill batch (8 sequences x
+    4096 tokens; 32 heads, head_dim = d_state = 128, d_xb = 1024, conv width 4 with
+    bias, fp32 state pool of 8 slots, B/C RMSNorm): the reference layer's call
+    sequence over hmx ops (primed_mamba2_layer.py:663-669 norms, :775-790 conv,
+    :800-835 rearrange + repeat_kv copies, :812-824 gather, :844-863 scan, :941
+    scatter) against hmx.serving.mamba2_conv_ssm_forward."""
+    from types import SimpleNamespace
+    import torch
+    import hmx
+    import hmx.serving as srv
+    T, H, P, nseq, W = 32768, 32, 128, 8, 4
+    N, XB = P, 1024
+    I, HX = H * P, XB // P
+    CD = I + 2 * XB
+    dproj = 2 * I + 2 * XB + H
+    g = torch.Generator(device=dev).manual_seed(7)
+    rnd = lambda *s, sc=1.0: torch.randn(*s, generator=g, device=dev) * sc
+
+    class Norm:
+        """Stand-in for the layer's fused vLLM RMSNorm modules: one pass."""
+        def __init__(self):
+            self.weight = (torch.rand(P, generator=g, device=dev) + 0.5).bfloat16()
+
+        def __call__(self, x):
+            return hmx.rms_norm_gated(x, None, self.weight, 1e-6)
+
+    lay = SimpleNamespace(
+        tp_size=1, tped_intermediate_size=I, tped_conv_size=CD, dt_pad=0, num_heads=H,
+        xb_size=XB, ssm_state_size=N, head_dim=P, n_groups=H, chunk_size=256,
+        conv_weights=rnd(CD, W, sc=0.4).bfloat16(), conv1d=SimpleNamespace(bias=rnd(CD, sc=0.1).bfloat16()),
+        activation="silu", A=-torch.exp(torch.rand(H, generator=g, device=dev) * 2), D=rnd(H),
+        dt_bias=rnd(H, sc=0.5), B_norm=Norm(), C_norm=Norm(), use_pos_embed=False,
+        cache_config=SimpleNamespace(mamba_cache_mode="none"))
+    proj = rnd(T, dproj).bfloat16()
+    proj[:, I + CD:] = proj[:, I + CD:] * 0.5 - 1.5
+    conv_cache = rnd(nseq, W - 1, CD).bfloat16()
+    pool = rnd(nseq, H, P, N, sc=0.05)
+    idx = torch.randperm(nseq, generator=g, device=dev).to(torch.int32)
+    has = torch.ones(nseq, dtype=torch.bool, device=dev)
+    qsl = torch.arange(0, T + 1, T // nseq, dtype=torch.int32, device=dev)
+    md = SimpleNamespace(num_prefills=nseq, num_decode_tokens=0, num_prefill_tokens=T,
+                         state_indices_tensor=idx, has_initial_states_p=has,
+                         prep_initial_states=True, query_start_loc_p=qsl)
+    output = torch.empty(T, I, dtype=torch.bfloat16, device=dev)
+    cs = conv_cache.transpose(1, 2)
+
+    def reference_sequence():
+        hbc = proj[:, I:I + CD]
+        hs, B, C = torch.split(hbc, [XB, XB, I], dim=-1)
+        B = lay.B_norm(B.reshape(-1, P)).view(B.shape)
+        C = lay.C_norm(C.reshape(-1, P)).view(C.shape)
+        hbc = torch.cat([hs, B, C], dim=-1)
+        x = hmx.causal_conv1d_fn(hbc.t(), lay.conv_weights, lay.conv1d.bias, conv_states=cs,
+                                 has_initial_state=has, cache_indices=idx,
+                                 query_start_loc=qsl).t()
+        hs, B, C = torch.split(x, [XB, XB, I], dim=-1)
+        rep = lambda t: (t.reshape(T, HX, P).permute(1, 0, 2)[:, None]
+                         .expand(HX, H // HX, T, P).reshape(H, T, P))        # repeat_kv
+        hs, B = rep(hs).permute(1, 0, 2), rep(B).permute(1, 0, 2)
+        init = torch.where(has[:, None, None, None], pool[idx.long()], 0)
+        st = hmx.mamba_chunk_scan_combined_varlen(
+            hs, proj[:, I + CD:], lay.A, B, C.reshape(T, H, N), 256, cu_seqlens=qsl,
+            out=output.view(T, H, P), D=lay.D, dt_bias=lay.dt_bias, initial_states=init,
+            dt_softplus=True)
+        pool[idx.long()] = st
+
+    def hmx_core():
+        srv.mamba2_conv_ssm_forward(lay, proj, output, md, cs, pool)
+
+    ms_ref = _timed(reference_sequence, steps, warmup)
+    ms_core = _timed(hmx_core, steps, warmup)
+    return dict(ms_ref=ms_ref, ms_core=ms_core, tokens=T)
+
+
 def bench_core(dev, steps, warmup):
     """The GDN layer's core at the C1 shape (8 sequences x 4096 tokens, H = HKV = 32,
     d = 128, conv width 4, state pools of 8 slots): the reference layer's call
@@ -489,6 +564,7 @@ def main():
         out["conv"] = bench_conv(dev, a.steps, a.warmup)
     if a.only in (None, "core"):
         out["core"] = bench_core(dev, max(2, a.steps // 2), a.warmup)
+        out["mamba2_core"] = bench_mamba2_core(dev, max(2, a.steps // 2), a.warmup)
     if a.only in (None, "decode"):
         out["decode"] = bench_decode(dev)
         out["gka_decode"] = bench_gka_decode(dev)
@@ -597,6 +673,16 @@ def main():
         line["gdn_layer_core"] = {
             "config": {"workload": "GDN layer core + output norm at C1 (8 seqs x 4096 tokens, "
                                    "H=HKV=32, d=128, conv width 4, pooled states)"},
+            "reference_call_sequence_ms": round(r["ms_ref"], 4),
+            "hmx_serving_core_ms": round(r["ms_core"], 4),
+            "tokens_per_s": round(r["tokens"] / (r["ms_core"] * 1e-3), 1),
+        }
+    if "mamba2_core" in out:
+        r = out["mamba2_core"]
+        line["mamba2_layer_core"] = {
+            "config": {"workload": "Mamba2 conv_ssm_forward, prefill of 8 seqs x 4096 tokens "
+                                   "(H=32, head_dim=d_state=128, d_xb=1024, conv width 4, "
+                                   "B/C norm, fp32 pool)"},
             "reference_call_sequence_ms": round(r["ms_ref"], 4),
             "hmx_serving_core_ms": round(r["ms_core"], 4),
             "tokens_per_s": round(r["tokens"] / (r["ms_core"] * 1e-3), 1),
