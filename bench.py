@@ -251,6 +251,78 @@ def bench_mamba2_core(dev, steps, warmup):
     return dict(ms_ref=ms_ref, ms_core=ms_core, tokens=T)
 
 
+def bench_gka_core(dev, steps, warmup):
+    """The GKA layer's core on the same prefill batch (8 sequences x 4096 tokens,
+    H = HKV = 32, d = 128, num_iter 8): the reference call sequence over hmx ops
+    (primed_gka_layer.py:1060-1300 then o_norm: conv to a new tensor, contiguous
+    q/k/v, gating, gather and zeroing of both pools, prefill, scatter of both,
+    copy into core_attn_out, separate norm) against hmx.serving.gka_forward_core
+    with the norm fused."""
+    from types import SimpleNamespace
+    import torch
+    import hmx
+    import hmx.serving as srv
+    from hmx import workloads as wl
+    T, H, D, nseq = 32768, 32, 128, 8
+    cd = 3 * H * D
+    g = torch.Generator(device=dev).manual_seed(wl.SEED_BASE + 9)
+    lay = SimpleNamespace(
+        conv1d=SimpleNamespace(weight=(torch.randn(cd, 1, 4, generator=g, device=dev) * 0.4)
+                               .bfloat16()),
+        activation="silu", A=torch.rand(H, generator=g, device=dev),
+        dt_bias=torch.randn(H, generator=g, device=dev), key_dim=H * D, kv_k_dim=H * D,
+        kv_v_dim=H * D, num_heads=H, num_kv_heads=H, head_k_dim=D, head_v_dim=D, tp_size=1,
+        proj_k=None, use_forgetting_gate=True, use_forgetting_gate_kk=True, use_beta_gate=True,
+        num_iter=8, ridge_strength=0.02, gla_scale=D ** -0.5, _alpha_idx=None)
+    mixed = torch.randn(T, cd, generator=g, device=dev).bfloat16()
+    a, alpha_in, b = (torch.randn(T, H, generator=g, device=dev).bfloat16() for _ in range(3))
+    z = torch.randn(T, H, D, generator=g, device=dev).bfloat16()
+    wn = torch.rand(D, generator=g, device=dev) + 0.5
+    conv_cache = torch.randn(nseq, 3, cd, generator=g, device=dev).bfloat16()
+    x16 = torch.randn(nseq, H, D, 16, generator=g, device=dev) * 0.05
+    hkk = x16 @ x16.transpose(-1, -2)
+    hkv = torch.randn(nseq, H, D, D, generator=g, device=dev) * 0.02
+    qs = torch.arange(0, T + 1, T // nseq, dtype=torch.int32, device=dev)
+    idx = torch.randperm(nseq, generator=g, device=dev).to(torch.int32)
+    has = torch.ones(nseq, dtype=torch.bool, device=dev)
+    md = SimpleNamespace(spec_sequence_masks=None, num_actual_tokens=T, num_decodes=0,
+                         num_decode_tokens=0, num_prefills=nseq, non_spec_query_start_loc=qs,
+                         non_spec_state_indices_tensor=idx, has_initial_state=has,
+                         non_spec_query_start_loc_d=None, non_spec_query_start_loc_p=None)
+    core = torch.zeros(T, H, D, dtype=torch.bfloat16, device=dev)
+    cs = conv_cache.transpose(1, 2)
+    w2 = lay.conv1d.weight.view(cd, 4)
+
+    def reference_sequence():
+        x = hmx.causal_conv1d_fn(mixed.t(), w2, None, conv_states=cs, query_start_loc=qs,
+                                 cache_indices=idx, has_initial_state=has).t()
+        q = x[:, :H * D].reshape(1, T, H, D).contiguous()
+        k = x[:, H * D:2 * H * D].reshape(1, T, H, D).contiguous()
+        v = x[:, 2 * H * D:].reshape(1, T, H, D).contiguous()
+        gg, alpha, beta = hmx.fused_gka_gating(lay.A, a, alpha_in, b, lay.dt_bias)
+        alpha = alpha + 0.5
+        il = idx.long()
+        kk0, kv0 = hkk[il].contiguous(), hkv[il].contiguous()
+        kk0[~has] = 0
+        kv0[~has] = 0
+        o, kkf, kvf = hmx.gka_chebyshev_gla_prefill(
+            q, k, v, alpha, gg, gg, beta, lay.gla_scale, ridge_ratio=lay.ridge_strength,
+            num_iter=lay.num_iter, h_kk_initial=kk0, h_kv_initial=kv0,
+            output_final_state=True, cu_seqlens=qs)
+        hkk[il] = kkf
+        hkv[il] = kvf
+        core[:T] = o.squeeze(0)
+        return hmx.rms_norm_gated(core, z, wn, 1e-6)
+
+    def hmx_core():
+        srv.gka_forward_core(lay, mixed, a, alpha_in, b, core, md, cs, hkk, hkv,
+                             o_norm=(wn, z, 1e-6))
+
+    ms_ref = _timed(reference_sequence, steps, warmup)
+    ms_core = _timed(hmx_core, steps, warmup)
+    return dict(ms_ref=ms_ref, ms_core=ms_core, tokens=T)
+
+
 def bench_core(dev, steps, warmup):
     """The GDN layer's core at the C1 shape (8 sequences x 4096 tokens, H = HKV = 32,
     d = 128, conv width 4, state pools of 8 slots): the reference layer's call
@@ -565,6 +637,7 @@ def main():
     if a.only in (None, "core"):
         out["core"] = bench_core(dev, max(2, a.steps // 2), a.warmup)
         out["mamba2_core"] = bench_mamba2_core(dev, max(2, a.steps // 2), a.warmup)
+        out["gka_core"] = bench_gka_core(dev, max(2, a.steps // 4), 1)
     if a.only in (None, "decode"):
         out["decode"] = bench_decode(dev)
         out["gka_decode"] = bench_gka_decode(dev)
@@ -673,6 +746,15 @@ def main():
         line["gdn_layer_core"] = {
             "config": {"workload": "GDN layer core + output norm at C1 (8 seqs x 4096 tokens, "
                                    "H=HKV=32, d=128, conv width 4, pooled states)"},
+            "reference_call_sequence_ms": round(r["ms_ref"], 4),
+            "hmx_serving_core_ms": round(r["ms_core"], 4),
+            "tokens_per_s": round(r["tokens"] / (r["ms_core"] * 1e-3), 1),
+        }
+    if "gka_core" in out:
+        r = out["gka_core"]
+        line["gka_layer_core"] = {
+            "config": {"workload": "GKA layer core + output norm, prefill of 8 seqs x 4096 "
+                                   "tokens (H=HKV=32, d=128, num_iter 8, pooled states)"},
             "reference_call_sequence_ms": round(r["ms_ref"], 4),
             "hmx_serving_core_ms": round(r["ms_core"], 4),
             "tokens_per_s": round(r["tokens"] / (r["ms_core"] * 1e-3), 1),
