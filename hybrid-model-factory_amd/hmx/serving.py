@@ -262,7 +262,7 @@ def mamba2_conv_ssm_forward(layer, projected_states: torch.Tensor, output: torch
     out = output[:n].view(n, H, P)
     if npf > 0:
         idx_p = idx[nd:nd + npf]
-        has_c = md.has_initial_states_p                  # the conv takes the flags as given (:782)
+        has_c = md.has_initial_states_p                  # the conv takes the flags as given (:788)
         has = has_c
         if has is None or not md.prep_initial_states:    # the scan starts from zeros (:811-824)
             has = torch.zeros(npf, dtype=torch.bool, device=hbc.device)
