@@ -110,7 +110,7 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(RecurrentParams p) {
     write_row = p.idx[(int64_t)n * p.idx_stride];
     if (write_row < 0) return;
   } else {
-    write_row = n;
+    write_row = bos;   // fused_recurrent_gqa.py:137-139: row bos of the [B*T] rows
   }
 
   __shared__ float part[2][4];   // NORM: per-wave sums of squares, by token parity

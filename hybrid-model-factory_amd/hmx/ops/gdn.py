@@ -99,7 +99,9 @@ def fused_recurrent_gated_delta_rule_gqa(
     [B,T,H,V].  With ``inplace_final_state`` the state pool ``initial_state``
     [slots,H,K,V] is updated in place at ``ssm_state_indices`` and returned;
     otherwise a new [B,T,H,K,V] tensor holds sequence n's final state in flat
-    row n.  Returns (o [B,T,H,V], final_state)  (fused_recurrent_gqa.py:227-277).
+    row bos_n (its first token's row over B*T, as fused_recurrent_gqa.py:137-139
+    stores it); the other rows are left unwritten.  Returns (o [B,T,H,V],
+    final_state)  (fused_recurrent_gqa.py:227-277).
 
     Keyword-only extension (no reference counterpart): ``o_norm_weight`` [V] (and
     optionally ``o_norm_gate`` [B,T,H,V], q.dtype) returns the layer's gated
@@ -233,6 +235,19 @@ def _cu_count(device: torch.device) -> int:
 
 _SEG_CACHE: "collections.OrderedDict[tuple, torch.Tensor]" = collections.OrderedDict()
 _SEG_CACHE_SIZE = 64
+
+
+def seq_bounds(cu_seqlens: torch.Tensor | None, B: int, T: int) -> list[tuple[int, int]]:
+    """(bos, eos) of every sequence over the B*T flattened tokens: the B rows, or the
+    cu_seqlens runs (B == 1).  Rejects cu_seqlens that do not start at 0, decrease,
+    or end past the tokens (ValueError), so no kernel reads or writes past them."""
+    if cu_seqlens is None:
+        return [(n * T, n * T + T) for n in range(B)]
+    cs = [int(x) for x in cu_seqlens.tolist()]
+    bounds = [(cs[n], cs[n + 1]) for n in range(len(cs) - 1)]
+    if not cs or cs[0] != 0 or cs[-1] > B * T or any(b < a for a, b in bounds):
+        raise ValueError(f"cu_seqlens must be non-decreasing from 0 to <= {B * T}: {cs}")
+    return bounds
 
 
 def _device_table(rows: list[list[int]], device) -> torch.Tensor:
@@ -374,13 +389,7 @@ def chunk_gated_delta_rule_gqa(
         raise ValueError(f"bad GQA shapes q{tuple(q.shape)} k{tuple(k.shape)} v{tuple(v.shape)}")
     if g.shape != (B, T, H) or beta.shape != (B, T, H):
         raise ValueError(f"g {tuple(g.shape)} and beta {tuple(beta.shape)} must be [B,T,H]")
-    if cu_seqlens is None:
-        bounds = [(n * T, n * T + T) for n in range(B)]
-    else:
-        cs = [int(x) for x in cu_seqlens.tolist()]
-        bounds = [(cs[n], cs[n + 1]) for n in range(len(cs) - 1)]
-        if cs[0] != 0 or cs[-1] > T or any(b < a for a, b in bounds):
-            raise ValueError(f"cu_seqlens must be non-decreasing from 0 to <= {T}: {cs}")
+    bounds = seq_bounds(cu_seqlens, B, T)
     N = len(bounds)
     _lib.require_gpu(ssm_state_indices, has_initial_state, out)
     idx = None
@@ -460,6 +469,16 @@ def chunk_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None,
                            output_final_state=False, cu_seqlens=None,
                            use_qk_l2norm_in_kernel=False):
     """fla-style prefill entry (training/src/hmf/.../gated_deltanet/gdn.py:462-476):
-    the GQA op with k, v already expanded to H heads."""
+    the GQA op with k, v already expanded to H heads.  Returns (o, final_state
+    [N,H,K,V] fp32 or None).
+
+    The training layer passes q, k, v in the model's dtype.  bf16/fp16 inputs run
+    the chunked kernel; fp32 inputs (which the chunked kernel's bf16 MFMA products
+    would round) run the fp32 recurrent kernel over the same tokens, so an fp32
+    model gets fp32 arithmetic throughout."""
+    if q.dtype == torch.float32:
+        return fused_recurrent_gated_delta_rule(q, k, v, g, beta, scale, initial_state,
+                                                output_final_state, cu_seqlens,
+                                                use_qk_l2norm_in_kernel)
     return chunk_gated_delta_rule_gqa(q, k, v, g, beta, scale, initial_state, output_final_state,
                                       cu_seqlens, use_qk_l2norm_in_kernel)

@@ -18,7 +18,8 @@ import logging
 import torch
 
 from .. import _lib
-from .gdn import _cu_count, _device_table, _gate_rows, _i32, _segment_table, _token_rows
+from .gdn import (_cu_count, _device_table, _gate_rows, _i32, _segment_table, _token_rows,
+                  seq_bounds)
 
 GKA_WORKGROUPS_PER_CU = 1
 _warned_num_iter_zero = False
@@ -220,11 +221,7 @@ def _gka_prefill(q, k, v, alpha, g, gk, beta, gla_scale, ridge_ratio, num_iter, 
                      state_indices, has_initial_state, out)
     B, T, H, D = q.shape
     HKV, V = k.shape[2], v.shape[-1]
-    if cu_seqlens is None:
-        bounds = [(n * T, n * T + T) for n in range(B)]
-    else:
-        cs = [int(x) for x in cu_seqlens.tolist()]
-        bounds = [(cs[n], cs[n + 1]) for n in range(len(cs) - 1)]
+    bounds = seq_bounds(cu_seqlens, B, T)
     N = len(bounds)
     idx = None
     if state_indices is not None:

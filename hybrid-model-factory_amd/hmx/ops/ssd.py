@@ -13,7 +13,7 @@ from __future__ import annotations
 import torch
 
 from .. import _lib
-from .gdn import _cu_count, _device_table, _segment_table
+from .gdn import _cu_count, _device_table, _segment_table, seq_bounds
 
 SSD_CHUNK = 64                 # the kernel's internal chunk length (tokens)
 SSD_WORKGROUPS_PER_CU = 2
@@ -62,6 +62,13 @@ def _ssd_scan(x, dt, A, B, C, D, z, dt_bias, dt_softplus, dt_limit, bounds, h0, 
                          f"x's heads {HX}")
     if tuple(C.shape) != (T, GC, N) or tuple(y.shape) != (T, H, P):
         raise ValueError(f"C must be [{T}, groups, {N}] and out [{T}, {H}, {P}]")
+    if B.shape[0] != T or tuple(dt.shape) != (T, H):
+        raise ValueError(f"B must be [{T}, groups, {N}] and dt [{T}, {H}], got "
+                         f"{tuple(B.shape)} and {tuple(dt.shape)}")
+    if z is not None and tuple(z.shape) != (T, H, P):
+        raise ValueError(f"z must be [{T}, {H}, {P}], got {tuple(z.shape)}")
+    if any(a < 0 or b < a or b > T for a, b in bounds):
+        raise ValueError(f"sequence bounds must lie within the {T} tokens")
     x, B, C, y = _prep3(x), _prep3(B), _prep3(C), y
     z = None if z is None else _prep3(z)
     if not _vec_ok(y, (0, 1)):
@@ -143,8 +150,7 @@ def mamba_chunk_scan_combined(x, dt, A, B, C, chunk_size, D=None, z=None, dt_bia
         rows = seq_idx.to(torch.int64).cpu().tolist()
         runs_per_row = [_runs(r) for r in rows]
     elif cu_seqlens is not None:
-        cs = [int(v) for v in cu_seqlens.tolist()]
-        runs_per_row = [[(cs[i], cs[i + 1]) for i in range(len(cs) - 1) if cs[i + 1] > cs[i]]]
+        runs_per_row = [[(a, e) for a, e in seq_bounds(cu_seqlens, 1, l) if e > a]]
     else:
         runs_per_row = [[(0, l)] for _ in range(b)]
     bounds, first_of_row, last_of_row, end_at = [], [], [], {}
@@ -223,8 +229,7 @@ def mamba_chunk_scan_combined_varlen(x, dt, A, B, C, chunk_size, cu_seqlens, cu_
     T, P = x.shape[0], x.shape[2]
     H = dt.shape[1]
     N = B.shape[-1]
-    cs = [int(v) for v in cu_seqlens.tolist()]
-    bounds = [(cs[i], cs[i + 1]) for i in range(len(cs) - 1)]
+    bounds = seq_bounds(cu_seqlens, 1, T)
     pooled = h0 = None
     if ssm_state_indices is not None:
         _lib.require_gpu(ssm_state_indices, has_initial_state)

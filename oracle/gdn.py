@@ -215,8 +215,9 @@ def fused_recurrent_gated_delta_rule_gqa(q, k, v, g, beta=None, scale=None,
     Returns (o [B,T,H,V] in ``dtype``, final) where ``final`` is an updated
     COPY of the state pool when ``inplace_final_state`` (slot
     ``ssm_state_indices[n, 0]`` receives sequence n's last state, FR:135-144), else
-    a new [B,T,H,K,V] tensor whose flat row n (over B*T) holds sequence n's
-    final state.  The initial state of sequence n is pool row
+    a new [B,T,H,K,V] tensor whose flat row ``bos`` (over B*T; the sequence's first
+    token) holds sequence n's final state (FR:137-139: the store pointer is not
+    advanced without ``inplace_final_state``).  The initial state of sequence n is pool row
     ``ssm_state_indices[n, num_accepted_tokens[n]-1]`` (column 0 without
     ``num_accepted_tokens``, FR:95-105), or row ``bos`` of ``initial_state``
     without indices (FR:107).  Zero-length sequences are skipped (FR:67-68).
@@ -256,5 +257,5 @@ def fused_recurrent_gated_delta_rule_gqa(q, k, v, g, beta=None, scale=None,
         if inplace_final_state:
             ff[int(idx[n, 0])] = Sn
         else:
-            ff[n] = Sn
+            ff[bos] = Sn
     return o, final

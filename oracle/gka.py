@@ -104,6 +104,62 @@ def gka_seq(q, k, v, alpha, g, gk, beta, scale, ridge_ratio, num_iter, h_kk0=Non
     return o, (Hs if num_iter > 0 else None), S
 
 
+def gka_seq_blocked(q, k, v, alpha, g, gk, beta, scale, ridge_ratio, num_iter, h_kk0=None,
+                    h_kv0=None, dtype=DEFAULT, block=256):
+    """``gka_seq`` (normalize=True) batched over blocks of up to ``block`` tokens: the
+    states H_t and S_t of every token of a block are formed at once by unrolling the
+    recurrences (a cumulative sum of e^{-G_j}-scaled outer products, then e^{G_t}),
+    then every token's Chebyshev solve and output run as one batched call.  The same
+    per-token states and solves in fp64, in another summation order; used where
+    ``gka_seq``'s per-token Python loop is too slow (full-length C3 heads)."""
+    T, H, D = q.shape
+    V = v.shape[-1]
+    q = l2n(q.to(dtype))
+    k = _expand(l2n(k.to(dtype)), H)
+    v = _expand(v.to(dtype), H)
+    be = None if beta is None else beta.to(dtype) + EPS
+    if be is not None:
+        k = k * be[..., None]
+        v = v * be[..., None]
+    Hs = torch.zeros(H, D, D, dtype=dtype) if h_kk0 is None else h_kk0.to(dtype).clone()
+    S = torch.zeros(H, D, V, dtype=dtype) if h_kv0 is None else h_kv0.to(dtype).clone()
+    o = torch.zeros(T, H, V, dtype=dtype)
+    gk_log = torch.zeros(T, H, dtype=dtype) if gk is None else gk.to(dtype)
+    g_log = g.to(dtype)
+    t0 = 0
+    while t0 < T:
+        # block [t0, t1): at most ``block`` tokens, and short enough that the
+        # in-block log-decay sums stay above -500 (so e^{-G} stays finite)
+        t1 = min(T, t0 + block)
+        dec = torch.minimum(torch.cumsum(gk_log[t0:t1], 0).min(-1).values,
+                            torch.cumsum(g_log[t0:t1], 0).min(-1).values)
+        over = torch.nonzero(dec < -500.0)
+        if len(over):
+            t1 = t0 + max(1, int(over[0]))
+        L = t1 - t0
+        # the per-token recurrences H_t = e^{gk_t} H_{t-1} + k~ k~^T and
+        # S_t = e^{g_t} S_{t-1} + k~ v~^T, unrolled over the block:
+        #   X_t = e^{G_t} (X_{t0-1} + sum_{j<=t} e^{-G_j} x_j),  G = in-block cumsum
+        kb, vb = k[t0:t1], v[t0:t1]
+        Sst = None
+        if num_iter > 0:
+            G = torch.cumsum(gk_log[t0:t1], 0)
+            Hst = torch.einsum("lhd,lhe->lhde", kb * torch.exp(-G)[..., None], kb)
+            Hst = torch.cumsum(Hst, 0).add_(Hs).mul_(torch.exp(G)[..., None, None])
+            Hs = Hst[L - 1].clone()
+        G = torch.cumsum(g_log[t0:t1], 0)
+        Sst = torch.einsum("lhd,lhe->lhde", kb * torch.exp(-G)[..., None], vb)
+        Sst = torch.cumsum(Sst, 0).add_(S).mul_(torch.exp(G)[..., None, None])
+        S = Sst[L - 1].clone()
+        xq = q[t0:t1]
+        if num_iter > 0:
+            x, _ = chebyshev(Hst, xq, ridge_ratio, num_iter)
+            xq = xq + alpha[t0:t1].to(dtype)[..., None] * (x - xq)
+        o[t0:t1] = scale * torch.einsum("lhkv,lhk->lhv", Sst, xq)
+        t0 = t1
+    return o, (Hs if num_iter > 0 else None), S
+
+
 def gka_chebyshev_gla_prefill(q, k, v, alpha, g, gk, beta, gla_scale, ridge_ratio=0.02,
                               num_iter=30, h_kk_initial=None, h_kv_initial=None,
                               output_final_state=True, cu_seqlens=None, dtype=DEFAULT):

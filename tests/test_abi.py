@@ -64,3 +64,39 @@ def test_wrappers_raise_reference_errors_on_cpu():
     with pytest.raises(RuntimeError, match="GPU"):
         hmx.fused_recurrent_gated_delta_rule_gqa(q, q, q, g, g, initial_state=None,
                                                  inplace_final_state=False)
+
+
+@pytest.mark.parametrize("cs", [[1, 4], [0, 5, 3], [0, 4, 9], []])
+def test_bad_cu_seqlens_rejected(cs):
+    """Sequence bounds are checked on the host before any kernel reads them:
+    cu_seqlens must start at 0, not decrease and end within the tokens."""
+    from hmx.ops.gdn import seq_bounds
+    with pytest.raises(ValueError, match="cu_seqlens"):
+        seq_bounds(torch.tensor(cs, dtype=torch.int32), 1, 8)
+
+
+def test_good_cu_seqlens_bounds():
+    from hmx.ops.gdn import seq_bounds
+    assert seq_bounds(torch.tensor([0, 0, 3, 8]), 1, 8) == [(0, 0), (0, 3), (3, 8)]
+    assert seq_bounds(None, 2, 5) == [(0, 5), (5, 10)]
+
+
+def test_ssd_scan_rejects_mismatched_operands():
+    """The SSD launcher checks every operand's token count (and z's shape) against
+    x before launching."""
+    from hmx.ops.ssd import _ssd_scan
+    T, H, P, G, N = 16, 4, 64, 2, 128
+    x = torch.zeros(T, H, P, dtype=torch.bfloat16)
+    Bm = torch.zeros(T, G, N, dtype=torch.bfloat16)
+    dt = torch.zeros(T, H)
+    y = torch.zeros(T, H, P, dtype=torch.bfloat16)
+    A = torch.zeros(H)
+    bad = [dict(B=Bm[:8]), dict(dt=dt[:8]), dict(z=torch.zeros(T, H, 32, dtype=torch.bfloat16)),
+           dict(bounds=[(0, T + 1)])]
+    for kw in bad:
+        args = dict(x=x, dt=dt, A=A, B=Bm, C=Bm, D=None, z=None, dt_bias=None, dt_softplus=False,
+                    dt_limit=(0.0, float("inf")), bounds=[(0, T)], h0=None, y=y, want_final=False)
+        args.update(kw)
+        with pytest.raises(ValueError):
+            _ssd_scan(**args)
+

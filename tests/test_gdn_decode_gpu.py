@@ -78,9 +78,9 @@ def test_decode_spec_varlen(dev):
     assert_state_close(pool_d, pool_ref)
 
 
-@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
-def test_decode_not_inplace_headwise_beta(dev, dtype):
-    H, HKV, K, V, B, T = 4, 4, 128, 64, 3, 1
+@pytest.mark.parametrize("dtype,T", [(torch.float16, 1), (torch.float32, 1), (torch.float32, 3)])
+def test_decode_not_inplace_headwise_beta(dev, dtype, T):
+    H, HKV, K, V, B = 4, 4, 128, 64, 3
     g0 = torch.Generator().manual_seed(3)
     q = torch.randn(B, T, H, K, generator=g0).to(dtype)
     k = torch.randn(B, T, HKV, K, generator=g0).to(dtype)
@@ -97,7 +97,26 @@ def test_decode_not_inplace_headwise_beta(dev, dtype):
     torch.cuda.synchronize()
     assert f.shape == (B, T, H, K, V)
     assert_out_close(o, o_ref)
-    assert_state_close(f, f_ref)
+    rows = [n * T for n in range(B)]    # sequence n's final state sits at row bos = n*T
+    assert_state_close(f.view(B * T, H, K, V)[rows], f_ref.view(B * T, H, K, V)[rows])
+
+
+def test_decode_not_inplace_varlen_rows(dev):
+    """Without inplace_final_state, sequence n's state goes to flat row cu_seqlens[n]
+    (fused_recurrent_gqa.py:137-139), also after a leading empty sequence."""
+    H, K, V = 2, 128, 128
+    q, k, v, g, beta, gen = _mk(5, H, H, K, V, torch.bfloat16, 12)
+    cu = torch.tensor([0, 0, 2, 5], dtype=torch.int32)
+    h0 = torch.randn(5, H, K, V, generator=gen) * 0.05
+    o_ref, f_ref = ref.fused_recurrent_gated_delta_rule_gqa(
+        q, k, v, g, beta, initial_state=h0, inplace_final_state=False, cu_seqlens=cu,
+        use_qk_l2norm_in_kernel=True)
+    o, f = hmx.fused_recurrent_gated_delta_rule_gqa(
+        q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta.to(dev), initial_state=h0.to(dev),
+        inplace_final_state=False, cu_seqlens=cu.to(dev), use_qk_l2norm_in_kernel=True)
+    torch.cuda.synchronize()
+    assert_out_close(o, o_ref)
+    assert_state_close(f.view(5, H, K, V)[[0, 2]], f_ref.view(5, H, K, V)[[0, 2]])
 
 
 def test_decode_bf16_state_and_no_l2norm(dev):

@@ -165,3 +165,70 @@ def test_prefill_c1_varlen(dev):
     T = int(cu[-1])
     d = wl.gdn_inputs(T=T, H=8, HKV=8, D=128, config_id=1)
     _check(dev, *(d[n] for n in ("q", "k", "v", "g", "beta")), cu=cu)
+
+
+def test_c0_exact_shape(dev):
+    """C0 at its exact shape (B=1, T=2048, H=16, d=128, fp32 inputs, zero initial
+    state, in-kernel L2 norm): the fp32 inputs through the fp32 recurrent kernel and
+    their bf16 casts through the chunked kernel, each against the oracle's chunked
+    fp32 form on the same inputs (and the recurrent fp64 form for the first)."""
+    d = wl.gdn_inputs(T=2048, H=16, HKV=16, D=128, dtype=torch.float32, config_id=0)
+    q, k, v, g, beta = (d[n] for n in ("q", "k", "v", "g", "beta"))
+    o32, s32 = hmx.chunk_gated_delta_rule(
+        *[x.to(dev) for x in (q, k, v, g, beta)], output_final_state=True,
+        use_qk_l2norm_in_kernel=True)
+    torch.cuda.synchronize()
+    o_ref, s_ref = ref.chunk_gated_delta_rule_gqa(q, k, v, g, beta, output_final_state=True,
+                                                 use_qk_l2norm_in_kernel=True,
+                                                 dtype=torch.float32)
+    assert o32.dtype == torch.float32 and s32.shape == (1, 16, 128, 128)
+    assert_out_close(o32, o_ref, what="C0 fp32 o (recurrent kernel)")
+    assert_state_close(s32, s_ref, what="C0 fp32 state (recurrent kernel)")
+    o_rr, s_rr = ref.fused_recurrent_gated_delta_rule_gqa(
+        q, k, v, g, beta, initial_state=torch.zeros(1, 16, 128, 128),
+        inplace_final_state=True, ssm_state_indices=torch.zeros(1, dtype=torch.int32),
+        use_qk_l2norm_in_kernel=True)
+    assert_state_close(s32, s_rr[0:1], rel_tol=1e-5, what="C0 fp32 state vs fp64 recurrence")
+    qb, kb, vb = (x.bfloat16() for x in (q, k, v))
+    ob, sb = _run(dev, qb, kb, vb, g, beta)
+    o_ref_b, s_ref_b = ref.chunk_gated_delta_rule_gqa(qb, kb, vb, g, beta, output_final_state=True,
+                                                     use_qk_l2norm_in_kernel=True,
+                                                     dtype=torch.float32)
+    assert_out_close(ob, o_ref_b, what="C0 bf16 o (chunked kernel)")
+    assert_state_close(sb, s_ref_b, what="C0 bf16 state (chunked kernel)")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_fla_chunk_gated_delta_rule(dev, dtype):
+    """The training layer's call (gdn.py:462-476): fla keyword arguments, k/v with H
+    heads, B > 1 with initial_state and output_final_state, then the same tokens
+    packed with cu_seqlens (B = 1)."""
+    B, T, H = 3, 150, 2
+    q, k, v, g, beta, g0 = _mk(B, T, H, H, 13, normalize=False)
+    if dtype == torch.float32:
+        q, k, v = (x.float() for x in (q, k, v))
+    h0 = torch.randn(B, H, 128, 128, generator=g0) * 0.05
+    d = lambda x: x.to(dev)
+    o, s = hmx.chunk_gated_delta_rule(q=d(q), k=d(k), v=d(v), g=d(g), beta=d(beta),
+                                      initial_state=d(h0), output_final_state=True,
+                                      cu_seqlens=None, use_qk_l2norm_in_kernel=True)
+    torch.cuda.synchronize()
+    o_ref, s_ref = ref.chunk_gated_delta_rule_gqa(q, k, v, g, beta, initial_state=h0,
+                                                 output_final_state=True,
+                                                 use_qk_l2norm_in_kernel=True)
+    assert o.dtype == dtype and s.dtype == torch.float32
+    assert_out_close(o, o_ref)
+    assert_state_close(s, s_ref)
+    cu = torch.arange(0, (B + 1) * T, T, dtype=torch.int32)
+    flat = lambda x: x.reshape(1, B * T, *x.shape[2:])
+    o2, s2 = hmx.chunk_gated_delta_rule(q=d(flat(q)), k=d(flat(k)), v=d(flat(v)), g=d(flat(g)),
+                                        beta=d(flat(beta)), initial_state=d(h0),
+                                        output_final_state=True, cu_seqlens=d(cu),
+                                        use_qk_l2norm_in_kernel=True)
+    o3, s3 = hmx.chunk_gated_delta_rule(q=d(flat(q)), k=d(flat(k)), v=d(flat(v)), g=d(flat(g)),
+                                        beta=d(flat(beta)), cu_seqlens=d(cu),
+                                        use_qk_l2norm_in_kernel=True)
+    torch.cuda.synchronize()
+    assert_out_close(o2, o_ref.reshape(1, B * T, H, 128))
+    assert_state_close(s2, s_ref)
+    assert s3 is None and o3.shape == (1, B * T, H, 128)

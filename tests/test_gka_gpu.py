@@ -3,8 +3,9 @@
 Decode covers slot-indexed pools, GQA, beta/gk present or absent, bf16 h_kv,
 num_iter 1/8/30, zero-length entries and the num_iter=0 -> 1 rule.  Prefill
 covers num_iter 0/8/32, initial states, multi-segment (exact scalar-decay
-combine), varlen with empty sequences, no beta/gk, and C3 (T=32768, H=32) on
-its first heads/tokens plus prefill == T decode steps on one head.
+combine), varlen with empty sequences, no beta/gk, C3 (T=32768, H=32) at num_iter
+8 and 32 on two whole heads against the fp64 recurrence (across the planner's
+segment edges, and the final states), and prefill == T decode steps.
 """
 import pytest
 import torch
@@ -153,21 +154,75 @@ def test_gka_prefill_varlen(dev):
         assert torch.equal(hkv[1].cpu(), h0kv[1])
 
 
-def test_gka_prefill_c3_subset(dev):
-    """C3 shape (T=32768, H=32, bf16, ridge 0.01, n=8): heads 0-1 over the first
-    512 tokens vs the fp64 oracle (the per-token oracle is the slow part), and
-    the full-size call checked for finiteness and state shapes."""
-    from hmx import workloads as wl
-    d = wl.gka_inputs(T=32768, H=32, HKV=32, D=128, config_id=3)
+_C3_CACHE = {}
+
+
+def _c3_inputs():
+    if "d" not in _C3_CACHE:
+        from hmx import workloads as wl
+        _C3_CACHE["d"] = wl.gka_inputs(T=32768, H=32, HKV=32, D=128, config_id=3)
+    return _C3_CACHE["d"]
+
+
+@pytest.mark.parametrize("num_iter", [8, 32])
+def test_gka_prefill_c3_full_size(dev, num_iter):
+    """C3 (T=32768, H=32, bf16, ridge 0.01) at num_iter 8 and 32: two heads over the
+    whole sequence vs the fp64 per-token recurrence (its block-batched form), with
+    the output window around the first segment boundary the planner cuts, the whole
+    output of both heads and their final h_kk / h_kv."""
+    from hmx.ops import gdn as gops
+    from hmx.ops.gka import GKA_WORKGROUPS_PER_CU
+    d = _c3_inputs()
+    T, H = 32768, 32
     args = [d[n] for n in ("q", "k", "v", "alpha", "g", "gk", "beta")]
-    dev_args = [a.to(dev) for a in args]
-    o, hkk, hkv = hmx.gka_chebyshev_gla_prefill(*dev_args, 128 ** -0.5, ridge_ratio=0.01,
-                                                num_iter=8)
+    o, hkk, hkv = hmx.gka_chebyshev_gla_prefill(*[a.to(dev) for a in args], 128 ** -0.5,
+                                                ridge_ratio=0.01, num_iter=num_iter)
     torch.cuda.synchronize()
-    assert torch.isfinite(o.float()).all() and hkk.shape == (1, 32, 128, 128)
-    sub = [a[:, :512, :2] for a in args]
-    o_r, _, _ = ref.gka_chebyshev_gla_prefill(*sub, 128 ** -0.5, ridge_ratio=0.01, num_iter=8)
-    assert_out_close(o[:, :512, :2], o_r)
+    rows = gops._segment_table([(0, T)], H, GKA_WORKGROUPS_PER_CU * gops._cu_count(dev))
+    assert len(rows) > 1, "C3 is expected to run as several segments per head"
+    edge = rows[1][3] * gops.CHUNK          # first token of the second segment
+    hs = [0, 17]
+    sub = [a[0][:, hs] for a in args]
+    o_r, hkk_r, hkv_r = ref.gka_seq_blocked(*sub, 128 ** -0.5, 0.01, num_iter)
+    o_h = o[0][:, hs]
+    win = slice(edge - 256, edge + 256)
+    assert_out_close(o_h[win], o_r[win], what=f"o around the segment edge at {edge}")
+    assert_out_close(o_h, o_r, what="o, whole sequence")
+    assert_state_close(hkk[0, hs], hkk_r, what="h_kk final")
+    assert_state_close(hkv[0, hs], hkv_r, what="h_kv final")
+    assert torch.isfinite(o.float()).all()
+
+
+def test_gka_prefill_equals_decode_steps(dev):
+    """A prefill over T tokens equals T single-token decode steps through a pool slot
+    (decode decays both states by gk, so g = gk here): outputs token by token and
+    the final h_kk / h_kv."""
+    T, H, HKV = 150, 2, 1
+    q, k, v, alpha, _, gk, beta, g0 = _mk(T, H, HKV, 42)
+    h0kk = _psd_pool(1, H, g0)
+    h0kv = torch.randn(1, H, 128, 128, generator=g0) * 0.02
+    d = lambda x: x.to(dev)
+    o_p, hkk_p, hkv_p = hmx.gka_chebyshev_gla_prefill(
+        d(q), d(k), d(v), d(alpha), d(gk), d(gk), d(beta), 0.09, ridge_ratio=0.02, num_iter=8,
+        h_kk_initial=d(h0kk), h_kv_initial=d(h0kv), _segment_chunks=2)
+    pool_kk = torch.zeros(3, H, 128, 128, device=dev)
+    pool_kv = torch.zeros(3, H, 128, 128, device=dev)
+    pool_kk[1], pool_kv[1] = d(h0kk[0]), d(h0kv[0])
+    idx = torch.tensor([1], dtype=torch.int32, device=dev)
+    cu = torch.tensor([0, 1], dtype=torch.int32, device=dev)
+    o_d = torch.empty_like(o_p)
+    for t in range(T):
+        sl = slice(t, t + 1)
+        gt = d(gk[:, sl])
+        o_t, _, _ = hmx.gka_chebyshev_gla_decode(
+            d(q[:, sl]), d(k[:, sl]), d(v[:, sl]), d(alpha[:, sl]), gt, gt, d(beta[:, sl]), 0.09,
+            ridge_ratio=0.02, num_iter=8, h_kk=pool_kk, h_kv=pool_kv, cu_seqlens=cu,
+            ssm_state_indices=idx)
+        o_d[:, sl] = o_t
+    torch.cuda.synchronize()
+    assert_out_close(o_p, o_d.float(), what="prefill vs decode o")
+    assert_state_close(hkk_p[0], pool_kk[1], what="prefill vs decode h_kk")
+    assert_state_close(hkv_p[0], pool_kv[1], what="prefill vs decode h_kv")
 
 
 def _layer_prepared(B, T, H, seed):

@@ -129,6 +129,28 @@ def test_prefill_equals_decode_steps():
     assert torch.allclose(hkv[2], hkv_p[0], atol=1e-10)
 
 
+@pytest.mark.parametrize("block,num_iter,gates", [(1, 6, True), (5, 6, True), (64, 0, True),
+                                                  (16, 4, False)])
+def test_blocked_form_equals_per_token_form(block, num_iter, gates):
+    """gka_seq_blocked (solves batched over token blocks) == gka_seq token by token,
+    including a ragged last block and initial states."""
+    T, H, HKV, D = 37, 2, 1, 8
+    q, k, v, alpha, g, gk, beta = _inputs(T, H, HKV, D, 11, beta=gates, gk=gates)
+    g0 = torch.Generator().manual_seed(12)
+    kx = torch.randn(H, D, 3, generator=g0, dtype=D64)
+    h0kk = kx @ kx.transpose(-1, -2)
+    h0kv = torch.randn(H, D, D, generator=g0, dtype=D64) * 0.1
+    a = ref.gka_seq(q, k, v, alpha, g, gk, beta, 0.3, 0.02, num_iter, h0kk, h0kv)
+    b = ref.gka_seq_blocked(q, k, v, alpha, g, gk, beta, 0.3, 0.02, num_iter, h0kk, h0kv,
+                            block=block)
+    assert torch.allclose(a[0], b[0], rtol=1e-12, atol=1e-12)
+    if num_iter:
+        assert torch.allclose(a[1], b[1], rtol=1e-12, atol=1e-12)
+    else:
+        assert a[1] is None and b[1] is None
+    assert torch.allclose(a[2], b[2], rtol=1e-12, atol=1e-12)
+
+
 def test_state_passing_is_linear():
     T, H, D = 12, 2, 8
     q, k, v, alpha, g, gk, beta = _inputs(T, H, H, D, 6)
