@@ -41,6 +41,10 @@ SIGNATURES: dict[str, list] = {
                           _P, _I32, _I32, _I32, _I32, _I32, _I32, _F32,
                           _I32, _I32, _F32, _P, ctypes.c_size_t, _P, _P],
     "hmx_gdn_chunk_workspace_bytes": [_I32, _I32, _I32, _I32],
+    "hmx_gdn_chunk_fwd_noalloc": [_P, _I64, _P, _I64, _P, _I64, _I32, _P, _I32, _P, _I32, _P,
+                                  _P, _P, _I64, _I32, _P, _P,
+                                  _P, _I32, _I32, _I32, _I32, _I32, _I32, _F32,
+                                  _I32, _I32, _F32, _P, _P],
     "hmx_gka_gating": [_P, _I32, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I32, _P, _I32,
                        _P, _P, _P, _I32, _I64, _I32, _F32, _F32, _P],
     "hmx_gka_decode_fwd": [_P, _I64, _P, _I64, _P, _I64, _I32, _P, _I32, _P, _I32, _P, _I32, _P,

@@ -154,6 +154,31 @@ int hmx_gdn_chunk_fwd(const void* q, int64_t q_token_stride, const void* k,
                       void* workspace, size_t workspace_bytes, const hmx_gated_norm* o_norm,
                       void* stream);
 
+/*
+ * hmx_gdn_chunk_fwd without a workspace argument: the workspace is a static device
+ * array of HMX_GDN_CHUNK_SCRATCH_BYTES per device, and the call allocates nothing
+ * (no hipMalloc / hipFree, no allocating library routine).  Arguments and results
+ * as hmx_gdn_chunk_fwd.  Returns HMX_EINVAL when the segment table needs more
+ * workspace than the array holds (hmx_gdn_chunk_workspace_bytes > the limit).
+ * The array's address is looked up once per device, on the first call with that
+ * device current; later calls on the device reuse it.  The stream must belong to
+ * the current device.  Calls that overlap on one device share the array and race:
+ * serialise them (one stream, or events).
+ * No counterpart in the reference: for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid it).
+ */
+#define HMX_GDN_CHUNK_SCRATCH_BYTES (64u << 20)
+int hmx_gdn_chunk_fwd_noalloc(const void* q, int64_t q_token_stride, const void* k,
+                              int64_t k_token_stride, const void* v, int64_t v_token_stride,
+                              int32_t qkv_dtype, const void* g, int32_t g_dtype,
+                              const void* beta, int32_t beta_dtype, void* o, const void* h0,
+                              void* ht, int64_t state_slot_stride, int32_t state_dtype,
+                              const int32_t* state_indices, const uint8_t* has_initial_state,
+                              const int32_t* seg_table, int32_t nseg_total, int32_t N,
+                              int32_t H, int32_t HKV, int32_t K, int32_t V, float scale,
+                              int32_t use_qk_l2norm, int32_t max_warm_chunks,
+                              float decay_threshold, const hmx_gated_norm* o_norm, void* stream);
+
 /* Workspace bytes hmx_gdn_chunk_fwd needs for a given segment table (host-only
  * arithmetic); pooled != 0 when the call passes state_indices.  Companion of
  * hmx_gdn_chunk_fwd; no reference counterpart (the reference allocates its

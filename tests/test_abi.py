@@ -100,3 +100,15 @@ def test_ssd_scan_rejects_mismatched_operands():
         with pytest.raises(ValueError):
             _ssd_scan(**args)
 
+
+def test_noalloc_entry_rejects_oversized_table():
+    """hmx_gdn_chunk_fwd_noalloc refuses a segment table whose workspace exceeds its
+    static array, before touching the GPU."""
+    lib = _lib.load()
+    H, N, nseg = 64, 1, 64          # 3 * 64 * 64 * 64 KiB = 768 MiB of workspace
+    assert lib.hmx_gdn_chunk_workspace_bytes(nseg, N, H, 0) > (64 << 20)
+    with pytest.raises(ValueError, match="static scratch"):
+        _lib.call("hmx_gdn_chunk_fwd_noalloc", None, H * 128, None, H * 128, None, H * 128,
+                  _lib.HMX_BF16, None, _lib.HMX_F32, None, _lib.HMX_F32, None, None, None, 0,
+                  _lib.HMX_F32, None, None, None, nseg, N, H, H, 128, 128, 1.0, 1, 16, 60.0,
+                  None, None)
