@@ -12,7 +12,7 @@
 // Forming V_new from K S instead of W S needs no W: T is applied to the 32 x 32
 // right-hand side in registers, by blockwise substitution over its two 16-row
 // blocks (no merged T_10), with beta folded into T's columns (T' = T diag(beta))
-// and A_10 = diag(beta_1) M_10:
+// and A = diag(beta) M, M_ij = k_i.k_j e^{G_i-G_j} (j < i):
 //   V_new_0 = T'_00 Y_0,  V_new_1 = T'_11 (Y_1 - M_10 V_new_0),  Y = V - e^G K S.
 //
 // The chunk length is an internal choice (the result is the same recurrence at
@@ -41,13 +41,17 @@
 // Phase 2 forms V_new, O and the state update, then stages the next chunk into
 // the other of two LDS buffers.
 //
-// Numerics: MFMA operands are bf16 with fp32 accumulation.  k and q enter the
-// products raw (exact bf16 inputs); the L2 normalisation is applied as fp32 row
-// and column factors (A, P) and row factors (K S, Q S, the state update).  The
-// state enters K S as a bf16 hi + lo pair, and T, A_10 and the right-hand sides
-// of the substitution as hi/lo pairs (two MFMAs per product, see mm_hl), giving
-// ~fp32 accuracy where the state is sensitive; P, V_new in P V_new and the
-// state in Q S are bf16.
+// Numerics: every MFMA operand is fp16 (one round-to-nearest-even rounding) with
+// fp32 accumulation.  k and q enter as k_n = rk k and q_n = scale rq q with the
+// in-kernel L2 factors applied in fp32 before the rounding (|k_n|, |q_n| <= 1),
+// so no product needs row factors afterwards; the state, T, M_10, P and the
+// substitution right-hand sides are rounded from their fp32 accumulators.  fp16
+// keeps 11 significant bits where bf16 keeps 8: one rounding per operand gives
+// ~5e-4 relative state error, inside the 1e-3 bound, where bf16 needed hi + lo
+// pairs (two MFMAs and a split per product).  The range is fp16's: without
+// in-kernel normalisation |k|, |q| must stay below 65504, and so must the state
+// and V_new entries (they are O(|v|) for normalised keys).  The state is kept
+// exact in fp32 and decayed explicitly each chunk.
 //
 // Roofline: HBM-bound at the algorithmic minimum (q,k,v,o bf16 + g,beta +
 // final state); FLOPs 2*T*H*(5*C*d + 3*d^2).
@@ -64,23 +68,22 @@ constexpr int C = 32;          // chunk length (tokens)
 constexpr int MT = C / 16;     // 16-row tiles per chunk
 constexpr int D = 128;         // head dim (K == V == 128)
 constexpr int NTHR = 256;      // 4 waves
-constexpr int LDQ = D + 8;     // bf16 [C][128] row stride (q, k, v, O staging)
-constexpr int LDT = C + 8;     // bf16 [C][C] row stride (P, T/A hi/lo)
+constexpr int LDQ = D + 8;     // [C][128] row stride (k, q, v and O staging)
+constexpr int LDT = C + 8;     // [C][C] row stride (P, T blocks)
 static_assert(C == 32, "chunk length: the substitution and the g scan are written for 32");
 
 enum Mode { MODE_OUT = 0, MODE_S0 = 1, MODE_PHI = 2 };
 
-// shared-memory layout (bytes): two staging buffers (K, Q, V, per-token
-// scalars), the O staging tile, T/A hi and lo, P
+// shared-memory layout (bytes): two staging buffers (K, Q as normalised fp16,
+// V raw bf16, per-token scalars), the O staging tile, T/M blocks, P
 constexpr int SZ_Q = C * LDQ * 2;
-constexpr int SZ_SC = 9 * C * 4;                 // per-token scalars (see Stage)
+constexpr int SZ_SC = 4 * C * 4;                 // per-token scalars (see Stage)
 constexpr int SZ_BUF = 3 * SZ_Q + SZ_SC;
 constexpr int SZ_P = C * LDT * 2;
 constexpr int OFF_O = 2 * SZ_BUF;
-constexpr int OFF_TH = OFF_O + SZ_Q;   // rows 0-15: T_00 | rows 16-31: -A_10, T_11
-constexpr int OFF_TL = OFF_TH + SZ_P;
-constexpr int OFF_P = OFF_TL + SZ_P;
-constexpr int OFF_NW = OFF_P + SZ_P;        // fp32 [D] output-norm weight (NORM)
+constexpr int OFF_T = OFF_O + SZ_Q;    // rows 0-15: T'_00 | rows 16-31: -M_10, T'_11 (fp16)
+constexpr int OFF_P = OFF_T + SZ_P;    // P (fp16, lower triangle; the upper tile stays 0)
+constexpr int OFF_NW = OFF_P + SZ_P;   // fp32 [D] output-norm weight (NORM)
 constexpr int SMEM = OFF_NW + D * 4;
 static_assert(SMEM <= 80 * 1024, "LDS budget: two workgroups per CU");
 
@@ -181,31 +184,24 @@ __device__ __forceinline__ void load_raw(RawChunk& r, const Params& p, const bf1
   }
 }
 
-// One staged chunk in LDS: raw k, q, v rows and per-token scalars.  With
-// in-kernel L2 normalisation k_n = rk k and q_n = rq q; the row factors rk, rq
-// are applied to the products (A, P, K S, Q S, the state update) in fp32.
+// One staged chunk in LDS.  K and Q hold the rows as the products use them, in
+// fp16: k_n = rk k and q_n = scale rq q, with rk, rq the in-kernel L2
+// normalisation (1 without it); V holds the raw bf16 rows.
 struct Stage {
-  bf16* K; bf16* Q; bf16* V;
+  f16* K; f16* Q; bf16* V;
   float* G; float* B; float* EG; float* EDL;   // G, beta, e^G, e^{G_last-G}
-  float* RK; float* RQ;                        // rk, rq (1 without normalisation)
-  float* EGK; float* EGQ; float* EDLK;         // e^G rk, scale e^G rq, e^{G_last-G} rk
 };
 
 __device__ __forceinline__ Stage stage_at(unsigned char* smem, int bi) {
   unsigned char* b = smem + bi * SZ_BUF;
   Stage s;
-  s.K = reinterpret_cast<bf16*>(b);
-  s.Q = reinterpret_cast<bf16*>(b + SZ_Q);
+  s.K = reinterpret_cast<f16*>(b);
+  s.Q = reinterpret_cast<f16*>(b + SZ_Q);
   s.V = reinterpret_cast<bf16*>(b + 2 * SZ_Q);
   s.G = reinterpret_cast<float*>(b + 3 * SZ_Q);
   s.B = s.G + C;
   s.EG = s.B + C;
   s.EDL = s.EG + C;
-  s.RK = s.EDL + C;
-  s.RQ = s.RK + C;
-  s.EGK = s.RQ + C;
-  s.EGQ = s.EGK + C;
-  s.EDLK = s.EGQ + C;
   return s;
 }
 
@@ -221,11 +217,11 @@ __device__ __forceinline__ float row_inv_norm(const bf16x8& raw) {
 
 // Row factors of the prefetched rows (1 without in-kernel normalisation).
 template <int MODE>
-__device__ __forceinline__ void prep_rows(RawChunk& r, bool norm) {
+__device__ __forceinline__ void prep_rows(RawChunk& r, bool norm, float scale) {
 #pragma unroll
   for (int pass = 0; pass < MT; ++pass) {
     r.rk[pass] = norm ? row_inv_norm(r.k[pass]) : 1.f;
-    if (MODE == MODE_OUT) r.rq[pass] = norm ? row_inv_norm(r.q[pass]) : 1.f;
+    if (MODE == MODE_OUT) r.rq[pass] = (norm ? row_inv_norm(r.q[pass]) : 1.f) * scale;
   }
 }
 
@@ -239,6 +235,13 @@ __device__ __forceinline__ void prep_scan(RawChunk& r, int lane) {
   r.edl = fast_exp(glast - gv);
 }
 
+__device__ __forceinline__ f16x8 scale_h8(const bf16x8& x, float s) {
+  f16x8 y;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) y[j] = (f16)((float)x[j] * s);
+  return y;
+}
+
 // Write a prefetched, prepared chunk into staging buffer st.
 template <int MODE>
 __device__ __forceinline__ void stage_chunk(const Stage& st, const RawChunk& r, bool with_q,
@@ -247,13 +250,10 @@ __device__ __forceinline__ void stage_chunk(const Stage& st, const RawChunk& r, 
   for (int pass = 0; pass < MT; ++pass) {
     const int row = pass * 16 + (tid >> 4);
     const int f0 = (tid & 15) * 8;
-    *reinterpret_cast<bf16x8*>(st.K + row * LDQ + f0) = r.k[pass];
-    if ((tid & 15) == 0) st.RK[row] = r.rk[pass];
+    *reinterpret_cast<f16x8*>(st.K + row * LDQ + f0) = scale_h8(r.k[pass], r.rk[pass]);
     if (MODE != MODE_PHI) *reinterpret_cast<bf16x8*>(st.V + row * LDQ + f0) = r.v[pass];
-    if (MODE == MODE_OUT && with_q) {
-      *reinterpret_cast<bf16x8*>(st.Q + row * LDQ + f0) = r.q[pass];
-      if ((tid & 15) == 0) st.RQ[row] = r.rq[pass];
-    }
+    if (MODE == MODE_OUT && with_q)
+      *reinterpret_cast<f16x8*>(st.Q + row * LDQ + f0) = scale_h8(r.q[pass], r.rq[pass]);
   }
   if (wave == 0 && lane < C) {
     st.G[lane] = r.gs;
@@ -263,74 +263,29 @@ __device__ __forceinline__ void stage_chunk(const Stage& st, const RawChunk& r, 
   }
 }
 
-// ---------------------------------------------------------------------------
-// 16x16 products on bf16 hi + lo pairs (x ~= hi + lo, ~16 significant bits)
-// ---------------------------------------------------------------------------
-struct HL {
-  bf16x4 h, l;
-};
-
-__device__ __forceinline__ HL split_hl(const f32x4& x) {
-  bf16x2 h0, h1, l0, l1;
-  split2(x[0], x[1], h0, l0);
-  split2(x[2], x[3], h1, l1);
-  return HL{bf16x4{h0[0], h0[1], h1[0], h1[1]}, bf16x4{l0[0], l0[1], l1[0], l1[1]}};
-}
-
-// acc + X.Y from X^T and Y in C layout: lane (q, l16) holds X[l16][4q..4q+3]
-// (= its X^T values) and Y[4q..4q+3][l16], so the A operand {Xh, Xl} and the B
-// operands {Yh, Yh}, {Yl, Yl} agree on k; two MFMAs give (Xh + Xl)(Yh + Yl).
-__device__ __forceinline__ f32x4 mm_ct(const HL& xt, const HL& y, f32x4 acc) {
-  const bf16x8 a = {xt.h[0], xt.h[1], xt.h[2], xt.h[3], xt.l[0], xt.l[1], xt.l[2], xt.l[3]};
-  acc = mfma16(a, bf16x8{y.h[0], y.h[1], y.h[2], y.h[3], y.h[0], y.h[1], y.h[2], y.h[3]}, acc);
-  return mfma16(a, bf16x8{y.l[0], y.l[1], y.l[2], y.l[3], y.l[0], y.l[1], y.l[2], y.l[3]}, acc);
-}
-
 // (I + A)^-1 of a strictly-lower 16x16 block held in C layout (A) together
 // with its transpose (At), by the exact identity for nilpotent A (A^16 = 0):
 //   (I + A)^-1 = (I + A^8)(I + A^4)(I + A^2)(I - A)
-// (the factors commute).  Left operands enter transposed, so the chain forms
-// A^2, A^4 and their transposes, then (A^8)^T = (A^4)^T (A^4)^T.
+// (the factors commute).  Each product X.Y is one 16x16x16 fp16 MFMA on the C
+// layout of X^T and of Y, so the chain forms A^2, A^4 and their transposes, then
+// (A^8)^T = (A^4)^T (A^4)^T.
 __device__ __forceinline__ f32x4 inv_unit_lower16(const f32x4& A, const f32x4& At, int q4, int l16) {
   const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-  const HL a = split_hl(A), at = split_hl(At);
-  const f32x4 A2 = mm_ct(at, a, z), A2t = mm_ct(a, at, z);
-  const HL a2 = split_hl(A2), a2t = split_hl(A2t);
-  const f32x4 A4 = mm_ct(a2t, a2, z), A4t = mm_ct(a2, a2t, z);
-  const HL a4 = split_hl(A4), a4t = split_hl(A4t);
-  const HL a8t = split_hl(mm_ct(a4, a4t, z));
+  const f16x4 a = h4(A), at = h4(At);
+  const f16x4 a2 = h4(mfma16h_k16(at, a, z)), a2t = h4(mfma16h_k16(a, at, z));
+  const f16x4 a4 = h4(mfma16h_k16(a2t, a2, z)), a4t = h4(mfma16h_k16(a2, a2t, z));
+  const f16x4 a8t = h4(mfma16h_k16(a4, a4t, z));
   f32x4 R;
 #pragma unroll
   for (int v = 0; v < 4; ++v) R[v] = ((4 * q4 + v == l16) ? 1.f : 0.f) - A[v];
-  R = mm_ct(a2t, split_hl(R), R);
-  R = mm_ct(a4t, split_hl(R), R);
-  return mm_ct(a8t, split_hl(R), R);
+  R = mfma16h_k16(a2t, h4(R), R);
+  R = mfma16h_k16(a4t, h4(R), R);
+  return mfma16h_k16(a8t, h4(R), R);
 }
 
-// 16x16 blocks kept in LDS as hi/lo pairs
-__device__ __forceinline__ void put_hl(bf16* hi, bf16* lo, int r, int c, float x) {
-  const bf16 h = (bf16)x;
-  hi[r * LDT + c] = h;
-  lo[r * LDT + c] = (bf16)(x - (float)h);
-}
-
-// A operand of the 16x16 block at (r0, c0) of a hi/lo pair: lane (q, l16) holds
-// row r0+l16, columns c0+4q..c0+4q+3 of hi, then the same of lo.  Paired with a
-// B operand {y[0..3], y[0..3]} built from a C-layout tile (rows 4q..4q+3), one
-// 16x16x32 MFMA forms hi.Y + lo.Y.
-__device__ __forceinline__ bf16x8 ld_hl(const bf16* hi, const bf16* lo, int r0, int c0, int lane) {
-  const int off = (r0 + (lane & 15)) * LDT + c0 + 4 * (lane >> 4);
-  const bf16x4 a = *reinterpret_cast<const bf16x4*>(hi + off);
-  const bf16x4 b = *reinterpret_cast<const bf16x4*>(lo + off);
-  return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-}
-
-// acc + X.Y for a hi/lo block X (from ld_hl) and a C-layout fp32 tile Y split
-// into hi/lo: two MFMAs, (Xh + Xl)(Yh + Yl).
-__device__ __forceinline__ f32x4 mm_hl(const bf16x8& xa, const f32x4& y, f32x4 acc) {
-  const HL s = split_hl(y);
-  acc = mfma16(xa, bf16x8{s.h[0], s.h[1], s.h[2], s.h[3], s.h[0], s.h[1], s.h[2], s.h[3]}, acc);
-  return mfma16(xa, bf16x8{s.l[0], s.l[1], s.l[2], s.l[3], s.l[0], s.l[1], s.l[2], s.l[3]}, acc);
+// A operand (16x16x16) of the 16x16 block at (r0, c0) of an fp16 [C][LDT] matrix
+__device__ __forceinline__ f16x4 ld_blk(const f16* m, int r0, int c0, int lane) {
+  return *reinterpret_cast<const f16x4*>(m + (r0 + (lane & 15)) * LDT + c0 + 4 * (lane >> 4));
 }
 
 // ---------------------------------------------------------------------------
@@ -342,9 +297,8 @@ template <int MODE, bool NORM = false>
 __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
   __shared__ __align__(16) unsigned char smem[SMEM];
   bf16* sO = reinterpret_cast<bf16*>(smem + OFF_O);
-  bf16* sTh = reinterpret_cast<bf16*>(smem + OFF_TH);
-  bf16* sTl = reinterpret_cast<bf16*>(smem + OFF_TL);
-  bf16* sP = reinterpret_cast<bf16*>(smem + OFF_P);
+  f16* sT = reinterpret_cast<f16*>(smem + OFF_T);
+  f16* sP = reinterpret_cast<f16*>(smem + OFF_P);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int q4 = lane >> 4, l16 = lane & 15;
@@ -423,7 +377,7 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
 
   // P's strictly-upper 16x16 tile is never written by phase 1: zero it once.
   if (MODE == MODE_OUT) {
-    for (int i = tid; i < 16 * 16; i += NTHR) sP[(i >> 4) * LDT + 16 + (i & 15)] = (bf16)0.f;
+    for (int i = tid; i < 16 * 16; i += NTHR) sP[(i >> 4) * LDT + 16 + (i & 15)] = (f16)0.f;
   }
 
   const int64_t o_rs = (int64_t)H * D;
@@ -496,19 +450,13 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
     reinterpret_cast<float*>(smem + OFF_NW)[tid] = wv;
   }
 
-  // The state is kept as S / gam with a running scalar gam (the product of the
-  // chunk decays e^{G_last} since the last renormalisation): the decay then costs
-  // per-token factors instead of a multiply of every state element per chunk.
-  float gam = 1.f;
-  if (c_begin >= si.c_end) {
-    // nothing to scan (empty segment): only the end state below
-  } else {
+  if (c_begin < si.c_end) {
     RawChunk raw;
     {
       const int t0 = si.bos + c_begin * C;
       load_raw<MODE>(raw, p, qh, kh, vh, t0, min(C, si.eos - t0), c_begin >= c_out,
                      tid, h);
-      prep_rows<MODE>(raw, p.l2norm);
+      prep_rows<MODE>(raw, p.l2norm, p.scale);
       if (wave == 0) prep_scan(raw, lane);
       stage_chunk<MODE>(stage_at(smem, 0), raw, c_begin >= c_out, tid, wave, lane);
       if (c_begin + 1 < si.c_end) {
@@ -524,51 +472,43 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
       const Stage cur = stage_at(smem, bi);
       const int tok0 = si.bos + c * C;
       const bool out_chunk = (MODE == MODE_OUT) && (c >= c_out);
-      // gam after this chunk; renormalise (fold gam into the state) before 1/gam
-      // could overflow the update weights
-      const float graw = gam * cur.EG[C - 1];
-      const bool renorm = graw < 0x1p-60f;
-      const float gnext = renorm ? 1.f : graw;
 
-      // ---- phase 1: T blocks / P; K S and Q S; store the previous chunk's O ----
+      // ---- phase 1: T blocks / P; K S and (Q S)^T; store the previous chunk's O ----
       bf16x8 zr[MT];
       if (MODE == MODE_OUT && c > c_out) {
         if constexpr (NORM) load_gate(zr, tok0 - C, C);   // stored at the end of phase 1
         else store_o(tok0 - C, C);
       }
 
-      f32x4 X[MT][2], QS[MT][2];
+      // X[mt][ct] = (K S) tile (tokens 16mt.., state cols 32w+16ct..);
+      // QT[ct][mt] = (Q S)^T tile (state cols 32w+16ct.., tokens 16mt..)
+      f32x4 X[MT][2], QT[2][MT];
       auto phase1 = [&](auto role_c, auto outq_c) {
         constexpr int R = decltype(role_c)::value;
         constexpr bool OQ = decltype(outq_c)::value;
         if constexpr (R < MT) {
-          // A strip R: off-diagonal tile -> -A_10 (hi/lo), diagonal tile -> T_RR (hi/lo)
-          bf16x8 af[4];
+          // A strip R: off-diagonal tile -> -M_10, diagonal tile -> T'_RR (fp16 into sT)
+          f16x8 af[4];
 #pragma unroll
-          for (int ks = 0; ks < 4; ++ks) af[ks] = frag(cur.K, LDQ, 16 * R, 32 * ks, lane);
-          float gr[4], br[4], kr[4];
+          for (int ks = 0; ks < 4; ++ks) af[ks] = frag_h(cur.K, LDQ, 16 * R, 32 * ks, lane);
+          float gr[4], br[4];
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
             gr[v] = cur.G[16 * R + 4 * q4 + v];
-            kr[v] = cur.RK[16 * R + 4 * q4 + v];
-            br[v] = cur.B[16 * R + 4 * q4 + v] * kr[v];
+            br[v] = cur.B[16 * R + 4 * q4 + v];
           }
 #pragma unroll
           for (int j = 0; j <= R; ++j) {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks)
-              acc = mfma16(af[ks], frag(cur.K, LDQ, 16 * j, 32 * ks, lane), acc);
+              acc = mfma16h(af[ks], frag_h(cur.K, LDQ, 16 * j, 32 * ks, lane), acc);
             const int col = 16 * j + l16;
             const float gc = cur.G[col];
-            const float kc = cur.RK[col];
-#pragma unroll
-            for (int v = 0; v < 4; ++v) acc[v] *= kc;   // normalised k_r.k_c = kr kc (k_r.k_c)
             if (j < R) {
 #pragma unroll
               for (int v = 0; v < 4; ++v)
-                put_hl(sTh, sTl, 16 * R + 4 * q4 + v, col,
-                       -kr[v] * acc[v] * fast_exp(gr[v] - gc));
+                sT[(16 * R + 4 * q4 + v) * LDT + col] = (f16)(-acc[v] * fast_exp(gr[v] - gc));
             } else {
               // A and A^T of the diagonal tile in C layout (k.k^T is symmetric)
               const float bc = cur.B[col];
@@ -576,83 +516,69 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
 #pragma unroll
               for (int v = 0; v < 4; ++v) {
                 const int row = 16 * R + 4 * q4 + v;
-                Ad[v] = row > col ? br[v] * acc[v] * fast_exp(gr[v] - gc) : 0.f;
-                At_[v] = col > row ? bc * kr[v] * acc[v] * fast_exp(gc - gr[v]) : 0.f;
+                const float d = gr[v] - gc;
+                const float e = acc[v] * fast_exp(row > col ? d : -d);
+                Ad[v] = row > col ? br[v] * e : 0.f;
+                At_[v] = col > row ? bc * e : 0.f;
               }
               const f32x4 Tii = inv_unit_lower16(Ad, At_, q4, l16);
 #pragma unroll
-              for (int v = 0; v < 4; ++v) put_hl(sTh, sTl, 16 * R + 4 * q4 + v, col, Tii[v] * bc);
+              for (int v = 0; v < 4; ++v) sT[(16 * R + 4 * q4 + v) * LDT + col] = (f16)(Tii[v] * bc);
             }
           }
         } else if constexpr (OQ) {
-          // P strip i = R - MT: q_r.k_c e^{G_r-G_c} for c <= r
+          // P strip i = R - MT: q_n,r . k_n,c e^{G_r-G_c} for c <= r (scale is in q_n)
           constexpr int i = R - MT;
-          bf16x8 af[4];
+          f16x8 af[4];
 #pragma unroll
-          for (int ks = 0; ks < 4; ++ks) af[ks] = frag(cur.Q, LDQ, 16 * i, 32 * ks, lane);
-          float gr[4], qr[4];
+          for (int ks = 0; ks < 4; ++ks) af[ks] = frag_h(cur.Q, LDQ, 16 * i, 32 * ks, lane);
+          float gr[4];
 #pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            gr[v] = cur.G[16 * i + 4 * q4 + v];
-            qr[v] = cur.RQ[16 * i + 4 * q4 + v] * p.scale;
-          }
+          for (int v = 0; v < 4; ++v) gr[v] = cur.G[16 * i + 4 * q4 + v];
 #pragma unroll
           for (int j = 0; j <= i; ++j) {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks)
-              acc = mfma16(af[ks], frag(cur.K, LDQ, 16 * j, 32 * ks, lane), acc);
+              acc = mfma16h(af[ks], frag_h(cur.K, LDQ, 16 * j, 32 * ks, lane), acc);
             const int col = 16 * j + l16;
             const float gc = cur.G[col];
-            const float kc = cur.RK[col];
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
               const int row = 16 * i + 4 * q4 + v;
-              const float dcy = (row >= col) ? qr[v] * kc * fast_exp(gr[v] - gc) : 0.f;
-              sP[row * LDT + col] = (bf16)(acc[v] * dcy);
+              sP[row * LDT + col] = (f16)((row >= col) ? acc[v] * fast_exp(gr[v] - gc) : 0.f);
             }
           }
         }
-        if constexpr (R == MT) {
-          // per-token factors of phase 2 (k and q row norms folded in)
-          if (lane < C) {
-            const float eg = cur.EG[lane] * gam, rk = cur.RK[lane];
-            cur.EGK[lane] = eg * rk;
-            cur.EDLK[lane] = cur.EDL[lane] * rk / gnext;
-            if constexpr (OQ) cur.EGQ[lane] = eg * cur.RQ[lane] * p.scale;
-          }
-        }
-        // K S (state as hi + lo) and Q S (state as bf16) for this wave's columns
+        // K S and (Q S)^T for this wave's columns; one fp16 copy of the state
+        // serves as the B operand of K S and the A operand of (Q S)^T
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
           for (int ct = 0; ct < 2; ++ct) {
             X[mt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-            QS[mt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+            QT[ct][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
           }
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-          bf16x8 Sh[2], Sl[2];
+          f16x8 Sb[2];
 #pragma unroll
-          for (int ct = 0; ct < 2; ++ct) pack_b_hilo(S[2 * ks][ct], S[2 * ks + 1][ct], Sh[ct], Sl[ct]);
+          for (int ct = 0; ct < 2; ++ct) Sb[ct] = h8(S[2 * ks][ct], S[2 * ks + 1][ct]);
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) {
-            const bf16x8 a = frag_perm(cur.K, LDQ, 16 * mt, 32 * ks, lane);
+            const f16x8 a = frag_perm_h(cur.K, LDQ, 16 * mt, 32 * ks, lane);
 #pragma unroll
-            for (int ct = 0; ct < 2; ++ct) {
-              X[mt][ct] = mfma16(a, Sh[ct], X[mt][ct]);
-              X[mt][ct] = mfma16(a, Sl[ct], X[mt][ct]);
-            }
+            for (int ct = 0; ct < 2; ++ct) X[mt][ct] = mfma16h(a, Sb[ct], X[mt][ct]);
             if constexpr (OQ) {
-              const bf16x8 aq = frag_perm(cur.Q, LDQ, 16 * mt, 32 * ks, lane);
+              const f16x8 bq = frag_perm_h(cur.Q, LDQ, 16 * mt, 32 * ks, lane);
 #pragma unroll
-              for (int ct = 0; ct < 2; ++ct) QS[mt][ct] = mfma16(aq, Sh[ct], QS[mt][ct]);
+              for (int ct = 0; ct < 2; ++ct) QT[ct][mt] = mfma16h(Sb[ct], bq, QT[ct][mt]);
             }
           }
         }
         // the next chunk's row factors and g scan (its rows are in registers;
         // unused values when this is the segment's last chunk)
-        prep_rows<MODE>(raw, p.l2norm);
+        prep_rows<MODE>(raw, p.l2norm, p.scale);
         if constexpr (R == 0) prep_scan(raw, lane);
       };
       using I0 = std::integral_constant<int, 0>;
@@ -678,7 +604,7 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
       lds_barrier();
 
       __builtin_amdgcn_s_setprio(1);
-      // ---- phase 2: Y = beta (V - e^G K S); V_new by blockwise substitution --------
+      // ---- phase 2: Y = V - e^G K S; V_new by blockwise substitution --------------
       f32x4 Vn[MT][2];
       {
         f32x4 Y[MT][2];
@@ -689,76 +615,73 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
             bf16x4 vt = {};
             if (MODE != MODE_PHI) vt = ld_tr(cur.V, LDQ, 16 * mt + 4 * q4, 32 * wave + 16 * ct, lane);
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-              const int r = 16 * mt + 4 * q4 + v;
-              Y[mt][ct][v] = (float)vt[v] - cur.EGK[r] * X[mt][ct][v];
-            }
+            for (int v = 0; v < 4; ++v)
+              Y[mt][ct][v] = (float)vt[v] - cur.EG[16 * mt + 4 * q4 + v] * X[mt][ct][v];
           }
-        const bf16x8 t00 = ld_hl(sTh, sTl, 0, 0, lane);
-        const bf16x8 na10 = ld_hl(sTh, sTl, 16, 0, lane);
-        const bf16x8 t11 = ld_hl(sTh, sTl, 16, 16, lane);
+        const f16x4 t00 = ld_blk(sT, 0, 0, lane);
+        const f16x4 nm10 = ld_blk(sT, 16, 0, lane);
+        const f16x4 t11 = ld_blk(sT, 16, 16, lane);
         const f32x4 z = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) {
-          Vn[0][ct] = mm_hl(t00, Y[0][ct], z);
-          const f32x4 r1 = mm_hl(na10, Vn[0][ct], Y[1][ct]);
-          Vn[1][ct] = mm_hl(t11, r1, z);
+          Vn[0][ct] = mfma16h_k16(t00, h4(Y[0][ct]), z);
+          const f32x4 r1 = mfma16h_k16(nm10, h4(Vn[0][ct]), Y[1][ct]);
+          Vn[1][ct] = mfma16h_k16(t11, h4(r1), z);
         }
       }
 
-      // ---- O = scale [e^G (Q S) + P V_new] -> sO ----------------------------------
+      // ---- O^T = e^G (Q S)^T + V_new^T P^T -> sO (4 features of a token per lane) ----
       if (out_chunk) {
-        bf16x8 Vb[2];
+        f16x8 Va[2];
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct) Vb[ct] = pack_b(Vn[0][ct], Vn[1][ct]);
+        for (int ct = 0; ct < 2; ++ct) Va[ct] = h8(Vn[0][ct], Vn[1][ct]);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          f32x4 O[2];
+          const f16x8 bp = frag_perm_h(sP, LDT, 16 * mt, 0, lane);
+          const float eg = cur.EG[16 * mt + l16];
+#pragma unroll
+          for (int ct = 0; ct < 2; ++ct) {
+            f32x4 O;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) O[v] = QT[ct][mt][v] * eg;
+            O = mfma16h(Va[ct], bp, O);
+            *reinterpret_cast<bf16x4*>(sO + (16 * mt + l16) * LDQ + 32 * wave + 16 * ct + 4 * q4) =
+                bf16x4{(bf16)O[0], (bf16)O[1], (bf16)O[2], (bf16)O[3]};
+          }
+        }
+      }
+
+      // ---- S <- e^{G_last} S + K_n^T (e^{G_last-G} V_new) --------------------------
+      {
+        const float egl = cur.EG[C - 1];
+#pragma unroll
+        for (int rt = 0; rt < 8; ++rt)
 #pragma unroll
           for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) O[ct][v] = QS[mt][ct][v] * cur.EGQ[16 * mt + 4 * q4 + v];
-          const bf16x8 a = frag_perm(sP, LDT, 16 * mt, 0, lane);
+            for (int v = 0; v < 4; ++v) S[rt][ct][v] *= egl;
+        float e0[4], e1[4];
 #pragma unroll
-          for (int ct = 0; ct < 2; ++ct) {
-            O[ct] = mfma16(a, Vb[ct], O[ct]);
-#pragma unroll
-            for (int v = 0; v < 4; ++v)
-              sO[(16 * mt + 4 * q4 + v) * LDQ + 32 * wave + 16 * ct + l16] =
-                  (bf16)O[ct][v];
-          }
+        for (int v = 0; v < 4; ++v) {
+          e0[v] = cur.EDL[4 * q4 + v];
+          e1[v] = cur.EDL[16 + 4 * q4 + v];
         }
-      }
-
-      // ---- S <- e^{G_last} S + K^T (e^{G_last-G} V_new), V_new as hi/lo ----------
-      {
-        if (renorm) {
+        f16x8 Wb[2];
 #pragma unroll
-          for (int rt = 0; rt < 8; ++rt)
-#pragma unroll
-            for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-              for (int v = 0; v < 4; ++v) S[rt][ct][v] *= graw;
-        }
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
+        for (int ct = 0; ct < 2; ++ct) {
+          f32x4 w0, w1;
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
-            const float e = cur.EDLK[16 * mt + 4 * q4 + v];
-            Vn[mt][0][v] *= e;
-            Vn[mt][1][v] *= e;
+            w0[v] = Vn[0][ct][v] * e0[v];
+            w1[v] = Vn[1][ct][v] * e1[v];
           }
-        bf16x8 Vh[2], Vl[2];
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) pack_b_hilo(Vn[0][ct], Vn[1][ct], Vh[ct], Vl[ct]);
+          Wb[ct] = h8(w0, w1);
+        }
 #pragma unroll
         for (int rt = 0; rt < 8; ++rt) {
-          const bf16x8 a = frag_t_perm(cur.K, LDQ, 0, 16 * rt, lane);
+          const f16x8 a = frag_t_perm_h(cur.K, LDQ, 0, 16 * rt, lane);
 #pragma unroll
-          for (int ct = 0; ct < 2; ++ct) {
-            S[rt][ct] = mfma16(a, Vh[ct], S[rt][ct]);
-            S[rt][ct] = mfma16(a, Vl[ct], S[rt][ct]);
-          }
+          for (int ct = 0; ct < 2; ++ct) S[rt][ct] = mfma16h(a, Wb[ct], S[rt][ct]);
         }
       }
       __builtin_amdgcn_s_setprio(0);
@@ -772,7 +695,6 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
                          c + 2 >= c_out, tid, h);
         }
       }
-      gam = gnext;
       lds_barrier();
     }
     if (MODE == MODE_OUT && si.c_end > c_out) {
@@ -813,8 +735,8 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int i = (16 * rt + 4 * q4 + v) * D + 32 * wave + 16 * ct + l16;
-          if (dst) dst[i] = S[rt][ct][v] * gam;
-          else dst16[i] = (bf16)(S[rt][ct][v] * gam);
+          if (dst) dst[i] = S[rt][ct][v];
+          else dst16[i] = (bf16)S[rt][ct][v];
         }
   }
 }

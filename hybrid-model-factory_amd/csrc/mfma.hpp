@@ -130,6 +130,61 @@ __device__ __forceinline__ float scan32(float x) {
 }
 #undef HMX_DPP_F
 
+// ---------------------------------------------------------------------------
+// fp16 operands (v_mfma_f32_16x16x32_f16 / 16x16x16f16, v_cvt_pk_f16_f32): the
+// same fragment layouts as the bf16 helpers above, for 16-bit elements.
+// ---------------------------------------------------------------------------
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4 mfma16h(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// 16x16x16: lane (q, l16) holds A[l16][4q..4q+3] and B[4q..4q+3][l16] - the C/D
+// layout of a tile of A^T and of B, so C-layout tiles feed it directly.
+__device__ __forceinline__ f32x4 mfma16h_k16(f16x4 a, f16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+// round-to-nearest-even fp16 of a C-layout tile (two v_cvt_pk_f16_f32)
+__device__ __forceinline__ f16x4 h4(const f32x4& x) {
+  return f16x4{(f16)x[0], (f16)x[1], (f16)x[2], (f16)x[3]};
+}
+
+// operand from two vertically stacked C-layout tiles (k = 4q+v, then 16+4q+v)
+__device__ __forceinline__ f16x8 h8(const f32x4& t0, const f32x4& t1) {
+  return f16x8{(f16)t0[0], (f16)t0[1], (f16)t0[2], (f16)t0[3],
+               (f16)t1[0], (f16)t1[1], (f16)t1[2], (f16)t1[3]};
+}
+
+template <typename T>
+__device__ __forceinline__ f16x8 frag_h(const T* base, int ld, int r0, int k0, int lane) {
+  return *reinterpret_cast<const f16x8*>(base + (r0 + (lane & 15)) * ld + k0 + 8 * (lane >> 4));
+}
+
+__device__ __forceinline__ f16x8 frag_perm_h(const f16* base, int ld, int r0, int k0, int lane) {
+  const f16* p = base + (r0 + (lane & 15)) * ld + k0 + 4 * (lane >> 4);
+  const f16x4 a = *reinterpret_cast<const f16x4*>(p);
+  const f16x4 b = *reinterpret_cast<const f16x4*>(p + 16);
+  return f16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+__device__ __forceinline__ f16x4 ld_tr_h(const f16* base, int ld, int t0, int c0, int lane) {
+  const int s = lane & 15;
+  const f16* a = base + (t0 + (s >> 2)) * ld + c0 + 4 * (s & 3);
+  const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(a));
+  return __builtin_bit_cast(f16x4, r);
+}
+
+__device__ __forceinline__ f16x8 frag_t_perm_h(const f16* base, int ld, int t0, int c0, int lane) {
+  const int tq = t0 + 4 * (lane >> 4);
+  const f16x4 a = ld_tr_h(base, ld, tq, c0, lane);
+  const f16x4 b = ld_tr_h(base, ld, tq + 16, c0, lane);
+  return f16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
 // Workgroup barrier that orders LDS only: global loads issued before it stay in
 // flight (the next chunk's prefetch), unlike __syncthreads().
 __device__ __forceinline__ void lds_barrier() {
