@@ -33,31 +33,28 @@ HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 
 
-def _device_warmup(dev, seconds=0.5):
-    """Untimed: keep the GPU busy (matrix products and a 512 MiB copy) for about
-    ``seconds``, so it is in its loaded power state when a leg's warm-up steps
-    start.  The chip leaves that state within about a second of light load (input
-    generation is enough): a kernel trace of 20-call blocks of the C1 prefill
-    after input generation shows its main kernel at 474 us in the first block,
-    415 us in the second and 381-388 us from the fourth on, and the same again
-    after 2 s idle; with this warm-up right before the leg, the first block is
-    already within 3% of the later ones."""
+def _steady_state(fn, seconds=0.3, min_calls=3):
+    """Untimed: run the leg's own step back to back for about ``seconds`` so the
+    chip settles into the clock and power state of that op before the timed
+    steps.  Without it the first calls run at the idle state's clocks (after
+    input generation the C1 prefill's first 20 calls took 474 us against 381 us
+    later); a warm-up on another workload (dense GEMMs) leaves the power state of
+    that workload instead, which measured 25% slower for the prefill than its own
+    steady state."""
     import torch
-    a = torch.randn(4096, 4096, device=dev, dtype=torch.bfloat16)
-    src = torch.empty(256 << 20, device=dev, dtype=torch.bfloat16)
-    dst = torch.empty_like(src)
     t0 = time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        for _ in range(8):
-            a = (a @ a).clamp_(-1, 1)
-            dst.copy_(src)
-        torch.cuda.synchronize()
-    del a, src, dst
+    n = 0
+    while n < min_calls or time.perf_counter() - t0 < seconds:
+        fn()
+        n += 1
+        if n % 8 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
 
 
 def _timed(fn, steps, warmup, stream=None):
     import torch
-    _device_warmup(torch.device("cuda", torch.cuda.current_device()))
+    _steady_state(fn)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()

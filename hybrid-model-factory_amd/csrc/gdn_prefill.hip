@@ -68,7 +68,10 @@ constexpr int C = 32;          // chunk length (tokens)
 constexpr int MT = C / 16;     // 16-row tiles per chunk
 constexpr int D = 128;         // head dim (K == V == 128)
 constexpr int NTHR = 256;      // 4 waves
-constexpr int LDQ = D + 8;     // [C][128] row stride (k, q, v and O staging)
+// [C][128] row stride (k, q, v and O staging): 76 dwords = 12 mod 64 banks, so
+// the 16-row fragment reads (b128 / b64) and the 4-row transposing reads
+// (ds_read_b64_tr_b16) all hit distinct banks
+constexpr int LDQ = D + 24;
 constexpr int LDT = C + 8;     // [C][C] row stride (P, T blocks)
 static_assert(C == 32, "chunk length: the substitution and the g scan are written for 32");
 
@@ -131,6 +134,19 @@ __device__ __forceinline__ float ld_scalar(const void* p, int64_t i, int dt) {
   return (float)static_cast<const f16*>(p)[i];
 }
 
+// The element's bits, zero-extended (no conversion: a conversion right after the
+// load would make the wave wait for it, and for every load issued before it).
+__device__ __forceinline__ uint32_t ld_bits(const void* p, int64_t i, int dt) {
+  if (dt == HMX_F32) return static_cast<const uint32_t*>(p)[i];
+  return static_cast<const uint16_t*>(p)[i];
+}
+
+__device__ __forceinline__ float bits_f32(uint32_t b, int dt) {
+  if (dt == HMX_F32) return __builtin_bit_cast(float, b);
+  if (dt == HMX_BF16) return __builtin_bit_cast(float, b << 16);
+  return (float)__builtin_bit_cast(f16, (uint16_t)b);
+}
+
 __device__ __forceinline__ SegInfo load_seg(const int* seg, int s) {
   const int* r = seg + s * 8;
   return SegInfo{r[0], r[1], r[2], r[3], r[4], r[5], r[6], r[7]};
@@ -151,7 +167,7 @@ __device__ __forceinline__ bool seq_exact(const int* plan, const SegInfo& si, in
 // e^{G_last-G}, formed while the current chunk's MFMA work runs (prep_*).
 struct RawChunk {
   bf16x8 k[MT], v[MT], q[MT];
-  float g, b;
+  uint32_t gb, bb;              // g, beta as loaded (converted in prep_scan)
   float rk[MT], rq[MT];
   float gs, eg, edl;
 };
@@ -173,14 +189,12 @@ __device__ __forceinline__ void load_raw(RawChunk& r, const Params& p, const bf1
       r.q[pass] = (ok && need_q) ? *reinterpret_cast<const bf16x8*>(qh + tok * p.q_ts + f0)
                                  : bf16x8{};
   }
-  if (tid < C) {
-    const bool ok = tid < nval;
+  r.gb = 0u;
+  r.bb = 0u;
+  if (tid < nval && tid < C) {
     const int64_t gi = (int64_t)(tok0 + tid) * p.H + h;
-    r.g = ok ? ld_scalar(p.g, gi, p.g_dt) : 0.f;
-    r.b = ok ? ld_scalar(p.beta, gi, p.beta_dt) : 0.f;
-  } else {
-    r.g = 0.f;
-    r.b = 0.f;
+    r.gb = ld_bits(p.g, gi, p.g_dt);
+    r.bb = ld_bits(p.beta, gi, p.beta_dt);
   }
 }
 
@@ -226,8 +240,8 @@ __device__ __forceinline__ void prep_rows(RawChunk& r, bool norm, float scale) {
 }
 
 // In-chunk cumsum of g and the decay factors (wave 0; lanes 0-31 = tokens).
-__device__ __forceinline__ void prep_scan(RawChunk& r, int lane) {
-  const float gv = scan32(lane < C ? r.g : 0.f);
+__device__ __forceinline__ void prep_scan(RawChunk& r, int lane, int g_dt) {
+  const float gv = scan32(lane < C ? bits_f32(r.gb, g_dt) : 0.f);
   const float glast = __builtin_bit_cast(
       float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gv), C - 1));
   r.gs = gv;
@@ -245,7 +259,7 @@ __device__ __forceinline__ f16x8 scale_h8(const bf16x8& x, float s) {
 // Write a prefetched, prepared chunk into staging buffer st.
 template <int MODE>
 __device__ __forceinline__ void stage_chunk(const Stage& st, const RawChunk& r, bool with_q,
-                                            int tid, int wave, int lane) {
+                                            int tid, int wave, int lane, int beta_dt) {
 #pragma unroll
   for (int pass = 0; pass < MT; ++pass) {
     const int row = pass * 16 + (tid >> 4);
@@ -257,30 +271,37 @@ __device__ __forceinline__ void stage_chunk(const Stage& st, const RawChunk& r, 
   }
   if (wave == 0 && lane < C) {
     st.G[lane] = r.gs;
-    st.B[lane] = r.b;
+    st.B[lane] = bits_f32(r.bb, beta_dt);
     st.EG[lane] = r.eg;
     st.EDL[lane] = r.edl;
   }
 }
 
-// (I + A)^-1 of a strictly-lower 16x16 block held in C layout (A) together
+// ((I + A)^-1)^T of a strictly-lower 16x16 block held in C layout (A) together
 // with its transpose (At), by the exact identity for nilpotent A (A^16 = 0):
-//   (I + A)^-1 = (I + A^8)(I + A^4)(I + A^2)(I - A)
+//   ((I + A)^-1)^T = (I + (A^8)^T)(I + (A^4)^T)(I + (A^2)^T)(I - A^T)
 // (the factors commute).  Each product X.Y is one 16x16x16 fp16 MFMA on the C
-// layout of X^T and of Y, so the chain forms A^2, A^4 and their transposes, then
-// (A^8)^T = (A^4)^T (A^4)^T.
-__device__ __forceinline__ f32x4 inv_unit_lower16(const f32x4& A, const f32x4& At, int q4, int l16) {
+// layout of X^T and of Y, so the chain forms A^2, A^4, A^8 and (A^2)^T, (A^4)^T.
+// The result in C layout gives each lane 4 consecutive columns of one row of
+// (I + A)^-1.
+__device__ __forceinline__ f32x4 inv_unit_lower16_t(const f32x4& A, const f32x4& At, int q4,
+                                                    int l16) {
   const f32x4 z = {0.f, 0.f, 0.f, 0.f};
   const f16x4 a = h4(A), at = h4(At);
   const f16x4 a2 = h4(mfma16h_k16(at, a, z)), a2t = h4(mfma16h_k16(a, at, z));
   const f16x4 a4 = h4(mfma16h_k16(a2t, a2, z)), a4t = h4(mfma16h_k16(a2, a2t, z));
-  const f16x4 a8t = h4(mfma16h_k16(a4, a4t, z));
+  const f16x4 a8 = h4(mfma16h_k16(a4t, a4, z));
   f32x4 R;
 #pragma unroll
-  for (int v = 0; v < 4; ++v) R[v] = ((4 * q4 + v == l16) ? 1.f : 0.f) - A[v];
-  R = mfma16h_k16(a2t, h4(R), R);
-  R = mfma16h_k16(a4t, h4(R), R);
-  return mfma16h_k16(a8t, h4(R), R);
+  for (int v = 0; v < 4; ++v) R[v] = ((4 * q4 + v == l16) ? 1.f : 0.f) - At[v];
+  R = mfma16h_k16(a2, h4(R), R);
+  R = mfma16h_k16(a4, h4(R), R);
+  return mfma16h_k16(a8, h4(R), R);
+}
+
+// 4 consecutive fp16 of one row of a [C][LDT] tile (one 8-byte LDS write)
+__device__ __forceinline__ void put_row4(f16* m, int r, int c, const f32x4& x) {
+  *reinterpret_cast<f16x4*>(m + r * LDT + c) = h4(x);
 }
 
 // A operand (16x16x16) of the 16x16 block at (r0, c0) of an fp16 [C][LDT] matrix
@@ -457,8 +478,8 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
       load_raw<MODE>(raw, p, qh, kh, vh, t0, min(C, si.eos - t0), c_begin >= c_out,
                      tid, h);
       prep_rows<MODE>(raw, p.l2norm, p.scale);
-      if (wave == 0) prep_scan(raw, lane);
-      stage_chunk<MODE>(stage_at(smem, 0), raw, c_begin >= c_out, tid, wave, lane);
+      if (wave == 0) prep_scan(raw, lane, p.g_dt);
+      stage_chunk<MODE>(stage_at(smem, 0), raw, c_begin >= c_out, tid, wave, lane, p.beta_dt);
       if (c_begin + 1 < si.c_end) {
         const int t1 = t0 + C;
         load_raw<MODE>(raw, p, qh, kh, vh, t1, min(C, si.eos - t1),
@@ -473,11 +494,22 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
       const int tok0 = si.bos + c * C;
       const bool out_chunk = (MODE == MODE_OUT) && (c >= c_out);
 
-      // ---- phase 1: T blocks / P; K S and (Q S)^T; store the previous chunk's O ----
+      // ---- phase 1: stage the next chunk (its buffer was last read in the previous
+      // chunk's phase 2) and prefetch the one after, so the loads have a whole chunk
+      // to arrive; T blocks / P; K S and (Q S)^T; store the previous chunk's O -------
+      if (c + 1 < si.c_end) {
+        prep_rows<MODE>(raw, p.l2norm, p.scale);
+        if (wave == 0) prep_scan(raw, lane, p.g_dt);
+        stage_chunk<MODE>(stage_at(smem, bi ^ 1), raw, c + 1 >= c_out, tid, wave, lane,
+                          p.beta_dt);
+        if (c + 2 < si.c_end) {
+          const int t2 = tok0 + 2 * C;
+          load_raw<MODE>(raw, p, qh, kh, vh, t2, min(C, si.eos - t2), c + 2 >= c_out, tid, h);
+        }
+      }
       bf16x8 zr[MT];
-      if (MODE == MODE_OUT && c > c_out) {
-        if constexpr (NORM) load_gate(zr, tok0 - C, C);   // stored at the end of phase 1
-        else store_o(tok0 - C, C);
+      if constexpr (NORM) {
+        if (MODE == MODE_OUT && c > c_out) load_gate(zr, tok0 - C, C);
       }
 
       // X[mt][ct] = (K S) tile (tokens 16mt.., state cols 32w+16ct..);
@@ -486,69 +518,73 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
       auto phase1 = [&](auto role_c, auto outq_c) {
         constexpr int R = decltype(role_c)::value;
         constexpr bool OQ = decltype(outq_c)::value;
-        if constexpr (R < MT) {
-          // A strip R: off-diagonal tile -> -M_10, diagonal tile -> T'_RR (fp16 into sT)
-          f16x8 af[4];
+        // Role work, balanced over the waves (16x16x32-MFMA units in brackets):
+        //   wave 0: T'_00 [4 + 8 half]; wave 1: T'_11 [4 + 8 half];
+        //   wave 2: -M_10 and P_00 [4 + 4]; wave 3: P_10 and P_11 [4 + 4].
+        // Tiles are formed transposed (keys as rows), so each lane holds 4
+        // consecutive columns of one row and writes them with one 8-byte store.
+        auto gram = [&](const f16* X, int rx, const f16* Y, int ry) {
+          // C layout of X[rx..rx+15] . Y[ry..ry+15]^T (128-long rows)
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int ks = 0; ks < 4; ++ks) af[ks] = frag_h(cur.K, LDQ, 16 * R, 32 * ks, lane);
-          float gr[4], br[4];
+          for (int ks = 0; ks < 4; ++ks)
+            acc = mfma16h(frag_h(X, LDQ, rx, 32 * ks, lane), frag_h(Y, LDQ, ry, 32 * ks, lane), acc);
+          return acc;
+        };
+        if constexpr (R < MT) {
+          // T'_RR = (I + A_RR)^-1 diag(beta), A = diag(beta) M on the diagonal block
+          const int o = 16 * R;
+          const f32x4 kk = gram(cur.K, o, cur.K, o);   // symmetric
+          const float gc = cur.G[o + l16], bc = cur.B[o + l16];
+          f32x4 Ad, At_;
+          float br[4];
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
-            gr[v] = cur.G[16 * R + 4 * q4 + v];
-            br[v] = cur.B[16 * R + 4 * q4 + v];
+            const int row = 4 * q4 + v;
+            br[v] = cur.B[o + row];
+            const float d = cur.G[o + row] - gc;
+            const float e = kk[v] * fast_exp(row > l16 ? d : -d);
+            Ad[v] = row > l16 ? br[v] * e : 0.f;
+            At_[v] = l16 > row ? bc * e : 0.f;
           }
+          f32x4 Tt = inv_unit_lower16_t(Ad, At_, q4, l16);   // T[l16][4q4+v]
 #pragma unroll
-          for (int j = 0; j <= R; ++j) {
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+          for (int v = 0; v < 4; ++v) Tt[v] *= br[v];
+          put_row4(sT, o + l16, o + 4 * q4, Tt);
+        } else if constexpr (R == MT) {
+          // -M_10: row 16+l16, cols 4q4+v: -(k_i.k_j) e^{G_i-G_j}
+          const f32x4 m = gram(cur.K, 0, cur.K, 16);
+          const float gi = cur.G[16 + l16];
+          f32x4 nm;
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks)
-              acc = mfma16h(af[ks], frag_h(cur.K, LDQ, 16 * j, 32 * ks, lane), acc);
-            const int col = 16 * j + l16;
-            const float gc = cur.G[col];
-            if (j < R) {
-#pragma unroll
-              for (int v = 0; v < 4; ++v)
-                sT[(16 * R + 4 * q4 + v) * LDT + col] = (f16)(-acc[v] * fast_exp(gr[v] - gc));
-            } else {
-              // A and A^T of the diagonal tile in C layout (k.k^T is symmetric)
-              const float bc = cur.B[col];
-              f32x4 At_, Ad;
-#pragma unroll
-              for (int v = 0; v < 4; ++v) {
-                const int row = 16 * R + 4 * q4 + v;
-                const float d = gr[v] - gc;
-                const float e = acc[v] * fast_exp(row > col ? d : -d);
-                Ad[v] = row > col ? br[v] * e : 0.f;
-                At_[v] = col > row ? bc * e : 0.f;
-              }
-              const f32x4 Tii = inv_unit_lower16(Ad, At_, q4, l16);
-#pragma unroll
-              for (int v = 0; v < 4; ++v) sT[(16 * R + 4 * q4 + v) * LDT + col] = (f16)(Tii[v] * bc);
-            }
-          }
-        } else if constexpr (OQ) {
-          // P strip i = R - MT: q_n,r . k_n,c e^{G_r-G_c} for c <= r (scale is in q_n)
-          constexpr int i = R - MT;
-          f16x8 af[4];
-#pragma unroll
-          for (int ks = 0; ks < 4; ++ks) af[ks] = frag_h(cur.Q, LDQ, 16 * i, 32 * ks, lane);
-          float gr[4];
-#pragma unroll
-          for (int v = 0; v < 4; ++v) gr[v] = cur.G[16 * i + 4 * q4 + v];
-#pragma unroll
-          for (int j = 0; j <= i; ++j) {
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks)
-              acc = mfma16h(af[ks], frag_h(cur.K, LDQ, 16 * j, 32 * ks, lane), acc);
-            const int col = 16 * j + l16;
-            const float gc = cur.G[col];
+          for (int v = 0; v < 4; ++v) nm[v] = -m[v] * fast_exp(gi - cur.G[4 * q4 + v]);
+          put_row4(sT, 16 + l16, 4 * q4, nm);
+          if constexpr (OQ) {
+            // P_00: row l16 (query), cols 4q4+v (keys), c <= r
+            const f32x4 pt = gram(cur.K, 0, cur.Q, 0);
+            const float gr = cur.G[l16];
+            f32x4 pv;
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-              const int row = 16 * i + 4 * q4 + v;
-              sP[row * LDT + col] = (f16)((row >= col) ? acc[v] * fast_exp(gr[v] - gc) : 0.f);
+              const int c = 4 * q4 + v;
+              pv[v] = c <= l16 ? pt[v] * fast_exp(gr - cur.G[c]) : 0.f;
             }
+            put_row4(sP, l16, 4 * q4, pv);
           }
+        } else if constexpr (OQ) {
+          // P_10 (all c < r) and P_11 (c <= r): row 16+l16
+          const float gr = cur.G[16 + l16];
+          const f32x4 p0 = gram(cur.K, 0, cur.Q, 16);
+          const f32x4 p1 = gram(cur.K, 16, cur.Q, 16);
+          f32x4 v0, v1;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int c = 4 * q4 + v;
+            v0[v] = p0[v] * fast_exp(gr - cur.G[c]);
+            v1[v] = c <= l16 ? p1[v] * fast_exp(gr - cur.G[16 + c]) : 0.f;
+          }
+          put_row4(sP, 16 + l16, 4 * q4, v0);
+          put_row4(sP, 16 + l16, 16 + 4 * q4, v1);
         }
         // K S and (Q S)^T for this wave's columns; one fp16 copy of the state
         // serves as the B operand of K S and the A operand of (Q S)^T
@@ -576,10 +612,6 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
             }
           }
         }
-        // the next chunk's row factors and g scan (its rows are in registers;
-        // unused values when this is the segment's last chunk)
-        prep_rows<MODE>(raw, p.l2norm, p.scale);
-        if constexpr (R == 0) prep_scan(raw, lane);
       };
       using I0 = std::integral_constant<int, 0>;
       using I1 = std::integral_constant<int, 1>;
@@ -598,8 +630,9 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
         else if (wave == 2) phase1(I2{}, BF{});
         else phase1(I3{}, BF{});
       }
-      if constexpr (NORM) {
-        if (c > c_out) store_o_norm(tok0 - C, C, zr);
+      if (MODE == MODE_OUT && c > c_out) {
+        if constexpr (NORM) store_o_norm(tok0 - C, C, zr);
+        else store_o(tok0 - C, C);
       }
       lds_barrier();
 
@@ -686,15 +719,6 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
       }
       __builtin_amdgcn_s_setprio(0);
 
-      // ---- stage the next chunk into the other buffer; prefetch the one after -------
-      if (c + 1 < si.c_end) {
-        stage_chunk<MODE>(stage_at(smem, bi ^ 1), raw, c + 1 >= c_out, tid, wave, lane);
-        if (c + 2 < si.c_end) {
-          const int t2 = tok0 + 2 * C;
-          load_raw<MODE>(raw, p, qh, kh, vh, t2, min(C, si.eos - t2),
-                         c + 2 >= c_out, tid, h);
-        }
-      }
       lds_barrier();
     }
     if (MODE == MODE_OUT && si.c_end > c_out) {
