@@ -321,7 +321,10 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
   f16* sT = reinterpret_cast<f16*>(smem + OFF_T);
   f16* sP = reinterpret_cast<f16*>(smem + OFF_P);
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  // the wave index as a scalar: branches on it are uniform (an EXEC-masked region
+  // would still run its MFMAs, which ignore EXEC)
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int q4 = lane >> 4, l16 = lane & 15;
   const int s_id = blockIdx.x, h = blockIdx.y;
   const SegInfo si = load_seg(p.seg, s_id);

@@ -5,83 +5,58 @@
 // Semantics (per token t, head h; reference files under
 // vllm-inference/src/primed_vllm/gka/):
 //   q, k <- q/|q|, k/|k| (no eps)                          gka_forward.py:114-159
-//   k~ = (beta+1e-6) k
+//   k~ = (beta+1e-6) k,  v~ = (beta+1e-6) v
 //   H_t = e^{Gk_t} H_c + sum_{j<=t} e^{Gk_t-Gk_j} k~_j k~_j^T  chebyshev_prefill_gqa.py:28-106
 //   f_t = |H_t|_F (closed form, :227-235); lam = r f; tau = 2/(2lam+f);
 //   c = (f/(2lam+f)/2)^2; x = tau q; num_iter x { w <- 1/(1-cw);
 //   x, x_prev <- w x - tau w (H_t x + lam x - q) - (w-1) x_prev, x }  :243-263
 //   q <- q + alpha (x - q)                                  gka_forward.py:225
-//   o_t = scale [e^{G_t} q^T S_c + sum_{j<=t} e^{G_t-G_j} (q.k_j)(beta_j+1e-6)^2 v_j]
-//                                                           ops/chunk_o_gqa.py:25-114
-//   S_{c+1} = e^{G_last} S_c + K^T (e^{G_last-G} (beta+1e-6)^2 V)   chunk_simple_gla_gqa.py:33-101
-//   H_{c+1} = e^{Gk_last} H_c + K~^T (e^{Gk_last-Gk} K~)
+//   o_t = scale [e^{G_t} q^T S_c + sum_{j<=t} e^{G_t-G_j} (q.k~_j) v~_j]   ops/chunk_o_gqa.py:25-114
+//   S <- e^{g} S + k~ v~^T,  H <- e^{gk} H + k~ k~^T        chunk_simple_gla_gqa.py:33-101
 //
-// Decomposition.  One 256-thread workgroup per (segment, head) walks 32-token
-// chunks with H and S in MFMA accumulator registers (wave w owns columns
-// [32w, 32w+32) of both).  Both state recurrences are linear with a scalar
-// decay, so a segment's start state is exact from a scalar-decay combine of the
-// other segments' zero-start end states (pass LOCAL + combine), no transition
-// matrices needed.
+// Decomposition (the reference's split of the state recurrence from the solve,
+// chebyshev_prefill_gqa.py:291-314).  The solve and the output of a token need
+// only the states at its 64-token block's start; nothing they compute feeds the
+// recurrences.  So:
+//   * gka_walk_kernel: one workgroup per (segment, head) walks 32-token chunks
+//     from a zero state with H and S in MFMA accumulators (wave w owns columns
+//     [32w, 32w+32)), writing the zero-start states at every 64-token block start
+//     (fp16) and the segment's end states (fp32).
+//   * gka_combine_kernel: both recurrences have a scalar decay, so a segment's
+//     true start state is the exact combine e^{D_s} X_s + dX_s of the segments
+//     before it; it also reads and writes the caller's state pools.
+//   * gka_solve_kernel: one workgroup per (64-token block, head), all blocks in
+//     parallel: block-start states H_c = dH_b + e^{Gk(seg..b)} H_seg (same for S),
+//     |H_t|_F in closed form, the Chebyshev iterations and the GLA output.  Wave w
+//     owns the block's tokens [16w, 16w+16) and keeps its iterate transposed
+//     (X^T, state dimension as rows) in C-layout registers, which is the B operand
+//     layout of the next product: the iterations need no LDS exchange and no
+//     barrier.
 //
-// Numerics.  Raw k stays exact in bf16; the L2 normalisation and (beta+1e-6)
-// become fp32 per-token scales folded into fp32 epilogues or into B operands
-// that are then split into bf16 hi + lo.  The Chebyshev iterate and H are used
-// as hi/lo pairs in the solver's products; the GLA output uses bf16 operands.
+// Numerics.  MFMA operands are fp16 with fp32 accumulation: k~, v~, the block-start
+// states (one rounding each) and, as fp16 hi + lo pairs, the iterate X, the
+// masked in-block products X.k~ and the blended query (the iterate is large off
+// the key span, and a single rounding of it moves o by ~3e-2).  The walk keeps H
+// and S in fp32 accumulators; its update operands are single fp16 roundings.
 //
 // Roofline: MFMA-bound at num_iter >= 8 (2*num_iter*(C*d^2 + 2*C^2*d) flops per
-// chunk-head for the solver) plus the HBM minimum (q,k,v,o bf16 + gates +
-// states).
+// block-head for the solver) plus the HBM minimum (q,k,v,o bf16 + gates +
+// states) and the block-start states (2 * 32 KiB per 64-token block and head).
 #include "common.hpp"
 #include "mfma.hpp"
 
 namespace hmx {
 namespace gkap {
 
-constexpr int C = 32;           // tokens per chunk
-constexpr int MT = C / 16;
 constexpr int D = 128;
-#ifndef HMX_GKA_WAVES
-#define HMX_GKA_WAVES 8
-#endif
-constexpr int NW = HMX_GKA_WAVES;   // waves per workgroup (one workgroup per CU)
-constexpr int NTHR = 64 * NW;
-constexpr int CW = D / NW;          // state columns owned by one wave
-constexpr int NCT = CW / 16;        // 16-column tiles per wave
-constexpr int RPP = NTHR / 16;      // chunk rows staged per pass (16 lanes per row)
-constexpr int NPASS = C / RPP;      // staging passes per chunk
-static_assert(NW == 4 || NW == 8, "4 or 8 waves");
-constexpr int LDQ = D + 8;      // bf16 [C][D] row stride (q, k, v, O)
-constexpr int LDX = C + 8;      // bf16 [D][C] row stride (X^T hi/lo, Q^T)
-constexpr int LDZ = C + 8;      // bf16 [C][C] row stride (Z, A2)
-constexpr int LDK = C + 1;      // fp32 [C][C] (scaled k.k Gram)
+constexpr int CB = 64;          // block: the solve's unit and the state-storage interval
+constexpr int CW = 32;          // walk chunk
+constexpr int NTHR = 256;       // 4 waves
+// fp16 [rows][128] LDS row stride: 76 dwords = 12 mod 64 banks, so the 16-row
+// fragment reads and the 4-row transposing reads (ds_read_b64_tr_b16) are
+// conflict-free
+constexpr int LDQ = D + 24;
 constexpr float EPS = 1e-6f;
-
-enum Mode { MODE_OUT = 0, MODE_LOCAL = 1 };
-
-// LDS layout (bytes)
-constexpr int SZ_Q = C * LDQ * 2;   // 8704
-constexpr int SZ_XT = D * LDX * 2;  // 10240
-constexpr int SZ_Z = C * LDZ * 2;   // 2560
-constexpr int OFF_Q = 0;
-constexpr int OFF_K = OFF_Q + SZ_Q;
-constexpr int OFF_V = OFF_K + SZ_Q;
-constexpr int OFF_O = OFF_V + SZ_Q;
-constexpr int OFF_XH = OFF_O + SZ_Q;
-constexpr int OFF_XL = OFF_XH + SZ_XT;
-constexpr int OFF_ZH = OFF_XL + SZ_XT;
-constexpr int OFF_ZL = OFF_ZH + SZ_Z;
-constexpr int OFF_KK = OFF_ZL + SZ_Z;              // fp32 [C][LDK]
-constexpr int OFF_S = OFF_KK + C * LDK * 4;         // fp32 per-token scalars
-constexpr int NSC = 25;                             // scalar arrays of C floats
-constexpr int OFF_NW = OFF_S + NSC * C * 4;        // fp32 [D] output-norm weight (NORM)
-constexpr int SMEM = OFF_NW + D * 4;
-static_assert(SMEM <= 80 * 1024, "LDS budget");
-// per-token scalar array indices
-enum { S_G, S_GK, S_EG, S_EGK, S_EDL, S_EDLK, S_BE, S_SK, S_IQ, S_ALPHA, S_KN2, S_QN2,
-       S_U0 };                                        // S_U0 .. S_U0 + NW - 1: per-wave u partials
-constexpr int S_F0 = S_U0 + NW, S_F1 = S_F0 + 1, S_TAU = S_F1 + 1, S_LAM = S_TAU + 1,
-              S_CC = S_LAM + 1;
-static_assert(S_CC < NSC, "scalar slots");
 
 struct SegInfo { int n, bos, eos, c_start, c_end, seg_idx, first_seg, nseg; };
 
@@ -91,35 +66,27 @@ struct Pool {
   const void* in; void* out; int64_t ss; int dt;
 };
 
-__device__ __forceinline__ float pool_ld(const Pool& pl, int64_t i) {
-  return pl.dt == HMX_BF16 ? (float)static_cast<const bf16*>(pl.in)[i]
-                           : static_cast<const float*>(pl.in)[i];
-}
-
-__device__ __forceinline__ void pool_st(const Pool& pl, int64_t i, float x) {
-  if (pl.dt == HMX_BF16) static_cast<bf16*>(pl.out)[i] = (bf16)x;
-  else static_cast<float*>(pl.out)[i] = x;
-}
-
 struct Params {
   const bf16* q; const bf16* k; const bf16* v;
   int64_t q_ts, kv_ts;                    // token strides (elements; k and v share one)
   const void* alpha; int alpha_dt;
   const void* g; int g_dt;
-  const void* gk; int gk_dt;       // null: no h_kk decay
-  const void* beta; int beta_dt;   // null: no beta
+  const void* gk; int gk_dt;              // null: no h_kk decay
+  const void* beta; int beta_dt;          // null: no beta
   bf16* o;
   // Sequence n's states: slot sidx[n] (or n) of the h_kk / h_kv pools; a negative
   // slot or hinit[n] == 0 starts from zero, and a negative slot writes nothing.
-  // Only the combine launch and single-segment workgroups read the pools, so the
-  // last segment may write its end state straight into the slot.
+  // Only the combine launch reads and writes the pools.
   Pool hkk, hkv;
   const int* sidx;                        // [N] or null
   const uint8_t* hinit;                   // [N] or null
-  const int* seg; int nseg_total;
-  float* ws_dh; float* ws_ds;             // [nseg][H][D][D] zero-start segment end states
+  const int* seg; int nseg_total; int nblk_total;
+  int* segblk;                            // [nseg+1]: first global block of each segment
+  f16* ws_hb; f16* ws_sb;                 // [nblk][H][D][D]: zero-start block-start H, S^T
+  float* ws_boff;                         // [nblk][H][2]: sum gk, sum g, segment start -> block
+  float* ws_dh; float* ws_ds;             // [nseg][H][D][D]: zero-start end states H, S^T
   float* ws_dec;                          // [nseg][H][2]: sum gk, sum g over the segment
-  float* ws_h0; float* ws_s0;             // [nseg][H][D][D] segment start states
+  f16* ws_h0; f16* ws_s0;                 // [nseg][H][D][D]: segment start states H, S^T
   int H, HKV, num_iter;
   float ridge_ratio, scale;
   int l2norm;                             // 0: q, k are used as given
@@ -140,85 +107,7 @@ __device__ __forceinline__ SegInfo load_seg(const int* seg, int s) {
   return SegInfo{r[0], r[1], r[2], r[3], r[4], r[5], r[6], r[7]};
 }
 
-// One [D][D] state into accumulator tiles (rows 16rt+4q4+v, columns CW wave +
-// 16ct + l16): from fp32 workspace, or from a pool slot (f32 or bf16), or zeros.
-// (The pool comes by value: a pointer into the kernel's argument struct would move
-// the whole struct to scratch.)
-__device__ __forceinline__ void load_state(f32x4 (&X)[8][NCT], const float* ws, bool use_pool,
-                                           Pool pl, int64_t slot, int64_t hoff, int wave, int q4,
-                                           int l16) {
-#define HMX_GKA_STATE_LOOP(EXPR)                                                   \
-  _Pragma("unroll") for (int rt = 0; rt < 8; ++rt)                                \
-  _Pragma("unroll") for (int ct = 0; ct < NCT; ++ct)                              \
-  _Pragma("unroll") for (int v = 0; v < 4; ++v) {                                 \
-    const int off = (16 * rt + 4 * q4 + v) * D + CW * wave + 16 * ct + l16;      \
-    X[rt][ct][v] = (EXPR);                                                        \
-  }
-  if (ws) {
-    HMX_GKA_STATE_LOOP(ws[off])
-  } else if (use_pool && pl.dt == HMX_BF16) {
-    const bf16* b = static_cast<const bf16*>(pl.in) + slot * pl.ss + hoff;
-    HMX_GKA_STATE_LOOP((float)b[off])
-  } else if (use_pool) {
-    const float* f = static_cast<const float*>(pl.in) + slot * pl.ss + hoff;
-    HMX_GKA_STATE_LOOP(f[off])
-  } else {
-    HMX_GKA_STATE_LOOP(0.f)
-  }
-#undef HMX_GKA_STATE_LOOP
-}
-
-// One [D][D] state from accumulator tiles into a pool slot (f32 or bf16), or
-// zeros into it (clear).
-__device__ __forceinline__ void store_state(const f32x4 (&X)[8][NCT], Pool pl, int64_t slot,
-                                            int64_t hoff, int wave, int q4, int l16, bool clear) {
-#define HMX_GKA_STORE_LOOP(STMT)                                                   \
-  _Pragma("unroll") for (int rt = 0; rt < 8; ++rt)                                \
-  _Pragma("unroll") for (int ct = 0; ct < NCT; ++ct)                              \
-  _Pragma("unroll") for (int v = 0; v < 4; ++v) {                                 \
-    const int off = (16 * rt + 4 * q4 + v) * D + CW * wave + 16 * ct + l16;      \
-    const float x = clear ? 0.f : X[rt][ct][v];                                   \
-    STMT;                                                                         \
-  }
-  if (pl.dt == HMX_BF16) {
-    bf16* b = static_cast<bf16*>(pl.out) + slot * pl.ss + hoff;
-    HMX_GKA_STORE_LOOP(b[off] = (bf16)x)
-  } else {
-    float* f = static_cast<float*>(pl.out) + slot * pl.ss + hoff;
-    HMX_GKA_STORE_LOOP(f[off] = x)
-  }
-#undef HMX_GKA_STORE_LOOP
-}
-
-struct Raw {
-  bf16x8 k[NPASS], v[NPASS], q[NPASS];
-  float g, gk, b, a;
-};
-
-template <int MODE>
-__device__ __forceinline__ void load_raw(Raw& r, const Params& p, const bf16* qh, const bf16* kh,
-                                         const bf16* vh, int tok0, int nval, int tid, int h) {
-#pragma unroll
-  for (int pass = 0; pass < NPASS; ++pass) {
-    const int row = pass * RPP + (tid >> 4), f0 = (tid & 15) * 8;
-    const bool ok = row < nval;
-    const int64_t tok = tok0 + row;
-    r.k[pass] = ok ? *reinterpret_cast<const bf16x8*>(kh + tok * p.kv_ts + f0) : bf16x8{};
-    r.v[pass] = ok ? *reinterpret_cast<const bf16x8*>(vh + tok * p.kv_ts + f0) : bf16x8{};
-    if (MODE == MODE_OUT)
-      r.q[pass] = ok ? *reinterpret_cast<const bf16x8*>(qh + tok * p.q_ts + f0) : bf16x8{};
-  }
-  if (tid < C) {
-    const bool ok = tid < nval;
-    const int64_t i = (int64_t)(tok0 + tid) * p.H + h;
-    r.g = ok ? ldsc(p.g, i, p.g_dt) : 0.f;
-    r.gk = (ok && p.gk) ? ldsc(p.gk, i, p.gk_dt) : 0.f;
-    r.b = (ok && p.beta) ? ldsc(p.beta, i, p.beta_dt) : 0.f;
-    r.a = (ok && MODE == MODE_OUT) ? ldsc(p.alpha, i, p.alpha_dt) : 0.f;
-  }
-}
-
-// Sum of squares of a staged 8-feature slice over its 16-lane row.
+// Sum of squares of an 8-feature slice over the 16 lanes of its DPP row.
 __device__ __forceinline__ float row_sumsq(const bf16x8& x) {
   float s = 0.f;
 #pragma unroll
@@ -226,655 +115,804 @@ __device__ __forceinline__ float row_sumsq(const bf16x8& x) {
   return row16_sum(s);
 }
 
-// Writes a C-layout 16x16 register tile transposed (M^T[col][row]) as bf16 hi/lo,
-// 4 consecutive rows per lane -> one 8-byte store each.
-__device__ __forceinline__ void put_t_hilo(bf16* th, bf16* tl, int ld, int r0, int c0,
-                                           const f32x4& x, int q4, int l16) {
-  bf16x4 hi, lo;
-#pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    hi[v] = (bf16)x[v];
-    lo[v] = (bf16)(x[v] - (float)hi[v]);
-  }
-  const int a = (c0 + l16) * ld + r0 + 4 * q4;
-  *reinterpret_cast<bf16x4*>(th + a) = hi;
-  if (tl) *reinterpret_cast<bf16x4*>(tl + a) = lo;
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ float scan64(float x) {
+  const float lo = scan32(x);          // lanes 0-31 and 32-63 scanned separately
+  const float carry = __builtin_bit_cast(
+      float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lo), 31));
+  return (threadIdx.x & 63) >= 32 ? lo + carry : lo;
 }
 
-// One workgroup per CU: NW / 4 waves per SIMD (the second bound is waves per SIMD).
-// NORM: the output rows pass through the gated RMSNorm of hmx_rms_norm_gated (norm
-// before gate) on their way out of sO.
-template <int MODE, bool NORM = false>
-__global__ __launch_bounds__(NTHR, NW / 4) void gka_chunk_kernel(Params p) {
+// The k~ scale of a row: (beta+1e-6) / |k| (or without the norm / without beta).
+__device__ __forceinline__ float key_scale(const Params& p, float ss, int64_t gi, bool ok) {
+  if (!ok) return 0.f;
+  const float be = p.beta ? ldsc(p.beta, gi, p.beta_dt) + EPS : 1.f;
+  return p.l2norm ? be / sqrtf(ss) : be;
+}
+
+__device__ __forceinline__ float beta_eps(const Params& p, int64_t gi, bool ok) {
+  if (!ok) return 0.f;
+  return p.beta ? ldsc(p.beta, gi, p.beta_dt) + EPS : 1.f;
+}
+
+__device__ __forceinline__ f16x8 scale_h8(const bf16x8& x, float s) {
+  f16x8 y;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) y[j] = (f16)((float)x[j] * s);
+  return y;
+}
+
+// ===========================================================================
+// Pass A: the state walk
+// ===========================================================================
+namespace walk {
+constexpr int SZ_T = CW * LDQ * 2;                 // one fp16 [32][LDQ] tile
+constexpr int SZ_BUF = 3 * SZ_T + 2 * CW * 4;      // K~, K~ e^{GkL-Gk}, V~ e^{GL-G}; sum gk, sum g
+constexpr int SMEM = 2 * SZ_BUF;
+static_assert(SMEM <= 80 * 1024, "LDS budget");
+
+struct Stage {
+  f16* K; f16* KD; f16* VD; float* tot;   // tot[0] = chunk sum gk, tot[1] = chunk sum g
+};
+__device__ __forceinline__ Stage stage_at(unsigned char* smem, int bi) {
+  unsigned char* b = smem + bi * SZ_BUF;
+  return Stage{reinterpret_cast<f16*>(b), reinterpret_cast<f16*>(b + SZ_T),
+               reinterpret_cast<f16*>(b + 2 * SZ_T), reinterpret_cast<float*>(b + 3 * SZ_T)};
+}
+
+struct Raw {
+  bf16x8 k[2], v[2];
+  float b[2];                 // beta of the thread's two rows
+  float g, gk;                // gates of token `lane` (lanes 0-31 of every wave)
+};
+
+__device__ __forceinline__ void load_raw(Raw& r, const Params& p, const bf16* kh, const bf16* vh,
+                                         int tok0, int nval, int tid, int h) {
+#pragma unroll
+  for (int pass = 0; pass < 2; ++pass) {
+    const int row = pass * 16 + (tid >> 4), f0 = (tid & 15) * 8;
+    const bool ok = row < nval;
+    const int64_t tok = tok0 + row;
+    r.k[pass] = ok ? *reinterpret_cast<const bf16x8*>(kh + tok * p.kv_ts + f0) : bf16x8{};
+    r.v[pass] = ok ? *reinterpret_cast<const bf16x8*>(vh + tok * p.kv_ts + f0) : bf16x8{};
+    r.b[pass] = (ok && p.beta) ? ldsc(p.beta, tok * p.H + h, p.beta_dt) : 0.f;
+  }
+  const int lane = tid & 63;
+  const bool okg = lane < nval && lane < CW;
+  const int64_t gi = (int64_t)(tok0 + lane) * p.H + h;
+  r.g = okg ? ldsc(p.g, gi, p.g_dt) : 0.f;
+  r.gk = (okg && p.gk) ? ldsc(p.gk, gi, p.gk_dt) : 0.f;
+}
+
+// Stage one chunk: rows as the update uses them (fp16, k~ and v~ with the decay to
+// the chunk end folded into the B-operand copies) and the chunk's gate sums.  Every
+// wave forms the 32 in-chunk cumsums itself (lanes 0-31) and hands each staging
+// lane its row's decay with a lane permute, so no LDS round trip is needed.
+__device__ __forceinline__ void stage(const Stage& st, const Raw& r, const Params& p, int tid,
+                                      int lane, int tok0, int nval, int h, bool track_h) {
+  const float G = scan32(lane < CW ? r.g : 0.f);
+  const float Gk = scan32(lane < CW ? r.gk : 0.f);
+  const float GL = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, G), CW - 1));
+  const float GkL = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, Gk), CW - 1));
+  const float dl = fast_exp(GL - G), dlk = fast_exp(GkL - Gk);   // per token `lane`
+#pragma unroll
+  for (int pass = 0; pass < 2; ++pass) {
+    const int row = pass * 16 + (tid >> 4), f0 = (tid & 15) * 8;
+    const bool ok = row < nval;
+    const float ss = row_sumsq(r.k[pass]);
+    const float be = ok ? (p.beta ? r.b[pass] + EPS : 1.f) : 0.f;
+    const float sk = !ok ? 0.f : (p.l2norm ? be / sqrtf(ss) : be);
+    const float sv = be;
+    const float drow = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(row << 2, __builtin_bit_cast(int, dl)));
+    const float dkrow = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(row << 2, __builtin_bit_cast(int, dlk)));
+    *reinterpret_cast<f16x8*>(st.K + row * LDQ + f0) = scale_h8(r.k[pass], sk);
+    if (track_h) *reinterpret_cast<f16x8*>(st.KD + row * LDQ + f0) = scale_h8(r.k[pass], sk * dkrow);
+    *reinterpret_cast<f16x8*>(st.VD + row * LDQ + f0) = scale_h8(r.v[pass], sv * drow);
+  }
+  if (tid == 0) {
+    st.tot[0] = GkL;
+    st.tot[1] = GL;
+  }
+}
+
+template <bool TRACK_H>
+__global__ __launch_bounds__(NTHR, 2) void gka_walk_kernel(Params p) {
   __shared__ __align__(16) unsigned char smem[SMEM];
-  bf16* sQ = reinterpret_cast<bf16*>(smem + OFF_Q);
-  bf16* sK = reinterpret_cast<bf16*>(smem + OFF_K);
-  bf16* sV = reinterpret_cast<bf16*>(smem + OFF_V);
-  bf16* sO = reinterpret_cast<bf16*>(smem + OFF_O);
-  bf16* sXh = reinterpret_cast<bf16*>(smem + OFF_XH);
-  bf16* sXl = reinterpret_cast<bf16*>(smem + OFF_XL);
-  bf16* sZh = reinterpret_cast<bf16*>(smem + OFF_ZH);
-  bf16* sZl = reinterpret_cast<bf16*>(smem + OFF_ZL);
-  float* sKK = reinterpret_cast<float*>(smem + OFF_KK);
-  float* sc = reinterpret_cast<float*>(smem + OFF_S);
-  auto SC = [&](int slot, int t) -> float& { return sc[slot * C + t]; };
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  // the wave index as a scalar: branches on it are uniform (an EXEC-masked region
+  // would still run its MFMAs, which ignore EXEC)
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int q4 = lane >> 4, l16 = lane & 15;
-  const int s_id = blockIdx.x, h = blockIdx.y;
+  const int s_id = blockIdx.x, h = blockIdx.y, H = p.H;
   const SegInfo si = load_seg(p.seg, s_id);
-  const int H = p.H, hk = h / (H / p.HKV);
-  const bool solve = (MODE == MODE_OUT) && p.num_iter > 0;
-  const bool track_h = p.num_iter > 0;
+  const int hk = h / (H / p.HKV);
 
-  if (MODE == MODE_LOCAL && si.seg_idx == si.nseg - 1) return;
-  if (NORM && tid < D) {
-    float wv;
-    if (p.onw_dt == HMX_F32) wv = static_cast<const float*>(p.onw)[tid];
-    else if (p.onw_dt == HMX_BF16) wv = (float)static_cast<const bf16*>(p.onw)[tid];
-    else wv = (float)static_cast<const f16*>(p.onw)[tid];
-    reinterpret_cast<float*>(smem + OFF_NW)[tid] = wv;   // read after the chunk's barriers
-  }
-
-  // ---- initial states ----------------------------------------------------
-  // A split sequence's segments (its first included) start from the workspace
-  // the combine launch filled; a single-segment sequence reads its pool slot.
-  const int64_t slot = p.sidx ? (int64_t)p.sidx[si.n] : si.n;
-  const int64_t hoff = (int64_t)h * D * D;
-  f32x4 Hs[8][NCT], Ss[8][NCT];
+  // this segment's first global block: the blocks of the segments before it
+  __shared__ int red[NTHR / 64];
   {
-    const float *hsrc = nullptr, *ssrc = nullptr;
-    bool pooled = false;
-    if (MODE == MODE_OUT) {
-      if (si.nseg == 1) {
-        pooled = slot >= 0 && (!p.hinit || p.hinit[si.n]);
-      } else {
-        hsrc = p.ws_h0 + ((int64_t)s_id * H + h) * D * D;
-        ssrc = p.ws_s0 + ((int64_t)s_id * H + h) * D * D;
-      }
+    int cnt = 0;
+    for (int s = tid; s < s_id; s += NTHR) {
+      const int* r = p.seg + s * 8;
+      cnt += r[4] - r[3];
     }
-    // h_kk then h_kv, each from one source chosen by a uniform branch (a per-element
-    // choice costs registers)
-    load_state(Hs, hsrc && track_h ? hsrc : nullptr, pooled && track_h && p.hkk.in, p.hkk, slot,
-               hoff, wave, q4, l16);
-    load_state(Ss, ssrc, pooled && p.hkv.in, p.hkv, slot, hoff, wave, q4, l16);
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) cnt += __shfl_xor(cnt, m, 64);
+    if (lane == 0) red[wave] = cnt;
+  }
+  __syncthreads();
+  const int base = red[0] + red[1] + red[2] + red[3];
+  if (h == 0 && tid == 0) {
+    p.segblk[s_id] = base;
+    if (s_id == p.nseg_total - 1) p.segblk[p.nseg_total] = base + si.c_end - si.c_start;
   }
 
-  const int64_t o_rs = (int64_t)H * D;
-  const bf16* qh = p.q + (int64_t)h * D;
-  const bf16* kh = p.k + (int64_t)hk * D;
-  const bf16* vh = p.v + (int64_t)hk * D;
-  float seg_gk = 0.f, seg_g = 0.f;
-
-  Raw raw;
-  if (si.c_start < si.c_end)
-    load_raw<MODE>(raw, p, qh, kh, vh, si.bos + si.c_start * C,
-                   min(C, si.eos - (si.bos + si.c_start * C)), tid, h);
-
-  for (int c = si.c_start; c < si.c_end; ++c) {
-    const int tok0 = si.bos + c * C;
-    const int nval = min(C, si.eos - tok0);
-
-    // ---- P0: stage raw rows, row norms, per-token gates ---------------------
-#pragma unroll
-    for (int pass = 0; pass < NPASS; ++pass) {
-      const int row = pass * RPP + (tid >> 4), f0 = (tid & 15) * 8;
-      *reinterpret_cast<bf16x8*>(sK + row * LDQ + f0) = raw.k[pass];
-      *reinterpret_cast<bf16x8*>(sV + row * LDQ + f0) = raw.v[pass];
-      const float kn2 = row_sumsq(raw.k[pass]);
-      if ((tid & 15) == 0) SC(S_KN2, row) = kn2;
-      if (MODE == MODE_OUT) {
-        *reinterpret_cast<bf16x8*>(sQ + row * LDQ + f0) = raw.q[pass];
-        const float qn2 = row_sumsq(raw.q[pass]);
-        if ((tid & 15) == 0) SC(S_QN2, row) = qn2;
-      }
-    }
-    if (wave == 0) {
-      const bool ok = lane < C;
-      const float G = scan32(ok ? raw.g : 0.f);
-      const float Gk = scan32(ok ? raw.gk : 0.f);
-      const float GL = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, G), C - 1));
-      const float GkL = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, Gk), C - 1));
-      if (ok) {
-        SC(S_G, lane) = G;
-        SC(S_GK, lane) = Gk;
-        SC(S_EG, lane) = fast_exp(G);
-        SC(S_EGK, lane) = fast_exp(Gk);
-        SC(S_EDL, lane) = fast_exp(GL - G);
-        SC(S_EDLK, lane) = fast_exp(GkL - Gk);
-        SC(S_BE, lane) = p.beta ? raw.b + EPS : 1.0f;
-        SC(S_ALPHA, lane) = raw.a;
-      }
-      seg_g += GL;
-      seg_gk += GkL;
-    }
-    if (c + 1 < si.c_end) {
-      const int t1 = tok0 + C;
-      load_raw<MODE>(raw, p, qh, kh, vh, t1, min(C, si.eos - t1), tid, h);
-    }
-    lds_barrier();
-    // per-token scales: s_t = (beta_t+eps)/|k_t| (k~ = s k), iq_t = 1/|q_t|
-    // (without in-kernel normalisation: s_t = beta_t+eps or 1, iq_t = 1)
-    if (tid < C) {
-      const float kn2 = SC(S_KN2, tid);
-      SC(S_SK, tid) = tid < nval ? SC(S_BE, tid) * (p.l2norm ? 1.0f / sqrtf(kn2) : 1.f) : 0.f;
-      if (MODE == MODE_OUT)
-        SC(S_IQ, tid) = tid < nval ? (p.l2norm ? 1.0f / sqrtf(SC(S_QN2, tid)) : 1.f) : 0.f;
-    }
-
-    lds_barrier();
-    // q^ for this wave's columns (C layout), fp32
-    f32x4 qv[MT][NCT];
-    if (MODE == MODE_OUT) {
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int ct = 0; ct < NCT; ++ct)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const int t = 16 * mt + 4 * q4 + v;
-            qv[mt][ct][v] = (float)sQ[t * LDQ + CW * wave + 16 * ct + l16] * SC(S_IQ, t);
-          }
-    }
-
-    // ---- P1: the Chebyshev solve (OUT, num_iter > 0) -------------------------
-    f32x4 xq[MT][NCT];  // the query fed to the GLA (solved + alpha-blended, or q^)
-    if (MODE == MODE_OUT) {
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int ct = 0; ct < NCT; ++ct) xq[mt][ct] = qv[mt][ct];
-    }
-    if (solve) {
-      // P1a: u_j = k~_j H_c k~_j^T (per-wave partials), |H_c|^2, scaled Gram k~.k~
-      {
-        float u[MT][4];
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) u[mt][v] = 0.f;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          bf16x8 Hh[NCT], Hl[NCT];
-#pragma unroll
-          for (int ct = 0; ct < NCT; ++ct) pack_b_hilo(Hs[2 * ks][ct], Hs[2 * ks + 1][ct], Hh[ct], Hl[ct]);
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt) {
-            const bf16x8 a = frag_perm(sK, LDQ, 16 * mt, 32 * ks, lane);
-#pragma unroll
-            for (int ct = 0; ct < NCT; ++ct) {
-              f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-              acc = mfma16(a, Hh[ct], acc);
-              acc = mfma16(a, Hl[ct], acc);
-#pragma unroll
-              for (int v = 0; v < 4; ++v)
-                u[mt][v] += acc[v] *
-                            (float)sK[(16 * mt + 4 * q4 + v) * LDQ + CW * wave + 16 * ct + l16];
-            }
-          }
-        }
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const float s = row16_sum(u[mt][v]);
-            if (l16 == 0) SC(S_U0 + wave, 16 * mt + 4 * q4 + v) = s;
-          }
-        float hn = 0.f;
-#pragma unroll
-        for (int rt = 0; rt < 8; ++rt)
-#pragma unroll
-          for (int ct = 0; ct < NCT; ++ct)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) hn += Hs[rt][ct][v] * Hs[rt][ct][v];
-        hn = wave_sum(hn);
-        if (lane == 0) SC(S_F0, C - 1 - wave) = hn;  // |H_c|^2 partials in the F0 tail
-        // Gram tiles (0,0), (1,0), (1,1) on waves 0..2: sKK[t][j] = s_t s_j k_t.k_j
-        if (wave < 3) {
-          const int a = (wave == 0) ? 0 : 1, b = (wave == 2) ? 1 : 0;
-          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int ks = 0; ks < 4; ++ks)
-            acc = mfma16(frag(sK, LDQ, 16 * a, 32 * ks, lane), frag(sK, LDQ, 16 * b, 32 * ks, lane), acc);
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const int t = 16 * a + 4 * q4 + v, j = 16 * b + l16;
-            sKK[t * LDK + j] = acc[v] * SC(S_SK, t) * SC(S_SK, j);
-          }
-        }
-      }
-      lds_barrier();
-      // P1b: in-chunk part of |H_t|_F^2 = sum_l M_tl (M . KK^2)_tl, M_tj = e^{Gk_t-Gk_j} (t>=j)
-      float hc2 = 0.f;
-#pragma unroll
-      for (int w = 0; w < NW; ++w) hc2 += SC(S_F0, C - 1 - w);
-      lds_barrier();
-      if (wave < 3) {
-        const int a = (wave == 0) ? 0 : 1, b = (wave == 2) ? 1 : 0;
-        f32x4 R = {0.f, 0.f, 0.f, 0.f};
-        // R_tl = sum_j M_tj KK_jl^2 over j <= t (KK symmetric; only j >= l contributes via M? no:
-        // every j <= t contributes); k in natural order j = 4s + q (two 16-blocks)
-        for (int jb = 0; jb <= a; ++jb) {
-#pragma unroll
-          for (int s = 0; s < 4; ++s) {
-            const int t = 16 * a + l16, j = 16 * jb + 4 * s + q4, l = 16 * b + l16;
-            const float m = (t >= j) ? fast_exp(SC(S_GK, t) - SC(S_GK, j)) : 0.f;
-            const float kk = (j >= l) ? sKK[j * LDK + l] : sKK[l * LDK + j];
-            R = mfma16f(m, kk * kk, R);
-          }
-        }
-        float fp[4];
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int t = 16 * a + 4 * q4 + v, l = 16 * b + l16;
-          const float m = (t >= l) ? fast_exp(SC(S_GK, t) - SC(S_GK, l)) : 0.f;
-          fp[v] = row16_sum(R[v] * m);
-        }
-        if (l16 == 0) {
-#pragma unroll
-          for (int v = 0; v < 4; ++v) SC(b == 0 ? S_F0 : S_F1, 16 * a + 4 * q4 + v) = fp[v];
-        }
-        if (a == 0 && l16 == 0) {
-#pragma unroll
-          for (int v = 0; v < 4; ++v) SC(S_F1, 4 * q4 + v) = 0.f;  // tile (0,1) is empty
-        }
-      }
-      lds_barrier();
-      // P1c: per-token f, lam, tau, c
-      if (tid < C) {
-        const int t = tid;
-        float cross = 0.f;
-        for (int j = 0; j <= t; ++j) {
-          float usum = 0.f;
-#pragma unroll
-          for (int w = 0; w < NW; ++w) usum += SC(S_U0 + w, j);
-          const float uj = usum * SC(S_SK, j) * SC(S_SK, j);
-          cross += fast_exp(SC(S_GK, t) - SC(S_GK, j)) * uj;
-        }
-        const float egk = SC(S_EGK, t);
-        const float f2 = egk * egk * hc2 + 2.f * egk * cross + SC(S_F0, t) + SC(S_F1, t);
-        const float f = sqrtf(f2);
-        const float lam = p.ridge_ratio * f;
-        const float inv = 1.0f / (2.f * lam + f);
-        SC(S_TAU, t) = 2.f * inv;
-        SC(S_LAM, t) = lam;
-        const float cc = f * inv * 0.5f;
-        SC(S_CC, t) = cc * cc;
-      }
-      lds_barrier();
-
-      // P1d: the iteration.  Each wave owns X[:, 32w..32w+32) in registers.
-      float tau[MT][4], lam[MT][4], ccv[MT][4], om[MT][4];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int t = 16 * mt + 4 * q4 + v;
-          tau[mt][v] = SC(S_TAU, t);
-          lam[mt][v] = SC(S_LAM, t);
-          ccv[mt][v] = SC(S_CC, t);
-          om[mt][v] = 2.0f;
-        }
-      f32x4 X[MT][NCT], Xp[MT][NCT];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int ct = 0; ct < NCT; ++ct) {
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            X[mt][ct][v] = tau[mt][v] * qv[mt][ct][v];
-            Xp[mt][ct][v] = 0.f;
-          }
-        }
-      // Z~ weights M_tj s_j^2 (j <= t) of this wave's tile, fixed over the iterations
-      f32x4 zw = {0.f, 0.f, 0.f, 0.f};
-      if (wave < 3) {
-        const int a = (wave == 0) ? 0 : 1, b = (wave == 2) ? 1 : 0;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int t = 16 * a + 4 * q4 + v, j = 16 * b + l16;
-          const float sj = SC(S_SK, j);
-          zw[v] = (t >= j) ? sj * sj * fast_exp(SC(S_GK, t) - SC(S_GK, j)) : 0.f;
-        }
-      }
-      for (int it = 0; it < p.num_iter; ++it) {
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-          for (int ct = 0; ct < NCT; ++ct)
-            put_t_hilo(sXh, sXl, LDX, 16 * mt, CW * wave + 16 * ct, X[mt][ct], q4, l16);
-        lds_barrier();
-        // Z~_tj = M_tj s_j^2 (x_t . k_j) for j <= t on waves 0..2
-        if (wave < 3) {
-          const int a = (wave == 0) ? 0 : 1, b = (wave == 2) ? 1 : 0;
-          f32x4 z = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int ks = 0; ks < 4; ++ks) {
-            const bf16x8 bk = frag(sK, LDQ, 16 * b, 32 * ks, lane);
-            z = mfma16(frag_t(sXh, LDX, 32 * ks, 16 * a, lane), bk, z);
-            z = mfma16(frag_t(sXl, LDX, 32 * ks, 16 * a, lane), bk, z);
-          }
-          f32x4 zs;
-#pragma unroll
-          for (int v = 0; v < 4; ++v) zs[v] = z[v] * zw[v];
-          // store Z~ row-major (t, j): 2-byte writes
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const int t = 16 * a + 4 * q4 + v, j = 16 * b + l16;
-            const bf16 hi = (bf16)zs[v];
-            sZh[t * LDZ + j] = hi;
-            sZl[t * LDZ + j] = (bf16)(zs[v] - (float)hi);
-          }
-        } else if (wave == 3) {
-          // wave 3 zeroes the empty upper tile (0,1)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            sZh[(4 * q4 + v) * LDZ + 16 + l16] = (bf16)0.f;
-            sZl[(4 * q4 + v) * LDZ + 16 + l16] = (bf16)0.f;
-          }
-        }
-        // Y = e^{Gk} (X H_c) for this wave's columns (X, H as hi/lo)
-        f32x4 Y[MT][NCT];
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-          for (int ct = 0; ct < NCT; ++ct) Y[mt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          bf16x8 Hh[NCT], Hl[NCT];
-#pragma unroll
-          for (int ct = 0; ct < NCT; ++ct) pack_b_hilo(Hs[2 * ks][ct], Hs[2 * ks + 1][ct], Hh[ct], Hl[ct]);
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt) {
-            const bf16x8 ah = frag_t_perm(sXh, LDX, 32 * ks, 16 * mt, lane);
-            const bf16x8 al = frag_t_perm(sXl, LDX, 32 * ks, 16 * mt, lane);
-#pragma unroll
-            for (int ct = 0; ct < NCT; ++ct) {
-              Y[mt][ct] = mfma16(ah, Hh[ct], Y[mt][ct]);
-              Y[mt][ct] = mfma16(ah, Hl[ct], Y[mt][ct]);
-              Y[mt][ct] = mfma16(al, Hh[ct], Y[mt][ct]);
-            }
-          }
-        }
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const float e = SC(S_EGK, 16 * mt + 4 * q4 + v);
-#pragma unroll
-            for (int ct = 0; ct < NCT; ++ct) Y[mt][ct][v] *= e;
-          }
-        lds_barrier();
-        // Y += Z~ K (Z~ hi/lo, raw K exact)
-#pragma unroll
-        for (int ct = 0; ct < NCT; ++ct) {
-          const bf16x8 bk = frag_t(sK, LDQ, 0, CW * wave + 16 * ct, lane);
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt) {
-            Y[mt][ct] = mfma16(frag(sZh, LDZ, 16 * mt, 0, lane), bk, Y[mt][ct]);
-            Y[mt][ct] = mfma16(frag(sZl, LDZ, 16 * mt, 0, lane), bk, Y[mt][ct]);
-          }
-        }
-        // Chebyshev update
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            // w <= 2 (c <= 1/4, omega <= 2): the hardware reciprocal (1 ulp) suffices
-            const float w = __builtin_amdgcn_rcpf(1.0f - ccv[mt][v] * om[mt][v]);
-            om[mt][v] = w;
-#pragma unroll
-            for (int ct = 0; ct < NCT; ++ct) {
-              const float x = X[mt][ct][v];
-              const float grad = tau[mt][v] * w * (Y[mt][ct][v] + lam[mt][v] * x - qv[mt][ct][v]) +
-                                 (w - 1.0f) * Xp[mt][ct][v];
-              Xp[mt][ct][v] = x;
-              X[mt][ct][v] = w * x - grad;
-            }
-          }
-      }
-      // alpha blend
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const float al = SC(S_ALPHA, 16 * mt + 4 * q4 + v);
-#pragma unroll
-          for (int ct = 0; ct < NCT; ++ct)
-            xq[mt][ct][v] = qv[mt][ct][v] + al * (X[mt][ct][v] - qv[mt][ct][v]);
-        }
-    }
-
-    // ---- P2: GLA output (OUT) ------------------------------------------------
-    if (MODE == MODE_OUT) {
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int ct = 0; ct < NCT; ++ct)
-          put_t_hilo(sXh, sXl, LDX, 16 * mt, CW * wave + 16 * ct, xq[mt][ct], q4, l16);
-      lds_barrier();
-      // A2_tj = e^{G_t-G_j} (xq_t . k_j) s_j (beta_j+eps)  (j <= t), waves 0..2
-      if (wave < 3) {
-        const int a = (wave == 0) ? 0 : 1, b = (wave == 2) ? 1 : 0;
-        f32x4 z = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          const bf16x8 bk = frag(sK, LDQ, 16 * b, 32 * ks, lane);
-          z = mfma16(frag_t(sXh, LDX, 32 * ks, 16 * a, lane), bk, z);
-          z = mfma16(frag_t(sXl, LDX, 32 * ks, 16 * a, lane), bk, z);
-        }
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int t = 16 * a + 4 * q4 + v, j = 16 * b + l16;
-          const float w = (t >= j) ? fast_exp(SC(S_G, t) - SC(S_G, j)) * SC(S_SK, j) * SC(S_BE, j) : 0.f;
-          sZh[t * LDZ + j] = (bf16)(z[v] * w);
-        }
-      } else if (wave == 3) {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) sZh[(4 * q4 + v) * LDZ + 16 + l16] = (bf16)0.f;
-      }
-      f32x4 O[MT][NCT];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int ct = 0; ct < NCT; ++ct) O[mt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        // The solved query is large off the key span, so both operands carry a
-        // bf16 remainder: a single bf16 rounding of either costs ~3% of |o|.
-        bf16x8 Sh[NCT], Sl[NCT];
-#pragma unroll
-        for (int ct = 0; ct < NCT; ++ct) pack_b_hilo(Ss[2 * ks][ct], Ss[2 * ks + 1][ct], Sh[ct], Sl[ct]);
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const bf16x8 ah = frag_t_perm(sXh, LDX, 32 * ks, 16 * mt, lane);
-          const bf16x8 al = frag_t_perm(sXl, LDX, 32 * ks, 16 * mt, lane);
-#pragma unroll
-          for (int ct = 0; ct < NCT; ++ct) {
-            O[mt][ct] = mfma16(ah, Sh[ct], O[mt][ct]);
-            O[mt][ct] = mfma16(al, Sh[ct], O[mt][ct]);
-            O[mt][ct] = mfma16(ah, Sl[ct], O[mt][ct]);
-          }
-        }
-      }
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const float e = SC(S_EG, 16 * mt + 4 * q4 + v);
-#pragma unroll
-          for (int ct = 0; ct < NCT; ++ct) O[mt][ct][v] *= e;
-        }
-      lds_barrier();
-#pragma unroll
-      for (int ct = 0; ct < NCT; ++ct) {
-        const bf16x8 bv = frag_t(sV, LDQ, 0, CW * wave + 16 * ct, lane);
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) O[mt][ct] = mfma16(frag(sZh, LDZ, 16 * mt, 0, lane), bv, O[mt][ct]);
-      }
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int ct = 0; ct < NCT; ++ct)
-#pragma unroll
-          for (int v = 0; v < 4; ++v)
-            sO[(16 * mt + 4 * q4 + v) * LDQ + CW * wave + 16 * ct + l16] = (bf16)(O[mt][ct][v] * p.scale);
-    }
-
-    // ---- P3: state updates (hi/lo B operands); the output-norm gate is loaded
-    // here, a phase before the O store uses it ---------------------------------
-    bf16x8 zr[NPASS];
-    if constexpr (NORM) {
-#pragma unroll
-      for (int pass = 0; pass < NPASS; ++pass) {
-        const int row = pass * RPP + (tid >> 4);
-        zr[pass] = (p.zg && row < nval)
-                       ? *reinterpret_cast<const bf16x8*>(p.zg + (int64_t)(tok0 + row) * p.zg_ts +
-                                                          (int64_t)h * p.zg_hs + (tid & 15) * 8)
-                       : bf16x8{};
-      }
-    }
-    {
-      const float egl = SC(S_EG, C - 1), egkl = SC(S_EGK, C - 1);
-#pragma unroll
-      for (int rt = 0; rt < 8; ++rt)
-#pragma unroll
-        for (int ct = 0; ct < NCT; ++ct)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            Ss[rt][ct][v] *= egl;
-            if (track_h) Hs[rt][ct][v] *= egkl;
-          }
-      float fs[8], fh[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int t = 8 * q4 + j;
-        const float s = SC(S_SK, t);
-        fs[j] = s * SC(S_BE, t) * SC(S_EDL, t);
-        fh[j] = s * s * SC(S_EDLK, t);
-      }
-#pragma unroll
-      for (int ct = 0; ct < NCT; ++ct) {
-        const bf16x8 vr = frag_t(sV, LDQ, 0, CW * wave + 16 * ct, lane);
-        const bf16x8 kr = frag_t(sK, LDQ, 0, CW * wave + 16 * ct, lane);
-        bf16x8 vh, vl, kh_, kl_;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float x = (float)vr[j] * fs[j];
-          vh[j] = (bf16)x;
-          vl[j] = (bf16)(x - (float)vh[j]);
-          const float y = (float)kr[j] * fh[j];
-          kh_[j] = (bf16)y;
-          kl_[j] = (bf16)(y - (float)kh_[j]);
-        }
-#pragma unroll
-        for (int rt = 0; rt < 8; ++rt) {
-          const bf16x8 a = frag_t(sK, LDQ, 0, 16 * rt, lane);
-          Ss[rt][ct] = mfma16(a, vh, Ss[rt][ct]);
-          Ss[rt][ct] = mfma16(a, vl, Ss[rt][ct]);
-          if (track_h) {
-            Hs[rt][ct] = mfma16(a, kh_, Hs[rt][ct]);
-            Hs[rt][ct] = mfma16(a, kl_, Hs[rt][ct]);
-          }
-        }
-      }
-    }
-    lds_barrier();
-
-    // ---- store O (NORM: out = o / sqrt(mean(o^2) + eps) * w * silu(z) per row) -
-    if (MODE == MODE_OUT) {
-      bf16* oh = p.o + (int64_t)h * D;
-#pragma unroll
-      for (int pass = 0; pass < NPASS; ++pass) {
-        const int row = pass * RPP + (tid >> 4), f0 = (tid & 15) * 8;
-        bf16x8 ov = *reinterpret_cast<const bf16x8*>(sO + row * LDQ + f0);
-        if constexpr (NORM) {
-          const float* sNW = reinterpret_cast<const float*>(smem + OFF_NW);
-          float f[8], ss = 0.f;
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            f[j] = (float)ov[j];
-            ss += f[j] * f[j];
-          }
-          const float rstd = 1.0f / sqrtf(row16_sum(ss) * (1.0f / D) + p.on_eps);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            float y = f[j] * rstd * sNW[f0 + j];
-            if (p.zg) {
-              const float z = (float)zr[pass][j];
-              y *= z * __builtin_amdgcn_rcpf(1.0f + fast_exp(-z));
-            }
-            ov[j] = (bf16)y;
-          }
-        }
-        if (row < nval) *reinterpret_cast<bf16x8*>(oh + (int64_t)(tok0 + row) * o_rs + f0) = ov;
-      }
-    }
-  }
-
-  // ---- end states ----------------------------------------------------------
-  float *hd = nullptr, *sd = nullptr;
-  if (MODE == MODE_OUT) {
-    if (si.seg_idx == si.nseg - 1 && slot >= 0) {
-      // without the solver (num_iter 0) h_kk is not tracked: a pooled h_kk slot of a
-      // sequence without an initial state is cleared, the others keep their value
-      if (p.hkk.out && (track_h || (p.hinit && !p.hinit[si.n])))
-        store_state(Hs, p.hkk, slot, hoff, wave, q4, l16, !track_h);
-      if (p.hkv.out) store_state(Ss, p.hkv, slot, hoff, wave, q4, l16, false);
-    }
-  } else {
-    hd = track_h ? p.ws_dh + ((int64_t)s_id * H + h) * D * D : nullptr;
-    sd = p.ws_ds + ((int64_t)s_id * H + h) * D * D;
-    if (tid == 0) {
-      p.ws_dec[((int64_t)s_id * H + h) * 2 + 0] = seg_gk;
-      p.ws_dec[((int64_t)s_id * H + h) * 2 + 1] = seg_g;
-    }
-  }
+  const int t_begin = si.bos + si.c_start * CB;
+  const int t_end = min(si.eos, si.bos + si.c_end * CB);
+  f32x4 Hs[8][2], Ss[8][2];
 #pragma unroll
   for (int rt = 0; rt < 8; ++rt)
 #pragma unroll
-    for (int ct = 0; ct < NCT; ++ct)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int off = (16 * rt + 4 * q4 + v) * D + CW * wave + 16 * ct + l16;
-        if (hd) hd[off] = Hs[rt][ct][v];
-        if (sd) sd[off] = Ss[rt][ct][v];
-      }
-}
+    for (int ct = 0; ct < 2; ++ct) {
+      Hs[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+      Ss[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  float acc_gk = 0.f, acc_g = 0.f;        // decay sums from the segment start
+  const bf16* kh = p.k + (int64_t)hk * D;
+  const bf16* vh = p.v + (int64_t)hk * D;
+  const int64_t DD = (int64_t)D * D;
 
-// Segment start states: X_0 = initial, X_{s+1} = e^{D_s} X_s + dX_s (elementwise).
-__global__ __launch_bounds__(256) void gka_seg_combine_kernel(Params p) {
+  // the zero-start block-start states of block gb, transposed (column-major: a
+  // lane's 4 consecutive rows of one column are one 8-byte store; H is symmetric)
+  auto store_block = [&](int gb) {
+    f16* hb = p.ws_hb + ((int64_t)gb * H + h) * DD;
+    f16* sb = p.ws_sb + ((int64_t)gb * H + h) * DD;
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        const int64_t off = (int64_t)(32 * wave + 16 * ct + l16) * D + 16 * rt + 4 * q4;
+        if (TRACK_H) *reinterpret_cast<f16x4*>(hb + off) = h4(Hs[rt][ct]);
+        *reinterpret_cast<f16x4*>(sb + off) = h4(Ss[rt][ct]);
+      }
+    if (tid == 0) {
+      p.ws_boff[((int64_t)gb * H + h) * 2 + 0] = acc_gk;
+      p.ws_boff[((int64_t)gb * H + h) * 2 + 1] = acc_g;
+    }
+  };
+
+  if (t_begin < t_end) {
+    // rows are prefetched two chunks ahead: ra holds chunk t0 + CW, rb chunk t0 + 2 CW
+    Raw ra, rb;
+    load_raw(ra, p, kh, vh, t_begin, min(CW, t_end - t_begin), tid, h);
+    stage(stage_at(smem, 0), ra, p, tid, lane, t_begin, min(CW, t_end - t_begin), h, TRACK_H);
+    if (t_begin + CW < t_end)
+      load_raw(ra, p, kh, vh, t_begin + CW, min(CW, t_end - t_begin - CW), tid, h);
+    if (t_begin + 2 * CW < t_end)
+      load_raw(rb, p, kh, vh, t_begin + 2 * CW, min(CW, t_end - t_begin - 2 * CW), tid, h);
+    lds_barrier();
+    int bi = 0;
+    for (int t0 = t_begin; t0 < t_end; t0 += CW, bi ^= 1) {
+      const Stage cur = stage_at(smem, bi);
+      // stage the next chunk (its buffer was last read before the previous barrier)
+      if (t0 + CW < t_end) {
+        const int t1 = t0 + CW;
+        stage(stage_at(smem, bi ^ 1), ra, p, tid, lane, t1, min(CW, t_end - t1), h, TRACK_H);
+        ra = rb;
+        if (t1 + 2 * CW < t_end)
+          load_raw(rb, p, kh, vh, t1 + 2 * CW, min(CW, t_end - t1 - 2 * CW), tid, h);
+      }
+      // block start: the zero-start states so far (block 0 of a segment starts at zero)
+      if (((t0 - t_begin) % CB) == 0) {
+        const int gb = base + (t0 - t_begin) / CB;
+        if (t0 > t_begin) store_block(gb);
+        else if (tid == 0) {
+          p.ws_boff[((int64_t)gb * H + h) * 2 + 0] = 0.f;
+          p.ws_boff[((int64_t)gb * H + h) * 2 + 1] = 0.f;
+        }
+      }
+      // S <- e^{GL} S + K~^T (e^{GL-G} V~);  H <- e^{GkL} H + K~^T (e^{GkL-Gk} K~)
+      const float egl = fast_exp(cur.tot[1]), egkl = fast_exp(cur.tot[0]);
+      acc_g += cur.tot[1];
+      acc_gk += cur.tot[0];
+#pragma unroll
+      for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            Ss[rt][ct][v] *= egl;
+            if (TRACK_H) Hs[rt][ct][v] *= egkl;
+          }
+      f16x8 bs[2], bh[2];
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        bs[ct] = frag_t_perm_h(cur.VD, LDQ, 0, 32 * wave + 16 * ct, lane);
+        if (TRACK_H) bh[ct] = frag_t_perm_h(cur.KD, LDQ, 0, 32 * wave + 16 * ct, lane);
+      }
+#pragma unroll
+      for (int rt = 0; rt < 8; ++rt) {
+        const f16x8 a = frag_t_perm_h(cur.K, LDQ, 0, 16 * rt, lane);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+          Ss[rt][ct] = mfma16h(a, bs[ct], Ss[rt][ct]);
+          if (TRACK_H) Hs[rt][ct] = mfma16h(a, bh[ct], Hs[rt][ct]);
+        }
+      }
+      lds_barrier();
+    }
+  }
+
+  // zero-start end states (H as is, S transposed) and the segment's decay sums
+  float* hd = p.ws_dh + ((int64_t)s_id * H + h) * DD;
+  float* sd = p.ws_ds + ((int64_t)s_id * H + h) * DD;
+#pragma unroll
+  for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      const int64_t off = (int64_t)(32 * wave + 16 * ct + l16) * D + 16 * rt + 4 * q4;
+      if (TRACK_H) *reinterpret_cast<f32x4*>(hd + off) = Hs[rt][ct];
+      *reinterpret_cast<f32x4*>(sd + off) = Ss[rt][ct];
+    }
+  if (tid == 0) {
+    p.ws_dec[((int64_t)s_id * H + h) * 2 + 0] = acc_gk;
+    p.ws_dec[((int64_t)s_id * H + h) * 2 + 1] = acc_g;
+  }
+}
+}  // namespace walk
+
+// ===========================================================================
+// combine: segment start states and the final states (the only pool access)
+// ===========================================================================
+// One workgroup per (sequence, head, 32x32 tile of the state).  H is kept as is
+// and S transposed in the workspace; the pools hold S as [K][V], so the S tile is
+// read and written through an LDS transpose.
+__global__ __launch_bounds__(256) void gka_combine_kernel(Params p, int track_h) {
+  __shared__ float tile[32][33];
   const int nh = blockIdx.x, H = p.H;
   const int n = nh / H, h = nh % H;
+  const int tr = blockIdx.y >> 2, tc = blockIdx.y & 3;      // tile row / column (of 4x4)
+  const int tid = threadIdx.x;
   int first = -1, nseg = 0;
   for (int s = 0; s < p.nseg_total; ++s) {
     const SegInfo si = load_seg(p.seg, s);
     if (si.n == n) { first = si.first_seg; nseg = si.nseg; break; }
   }
-  if (first < 0 || nseg < 2) return;
-  const bool track_h = p.num_iter > 0;
+  if (first < 0) return;
   const int64_t slot = p.sidx ? (int64_t)p.sidx[n] : n;
   const bool init = slot >= 0 && (!p.hinit || p.hinit[n]);
-  const int64_t hoff = (int64_t)h * D * D;
-  for (int e = blockIdx.y * 256 + threadIdx.x; e < D * D; e += gridDim.y * 256) {
-    float hx = (track_h && init && p.hkk.in) ? pool_ld(p.hkk, slot * p.hkk.ss + hoff + e) : 0.f;
-    float sx = (init && p.hkv.in) ? pool_ld(p.hkv, slot * p.hkv.ss + hoff + e) : 0.f;
-    {   // the first segment's start state, so that no OUT workgroup reads the pool
-      const int64_t fb = ((int64_t)first * H + h) * D * D + e;
-      if (track_h) p.ws_h0[fb] = hx;
-      p.ws_s0[fb] = sx;
+  const int64_t DD = (int64_t)D * D;
+  const int64_t hoff = (int64_t)h * DD;
+  // element (r, c) of this thread's 4 elements: r = 32 tr + (tid >> 3), c = 32 tc + 4 (tid & 7) + j
+  const int r = 32 * tr + (tid >> 3), c0 = 32 * tc + 4 * (tid & 7);
+  auto pool_f = [&](const Pool& pl, int64_t i) -> float {
+    return pl.dt == HMX_BF16 ? (float)static_cast<const bf16*>(pl.in)[i]
+                             : static_cast<const float*>(pl.in)[i];
+  };
+  auto pool_w = [&](const Pool& pl, int64_t i, float x) {
+    if (pl.dt == HMX_BF16) static_cast<bf16*>(pl.out)[i] = (bf16)x;
+    else static_cast<float*>(pl.out)[i] = x;
+  };
+  // h_kk: start states in the stored layout [r][c] (symmetric, no transpose)
+  if (track_h) {
+    float x[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      x[j] = (init && p.hkk.in) ? pool_f(p.hkk, slot * p.hkk.ss + hoff + r * D + c0 + j) : 0.f;
+    for (int s = 0; s < nseg; ++s) {
+      const int64_t b = (int64_t)(first + s) * H + h;
+      *reinterpret_cast<f16x4*>(p.ws_h0 + b * DD + r * D + c0) = f16x4{(f16)x[0], (f16)x[1], (f16)x[2], (f16)x[3]};
+      const float dk = expf(p.ws_dec[b * 2 + 0]);
+      const f32x4 e = *reinterpret_cast<const f32x4*>(p.ws_dh + b * DD + r * D + c0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[j] = x[j] * dk + e[j];
     }
-    for (int s = 0; s < nseg - 1; ++s) {
-      const int64_t b = ((int64_t)(first + s) * H + h);
-      const float dk = expf(p.ws_dec[b * 2 + 0]), dg = expf(p.ws_dec[b * 2 + 1]);
-      if (track_h) hx = hx * dk + p.ws_dh[b * D * D + e];
-      sx = sx * dg + p.ws_ds[b * D * D + e];
-      const int64_t nb = ((int64_t)(first + s + 1) * H + h) * D * D + e;
-      if (track_h) p.ws_h0[nb] = hx;
-      p.ws_s0[nb] = sx;
+    if (slot >= 0 && p.hkk.out) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) pool_w(p.hkk, slot * p.hkk.ss + hoff + r * D + c0 + j, x[j]);
+    }
+  } else if (slot >= 0 && p.hkk.out && p.hinit && !p.hinit[n]) {
+    // without the solver h_kk is not tracked: a pooled slot of a sequence without an
+    // initial state is cleared, the others keep their value
+#pragma unroll
+    for (int j = 0; j < 4; ++j) pool_w(p.hkk, slot * p.hkk.ss + hoff + r * D + c0 + j, 0.f);
+  }
+  // h_kv: the workspace holds S^T; this thread owns S^T rows r (= S columns),
+  // S^T columns c0..c0+3.  The pool tile is read / written transposed via LDS.
+  {
+    float x[4];
+    // pool S[c][r] for c in this tile's columns: thread reads S[32 tr' ...] coalesced
+    // as (row = 32 tc + (tid >> 3), cols 32 tr + 4 (tid & 7) + j), then transposes
+    const int pr = 32 * tc + (tid >> 3), pc0 = 32 * tr + 4 * (tid & 7);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      tile[tid >> 3][4 * (tid & 7) + j] =
+          (init && p.hkv.in) ? pool_f(p.hkv, slot * p.hkv.ss + hoff + pr * D + pc0 + j) : 0.f;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x[j] = tile[4 * (tid & 7) + j][tid >> 3];
+    for (int s = 0; s < nseg; ++s) {
+      const int64_t b = (int64_t)(first + s) * H + h;
+      *reinterpret_cast<f16x4*>(p.ws_s0 + b * DD + r * D + c0) = f16x4{(f16)x[0], (f16)x[1], (f16)x[2], (f16)x[3]};
+      const float dg = expf(p.ws_dec[b * 2 + 1]);
+      const f32x4 e = *reinterpret_cast<const f32x4*>(p.ws_ds + b * DD + r * D + c0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[j] = x[j] * dg + e[j];
+    }
+    if (slot >= 0 && p.hkv.out) {
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < 4; ++j) tile[4 * (tid & 7) + j][tid >> 3] = x[j];
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        pool_w(p.hkv, slot * p.hkv.ss + hoff + pr * D + pc0 + j, tile[tid >> 3][4 * (tid & 7) + j]);
     }
   }
 }
+
+// ===========================================================================
+// Pass B: the parallel solve and GLA output
+// ===========================================================================
+namespace solve {
+constexpr int SZ_K = CB * LDQ * 2;        // fp16 [64][LDQ]
+constexpr int SZ_H = D * LDQ * 2;         // fp16 [128][LDQ]
+constexpr int OFF_K = 0;
+constexpr int OFF_V = OFF_K + SZ_K;
+constexpr int OFF_H = OFF_V + SZ_K;       // H_c, then S_c^T
+constexpr int OFF_SC = OFF_H + SZ_H;
+enum { SC_G, SC_GK, SC_AL, SC_D, SC_G2, SC_HN, NSC };
+constexpr int OFF_NW = OFF_SC + NSC * CB * 4;
+constexpr int SMEM = OFF_NW + D * 4;
+static_assert(2 * SMEM <= 160 * 1024, "two workgroups per CU");
+
+// hi/lo fp16 pair of a B operand built from two stacked C-layout tiles
+__device__ __forceinline__ void h8_hilo(const f32x4& t0, const f32x4& t1, f16x8& hi, f16x8& lo) {
+  hi = h8(t0, t1);
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    lo[v] = (f16)(t0[v] - (float)hi[v]);
+    lo[4 + v] = (f16)(t1[v] - (float)hi[4 + v]);
+  }
+}
+
+// A block-start state X = dX_b + e^{off} X_seg (both fp16; dX_b is zero for a
+// segment's first block), this thread's 64 elements: row tid/2, half tid&1.
+struct StateLd { f16x8 b[8], s[8]; };
+
+__device__ __forceinline__ void state_issue(StateLd& L, const f16* xb, const f16* xs, int tid) {
+  const int r = tid >> 1, c0 = (tid & 1) * 64;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    L.s[j] = *reinterpret_cast<const f16x8*>(xs + r * D + c0 + 8 * j);
+    L.b[j] = xb ? *reinterpret_cast<const f16x8*>(xb + r * D + c0 + 8 * j) : f16x8{};
+  }
+}
+
+// Writes the state into LDS as fp16 rows; returns this thread's sum of squares.
+__device__ __forceinline__ float state_store(f16* dst, const StateLd& L, float dec, int tid) {
+  const int r = tid >> 1, c0 = (tid & 1) * 64;
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    f16x8 y;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float u = (float)L.b[j][i] + dec * (float)L.s[j][i];
+      ss += u * u;
+      y[i] = (f16)u;
+    }
+    *reinterpret_cast<f16x8*>(dst + r * LDQ + c0 + 8 * j) = y;
+  }
+  return ss;
+}
+
+template <bool SOLVE, bool NORM>
+__global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
+  __shared__ __align__(16) unsigned char smem[SMEM];
+  f16* sK = reinterpret_cast<f16*>(smem + OFF_K);
+  f16* sV = reinterpret_cast<f16*>(smem + OFF_V);
+  f16* sH = reinterpret_cast<f16*>(smem + OFF_H);
+  float* sc = reinterpret_cast<float*>(smem + OFF_SC);
+  auto SC = [&](int slot, int t) -> float& { return sc[slot * CB + t]; };
+  const int tid = threadIdx.x, lane = tid & 63;
+  // the wave index as a scalar: branches on it are uniform (an EXEC-masked region
+  // would still run its MFMAs, which ignore EXEC)
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q4 = lane >> 4, l16 = lane & 15;
+  const int gb = blockIdx.x, h = blockIdx.y, H = p.H;
+  const int hk = h / (H / p.HKV);
+  const int64_t DD = (int64_t)D * D;
+
+  // ---- which segment / block -------------------------------------------------
+  int lo = 0, hi = p.nseg_total;        // last s with segblk[s] <= gb
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (p.segblk[mid] <= gb) lo = mid; else hi = mid;
+  }
+  const int s_id = lo;
+  const SegInfo si = load_seg(p.seg, s_id);
+  const int lb = gb - p.segblk[s_id];                 // block index within the segment
+  const int tok0 = si.bos + (si.c_start + lb) * CB;
+  const int nval = min(CB, si.eos - tok0);
+  if (nval <= 0) return;
+
+  // block-start decay offsets (segment start -> this block); the state loads go
+  // out first so their latency overlaps the staging below
+  const int64_t bo = ((int64_t)gb * H + h) * 2;
+  const int64_t so = ((int64_t)s_id * H + h) * DD;
+  const int64_t bso = ((int64_t)gb * H + h) * DD;
+  StateLd hst;
+  if constexpr (SOLVE) state_issue(hst, lb > 0 ? p.ws_hb + bso : nullptr, p.ws_h0 + so, tid);
+
+  // ---- stage k~, v~ (fp16), gates; q rows into registers --------------------
+#pragma unroll
+  for (int pass = 0; pass < CB / 16; ++pass) {
+    const int row = pass * 16 + (tid >> 4), f0 = (tid & 15) * 8;
+    const bool ok = row < nval;
+    const int64_t tok = tok0 + row;
+    const bf16x8 kr = ok ? *reinterpret_cast<const bf16x8*>(p.k + tok * p.kv_ts + hk * D + f0) : bf16x8{};
+    const bf16x8 vr = ok ? *reinterpret_cast<const bf16x8*>(p.v + tok * p.kv_ts + hk * D + f0) : bf16x8{};
+    const int64_t gi = tok * H + h;
+    const float sk = key_scale(p, row_sumsq(kr), gi, ok);
+    *reinterpret_cast<f16x8*>(sK + row * LDQ + f0) = scale_h8(kr, sk);
+    *reinterpret_cast<f16x8*>(sV + row * LDQ + f0) = scale_h8(vr, beta_eps(p, gi, ok));
+  }
+  if (wave == 0) {
+    const bool ok = lane < nval;
+    const int64_t gi = (int64_t)(tok0 + lane) * H + h;
+    const float G = scan64(ok ? ldsc(p.g, gi, p.g_dt) : 0.f);
+    const float Gk = scan64((ok && p.gk) ? ldsc(p.gk, gi, p.gk_dt) : 0.f);
+    SC(SC_G, lane) = G;
+    SC(SC_GK, lane) = Gk;
+    SC(SC_AL, lane) = ok ? ldsc(p.alpha, gi, p.alpha_dt) : 0.f;
+  }
+  if (NORM && tid < D) {
+    float wv;
+    if (p.onw_dt == HMX_F32) wv = static_cast<const float*>(p.onw)[tid];
+    else if (p.onw_dt == HMX_BF16) wv = (float)static_cast<const bf16*>(p.onw)[tid];
+    else wv = (float)static_cast<const f16*>(p.onw)[tid];
+    reinterpret_cast<float*>(smem + OFF_NW)[tid] = wv;
+  }
+  const float off_gk = p.ws_boff[bo + 0], off_g = p.ws_boff[bo + 1];
+  float* red = sc + SC_HN * CB;           // 4 partial sums
+  if constexpr (SOLVE) {
+    const float ss = wave_sum(state_store(sH, hst, fast_exp(off_gk), tid));
+    if (lane == 0) red[wave] = ss;
+  }
+  // this lane's token t (16 per wave) and its q^ slice: Q[nt][v] = q^[t][16 nt + 4 q4 + v]
+  const int tb = 16 * wave + l16;
+  const bool tok_ok = tb < nval;
+  f32x4 Q[8];
+  {
+    const bf16* qr = p.q + (int64_t)(tok0 + tb) * p.q_ts + (int64_t)h * D + 4 * q4;
+    float ss = 0.f;
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      const bf16x4 x = tok_ok ? *reinterpret_cast<const bf16x4*>(qr + 16 * nt) : bf16x4{};
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        Q[nt][v] = (float)x[v];
+        ss += Q[nt][v] * Q[nt][v];
+      }
+    }
+    ss += __shfl_xor(ss, 16, 64);
+    ss += __shfl_xor(ss, 32, 64);
+    const float rq = (!tok_ok) ? 0.f : (p.l2norm ? 1.0f / sqrtf(ss) : 1.f);
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) Q[nt][v] *= rq;
+  }
+
+  f32x4 X[8];                             // the query fed to the GLA, transposed C layout
+  if constexpr (SOLVE) {
+    lds_barrier();
+    const float hn = red[0] + red[1] + red[2] + red[3];   // |H_c|^2
+    const float GkT = SC(SC_GK, tb);
+
+    // d_j = k~_j^T H_c k~_j for this wave's tokens j = 16 wave + l16
+    {
+      f32x4 Pd[8];
+#pragma unroll
+      for (int nt = 0; nt < 8; ++nt) Pd[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const f16x8 b = frag_perm_h(sK, LDQ, 16 * wave, 32 * ks, lane);
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) Pd[nt] = mfma16h(frag_perm_h(sH, LDQ, 16 * nt, 32 * ks, lane), b, Pd[nt]);
+      }
+      float d = 0.f;
+#pragma unroll
+      for (int nt = 0; nt < 8; ++nt) {
+        const f16x4 kk = *reinterpret_cast<const f16x4*>(sK + tb * LDQ + 16 * nt + 4 * q4);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) d += Pd[nt][v] * (float)kk[v];
+      }
+      d += __shfl_xor(d, 16, 64);
+      d += __shfl_xor(d, 32, 64);
+      if (q4 == 0) SC(SC_D, tb) = d;
+    }
+    // Gram part of |H_t|^2: g2_t = sum_{i,j<=t} a_ti a_tj (k~_i.k~_j)^2, a_tj = e^{Gk_t-Gk_j},
+    // as the row sums of a . (A B) with B = (K K^T)^2 over this wave's key range
+    {
+      f32x4 U[4];
+#pragma unroll
+      for (int I = 0; I < 4; ++I) U[I] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int J = 0; J < 4; ++J) {
+        if (J > wave) break;
+        // a[t = tb][j = 16J + 4q4 + v]
+        f16x4 aJ;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int j = 16 * J + 4 * q4 + v;
+          aJ[v] = (f16)(j <= tb ? fast_exp(GkT - SC(SC_GK, j)) : 0.f);
+        }
+#pragma unroll
+        for (int I = 0; I < 4; ++I) {
+          if (I > wave) break;
+          f32x4 kk = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks)
+            kk = mfma16h(frag_h(sK, LDQ, 16 * J, 32 * ks, lane), frag_h(sK, LDQ, 16 * I, 32 * ks, lane), kk);
+          f32x4 sq;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) sq[v] = kk[v] * kk[v];
+          U[I] = mfma16h_k16(aJ, h4(sq), U[I]);
+        }
+      }
+      // U[I][v]: row t = 16 wave + 4 q4 + v, column i = 16 I + l16
+      float g2[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int I = 0; I < 4; ++I) {
+        if (I > wave) break;
+        const int i = 16 * I + l16;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int t = 16 * wave + 4 * q4 + v;
+          g2[v] += (i <= t) ? U[I][v] * fast_exp(SC(SC_GK, t) - SC(SC_GK, i)) : 0.f;
+        }
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float s = row16_sum(g2[v]);
+        if (l16 == 0) SC(SC_G2, 16 * wave + 4 * q4 + v) = s;
+      }
+    }
+    lds_barrier();
+    // f_t, lam, tau, c for this lane's token
+    float tau, lam, cc;
+    {
+      float cross = 0.f;
+      for (int j = q4; j <= tb; j += 4) cross += fast_exp(GkT - SC(SC_GK, j)) * SC(SC_D, j);
+      cross += __shfl_xor(cross, 16, 64);
+      cross += __shfl_xor(cross, 32, 64);
+      const float e = fast_exp(GkT);
+      const float f = sqrtf(fmaxf(e * e * hn + 2.f * e * cross + SC(SC_G2, tb), 0.f));
+      lam = p.ridge_ratio * f;
+      const float inv = 1.0f / (2.f * lam + f);
+      tau = 2.f * inv;
+      const float c = f * inv * 0.5f;
+      cc = c * c;
+      if (!tok_ok) { tau = 0.f; lam = 0.f; cc = 0.f; }
+    }
+
+    // ---- the Chebyshev iterations -----------------------------------------
+    f32x4 Xp[8];
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        X[nt][v] = tau * Q[nt][v];
+        Xp[nt][v] = 0.f;
+      }
+    float om = 2.f;
+    const float egk = fast_exp(GkT);
+    for (int it = 0; it < p.num_iter; ++it) {
+      // X^T as B operands (hi + lo): k = state rows 32ks + {4q4+v, 16+4q4+v}, n = token
+      f16x8 xh[4], xl[4];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) h8_hilo(X[2 * ks], X[2 * ks + 1], xh[ks], xl[ks]);
+      // Z~^T[j][t] = m_tj (k~_j . x_t) for the keys j of tiles 0..wave, as hi/lo B operands
+      f16x8 zh[2], zl[2];
+      {
+        f32x4 Z[4];
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt) Z[jt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          f16x8 a[4];
+#pragma unroll
+          for (int jt = 0; jt < 4; ++jt)
+            if (jt <= wave) a[jt] = frag_perm_h(sK, LDQ, 16 * jt, 32 * ks, lane);
+#pragma unroll
+          for (int jt = 0; jt < 4; ++jt)
+            if (jt <= wave) Z[jt] = mfma16h(a[jt], xh[ks], Z[jt]);
+#pragma unroll
+          for (int jt = 0; jt < 4; ++jt)
+            if (jt <= wave) Z[jt] = mfma16h(a[jt], xl[ks], Z[jt]);
+        }
+        // in-block decays m_tj = e^{Gk_t-Gk_j} (j <= t), formed again each iteration
+        // (cheaper than holding 16 more registers through the iteration)
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt) {
+          if (jt > wave) continue;
+          const f32x4 gkj = *reinterpret_cast<const f32x4*>(&SC(SC_GK, 16 * jt + 4 * q4));
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            Z[jt][v] = (16 * jt + 4 * q4 + v <= tb) ? Z[jt][v] * fast_exp(GkT - gkj[v]) : 0.f;
+        }
+        h8_hilo(Z[0], Z[1], zh[0], zl[0]);
+        h8_hilo(Z[2], Z[3], zh[1], zl[1]);
+      }
+      // x, x_prev <- w x - tau w (H x + lam x - q) - (w-1) x_prev, x, four 16-row tiles
+      // of H x = e^{Gk_t} H_c x + K~^T Z~^T at a time (four independent accumulation
+      // chains keep the MFMA pipe busy; w <= 2 since c <= 1/4, so the hardware
+      // reciprocal suffices)
+      om = __builtin_amdgcn_rcpf(1.0f - cc * om);
+      const float tw = tau * om, ca = om - tw * lam, cd = 1.0f - om;
+#pragma unroll
+      for (int g4 = 0; g4 < 8; g4 += 4) {
+        f32x4 hx[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) hx[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          f16x8 a[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) a[u] = frag_perm_h(sH, LDQ, 16 * (g4 + u), 32 * ks, lane);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) hx[u] = mfma16h(a[u], xh[ks], hx[u]);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) hx[u] = mfma16h(a[u], xl[ks], hx[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) hx[u][v] *= egk;
+#pragma unroll
+        for (int jk = 0; jk < 2; ++jk) {
+          if (2 * jk > wave) continue;
+          f16x8 a[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) a[u] = frag_t_perm_h(sK, LDQ, 32 * jk, 16 * (g4 + u), lane);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) hx[u] = mfma16h(a[u], zh[jk], hx[u]);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) hx[u] = mfma16h(a[u], zl[jk], hx[u]);
+        }
+        // x' = w x - tau w (hx + lam x - q) - (w-1) x_prev = ca x - tw hx + tw q + cd x_prev
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int nt = g4 + u;
+            const float x = X[nt][v], xp = Xp[nt][v];
+            Xp[nt][v] = x;
+            X[nt][v] = ca * x - tw * (hx[u][v] - Q[nt][v]) + cd * xp;
+          }
+        // bound the scheduler's hoisting of LDS operands to one group of tiles
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    // alpha blend
+    const float al = SC(SC_AL, tb);
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) X[nt][v] = Q[nt][v] + al * (X[nt][v] - Q[nt][v]);
+    lds_barrier();      // every wave is done with H_c
+  } else {
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) X[nt] = Q[nt];
+  }
+
+  // ---- GLA output: o^T = scale [e^{G_t} S_c^T x^ + V~^T Z'^T] ---------------
+  // The S_c loads go out first; the in-block products (they need only k~) run while
+  // they arrive.
+  StateLd sst;
+  state_issue(sst, lb > 0 ? p.ws_sb + bso : nullptr, p.ws_s0 + so, tid);
+  if constexpr (!SOLVE) lds_barrier();     // the staged k~, v~ and gates
+  f32x4 O[8];
+  {
+    f16x8 xh[4], xl[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) h8_hilo(X[2 * ks], X[2 * ks + 1], xh[ks], xl[ks]);
+    const float GT = SC(SC_G, tb), eg = fast_exp(GT);
+    // Z'^T[j][t] = e^{G_t-G_j} (k~_j . x^_t), j <= t
+    f32x4 Z[4];
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) Z[jt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      f16x8 a[4];
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt)
+        if (jt <= wave) a[jt] = frag_perm_h(sK, LDQ, 16 * jt, 32 * ks, lane);
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt)
+        if (jt <= wave) Z[jt] = mfma16h(a[jt], xh[ks], Z[jt]);
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt)
+        if (jt <= wave) Z[jt] = mfma16h(a[jt], xl[ks], Z[jt]);
+    }
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int j = 16 * jt + 4 * q4 + v;
+        Z[jt][v] = (jt <= wave && j <= tb) ? Z[jt][v] * fast_exp(GT - SC(SC_G, j)) : 0.f;
+      }
+    const f16x8 zb0 = h8(Z[0], Z[1]), zb1 = h8(Z[2], Z[3]);
+    // S_c into LDS (every wave is past its last read of H_c)
+    state_store(sH, sst, fast_exp(off_g), tid);
+    lds_barrier();
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) O[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int nt = 0; nt < 8; ++nt) {
+        const f16x8 a = frag_perm_h(sH, LDQ, 16 * nt, 32 * ks, lane);
+        O[nt] = mfma16h(a, xh[ks], O[nt]);
+        O[nt] = mfma16h(a, xl[ks], O[nt]);
+      }
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) O[nt][v] *= eg;
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      O[nt] = mfma16h(frag_t_perm_h(sV, LDQ, 0, 16 * nt, lane), zb0, O[nt]);
+      if (wave >= 2) O[nt] = mfma16h(frag_t_perm_h(sV, LDQ, 32, 16 * nt, lane), zb1, O[nt]);
+    }
+  }
+
+  // ---- store (NORM: out = o / sqrt(mean(o^2) + eps) * w * silu(z) per token) ---
+  if (tok_ok) {
+    bf16* orow = p.o + (int64_t)(tok0 + tb) * H * D + (int64_t)h * D + 4 * q4;
+    float rstd = 1.f;
+    if constexpr (NORM) {
+      float ss = 0.f;
+#pragma unroll
+      for (int nt = 0; nt < 8; ++nt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float y = (float)(bf16)(O[nt][v] * p.scale);   // o as rounded to bf16
+          O[nt][v] = y;
+          ss += y * y;
+        }
+      ss += __shfl_xor(ss, 16, 64);
+      ss += __shfl_xor(ss, 32, 64);
+      rstd = 1.0f / sqrtf(ss * (1.0f / D) + p.on_eps);
+    }
+    const bf16* zr = (NORM && p.zg) ? p.zg + (int64_t)(tok0 + tb) * p.zg_ts + (int64_t)h * p.zg_hs + 4 * q4
+                                    : nullptr;
+    const float* sNW = reinterpret_cast<const float*>(smem + OFF_NW);
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      bf16x4 out;
+      if constexpr (NORM) {
+        bf16x4 z = {};
+        if (zr) z = *reinterpret_cast<const bf16x4*>(zr + 16 * nt);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          float y = O[nt][v] * rstd * sNW[16 * nt + 4 * q4 + v];
+          if (zr) {
+            const float zz = (float)z[v];
+            y *= zz * __builtin_amdgcn_rcpf(1.0f + fast_exp(-zz));
+          }
+          out[v] = (bf16)y;
+        }
+      } else {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) out[v] = (bf16)(O[nt][v] * p.scale);
+      }
+      *reinterpret_cast<bf16x4*>(orow + 16 * nt) = out;
+    }
+  }
+}
+}  // namespace solve
 
 }  // namespace gkap
 }  // namespace hmx
@@ -882,10 +920,36 @@ __global__ __launch_bounds__(256) void gka_seg_combine_kernel(Params p) {
 using namespace hmx;
 using namespace hmx::gkap;
 
-extern "C" size_t hmx_gka_chunk_workspace_bytes(int32_t nseg_total, int32_t N, int32_t H) {
-  if (nseg_total <= N) return 16;
-  const size_t st = (size_t)nseg_total * H * D * D * sizeof(float);
-  return 4 * st + (size_t)nseg_total * H * 2 * sizeof(float);
+// Workspace carve-up (256-byte aligned pieces), in this order: block states (H, S^T
+// fp16), segment states (dH, dS^T, H0, S0^T fp32), block offsets, segment decays,
+// the segment -> block prefix.
+namespace {
+struct WsLayout { size_t hb, sb, dh, ds, h0, s0, boff, dec, segblk, total; };
+size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
+WsLayout ws_layout(int32_t nseg, int32_t nblk, int32_t H) {
+  WsLayout w;
+  const size_t blk_st = (size_t)nblk * H * D * D * sizeof(f16);
+  const size_t seg_st = (size_t)nseg * H * D * D * sizeof(float);
+  const size_t seg_h = (size_t)nseg * H * D * D * sizeof(f16);
+  size_t o = 0;
+  w.hb = o; o = al256(o + blk_st);
+  w.sb = o; o = al256(o + blk_st);
+  w.dh = o; o = al256(o + seg_st);
+  w.ds = o; o = al256(o + seg_st);
+  w.h0 = o; o = al256(o + seg_h);
+  w.s0 = o; o = al256(o + seg_h);
+  w.boff = o; o = al256(o + (size_t)nblk * H * 2 * sizeof(float));
+  w.dec = o; o = al256(o + (size_t)nseg * H * 2 * sizeof(float));
+  w.segblk = o; o = al256(o + (size_t)(nseg + 1) * sizeof(int));
+  w.total = o;
+  return w;
+}
+}  // namespace
+
+extern "C" size_t hmx_gka_chunk_workspace_bytes(int32_t nseg_total, int32_t nblock_total,
+                                                int32_t N, int32_t H) {
+  (void)N;
+  return ws_layout(nseg_total, nblock_total, H).total;
 }
 
 extern "C" int hmx_gka_chunk_fwd(const void* q, int64_t q_token_stride, const void* k,
@@ -898,10 +962,11 @@ extern "C" int hmx_gka_chunk_fwd(const void* q, int64_t q_token_stride, const vo
                                  int64_t h_kv_slot_stride, int32_t h_kv_dtype,
                                  const int32_t* state_indices, const uint8_t* has_initial_state,
                                  const int32_t* seg_table, int32_t nseg_total,
-                                 int32_t N, int32_t H, int32_t HKV, int32_t D_, int32_t V,
-                                 int32_t num_iter, float ridge_ratio, float scale,
-                                 int32_t use_qk_l2norm, void* workspace, size_t workspace_bytes,
-                                 const hmx_gated_norm* o_norm, void* stream) {
+                                 int32_t nblock_total, int32_t N, int32_t H, int32_t HKV,
+                                 int32_t D_, int32_t V, int32_t num_iter, float ridge_ratio,
+                                 float scale, int32_t use_qk_l2norm, void* workspace,
+                                 size_t workspace_bytes, const hmx_gated_norm* o_norm,
+                                 void* stream) {
   HMX_REQUIRE(qkv_dtype == HMX_BF16, HMX_EUNSUPPORTED,
               "hmx_gka_chunk_fwd: q/k/v must be bfloat16 (got dtype code %d)", qkv_dtype);
   HMX_REQUIRE(D_ == D && V == D, HMX_EUNSUPPORTED,
@@ -910,6 +975,8 @@ extern "C" int hmx_gka_chunk_fwd(const void* q, int64_t q_token_stride, const vo
   HMX_REQUIRE(q && k && v && alpha && g && o && seg_table, HMX_EINVAL,
               "hmx_gka_chunk_fwd: null tensor pointer");
   HMX_REQUIRE(num_iter >= 0, HMX_EINVAL, "hmx_gka_chunk_fwd: num_iter=%d", num_iter);
+  HMX_REQUIRE(nseg_total >= 0 && nblock_total >= 0, HMX_EINVAL,
+              "hmx_gka_chunk_fwd: nseg_total=%d nblock_total=%d", nseg_total, nblock_total);
   HMX_REQUIRE(q_token_stride % 8 == 0 && k_token_stride % 8 == 0 && v_token_stride % 8 == 0 &&
                   ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)o) % 16 == 0,
               HMX_EINVAL, "hmx_gka_chunk_fwd: q/k/v/o rows must be 16-byte aligned");
@@ -920,9 +987,10 @@ extern "C" int hmx_gka_chunk_fwd(const void* q, int64_t q_token_stride, const vo
                   (h_kv_dtype == HMX_F32 || h_kv_dtype == HMX_BF16),
               HMX_EUNSUPPORTED, "hmx_gka_chunk_fwd: state dtypes must be f32 or bf16");
   if (nseg_total == 0) return HMX_OK;
-  const size_t need = hmx_gka_chunk_workspace_bytes(nseg_total, N, H);
-  HMX_REQUIRE(workspace && workspace_bytes >= need, HMX_EINVAL,
-              "hmx_gka_chunk_fwd: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  const WsLayout wl = ws_layout(nseg_total, nblock_total, H);
+  HMX_REQUIRE(workspace && workspace_bytes >= wl.total, HMX_EINVAL,
+              "hmx_gka_chunk_fwd: workspace of %zu bytes needed, %zu given", wl.total,
+              workspace_bytes);
   Params p;
   p.q = static_cast<const bf16*>(q); p.k = static_cast<const bf16*>(k);
   p.v = static_cast<const bf16*>(v);
@@ -932,10 +1000,10 @@ extern "C" int hmx_gka_chunk_fwd(const void* q, int64_t q_token_stride, const vo
   if (o_norm) {
     HMX_REQUIRE(o_norm->weight && o_norm->weight_dtype >= 0 && o_norm->weight_dtype <= 2,
                 HMX_EINVAL, "hmx_gka_chunk_fwd: o_norm needs a weight (dtype code 0-2)");
-    HMX_REQUIRE(!o_norm->gate || ((uintptr_t)o_norm->gate % 16 == 0 &&
-                                  o_norm->gate_token_stride % 8 == 0 &&
-                                  o_norm->gate_head_stride % 8 == 0),
-                HMX_EINVAL, "hmx_gka_chunk_fwd: o_norm gate rows must be 16-byte aligned");
+    HMX_REQUIRE(!o_norm->gate || ((uintptr_t)o_norm->gate % 8 == 0 &&
+                                  o_norm->gate_token_stride % 4 == 0 &&
+                                  o_norm->gate_head_stride % 4 == 0),
+                HMX_EINVAL, "hmx_gka_chunk_fwd: o_norm gate rows must be 8-byte aligned");
     p.zg = static_cast<const bf16*>(o_norm->gate);
     p.zg_ts = o_norm->gate_token_stride; p.zg_hs = o_norm->gate_head_stride;
     p.onw = o_norm->weight; p.onw_dt = o_norm->weight_dtype; p.on_eps = o_norm->eps;
@@ -945,25 +1013,30 @@ extern "C" int hmx_gka_chunk_fwd(const void* q, int64_t q_token_stride, const vo
   p.hkk = Pool{h_kk0, h_kk_final, h_kk_slot_stride, h_kk_dtype};
   p.hkv = Pool{h_kv0, h_kv_final, h_kv_slot_stride, h_kv_dtype};
   p.sidx = state_indices; p.hinit = has_initial_state;
-  p.seg = seg_table; p.nseg_total = nseg_total;
+  p.seg = seg_table; p.nseg_total = nseg_total; p.nblk_total = nblock_total;
   p.H = H; p.HKV = HKV; p.num_iter = num_iter; p.ridge_ratio = ridge_ratio; p.scale = scale;
   p.l2norm = use_qk_l2norm;
-  const bool multi = nseg_total > N;
-  const size_t st = (size_t)nseg_total * H * D * D;
-  float* ws = static_cast<float*>(workspace);
-  p.ws_dh = multi ? ws : nullptr;
-  p.ws_ds = multi ? ws + st : nullptr;
-  p.ws_h0 = multi ? ws + 2 * st : nullptr;
-  p.ws_s0 = multi ? ws + 3 * st : nullptr;
-  p.ws_dec = multi ? ws + 4 * st : nullptr;
+  char* ws = static_cast<char*>(workspace);
+  p.ws_hb = reinterpret_cast<f16*>(ws + wl.hb);
+  p.ws_sb = reinterpret_cast<f16*>(ws + wl.sb);
+  p.ws_dh = reinterpret_cast<float*>(ws + wl.dh);
+  p.ws_ds = reinterpret_cast<float*>(ws + wl.ds);
+  p.ws_h0 = reinterpret_cast<f16*>(ws + wl.h0);
+  p.ws_s0 = reinterpret_cast<f16*>(ws + wl.s0);
+  p.ws_boff = reinterpret_cast<float*>(ws + wl.boff);
+  p.ws_dec = reinterpret_cast<float*>(ws + wl.dec);
+  p.segblk = reinterpret_cast<int*>(ws + wl.segblk);
+  const bool solve_ = num_iter > 0;
   hipStream_t s = (hipStream_t)stream;
-  if (multi) {
-    hipLaunchKernelGGL(gka_chunk_kernel<MODE_LOCAL>, dim3(nseg_total, H), dim3(NTHR), 0, s, p);
-    hipLaunchKernelGGL(gka_seg_combine_kernel, dim3(N * H, 16), dim3(256), 0, s, p);
+  if (solve_) hipLaunchKernelGGL(walk::gka_walk_kernel<true>, dim3(nseg_total, H), dim3(NTHR), 0, s, p);
+  else hipLaunchKernelGGL(walk::gka_walk_kernel<false>, dim3(nseg_total, H), dim3(NTHR), 0, s, p);
+  hipLaunchKernelGGL(gka_combine_kernel, dim3(N * H, 16), dim3(256), 0, s, p, (int)solve_);
+  if (nblock_total > 0) {
+    const dim3 grid(nblock_total, H);
+    if (solve_ && o_norm) hipLaunchKernelGGL((solve::gka_solve_kernel<true, true>), grid, dim3(NTHR), 0, s, p);
+    else if (solve_) hipLaunchKernelGGL((solve::gka_solve_kernel<true, false>), grid, dim3(NTHR), 0, s, p);
+    else if (o_norm) hipLaunchKernelGGL((solve::gka_solve_kernel<false, true>), grid, dim3(NTHR), 0, s, p);
+    else hipLaunchKernelGGL((solve::gka_solve_kernel<false, false>), grid, dim3(NTHR), 0, s, p);
   }
-  if (o_norm)
-    hipLaunchKernelGGL((gka_chunk_kernel<MODE_OUT, true>), dim3(nseg_total, H), dim3(NTHR), 0, s, p);
-  else
-    hipLaunchKernelGGL(gka_chunk_kernel<MODE_OUT>, dim3(nseg_total, H), dim3(NTHR), 0, s, p);
   return check_launch("hmx_gka_chunk_fwd");
 }

@@ -54,9 +54,9 @@ SIGNATURES: dict[str, list] = {
     "hmx_gka_chunk_fwd": [_P, _I64, _P, _I64, _P, _I64, _I32, _P, _I32, _P, _I32, _P, _I32,
                           _P, _I32, _P,
                           _P, _P, _I64, _I32, _P, _P, _I64, _I32, _P, _P,
-                          _P, _I32, _I32, _I32, _I32, _I32, _I32,
+                          _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32,
                           _I32, _F32, _F32, _I32, _P, ctypes.c_size_t, _P, _P],
-    "hmx_gka_chunk_workspace_bytes": [_I32, _I32, _I32],
+    "hmx_gka_chunk_workspace_bytes": [_I32, _I32, _I32, _I32],
     "hmx_ssd_chunk_fwd": [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I32,
                           _P, _I32, _I64, _I64, _P, _P, _P, _P, _I64, _I64,
                           _P, _I64, _I64, _P, _P, _I64, _I32, _P, _P, _P, _I32, _I32,

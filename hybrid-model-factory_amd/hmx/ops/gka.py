@@ -21,7 +21,8 @@ from .. import _lib
 from .gdn import (_cu_count, _device_table, _gate_rows, _i32, _segment_table, _token_rows,
                   seq_bounds)
 
-GKA_WORKGROUPS_PER_CU = 1
+GKA_WORKGROUPS_PER_CU = 2   # the state walk's workgroups (segments) per CU
+GKA_BLOCK = 64              # tokens per block: the solve kernel's unit and the planner's chunk
 _warned_num_iter_zero = False
 
 
@@ -273,10 +274,12 @@ def _gka_prefill(q, k, v, alpha, g, gk, beta, gla_scale, ridge_ratio, num_iter, 
         o = torch.empty(B, T, H, V, dtype=q.dtype, device=q.device)
     if cu_seqlens is not None and bounds and bounds[-1][1] < T:
         o[:, bounds[-1][1]:].zero_()
-    rows = _segment_table(bounds, H, GKA_WORKGROUPS_PER_CU * _cu_count(q.device), segment_chunks)
+    rows = _segment_table(bounds, H, GKA_WORKGROUPS_PER_CU * _cu_count(q.device), segment_chunks,
+                          chunk=GKA_BLOCK)
+    nblk = sum(r[4] - r[3] for r in rows)
     seg = _device_table(rows, q.device)
     lib = _lib.load()
-    ws_bytes = int(lib.hmx_gka_chunk_workspace_bytes(len(rows), N, H))
+    ws_bytes = int(lib.hmx_gka_chunk_workspace_bytes(len(rows), nblk, N, H))
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=q.device)
     _lib.call("hmx_gka_chunk_fwd",
               _lib.ptr(q), q_ts, _lib.ptr(k), k_ts, _lib.ptr(v), v_ts, _lib.dtype_code(q),
@@ -285,7 +288,7 @@ def _gka_prefill(q, k, v, alpha, g, gk, beta, gla_scale, ridge_ratio, num_iter, 
               _lib.ptr(beta), 0 if beta is None else _lib.dtype_code(beta),
               _lib.ptr(o), _lib.ptr(hkk0), _lib.ptr(hkk_t), ss_kk, dt_kk,
               _lib.ptr(hkv0), _lib.ptr(hkv_t), ss_kv, dt_kv, _lib.ptr(idx), _lib.ptr(hinit),
-              _lib.ptr(seg), len(rows), N, H, HKV, D, V, int(num_iter), float(ridge_ratio),
+              _lib.ptr(seg), len(rows), nblk, N, H, HKV, D, V, int(num_iter), float(ridge_ratio),
               float(gla_scale), int(bool(l2norm)), _lib.ptr(ws), ws.numel(),
               _onorm(*o_norm, tuple(o.shape), q.dtype), _lib.stream_of(q))
     if idx is not None and num_iter == 0:

@@ -26,11 +26,12 @@
 extern "C" {
 #endif
 
-#define HMX_ABI_VERSION 4  /* 2: optional hmx_gated_norm output epilogue in the GDN ops;
+#define HMX_ABI_VERSION 5  /* 2: optional hmx_gated_norm output epilogue in the GDN ops;
                               3: q/k/v token strides in the GDN and GKA ops; slot-indexed
                               state pools and has_initial_state in the GDN, GKA and SSD
                               prefills;
-                              4: grouped x heads (HX) and C groups (GC) in the SSD ops */
+                              4: grouped x heads (HX) and C groups (GC) in the SSD ops;
+                              5: nblock_total in hmx_gka_chunk_fwd and its workspace size */
 
 enum hmx_status {
   HMX_OK = 0,
@@ -233,8 +234,9 @@ int hmx_gka_decode_fwd(const void* q, int64_t q_token_stride, const void* k,
 
 /*
  * GKA chunked prefill forward (Chebyshev ridge solve + beta^2 GLA), GQA-native,
- * varlen via the same segment table layout as hmx_gdn_chunk_fwd (chunks of 32
- * tokens).  q [T_total, H, 128]; k, v [T_total, HKV, 128] bf16 (raw: q and k are
+ * varlen via the segment table layout of hmx_gdn_chunk_fwd over 64-token blocks
+ * (c_start / c_end count blocks of 64 tokens from the sequence start);
+ * nblock_total = the sum over rows of c_end - c_start.  q [T_total, H, 128]; k, v [T_total, HKV, 128] bf16 (raw: q and k are
  * L2-normalised inside, without eps), rows *_token_stride elements apart
  * (multiples of 8; 16-byte aligned bases), heads contiguous in a row; alpha, g
  * [T_total, H]; gk, beta [T_total, H] or NULL; o [T_total, H, 128] bf16
@@ -267,8 +269,8 @@ int hmx_gka_chunk_fwd(const void* q, int64_t q_token_stride, const void* k,
                       int32_t h_kk_dtype, const void* h_kv0, void* h_kv_final,
                       int64_t h_kv_slot_stride, int32_t h_kv_dtype,
                       const int32_t* state_indices, const uint8_t* has_initial_state,
-                      const int32_t* seg_table, int32_t nseg_total, int32_t N,
-                      int32_t H, int32_t HKV, int32_t D, int32_t V,
+                      const int32_t* seg_table, int32_t nseg_total, int32_t nblock_total,
+                      int32_t N, int32_t H, int32_t HKV, int32_t D, int32_t V,
                       int32_t num_iter, float ridge_ratio, float scale, int32_t use_qk_l2norm,
                       void* workspace, size_t workspace_bytes,
                       const hmx_gated_norm* o_norm, void* stream);
@@ -276,7 +278,8 @@ int hmx_gka_chunk_fwd(const void* q, int64_t q_token_stride, const void* k,
 /* Workspace bytes hmx_gka_chunk_fwd needs (host-only arithmetic).  Companion of
  * hmx_gka_chunk_fwd; no reference counterpart (the reference allocates its
  * chunk states inside the op, chebyshev_prefill_gqa.py:137). */
-size_t hmx_gka_chunk_workspace_bytes(int32_t nseg_total, int32_t N, int32_t H);
+size_t hmx_gka_chunk_workspace_bytes(int32_t nseg_total, int32_t nblock_total, int32_t N,
+                                     int32_t H);
 
 /*
  * Mamba2 SSD chunk scan forward, bf16 x/B/C/z/y, fp32 states, varlen via a

@@ -171,16 +171,17 @@ def test_gka_prefill_c3_full_size(dev, num_iter):
     the output window around the first segment boundary the planner cuts, the whole
     output of both heads and their final h_kk / h_kv."""
     from hmx.ops import gdn as gops
-    from hmx.ops.gka import GKA_WORKGROUPS_PER_CU
+    from hmx.ops.gka import GKA_BLOCK, GKA_WORKGROUPS_PER_CU
     d = _c3_inputs()
     T, H = 32768, 32
     args = [d[n] for n in ("q", "k", "v", "alpha", "g", "gk", "beta")]
     o, hkk, hkv = hmx.gka_chebyshev_gla_prefill(*[a.to(dev) for a in args], 128 ** -0.5,
                                                 ridge_ratio=0.01, num_iter=num_iter)
     torch.cuda.synchronize()
-    rows = gops._segment_table([(0, T)], H, GKA_WORKGROUPS_PER_CU * gops._cu_count(dev))
+    rows = gops._segment_table([(0, T)], H, GKA_WORKGROUPS_PER_CU * gops._cu_count(dev),
+                               chunk=GKA_BLOCK)
     assert len(rows) > 1, "C3 is expected to run as several segments per head"
-    edge = rows[1][3] * gops.CHUNK          # first token of the second segment
+    edge = rows[1][3] * GKA_BLOCK           # first token of the second segment
     hs = [0, 17]
     sub = [a[0][:, hs] for a in args]
     o_r, hkk_r, hkv_r = ref.gka_seq_blocked(*sub, 128 ** -0.5, 0.01, num_iter)
