@@ -52,10 +52,10 @@ constexpr int D = 128;
 constexpr int CB = 64;          // block: the solve's unit and the state-storage interval
 constexpr int CW = 32;          // walk chunk
 constexpr int NTHR = 256;       // 4 waves
-// fp16 [rows][128] LDS row stride: 76 dwords = 12 mod 64 banks, so the 16-row
-// fragment reads and the 4-row transposing reads (ds_read_b64_tr_b16) are
-// conflict-free
-constexpr int LDQ = D + 24;
+// fp16 [rows][128] LDS row stride of the walk's tiles: 72 dwords = 8 mod 64 banks,
+// so the transposing reads (ds_read_b64_tr_b16: 8 rows of 8 dwords per 32 lanes)
+// are bank-conflict-free
+constexpr int LDQ = D + 16;
 constexpr float EPS = 1e-6f;
 
 struct SegInfo { int n, bos, eos, c_start, c_end, seg_idx, first_seg, nseg; };
@@ -454,25 +454,79 @@ __global__ __launch_bounds__(256) void gka_combine_kernel(Params p, int track_h)
 // Pass B: the parallel solve and GLA output
 // ===========================================================================
 namespace solve {
-constexpr int SZ_K = CB * LDQ * 2;        // fp16 [64][LDQ]
-constexpr int SZ_H = D * LDQ * 2;         // fp16 [128][LDQ]
+// LDS rows of H_c / S_c, k~ and v~ are 72 dwords apart (8 mod 64 banks): 128-bit
+// row-fragment reads (lane pairs q, q+1 of 8 rows share a cycle) and transposed
+// ds_read_b64_tr_b16 reads (8 rows of 8 dwords per 32 lanes) are then both
+// bank-conflict-free.  H_c, S_c and k~ keep their features in an interleaved order:
+// within each 32-feature block, 4-feature chunk m of half h sits at 8m + 4h, so one
+// 128-bit read at 8q returns features {4q..4q+3, 16+4q..16+4q+3} - the operand
+// order of two stacked C-layout tiles (x^T as a B operand) - where the natural
+// order needs two 64-bit reads.  v~ (read transposed only) keeps the natural order.
+constexpr int LDP = D + 16;
+constexpr int SZ_K = CB * LDP * 2;        // fp16 [64][LDP]
+constexpr int SZ_H = D * LDP * 2;         // fp16 [128][LDP]
+__device__ __forceinline__ int pcol(int f) {
+  return (f & ~31) | ((f & 12) << 1) | ((f & 16) >> 2) | (f & 3);
+}
+// A/B operand of interleaved rows r0..r0+15, k = k0 + {4q+v, 16+4q+v}
+__device__ __forceinline__ f16x8 pfrag(const f16* b, int r0, int k0, int lane) {
+  return *reinterpret_cast<const f16x8*>(b + (r0 + (lane & 15)) * LDP + k0 + 8 * (lane >> 4));
+}
+// transposed 16x16 read at rows row.., features c0 + 4(s&3).. (fcol maps a feature
+// to its stored column)
+template <bool INTERLEAVED>
+__device__ __forceinline__ f16x4 ld_tr_p(const f16* b, int row, int c0, int lane) {
+  const int s = lane & 15, f = c0 + 4 * (s & 3);
+  const f16* a = b + (row + (s >> 2)) * LDP + (INTERLEAVED ? pcol(f) : f);
+  const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(a));
+  return __builtin_bit_cast(f16x4, r);
+}
+// element (row c0 + l16, k) = b[t0 + k][c0 + l16], k in the perm order
+template <bool INTERLEAVED>
+__device__ __forceinline__ f16x8 pfrag_t(const f16* b, int t0, int c0, int lane) {
+  const int tq = t0 + 4 * (lane >> 4);
+  const f16x4 x = ld_tr_p<INTERLEAVED>(b, tq, c0, lane);
+  const f16x4 y = ld_tr_p<INTERLEAVED>(b, tq + 16, c0, lane);
+  return f16x8{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+}
+// stores features f0..f0+7 (f0 a multiple of 8) of an interleaved row
+__device__ __forceinline__ void pstore8(f16* row, int f0, const f16x8& y) {
+  *reinterpret_cast<f16x4*>(row + pcol(f0)) = f16x4{y[0], y[1], y[2], y[3]};
+  *reinterpret_cast<f16x4*>(row + pcol(f0 + 4)) = f16x4{y[4], y[5], y[6], y[7]};
+}
 constexpr int OFF_K = 0;
 constexpr int OFF_V = OFF_K + SZ_K;
-constexpr int OFF_H = OFF_V + SZ_K;       // H_c, then S_c^T
+constexpr int OFF_H = OFF_V + SZ_K;       // H_c, then S_c
 constexpr int OFF_SC = OFF_H + SZ_H;
 enum { SC_G, SC_GK, SC_AL, SC_D, SC_G2, SC_HN, NSC };
 constexpr int OFF_NW = OFF_SC + NSC * CB * 4;
 constexpr int SMEM = OFF_NW + D * 4;
 static_assert(2 * SMEM <= 160 * 1024, "two workgroups per CU");
 
-// hi/lo fp16 pair of a B operand built from two stacked C-layout tiles
-__device__ __forceinline__ void h8_hilo(const f32x4& t0, const f32x4& t1, f16x8& hi, f16x8& lo) {
-  hi = h8(t0, t1);
-#pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    lo[v] = (f16)(t0[v] - (float)hi[v]);
-    lo[4 + v] = (f16)(t1[v] - (float)hi[4 + v]);
-  }
+// hi/lo fp16 pair of a B operand built from two stacked C-layout tiles:
+// hi = fp16 of x rounded toward zero (v_cvt_pkrtz, two per register), lo =
+// fp16(x - hi), where x - hi is exact in fp32 and comes from v_fma_mix reading the
+// packed hi halves directly.  hi + lo carries x to 2^-21 relative.  `one` is 1.0
+// held in a register the compiler cannot see through, so that x*one - hi stays a
+// fused multiply-add (which selects v_fma_mix) instead of being folded into a
+// subtraction of a separately converted hi.
+__device__ __forceinline__ float opaque_one() {
+  float one;
+  asm volatile("v_mov_b32 %0, 1.0" : "=v"(one));
+  return one;
+}
+__device__ __forceinline__ void h8_hilo(const f32x4& t0, const f32x4& t1, f16x8& hi, f16x8& lo,
+                                        float one) {
+  typedef f16 f16x2 __attribute__((ext_vector_type(2)));
+  const f16x2 h0 = __builtin_bit_cast(f16x2, __builtin_amdgcn_cvt_pkrtz(t0[0], t0[1]));
+  const f16x2 h1 = __builtin_bit_cast(f16x2, __builtin_amdgcn_cvt_pkrtz(t0[2], t0[3]));
+  const f16x2 h2 = __builtin_bit_cast(f16x2, __builtin_amdgcn_cvt_pkrtz(t1[0], t1[1]));
+  const f16x2 h3 = __builtin_bit_cast(f16x2, __builtin_amdgcn_cvt_pkrtz(t1[2], t1[3]));
+  hi = f16x8{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
+  lo = f16x8{(f16)__builtin_fmaf(t0[0], one, -(float)h0[0]), (f16)__builtin_fmaf(t0[1], one, -(float)h0[1]),
+             (f16)__builtin_fmaf(t0[2], one, -(float)h1[0]), (f16)__builtin_fmaf(t0[3], one, -(float)h1[1]),
+             (f16)__builtin_fmaf(t1[0], one, -(float)h2[0]), (f16)__builtin_fmaf(t1[1], one, -(float)h2[1]),
+             (f16)__builtin_fmaf(t1[2], one, -(float)h3[0]), (f16)__builtin_fmaf(t1[3], one, -(float)h3[1])};
 }
 
 // A block-start state X = dX_b + e^{off} X_seg (both fp16; dX_b is zero for a
@@ -501,9 +555,25 @@ __device__ __forceinline__ float state_store(f16* dst, const StateLd& L, float d
       ss += u * u;
       y[i] = (f16)u;
     }
-    *reinterpret_cast<f16x8*>(dst + r * LDQ + c0 + 8 * j) = y;
+    pstore8(dst + r * LDP, c0 + 8 * j, y);
   }
   return ss;
+}
+
+// Runs f(WaveIdx<w>{}) for the workgroup's wave w.  Wave w's tokens are
+// 16w..16w+15, so its causal key range is tiles 0..w; with w a compile-time
+// constant the loops over that range are straight-line code.  Only the
+// w-dependent stages go through this (the rest is shared, which keeps the kernel
+// within the instruction cache).
+template <int N> struct WaveIdx { static constexpr int value = N; };
+template <typename F>
+__device__ __forceinline__ void with_wave(int wave, F&& f) {
+  switch (wave) {
+    case 0: f(WaveIdx<0>{}); break;
+    case 1: f(WaveIdx<1>{}); break;
+    case 2: f(WaveIdx<2>{}); break;
+    default: f(WaveIdx<3>{}); break;
+  }
 }
 
 template <bool SOLVE, bool NORM>
@@ -515,9 +585,9 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
   float* sc = reinterpret_cast<float*>(smem + OFF_SC);
   auto SC = [&](int slot, int t) -> float& { return sc[slot * CB + t]; };
   const int tid = threadIdx.x, lane = tid & 63;
-  // the wave index as a scalar: branches on it are uniform (an EXEC-masked region
-  // would still run its MFMAs, which ignore EXEC)
+  // the wave index as a scalar: branches on it are uniform
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const float one = opaque_one();
   const int q4 = lane >> 4, l16 = lane & 15;
   const int gb = blockIdx.x, h = blockIdx.y, H = p.H;
   const int hk = h / (H / p.HKV);
@@ -554,8 +624,8 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
     const bf16x8 vr = ok ? *reinterpret_cast<const bf16x8*>(p.v + tok * p.kv_ts + hk * D + f0) : bf16x8{};
     const int64_t gi = tok * H + h;
     const float sk = key_scale(p, row_sumsq(kr), gi, ok);
-    *reinterpret_cast<f16x8*>(sK + row * LDQ + f0) = scale_h8(kr, sk);
-    *reinterpret_cast<f16x8*>(sV + row * LDQ + f0) = scale_h8(vr, beta_eps(p, gi, ok));
+    pstore8(sK + row * LDP, f0, scale_h8(kr, sk));
+    *reinterpret_cast<f16x8*>(sV + row * LDP + f0) = scale_h8(vr, beta_eps(p, gi, ok));
   }
   if (wave == 0) {
     const bool ok = lane < nval;
@@ -617,14 +687,14 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
       for (int nt = 0; nt < 8; ++nt) Pd[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        const f16x8 b = frag_perm_h(sK, LDQ, 16 * wave, 32 * ks, lane);
+        const f16x8 b = pfrag(sK, 16 * wave, 32 * ks, lane);
 #pragma unroll
-        for (int nt = 0; nt < 8; ++nt) Pd[nt] = mfma16h(frag_perm_h(sH, LDQ, 16 * nt, 32 * ks, lane), b, Pd[nt]);
+        for (int nt = 0; nt < 8; ++nt) Pd[nt] = mfma16h(pfrag(sH, 16 * nt, 32 * ks, lane), b, Pd[nt]);
       }
       float d = 0.f;
 #pragma unroll
       for (int nt = 0; nt < 8; ++nt) {
-        const f16x4 kk = *reinterpret_cast<const f16x4*>(sK + tb * LDQ + 16 * nt + 4 * q4);
+        const f16x4 kk = *reinterpret_cast<const f16x4*>(sK + tb * LDP + pcol(16 * nt + 4 * q4));
 #pragma unroll
         for (int v = 0; v < 4; ++v) d += Pd[nt][v] * (float)kk[v];
       }
@@ -634,13 +704,14 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
     }
     // Gram part of |H_t|^2: g2_t = sum_{i,j<=t} a_ti a_tj (k~_i.k~_j)^2, a_tj = e^{Gk_t-Gk_j},
     // as the row sums of a . (A B) with B = (K K^T)^2 over this wave's key range
-    {
+    with_wave(wave, [&](auto Wc) {
+      constexpr int W = decltype(Wc)::value;
       f32x4 U[4];
 #pragma unroll
       for (int I = 0; I < 4; ++I) U[I] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int J = 0; J < 4; ++J) {
-        if (J > wave) break;
+        if (J > W) break;
         // a[t = tb][j = 16J + 4q4 + v]
         f16x4 aJ;
 #pragma unroll
@@ -650,11 +721,11 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
         }
 #pragma unroll
         for (int I = 0; I < 4; ++I) {
-          if (I > wave) break;
+          if (I > W) break;
           f32x4 kk = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int ks = 0; ks < 4; ++ks)
-            kk = mfma16h(frag_h(sK, LDQ, 16 * J, 32 * ks, lane), frag_h(sK, LDQ, 16 * I, 32 * ks, lane), kk);
+            kk = mfma16h(pfrag(sK, 16 * J, 32 * ks, lane), pfrag(sK, 16 * I, 32 * ks, lane), kk);
           f32x4 sq;
 #pragma unroll
           for (int v = 0; v < 4; ++v) sq[v] = kk[v] * kk[v];
@@ -665,20 +736,20 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
       float g2[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int I = 0; I < 4; ++I) {
-        if (I > wave) break;
+        if (I > W) break;
         const int i = 16 * I + l16;
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          const int t = 16 * wave + 4 * q4 + v;
+          const int t = 16 * W + 4 * q4 + v;
           g2[v] += (i <= t) ? U[I][v] * fast_exp(SC(SC_GK, t) - SC(SC_GK, i)) : 0.f;
         }
       }
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const float s = row16_sum(g2[v]);
-        if (l16 == 0) SC(SC_G2, 16 * wave + 4 * q4 + v) = s;
+        if (l16 == 0) SC(SC_G2, 16 * W + 4 * q4 + v) = s;
       }
-    }
+    });
     lds_barrier();
     // f_t, lam, tau, c for this lane's token
     float tau, lam, cc;
@@ -698,6 +769,7 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
     }
 
     // ---- the Chebyshev iterations -----------------------------------------
+    {
     f32x4 Xp[8];
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt)
@@ -706,14 +778,31 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
         X[nt][v] = tau * Q[nt][v];
         Xp[nt][v] = 0.f;
       }
+    // in-block decays m_tj = e^{Gk_t-Gk_j} (j <= t, else 0) of the four key tiles
+    f32x4 mz[4];
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) {
+      const f32x4 gkj = *reinterpret_cast<const f32x4*>(&SC(SC_GK, 16 * jt + 4 * q4));
+#pragma unroll
+      for (int v = 0; v < 4; ++v) mz[jt][v] = (16 * jt + 4 * q4 + v <= tb) ? fast_exp(GkT - gkj[v]) : 0.f;
+    }
     float om = 2.f;
     const float egk = fast_exp(GkT);
-    for (int it = 0; it < p.num_iter; ++it) {
-      // X^T as B operands (hi + lo): k = state rows 32ks + {4q4+v, 16+4q4+v}, n = token
+    // One step from (x = A, x_prev = B), written over B:
+    //   x' = w x - tau w (H x + lam x - q) - (w-1) x_prev = ca x - tw (H x - q) + cd x_prev
+    // with H x = e^{Gk_t} H_c x + K~^T Z~^T, eight 16-row tiles in two groups of four
+    // (four independent accumulation chains keep the MFMA pipe busy; w <= 2 since
+    // c <= 1/4, so the hardware reciprocal suffices).
+    auto step = [&](f32x4 (&A)[8], f32x4 (&B)[8]) {
+      // x^T as B operands (hi + lo): k = state rows 32ks + {4q4+v, 16+4q4+v}, n = token
       f16x8 xh[4], xl[4];
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) h8_hilo(X[2 * ks], X[2 * ks + 1], xh[ks], xl[ks]);
-      // Z~^T[j][t] = m_tj (k~_j . x_t) for the keys j of tiles 0..wave, as hi/lo B operands
+      for (int ks = 0; ks < 4; ++ks) h8_hilo(A[2 * ks], A[2 * ks + 1], xh[ks], xl[ks], one);
+      // Z~^T[j][t] = m_tj (k~_j . x_t), as hi/lo B operands, over all four key tiles:
+      // the keys past this wave's tokens get m = 0.  Wave 3 needs all four and sets
+      // the block's pace, so the shorter ranges of waves 0-2 would save no time (two
+      // workgroups share each CU's SIMDs); one uniform instruction stream keeps the
+      // loop straight-line and small.
       f16x8 zh[2], zl[2];
       {
         f32x4 Z[4];
@@ -723,32 +812,19 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
         for (int ks = 0; ks < 4; ++ks) {
           f16x8 a[4];
 #pragma unroll
-          for (int jt = 0; jt < 4; ++jt)
-            if (jt <= wave) a[jt] = frag_perm_h(sK, LDQ, 16 * jt, 32 * ks, lane);
+          for (int jt = 0; jt < 4; ++jt) a[jt] = pfrag(sK, 16 * jt, 32 * ks, lane);
 #pragma unroll
-          for (int jt = 0; jt < 4; ++jt)
-            if (jt <= wave) Z[jt] = mfma16h(a[jt], xh[ks], Z[jt]);
+          for (int jt = 0; jt < 4; ++jt) Z[jt] = mfma16h(a[jt], xh[ks], Z[jt]);
 #pragma unroll
-          for (int jt = 0; jt < 4; ++jt)
-            if (jt <= wave) Z[jt] = mfma16h(a[jt], xl[ks], Z[jt]);
+          for (int jt = 0; jt < 4; ++jt) Z[jt] = mfma16h(a[jt], xl[ks], Z[jt]);
         }
-        // in-block decays m_tj = e^{Gk_t-Gk_j} (j <= t), formed again each iteration
-        // (cheaper than holding 16 more registers through the iteration)
 #pragma unroll
-        for (int jt = 0; jt < 4; ++jt) {
-          if (jt > wave) continue;
-          const f32x4 gkj = *reinterpret_cast<const f32x4*>(&SC(SC_GK, 16 * jt + 4 * q4));
+        for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
-          for (int v = 0; v < 4; ++v)
-            Z[jt][v] = (16 * jt + 4 * q4 + v <= tb) ? Z[jt][v] * fast_exp(GkT - gkj[v]) : 0.f;
-        }
-        h8_hilo(Z[0], Z[1], zh[0], zl[0]);
-        h8_hilo(Z[2], Z[3], zh[1], zl[1]);
+          for (int v = 0; v < 4; ++v) Z[jt][v] *= mz[jt][v];
+#pragma unroll
+        for (int jk = 0; jk < 2; ++jk) h8_hilo(Z[2 * jk], Z[2 * jk + 1], zh[jk], zl[jk], one);
       }
-      // x, x_prev <- w x - tau w (H x + lam x - q) - (w-1) x_prev, x, four 16-row tiles
-      // of H x = e^{Gk_t} H_c x + K~^T Z~^T at a time (four independent accumulation
-      // chains keep the MFMA pipe busy; w <= 2 since c <= 1/4, so the hardware
-      // reciprocal suffices)
       om = __builtin_amdgcn_rcpf(1.0f - cc * om);
       const float tw = tau * om, ca = om - tw * lam, cd = 1.0f - om;
 #pragma unroll
@@ -760,40 +836,46 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
         for (int ks = 0; ks < 4; ++ks) {
           f16x8 a[4];
 #pragma unroll
-          for (int u = 0; u < 4; ++u) a[u] = frag_perm_h(sH, LDQ, 16 * (g4 + u), 32 * ks, lane);
+          for (int u = 0; u < 4; ++u) a[u] = pfrag(sH, 16 * (g4 + u), 32 * ks, lane);
 #pragma unroll
           for (int u = 0; u < 4; ++u) hx[u] = mfma16h(a[u], xh[ks], hx[u]);
 #pragma unroll
           for (int u = 0; u < 4; ++u) hx[u] = mfma16h(a[u], xl[ks], hx[u]);
         }
+        // e^{Gk_t} H_c x - q, then the in-block part accumulates on top
 #pragma unroll
         for (int u = 0; u < 4; ++u)
 #pragma unroll
-          for (int v = 0; v < 4; ++v) hx[u][v] *= egk;
+          for (int v = 0; v < 4; ++v) hx[u][v] = egk * hx[u][v] - Q[g4 + u][v];
 #pragma unroll
         for (int jk = 0; jk < 2; ++jk) {
-          if (2 * jk > wave) continue;
           f16x8 a[4];
 #pragma unroll
-          for (int u = 0; u < 4; ++u) a[u] = frag_t_perm_h(sK, LDQ, 32 * jk, 16 * (g4 + u), lane);
+          for (int u = 0; u < 4; ++u) a[u] = pfrag_t<true>(sK, 32 * jk, 16 * (g4 + u), lane);
 #pragma unroll
           for (int u = 0; u < 4; ++u) hx[u] = mfma16h(a[u], zh[jk], hx[u]);
 #pragma unroll
           for (int u = 0; u < 4; ++u) hx[u] = mfma16h(a[u], zl[jk], hx[u]);
         }
-        // x' = w x - tau w (hx + lam x - q) - (w-1) x_prev = ca x - tw hx + tw q + cd x_prev
 #pragma unroll
         for (int u = 0; u < 4; ++u)
 #pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const int nt = g4 + u;
-            const float x = X[nt][v], xp = Xp[nt][v];
-            Xp[nt][v] = x;
-            X[nt][v] = ca * x - tw * (hx[u][v] - Q[nt][v]) + cd * xp;
-          }
+          for (int v = 0; v < 4; ++v)
+            B[g4 + u][v] = ca * A[g4 + u][v] + cd * B[g4 + u][v] - tw * hx[u][v];
         // bound the scheduler's hoisting of LDS operands to one group of tiles
         __builtin_amdgcn_sched_barrier(0);
       }
+    };
+    // two steps per trip, so x and x_prev trade registers instead of being copied
+    for (int it = 0; it < p.num_iter; it += 2) {
+      step(X, Xp);
+      if (it + 1 == p.num_iter) {
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) X[nt] = Xp[nt];
+        break;
+      }
+      step(Xp, X);
+    }
     }
     // alpha blend
     const float al = SC(SC_AL, tb);
@@ -817,33 +899,35 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
   {
     f16x8 xh[4], xl[4];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) h8_hilo(X[2 * ks], X[2 * ks + 1], xh[ks], xl[ks]);
+    for (int ks = 0; ks < 4; ++ks) h8_hilo(X[2 * ks], X[2 * ks + 1], xh[ks], xl[ks], one);
     const float GT = SC(SC_G, tb), eg = fast_exp(GT);
     // Z'^T[j][t] = e^{G_t-G_j} (k~_j . x^_t), j <= t
-    f32x4 Z[4];
+    f16x8 zb0, zb1 = {};
+    with_wave(wave, [&](auto Wc) {
+      constexpr int W = decltype(Wc)::value;
+      f32x4 Z[4];
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt) Z[jt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int jt = 0; jt < 4; ++jt) Z[jt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      f16x8 a[4];
+      for (int ks = 0; ks < 4; ++ks) {
+        f16x8 a[W + 1];
 #pragma unroll
-      for (int jt = 0; jt < 4; ++jt)
-        if (jt <= wave) a[jt] = frag_perm_h(sK, LDQ, 16 * jt, 32 * ks, lane);
+        for (int jt = 0; jt <= W; ++jt) a[jt] = pfrag(sK, 16 * jt, 32 * ks, lane);
 #pragma unroll
-      for (int jt = 0; jt < 4; ++jt)
-        if (jt <= wave) Z[jt] = mfma16h(a[jt], xh[ks], Z[jt]);
+        for (int jt = 0; jt <= W; ++jt) Z[jt] = mfma16h(a[jt], xh[ks], Z[jt]);
 #pragma unroll
-      for (int jt = 0; jt < 4; ++jt)
-        if (jt <= wave) Z[jt] = mfma16h(a[jt], xl[ks], Z[jt]);
-    }
-#pragma unroll
-    for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int j = 16 * jt + 4 * q4 + v;
-        Z[jt][v] = (jt <= wave && j <= tb) ? Z[jt][v] * fast_exp(GT - SC(SC_G, j)) : 0.f;
+        for (int jt = 0; jt <= W; ++jt) Z[jt] = mfma16h(a[jt], xl[ks], Z[jt]);
       }
-    const f16x8 zb0 = h8(Z[0], Z[1]), zb1 = h8(Z[2], Z[3]);
+#pragma unroll
+      for (int jt = 0; jt <= W; ++jt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int j = 16 * jt + 4 * q4 + v;
+          Z[jt][v] = (j <= tb) ? Z[jt][v] * fast_exp(GT - SC(SC_G, j)) : 0.f;
+        }
+      zb0 = h8(Z[0], Z[1]);
+      if constexpr (W >= 2) zb1 = h8(Z[2], Z[3]);
+    });
     // S_c into LDS (every wave is past its last read of H_c)
     state_store(sH, sst, fast_exp(off_g), tid);
     lds_barrier();
@@ -853,7 +937,7 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
       for (int nt = 0; nt < 8; ++nt) {
-        const f16x8 a = frag_perm_h(sH, LDQ, 16 * nt, 32 * ks, lane);
+        const f16x8 a = pfrag(sH, 16 * nt, 32 * ks, lane);
         O[nt] = mfma16h(a, xh[ks], O[nt]);
         O[nt] = mfma16h(a, xl[ks], O[nt]);
       }
@@ -863,8 +947,8 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
       for (int v = 0; v < 4; ++v) O[nt][v] *= eg;
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt) {
-      O[nt] = mfma16h(frag_t_perm_h(sV, LDQ, 0, 16 * nt, lane), zb0, O[nt]);
-      if (wave >= 2) O[nt] = mfma16h(frag_t_perm_h(sV, LDQ, 32, 16 * nt, lane), zb1, O[nt]);
+      O[nt] = mfma16h(pfrag_t<false>(sV, 0, 16 * nt, lane), zb0, O[nt]);
+      if (wave >= 2) O[nt] = mfma16h(pfrag_t<false>(sV, 32, 16 * nt, lane), zb1, O[nt]);
     }
   }
 
@@ -912,6 +996,7 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
     }
   }
 }
+
 }  // namespace solve
 
 }  // namespace gkap
