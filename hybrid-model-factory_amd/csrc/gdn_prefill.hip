@@ -68,10 +68,11 @@ constexpr int C = 32;          // chunk length (tokens)
 constexpr int MT = C / 16;     // 16-row tiles per chunk
 constexpr int D = 128;         // head dim (K == V == 128)
 constexpr int NTHR = 256;      // 4 waves
-// [C][128] row stride (k, q, v and O staging): 76 dwords = 12 mod 64 banks, so
-// the 16-row fragment reads (b128 / b64) and the 4-row transposing reads
-// (ds_read_b64_tr_b16) all hit distinct banks
-constexpr int LDQ = D + 24;
+// [C][128] row stride (k, q, v and O staging): 72 dwords = 8 mod 64 banks, which
+// makes the 128-bit row-fragment reads and the transposing reads of natural-order
+// rows (ds_read_b64_tr_b16) bank-conflict-free.  k and q are staged in the
+// interleaved feature order (icol), so every k / q operand is one 128-bit read.
+constexpr int LDQ = D + 16;
 constexpr int LDT = C + 8;     // [C][C] row stride (P, T blocks)
 static_assert(C == 32, "chunk length: the substitution and the g scan are written for 32");
 
@@ -264,10 +265,10 @@ __device__ __forceinline__ void stage_chunk(const Stage& st, const RawChunk& r, 
   for (int pass = 0; pass < MT; ++pass) {
     const int row = pass * 16 + (tid >> 4);
     const int f0 = (tid & 15) * 8;
-    *reinterpret_cast<f16x8*>(st.K + row * LDQ + f0) = scale_h8(r.k[pass], r.rk[pass]);
+    store8_i(st.K + row * LDQ, f0, scale_h8(r.k[pass], r.rk[pass]));
     if (MODE != MODE_PHI) *reinterpret_cast<bf16x8*>(st.V + row * LDQ + f0) = r.v[pass];
     if (MODE == MODE_OUT && with_q)
-      *reinterpret_cast<f16x8*>(st.Q + row * LDQ + f0) = scale_h8(r.q[pass], r.rq[pass]);
+      store8_i(st.Q + row * LDQ, f0, scale_h8(r.q[pass], r.rq[pass]));
   }
   if (wave == 0 && lane < C) {
     st.G[lane] = r.gs;
@@ -531,7 +532,7 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
           f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int ks = 0; ks < 4; ++ks)
-            acc = mfma16h(frag_h(X, LDQ, rx, 32 * ks, lane), frag_h(Y, LDQ, ry, 32 * ks, lane), acc);
+            acc = mfma16h(frag_i(X, LDQ, rx, 32 * ks, lane), frag_i(Y, LDQ, ry, 32 * ks, lane), acc);
           return acc;
         };
         if constexpr (R < MT) {
@@ -605,11 +606,11 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
           for (int ct = 0; ct < 2; ++ct) Sb[ct] = h8(S[2 * ks][ct], S[2 * ks + 1][ct]);
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) {
-            const f16x8 a = frag_perm_h(cur.K, LDQ, 16 * mt, 32 * ks, lane);
+            const f16x8 a = frag_i(cur.K, LDQ, 16 * mt, 32 * ks, lane);
 #pragma unroll
             for (int ct = 0; ct < 2; ++ct) X[mt][ct] = mfma16h(a, Sb[ct], X[mt][ct]);
             if constexpr (OQ) {
-              const f16x8 bq = frag_perm_h(cur.Q, LDQ, 16 * mt, 32 * ks, lane);
+              const f16x8 bq = frag_i(cur.Q, LDQ, 16 * mt, 32 * ks, lane);
 #pragma unroll
               for (int ct = 0; ct < 2; ++ct) QT[ct][mt] = mfma16h(Sb[ct], bq, QT[ct][mt]);
             }
@@ -715,7 +716,7 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
         }
 #pragma unroll
         for (int rt = 0; rt < 8; ++rt) {
-          const f16x8 a = frag_t_perm_h(cur.K, LDQ, 0, 16 * rt, lane);
+          const f16x8 a = frag_t_i(cur.K, LDQ, 0, 16 * rt, lane);
 #pragma unroll
           for (int ct = 0; ct < 2; ++ct) S[rt][ct] = mfma16h(a, Wb[ct], S[rt][ct]);
         }

@@ -456,44 +456,13 @@ __global__ __launch_bounds__(256) void gka_combine_kernel(Params p, int track_h)
 namespace solve {
 // LDS rows of H_c / S_c, k~ and v~ are 72 dwords apart (8 mod 64 banks): 128-bit
 // row-fragment reads (lane pairs q, q+1 of 8 rows share a cycle) and transposed
-// ds_read_b64_tr_b16 reads (8 rows of 8 dwords per 32 lanes) are then both
-// bank-conflict-free.  H_c, S_c and k~ keep their features in an interleaved order:
-// within each 32-feature block, 4-feature chunk m of half h sits at 8m + 4h, so one
-// 128-bit read at 8q returns features {4q..4q+3, 16+4q..16+4q+3} - the operand
-// order of two stacked C-layout tiles (x^T as a B operand) - where the natural
-// order needs two 64-bit reads.  v~ (read transposed only) keeps the natural order.
+// ds_read_b64_tr_b16 reads of natural-order rows (8 rows of 8 dwords per 32 lanes)
+// are then bank-conflict-free.  H_c, S_c and k~ keep their features in the
+// interleaved order (icol), so each of their MFMA operands is one 128-bit read;
+// v~ (read transposed only) keeps the natural order.
 constexpr int LDP = D + 16;
 constexpr int SZ_K = CB * LDP * 2;        // fp16 [64][LDP]
 constexpr int SZ_H = D * LDP * 2;         // fp16 [128][LDP]
-__device__ __forceinline__ int pcol(int f) {
-  return (f & ~31) | ((f & 12) << 1) | ((f & 16) >> 2) | (f & 3);
-}
-// A/B operand of interleaved rows r0..r0+15, k = k0 + {4q+v, 16+4q+v}
-__device__ __forceinline__ f16x8 pfrag(const f16* b, int r0, int k0, int lane) {
-  return *reinterpret_cast<const f16x8*>(b + (r0 + (lane & 15)) * LDP + k0 + 8 * (lane >> 4));
-}
-// transposed 16x16 read at rows row.., features c0 + 4(s&3).. (fcol maps a feature
-// to its stored column)
-template <bool INTERLEAVED>
-__device__ __forceinline__ f16x4 ld_tr_p(const f16* b, int row, int c0, int lane) {
-  const int s = lane & 15, f = c0 + 4 * (s & 3);
-  const f16* a = b + (row + (s >> 2)) * LDP + (INTERLEAVED ? pcol(f) : f);
-  const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(a));
-  return __builtin_bit_cast(f16x4, r);
-}
-// element (row c0 + l16, k) = b[t0 + k][c0 + l16], k in the perm order
-template <bool INTERLEAVED>
-__device__ __forceinline__ f16x8 pfrag_t(const f16* b, int t0, int c0, int lane) {
-  const int tq = t0 + 4 * (lane >> 4);
-  const f16x4 x = ld_tr_p<INTERLEAVED>(b, tq, c0, lane);
-  const f16x4 y = ld_tr_p<INTERLEAVED>(b, tq + 16, c0, lane);
-  return f16x8{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
-}
-// stores features f0..f0+7 (f0 a multiple of 8) of an interleaved row
-__device__ __forceinline__ void pstore8(f16* row, int f0, const f16x8& y) {
-  *reinterpret_cast<f16x4*>(row + pcol(f0)) = f16x4{y[0], y[1], y[2], y[3]};
-  *reinterpret_cast<f16x4*>(row + pcol(f0 + 4)) = f16x4{y[4], y[5], y[6], y[7]};
-}
 constexpr int OFF_K = 0;
 constexpr int OFF_V = OFF_K + SZ_K;
 constexpr int OFF_H = OFF_V + SZ_K;       // H_c, then S_c
@@ -555,7 +524,7 @@ __device__ __forceinline__ float state_store(f16* dst, const StateLd& L, float d
       ss += u * u;
       y[i] = (f16)u;
     }
-    pstore8(dst + r * LDP, c0 + 8 * j, y);
+    store8_i(dst + r * LDP, c0 + 8 * j, y);
   }
   return ss;
 }
@@ -624,7 +593,7 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
     const bf16x8 vr = ok ? *reinterpret_cast<const bf16x8*>(p.v + tok * p.kv_ts + hk * D + f0) : bf16x8{};
     const int64_t gi = tok * H + h;
     const float sk = key_scale(p, row_sumsq(kr), gi, ok);
-    pstore8(sK + row * LDP, f0, scale_h8(kr, sk));
+    store8_i(sK + row * LDP, f0, scale_h8(kr, sk));
     *reinterpret_cast<f16x8*>(sV + row * LDP + f0) = scale_h8(vr, beta_eps(p, gi, ok));
   }
   if (wave == 0) {
@@ -687,14 +656,14 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
       for (int nt = 0; nt < 8; ++nt) Pd[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        const f16x8 b = pfrag(sK, 16 * wave, 32 * ks, lane);
+        const f16x8 b = frag_i(sK, LDP, 16 * wave, 32 * ks, lane);
 #pragma unroll
-        for (int nt = 0; nt < 8; ++nt) Pd[nt] = mfma16h(pfrag(sH, 16 * nt, 32 * ks, lane), b, Pd[nt]);
+        for (int nt = 0; nt < 8; ++nt) Pd[nt] = mfma16h(frag_i(sH, LDP, 16 * nt, 32 * ks, lane), b, Pd[nt]);
       }
       float d = 0.f;
 #pragma unroll
       for (int nt = 0; nt < 8; ++nt) {
-        const f16x4 kk = *reinterpret_cast<const f16x4*>(sK + tb * LDP + pcol(16 * nt + 4 * q4));
+        const f16x4 kk = *reinterpret_cast<const f16x4*>(sK + tb * LDP + icol(16 * nt + 4 * q4));
 #pragma unroll
         for (int v = 0; v < 4; ++v) d += Pd[nt][v] * (float)kk[v];
       }
@@ -725,7 +694,7 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
           f32x4 kk = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int ks = 0; ks < 4; ++ks)
-            kk = mfma16h(pfrag(sK, 16 * J, 32 * ks, lane), pfrag(sK, 16 * I, 32 * ks, lane), kk);
+            kk = mfma16h(frag_i(sK, LDP, 16 * J, 32 * ks, lane), frag_i(sK, LDP, 16 * I, 32 * ks, lane), kk);
           f32x4 sq;
 #pragma unroll
           for (int v = 0; v < 4; ++v) sq[v] = kk[v] * kk[v];
@@ -812,7 +781,7 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
         for (int ks = 0; ks < 4; ++ks) {
           f16x8 a[4];
 #pragma unroll
-          for (int jt = 0; jt < 4; ++jt) a[jt] = pfrag(sK, 16 * jt, 32 * ks, lane);
+          for (int jt = 0; jt < 4; ++jt) a[jt] = frag_i(sK, LDP, 16 * jt, 32 * ks, lane);
 #pragma unroll
           for (int jt = 0; jt < 4; ++jt) Z[jt] = mfma16h(a[jt], xh[ks], Z[jt]);
 #pragma unroll
@@ -836,7 +805,7 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
         for (int ks = 0; ks < 4; ++ks) {
           f16x8 a[4];
 #pragma unroll
-          for (int u = 0; u < 4; ++u) a[u] = pfrag(sH, 16 * (g4 + u), 32 * ks, lane);
+          for (int u = 0; u < 4; ++u) a[u] = frag_i(sH, LDP, 16 * (g4 + u), 32 * ks, lane);
 #pragma unroll
           for (int u = 0; u < 4; ++u) hx[u] = mfma16h(a[u], xh[ks], hx[u]);
 #pragma unroll
@@ -851,7 +820,7 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
         for (int jk = 0; jk < 2; ++jk) {
           f16x8 a[4];
 #pragma unroll
-          for (int u = 0; u < 4; ++u) a[u] = pfrag_t<true>(sK, 32 * jk, 16 * (g4 + u), lane);
+          for (int u = 0; u < 4; ++u) a[u] = frag_t_i(sK, LDP, 32 * jk, 16 * (g4 + u), lane);
 #pragma unroll
           for (int u = 0; u < 4; ++u) hx[u] = mfma16h(a[u], zh[jk], hx[u]);
 #pragma unroll
@@ -912,7 +881,7 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
       for (int ks = 0; ks < 4; ++ks) {
         f16x8 a[W + 1];
 #pragma unroll
-        for (int jt = 0; jt <= W; ++jt) a[jt] = pfrag(sK, 16 * jt, 32 * ks, lane);
+        for (int jt = 0; jt <= W; ++jt) a[jt] = frag_i(sK, LDP, 16 * jt, 32 * ks, lane);
 #pragma unroll
         for (int jt = 0; jt <= W; ++jt) Z[jt] = mfma16h(a[jt], xh[ks], Z[jt]);
 #pragma unroll
@@ -937,7 +906,7 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
       for (int nt = 0; nt < 8; ++nt) {
-        const f16x8 a = pfrag(sH, 16 * nt, 32 * ks, lane);
+        const f16x8 a = frag_i(sH, LDP, 16 * nt, 32 * ks, lane);
         O[nt] = mfma16h(a, xh[ks], O[nt]);
         O[nt] = mfma16h(a, xl[ks], O[nt]);
       }
@@ -947,8 +916,8 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
       for (int v = 0; v < 4; ++v) O[nt][v] *= eg;
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt) {
-      O[nt] = mfma16h(pfrag_t<false>(sV, 0, 16 * nt, lane), zb0, O[nt]);
-      if (wave >= 2) O[nt] = mfma16h(pfrag_t<false>(sV, 32, 16 * nt, lane), zb1, O[nt]);
+      O[nt] = mfma16h(frag_t_perm_h(sV, LDP, 0, 16 * nt, lane), zb0, O[nt]);
+      if (wave >= 2) O[nt] = mfma16h(frag_t_perm_h(sV, LDP, 32, 16 * nt, lane), zb1, O[nt]);
     }
   }
 

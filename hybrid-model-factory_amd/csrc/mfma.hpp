@@ -185,6 +185,38 @@ __device__ __forceinline__ f16x8 frag_t_perm_h(const f16* base, int ld, int t0, 
   return f16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
+// Interleaved feature order for fp16 rows read as MFMA operands: within each
+// 32-feature block, 4-feature chunk m of half h is stored at 8m + 4h.  One 128-bit
+// read at 8q then returns features {4q..4q+3, 16+4q..16+4q+3}, the k order of a B
+// operand built from two stacked C-layout tiles (frag_perm_h's order), which the
+// natural order serves only with two 64-bit reads.  At a row stride of 72 dwords
+// (8 mod 64 banks) these 128-bit row-fragment reads are bank-conflict-free.
+__device__ __forceinline__ int icol(int f) {
+  return (f & ~31) | ((f & 12) << 1) | ((f & 16) >> 2) | (f & 3);
+}
+// rows r0..r0+15 of an interleaved array, k = k0 + {4q+v, 16+4q+v}
+__device__ __forceinline__ f16x8 frag_i(const f16* b, int ld, int r0, int k0, int lane) {
+  return *reinterpret_cast<const f16x8*>(b + (r0 + (lane & 15)) * ld + k0 + 8 * (lane >> 4));
+}
+// frag_t_perm_h of an interleaved array: element (row c0 + l16, k) = b[t0 + k][c0 + l16]
+__device__ __forceinline__ f16x4 ld_tr_i(const f16* b, int ld, int row, int c0, int lane) {
+  const int s = lane & 15;
+  const f16* a = b + (row + (s >> 2)) * ld + icol(c0 + 4 * (s & 3));
+  const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(a));
+  return __builtin_bit_cast(f16x4, r);
+}
+__device__ __forceinline__ f16x8 frag_t_i(const f16* b, int ld, int t0, int c0, int lane) {
+  const int tq = t0 + 4 * (lane >> 4);
+  const f16x4 x = ld_tr_i(b, ld, tq, c0, lane);
+  const f16x4 y = ld_tr_i(b, ld, tq + 16, c0, lane);
+  return f16x8{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+}
+// stores features f0..f0+7 (f0 a multiple of 8) of an interleaved row
+__device__ __forceinline__ void store8_i(f16* row, int f0, const f16x8& y) {
+  *reinterpret_cast<f16x4*>(row + icol(f0)) = f16x4{y[0], y[1], y[2], y[3]};
+  *reinterpret_cast<f16x4*>(row + icol(f0 + 4)) = f16x4{y[4], y[5], y[6], y[7]};
+}
+
 // Workgroup barrier that orders LDS only: global loads issued before it stay in
 // flight (the next chunk's prefetch), unlike __syncthreads().
 __device__ __forceinline__ void lds_barrier() {
