@@ -11,6 +11,7 @@ import ctypes
 import os
 from pathlib import Path
 
+import numpy as np
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libhmx.so"
@@ -57,6 +58,8 @@ SIGNATURES: dict[str, list] = {
                           _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32,
                           _I32, _F32, _F32, _I32, _P, ctypes.c_size_t, _P, _P],
     "hmx_gka_chunk_workspace_bytes": [_I32, _I32, _I32, _I32],
+    "hmx_plan_segments": [_I32, _P, _I32, _I32, _I64, _I32, _I32, _I32, _P, _I32, _P, _P],
+    "hmx_plan_segments_bounds": [_I32, _P, _I32, _I64, _I32, _I32, _I32, _P, _I32, _P, _P],
     "hmx_ssd_chunk_fwd": [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I32,
                           _P, _I32, _I64, _I64, _P, _P, _P, _P, _I64, _I64,
                           _P, _I64, _I64, _P, _P, _I64, _I32, _P, _P, _P, _I32, _I32,
@@ -139,6 +142,24 @@ def ptr(t: torch.Tensor | None):
 
 def stream_of(t: torch.Tensor):
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+PLAN_GDN, PLAN_GKA, PLAN_SSD = 0, 1, 2
+
+
+def plan_segments(op: int, bounds: list[tuple[int, int]], tokens: int, H: int, cu_count: int,
+                  segment_chunks: int | None = None) -> tuple[np.ndarray, int]:
+    """The segment table of a chunked prefill (hmx_plan_segments_bounds, host code)
+    as an int32 [rows, 8] array, and the chunks of all sequences."""
+    be = np.ascontiguousarray(np.asarray(bounds, dtype=np.int64).reshape(-1, 2))
+    nrows, nblk = ctypes.c_int32(0), ctypes.c_int32(0)
+    args = (op, be.ctypes.data_as(_P), len(be), int(tokens), int(H), int(cu_count),
+            int(segment_chunks or 0))
+    call("hmx_plan_segments_bounds", *args, None, 0, ctypes.byref(nrows), ctypes.byref(nblk))
+    table = np.empty((nrows.value, 8), dtype=np.int32)
+    call("hmx_plan_segments_bounds", *args, table.ctypes.data_as(_P), nrows.value,
+         ctypes.byref(nrows), ctypes.byref(nblk))
+    return table, nblk.value
 
 
 def require_gpu(*tensors: torch.Tensor | None) -> None:

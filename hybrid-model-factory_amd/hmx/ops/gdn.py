@@ -16,8 +16,8 @@ stream.  There is no CPU fallback.
 from __future__ import annotations
 
 import collections
-import heapq
 
+import numpy as np
 import torch
 
 from .. import _lib
@@ -214,15 +214,13 @@ def fused_recurrent_gated_delta_rule(q, k, v, g, beta=None, scale=None, initial_
     return o.reshape(B, T, H, V), (pool if output_final_state else None)
 
 
-# Segmented chunk-scan planning (host side).  A segment is a run of CHUNK-token
-# chunks of one sequence that one workgroup walks serially; more segments give
-# more parallelism at the cost of a short warm-up (or the exact scan) per
-# segment boundary.  CHUNK matches the kernel's internal chunk length.
-CHUNK = 32
-MIN_SEGMENT_CHUNKS = 16
+# Segmented chunk-scan planning.  A segment is a run of CHUNK-token chunks of one
+# sequence that one workgroup walks serially; more segments give more parallelism
+# at the cost of a short warm-up (or the exact scan) per segment boundary.  The
+# segment table comes from the library's host planner (hmx_plan_segments_bounds).
+CHUNK = 32               # the kernel's chunk length
 MAX_WARM_CHUNKS = 16
 DECAY_THRESHOLD = 60.0   # warm-up drops history bounded by exp(-60)
-WORKGROUPS_PER_CU = 2
 _CU_COUNT: dict[int, int] = {}
 
 
@@ -240,7 +238,10 @@ _SEG_CACHE_SIZE = 64
 def seq_bounds(cu_seqlens: torch.Tensor | None, B: int, T: int) -> list[tuple[int, int]]:
     """(bos, eos) of every sequence over the B*T flattened tokens: the B rows, or the
     cu_seqlens runs (B == 1).  Rejects cu_seqlens that do not start at 0, decrease,
-    or end past the tokens (ValueError), so no kernel reads or writes past them."""
+    or end past the tokens (ValueError), so no kernel reads or writes past them.
+    The kernels never read cu_seqlens itself: a host (CPU) tensor, such as vLLM's
+    query_start_loc_cpu, plans the call without a device-to-host copy; a device
+    tensor is read back once here."""
     if cu_seqlens is None:
         return [(n * T, n * T + T) for n in range(B)]
     cs = [int(x) for x in cu_seqlens.tolist()]
@@ -250,20 +251,21 @@ def seq_bounds(cu_seqlens: torch.Tensor | None, B: int, T: int) -> list[tuple[in
     return bounds
 
 
-def _device_table(rows: list[list[int]], device) -> torch.Tensor:
-    """The segment table as an int32 device tensor, without blocking the host.
+def _device_table(rows, device) -> torch.Tensor:
+    """An int32 host table (segment rows) as a device tensor, without blocking the host.
 
     A copy from pageable memory waits for the stream to drain, which leaves the
     GPU idle for the host's per-call work; the table is therefore staged in
     pinned memory (the copy is then asynchronous), and the device copies of the
     last few distinct tables are kept, so a repeated batch shape uploads nothing.
     Kernels only read the table."""
-    key = (str(device), tuple(map(tuple, rows)))
+    arr = np.ascontiguousarray(np.asarray(rows, dtype=np.int32))
+    key = (str(device), arr.shape, arr.tobytes())
     t = _SEG_CACHE.get(key)
     if t is not None:
         _SEG_CACHE.move_to_end(key)
         return t
-    host = torch.tensor(rows, dtype=torch.int32).pin_memory()
+    host = torch.from_numpy(arr.copy()).pin_memory()
     t = host.to(device, non_blocking=True)
     _SEG_CACHE[key] = t
     if len(_SEG_CACHE) > _SEG_CACHE_SIZE:
@@ -271,57 +273,13 @@ def _device_table(rows: list[list[int]], device) -> torch.Tensor:
     return t
 
 
-def _balanced_counts(chunks: list[int], budget: int, min_seg: int) -> list[int]:
-    """Segments per sequence, at most ``budget`` in all, given one at a time to the
-    sequence whose segments are currently the longest (the longest segment bounds
-    the runtime when all segments run at once), down to ``min_seg`` chunks."""
-    ns = [1] * len(chunks)
-    heap = [(-c, n) for n, c in enumerate(chunks)]
-    heapq.heapify(heap)
-    total = len(chunks)
-    while total < budget and heap:
-        neg, n = heapq.heappop(heap)
-        if -neg < 2 * min_seg or chunks[n] / (ns[n] + 1) < min_seg:
-            continue          # too short to split further
-        ns[n] += 1
-        total += 1
-        heapq.heappush(heap, (-chunks[n] / ns[n], n))
-    return ns
-
-
-def _segment_table(bounds: list[tuple[int, int]], H: int, workgroups: int,
-                   segment_chunks: int | None = None, chunk: int = CHUNK,
-                   warm_chunks: int = 3) -> list[list[int]]:
-    """Rows (n, bos, eos, c_start, c_end, seg_idx, first_seg, nseg) for every sequence,
-    over ``chunk``-token chunks.
-
-    With ``segment_chunks`` every sequence is cut into equal segments of at most
-    that many chunks (tests).  Otherwise the segment counts are balanced for
-    ``workgroups`` concurrent workgroups (``H`` per segment): one wave of segments
-    (at most workgroups / H per head) or two waves of shorter ones, whichever has
-    the smaller estimated makespan (the longest segment, plus ``warm_chunks`` of
-    warm-up for a split one, times the waves)."""
-    chunks = [-(-(eos - bos) // chunk) for bos, eos in bounds]
-    if segment_chunks is not None:
-        counts = [max(1, -(-nc // segment_chunks)) for nc in chunks]
-    else:
-        slots = max(1, workgroups // max(1, H))
-        best = None
-        for waves in (1, 2):
-            cnt = _balanced_counts(chunks, waves * slots, MIN_SEGMENT_CHUNKS)
-            longest = max((-(-nc // ns) + (warm_chunks if ns > 1 else 0)
-                           for nc, ns in zip(chunks, cnt)), default=0)
-            # segments beyond one wave of slots queue behind the first wave
-            est = longest * min(waves, -(-sum(cnt) // slots))
-            if best is None or est < best[0]:
-                best = (est, cnt)
-        counts = best[1]
-    rows: list[list[int]] = []
-    for n, ((bos, eos), nc, ns) in enumerate(zip(bounds, chunks, counts)):
-        first = len(rows)
-        for i in range(ns):
-            rows.append([n, bos, eos, i * nc // ns, (i + 1) * nc // ns, i, first, ns])
-    return rows
+def _segment_table(op: int, bounds: list[tuple[int, int]], tokens: int, H: int,
+                   device: torch.device, segment_chunks: int | None = None):
+    """The segment table (int32 [rows, 8]: n, bos, eos, c_start, c_end, seg_idx,
+    first_seg, nseg) and the total chunk count for prefill ``op`` on ``device``,
+    from the library's host planner.  With ``segment_chunks`` every sequence is cut
+    into equal segments of at most that many chunks (tests)."""
+    return _lib.plan_segments(op, bounds, tokens, H, _cu_count(device), segment_chunks)
 
 
 def chunk_gated_delta_rule_gqa(
@@ -382,7 +340,7 @@ def chunk_gated_delta_rule_gqa(
                              f"{len(cu_seqlens) - 1}")
     if scale is None:
         scale = k.shape[-1] ** -0.5
-    _lib.require_gpu(q, k, v, g, beta, initial_state, cu_seqlens)
+    _lib.require_gpu(q, k, v, g, beta, initial_state)    # cu_seqlens: host or device
     B, T, H, K = q.shape
     HKV, V = k.shape[2], v.shape[-1]
     if k.shape != (B, T, HKV, K) or v.shape[:3] != (B, T, HKV) or H % HKV != 0:
@@ -432,7 +390,7 @@ def chunk_gated_delta_rule_gqa(
         o = torch.empty(B, T, H, V, dtype=q.dtype, device=q.device)
     if cu_seqlens is not None and bounds and bounds[-1][1] < T:
         o[:, bounds[-1][1]:].zero_()  # tokens past the last sequence are not computed
-    rows = _segment_table(bounds, H, WORKGROUPS_PER_CU * _cu_count(q.device), _segment_chunks)
+    rows, _ = _segment_table(_lib.PLAN_GDN, bounds, B * T, H, q.device, _segment_chunks)
     seg = _device_table(rows, q.device)
     lib = _lib.load()
     ws_bytes = int(lib.hmx_gdn_chunk_workspace_bytes(len(rows), N, H, int(idx is not None)))

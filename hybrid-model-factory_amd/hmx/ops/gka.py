@@ -21,7 +21,6 @@ from .. import _lib
 from .gdn import (_cu_count, _device_table, _gate_rows, _i32, _segment_table, _token_rows,
                   seq_bounds)
 
-GKA_WORKGROUPS_PER_CU = 2   # the state walk's workgroups (segments) per CU
 GKA_BLOCK = 64              # tokens per block: the solve kernel's unit and the planner's chunk
 _warned_num_iter_zero = False
 
@@ -218,8 +217,8 @@ def _onorm(weight, gate, eps, shape, dtype):
 def _gka_prefill(q, k, v, alpha, g, gk, beta, gla_scale, ridge_ratio, num_iter, h_kk_initial,
                  h_kv_initial, output_final_state, cu_seqlens, l2norm, segment_chunks=None,
                  o_norm=(None, None, 1e-6), state_indices=None, has_initial_state=None, out=None):
-    _lib.require_gpu(q, k, v, alpha, g, gk, beta, h_kk_initial, h_kv_initial, cu_seqlens,
-                     state_indices, has_initial_state, out)
+    _lib.require_gpu(q, k, v, alpha, g, gk, beta, h_kk_initial, h_kv_initial,
+                     state_indices, has_initial_state, out)   # cu_seqlens: host or device
     B, T, H, D = q.shape
     HKV, V = k.shape[2], v.shape[-1]
     bounds = seq_bounds(cu_seqlens, B, T)
@@ -274,9 +273,7 @@ def _gka_prefill(q, k, v, alpha, g, gk, beta, gla_scale, ridge_ratio, num_iter, 
         o = torch.empty(B, T, H, V, dtype=q.dtype, device=q.device)
     if cu_seqlens is not None and bounds and bounds[-1][1] < T:
         o[:, bounds[-1][1]:].zero_()
-    rows = _segment_table(bounds, H, GKA_WORKGROUPS_PER_CU * _cu_count(q.device), segment_chunks,
-                          chunk=GKA_BLOCK)
-    nblk = sum(r[4] - r[3] for r in rows)
+    rows, nblk = _segment_table(_lib.PLAN_GKA, bounds, B * T, H, q.device, segment_chunks)
     seg = _device_table(rows, q.device)
     lib = _lib.load()
     ws_bytes = int(lib.hmx_gka_chunk_workspace_bytes(len(rows), nblk, N, H))

@@ -16,7 +16,6 @@ from .. import _lib
 from .gdn import _cu_count, _device_table, _segment_table, seq_bounds
 
 SSD_CHUNK = 64                 # the kernel's internal chunk length (tokens)
-SSD_WORKGROUPS_PER_CU = 2
 PAD_SLOT_ID = -1
 
 
@@ -89,8 +88,7 @@ def _ssd_scan(x, dt, A, B, C, D, z, dt_bias, dt_softplus, dt_limit, bounds, h0, 
         hT = (torch.empty(nseq, H, P, N, dtype=torch.float32, device=x.device)
               if want_final else None)
         st_ss, st_dt = H * P * N, _lib.HMX_F32
-    rows = _segment_table(bounds, H, SSD_WORKGROUPS_PER_CU * _cu_count(x.device), segment_chunks,
-                          chunk=SSD_CHUNK)
+    rows, _ = _segment_table(_lib.PLAN_SSD, bounds, x.shape[0], H, x.device, segment_chunks)
     seg = _device_table(rows, x.device)
     lib = _lib.load()
     ws_bytes = int(lib.hmx_ssd_chunk_workspace_bytes(len(rows), nseq, H, P, N))
@@ -139,7 +137,8 @@ def mamba_chunk_scan_combined(x, dt, A, B, C, chunk_size, D=None, z=None, dt_bia
         raise ValueError("return_varlen_states requires cu_seqlens")
     if cu_seqlens is not None and x.shape[0] != 1:
         raise ValueError(f"cu_seqlens needs batch size 1, got {x.shape[0]}")
-    _lib.require_gpu(x, dt, A, B, C, D, z, dt_bias, initial_states, seq_idx, cu_seqlens)
+    # seq_idx and cu_seqlens are read on the host only (a CPU tensor costs no copy)
+    _lib.require_gpu(x, dt, A, B, C, D, z, dt_bias, initial_states)
     b, l, H, P = x.shape
     G, N = B.shape[2], B.shape[3]
     if initial_states is not None and tuple(initial_states.shape) != (b, H, P, N):
@@ -225,7 +224,7 @@ def mamba_chunk_scan_combined_varlen(x, dt, A, B, C, chunk_size, cu_seqlens, cu_
     if return_intermediate_states:
         raise NotImplementedError("return_intermediate_states (prefix-cache chunk states) is "
                                   "not supported by the hmx SSD scan")
-    _lib.require_gpu(x, dt, A, B, C, D, z, dt_bias, initial_states, cu_seqlens, out)
+    _lib.require_gpu(x, dt, A, B, C, D, z, dt_bias, initial_states, out)   # cu_seqlens: host or device
     T, P = x.shape[0], x.shape[2]
     H = dt.shape[1]
     N = B.shape[-1]

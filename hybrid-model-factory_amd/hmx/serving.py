@@ -99,7 +99,17 @@ def _qkv(layer, x):
     return q, k, v
 
 
-def _split(md):
+def _host_prefill_offsets(num_decodes: int, query_start_loc_cpu):
+    """The prefill sequences' offsets from the host copy of the batch's
+    query_start_loc (decodes come first in the batch), so that the prefill plans
+    its segments without reading a device tensor back."""
+    if query_start_loc_cpu is None:
+        return None
+    q = query_start_loc_cpu[num_decodes:]
+    return q - q[0]
+
+
+def _split(md, query_start_loc_cpu=None):
     nd, ndt, npf = md.num_decodes, md.num_decode_tokens, md.num_prefills
     idx, has = md.non_spec_state_indices_tensor, md.has_initial_state
     mixed = nd > 0 and npf > 0
@@ -109,7 +119,9 @@ def _split(md):
         dec = (cu_d, idx[:nd] if mixed else idx)
     pre = None
     if npf > 0:
-        cu_p = md.non_spec_query_start_loc_p if mixed else md.non_spec_query_start_loc
+        cu_p = _host_prefill_offsets(nd, query_start_loc_cpu)
+        if cu_p is None:
+            cu_p = md.non_spec_query_start_loc_p if mixed else md.non_spec_query_start_loc
         pre = (cu_p, idx[nd:] if mixed else idx,
                None if has is None else (has[nd:] if mixed else has))
     return ndt, dec, pre
@@ -125,9 +137,11 @@ def _norm_args(o_norm, lo, hi):
 
 def gdn_forward_core(layer, mixed_qkv: torch.Tensor, b: torch.Tensor, a: torch.Tensor,
                      core_attn_out: torch.Tensor, attn_metadata, conv_state: torch.Tensor,
-                     ssm_state: torch.Tensor, *, o_norm=None) -> None:
+                     ssm_state: torch.Tensor, *, o_norm=None, query_start_loc_cpu=None) -> None:
     """primed_gdn_layer.py:635-936 over hmx ops (see the module docstring).
-    ``o_norm=(weight, z [tokens, H, V], eps)`` fuses the layer's output norm."""
+    ``o_norm=(weight, z [tokens, H, V], eps)`` fuses the layer's output norm;
+    ``query_start_loc_cpu`` (vLLM's host copy of the batch's query_start_loc) lets
+    the prefill plan without a device-to-host copy."""
     md = attn_metadata
     if md is None:
         return
@@ -140,7 +154,7 @@ def gdn_forward_core(layer, mixed_qkv: torch.Tensor, b: torch.Tensor, a: torch.T
     if getattr(layer, "allow_neg_eigval", False):
         beta = beta * 2.0
     out = core_attn_out[:n].unsqueeze(0)
-    ndt, dec, pre = _split(md)
+    ndt, dec, pre = _split(md, query_start_loc_cpu)
     if dec is not None:
         cu_d, idx_d = dec
         ops.fused_recurrent_gated_delta_rule_gqa(
@@ -160,9 +174,10 @@ def gdn_forward_core(layer, mixed_qkv: torch.Tensor, b: torch.Tensor, a: torch.T
 def gka_forward_core(layer, mixed_qkv: torch.Tensor, a: torch.Tensor, alpha_in: torch.Tensor,
                      b: torch.Tensor | None, core_attn_out: torch.Tensor, attn_metadata,
                      conv_state: torch.Tensor, h_kk_state: torch.Tensor,
-                     h_kv_state: torch.Tensor, *, o_norm=None) -> None:
+                     h_kv_state: torch.Tensor, *, o_norm=None, query_start_loc_cpu=None) -> None:
     """primed_gka_layer.py:962-1338 over hmx ops (see the module docstring).
-    ``o_norm=(weight, z [tokens, H, V], eps)`` fuses the layer's output norm."""
+    ``o_norm=(weight, z [tokens, H, V], eps)`` fuses the layer's output norm;
+    ``query_start_loc_cpu`` as for gdn_forward_core."""
     md = attn_metadata
     if md is None:
         return
@@ -188,7 +203,7 @@ def gka_forward_core(layer, mixed_qkv: torch.Tensor, a: torch.Tensor, alpha_in: 
         alpha = alpha + 0.5
     kk_gate = layer.use_forgetting_gate_kk
     out = core_attn_out[:n].unsqueeze(0)
-    ndt, dec, pre = _split(md)
+    ndt, dec, pre = _split(md, query_start_loc_cpu)
     sl = lambda t, lo, hi: None if t is None else t[:, lo:hi]
     common = dict(gla_scale=layer.gla_scale, ridge_ratio=layer.ridge_strength,
                   num_iter=layer.num_iter)
@@ -211,7 +226,7 @@ def gka_forward_core(layer, mixed_qkv: torch.Tensor, a: torch.Tensor, alpha_in: 
 
 def mamba2_conv_ssm_forward(layer, projected_states: torch.Tensor, output: torch.Tensor,
                             attn_metadata, conv_state: torch.Tensor,
-                            ssm_state: torch.Tensor) -> None:
+                            ssm_state: torch.Tensor, *, query_start_loc_cpu=None) -> None:
     """primed_mamba2_layer.py:615-1021 over hmx ops (see the module docstring).
 
     ``layer`` carries the reference's attributes (tped_intermediate_size,
@@ -223,7 +238,9 @@ def mamba2_conv_ssm_forward(layer, projected_states: torch.Tensor, output: torch
     prep_initial_states, query_start_loc_p); ``conv_state`` is
     ``kv_cache[0].transpose(-1, -2)`` and ``ssm_state`` ``kv_cache[1]``
     (:650-653).  Writes ``output[:num_actual_tokens]`` ([tokens, intermediate],
-    decodes first) and updates both pools in place."""
+    decodes first) and updates both pools in place.  ``query_start_loc_cpu``
+    (vLLM's host copy of the batch's query_start_loc) lets the prefill scan plan
+    without a device-to-host copy."""
     md = attn_metadata
     if md is None:
         raise NotImplementedError("the profile run (attn_metadata None) is not handled by the "
@@ -270,9 +287,11 @@ def mamba2_conv_ssm_forward(layer, projected_states: torch.Tensor, output: torch
         ops.conv.conv_fwd_rows(hbc[nd:n].t(), w, bias, conv_state, qsl, idx_p, has_c, act,
                                out=x[nd:])
         xp = x[nd:]
+        qsl_h = _host_prefill_offsets(nd, query_start_loc_cpu)
         ops.mamba_chunk_scan_combined_varlen(
             xp[:, :xb].view(-1, HX, P), dt[nd:n], layer.A, xp[:, xb:2 * xb].view(-1, HX, N),
-            xp[:, 2 * xb:].view(-1, H, N), layer.chunk_size, cu_seqlens=qsl, out=out[nd:],
+            xp[:, 2 * xb:].view(-1, H, N), layer.chunk_size,
+            cu_seqlens=qsl if qsl_h is None else qsl_h, out=out[nd:],
             D=layer.D, dt_bias=layer.dt_bias, initial_states=ssm_state, dt_softplus=True,
             dt_limit=(0.0, float("inf")), ssm_state_indices=idx_p, has_initial_state=has)
     if nd > 0:

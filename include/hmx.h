@@ -26,12 +26,13 @@
 extern "C" {
 #endif
 
-#define HMX_ABI_VERSION 5  /* 2: optional hmx_gated_norm output epilogue in the GDN ops;
+#define HMX_ABI_VERSION 6  /* 2: optional hmx_gated_norm output epilogue in the GDN ops;
                               3: q/k/v token strides in the GDN and GKA ops; slot-indexed
                               state pools and has_initial_state in the GDN, GKA and SSD
                               prefills;
                               4: grouped x heads (HX) and C groups (GC) in the SSD ops;
-                              5: nblock_total in hmx_gka_chunk_fwd and its workspace size */
+                              5: nblock_total in hmx_gka_chunk_fwd and its workspace size;
+                              6: host segment planner hmx_plan_segments(_bounds) */
 
 enum hmx_status {
   HMX_OK = 0,
@@ -113,6 +114,41 @@ int hmx_gdn_recurrent_fwd(const void* q, int64_t q_token_stride, const void* k,
                           float scale, int32_t use_qk_l2norm, int32_t inplace_final_state,
                           const hmx_gated_norm* o_norm, void* stream);
 
+/*
+ * Segment planner (host code: host pointers, no GPU access, no allocation the
+ * caller sees).  Builds the seg_table of hmx_gdn_chunk_fwd (op HMX_PLAN_GDN),
+ * hmx_gka_chunk_fwd (HMX_PLAN_GKA) and hmx_ssd_chunk_fwd (HMX_PLAN_SSD) from the
+ * sequence bounds, so a C/C++ caller drives the prefills without Python.  It
+ * replaces the reference's per-call varlen bookkeeping, the cu_seqlens ->
+ * chunk indices/offsets of vLLM's fla prepare_chunk_indices/_offsets
+ * (vllm-inference/src/primed_vllm/gka/ops/chebyshev_prefill_gqa.py:133-134, :299;
+ * inside each fla op that gdn/ops/chunk_gqa.py:63-81 passes cu_seqlens to); here
+ * it runs on host offsets (vLLM's query_start_loc_cpu), so the prefill needs no
+ * device-to-host copy.
+ *  cu_seqlens: host int64 [nseq+1] offsets over the B*T tokens (non-decreasing
+ *    from 0, ending <= B*T), or NULL for B sequences of T tokens (nseq == B).
+ *  cu_count: compute units of the device the prefill runs on
+ *    (hipDeviceAttributeMultiprocessorCount); the segment counts fill
+ *    2 * cu_count / H workgroup slots (one or two waves).
+ *  segment_chunks: > 0 cuts every sequence into equal segments of at most that
+ *    many chunks (32 tokens for GDN, 64 for GKA and SSD) instead.
+ *  table: host int32 [max_rows][8] rows (n, bos, eos, c_start, c_end, seg_idx,
+ *    first_seg, nseg), or NULL to query *nrows only.
+ *  nrows: rows of the plan (every sequence, even empty, has >= 1).
+ *  nblock_total (may be NULL): the chunks of all sequences (hmx_gka_chunk_fwd's
+ *    nblock_total for HMX_PLAN_GKA).
+ * HMX_EINVAL for malformed offsets or a table with fewer than *nrows rows.
+ */
+enum hmx_plan_op { HMX_PLAN_GDN = 0, HMX_PLAN_GKA = 1, HMX_PLAN_SSD = 2 };
+int hmx_plan_segments(int32_t op, const int64_t* cu_seqlens, int32_t nseq, int32_t B, int64_t T,
+                      int32_t H, int32_t cu_count, int32_t segment_chunks, int32_t* table,
+                      int32_t max_rows, int32_t* nrows, int32_t* nblock_total);
+/* The same from explicit (bos, eos) token ranges: host int64 [nseq][2], each
+ * within [0, tokens] (sequences need not be adjacent: the SSD scan's seq_idx
+ * runs). */
+int hmx_plan_segments_bounds(int32_t op, const int64_t* bos_eos, int32_t nseq, int64_t tokens,
+                             int32_t H, int32_t cu_count, int32_t segment_chunks, int32_t* table,
+                             int32_t max_rows, int32_t* nrows, int32_t* nblock_total);
 
 /*
  * GDN chunked prefill forward, GQA-native, varlen via a segment table (the kernel
@@ -132,7 +168,7 @@ int hmx_gdn_recurrent_fwd(const void* q, int64_t q_token_stride, const void* k,
  *  seg_table: int32 [nseg_total][8] rows (n, bos, eos, c_start, c_end, seg_idx,
  *    first_seg, nseg) - the chunks [c_start, c_end) of sequence n (tokens
  *    [bos, eos)) form segment seg_idx of nseg; rows sorted by sequence, every
- *    sequence (even empty) has >= 1 segment.  Built by the host from cu_seqlens.
+ *    sequence (even empty) has >= 1 segment.  Built by hmx_plan_segments.
  *  max_warm_chunks / decay_threshold: a segment's start state is recomputed
  *    from zero over at most max_warm_chunks preceding chunks when the dropped
  *    history is bounded below exp(-decay_threshold); otherwise the exact

@@ -170,16 +170,16 @@ def test_gka_prefill_c3_full_size(dev, num_iter):
     whole sequence vs the fp64 per-token recurrence (its block-batched form), with
     the output window around the first segment boundary the planner cuts, the whole
     output of both heads and their final h_kk / h_kv."""
+    from hmx import _lib
     from hmx.ops import gdn as gops
-    from hmx.ops.gka import GKA_BLOCK, GKA_WORKGROUPS_PER_CU
+    from hmx.ops.gka import GKA_BLOCK
     d = _c3_inputs()
     T, H = 32768, 32
     args = [d[n] for n in ("q", "k", "v", "alpha", "g", "gk", "beta")]
     o, hkk, hkv = hmx.gka_chebyshev_gla_prefill(*[a.to(dev) for a in args], 128 ** -0.5,
                                                 ridge_ratio=0.01, num_iter=num_iter)
     torch.cuda.synchronize()
-    rows = gops._segment_table([(0, T)], H, GKA_WORKGROUPS_PER_CU * gops._cu_count(dev),
-                               chunk=GKA_BLOCK)
+    rows, _ = gops._segment_table(_lib.PLAN_GKA, [(0, T)], T, H, dev)
     assert len(rows) > 1, "C3 is expected to run as several segments per head"
     edge = rows[1][3] * GKA_BLOCK           # first token of the second segment
     hs = [0, 17]

@@ -76,7 +76,8 @@ def _meta(kind, dev):
         spec_sequence_masks=None, num_actual_tokens=int(qsl[-1]), num_decodes=nd,
         num_decode_tokens=nd, num_prefills=len(plens), non_spec_query_start_loc=qsl.to(dev),
         non_spec_state_indices_tensor=idx.to(dev), has_initial_state=has.to(dev),
-        non_spec_query_start_loc_d=None, non_spec_query_start_loc_p=None)
+        non_spec_query_start_loc_d=None, non_spec_query_start_loc_p=None,
+        query_start_loc_cpu=qsl)
     if nd and plens:
         md.non_spec_query_start_loc_d = qsl[:nd + 1].to(dev)
         md.non_spec_query_start_loc_p = (qsl[nd:] - qsl[nd]).to(dev)
@@ -135,7 +136,7 @@ def _expected(kind, lay, md_lens, idx, has, nd, mixed_qkv, gates, conv_cache, st
     return torch.cat(outs), conv_new, st_new
 
 
-def _run(kind, batch, dev, o_norm=False, seed=1, **extra):
+def _run(kind, batch, dev, o_norm=False, seed=1, host_offsets=False, **extra):
     lay = _layer(kind, seed, **extra)
     md, lens, idx, has = _meta(batch, dev)
     nd = BATCHES[batch][0]
@@ -155,12 +156,14 @@ def _run(kind, batch, dev, o_norm=False, seed=1, **extra):
     if kind == "gdn":
         ssm = s1.to(dev)
         srv.gdn_forward_core(lay_d, mixed_qkv.to(dev), b.to(dev), a.to(dev), core, md,
-                             cc_d.transpose(1, 2), ssm, o_norm=onorm)
+                             cc_d.transpose(1, 2), ssm, o_norm=onorm,
+                             query_start_loc_cpu=md.query_start_loc_cpu if host_offsets else None)
         states_d, states, gates = [ssm], [s1], (a, b)
     else:
         hkv_d, hkk_d = s1.to(dev), hkk.to(dev)
         srv.gka_forward_core(lay_d, mixed_qkv.to(dev), a.to(dev), alpha_in.to(dev), b.to(dev),
-                             core, md, cc_d.transpose(1, 2), hkk_d, hkv_d, o_norm=onorm)
+                             core, md, cc_d.transpose(1, 2), hkk_d, hkv_d, o_norm=onorm,
+                             query_start_loc_cpu=md.query_start_loc_cpu if host_offsets else None)
         states_d, states, gates = [hkv_d, hkk_d], [s1, hkk], (a, alpha_in, b)
     torch.cuda.synchronize()
     return dict(lay=lay, md=md, lens=lens, idx=idx, has=has, nd=nd, n=n, pad=pad,
@@ -185,6 +188,17 @@ def test_forward_core_matches_oracle(dev, kind, batch):
                 assert_state_close(got[s], exp[s], what=f"slot {s}")
             else:
                 assert torch.equal(got[s], orig[s])
+
+
+@pytest.mark.parametrize("kind", ["gdn", "gka"])
+@pytest.mark.parametrize("batch", ["mixed", "prefill"])
+def test_forward_core_host_offsets_equal_device(dev, kind, batch):
+    """The prefill planned from the host copy of query_start_loc gives the same
+    outputs and states as from the device offsets."""
+    a, b = _run(kind, batch, dev), _run(kind, batch, dev, host_offsets=True)
+    assert torch.equal(a["core"], b["core"]) and torch.equal(a["cc"], b["cc"])
+    for x, y in zip(a["states_d"], b["states_d"]):
+        assert torch.equal(x, y)
 
 
 @pytest.mark.parametrize("kind", ["gdn", "gka"])

@@ -32,8 +32,8 @@ def _call(name, q, k, v, g, beta, h0, bounds, seg_chunks, workspace):
     dev = q.device
     H, HKV = q.shape[2], k.shape[2]
     N = len(bounds)
-    rows = gops._segment_table(bounds, H, 512, seg_chunks)
-    seg = torch.tensor(rows, dtype=torch.int32, device=dev)
+    rows, _ = _lib.plan_segments(_lib.PLAN_GDN, bounds, q.shape[0] * q.shape[1], H, 256, seg_chunks)
+    seg = torch.from_numpy(rows).to(dev)
     o = torch.zeros_like(q)
     ht = torch.zeros(N, H, 128, 128, device=dev)
     args = [_lib.ptr(q), H * 128, _lib.ptr(k), HKV * 128, _lib.ptr(v), HKV * 128, _lib.HMX_BF16,
