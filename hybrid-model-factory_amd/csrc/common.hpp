@@ -120,15 +120,86 @@ __device__ __forceinline__ float fast_exp(float x) {
   return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
 }
 
-// softplus with mamba's threshold (x for x > 20): max(x, 0) + log1p(e^{-|x|}),
-// log1p by Goldberg's correction log(w) u / (w - 1), w = 1 + u (exact for u
-// below w's rounding), on the hardware exp/log.
-__device__ __forceinline__ float softplus20(float x) {
-  if (x > 20.f) return x;
-  const float u = fast_exp(-fabsf(x));
+
+// ----------------------------------------------------------------------------
+// gates from the layer's raw projections (hmx_gate_proj): one definition for the
+// standalone gating kernels and the mixer kernels' fused loads, so both paths
+// give the same values
+// ----------------------------------------------------------------------------
+__device__ __forceinline__ float load_any(const void* p, int64_t i, int dtype) {
+  if (dtype == HMX_F32) return static_cast<const float*>(p)[i];
+  if (dtype == HMX_BF16) return (float)static_cast<const bf16*>(p)[i];
+  return (float)static_cast<const f16*>(p)[i];
+}
+
+// x as stored in a tensor of `dtype` and read back
+__device__ __forceinline__ float round_to(float x, int dtype) {
+  if (dtype == HMX_BF16) return (float)(bf16)x;
+  if (dtype == HMX_F16) return (float)(f16)x;
+  return x;
+}
+
+// log(1 + e^y) = max(y, 0) + log1p(e^{-|y|}), log1p by Goldberg's correction
+// log(w) u / (w - 1), w = 1 + u (exact for u below w's rounding), on the hardware
+// exp / log: a few fp32 ulps, cheap enough for the mixer kernels' gate loads
+__device__ __forceinline__ float softplus_core(float y) {
+  const float u = fast_exp(-fabsf(y));
   const float w = 1.f + u;
   const float l1p = (w == 1.f) ? u : __logf(w) * (u / (w - 1.f));
-  return fmaxf(x, 0.f) + l1p;
+  return fmaxf(y, 0.f) + l1p;
 }
+
+// softplus with mamba's threshold (x for x > 20)
+__device__ __forceinline__ float softplus20(float x) { return x > 20.f ? x : softplus_core(x); }
+
+// -exp(A_log) * softplus(x), softplus(x) = log(1 + e^{beta x}) / beta, or x past
+// the threshold (fused_gdn_gating.py:66-71); eA = exp(A_log)
+__device__ __forceinline__ float gate_decay_e(float eA, float x, float sp_beta, float threshold) {
+  const float bx = sp_beta * x;
+  const float sp = (bx <= threshold) ? softplus_core(bx) / sp_beta : x;
+  return -eA * sp;
+}
+__device__ __forceinline__ float gate_exp(float A_log) { return fast_exp(A_log); }
+__device__ __forceinline__ float gate_decay(float A_log, float x, float sp_beta, float threshold) {
+  return gate_decay_e(gate_exp(A_log), x, sp_beta, threshold);
+}
+
+__device__ __forceinline__ float gate_sigmoid(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + fast_exp(-x));
+}
+
+// the gates as the reference's gate tensors hold them, from the raw projection
+// values a, b, alpha_in of one token (eA_h, dtb_h: the head's exp(A_log) and dt_bias)
+__device__ __forceinline__ float gp_g_of(const hmx_gate_proj& gp, float a, float eA_h, float dtb_h) {
+  return round_to(gate_decay_e(eA_h, a + dtb_h, gp.softplus_beta, gp.softplus_threshold),
+                  gp.in_dtype);
+}
+__device__ __forceinline__ float gp_beta_of(const hmx_gate_proj& gp, float b) {
+  const float s = round_to(gate_sigmoid(b), gp.in_dtype);
+  return gp.beta_scale == 1.f ? s : round_to(s * gp.beta_scale, gp.in_dtype);
+}
+__device__ __forceinline__ float gp_alpha_of(const hmx_gate_proj& gp, float ai) {
+  if (gp.alpha_zero) return 0.f;
+  const float s = round_to(gate_sigmoid(ai), gp.in_dtype);
+  return gp.alpha_add == 0.f ? s : round_to(s + gp.alpha_add, gp.in_dtype);
+}
+// the same, loading token t, head h
+__device__ __forceinline__ float gp_g(const hmx_gate_proj& gp, int64_t t, int h) {
+  if (!gp.A_log) return 0.f;
+  return gp_g_of(gp, load_any(gp.a, t * gp.a_token_stride + h * gp.a_head_stride, gp.in_dtype),
+                 gate_exp(load_any(gp.A_log, h, gp.A_log_dtype)),
+                 load_any(gp.dt_bias, h, gp.dt_bias_dtype));
+}
+__device__ __forceinline__ float gp_beta(const hmx_gate_proj& gp, int64_t t, int h) {
+  return gp_beta_of(gp, load_any(gp.b, t * gp.b_token_stride + h * gp.b_head_stride, gp.in_dtype));
+}
+__device__ __forceinline__ float gp_alpha(const hmx_gate_proj& gp, int64_t t, int h) {
+  if (gp.alpha_zero) return 0.f;
+  return gp_alpha_of(gp, load_any(gp.alpha_in, t * gp.alpha_token_stride + h * gp.alpha_head_stride,
+                                  gp.in_dtype));
+}
+
+// host-side check of a gate descriptor
+int check_gates(const hmx_gate_proj* gp, bool gka, const char* what);
 
 }  // namespace hmx

@@ -9,12 +9,6 @@
 
 namespace hmx {
 
-__device__ __forceinline__ float load_any(const void* p, int64_t i, int dtype) {
-  if (dtype == HMX_F32) return static_cast<const float*>(p)[i];
-  if (dtype == HMX_BF16) return (float)static_cast<const bf16*>(p)[i];
-  return (float)static_cast<const f16*>(p)[i];
-}
-
 __device__ __forceinline__ void store_any(void* p, int64_t i, int dtype, float x) {
   if (dtype == HMX_F32) static_cast<float*>(p)[i] = x;
   else if (dtype == HMX_BF16) static_cast<bf16*>(p)[i] = (bf16)x;
@@ -31,10 +25,8 @@ __global__ __launch_bounds__(256) void gdn_gating_kernel(
     const int64_t t = i / H;
     const int h = (int)(i - t * H);
     const float x = load_any(a, t * as0 + h * as1, ab_dt) + load_any(dt_bias, h, db_dt);
-    const float bx = sp_beta * x;
-    const float sp = (bx <= threshold) ? log1pf(expf(bx)) / sp_beta : x;
-    const float gv = -expf(load_any(A_log, h, A_dt)) * sp;
-    const float bv = 1.0f / (1.0f + expf(-load_any(b, t * bs0 + h * bs1, ab_dt)));
+    const float gv = gate_decay(load_any(A_log, h, A_dt), x, sp_beta, threshold);
+    const float bv = gate_sigmoid(load_any(b, t * bs0 + h * bs1, ab_dt));
     store_any(g, i, out_dt, gv);
     store_any(beta, i, out_dt, bv);
   }
@@ -51,12 +43,27 @@ __global__ __launch_bounds__(256) void gka_gating_kernel(
     const int64_t t = i / H;
     const int h = (int)(i - t * H);
     const float x = load_any(a, t * as0 + h * as1, in_dt) + load_any(dt_bias, h, db_dt);
-    const float bx = sp_beta * x;
-    const float sp = (bx <= threshold) ? log1pf(expf(bx)) / sp_beta : x;
-    store_any(g, i, out_dt, -expf(load_any(A_log, h, A_dt)) * sp);
-    store_any(alpha, i, out_dt, 1.0f / (1.0f + expf(-load_any(ai, t * is0 + h * is1, in_dt))));
-    if (b) store_any(beta, i, out_dt, 1.0f / (1.0f + expf(-load_any(b, t * bs0 + h * bs1, in_dt))));
+    store_any(g, i, out_dt, gate_decay(load_any(A_log, h, A_dt), x, sp_beta, threshold));
+    store_any(alpha, i, out_dt, gate_sigmoid(load_any(ai, t * is0 + h * is1, in_dt)));
+    if (b) store_any(beta, i, out_dt, gate_sigmoid(load_any(b, t * bs0 + h * bs1, in_dt)));
   }
+}
+
+int check_gates(const hmx_gate_proj* gp, bool gka, const char* what) {
+  auto dt_ok = [](int d) { return d == HMX_F32 || d == HMX_BF16 || d == HMX_F16; };
+  HMX_REQUIRE(gp->a || !gp->A_log, HMX_EINVAL, "%s: gates.A_log needs gates.a", what);
+  HMX_REQUIRE(!gp->A_log || (gp->dt_bias && dt_ok(gp->A_log_dtype) && dt_ok(gp->dt_bias_dtype)),
+              HMX_EINVAL, "%s: gates.A_log needs gates.dt_bias (dtype codes 0-2)", what);
+  HMX_REQUIRE(dt_ok(gp->in_dtype), HMX_EUNSUPPORTED, "%s: gates.in_dtype code %d", what,
+              gp->in_dtype);
+  HMX_REQUIRE(gp->softplus_beta > 0.f, HMX_EINVAL, "%s: gates.softplus_beta must be > 0", what);
+  if (gka) {
+    HMX_REQUIRE(gp->alpha_in || gp->alpha_zero, HMX_EINVAL, "%s: gates.alpha_in is NULL", what);
+  } else {
+    HMX_REQUIRE(gp->A_log && gp->b, HMX_EINVAL, "%s: GDN gates need A_log, a, dt_bias and b",
+                what);
+  }
+  return HMX_OK;
 }
 
 }  // namespace hmx

@@ -28,6 +28,7 @@ struct RecurrentParams {
   int64_t q_ts, k_ts, v_ts;   // token strides (elements); heads are K (V for v) apart
   const void* g; int g_dt;
   const void* beta; int beta_dt; int beta_headwise;
+  hmx_gate_proj gp;          // ProjG kernels: g, beta from the raw projections
   void* o;
   const void* h0; int64_t h0_rs;
   void* ht; int64_t ht_rs;
@@ -51,9 +52,10 @@ __device__ __forceinline__ float load_scalar(const void* p, int64_t i, int dtype
 }
 
 // Loads of g and beta: a fixed element type (one code path, so the state and
-// per-token loads of a thread are all in flight together) or DynG (the dtype
-// code decides at run time).
+// per-token loads of a thread are all in flight together), DynG (the dtype code
+// decides at run time) or ProjG (formed from the layer's raw projections).
 struct DynG {};
+struct ProjG {};
 
 template <typename TG>
 __device__ __forceinline__ float load_gate(const void* p, int64_t i, int dtype) {
@@ -144,7 +146,12 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(RecurrentParams p) {
       }
     }
     load_vec<4>(static_cast<const TQ*>(p.v) + tok * p.v_ts + (int64_t)hk * V + col, vv);
-    const float gt = load_gate<TG>(p.g, tok * p.H + h, p.g_dt);
+    float gt;
+    if constexpr (std::is_same_v<TG, ProjG>) {
+      gt = gp_g(p.gp, tok, h);
+      bb[0] = bb[1] = bb[2] = bb[3] = gp_beta(p.gp, tok, h);
+    } else {
+    gt = load_gate<TG>(p.g, tok * p.H + h, p.g_dt);
     if (p.beta_headwise) {
 #pragma unroll
       for (int j = 0; j < 4; ++j)
@@ -152,6 +159,7 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(RecurrentParams p) {
     } else {
       const float bs = load_gate<TG>(p.beta, tok * p.H + h, p.beta_dt);
       bb[0] = bb[1] = bb[2] = bb[3] = bs;
+    }
     }
 
     float qs = p.scale;
@@ -239,7 +247,9 @@ static void launch(const RecurrentParams& p, int64_t N, hipStream_t s) {
   const dim3 grid((unsigned)(N * p.H), (unsigned)((waves + 3) / 4)),
       block(64 * (waves < 4 ? waves : 4));
   // typed g/beta paths for bf16 q/k/v with g and beta both fp32 or both bf16
-  if (std::is_same_v<TQ, bf16> && p.g_dt == p.beta_dt && p.g_dt == HMX_F32)
+  if (p.gp.a)
+    launch_g<K, TQ, TS, ProjG>(p, grid, block, s);
+  else if (std::is_same_v<TQ, bf16> && p.g_dt == p.beta_dt && p.g_dt == HMX_F32)
     launch_g<K, TQ, TS, float>(p, grid, block, s);
   else if (std::is_same_v<TQ, bf16> && p.g_dt == p.beta_dt && p.g_dt == HMX_BF16)
     launch_g<K, TQ, TS, bf16>(p, grid, block, s);
@@ -274,15 +284,21 @@ extern "C" int hmx_gdn_recurrent_fwd(
     const int32_t* cu_seqlens, const int32_t* ssm_state_indices, int64_t idx_stride,
     const int32_t* num_accepted_tokens, int64_t B, int64_t T, int64_t N, int32_t H, int32_t HKV,
     int32_t K, int32_t V, float scale, int32_t use_qk_l2norm, int32_t inplace_final_state,
-    const hmx_gated_norm* o_norm, void* stream) {
+    const hmx_gated_norm* o_norm, const hmx_gate_proj* gates, void* stream) {
   using namespace hmx;
   HMX_REQUIRE(H > 0 && HKV > 0 && H % HKV == 0, HMX_EINVAL,
               "hmx_gdn_recurrent_fwd: H=%d must be a positive multiple of HKV=%d", H, HKV);
+  if (gates) {
+    const int rc = check_gates(gates, false, "hmx_gdn_recurrent_fwd");
+    if (rc != HMX_OK) return rc;
+    HMX_REQUIRE(!beta_headwise, HMX_EINVAL,
+                "hmx_gdn_recurrent_fwd: gates give one beta per head (beta_headwise = 0)");
+  }
   HMX_REQUIRE(K == 64 || K == 128 || K == 256, HMX_EUNSUPPORTED,
               "hmx_gdn_recurrent_fwd: K=%d not in {64,128,256}", K);
   HMX_REQUIRE(V > 0 && V % 32 == 0 && V <= 256, HMX_EUNSUPPORTED,
               "hmx_gdn_recurrent_fwd: V=%d must be a multiple of 32 and <= 256", V);
-  HMX_REQUIRE(q && k && v && g && beta && o && ht, HMX_EINVAL,
+  HMX_REQUIRE(q && k && v && (gates || (g && beta)) && o && ht, HMX_EINVAL,
               "hmx_gdn_recurrent_fwd: null tensor pointer");
   HMX_REQUIRE(!inplace_final_state || ssm_state_indices, HMX_EINVAL,
               "hmx_gdn_recurrent_fwd: in-place final state needs ssm_state_indices");
@@ -291,8 +307,8 @@ extern "C" int hmx_gdn_recurrent_fwd(
   HMX_REQUIRE(cu_seqlens || N == B, HMX_EINVAL,
               "hmx_gdn_recurrent_fwd: N=%lld must equal B=%lld without cu_seqlens",
               (long long)N, (long long)B);
-  HMX_REQUIRE(g_dtype >= 0 && g_dtype <= 2 && beta_dtype >= 0 && beta_dtype <= 2, HMX_EUNSUPPORTED,
-              "hmx_gdn_recurrent_fwd: g/beta dtype");
+  HMX_REQUIRE(gates || (g_dtype >= 0 && g_dtype <= 2 && beta_dtype >= 0 && beta_dtype <= 2),
+              HMX_EUNSUPPORTED, "hmx_gdn_recurrent_fwd: g/beta dtype");
   HMX_REQUIRE(q_token_stride % 4 == 0 && k_token_stride % 4 == 0 && v_token_stride % 4 == 0 &&
                   ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) % 16 == 0,
               HMX_EINVAL, "hmx_gdn_recurrent_fwd: q/k/v token strides must be multiples of 4 "
@@ -302,6 +318,7 @@ extern "C" int hmx_gdn_recurrent_fwd(
   p.q = q; p.k = k; p.v = v; p.g = g; p.g_dt = g_dtype;
   p.q_ts = q_token_stride; p.k_ts = k_token_stride; p.v_ts = v_token_stride;
   p.beta = beta; p.beta_dt = beta_dtype; p.beta_headwise = beta_headwise;
+  p.gp = gates ? *gates : hmx_gate_proj{};
   p.o = o; p.h0 = h0; p.h0_rs = h0_row_stride; p.ht = ht; p.ht_rs = ht_row_stride;
   p.cu_seqlens = cu_seqlens; p.idx = ssm_state_indices; p.idx_stride = idx_stride;
   p.num_accepted = num_accepted_tokens; p.T = T; p.H = H; p.HKV = HKV; p.V = V;

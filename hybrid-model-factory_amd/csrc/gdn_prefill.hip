@@ -100,6 +100,7 @@ struct Params {
   int64_t q_ts, kv_ts;       // token strides (elements; k and v share one); heads are D apart
   const void* g; int g_dt;
   const void* beta; int beta_dt;
+  hmx_gate_proj gp; int fused;   // fused: g, beta from the raw projections in gp
   bf16* o;
   // States: slot sidx[n] (or n) of the h0 / ht bases, st_ss elements apart, in
   // st_dt (f32 or bf16); a negative slot or hinit[n] == 0 starts from zero, and a
@@ -153,6 +154,47 @@ __device__ __forceinline__ SegInfo load_seg(const int* seg, int s) {
   return SegInfo{r[0], r[1], r[2], r[3], r[4], r[5], r[6], r[7]};
 }
 
+// How a chunk's loaded gate bits become g and beta: as stored (g_dt / beta_dt),
+// or, with fused gates, from the raw projection bits (gp.in_dtype) and the head's
+// A_log and dt_bias.  Lanes past the sequence end hold NO_TOKEN (zero bits read
+// as a gate give g = 0, but a zero projection does not) and give g = beta = 0.
+constexpr uint32_t NO_TOKEN = 0xffffffffu;   // no 16-bit load yields it
+template <bool FG>
+struct GateConv {
+  const Params& p;
+  float eA_h, dtb_h;   // fused: the head's exp(A_log), dt_bias
+  __device__ __forceinline__ float g(uint32_t bits) const {
+    if constexpr (FG)
+      return bits == NO_TOKEN ? 0.f : gp_g_of(p.gp, bits_f32(bits, p.gp.in_dtype), eA_h, dtb_h);
+    else return bits_f32(bits, p.g_dt);
+  }
+  __device__ __forceinline__ float beta(uint32_t bits) const {
+    if constexpr (FG)
+      return bits == NO_TOKEN ? 0.f : gp_beta_of(p.gp, bits_f32(bits, p.gp.in_dtype));
+    else return bits_f32(bits, p.beta_dt);
+  }
+};
+template <bool FG>
+__device__ __forceinline__ GateConv<FG> gate_conv(const Params& p, int h) {
+  if constexpr (FG)
+    return GateConv<FG>{p, gate_exp(load_any(p.gp.A_log, h, p.gp.A_log_dtype)),
+                        load_any(p.gp.dt_bias, h, p.gp.dt_bias_dtype)};
+  else return GateConv<FG>{p, 0.f, 0.f};
+}
+// the token's gate bits as stored, or its raw projection bits (fused)
+template <bool FG>
+__device__ __forceinline__ void ld_gate_bits(const Params& p, int64_t tok, int h, uint32_t& gb,
+                                             uint32_t& bb) {
+  if constexpr (FG) {
+    gb = ld_bits(p.gp.a, tok * p.gp.a_token_stride + h * p.gp.a_head_stride, p.gp.in_dtype);
+    bb = ld_bits(p.gp.b, tok * p.gp.b_token_stride + h * p.gp.b_head_stride, p.gp.in_dtype);
+  } else {
+    const int64_t gi = tok * p.H + h;
+    gb = ld_bits(p.g, gi, p.g_dt);
+    bb = ld_bits(p.beta, gi, p.beta_dt);
+  }
+}
+
 // A sequence/head pair needs the exact segment scan when any of its later
 // segments found no warm-up start (plan == -1).
 __device__ __forceinline__ bool seq_exact(const int* plan, const SegInfo& si, int H, int h) {
@@ -173,7 +215,7 @@ struct RawChunk {
   float gs, eg, edl;
 };
 
-template <int MODE>
+template <int MODE, bool FG>
 __device__ __forceinline__ void load_raw(RawChunk& r, const Params& p, const bf16* qh,
                                          const bf16* kh, const bf16* vh, int tok0, int nval,
                                          bool need_q, int tid, int h) {
@@ -190,13 +232,8 @@ __device__ __forceinline__ void load_raw(RawChunk& r, const Params& p, const bf1
       r.q[pass] = (ok && need_q) ? *reinterpret_cast<const bf16x8*>(qh + tok * p.q_ts + f0)
                                  : bf16x8{};
   }
-  r.gb = 0u;
-  r.bb = 0u;
-  if (tid < nval && tid < C) {
-    const int64_t gi = (int64_t)(tok0 + tid) * p.H + h;
-    r.gb = ld_bits(p.g, gi, p.g_dt);
-    r.bb = ld_bits(p.beta, gi, p.beta_dt);
-  }
+  r.gb = r.bb = FG ? NO_TOKEN : 0u;
+  if (tid < nval && tid < C) ld_gate_bits<FG>(p, (int64_t)(tok0 + tid), h, r.gb, r.bb);
 }
 
 // One staged chunk in LDS.  K and Q hold the rows as the products use them, in
@@ -241,8 +278,9 @@ __device__ __forceinline__ void prep_rows(RawChunk& r, bool norm, float scale) {
 }
 
 // In-chunk cumsum of g and the decay factors (wave 0; lanes 0-31 = tokens).
-__device__ __forceinline__ void prep_scan(RawChunk& r, int lane, int g_dt) {
-  const float gv = scan32(lane < C ? bits_f32(r.gb, g_dt) : 0.f);
+template <bool FG>
+__device__ __forceinline__ void prep_scan(RawChunk& r, int lane, const GateConv<FG>& gc) {
+  const float gv = scan32(lane < C ? gc.g(r.gb) : 0.f);
   const float glast = __builtin_bit_cast(
       float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gv), C - 1));
   r.gs = gv;
@@ -258,9 +296,9 @@ __device__ __forceinline__ f16x8 scale_h8(const bf16x8& x, float s) {
 }
 
 // Write a prefetched, prepared chunk into staging buffer st.
-template <int MODE>
+template <int MODE, typename GC>
 __device__ __forceinline__ void stage_chunk(const Stage& st, const RawChunk& r, bool with_q,
-                                            int tid, int wave, int lane, int beta_dt) {
+                                            int tid, int wave, int lane, const GC& gc) {
 #pragma unroll
   for (int pass = 0; pass < MT; ++pass) {
     const int row = pass * 16 + (tid >> 4);
@@ -272,7 +310,7 @@ __device__ __forceinline__ void stage_chunk(const Stage& st, const RawChunk& r, 
   }
   if (wave == 0 && lane < C) {
     st.G[lane] = r.gs;
-    st.B[lane] = bits_f32(r.bb, beta_dt);
+    st.B[lane] = gc.beta(r.bb);
     st.EG[lane] = r.eg;
     st.EDL[lane] = r.edl;
   }
@@ -315,7 +353,7 @@ __device__ __forceinline__ f16x4 ld_blk(const f16* m, int r0, int c0, int lane) 
 // ---------------------------------------------------------------------------
 // NORM: the output rows pass through the gated RMSNorm of hmx_rms_norm_gated
 // (norm before gate) on their way out of sO.
-template <int MODE, bool NORM = false>
+template <int MODE, bool NORM = false, bool FG = false>
 __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
   __shared__ __align__(16) unsigned char smem[SMEM];
   bf16* sO = reinterpret_cast<bf16*>(smem + OFF_O);
@@ -328,6 +366,7 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int q4 = lane >> 4, l16 = lane & 15;
   const int s_id = blockIdx.x, h = blockIdx.y;
+  const GateConv<FG> gc = gate_conv<FG>(p, h);
   const SegInfo si = load_seg(p.seg, s_id);
   const int H = p.H;
   const int hk = h / (H / p.HKV);
@@ -479,14 +518,14 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
     RawChunk raw;
     {
       const int t0 = si.bos + c_begin * C;
-      load_raw<MODE>(raw, p, qh, kh, vh, t0, min(C, si.eos - t0), c_begin >= c_out,
+      load_raw<MODE, FG>(raw, p, qh, kh, vh, t0, min(C, si.eos - t0), c_begin >= c_out,
                      tid, h);
       prep_rows<MODE>(raw, p.l2norm, p.scale);
-      if (wave == 0) prep_scan(raw, lane, p.g_dt);
-      stage_chunk<MODE>(stage_at(smem, 0), raw, c_begin >= c_out, tid, wave, lane, p.beta_dt);
+      if (wave == 0) prep_scan(raw, lane, gc);
+      stage_chunk<MODE>(stage_at(smem, 0), raw, c_begin >= c_out, tid, wave, lane, gc);
       if (c_begin + 1 < si.c_end) {
         const int t1 = t0 + C;
-        load_raw<MODE>(raw, p, qh, kh, vh, t1, min(C, si.eos - t1),
+        load_raw<MODE, FG>(raw, p, qh, kh, vh, t1, min(C, si.eos - t1),
                        c_begin + 1 >= c_out, tid, h);
       }
     }
@@ -503,12 +542,11 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
       // to arrive; T blocks / P; K S and (Q S)^T; store the previous chunk's O -------
       if (c + 1 < si.c_end) {
         prep_rows<MODE>(raw, p.l2norm, p.scale);
-        if (wave == 0) prep_scan(raw, lane, p.g_dt);
-        stage_chunk<MODE>(stage_at(smem, bi ^ 1), raw, c + 1 >= c_out, tid, wave, lane,
-                          p.beta_dt);
+        if (wave == 0) prep_scan(raw, lane, gc);
+        stage_chunk<MODE>(stage_at(smem, bi ^ 1), raw, c + 1 >= c_out, tid, wave, lane, gc);
         if (c + 2 < si.c_end) {
           const int t2 = tok0 + 2 * C;
-          load_raw<MODE>(raw, p, qh, kh, vh, t2, min(C, si.eos - t2), c + 2 >= c_out, tid, h);
+          load_raw<MODE, FG>(raw, p, qh, kh, vh, t2, min(C, si.eos - t2), c + 2 >= c_out, tid, h);
         }
       }
       bf16x8 zr[MT];
@@ -772,9 +810,11 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
 // ---------------------------------------------------------------------------
 // plan: warm-up start chunk per (segment, head); exact flag per (sequence, head)
 // ---------------------------------------------------------------------------
+template <bool FG>
 __global__ __launch_bounds__(64) void gdn_plan_kernel(Params p) {
   const int s = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
   const int H = p.H;
+  const GateConv<FG> gc = gate_conv<FG>(p, h);
   const SegInfo si = load_seg(p.seg, s);
   int plan = 0;
   if (si.seg_idx > 0) {
@@ -786,9 +826,9 @@ __global__ __launch_bounds__(64) void gdn_plan_kernel(Params p) {
         const int t = si.bos + c * C + lane;
         float b = 0.f;
         if (lane < C && t < si.eos) {
-          const int64_t gi = (int64_t)t * H + h;
-          const float gv = ld_scalar(p.g, gi, p.g_dt);
-          const float bv = ld_scalar(p.beta, gi, p.beta_dt);
+          uint32_t gbits, bbits;
+          ld_gate_bits<FG>(p, t, h, gbits, bbits);
+          const float gv = gc.g(gbits), bv = gc.beta(bbits);
           b = gv + logf(fmaxf(1.f, fabsf(1.f - bv)));
         }
         acc += wave_sum(b);
@@ -893,17 +933,22 @@ extern "C" int hmx_gdn_chunk_fwd(const void* q, int64_t q_token_stride, const vo
                                  int32_t H, int32_t HKV, int32_t K, int32_t V, float scale,
                                  int32_t use_qk_l2norm, int32_t max_warm_chunks,
                                  float decay_threshold, void* workspace, size_t workspace_bytes,
-                                 const hmx_gated_norm* o_norm, void* stream) {
+                                 const hmx_gated_norm* o_norm, const hmx_gate_proj* gates,
+                                 void* stream) {
   HMX_REQUIRE(qkv_dtype == HMX_BF16, HMX_EUNSUPPORTED,
               "hmx_gdn_chunk_fwd: q/k/v must be bfloat16 (got dtype code %d)", qkv_dtype);
   HMX_REQUIRE(K == D && V == D, HMX_EUNSUPPORTED,
               "hmx_gdn_chunk_fwd: only K == V == 128 is supported (got K=%d V=%d)", K, V);
   HMX_REQUIRE(H > 0 && HKV > 0 && H % HKV == 0, HMX_EINVAL,
               "hmx_gdn_chunk_fwd: H=%d must be a positive multiple of HKV=%d", H, HKV);
-  HMX_REQUIRE(q && k && v && g && beta && o && seg_table, HMX_EINVAL,
+  HMX_REQUIRE(q && k && v && (gates || (g && beta)) && o && seg_table, HMX_EINVAL,
               "hmx_gdn_chunk_fwd: null tensor pointer");
-  HMX_REQUIRE(g_dtype >= 0 && g_dtype <= 2 && beta_dtype >= 0 && beta_dtype <= 2,
+  HMX_REQUIRE(gates || (g_dtype >= 0 && g_dtype <= 2 && beta_dtype >= 0 && beta_dtype <= 2),
               HMX_EUNSUPPORTED, "hmx_gdn_chunk_fwd: g/beta dtype");
+  if (gates) {
+    const int rc = check_gates(gates, false, "hmx_gdn_chunk_fwd");
+    if (rc != HMX_OK) return rc;
+  }
   HMX_REQUIRE(q_token_stride % 8 == 0 && k_token_stride % 8 == 0 && v_token_stride % 8 == 0 &&
                   ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)o) % 16 == 0,
               HMX_EINVAL, "hmx_gdn_chunk_fwd: q/k/v/o rows must be 16-byte aligned");
@@ -926,6 +971,8 @@ extern "C" int hmx_gdn_chunk_fwd(const void* q, int64_t q_token_stride, const vo
   p.v = static_cast<const bf16*>(v);
   p.q_ts = q_token_stride; p.kv_ts = k_token_stride;
   p.g = g; p.g_dt = g_dtype; p.beta = beta; p.beta_dt = beta_dtype;
+  p.fused = gates != nullptr;
+  p.gp = gates ? *gates : hmx_gate_proj{};
   p.o = static_cast<bf16*>(o); p.h0 = h0; p.ht = ht;
   p.st_ss = state_slot_stride; p.st_dt = state_dtype;
   p.sidx = state_indices; p.hinit = has_initial_state;
@@ -955,18 +1002,29 @@ extern "C" int hmx_gdn_chunk_fwd(const void* q, int64_t q_token_stride, const vo
   char* tail = ws + (multi ? 3 * st : 0) + (multi && pooled ? (size_t)N * H * D * D * 4 : 0);
   p.plan = reinterpret_cast<int*>(tail);
   hipStream_t s = (hipStream_t)stream;
+  const dim3 grid(nseg_total, H);
   if (multi) {
-    hipLaunchKernelGGL(gdn_plan_kernel, dim3(nseg_total, H), dim3(64), 0, s, p);
-    hipLaunchKernelGGL(gdn_chunk_kernel<MODE_S0>, dim3(nseg_total, H), dim3(NTHR), 0, s, p);
-    hipLaunchKernelGGL(gdn_chunk_kernel<MODE_PHI>, dim3(nseg_total, H), dim3(NTHR), 0, s, p);
+    if (p.fused) {
+      hipLaunchKernelGGL(gdn_plan_kernel<true>, grid, dim3(64), 0, s, p);
+      hipLaunchKernelGGL((gdn_chunk_kernel<MODE_S0, false, true>), grid, dim3(NTHR), 0, s, p);
+      hipLaunchKernelGGL((gdn_chunk_kernel<MODE_PHI, false, true>), grid, dim3(NTHR), 0, s, p);
+    } else {
+      hipLaunchKernelGGL(gdn_plan_kernel<false>, grid, dim3(64), 0, s, p);
+      hipLaunchKernelGGL(gdn_chunk_kernel<MODE_S0>, grid, dim3(NTHR), 0, s, p);
+      hipLaunchKernelGGL(gdn_chunk_kernel<MODE_PHI>, grid, dim3(NTHR), 0, s, p);
+    }
     hipLaunchKernelGGL(gdn_seg_combine_kernel, dim3(N * H, D / 16), dim3(NTHR), 0, s, p, N);
   } else {
     p.plan = nullptr;  // one segment per sequence: every segment starts from h0
   }
-  if (o_norm)
-    hipLaunchKernelGGL((gdn_chunk_kernel<MODE_OUT, true>), dim3(nseg_total, H), dim3(NTHR), 0, s, p);
+  if (o_norm && p.fused)
+    hipLaunchKernelGGL((gdn_chunk_kernel<MODE_OUT, true, true>), grid, dim3(NTHR), 0, s, p);
+  else if (o_norm)
+    hipLaunchKernelGGL((gdn_chunk_kernel<MODE_OUT, true>), grid, dim3(NTHR), 0, s, p);
+  else if (p.fused)
+    hipLaunchKernelGGL((gdn_chunk_kernel<MODE_OUT, false, true>), grid, dim3(NTHR), 0, s, p);
   else
-    hipLaunchKernelGGL(gdn_chunk_kernel<MODE_OUT>, dim3(nseg_total, H), dim3(NTHR), 0, s, p);
+    hipLaunchKernelGGL(gdn_chunk_kernel<MODE_OUT>, grid, dim3(NTHR), 0, s, p);
   if (staged) hipLaunchKernelGGL(gdn_state_copy_kernel, dim3(N, H), dim3(NTHR), 0, s, p);
   return check_launch("hmx_gdn_chunk_fwd");
 }
@@ -1029,7 +1087,8 @@ extern "C" int hmx_gdn_chunk_fwd_noalloc(
     int32_t state_dtype, const int32_t* state_indices, const uint8_t* has_initial_state,
     const int32_t* seg_table, int32_t nseg_total, int32_t N, int32_t H, int32_t HKV, int32_t K,
     int32_t V, float scale, int32_t use_qk_l2norm, int32_t max_warm_chunks,
-    float decay_threshold, const hmx_gated_norm* o_norm, void* stream) {
+    float decay_threshold, const hmx_gated_norm* o_norm, const hmx_gate_proj* gates,
+    void* stream) {
   HMX_REQUIRE(nseg_total >= 0 && N >= 0 && H > 0, HMX_EINVAL,
               "hmx_gdn_chunk_fwd_noalloc: bad sizes (nseg_total=%d N=%d H=%d)", nseg_total, N, H);
   if (nseg_total == 0) return HMX_OK;
@@ -1045,5 +1104,5 @@ extern "C" int hmx_gdn_chunk_fwd_noalloc(
                            g_dtype, beta, beta_dtype, o, h0, ht, state_slot_stride, state_dtype,
                            state_indices, has_initial_state, seg_table, nseg_total, N, H, HKV, K,
                            V, scale, use_qk_l2norm, max_warm_chunks, decay_threshold, ws,
-                           (size_t)HMX_GDN_CHUNK_SCRATCH_BYTES, o_norm, stream);
+                           (size_t)HMX_GDN_CHUNK_SCRATCH_BYTES, o_norm, gates, stream);
 }

@@ -24,12 +24,23 @@ namespace gkad {
 
 constexpr int D = 128;
 
+// The decode's gates from the raw projections.  Kept out of line, so every kernel
+// variant (with and without the output norm) runs the same instructions and
+// updates the states identically.
+__device__ __attribute__((noinline)) void proj_gates(const hmx_gate_proj& gp, int64_t t, int h,
+                                                     float& alpha, float& egk, float& bscale) {
+  alpha = gp_alpha(gp, t, h);
+  egk = gp.gk_from_g ? expf(gp_g(gp, t, h)) : 1.0f;
+  bscale = gp.b ? gp_beta(gp, t, h) + 1e-6f : 1.0f;
+}
+
 struct Params {
   const void* q; const void* k; const void* v;
   int64_t q_ts, k_ts, v_ts;           // token strides (elements); heads are D apart
   const void* alpha; int alpha_dt;
   const void* gk; int gk_dt;          // may be null (no decay)
   const void* beta; int beta_dt;      // may be null
+  hmx_gate_proj gp; int fused;        // fused: alpha, gk, beta from the raw projections
   void* o;
   const float* hkk_in; float* hkk_out; int64_t hkk_in_rs, hkk_out_rs;
   const void* hkv_in; void* hkv_out; int64_t hkv_in_rs, hkv_out_rs;
@@ -104,9 +115,14 @@ __global__ __launch_bounds__(256) void gka_decode_kernel(Params p) {
   load_vec<4>(qp + col, qc);
   load_vec<4>(vp + col, vc);
   const int64_t si = bos * p.H + h;
-  const float alpha = ld_scalar(p.alpha, si, p.alpha_dt);
-  const float egk = p.gk ? expf(ld_scalar(p.gk, si, p.gk_dt)) : 1.0f;
-  const float bscale = p.beta ? ld_scalar(p.beta, si, p.beta_dt) + 1e-6f : 1.0f;
+  float alpha, egk, bscale;
+  if (p.fused) {          // the gates from the layer's raw projections
+    proj_gates(p.gp, bos, h, alpha, egk, bscale);
+  } else {
+    alpha = ld_scalar(p.alpha, si, p.alpha_dt);
+    egk = p.gk ? expf(ld_scalar(p.gk, si, p.gk_dt)) : 1.0f;
+    bscale = p.beta ? ld_scalar(p.beta, si, p.beta_dt) + 1e-6f : 1.0f;
+  }
 
   float sk = 0.f, sq = 0.f;
 #pragma unroll
@@ -268,13 +284,17 @@ extern "C" int hmx_gka_decode_fwd(const void* q, int64_t q_token_stride, const v
                                   int64_t idx_stride, int64_t B, int64_t T, int64_t N, int32_t H,
                                   int32_t HKV, int32_t D, int32_t V, int32_t num_iter,
                                   float ridge_ratio, float scale, const hmx_gated_norm* o_norm,
-                                  void* stream) {
+                                  const hmx_gate_proj* gates, void* stream) {
   using namespace hmx;
+  if (gates) {
+    const int rc = check_gates(gates, true, "hmx_gka_decode_fwd");
+    if (rc != HMX_OK) return rc;
+  }
   HMX_REQUIRE(D == gkad::D && V == gkad::D, HMX_EUNSUPPORTED,
               "hmx_gka_decode_fwd: only D == V == 128 is supported (got D=%d V=%d)", D, V);
   HMX_REQUIRE(H > 0 && HKV > 0 && H % HKV == 0, HMX_EINVAL,
               "hmx_gka_decode_fwd: H=%d must be a positive multiple of HKV=%d", H, HKV);
-  HMX_REQUIRE(q && k && v && alpha && o && h_kk_in && h_kk_out && h_kv_in && h_kv_out, HMX_EINVAL,
+  HMX_REQUIRE(q && k && v && (alpha || gates) && o && h_kk_in && h_kk_out && h_kv_in && h_kv_out, HMX_EINVAL,
               "hmx_gka_decode_fwd: null tensor pointer");
   HMX_REQUIRE(num_iter >= 0, HMX_EINVAL, "hmx_gka_decode_fwd: num_iter=%d", num_iter);
   HMX_REQUIRE(cu_seqlens || N == B, HMX_EINVAL, "hmx_gka_decode_fwd: N != B without cu_seqlens");
@@ -288,6 +308,8 @@ extern "C" int hmx_gka_decode_fwd(const void* q, int64_t q_token_stride, const v
   p.q_ts = q_token_stride; p.k_ts = k_token_stride; p.v_ts = v_token_stride;
   p.alpha = alpha; p.alpha_dt = alpha_dtype; p.gk = gk; p.gk_dt = gk_dtype;
   p.beta = beta; p.beta_dt = beta_dtype; p.o = o;
+  p.fused = gates != nullptr;
+  p.gp = gates ? *gates : hmx_gate_proj{};
   p.hkk_in = h_kk_in; p.hkk_out = h_kk_out; p.hkk_in_rs = h_kk_in_row_stride;
   p.hkk_out_rs = h_kk_out_row_stride;
   p.hkv_in = h_kv_in; p.hkv_out = h_kv_out; p.hkv_in_rs = h_kv_in_row_stride;

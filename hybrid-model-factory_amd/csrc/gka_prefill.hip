@@ -73,6 +73,7 @@ struct Params {
   const void* g; int g_dt;
   const void* gk; int gk_dt;              // null: no h_kk decay
   const void* beta; int beta_dt;          // null: no beta
+  hmx_gate_proj gp; int fused;            // fused: the gates from the raw projections in gp
   bf16* o;
   // Sequence n's states: slot sidx[n] (or n) of the h_kk / h_kv pools; a negative
   // slot or hinit[n] == 0 starts from zero, and a negative slot writes nothing.
@@ -123,16 +124,37 @@ __device__ __forceinline__ float scan64(float x) {
   return (threadIdx.x & 63) >= 32 ? lo + carry : lo;
 }
 
+// Gate reads: the op's gate tensors, or (fused) the gates formed from the raw
+// projections in gp.  Token tok is the op's flattened token index.
+__device__ __forceinline__ bool has_beta(const Params& p) {
+  return p.fused ? p.gp.b != nullptr : p.beta != nullptr;
+}
+__device__ __forceinline__ bool has_gk(const Params& p) {
+  return p.fused ? p.gp.gk_from_g != 0 : p.gk != nullptr;
+}
+__device__ __forceinline__ float beta_at(const Params& p, int64_t tok, int h) {
+  return p.fused ? gp_beta(p.gp, tok, h) : ldsc(p.beta, tok * p.H + h, p.beta_dt);
+}
+__device__ __forceinline__ float g_at(const Params& p, int64_t tok, int h) {
+  return p.fused ? gp_g(p.gp, tok, h) : ldsc(p.g, tok * p.H + h, p.g_dt);
+}
+__device__ __forceinline__ float gk_at(const Params& p, int64_t tok, int h) {   // has_gk(p)
+  return p.fused ? gp_g(p.gp, tok, h) : ldsc(p.gk, tok * p.H + h, p.gk_dt);
+}
+__device__ __forceinline__ float alpha_at(const Params& p, int64_t tok, int h) {
+  return p.fused ? gp_alpha(p.gp, tok, h) : ldsc(p.alpha, tok * p.H + h, p.alpha_dt);
+}
+
 // The k~ scale of a row: (beta+1e-6) / |k| (or without the norm / without beta).
-__device__ __forceinline__ float key_scale(const Params& p, float ss, int64_t gi, bool ok) {
+__device__ __forceinline__ float key_scale(const Params& p, float ss, int64_t tok, int h, bool ok) {
   if (!ok) return 0.f;
-  const float be = p.beta ? ldsc(p.beta, gi, p.beta_dt) + EPS : 1.f;
+  const float be = has_beta(p) ? beta_at(p, tok, h) + EPS : 1.f;
   return p.l2norm ? be / sqrtf(ss) : be;
 }
 
-__device__ __forceinline__ float beta_eps(const Params& p, int64_t gi, bool ok) {
+__device__ __forceinline__ float beta_eps(const Params& p, int64_t tok, int h, bool ok) {
   if (!ok) return 0.f;
-  return p.beta ? ldsc(p.beta, gi, p.beta_dt) + EPS : 1.f;
+  return has_beta(p) ? beta_at(p, tok, h) + EPS : 1.f;
 }
 
 __device__ __forceinline__ f16x8 scale_h8(const bf16x8& x, float s) {
@@ -166,6 +188,7 @@ struct Raw {
   float g, gk;                // gates of token `lane` (lanes 0-31 of every wave)
 };
 
+template <bool FG>
 __device__ __forceinline__ void load_raw(Raw& r, const Params& p, const bf16* kh, const bf16* vh,
                                          int tok0, int nval, int tid, int h) {
 #pragma unroll
@@ -175,23 +198,43 @@ __device__ __forceinline__ void load_raw(Raw& r, const Params& p, const bf16* kh
     const int64_t tok = tok0 + row;
     r.k[pass] = ok ? *reinterpret_cast<const bf16x8*>(kh + tok * p.kv_ts + f0) : bf16x8{};
     r.v[pass] = ok ? *reinterpret_cast<const bf16x8*>(vh + tok * p.kv_ts + f0) : bf16x8{};
-    r.b[pass] = (ok && p.beta) ? ldsc(p.beta, tok * p.H + h, p.beta_dt) : 0.f;
+    // fused: b itself (the gate is formed at staging, so no load is waited for here)
+    r.b[pass] = !(ok && has_beta(p)) ? 0.f
+                : FG ? load_any(p.gp.b, tok * p.gp.b_token_stride + h * p.gp.b_head_stride,
+                                     p.gp.in_dtype)
+                          : ldsc(p.beta, tok * p.H + h, p.beta_dt);
   }
   const int lane = tid & 63;
   const bool okg = lane < nval && lane < CW;
-  const int64_t gi = (int64_t)(tok0 + lane) * p.H + h;
-  r.g = okg ? ldsc(p.g, gi, p.g_dt) : 0.f;
-  r.gk = (okg && p.gk) ? ldsc(p.gk, gi, p.gk_dt) : 0.f;
+  const int64_t tk = tok0 + lane, gi = tk * p.H + h;
+  if constexpr (FG) {     // a itself (fused: g and gk are formed at staging)
+    r.g = (okg && p.gp.A_log)
+              ? load_any(p.gp.a, tk * p.gp.a_token_stride + h * p.gp.a_head_stride, p.gp.in_dtype)
+              : 0.f;
+    r.gk = 0.f;
+  } else {
+    r.g = okg ? ldsc(p.g, gi, p.g_dt) : 0.f;
+    r.gk = (okg && p.gk) ? ldsc(p.gk, gi, p.gk_dt) : 0.f;
+  }
 }
 
 // Stage one chunk: rows as the update uses them (fp16, k~ and v~ with the decay to
 // the chunk end folded into the B-operand copies) and the chunk's gate sums.  Every
 // wave forms the 32 in-chunk cumsums itself (lanes 0-31) and hands each staging
 // lane its row's decay with a lane permute, so no LDS round trip is needed.
+template <bool FG>
 __device__ __forceinline__ void stage(const Stage& st, const Raw& r, const Params& p, int tid,
                                       int lane, int tok0, int nval, int h, bool track_h) {
-  const float G = scan32(lane < CW ? r.g : 0.f);
-  const float Gk = scan32(lane < CW ? r.gk : 0.f);
+  float gt = r.g, gkt = r.gk;
+  if constexpr (FG) {     // the gates from the raw a (lanes of valid tokens)
+    gt = (lane < nval && p.gp.A_log)
+             ? gp_g_of(p.gp, r.g, gate_exp(load_any(p.gp.A_log, h, p.gp.A_log_dtype)),
+                       load_any(p.gp.dt_bias, h, p.gp.dt_bias_dtype))
+             : 0.f;
+    gkt = p.gp.gk_from_g ? gt : 0.f;
+  }
+  const float G = scan32(lane < CW ? gt : 0.f);
+  const float Gk = scan32(lane < CW ? gkt : 0.f);
   const float GL = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, G), CW - 1));
   const float GkL = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, Gk), CW - 1));
   const float dl = fast_exp(GL - G), dlk = fast_exp(GkL - Gk);   // per token `lane`
@@ -200,7 +243,9 @@ __device__ __forceinline__ void stage(const Stage& st, const Raw& r, const Param
     const int row = pass * 16 + (tid >> 4), f0 = (tid & 15) * 8;
     const bool ok = row < nval;
     const float ss = row_sumsq(r.k[pass]);
-    const float be = ok ? (p.beta ? r.b[pass] + EPS : 1.f) : 0.f;
+    const float be = !ok ? 0.f
+                     : !has_beta(p) ? 1.f
+                     : (FG ? gp_beta_of(p.gp, r.b[pass]) : r.b[pass]) + EPS;
     const float sk = !ok ? 0.f : (p.l2norm ? be / sqrtf(ss) : be);
     const float sv = be;
     const float drow = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(row << 2, __builtin_bit_cast(int, dl)));
@@ -215,7 +260,7 @@ __device__ __forceinline__ void stage(const Stage& st, const Raw& r, const Param
   }
 }
 
-template <bool TRACK_H>
+template <bool TRACK_H, bool FG>
 __global__ __launch_bounds__(NTHR, 2) void gka_walk_kernel(Params p) {
   __shared__ __align__(16) unsigned char smem[SMEM];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -283,12 +328,12 @@ __global__ __launch_bounds__(NTHR, 2) void gka_walk_kernel(Params p) {
   if (t_begin < t_end) {
     // rows are prefetched two chunks ahead: ra holds chunk t0 + CW, rb chunk t0 + 2 CW
     Raw ra, rb;
-    load_raw(ra, p, kh, vh, t_begin, min(CW, t_end - t_begin), tid, h);
-    stage(stage_at(smem, 0), ra, p, tid, lane, t_begin, min(CW, t_end - t_begin), h, TRACK_H);
+    load_raw<FG>(ra, p, kh, vh, t_begin, min(CW, t_end - t_begin), tid, h);
+    stage<FG>(stage_at(smem, 0), ra, p, tid, lane, t_begin, min(CW, t_end - t_begin), h, TRACK_H);
     if (t_begin + CW < t_end)
-      load_raw(ra, p, kh, vh, t_begin + CW, min(CW, t_end - t_begin - CW), tid, h);
+      load_raw<FG>(ra, p, kh, vh, t_begin + CW, min(CW, t_end - t_begin - CW), tid, h);
     if (t_begin + 2 * CW < t_end)
-      load_raw(rb, p, kh, vh, t_begin + 2 * CW, min(CW, t_end - t_begin - 2 * CW), tid, h);
+      load_raw<FG>(rb, p, kh, vh, t_begin + 2 * CW, min(CW, t_end - t_begin - 2 * CW), tid, h);
     lds_barrier();
     int bi = 0;
     for (int t0 = t_begin; t0 < t_end; t0 += CW, bi ^= 1) {
@@ -296,10 +341,10 @@ __global__ __launch_bounds__(NTHR, 2) void gka_walk_kernel(Params p) {
       // stage the next chunk (its buffer was last read before the previous barrier)
       if (t0 + CW < t_end) {
         const int t1 = t0 + CW;
-        stage(stage_at(smem, bi ^ 1), ra, p, tid, lane, t1, min(CW, t_end - t1), h, TRACK_H);
+        stage<FG>(stage_at(smem, bi ^ 1), ra, p, tid, lane, t1, min(CW, t_end - t1), h, TRACK_H);
         ra = rb;
         if (t1 + 2 * CW < t_end)
-          load_raw(rb, p, kh, vh, t1 + 2 * CW, min(CW, t_end - t1 - 2 * CW), tid, h);
+          load_raw<FG>(rb, p, kh, vh, t1 + 2 * CW, min(CW, t_end - t1 - 2 * CW), tid, h);
       }
       // block start: the zero-start states so far (block 0 of a segment starts at zero)
       if (((t0 - t_begin) % CB) == 0) {
@@ -591,19 +636,19 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
     const int64_t tok = tok0 + row;
     const bf16x8 kr = ok ? *reinterpret_cast<const bf16x8*>(p.k + tok * p.kv_ts + hk * D + f0) : bf16x8{};
     const bf16x8 vr = ok ? *reinterpret_cast<const bf16x8*>(p.v + tok * p.kv_ts + hk * D + f0) : bf16x8{};
-    const int64_t gi = tok * H + h;
-    const float sk = key_scale(p, row_sumsq(kr), gi, ok);
+    const float sk = key_scale(p, row_sumsq(kr), tok, h, ok);
     store8_i(sK + row * LDP, f0, scale_h8(kr, sk));
-    *reinterpret_cast<f16x8*>(sV + row * LDP + f0) = scale_h8(vr, beta_eps(p, gi, ok));
+    *reinterpret_cast<f16x8*>(sV + row * LDP + f0) = scale_h8(vr, beta_eps(p, tok, h, ok));
   }
   if (wave == 0) {
     const bool ok = lane < nval;
-    const int64_t gi = (int64_t)(tok0 + lane) * H + h;
-    const float G = scan64(ok ? ldsc(p.g, gi, p.g_dt) : 0.f);
-    const float Gk = scan64((ok && p.gk) ? ldsc(p.gk, gi, p.gk_dt) : 0.f);
+    const int64_t tk = tok0 + lane;
+    const float gt = ok ? g_at(p, tk, h) : 0.f;
+    const float G = scan64(gt);
+    const float Gk = scan64((ok && has_gk(p)) ? (p.fused ? gt : gk_at(p, tk, h)) : 0.f);
     SC(SC_G, lane) = G;
     SC(SC_GK, lane) = Gk;
-    SC(SC_AL, lane) = ok ? ldsc(p.alpha, gi, p.alpha_dt) : 0.f;
+    SC(SC_AL, lane) = ok ? alpha_at(p, tk, h) : 0.f;
   }
   if (NORM && tid < D) {
     float wv;
@@ -1020,13 +1065,17 @@ extern "C" int hmx_gka_chunk_fwd(const void* q, int64_t q_token_stride, const vo
                                  int32_t D_, int32_t V, int32_t num_iter, float ridge_ratio,
                                  float scale, int32_t use_qk_l2norm, void* workspace,
                                  size_t workspace_bytes, const hmx_gated_norm* o_norm,
-                                 void* stream) {
+                                 const hmx_gate_proj* gates, void* stream) {
   HMX_REQUIRE(qkv_dtype == HMX_BF16, HMX_EUNSUPPORTED,
               "hmx_gka_chunk_fwd: q/k/v must be bfloat16 (got dtype code %d)", qkv_dtype);
+  if (gates) {
+    const int rc = check_gates(gates, true, "hmx_gka_chunk_fwd");
+    if (rc != HMX_OK) return rc;
+  }
   HMX_REQUIRE(D_ == D && V == D, HMX_EUNSUPPORTED,
               "hmx_gka_chunk_fwd: only D == V == 128 is supported (got D=%d V=%d)", D_, V);
   HMX_REQUIRE(H > 0 && HKV > 0 && H % HKV == 0, HMX_EINVAL, "hmx_gka_chunk_fwd: H/HKV");
-  HMX_REQUIRE(q && k && v && alpha && g && o && seg_table, HMX_EINVAL,
+  HMX_REQUIRE(q && k && v && (gates || (alpha && g)) && o && seg_table, HMX_EINVAL,
               "hmx_gka_chunk_fwd: null tensor pointer");
   HMX_REQUIRE(num_iter >= 0, HMX_EINVAL, "hmx_gka_chunk_fwd: num_iter=%d", num_iter);
   HMX_REQUIRE(nseg_total >= 0 && nblock_total >= 0, HMX_EINVAL,
@@ -1050,6 +1099,8 @@ extern "C" int hmx_gka_chunk_fwd(const void* q, int64_t q_token_stride, const vo
   p.v = static_cast<const bf16*>(v);
   p.alpha = alpha; p.alpha_dt = alpha_dtype; p.g = g; p.g_dt = g_dtype;
   p.gk = gk; p.gk_dt = gk_dtype; p.beta = beta; p.beta_dt = beta_dtype;
+  p.fused = gates != nullptr;
+  p.gp = gates ? *gates : hmx_gate_proj{};
   p.zg = nullptr; p.zg_ts = p.zg_hs = 0; p.onw = nullptr; p.onw_dt = HMX_F32; p.on_eps = 0.f;
   if (o_norm) {
     HMX_REQUIRE(o_norm->weight && o_norm->weight_dtype >= 0 && o_norm->weight_dtype <= 2,
@@ -1082,8 +1133,11 @@ extern "C" int hmx_gka_chunk_fwd(const void* q, int64_t q_token_stride, const vo
   p.segblk = reinterpret_cast<int*>(ws + wl.segblk);
   const bool solve_ = num_iter > 0;
   hipStream_t s = (hipStream_t)stream;
-  if (solve_) hipLaunchKernelGGL(walk::gka_walk_kernel<true>, dim3(nseg_total, H), dim3(NTHR), 0, s, p);
-  else hipLaunchKernelGGL(walk::gka_walk_kernel<false>, dim3(nseg_total, H), dim3(NTHR), 0, s, p);
+  const dim3 wgrid(nseg_total, H);
+  if (solve_ && p.fused) hipLaunchKernelGGL((walk::gka_walk_kernel<true, true>), wgrid, dim3(NTHR), 0, s, p);
+  else if (solve_) hipLaunchKernelGGL((walk::gka_walk_kernel<true, false>), wgrid, dim3(NTHR), 0, s, p);
+  else if (p.fused) hipLaunchKernelGGL((walk::gka_walk_kernel<false, true>), wgrid, dim3(NTHR), 0, s, p);
+  else hipLaunchKernelGGL((walk::gka_walk_kernel<false, false>), wgrid, dim3(NTHR), 0, s, p);
   hipLaunchKernelGGL(gka_combine_kernel, dim3(N * H, 16), dim3(256), 0, s, p, (int)solve_);
   if (nblock_total > 0) {
     const dim3 grid(nblock_total, H);

@@ -36,27 +36,27 @@ SIGNATURES: dict[str, list] = {
                               _P, _I64, _P, _I64, _I32,
                               _P, _P, _I64, _P,
                               _I64, _I64, _I64, _I32, _I32, _I32, _I32,
-                              _F32, _I32, _I32, _P, _P],
+                              _F32, _I32, _I32, _P, _P, _P],
     "hmx_gdn_chunk_fwd": [_P, _I64, _P, _I64, _P, _I64, _I32, _P, _I32, _P, _I32, _P,
                           _P, _P, _I64, _I32, _P, _P,
                           _P, _I32, _I32, _I32, _I32, _I32, _I32, _F32,
-                          _I32, _I32, _F32, _P, ctypes.c_size_t, _P, _P],
+                          _I32, _I32, _F32, _P, ctypes.c_size_t, _P, _P, _P],
     "hmx_gdn_chunk_workspace_bytes": [_I32, _I32, _I32, _I32],
     "hmx_gdn_chunk_fwd_noalloc": [_P, _I64, _P, _I64, _P, _I64, _I32, _P, _I32, _P, _I32, _P,
                                   _P, _P, _I64, _I32, _P, _P,
                                   _P, _I32, _I32, _I32, _I32, _I32, _I32, _F32,
-                                  _I32, _I32, _F32, _P, _P],
+                                  _I32, _I32, _F32, _P, _P, _P],
     "hmx_gka_gating": [_P, _I32, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I32, _P, _I32,
                        _P, _P, _P, _I32, _I64, _I32, _F32, _F32, _P],
     "hmx_gka_decode_fwd": [_P, _I64, _P, _I64, _P, _I64, _I32, _P, _I32, _P, _I32, _P, _I32, _P,
                            _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I32,
                            _P, _P, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _I32,
-                           _I32, _F32, _F32, _P, _P],
+                           _I32, _F32, _F32, _P, _P, _P],
     "hmx_gka_chunk_fwd": [_P, _I64, _P, _I64, _P, _I64, _I32, _P, _I32, _P, _I32, _P, _I32,
                           _P, _I32, _P,
                           _P, _P, _I64, _I32, _P, _P, _I64, _I32, _P, _P,
                           _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32,
-                          _I32, _F32, _F32, _I32, _P, ctypes.c_size_t, _P, _P],
+                          _I32, _F32, _F32, _I32, _P, ctypes.c_size_t, _P, _P, _P],
     "hmx_gka_chunk_workspace_bytes": [_I32, _I32, _I32, _I32],
     "hmx_plan_segments": [_I32, _P, _I32, _I32, _I64, _I32, _I32, _I32, _P, _I32, _P, _P],
     "hmx_plan_segments_bounds": [_I32, _P, _I32, _I64, _I32, _I32, _I32, _P, _I32, _P, _P],
@@ -100,6 +100,40 @@ def gated_norm(gate: torch.Tensor | None, weight: torch.Tensor, eps: float, V: i
                   0 if gate is None else gate.stride(0), 0 if gate is None else gate.stride(1),
                   ctypes.c_void_p(w.data_ptr()), dtype_code(w), float(eps))
     s._keep = (gate, w)   # the tensors outlive the call
+    return ctypes.pointer(s)
+
+
+class GateProj(ctypes.Structure):
+    """hmx_gate_proj (include/hmx.h): gates formed from the raw projections."""
+    _fields_ = [("A_log", _P), ("A_log_dtype", _I32), ("dt_bias", _P), ("dt_bias_dtype", _I32),
+                ("a", _P), ("a_token_stride", _I64), ("a_head_stride", _I64),
+                ("b", _P), ("b_token_stride", _I64), ("b_head_stride", _I64),
+                ("alpha_in", _P), ("alpha_token_stride", _I64), ("alpha_head_stride", _I64),
+                ("in_dtype", _I32), ("softplus_beta", _F32), ("softplus_threshold", _F32),
+                ("beta_scale", _F32), ("alpha_add", _F32), ("alpha_zero", _I32),
+                ("gk_from_g", _I32)]
+
+
+def gate_proj(pg):
+    """ctypes pointer to an hmx_gate_proj for an hmx.ops.ProjGates (None -> NULL)."""
+    if pg is None:
+        return None
+    ts = [t for t in (pg.a, pg.b, pg.alpha_in) if t is not None]
+    if not ts:
+        raise ValueError("ProjGates needs at least one of a, b, alpha_in")
+    in_dt = ts[0].dtype
+    for t in ts:
+        if t.dim() != 2 or t.dtype != in_dt:
+            raise ValueError("ProjGates a / b / alpha_in must be [tokens, heads] of one dtype")
+    require_gpu(pg.A_log, pg.dt_bias, *ts)
+    st = lambda t: (0, 0) if t is None else (t.stride(0), t.stride(1))
+    s = GateProj(ptr(pg.A_log), 0 if pg.A_log is None else dtype_code(pg.A_log),
+                 ptr(pg.dt_bias), 0 if pg.dt_bias is None else dtype_code(pg.dt_bias),
+                 ptr(pg.a), *st(pg.a), ptr(pg.b), *st(pg.b), ptr(pg.alpha_in), *st(pg.alpha_in),
+                 _DTYPE_CODE[in_dt], float(pg.softplus_beta), float(pg.softplus_threshold),
+                 float(pg.beta_scale), float(pg.alpha_add), int(bool(pg.alpha_zero)),
+                 int(bool(pg.gk_from_g)))
+    s._keep = (pg.A_log, pg.dt_bias, *ts)
     return ctypes.pointer(s)
 
 

@@ -21,6 +21,7 @@ import numpy as np
 import torch
 
 from .. import _lib
+from .gates import ProjGates
 
 
 def _i32(t: torch.Tensor | None) -> torch.Tensor | None:
@@ -92,6 +93,7 @@ def fused_recurrent_gated_delta_rule_gqa(
     o_norm_gate: torch.Tensor | None = None,
     o_norm_eps: float = 1e-5,
     out: torch.Tensor | None = None,
+    gates: ProjGates | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """GQA-native fused recurrent gated delta rule (decode).
 
@@ -107,17 +109,23 @@ def fused_recurrent_gated_delta_rule_gqa(
     optionally ``o_norm_gate`` [B,T,H,V], q.dtype) returns the layer's gated
     RMSNorm ``o_norm(o, z)`` (primed_gdn_layer.py:621-626) instead of o, fused into
     the kernel's output for V <= 128 (a separate hmx.rms_norm_gated call otherwise).
-    ``out`` [B,T,H,V] (q.dtype, contiguous) receives o when given.
+    ``out`` [B,T,H,V] (q.dtype, contiguous) receives o when given.  ``gates``
+    (hmx.ProjGates) forms g and beta in the kernel from the layer's raw
+    projections, in place of the gate tensors (g and beta are then ignored).
     """
     if cu_seqlens is not None and q.shape[0] != 1:
         raise ValueError(f"Batch size expected to be 1 with cu_seqlens, got {q.shape[0]}")
     if scale is None:
         scale = k.shape[-1] ** -0.5
-    if beta is None:
+    if gates is not None:
+        gates.check(q.shape[0] * q.shape[1], q.shape[2], gka=False)
+        g = beta = None
+    elif beta is None:
         beta = torch.ones_like(g)
     _lib.require_gpu(q, k, v, g, beta, initial_state, cu_seqlens, ssm_state_indices,
                      num_accepted_tokens)
-    g, beta = g.contiguous(), beta.contiguous()
+    if gates is None:
+        g, beta = g.contiguous(), beta.contiguous()
     (q, q_ts), (k, k_ts), (v, v_ts) = (_token_rows(x, 4) for x in (q, k, v))
     if not (q.dtype == k.dtype == v.dtype):
         raise AssertionError("q, k, v must share a dtype")
@@ -126,7 +134,7 @@ def fused_recurrent_gated_delta_rule_gqa(
     if k.shape != (B, T, HKV, K) or v.shape[:3] != (B, T, HKV) or H % HKV != 0:
         raise ValueError(f"bad GQA shapes q{tuple(q.shape)} k{tuple(k.shape)} v{tuple(v.shape)}")
     N = B if cu_seqlens is None else len(cu_seqlens) - 1
-    beta_headwise = beta.dim() == q.dim()
+    beta_headwise = beta is not None and beta.dim() == q.dim()
     if inplace_final_state:
         if initial_state is None or ssm_state_indices is None:
             raise ValueError("inplace_final_state=True needs initial_state (the state pool) "
@@ -164,8 +172,8 @@ def fused_recurrent_gated_delta_rule_gqa(
         raise ValueError("o_norm_gate needs o_norm_weight")
     _lib.call("hmx_gdn_recurrent_fwd",
               _lib.ptr(q), q_ts, _lib.ptr(k), k_ts, _lib.ptr(v), v_ts, _lib.dtype_code(q),
-              _lib.ptr(g), _lib.dtype_code(g),
-              _lib.ptr(beta), _lib.dtype_code(beta), int(beta_headwise),
+              _lib.ptr(g), 0 if g is None else _lib.dtype_code(g),
+              _lib.ptr(beta), 0 if beta is None else _lib.dtype_code(beta), int(beta_headwise),
               _lib.ptr(o),
               _lib.ptr(initial_state), 0 if initial_state is None else initial_state.stride(0),
               _lib.ptr(final_state), final_state.stride(0) if inplace_final_state else H * K * V,
@@ -173,7 +181,7 @@ def fused_recurrent_gated_delta_rule_gqa(
               _lib.ptr(_i32(cu_seqlens)), _lib.ptr(idx), idx_stride,
               _lib.ptr(_i32(num_accepted_tokens)),
               B, T, N, H, HKV, K, V, float(scale), int(bool(use_qk_l2norm_in_kernel)),
-              int(bool(inplace_final_state)), onorm, _lib.stream_of(q))
+              int(bool(inplace_final_state)), onorm, _lib.gate_proj(gates), _lib.stream_of(q))
     if norm_after:
         from .norm import rms_norm_gated
         normed = rms_norm_gated(o, o_norm_gate, o_norm_weight, eps=o_norm_eps)
@@ -300,6 +308,7 @@ def chunk_gated_delta_rule_gqa(
     ssm_state_indices: torch.Tensor | None = None,
     has_initial_state: torch.Tensor | None = None,
     out: torch.Tensor | None = None,
+    gates: ProjGates | None = None,
     _segment_chunks: int | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor | None]:
     """GQA-native chunked gated delta rule (prefill).
@@ -325,13 +334,19 @@ def chunk_gated_delta_rule_gqa(
       nothing.
     - ``has_initial_state`` [N] bool: sequences with False start from zero.
     - ``out`` [B,T,H,V] (q.dtype, contiguous): o is written there.
+    - ``gates`` (hmx.ProjGates): g and beta are formed in the kernel from the
+      layer's raw projections (A_log, dt_bias, a, b) instead of the gate tensors,
+      which are then ignored (fused_gdn_gating.py:79-125 and its launch fused away).
 
     q, k and v may be the column slices of one fused projection (token stride
     larger than heads x dim): they are read in place.
     """
     assert q.dtype == k.dtype == v.dtype
     assert q.dtype != torch.float32, "Does not support float32. Use bfloat16."
-    assert len(beta.shape) == 3, "beta must be [B, T, H]"
+    if gates is not None:
+        gates.check(q.shape[0] * q.shape[1], q.shape[2], gka=False)
+        g = beta = None
+    assert beta is None or len(beta.shape) == 3, "beta must be [B, T, H]"
     if cu_seqlens is not None and q.shape[0] != 1:
         raise ValueError(f"Batch size expected to be 1 with cu_seqlens, got {q.shape[0]}")
     if cu_seqlens is not None and initial_state is not None and ssm_state_indices is None:
@@ -345,7 +360,7 @@ def chunk_gated_delta_rule_gqa(
     HKV, V = k.shape[2], v.shape[-1]
     if k.shape != (B, T, HKV, K) or v.shape[:3] != (B, T, HKV) or H % HKV != 0:
         raise ValueError(f"bad GQA shapes q{tuple(q.shape)} k{tuple(k.shape)} v{tuple(v.shape)}")
-    if g.shape != (B, T, H) or beta.shape != (B, T, H):
+    if gates is None and (g.shape != (B, T, H) or beta.shape != (B, T, H)):
         raise ValueError(f"g {tuple(g.shape)} and beta {tuple(beta.shape)} must be [B,T,H]")
     bounds = seq_bounds(cu_seqlens, B, T)
     N = len(bounds)
@@ -377,7 +392,8 @@ def chunk_gated_delta_rule_gqa(
         if has_initial_state.shape != (N,):
             raise ValueError(f"has_initial_state must be [{N}], got {tuple(has_initial_state.shape)}")
         hinit = has_initial_state.to(torch.uint8).contiguous()
-    g, beta = g.contiguous(), beta.contiguous()
+    if gates is None:
+        g, beta = g.contiguous(), beta.contiguous()
     (q, q_ts), (k, k_ts), (v, v_ts) = (_token_rows(x, 8) for x in (q, k, v))
     if k_ts != v_ts:    # the prefill kernels read k and v at one token stride
         (k, k_ts), (v, v_ts) = _token_rows(k.contiguous(), 8), _token_rows(v.contiguous(), 8)
@@ -404,11 +420,12 @@ def chunk_gated_delta_rule_gqa(
         raise ValueError("o_norm_gate needs o_norm_weight")
     _lib.call("hmx_gdn_chunk_fwd",
               _lib.ptr(q), q_ts, _lib.ptr(k), k_ts, _lib.ptr(v), v_ts, _lib.dtype_code(q),
-              _lib.ptr(g), _lib.dtype_code(g), _lib.ptr(beta), _lib.dtype_code(beta),
+              _lib.ptr(g), 0 if g is None else _lib.dtype_code(g),
+              _lib.ptr(beta), 0 if beta is None else _lib.dtype_code(beta),
               _lib.ptr(o), _lib.ptr(h0), _lib.ptr(ht), st_ss, st_dt, _lib.ptr(idx),
               _lib.ptr(hinit), _lib.ptr(seg), len(rows), N, H, HKV, K, V, float(scale),
               int(bool(use_qk_l2norm_in_kernel)), MAX_WARM_CHUNKS, DECAY_THRESHOLD,
-              _lib.ptr(ws), ws.numel(), onorm, _lib.stream_of(q))
+              _lib.ptr(ws), ws.numel(), onorm, _lib.gate_proj(gates), _lib.stream_of(q))
     return o, ht
 
 

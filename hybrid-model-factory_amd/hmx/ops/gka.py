@@ -18,6 +18,7 @@ import logging
 import torch
 
 from .. import _lib
+from .gates import ProjGates
 from .gdn import (_cu_count, _device_table, _gate_rows, _i32, _segment_table, _token_rows,
                   seq_bounds)
 
@@ -69,7 +70,7 @@ def chebyshev_iteration_gqa(k, q, v, alpha, gk=None, beta=None, num_iter: int = 
                             output_final_state: bool = True, inplace_final_state: bool = True,
                             cu_seqlens=None, ssm_state_indices=None, *,
                             o_norm_weight=None, o_norm_gate=None, o_norm_eps: float = 1e-6,
-                            out=None):
+                            out=None, gates: ProjGates | None = None):
     """Fused GKA decode step (chebyshev_iteration_gqa.py:173-238).
 
     k [B,T,HKV,D]; q [B,T,H,D]; v [B,T,HKV,V]; alpha, gk, beta [B,T,H].
@@ -80,8 +81,13 @@ def chebyshev_iteration_gqa(k, q, v, alpha, gk=None, beta=None, num_iter: int = 
     Keyword-only extension (no reference counterpart): ``o_norm_weight`` [V] (and
     optionally ``o_norm_gate`` [B,T,H,V], q.dtype) returns the layer's gated
     RMSNorm ``o_norm(o, z)`` (primed_gka_layer.py:944-949) fused into the kernel's
-    output instead of o; ``out`` [B,T,H,V] (q.dtype, contiguous) receives o.
+    output instead of o; ``out`` [B,T,H,V] (q.dtype, contiguous) receives o;
+    ``gates`` (hmx.ProjGates) forms alpha, gk and beta in the kernel from the
+    layer's raw projections (the gate tensors are then ignored).
     """
+    if gates is not None:
+        gates.check(q.shape[0] * q.shape[1], q.shape[2], gka=True)
+        alpha = gk = beta = None
     if cu_seqlens is not None and q.shape[0] != 1:
         raise ValueError(f"Batch size must be 1 when using cu_seqlens, got {q.shape[0]}.")
     B, T, H, D = q.shape
@@ -101,7 +107,7 @@ def chebyshev_iteration_gqa(k, q, v, alpha, gk=None, beta=None, num_iter: int = 
         if tuple(st.shape[1:]) != (H, D, last) or not st[0].is_contiguous():
             raise ValueError(f"state must be [rows,{H},{D},{last}] with contiguous rows, "
                              f"got {tuple(st.shape)}")
-    alpha = alpha.contiguous()
+    alpha = None if alpha is None else alpha.contiguous()
     (q, q_ts), (k, k_ts), (v, v_ts) = (_token_rows(x, 4) for x in (q, k, v))
     gk = None if gk is None else gk.contiguous()
     beta = None if beta is None else beta.contiguous()
@@ -121,7 +127,7 @@ def chebyshev_iteration_gqa(k, q, v, alpha, gk=None, beta=None, num_iter: int = 
     onorm = _onorm(o_norm_weight, o_norm_gate, o_norm_eps, (B, T, H, V), q.dtype)
     _lib.call("hmx_gka_decode_fwd",
               _lib.ptr(q), q_ts, _lib.ptr(k), k_ts, _lib.ptr(v), v_ts, _lib.dtype_code(q),
-              _lib.ptr(alpha), _lib.dtype_code(alpha),
+              _lib.ptr(alpha), 0 if alpha is None else _lib.dtype_code(alpha),
               _lib.ptr(gk), 0 if gk is None else _lib.dtype_code(gk),
               _lib.ptr(beta), 0 if beta is None else _lib.dtype_code(beta),
               _lib.ptr(o),
@@ -129,7 +135,7 @@ def chebyshev_iteration_gqa(k, q, v, alpha, gk=None, beta=None, num_iter: int = 
               _lib.ptr(hkv), hkv.stride(0), _lib.ptr(hkv), hkv.stride(0), _lib.dtype_code(hkv),
               _lib.ptr(_i32(cu_seqlens)), _lib.ptr(idx), 0 if idx is None else idx.stride(0),
               B, T, N, H, HKV, D, V, int(num_iter), float(ridge_ratio), float(scale),
-              onorm, _lib.stream_of(q))
+              onorm, _lib.gate_proj(gates), _lib.stream_of(q))
     if not output_final_state:
         return o, None, None
     if not inplace_final_state and idx is not None:
@@ -143,9 +149,9 @@ def gka_chebyshev_gla_decode(q, k, v, alpha, g, gk, beta, gla_scale: float,
                              num_iter: int = 30, gka=None, h_kk=None, h_kv=None,
                              cu_seqlens=None, ssm_state_indices=None, *,
                              o_norm_weight=None, o_norm_gate=None, o_norm_eps: float = 1e-6,
-                             out=None):
-    """Single-token GKA decode (gka_forward.py:248-326).  ``o_norm_*`` and ``out``:
-    see chebyshev_iteration_gqa."""
+                             out=None, gates: ProjGates | None = None):
+    """Single-token GKA decode (gka_forward.py:248-326).  ``o_norm_*``, ``out`` and
+    ``gates``: see chebyshev_iteration_gqa."""
     global _warned_num_iter_zero
     _check_sketching_constraints(gka, num_sketches_per_head, "gka_chebyshev_gla_decode")
     if num_iter == 0:
@@ -154,14 +160,17 @@ def gka_chebyshev_gla_decode(q, k, v, alpha, g, gk, beta, gla_scale: float,
                             "Ensure alpha is zeroed out by the caller to skip query correction.")
             _warned_num_iter_zero = True
         num_iter = 1
-    assert g is gk, "GLA gate g not equal to GKA gate gk is not supported for decoding."
+    if gates is None:
+        assert g is gk, "GLA gate g not equal to GKA gate gk is not supported for decoding."
+    elif not gates.gk_from_g and gates.A_log is not None:
+        raise AssertionError("GLA gate g not equal to GKA gate gk is not supported for decoding.")
     return chebyshev_iteration_gqa(k=k, q=q, v=v, alpha=alpha, gk=gk, beta=beta,
                                    num_iter=num_iter, scale=gla_scale, ridge_ratio=ridge_ratio,
                                    initial_state_kk=h_kk, initial_state_kv=h_kv,
                                    output_final_state=True, inplace_final_state=True,
                                    cu_seqlens=cu_seqlens, ssm_state_indices=ssm_state_indices,
                                    o_norm_weight=o_norm_weight, o_norm_gate=o_norm_gate,
-                                   o_norm_eps=o_norm_eps, out=out)
+                                   o_norm_eps=o_norm_eps, out=out, gates=gates)
 
 
 def gka_chebyshev_gla_prefill(q, k, v, alpha, g, gk, beta, gla_scale: float,
@@ -170,6 +179,7 @@ def gka_chebyshev_gla_prefill(q, k, v, alpha, g, gk, beta, gla_scale: float,
                               output_final_state: bool = True, cu_seqlens=None, *,
                               o_norm_weight=None, o_norm_gate=None, o_norm_eps: float = 1e-6,
                               ssm_state_indices=None, has_initial_state=None, out=None,
+                              gates: ProjGates | None = None,
                               _segment_chunks: int | None = None):
     """Full GKA prefill: Chebyshev query refinement + beta^2 simple GLA
     (gka_forward.py:161-242).  Returns (o, h_kk_final, h_kv_final); h_kk_final is
@@ -189,18 +199,24 @@ def gka_chebyshev_gla_prefill(q, k, v, alpha, g, gk, beta, gla_scale: float,
       that update does.  A negative slot starts from zero and writes nothing.
     - ``has_initial_state`` [N] bool: sequences with False start from zero.
     - ``out`` [B,T,H,V] (q.dtype, contiguous): o is written there.
+    - ``gates`` (hmx.ProjGates): alpha, g, gk and beta are formed in the kernels
+      from the layer's raw projections (primed_gka_layer.py:224-358, :1138-1153)
+      instead of the gate tensors, which are then ignored.
 
     q, k and v may be the column slices of one fused projection: they are read in
     place."""
     _check_sketching_constraints(gka, num_sketches_per_head, "gka_chebyshev_gla_prefill")
     if cu_seqlens is not None and q.shape[0] != 1:
         raise ValueError(f"Batch size must be 1 when using cu_seqlens, got {q.shape[0]}")
-    if g is None:     # no GLA decay (the layer without a forgetting gate): e^0 = 1
+    if gates is not None:
+        gates.check(q.shape[0] * q.shape[1], q.shape[2], gka=True)
+        alpha = g = gk = beta = None
+    elif g is None:   # no GLA decay (the layer without a forgetting gate): e^0 = 1
         g = torch.zeros(q.shape[:3], dtype=torch.float32, device=q.device)
     return _gka_prefill(q, k, v, alpha, g, gk, beta, gla_scale, ridge_ratio, num_iter,
                         h_kk_initial, h_kv_initial, output_final_state, cu_seqlens, True,
                         _segment_chunks, (o_norm_weight, o_norm_gate, o_norm_eps),
-                        ssm_state_indices, has_initial_state, out)
+                        ssm_state_indices, has_initial_state, out, gates)
 
 
 def _onorm(weight, gate, eps, shape, dtype):
@@ -216,7 +232,8 @@ def _onorm(weight, gate, eps, shape, dtype):
 
 def _gka_prefill(q, k, v, alpha, g, gk, beta, gla_scale, ridge_ratio, num_iter, h_kk_initial,
                  h_kv_initial, output_final_state, cu_seqlens, l2norm, segment_chunks=None,
-                 o_norm=(None, None, 1e-6), state_indices=None, has_initial_state=None, out=None):
+                 o_norm=(None, None, 1e-6), state_indices=None, has_initial_state=None, out=None,
+                 gates=None):
     _lib.require_gpu(q, k, v, alpha, g, gk, beta, h_kk_initial, h_kv_initial,
                      state_indices, has_initial_state, out)   # cu_seqlens: host or device
     B, T, H, D = q.shape
@@ -258,7 +275,8 @@ def _gka_prefill(q, k, v, alpha, g, gk, beta, gla_scale, ridge_ratio, num_iter, 
         if has_initial_state.shape != (N,):
             raise ValueError(f"has_initial_state must be [{N}], got {tuple(has_initial_state.shape)}")
         hinit = has_initial_state.to(torch.uint8).contiguous()
-    alpha, g = alpha.contiguous(), g.contiguous()
+    if gates is None:
+        alpha, g = alpha.contiguous(), g.contiguous()
     (q, q_ts), (k, k_ts), (v, v_ts) = (_token_rows(x, 8) for x in (q, k, v))
     if k_ts != v_ts:    # the prefill kernels read k and v at one token stride
         (k, k_ts), (v, v_ts) = _token_rows(k.contiguous(), 8), _token_rows(v.contiguous(), 8)
@@ -280,14 +298,16 @@ def _gka_prefill(q, k, v, alpha, g, gk, beta, gla_scale, ridge_ratio, num_iter, 
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=q.device)
     _lib.call("hmx_gka_chunk_fwd",
               _lib.ptr(q), q_ts, _lib.ptr(k), k_ts, _lib.ptr(v), v_ts, _lib.dtype_code(q),
-              _lib.ptr(alpha), _lib.dtype_code(alpha), _lib.ptr(g), _lib.dtype_code(g),
+              _lib.ptr(alpha), 0 if alpha is None else _lib.dtype_code(alpha),
+              _lib.ptr(g), 0 if g is None else _lib.dtype_code(g),
               _lib.ptr(gk), 0 if gk is None else _lib.dtype_code(gk),
               _lib.ptr(beta), 0 if beta is None else _lib.dtype_code(beta),
               _lib.ptr(o), _lib.ptr(hkk0), _lib.ptr(hkk_t), ss_kk, dt_kk,
               _lib.ptr(hkv0), _lib.ptr(hkv_t), ss_kv, dt_kv, _lib.ptr(idx), _lib.ptr(hinit),
               _lib.ptr(seg), len(rows), nblk, N, H, HKV, D, V, int(num_iter), float(ridge_ratio),
               float(gla_scale), int(bool(l2norm)), _lib.ptr(ws), ws.numel(),
-              _onorm(*o_norm, tuple(o.shape), q.dtype), _lib.stream_of(q))
+              _onorm(*o_norm, tuple(o.shape), q.dtype), _lib.gate_proj(gates),
+              _lib.stream_of(q))
     if idx is not None and num_iter == 0:
         return o, None, hkv_t
     return o, hkk_t, hkv_t

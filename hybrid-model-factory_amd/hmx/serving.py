@@ -150,25 +150,26 @@ def gdn_forward_core(layer, mixed_qkv: torch.Tensor, b: torch.Tensor, a: torch.T
     mixed_qkv, b, a = mixed_qkv[:n], b[:n], a[:n]
     x = _conv(layer, md, mixed_qkv, conv_state)
     q, k, v = _qkv(layer, x)
-    g, beta = ops.fused_gdn_gating(layer.A, a, b, layer.dt_bias)
-    if getattr(layer, "allow_neg_eigval", False):
-        beta = beta * 2.0
+    # g and beta as fused_gdn_gating and the layer form them (:798-802), computed in
+    # the mixer kernels' loads instead of a separate launch
+    gates = ops.ProjGates(layer.A, layer.dt_bias, a, b,
+                          beta_scale=2.0 if getattr(layer, "allow_neg_eigval", False) else 1.0)
     out = core_attn_out[:n].unsqueeze(0)
     ndt, dec, pre = _split(md, query_start_loc_cpu)
     if dec is not None:
         cu_d, idx_d = dec
         ops.fused_recurrent_gated_delta_rule_gqa(
-            q[:, :ndt], k[:, :ndt], v[:, :ndt], g[:, :ndt], beta[:, :ndt],
+            q[:, :ndt], k[:, :ndt], v[:, :ndt], None, None,
             initial_state=ssm_state, inplace_final_state=True, cu_seqlens=cu_d,
             ssm_state_indices=idx_d, use_qk_l2norm_in_kernel=True, out=out[:, :ndt],
-            **_norm_args(o_norm, 0, ndt))
+            gates=gates.tokens(0, ndt), **_norm_args(o_norm, 0, ndt))
     if pre is not None:
         cu_p, idx_p, has_p = pre
         ops.chunk_gated_delta_rule_gqa(
-            q[:, ndt:], k[:, ndt:], v[:, ndt:], g[:, ndt:], beta[:, ndt:],
+            q[:, ndt:], k[:, ndt:], v[:, ndt:], None, None,
             initial_state=ssm_state, output_final_state=True, cu_seqlens=cu_p,
             use_qk_l2norm_in_kernel=True, ssm_state_indices=idx_p, has_initial_state=has_p,
-            out=out[:, ndt:], **_norm_args(o_norm, ndt, n))
+            out=out[:, ndt:], gates=gates.tokens(ndt, n), **_norm_args(o_norm, ndt, n))
 
 
 def gka_forward_core(layer, mixed_qkv: torch.Tensor, a: torch.Tensor, alpha_in: torch.Tensor,
@@ -189,39 +190,32 @@ def gka_forward_core(layer, mixed_qkv: torch.Tensor, a: torch.Tensor, alpha_in: 
         b = b[:n]
     x = _conv(layer, md, mixed_qkv, conv_state)
     q, k, v = _qkv(layer, x)
-    # gating as primed_gka_layer.py:1138-1153
-    if layer.use_forgetting_gate:
-        g, alpha, beta = ops.fused_gka_gating(layer.A, a, alpha_in, b if use_beta else None,
-                                              layer.dt_bias)
-    else:                                  # no decay: g = None (:1144-1148)
-        g = None
-        alpha = alpha_in.sigmoid().unsqueeze(0)
-        beta = b.sigmoid().unsqueeze(0) if use_beta else None
-    if layer.num_iter == 0:
-        alpha = torch.zeros_like(alpha)
-    elif layer._alpha_idx is None:
-        alpha = alpha + 0.5
-    kk_gate = layer.use_forgetting_gate_kk
+    # gates as primed_gka_layer.py:1138-1153 form them (fused_gka_gating, or the
+    # sigmoids without a forgetting gate; alpha zeroed for num_iter 0 or + 0.5),
+    # computed in the mixer kernels' loads instead of separate launches
+    fg = layer.use_forgetting_gate
+    gates = ops.ProjGates(
+        layer.A if fg else None, layer.dt_bias, a, b if use_beta else None, alpha_in,
+        alpha_add=0.5 if (layer.num_iter != 0 and layer._alpha_idx is None) else 0.0,
+        alpha_zero=layer.num_iter == 0, gk_from_g=fg and layer.use_forgetting_gate_kk)
     out = core_attn_out[:n].unsqueeze(0)
     ndt, dec, pre = _split(md, query_start_loc_cpu)
-    sl = lambda t, lo, hi: None if t is None else t[:, lo:hi]
     common = dict(gla_scale=layer.gla_scale, ridge_ratio=layer.ridge_strength,
                   num_iter=layer.num_iter)
     if dec is not None:
         cu_d, idx_d = dec
-        g_d = sl(g, 0, ndt)
         ops.gka_chebyshev_gla_decode(
-            q[:, :ndt], k[:, :ndt], v[:, :ndt], alpha[:, :ndt], g_d, g_d if kk_gate else None,
-            sl(beta, 0, ndt), h_kk=h_kk_state, h_kv=h_kv_state, cu_seqlens=cu_d,
-            ssm_state_indices=idx_d, out=out[:, :ndt], **common, **_norm_args(o_norm, 0, ndt))
+            q[:, :ndt], k[:, :ndt], v[:, :ndt], None, None, None, None,
+            h_kk=h_kk_state, h_kv=h_kv_state, cu_seqlens=cu_d, ssm_state_indices=idx_d,
+            out=out[:, :ndt], gates=gates.tokens(0, ndt), **common,
+            **_norm_args(o_norm, 0, ndt))
     if pre is not None:
         cu_p, idx_p, has_p = pre
-        g_p = sl(g, ndt, n)
         ops.gka_chebyshev_gla_prefill(
-            q[:, ndt:], k[:, ndt:], v[:, ndt:], alpha[:, ndt:], g_p, g_p if kk_gate else None,
-            sl(beta, ndt, n), h_kk_initial=h_kk_state, h_kv_initial=h_kv_state,
-            output_final_state=True, cu_seqlens=cu_p, ssm_state_indices=idx_p,
-            has_initial_state=has_p, out=out[:, ndt:], **common, **_norm_args(o_norm, ndt, n))
+            q[:, ndt:], k[:, ndt:], v[:, ndt:], None, None, None, None,
+            h_kk_initial=h_kk_state, h_kv_initial=h_kv_state, output_final_state=True,
+            cu_seqlens=cu_p, ssm_state_indices=idx_p, has_initial_state=has_p, out=out[:, ndt:],
+            gates=gates.tokens(ndt, n), **common, **_norm_args(o_norm, ndt, n))
 
 
 def mamba2_conv_ssm_forward(layer, projected_states: torch.Tensor, output: torch.Tensor,

@@ -26,13 +26,15 @@
 extern "C" {
 #endif
 
-#define HMX_ABI_VERSION 6  /* 2: optional hmx_gated_norm output epilogue in the GDN ops;
+#define HMX_ABI_VERSION 7  /* 2: optional hmx_gated_norm output epilogue in the GDN ops;
                               3: q/k/v token strides in the GDN and GKA ops; slot-indexed
                               state pools and has_initial_state in the GDN, GKA and SSD
                               prefills;
                               4: grouped x heads (HX) and C groups (GC) in the SSD ops;
                               5: nblock_total in hmx_gka_chunk_fwd and its workspace size;
-                              6: host segment planner hmx_plan_segments(_bounds) */
+                              6: host segment planner hmx_plan_segments(_bounds);
+                              7: gates from raw projections (hmx_gate_proj) in the GDN and
+                                 GKA prefill / decode entry points */
 
 enum hmx_status {
   HMX_OK = 0,
@@ -60,6 +62,40 @@ typedef struct hmx_gated_norm {
   float eps;
 } hmx_gated_norm;
 const char* hmx_last_error(void);
+
+/*
+ * Gates computed from the layer's raw projections inside the mixer kernels' loads,
+ * in place of a separate gating launch and its [tokens, H] gate tensors.  It fuses
+ * vllm-inference/src/primed_vllm/gdn/ops/fused_gdn_gating.py:79-125 (with the
+ * layer's beta *= 2 for negative eigenvalues, primed_gdn_layer.py:798-802) and
+ * primed_gka_layer.py:224-358 (with the layer's alpha post-processing,
+ * primed_gka_layer.py:1138-1153) into hmx_gdn_chunk_fwd, hmx_gdn_recurrent_fwd,
+ * hmx_gka_chunk_fwd and hmx_gka_decode_fwd.  Per token t (the op's flattened
+ * token index) and head h, each gate is rounded to in_dtype as the reference
+ * stores it before the kernel reads it:
+ *   g     = -exp(A_log[h]) * softplus(a[t,h] + dt_bias[h])   (softplus with
+ *           softplus_beta / softplus_threshold as the reference); 0 when A_log is
+ *           NULL (the GKA layer without a forgetting gate)
+ *   beta  = sigmoid(b[t,h]), then * beta_scale (rounded again); none when b is NULL
+ *   alpha = sigmoid(alpha_in[t,h]), then + alpha_add (rounded again), or 0 when
+ *           alpha_zero (GKA only)
+ *   gk    = g when gk_from_g, else none (GKA only)
+ * An op given gates ignores its g / gk / beta / alpha pointers.
+ */
+typedef struct hmx_gate_proj {
+  const void* A_log; int32_t A_log_dtype;            /* [H] or NULL */
+  const void* dt_bias; int32_t dt_bias_dtype;        /* [H] */
+  const void* a; int64_t a_token_stride, a_head_stride;            /* [tokens, H] */
+  const void* b; int64_t b_token_stride, b_head_stride;            /* [tokens, H] or NULL */
+  const void* alpha_in; int64_t alpha_token_stride, alpha_head_stride;  /* GKA [tokens, H] */
+  int32_t in_dtype;                                  /* dtype of a, b, alpha_in */
+  float softplus_beta, softplus_threshold;           /* 1, 20 in the layers */
+  float beta_scale;                                  /* 1, or 2 for negative eigenvalues */
+  float alpha_add;                                   /* GKA: 0.5, or 0 */
+  int32_t alpha_zero;                                /* GKA: alpha = 0 (num_iter == 0) */
+  int32_t gk_from_g;                                 /* GKA: gk = g (use_forgetting_gate_kk) */
+} hmx_gate_proj;
+
 
 /*
  * GDN gating: g = -exp(A_log) * softplus(a + dt_bias), beta_out = sigmoid(b).
@@ -112,7 +148,7 @@ int hmx_gdn_recurrent_fwd(const void* q, int64_t q_token_stride, const void* k,
                           int64_t B, int64_t T, int64_t N,
                           int32_t H, int32_t HKV, int32_t K, int32_t V,
                           float scale, int32_t use_qk_l2norm, int32_t inplace_final_state,
-                          const hmx_gated_norm* o_norm, void* stream);
+                          const hmx_gated_norm* o_norm, const hmx_gate_proj* gates, void* stream);
 
 /*
  * Segment planner (host code: host pointers, no GPU access, no allocation the
@@ -189,7 +225,7 @@ int hmx_gdn_chunk_fwd(const void* q, int64_t q_token_stride, const void* k,
                       int32_t H, int32_t HKV, int32_t K, int32_t V, float scale,
                       int32_t use_qk_l2norm, int32_t max_warm_chunks, float decay_threshold,
                       void* workspace, size_t workspace_bytes, const hmx_gated_norm* o_norm,
-                      void* stream);
+                      const hmx_gate_proj* gates, void* stream);
 
 /*
  * hmx_gdn_chunk_fwd without a workspace argument: the workspace is a static device
@@ -214,7 +250,7 @@ int hmx_gdn_chunk_fwd_noalloc(const void* q, int64_t q_token_stride, const void*
                               const int32_t* seg_table, int32_t nseg_total, int32_t N,
                               int32_t H, int32_t HKV, int32_t K, int32_t V, float scale,
                               int32_t use_qk_l2norm, int32_t max_warm_chunks,
-                              float decay_threshold, const hmx_gated_norm* o_norm, void* stream);
+                              float decay_threshold, const hmx_gated_norm* o_norm, const hmx_gate_proj* gates, void* stream);
 
 /* Workspace bytes hmx_gdn_chunk_fwd needs for a given segment table (host-only
  * arithmetic); pooled != 0 when the call passes state_indices.  Companion of
@@ -266,7 +302,7 @@ int hmx_gka_decode_fwd(const void* q, int64_t q_token_stride, const void* k,
                        int64_t idx_stride, int64_t B, int64_t T, int64_t N,
                        int32_t H, int32_t HKV, int32_t D, int32_t V,
                        int32_t num_iter, float ridge_ratio, float scale,
-                       const hmx_gated_norm* o_norm, void* stream);
+                       const hmx_gated_norm* o_norm, const hmx_gate_proj* gates, void* stream);
 
 /*
  * GKA chunked prefill forward (Chebyshev ridge solve + beta^2 GLA), GQA-native,
@@ -309,7 +345,7 @@ int hmx_gka_chunk_fwd(const void* q, int64_t q_token_stride, const void* k,
                       int32_t N, int32_t H, int32_t HKV, int32_t D, int32_t V,
                       int32_t num_iter, float ridge_ratio, float scale, int32_t use_qk_l2norm,
                       void* workspace, size_t workspace_bytes,
-                      const hmx_gated_norm* o_norm, void* stream);
+                      const hmx_gated_norm* o_norm, const hmx_gate_proj* gates, void* stream);
 
 /* Workspace bytes hmx_gka_chunk_fwd needs (host-only arithmetic).  Companion of
  * hmx_gka_chunk_fwd; no reference counterpart (the reference allocates its

@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_string():
     lib = _lib.load()
-    assert lib.hmx_abi_version() == 6
+    assert lib.hmx_abi_version() == 7
     assert isinstance(lib.hmx_last_error(), bytes)
 
 
@@ -43,13 +43,13 @@ def test_invalid_args_map_to_status_codes():
     lib = _lib.load()
     rc = lib.hmx_gdn_recurrent_fwd(None, 0, None, 0, None, 0, 1, None, 0, None, 0, 0, None, None,
                                    0, None, 0, 0, None, None, 0, None, 1, 1, 1, 4, 4, 96, 128, 1.0,
-                                   1, 0, None, None)
+                                   1, 0, None, None, None)
     assert rc == _lib.HMX_EUNSUPPORTED
     assert b"K=96" in lib.hmx_last_error()
     with pytest.raises(NotImplementedError):
         _lib.call("hmx_gdn_recurrent_fwd", None, 0, None, 0, None, 0, 1, None, 0, None, 0, 0, None,
                   None, 0, None, 0, 0, None, None, 0, None, 1, 1, 1, 4, 4, 96, 128, 1.0, 1, 0, None,
-                  None)
+                  None, None)
     with pytest.raises(ValueError):
         _lib.call("hmx_gdn_gating", None, 0, None, 0, 0, None, 0, 0, 1, None, 0, None, None, 1,
                   -1, 4, 1.0, 20.0, None)
@@ -111,4 +111,4 @@ def test_noalloc_entry_rejects_oversized_table():
         _lib.call("hmx_gdn_chunk_fwd_noalloc", None, H * 128, None, H * 128, None, H * 128,
                   _lib.HMX_BF16, None, _lib.HMX_F32, None, _lib.HMX_F32, None, None, None, 0,
                   _lib.HMX_F32, None, None, None, nseg, N, H, H, 128, 128, 1.0, 1, 16, 60.0,
-                  None, None)
+                  None, None, None)

@@ -45,7 +45,7 @@ def _call(name, q, k, v, g, beta, h0, bounds, seg_chunks, workspace):
         nb = int(lib.hmx_gdn_chunk_workspace_bytes(len(rows), N, H, 0))
         ws = torch.empty(nb, dtype=torch.uint8, device=dev)
         args += [_lib.ptr(ws), nb]
-    _lib.call(name, *args, None, _lib.stream_of(q))
+    _lib.call(name, *args, None, None, _lib.stream_of(q))
     torch.cuda.synchronize()
     return o, ht, len(rows)
 
