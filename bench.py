@@ -88,6 +88,32 @@ def bench_prefill(dev, steps, warmup, HKV=32):
     return dict(ms=ms, tokens_per_s=T / (ms * 1e-3), bytes=by, flops=fl, GBps=gbs, TFLOPs=tfs)
 
 
+def bench_prefill_layer_gates(dev, steps, warmup):
+    """C1 with the gates a GDN layer forms at initialisation (A_log ~ log U(1,16),
+    dt_bias from dt ~ logU(1e-3, 1e-1), fused_gdn_gating of N(0,1) projections):
+    weak decay on some heads sends their later segments through the exact segment
+    scan.  Reports how many (segment, head) pairs take it."""
+    import hmx
+    from hmx import _lib, workloads as wl
+    T, H, D = 32768, 32, 128
+    d = wl.gdn_inputs(T=T, H=H, HKV=H, D=D, config_id=1, device=dev, gen_device=dev)
+    g, beta = wl.gdn_layer_gates(T, H, device=dev, gen_device=dev)
+    args = [d["q"], d["k"], d["v"], g, beta]
+
+    def step():
+        hmx.chunk_gated_delta_rule_gqa(*args, output_final_state=True,
+                                       use_qk_l2norm_in_kernel=True)
+
+    ms = _timed(step, steps, warmup)
+    import torch
+    table, _ = _lib.plan_segments(_lib.PLAN_GDN, [(0, T)], T, H,
+                                  torch.cuda.get_device_properties(dev).multi_processor_count)
+    pairs, heads = wl.gdn_exact_pairs(g, beta, table)
+    by = wl.gdn_prefill_bytes(T, H, H)
+    return dict(ms=ms, tokens_per_s=T / (ms * 1e-3), bytes=by, GBps=by / (ms * 1e-3) / 1e9,
+                segments=len(table), exact_pairs=pairs, exact_heads=int(heads.sum()))
+
+
 def bench_prefill_varlen(dev, steps, warmup):
     """C1 varlen: 8 sequences with randint(1024, 8193) tokens (the config generator's
     first draw), zero fp32 initial states, final states out."""
@@ -627,6 +653,7 @@ def main():
         out["prefill"] = pf
         out["prefill_gqa"] = bench_prefill(dev, a.steps, a.warmup, HKV=8)
         out["prefill_varlen"] = bench_prefill_varlen(dev, a.steps, a.warmup)
+        out["prefill_layer_gates"] = bench_prefill_layer_gates(dev, a.steps, a.warmup)
     if a.only in (None, "onorm"):
         out["onorm"] = bench_onorm(dev, a.steps, a.warmup)
     if a.only in (None, "conv"):
@@ -657,7 +684,7 @@ def main():
             "value": round(pf["tokens_per_s"], 1), "unit": "tokens/s",
             "ms_per_step": round(pf["ms"], 4),
             "config": {"workload": "C1 GDN chunked prefill (chunk_gated_delta_rule_gqa)",
-                       "B": 1, "T": 32768, "H": 32, "HKV": 32, "d": 128, "chunk": 64,
+                       "B": 1, "T": 32768, "H": 32, "HKV": 32, "d": 128, "chunk": 32,
                        "qkv_dtype": "bf16", "state_dtype": "fp32"},
             "roofline": {"bound": "hbm", "achieved": round(pf["GBps"], 1),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -685,6 +712,21 @@ def main():
             "config": {"workload": "C1 varlen: 8 sequences, randint(1024, 8193) tokens",
                        "lengths": r["lengths"], "tokens": r["tokens"], "H": 32, "d": 128,
                        "initial_state": "zeros fp32 [8,32,128,128]"},
+            "roofline": {"bound": "hbm", "achieved": round(r["GBps"], 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(r["GBps"] / HBM_PEAK_GBS, 4),
+                         "algorithmic_bytes": r["bytes"], "traffic": None},
+        }
+    if "prefill_layer_gates" in out:
+        r = out["prefill_layer_gates"]
+        line["prefill_layer_gates"] = {
+            "value": round(r["tokens_per_s"], 1), "unit": "tokens/s", "ms_per_step": round(r["ms"], 4),
+            "vs_c1_bench_gates": round(r["ms"] / out["prefill"]["ms"], 3),
+            "config": {"workload": "C1 with layer-initialisation gates (A_log ~ log U(1,16), "
+                                   "dt ~ logU(1e-3, 1e-1), a, b ~ N(0,1))",
+                       "T": 32768, "H": 32, "HKV": 32, "d": 128, "segments": r["segments"],
+                       "exact_scan_pairs": r["exact_pairs"],
+                       "exact_scan_pairs_of": (r["segments"] - 1) * 32,
+                       "heads_running_exact_scan": r["exact_heads"]},
             "roofline": {"bound": "hbm", "achieved": round(r["GBps"], 1), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(r["GBps"] / HBM_PEAK_GBS, 4),
                          "algorithmic_bytes": r["bytes"], "traffic": None},

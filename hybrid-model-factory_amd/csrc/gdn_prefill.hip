@@ -76,7 +76,9 @@ constexpr int LDQ = D + 16;
 constexpr int LDT = C + 8;     // [C][C] row stride (P, T blocks)
 static_assert(C == 32, "chunk length: the substitution and the g scan are written for 32");
 
-enum Mode { MODE_OUT = 0, MODE_S0 = 1, MODE_PHI = 2 };
+// MODE_OUT: the output walk.  MODE_PRE: the exact scan's pre-pass walk of a
+// segment, from zero with the values (S0) or from I without them (Phi).
+enum Mode { MODE_OUT = 0, MODE_PRE = 1 };
 
 // shared-memory layout (bytes): two staging buffers (K, Q as normalised fp16,
 // V raw bf16, per-token scalars), the O staging tile, T/M blocks, P
@@ -196,12 +198,29 @@ __device__ __forceinline__ void ld_gate_bits(const Params& p, int64_t tok, int h
 }
 
 // A sequence/head pair needs the exact segment scan when any of its later
-// segments found no warm-up start (plan == -1).
-__device__ __forceinline__ bool seq_exact(const int* plan, const SegInfo& si, int H, int h) {
+// segments found no warm-up start (plan == -1).  The lanes of a wave read 64
+// plan entries at a time (one load latency, not one per segment); the result
+// is wave-uniform.
+__device__ __forceinline__ bool seq_exact(const int* plan, const SegInfo& si, int H, int h,
+                                          int lane) {
   if (!plan) return false;
-  for (int s = si.first_seg + 1; s < si.first_seg + si.nseg; ++s)
-    if (plan[s * H + h] < 0) return true;
+  const int end = si.first_seg + si.nseg;
+  for (int s0 = si.first_seg + 1; s0 < end; s0 += 64) {
+    const int s = s0 + lane;
+    if (__ballot(s < end && plan[s * H + h] < 0)) return true;
+  }
   return false;
+}
+
+// The first segment-table row of sequence n (rows are grouped by sequence), or
+// -1; 64 rows per load round.
+__device__ __forceinline__ int find_seq_row(const int* seg, int nseg_total, int n, int lane) {
+  for (int s0 = 0; s0 < nseg_total; s0 += 64) {
+    const int s = s0 + lane;
+    const unsigned long long m = __ballot(s < nseg_total && seg[s * 8] == n);
+    if (m) return s0 + __builtin_ctzll(m);
+  }
+  return -1;
 }
 
 // One chunk's raw inputs for this thread: 2 rows x 8 features of k, v, q and
@@ -218,7 +237,7 @@ struct RawChunk {
 template <int MODE, bool FG>
 __device__ __forceinline__ void load_raw(RawChunk& r, const Params& p, const bf16* qh,
                                          const bf16* kh, const bf16* vh, int tok0, int nval,
-                                         bool need_q, int tid, int h) {
+                                         bool need_q, bool with_v, int tid, int h) {
 #pragma unroll
   for (int pass = 0; pass < MT; ++pass) {
     const int row = pass * 16 + (tid >> 4);
@@ -226,7 +245,7 @@ __device__ __forceinline__ void load_raw(RawChunk& r, const Params& p, const bf1
     const bool ok = row < nval;
     const int64_t tok = tok0 + row;
     r.k[pass] = ok ? *reinterpret_cast<const bf16x8*>(kh + tok * p.kv_ts + f0) : bf16x8{};
-    if (MODE != MODE_PHI)
+    if (MODE == MODE_OUT || with_v)
       r.v[pass] = ok ? *reinterpret_cast<const bf16x8*>(vh + tok * p.kv_ts + f0) : bf16x8{};
     if (MODE == MODE_OUT)
       r.q[pass] = (ok && need_q) ? *reinterpret_cast<const bf16x8*>(qh + tok * p.q_ts + f0)
@@ -298,13 +317,15 @@ __device__ __forceinline__ f16x8 scale_h8(const bf16x8& x, float s) {
 // Write a prefetched, prepared chunk into staging buffer st.
 template <int MODE, typename GC>
 __device__ __forceinline__ void stage_chunk(const Stage& st, const RawChunk& r, bool with_q,
-                                            int tid, int wave, int lane, const GC& gc) {
+                                            bool with_v, int tid, int wave, int lane,
+                                            const GC& gc) {
 #pragma unroll
   for (int pass = 0; pass < MT; ++pass) {
     const int row = pass * 16 + (tid >> 4);
     const int f0 = (tid & 15) * 8;
     store8_i(st.K + row * LDQ, f0, scale_h8(r.k[pass], r.rk[pass]));
-    if (MODE != MODE_PHI) *reinterpret_cast<bf16x8*>(st.V + row * LDQ + f0) = r.v[pass];
+    if (MODE == MODE_OUT || with_v)
+      *reinterpret_cast<bf16x8*>(st.V + row * LDQ + f0) = r.v[pass];
     if (MODE == MODE_OUT && with_q)
       store8_i(st.Q + row * LDQ, f0, scale_h8(r.q[pass], r.rq[pass]));
   }
@@ -353,9 +374,11 @@ __device__ __forceinline__ f16x4 ld_blk(const f16* m, int r0, int c0, int lane) 
 // ---------------------------------------------------------------------------
 // NORM: the output rows pass through the gated RMSNorm of hmx_rms_norm_gated
 // (norm before gate) on their way out of sO.
-template <int MODE, bool NORM = false, bool FG = false>
-__global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
-  __shared__ __align__(16) unsigned char smem[SMEM];
+// One workgroup's walk of segment s_id for head h: its output (OUT), or the S0
+// (phi false) or Phi (phi true) pre-pass walk of an exact pair's segment (PRE).
+template <int MODE, bool NORM, bool FG>
+__device__ __forceinline__ void chunk_walk(const Params& p, unsigned char* smem, int s_id, int h,
+                                           bool phi) {
   bf16* sO = reinterpret_cast<bf16*>(smem + OFF_O);
   f16* sT = reinterpret_cast<f16*>(smem + OFF_T);
   f16* sP = reinterpret_cast<f16*>(smem + OFF_P);
@@ -365,14 +388,14 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
   // would still run its MFMAs, which ignore EXEC)
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int q4 = lane >> 4, l16 = lane & 15;
-  const int s_id = blockIdx.x, h = blockIdx.y;
   const GateConv<FG> gc = gate_conv<FG>(p, h);
   const SegInfo si = load_seg(p.seg, s_id);
   const int H = p.H;
   const int hk = h / (H / p.HKV);
 
   // ---- decide the chunk range and the initial state ------------------------
-  const bool exact = seq_exact(p.plan, si, H, h);
+  const bool exact = seq_exact(p.plan, si, H, h, lane);
+  const bool with_v = MODE == MODE_OUT || !phi;
   int c_begin = si.c_start;            // first chunk processed
   const int c_out = si.c_start;        // first chunk whose output is written
   int init_kind;                       // 0 zero, 1 h0, 2 ws_init, 3 identity
@@ -388,7 +411,7 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
     }
   } else {
     if (!exact || si.seg_idx == si.nseg - 1) return;
-    if (MODE == MODE_PHI) {
+    if (phi) {
       if (si.seg_idx == 0) return;
       init_kind = 3;
     } else {
@@ -519,14 +542,14 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
     {
       const int t0 = si.bos + c_begin * C;
       load_raw<MODE, FG>(raw, p, qh, kh, vh, t0, min(C, si.eos - t0), c_begin >= c_out,
-                     tid, h);
+                         with_v, tid, h);
       prep_rows<MODE>(raw, p.l2norm, p.scale);
       if (wave == 0) prep_scan(raw, lane, gc);
-      stage_chunk<MODE>(stage_at(smem, 0), raw, c_begin >= c_out, tid, wave, lane, gc);
+      stage_chunk<MODE>(stage_at(smem, 0), raw, c_begin >= c_out, with_v, tid, wave, lane, gc);
       if (c_begin + 1 < si.c_end) {
         const int t1 = t0 + C;
         load_raw<MODE, FG>(raw, p, qh, kh, vh, t1, min(C, si.eos - t1),
-                       c_begin + 1 >= c_out, tid, h);
+                           c_begin + 1 >= c_out, with_v, tid, h);
       }
     }
     lds_barrier();
@@ -543,10 +566,12 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
       if (c + 1 < si.c_end) {
         prep_rows<MODE>(raw, p.l2norm, p.scale);
         if (wave == 0) prep_scan(raw, lane, gc);
-        stage_chunk<MODE>(stage_at(smem, bi ^ 1), raw, c + 1 >= c_out, tid, wave, lane, gc);
+        stage_chunk<MODE>(stage_at(smem, bi ^ 1), raw, c + 1 >= c_out, with_v, tid, wave, lane,
+                          gc);
         if (c + 2 < si.c_end) {
           const int t2 = tok0 + 2 * C;
-          load_raw<MODE, FG>(raw, p, qh, kh, vh, t2, min(C, si.eos - t2), c + 2 >= c_out, tid, h);
+          load_raw<MODE, FG>(raw, p, qh, kh, vh, t2, min(C, si.eos - t2), c + 2 >= c_out,
+                             with_v, tid, h);
         }
       }
       bf16x8 zr[MT];
@@ -688,7 +713,7 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
 #pragma unroll
           for (int ct = 0; ct < 2; ++ct) {
             bf16x4 vt = {};
-            if (MODE != MODE_PHI) vt = ld_tr(cur.V, LDQ, 16 * mt + 4 * q4, 32 * wave + 16 * ct, lane);
+            if (with_v) vt = ld_tr(cur.V, LDQ, 16 * mt + 4 * q4, 32 * wave + 16 * ct, lane);
 #pragma unroll
             for (int v = 0; v < 4; ++v)
               Y[mt][ct][v] = (float)vt[v] - cur.EG[16 * mt + 4 * q4 + v] * X[mt][ct][v];
@@ -788,10 +813,8 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
         else dst = static_cast<float*>(p.ht) + off;
       }
     }
-  } else if (MODE == MODE_S0) {
-    dst = p.ws_s0 + ((int64_t)s_id * H + h) * D * D;
   } else {
-    dst = p.ws_phi + ((int64_t)s_id * H + h) * D * D;
+    dst = (phi ? p.ws_phi : p.ws_s0) + ((int64_t)s_id * H + h) * D * D;
   }
   if (dst || dst16) {
 #pragma unroll
@@ -807,6 +830,22 @@ __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
   }
 }
 
+// The output walks (after the exact pairs' segment combine).
+template <bool NORM, bool FG>
+__global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
+  __shared__ __align__(16) unsigned char smem[SMEM];
+  chunk_walk<MODE_OUT, NORM, FG>(p, smem, blockIdx.x, blockIdx.y, false);
+}
+
+// The exact pairs' pre-pass: blockIdx.z 0 walks S0, 1 walks Phi.  The two are
+// independent and share the GPU in one launch; the output walks follow in a
+// launch of their own, which the warm-up pairs fill alongside the exact ones.
+template <bool FG>
+__global__ __launch_bounds__(NTHR, 2) void gdn_pre_kernel(Params p) {
+  __shared__ __align__(16) unsigned char smem[SMEM];
+  chunk_walk<MODE_PRE, false, FG>(p, smem, blockIdx.x, blockIdx.y, blockIdx.z == 1);
+}
+
 // ---------------------------------------------------------------------------
 // plan: warm-up start chunk per (segment, head); exact flag per (sequence, head)
 // ---------------------------------------------------------------------------
@@ -820,20 +859,35 @@ __global__ __launch_bounds__(64) void gdn_plan_kernel(Params p) {
   if (si.seg_idx > 0) {
     plan = -1;
     if (p.l2norm) {
-      float acc = 0.f;
+      // Walk back from the segment start over at most max_warm chunks, summing each
+      // chunk's decay bound, until the sum drops below -decay_thresh (start there)
+      // or the sequence start is reached (start from h0).  4 chunks per round:
+      // lanes 16j..16j+15 load chunk c_hi - 1 - j, 2 tokens each, in one go.
       const int lo = max(0, si.c_start - p.max_warm);
-      for (int c = si.c_start - 1; c >= lo; --c) {
-        const int t = si.bos + c * C + lane;
+      float acc = 0.f;
+      for (int c_hi = si.c_start; c_hi > lo && plan < 0; c_hi -= 4) {
+        const int c = c_hi - 1 - (lane >> 4);
         float b = 0.f;
-        if (lane < C && t < si.eos) {
-          uint32_t gbits, bbits;
-          ld_gate_bits<FG>(p, t, h, gbits, bbits);
-          const float gv = gc.g(gbits), bv = gc.beta(bbits);
-          b = gv + logf(fmaxf(1.f, fabsf(1.f - bv)));
+        if (c >= lo) {
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            const int t = si.bos + c * C + (lane & 15) * 2 + i;
+            if (t < si.eos) {
+              uint32_t gbits, bbits;
+              ld_gate_bits<FG>(p, t, h, gbits, bbits);
+              b += gc.g(gbits) + logf(fmaxf(1.f, fabsf(1.f - gc.beta(bbits))));
+            }
+          }
         }
-        acc += wave_sum(b);
-        if (acc < -p.decay_thresh) { plan = c; break; }
-        if (c == 0) { plan = 0; break; }  // reached the sequence start: exact from h0
+        b = row16_sum(b);
+        bool done = false;
+        for (int j = 0; j < 4 && !done; ++j) {   // uniform: every lane holds every sum
+          const int cj = c_hi - 1 - j;
+          if (cj < lo) break;
+          acc += __shfl(b, 16 * j);
+          if (acc < -p.decay_thresh) { plan = cj; done = true; }
+          else if (cj == 0) { plan = 0; done = true; }  // sequence start: exact from h0
+        }
       }
     }
   }
@@ -841,53 +895,95 @@ __global__ __launch_bounds__(64) void gdn_plan_kernel(Params p) {
 }
 
 // ---------------------------------------------------------------------------
-// exact segment scan: S_1 = S0_0; S_{s+1} = Phi_s S_s + S0_s  (fp32)
-// one workgroup per (sequence, head, 16-column slice)
+// exact segment scan: S_1 = S0_0; S_{s+1} = Phi_s S_s + S0_s, in fp32 MFMAs
+// (16x16x4 f32).  One 512-thread workgroup per (sequence, head, 16-column slice
+// of the state); wave w forms rows [16w, 16w+16) of the slice, two waves per
+// SIMD.  The slice of S_s lives in LDS transposed (column-major, 132-dword
+// columns: the 4 K-values a lane feeds are one conflict-free 128-bit read),
+// double-buffered so a step needs one barrier.  Phi_s and S0_s do not depend on
+// the chain: they are loaded into registers two steps ahead.  The 8 slices of a
+// (sequence, head) are blocks b with equal b mod 8, which the dispatcher places
+// on one XCD, so each Phi_s is fetched into one L2 once.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(NTHR) void gdn_seg_combine_kernel(Params p, int N) {
-  __shared__ float sS[D * 16];
-  const int nh = blockIdx.x, cb = blockIdx.y, tid = threadIdx.x;
-  const int H = p.H, n = nh / H, h = nh % H;
-  int first = -1, nseg = 0;
-  SegInfo si{};
-  for (int s = 0; s < p.nseg_total; ++s) {
-    si = load_seg(p.seg, s);
-    if (si.n == n) { first = si.first_seg; nseg = si.nseg; break; }
-  }
-  if (first < 0 || nseg < 2 || !seq_exact(p.plan, si, H, h)) return;
-  const int row = tid >> 1, c0 = (tid & 1) * 8;
-  const int64_t hoff = (int64_t)h * D * D;
-  // S_1
-  {
-    const float* s0 = p.ws_s0 + (int64_t)first * H * D * D + hoff;
-    float* init = p.ws_init + (int64_t)(first + 1) * H * D * D + hoff;
+constexpr int CMB_LD = D + 4;
+constexpr int CMB_THR = 512;
+
+__global__ __launch_bounds__(CMB_THR) void gdn_seg_combine_kernel(Params p, int N) {
+  __shared__ __align__(16) float sST[2][16 * CMB_LD];
+  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q4 = lane >> 4, l16 = lane & 15;
+  const int cb = (b >> 3) & 7, nh = (b & 7) + 8 * (b >> 6);
+  const int H = p.H;
+  if (nh >= N * H) return;
+  const int n = nh / H, h = nh % H;
+  const int row = find_seq_row(p.seg, p.nseg_total, n, lane);
+  if (row < 0) return;
+  const SegInfo si = load_seg(p.seg, row);
+  const int first = si.first_seg, nseg = si.nseg;
+  if (nseg < 2 || !seq_exact(p.plan, si, H, h, lane)) return;
+  const int64_t hoff = (int64_t)h * D * D, sstride = (int64_t)H * D * D;
+  const int col = cb * 16 + l16, r0 = 16 * wave;
+  // Phi_s rows r0 + l16, features 16j + 4q4..+3 (A operands) and S0_s in the
+  // accumulator layout (rows r0 + 4q4 + v, column col)
+  struct StepIn { f32x4 phi[8], s0; };
+  auto load_step = [&](StepIn& in, int s) {
+    const float* ph = p.ws_phi + (first + s) * sstride + hoff;
+    const float* z = p.ws_s0 + (first + s) * sstride + hoff;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      in.phi[j] = *reinterpret_cast<const f32x4*>(ph + (r0 + l16) * D + 16 * j + 4 * q4);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) in.s0[v] = z[(r0 + 4 * q4 + v) * D + col];
+  };
+  auto put = [&](int buf, const f32x4& x) {
+    *reinterpret_cast<f32x4*>(&sST[buf][l16 * CMB_LD + r0 + 4 * q4]) = x;
+  };
+  // S_s (LDS buffer buf, after a barrier) -> its ws_init slice: thread tid writes
+  // row tid / 4, columns 4 (tid & 3)..+3 (the stores never read the MFMA
+  // accumulators, so the next step need not wait for them)
+  auto flush = [&](int buf, int s) {
+    float* init = p.ws_init + (first + s) * sstride + hoff;
+    const int r = tid >> 2, c0 = (tid & 3) * 4;
+    f32x4 x;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[e] = sST[buf][(c0 + e) * CMB_LD + r];
+    *reinterpret_cast<f32x4*>(init + r * D + cb * 16 + c0) = x;
+  };
+  const int last = nseg - 2;   // the last step forms S_{nseg-1}
+  // three input sets in rotation: step s consumes one while the loads of steps
+  // s + 1 and s + 2 are in flight (issued at the starts of steps s - 1 and s)
+  StepIn b0, b1, b2;
+  auto step = [&](StepIn& in, StepIn& ahead, int s) {
+    const int cur = (s - 1) & 1;
+    load_step(ahead, min(s + 2, last));   // unconditional: the last steps reload their own
+    __builtin_amdgcn_sched_barrier(0);
+    f32x4 acc[2] = {in.s0, f32x4{0.f, 0.f, 0.f, 0.f}};   // two chains: even / odd j
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float x = s0[row * D + cb * 16 + c0 + j];
-      sS[row * 16 + c0 + j] = x;
-      init[row * D + cb * 16 + c0 + j] = x;
+      const f32x4 bk = *reinterpret_cast<const f32x4*>(&sST[cur][l16 * CMB_LD + 16 * j + 4 * q4]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[j & 1] = mfma16f(in.phi[j][e], bk[e], acc[j & 1]);
     }
-  }
+    put(cur ^ 1, acc[0] + acc[1]);
+    __syncthreads();
+    flush(cur ^ 1, s + 1);
+  };
+  // S_1 = S0_0
+  load_step(b0, 0);
+  put(0, b0.s0);
+  load_step(b1, min(1, last));
+  load_step(b2, min(2, last));
   __syncthreads();
-  for (int s = 1; s < nseg - 1; ++s) {
-    const float* phi = p.ws_phi + (int64_t)(first + s) * H * D * D + hoff;
-    const float* s0 = p.ws_s0 + (int64_t)(first + s) * H * D * D + hoff;
-    float acc[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] = s0[row * D + cb * 16 + c0 + j];
-    for (int kk = 0; kk < D; ++kk) {
-      const float a = phi[row * D + kk];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc[j] += a * sS[kk * 16 + c0 + j];
-    }
-    __syncthreads();
-    float* init = p.ws_init + (int64_t)(first + s + 1) * H * D * D + hoff;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      sS[row * 16 + c0 + j] = acc[j];
-      init[row * D + cb * 16 + c0 + j] = acc[j];
-    }
-    __syncthreads();
+  flush(0, 1);
+  // step s reads b[s % 3] and loads step s + 2 into b[(s + 2) % 3], whose step
+  // s - 1 is done
+  for (int s = 1; s <= last; s += 3) {
+    step(b1, b0, s);
+    if (s + 1 > last) break;
+    step(b2, b1, s + 1);
+    if (s + 2 > last) break;
+    step(b0, b2, s + 2);
   }
 }
 
@@ -897,13 +993,9 @@ __global__ __launch_bounds__(NTHR) void gdn_seg_combine_kernel(Params p, int N) 
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(NTHR) void gdn_state_copy_kernel(Params p) {
   const int n = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
-  int nseg = 0;
-  for (int s = 0; s < p.nseg_total; ++s) {
-    const SegInfo si = load_seg(p.seg, s);
-    if (si.n == n) { nseg = si.nseg; break; }
-  }
+  const int row = find_seq_row(p.seg, p.nseg_total, n, tid & 63);
   const int64_t slot = p.sidx[n];
-  if (nseg < 2 || slot < 0) return;
+  if (row < 0 || p.seg[row * 8 + 7] < 2 || slot < 0) return;
   const float* src = p.ws_ht + ((int64_t)n * p.H + h) * D * D;
   const int64_t off = slot * p.st_ss + (int64_t)h * D * D;
   for (int i = tid * 4; i < D * D; i += NTHR * 4) {
@@ -1003,28 +1095,32 @@ extern "C" int hmx_gdn_chunk_fwd(const void* q, int64_t q_token_stride, const vo
   p.plan = reinterpret_cast<int*>(tail);
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid(nseg_total, H);
+  // multi-segment: plan; the exact pairs' S0 / Phi pre-pass; their segment
+  // combine; every output walk.  One segment per sequence: every walk starts
+  // from h0.
   if (multi) {
+    const dim3 pre(nseg_total, H, 2);
     if (p.fused) {
       hipLaunchKernelGGL(gdn_plan_kernel<true>, grid, dim3(64), 0, s, p);
-      hipLaunchKernelGGL((gdn_chunk_kernel<MODE_S0, false, true>), grid, dim3(NTHR), 0, s, p);
-      hipLaunchKernelGGL((gdn_chunk_kernel<MODE_PHI, false, true>), grid, dim3(NTHR), 0, s, p);
+      hipLaunchKernelGGL(gdn_pre_kernel<true>, pre, dim3(NTHR), 0, s, p);
     } else {
       hipLaunchKernelGGL(gdn_plan_kernel<false>, grid, dim3(64), 0, s, p);
-      hipLaunchKernelGGL(gdn_chunk_kernel<MODE_S0>, grid, dim3(NTHR), 0, s, p);
-      hipLaunchKernelGGL(gdn_chunk_kernel<MODE_PHI>, grid, dim3(NTHR), 0, s, p);
+      hipLaunchKernelGGL(gdn_pre_kernel<false>, pre, dim3(NTHR), 0, s, p);
     }
-    hipLaunchKernelGGL(gdn_seg_combine_kernel, dim3(N * H, D / 16), dim3(NTHR), 0, s, p, N);
+    // blocks b: slice (b / 8) % 8 of pair (b % 8) + 8 (b / 64)
+    hipLaunchKernelGGL(gdn_seg_combine_kernel, dim3((N * H + 7) / 8 * 64), dim3(CMB_THR), 0, s,
+                       p, N);
   } else {
-    p.plan = nullptr;  // one segment per sequence: every segment starts from h0
+    p.plan = nullptr;
   }
   if (o_norm && p.fused)
-    hipLaunchKernelGGL((gdn_chunk_kernel<MODE_OUT, true, true>), grid, dim3(NTHR), 0, s, p);
+    hipLaunchKernelGGL((gdn_chunk_kernel<true, true>), grid, dim3(NTHR), 0, s, p);
   else if (o_norm)
-    hipLaunchKernelGGL((gdn_chunk_kernel<MODE_OUT, true>), grid, dim3(NTHR), 0, s, p);
+    hipLaunchKernelGGL((gdn_chunk_kernel<true, false>), grid, dim3(NTHR), 0, s, p);
   else if (p.fused)
-    hipLaunchKernelGGL((gdn_chunk_kernel<MODE_OUT, false, true>), grid, dim3(NTHR), 0, s, p);
+    hipLaunchKernelGGL((gdn_chunk_kernel<false, true>), grid, dim3(NTHR), 0, s, p);
   else
-    hipLaunchKernelGGL(gdn_chunk_kernel<MODE_OUT>, grid, dim3(NTHR), 0, s, p);
+    hipLaunchKernelGGL((gdn_chunk_kernel<false, false>), grid, dim3(NTHR), 0, s, p);
   if (staged) hipLaunchKernelGGL(gdn_state_copy_kernel, dim3(N, H), dim3(NTHR), 0, s, p);
   return check_launch("hmx_gdn_chunk_fwd");
 }

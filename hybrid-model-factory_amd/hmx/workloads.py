@@ -49,6 +49,49 @@ def gdn_inputs(T: int, H: int, HKV: int, D: int, dtype=torch.bfloat16, config_id
     return {n: t.to(device) for n, t in out.items()}
 
 
+def gdn_layer_gates(T: int, H: int, config_id: int = 11, device="cpu", gen_device="cpu"):
+    """Gates as a GDN layer forms them (fused_gdn_gating.py:66-76):
+    g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b), with A_log = log U(1, 16),
+    dt_bias the inverse softplus of dt ~ exp(U(log 1e-3, log 1e-1)) (the Mamba2
+    initialisation, training/.../layers/mamba/mamba2.py:194-201) and a, b ~ N(0, 1).
+    Many heads then decay by far less than e^-60 over a 512-token window.  Returns
+    (g, beta) as fp32 [1, T, H] on ``device``."""
+    gd = gen(config_id, gen_device)
+    A_log = torch.log(torch.rand(H, generator=gd, device=gen_device) * 15 + 1)
+    dt = torch.exp(torch.rand(H, generator=gd, device=gen_device) * (math.log(0.1) - math.log(1e-3))
+                   + math.log(1e-3))
+    dt_bias = dt + torch.log(-torch.expm1(-dt))
+    a = _randn(gd, (T, H), gen_device)
+    b = _randn(gd, (T, H), gen_device)
+    g = -torch.exp(A_log) * F.softplus(a + dt_bias)
+    return g.unsqueeze(0).to(device), torch.sigmoid(b).unsqueeze(0).to(device)
+
+
+def gdn_exact_pairs(g: torch.Tensor, beta: torch.Tensor, table, max_warm: int = 16,
+                    threshold: float = 60.0, chunk: int = 32) -> tuple[int, torch.Tensor]:
+    """The prefill plan's use of the exact segment scan, by the kernel's own rule:
+    (segment, head) pairs whose preceding max_warm chunks neither decay the dropped
+    history below e^-threshold (the decay bound of a token being
+    g + log max(1, |1 - beta|)) nor reach the sequence start, and the [H] mask of
+    heads with any such segment, which run the scan.  g, beta [1, T, H]; table: the
+    plan's [rows, 8] segment table."""
+    dec = (g[0].double() + torch.log(torch.clamp((1 - beta[0].double()).abs(), min=1.0))).cpu()
+    cs = torch.cat([torch.zeros(1, dec.shape[1], dtype=dec.dtype), dec.cumsum(0)])
+    pairs, heads = 0, torch.zeros(dec.shape[1], dtype=torch.bool)
+    for r in [list(map(int, x)) for x in table]:
+        n, bos, eos, c0 = r[:4]
+        if r[5] == 0:
+            continue
+        lo = max(0, c0 - max_warm)
+        if lo == 0:
+            continue                       # the warm-up starts at the sequence start
+        t0, t1 = bos + lo * chunk, min(eos, bos + c0 * chunk)
+        need = (cs[t1] - cs[t0]) > -threshold
+        pairs += int(need.sum())
+        heads |= need
+    return pairs, heads
+
+
 def varlen_lengths(n_seqs: int = 8, lo: int = 1024, hi: int = 8192, config_id: int = 1):
     """Sequence lengths ~ randint(lo, hi+1) from the config generator (drawn first)."""
     gd = gen(config_id)

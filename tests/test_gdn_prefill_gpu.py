@@ -4,8 +4,9 @@ recurrent kernel at the full C1 size.
 Covers: single segment with h0, ragged tails, GQA, multi-segment warm-up start
 states, the exact segment scan (weak decay, and use_qk_l2norm_in_kernel=False),
 heads mixing both, varlen with empty and 1-token sequences, B > 1 without
-cu_seqlens, bf16 g/beta, and C1 (T=32768, H=32, HKV 32 and 8) plus the
-8-sequence varlen C1 case.
+cu_seqlens, bf16 g/beta, and C1 (T=32768, H=32, HKV 32 and 8) with the benchmark's
+gates and with a freshly initialised layer's gates, plus the 8-sequence varlen C1
+case.
 """
 import pytest
 import torch
@@ -157,6 +158,40 @@ def test_prefill_c1_full_size(dev, HKV):
         output_final_state=True, use_qk_l2norm_in_kernel=True)
     assert_out_close(o[:, :, :hs], o_ref)
     assert_state_close(s[:, :hs], s_ref)
+
+
+def test_prefill_c1_layer_gates(dev):
+    """C1 with the gates of a freshly initialised GDN layer (weak decay on several
+    heads, so later segments of those heads take the exact segment scan).  All heads
+    vs the GPU recurrent kernel; the fp64 oracle on two heads that run the exact scan
+    and two that do not."""
+    from hmx import _lib
+    T, H = 32768, 32
+    d = wl.gdn_inputs(T=T, H=H, HKV=H, D=128, config_id=1)
+    q, k, v = d["q"], d["k"], d["v"]
+    g, beta = wl.gdn_layer_gates(T, H)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    table, _ = _lib.plan_segments(_lib.PLAN_GDN, [(0, T)], T, H, cus)
+    pairs, exact = wl.gdn_exact_pairs(g, beta, table)
+    print(f"{len(table)} segments, {pairs} exact (segment, head) pairs, "
+          f"{int(exact.sum())} heads", flush=True)
+    assert pairs > 0 and 0 < int(exact.sum()) < H
+    o, s = _run(dev, q, k, v, g, beta)
+    pool = torch.zeros(1, H, 128, 128, device=dev)
+    o_r, _ = hmx.fused_recurrent_gated_delta_rule_gqa(
+        *[x.to(dev) for x in (q, k, v, g, beta)], initial_state=pool, inplace_final_state=True,
+        cu_seqlens=torch.tensor([0, T], dtype=torch.int32, device=dev),
+        ssm_state_indices=torch.zeros(1, dtype=torch.int32, device=dev),
+        use_qk_l2norm_in_kernel=True)
+    torch.cuda.synchronize()
+    assert_out_close(o, o_r.float(), what="chunked vs recurrent o")
+    assert_state_close(s, pool, what="chunked vs recurrent state")
+    idx = torch.cat([exact.nonzero()[:2, 0], (~exact).nonzero()[:2, 0]])
+    o_ref, s_ref = ref.chunk_gated_delta_rule_gqa(
+        *(x[:, :, idx] for x in (q, k, v, g, beta)), output_final_state=True,
+        use_qk_l2norm_in_kernel=True)
+    assert_out_close(o[:, :, idx.to(dev)], o_ref)
+    assert_state_close(s[:, idx.to(dev)], s_ref)
 
 
 def test_prefill_c1_varlen(dev):
