@@ -16,14 +16,22 @@
 //   S^T    <- e^{A_L} S^T + B^T diag(dt' e^{A_L - A}) X
 // The state lives transposed (S^T, rows n, columns p) in MFMA accumulator
 // registers: wave w owns p-columns [16 PB w, 16 PB (w+1)) for every n, so the
-// C S^T product and the state update never leave the wave.  The state is linear
-// with a scalar decay per chunk, so a segment's start state is exact from a
-// scalar-decay combine of the other segments' zero-start end states (pass
-// LOCAL + combine, the carry of mamba_mixer_cp_utils.py:44-65).
+// products with the state never leave the wave.  The output is formed
+// transposed too (Y^T = S C^T + X^T M^T, rows p, columns t), and M as M^T = B C^T,
+// so every tile leaves the accumulators as 4 consecutive features of one row (one
+// 8-byte LDS write).  The state is linear with a scalar decay per chunk, so a
+// segment's start state is exact from a scalar-decay combine of the other
+// segments' zero-start end states (pass LOCAL + combine, the carry of
+// mamba_mixer_cp_utils.py:44-65).
 //
-// Numerics: x, B, C enter the MFMAs exactly (bf16 inputs); the fp32 factors
-// M, S and w x are each split into bf16 hi + lo so no product rounds them to
-// 8 bits (one rounding of M alone costs ~6e-3 absolute at |y| ~ 7).
+// Numerics: every MFMA operand is fp16 with fp32 accumulation.  x, B and C are
+// bf16 inputs, which fp16 holds exactly within its range (|v| < 65504; below
+// 6.1e-5 it keeps an absolute 6e-8); the fp32 factors S, M and w x are rounded
+// to fp16 once each (11 significant bits, against bf16's 8: one bf16 rounding of
+// M cost ~6e-3 absolute at |y| ~ 7, fp16's ~8e-4).  B and C are staged in the
+// interleaved feature order (icol) so the operands that pair with a state built
+// from two C-layout tiles are single 128-bit reads; row strides of 36 or 72
+// dwords keep those reads bank-conflict-free.
 //
 // Workgroup order: the 1-D grid maps block ids so that the heads sharing one
 // B/C group and segment have ids equal mod 8, i.e. land on one XCD and share
@@ -31,6 +39,8 @@
 //
 // Roofline: HBM-bound at the C4 shape (x, y, B, C, dt and the final state move
 // once; the LOCAL pass re-reads x, B and dt of all but the last segment).
+#include <type_traits>
+
 #include "common.hpp"
 #include "mfma.hpp"
 
@@ -39,7 +49,6 @@ namespace ssd {
 
 constexpr int L = 64;          // tokens per chunk
 constexpr int NTHR = 256;
-constexpr int LDM = L + 8;     // bf16 [L][L] row stride of M
 
 enum Mode { MODE_OUT = 0, MODE_LOCAL = 1 };
 
@@ -75,26 +84,29 @@ struct Params {
   float dt_min, dt_max;
 };
 
+// fp16 row strides (elements) for 64- and 128-wide rows: 36 and 72 dwords
+constexpr int row_ld(int w) { return w == 64 ? w + 8 : w + 16; }
+
 template <int P, int N>
 struct Cfg {
-  static constexpr int LDX = P + 8;   // bf16 [L][P] (x, y / z staging)
-  static constexpr int LDB = N + 8;   // bf16 [L][N] (B, C)
-  static constexpr int PB = P / 64;   // 16-wide p-blocks per wave
-  static constexpr int NB = N / 16;   // 16-row n-blocks of S^T
+  static constexpr int LDX = row_ld(P);   // fp16 [L][P] x; bf16 [L][P] y / z staging
+  static constexpr int LDB = row_ld(N);   // fp16 [L][N] B, C (interleaved features)
+  static constexpr int LDM = row_ld(L);   // fp16 [L][L] M (interleaved columns)
+  static constexpr int PB = P / 64;       // 16-wide p-blocks per wave
+  static constexpr int NB = N / 16;       // 16-row n-blocks of S^T
   static constexpr int VX = L * P / 8 / NTHR;   // 16-byte x vectors per thread
   static constexpr int VB = L * N / 8 / NTHR;   // 16-byte B (or C) vectors per thread
   static constexpr int OFF_X = 0;
   static constexpr int OFF_B = OFF_X + L * LDX * 2;
-  static constexpr int OFF_C = OFF_B + L * LDB * 2;
+  static constexpr int OFF_S = OFF_B + L * LDB * 2;
+  static constexpr int OFF_C = OFF_S + 2 * 4 * L * 4;   // two buffers of 4 scalar arrays
   static constexpr int OFF_M = OFF_C + L * LDB * 2;
   static constexpr int OFF_Y = OFF_M + L * LDM * 2;
-  static constexpr int OFF_S = OFF_Y + L * LDX * 2;
-  static constexpr int OFF_ML = OFF_S + 2 * 4 * L * 4;   // two buffers of 4 scalar arrays
-  // M's low half gets its own region when it fits (no barrier before writing M);
-  // otherwise it reuses C's space once every wave is done with C.
-  static constexpr bool SEP_ML = OFF_ML + L * LDM * 2 <= 80 * 1024;
-  static constexpr int SMEM = SEP_ML ? OFF_ML + L * LDM * 2 : OFF_ML;
-  static_assert(SMEM <= 80 * 1024, "LDS budget: two workgroups per CU");
+  static constexpr int SMEM_LOCAL = OFF_C;              // x, B, scalars
+  static constexpr int SMEM_OUT = OFF_Y + L * LDX * 2;
+  // two workgroups per CU, except the OUT pass at P = 128 (one; see the kernel)
+  static_assert(SMEM_LOCAL <= 80 * 1024, "LDS budget: two workgroups per CU");
+  static_assert(SMEM_OUT <= (P == 128 ? 160 : 80) * 1024, "LDS budget");
   static_assert(P % 64 == 0 && N % 32 == 0, "tile shape");
 };
 
@@ -153,28 +165,36 @@ __device__ __forceinline__ void load_raw(Raw<P, N>& r, const Params& p, int tok0
     r.dt = t < nval ? ld_any(p.dt, (int64_t)(tok0 + t) * p.dt_ts + h * p.dt_hs, p.dt_dt) : 0.f;
 }
 
-// Two workgroups per CU, except the OUT pass at P = 128: its 128x128 state and
-// staging need more than 256 registers, which at two waves per SIMD spilled 204 B
-// per lane; at one wave per SIMD it keeps them in VGPRs + AGPRs and runs 18%
-// faster (1.38 -> 1.13 ms at b=2, T=16384, H=G=64, P=N=128).
+__device__ __forceinline__ f16x8 to_h8(const bf16x8& x) {
+  f16x8 y;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) y[j] = (f16)(float)x[j];
+  return y;
+}
+
+// Two workgroups per CU, except the OUT pass at P = 128: its 128x128 state needs
+// more than 256 registers, which at two waves per SIMD spill; at one wave per
+// SIMD it keeps them in VGPRs + AGPRs.
 template <int P, int N, int MODE>
 __global__ __launch_bounds__(NTHR, (P == 128 && MODE == MODE_OUT) ? 1 : 2) void ssd_chunk_kernel(Params p) {
   using K = Cfg<P, N>;
-  constexpr int LDX = K::LDX, LDB = K::LDB, PB = K::PB, NB = K::NB;
-  __shared__ __align__(16) unsigned char smem[K::SMEM];
-  bf16* sX = reinterpret_cast<bf16*>(smem + K::OFF_X);
-  bf16* sB = reinterpret_cast<bf16*>(smem + K::OFF_B);
-  bf16* sC = reinterpret_cast<bf16*>(smem + K::OFF_C);
-  bf16* sM = reinterpret_cast<bf16*>(smem + K::OFF_M);
-  bf16* sY = reinterpret_cast<bf16*>(smem + K::OFF_Y);
+  constexpr int LDX = K::LDX, LDB = K::LDB, LDM = K::LDM, PB = K::PB, NB = K::NB;
+  __shared__ __align__(16) unsigned char smem[MODE == MODE_OUT ? K::SMEM_OUT : K::SMEM_LOCAL];
+  f16* sX = reinterpret_cast<f16*>(smem + K::OFF_X);
+  f16* sB = reinterpret_cast<f16*>(smem + K::OFF_B);
   float* sc = reinterpret_cast<float*>(smem + K::OFF_S);
+  f16* sC = reinterpret_cast<f16*>(smem + K::OFF_C);     // OUT only
+  f16* sM = reinterpret_cast<f16*>(smem + K::OFF_M);     // OUT only
+  bf16* sY = reinterpret_cast<bf16*>(smem + K::OFF_Y);   // OUT only
   // per-token scalars, double-buffered by chunk parity: SC(buf, slot, t)
   auto SC = [&](int buf, int slot, int t) -> float& { return sc[(buf * 4 + slot) * L + t]; };
   auto SC4 = [&](int buf, int slot, int t) -> f32x4 {
     return *reinterpret_cast<const f32x4*>(&sc[(buf * 4 + slot) * L + t]);
   };
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  // the wave index as a scalar: branches on it are uniform (MFMAs ignore EXEC)
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int q4 = lane >> 4, l16 = lane & 15;
   // XCD-aware block order: ids of the heads of one (segment, group) agree mod 8.
   const int H = p.H, G = p.G, HG = H / G;
@@ -261,22 +281,22 @@ __global__ __launch_bounds__(NTHR, (P == 128 && MODE == MODE_OUT) ? 1 : 2) void 
     }
   };
 
-  // Per chunk (OUT): stage | C S^T, M, state update | M X + epilogue, with the
-  // previous chunk's y stored while this one is staged.
+  // Per chunk (OUT): stage | Y^T = S C^T, M^T, state update | Y^T += X^T M^T +
+  // epilogue, with the previous chunk's y stored while this one is staged.
   const auto chunk = [&](Raw<P, N>& cur, Raw<P, N>& nxt, int c) {
     const int tok0 = si.bos + c * L;
     const int cb = (c - si.c_start) & 1;
-    // ---- stage chunk c, then refill `cur` with chunk c + AHEAD -------------------
+    // ---- stage chunk c (fp16; B and C interleaved), then refill `cur` ------------
 #pragma unroll
     for (int i = 0; i < K::VX; ++i) {
       const int e = tid + NTHR * i, row = e / (P / 8), c8 = (e % (P / 8)) * 8;
-      *reinterpret_cast<bf16x8*>(sX + row * LDX + c8) = cur.x[i];
+      *reinterpret_cast<f16x8*>(sX + row * LDX + c8) = to_h8(cur.x[i]);
     }
 #pragma unroll
     for (int i = 0; i < K::VB; ++i) {
       const int e = tid + NTHR * i, row = e / (N / 8), c8 = (e % (N / 8)) * 8;
-      *reinterpret_cast<bf16x8*>(sB + row * LDB + c8) = cur.b[i];
-      if (MODE == MODE_OUT) *reinterpret_cast<bf16x8*>(sC + row * LDB + c8) = cur.c[i];
+      store8_i(sB + row * LDB, c8, to_h8(cur.b[i]));
+      if (MODE == MODE_OUT) store8_i(sC + row * LDB, c8, to_h8(cur.c[i]));
     }
     if (MODE == MODE_OUT && c > si.c_start) store_y(tok0 - L, L);
     bf16x8 zst[K::VX];
@@ -289,9 +309,19 @@ __global__ __launch_bounds__(NTHR, (P == 128 && MODE == MODE_OUT) ? 1 : 2) void 
     lds_barrier();
     const float al = SC(cb, S_ACS, L - 1);
 
-    f32x4 Y[4][PB];
+    // X^T operands of this wave's p-columns, t in the paired-tile order
+    // (t0 + 4q4 + v, t0 + 16 + 4q4 + v): the B operand of the state update (scaled
+    // by w) and the A operand of X^T M^T
+    f16x8 xt[PB][2];
+#pragma unroll
+    for (int i = 0; i < PB; ++i)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        xt[i][ks] = frag_t_perm_h(sX, LDX, 32 * ks, 16 * (PB * wave + i), lane);
+
+    f32x4 YT[PB][4];   // Y^T tile (p rows 16(PB wave + i) + 4q4 + v, t columns 16tb + l16)
     if (MODE == MODE_OUT) {
-      // z into the y staging buffer (read back in C layout by the owner lanes)
+      // z into the y staging buffer (read back per row by the owner lanes)
       if (p.z) {
 #pragma unroll
         for (int i = 0; i < K::VX; ++i) {
@@ -299,97 +329,82 @@ __global__ __launch_bounds__(NTHR, (P == 128 && MODE == MODE_OUT) ? 1 : 2) void 
           *reinterpret_cast<bf16x8*>(sY + row * LDX + c8) = zst[i];
         }
       }
-      // ---- Y = diag(e^A) C S^T (S as bf16 hi + lo) ------------------------------
+      // ---- Y^T = S C^T diag(e^A): A = S (two C-layout tiles), B = C rows ----------
 #pragma unroll
-      for (int tb = 0; tb < 4; ++tb)
+      for (int i = 0; i < PB; ++i)
 #pragma unroll
-        for (int i = 0; i < PB; ++i) Y[tb][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int tb = 0; tb < 4; ++tb) YT[i][tb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < N / 32; ++ks) {
-        bf16x8 bh[PB], bl[PB];
+        f16x8 sa[PB];
 #pragma unroll
-        for (int i = 0; i < PB; ++i) pack_b_hilo(ST[2 * ks][i], ST[2 * ks + 1][i], bh[i], bl[i]);
+        for (int i = 0; i < PB; ++i) sa[i] = h8(ST[2 * ks][i], ST[2 * ks + 1][i]);
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) {
-          const bf16x8 a = frag_perm(sC, LDB, 16 * tb, 32 * ks, lane);
+          const f16x8 bc = frag_i(sC, LDB, 16 * tb, 32 * ks, lane);
 #pragma unroll
-          for (int i = 0; i < PB; ++i) {
-            Y[tb][i] = mfma16(a, bh[i], Y[tb][i]);
-            Y[tb][i] = mfma16(a, bl[i], Y[tb][i]);
-          }
+          for (int i = 0; i < PB; ++i) YT[i][tb] = mfma16h(sa[i], bc, YT[i][tb]);
         }
       }
 #pragma unroll
       for (int tb = 0; tb < 4; ++tb) {
-        const f32x4 ea4 = SC4(cb, S_EA, 16 * tb + 4 * q4);
+        const float e = SC(cb, S_EA, 16 * tb + l16);
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const float e = ea4[v];
+        for (int i = 0; i < PB; ++i)
 #pragma unroll
-          for (int i = 0; i < PB; ++i) Y[tb][i][v] *= e;
-        }
+          for (int v = 0; v < 4; ++v) YT[i][tb][v] *= e;
       }
-      // ---- M = (C B^T) o decay o dt as bf16 hi + lo (lower tiles; (0,1), (2,3)
-      // zeroed).  Tiles per wave: w0 (0,0)(1,0)(2,0)+zero(0,1);
-      // w1 (1,1)(2,1)(3,0)+zero(2,3); w2 (2,2)(3,1); w3 (3,2)(3,3) -------------
+      // ---- M^T = B C^T o decay o dt: tile (tb, jb) holds M[t = 16tb + l16][j =
+      // 16jb + 4q4 + v], written as 4 consecutive (interleaved) columns of row t.
+      // Lower tiles only; (0,1) and (2,3) are zeroed (M X reads them).  Tiles per
+      // wave: w0 (0,0)(1,0)(2,0)+zero(0,1); w1 (1,1)(2,1)(3,0)+zero(2,3);
+      // w2 (2,2)(3,1); w3 (3,2)(3,3) --------------------------------------------
       constexpr int TT[4][3][2] = {{{0, 0}, {1, 0}, {2, 0}}, {{1, 1}, {2, 1}, {3, 0}},
                                    {{2, 2}, {3, 1}, {-1, -1}}, {{3, 2}, {3, 3}, {-1, -1}}};
-      bf16x4 mh[3], ml[3];
+      auto m_tile = [&](auto w_c) {
+        constexpr int W = decltype(w_c)::value;
 #pragma unroll
-      for (int k = 0; k < 3; ++k) {
-        const int tb = TT[wave][k][0], jb = TT[wave][k][1];
-        if (tb < 0) continue;
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        for (int k = 0; k < 3; ++k) {
+          constexpr int tb_[3] = {TT[W][0][0], TT[W][1][0], TT[W][2][0]};
+          constexpr int jb_[3] = {TT[W][0][1], TT[W][1][1], TT[W][2][1]};
+          const int tb = tb_[k], jb = jb_[k];
+          if (tb < 0) continue;
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ks = 0; ks < N / 32; ++ks)
-          acc = mfma16(frag(sC, LDB, 16 * tb, 32 * ks, lane), frag(sB, LDB, 16 * jb, 32 * ks, lane), acc);
-        const int j = 16 * jb + l16;
-        const float aj = SC(cb, S_ACS, j), dj = SC(cb, S_DT, j);
-        const f32x4 at4 = SC4(cb, S_ACS, 16 * tb + 4 * q4);
-        f32x4 m;
+          for (int ks = 0; ks < N / 32; ++ks)
+            acc = mfma16h(frag_i(sB, LDB, 16 * jb, 32 * ks, lane),
+                          frag_i(sC, LDB, 16 * tb, 32 * ks, lane), acc);
+          const int t = 16 * tb + l16, j0 = 16 * jb + 4 * q4;
+          const float at = SC(cb, S_ACS, t);
+          const f32x4 aj = SC4(cb, S_ACS, j0), dj = SC4(cb, S_DT, j0);
+          f32x4 m;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int t = 16 * tb + 4 * q4 + v;
-          m[v] = (t >= j) ? acc[v] * fast_exp(at4[v] - aj) * dj : 0.f;
+          for (int v = 0; v < 4; ++v) m[v] = (t >= j0 + v) ? acc[v] * fast_exp(at - aj[v]) * dj[v] : 0.f;
+          *reinterpret_cast<f16x4*>(sM + t * LDM + icol(j0)) = h4(m);
         }
-        bf16x2 h0, h1, l0, l1;
-        split2(m[0], m[1], h0, l0);
-        split2(m[2], m[3], h1, l1);
-        mh[k] = bf16x4{h0[0], h0[1], h1[0], h1[1]};
-        ml[k] = bf16x4{l0[0], l0[1], l1[0], l1[1]};
-      }
+        if constexpr (W < 2) {
+          constexpr int tb = W == 0 ? 0 : 2;
+          *reinterpret_cast<f16x4*>(sM + (16 * tb + l16) * LDM + icol(16 * (tb + 1) + 4 * q4)) =
+              f16x4{0.f, 0.f, 0.f, 0.f};
+        }
+      };
+      using I0 = std::integral_constant<int, 0>;
+      using I1 = std::integral_constant<int, 1>;
+      using I2 = std::integral_constant<int, 2>;
+      using I3 = std::integral_constant<int, 3>;
+      if (wave == 0) m_tile(I0{});
+      else if (wave == 1) m_tile(I1{});
+      else if (wave == 2) m_tile(I2{});
+      else m_tile(I3{});
       // the last wave (fewest tiles) turns the next chunk's dt into its scalars
       if (wave == NTHR / 64 - 1 && c + 1 < si.c_end) make_scalars(nxt.dt, c + 1, cb ^ 1);
-      if constexpr (!K::SEP_ML) lds_barrier();   // every wave is done with sC: M's low half goes there
-      bf16* sML = K::SEP_ML ? reinterpret_cast<bf16*>(smem + K::OFF_ML) : sC;
-#pragma unroll
-      for (int k = 0; k < 3; ++k) {
-        const int tb = TT[wave][k][0], jb = TT[wave][k][1];
-        if (tb < 0) continue;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int a = (16 * tb + 4 * q4 + v) * LDM + 16 * jb + l16;
-          sM[a] = mh[k][v];
-          sML[a] = ml[k][v];
-        }
-      }
-      if (wave < 2) {
-        const int tb = wave == 0 ? 0 : 2;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int a = (16 * tb + 4 * q4 + v) * LDM + 16 * (tb + 1) + l16;
-          sM[a] = (bf16)0.f;
-          sML[a] = (bf16)0.f;
-        }
-      }
     } else if (wave == NTHR / 64 - 1 && c + 1 < si.c_end) {
       make_scalars(nxt.dt, c + 1, cb ^ 1);
     }
 
-    // ---- S^T <- e^{A_L} S^T + B^T diag(w) X (after C S^T used the chunk's start
-    // state).  With one p-block per wave it runs before the M X phase; with two,
-    // after it, where the Y accumulators of C S^T are no longer live next to it.
-    const auto state_update = [&]() {
+    // ---- S^T <- e^{A_L} S^T + B^T diag(w) X (after Y^T used the chunk's start
+    // state): A = B^T (transposing read), B = w X (one rounding) -----------------
+    {
       const float ea = fast_exp(al);
       dsum += al;
 #pragma unroll
@@ -400,78 +415,60 @@ __global__ __launch_bounds__(NTHR, (P == 128 && MODE == MODE_OUT) ? 1 : 2) void 
           for (int v = 0; v < 4; ++v) ST[nb][i][v] *= ea;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        const f32x4 w0 = SC4(cb, S_W, 32 * ks + 8 * q4), w1 = SC4(cb, S_W, 32 * ks + 8 * q4 + 4);
-        const float w[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
-        // w x as bf16 hi + lo: one rounding of it would cost ~1e-3 of |S|
-        bf16x8 bwh[PB], bwl[PB];
+        const f32x4 w0 = SC4(cb, S_W, 32 * ks + 4 * q4), w1 = SC4(cb, S_W, 32 * ks + 16 + 4 * q4);
+        f16x8 bw[PB];
 #pragma unroll
-        for (int i = 0; i < PB; ++i) {
-          const bf16x8 xr = frag_t(sX, LDX, 32 * ks, 16 * (PB * wave + i), lane);
+        for (int i = 0; i < PB; ++i)
 #pragma unroll
-          for (int j = 0; j < 8; j += 2) {
-            bf16x2 hh, ll;
-            split2((float)xr[j] * w[j], (float)xr[j + 1] * w[j + 1], hh, ll);
-            bwh[i][j] = hh[0]; bwh[i][j + 1] = hh[1];
-            bwl[i][j] = ll[0]; bwl[i][j + 1] = ll[1];
+          for (int v = 0; v < 4; ++v) {
+            bw[i][v] = (f16)((float)xt[i][ks][v] * w0[v]);
+            bw[i][4 + v] = (f16)((float)xt[i][ks][4 + v] * w1[v]);
           }
-        }
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-          const bf16x8 a = frag_t(sB, LDB, 32 * ks, 16 * nb, lane);
+          const f16x8 a = frag_t_i(sB, LDB, 32 * ks, 16 * nb, lane);
 #pragma unroll
-          for (int i = 0; i < PB; ++i) {
-            ST[nb][i] = mfma16(a, bwh[i], ST[nb][i]);
-            ST[nb][i] = mfma16(a, bwl[i], ST[nb][i]);
-          }
+          for (int i = 0; i < PB; ++i) ST[nb][i] = mfma16h(a, bw[i], ST[nb][i]);
         }
       }
-    };
-    constexpr bool EARLY_UPDATE = (PB == 1) || (MODE == MODE_LOCAL);
-    if (EARLY_UPDATE) state_update();
+    }
 
     if (MODE == MODE_OUT) {
       lds_barrier();   // M complete
-      // ---- Y += M X (+ D x, z gate) -> sY -----------------------------------------
-      const bf16* sML = K::SEP_ML ? reinterpret_cast<const bf16*>(smem + K::OFF_ML) : sC;
-      bf16x8 bx[2][PB];
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-        for (int i = 0; i < PB; ++i) bx[ks][i] = frag_t(sX, LDX, 32 * ks, 16 * (PB * wave + i), lane);
+      // ---- Y^T += X^T M^T (+ D x, z gate) -> sY ------------------------------------
 #pragma unroll
       for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
         for (int ks = 0; ks <= tb / 2; ++ks) {
-          const bf16x8 ah = frag(sM, LDM, 16 * tb, 32 * ks, lane);
-          const bf16x8 a_l = frag(sML, LDM, 16 * tb, 32 * ks, lane);
+          const f16x8 bm = frag_i(sM, LDM, 16 * tb, 32 * ks, lane);
 #pragma unroll
-          for (int i = 0; i < PB; ++i) {
-            Y[tb][i] = mfma16(ah, bx[ks][i], Y[tb][i]);
-            Y[tb][i] = mfma16(a_l, bx[ks][i], Y[tb][i]);
-          }
+          for (int i = 0; i < PB; ++i) YT[i][tb] = mfma16h(xt[i][ks], bm, YT[i][tb]);
         }
 #pragma unroll
       for (int i = 0; i < PB; ++i) {
-        const int pc = 16 * (PB * wave + i);
-        const float dv = p.D ? p.D[h * P + pc + l16] : 0.f;
+        const int p0 = 16 * (PB * wave + i) + 4 * q4;
+        const f32x4 dv = p.D ? *reinterpret_cast<const f32x4*>(p.D + h * P + p0)
+                             : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) {
-          const bf16x4 xv = ld_tr(sX, LDX, 16 * tb + 4 * q4, pc, lane);
+          const int t = 16 * tb + l16;
+          const f16x4 xv = *reinterpret_cast<const f16x4*>(sX + t * LDX + p0);
           bf16x4 zv;
-          if (p.z) zv = ld_tr(sY, LDX, 16 * tb + 4 * q4, pc, lane);
+          if (p.z) zv = *reinterpret_cast<const bf16x4*>(sY + t * LDX + p0);
+          bf16x4 out;
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
-            float yv = Y[tb][i][v] + dv * (float)xv[v];
+            float yv = YT[i][tb][v] + dv[v] * (float)xv[v];
             if (p.z) {
               const float zz = (float)zv[v];
               yv *= zz / (1.f + fast_exp(-zz));
             }
-            sY[(16 * tb + 4 * q4 + v) * LDX + pc + l16] = (bf16)yv;
+            out[v] = (bf16)yv;
           }
+          *reinterpret_cast<bf16x4*>(sY + t * LDX + p0) = out;
         }
       }
     }
-    if (!EARLY_UPDATE) state_update();
     lds_barrier();
   };
 
