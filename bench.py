@@ -1,7 +1,7 @@
 """Benchmark of the linear-recurrent mixer hot path on one MI355X.
 
 Headline (``value``): GDN chunked prefill at BASELINE config C1 — B=1, T=32768,
-H=32, d=128, chunk 64, bf16 q/k/v, fp32 g/beta, zero initial state, fp32 final
+H=32, d=128 (the kernel walks 32-token chunks), bf16 q/k/v, fp32 g/beta, zero initial state, fp32 final
 state — in tokens/s; one "step" is one call of chunk_gated_delta_rule_gqa over
 the whole sequence with inputs resident in HBM.  Also reported: GDN decode at
 C2 (256 sequences x 1 token, H=32, fp32 state pool of 512 MiB through a random
@@ -13,7 +13,12 @@ reported under ``gka`` against the bf16 MFMA roofline; the Mamba2 SSD chunk scan
 at C4 under ``ssd`` and its single-token state update under ``ssd_decode``, both
 against HBM.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only prefill|decode|gka|ssd|onorm|conv|core]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only LEGS]
+  --only takes comma-separated legs (c1, prefill_gqa, prefill_varlen,
+  prefill_layer_gates, onorm, conv, gdn_core, mamba2_core, gka_core, gdn_decode,
+  gka_decode, ssd_c4, ssd_primed, ssd_decode, gka8, gka32) or groups (prefill, core,
+  decode, ssd, gka); one leg alone is what the committed rocprofv3 counter runs
+  profile.
 """
 from __future__ import annotations
 
@@ -540,6 +545,17 @@ def bench_ssd_decode(dev, steps=64, warmup=4):
     return dict(ms=ms, steps_per_s=1e3 / ms, bytes=by, GBps=by / (ms * 1e-3) / 1e9)
 
 
+def cpu_model():
+    """The host CPU's model name (as lscpu reports it), from /proc/cpuinfo."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(sample_tokens=32768):
     """The oracle's chunked fp32 restatement on the host, on the whole C1 workload
     (T=32768, H=32; a few seconds on the box's host cores)."""
@@ -557,7 +573,7 @@ def cpu_baseline(sample_tokens=32768):
                                    dtype=torch.float32)
     dt = time.perf_counter() - t0
     return dict(value=sample_tokens / dt, unit="tokens/s", cores=torch.get_num_threads(),
-                kind="port", sample=f"C1 {sample_tokens} tokens x 32 heads (the whole workload), "
+                cpu=cpu_model(), kind="port", sample=f"C1 {sample_tokens} tokens x 32 heads (the whole workload), "
                 f"oracle chunked form (chunk 64) in fp32 torch on CPU, {dt:.2f} s")
 
 
@@ -583,7 +599,7 @@ def cpu_baselines_more():
             inplace_final_state=True, cu_seqlens=d["cu_seqlens"], ssm_state_indices=d["idx"],
             use_qk_l2norm_in_kernel=True, dtype=f32)
     dt = time.perf_counter() - t0
-    out["decode"] = dict(value=steps / dt, unit="steps/s", cores=cores, kind="port",
+    out["decode"] = dict(value=steps / dt, unit="steps/s", cores=cores, cpu=cpu_model(), kind="port",
                          sample=f"C2 {steps} of 512 steps (256 seqs x 32 heads), oracle "
                                 f"recurrence in fp32 torch on CPU, {dt:.2f} s")
     T = 1024
@@ -593,7 +609,7 @@ def cpu_baselines_more():
                                    g["beta"], 128 ** -0.5, ridge_ratio=0.01, num_iter=8,
                                    dtype=f32)
     dt = time.perf_counter() - t0
-    out["gka_num_iter_8"] = dict(value=T / dt, unit="tokens/s", cores=cores, kind="port",
+    out["gka_num_iter_8"] = dict(value=T / dt, unit="tokens/s", cores=cores, cpu=cpu_model(), kind="port",
                                  sample=f"C3 first {T} tokens x 32 heads, num_iter 8, oracle "
                                         f"per-token form in fp32 torch on CPU, {dt:.2f} s")
     x = wl.ssd_inputs()
@@ -602,7 +618,7 @@ def cpu_baselines_more():
                                    dt_bias=x["dt_bias"], dt_softplus=True,
                                    return_final_states=True, dtype=f32)
     dt = time.perf_counter() - t0
-    out["ssd"] = dict(value=2 * 16384 / dt, unit="tokens/s", cores=cores, kind="port",
+    out["ssd"] = dict(value=2 * 16384 / dt, unit="tokens/s", cores=cores, cpu=cpu_model(), kind="port",
                       sample=f"C4 whole workload (2 x 16384 tokens x 64 heads), oracle chunked "
                              f"form in fp32 torch on CPU, {dt:.2f} s")
     return out
@@ -627,13 +643,35 @@ def measured_traffic(key):
         return None
 
 
+# bench legs in run order (the long compute-bound GKA legs last), and the groups
+# --only accepts beside single legs
+LEGS = ["c1", "prefill_gqa", "prefill_varlen", "prefill_layer_gates", "onorm", "conv", "gdn_core",
+        "mamba2_core", "gka_core", "gdn_decode", "gka_decode", "ssd_c4", "ssd_primed",
+        "ssd_decode", "gka8", "gka32"]
+GROUPS = {"prefill": ["c1", "prefill_gqa", "prefill_varlen", "prefill_layer_gates"],
+          "core": ["gdn_core", "mamba2_core", "gka_core"], "decode": ["gdn_decode", "gka_decode"],
+          "ssd": ["ssd_c4", "ssd_primed", "ssd_decode"], "gka": ["gka8", "gka32"]}
+
+
+def measured_mfma_busy(key):
+    """Counter-based MFMA busy fraction of the leg's dominant kernel
+    (SQ_VALU_MFMA_BUSY_CYCLES over the SIMDs' cycles) from the committed summary."""
+    f = REPO / "profiles" / "traffic.json"
+    try:
+        return json.loads(f.read_text())[key]["mfma_busy"]["frac"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "decode", "gka", "ssd", "onorm", "conv", "core"], default=None)
+    ap.add_argument("--only", default=None,
+                    help="comma-separated legs (" + ", ".join(LEGS) + ") or groups (" +
+                         ", ".join(GROUPS) + "); default: all")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (HBM counter calibration)")
     a = ap.parse_args()
@@ -642,36 +680,45 @@ def main():
               "communication inside the op, so multi-GPU runs are not part of this build.",
               file=sys.stderr)
         sys.exit(2)
+    sel = []
+    for name in (a.only.split(",") if a.only else LEGS):
+        name = name.strip()
+        if name in GROUPS:
+            sel += GROUPS[name]
+        elif name in LEGS:
+            sel.append(name)
+        else:
+            ap.error(f"unknown leg {name!r}")
     import torch
     dev = torch.device("cuda:0")
     if a.copy_calibration:
         print(json.dumps({"copy_calibration": copy_calibration(dev)}), flush=True)
         return
     out = {}
-    if a.only in (None, "prefill"):
-        pf = bench_prefill(dev, a.steps, a.warmup)
-        out["prefill"] = pf
-        out["prefill_gqa"] = bench_prefill(dev, a.steps, a.warmup, HKV=8)
-        out["prefill_varlen"] = bench_prefill_varlen(dev, a.steps, a.warmup)
-        out["prefill_layer_gates"] = bench_prefill_layer_gates(dev, a.steps, a.warmup)
-    if a.only in (None, "onorm"):
-        out["onorm"] = bench_onorm(dev, a.steps, a.warmup)
-    if a.only in (None, "conv"):
-        out["conv"] = bench_conv(dev, a.steps, a.warmup)
-    if a.only in (None, "core"):
-        out["core"] = bench_core(dev, max(2, a.steps // 2), a.warmup)
-        out["mamba2_core"] = bench_mamba2_core(dev, max(2, a.steps // 2), a.warmup)
-        out["gka_core"] = bench_gka_core(dev, max(2, a.steps // 4), 1)
-    if a.only in (None, "decode"):
-        out["decode"] = bench_decode(dev)
-        out["gka_decode"] = bench_gka_decode(dev)
-    if a.only in (None, "ssd"):
-        out["ssd"] = bench_ssd(dev, a.steps, a.warmup)
-        out["ssd_primed"] = bench_ssd(dev, max(2, a.steps // 2), a.warmup, P=128, N=128, G=64)
-        out["ssd_decode"] = bench_ssd_decode(dev)
-    # last: the GKA legs are long and compute-bound
-    if a.only in (None, "gka"):
-        out["gka"] = {n: bench_gka(dev, max(2, a.steps // 4), 1, n) for n in (8, 32)}
+    S, W = a.steps, a.warmup
+    run = {
+        "c1": lambda: out.__setitem__("prefill", bench_prefill(dev, S, W)),
+        "prefill_gqa": lambda: out.__setitem__("prefill_gqa", bench_prefill(dev, S, W, HKV=8)),
+        "prefill_varlen": lambda: out.__setitem__("prefill_varlen", bench_prefill_varlen(dev, S, W)),
+        "prefill_layer_gates": lambda: out.__setitem__("prefill_layer_gates",
+                                                       bench_prefill_layer_gates(dev, S, W)),
+        "onorm": lambda: out.__setitem__("onorm", bench_onorm(dev, S, W)),
+        "conv": lambda: out.__setitem__("conv", bench_conv(dev, S, W)),
+        "gdn_core": lambda: out.__setitem__("core", bench_core(dev, max(2, S // 2), W)),
+        "mamba2_core": lambda: out.__setitem__("mamba2_core", bench_mamba2_core(dev, max(2, S // 2), W)),
+        "gka_core": lambda: out.__setitem__("gka_core", bench_gka_core(dev, max(2, S // 4), 1)),
+        "gdn_decode": lambda: out.__setitem__("decode", bench_decode(dev)),
+        "gka_decode": lambda: out.__setitem__("gka_decode", bench_gka_decode(dev)),
+        "ssd_c4": lambda: out.__setitem__("ssd", bench_ssd(dev, S, W)),
+        "ssd_primed": lambda: out.__setitem__(
+            "ssd_primed", bench_ssd(dev, max(2, S // 2), W, P=128, N=128, G=64)),
+        "ssd_decode": lambda: out.__setitem__("ssd_decode", bench_ssd_decode(dev)),
+        "gka8": lambda: out.setdefault("gka", {}).__setitem__(8, bench_gka(dev, max(2, S // 4), 1, 8)),
+        "gka32": lambda: out.setdefault("gka", {}).__setitem__(32, bench_gka(dev, max(2, S // 4), 1, 32)),
+    }
+    for name in LEGS:           # run order: the long compute-bound GKA legs last
+        if name in sel:
+            run[name]()
     line = {
         "metric": "mixer prefill tokens/sec + decode steps/sec at 8B shape; % of roofline (1 GPU)",
         "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
@@ -693,7 +740,8 @@ def main():
                          "kernel": "all launches of one prefill op call",
                          "algorithmic_bytes": pf["bytes"],
                          "mfma_TFLOPs": round(pf["TFLOPs"], 1),
-                         "mfma_frac": round(pf["TFLOPs"] / BF16_PEAK_TFLOPS, 4)},
+                         "mfma_frac": round(pf["TFLOPs"] / BF16_PEAK_TFLOPS, 4),
+                         "mfma_busy_counter": measured_mfma_busy("gdn_prefill_c1")},
         })
     if "prefill_gqa" in out:
         r = out["prefill_gqa"]
@@ -703,9 +751,11 @@ def main():
                        "HKV": 8, "d": 128},
             "roofline": {"bound": "hbm", "achieved": round(r["GBps"], 1), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(r["GBps"] / HBM_PEAK_GBS, 4),
-                         "algorithmic_bytes": r["bytes"], "traffic": None,
+                         "algorithmic_bytes": r["bytes"],
+                         "traffic": measured_traffic("gdn_prefill_gqa"),
                          "mfma_TFLOPs": round(r["TFLOPs"], 1)},
         }
+    if "prefill_varlen" in out:
         r = out["prefill_varlen"]
         line["prefill_varlen"] = {
             "value": round(r["tokens_per_s"], 1), "unit": "tokens/s", "ms_per_step": round(r["ms"], 4),
@@ -714,13 +764,15 @@ def main():
                        "initial_state": "zeros fp32 [8,32,128,128]"},
             "roofline": {"bound": "hbm", "achieved": round(r["GBps"], 1), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(r["GBps"] / HBM_PEAK_GBS, 4),
-                         "algorithmic_bytes": r["bytes"], "traffic": None},
+                         "algorithmic_bytes": r["bytes"],
+                         "traffic": measured_traffic("gdn_prefill_varlen")},
         }
     if "prefill_layer_gates" in out:
         r = out["prefill_layer_gates"]
         line["prefill_layer_gates"] = {
             "value": round(r["tokens_per_s"], 1), "unit": "tokens/s", "ms_per_step": round(r["ms"], 4),
-            "vs_c1_bench_gates": round(r["ms"] / out["prefill"]["ms"], 3),
+            "vs_c1_bench_gates": (round(r["ms"] / out["prefill"]["ms"], 3)
+                                  if "prefill" in out else None),
             "config": {"workload": "C1 with layer-initialisation gates (A_log ~ log U(1,16), "
                                    "dt ~ logU(1e-3, 1e-1), a, b ~ N(0,1))",
                        "T": 32768, "H": 32, "HKV": 32, "d": 128, "segments": r["segments"],
@@ -729,7 +781,8 @@ def main():
                        "heads_running_exact_scan": r["exact_heads"]},
             "roofline": {"bound": "hbm", "achieved": round(r["GBps"], 1), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(r["GBps"] / HBM_PEAK_GBS, 4),
-                         "algorithmic_bytes": r["bytes"], "traffic": None},
+                         "algorithmic_bytes": r["bytes"],
+                         "traffic": measured_traffic("gdn_prefill_layer_gates")},
         }
     if "decode" in out:
         dc = out["decode"]
@@ -759,7 +812,8 @@ def main():
             "norm_roofline": {"bound": "hbm", "achieved": round(r["norm_GBps"], 1),
                               "peak": HBM_PEAK_GBS, "unit": "GB/s",
                               "frac": round(r["norm_GBps"] / HBM_PEAK_GBS, 4),
-                              "algorithmic_bytes": r["norm_bytes"], "traffic": None},
+                              "algorithmic_bytes": r["norm_bytes"],
+                              "traffic": measured_traffic("gated_norm")},
         }
     if "conv" in out:
         r = out["conv"]
@@ -773,12 +827,14 @@ def main():
             "prefill_roofline": {"bound": "hbm", "achieved": round(r["fwd_GBps"], 1),
                                  "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                  "frac": round(r["fwd_GBps"] / HBM_PEAK_GBS, 4),
-                                 "algorithmic_bytes": r["fwd_bytes"], "traffic": None},
+                                 "algorithmic_bytes": r["fwd_bytes"],
+                                 "traffic": measured_traffic("conv1d_prefill")},
             "decode_ms": round(r["ms_dec"], 4),
             "decode_roofline": {"bound": "hbm", "achieved": round(r["dec_GBps"], 1),
                                 "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                 "frac": round(r["dec_GBps"] / HBM_PEAK_GBS, 4),
-                                "algorithmic_bytes": r["dec_bytes"], "traffic": None},
+                                "algorithmic_bytes": r["dec_bytes"],
+                                "traffic": measured_traffic("conv1d_decode")},
         }
     if "core" in out:
         r = out["core"]
@@ -820,6 +876,7 @@ def main():
                              "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                              "frac": round(r["TFLOPs"] / BF16_PEAK_TFLOPS, 4),
                              "traffic": measured_traffic(f"gka_prefill_c3_n{n}"),
+                             "mfma_busy_counter": measured_mfma_busy(f"gka_prefill_c3_n{n}"),
                              "algorithmic_flops": r["flops"],
                              "hbm_GBps": round(r["GBps"], 1)},
             }
@@ -833,8 +890,10 @@ def main():
                          "unit": "GB/s", "frac": round(r["GBps"] / HBM_PEAK_GBS, 4),
                          "traffic": measured_traffic("ssd_c4"), "algorithmic_bytes": r["bytes"],
                          "mfma_TFLOPs": round(r["TFLOPs"], 1),
-                         "mfma_frac": round(r["TFLOPs"] / BF16_PEAK_TFLOPS, 4)},
+                         "mfma_frac": round(r["TFLOPs"] / BF16_PEAK_TFLOPS, 4),
+                         "mfma_busy_counter": measured_mfma_busy("ssd_c4")},
         }
+    if "ssd_primed" in out:
         r = out["ssd_primed"]
         line["ssd_primed"] = {
             "value": round(r["tokens_per_s"], 1), "unit": "tokens/s", "ms_per_step": round(r["ms"], 4),
@@ -842,8 +901,9 @@ def main():
                        "T": 16384, "H": 64, "P": 128, "N": 128, "G": 64},
             "roofline": {"bound": "hbm", "achieved": round(r["GBps"], 1), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(r["GBps"] / HBM_PEAK_GBS, 4),
-                         "algorithmic_bytes": r["bytes"], "traffic": None},
+                         "algorithmic_bytes": r["bytes"], "traffic": measured_traffic("ssd_primed")},
         }
+    if "ssd_decode" in out:
         r = out["ssd_decode"]
         line["ssd_decode"] = {
             "value": round(r["steps_per_s"], 1), "unit": "steps/s", "ms_per_step": round(r["ms"], 4),
@@ -862,7 +922,7 @@ def main():
                        "H": 32, "d": 128, "num_iter": 8, "pools": "fp32 h_kk, h_kv [256,32,128,128]"},
             "roofline": {"bound": "hbm", "achieved": round(r["GBps"], 1), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(r["GBps"] / HBM_PEAK_GBS, 4),
-                         "traffic": None, "algorithmic_bytes": r["bytes"]},
+                         "traffic": measured_traffic("gka_decode"), "algorithmic_bytes": r["bytes"]},
         }
     if not a.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
