@@ -24,11 +24,9 @@ namespace gkad {
 
 constexpr int D = 128;
 
-// The decode's gates from the raw projections.  Kept out of line, so every kernel
-// variant (with and without the output norm) runs the same instructions and
-// updates the states identically.
-__device__ __attribute__((noinline)) void proj_gates(const hmx_gate_proj& gp, int64_t t, int h,
-                                                     float& alpha, float& egk, float& bscale) {
+// The decode's gates from the raw projections.
+__device__ __forceinline__ void proj_gates(const hmx_gate_proj& gp, int64_t t, int h,
+                                           float& alpha, float& egk, float& bscale) {
   alpha = gp_alpha(gp, t, h);
   egk = gp.gk_from_g ? expf(gp_g(gp, t, h)) : 1.0f;
   bscale = gp.b ? gp_beta(gp, t, h) + 1e-6f : 1.0f;
@@ -123,6 +121,9 @@ __global__ __launch_bounds__(256) void gka_decode_kernel(Params p) {
     egk = p.gk ? expf(ld_scalar(p.gk, si, p.gk_dt)) : 1.0f;
     bscale = p.beta ? ld_scalar(p.beta, si, p.beta_dt) + 1e-6f : 1.0f;
   }
+  // The state updates below spell out their fused multiply-adds: every kernel
+  // variant (with or without the output norm, gates loaded or formed) then rounds
+  // them identically, whatever the compiler would contract in each.
 
   float sk = 0.f, sq = 0.f;
 #pragma unroll
@@ -141,7 +142,7 @@ __global__ __launch_bounds__(256) void gka_decode_kernel(Params p) {
   for (int i = 0; i < 16; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      Hs[i][j] = Hs[i][j] * egk + kr[i] * kc[j];
+      Hs[i][j] = __builtin_fmaf(kr[i], kc[j], Hs[i][j] * egk);
       fro2 += Hs[i][j] * Hs[i][j];
     }
   {
@@ -212,7 +213,7 @@ __global__ __launch_bounds__(256) void gka_decode_kernel(Params p) {
   for (int i = 0; i < 16; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      Ss[i][j] = Ss[i][j] * egk + kr[i] * vc[j];
+      Ss[i][j] = __builtin_fmaf(kr[i], vc[j], Ss[i][j] * egk);
       ov[j] += Ss[i][j] * xr[i];
     }
   {
