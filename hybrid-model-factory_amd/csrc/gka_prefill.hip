@@ -58,6 +58,13 @@ constexpr int NTHR = 256;       // 4 waves
 constexpr int LDQ = D + 16;
 constexpr float EPS = 1e-6f;
 
+// Element (r, c) of a block-start state in its tile-major layout: 16x16 tiles,
+// row-major within a tile and in tile order (the walk writes whole tiles; a row
+// segment of 8 elements stays contiguous for the solve's 16-byte loads)
+__device__ __forceinline__ int blk_index(int r, int c) {
+  return ((r >> 4) * (D / 16) + (c >> 4)) * 256 + (r & 15) * 16 + (c & 15);
+}
+
 struct SegInfo { int n, bos, eos, c_start, c_end, seg_idx, first_seg, nseg; };
 
 // A state pool: slots of [H, D, D] states, ss elements apart, f32 or bf16; `in`
@@ -84,6 +91,7 @@ struct Params {
   const int* seg; int nseg_total; int nblk_total;
   int* segblk;                            // [nseg+1]: first global block of each segment
   f16* ws_hb; f16* ws_sb;                 // [nblk][H][D][D]: zero-start block-start H, S^T
+                                          // (tile-major, see blk_index)
   float* ws_boff;                         // [nblk][H][2]: sum gk, sum g, segment start -> block
   float* ws_dh; float* ws_ds;             // [nseg][H][D][D]: zero-start end states H, S^T
   float* ws_dec;                          // [nseg][H][2]: sum gk, sum g over the segment
@@ -306,8 +314,9 @@ __global__ __launch_bounds__(NTHR, 2) void gka_walk_kernel(Params p) {
   const bf16* vh = p.v + (int64_t)hk * D;
   const int64_t DD = (int64_t)D * D;
 
-  // the zero-start block-start states of block gb, transposed (column-major: a
-  // lane's 4 consecutive rows of one column are one 8-byte store; H is symmetric)
+  // the zero-start block-start states of block gb, transposed (H is symmetric) and
+  // tile-major: a C-layout tile is 4 consecutive elements of one stored row per
+  // lane, and the 64 lanes' 8-byte stores fill one contiguous 512-byte tile
   auto store_block = [&](int gb) {
     f16* hb = p.ws_hb + ((int64_t)gb * H + h) * DD;
     f16* sb = p.ws_sb + ((int64_t)gb * H + h) * DD;
@@ -315,7 +324,7 @@ __global__ __launch_bounds__(NTHR, 2) void gka_walk_kernel(Params p) {
     for (int rt = 0; rt < 8; ++rt)
 #pragma unroll
       for (int ct = 0; ct < 2; ++ct) {
-        const int64_t off = (int64_t)(32 * wave + 16 * ct + l16) * D + 16 * rt + 4 * q4;
+        const int64_t off = blk_index(32 * wave + 16 * ct + l16, 16 * rt + 4 * q4);
         if (TRACK_H) *reinterpret_cast<f16x4*>(hb + off) = h4(Hs[rt][ct]);
         *reinterpret_cast<f16x4*>(sb + off) = h4(Ss[rt][ct]);
       }
@@ -549,10 +558,11 @@ struct StateLd { f16x8 b[8], s[8]; };
 
 __device__ __forceinline__ void state_issue(StateLd& L, const f16* xb, const f16* xs, int tid) {
   const int r = tid >> 1, c0 = (tid & 1) * 64;
+  const f16* xbr = xb ? xb + blk_index(r, c0) : nullptr;   // 8-element pieces: fixed offsets
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     L.s[j] = *reinterpret_cast<const f16x8*>(xs + r * D + c0 + 8 * j);
-    L.b[j] = xb ? *reinterpret_cast<const f16x8*>(xb + r * D + c0 + 8 * j) : f16x8{};
+    L.b[j] = xbr ? *reinterpret_cast<const f16x8*>(xbr + (j >> 1) * 256 + (j & 1) * 8) : f16x8{};
   }
 }
 
