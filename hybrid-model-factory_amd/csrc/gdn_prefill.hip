@@ -27,7 +27,7 @@
 //   * the sequence's initial state (first segment);
 //   * a warm-up: the chain is re-run from a zero state over the preceding
 //     chunks, far enough back that the dropped history is bounded by
-//     prod e^{g_t} max(1,|1-beta_t|) < e^{-60} (the transition
+//     prod e^{g_t} max(1,|1-beta_t|) < e^{-decay_threshold} (the transition
 //     e^{g}(I - beta k k^T) has spectral norm <= e^{g} max(1,|1-beta|) for
 //     |k| <= 1, which in-kernel L2 normalisation guarantees) - exact to fp32;
 //   * the exact segment scan when that bound is not reached within a few chunks

@@ -54,7 +54,7 @@ def gdn_layer_gates(T: int, H: int, config_id: int = 11, device="cpu", gen_devic
     g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b), with A_log = log U(1, 16),
     dt_bias the inverse softplus of dt ~ exp(U(log 1e-3, log 1e-1)) (the Mamba2
     initialisation, training/.../layers/mamba/mamba2.py:194-201) and a, b ~ N(0, 1).
-    Many heads then decay by far less than e^-60 over a 512-token window.  Returns
+    Many heads then decay by far less than e^-20 over a 512-token window.  Returns
     (g, beta) as fp32 [1, T, H] on ``device``."""
     gd = gen(config_id, gen_device)
     A_log = torch.log(torch.rand(H, generator=gd, device=gen_device) * 15 + 1)
@@ -68,7 +68,7 @@ def gdn_layer_gates(T: int, H: int, config_id: int = 11, device="cpu", gen_devic
 
 
 def gdn_exact_pairs(g: torch.Tensor, beta: torch.Tensor, table, max_warm: int = 16,
-                    threshold: float = 60.0, chunk: int = 32) -> tuple[int, torch.Tensor]:
+                    threshold: float = 20.0, chunk: int = 32) -> tuple[int, torch.Tensor]:
     """The prefill plan's use of the exact segment scan, by the kernel's own rule:
     (segment, head) pairs whose preceding max_warm chunks neither decay the dropped
     history below e^-threshold (the decay bound of a token being
