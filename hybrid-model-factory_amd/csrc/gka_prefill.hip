@@ -556,15 +556,25 @@ __device__ __forceinline__ void h8_hilo(const f32x4& t0, const f32x4& t1, f16x8&
 // segment's first block), this thread's 64 elements: row tid/2, half tid&1.
 struct StateLd { f16x8 b[8], s[8]; };
 
-__device__ __forceinline__ void state_issue(StateLd& L, const f16* xb, const f16* xs, int tid) {
+// The loads of a block-start state (tile-major; null: zero) and of its segment's
+// start state (rows; null: dropped), issued separately so the second can wait for
+// the decay that decides whether it is needed.
+__device__ __forceinline__ void state_issue_b(StateLd& L, const f16* xb, int tid) {
   const int r = tid >> 1, c0 = (tid & 1) * 64;
   const f16* xbr = xb ? xb + blk_index(r, c0) : nullptr;   // 8-element pieces: fixed offsets
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    L.s[j] = *reinterpret_cast<const f16x8*>(xs + r * D + c0 + 8 * j);
+  for (int j = 0; j < 8; ++j)
     L.b[j] = xbr ? *reinterpret_cast<const f16x8*>(xbr + (j >> 1) * 256 + (j & 1) * 8) : f16x8{};
-  }
 }
+__device__ __forceinline__ void state_issue_s(StateLd& L, const f16* xs, int tid) {
+  const int r = tid >> 1, c0 = (tid & 1) * 64;
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    L.s[j] = xs ? *reinterpret_cast<const f16x8*>(xs + r * D + c0 + 8 * j) : f16x8{};
+}
+// A segment's start state enters a block's state decayed by e^{off}; below e^-20
+// (2e-9 of its norm, under fp32 rounding) it is dropped and not loaded.
+constexpr float SEG_STATE_DROP = -20.f;
 
 // Writes the state into LDS as fp16 rows; returns this thread's sum of squares.
 __device__ __forceinline__ float state_store(f16* dst, const StateLd& L, float dec, int tid) {
@@ -636,7 +646,10 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
   const int64_t so = ((int64_t)s_id * H + h) * DD;
   const int64_t bso = ((int64_t)gb * H + h) * DD;
   StateLd hst;
-  if constexpr (SOLVE) state_issue(hst, lb > 0 ? p.ws_hb + bso : nullptr, p.ws_h0 + so, tid);
+  if constexpr (SOLVE) state_issue_b(hst, lb > 0 ? p.ws_hb + bso : nullptr, tid);
+  const float off_gk = p.ws_boff[bo + 0], off_g = p.ws_boff[bo + 1];
+  if constexpr (SOLVE)
+    state_issue_s(hst, (lb == 0 || off_gk > SEG_STATE_DROP) ? p.ws_h0 + so : nullptr, tid);
 
   // ---- stage k~, v~ (fp16), gates; q rows into registers --------------------
 #pragma unroll
@@ -667,7 +680,6 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
     else wv = (float)static_cast<const f16*>(p.onw)[tid];
     reinterpret_cast<float*>(smem + OFF_NW)[tid] = wv;
   }
-  const float off_gk = p.ws_boff[bo + 0], off_g = p.ws_boff[bo + 1];
   float* red = sc + SC_HN * CB;           // 4 partial sums
   if constexpr (SOLVE) {
     const float ss = wave_sum(state_store(sH, hst, fast_exp(off_gk), tid));
@@ -917,7 +929,8 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
   // The S_c loads go out first; the in-block products (they need only k~) run while
   // they arrive.
   StateLd sst;
-  state_issue(sst, lb > 0 ? p.ws_sb + bso : nullptr, p.ws_s0 + so, tid);
+  state_issue_b(sst, lb > 0 ? p.ws_sb + bso : nullptr, tid);
+  state_issue_s(sst, (lb == 0 || off_g > SEG_STATE_DROP) ? p.ws_s0 + so : nullptr, tid);
   if constexpr (!SOLVE) lds_barrier();     // the staged k~, v~ and gates
   f32x4 O[8];
   {
