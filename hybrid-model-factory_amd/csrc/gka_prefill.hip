@@ -325,7 +325,8 @@ __global__ __launch_bounds__(NTHR, 2) void gka_walk_kernel(Params p) {
 #pragma unroll
       for (int ct = 0; ct < 2; ++ct) {
         const int64_t off = blk_index(32 * wave + 16 * ct + l16, 16 * rt + 4 * q4);
-        if (TRACK_H) *reinterpret_cast<f16x4*>(hb + off) = h4(Hs[rt][ct]);
+        // H is symmetric: only its upper tiles (tile row <= tile column) are kept
+        if (TRACK_H && 2 * wave + ct <= rt) *reinterpret_cast<f16x4*>(hb + off) = h4(Hs[rt][ct]);
         *reinterpret_cast<f16x4*>(sb + off) = h4(Ss[rt][ct]);
       }
     if (tid == 0) {
@@ -559,39 +560,72 @@ struct StateLd { f16x8 b[8], s[8]; };
 // The loads of a block-start state (tile-major; null: zero) and of its segment's
 // start state (rows; null: dropped), issued separately so the second can wait for
 // the decay that decides whether it is needed.
+// SYM (H): only the pieces in upper 16x16 tiles (tile row <= tile column) are
+// loaded; state_fill_lower mirrors the rest in LDS.
+template <bool SYM>
+__device__ __forceinline__ bool piece_kept(int r, int c) {
+  return !SYM || (r >> 4) <= (c >> 4);
+}
+template <bool SYM>
 __device__ __forceinline__ void state_issue_b(StateLd& L, const f16* xb, int tid) {
   const int r = tid >> 1, c0 = (tid & 1) * 64;
   const f16* xbr = xb ? xb + blk_index(r, c0) : nullptr;   // 8-element pieces: fixed offsets
 #pragma unroll
   for (int j = 0; j < 8; ++j)
-    L.b[j] = xbr ? *reinterpret_cast<const f16x8*>(xbr + (j >> 1) * 256 + (j & 1) * 8) : f16x8{};
+    L.b[j] = (xbr && piece_kept<SYM>(r, c0 + 8 * j))
+                 ? *reinterpret_cast<const f16x8*>(xbr + (j >> 1) * 256 + (j & 1) * 8)
+                 : f16x8{};
 }
+template <bool SYM>
 __device__ __forceinline__ void state_issue_s(StateLd& L, const f16* xs, int tid) {
   const int r = tid >> 1, c0 = (tid & 1) * 64;
 #pragma unroll
   for (int j = 0; j < 8; ++j)
-    L.s[j] = xs ? *reinterpret_cast<const f16x8*>(xs + r * D + c0 + 8 * j) : f16x8{};
+    L.s[j] = (xs && piece_kept<SYM>(r, c0 + 8 * j))
+                 ? *reinterpret_cast<const f16x8*>(xs + r * D + c0 + 8 * j)
+                 : f16x8{};
 }
 // A segment's start state enters a block's state decayed by e^{off}; below e^-20
 // (2e-9 of its norm, under fp32 rounding) it is dropped and not loaded.
 constexpr float SEG_STATE_DROP = -20.f;
 
 // Writes the state into LDS as fp16 rows; returns this thread's sum of squares.
+// (SYM: of the upper tiles, each off-diagonal tile standing for itself and its
+// mirror in the sum of squares.)
+template <bool SYM>
 __device__ __forceinline__ float state_store(f16* dst, const StateLd& L, float dec, int tid) {
   const int r = tid >> 1, c0 = (tid & 1) * 64;
   float ss = 0.f;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
+    const int c = c0 + 8 * j;
+    if (!piece_kept<SYM>(r, c)) continue;
     f16x8 y;
+    float sj = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const float u = (float)L.b[j][i] + dec * (float)L.s[j][i];
-      ss += u * u;
+      sj += u * u;
       y[i] = (f16)u;
     }
-    store8_i(dst + r * LDP, c0 + 8 * j, y);
+    ss += (SYM && (r >> 4) != (c >> 4)) ? 2.f * sj : sj;
+    store8_i(dst + r * LDP, c, y);
   }
   return ss;
+}
+
+// The lower 16x16 tiles of the symmetric H in LDS from their upper mirrors: a
+// transposing read of 4 rows x 16 columns of tile (C, R) is 4 consecutive columns
+// of one row of tile (R, C) per lane.  Wave w fills lower tiles w, w+4, ... (28).
+__device__ __forceinline__ void state_fill_lower(f16* sH, int wave, int lane) {
+  const int q4 = lane >> 4, l16 = lane & 15;
+  for (int k = wave; k < 28; k += 4) {
+    int R = 1, m = k;                   // k-th lower tile (R, C), C < R, row-major
+    while (m >= R) { m -= R; ++R; }
+    const int C = m;
+    const f16x4 x = ld_tr_i(sH, LDP, 16 * C + 4 * q4, 16 * R, lane);
+    *reinterpret_cast<f16x4*>(sH + (16 * R + l16) * LDP + icol(16 * C + 4 * q4)) = x;
+  }
 }
 
 // Runs f(WaveIdx<w>{}) for the workgroup's wave w.  Wave w's tokens are
@@ -646,10 +680,10 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
   const int64_t so = ((int64_t)s_id * H + h) * DD;
   const int64_t bso = ((int64_t)gb * H + h) * DD;
   StateLd hst;
-  if constexpr (SOLVE) state_issue_b(hst, lb > 0 ? p.ws_hb + bso : nullptr, tid);
+  if constexpr (SOLVE) state_issue_b<true>(hst, lb > 0 ? p.ws_hb + bso : nullptr, tid);
   const float off_gk = p.ws_boff[bo + 0], off_g = p.ws_boff[bo + 1];
   if constexpr (SOLVE)
-    state_issue_s(hst, (lb == 0 || off_gk > SEG_STATE_DROP) ? p.ws_h0 + so : nullptr, tid);
+    state_issue_s<true>(hst, (lb == 0 || off_gk > SEG_STATE_DROP) ? p.ws_h0 + so : nullptr, tid);
 
   // ---- stage k~, v~ (fp16), gates; q rows into registers --------------------
 #pragma unroll
@@ -682,7 +716,7 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
   }
   float* red = sc + SC_HN * CB;           // 4 partial sums
   if constexpr (SOLVE) {
-    const float ss = wave_sum(state_store(sH, hst, fast_exp(off_gk), tid));
+    const float ss = wave_sum(state_store<true>(sH, hst, fast_exp(off_gk), tid));
     if (lane == 0) red[wave] = ss;
   }
   // this lane's token t (16 per wave) and its q^ slice: Q[nt][v] = q^[t][16 nt + 4 q4 + v]
@@ -712,6 +746,8 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
 
   f32x4 X[8];                             // the query fed to the GLA, transposed C layout
   if constexpr (SOLVE) {
+    lds_barrier();
+    state_fill_lower(sH, wave, lane);
     lds_barrier();
     const float hn = red[0] + red[1] + red[2] + red[3];   // |H_c|^2
     const float GkT = SC(SC_GK, tb);
@@ -929,8 +965,8 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
   // The S_c loads go out first; the in-block products (they need only k~) run while
   // they arrive.
   StateLd sst;
-  state_issue_b(sst, lb > 0 ? p.ws_sb + bso : nullptr, tid);
-  state_issue_s(sst, (lb == 0 || off_g > SEG_STATE_DROP) ? p.ws_s0 + so : nullptr, tid);
+  state_issue_b<false>(sst, lb > 0 ? p.ws_sb + bso : nullptr, tid);
+  state_issue_s<false>(sst, (lb == 0 || off_g > SEG_STATE_DROP) ? p.ws_s0 + so : nullptr, tid);
   if constexpr (!SOLVE) lds_barrier();     // the staged k~, v~ and gates
   f32x4 O[8];
   {
@@ -966,7 +1002,7 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
       if constexpr (W >= 2) zb1 = h8(Z[2], Z[3]);
     });
     // S_c into LDS (every wave is past its last read of H_c)
-    state_store(sH, sst, fast_exp(off_g), tid);
+    state_store<false>(sH, sst, fast_exp(off_g), tid);
     lds_barrier();
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt) O[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
