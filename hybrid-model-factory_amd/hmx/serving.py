@@ -21,8 +21,9 @@ reference sequence of calls they drop every copy around the ops:
 
 ``layer`` is the vLLM layer object (or anything with the attributes the
 reference reads: conv1d.weight, activation, A, dt_bias, key_dim, kv_k_dim,
-kv_v_dim, num_heads, num_kv_heads, head_k_dim, head_v_dim, tp_size, proj_k, and
-allow_neg_eigval for GDN / the gka_config attributes for GKA);
+kv_v_dim, num_heads, num_kv_heads, head_k_dim, head_v_dim, tp_size, proj_k / proj_v
+(None without the low-rank projection), k_rep / v_rep, and allow_neg_eigval for
+GDN / the gka_config attributes for GKA);
 ``attn_metadata`` is the layer's GDNAttentionMetadata (the fields the reference
 reads, with the primed builder's ``non_spec_query_start_loc_d/_p`` in mixed
 batches, primed_gdn_attn.py:40-113); ``conv_state`` is
@@ -35,8 +36,11 @@ primed_gka_layer.py:1083) while its recurrent prefill uses the prefill slice
 (primed_gdn_layer.py:870, primed_gka_layer.py:1247); here both use the prefill
 slice.
 
-Speculative decoding (``spec_sequence_masks``) and the low-rank k/v projection
-(``proj_k``) raise NotImplementedError.
+With the low-rank k/v projection (``proj_k``, ``proj_v`` and the optional
+learnable residual mixes ``k_rep`` / ``v_rep``), k and v are upsampled to the
+query heads before the ops, as the layers' rearrange step does (a library GEMM
+through the layer's own modules plus the residual); it needs ``tp_size == 1``.
+Speculative decoding (``spec_sequence_masks``) raises NotImplementedError.
 
 ``mamba2_conv_ssm_forward`` restates ``PrimedMamba2Layer.conv_ssm_forward``
 (primed_mamba2_layer.py:615-1021) the same way: the decode and prefill convs write
@@ -59,9 +63,10 @@ def _check(layer, md):
     if md.spec_sequence_masks is not None:
         raise NotImplementedError("speculative decoding batches (spec_sequence_masks) are not "
                                   "supported by the hmx mixer cores")
-    if getattr(layer, "proj_k", None) is not None:
-        raise NotImplementedError("the low-rank k/v projection (kv_proj_rank) is not supported "
-                                  "by the hmx mixer cores")
+    if getattr(layer, "proj_k", None) is not None and layer.tp_size != 1:
+        raise NotImplementedError("the low-rank k/v projection needs the k/v all-gather of "
+                                  "tensor parallelism, which the hmx mixer cores do not run; "
+                                  "tp_size must be 1")
 
 
 def _conv(layer, md, mixed_qkv, cs):
@@ -96,7 +101,27 @@ def _qkv(layer, x):
     q = x[:, :kd].view(1, n, H, layer.head_k_dim)
     k = x[:, kd:kd + kk].view(1, n, HKV, layer.head_k_dim)
     v = x[:, kd + kk:].view(1, n, HKV, layer.head_v_dim)
-    return q, k, v
+    if getattr(layer, "proj_k", None) is None:
+        return q, k, v
+    return (q, _low_rank(layer.proj_k, getattr(layer, "k_rep", None), k[0], H),
+            _low_rank(layer.proj_v, getattr(layer, "v_rep", None), v[0], H))
+
+
+def _low_rank(proj, rep, kv, H):
+    """k (or v) upsampled from HKV to H heads at tp_size 1, as the layers'
+    rearrange step forms it (primed_gdn_layer.py:511-545, primed_gka_layer.py:794-829):
+    proj(kv) plus kv repeated over each head group, or plus rep @ kv per token when
+    the residual is learnable (rep [H, HKV]).  kv [n, HKV, d] -> [1, n, H, d]."""
+    n, HKV, d = kv.shape
+    y = proj(kv.reshape(n, HKV * d))
+    if isinstance(y, tuple):                 # vLLM linear layers return (out, bias)
+        y = y[0]
+    y = y.view(n, H, d)
+    if rep is None:                          # repeat_interleave residual, added in place
+        y.view(n, HKV, H // HKV, d).add_(kv.unsqueeze(2))
+    else:
+        y = y + torch.matmul(rep, kv.contiguous())
+    return y.unsqueeze(0)
 
 
 def _host_prefill_offsets(num_decodes: int, query_start_loc_cpu):

@@ -14,10 +14,12 @@ num_actual_tokens untouched), recurrent pool slots within the state tolerance
 fused output norm within 2 half-ulps of the unfused core followed by
 hmx.rms_norm_gated.
 """
+import copy
 from types import SimpleNamespace
 
 import pytest
 import torch
+import torch.nn.functional as F
 
 import hmx
 import hmx.serving as srv
@@ -34,7 +36,22 @@ CONV_DIM = (H + 2 * HKV) * D
 SLOTS = 8
 
 
-def _layer(kind, seed, **extra):
+class _LowRank(torch.nn.Module):
+    """LinearLowRank's forward without activation (primed_gka_layer.py:59-106):
+    x -> linearA (rank) -> linearB, both bias-free, in the weights' dtype."""
+
+    def __init__(self, fin, fout, rank, g0):
+        super().__init__()
+        self.wa = torch.nn.Parameter((torch.randn(rank, fin, generator=g0) * fin ** -0.5)
+                                     .bfloat16(), requires_grad=False)
+        self.wb = torch.nn.Parameter((torch.randn(fout, rank, generator=g0) * rank ** -0.5 * 0.3)
+                                     .bfloat16(), requires_grad=False)
+
+    def forward(self, x):
+        return F.linear(F.linear(x, self.wa), self.wb)
+
+
+def _layer(kind, seed, low_rank=None, **extra):
     g0 = torch.Generator().manual_seed(seed)
     w = (torch.randn(CONV_DIM, 1, 4, generator=g0) * 0.4).bfloat16()
     lay = SimpleNamespace(
@@ -47,6 +64,14 @@ def _layer(kind, seed, **extra):
     else:
         lay.use_forgetting_gate, lay.use_forgetting_gate_kk, lay.use_beta_gate = True, True, True
         lay.num_iter, lay.ridge_strength, lay.gla_scale, lay._alpha_idx = 8, 0.02, D ** -0.5, None
+    if low_rank is not None:     # kv_proj_rank 32; "learnable": kv_learnable_residual
+        lay.proj_k = _LowRank(HKV * D, H * D, 32, g0)
+        lay.proj_v = _LowRank(HKV * D, H * D, 32, g0)
+        lay.k_rep = lay.v_rep = None
+        if low_rank == "learnable":
+            rep = torch.arange(H)[:, None] // (H // HKV) == torch.arange(HKV)[None]
+            lay.k_rep = (rep + 0.3 * torch.randn(H, HKV, generator=g0)).bfloat16()
+            lay.v_rep = (rep + 0.3 * torch.randn(H, HKV, generator=g0)).bfloat16()
     lay.__dict__.update(extra)
     return lay
 
@@ -54,7 +79,24 @@ def _layer(kind, seed, **extra):
 def _to(lay, dev):
     lay.conv1d.weight = lay.conv1d.weight.to(dev)
     lay.A, lay.dt_bias = lay.A.to(dev), lay.dt_bias.to(dev)
+    if lay.proj_k is not None:
+        lay.proj_k, lay.proj_v = lay.proj_k.to(dev), lay.proj_v.to(dev)
+        if lay.k_rep is not None:
+            lay.k_rep, lay.v_rep = lay.k_rep.to(dev), lay.v_rep.to(dev)
     return lay
+
+
+def _low_rank_ref(proj, rep, kv):
+    """The layers' k / v upsampling at tp 1 (primed_gdn_layer.py:511-545), on the
+    CPU in bf16: proj(kv) + kv repeat_interleaved over the head groups, or + the
+    learnable mix einsum("kh,lhd->lkd", rep, kv)."""
+    L = kv.shape[0]
+    y = copy.deepcopy(proj).cpu()(kv.reshape(L, HKV * D)).view(L, H, D)
+    if rep is None:
+        res = kv.repeat_interleave(H // HKV, dim=1)
+    else:
+        res = torch.einsum("kh,lhd->lkd", rep.cpu(), kv)
+    return y + res
 
 
 BATCHES = {   # decode sequences (1 token each) first, then prefill lengths
@@ -109,6 +151,8 @@ def _expected(kind, lay, md_lens, idx, has, nd, mixed_qkv, gates, conv_cache, st
         q = xb[:, :H * D].view(L, H, D)
         k = xb[:, H * D:(H + HKV) * D].view(L, HKV, D)
         v = xb[:, (H + HKV) * D:].view(L, HKV, D)
+        if lay.proj_k is not None:
+            k, v = _low_rank_ref(lay.proj_k, lay.k_rep, k), _low_rank_ref(lay.proj_v, lay.v_rep, v)
         if kind == "gdn":
             a, b = gates
             g, beta = gref.gdn_gating(lay.A.cpu(), a[sl], b[sl], lay.dt_bias.cpu())
@@ -136,8 +180,8 @@ def _expected(kind, lay, md_lens, idx, has, nd, mixed_qkv, gates, conv_cache, st
     return torch.cat(outs), conv_new, st_new
 
 
-def _run(kind, batch, dev, o_norm=False, seed=1, host_offsets=False, **extra):
-    lay = _layer(kind, seed, **extra)
+def _run(kind, batch, dev, o_norm=False, seed=1, host_offsets=False, low_rank=None, **extra):
+    lay = _layer(kind, seed, low_rank, **extra)
     md, lens, idx, has = _meta(batch, dev)
     nd = BATCHES[batch][0]
     n = md.num_actual_tokens
@@ -171,10 +215,7 @@ def _run(kind, batch, dev, o_norm=False, seed=1, host_offsets=False, **extra):
                 core=core.cpu(), cc=cc_d.cpu(), states_d=[s.cpu() for s in states_d], z=z, wn=wn)
 
 
-@pytest.mark.parametrize("kind", ["gdn", "gka"])
-@pytest.mark.parametrize("batch", ["mixed", "prefill", "decode"])
-def test_forward_core_matches_oracle(dev, kind, batch):
-    r = _run(kind, batch, dev)
+def _check_against_oracle(kind, r):
     o_r, conv_r, st_r = _expected(kind, r["lay"], r["lens"], r["idx"], r["has"], r["nd"],
                                   r["mixed_qkv"], r["gates"], r["conv_cache"], r["states"])
     n = r["n"]
@@ -188,6 +229,28 @@ def test_forward_core_matches_oracle(dev, kind, batch):
                 assert_state_close(got[s], exp[s], what=f"slot {s}")
             else:
                 assert torch.equal(got[s], orig[s])
+
+
+@pytest.mark.parametrize("kind", ["gdn", "gka"])
+@pytest.mark.parametrize("batch", ["mixed", "prefill", "decode"])
+def test_forward_core_matches_oracle(dev, kind, batch):
+    _check_against_oracle(kind, _run(kind, batch, dev))
+
+
+@pytest.mark.parametrize("kind", ["gdn", "gka"])
+@pytest.mark.parametrize("low_rank", ["repeat", "learnable"])
+def test_forward_core_low_rank_kv(dev, kind, low_rank):
+    """kv_proj_rank: k and v upsampled from HKV to H heads by the layer's low-rank
+    projection plus the repeat or learnable residual before the ops."""
+    _check_against_oracle(kind, _run(kind, "mixed", dev, low_rank=low_rank))
+
+
+def test_forward_core_low_rank_needs_tp1(dev):
+    lay = _layer("gdn", 3, low_rank="repeat")
+    lay.tp_size = 2
+    md, *_ = _meta("decode", dev)
+    with pytest.raises(NotImplementedError):
+        srv.gdn_forward_core(lay, None, None, None, None, md, None, None)
 
 
 @pytest.mark.parametrize("kind", ["gdn", "gka"])
