@@ -103,6 +103,9 @@ struct Params {
   const bf16* zg; int64_t zg_ts, zg_hs;   // gate rows, or null (plain RMSNorm)
   const void* onw; int onw_dt;            // weight [D]
   float on_eps;
+  // the training solve (SM_X / SM_DQ solve kernels): |H_t|_F per token [tokens][H]
+  // (written by SM_X, read by SM_DQ) and the fp32 solution of SM_DQ [tokens][H][D]
+  float* fro; float* xo32;
 };
 
 __device__ __forceinline__ float ldsc(const void* p, int64_t i, int dt) {
@@ -221,7 +224,7 @@ __device__ __forceinline__ void load_raw(Raw& r, const Params& p, const bf16* kh
               : 0.f;
     r.gk = 0.f;
   } else {
-    r.g = okg ? ldsc(p.g, gi, p.g_dt) : 0.f;
+    r.g = (okg && p.g) ? ldsc(p.g, gi, p.g_dt) : 0.f;
     r.gk = (okg && p.gk) ? ldsc(p.gk, gi, p.gk_dt) : 0.f;
   }
 }
@@ -644,8 +647,15 @@ __device__ __forceinline__ void with_wave(int wave, F&& f) {
   }
 }
 
-template <bool SOLVE, bool NORM>
+// What the solve kernel produces: the GLA output (serving prefill), or the solution
+// x of the Chebyshev solve itself (training): SM_X writes x (bf16, into p.o) and
+// |H_t|_F; SM_DQ solves for the right-hand side in p.q with the |H_t|_F of the
+// forward read back (the backward's dq) and writes fp32 (p.xo32).
+enum SolveMode { SM_GLA = 0, SM_X = 1, SM_DQ = 2 };
+
+template <bool SOLVE, bool NORM, int MODE = SM_GLA>
 __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
+  static_assert(MODE == SM_GLA || (SOLVE && !NORM), "the x outputs need the solver");
   __shared__ __align__(16) unsigned char smem[SMEM];
   f16* sK = reinterpret_cast<f16*>(smem + OFF_K);
   f16* sV = reinterpret_cast<f16*>(smem + OFF_V);
@@ -695,17 +705,18 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
     const bf16x8 vr = ok ? *reinterpret_cast<const bf16x8*>(p.v + tok * p.kv_ts + hk * D + f0) : bf16x8{};
     const float sk = key_scale(p, row_sumsq(kr), tok, h, ok);
     store8_i(sK + row * LDP, f0, scale_h8(kr, sk));
-    *reinterpret_cast<f16x8*>(sV + row * LDP + f0) = scale_h8(vr, beta_eps(p, tok, h, ok));
+    if constexpr (MODE == SM_GLA)
+      *reinterpret_cast<f16x8*>(sV + row * LDP + f0) = scale_h8(vr, beta_eps(p, tok, h, ok));
   }
   if (wave == 0) {
     const bool ok = lane < nval;
     const int64_t tk = tok0 + lane;
-    const float gt = ok ? g_at(p, tk, h) : 0.f;
+    const float gt = (MODE == SM_GLA && ok) ? g_at(p, tk, h) : 0.f;
     const float G = scan64(gt);
     const float Gk = scan64((ok && has_gk(p)) ? (p.fused ? gt : gk_at(p, tk, h)) : 0.f);
     SC(SC_G, lane) = G;
     SC(SC_GK, lane) = Gk;
-    SC(SC_AL, lane) = ok ? alpha_at(p, tk, h) : 0.f;
+    SC(SC_AL, lane) = (MODE == SM_GLA && ok) ? alpha_at(p, tk, h) : 0.f;
   }
   if (NORM && tid < D) {
     float wv;
@@ -753,7 +764,7 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
     const float GkT = SC(SC_GK, tb);
 
     // d_j = k~_j^T H_c k~_j for this wave's tokens j = 16 wave + l16
-    {
+    if constexpr (MODE != SM_DQ) {
       f32x4 Pd[8];
 #pragma unroll
       for (int nt = 0; nt < 8; ++nt) Pd[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -776,7 +787,7 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
     }
     // Gram part of |H_t|^2: g2_t = sum_{i,j<=t} a_ti a_tj (k~_i.k~_j)^2, a_tj = e^{Gk_t-Gk_j},
     // as the row sums of a . (A B) with B = (K K^T)^2 over this wave's key range
-    with_wave(wave, [&](auto Wc) {
+    if constexpr (MODE != SM_DQ) with_wave(wave, [&](auto Wc) {
       constexpr int W = decltype(Wc)::value;
       f32x4 U[4];
 #pragma unroll
@@ -826,12 +837,18 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
     // f_t, lam, tau, c for this lane's token
     float tau, lam, cc;
     {
-      float cross = 0.f;
-      for (int j = q4; j <= tb; j += 4) cross += fast_exp(GkT - SC(SC_GK, j)) * SC(SC_D, j);
-      cross += __shfl_xor(cross, 16, 64);
-      cross += __shfl_xor(cross, 32, 64);
-      const float e = fast_exp(GkT);
-      const float f = sqrtf(fmaxf(e * e * hn + 2.f * e * cross + SC(SC_G2, tb), 0.f));
+      float f;
+      if constexpr (MODE == SM_DQ) {
+        f = tok_ok ? p.fro[(int64_t)(tok0 + tb) * H + h] : 0.f;
+      } else {
+        float cross = 0.f;
+        for (int j = q4; j <= tb; j += 4) cross += fast_exp(GkT - SC(SC_GK, j)) * SC(SC_D, j);
+        cross += __shfl_xor(cross, 16, 64);
+        cross += __shfl_xor(cross, 32, 64);
+        const float e = fast_exp(GkT);
+        f = sqrtf(fmaxf(e * e * hn + 2.f * e * cross + SC(SC_G2, tb), 0.f));
+        if (MODE == SM_X && tok_ok && q4 == 0) p.fro[(int64_t)(tok0 + tb) * H + h] = f;
+      }
       lam = p.ridge_ratio * f;
       const float inv = 1.0f / (2.f * lam + f);
       tau = 2.f * inv;
@@ -948,6 +965,24 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
       }
       step(Xp, X);
     }
+    }
+    if constexpr (MODE != SM_GLA) {
+      // the solution of this lane's token: X[nt][v] = x[16 nt + 4 q4 + v]
+      if (tok_ok) {
+        const int64_t ro = ((int64_t)(tok0 + tb) * H + h) * D + 4 * q4;
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) {
+          if constexpr (MODE == SM_X) {
+            bf16x4 y;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) y[v] = (bf16)X[nt][v];
+            *reinterpret_cast<bf16x4*>(p.o + ro + 16 * nt) = y;
+          } else {
+            *reinterpret_cast<f32x4*>(p.xo32 + ro + 16 * nt) = X[nt];
+          }
+        }
+      }
+      return;
     }
     // alpha blend
     const float al = SC(SC_AL, tb);
@@ -1206,4 +1241,676 @@ extern "C" int hmx_gka_chunk_fwd(const void* q, int64_t q_token_stride, const vo
     else hipLaunchKernelGGL((solve::gka_solve_kernel<false, false>), grid, dim3(NTHR), 0, s, p);
   }
   return check_launch("hmx_gka_chunk_fwd");
+}
+
+// ===========================================================================
+// The training backward of the Chebyshev solve: dk and dgk
+// ===========================================================================
+// With x treated as the exact solution, dL/dH_t = G_t = -dq_t x_t^T + a_t H_t, where
+// a_t = -r (dq_t . x_t) / |H_t|_F carries the ridge's dependence on |H_t|_F (0
+// without bp_lambda).  Per 64-token block c with in-block decays g_t (inclusive
+// cumsum of gk from the block start), block total Gam = g at the last token, and
+// block-start state h_c (H_t = e^{g_t} h_c + sum_{s<=t} e^{g_t-g_s} k_s k_s^T):
+//   E_c = sum_t e^{g_t} (G_t + G_t^T)   (the block's share of dL/dh_c, symmetrised)
+//   Dn_c = sum over later blocks, decayed to block c's end: Dn_c = E_{c+1} + e^{Gam_{c+1}} Dn_{c+1}
+//   dk_s = -sum_{t>=s} e^{g_t-g_s} [dq_t (x_t.k_s) + x_t (dq_t.k_s)]
+//          + 2 beta_s h_c k_s + 2 sum_u W_su (k_u.k_s) k_u + e^{Gam-g_s} Dn k_s
+//   with rho_m = sum_{t>=m} a_t e^{2(g_t-g_m)}, beta_s = e^{g_s} rho_s,
+//   W_su = e^{(g_m-g_s)+(g_m-g_u)} rho_m (m = max(s,u));
+//   dL/dg_t = <G_t, H_t> - sum_{t'>=t} e^{g_t'-g_t} <G_t', k_t k_t^T> - e^{Gam-g_t} k_t^T Dn k_t / 2
+//             (+ <Dn, h_{c+1}> / 2 at the block's last token),
+//   and dgk is its in-block reverse cumsum (the derivative through the chunk-local
+//   cumsum of gk).  These are the terms of chunk_dk_backward_gating.py's two passes
+//   and chunk_bwd_dh (chebyshev_iteration.py:646-688), in this kernel's arrangement.
+namespace hmx {
+namespace gkap {
+namespace train {
+using solve::LDP;
+using solve::SZ_K;
+using solve::SZ_H;
+using solve::StateLd;
+
+struct Bwd {
+  const bf16* x;          // [tokens][H][D] the forward's solution
+  const float* dq;        // [tokens][H][D] the backward's solve of dx
+  const float* fro;       // [tokens][H]
+  float* e;               // [nblk][H][D][D] fp32 tile-major: E_c, then Dn_c
+  float* gam;             // [nblk][H] block totals of gk
+  float* dk;              // [tokens][H][D]
+  float* dgk;             // [tokens][H]
+  int bp_lambda;
+};
+
+struct Blk { int s_id, lb, tok0, nval; };
+__device__ __forceinline__ Blk block_of(const Params& p, int gb) {
+  int lo = 0, hi = p.nseg_total;         // last s with segblk[s] <= gb
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (p.segblk[mid] <= gb) lo = mid; else hi = mid;
+  }
+  const SegInfo si = load_seg(p.seg, lo);
+  const int lb = gb - p.segblk[lo];
+  const int tok0 = si.bos + (si.c_start + lb) * CB;
+  return Blk{lo, lb, tok0, min(CB, si.eos - tok0)};
+}
+
+// h_c of block gb into sH (fp16, interleaved rows, both triangles), as the solve forms it
+__device__ __forceinline__ void load_hc(const Params& p, f16* sH, const Blk& b, int gb, int h,
+                                        int tid, int wave, int lane) {
+  const int64_t DD = (int64_t)D * D;
+  const int64_t so = ((int64_t)b.s_id * p.H + h) * DD;
+  const int64_t bso = ((int64_t)gb * p.H + h) * DD;
+  StateLd hst;
+  solve::state_issue_b<true>(hst, b.lb > 0 ? p.ws_hb + bso : nullptr, tid);
+  const float off_gk = p.ws_boff[((int64_t)gb * p.H + h) * 2];
+  solve::state_issue_s<true>(hst, (b.lb == 0 || off_gk > solve::SEG_STATE_DROP) ? p.ws_h0 + so : nullptr, tid);
+  solve::state_store<true>(sH, hst, fast_exp(off_gk), tid);
+  lds_barrier();
+  solve::state_fill_lower(sH, wave, lane);
+}
+
+// in-block inclusive cumsum of gk for lanes 0-63 (wave 0); 0 past the block's tokens
+__device__ __forceinline__ float block_decay(const Params& p, const Blk& b, int h, int lane) {
+  const bool ok = lane < b.nval;
+  return scan64((ok && p.gk) ? ldsc(p.gk, (int64_t)(b.tok0 + lane) * p.H + h, p.gk_dt) : 0.f);
+}
+
+// a_t = -r (dq_t . x_t) / |H_t|_F for token row `row` (one 16-lane group per row)
+__device__ __forceinline__ float lambda_weight(const Params& p, const Bwd& w, const Blk& b, int row,
+                                               int h, int l16) {
+  float d = 0.f;
+  if (row < b.nval && w.bp_lambda) {
+    const int64_t ro = ((int64_t)(b.tok0 + row) * p.H + h) * D + 8 * l16;
+    const f32x4 q0 = *reinterpret_cast<const f32x4*>(w.dq + ro);
+    const f32x4 q1 = *reinterpret_cast<const f32x4*>(w.dq + ro + 4);
+    const bf16x8 xv = *reinterpret_cast<const bf16x8*>(w.x + ro);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) d += q0[v] * (float)xv[v] + q1[v] * (float)xv[4 + v];
+  }
+  d = row16_sum(d);
+  const float f = (row < b.nval && w.bp_lambda) ? w.fro[(int64_t)(b.tok0 + row) * p.H + h] : 0.f;
+  return f > 0.f ? -p.ridge_ratio * d / f : 0.f;
+}
+
+// x, dq and the ridge weights grow like 1 / |H_t|_F, which is small at a
+// sequence's start: the fp16 operands built from them are scaled by a power of two
+// (exact) chosen from their largest magnitude, and the products unscaled in fp32.
+// pow2_scale(m): 2^j with m 2^j < 2^8 (1 when m is below that already)
+__device__ __forceinline__ float pow2_scale(float m) {
+  int e;
+  (void)frexpf(m, &e);                   // m < 2^e
+  return e > 8 ? ldexpf(1.f, 8 - e) : 1.f;
+}
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) x = fmaxf(x, __shfl_xor(x, m, 64));
+  return x;
+}
+__device__ __forceinline__ float absmax8(const bf16x8& x) {
+  float m = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf((float)x[j]));
+  return m;
+}
+__device__ __forceinline__ float absmax4(const f32x4& x) {
+  return fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
+}
+// The workgroup's maxima of NV per-thread values: slot[NV * 4] of LDS scratch;
+// includes a barrier.
+template <int NV>
+__device__ __forceinline__ void block_max(float (&v)[NV], float* slot, int wave, int lane) {
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    v[i] = wave_max(v[i]);
+    if (lane == 0) slot[4 * i + wave] = v[i];
+  }
+  lds_barrier();
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+    v[i] = fmaxf(fmaxf(slot[4 * i], slot[4 * i + 1]), fmaxf(slot[4 * i + 2], slot[4 * i + 3]));
+}
+__device__ __forceinline__ f16x8 h8_of(const f32x4& a, const f32x4& b, float s) {
+  return f16x8{(f16)(s * a[0]), (f16)(s * a[1]), (f16)(s * a[2]), (f16)(s * a[3]),
+               (f16)(s * b[0]), (f16)(s * b[1]), (f16)(s * b[2]), (f16)(s * b[3])};
+}
+
+constexpr int E_OFF_K = 0, E_OFF_KB = SZ_K, E_OFF_Q = 2 * SZ_K, E_OFF_X = 3 * SZ_K;
+constexpr int E_OFF_H = 4 * SZ_K, E_OFF_SC = E_OFF_H + SZ_H;
+constexpr int E_SMEM = E_OFF_SC + 3 * CB * 4 + 16 * 4;
+static_assert(E_SMEM <= 160 * 1024, "LDS budget");
+
+// E_c = -(Ql^T X + X^T Ql) + 2 (alpha h_c + K^T diag(beta) K), Ql = e^{g} dq, of block gb
+__global__ __launch_bounds__(NTHR, 1) void cheb_e_kernel(Params p, Bwd w) {
+  __shared__ __align__(16) unsigned char smem[E_SMEM];
+  f16* sK = reinterpret_cast<f16*>(smem + E_OFF_K);
+  f16* sKb = reinterpret_cast<f16*>(smem + E_OFF_KB);
+  f16* sQ = reinterpret_cast<f16*>(smem + E_OFF_Q);
+  f16* sX = reinterpret_cast<f16*>(smem + E_OFF_X);
+  f16* sH = reinterpret_cast<f16*>(smem + E_OFF_H);
+  float* sG = reinterpret_cast<float*>(smem + E_OFF_SC);     // g_t
+  float* sA = sG + CB;                                        // a_t
+  float* sB = sA + CB;                                        // 2 beta_t, then [CB-1 + 1] unused
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q4 = lane >> 4, l16 = lane & 15;
+  const int gb = blockIdx.x, h = blockIdx.y, H = p.H;
+  const Blk b = block_of(p, gb);
+  if (b.nval <= 0) return;
+
+  load_hc(p, sH, b, gb, h, tid, wave, lane);
+  if (wave == 0) {
+    const float g = block_decay(p, b, h, lane);
+    sG[lane] = g;
+    if (lane == b.nval - 1) w.gam[(int64_t)gb * H + h] = g;
+  }
+#pragma unroll
+  for (int pass = 0; pass < CB / 16; ++pass) {
+    const int row = pass * 16 + (tid >> 4);
+    const float a = lambda_weight(p, w, b, row, h, l16);
+    if (l16 == 0) sA[row] = a;
+  }
+  lds_barrier();
+  // rho_t = sum_{t'>=t} a_t' e^{2(g_t'-g_t)} (lane t of wave 0), beta_t = e^{g_t} rho_t
+  float alpha = 0.f;
+  if (wave == 0) {
+    float rho = 0.f;
+    const float gt = sG[lane];
+    for (int t2 = lane; t2 < b.nval; ++t2) rho += sA[t2] * fast_exp(2.f * (sG[t2] - gt));
+    sB[lane] = lane < b.nval ? 2.f * fast_exp(gt) * rho : 0.f;
+    alpha = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                          __builtin_bit_cast(int, fast_exp(2.f * gt) * rho), 0));
+  }
+  __shared__ float s_alpha;
+  if (tid == 0) s_alpha = alpha;
+  lds_barrier();
+  // stage k, 2 beta k, -e^{g} dq, x (fp16, interleaved; the last three scaled)
+  bf16x8 kr[CB / 16], xr[CB / 16];
+  f32x4 q0[CB / 16], q1[CB / 16];
+  float mx[3] = {0.f, 0.f, 0.f};            // max |x|, |e^g dq|, |2 beta k|
+#pragma unroll
+  for (int pass = 0; pass < CB / 16; ++pass) {
+    const int row = pass * 16 + (tid >> 4), f0 = (tid & 15) * 8;
+    const bool ok = row < b.nval;
+    const int64_t ro = ((int64_t)(b.tok0 + row) * H + h) * D + f0;
+    kr[pass] = ok ? *reinterpret_cast<const bf16x8*>(p.k + (int64_t)(b.tok0 + row) * p.kv_ts + h * D + f0) : bf16x8{};
+    xr[pass] = ok ? *reinterpret_cast<const bf16x8*>(w.x + ro) : bf16x8{};
+    const float eg = ok ? -fast_exp(sG[row]) : 0.f;
+    q0[pass] = ok ? *reinterpret_cast<const f32x4*>(w.dq + ro) : f32x4{0.f, 0.f, 0.f, 0.f};
+    q1[pass] = ok ? *reinterpret_cast<const f32x4*>(w.dq + ro + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      q0[pass][v] *= eg;
+      q1[pass][v] *= eg;
+    }
+    mx[0] = fmaxf(mx[0], absmax8(xr[pass]));
+    mx[1] = fmaxf(mx[1], fmaxf(absmax4(q0[pass]), absmax4(q1[pass])));
+    mx[2] = fmaxf(mx[2], fabsf(sB[row]) * absmax8(kr[pass]));
+  }
+  block_max(mx, reinterpret_cast<float*>(smem + E_OFF_SC + 3 * CB * 4), wave, lane);
+  const float sx = pow2_scale(mx[0]), sq = pow2_scale(mx[1]), sb = pow2_scale(mx[2]);
+#pragma unroll
+  for (int pass = 0; pass < CB / 16; ++pass) {
+    const int row = pass * 16 + (tid >> 4), f0 = (tid & 15) * 8;
+    store8_i(sK + row * LDP, f0, scale_h8(kr[pass], 1.f));
+    store8_i(sKb + row * LDP, f0, scale_h8(kr[pass], sb * sB[row]));
+    store8_i(sX + row * LDP, f0, scale_h8(xr[pass], sx));
+    store8_i(sQ + row * LDP, f0, h8_of(q0[pass], q1[pass], sq));
+  }
+  lds_barrier();
+  const float a2 = 2.f * s_alpha;
+  const float u12 = 1.f / (sx * sq), u3 = 1.f / sb;
+  // wave w: tile rows 2w, 2w+1 (state rows 32w..32w+31), all 8 tile columns
+  float* eo = w.e + ((int64_t)gb * H + h) * D * D;
+#pragma unroll
+  for (int ir = 0; ir < 2; ++ir) {
+    const int it = 2 * wave + ir;
+    f32x4 E[8], E3[8];
+#pragma unroll
+    for (int jt = 0; jt < 8; ++jt) {
+      E[jt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      E3[jt] = E[jt];
+    }
+#pragma unroll
+    for (int jk = 0; jk < 2; ++jk) {
+      const f16x8 aq = frag_t_i(sQ, LDP, 32 * jk, 16 * it, lane);
+      const f16x8 ax = frag_t_i(sX, LDP, 32 * jk, 16 * it, lane);
+      const f16x8 ab = frag_t_i(sKb, LDP, 32 * jk, 16 * it, lane);
+#pragma unroll
+      for (int jt = 0; jt < 8; ++jt) {
+        E[jt] = mfma16h(aq, frag_t_i(sX, LDP, 32 * jk, 16 * jt, lane), E[jt]);
+        E[jt] = mfma16h(ax, frag_t_i(sQ, LDP, 32 * jk, 16 * jt, lane), E[jt]);
+        E3[jt] = mfma16h(ab, frag_t_i(sK, LDP, 32 * jk, 16 * jt, lane), E3[jt]);
+      }
+    }
+    // E[jt][v] = E_c[16 it + 4 q4 + v][16 jt + l16]; E_c is symmetric, so the lane
+    // writes it as row 16 jt + l16, columns 16 it + 4 q4 .. +3 of the tile-major store
+#pragma unroll
+    for (int jt = 0; jt < 8; ++jt) {
+      const f16x4 hc = *reinterpret_cast<const f16x4*>(sH + (16 * jt + l16) * LDP + icol(16 * it + 4 * q4));
+      f32x4 y;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) y[v] = u12 * E[jt][v] + u3 * E3[jt][v] + a2 * (float)hc[v];
+      *reinterpret_cast<f32x4*>(eo + blk_index(16 * jt + l16, 16 * it + 4 * q4)) = y;
+    }
+  }
+}
+
+// Dn_c = sum over the later blocks of the sequence: one workgroup per (sequence,
+// head, 1024 elements), the sequence's blocks in reverse.  E_c is replaced by Dn_c.
+__global__ __launch_bounds__(256) void cheb_dscan_kernel(Params p, Bwd w) {
+  const int nh = blockIdx.x, H = p.H;
+  const int n = nh / H, h = nh % H;
+  int first = -1, nseg = 0;
+  for (int s = 0; s < p.nseg_total; ++s) {
+    const SegInfo si = load_seg(p.seg, s);
+    if (si.n == n) { first = si.first_seg; nseg = si.nseg; break; }
+  }
+  if (first < 0) return;
+  const int b0 = p.segblk[first], b1 = p.segblk[first + nseg];
+  const int64_t DD = (int64_t)D * D;
+  const int64_t el = (int64_t)blockIdx.y * 1024 + 4 * threadIdx.x;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int c = b1 - 1; c >= b0; --c) {
+    float* ec = w.e + ((int64_t)c * H + h) * DD + el;
+    const f32x4 e = *reinterpret_cast<const f32x4*>(ec);
+    const float dg = fast_exp(w.gam[(int64_t)c * H + h]);
+    *reinterpret_cast<f32x4*>(ec) = acc;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[v] = e[v] + dg * acc[v];
+  }
+}
+
+constexpr int C_OFF_K = 0, C_OFF_X = SZ_K, C_OFF_Q = 2 * SZ_K, C_OFF_H = 3 * SZ_K;
+constexpr int C_OFF_DN = C_OFF_H + SZ_H, C_OFF_SC = C_OFF_DN + SZ_H;
+enum { CS_G, CS_A, CS_RHO, CS_DG, CS_COL0, NCS = CS_COL0 + 4 };
+constexpr int C_SMEM = C_OFF_SC + NCS * CB * 4 + 16 * 4 + 16 * 4;
+static_assert(C_SMEM <= 160 * 1024, "LDS budget");
+
+// dk and dgk of block gb (see the section comment)
+__global__ __launch_bounds__(NTHR, 1) void cheb_dk_kernel(Params p, Bwd w) {
+  __shared__ __align__(16) unsigned char smem[C_SMEM];
+  f16* sK = reinterpret_cast<f16*>(smem + C_OFF_K);
+  f16* sX = reinterpret_cast<f16*>(smem + C_OFF_X);
+  f16* sQ = reinterpret_cast<f16*>(smem + C_OFF_Q);
+  f16* sH = reinterpret_cast<f16*>(smem + C_OFF_H);
+  f16* sDn = reinterpret_cast<f16*>(smem + C_OFF_DN);
+  float* sc = reinterpret_cast<float*>(smem + C_OFF_SC);
+  float* red = sc + NCS * CB;            // 16 floats of cross-wave sums
+  float* mslot = red + 16;               // 16 floats for block_max
+  auto SC = [&](int slot, int t) -> float& { return sc[slot * CB + t]; };
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q4 = lane >> 4, l16 = lane & 15;
+  const int gb = blockIdx.x, h = blockIdx.y, H = p.H;
+  const Blk b = block_of(p, gb);
+  if (b.nval <= 0) return;
+  const int64_t DD = (int64_t)D * D;
+
+  load_hc(p, sH, b, gb, h, tid, wave, lane);
+  if (wave == 0) SC(CS_G, lane) = block_decay(p, b, h, lane);
+  // the rows (x, dq and Dn scaled into fp16's range) and a_t
+  bf16x8 kr[CB / 16], xr[CB / 16];
+  f32x4 q0[CB / 16], q1[CB / 16];
+  const float* dn = w.e + ((int64_t)gb * H + h) * DD;
+  const int dr = tid >> 1, dc0 = (tid & 1) * 64;    // this thread's Dn: row dr, columns dc0..+63
+  f32x4 u[16];
+  float mx[3] = {0.f, 0.f, 0.f};            // max |x|, |dq|, |Dn|
+#pragma unroll
+  for (int pass = 0; pass < CB / 16; ++pass) {
+    const int row = pass * 16 + (tid >> 4), f0 = (tid & 15) * 8;
+    const bool ok = row < b.nval;
+    const int64_t ro = ((int64_t)(b.tok0 + row) * H + h) * D + f0;
+    kr[pass] = ok ? *reinterpret_cast<const bf16x8*>(p.k + (int64_t)(b.tok0 + row) * p.kv_ts + h * D + f0) : bf16x8{};
+    xr[pass] = ok ? *reinterpret_cast<const bf16x8*>(w.x + ro) : bf16x8{};
+    q0[pass] = ok ? *reinterpret_cast<const f32x4*>(w.dq + ro) : f32x4{0.f, 0.f, 0.f, 0.f};
+    q1[pass] = ok ? *reinterpret_cast<const f32x4*>(w.dq + ro + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+    mx[0] = fmaxf(mx[0], absmax8(xr[pass]));
+    mx[1] = fmaxf(mx[1], fmaxf(absmax4(q0[pass]), absmax4(q1[pass])));
+    const float a = lambda_weight(p, w, b, row, h, l16);
+    if (l16 == 0) SC(CS_A, row) = a;
+  }
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    u[j] = *reinterpret_cast<const f32x4*>(dn + blk_index(dr, dc0 + 4 * j));
+    mx[2] = fmaxf(mx[2], absmax4(u[j]));
+  }
+  block_max(mx, mslot, wave, lane);       // (its barrier also orders h_c's lower tiles)
+  const float sx = pow2_scale(mx[0]), sq = pow2_scale(mx[1]), sd = pow2_scale(mx[2]);
+#pragma unroll
+  for (int pass = 0; pass < CB / 16; ++pass) {
+    const int row = pass * 16 + (tid >> 4), f0 = (tid & 15) * 8;
+    store8_i(sK + row * LDP, f0, scale_h8(kr[pass], 1.f));
+    store8_i(sX + row * LDP, f0, scale_h8(xr[pass], sx));
+    store8_i(sQ + row * LDP, f0, h8_of(q0[pass], q1[pass], sq));
+  }
+  // Dn into LDS and <Dn, h_c> in fp32
+  float dnh = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int c = dc0 + 8 * j;
+    const f16x4 h0 = *reinterpret_cast<const f16x4*>(sH + dr * LDP + icol(c));
+    const f16x4 h1 = *reinterpret_cast<const f16x4*>(sH + dr * LDP + icol(c + 4));
+#pragma unroll
+    for (int v = 0; v < 4; ++v) dnh += u[2 * j][v] * (float)h0[v] + u[2 * j + 1][v] * (float)h1[v];
+    store8_i(sDn + dr * LDP, c, h8_of(u[2 * j], u[2 * j + 1], sd));
+  }
+  dnh = wave_sum(dnh);
+  // rho_t (lane t of wave 0)
+  if (wave == 0) {
+    float rho = 0.f;
+    const float gt = SC(CS_G, lane);
+    for (int t2 = lane; t2 < b.nval; ++t2) rho += SC(CS_A, t2) * fast_exp(2.f * (SC(CS_G, t2) - gt));
+    SC(CS_RHO, lane) = rho;
+  }
+  if (lane == 0) red[wave] = dnh;
+  lds_barrier();
+
+  const int s = 16 * wave + l16;            // this lane's key / token column
+  const bool s_ok = s < b.nval;
+  const float gs = SC(CS_G, s);
+  const float Gam = SC(CS_G, b.nval - 1);
+  // products with h_c and Dn: HK = h_c k_s, HX = h_c x_s, P = Dn k_s (rows f, column s)
+  f32x4 HK[8], HX[8], P[8];
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) {
+    HK[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    HX[nt] = HK[nt];
+    P[nt] = HK[nt];
+  }
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const f16x8 bk = frag_i(sK, LDP, 16 * wave, 32 * ks, lane);
+    const f16x8 bx = frag_i(sX, LDP, 16 * wave, 32 * ks, lane);
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      const f16x8 ah = frag_i(sH, LDP, 16 * nt, 32 * ks, lane);
+      HK[nt] = mfma16h(ah, bk, HK[nt]);
+      HX[nt] = mfma16h(ah, bx, HX[nt]);
+      P[nt] = mfma16h(frag_i(sDn, LDP, 16 * nt, 32 * ks, lane), bk, P[nt]);
+    }
+  }
+  // in-block products over the 64 tokens t (rows) for this wave's columns s:
+  // XK = x_t . k_s, QK = dq_t . k_s, KK = k_t . k_s
+  f32x4 XK[4], QK[4], KK[4];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    XK[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    QK[tt] = XK[tt];
+    KK[tt] = XK[tt];
+  }
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const f16x8 bk = frag_i(sK, LDP, 16 * wave, 32 * ks, lane);
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      XK[tt] = mfma16h(frag_i(sX, LDP, 16 * tt, 32 * ks, lane), bk, XK[tt]);
+      QK[tt] = mfma16h(frag_i(sQ, LDP, 16 * tt, 32 * ks, lane), bk, QK[tt]);
+      KK[tt] = mfma16h(frag_i(sK, LDP, 16 * tt, 32 * ks, lane), bk, KK[tt]);
+    }
+  }
+  // masks and the scalar sums: m_ts = e^{g_t - g_s} (t >= s); dm = (x_t.k_s)(dq_t.k_s) m_ts
+  // (XK carries the scale sx and QK sq: S1 and S2 keep them, dm is unscaled)
+  const float rho_s = SC(CS_RHO, s);
+  const float uxq = 1.f / (sx * sq);
+  float rowdm = 0.f, sw;
+  f16x8 s1[2], s2[2], wk[2];
+  {
+    f32x4 S1[4], S2[4], WK[4];
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      const f32x4 gt4 = *reinterpret_cast<const f32x4*>(&SC(CS_G, 16 * tt + 4 * q4));
+      const f32x4 rt4 = *reinterpret_cast<const f32x4*>(&SC(CS_RHO, 16 * tt + 4 * q4));
+      float col[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int t = 16 * tt + 4 * q4 + v;
+        const float m = (t >= s && t < b.nval) ? fast_exp(gt4[v] - gs) : 0.f;
+        S1[tt][v] = -XK[tt][v] * m;
+        S2[tt][v] = -QK[tt][v] * m;
+        const float dm = XK[tt][v] * QK[tt][v] * m * uxq;
+        rowdm += dm;
+        col[v] = dm;
+        // W_st with mm = max(s, t): e^{(g_mm - g_s) + (g_mm - g_t)} rho_mm
+        const bool sl = t >= s;
+        const float gm = sl ? gt4[v] : gs;
+        const float wst = (t < b.nval && s_ok) ? fast_exp((gm - gs) + (gm - gt4[v])) * (sl ? rt4[v] : rho_s) : 0.f;
+        WK[tt][v] = 2.f * wst * KK[tt][v];
+      }
+      // column sums over this wave's s (the 16 lanes of each row group)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float cs = row16_sum(col[v]);
+        if (l16 == 0) SC(CS_COL0 + wave, 16 * tt + 4 * q4 + v) = cs;
+      }
+    }
+    float mw = 0.f;
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) mw = fmaxf(mw, absmax4(WK[tt]));
+    sw = pow2_scale(wave_max(mw));
+#pragma unroll
+    for (int jk = 0; jk < 2; ++jk) {
+      s1[jk] = h8(S1[2 * jk], S1[2 * jk + 1]);
+      s2[jk] = h8(S2[2 * jk], S2[2 * jk + 1]);
+      wk[jk] = h8_of(WK[2 * jk], WK[2 * jk + 1], sw);
+    }
+  }
+  rowdm += __shfl_xor(rowdm, 16, 64);
+  rowdm += __shfl_xor(rowdm, 32, 64);
+  // dk^T accumulators (rows f, column s): in-block terms, then the lambda terms L
+  f32x4 DK[8], L[8];
+  const float beta2 = 2.f * fast_exp(gs) * rho_s;
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) {
+    DK[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    L[nt] = DK[nt];
+  }
+#pragma unroll
+  for (int jk = 0; jk < 2; ++jk)
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      DK[nt] = mfma16h(frag_t_i(sQ, LDP, 32 * jk, 16 * nt, lane), s1[jk], DK[nt]);
+      DK[nt] = mfma16h(frag_t_i(sX, LDP, 32 * jk, 16 * nt, lane), s2[jk], DK[nt]);
+      L[nt] = mfma16h(frag_t_i(sK, LDP, 32 * jk, 16 * nt, lane), wk[jk], L[nt]);
+    }
+  // unscale: DK (sx sq), L's MFMA part (sw), P (sd), HX (sx)
+  const float uw = 1.f / sw, ud = 1.f / sd, ux = 1.f / sx;
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      DK[nt][v] *= uxq;
+      L[nt][v] = uw * L[nt][v] + beta2 * HK[nt][v];
+      P[nt][v] *= ud;
+      HX[nt][v] *= ux;
+    }
+  // per-column dot products with k_s, dq_s (fp32 from memory)
+  const float ec = fast_exp(Gam - gs);
+  float kl = 0.f, kp = 0.f, qhx = 0.f;
+  {
+    const int64_t ro = ((int64_t)(b.tok0 + s) * H + h) * D + 4 * q4;
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      const f16x4 kk = *reinterpret_cast<const f16x4*>(sK + s * LDP + icol(16 * nt + 4 * q4));
+      const f32x4 dq = s_ok ? *reinterpret_cast<const f32x4*>(w.dq + ro + 16 * nt) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        kl += (float)kk[v] * L[nt][v];
+        kp += (float)kk[v] * P[nt][v];
+        qhx += dq[v] * HX[nt][v];
+      }
+    }
+    kl += __shfl_xor(kl, 16, 64);
+    kl += __shfl_xor(kl, 32, 64);
+    kp += __shfl_xor(kp, 16, 64);
+    kp += __shfl_xor(kp, 32, 64);
+    qhx += __shfl_xor(qhx, 16, 64);
+    qhx += __shfl_xor(qhx, 32, 64);
+  }
+  // store dk_s = DK + L + e^{Gam - g_s} P
+  if (s_ok) {
+    float* dko = w.dk + ((int64_t)(b.tok0 + s) * H + h) * D + 4 * q4;
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      f32x4 y;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) y[v] = DK[nt][v] + L[nt][v] + ec * P[nt][v];
+      *reinterpret_cast<f32x4*>(dko + 16 * nt) = y;
+    }
+  }
+  // dL/dg_s without the cross-wave column sums
+  const float phi = s_ok ? 0.5f * ec * kp : 0.f;
+  float dg = 0.f;
+  if (s_ok) {
+    const float f = w.fro[(int64_t)(b.tok0 + s) * H + h];
+    dg = rowdm - fast_exp(gs) * qhx + SC(CS_A, s) * f * f - 0.5f * kl - phi;
+  }
+  // sum of phi over the block (for the last token)
+  float ph = phi;
+#pragma unroll
+  for (int m = 1; m < 16; m <<= 1) ph += __shfl_xor(ph, m, 64);
+  lds_barrier();       // the column sums, and every read of red[0..3]
+  const float dnh_all = red[0] + red[1] + red[2] + red[3];
+  lds_barrier();
+  if (lane == 0) red[4 + wave] = ph;
+  lds_barrier();
+  if (s_ok) {
+    dg -= SC(CS_COL0 + 0, s) + SC(CS_COL0 + 1, s) + SC(CS_COL0 + 2, s) + SC(CS_COL0 + 3, s);
+    if (s == b.nval - 1) dg += 0.5f * fast_exp(Gam) * dnh_all + red[4] + red[5] + red[6] + red[7];
+  }
+  // dgk_u = sum_{t >= u} dL/dg_t within the block
+  if (q4 == 0) SC(CS_DG, s) = s_ok ? dg : 0.f;
+  lds_barrier();
+  if (w.dgk && wave == 0 && lane < b.nval) {
+    float acc = 0.f;
+    for (int t2 = lane; t2 < b.nval; ++t2) acc += SC(CS_DG, t2);
+    w.dgk[(int64_t)(b.tok0 + lane) * H + h] = acc;
+  }
+}
+}  // namespace train
+}  // namespace gkap
+}  // namespace hmx
+
+// ---------------------------------------------------------------------------
+// The training-side Chebyshev solve (ChebyshevIteration of the training layer):
+// k, q [tokens, H, D] bf16 with k at H heads, the h_kk recurrence only (no GLA),
+// no initial state.  The forward leaves the walk's block-start states in the
+// workspace; the backward's dq solve reads them from there.
+// ---------------------------------------------------------------------------
+namespace {
+int cheb_params(Params& p, const char* fn, const void* k, int64_t k_ts, const void* rhs,
+                int64_t rhs_ts, int32_t dtype, const void* gk, int32_t gk_dtype,
+                const int32_t* seg_table, int32_t nseg_total, int32_t nblock_total, int32_t N,
+                int32_t H, int32_t D_, int32_t num_iter, float ridge_ratio, void* workspace,
+                size_t workspace_bytes) {
+  HMX_REQUIRE(dtype == HMX_BF16, HMX_EUNSUPPORTED, "%s: k and q must be bfloat16 (dtype code %d)",
+              fn, dtype);
+  HMX_REQUIRE(D_ == D, HMX_EUNSUPPORTED, "%s: only D == 128 is supported (got %d)", fn, D_);
+  HMX_REQUIRE(H > 0 && N >= 0 && num_iter >= 0, HMX_EINVAL, "%s: H=%d N=%d num_iter=%d", fn, H,
+              N, num_iter);
+  HMX_REQUIRE(k && rhs && seg_table, HMX_EINVAL, "%s: null tensor pointer", fn);
+  HMX_REQUIRE(k_ts % 8 == 0 && rhs_ts % 8 == 0 && ((uintptr_t)k | (uintptr_t)rhs) % 16 == 0,
+              HMX_EINVAL, "%s: k / q rows must be 16-byte aligned", fn);
+  HMX_REQUIRE(!gk || gk_dtype == HMX_F32 || gk_dtype == HMX_BF16 || gk_dtype == HMX_F16,
+              HMX_EUNSUPPORTED, "%s: gk dtype code %d", fn, gk_dtype);
+  HMX_REQUIRE(nseg_total >= 0 && nblock_total >= 0, HMX_EINVAL, "%s: nseg_total=%d nblock_total=%d",
+              fn, nseg_total, nblock_total);
+  const WsLayout wl = ws_layout(nseg_total, nblock_total, H);
+  HMX_REQUIRE(nseg_total == 0 || (workspace && workspace_bytes >= wl.total), HMX_EINVAL,
+              "%s: workspace of %zu bytes needed, %zu given", fn, wl.total, workspace_bytes);
+  p = Params{};
+  p.k = static_cast<const bf16*>(k); p.v = p.k; p.kv_ts = k_ts;
+  p.q = static_cast<const bf16*>(rhs); p.q_ts = rhs_ts;
+  p.gk = gk; p.gk_dt = gk_dtype;
+  p.fused = 0; p.gp = hmx_gate_proj{};
+  p.onw_dt = HMX_F32;
+  p.hkk = Pool{nullptr, nullptr, (int64_t)H * D * D, HMX_F32};
+  p.hkv = Pool{nullptr, nullptr, (int64_t)H * D * D, HMX_F32};
+  p.seg = seg_table; p.nseg_total = nseg_total; p.nblk_total = nblock_total;
+  p.H = H; p.HKV = H; p.num_iter = num_iter; p.ridge_ratio = ridge_ratio; p.scale = 1.f;
+  p.l2norm = 0;
+  char* ws = static_cast<char*>(workspace);
+  p.ws_hb = reinterpret_cast<f16*>(ws + wl.hb);
+  p.ws_sb = reinterpret_cast<f16*>(ws + wl.sb);
+  p.ws_dh = reinterpret_cast<float*>(ws + wl.dh);
+  p.ws_ds = reinterpret_cast<float*>(ws + wl.ds);
+  p.ws_h0 = reinterpret_cast<f16*>(ws + wl.h0);
+  p.ws_s0 = reinterpret_cast<f16*>(ws + wl.s0);
+  p.ws_boff = reinterpret_cast<float*>(ws + wl.boff);
+  p.ws_dec = reinterpret_cast<float*>(ws + wl.dec);
+  p.segblk = reinterpret_cast<int*>(ws + wl.segblk);
+  return HMX_OK;
+}
+}  // namespace
+
+extern "C" int hmx_gka_cheb_fwd(const void* k, int64_t k_token_stride, const void* q,
+                                int64_t q_token_stride, int32_t qk_dtype, const void* gk,
+                                int32_t gk_dtype, void* x, float* fro, float* h_kk_final,
+                                const int32_t* seg_table, int32_t nseg_total,
+                                int32_t nblock_total, int32_t N, int32_t H, int32_t D_,
+                                int32_t num_iter, float ridge_ratio, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+  Params p;
+  const int rc = cheb_params(p, "hmx_gka_cheb_fwd", k, k_token_stride, q, q_token_stride, qk_dtype,
+                             gk, gk_dtype, seg_table, nseg_total, nblock_total, N, H, D_,
+                             num_iter, ridge_ratio, workspace, workspace_bytes);
+  if (rc != HMX_OK) return rc;
+  HMX_REQUIRE(x && fro && ((uintptr_t)x % 16) == 0, HMX_EINVAL,
+              "hmx_gka_cheb_fwd: x (16-byte aligned) and fro are required");
+  if (nseg_total == 0) return HMX_OK;
+  p.o = static_cast<bf16*>(x);
+  p.fro = fro;
+  p.hkk.out = h_kk_final;
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL((walk::gka_walk_kernel<true, false>), dim3(nseg_total, H), dim3(NTHR), 0, s, p);
+  hipLaunchKernelGGL(gka_combine_kernel, dim3(N * H, 16), dim3(256), 0, s, p, 1);
+  if (nblock_total > 0)
+    hipLaunchKernelGGL((solve::gka_solve_kernel<true, false, solve::SM_X>), dim3(nblock_total, H),
+                       dim3(NTHR), 0, s, p);
+  return check_launch("hmx_gka_cheb_fwd");
+}
+
+extern "C" size_t hmx_gka_cheb_bwd_workspace_bytes(int32_t nblock_total, int32_t H) {
+  return al256((size_t)nblock_total * H * D * D * sizeof(float)) +
+         al256((size_t)nblock_total * H * sizeof(float));
+}
+
+extern "C" int hmx_gka_cheb_bwd(const void* k, int64_t k_token_stride, const void* x,
+                                const void* dx, int64_t dx_token_stride, int32_t dtype,
+                                const void* gk, int32_t gk_dtype, const float* fro, float* dq,
+                                float* dk, float* dgk, const int32_t* seg_table,
+                                int32_t nseg_total, int32_t nblock_total, int32_t N, int32_t H,
+                                int32_t D_, int32_t num_iter, float ridge_ratio,
+                                int32_t bp_lambda, void* fwd_workspace, size_t fwd_workspace_bytes,
+                                void* bwd_workspace, size_t bwd_workspace_bytes, void* stream) {
+  Params p;
+  const int rc = cheb_params(p, "hmx_gka_cheb_bwd", k, k_token_stride, dx, dx_token_stride, dtype,
+                             gk, gk_dtype, seg_table, nseg_total, nblock_total, N, H, D_,
+                             num_iter, ridge_ratio, fwd_workspace, fwd_workspace_bytes);
+  if (rc != HMX_OK) return rc;
+  HMX_REQUIRE(x && fro && dq && dk && (!gk || dgk) &&
+                  (((uintptr_t)x | (uintptr_t)dq | (uintptr_t)dk) % 16) == 0,
+              HMX_EINVAL, "hmx_gka_cheb_bwd: x, fro, dq, dk (16-byte aligned) and dgk (with gk) "
+                          "are required");
+  const size_t need = hmx_gka_cheb_bwd_workspace_bytes(nblock_total, H);
+  HMX_REQUIRE(nblock_total == 0 || (bwd_workspace && bwd_workspace_bytes >= need), HMX_EINVAL,
+              "hmx_gka_cheb_bwd: backward workspace of %zu bytes needed, %zu given", need,
+              bwd_workspace_bytes);
+  if (nseg_total == 0 || nblock_total == 0) return HMX_OK;
+  p.fro = const_cast<float*>(fro);
+  p.xo32 = dq;
+  train::Bwd w;
+  w.x = static_cast<const bf16*>(x);
+  w.dq = dq; w.fro = fro;
+  w.e = static_cast<float*>(bwd_workspace);
+  w.gam = reinterpret_cast<float*>(static_cast<char*>(bwd_workspace) +
+                                   al256((size_t)nblock_total * H * D * D * sizeof(float)));
+  w.dk = dk; w.dgk = gk ? dgk : nullptr;
+  w.bp_lambda = bp_lambda;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid(nblock_total, H);
+  hipLaunchKernelGGL((solve::gka_solve_kernel<true, false, solve::SM_DQ>), grid, dim3(NTHR), 0, s, p);
+  hipLaunchKernelGGL(train::cheb_e_kernel, grid, dim3(NTHR), 0, s, p, w);
+  hipLaunchKernelGGL(train::cheb_dscan_kernel, dim3(N * H, 16), dim3(256), 0, s, p, w);
+  hipLaunchKernelGGL(train::cheb_dk_kernel, grid, dim3(NTHR), 0, s, p, w);
+  return check_launch("hmx_gka_cheb_bwd");
 }

@@ -1,0 +1,120 @@
+"""The training layer's Chebyshev solve with its backward, over libhmx.
+
+Entry points (reference paths relative to the reference repository root,
+training/src/hmf/model/hybrid_zoo/layers/gated_kalmanet/ops/chebyshev/):
+
+- ``ChebyshevIteration`` — chebyshev_iteration.py:560-688, the autograd function
+  ``apply(k, q, gk=None, num_iter=30, ridge_ratio=0.02, bp_lambda=True, h0=None,
+  chunk_size=64) -> (x, h_kk_final)``: per token x_t solves
+  (H_t + r |H_t|_F I) x_t = q_t by the Chebyshev recurrence, H_t = e^{gk_t} H_{t-1}
+  + k_t k_t^T from zero.  Its backward returns (dk, dq, dgk) as the reference's
+  does: dq by the same recurrence on dx with the forward's |H_t|_F, dk and dgk
+  from dL/dH_t = -dq_t x_t^T (- r (dq_t . x_t) H_t / |H_t|_F with bp_lambda); the
+  gradient of h_kk_final is not propagated (the reference drops it, :638).
+- ``latent_chebyshev`` — gka_chebyshev_solve.py:74-104, the dispatcher over it.
+
+Kernels (libhmx ``hmx_gka_cheb_fwd`` / ``hmx_gka_cheb_bwd``): the serving prefill's
+state walk and combine, and its solve kernel writing x and |H_t|_F instead of the
+GLA output; the backward runs the solve on dx reading the saved |H_t|_F and the
+forward's block-start states, then three launches for dk and dgk (the blocks'
+contributions to the state gradient, its reverse scan over the blocks, and the
+per-block dk / dgk).  k, q must be bfloat16 with head dim 128; ``chunk_size``
+only tiles the reference's kernels (the blocks here are 64 tokens) and h0 (the
+sequence-parallel initial state) is not supported.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+from .gdn import _device_table, _segment_table
+
+
+def _check(k, q, gk):
+    if q.dim() != 4 or k.shape != q.shape:
+        raise ValueError(f"k and q must both be [B, T, H, D], got {tuple(k.shape)} and "
+                         f"{tuple(q.shape)}")
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16:
+        raise NotImplementedError(f"hmx ChebyshevIteration: k and q must be bfloat16, got "
+                                  f"{k.dtype} / {q.dtype}")
+    if q.shape[-1] != 128:
+        raise NotImplementedError(f"hmx ChebyshevIteration: head dim must be 128, got {q.shape[-1]}")
+    if gk is not None and tuple(gk.shape) != tuple(q.shape[:3]):
+        raise ValueError(f"gk must be [B, T, H] = {tuple(q.shape[:3])}, got {tuple(gk.shape)}")
+    _lib.require_gpu(k, q, gk)
+
+
+def cheb_forward(k, q, gk, num_iter: int, ridge_ratio: float, segment_chunks=None):
+    """The forward launches: (x, |H_t|_F [B,T,H] fp32, h_kk_final [B,H,D,D] fp32,
+    and what the backward needs of the call: the workspace with the block-start
+    states, the segment table and its sizes).  ``segment_chunks`` cuts every
+    sequence into segments of at most that many 64-token blocks (tests)."""
+    _check(k, q, gk)
+    B, T, H, D = q.shape
+    dev = q.device
+    k2, q2 = k.contiguous(), q.contiguous()
+    gk2 = None if gk is None else gk.contiguous()
+    rows, nblk = _segment_table(_lib.PLAN_GKA, [(n * T, n * T + T) for n in range(B)],
+                                B * T, H, dev, segment_chunks)
+    seg = _device_table(rows, dev)
+    lib = _lib.load()
+    ws = torch.empty(max(int(lib.hmx_gka_chunk_workspace_bytes(len(rows), nblk, B, H)), 16),
+                     dtype=torch.uint8, device=dev)
+    x = torch.empty_like(q2)
+    fro = torch.empty(B, T, H, dtype=torch.float32, device=dev)
+    h_final = torch.empty(B, H, D, D, dtype=torch.float32, device=dev)
+    _lib.call("hmx_gka_cheb_fwd", _lib.ptr(k2), H * D, _lib.ptr(q2), H * D,
+              _lib.dtype_code(q2), _lib.ptr(gk2), 0 if gk2 is None else _lib.dtype_code(gk2),
+              _lib.ptr(x), _lib.ptr(fro), _lib.ptr(h_final), _lib.ptr(seg), len(rows), nblk,
+              B, H, D, int(num_iter), float(ridge_ratio), _lib.ptr(ws), ws.numel(),
+              _lib.stream_of(q2))
+    return x, fro, h_final, (k2, gk2, ws, seg, len(rows), nblk)
+
+
+class ChebyshevIteration(torch.autograd.Function):
+    """chebyshev_iteration.py:560-688 (see the module docstring)."""
+
+    @staticmethod
+    def forward(ctx, k, q, gk=None, num_iter: int = 30, ridge_ratio: float = 0.02,
+                bp_lambda: bool = True, h0=None, chunk_size: int = 64, _segment_chunks=None):
+        if h0 is not None:
+            raise NotImplementedError("hmx ChebyshevIteration: an initial state h0 (the "
+                                      "sequence-parallel path) is not supported")
+        x, fro, h_final, (k2, gk2, ws, seg, nrows, nblk) = cheb_forward(
+            k, q, gk, num_iter, ridge_ratio, _segment_chunks)
+        ctx.save_for_backward(k2, x, fro, gk2, ws, seg)
+        ctx.meta = (nrows, nblk, int(num_iter), float(ridge_ratio), bool(bp_lambda),
+                    q.dtype, None if gk is None else gk.dtype)
+        return x, h_final
+
+    @staticmethod
+    def backward(ctx, dx, d_kk_final=None):
+        k, x, fro, gk, ws, seg = ctx.saved_tensors
+        nrows, nblk, num_iter, ridge, bp_lambda, q_dtype, gk_dtype = ctx.meta
+        B, T, H, D = k.shape
+        dev = k.device
+        if dx is None:
+            dx = torch.zeros_like(x)
+        # the kernels read dx as bfloat16 rows (x's dtype, which autograd hands back)
+        dx2 = dx.to(torch.bfloat16).contiguous()
+        dq = torch.empty(B, T, H, D, dtype=torch.float32, device=dev)
+        dk = torch.empty_like(dq)
+        dgk = None if gk is None else torch.empty(B, T, H, dtype=torch.float32, device=dev)
+        lib = _lib.load()
+        bws = torch.empty(max(int(lib.hmx_gka_cheb_bwd_workspace_bytes(nblk, H)), 16),
+                          dtype=torch.uint8, device=dev)
+        _lib.call("hmx_gka_cheb_bwd", _lib.ptr(k), H * D, _lib.ptr(x), _lib.ptr(dx2), H * D,
+                  _lib.dtype_code(k), _lib.ptr(gk), 0 if gk is None else _lib.dtype_code(gk),
+                  _lib.ptr(fro), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dgk), _lib.ptr(seg), nrows,
+                  nblk, B, H, D, num_iter, ridge, int(bp_lambda), _lib.ptr(ws), ws.numel(),
+                  _lib.ptr(bws), bws.numel(), _lib.stream_of(k))
+        return (dk.to(k.dtype), dq.to(q_dtype), None if dgk is None else dgk.to(gk_dtype),
+                None, None, None, None, None, None)
+
+
+def latent_chebyshev(k, q, ridge_strength, num_iter, solver_type, bp_lambda, gk, chunk_size):
+    """gka_chebyshev_solve.py:74-104: (x, kk_final) of the ridge solve."""
+    if solver_type != "chebyshev":
+        raise ValueError(f"Unknown GKA solver type: {solver_type}")
+    return ChebyshevIteration.apply(k, q, gk, num_iter, ridge_strength, bp_lambda, None,
+                                    chunk_size)

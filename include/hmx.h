@@ -353,6 +353,49 @@ int hmx_gka_chunk_fwd(const void* q, int64_t q_token_stride, const void* k,
 size_t hmx_gka_chunk_workspace_bytes(int32_t nseg_total, int32_t nblock_total, int32_t N,
                                      int32_t H);
 
+/* The training layer's Chebyshev solve, forward and backward.
+ *
+ * hmx_gka_cheb_fwd: per token x_t = the Chebyshev recurrence for
+ * (H_t + r |H_t|_F I) x = q_t, H_t = e^{gk_t} H_{t-1} + k_t k_t^T from zero, for
+ * N sequences of tokens given by seg_table (as hmx_gka_chunk_fwd's, HMX_PLAN_GKA).
+ * k, q: [tokens][H][D] rows at their token strides, bf16, D = 128; gk [tokens][H]
+ * f32/bf16/f16 or NULL (no decay).  Writes x [tokens][H][D] bf16 (contiguous),
+ * fro = |H_t|_F [tokens][H] f32 and h_kk_final [N][H][D][D] f32.  The workspace
+ * (hmx_gka_chunk_workspace_bytes) keeps the block-start states for the backward.
+ * Replaces: ChebyshevIteration.forward
+ *   training/src/hmf/model/hybrid_zoo/layers/gated_kalmanet/ops/chebyshev/
+ *   chebyshev_iteration.py:569-604 (chebyshev_iteration_forward_triton :462-557
+ *   and its kernels :167-460, chunk_fwd_h of fla for h_kk).
+ */
+int hmx_gka_cheb_fwd(const void* k, int64_t k_token_stride, const void* q,
+                     int64_t q_token_stride, int32_t qk_dtype, const void* gk, int32_t gk_dtype,
+                     void* x, float* fro, float* h_kk_final, const int32_t* seg_table,
+                     int32_t nseg_total, int32_t nblock_total, int32_t N, int32_t H, int32_t D,
+                     int32_t num_iter, float ridge_ratio, void* workspace,
+                     size_t workspace_bytes, void* stream);
+
+/* hmx_gka_cheb_bwd: the backward of hmx_gka_cheb_fwd on the same k, gk, seg_table
+ * and forward workspace (unchanged since the forward), its x and fro, and dx
+ * ([tokens][H][D] bf16 rows at dx_token_stride).  Writes dq, dk [tokens][H][D] f32
+ * (contiguous) and, with gk, dgk [tokens][H] f32: dq solves for dx with the saved
+ * |H_t|_F; dk, dgk follow from dL/dH_t = -dq_t x_t^T, minus
+ * r (dq_t . x_t) H_t / |H_t|_F when bp_lambda.  bwd_workspace:
+ * hmx_gka_cheb_bwd_workspace_bytes(nblock_total, H) bytes.
+ * Replaces: ChebyshevIteration.backward
+ *   training/.../ops/chebyshev/chebyshev_iteration.py:606-688 (with
+ *   chunk_dk_backward.py:372-445, chunk_dk_backward_gating.py:287-373,
+ *   chunk_dh_kk_to_dk_backward.py:96-135, chunk_dh_kk_to_dk_gating_backward.py:146-198 and
+ *   chunk_bwd_dh of fla).
+ */
+int hmx_gka_cheb_bwd(const void* k, int64_t k_token_stride, const void* x, const void* dx,
+                     int64_t dx_token_stride, int32_t dtype, const void* gk, int32_t gk_dtype,
+                     const float* fro, float* dq, float* dk, float* dgk,
+                     const int32_t* seg_table, int32_t nseg_total, int32_t nblock_total,
+                     int32_t N, int32_t H, int32_t D, int32_t num_iter, float ridge_ratio,
+                     int32_t bp_lambda, void* fwd_workspace, size_t fwd_workspace_bytes,
+                     void* bwd_workspace, size_t bwd_workspace_bytes, void* stream);
+size_t hmx_gka_cheb_bwd_workspace_bytes(int32_t nblock_total, int32_t H);
+
 /*
  * Mamba2 SSD chunk scan forward, bf16 x/B/C/z/y, fp32 states, varlen via a
  * segment table of rows (n, bos, eos, c_start, c_end, seg_idx, first_seg, nseg)

@@ -1,0 +1,117 @@
+"""GPU: hmx.ChebyshevIteration (the training layer's solve with its backward,
+chebyshev_iteration.py:560-688) through autograd against the float64 oracle
+(oracle/gka_train.py, pinned in test_oracle_gka_train.py).
+
+Inputs as the training layer prepares them (gka.py:477-490): unit-norm q, k
+scaled by beta in (0, 1), gk a negative log-decay.  The forward is checked on x
+(bf16, output tolerance), |H_t|_F and the final state (state tolerance).  The
+backward is checked on the HIP path's own saved x and |H_t|_F fed to the oracle
+(the reference's backward reads exactly these), so its tolerance measures the
+backward kernels alone: norm-wise relative 1e-2 on dq, dk and dgk.  The backward
+kernels round their operands once to fp16 (2^-11 relative); the reference's
+kernels round theirs to bf16 (2^-8)."""
+import pytest
+import torch
+
+import hmx
+from hmx.ops.gka_train import cheb_forward
+from oracle import gka_train as tr
+from util import STATE_REL, rel_err
+
+pytestmark = pytest.mark.gpu
+
+D = 128
+GRAD_REL = 1e-2
+OUT_ROW_REL = 1e-2
+
+
+def _inputs(B, T, H, seed, gated, dev):
+    g0 = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, T, H, D, generator=g0)
+    q = q / q.norm(dim=-1, keepdim=True)
+    k = torch.randn(B, T, H, D, generator=g0)
+    beta = torch.rand(B, T, H, 1, generator=g0) * 0.9 + 0.1
+    k = k / k.norm(dim=-1, keepdim=True) * beta
+    gk = -0.1 * torch.rand(B, T, H, generator=g0) if gated else None
+    dx = torch.randn(B, T, H, D, generator=g0)
+    bf = lambda t: t.bfloat16().to(dev)
+    return bf(q), bf(k), (None if gk is None else gk.to(dev)), bf(dx)
+
+
+CASES = [  # B, T, H, gated, num_iter, bp_lambda, blocks per segment (None: the planner's)
+    (2, 200, 2, True, 8, True, None),
+    (1, 256, 2, False, 8, True, None),
+    (2, 130, 2, True, 30, False, None),
+    (1, 70, 3, True, 0, True, None),
+    (2, 300, 2, True, 8, True, 1),      # segments of one block: the combine carries the states
+    (1, 2048, 2, True, 8, True, None),  # one long sequence, which the planner cuts in two
+]
+
+
+@pytest.mark.parametrize("B,T,H,gated,num_iter,bp_lambda,seg", CASES)
+def test_chebyshev_iteration_matches_oracle(dev, B, T, H, gated, num_iter, bp_lambda, seg):
+    q, k, gk, dx = _inputs(B, T, H, 11, gated, dev)
+    qq, kk = q.clone().requires_grad_(True), k.clone().requires_grad_(True)
+    gg = None if gk is None else gk.clone().requires_grad_(True)
+    x, h_final = hmx.ChebyshevIteration.apply(kk, qq, gg, num_iter, 0.02, bp_lambda, None, 64,
+                                              seg)
+    x_r, fro_r, h_r = tr.chebyshev_iteration_fwd(k.cpu(), q.cpu(), None if gk is None else gk.cpu(),
+                                                 num_iter, 0.02)
+    assert x.dtype == torch.bfloat16 and tuple(x.shape) == (B, T, H, D)
+    (x.float() * dx.float()).sum().backward()
+    # the oracle's backward on the saved x and |H_t|_F of this call
+    ctx_fro = _saved_fro(kk, qq, gg, num_iter, seg)
+    dk_r, dq_r, dgk_r = tr.chebyshev_iteration_bwd(k.cpu(), x.detach().cpu(), ctx_fro, None if gk is None
+                                                   else gk.cpu(), dx.cpu(), num_iter, 0.02, bp_lambda)
+    errs = {"x rows": _row_rel(x, x_r), "fro": rel_err(ctx_fro, fro_r),
+            "h_kk_final": rel_err(h_final, h_r)}
+    for got, exp, name in ((qq.grad, dq_r, "dq"), (kk.grad, dk_r, "dk"),
+                           (None if gg is None else gg.grad, dgk_r, "dgk")):
+        if exp is None:
+            assert got is None
+            continue
+        assert torch.isfinite(got.float()).all(), name
+        errs[name] = rel_err(got, exp)
+    print("errors", {n: f"{e:.2e}" for n, e in errs.items()})
+    # x grows like q / (r |H_t|_F): each token's row is compared norm-wise
+    assert errs["x rows"] < OUT_ROW_REL
+    assert errs["fro"] < 1e-4 and errs["h_kk_final"] < STATE_REL
+    for name in ("dq", "dk", "dgk"):
+        if name in errs:
+            assert errs[name] < GRAD_REL, f"{name}: rel {errs[name]:.3e}"
+
+
+def _row_rel(x, ref):
+    """max over token rows of |x_t - ref_t| / |ref_t|"""
+    d = (x.detach().double().cpu() - ref).norm(dim=-1)
+    return (d / ref.norm(dim=-1)).max().item()
+
+
+def _saved_fro(kk, qq, gg, num_iter, seg):
+    """|H_t|_F as the forward saves it (the forward launches again; they are
+    deterministic)."""
+    with torch.no_grad():
+        return cheb_forward(kk.detach(), qq.detach(), None if gg is None else gg.detach(),
+                            num_iter, 0.02, seg)[1].cpu()
+
+
+def test_chebyshev_iteration_deterministic(dev):
+    q, k, gk, dx = _inputs(1, 150, 2, 5, True, dev)
+    outs = []
+    for _ in range(2):
+        qq, kk, gg = (t.clone().requires_grad_(True) for t in (q, k, gk))
+        x, hT = hmx.ChebyshevIteration.apply(kk, qq, gg, 8, 0.02, True)
+        (x.float() * dx.float()).sum().backward()
+        outs.append([x, hT, qq.grad, kk.grad, gg.grad])
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+
+
+def test_chebyshev_iteration_rejects(dev):
+    q, k, gk, _ = _inputs(1, 10, 2, 1, True, dev)
+    with pytest.raises(NotImplementedError):
+        hmx.ChebyshevIteration.apply(k, q, gk, 8, 0.02, True, torch.zeros(1, 2, D, D, device=dev))
+    with pytest.raises(NotImplementedError):
+        hmx.ChebyshevIteration.apply(k.float(), q.float(), gk, 8, 0.02, True)
+    with pytest.raises(ValueError):
+        hmx.ChebyshevIteration.apply(k, q, gk[:, :5], 8, 0.02, True)
