@@ -494,6 +494,41 @@ def bench_gka(dev, steps, warmup, num_iter):
                 GBps=by / (ms * 1e-3) / 1e9)
 
 
+def bench_gka_train(dev, steps, warmup, num_iter=8, B=8, T=4096, H=32):
+    """F4: the training layer's Chebyshev solve (hmx.ChebyshevIteration) forward and
+    forward + backward through autograd, B=8 x T=4096 tokens (the C3 token count),
+    H=32, d=128, ridge 0.02, bp_lambda; inputs as the layer prepares them (unit q,
+    k = beta k^ with beta in (0.1, 1), gk = logsigmoid(N(2, 1)) / 8)."""
+    import torch
+    import torch.nn.functional as F
+    import hmx
+    from hmx import workloads as wl
+    D = 128
+    g = torch.Generator(device=dev).manual_seed(wl.SEED_BASE + 12)
+    q = F.normalize(torch.randn(B, T, H, D, generator=g, device=dev), dim=-1).bfloat16()
+    beta = torch.rand(B, T, H, 1, generator=g, device=dev) * 0.9 + 0.1
+    k = (F.normalize(torch.randn(B, T, H, D, generator=g, device=dev), dim=-1) * beta).bfloat16()
+    gk = F.logsigmoid(torch.randn(B, T, H, generator=g, device=dev) + 2.0) / 8
+    dx = torch.randn(B, T, H, D, generator=g, device=dev).bfloat16()
+    kk, qq, gg = (t.clone().requires_grad_(True) for t in (k, q, gk))
+
+    def fwd():
+        with torch.no_grad():
+            hmx.ChebyshevIteration.apply(k, q, gk, num_iter, 0.02, True)
+
+    def fwd_bwd():
+        x, _ = hmx.ChebyshevIteration.apply(kk, qq, gg, num_iter, 0.02, True)
+        torch.autograd.backward(x, dx)
+
+    ms_f = _timed(fwd, steps, warmup)
+    ms_fb = _timed(fwd_bwd, steps, warmup)
+    ff, fb = wl.gka_train_flops(B * T, H, num_iter)
+    return dict(ms_fwd=ms_f, ms_fwd_bwd=ms_fb, flops_fwd=ff, flops_bwd=fb,
+                tokens_per_s=B * T / (ms_fb * 1e-3),
+                TFLOPs_fwd=ff / (ms_f * 1e-3) / 1e12,
+                TFLOPs_fwd_bwd=(ff + fb) / (ms_fb * 1e-3) / 1e12)
+
+
 def bench_ssd(dev, steps, warmup, b=2, T=16384, H=64, P=64, N=128, G=8):
     """C4: mamba_chunk_scan_combined, b=2, T=16384, H=64, P=64, N=128, G=8, fp32 final
     state (other shapes through the keywords: the primed layout is P = N = 128, G = H)."""
@@ -647,10 +682,11 @@ def measured_traffic(key):
 # --only accepts beside single legs
 LEGS = ["c1", "prefill_gqa", "prefill_varlen", "prefill_layer_gates", "onorm", "conv", "gdn_core",
         "mamba2_core", "gka_core", "gdn_decode", "gka_decode", "ssd_c4", "ssd_primed",
-        "ssd_decode", "gka8", "gka32"]
+        "ssd_decode", "gka8", "gka32", "gka_train"]
 GROUPS = {"prefill": ["c1", "prefill_gqa", "prefill_varlen", "prefill_layer_gates"],
           "core": ["gdn_core", "mamba2_core", "gka_core"], "decode": ["gdn_decode", "gka_decode"],
-          "ssd": ["ssd_c4", "ssd_primed", "ssd_decode"], "gka": ["gka8", "gka32"]}
+          "ssd": ["ssd_c4", "ssd_primed", "ssd_decode"], "gka": ["gka8", "gka32"],
+          "train": ["gka_train"]}
 
 
 def measured_mfma_busy(key):
@@ -715,6 +751,7 @@ def main():
         "ssd_decode": lambda: out.__setitem__("ssd_decode", bench_ssd_decode(dev)),
         "gka8": lambda: out.setdefault("gka", {}).__setitem__(8, bench_gka(dev, max(2, S // 4), 1, 8)),
         "gka32": lambda: out.setdefault("gka", {}).__setitem__(32, bench_gka(dev, max(2, S // 4), 1, 32)),
+        "gka_train": lambda: out.__setitem__("gka_train", bench_gka_train(dev, max(2, S // 4), 1)),
     }
     for name in LEGS:           # run order: the long compute-bound GKA legs last
         if name in sel:
@@ -880,6 +917,21 @@ def main():
                              "algorithmic_flops": r["flops"],
                              "hbm_GBps": round(r["GBps"], 1)},
             }
+    if "gka_train" in out:
+        r = out["gka_train"]
+        line["gka_train"] = {
+            "value": round(r["tokens_per_s"], 1), "unit": "tokens/s (forward + backward)",
+            "ms_fwd": round(r["ms_fwd"], 4), "ms_fwd_bwd": round(r["ms_fwd_bwd"], 4),
+            "config": {"workload": "F4 GKA training solve (ChebyshevIteration fwd + bwd)",
+                       "B": 8, "T": 4096, "H": 32, "d": 128, "num_iter": 8, "ridge_ratio": 0.02,
+                       "bp_lambda": True},
+            "roofline": {"bound": "mfma", "achieved": round(r["TFLOPs_fwd_bwd"], 1),
+                         "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(r["TFLOPs_fwd_bwd"] / BF16_PEAK_TFLOPS, 4),
+                         "forward_TFLOPs": round(r["TFLOPs_fwd"], 1),
+                         "algorithmic_flops_fwd": r["flops_fwd"],
+                         "algorithmic_flops_bwd": r["flops_bwd"]},
+        }
     if "ssd" in out:
         r = out["ssd"]
         line["ssd"] = {

@@ -1315,18 +1315,14 @@ __device__ __forceinline__ float block_decay(const Params& p, const Blk& b, int 
   return scan64((ok && p.gk) ? ldsc(p.gk, (int64_t)(b.tok0 + lane) * p.H + h, p.gk_dt) : 0.f);
 }
 
-// a_t = -r (dq_t . x_t) / |H_t|_F for token row `row` (one 16-lane group per row)
+// a_t = -r (dq_t . x_t) / |H_t|_F for token row `row` from the row's staged
+// pieces (features 8 l16 .. 8 l16 + 7 in each lane of its 16-lane group)
 __device__ __forceinline__ float lambda_weight(const Params& p, const Bwd& w, const Blk& b, int row,
-                                               int h, int l16) {
+                                               int h, const f32x4& q0, const f32x4& q1,
+                                               const bf16x8& xv) {
   float d = 0.f;
-  if (row < b.nval && w.bp_lambda) {
-    const int64_t ro = ((int64_t)(b.tok0 + row) * p.H + h) * D + 8 * l16;
-    const f32x4 q0 = *reinterpret_cast<const f32x4*>(w.dq + ro);
-    const f32x4 q1 = *reinterpret_cast<const f32x4*>(w.dq + ro + 4);
-    const bf16x8 xv = *reinterpret_cast<const bf16x8*>(w.x + ro);
 #pragma unroll
-    for (int v = 0; v < 4; ++v) d += q0[v] * (float)xv[v] + q1[v] * (float)xv[4 + v];
-  }
+  for (int v = 0; v < 4; ++v) d += q0[v] * (float)xv[v] + q1[v] * (float)xv[4 + v];
   d = row16_sum(d);
   const float f = (row < b.nval && w.bp_lambda) ? w.fro[(int64_t)(b.tok0 + row) * p.H + h] : 0.f;
   return f > 0.f ? -p.ridge_ratio * d / f : 0.f;
@@ -1403,10 +1399,19 @@ __global__ __launch_bounds__(NTHR, 1) void cheb_e_kernel(Params p, Bwd w) {
     sG[lane] = g;
     if (lane == b.nval - 1) w.gam[(int64_t)gb * H + h] = g;
   }
+  // the rows, and a_t from them
+  bf16x8 kr[CB / 16], xr[CB / 16];
+  f32x4 q0[CB / 16], q1[CB / 16];
 #pragma unroll
   for (int pass = 0; pass < CB / 16; ++pass) {
-    const int row = pass * 16 + (tid >> 4);
-    const float a = lambda_weight(p, w, b, row, h, l16);
+    const int row = pass * 16 + (tid >> 4), f0 = (tid & 15) * 8;
+    const bool ok = row < b.nval;
+    const int64_t ro = ((int64_t)(b.tok0 + row) * H + h) * D + f0;
+    kr[pass] = ok ? *reinterpret_cast<const bf16x8*>(p.k + (int64_t)(b.tok0 + row) * p.kv_ts + h * D + f0) : bf16x8{};
+    xr[pass] = ok ? *reinterpret_cast<const bf16x8*>(w.x + ro) : bf16x8{};
+    q0[pass] = ok ? *reinterpret_cast<const f32x4*>(w.dq + ro) : f32x4{0.f, 0.f, 0.f, 0.f};
+    q1[pass] = ok ? *reinterpret_cast<const f32x4*>(w.dq + ro + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+    const float a = lambda_weight(p, w, b, row, h, q0[pass], q1[pass], xr[pass]);
     if (l16 == 0) sA[row] = a;
   }
   lds_barrier();
@@ -1424,19 +1429,11 @@ __global__ __launch_bounds__(NTHR, 1) void cheb_e_kernel(Params p, Bwd w) {
   if (tid == 0) s_alpha = alpha;
   lds_barrier();
   // stage k, 2 beta k, -e^{g} dq, x (fp16, interleaved; the last three scaled)
-  bf16x8 kr[CB / 16], xr[CB / 16];
-  f32x4 q0[CB / 16], q1[CB / 16];
   float mx[3] = {0.f, 0.f, 0.f};            // max |x|, |e^g dq|, |2 beta k|
 #pragma unroll
   for (int pass = 0; pass < CB / 16; ++pass) {
-    const int row = pass * 16 + (tid >> 4), f0 = (tid & 15) * 8;
-    const bool ok = row < b.nval;
-    const int64_t ro = ((int64_t)(b.tok0 + row) * H + h) * D + f0;
-    kr[pass] = ok ? *reinterpret_cast<const bf16x8*>(p.k + (int64_t)(b.tok0 + row) * p.kv_ts + h * D + f0) : bf16x8{};
-    xr[pass] = ok ? *reinterpret_cast<const bf16x8*>(w.x + ro) : bf16x8{};
-    const float eg = ok ? -fast_exp(sG[row]) : 0.f;
-    q0[pass] = ok ? *reinterpret_cast<const f32x4*>(w.dq + ro) : f32x4{0.f, 0.f, 0.f, 0.f};
-    q1[pass] = ok ? *reinterpret_cast<const f32x4*>(w.dq + ro + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+    const int row = pass * 16 + (tid >> 4);
+    const float eg = row < b.nval ? -fast_exp(sG[row]) : 0.f;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       q0[pass][v] *= eg;
@@ -1566,7 +1563,7 @@ __global__ __launch_bounds__(NTHR, 1) void cheb_dk_kernel(Params p, Bwd w) {
     q1[pass] = ok ? *reinterpret_cast<const f32x4*>(w.dq + ro + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
     mx[0] = fmaxf(mx[0], absmax8(xr[pass]));
     mx[1] = fmaxf(mx[1], fmaxf(absmax4(q0[pass]), absmax4(q1[pass])));
-    const float a = lambda_weight(p, w, b, row, h, l16);
+    const float a = lambda_weight(p, w, b, row, h, q0[pass], q1[pass], xr[pass]);
     if (l16 == 0) SC(CS_A, row) = a;
   }
 #pragma unroll

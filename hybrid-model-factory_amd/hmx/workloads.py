@@ -145,6 +145,17 @@ def gka_prefill_flops(T: int, H: int, num_iter: int, d: int = 128, C: int = 64) 
     return 2.0 * T * H * ((4 + n) * d * d + (3 + 2 * n) * C * d + C * C)
 
 
+def gka_train_flops(T: int, H: int, num_iter: int, d: int = 128, C: int = 64):
+    """(forward, backward) FLOPs of the training Chebyshev solve over T tokens x H heads.
+    Forward: 2*T*H*[(2+n) d^2 + (1+2n) C d + C^2] (h_kk update, exact-fro terms, n
+    iterations).  Backward: 2*T*H*[(n+6) d^2 + (2n+6) C d] (the dq solve's n
+    iterations; the block contributions dq^T x, x^T dq, K^T diag K; h_c k, h_c x,
+    Dn k; and the in-block x.k, dq.k, k.k products with their three products back)."""
+    n = num_iter
+    return (2.0 * T * H * ((2 + n) * d * d + (1 + 2 * n) * C * d + C * C),
+            2.0 * T * H * ((n + 6) * d * d + (2 * n + 6) * C * d))
+
+
 def gka_prefill_bytes(T: int, H: int, HKV: int, d: int = 128, n_seqs: int = 1) -> float:
     """q,o [T,H,d] + k,v [T,HKV,d] bf16 + alpha,beta,g fp32 + two fp32 final states."""
     return T * H * 2 * d * 2 + T * HKV * 2 * d * 2 + 3 * T * H * 4 + 2 * n_seqs * H * d * d * 4
