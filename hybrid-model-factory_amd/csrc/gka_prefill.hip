@@ -103,9 +103,12 @@ struct Params {
   const bf16* zg; int64_t zg_ts, zg_hs;   // gate rows, or null (plain RMSNorm)
   const void* onw; int onw_dt;            // weight [D]
   float on_eps;
-  // the training solve (SM_X / SM_DQ solve kernels): |H_t|_F per token [tokens][H]
-  // (written by SM_X, read by SM_DQ) and the fp32 solution of SM_DQ [tokens][H][D]
-  float* fro; float* xo32;
+  // the training solve (SM_X / SM_DQ / SM_GLA_SAVE solve kernels): |H_t|_F per token
+  // [tokens][H] (written by SM_X and SM_GLA_SAVE, read by SM_DQ), the fp32 solution
+  // of SM_DQ [tokens][H][D] (added to what it holds when xo32_acc), and the solution
+  // x (before the alpha blend) saved by SM_GLA_SAVE [tokens][H][D] bf16
+  float* fro; float* xo32; int xo32_acc; bf16* xs;
+  const float* rhs32;                     // SM_DQ: an fp32 right-hand side in place of p.q
 };
 
 __device__ __forceinline__ float ldsc(const void* p, int64_t i, int dt) {
@@ -650,12 +653,14 @@ __device__ __forceinline__ void with_wave(int wave, F&& f) {
 // What the solve kernel produces: the GLA output (serving prefill), or the solution
 // x of the Chebyshev solve itself (training): SM_X writes x (bf16, into p.o) and
 // |H_t|_F; SM_DQ solves for the right-hand side in p.q with the |H_t|_F of the
-// forward read back (the backward's dq) and writes fp32 (p.xo32).
-enum SolveMode { SM_GLA = 0, SM_X = 1, SM_DQ = 2 };
+// forward read back (the backward's dq) and writes fp32 (p.xo32); SM_GLA_SAVE is
+// the GLA output that also saves x (p.xs) and |H_t|_F for the training backward.
+enum SolveMode { SM_GLA = 0, SM_X = 1, SM_DQ = 2, SM_GLA_SAVE = 3 };
 
 template <bool SOLVE, bool NORM, int MODE = SM_GLA>
 __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
   static_assert(MODE == SM_GLA || (SOLVE && !NORM), "the x outputs need the solver");
+  constexpr bool GLA = MODE == SM_GLA || MODE == SM_GLA_SAVE;
   __shared__ __align__(16) unsigned char smem[SMEM];
   f16* sK = reinterpret_cast<f16*>(smem + OFF_K);
   f16* sV = reinterpret_cast<f16*>(smem + OFF_V);
@@ -705,18 +710,18 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
     const bf16x8 vr = ok ? *reinterpret_cast<const bf16x8*>(p.v + tok * p.kv_ts + hk * D + f0) : bf16x8{};
     const float sk = key_scale(p, row_sumsq(kr), tok, h, ok);
     store8_i(sK + row * LDP, f0, scale_h8(kr, sk));
-    if constexpr (MODE == SM_GLA)
+    if constexpr (GLA)
       *reinterpret_cast<f16x8*>(sV + row * LDP + f0) = scale_h8(vr, beta_eps(p, tok, h, ok));
   }
   if (wave == 0) {
     const bool ok = lane < nval;
     const int64_t tk = tok0 + lane;
-    const float gt = (MODE == SM_GLA && ok) ? g_at(p, tk, h) : 0.f;
+    const float gt = (GLA && ok) ? g_at(p, tk, h) : 0.f;
     const float G = scan64(gt);
     const float Gk = scan64((ok && has_gk(p)) ? (p.fused ? gt : gk_at(p, tk, h)) : 0.f);
     SC(SC_G, lane) = G;
     SC(SC_GK, lane) = Gk;
-    SC(SC_AL, lane) = (MODE == SM_GLA && ok) ? alpha_at(p, tk, h) : 0.f;
+    SC(SC_AL, lane) = (GLA && ok) ? alpha_at(p, tk, h) : 0.f;
   }
   if (NORM && tid < D) {
     float wv;
@@ -739,12 +744,17 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
     float ss = 0.f;
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt) {
-      const bf16x4 x = tok_ok ? *reinterpret_cast<const bf16x4*>(qr + 16 * nt) : bf16x4{};
+      if (MODE == SM_DQ && p.rhs32) {
+        Q[nt] = tok_ok ? *reinterpret_cast<const f32x4*>(p.rhs32 + ((int64_t)(tok0 + tb) * H + h) * D +
+                                                         4 * q4 + 16 * nt)
+                       : f32x4{0.f, 0.f, 0.f, 0.f};
+      } else {
+        const bf16x4 x = tok_ok ? *reinterpret_cast<const bf16x4*>(qr + 16 * nt) : bf16x4{};
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        Q[nt][v] = (float)x[v];
-        ss += Q[nt][v] * Q[nt][v];
+        for (int v = 0; v < 4; ++v) Q[nt][v] = (float)x[v];
       }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) ss += Q[nt][v] * Q[nt][v];
     }
     ss += __shfl_xor(ss, 16, 64);
     ss += __shfl_xor(ss, 32, 64);
@@ -847,7 +857,8 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
         cross += __shfl_xor(cross, 32, 64);
         const float e = fast_exp(GkT);
         f = sqrtf(fmaxf(e * e * hn + 2.f * e * cross + SC(SC_G2, tb), 0.f));
-        if (MODE == SM_X && tok_ok && q4 == 0) p.fro[(int64_t)(tok0 + tb) * H + h] = f;
+        if ((MODE == SM_X || MODE == SM_GLA_SAVE) && tok_ok && q4 == 0)
+          p.fro[(int64_t)(tok0 + tb) * H + h] = f;
       }
       lam = p.ridge_ratio * f;
       const float inv = 1.0f / (2.f * lam + f);
@@ -972,17 +983,23 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
         const int64_t ro = ((int64_t)(tok0 + tb) * H + h) * D + 4 * q4;
 #pragma unroll
         for (int nt = 0; nt < 8; ++nt) {
-          if constexpr (MODE == SM_X) {
+          if constexpr (MODE == SM_X || MODE == SM_GLA_SAVE) {
             bf16x4 y;
 #pragma unroll
             for (int v = 0; v < 4; ++v) y[v] = (bf16)X[nt][v];
-            *reinterpret_cast<bf16x4*>(p.o + ro + 16 * nt) = y;
+            *reinterpret_cast<bf16x4*>((MODE == SM_X ? p.o : p.xs) + ro + 16 * nt) = y;
           } else {
-            *reinterpret_cast<f32x4*>(p.xo32 + ro + 16 * nt) = X[nt];
+            f32x4 y = X[nt];
+            if (p.xo32_acc) {
+              const f32x4 o0 = *reinterpret_cast<const f32x4*>(p.xo32 + ro + 16 * nt);
+#pragma unroll
+              for (int v = 0; v < 4; ++v) y[v] += o0[v];
+            }
+            *reinterpret_cast<f32x4*>(p.xo32 + ro + 16 * nt) = y;
           }
         }
       }
-      return;
+      if constexpr (!GLA) return;
     }
     // alpha blend
     const float al = SC(SC_AL, tb);
@@ -1276,9 +1293,10 @@ struct Bwd {
   const float* fro;       // [tokens][H]
   float* e;               // [nblk][H][D][D] fp32 tile-major: E_c, then Dn_c
   float* gam;             // [nblk][H] block totals of gk
-  float* dk;              // [tokens][H][D]
+  float* dk;              // [tokens][H][D] (added to what it holds when dk_acc)
   float* dgk;             // [tokens][H]
-  int bp_lambda;
+  float* dq_out;          // null, or [tokens][H][D] that dq is added to
+  int bp_lambda, dk_acc;
 };
 
 struct Blk { int s_id, lb, tok0, nval; };
@@ -1565,6 +1583,18 @@ __global__ __launch_bounds__(NTHR, 1) void cheb_dk_kernel(Params p, Bwd w) {
     mx[1] = fmaxf(mx[1], fmaxf(absmax4(q0[pass]), absmax4(q1[pass])));
     const float a = lambda_weight(p, w, b, row, h, q0[pass], q1[pass], xr[pass]);
     if (l16 == 0) SC(CS_A, row) = a;
+    if (w.dq_out && ok) {                 // the caller's dq += this solve's dq
+      float* o = w.dq_out + ro;
+      const f32x4 o0 = *reinterpret_cast<const f32x4*>(o), o1 = *reinterpret_cast<const f32x4*>(o + 4);
+      f32x4 y0, y1;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        y0[v] = o0[v] + q0[pass][v];
+        y1[v] = o1[v] + q1[pass][v];
+      }
+      *reinterpret_cast<f32x4*>(o) = y0;
+      *reinterpret_cast<f32x4*>(o + 4) = y1;
+    }
   }
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
@@ -1751,6 +1781,11 @@ __global__ __launch_bounds__(NTHR, 1) void cheb_dk_kernel(Params p, Bwd w) {
       f32x4 y;
 #pragma unroll
       for (int v = 0; v < 4; ++v) y[v] = DK[nt][v] + L[nt][v] + ec * P[nt][v];
+      if (w.dk_acc) {
+        const f32x4 o0 = *reinterpret_cast<const f32x4*>(dko + 16 * nt);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) y[v] += o0[v];
+      }
       *reinterpret_cast<f32x4*>(dko + 16 * nt) = y;
     }
   }
@@ -1781,6 +1816,431 @@ __global__ __launch_bounds__(NTHR, 1) void cheb_dk_kernel(Params p, Bwd w) {
     float acc = 0.f;
     for (int t2 = lane; t2 < b.nval; ++t2) acc += SC(CS_DG, t2);
     w.dgk[(int64_t)(b.tok0 + lane) * H + h] = acc;
+  }
+}
+
+// ===========================================================================
+// The training backward of the GLA readout (chunk_simple_gla's backward)
+// ===========================================================================
+// o_t = scale (e^{G_t} S_c^T u_t + sum_{s<=t in block} e^{G_t-G_s} (u_t.k_s) v_s), with
+// u_t = q_t + alpha_t (x_t - q_t) the blended query, G the in-block cumsum of g and
+// S_c the block-start K x V state.  With dSn_c the gradient of S_{c+1} (the later
+// blocks' share, the same reverse scan as the solve's):
+//   E'_c = scale sum_t e^{G_t} u_t do_t^T,   dSn_c = E'_{c+1} + e^{Gam_{c+1}} dSn_{c+1}
+//   du_t = scale (e^{G_t} S_c do_t + sum_{s<=t} e^{G_t-G_s} (do_t.v_s) k_s)
+//   dk_s = scale sum_{t>=s} e^{G_t-G_s} (do_t.v_s) u_t + e^{Gam-G_s} dSn v_s
+//   dv_s = scale sum_{t>=s} e^{G_t-G_s} (u_t.k_s) do_t + e^{Gam-G_s} dSn^T k_s
+//   dL/dG_t = u_t.du_t - k_t.dk_t (+ <dSn, S_{c+1}> at the block's last token)
+// and dg is its in-block reverse cumsum; the blend gives dx = alpha du,
+// dq = (1 - alpha) du, dalpha = du.(x - q).
+struct GlaBwd {
+  const bf16* q; const bf16* x; const bf16* v; const bf16* dout;   // [tokens][H][D]
+  const void* alpha; int alpha_dt;        // [tokens][H]
+  float* e; float* gam;                   // as Bwd
+  float* dx;                              // [tokens][H][D]: alpha du (the solve's dx)
+  float* dq; float* dk; float* dv;        // [tokens][H][D]
+  float* dalpha; float* dg;               // [tokens][H]
+  float scale;
+  int solve;                              // 0: num_iter == 0 (u = q, no x, alpha unused)
+};
+
+__device__ __forceinline__ float gla_alpha(const GlaBwd& w, int64_t i) {
+  return w.solve ? ldsc(w.alpha, i, w.alpha_dt) : 0.f;
+}
+
+// E'_c of block gb (tile-major, row-major K x V) and the block's g total
+constexpr int GE_OFF_U = 0, GE_OFF_DO = SZ_K, GE_OFF_SC = 2 * SZ_K;
+constexpr int GE_SMEM = GE_OFF_SC + CB * 4 + 16 * 4;
+__global__ __launch_bounds__(NTHR, 2) void gla_e_kernel(Params p, GlaBwd w) {
+  __shared__ __align__(16) unsigned char smem[GE_SMEM];
+  f16* sU = reinterpret_cast<f16*>(smem + GE_OFF_U);
+  f16* sDo = reinterpret_cast<f16*>(smem + GE_OFF_DO);
+  float* sG = reinterpret_cast<float*>(smem + GE_OFF_SC);
+  float* mslot = sG + CB;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q4 = lane >> 4, l16 = lane & 15;
+  const int gb = blockIdx.x, h = blockIdx.y, H = p.H;
+  const Blk b = block_of(p, gb);
+  if (b.nval <= 0) return;
+  if (wave == 0) {
+    const bool ok = lane < b.nval;
+    const float G = scan64(ok ? ldsc(p.g, (int64_t)(b.tok0 + lane) * H + h, p.g_dt) : 0.f);
+    sG[lane] = G;
+    if (lane == b.nval - 1) w.gam[(int64_t)gb * H + h] = G;
+  }
+  lds_barrier();
+  // rows: e^{G_t} scale u_t and do_t (fp32), then scaled into fp16
+  f32x4 u0[CB / 16], u1[CB / 16];
+  bf16x8 dr[CB / 16];
+  float mx[2] = {0.f, 0.f};
+#pragma unroll
+  for (int pass = 0; pass < CB / 16; ++pass) {
+    const int row = pass * 16 + (tid >> 4), f0 = (tid & 15) * 8;
+    const bool ok = row < b.nval;
+    const int64_t ti = (int64_t)(b.tok0 + row) * H + h, ro = ti * D + f0;
+    const bf16x8 qr = ok ? *reinterpret_cast<const bf16x8*>(w.q + ro) : bf16x8{};
+    const bf16x8 xr = (ok && w.solve) ? *reinterpret_cast<const bf16x8*>(w.x + ro) : bf16x8{};
+    dr[pass] = ok ? *reinterpret_cast<const bf16x8*>(w.dout + ro) : bf16x8{};
+    const float al = ok ? gla_alpha(w, ti) : 0.f;
+    const float eg = ok ? w.scale * fast_exp(sG[row]) : 0.f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      u0[pass][v] = eg * ((float)qr[v] + al * ((float)xr[v] - (float)qr[v]));
+      u1[pass][v] = eg * ((float)qr[4 + v] + al * ((float)xr[4 + v] - (float)qr[4 + v]));
+    }
+    mx[0] = fmaxf(mx[0], fmaxf(absmax4(u0[pass]), absmax4(u1[pass])));
+    mx[1] = fmaxf(mx[1], absmax8(dr[pass]));
+  }
+  block_max(mx, mslot, wave, lane);
+  const float su = pow2_scale(mx[0]), sd = pow2_scale(mx[1]);
+#pragma unroll
+  for (int pass = 0; pass < CB / 16; ++pass) {
+    const int row = pass * 16 + (tid >> 4), f0 = (tid & 15) * 8;
+    store8_i(sU + row * LDP, f0, h8_of(u0[pass], u1[pass], su));
+    store8_i(sDo + row * LDP, f0, scale_h8(dr[pass], sd));
+  }
+  lds_barrier();
+  const float un = 1.f / (su * sd);
+  float* eo = w.e + ((int64_t)gb * H + h) * D * D;
+  // wave w: E'^T tile rows (V) 2w, 2w+1 by all 8 tile columns (K); the lane's 4
+  // values are 4 consecutive V columns of one K row of E'
+#pragma unroll
+  for (int ir = 0; ir < 2; ++ir) {
+    const int jt = 2 * wave + ir;
+    f32x4 E[8];
+#pragma unroll
+    for (int it = 0; it < 8; ++it) E[it] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int jk = 0; jk < 2; ++jk) {
+      const f16x8 ad = frag_t_i(sDo, LDP, 32 * jk, 16 * jt, lane);
+#pragma unroll
+      for (int it = 0; it < 8; ++it) E[it] = mfma16h(ad, frag_t_i(sU, LDP, 32 * jk, 16 * it, lane), E[it]);
+    }
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      f32x4 y;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) y[v] = un * E[it][v];
+      *reinterpret_cast<f32x4*>(eo + blk_index(16 * it + l16, 16 * jt + 4 * q4)) = y;
+    }
+  }
+}
+
+constexpr int GB_OFF_K = 0, GB_OFF_V = SZ_K, GB_OFF_DO = 2 * SZ_K, GB_OFF_U = 3 * SZ_K;
+constexpr int GB_OFF_S = 4 * SZ_K, GB_OFF_DS = GB_OFF_S + SZ_H, GB_OFF_SC = GB_OFF_DS + SZ_H;
+enum { GS_G, GS_DG, NGS };
+constexpr int GB_SMEM = GB_OFF_SC + NGS * CB * 4 + 32 * 4;
+static_assert(GB_SMEM <= 160 * 1024, "LDS budget");
+
+// du (-> dx, dq, dalpha), dk, dv, dg of block gb (see the section comment)
+__global__ __launch_bounds__(NTHR, 1) void gla_bwd_kernel(Params p, GlaBwd w) {
+  __shared__ __align__(16) unsigned char smem[GB_SMEM];
+  f16* sK = reinterpret_cast<f16*>(smem + GB_OFF_K);
+  f16* sV = reinterpret_cast<f16*>(smem + GB_OFF_V);
+  f16* sDo = reinterpret_cast<f16*>(smem + GB_OFF_DO);
+  f16* sU = reinterpret_cast<f16*>(smem + GB_OFF_U);
+  f16* sS = reinterpret_cast<f16*>(smem + GB_OFF_S);      // S_c^T: rows V, columns K
+  f16* sDS = reinterpret_cast<f16*>(smem + GB_OFF_DS);    // dSn: rows K, columns V
+  float* sc = reinterpret_cast<float*>(smem + GB_OFF_SC);
+  float* red = sc + NGS * CB;            // 8 floats of cross-wave sums
+  float* mslot = red + 8;                // 12 floats for block_max
+  auto SC = [&](int slot, int t) -> float& { return sc[slot * CB + t]; };
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q4 = lane >> 4, l16 = lane & 15;
+  const int gb = blockIdx.x, h = blockIdx.y, H = p.H;
+  const Blk b = block_of(p, gb);
+  if (b.nval <= 0) return;
+  const int64_t DD = (int64_t)D * D;
+
+  // S_c (as the solve forms it: zero-start block state + decayed segment start)
+  {
+    const int64_t so = ((int64_t)b.s_id * H + h) * DD;
+    const int64_t bso = ((int64_t)gb * H + h) * DD;
+    StateLd sst;
+    solve::state_issue_b<false>(sst, b.lb > 0 ? p.ws_sb + bso : nullptr, tid);
+    const float off_g = p.ws_boff[((int64_t)gb * H + h) * 2 + 1];
+    solve::state_issue_s<false>(sst, (b.lb == 0 || off_g > solve::SEG_STATE_DROP) ? p.ws_s0 + so : nullptr, tid);
+    solve::state_store<false>(sS, sst, fast_exp(off_g), tid);
+  }
+  if (wave == 0) {
+    const bool ok = lane < b.nval;
+    SC(GS_G, lane) = scan64(ok ? ldsc(p.g, (int64_t)(b.tok0 + lane) * H + h, p.g_dt) : 0.f);
+  }
+  lds_barrier();
+  // rows k, v (fp16 as given), do and u (scaled); dSn (scaled) and <dSn, S_c>
+  bf16x8 kr[CB / 16], vr[CB / 16], dr[CB / 16];
+  f32x4 u0[CB / 16], u1[CB / 16];
+  const float* dn = w.e + ((int64_t)gb * H + h) * DD;
+  const int drw = tid >> 1, dc0 = (tid & 1) * 64;
+  f32x4 dsv[16];
+  float mx[3] = {0.f, 0.f, 0.f};          // max |do|, |u|, |dSn|
+#pragma unroll
+  for (int pass = 0; pass < CB / 16; ++pass) {
+    const int row = pass * 16 + (tid >> 4), f0 = (tid & 15) * 8;
+    const bool ok = row < b.nval;
+    const int64_t ti = (int64_t)(b.tok0 + row) * H + h, ro = ti * D + f0;
+    kr[pass] = ok ? *reinterpret_cast<const bf16x8*>(p.k + (int64_t)(b.tok0 + row) * p.kv_ts + h * D + f0) : bf16x8{};
+    vr[pass] = ok ? *reinterpret_cast<const bf16x8*>(w.v + ro) : bf16x8{};
+    dr[pass] = ok ? *reinterpret_cast<const bf16x8*>(w.dout + ro) : bf16x8{};
+    const bf16x8 qr = ok ? *reinterpret_cast<const bf16x8*>(w.q + ro) : bf16x8{};
+    const bf16x8 xr = (ok && w.solve) ? *reinterpret_cast<const bf16x8*>(w.x + ro) : bf16x8{};
+    const float al = ok ? gla_alpha(w, ti) : 0.f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      u0[pass][v] = (float)qr[v] + al * ((float)xr[v] - (float)qr[v]);
+      u1[pass][v] = (float)qr[4 + v] + al * ((float)xr[4 + v] - (float)qr[4 + v]);
+    }
+    mx[0] = fmaxf(mx[0], absmax8(dr[pass]));
+    mx[1] = fmaxf(mx[1], fmaxf(absmax4(u0[pass]), absmax4(u1[pass])));
+  }
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    dsv[j] = *reinterpret_cast<const f32x4*>(dn + blk_index(drw, dc0 + 4 * j));
+    mx[2] = fmaxf(mx[2], absmax4(dsv[j]));
+  }
+  block_max(mx, mslot, wave, lane);
+  const float sdo = pow2_scale(mx[0]), su = pow2_scale(mx[1]), sds = pow2_scale(mx[2]);
+#pragma unroll
+  for (int pass = 0; pass < CB / 16; ++pass) {
+    const int row = pass * 16 + (tid >> 4), f0 = (tid & 15) * 8;
+    store8_i(sK + row * LDP, f0, scale_h8(kr[pass], 1.f));
+    store8_i(sV + row * LDP, f0, scale_h8(vr[pass], 1.f));
+    store8_i(sDo + row * LDP, f0, scale_h8(dr[pass], sdo));
+    store8_i(sU + row * LDP, f0, h8_of(u0[pass], u1[pass], su));
+  }
+  float dss = 0.f;                        // <dSn, S_c> over this thread's elements
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int c = dc0 + 4 * j + v;      // V index; S_c^T[c][drw] in sS
+      dss += dsv[j][v] * (float)sS[c * LDP + icol(drw)];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    store8_i(sDS + drw * LDP, dc0 + 8 * j, h8_of(dsv[2 * j], dsv[2 * j + 1], sds));
+  dss = wave_sum(dss);
+  if (lane == 0) red[wave] = dss;
+  lds_barrier();
+
+  const int s = 16 * wave + l16;          // this lane's token / key column
+  const bool s_ok = s < b.nval;
+  const float Gs = SC(GS_G, s), Gam = SC(GS_G, b.nval - 1);
+  const float ec = fast_exp(Gam - Gs), egs = fast_exp(Gs);
+  const int64_t ti = (int64_t)(b.tok0 + s) * H + h;
+  const int64_t ro = ti * D + 4 * q4;     // + 16 nt: features 16 nt + 4 q4 .. +3
+  float dG = 0.f;
+
+  // ---- du (rows f = K, column t = s) -------------------------------------
+  {
+    f32x4 DQ[8], DI[8];
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      DQ[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      DI[nt] = DQ[nt];
+    }
+    // S_c do_t: A = S_c rows (K) over V, read transposed from S_c^T
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const f16x8 bd = frag_i(sDo, LDP, 16 * wave, 32 * ks, lane);
+#pragma unroll
+      for (int nt = 0; nt < 8; ++nt) DQ[nt] = mfma16h(frag_t_i(sS, LDP, 32 * ks, 16 * nt, lane), bd, DQ[nt]);
+    }
+    // P[j][t] = e^{G_t-G_j} (do_t.v_j), j <= t: rows j over the block, column t
+    f16x8 pb[2];
+    {
+      f32x4 P[4];
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) P[jt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const f16x8 bd = frag_i(sDo, LDP, 16 * wave, 32 * ks, lane);
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt) P[jt] = mfma16h(frag_i(sV, LDP, 16 * jt, 32 * ks, lane), bd, P[jt]);
+      }
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) {
+        const f32x4 gj = *reinterpret_cast<const f32x4*>(&SC(GS_G, 16 * jt + 4 * q4));
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int j = 16 * jt + 4 * q4 + v;
+          P[jt][v] = (j <= s && j < b.nval) ? P[jt][v] * fast_exp(Gs - gj[v]) : 0.f;
+        }
+      }
+      pb[0] = h8(P[0], P[1]);
+      pb[1] = h8(P[2], P[3]);
+    }
+#pragma unroll
+    for (int jk = 0; jk < 2; ++jk)
+#pragma unroll
+      for (int nt = 0; nt < 8; ++nt) DI[nt] = mfma16h(frag_t_i(sK, LDP, 32 * jk, 16 * nt, lane), pb[jk], DI[nt]);
+    // du = scale (e^{G_t} DQ + DI) / sdo; dx, dq, dalpha and u.du
+    const float cu = w.scale / sdo;
+    const float al = s_ok ? gla_alpha(w, ti) : 0.f;
+    float dal = 0.f, udu = 0.f;
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      const bf16x4 qv = s_ok ? *reinterpret_cast<const bf16x4*>(w.q + ro + 16 * nt) : bf16x4{};
+      const bf16x4 xv = (s_ok && w.solve) ? *reinterpret_cast<const bf16x4*>(w.x + ro + 16 * nt) : bf16x4{};
+      f32x4 du, dqo, dxo;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        du[v] = cu * (egs * DQ[nt][v] + DI[nt][v]);
+        const float qf = (float)qv[v], xf = (float)xv[v];
+        dal += du[v] * (xf - qf);
+        udu += du[v] * (qf + al * (xf - qf));
+        dqo[v] = (1.f - al) * du[v];
+        dxo[v] = al * du[v];
+      }
+      if (s_ok) {
+        *reinterpret_cast<f32x4*>(w.dq + ro + 16 * nt) = dqo;
+        if (w.solve) *reinterpret_cast<f32x4*>(w.dx + ro + 16 * nt) = dxo;
+      }
+    }
+    dal += __shfl_xor(dal, 16, 64);
+    dal += __shfl_xor(dal, 32, 64);
+    udu += __shfl_xor(udu, 16, 64);
+    udu += __shfl_xor(udu, 32, 64);
+    if (s_ok && q4 == 0 && w.solve) w.dalpha[ti] = dal;
+    dG += udu;
+  }
+  // ---- dk (rows f = K, column s) --------------------------------------------
+  float kdkx = 0.f;                       // k_s . (dSn v_s) e^{Gam-G_s}
+  {
+    f32x4 DK[8], DX[8];
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      DK[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      DX[nt] = DK[nt];
+    }
+    // R[t][s] = e^{G_t-G_s} (do_t.v_s), t >= s
+    f16x8 rb[2];
+    {
+      f32x4 R[4];
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) R[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const f16x8 bv = frag_i(sV, LDP, 16 * wave, 32 * ks, lane);
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) R[tt] = mfma16h(frag_i(sDo, LDP, 16 * tt, 32 * ks, lane), bv, R[tt]);
+      }
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        const f32x4 gt = *reinterpret_cast<const f32x4*>(&SC(GS_G, 16 * tt + 4 * q4));
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int t = 16 * tt + 4 * q4 + v;
+          R[tt][v] = (t >= s && t < b.nval) ? R[tt][v] * fast_exp(gt[v] - Gs) : 0.f;
+        }
+      }
+      rb[0] = h8(R[0], R[1]);
+      rb[1] = h8(R[2], R[3]);
+    }
+#pragma unroll
+    for (int jk = 0; jk < 2; ++jk)
+#pragma unroll
+      for (int nt = 0; nt < 8; ++nt) DK[nt] = mfma16h(frag_t_i(sU, LDP, 32 * jk, 16 * nt, lane), rb[jk], DK[nt]);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const f16x8 bv = frag_i(sV, LDP, 16 * wave, 32 * ks, lane);
+#pragma unroll
+      for (int nt = 0; nt < 8; ++nt) DX[nt] = mfma16h(frag_i(sDS, LDP, 16 * nt, 32 * ks, lane), bv, DX[nt]);
+    }
+    const float ci = w.scale / (su * sdo), cx = ec / sds;
+    float kdk = 0.f;
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      const f16x4 kk = *reinterpret_cast<const f16x4*>(sK + s * LDP + icol(16 * nt + 4 * q4));
+      f32x4 y;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float xpart = cx * DX[nt][v];
+        y[v] = ci * DK[nt][v] + xpart;
+        kdk += (float)kk[v] * y[v];
+        kdkx += (float)kk[v] * xpart;
+      }
+      if (s_ok) *reinterpret_cast<f32x4*>(w.dk + ro + 16 * nt) = y;
+    }
+    kdk += __shfl_xor(kdk, 16, 64);
+    kdk += __shfl_xor(kdk, 32, 64);
+    kdkx += __shfl_xor(kdkx, 16, 64);
+    kdkx += __shfl_xor(kdkx, 32, 64);
+    dG -= kdk;
+  }
+  // ---- dv (rows f = V, column s) --------------------------------------------
+  {
+    f32x4 DV[8], DX[8];
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      DV[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      DX[nt] = DV[nt];
+    }
+    // U[t][s] = e^{G_t-G_s} (u_t.k_s), t >= s
+    f16x8 ub[2];
+    {
+      f32x4 U[4];
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) U[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const f16x8 bk = frag_i(sK, LDP, 16 * wave, 32 * ks, lane);
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) U[tt] = mfma16h(frag_i(sU, LDP, 16 * tt, 32 * ks, lane), bk, U[tt]);
+      }
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        const f32x4 gt = *reinterpret_cast<const f32x4*>(&SC(GS_G, 16 * tt + 4 * q4));
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int t = 16 * tt + 4 * q4 + v;
+          U[tt][v] = (t >= s && t < b.nval) ? U[tt][v] * fast_exp(gt[v] - Gs) : 0.f;
+        }
+      }
+      ub[0] = h8(U[0], U[1]);
+      ub[1] = h8(U[2], U[3]);
+    }
+#pragma unroll
+    for (int jk = 0; jk < 2; ++jk)
+#pragma unroll
+      for (int nt = 0; nt < 8; ++nt) DV[nt] = mfma16h(frag_t_i(sDo, LDP, 32 * jk, 16 * nt, lane), ub[jk], DV[nt]);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const f16x8 bk = frag_i(sK, LDP, 16 * wave, 32 * ks, lane);
+#pragma unroll
+      for (int nt = 0; nt < 8; ++nt) DX[nt] = mfma16h(frag_t_i(sDS, LDP, 32 * ks, 16 * nt, lane), bk, DX[nt]);
+    }
+    const float ci = w.scale / (su * sdo), cx = ec / sds;
+    if (s_ok) {
+#pragma unroll
+      for (int nt = 0; nt < 8; ++nt) {
+        f32x4 y;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) y[v] = ci * DV[nt][v] + cx * DX[nt][v];
+        *reinterpret_cast<f32x4*>(w.dv + ro + 16 * nt) = y;
+      }
+    }
+  }
+  // ---- dg: dL/dG_t, the last token's <dSn, S_{c+1}>, the in-block reverse cumsum
+  float kx = s_ok ? kdkx : 0.f;
+#pragma unroll
+  for (int m = 1; m < 16; m <<= 1) kx += __shfl_xor(kx, m, 64);
+  if (lane == 0) red[4 + wave] = kx;
+  lds_barrier();
+  if (s_ok && q4 == 0) {
+    float d = dG;
+    if (s == b.nval - 1)
+      d += fast_exp(Gam) * (red[0] + red[1] + red[2] + red[3]) + red[4] + red[5] + red[6] + red[7];
+    SC(GS_DG, s) = d;
+  }
+  lds_barrier();
+  if (wave == 0 && lane < b.nval) {
+    float acc = 0.f;
+    for (int t2 = lane; t2 < b.nval; ++t2) acc += SC(GS_DG, t2);
+    w.dg[(int64_t)(b.tok0 + lane) * H + h] = acc;
   }
 }
 }  // namespace train
@@ -1895,7 +2355,7 @@ extern "C" int hmx_gka_cheb_bwd(const void* k, int64_t k_token_stride, const voi
   if (nseg_total == 0 || nblock_total == 0) return HMX_OK;
   p.fro = const_cast<float*>(fro);
   p.xo32 = dq;
-  train::Bwd w;
+  train::Bwd w{};
   w.x = static_cast<const bf16*>(x);
   w.dq = dq; w.fro = fro;
   w.e = static_cast<float*>(bwd_workspace);
@@ -1910,4 +2370,142 @@ extern "C" int hmx_gka_cheb_bwd(const void* k, int64_t k_token_stride, const voi
   hipLaunchKernelGGL(train::cheb_dscan_kernel, dim3(N * H, 16), dim3(256), 0, s, p, w);
   hipLaunchKernelGGL(train::cheb_dk_kernel, grid, dim3(NTHR), 0, s, p, w);
   return check_launch("hmx_gka_cheb_bwd");
+}
+
+// ---------------------------------------------------------------------------
+// The training GKA forward with its backward (gka_chebyshev_gla): the solve, the
+// alpha blend and the GLA readout; q, k, v [tokens][H][D] bf16 (contiguous, k and
+// v at H heads), no initial states, beta already applied by the layer.
+// ---------------------------------------------------------------------------
+namespace {
+int train_params(Params& p, const char* fn, const void* q, const void* k, const void* v,
+                 int32_t dtype, const void* alpha, int32_t alpha_dtype, const void* g,
+                 int32_t g_dtype, const void* gk, int32_t gk_dtype, const int32_t* seg_table,
+                 int32_t nseg_total, int32_t nblock_total, int32_t N, int32_t H, int32_t D_,
+                 int32_t num_iter, float ridge_ratio, float scale, void* workspace,
+                 size_t workspace_bytes) {
+  const int rc = cheb_params(p, fn, k, (int64_t)H * D, q, (int64_t)H * D, dtype, gk, gk_dtype,
+                             seg_table, nseg_total, nblock_total, N, H, D_, num_iter,
+                             ridge_ratio, workspace, workspace_bytes);
+  if (rc != HMX_OK) return rc;
+  HMX_REQUIRE(v && g && alpha && ((uintptr_t)v % 16) == 0, HMX_EINVAL,
+              "%s: v (16-byte aligned), g and alpha are required", fn);
+  HMX_REQUIRE(g_dtype >= 0 && g_dtype <= 2 && (!alpha || (alpha_dtype >= 0 && alpha_dtype <= 2)),
+              HMX_EUNSUPPORTED, "%s: gate dtype codes must be 0-2", fn);
+  p.v = static_cast<const bf16*>(v);
+  p.alpha = alpha; p.alpha_dt = alpha_dtype; p.g = g; p.g_dt = g_dtype;
+  p.scale = scale;
+  return HMX_OK;
+}
+}  // namespace
+
+extern "C" int hmx_gka_train_fwd(const void* q, const void* k, const void* v, int32_t dtype,
+                                 const void* alpha, int32_t alpha_dtype, const void* g,
+                                 int32_t g_dtype, const void* gk, int32_t gk_dtype, void* o,
+                                 void* x, float* fro, float* h_kk_final, float* h_kv_final,
+                                 const int32_t* seg_table, int32_t nseg_total,
+                                 int32_t nblock_total, int32_t N, int32_t H, int32_t D_,
+                                 int32_t num_iter, float ridge_ratio, float scale,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  Params p;
+  const int rc = train_params(p, "hmx_gka_train_fwd", q, k, v, dtype, alpha, alpha_dtype, g,
+                              g_dtype, gk, gk_dtype, seg_table, nseg_total, nblock_total, N, H,
+                              D_, num_iter, ridge_ratio, scale, workspace, workspace_bytes);
+  if (rc != HMX_OK) return rc;
+  HMX_REQUIRE(o && h_kv_final && ((uintptr_t)o % 16) == 0 &&
+                  (num_iter == 0 || (x && fro && h_kk_final && ((uintptr_t)x % 16) == 0)),
+              HMX_EINVAL, "hmx_gka_train_fwd: o, h_kv_final (and with the solver x, fro, "
+                          "h_kk_final) are required, 16-byte aligned");
+  if (nseg_total == 0) return HMX_OK;
+  p.o = static_cast<bf16*>(o);
+  p.xs = static_cast<bf16*>(x);
+  p.fro = fro;
+  p.hkk.out = num_iter > 0 ? h_kk_final : nullptr;
+  p.hkv.out = h_kv_final;
+  const bool solve_ = num_iter > 0;
+  hipStream_t s = (hipStream_t)stream;
+  if (solve_) hipLaunchKernelGGL((walk::gka_walk_kernel<true, false>), dim3(nseg_total, H), dim3(NTHR), 0, s, p);
+  else hipLaunchKernelGGL((walk::gka_walk_kernel<false, false>), dim3(nseg_total, H), dim3(NTHR), 0, s, p);
+  hipLaunchKernelGGL(gka_combine_kernel, dim3(N * H, 16), dim3(256), 0, s, p, (int)solve_);
+  if (nblock_total > 0) {
+    if (solve_)
+      hipLaunchKernelGGL((solve::gka_solve_kernel<true, false, solve::SM_GLA_SAVE>),
+                         dim3(nblock_total, H), dim3(NTHR), 0, s, p);
+    else
+      hipLaunchKernelGGL((solve::gka_solve_kernel<false, false>), dim3(nblock_total, H),
+                         dim3(NTHR), 0, s, p);
+  }
+  return check_launch("hmx_gka_train_fwd");
+}
+
+extern "C" size_t hmx_gka_train_bwd_workspace_bytes(int32_t nblock_total, int32_t H,
+                                                    int64_t tokens) {
+  return hmx_gka_cheb_bwd_workspace_bytes(nblock_total, H) +
+         2 * al256((size_t)tokens * H * D * sizeof(float));
+}
+
+extern "C" int hmx_gka_train_bwd(const void* q, const void* k, const void* v, int32_t dtype,
+                                 const void* alpha, int32_t alpha_dtype, const void* g,
+                                 int32_t g_dtype, const void* gk, int32_t gk_dtype,
+                                 const void* x, const float* fro, const void* dout, float* dq,
+                                 float* dk, float* dv, float* dalpha, float* dg, float* dgk,
+                                 const int32_t* seg_table, int32_t nseg_total,
+                                 int32_t nblock_total, int32_t N, int32_t H, int32_t D_,
+                                 int64_t tokens, int32_t num_iter, float ridge_ratio, float scale,
+                                 int32_t bp_lambda, void* fwd_workspace,
+                                 size_t fwd_workspace_bytes, void* bwd_workspace,
+                                 size_t bwd_workspace_bytes, void* stream) {
+  Params p;
+  const int rc = train_params(p, "hmx_gka_train_bwd", q, k, v, dtype, alpha, alpha_dtype, g,
+                              g_dtype, gk, gk_dtype, seg_table, nseg_total, nblock_total, N, H,
+                              D_, num_iter, ridge_ratio, scale, fwd_workspace,
+                              fwd_workspace_bytes);
+  if (rc != HMX_OK) return rc;
+  const bool solve_ = num_iter > 0;
+  HMX_REQUIRE(dout && dq && dk && dv && dg && tokens >= 0 &&
+                  (!solve_ || (x && fro && dalpha && (!gk || dgk))) &&
+                  (((uintptr_t)dout | (uintptr_t)dq | (uintptr_t)dk | (uintptr_t)dv |
+                    (uintptr_t)x) % 16) == 0,
+              HMX_EINVAL, "hmx_gka_train_bwd: dout, dq, dk, dv, dg (and with the solver x, fro, "
+                          "dalpha, dgk) are required, 16-byte aligned");
+  const size_t need = hmx_gka_train_bwd_workspace_bytes(nblock_total, H, tokens);
+  HMX_REQUIRE(nblock_total == 0 || (bwd_workspace && bwd_workspace_bytes >= need), HMX_EINVAL,
+              "hmx_gka_train_bwd: backward workspace of %zu bytes needed, %zu given", need,
+              bwd_workspace_bytes);
+  if (nseg_total == 0 || nblock_total == 0) return HMX_OK;
+  char* bw = static_cast<char*>(bwd_workspace);
+  const size_t e_bytes = al256((size_t)nblock_total * H * D * D * sizeof(float));
+  const size_t cb_bytes = hmx_gka_cheb_bwd_workspace_bytes(nblock_total, H);
+  train::GlaBwd gw{};
+  gw.q = static_cast<const bf16*>(q); gw.x = static_cast<const bf16*>(x);
+  gw.v = static_cast<const bf16*>(v); gw.dout = static_cast<const bf16*>(dout);
+  gw.alpha = alpha; gw.alpha_dt = alpha_dtype;
+  gw.e = reinterpret_cast<float*>(bw);
+  gw.gam = reinterpret_cast<float*>(bw + e_bytes);
+  gw.dx = reinterpret_cast<float*>(bw + cb_bytes);
+  float* dq_cheb = reinterpret_cast<float*>(bw + cb_bytes + al256((size_t)tokens * H * D * sizeof(float)));
+  gw.dq = dq; gw.dk = dk; gw.dv = dv; gw.dalpha = dalpha; gw.dg = dg;
+  gw.scale = scale; gw.solve = solve_;
+  train::Bwd cw{};
+  cw.e = gw.e; cw.gam = gw.gam;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid(nblock_total, H), sgrid(N * H, 16);
+  hipLaunchKernelGGL(train::gla_e_kernel, grid, dim3(NTHR), 0, s, p, gw);
+  hipLaunchKernelGGL(train::cheb_dscan_kernel, sgrid, dim3(256), 0, s, p, cw);
+  hipLaunchKernelGGL(train::gla_bwd_kernel, grid, dim3(NTHR), 0, s, p, gw);
+  if (solve_) {
+    // the solve's backward on dx = alpha du: its dq is added to dq, its dk to dk
+    Params pc = p;
+    pc.rhs32 = gw.dx;
+    pc.fro = const_cast<float*>(fro);
+    pc.xo32 = dq_cheb; pc.xo32_acc = 0;
+    cw.x = gw.x; cw.dq = dq_cheb; cw.fro = fro;
+    cw.dk = dk; cw.dk_acc = 1; cw.dgk = gk ? dgk : nullptr; cw.dq_out = dq;
+    cw.bp_lambda = bp_lambda;
+    hipLaunchKernelGGL((solve::gka_solve_kernel<true, false, solve::SM_DQ>), grid, dim3(NTHR), 0, s, pc);
+    hipLaunchKernelGGL(train::cheb_e_kernel, grid, dim3(NTHR), 0, s, pc, cw);
+    hipLaunchKernelGGL(train::cheb_dscan_kernel, sgrid, dim3(256), 0, s, pc, cw);
+    hipLaunchKernelGGL(train::cheb_dk_kernel, grid, dim3(NTHR), 0, s, pc, cw);
+  }
+  return check_launch("hmx_gka_train_bwd");
 }

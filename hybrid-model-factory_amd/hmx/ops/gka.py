@@ -321,12 +321,18 @@ def gka_chebyshev_gla(q, k, v, alpha, g, gk, gla_scale, ridge_strength: float = 
     already normalised and beta already applied to k and v by the layer
     (gka.py:477-490), no initial state.  ridge_strength is the ratio to |H_t|_F.
     Returns (o, kk_final [B,H,D,D] fp32 or None when num_iter == 0, kv_final).
-    Forward only: bp_lambda and chunk_size only concern the reference's backward
-    and its tiling."""
+    When a gradient is needed (grad mode on and an input requires it) the call runs
+    through GkaChebyshevGla (hmx.ops.gka_train), whose backward follows the
+    reference's (bp_lambda as there); chunk_size only tiles the reference's kernels."""
     if solver_type != "chebyshev":
         raise ValueError(f"Unknown GKA solver type: {solver_type}")
     if g is None:
         g = torch.zeros(q.shape[:3], dtype=torch.float32, device=q.device)
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad
+                                       for t in (q, k, v, alpha, g, gk)):
+        from .gka_train import GkaChebyshevGla
+        return GkaChebyshevGla.apply(q, k, v, alpha, g, gk, gla_scale, ridge_strength,
+                                     num_iter, bp_lambda)
     return _gka_prefill(q, k, v, alpha, g, gk, None, gla_scale, ridge_strength, num_iter,
                         None, None, True, None, False)
 

@@ -12,6 +12,13 @@ training/src/hmf/model/hybrid_zoo/layers/gated_kalmanet/ops/chebyshev/):
   from dL/dH_t = -dq_t x_t^T (- r (dq_t . x_t) H_t / |H_t|_F with bp_lambda); the
   gradient of h_kk_final is not propagated (the reference drops it, :638).
 - ``latent_chebyshev`` — gka_chebyshev_solve.py:74-104, the dispatcher over it.
+- ``GkaChebyshevGla`` — the whole training forward gka_chebyshev_gla
+  (gka_chebyshev_solve.py:107-164: the solve, the alpha blend, fla's
+  chunk_simple_gla) as one autograd function; ``hmx.gka_chebyshev_gla`` routes
+  through it when a gradient is needed.  Its backward runs the GLA readout's
+  backward (dq~, dk, dv, dg, then dx = alpha dq~, dalpha = dq~ . (x - q)) and the
+  solve's backward on dx, adding into dq and dk.  Gradients of the final states
+  are not propagated.
 
 Kernels (libhmx ``hmx_gka_cheb_fwd`` / ``hmx_gka_cheb_bwd``): the serving prefill's
 state walk and combine, and its solve kernel writing x and |H_t|_F instead of the
@@ -118,3 +125,79 @@ def latent_chebyshev(k, q, ridge_strength, num_iter, solver_type, bp_lambda, gk,
         raise ValueError(f"Unknown GKA solver type: {solver_type}")
     return ChebyshevIteration.apply(k, q, gk, num_iter, ridge_strength, bp_lambda, None,
                                     chunk_size)
+
+
+class GkaChebyshevGla(torch.autograd.Function):
+    """gka_chebyshev_solve.py:107-164 with its backward (see the module docstring).
+    apply(q, k, v, alpha, g, gk, gla_scale, ridge_strength, num_iter, bp_lambda,
+    _segment_chunks) -> (o, kk_final or None, kv_final)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, alpha, g, gk, gla_scale, ridge_strength, num_iter, bp_lambda,
+                _segment_chunks=None):
+        _check(k, q, gk)
+        if v.shape != q.shape or v.dtype != q.dtype:
+            raise ValueError(f"v must match q [B, T, H, 128] bf16, got {tuple(v.shape)} {v.dtype}")
+        for name, t in (("alpha", alpha), ("g", g)):
+            if tuple(t.shape) != tuple(q.shape[:3]):
+                raise ValueError(f"{name} must be [B, T, H] = {tuple(q.shape[:3])}, got "
+                                 f"{tuple(t.shape)}")
+        _lib.require_gpu(v, alpha, g)
+        B, T, H, D = q.shape
+        dev = q.device
+        q2, k2, v2 = q.contiguous(), k.contiguous(), v.contiguous()
+        a2, g2 = alpha.contiguous(), g.contiguous()
+        gk2 = None if gk is None else gk.contiguous()
+        n = int(num_iter)
+        rows, nblk = _segment_table(_lib.PLAN_GKA, [(i * T, i * T + T) for i in range(B)],
+                                    B * T, H, dev, _segment_chunks)
+        seg = _device_table(rows, dev)
+        lib = _lib.load()
+        ws = torch.empty(max(int(lib.hmx_gka_chunk_workspace_bytes(len(rows), nblk, B, H)), 16),
+                         dtype=torch.uint8, device=dev)
+        o = torch.empty_like(q2)
+        x = torch.empty_like(q2) if n > 0 else None
+        fro = torch.empty(B, T, H, dtype=torch.float32, device=dev) if n > 0 else None
+        hkk = torch.empty(B, H, D, D, dtype=torch.float32, device=dev) if n > 0 else None
+        hkv = torch.empty(B, H, D, D, dtype=torch.float32, device=dev)
+        _lib.call("hmx_gka_train_fwd", _lib.ptr(q2), _lib.ptr(k2), _lib.ptr(v2),
+                  _lib.dtype_code(q2), _lib.ptr(a2), _lib.dtype_code(a2), _lib.ptr(g2),
+                  _lib.dtype_code(g2), _lib.ptr(gk2), 0 if gk2 is None else _lib.dtype_code(gk2),
+                  _lib.ptr(o), _lib.ptr(x), _lib.ptr(fro), _lib.ptr(hkk), _lib.ptr(hkv),
+                  _lib.ptr(seg), len(rows), nblk, B, H, D, n, float(ridge_strength),
+                  float(gla_scale), _lib.ptr(ws), ws.numel(), _lib.stream_of(q2))
+        ctx.save_for_backward(q2, k2, v2, a2, g2, gk2, x, fro, ws, seg)
+        ctx.meta = (len(rows), nblk, n, float(ridge_strength), float(gla_scale), bool(bp_lambda),
+                    (q.dtype, k.dtype, v.dtype, alpha.dtype, g.dtype,
+                     None if gk is None else gk.dtype))
+        return o, hkk, hkv
+
+    @staticmethod
+    def backward(ctx, do, d_kk=None, d_kv=None):
+        q, k, v, alpha, g, gk, x, fro, ws, seg = ctx.saved_tensors
+        nrows, nblk, n, ridge, scale, bp_lambda, dts = ctx.meta
+        B, T, H, D = q.shape
+        dev = q.device
+        if do is None:
+            do = torch.zeros_like(q)
+        do2 = do.to(torch.bfloat16).contiguous()
+        f32 = dict(dtype=torch.float32, device=dev)
+        dq, dk, dv = (torch.empty(B, T, H, D, **f32) for _ in range(3))
+        dg = torch.empty(B, T, H, **f32)
+        dalpha = torch.empty(B, T, H, **f32) if n > 0 else None
+        dgk = torch.empty(B, T, H, **f32) if (n > 0 and gk is not None) else None
+        lib = _lib.load()
+        bws = torch.empty(max(int(lib.hmx_gka_train_bwd_workspace_bytes(nblk, H, B * T)), 16),
+                          dtype=torch.uint8, device=dev)
+        _lib.call("hmx_gka_train_bwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.dtype_code(q),
+                  _lib.ptr(alpha), _lib.dtype_code(alpha), _lib.ptr(g), _lib.dtype_code(g),
+                  _lib.ptr(gk), 0 if gk is None else _lib.dtype_code(gk), _lib.ptr(x),
+                  _lib.ptr(fro), _lib.ptr(do2), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv),
+                  _lib.ptr(dalpha), _lib.ptr(dg), _lib.ptr(dgk), _lib.ptr(seg), nrows, nblk, B,
+                  H, D, B * T, n, ridge, scale, int(bp_lambda), _lib.ptr(ws), ws.numel(),
+                  _lib.ptr(bws), bws.numel(), _lib.stream_of(q))
+        cast = lambda t, dt: None if (t is None or dt is None) else t.to(dt)
+        if gk is None or n == 0:
+            dgk = None
+        return (cast(dq, dts[0]), cast(dk, dts[1]), cast(dv, dts[2]), cast(dalpha, dts[3]),
+                cast(dg, dts[4]), cast(dgk, dts[5]), None, None, None, None, None)

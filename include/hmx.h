@@ -396,6 +396,49 @@ int hmx_gka_cheb_bwd(const void* k, int64_t k_token_stride, const void* x, const
                      void* bwd_workspace, size_t bwd_workspace_bytes, void* stream);
 size_t hmx_gka_cheb_bwd_workspace_bytes(int32_t nblock_total, int32_t H);
 
+/* hmx_gka_train_fwd: the training GKA forward in one pass: the Chebyshev solve
+ * (as hmx_gka_cheb_fwd), the blend u = q + alpha (x - q) and the GLA readout
+ * o_t = scale S_t^T u_t, S_t = e^{g_t} S_{t-1} + k_t v_t^T from zero.  q, k, v
+ * [tokens][H][D] bf16 contiguous (k, v at H heads, beta applied by the caller);
+ * alpha, g [tokens][H] (f32/bf16/f16), gk [tokens][H] or NULL.  Writes o
+ * [tokens][H][D] bf16, h_kv_final [N][H][D][D] f32 and, when num_iter > 0, x
+ * [tokens][H][D] bf16, fro [tokens][H] f32 and h_kk_final [N][H][D][D] f32 for the
+ * backward.  The workspace (hmx_gka_chunk_workspace_bytes) keeps the block-start
+ * states for the backward.
+ * Replaces: gka_chebyshev_gla
+ *   training/.../ops/chebyshev/gka_chebyshev_solve.py:107-164 (ChebyshevIteration,
+ *   the blend, and fla's chunk_simple_gla).
+ */
+int hmx_gka_train_fwd(const void* q, const void* k, const void* v, int32_t dtype,
+                      const void* alpha, int32_t alpha_dtype, const void* g, int32_t g_dtype,
+                      const void* gk, int32_t gk_dtype, void* o, void* x, float* fro,
+                      float* h_kk_final, float* h_kv_final, const int32_t* seg_table,
+                      int32_t nseg_total, int32_t nblock_total, int32_t N, int32_t H, int32_t D,
+                      int32_t num_iter, float ridge_ratio, float scale, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+/* hmx_gka_train_bwd: the backward of hmx_gka_train_fwd (same inputs, its x, fro and
+ * workspace) for dout [tokens][H][D] bf16: writes dq, dk, dv [tokens][H][D] f32, dg
+ * [tokens][H] f32 and, when num_iter > 0, dalpha and (with gk) dgk [tokens][H] f32.
+ * The GLA readout's backward gives du, dk, dv, dg; dx = alpha du feeds the solve's
+ * backward (as hmx_gka_cheb_bwd) whose dq and dk are added.  Gradients of the
+ * final states are not taken.  bwd_workspace:
+ * hmx_gka_train_bwd_workspace_bytes(nblock_total, H, tokens) bytes.
+ * Replaces: the backward of gka_chebyshev_gla (ChebyshevIteration.backward,
+ *   chebyshev_iteration.py:606-688, torch's autograd of the blend at
+ *   gka_chebyshev_solve.py:156, and fla's chunk_simple_gla backward).
+ */
+int hmx_gka_train_bwd(const void* q, const void* k, const void* v, int32_t dtype,
+                      const void* alpha, int32_t alpha_dtype, const void* g, int32_t g_dtype,
+                      const void* gk, int32_t gk_dtype, const void* x, const float* fro,
+                      const void* dout, float* dq, float* dk, float* dv, float* dalpha,
+                      float* dg, float* dgk, const int32_t* seg_table, int32_t nseg_total,
+                      int32_t nblock_total, int32_t N, int32_t H, int32_t D, int64_t tokens,
+                      int32_t num_iter, float ridge_ratio, float scale, int32_t bp_lambda,
+                      void* fwd_workspace, size_t fwd_workspace_bytes, void* bwd_workspace,
+                      size_t bwd_workspace_bytes, void* stream);
+size_t hmx_gka_train_bwd_workspace_bytes(int32_t nblock_total, int32_t H, int64_t tokens);
+
 /*
  * Mamba2 SSD chunk scan forward, bf16 x/B/C/z/y, fp32 states, varlen via a
  * segment table of rows (n, bos, eos, c_start, c_end, seg_idx, first_seg, nseg)

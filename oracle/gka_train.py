@@ -101,3 +101,57 @@ def chebyshev_iteration_bwd(k, x, fro, gk, dx, num_iter=30, ridge_ratio=0.02, bp
     sur = (G * h_states(kk, gg, dtype)).sum()
     grads = torch.autograd.grad(sur, [kk] + ([gg] if gg is not None else []))
     return grads[0], dq, (grads[1] if gg is not None else None)
+
+
+# ---------------------------------------------------------------------------
+# The whole training forward gka_chebyshev_gla (gka_chebyshev_solve.py:107-164):
+# x = ChebyshevIteration(k, q, gk); u = q + alpha (x - q); o = chunk_simple_gla(u, k,
+# v, scale, g) of fla (un-vendored; o_t = scale S_t^T u_t with S_t = e^{g_t} S_{t-1}
+# + k_t v_t^T from zero).  Its backward is fla's GLA backward (the exact gradient,
+# taken here by autograd of the recurrence), torch's autograd of the blend, and
+# ChebyshevIteration.backward on dx = alpha du.
+# ---------------------------------------------------------------------------
+def gla(u, k, v, g, scale, dtype=DEFAULT):
+    """o [B,T,H,V] and the final state [B,H,K,V] of the GLA recurrence (autograd-able)."""
+    B, T, H, K = u.shape
+    S = torch.zeros(B, H, K, v.shape[-1], dtype=dtype)
+    out = []
+    for t in range(T):
+        S = S * torch.exp(g[:, t].to(dtype))[..., None, None] + k[:, t, :, :, None] * v[:, t, :, None, :]
+        out.append(scale * (S * u[:, t, :, :, None]).sum(-2))
+    return torch.stack(out, dim=1), S
+
+
+def gka_chebyshev_gla_fwd(q, k, v, alpha, g, gk, scale, ridge_ratio, num_iter, dtype=DEFAULT):
+    """(o, kk_final or None, kv_final, x or None, fro or None) in ``dtype``."""
+    q, k, v = q.to(dtype), k.to(dtype), v.to(dtype)
+    x = fro = hkk = None
+    u = q
+    if num_iter > 0:
+        x, fro, hkk = chebyshev_iteration_fwd(k, q, gk, num_iter, ridge_ratio, dtype)
+        u = q + alpha.to(dtype)[..., None] * (x - q)
+    o, hkv = gla(u, k, v, g, scale, dtype)
+    return o, hkk, hkv, x, fro
+
+
+def gka_chebyshev_gla_bwd(q, k, v, alpha, g, gk, scale, ridge_ratio, num_iter, bp_lambda, do,
+                          x=None, fro=None, dtype=DEFAULT):
+    """Gradients (dq, dk, dv, dalpha or None, dg, dgk or None) of sum(o * do), with
+    the solve's part as ChebyshevIteration.backward computes it, given the forward's
+    saved x and |H_t|_F."""
+    q, k, v, do = q.to(dtype), k.to(dtype), v.to(dtype), do.to(dtype)
+    u = q if num_iter == 0 else q + alpha.to(dtype)[..., None] * (x.to(dtype) - q)
+    uu = u.detach().requires_grad_(True)
+    kk = k.detach().requires_grad_(True)
+    vv = v.detach().requires_grad_(True)
+    gg = g.to(dtype).detach().requires_grad_(True)
+    o, _ = gla(uu, kk, vv, gg, scale, dtype)
+    du, dk, dv, dg = torch.autograd.grad((o * do).sum(), [uu, kk, vv, gg])
+    if num_iter == 0:
+        return du, dk, dv, None, dg, None
+    a = alpha.to(dtype)[..., None]
+    xd = x.to(dtype)
+    dalpha = (du * (xd - q)).sum(-1)
+    dk_c, dq_c, dgk = chebyshev_iteration_bwd(k, xd, fro, gk, a * du, num_iter, ridge_ratio,
+                                              bp_lambda, dtype)
+    return (1 - a) * du + dq_c, dk + dk_c, dv, dalpha, dg, dgk

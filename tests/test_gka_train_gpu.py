@@ -14,7 +14,7 @@ import pytest
 import torch
 
 import hmx
-from hmx.ops.gka_train import cheb_forward
+from hmx.ops.gka_train import GkaChebyshevGla, cheb_forward
 from oracle import gka_train as tr
 from util import STATE_REL, rel_err
 
@@ -115,3 +115,66 @@ def test_chebyshev_iteration_rejects(dev):
         hmx.ChebyshevIteration.apply(k.float(), q.float(), gk, 8, 0.02, True)
     with pytest.raises(ValueError):
         hmx.ChebyshevIteration.apply(k, q, gk[:, :5], 8, 0.02, True)
+
+
+GLA_CASES = [  # B, T, H, gated gk, num_iter, bp_lambda, blocks per segment
+    (2, 200, 2, True, 8, True, None),
+    (1, 130, 2, False, 8, False, None),
+    (1, 300, 2, True, 30, True, 1),
+    (1, 100, 2, True, 0, True, None),
+]
+
+
+@pytest.mark.parametrize("B,T,H,gated,num_iter,bp_lambda,seg", GLA_CASES)
+def test_gka_chebyshev_gla_backward_matches_oracle(dev, B, T, H, gated, num_iter, bp_lambda, seg):
+    """The training GKA forward (gka_chebyshev_solve.py:107-164) with its backward:
+    o and the final states against the oracle's forward, the six gradients against
+    the oracle's backward on this call's saved x and |H_t|_F."""
+    q, k, gk, _ = _inputs(B, T, H, 21, gated, dev)
+    g0 = torch.Generator().manual_seed(22)
+    v = torch.randn(B, T, H, D, generator=g0).bfloat16().to(dev)
+    alpha = torch.rand(B, T, H, generator=g0).to(dev)
+    g = (-0.1 * torch.rand(B, T, H, generator=g0)).to(dev)
+    do = torch.randn(B, T, H, D, generator=g0).bfloat16().to(dev)
+    ins = [None if t is None else t.clone().requires_grad_(True) for t in (q, k, v, alpha, g, gk)]
+    o, hkk, hkv = GkaChebyshevGla.apply(*ins, 0.3, 0.02, num_iter, bp_lambda, seg)
+    saved = o.grad_fn.saved_tensors
+    x_s, fro_s = saved[6], saved[7]
+    cpu = lambda t: None if t is None else t.detach().cpu()
+    o_r, hkk_r, hkv_r, _, _ = tr.gka_chebyshev_gla_fwd(*(cpu(t) for t in (q, k, v, alpha, g, gk)),
+                                                     0.3, 0.02, num_iter)
+    (o.float() * do.float()).sum().backward()
+    exp = tr.gka_chebyshev_gla_bwd(*(cpu(t) for t in (q, k, v, alpha, g, gk)), 0.3, 0.02,
+                                   num_iter, bp_lambda, do.cpu(), cpu(x_s), cpu(fro_s))
+    errs = {"o rows": _row_rel(o, o_r), "h_kv_final": rel_err(hkv, hkv_r)}
+    if num_iter > 0:
+        errs["h_kk_final"] = rel_err(hkk, hkk_r)
+    for name, t, e in zip(["dq", "dk", "dv", "dalpha", "dg", "dgk"], ins, exp):
+        if e is None:
+            assert t is None or t.grad is None, name
+            continue
+        assert torch.isfinite(t.grad.float()).all(), name
+        errs[name] = rel_err(t.grad, e)
+    print("errors", {n: f"{e:.2e}" for n, e in errs.items()})
+    assert errs["o rows"] < OUT_ROW_REL
+    assert errs["h_kv_final"] < STATE_REL and errs.get("h_kk_final", 0.0) < STATE_REL
+    for name in ("dq", "dk", "dv", "dalpha", "dg", "dgk"):
+        if name in errs:
+            assert errs[name] < GRAD_REL, f"{name}: rel {errs[name]:.3e}"
+
+
+def test_gka_chebyshev_gla_routes_through_autograd(dev):
+    """hmx.gka_chebyshev_gla takes the differentiable path when an input requires a
+    gradient, with the same outputs as the forward-only path."""
+    q, k, gk, _ = _inputs(1, 150, 2, 31, True, dev)
+    v = torch.randn(1, 150, 2, D, device=dev).bfloat16()
+    alpha = torch.rand(1, 150, 2, device=dev)
+    g = -0.1 * torch.rand(1, 150, 2, device=dev)
+    with torch.no_grad():
+        o0, kk0, kv0 = hmx.gka_chebyshev_gla(q, k, v, alpha, g, gk, 0.3, 0.02, num_iter=8)
+    qq = q.clone().requires_grad_(True)
+    o1, kk1, kv1 = hmx.gka_chebyshev_gla(qq, k, v, alpha, g, gk, 0.3, 0.02, num_iter=8)
+    assert o1.grad_fn is not None
+    assert torch.equal(o0, o1) and torch.equal(kk0, kk1) and torch.equal(kv0, kv1)
+    o1.float().sum().backward()
+    assert qq.grad is not None and torch.isfinite(qq.grad.float()).all()

@@ -12,6 +12,8 @@ mathematics it stands for.
 - dq at any iteration count: the recurrence is linear in its right-hand side with
   a symmetric polynomial of H_t, so dq is autograd of sum_t dx_t . x_t with respect
   to q through the unconverged recurrence itself.
+- The whole training forward (solve, alpha blend, GLA readout): at convergence its
+  backward equals autograd of the same chain with the exact ridge solve.
 """
 import pytest
 import torch
@@ -100,3 +102,31 @@ def test_dq_is_the_recurrence_adjoint(num_iter):
     xq = tr.chebyshev_fixed(tr.h_states(k, gk), qq, fro, 0.02, num_iter)
     (want,) = torch.autograd.grad((xq * dx).sum(), [qq])
     assert ((dq - want).norm() / want.norm()).item() < 1e-12
+
+
+def _ridge_gla(q, k, v, alpha, g, gk, r, lam_grad):
+    """The training forward with the exact ridge solution in place of the recurrence."""
+    x = _ridge_solve(tr.h_states(k, gk), q, r, lam_grad)
+    u = q + alpha[..., None] * (x - q)
+    return tr.gla(u, k, v, g, 0.3)[0]
+
+
+@pytest.mark.parametrize("bp_lambda", [True, False])
+def test_training_gka_backward_converged_equals_autograd(bp_lambda):
+    """gka_chebyshev_gla_bwd at convergence equals autograd of the whole forward with
+    the exact ridge solve (the GLA, the blend and the solve chained)."""
+    k, q, gk, _ = _inputs(5, B=1, T=16)
+    g0 = torch.Generator().manual_seed(6)
+    v = torch.randn(1, 16, 2, D, generator=g0, dtype=torch.float64)
+    alpha = torch.rand(1, 16, 2, generator=g0, dtype=torch.float64)
+    g = -0.2 * torch.rand(1, 16, 2, generator=g0, dtype=torch.float64)
+    do = torch.randn(1, 16, 2, D, generator=g0, dtype=torch.float64)
+    o, _, _, x, fro = tr.gka_chebyshev_gla_fwd(q, k, v, alpha, g, gk, 0.3, 0.5, 40)
+    got = tr.gka_chebyshev_gla_bwd(q, k, v, alpha, g, gk, 0.3, 0.5, 40, bp_lambda, do, x, fro)
+    ins = [t.clone().requires_grad_(True) for t in (q, k, v, alpha, g, gk)]
+    oe = _ridge_gla(*ins, 0.5, bp_lambda)
+    assert (oe - o).norm() / oe.norm() < 1e-12
+    want = torch.autograd.grad((oe * do).sum(), ins)
+    for name, a, b in zip(["dq", "dk", "dv", "dalpha", "dg", "dgk"], got, want):
+        err = ((a - b).norm() / b.norm()).item()
+        assert err < 1e-10, f"{name}: {err:.2e}"
