@@ -498,7 +498,9 @@ def bench_gka_train(dev, steps, warmup, num_iter=8, B=8, T=4096, H=32):
     """F4: the training layer's Chebyshev solve (hmx.ChebyshevIteration) forward and
     forward + backward through autograd, B=8 x T=4096 tokens (the C3 token count),
     H=32, d=128, ridge 0.02, bp_lambda; inputs as the layer prepares them (unit q,
-    k = beta k^ with beta in (0.1, 1), gk = logsigmoid(N(2, 1)) / 8)."""
+    k = beta k^ with beta in (0.1, 1), gk = logsigmoid(N(2, 1)) / 8).  Also the
+    whole training GKA op (hmx.gka_chebyshev_gla: solve, blend, GLA) forward +
+    backward on the same shape."""
     import torch
     import torch.nn.functional as F
     import hmx
@@ -523,10 +525,23 @@ def bench_gka_train(dev, steps, warmup, num_iter=8, B=8, T=4096, H=32):
     ms_f = _timed(fwd, steps, warmup)
     ms_fb = _timed(fwd_bwd, steps, warmup)
     ff, fb = wl.gka_train_flops(B * T, H, num_iter)
+    # the whole training GKA forward (solve, blend, GLA) with its backward
+    v = torch.randn(B, T, H, D, generator=g, device=dev).bfloat16()
+    alpha = torch.rand(B, T, H, generator=g, device=dev)
+    gg_ = F.logsigmoid(torch.randn(B, T, H, generator=g, device=dev) + 2.0) / 8
+    do = torch.randn(B, T, H, D, generator=g, device=dev).bfloat16()
+    ins = [t.clone().requires_grad_(True) for t in (q, k, v, alpha, gg_, gk)]
+
+    def layer_fwd_bwd():
+        o, _, _ = hmx.gka_chebyshev_gla(*ins, D ** -0.5, 0.02, num_iter=num_iter)
+        torch.autograd.backward(o, do)
+
+    ms_l = _timed(layer_fwd_bwd, steps, warmup)
     return dict(ms_fwd=ms_f, ms_fwd_bwd=ms_fb, flops_fwd=ff, flops_bwd=fb,
                 tokens_per_s=B * T / (ms_fb * 1e-3),
                 TFLOPs_fwd=ff / (ms_f * 1e-3) / 1e12,
-                TFLOPs_fwd_bwd=(ff + fb) / (ms_fb * 1e-3) / 1e12)
+                TFLOPs_fwd_bwd=(ff + fb) / (ms_fb * 1e-3) / 1e12,
+                ms_gka_chebyshev_gla_fwd_bwd=ms_l)
 
 
 def bench_ssd(dev, steps, warmup, b=2, T=16384, H=64, P=64, N=128, G=8):
@@ -922,6 +937,7 @@ def main():
         line["gka_train"] = {
             "value": round(r["tokens_per_s"], 1), "unit": "tokens/s (forward + backward)",
             "ms_fwd": round(r["ms_fwd"], 4), "ms_fwd_bwd": round(r["ms_fwd_bwd"], 4),
+            "gka_chebyshev_gla_ms_fwd_bwd": round(r["ms_gka_chebyshev_gla_fwd_bwd"], 4),
             "config": {"workload": "F4 GKA training solve (ChebyshevIteration fwd + bwd)",
                        "B": 8, "T": 4096, "H": 32, "d": 128, "num_iter": 8, "ridge_ratio": 0.02,
                        "bp_lambda": True},

@@ -5,10 +5,12 @@ as opaque and CUDA graphs capture (vllm-inference/src/primed_vllm/
 primed_gdn_layer.py:85-90), and the training mixers call the kernels under
 autograd.  These registrations give every hmx op a schema, a fake (meta)
 implementation for tracing, declared mutations for the in-place state pools,
-and, for the functional (prefill / scan) ops, an autograd rule: the kernels are
-forward-only, so a backward through them raises NotImplementedError instead of
-silently returning no gradient.  The in-place decode ops declare their
-mutations; torch refuses autograd through them by itself.
+and, for the functional (prefill / scan) ops, an autograd rule: these serving
+kernels are forward-only, so a backward through them raises NotImplementedError
+instead of silently returning no gradient.  The in-place decode ops declare their
+mutations; torch refuses autograd through them by itself.  The training GKA op
+with its backward is the autograd function behind ``hmx.gka_chebyshev_gla`` and
+``hmx.ChebyshevIteration`` (hmx.ops.gka_train).
 
 ``torch.ops.hmx.<name>`` is the registered op; the functions of the same name
 in this module wrap it with the reference's Python signature (optional
