@@ -622,10 +622,10 @@ __device__ __forceinline__ float state_store(f16* dst, const StateLd& L, float d
 
 // The lower 16x16 tiles of the symmetric H in LDS from their upper mirrors: a
 // transposing read of 4 rows x 16 columns of tile (C, R) is 4 consecutive columns
-// of one row of tile (R, C) per lane.  Wave w fills lower tiles w, w+4, ... (28).
-__device__ __forceinline__ void state_fill_lower(f16* sH, int wave, int lane) {
+// of one row of tile (R, C) per lane.  Wave w of nw fills lower tiles w, w+nw, ... (28).
+__device__ __forceinline__ void state_fill_lower(f16* sH, int wave, int lane, int nw = 4) {
   const int q4 = lane >> 4, l16 = lane & 15;
-  for (int k = wave; k < 28; k += 4) {
+  for (int k = wave; k < 28; k += nw) {
     int R = 1, m = k;                   // k-th lower tile (R, C), C < R, row-major
     while (m >= R) { m -= R; ++R; }
     const int C = m;
@@ -1268,7 +1268,8 @@ extern "C" int hmx_gka_chunk_fwd(const void* q, int64_t q_token_stride, const vo
 // without bp_lambda).  Per 64-token block c with in-block decays g_t (inclusive
 // cumsum of gk from the block start), block total Gam = g at the last token, and
 // block-start state h_c (H_t = e^{g_t} h_c + sum_{s<=t} e^{g_t-g_s} k_s k_s^T):
-//   E_c = sum_t e^{g_t} (G_t + G_t^T)   (the block's share of dL/dh_c, symmetrised)
+//   E_c = sum_t e^{g_t} (G_t + G_t^T)   (the block's share of dL/dh_c, symmetrised;
+//         stored bf16, the reverse scan accumulating in fp32)
 //   Dn_c = sum over later blocks, decayed to block c's end: Dn_c = E_{c+1} + e^{Gam_{c+1}} Dn_{c+1}
 //   dk_s = -sum_{t>=s} e^{g_t-g_s} [dq_t (x_t.k_s) + x_t (dq_t.k_s)]
 //          + 2 beta_s h_c k_s + 2 sum_u W_su (k_u.k_s) k_u + e^{Gam-g_s} Dn k_s
@@ -1291,7 +1292,7 @@ struct Bwd {
   const bf16* x;          // [tokens][H][D] the forward's solution
   const float* dq;        // [tokens][H][D] the backward's solve of dx
   const float* fro;       // [tokens][H]
-  float* e;               // [nblk][H][D][D] fp32 tile-major: E_c, then Dn_c
+  bf16* e;                // [nblk][H][D][D] bf16 tile-major: E_c, then Dn_c
   float* gam;             // [nblk][H] block totals of gk
   float* dk;              // [tokens][H][D] (added to what it holds when dk_acc)
   float* dgk;             // [tokens][H]
@@ -1312,19 +1313,22 @@ __device__ __forceinline__ Blk block_of(const Params& p, int gb) {
   return Blk{lo, lb, tok0, min(CB, si.eos - tok0)};
 }
 
-// h_c of block gb into sH (fp16, interleaved rows, both triangles), as the solve forms it
+// h_c of block gb into sH (fp16, interleaved rows, both triangles), as the solve
+// forms it; the first 256 threads load, all nw waves mirror
 __device__ __forceinline__ void load_hc(const Params& p, f16* sH, const Blk& b, int gb, int h,
-                                        int tid, int wave, int lane) {
-  const int64_t DD = (int64_t)D * D;
-  const int64_t so = ((int64_t)b.s_id * p.H + h) * DD;
-  const int64_t bso = ((int64_t)gb * p.H + h) * DD;
-  StateLd hst;
-  solve::state_issue_b<true>(hst, b.lb > 0 ? p.ws_hb + bso : nullptr, tid);
-  const float off_gk = p.ws_boff[((int64_t)gb * p.H + h) * 2];
-  solve::state_issue_s<true>(hst, (b.lb == 0 || off_gk > solve::SEG_STATE_DROP) ? p.ws_h0 + so : nullptr, tid);
-  solve::state_store<true>(sH, hst, fast_exp(off_gk), tid);
+                                        int tid, int wave, int lane, int nw = 4) {
+  if (tid < NTHR) {
+    const int64_t DD = (int64_t)D * D;
+    const int64_t so = ((int64_t)b.s_id * p.H + h) * DD;
+    const int64_t bso = ((int64_t)gb * p.H + h) * DD;
+    StateLd hst;
+    solve::state_issue_b<true>(hst, b.lb > 0 ? p.ws_hb + bso : nullptr, tid);
+    const float off_gk = p.ws_boff[((int64_t)gb * p.H + h) * 2];
+    solve::state_issue_s<true>(hst, (b.lb == 0 || off_gk > solve::SEG_STATE_DROP) ? p.ws_h0 + so : nullptr, tid);
+    solve::state_store<true>(sH, hst, fast_exp(off_gk), tid);
+  }
   lds_barrier();
-  solve::state_fill_lower(sH, wave, lane);
+  solve::state_fill_lower(sH, wave, lane, nw);
 }
 
 // in-block inclusive cumsum of gk for lanes 0-63 (wave 0); 0 past the block's tokens
@@ -1369,19 +1373,29 @@ __device__ __forceinline__ float absmax8(const bf16x8& x) {
 __device__ __forceinline__ float absmax4(const f32x4& x) {
   return fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
 }
-// The workgroup's maxima of NV per-thread values: slot[NV * 4] of LDS scratch;
-// includes a barrier.
-template <int NV>
+// The workgroup's maxima of NV per-thread values over NW waves: slot[NV * NW] of
+// LDS scratch; includes a barrier.
+template <int NV, int NW = 4>
 __device__ __forceinline__ void block_max(float (&v)[NV], float* slot, int wave, int lane) {
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     v[i] = wave_max(v[i]);
-    if (lane == 0) slot[4 * i + wave] = v[i];
+    if (lane == 0) slot[NW * i + wave] = v[i];
   }
   lds_barrier();
 #pragma unroll
-  for (int i = 0; i < NV; ++i)
-    v[i] = fmaxf(fmaxf(slot[4 * i], slot[4 * i + 1]), fmaxf(slot[4 * i + 2], slot[4 * i + 3]));
+  for (int i = 0; i < NV; ++i) {
+    float m = slot[NW * i];
+#pragma unroll
+    for (int j = 1; j < NW; ++j) m = fmaxf(m, slot[NW * i + j]);
+    v[i] = m;
+  }
+}
+__device__ __forceinline__ bf16x4 bf4(const f32x4& x) {
+  return bf16x4{(bf16)x[0], (bf16)x[1], (bf16)x[2], (bf16)x[3]};
+}
+__device__ __forceinline__ f32x4 f4(const bf16x4& x) {
+  return f32x4{(float)x[0], (float)x[1], (float)x[2], (float)x[3]};
 }
 __device__ __forceinline__ f16x8 h8_of(const f32x4& a, const f32x4& b, float s) {
   return f16x8{(f16)(s * a[0]), (f16)(s * a[1]), (f16)(s * a[2]), (f16)(s * a[3]),
@@ -1390,11 +1404,12 @@ __device__ __forceinline__ f16x8 h8_of(const f32x4& a, const f32x4& b, float s) 
 
 constexpr int E_OFF_K = 0, E_OFF_KB = SZ_K, E_OFF_Q = 2 * SZ_K, E_OFF_X = 3 * SZ_K;
 constexpr int E_OFF_H = 4 * SZ_K, E_OFF_SC = E_OFF_H + SZ_H;
-constexpr int E_SMEM = E_OFF_SC + 3 * CB * 4 + 16 * 4;
+constexpr int E_SMEM = E_OFF_SC + 3 * CB * 4 + 32 * 4;
+constexpr int E_NTHR = 512;             // 8 waves: wave w forms tile row w of E_c
 static_assert(E_SMEM <= 160 * 1024, "LDS budget");
 
 // E_c = -(Ql^T X + X^T Ql) + 2 (alpha h_c + K^T diag(beta) K), Ql = e^{g} dq, of block gb
-__global__ __launch_bounds__(NTHR, 1) void cheb_e_kernel(Params p, Bwd w) {
+__global__ __launch_bounds__(E_NTHR, 1) void cheb_e_kernel(Params p, Bwd w) {
   __shared__ __align__(16) unsigned char smem[E_SMEM];
   f16* sK = reinterpret_cast<f16*>(smem + E_OFF_K);
   f16* sKb = reinterpret_cast<f16*>(smem + E_OFF_KB);
@@ -1410,19 +1425,20 @@ __global__ __launch_bounds__(NTHR, 1) void cheb_e_kernel(Params p, Bwd w) {
   const int gb = blockIdx.x, h = blockIdx.y, H = p.H;
   const Blk b = block_of(p, gb);
   if (b.nval <= 0) return;
+  constexpr int NP = CB * 16 / E_NTHR;     // staging passes of 32 rows
 
-  load_hc(p, sH, b, gb, h, tid, wave, lane);
+  load_hc(p, sH, b, gb, h, tid, wave, lane, E_NTHR / 64);
   if (wave == 0) {
     const float g = block_decay(p, b, h, lane);
     sG[lane] = g;
     if (lane == b.nval - 1) w.gam[(int64_t)gb * H + h] = g;
   }
   // the rows, and a_t from them
-  bf16x8 kr[CB / 16], xr[CB / 16];
-  f32x4 q0[CB / 16], q1[CB / 16];
+  bf16x8 kr[NP], xr[NP];
+  f32x4 q0[NP], q1[NP];
 #pragma unroll
-  for (int pass = 0; pass < CB / 16; ++pass) {
-    const int row = pass * 16 + (tid >> 4), f0 = (tid & 15) * 8;
+  for (int pass = 0; pass < NP; ++pass) {
+    const int row = pass * 32 + (tid >> 4), f0 = (tid & 15) * 8;
     const bool ok = row < b.nval;
     const int64_t ro = ((int64_t)(b.tok0 + row) * H + h) * D + f0;
     kr[pass] = ok ? *reinterpret_cast<const bf16x8*>(p.k + (int64_t)(b.tok0 + row) * p.kv_ts + h * D + f0) : bf16x8{};
@@ -1449,8 +1465,8 @@ __global__ __launch_bounds__(NTHR, 1) void cheb_e_kernel(Params p, Bwd w) {
   // stage k, 2 beta k, -e^{g} dq, x (fp16, interleaved; the last three scaled)
   float mx[3] = {0.f, 0.f, 0.f};            // max |x|, |e^g dq|, |2 beta k|
 #pragma unroll
-  for (int pass = 0; pass < CB / 16; ++pass) {
-    const int row = pass * 16 + (tid >> 4);
+  for (int pass = 0; pass < NP; ++pass) {
+    const int row = pass * 32 + (tid >> 4);
     const float eg = row < b.nval ? -fast_exp(sG[row]) : 0.f;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
@@ -1461,11 +1477,11 @@ __global__ __launch_bounds__(NTHR, 1) void cheb_e_kernel(Params p, Bwd w) {
     mx[1] = fmaxf(mx[1], fmaxf(absmax4(q0[pass]), absmax4(q1[pass])));
     mx[2] = fmaxf(mx[2], fabsf(sB[row]) * absmax8(kr[pass]));
   }
-  block_max(mx, reinterpret_cast<float*>(smem + E_OFF_SC + 3 * CB * 4), wave, lane);
+  block_max<3, E_NTHR / 64>(mx, reinterpret_cast<float*>(smem + E_OFF_SC + 3 * CB * 4), wave, lane);
   const float sx = pow2_scale(mx[0]), sq = pow2_scale(mx[1]), sb = pow2_scale(mx[2]);
 #pragma unroll
-  for (int pass = 0; pass < CB / 16; ++pass) {
-    const int row = pass * 16 + (tid >> 4), f0 = (tid & 15) * 8;
+  for (int pass = 0; pass < NP; ++pass) {
+    const int row = pass * 32 + (tid >> 4), f0 = (tid & 15) * 8;
     store8_i(sK + row * LDP, f0, scale_h8(kr[pass], 1.f));
     store8_i(sKb + row * LDP, f0, scale_h8(kr[pass], sb * sB[row]));
     store8_i(sX + row * LDP, f0, scale_h8(xr[pass], sx));
@@ -1474,11 +1490,10 @@ __global__ __launch_bounds__(NTHR, 1) void cheb_e_kernel(Params p, Bwd w) {
   lds_barrier();
   const float a2 = 2.f * s_alpha;
   const float u12 = 1.f / (sx * sq), u3 = 1.f / sb;
-  // wave w: tile rows 2w, 2w+1 (state rows 32w..32w+31), all 8 tile columns
-  float* eo = w.e + ((int64_t)gb * H + h) * D * D;
-#pragma unroll
-  for (int ir = 0; ir < 2; ++ir) {
-    const int it = 2 * wave + ir;
+  // wave w: tile row w (state rows 16w..16w+15), all 8 tile columns
+  bf16* eo = w.e + ((int64_t)gb * H + h) * D * D;
+  {
+    const int it = wave;
     f32x4 E[8], E3[8];
 #pragma unroll
     for (int jt = 0; jt < 8; ++jt) {
@@ -1505,7 +1520,7 @@ __global__ __launch_bounds__(NTHR, 1) void cheb_e_kernel(Params p, Bwd w) {
       f32x4 y;
 #pragma unroll
       for (int v = 0; v < 4; ++v) y[v] = u12 * E[jt][v] + u3 * E3[jt][v] + a2 * (float)hc[v];
-      *reinterpret_cast<f32x4*>(eo + blk_index(16 * jt + l16, 16 * it + 4 * q4)) = y;
+      *reinterpret_cast<bf16x4*>(eo + blk_index(16 * jt + l16, 16 * it + 4 * q4)) = bf4(y);
     }
   }
 }
@@ -1526,10 +1541,10 @@ __global__ __launch_bounds__(256) void cheb_dscan_kernel(Params p, Bwd w) {
   const int64_t el = (int64_t)blockIdx.y * 1024 + 4 * threadIdx.x;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   for (int c = b1 - 1; c >= b0; --c) {
-    float* ec = w.e + ((int64_t)c * H + h) * DD + el;
-    const f32x4 e = *reinterpret_cast<const f32x4*>(ec);
+    bf16* ec = w.e + ((int64_t)c * H + h) * DD + el;
+    const f32x4 e = f4(*reinterpret_cast<const bf16x4*>(ec));
     const float dg = fast_exp(w.gam[(int64_t)c * H + h]);
-    *reinterpret_cast<f32x4*>(ec) = acc;
+    *reinterpret_cast<bf16x4*>(ec) = bf4(acc);
 #pragma unroll
     for (int v = 0; v < 4; ++v) acc[v] = e[v] + dg * acc[v];
   }
@@ -1566,7 +1581,7 @@ __global__ __launch_bounds__(NTHR, 1) void cheb_dk_kernel(Params p, Bwd w) {
   // the rows (x, dq and Dn scaled into fp16's range) and a_t
   bf16x8 kr[CB / 16], xr[CB / 16];
   f32x4 q0[CB / 16], q1[CB / 16];
-  const float* dn = w.e + ((int64_t)gb * H + h) * DD;
+  const bf16* dn = w.e + ((int64_t)gb * H + h) * DD;
   const int dr = tid >> 1, dc0 = (tid & 1) * 64;    // this thread's Dn: row dr, columns dc0..+63
   f32x4 u[16];
   float mx[3] = {0.f, 0.f, 0.f};            // max |x|, |dq|, |Dn|
@@ -1598,7 +1613,7 @@ __global__ __launch_bounds__(NTHR, 1) void cheb_dk_kernel(Params p, Bwd w) {
   }
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
-    u[j] = *reinterpret_cast<const f32x4*>(dn + blk_index(dr, dc0 + 4 * j));
+    u[j] = f4(*reinterpret_cast<const bf16x4*>(dn + blk_index(dr, dc0 + 4 * j)));
     mx[2] = fmaxf(mx[2], absmax4(u[j]));
   }
   block_max(mx, mslot, wave, lane);       // (its barrier also orders h_c's lower tiles)
@@ -1836,7 +1851,7 @@ __global__ __launch_bounds__(NTHR, 1) void cheb_dk_kernel(Params p, Bwd w) {
 struct GlaBwd {
   const bf16* q; const bf16* x; const bf16* v; const bf16* dout;   // [tokens][H][D]
   const void* alpha; int alpha_dt;        // [tokens][H]
-  float* e; float* gam;                   // as Bwd
+  bf16* e; float* gam;                    // as Bwd
   float* dx;                              // [tokens][H][D]: alpha du (the solve's dx)
   float* dq; float* dk; float* dv;        // [tokens][H][D]
   float* dalpha; float* dg;               // [tokens][H]
@@ -1902,7 +1917,7 @@ __global__ __launch_bounds__(NTHR, 2) void gla_e_kernel(Params p, GlaBwd w) {
   }
   lds_barrier();
   const float un = 1.f / (su * sd);
-  float* eo = w.e + ((int64_t)gb * H + h) * D * D;
+  bf16* eo = w.e + ((int64_t)gb * H + h) * D * D;
   // wave w: E'^T tile rows (V) 2w, 2w+1 by all 8 tile columns (K); the lane's 4
   // values are 4 consecutive V columns of one K row of E'
 #pragma unroll
@@ -1922,7 +1937,7 @@ __global__ __launch_bounds__(NTHR, 2) void gla_e_kernel(Params p, GlaBwd w) {
       f32x4 y;
 #pragma unroll
       for (int v = 0; v < 4; ++v) y[v] = un * E[it][v];
-      *reinterpret_cast<f32x4*>(eo + blk_index(16 * it + l16, 16 * jt + 4 * q4)) = y;
+      *reinterpret_cast<bf16x4*>(eo + blk_index(16 * it + l16, 16 * jt + 4 * q4)) = bf4(y);
     }
   }
 }
@@ -1972,7 +1987,7 @@ __global__ __launch_bounds__(NTHR, 1) void gla_bwd_kernel(Params p, GlaBwd w) {
   // rows k, v (fp16 as given), do and u (scaled); dSn (scaled) and <dSn, S_c>
   bf16x8 kr[CB / 16], vr[CB / 16], dr[CB / 16];
   f32x4 u0[CB / 16], u1[CB / 16];
-  const float* dn = w.e + ((int64_t)gb * H + h) * DD;
+  const bf16* dn = w.e + ((int64_t)gb * H + h) * DD;
   const int drw = tid >> 1, dc0 = (tid & 1) * 64;
   f32x4 dsv[16];
   float mx[3] = {0.f, 0.f, 0.f};          // max |do|, |u|, |dSn|
@@ -1997,7 +2012,7 @@ __global__ __launch_bounds__(NTHR, 1) void gla_bwd_kernel(Params p, GlaBwd w) {
   }
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
-    dsv[j] = *reinterpret_cast<const f32x4*>(dn + blk_index(drw, dc0 + 4 * j));
+    dsv[j] = f4(*reinterpret_cast<const bf16x4*>(dn + blk_index(drw, dc0 + 4 * j)));
     mx[2] = fmaxf(mx[2], absmax4(dsv[j]));
   }
   block_max(mx, mslot, wave, lane);
@@ -2327,7 +2342,7 @@ extern "C" int hmx_gka_cheb_fwd(const void* k, int64_t k_token_stride, const voi
 }
 
 extern "C" size_t hmx_gka_cheb_bwd_workspace_bytes(int32_t nblock_total, int32_t H) {
-  return al256((size_t)nblock_total * H * D * D * sizeof(float)) +
+  return al256((size_t)nblock_total * H * D * D * sizeof(bf16)) +
          al256((size_t)nblock_total * H * sizeof(float));
 }
 
@@ -2358,15 +2373,15 @@ extern "C" int hmx_gka_cheb_bwd(const void* k, int64_t k_token_stride, const voi
   train::Bwd w{};
   w.x = static_cast<const bf16*>(x);
   w.dq = dq; w.fro = fro;
-  w.e = static_cast<float*>(bwd_workspace);
+  w.e = static_cast<bf16*>(bwd_workspace);
   w.gam = reinterpret_cast<float*>(static_cast<char*>(bwd_workspace) +
-                                   al256((size_t)nblock_total * H * D * D * sizeof(float)));
+                                   al256((size_t)nblock_total * H * D * D * sizeof(bf16)));
   w.dk = dk; w.dgk = gk ? dgk : nullptr;
   w.bp_lambda = bp_lambda;
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid(nblock_total, H);
   hipLaunchKernelGGL((solve::gka_solve_kernel<true, false, solve::SM_DQ>), grid, dim3(NTHR), 0, s, p);
-  hipLaunchKernelGGL(train::cheb_e_kernel, grid, dim3(NTHR), 0, s, p, w);
+  hipLaunchKernelGGL(train::cheb_e_kernel, grid, dim3(train::E_NTHR), 0, s, p, w);
   hipLaunchKernelGGL(train::cheb_dscan_kernel, dim3(N * H, 16), dim3(256), 0, s, p, w);
   hipLaunchKernelGGL(train::cheb_dk_kernel, grid, dim3(NTHR), 0, s, p, w);
   return check_launch("hmx_gka_cheb_bwd");
@@ -2474,13 +2489,13 @@ extern "C" int hmx_gka_train_bwd(const void* q, const void* k, const void* v, in
               bwd_workspace_bytes);
   if (nseg_total == 0 || nblock_total == 0) return HMX_OK;
   char* bw = static_cast<char*>(bwd_workspace);
-  const size_t e_bytes = al256((size_t)nblock_total * H * D * D * sizeof(float));
+  const size_t e_bytes = al256((size_t)nblock_total * H * D * D * sizeof(bf16));
   const size_t cb_bytes = hmx_gka_cheb_bwd_workspace_bytes(nblock_total, H);
   train::GlaBwd gw{};
   gw.q = static_cast<const bf16*>(q); gw.x = static_cast<const bf16*>(x);
   gw.v = static_cast<const bf16*>(v); gw.dout = static_cast<const bf16*>(dout);
   gw.alpha = alpha; gw.alpha_dt = alpha_dtype;
-  gw.e = reinterpret_cast<float*>(bw);
+  gw.e = reinterpret_cast<bf16*>(bw);
   gw.gam = reinterpret_cast<float*>(bw + e_bytes);
   gw.dx = reinterpret_cast<float*>(bw + cb_bytes);
   float* dq_cheb = reinterpret_cast<float*>(bw + cb_bytes + al256((size_t)tokens * H * D * sizeof(float)));
@@ -2503,7 +2518,7 @@ extern "C" int hmx_gka_train_bwd(const void* q, const void* k, const void* v, in
     cw.dk = dk; cw.dk_acc = 1; cw.dgk = gk ? dgk : nullptr; cw.dq_out = dq;
     cw.bp_lambda = bp_lambda;
     hipLaunchKernelGGL((solve::gka_solve_kernel<true, false, solve::SM_DQ>), grid, dim3(NTHR), 0, s, pc);
-    hipLaunchKernelGGL(train::cheb_e_kernel, grid, dim3(NTHR), 0, s, pc, cw);
+    hipLaunchKernelGGL(train::cheb_e_kernel, grid, dim3(train::E_NTHR), 0, s, pc, cw);
     hipLaunchKernelGGL(train::cheb_dscan_kernel, sgrid, dim3(256), 0, s, pc, cw);
     hipLaunchKernelGGL(train::cheb_dk_kernel, grid, dim3(NTHR), 0, s, pc, cw);
   }
