@@ -1553,11 +1553,16 @@ __global__ __launch_bounds__(256) void cheb_dscan_kernel(Params p, Bwd w) {
 constexpr int C_OFF_K = 0, C_OFF_X = SZ_K, C_OFF_Q = 2 * SZ_K, C_OFF_H = 3 * SZ_K;
 constexpr int C_OFF_DN = C_OFF_H + SZ_H, C_OFF_SC = C_OFF_DN + SZ_H;
 enum { CS_G, CS_A, CS_RHO, CS_DG, CS_COL0, NCS = CS_COL0 + 4 };
-constexpr int C_SMEM = C_OFF_SC + NCS * CB * 4 + 16 * 4 + 16 * 4;
+// 8 waves: wave w takes the 16 columns s of group w & 3 and the feature half w >> 2
+constexpr int C_NTHR = 512;
+constexpr int C_OFF_RED = C_OFF_SC + NCS * CB * 4;        // 16 floats of cross-wave sums
+constexpr int C_OFF_MS = C_OFF_RED + 16 * 4;              // 24 floats for block_max
+constexpr int C_OFF_XCH = C_OFF_MS + 24 * 4;              // [2][64][4] feature-half dot products
+constexpr int C_SMEM = C_OFF_XCH + 2 * CB * 4 * 4;
 static_assert(C_SMEM <= 160 * 1024, "LDS budget");
 
 // dk and dgk of block gb (see the section comment)
-__global__ __launch_bounds__(NTHR, 1) void cheb_dk_kernel(Params p, Bwd w) {
+__global__ __launch_bounds__(C_NTHR, 1) void cheb_dk_kernel(Params p, Bwd w) {
   __shared__ __align__(16) unsigned char smem[C_SMEM];
   f16* sK = reinterpret_cast<f16*>(smem + C_OFF_K);
   f16* sX = reinterpret_cast<f16*>(smem + C_OFF_X);
@@ -1565,29 +1570,32 @@ __global__ __launch_bounds__(NTHR, 1) void cheb_dk_kernel(Params p, Bwd w) {
   f16* sH = reinterpret_cast<f16*>(smem + C_OFF_H);
   f16* sDn = reinterpret_cast<f16*>(smem + C_OFF_DN);
   float* sc = reinterpret_cast<float*>(smem + C_OFF_SC);
-  float* red = sc + NCS * CB;            // 16 floats of cross-wave sums
-  float* mslot = red + 16;               // 16 floats for block_max
+  float* red = reinterpret_cast<float*>(smem + C_OFF_RED);
+  float* mslot = reinterpret_cast<float*>(smem + C_OFF_MS);
+  float* xch = reinterpret_cast<float*>(smem + C_OFF_XCH);
   auto SC = [&](int slot, int t) -> float& { return sc[slot * CB + t]; };
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int cg = wave & 3, fh = wave >> 2;   // column group, feature half (nt 4 fh .. 4 fh + 3)
   const int q4 = lane >> 4, l16 = lane & 15;
   const int gb = blockIdx.x, h = blockIdx.y, H = p.H;
   const Blk b = block_of(p, gb);
   if (b.nval <= 0) return;
   const int64_t DD = (int64_t)D * D;
+  constexpr int NP = CB * 16 / C_NTHR;     // staging passes of 32 rows
 
-  load_hc(p, sH, b, gb, h, tid, wave, lane);
+  load_hc(p, sH, b, gb, h, tid, wave, lane, C_NTHR / 64);
   if (wave == 0) SC(CS_G, lane) = block_decay(p, b, h, lane);
   // the rows (x, dq and Dn scaled into fp16's range) and a_t
-  bf16x8 kr[CB / 16], xr[CB / 16];
-  f32x4 q0[CB / 16], q1[CB / 16];
+  bf16x8 kr[NP], xr[NP];
+  f32x4 q0[NP], q1[NP];
   const bf16* dn = w.e + ((int64_t)gb * H + h) * DD;
-  const int dr = tid >> 1, dc0 = (tid & 1) * 64;    // this thread's Dn: row dr, columns dc0..+63
-  f32x4 u[16];
+  const int dr = tid >> 2, dc0 = (tid & 3) * 32;    // this thread's Dn: row dr, columns dc0..+31
+  f32x4 u[8];
   float mx[3] = {0.f, 0.f, 0.f};            // max |x|, |dq|, |Dn|
 #pragma unroll
-  for (int pass = 0; pass < CB / 16; ++pass) {
-    const int row = pass * 16 + (tid >> 4), f0 = (tid & 15) * 8;
+  for (int pass = 0; pass < NP; ++pass) {
+    const int row = pass * 32 + (tid >> 4), f0 = (tid & 15) * 8;
     const bool ok = row < b.nval;
     const int64_t ro = ((int64_t)(b.tok0 + row) * H + h) * D + f0;
     kr[pass] = ok ? *reinterpret_cast<const bf16x8*>(p.k + (int64_t)(b.tok0 + row) * p.kv_ts + h * D + f0) : bf16x8{};
@@ -1612,15 +1620,15 @@ __global__ __launch_bounds__(NTHR, 1) void cheb_dk_kernel(Params p, Bwd w) {
     }
   }
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
+  for (int j = 0; j < 8; ++j) {
     u[j] = f4(*reinterpret_cast<const bf16x4*>(dn + blk_index(dr, dc0 + 4 * j)));
     mx[2] = fmaxf(mx[2], absmax4(u[j]));
   }
-  block_max(mx, mslot, wave, lane);       // (its barrier also orders h_c's lower tiles)
+  block_max<3, C_NTHR / 64>(mx, mslot, wave, lane);   // (its barrier also orders h_c's lower tiles)
   const float sx = pow2_scale(mx[0]), sq = pow2_scale(mx[1]), sd = pow2_scale(mx[2]);
 #pragma unroll
-  for (int pass = 0; pass < CB / 16; ++pass) {
-    const int row = pass * 16 + (tid >> 4), f0 = (tid & 15) * 8;
+  for (int pass = 0; pass < NP; ++pass) {
+    const int row = pass * 32 + (tid >> 4), f0 = (tid & 15) * 8;
     store8_i(sK + row * LDP, f0, scale_h8(kr[pass], 1.f));
     store8_i(sX + row * LDP, f0, scale_h8(xr[pass], sx));
     store8_i(sQ + row * LDP, f0, h8_of(q0[pass], q1[pass], sq));
@@ -1628,7 +1636,7 @@ __global__ __launch_bounds__(NTHR, 1) void cheb_dk_kernel(Params p, Bwd w) {
   // Dn into LDS and <Dn, h_c> in fp32
   float dnh = 0.f;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
+  for (int j = 0; j < 4; ++j) {
     const int c = dc0 + 8 * j;
     const f16x4 h0 = *reinterpret_cast<const f16x4*>(sH + dr * LDP + icol(c));
     const f16x4 h1 = *reinterpret_cast<const f16x4*>(sH + dr * LDP + icol(c + 4));
@@ -1647,32 +1655,34 @@ __global__ __launch_bounds__(NTHR, 1) void cheb_dk_kernel(Params p, Bwd w) {
   if (lane == 0) red[wave] = dnh;
   lds_barrier();
 
-  const int s = 16 * wave + l16;            // this lane's key / token column
+  const int s = 16 * cg + l16;              // this lane's key / token column
   const bool s_ok = s < b.nval;
   const float gs = SC(CS_G, s);
   const float Gam = SC(CS_G, b.nval - 1);
-  // products with h_c and Dn: HK = h_c k_s, HX = h_c x_s, P = Dn k_s (rows f, column s)
-  f32x4 HK[8], HX[8], P[8];
+  // products with h_c and Dn over this wave's feature half: HK = h_c k_s, HX = h_c x_s,
+  // P = Dn k_s (rows f = 16 (4 fh + i) + 4 q4 + v, column s)
+  f32x4 HK[4], HX[4], P[4];
 #pragma unroll
-  for (int nt = 0; nt < 8; ++nt) {
-    HK[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    HX[nt] = HK[nt];
-    P[nt] = HK[nt];
+  for (int i = 0; i < 4; ++i) {
+    HK[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    HX[i] = HK[i];
+    P[i] = HK[i];
   }
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
-    const f16x8 bk = frag_i(sK, LDP, 16 * wave, 32 * ks, lane);
-    const f16x8 bx = frag_i(sX, LDP, 16 * wave, 32 * ks, lane);
+    const f16x8 bk = frag_i(sK, LDP, 16 * cg, 32 * ks, lane);
+    const f16x8 bx = frag_i(sX, LDP, 16 * cg, 32 * ks, lane);
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
+    for (int i = 0; i < 4; ++i) {
+      const int nt = 4 * fh + i;
       const f16x8 ah = frag_i(sH, LDP, 16 * nt, 32 * ks, lane);
-      HK[nt] = mfma16h(ah, bk, HK[nt]);
-      HX[nt] = mfma16h(ah, bx, HX[nt]);
-      P[nt] = mfma16h(frag_i(sDn, LDP, 16 * nt, 32 * ks, lane), bk, P[nt]);
+      HK[i] = mfma16h(ah, bk, HK[i]);
+      HX[i] = mfma16h(ah, bx, HX[i]);
+      P[i] = mfma16h(frag_i(sDn, LDP, 16 * nt, 32 * ks, lane), bk, P[i]);
     }
   }
   // in-block products over the 64 tokens t (rows) for this wave's columns s:
-  // XK = x_t . k_s, QK = dq_t . k_s, KK = k_t . k_s
+  // XK = x_t . k_s, QK = dq_t . k_s, KK = k_t . k_s (both feature halves form them)
   f32x4 XK[4], QK[4], KK[4];
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt) {
@@ -1682,7 +1692,7 @@ __global__ __launch_bounds__(NTHR, 1) void cheb_dk_kernel(Params p, Bwd w) {
   }
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
-    const f16x8 bk = frag_i(sK, LDP, 16 * wave, 32 * ks, lane);
+    const f16x8 bk = frag_i(sK, LDP, 16 * cg, 32 * ks, lane);
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
       XK[tt] = mfma16h(frag_i(sX, LDP, 16 * tt, 32 * ks, lane), bk, XK[tt]);
@@ -1722,7 +1732,7 @@ __global__ __launch_bounds__(NTHR, 1) void cheb_dk_kernel(Params p, Bwd w) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const float cs = row16_sum(col[v]);
-        if (l16 == 0) SC(CS_COL0 + wave, 16 * tt + 4 * q4 + v) = cs;
+        if (fh == 0 && l16 == 0) SC(CS_COL0 + cg, 16 * tt + 4 * q4 + v) = cs;
       }
     }
     float mw = 0.f;
@@ -1738,47 +1748,49 @@ __global__ __launch_bounds__(NTHR, 1) void cheb_dk_kernel(Params p, Bwd w) {
   }
   rowdm += __shfl_xor(rowdm, 16, 64);
   rowdm += __shfl_xor(rowdm, 32, 64);
-  // dk^T accumulators (rows f, column s): in-block terms, then the lambda terms L
-  f32x4 DK[8], L[8];
+  // dk^T accumulators over this wave's feature half: in-block terms, then the lambda terms L
+  f32x4 DK[4], L[4];
   const float beta2 = 2.f * fast_exp(gs) * rho_s;
 #pragma unroll
-  for (int nt = 0; nt < 8; ++nt) {
-    DK[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    L[nt] = DK[nt];
+  for (int i = 0; i < 4; ++i) {
+    DK[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    L[i] = DK[i];
   }
 #pragma unroll
   for (int jk = 0; jk < 2; ++jk)
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
-      DK[nt] = mfma16h(frag_t_i(sQ, LDP, 32 * jk, 16 * nt, lane), s1[jk], DK[nt]);
-      DK[nt] = mfma16h(frag_t_i(sX, LDP, 32 * jk, 16 * nt, lane), s2[jk], DK[nt]);
-      L[nt] = mfma16h(frag_t_i(sK, LDP, 32 * jk, 16 * nt, lane), wk[jk], L[nt]);
+    for (int i = 0; i < 4; ++i) {
+      const int nt = 4 * fh + i;
+      DK[i] = mfma16h(frag_t_i(sQ, LDP, 32 * jk, 16 * nt, lane), s1[jk], DK[i]);
+      DK[i] = mfma16h(frag_t_i(sX, LDP, 32 * jk, 16 * nt, lane), s2[jk], DK[i]);
+      L[i] = mfma16h(frag_t_i(sK, LDP, 32 * jk, 16 * nt, lane), wk[jk], L[i]);
     }
   // unscale: DK (sx sq), L's MFMA part (sw), P (sd), HX (sx)
   const float uw = 1.f / sw, ud = 1.f / sd, ux = 1.f / sx;
 #pragma unroll
-  for (int nt = 0; nt < 8; ++nt)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      DK[nt][v] *= uxq;
-      L[nt][v] = uw * L[nt][v] + beta2 * HK[nt][v];
-      P[nt][v] *= ud;
-      HX[nt][v] *= ux;
+      DK[i][v] *= uxq;
+      L[i][v] = uw * L[i][v] + beta2 * HK[i][v];
+      P[i][v] *= ud;
+      HX[i][v] *= ux;
     }
-  // per-column dot products with k_s, dq_s (fp32 from memory)
+  // per-column dot products with k_s, dq_s (fp32 from memory) over both feature halves
   const float ec = fast_exp(Gam - gs);
+  const int64_t ro = ((int64_t)(b.tok0 + s) * H + h) * D + 4 * q4;
   float kl = 0.f, kp = 0.f, qhx = 0.f;
   {
-    const int64_t ro = ((int64_t)(b.tok0 + s) * H + h) * D + 4 * q4;
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
+    for (int i = 0; i < 4; ++i) {
+      const int nt = 4 * fh + i;
       const f16x4 kk = *reinterpret_cast<const f16x4*>(sK + s * LDP + icol(16 * nt + 4 * q4));
       const f32x4 dq = s_ok ? *reinterpret_cast<const f32x4*>(w.dq + ro + 16 * nt) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        kl += (float)kk[v] * L[nt][v];
-        kp += (float)kk[v] * P[nt][v];
-        qhx += dq[v] * HX[nt][v];
+        kl += (float)kk[v] * L[i][v];
+        kp += (float)kk[v] * P[i][v];
+        qhx += dq[v] * HX[i][v];
       }
     }
     kl += __shfl_xor(kl, 16, 64);
@@ -1787,15 +1799,20 @@ __global__ __launch_bounds__(NTHR, 1) void cheb_dk_kernel(Params p, Bwd w) {
     kp += __shfl_xor(kp, 32, 64);
     qhx += __shfl_xor(qhx, 16, 64);
     qhx += __shfl_xor(qhx, 32, 64);
+    if (q4 == 0) {
+      float* xo = xch + (fh * CB + s) * 4;
+      xo[0] = kl; xo[1] = kp; xo[2] = qhx;
+    }
   }
-  // store dk_s = DK + L + e^{Gam - g_s} P
+  // store this feature half of dk_s = DK + L + e^{Gam - g_s} P
   if (s_ok) {
     float* dko = w.dk + ((int64_t)(b.tok0 + s) * H + h) * D + 4 * q4;
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
+    for (int i = 0; i < 4; ++i) {
+      const int nt = 4 * fh + i;
       f32x4 y;
 #pragma unroll
-      for (int v = 0; v < 4; ++v) y[v] = DK[nt][v] + L[nt][v] + ec * P[nt][v];
+      for (int v = 0; v < 4; ++v) y[v] = DK[i][v] + L[i][v] + ec * P[i][v];
       if (w.dk_acc) {
         const f32x4 o0 = *reinterpret_cast<const f32x4*>(dko + 16 * nt);
 #pragma unroll
@@ -1804,28 +1821,34 @@ __global__ __launch_bounds__(NTHR, 1) void cheb_dk_kernel(Params p, Bwd w) {
       *reinterpret_cast<f32x4*>(dko + 16 * nt) = y;
     }
   }
-  // dL/dg_s without the cross-wave column sums
-  const float phi = s_ok ? 0.5f * ec * kp : 0.f;
-  float dg = 0.f;
-  if (s_ok) {
+  lds_barrier();       // the column sums, the feature halves' dot products, red[0..7]
+  // dL/dg_s (waves of the first feature half; the second has the same inputs)
+  float dg = 0.f, phi = 0.f;
+  if (fh == 0 && s_ok) {
+    const float* xo = xch + s * 4;
+    const float* xp = xch + (CB + s) * 4;
+    kl = xo[0] + xp[0];
+    kp = xo[1] + xp[1];
+    qhx = xo[2] + xp[2];
+    phi = 0.5f * ec * kp;
     const float f = w.fro[(int64_t)(b.tok0 + s) * H + h];
     dg = rowdm - fast_exp(gs) * qhx + SC(CS_A, s) * f * f - 0.5f * kl - phi;
+    dg -= SC(CS_COL0 + 0, s) + SC(CS_COL0 + 1, s) + SC(CS_COL0 + 2, s) + SC(CS_COL0 + 3, s);
   }
   // sum of phi over the block (for the last token)
   float ph = phi;
 #pragma unroll
   for (int m = 1; m < 16; m <<= 1) ph += __shfl_xor(ph, m, 64);
-  lds_barrier();       // the column sums, and every read of red[0..3]
-  const float dnh_all = red[0] + red[1] + red[2] + red[3];
+  float dnh_all = 0.f;
+#pragma unroll
+  for (int j = 0; j < C_NTHR / 64; ++j) dnh_all += red[j];
+  lds_barrier();       // every read of red[0..7]
+  if (fh == 0 && lane == 0) red[8 + cg] = ph;
   lds_barrier();
-  if (lane == 0) red[4 + wave] = ph;
-  lds_barrier();
-  if (s_ok) {
-    dg -= SC(CS_COL0 + 0, s) + SC(CS_COL0 + 1, s) + SC(CS_COL0 + 2, s) + SC(CS_COL0 + 3, s);
-    if (s == b.nval - 1) dg += 0.5f * fast_exp(Gam) * dnh_all + red[4] + red[5] + red[6] + red[7];
-  }
+  if (fh == 0 && s_ok && s == b.nval - 1)
+    dg += 0.5f * fast_exp(Gam) * dnh_all + red[8] + red[9] + red[10] + red[11];
   // dgk_u = sum_{t >= u} dL/dg_t within the block
-  if (q4 == 0) SC(CS_DG, s) = s_ok ? dg : 0.f;
+  if (fh == 0 && q4 == 0) SC(CS_DG, s) = s_ok ? dg : 0.f;
   lds_barrier();
   if (w.dgk && wave == 0 && lane < b.nval) {
     float acc = 0.f;
@@ -2383,7 +2406,7 @@ extern "C" int hmx_gka_cheb_bwd(const void* k, int64_t k_token_stride, const voi
   hipLaunchKernelGGL((solve::gka_solve_kernel<true, false, solve::SM_DQ>), grid, dim3(NTHR), 0, s, p);
   hipLaunchKernelGGL(train::cheb_e_kernel, grid, dim3(train::E_NTHR), 0, s, p, w);
   hipLaunchKernelGGL(train::cheb_dscan_kernel, dim3(N * H, 16), dim3(256), 0, s, p, w);
-  hipLaunchKernelGGL(train::cheb_dk_kernel, grid, dim3(NTHR), 0, s, p, w);
+  hipLaunchKernelGGL(train::cheb_dk_kernel, grid, dim3(train::C_NTHR), 0, s, p, w);
   return check_launch("hmx_gka_cheb_bwd");
 }
 
@@ -2520,7 +2543,7 @@ extern "C" int hmx_gka_train_bwd(const void* q, const void* k, const void* v, in
     hipLaunchKernelGGL((solve::gka_solve_kernel<true, false, solve::SM_DQ>), grid, dim3(NTHR), 0, s, pc);
     hipLaunchKernelGGL(train::cheb_e_kernel, grid, dim3(train::E_NTHR), 0, s, pc, cw);
     hipLaunchKernelGGL(train::cheb_dscan_kernel, sgrid, dim3(256), 0, s, pc, cw);
-    hipLaunchKernelGGL(train::cheb_dk_kernel, grid, dim3(NTHR), 0, s, pc, cw);
+    hipLaunchKernelGGL(train::cheb_dk_kernel, grid, dim3(train::C_NTHR), 0, s, pc, cw);
   }
   return check_launch("hmx_gka_train_bwd");
 }
