@@ -48,9 +48,10 @@ one buffer, the repeat_kv'd x and B and the per-head C are read in place from it
 by the SSD ops' grouped operands (no rearrange / repeat_kv / permute copies,
 :800-835, :972-985), the prefill scan reads and writes the state pool by slot (no
 gather and scatter, :812-824, :941), and both scans write ``output`` directly.
-The B/C RMSNorms run through the layer's own modules, as the reference calls
-them (:663-669).  Prefix caching (``mamba_cache_mode == "all"``) and the rotary
-position embedding (``use_pos_embed``) raise NotImplementedError.
+The B/C RMSNorms and the rotary position embedding of B and C
+(``use_pos_embed``) run through the layer's own modules, where and as the
+reference calls them (:663-671).  Prefix caching (``mamba_cache_mode == "all"``)
+raises NotImplementedError.
 """
 from __future__ import annotations
 
@@ -245,13 +246,16 @@ def gka_forward_core(layer, mixed_qkv: torch.Tensor, a: torch.Tensor, alpha_in: 
 
 def mamba2_conv_ssm_forward(layer, projected_states: torch.Tensor, output: torch.Tensor,
                             attn_metadata, conv_state: torch.Tensor,
-                            ssm_state: torch.Tensor, *, query_start_loc_cpu=None) -> None:
+                            ssm_state: torch.Tensor, *, query_start_loc_cpu=None,
+                            positions: torch.Tensor | None = None) -> None:
     """primed_mamba2_layer.py:615-1021 over hmx ops (see the module docstring).
 
     ``layer`` carries the reference's attributes (tped_intermediate_size,
     tped_conv_size, dt_pad, num_heads, tp_size, xb_size, ssm_state_size, head_dim,
     n_groups, conv_weights [conv_dim, W], conv1d.bias, activation, A, D, dt_bias,
-    B_norm / C_norm (or None), use_pos_embed, cache_config); ``attn_metadata`` is
+    B_norm / C_norm (or None), use_pos_embed with rotary_emb, cache_config);
+    ``positions`` are the tokens' positions the layer's forward receives (needed
+    with use_pos_embed); ``attn_metadata`` is
     the layer's Mamba2AttentionMetadata (num_prefills, num_decode_tokens,
     num_prefill_tokens, state_indices_tensor, has_initial_states_p,
     prep_initial_states, query_start_loc_p); ``conv_state`` is
@@ -268,9 +272,9 @@ def mamba2_conv_ssm_forward(layer, projected_states: torch.Tensor, output: torch
     if cc is not None and getattr(cc, "mamba_cache_mode", None) == "all":
         raise NotImplementedError("prefix caching (mamba_cache_mode 'all') is not supported by "
                                   "the hmx Mamba2 core")
-    if getattr(layer, "use_pos_embed", False):
-        raise NotImplementedError("the rotary position embedding (use_pos_embed) is not "
-                                  "supported by the hmx Mamba2 core")
+    rope = getattr(layer, "use_pos_embed", False)
+    if rope and positions is None:
+        raise ValueError("use_pos_embed needs the tokens' positions")
     tp = layer.tp_size
     I, CD = layer.tped_intermediate_size, layer.tped_conv_size
     H = layer.num_heads // tp
@@ -283,10 +287,13 @@ def mamba2_conv_ssm_forward(layer, projected_states: torch.Tensor, output: torch
                                   f"xb={xb}, H={H})")
     hbc = projected_states[:, I:I + CD]                  # :622-631
     dt = projected_states[:, I + CD:I + CD + H]          # dt_pad columns dropped (:633-634)
-    if layer.B_norm is not None:                         # :663-669
+    if layer.B_norm is not None or rope:                 # :663-671
         hs, B, C = torch.split(hbc, [xb, xb, CD - 2 * xb], dim=-1)
-        B = layer.B_norm(B.reshape(-1, layer.head_dim)).view(B.shape)
-        C = layer.C_norm(C.reshape(-1, layer.head_dim)).view(C.shape)
+        if layer.B_norm is not None:
+            B = layer.B_norm(B.reshape(-1, layer.head_dim)).view(B.shape)
+            C = layer.C_norm(C.reshape(-1, layer.head_dim)).view(C.shape)
+        if rope:
+            C, B = layer.rotary_emb(positions, C, B)
         hbc = torch.cat([hs, B, C], dim=-1)
     nd, npf = md.num_decode_tokens, md.num_prefills
     n = nd + md.num_prefill_tokens

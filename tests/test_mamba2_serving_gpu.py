@@ -108,6 +108,29 @@ class _RMSNorm:
         return y * self.weight
 
 
+class _Rope:
+    """Stand-in for the layer's vLLM rotary embedding (get_rope, primed_mamba2_layer.py
+    :555-566), called as rotary_emb(positions, C, B) -> (C, B): neox-style rotation of
+    every head_dim row, its halves (a, b) -> (a cos - b sin, b cos + a sin) at angle
+    position * 10000^(-2i/d), in fp32 and back to the input dtype."""
+
+    def __init__(self, d):
+        self.d = d
+
+    def _rot(self, positions, x):
+        d, half = self.d, self.d // 2
+        inv = 10000.0 ** (-torch.arange(half, device=x.device, dtype=torch.float32) * 2 / d)
+        ang = positions.float()[:, None] * inv[None]
+        cos, sin = ang.cos()[:, None], ang.sin()[:, None]
+        xr = x.float().view(x.shape[0], -1, d)
+        a, b = xr[..., :half], xr[..., half:]
+        y = torch.cat([a * cos - b * sin, b * cos + a * sin], dim=-1)
+        return y.to(x.dtype).view(x.shape)
+
+    def __call__(self, positions, q, k):
+        return self._rot(positions, q), self._rot(positions, k)
+
+
 def _layer(seed, dev):
     g0 = torch.Generator().manual_seed(seed)
     pad = (8 - (2 * I + 2 * XB + H) % 8) % 8
@@ -144,13 +167,15 @@ def _meta(kind, dev):
     return md, nd, plens, idx, has_p
 
 
-def _normed(lay, proj):
-    """The layer's own B/C RMSNorm step (:663-669), on proj's device: the norm
-    modules are the layer's, so the expected path applies them where the core
-    does (a reduction in another order could round differently)."""
+def _normed(lay, proj, positions=None):
+    """The layer's own B/C RMSNorm and rotary steps (:663-671), on proj's device: the
+    modules are the layer's, so the expected path applies them where the core does
+    (a reduction in another order could round differently)."""
     hs, B, C = torch.split(proj[:, I:I + CD], [XB, XB, CD - 2 * XB], dim=-1)
     B = lay.B_norm(B.reshape(-1, P)).view(B.shape)
     C = lay.C_norm(C.reshape(-1, P)).view(C.shape)
+    if lay.use_pos_embed:
+        C, B = lay.rotary_emb(positions, C, B)
     return torch.cat([hs, B, C], dim=-1)
 
 
@@ -179,9 +204,14 @@ def _expected(lay, nd, plens, idx, has_p, hbc, dt, conv_cache, pool):
     return torch.cat(outs), conv_new, pool_new
 
 
-@pytest.mark.parametrize("batch", ["mixed", "prefill", "decode"])
-def test_conv_ssm_forward_matches_oracle(dev, batch):
+@pytest.mark.parametrize("batch,rope", [("mixed", False), ("prefill", False), ("decode", False),
+                                        ("mixed", True)])
+def test_conv_ssm_forward_matches_oracle(dev, batch, rope):
+    """rope: use_pos_embed with the layer's rotary embedding of B and C before the
+    conv (primed_mamba2_layer.py:664-671)."""
     lay, dproj = _layer(1, dev)
+    lay.use_pos_embed = rope
+    lay.rotary_emb = _Rope(P)
     md, nd, plens, idx, has_p = _meta(batch, dev)
     n = nd + sum(plens)
     g0 = torch.Generator().manual_seed(20)
@@ -192,9 +222,12 @@ def test_conv_ssm_forward_matches_oracle(dev, batch):
     pool = torch.randn(SLOTS, H, P, N, generator=g0) * 0.1
     cc_d, pool_d = conv_cache.to(dev), pool.to(dev)
     output = torch.zeros(n + extra, I, dtype=torch.bfloat16, device=dev)
-    srv.mamba2_conv_ssm_forward(lay, proj.to(dev), output, md, cc_d.transpose(1, 2), pool_d)
+    positions = torch.randint(0, 4000, (n + extra,), generator=g0).to(dev)
+    srv.mamba2_conv_ssm_forward(lay, proj.to(dev), output, md, cc_d.transpose(1, 2), pool_d,
+                                positions=positions)
     torch.cuda.synchronize()
-    o_r, conv_r, pool_r = _expected(lay, nd, plens, idx, has_p, _normed(lay, proj.to(dev)).cpu(),
+    o_r, conv_r, pool_r = _expected(lay, nd, plens, idx, has_p,
+                                    _normed(lay, proj.to(dev), positions).cpu(),
                                     proj[:, I + CD:I + CD + H], conv_cache, pool)
     got = output.cpu()
     assert_out_close(got[:n].view(n, H, P), o_r)
@@ -214,6 +247,10 @@ def test_conv_ssm_forward_rejects_prefix_caching(dev):
     lay.cache_config.mamba_cache_mode = "all"
     md, *_ = _meta("decode", dev)
     with pytest.raises(NotImplementedError):
+        srv.mamba2_conv_ssm_forward(lay, None, None, md, None, None)
+    lay.cache_config.mamba_cache_mode = "none"
+    lay.use_pos_embed = True
+    with pytest.raises(ValueError):                 # the rotary embedding needs positions
         srv.mamba2_conv_ssm_forward(lay, None, None, md, None, None)
 
 
