@@ -201,6 +201,26 @@ def _(x, dt, A, B, C, chunk_size, cu_seqlens, out, D, z, dt_bias, initial_states
     return x.new_empty(cu_seqlens.shape[0] - 1, H, P, B.shape[-1], dtype=torch.float32)
 
 
+@torch.library.custom_op("hmx::mamba_chunk_scan_combined_varlen_chunks", mutates_args=("out",))
+def _ssd_varlen_chunks(x: Tensor, dt: Tensor, A: Tensor, B: Tensor, C: Tensor, chunk_size: int,
+                       cu_seqlens: Tensor, cu_chunk_seqlens: Tensor, seq_idx: Tensor, out: Tensor,
+                       D: Optional[Tensor], z: Optional[Tensor], dt_bias: Optional[Tensor],
+                       initial_states: Optional[Tensor], dt_softplus: bool, dt_min: float,
+                       dt_max: float) -> Tensor:
+    """The varlen scan returning the state after every chunk (prefix caching)."""
+    return ops.mamba_chunk_scan_combined_varlen(
+        x, dt, A, B, C, chunk_size, cu_seqlens, cu_chunk_seqlens=cu_chunk_seqlens,
+        seq_idx=seq_idx, out=out, D=D, z=z, dt_bias=dt_bias, initial_states=initial_states,
+        dt_softplus=dt_softplus, dt_limit=(dt_min, dt_max), return_intermediate_states=True)
+
+
+@_ssd_varlen_chunks.register_fake
+def _(x, dt, A, B, C, chunk_size, cu_seqlens, cu_chunk_seqlens, seq_idx, out, D, z, dt_bias,
+      initial_states, dt_softplus, dt_min, dt_max):
+    H, P = dt.shape[1], x.shape[2]
+    return x.new_empty(cu_chunk_seqlens.shape[0] - 1, H, P, B.shape[-1], dtype=torch.float32)
+
+
 
 
 @torch.library.custom_op("hmx::selective_state_update", mutates_args=("state", "out"))
@@ -320,11 +340,15 @@ def mamba_chunk_scan_combined_varlen(x, dt, A, B, C, chunk_size, cu_seqlens, cu_
                                      z=None, dt_bias=None, initial_states=None, dt_softplus=False,
                                      dt_limit=(0.0, float("inf")),
                                      return_intermediate_states=False, state_dtype=None):
-    """``torch.ops.hmx.mamba_chunk_scan_combined_varlen`` with vLLM's signature."""
-    if return_intermediate_states:
-        raise NotImplementedError("return_intermediate_states is not supported by hmx")
+    """``torch.ops.hmx.mamba_chunk_scan_combined_varlen`` with vLLM's signature
+    (return_intermediate_states through the ``_chunks`` op)."""
     if out is None:
         out = x.new_empty(x.shape[0], dt.shape[1], x.shape[2])
+    if return_intermediate_states:
+        st = torch.ops.hmx.mamba_chunk_scan_combined_varlen_chunks(
+            x, dt, A, B, C, int(chunk_size), cu_seqlens, cu_chunk_seqlens, seq_idx, out, D, z,
+            dt_bias, initial_states, bool(dt_softplus), float(dt_limit[0]), float(dt_limit[1]))
+        return st if state_dtype in (None, torch.float32) else st.to(state_dtype)
     st = torch.ops.hmx.mamba_chunk_scan_combined_varlen(
         x, dt, A, B, C, int(chunk_size), cu_seqlens, out, D, z, dt_bias, initial_states,
         bool(dt_softplus), float(dt_limit[0]), float(dt_limit[1]))

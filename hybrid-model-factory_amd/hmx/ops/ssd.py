@@ -40,14 +40,16 @@ def _prep3(t: torch.Tensor) -> torch.Tensor:
 
 
 def _ssd_scan(x, dt, A, B, C, D, z, dt_bias, dt_softplus, dt_limit, bounds, h0, y,
-              want_final: bool, segment_chunks=None, pooled=None):
+              want_final: bool, segment_chunks=None, pooled=None, seg_rows=None):
     """Core launcher over flattened tokens.  z, y [T,H,P]; dt [T,H]; x [T,HX,P],
     B [T,G,N], C [T,GC,N] with HX, G, GC dividing H (head h reads x head
     h // (H // HX), B group h // (H // G), C group h // (H // GC));
     bounds: list of (bos, eos); h0 fp32 [nseq,H,P,N] or None.  Returns the fp32 end
     states [nseq,H,P,N] (or None).  ``pooled`` = (pool, slot indices, has_initial_state
     or None): sequences read and (with want_final) write the pool's slots in place
-    instead, and the pool is returned."""
+    instead, and the pool is returned.  ``seg_rows`` (explicit segment rows, see
+    _chunk_rows) replaces the planner's table; the call then returns (states,
+    segment start states [rows,H,P,N] fp32 or None when no sequence has two)."""
     T, HX, P = x.shape
     H = dt.shape[1]
     G, N, GC = B.shape[1], B.shape[2], C.shape[1]
@@ -88,7 +90,10 @@ def _ssd_scan(x, dt, A, B, C, D, z, dt_bias, dt_softplus, dt_limit, bounds, h0, 
         hT = (torch.empty(nseq, H, P, N, dtype=torch.float32, device=x.device)
               if want_final else None)
         st_ss, st_dt = H * P * N, _lib.HMX_F32
-    rows, _ = _segment_table(_lib.PLAN_SSD, bounds, x.shape[0], H, x.device, segment_chunks)
+    if seg_rows is None:
+        rows, _ = _segment_table(_lib.PLAN_SSD, bounds, x.shape[0], H, x.device, segment_chunks)
+    else:
+        rows = seg_rows
     seg = _device_table(rows, x.device)
     lib = _lib.load()
     ws_bytes = int(lib.hmx_ssd_chunk_workspace_bytes(len(rows), nseq, H, P, N))
@@ -104,7 +109,43 @@ def _ssd_scan(x, dt, A, B, C, D, z, dt_bias, dt_softplus, dt_limit, bounds, h0, 
               _lib.ptr(idx), _lib.ptr(hinit),
               _lib.ptr(seg), len(rows), nseq, H, HX, G, GC, P, N, int(bool(dt_softplus)), lo, hi,
               _lib.ptr(ws), ws.numel(), _lib.stream_of(x))
-    return hT
+    if seg_rows is None:
+        return hT
+    starts = None
+    if len(rows) > nseq:     # the workspace: local end states, then the segment start states
+        st = len(rows) * H * P * N
+        starts = ws[:2 * st * 4].view(torch.float32)[st:].view(len(rows), H, P, N)
+    return hT, starts
+
+
+def _chunk_rows(cu_chunk, chunk_seq, bounds):
+    """Segment rows (n, bos, eos, c_start, c_end, seg_idx, first_seg, nseg) with one
+    segment per vLLM chunk [cu_chunk[c], cu_chunk[c+1]) of sequence chunk_seq[c]:
+    each segment walks its own 64-token tiles from its first token, and the
+    combine chains the segments of a sequence, so the start state of every chunk
+    (the end state of the one before) is formed.  Rejects chunks that are empty,
+    out of order or do not tile their sequences exactly."""
+    nch = len(chunk_seq)
+    if len(cu_chunk) != nch + 1:
+        raise ValueError(f"cu_chunk_seqlens must hold {nch + 1} offsets, got {len(cu_chunk)}")
+    rows, c = [], 0
+    for n, (bos, eos) in enumerate(bounds):
+        first, pos = c, bos
+        while c < nch and chunk_seq[c] == n:
+            a, e = cu_chunk[c], cu_chunk[c + 1]
+            if a != pos or e <= a or e > eos:
+                raise ValueError(f"chunk {c} [{a}, {e}) does not continue sequence {n} "
+                                 f"[{bos}, {eos}) at {pos}")
+            pos = e
+            c += 1
+        if pos != eos or (c == first and eos > bos):
+            raise ValueError(f"the chunks of sequence {n} do not cover [{bos}, {eos})")
+        for j in range(first, c):
+            a, e = cu_chunk[j], cu_chunk[j + 1]
+            rows.append((n, a, e, 0, (e - a + 63) // 64, j - first, first, c - first))
+    if c != nch:
+        raise ValueError("seq_idx must list the chunks' sequences in order")
+    return rows
 
 
 def _runs(row: list[int]) -> list[tuple[int, int]]:
@@ -204,8 +245,12 @@ def mamba_chunk_scan_combined_varlen(x, dt, A, B, C, chunk_size, cu_seqlens, cu_
     ``out`` [T,H,P] is written in place (allocated when None).  Returns
     varlen_states [n,H,P,N] in state_dtype (fp32 when None).  cu_chunk_seqlens,
     last_chunk_indices and seq_idx are chunking metadata derived from
-    cu_seqlens; the kernel uses its own 64-token chunks.  Per-chunk
-    (return_intermediate_states) output is not supported.
+    cu_seqlens; the kernel uses its own 64-token tiles.  With
+    return_intermediate_states (prefix caching, primed_mamba2_layer.py:862-921) the
+    return is instead the state after each chunk [nchunks,H,P,N] (state_dtype), the
+    chunks given by cu_chunk_seqlens and their sequences by seq_idx (one entry per
+    chunk): each chunk becomes one segment of the scan, whose combine forms every
+    chunk's start state (the scan's output y is unchanged).
 
     Keyword-only extension (no reference counterpart): with ``ssm_state_indices``
     [n], ``initial_states`` is the layer's state pool [slots,H,P,N] (fp32 or bf16):
@@ -221,9 +266,6 @@ def mamba_chunk_scan_combined_varlen(x, dt, A, B, C, chunk_size, cu_seqlens, cu_
     primed layer's repeat_kv'd x and B (primed_mamba2_layer.py:800-835) are read
     in place this way.
     """
-    if return_intermediate_states:
-        raise NotImplementedError("return_intermediate_states (prefix-cache chunk states) is "
-                                  "not supported by the hmx SSD scan")
     _lib.require_gpu(x, dt, A, B, C, D, z, dt_bias, initial_states, out)   # cu_seqlens: host or device
     T, P = x.shape[0], x.shape[2]
     H = dt.shape[1]
@@ -257,6 +299,30 @@ def mamba_chunk_scan_combined_varlen(x, dt, A, B, C, chunk_size, cu_seqlens, cu_
         out = torch.empty(T, H, P, dtype=x.dtype, device=x.device)
     if out.dtype != x.dtype:
         raise ValueError(f"out dtype {out.dtype} must match x dtype {x.dtype}")
+    if return_intermediate_states:
+        if cu_chunk_seqlens is None or seq_idx is None:
+            raise ValueError("return_intermediate_states needs cu_chunk_seqlens and seq_idx")
+        cc = [int(v) for v in cu_chunk_seqlens.tolist()]
+        cs_seq = [int(v) for v in seq_idx.reshape(-1).tolist()]
+        rows = _chunk_rows(cc, cs_seq, bounds)
+        hT, starts = _ssd_scan(x, dt, A, B, C, D, z, dt_bias, dt_softplus, dt_limit, bounds, h0,
+                               out, True, None, pooled, seg_rows=rows)
+        # the state after chunk c: the next chunk's start state, or its sequence's end state
+        nch = len(rows)
+        states = torch.empty(nch, H, P, N, dtype=torch.float32, device=x.device)
+        last = [i for i, r in enumerate(rows) if r[5] == r[7] - 1]
+        mid = [i for i, r in enumerate(rows) if r[5] < r[7] - 1]
+        if mid:
+            ti = lambda v: torch.tensor(v, dtype=torch.int64, device=x.device)
+            states[ti(mid)] = starts[ti([i + 1 for i in mid])]
+        if last:
+            ti = lambda v: torch.tensor(v, dtype=torch.int64, device=x.device)
+            seqs = ti([rows[i][0] for i in last])
+            fin = hT[pooled[1].long()[seqs]] if pooled is not None else hT[seqs]
+            states[ti(last)] = fin.to(torch.float32)
+        if last_chunk_indices is not None and [int(v) for v in last_chunk_indices.tolist()] != last:
+            raise ValueError("last_chunk_indices must index each sequence's last chunk")
+        return states if state_dtype in (None, torch.float32) else states.to(state_dtype)
     hT = _ssd_scan(x, dt, A, B, C, D, z, dt_bias, dt_softplus, dt_limit, bounds, h0, out, True,
                    _segment_chunks, pooled)
     if pooled is not None:

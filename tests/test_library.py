@@ -56,6 +56,11 @@ def test_fake_shapes_ssd():
         x[0], dt[0], A, Bm[0], Bm[0], 256, cu, torch.empty_like(x[0]), None, None, None, None, True,
         0.0, float("inf"))
     assert st.shape == (5, 8, 64, 128)
+    cc = torch.empty(9, device=M, dtype=torch.int32)
+    st = torch.ops.hmx.mamba_chunk_scan_combined_varlen_chunks(
+        x[0], dt[0], A, Bm[0], Bm[0], 256, cu, cc, cc[:8], torch.empty_like(x[0]), None, None,
+        None, None, True, 0.0, float("inf"))
+    assert st.shape == (8, 8, 64, 128)
 
 
 def test_backward_is_refused():

@@ -208,11 +208,89 @@ def test_errors(dev):
         hmx.mamba_chunk_scan_combined(*_d(dev, x[..., :32].contiguous(), dt, A, B, C), 256)
     with pytest.raises(RuntimeError):
         hmx.mamba_chunk_scan_combined(x, dt, A, B, C, 256)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(ValueError):                 # chunk states need the chunk metadata
         hmx.mamba_chunk_scan_combined_varlen(
             *_d(dev, x[0], dt[0], A, B[0], C[0]), 256,
             cu_seqlens=torch.tensor([0, 16], dtype=torch.int32, device=dev),
             return_intermediate_states=True)
+    with pytest.raises(ValueError):                 # chunks that do not tile the sequence
+        hmx.mamba_chunk_scan_combined_varlen(
+            *_d(dev, x[0], dt[0], A, B[0], C[0]), 256,
+            cu_seqlens=torch.tensor([0, 16], dtype=torch.int32, device=dev),
+            cu_chunk_seqlens=torch.tensor([0, 10], dtype=torch.int32),
+            seq_idx=torch.tensor([0], dtype=torch.int32), return_intermediate_states=True)
     with pytest.raises(ValueError):
         hmx.mamba_chunk_scan_combined(*_d(dev, x, dt, A, B, C), 256,
                                       initial_states=torch.zeros(2, 2, 64, 128, device=dev))
+
+
+def _prefix_chunks(lens, computed, chunk=256):
+    """vLLM's prefix-cache chunking (the metadata primed_mamba2_layer.py:862-921 reads):
+    chunk ends fall where the sequence's absolute position (num_computed_tokens plus
+    the offset) is a multiple of chunk, so a sequence's first chunk may be short."""
+    cu, seq, last, pos = [0], [], [], 0
+    for n, (L, nc) in enumerate(zip(lens, computed)):
+        off = 0
+        while off < L:
+            step = min(chunk - (nc + off) % chunk, L - off)
+            off += step
+            cu.append(pos + off)
+            seq.append(n)
+        pos += L
+        last.append(len(seq) - 1)
+    return cu, seq, last
+
+
+@pytest.mark.parametrize("pooled", [False, True])
+def test_varlen_intermediate_chunk_states(dev, pooled):
+    """return_intermediate_states (prefix caching): the state after every chunk of
+    cu_chunk_seqlens, each chunk's from the fp64 recurrence chained chunk by chunk
+    from the sequence's initial state; y as without it."""
+    H, P, N = 4, 64, 128
+    lens, computed = [300, 1, 640, 77], [100, 0, 256, 500]
+    T = sum(lens)
+    cs = [0] + list(torch.tensor(lens).cumsum(0).tolist())
+    cu_c, seq, last = _prefix_chunks(lens, computed)
+    g0 = torch.Generator().manual_seed(31)
+    x = torch.randn(T, H, P, generator=g0).bfloat16()
+    B = torch.randn(T, H, N, generator=g0).bfloat16()
+    C = torch.randn(T, H, N, generator=g0).bfloat16()
+    dt = torch.randn(T, H, generator=g0) * 0.5 - 2.0
+    bias = torch.randn(H, generator=g0) * 0.5 - 4.0
+    A = -torch.exp(torch.rand(H, generator=g0) * math.log(16))
+    D = torch.randn(H, generator=g0) * 0.1 + 1.0
+    h0 = torch.randn(len(lens), H, P, N, generator=g0) * 0.1
+    dtp = ref.dt_transform(dt, bias, True)
+    exp_states, y_r = [], torch.zeros(T, H, P, dtype=torch.float64)
+    for n in range(len(lens)):
+        S = h0[n]
+        for c in range(len(seq)):
+            if seq[c] != n:
+                continue
+            a, e = cu_c[c], cu_c[c + 1]
+            y_r[a:e], S = ref.ssd_seq(x[a:e], dtp[a:e], A, B[a:e], C[a:e], D, None, S)
+            exp_states.append(S)
+    exp_states = torch.stack(exp_states)
+    out = torch.empty(T, H, P, dtype=torch.bfloat16, device=dev)
+    kw = dict(cu_seqlens=torch.tensor(cs, dtype=torch.int32, device=dev),
+              cu_chunk_seqlens=torch.tensor(cu_c, dtype=torch.int32, device=dev),
+              seq_idx=torch.tensor(seq, dtype=torch.int32, device=dev),
+              last_chunk_indices=torch.tensor(last, dtype=torch.int32, device=dev), out=out,
+              D=D.to(dev), dt_bias=bias.to(dev), dt_softplus=True,
+              return_intermediate_states=True)
+    if pooled:
+        pool = torch.zeros(6, H, P, N, device=dev)
+        slots = torch.tensor([4, 0, 5, 2], dtype=torch.int32, device=dev)
+        pool[slots.long()] = h0.to(dev)
+        st = hmx.mamba_chunk_scan_combined_varlen(
+            *_d(dev, x, dt, A, B, C), 256, initial_states=pool, ssm_state_indices=slots, **kw)
+        for n in range(len(lens)):         # the pool holds each sequence's end state
+            assert_state_close(pool[int(slots[n])], exp_states[last[n]], what=f"pool slot {n}")
+    else:
+        st = hmx.mamba_chunk_scan_combined_varlen(*_d(dev, x, dt, A, B, C), 256,
+                                                  initial_states=h0.to(dev), **kw)
+    torch.cuda.synchronize()
+    assert st.shape == (len(seq), H, P, N)
+    assert_out_close(out, y_r, what="y")
+    for c in range(len(seq)):
+        assert_state_close(st[c], exp_states[c], what=f"chunk {c}")
