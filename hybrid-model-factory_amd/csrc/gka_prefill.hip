@@ -1294,10 +1294,12 @@ struct Bwd {
   const float* fro;       // [tokens][H]
   bf16* e;                // [nblk][H][D][D] bf16 tile-major: E_c, then Dn_c
   float* gam;             // [nblk][H] block totals of gk
-  float* dk;              // [tokens][H][D] (added to what it holds when dk_acc)
+  bf16* dk;               // [tokens][H][D] the gradient of k (+ dk_add when given)
+  const float* dk_add;    // null, or [tokens][H][D] fp32 added to dk
+  bf16* dq_out;           // [tokens][H][D] the gradient of the right-hand side (+ dq_add)
+  const float* dq_add;    // null, or [tokens][H][D] fp32 added to dq_out
   float* dgk;             // [tokens][H]
-  float* dq_out;          // null, or [tokens][H][D] that dq is added to
-  int bp_lambda, dk_acc;
+  int bp_lambda;
 };
 
 struct Blk { int s_id, lb, tok0, nval; };
@@ -1606,17 +1608,20 @@ __global__ __launch_bounds__(C_NTHR, 1) void cheb_dk_kernel(Params p, Bwd w) {
     mx[1] = fmaxf(mx[1], fmaxf(absmax4(q0[pass]), absmax4(q1[pass])));
     const float a = lambda_weight(p, w, b, row, h, q0[pass], q1[pass], xr[pass]);
     if (l16 == 0) SC(CS_A, row) = a;
-    if (w.dq_out && ok) {                 // the caller's dq += this solve's dq
-      float* o = w.dq_out + ro;
-      const f32x4 o0 = *reinterpret_cast<const f32x4*>(o), o1 = *reinterpret_cast<const f32x4*>(o + 4);
-      f32x4 y0, y1;
+    if (ok) {                             // the caller's dq: this solve's (+ dq_add), bf16
+      f32x4 y0 = q0[pass], y1 = q1[pass];
+      if (w.dq_add) {
+        const f32x4 o0 = *reinterpret_cast<const f32x4*>(w.dq_add + ro);
+        const f32x4 o1 = *reinterpret_cast<const f32x4*>(w.dq_add + ro + 4);
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        y0[v] = o0[v] + q0[pass][v];
-        y1[v] = o1[v] + q1[pass][v];
+        for (int v = 0; v < 4; ++v) {
+          y0[v] += o0[v];
+          y1[v] += o1[v];
+        }
       }
-      *reinterpret_cast<f32x4*>(o) = y0;
-      *reinterpret_cast<f32x4*>(o + 4) = y1;
+      *reinterpret_cast<bf16x8*>(w.dq_out + ro) =
+          bf16x8{(bf16)y0[0], (bf16)y0[1], (bf16)y0[2], (bf16)y0[3],
+                 (bf16)y1[0], (bf16)y1[1], (bf16)y1[2], (bf16)y1[3]};
     }
   }
 #pragma unroll
@@ -1806,19 +1811,19 @@ __global__ __launch_bounds__(C_NTHR, 1) void cheb_dk_kernel(Params p, Bwd w) {
   }
   // store this feature half of dk_s = DK + L + e^{Gam - g_s} P
   if (s_ok) {
-    float* dko = w.dk + ((int64_t)(b.tok0 + s) * H + h) * D + 4 * q4;
+    const int64_t dko = ((int64_t)(b.tok0 + s) * H + h) * D + 4 * q4;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int nt = 4 * fh + i;
       f32x4 y;
 #pragma unroll
       for (int v = 0; v < 4; ++v) y[v] = DK[i][v] + L[i][v] + ec * P[i][v];
-      if (w.dk_acc) {
-        const f32x4 o0 = *reinterpret_cast<const f32x4*>(dko + 16 * nt);
+      if (w.dk_add) {
+        const f32x4 o0 = *reinterpret_cast<const f32x4*>(w.dk_add + dko + 16 * nt);
 #pragma unroll
         for (int v = 0; v < 4; ++v) y[v] += o0[v];
       }
-      *reinterpret_cast<f32x4*>(dko + 16 * nt) = y;
+      *reinterpret_cast<bf16x4*>(w.dk + dko + 16 * nt) = bf4(y);
     }
   }
   lds_barrier();       // the column sums, the feature halves' dot products, red[0..7]
@@ -1876,7 +1881,9 @@ struct GlaBwd {
   const void* alpha; int alpha_dt;        // [tokens][H]
   bf16* e; float* gam;                    // as Bwd
   float* dx;                              // [tokens][H][D]: alpha du (the solve's dx)
-  float* dq; float* dk; float* dv;        // [tokens][H][D]
+  // [tokens][H][D]: dq and dk in fp32 when the solve's backward adds to them
+  // (dq32, dk32), else in bf16 (dq_bf, dk_bf); dv in bf16
+  float* dq32; float* dk32; bf16* dq_bf; bf16* dk_bf; bf16* dv;
   float* dalpha; float* dg;               // [tokens][H]
   float scale;
   int solve;                              // 0: num_iter == 0 (u = q, no x, alpha unused)
@@ -2134,7 +2141,8 @@ __global__ __launch_bounds__(NTHR, 1) void gla_bwd_kernel(Params p, GlaBwd w) {
         dxo[v] = al * du[v];
       }
       if (s_ok) {
-        *reinterpret_cast<f32x4*>(w.dq + ro + 16 * nt) = dqo;
+        if (w.dq32) *reinterpret_cast<f32x4*>(w.dq32 + ro + 16 * nt) = dqo;
+        else *reinterpret_cast<bf16x4*>(w.dq_bf + ro + 16 * nt) = bf4(dqo);
         if (w.solve) *reinterpret_cast<f32x4*>(w.dx + ro + 16 * nt) = dxo;
       }
     }
@@ -2201,7 +2209,10 @@ __global__ __launch_bounds__(NTHR, 1) void gla_bwd_kernel(Params p, GlaBwd w) {
         kdk += (float)kk[v] * y[v];
         kdkx += (float)kk[v] * xpart;
       }
-      if (s_ok) *reinterpret_cast<f32x4*>(w.dk + ro + 16 * nt) = y;
+      if (s_ok) {
+        if (w.dk32) *reinterpret_cast<f32x4*>(w.dk32 + ro + 16 * nt) = y;
+        else *reinterpret_cast<bf16x4*>(w.dk_bf + ro + 16 * nt) = bf4(y);
+      }
     }
     kdk += __shfl_xor(kdk, 16, 64);
     kdk += __shfl_xor(kdk, 32, 64);
@@ -2258,7 +2269,7 @@ __global__ __launch_bounds__(NTHR, 1) void gla_bwd_kernel(Params p, GlaBwd w) {
         f32x4 y;
 #pragma unroll
         for (int v = 0; v < 4; ++v) y[v] = ci * DV[nt][v] + cx * DX[nt][v];
-        *reinterpret_cast<f32x4*>(w.dv + ro + 16 * nt) = y;
+        *reinterpret_cast<bf16x4*>(w.dv + ro + 16 * nt) = bf4(y);
       }
     }
   }
@@ -2364,17 +2375,20 @@ extern "C" int hmx_gka_cheb_fwd(const void* k, int64_t k_token_stride, const voi
   return check_launch("hmx_gka_cheb_fwd");
 }
 
-extern "C" size_t hmx_gka_cheb_bwd_workspace_bytes(int32_t nblock_total, int32_t H) {
+// backward workspace: E/Dn (bf16), the blocks' gk totals, the solve's dq (fp32)
+extern "C" size_t hmx_gka_cheb_bwd_workspace_bytes(int32_t nblock_total, int32_t H,
+                                                   int64_t tokens) {
   return al256((size_t)nblock_total * H * D * D * sizeof(bf16)) +
-         al256((size_t)nblock_total * H * sizeof(float));
+         al256((size_t)nblock_total * H * sizeof(float)) +
+         al256((size_t)tokens * H * D * sizeof(float));
 }
 
 extern "C" int hmx_gka_cheb_bwd(const void* k, int64_t k_token_stride, const void* x,
                                 const void* dx, int64_t dx_token_stride, int32_t dtype,
-                                const void* gk, int32_t gk_dtype, const float* fro, float* dq,
-                                float* dk, float* dgk, const int32_t* seg_table,
+                                const void* gk, int32_t gk_dtype, const float* fro, void* dq,
+                                void* dk, float* dgk, const int32_t* seg_table,
                                 int32_t nseg_total, int32_t nblock_total, int32_t N, int32_t H,
-                                int32_t D_, int32_t num_iter, float ridge_ratio,
+                                int32_t D_, int64_t tokens, int32_t num_iter, float ridge_ratio,
                                 int32_t bp_lambda, void* fwd_workspace, size_t fwd_workspace_bytes,
                                 void* bwd_workspace, size_t bwd_workspace_bytes, void* stream) {
   Params p;
@@ -2386,20 +2400,23 @@ extern "C" int hmx_gka_cheb_bwd(const void* k, int64_t k_token_stride, const voi
                   (((uintptr_t)x | (uintptr_t)dq | (uintptr_t)dk) % 16) == 0,
               HMX_EINVAL, "hmx_gka_cheb_bwd: x, fro, dq, dk (16-byte aligned) and dgk (with gk) "
                           "are required");
-  const size_t need = hmx_gka_cheb_bwd_workspace_bytes(nblock_total, H);
-  HMX_REQUIRE(nblock_total == 0 || (bwd_workspace && bwd_workspace_bytes >= need), HMX_EINVAL,
-              "hmx_gka_cheb_bwd: backward workspace of %zu bytes needed, %zu given", need,
-              bwd_workspace_bytes);
+  const size_t need = hmx_gka_cheb_bwd_workspace_bytes(nblock_total, H, tokens);
+  HMX_REQUIRE(tokens >= 0 && (nblock_total == 0 || (bwd_workspace && bwd_workspace_bytes >= need)),
+              HMX_EINVAL, "hmx_gka_cheb_bwd: backward workspace of %zu bytes needed, %zu given",
+              need, bwd_workspace_bytes);
   if (nseg_total == 0 || nblock_total == 0) return HMX_OK;
+  char* bw = static_cast<char*>(bwd_workspace);
+  const size_t e_bytes = al256((size_t)nblock_total * H * D * D * sizeof(bf16));
+  float* dq32 = reinterpret_cast<float*>(bw + e_bytes + al256((size_t)nblock_total * H * sizeof(float)));
   p.fro = const_cast<float*>(fro);
-  p.xo32 = dq;
+  p.xo32 = dq32;
   train::Bwd w{};
   w.x = static_cast<const bf16*>(x);
-  w.dq = dq; w.fro = fro;
-  w.e = static_cast<bf16*>(bwd_workspace);
-  w.gam = reinterpret_cast<float*>(static_cast<char*>(bwd_workspace) +
-                                   al256((size_t)nblock_total * H * D * D * sizeof(bf16)));
-  w.dk = dk; w.dgk = gk ? dgk : nullptr;
+  w.dq = dq32; w.fro = fro;
+  w.e = reinterpret_cast<bf16*>(bw);
+  w.gam = reinterpret_cast<float*>(bw + e_bytes);
+  w.dk = static_cast<bf16*>(dk); w.dq_out = static_cast<bf16*>(dq);
+  w.dgk = gk ? dgk : nullptr;
   w.bp_lambda = bp_lambda;
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid(nblock_total, H);
@@ -2476,17 +2493,19 @@ extern "C" int hmx_gka_train_fwd(const void* q, const void* k, const void* v, in
   return check_launch("hmx_gka_train_fwd");
 }
 
+// backward workspace: the solve's backward workspace (with its dq), then dx, the
+// GLA's dq and dk (fp32)
 extern "C" size_t hmx_gka_train_bwd_workspace_bytes(int32_t nblock_total, int32_t H,
                                                     int64_t tokens) {
-  return hmx_gka_cheb_bwd_workspace_bytes(nblock_total, H) +
-         2 * al256((size_t)tokens * H * D * sizeof(float));
+  return hmx_gka_cheb_bwd_workspace_bytes(nblock_total, H, tokens) +
+         3 * al256((size_t)tokens * H * D * sizeof(float));
 }
 
 extern "C" int hmx_gka_train_bwd(const void* q, const void* k, const void* v, int32_t dtype,
                                  const void* alpha, int32_t alpha_dtype, const void* g,
                                  int32_t g_dtype, const void* gk, int32_t gk_dtype,
-                                 const void* x, const float* fro, const void* dout, float* dq,
-                                 float* dk, float* dv, float* dalpha, float* dg, float* dgk,
+                                 const void* x, const float* fro, const void* dout, void* dq,
+                                 void* dk, void* dv, float* dalpha, float* dg, float* dgk,
                                  const int32_t* seg_table, int32_t nseg_total,
                                  int32_t nblock_total, int32_t N, int32_t H, int32_t D_,
                                  int64_t tokens, int32_t num_iter, float ridge_ratio, float scale,
@@ -2513,7 +2532,8 @@ extern "C" int hmx_gka_train_bwd(const void* q, const void* k, const void* v, in
   if (nseg_total == 0 || nblock_total == 0) return HMX_OK;
   char* bw = static_cast<char*>(bwd_workspace);
   const size_t e_bytes = al256((size_t)nblock_total * H * D * D * sizeof(bf16));
-  const size_t cb_bytes = hmx_gka_cheb_bwd_workspace_bytes(nblock_total, H);
+  const size_t cb_bytes = hmx_gka_cheb_bwd_workspace_bytes(nblock_total, H, tokens);
+  const size_t tok_bytes = al256((size_t)tokens * H * D * sizeof(float));
   train::GlaBwd gw{};
   gw.q = static_cast<const bf16*>(q); gw.x = static_cast<const bf16*>(x);
   gw.v = static_cast<const bf16*>(v); gw.dout = static_cast<const bf16*>(dout);
@@ -2521,8 +2541,15 @@ extern "C" int hmx_gka_train_bwd(const void* q, const void* k, const void* v, in
   gw.e = reinterpret_cast<bf16*>(bw);
   gw.gam = reinterpret_cast<float*>(bw + e_bytes);
   gw.dx = reinterpret_cast<float*>(bw + cb_bytes);
-  float* dq_cheb = reinterpret_cast<float*>(bw + cb_bytes + al256((size_t)tokens * H * D * sizeof(float)));
-  gw.dq = dq; gw.dk = dk; gw.dv = dv; gw.dalpha = dalpha; gw.dg = dg;
+  float* dq_cheb = reinterpret_cast<float*>(bw + e_bytes + al256((size_t)nblock_total * H * sizeof(float)));
+  float* dq_gla = reinterpret_cast<float*>(bw + cb_bytes + tok_bytes);
+  float* dk_gla = reinterpret_cast<float*>(bw + cb_bytes + 2 * tok_bytes);
+  if (solve_) {           // the solve's backward adds its dq and dk, then writes bf16
+    gw.dq32 = dq_gla; gw.dk32 = dk_gla;
+  } else {
+    gw.dq_bf = static_cast<bf16*>(dq); gw.dk_bf = static_cast<bf16*>(dk);
+  }
+  gw.dv = static_cast<bf16*>(dv); gw.dalpha = dalpha; gw.dg = dg;
   gw.scale = scale; gw.solve = solve_;
   train::Bwd cw{};
   cw.e = gw.e; cw.gam = gw.gam;
@@ -2538,7 +2565,9 @@ extern "C" int hmx_gka_train_bwd(const void* q, const void* k, const void* v, in
     pc.fro = const_cast<float*>(fro);
     pc.xo32 = dq_cheb; pc.xo32_acc = 0;
     cw.x = gw.x; cw.dq = dq_cheb; cw.fro = fro;
-    cw.dk = dk; cw.dk_acc = 1; cw.dgk = gk ? dgk : nullptr; cw.dq_out = dq;
+    cw.dk = static_cast<bf16*>(dk); cw.dk_add = dk_gla;
+    cw.dq_out = static_cast<bf16*>(dq); cw.dq_add = dq_gla;
+    cw.dgk = gk ? dgk : nullptr;
     cw.bp_lambda = bp_lambda;
     hipLaunchKernelGGL((solve::gka_solve_kernel<true, false, solve::SM_DQ>), grid, dim3(NTHR), 0, s, pc);
     hipLaunchKernelGGL(train::cheb_e_kernel, grid, dim3(train::E_NTHR), 0, s, pc, cw);

@@ -61,9 +61,9 @@ SIGNATURES: dict[str, list] = {
     "hmx_gka_cheb_fwd": [_P, _I64, _P, _I64, _I32, _P, _I32, _P, _P, _P, _P, _I32, _I32, _I32,
                          _I32, _I32, _I32, _F32, _P, ctypes.c_size_t, _P],
     "hmx_gka_cheb_bwd": [_P, _I64, _P, _P, _I64, _I32, _P, _I32, _P, _P, _P, _P, _P, _I32, _I32,
-                         _I32, _I32, _I32, _I32, _F32, _I32, _P, ctypes.c_size_t, _P,
+                         _I32, _I32, _I32, _I64, _I32, _F32, _I32, _P, ctypes.c_size_t, _P,
                          ctypes.c_size_t, _P],
-    "hmx_gka_cheb_bwd_workspace_bytes": [_I32, _I32],
+    "hmx_gka_cheb_bwd_workspace_bytes": [_I32, _I32, _I64],
     "hmx_gka_train_fwd": [_P, _P, _P, _I32, _P, _I32, _P, _I32, _P, _I32, _P, _P, _P, _P, _P,
                           _P, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _F32, _P,
                           ctypes.c_size_t, _P],

@@ -103,19 +103,20 @@ class ChebyshevIteration(torch.autograd.Function):
         if dx is None:
             dx = torch.zeros_like(x)
         # the kernels read dx as bfloat16 rows (x's dtype, which autograd hands back)
+        # and write dq, dk in bf16 (k and q's dtype)
         dx2 = dx.to(torch.bfloat16).contiguous()
-        dq = torch.empty(B, T, H, D, dtype=torch.float32, device=dev)
+        dq = torch.empty(B, T, H, D, dtype=torch.bfloat16, device=dev)
         dk = torch.empty_like(dq)
         dgk = None if gk is None else torch.empty(B, T, H, dtype=torch.float32, device=dev)
         lib = _lib.load()
-        bws = torch.empty(max(int(lib.hmx_gka_cheb_bwd_workspace_bytes(nblk, H)), 16),
+        bws = torch.empty(max(int(lib.hmx_gka_cheb_bwd_workspace_bytes(nblk, H, B * T)), 16),
                           dtype=torch.uint8, device=dev)
         _lib.call("hmx_gka_cheb_bwd", _lib.ptr(k), H * D, _lib.ptr(x), _lib.ptr(dx2), H * D,
                   _lib.dtype_code(k), _lib.ptr(gk), 0 if gk is None else _lib.dtype_code(gk),
                   _lib.ptr(fro), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dgk), _lib.ptr(seg), nrows,
-                  nblk, B, H, D, num_iter, ridge, int(bp_lambda), _lib.ptr(ws), ws.numel(),
-                  _lib.ptr(bws), bws.numel(), _lib.stream_of(k))
-        return (dk.to(k.dtype), dq.to(q_dtype), None if dgk is None else dgk.to(gk_dtype),
+                  nblk, B, H, D, B * T, num_iter, ridge, int(bp_lambda), _lib.ptr(ws),
+                  ws.numel(), _lib.ptr(bws), bws.numel(), _lib.stream_of(k))
+        return (dk, dq.to(q_dtype), None if dgk is None else dgk.to(gk_dtype),
                 None, None, None, None, None, None)
 
 
@@ -182,7 +183,7 @@ class GkaChebyshevGla(torch.autograd.Function):
             do = torch.zeros_like(q)
         do2 = do.to(torch.bfloat16).contiguous()
         f32 = dict(dtype=torch.float32, device=dev)
-        dq, dk, dv = (torch.empty(B, T, H, D, **f32) for _ in range(3))
+        dq, dk, dv = (torch.empty(B, T, H, D, dtype=torch.bfloat16, device=dev) for _ in range(3))
         dg = torch.empty(B, T, H, **f32)
         dalpha = torch.empty(B, T, H, **f32) if n > 0 else None
         dgk = torch.empty(B, T, H, **f32) if (n > 0 and gk is not None) else None

@@ -376,11 +376,11 @@ int hmx_gka_cheb_fwd(const void* k, int64_t k_token_stride, const void* q,
 
 /* hmx_gka_cheb_bwd: the backward of hmx_gka_cheb_fwd on the same k, gk, seg_table
  * and forward workspace (unchanged since the forward), its x and fro, and dx
- * ([tokens][H][D] bf16 rows at dx_token_stride).  Writes dq, dk [tokens][H][D] f32
+ * ([tokens][H][D] bf16 rows at dx_token_stride).  Writes dq, dk [tokens][H][D] bf16
  * (contiguous) and, with gk, dgk [tokens][H] f32: dq solves for dx with the saved
  * |H_t|_F; dk, dgk follow from dL/dH_t = -dq_t x_t^T, minus
  * r (dq_t . x_t) H_t / |H_t|_F when bp_lambda.  bwd_workspace:
- * hmx_gka_cheb_bwd_workspace_bytes(nblock_total, H) bytes.
+ * hmx_gka_cheb_bwd_workspace_bytes(nblock_total, H, tokens) bytes.
  * Replaces: ChebyshevIteration.backward
  *   training/.../ops/chebyshev/chebyshev_iteration.py:606-688 (with
  *   chunk_dk_backward.py:372-445, chunk_dk_backward_gating.py:287-373,
@@ -389,12 +389,13 @@ int hmx_gka_cheb_fwd(const void* k, int64_t k_token_stride, const void* q,
  */
 int hmx_gka_cheb_bwd(const void* k, int64_t k_token_stride, const void* x, const void* dx,
                      int64_t dx_token_stride, int32_t dtype, const void* gk, int32_t gk_dtype,
-                     const float* fro, float* dq, float* dk, float* dgk,
+                     const float* fro, void* dq, void* dk, float* dgk,
                      const int32_t* seg_table, int32_t nseg_total, int32_t nblock_total,
-                     int32_t N, int32_t H, int32_t D, int32_t num_iter, float ridge_ratio,
-                     int32_t bp_lambda, void* fwd_workspace, size_t fwd_workspace_bytes,
-                     void* bwd_workspace, size_t bwd_workspace_bytes, void* stream);
-size_t hmx_gka_cheb_bwd_workspace_bytes(int32_t nblock_total, int32_t H);
+                     int32_t N, int32_t H, int32_t D, int64_t tokens, int32_t num_iter,
+                     float ridge_ratio, int32_t bp_lambda, void* fwd_workspace,
+                     size_t fwd_workspace_bytes, void* bwd_workspace, size_t bwd_workspace_bytes,
+                     void* stream);
+size_t hmx_gka_cheb_bwd_workspace_bytes(int32_t nblock_total, int32_t H, int64_t tokens);
 
 /* hmx_gka_train_fwd: the training GKA forward in one pass: the Chebyshev solve
  * (as hmx_gka_cheb_fwd), the blend u = q + alpha (x - q) and the GLA readout
@@ -418,7 +419,7 @@ int hmx_gka_train_fwd(const void* q, const void* k, const void* v, int32_t dtype
                       size_t workspace_bytes, void* stream);
 
 /* hmx_gka_train_bwd: the backward of hmx_gka_train_fwd (same inputs, its x, fro and
- * workspace) for dout [tokens][H][D] bf16: writes dq, dk, dv [tokens][H][D] f32, dg
+ * workspace) for dout [tokens][H][D] bf16: writes dq, dk, dv [tokens][H][D] bf16, dg
  * [tokens][H] f32 and, when num_iter > 0, dalpha and (with gk) dgk [tokens][H] f32.
  * The GLA readout's backward gives du, dk, dv, dg; dx = alpha du feeds the solve's
  * backward (as hmx_gka_cheb_bwd) whose dq and dk are added.  Gradients of the
@@ -431,7 +432,7 @@ int hmx_gka_train_fwd(const void* q, const void* k, const void* v, int32_t dtype
 int hmx_gka_train_bwd(const void* q, const void* k, const void* v, int32_t dtype,
                       const void* alpha, int32_t alpha_dtype, const void* g, int32_t g_dtype,
                       const void* gk, int32_t gk_dtype, const void* x, const float* fro,
-                      const void* dout, float* dq, float* dk, float* dv, float* dalpha,
+                      const void* dout, void* dq, void* dk, void* dv, float* dalpha,
                       float* dg, float* dgk, const int32_t* seg_table, int32_t nseg_total,
                       int32_t nblock_total, int32_t N, int32_t H, int32_t D, int64_t tokens,
                       int32_t num_iter, float ridge_ratio, float scale, int32_t bp_lambda,
