@@ -1975,11 +1975,16 @@ __global__ __launch_bounds__(NTHR, 2) void gla_e_kernel(Params p, GlaBwd w) {
 constexpr int GB_OFF_K = 0, GB_OFF_V = SZ_K, GB_OFF_DO = 2 * SZ_K, GB_OFF_U = 3 * SZ_K;
 constexpr int GB_OFF_S = 4 * SZ_K, GB_OFF_DS = GB_OFF_S + SZ_H, GB_OFF_SC = GB_OFF_DS + SZ_H;
 enum { GS_G, GS_DG, NGS };
-constexpr int GB_SMEM = GB_OFF_SC + NGS * CB * 4 + 32 * 4;
+// 8 waves: wave w takes the 16 columns s of group w & 3 and the feature half w >> 2
+constexpr int GB_NTHR = 512;
+constexpr int GB_OFF_RED = GB_OFF_SC + NGS * CB * 4;       // 16 floats of cross-wave sums
+constexpr int GB_OFF_MS = GB_OFF_RED + 16 * 4;             // 24 floats for block_max
+constexpr int GB_OFF_XCH = GB_OFF_MS + 24 * 4;             // [2][64][4] feature-half dot products
+constexpr int GB_SMEM = GB_OFF_XCH + 2 * CB * 4 * 4;
 static_assert(GB_SMEM <= 160 * 1024, "LDS budget");
 
 // du (-> dx, dq, dalpha), dk, dv, dg of block gb (see the section comment)
-__global__ __launch_bounds__(NTHR, 1) void gla_bwd_kernel(Params p, GlaBwd w) {
+__global__ __launch_bounds__(GB_NTHR, 1) void gla_bwd_kernel(Params p, GlaBwd w) {
   __shared__ __align__(16) unsigned char smem[GB_SMEM];
   f16* sK = reinterpret_cast<f16*>(smem + GB_OFF_K);
   f16* sV = reinterpret_cast<f16*>(smem + GB_OFF_V);
@@ -1988,19 +1993,22 @@ __global__ __launch_bounds__(NTHR, 1) void gla_bwd_kernel(Params p, GlaBwd w) {
   f16* sS = reinterpret_cast<f16*>(smem + GB_OFF_S);      // S_c^T: rows V, columns K
   f16* sDS = reinterpret_cast<f16*>(smem + GB_OFF_DS);    // dSn: rows K, columns V
   float* sc = reinterpret_cast<float*>(smem + GB_OFF_SC);
-  float* red = sc + NGS * CB;            // 8 floats of cross-wave sums
-  float* mslot = red + 8;                // 12 floats for block_max
+  float* red = reinterpret_cast<float*>(smem + GB_OFF_RED);
+  float* mslot = reinterpret_cast<float*>(smem + GB_OFF_MS);
+  float* xch = reinterpret_cast<float*>(smem + GB_OFF_XCH);
   auto SC = [&](int slot, int t) -> float& { return sc[slot * CB + t]; };
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int cg = wave & 3, fh = wave >> 2;   // column group, feature half (nt 4 fh .. 4 fh + 3)
   const int q4 = lane >> 4, l16 = lane & 15;
   const int gb = blockIdx.x, h = blockIdx.y, H = p.H;
   const Blk b = block_of(p, gb);
   if (b.nval <= 0) return;
   const int64_t DD = (int64_t)D * D;
+  constexpr int NP = CB * 16 / GB_NTHR;    // staging passes of 32 rows
 
   // S_c (as the solve forms it: zero-start block state + decayed segment start)
-  {
+  if (tid < NTHR) {
     const int64_t so = ((int64_t)b.s_id * H + h) * DD;
     const int64_t bso = ((int64_t)gb * H + h) * DD;
     StateLd sst;
@@ -2015,15 +2023,15 @@ __global__ __launch_bounds__(NTHR, 1) void gla_bwd_kernel(Params p, GlaBwd w) {
   }
   lds_barrier();
   // rows k, v (fp16 as given), do and u (scaled); dSn (scaled) and <dSn, S_c>
-  bf16x8 kr[CB / 16], vr[CB / 16], dr[CB / 16];
-  f32x4 u0[CB / 16], u1[CB / 16];
+  bf16x8 kr[NP], vr[NP], dr[NP];
+  f32x4 u0[NP], u1[NP];
   const bf16* dn = w.e + ((int64_t)gb * H + h) * DD;
-  const int drw = tid >> 1, dc0 = (tid & 1) * 64;
-  f32x4 dsv[16];
+  const int drw = tid >> 2, dc0 = (tid & 3) * 32;    // this thread's dSn: row drw, columns dc0..+31
+  f32x4 dsv[8];
   float mx[3] = {0.f, 0.f, 0.f};          // max |do|, |u|, |dSn|
 #pragma unroll
-  for (int pass = 0; pass < CB / 16; ++pass) {
-    const int row = pass * 16 + (tid >> 4), f0 = (tid & 15) * 8;
+  for (int pass = 0; pass < NP; ++pass) {
+    const int row = pass * 32 + (tid >> 4), f0 = (tid & 15) * 8;
     const bool ok = row < b.nval;
     const int64_t ti = (int64_t)(b.tok0 + row) * H + h, ro = ti * D + f0;
     kr[pass] = ok ? *reinterpret_cast<const bf16x8*>(p.k + (int64_t)(b.tok0 + row) * p.kv_ts + h * D + f0) : bf16x8{};
@@ -2041,15 +2049,15 @@ __global__ __launch_bounds__(NTHR, 1) void gla_bwd_kernel(Params p, GlaBwd w) {
     mx[1] = fmaxf(mx[1], fmaxf(absmax4(u0[pass]), absmax4(u1[pass])));
   }
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
+  for (int j = 0; j < 8; ++j) {
     dsv[j] = f4(*reinterpret_cast<const bf16x4*>(dn + blk_index(drw, dc0 + 4 * j)));
     mx[2] = fmaxf(mx[2], absmax4(dsv[j]));
   }
-  block_max(mx, mslot, wave, lane);
+  block_max<3, GB_NTHR / 64>(mx, mslot, wave, lane);
   const float sdo = pow2_scale(mx[0]), su = pow2_scale(mx[1]), sds = pow2_scale(mx[2]);
 #pragma unroll
-  for (int pass = 0; pass < CB / 16; ++pass) {
-    const int row = pass * 16 + (tid >> 4), f0 = (tid & 15) * 8;
+  for (int pass = 0; pass < NP; ++pass) {
+    const int row = pass * 32 + (tid >> 4), f0 = (tid & 15) * 8;
     store8_i(sK + row * LDP, f0, scale_h8(kr[pass], 1.f));
     store8_i(sV + row * LDP, f0, scale_h8(vr[pass], 1.f));
     store8_i(sDo + row * LDP, f0, scale_h8(dr[pass], sdo));
@@ -2057,7 +2065,7 @@ __global__ __launch_bounds__(NTHR, 1) void gla_bwd_kernel(Params p, GlaBwd w) {
   }
   float dss = 0.f;                        // <dSn, S_c> over this thread's elements
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
+  for (int j = 0; j < 8; ++j) {
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int c = dc0 + 4 * j + v;      // V index; S_c^T[c][drw] in sS
@@ -2065,34 +2073,35 @@ __global__ __launch_bounds__(NTHR, 1) void gla_bwd_kernel(Params p, GlaBwd w) {
     }
   }
 #pragma unroll
-  for (int j = 0; j < 8; ++j)
+  for (int j = 0; j < 4; ++j)
     store8_i(sDS + drw * LDP, dc0 + 8 * j, h8_of(dsv[2 * j], dsv[2 * j + 1], sds));
   dss = wave_sum(dss);
   if (lane == 0) red[wave] = dss;
   lds_barrier();
 
-  const int s = 16 * wave + l16;          // this lane's token / key column
+  const int s = 16 * cg + l16;            // this lane's token / key column
   const bool s_ok = s < b.nval;
   const float Gs = SC(GS_G, s), Gam = SC(GS_G, b.nval - 1);
   const float ec = fast_exp(Gam - Gs), egs = fast_exp(Gs);
   const int64_t ti = (int64_t)(b.tok0 + s) * H + h;
   const int64_t ro = ti * D + 4 * q4;     // + 16 nt: features 16 nt + 4 q4 .. +3
-  float dG = 0.f;
+  float* xo = xch + (fh * CB + s) * 4;    // this half's dot products of column s
 
-  // ---- du (rows f = K, column t = s) -------------------------------------
+  // ---- du (rows f = K of this half, column t = s) ---------------------------
   {
-    f32x4 DQ[8], DI[8];
+    f32x4 DQ[4], DI[4];
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
-      DQ[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      DI[nt] = DQ[nt];
+    for (int i = 0; i < 4; ++i) {
+      DQ[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      DI[i] = DQ[i];
     }
     // S_c do_t: A = S_c rows (K) over V, read transposed from S_c^T
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      const f16x8 bd = frag_i(sDo, LDP, 16 * wave, 32 * ks, lane);
+      const f16x8 bd = frag_i(sDo, LDP, 16 * cg, 32 * ks, lane);
 #pragma unroll
-      for (int nt = 0; nt < 8; ++nt) DQ[nt] = mfma16h(frag_t_i(sS, LDP, 32 * ks, 16 * nt, lane), bd, DQ[nt]);
+      for (int i = 0; i < 4; ++i)
+        DQ[i] = mfma16h(frag_t_i(sS, LDP, 32 * ks, 16 * (4 * fh + i), lane), bd, DQ[i]);
     }
     // P[j][t] = e^{G_t-G_j} (do_t.v_j), j <= t: rows j over the block, column t
     f16x8 pb[2];
@@ -2102,7 +2111,7 @@ __global__ __launch_bounds__(NTHR, 1) void gla_bwd_kernel(Params p, GlaBwd w) {
       for (int jt = 0; jt < 4; ++jt) P[jt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        const f16x8 bd = frag_i(sDo, LDP, 16 * wave, 32 * ks, lane);
+        const f16x8 bd = frag_i(sDo, LDP, 16 * cg, 32 * ks, lane);
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt) P[jt] = mfma16h(frag_i(sV, LDP, 16 * jt, 32 * ks, lane), bd, P[jt]);
       }
@@ -2121,19 +2130,21 @@ __global__ __launch_bounds__(NTHR, 1) void gla_bwd_kernel(Params p, GlaBwd w) {
 #pragma unroll
     for (int jk = 0; jk < 2; ++jk)
 #pragma unroll
-      for (int nt = 0; nt < 8; ++nt) DI[nt] = mfma16h(frag_t_i(sK, LDP, 32 * jk, 16 * nt, lane), pb[jk], DI[nt]);
-    // du = scale (e^{G_t} DQ + DI) / sdo; dx, dq, dalpha and u.du
+      for (int i = 0; i < 4; ++i)
+        DI[i] = mfma16h(frag_t_i(sK, LDP, 32 * jk, 16 * (4 * fh + i), lane), pb[jk], DI[i]);
+    // du = scale (e^{G_t} DQ + DI) / sdo; dx, dq, dalpha and u.du over this half
     const float cu = w.scale / sdo;
     const float al = s_ok ? gla_alpha(w, ti) : 0.f;
     float dal = 0.f, udu = 0.f;
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
+    for (int i = 0; i < 4; ++i) {
+      const int nt = 4 * fh + i;
       const bf16x4 qv = s_ok ? *reinterpret_cast<const bf16x4*>(w.q + ro + 16 * nt) : bf16x4{};
       const bf16x4 xv = (s_ok && w.solve) ? *reinterpret_cast<const bf16x4*>(w.x + ro + 16 * nt) : bf16x4{};
       f32x4 du, dqo, dxo;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        du[v] = cu * (egs * DQ[nt][v] + DI[nt][v]);
+        du[v] = cu * (egs * DQ[i][v] + DI[i][v]);
         const float qf = (float)qv[v], xf = (float)xv[v];
         dal += du[v] * (xf - qf);
         udu += du[v] * (qf + al * (xf - qf));
@@ -2150,17 +2161,18 @@ __global__ __launch_bounds__(NTHR, 1) void gla_bwd_kernel(Params p, GlaBwd w) {
     dal += __shfl_xor(dal, 32, 64);
     udu += __shfl_xor(udu, 16, 64);
     udu += __shfl_xor(udu, 32, 64);
-    if (s_ok && q4 == 0 && w.solve) w.dalpha[ti] = dal;
-    dG += udu;
+    if (q4 == 0) {
+      xo[0] = udu;
+      xo[1] = dal;
+    }
   }
-  // ---- dk (rows f = K, column s) --------------------------------------------
-  float kdkx = 0.f;                       // k_s . (dSn v_s) e^{Gam-G_s}
+  // ---- dk (rows f = K of this half, column s) ----------------------------------
   {
-    f32x4 DK[8], DX[8];
+    f32x4 DK[4], DX[4];
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
-      DK[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      DX[nt] = DK[nt];
+    for (int i = 0; i < 4; ++i) {
+      DK[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      DX[i] = DK[i];
     }
     // R[t][s] = e^{G_t-G_s} (do_t.v_s), t >= s
     f16x8 rb[2];
@@ -2170,7 +2182,7 @@ __global__ __launch_bounds__(NTHR, 1) void gla_bwd_kernel(Params p, GlaBwd w) {
       for (int tt = 0; tt < 4; ++tt) R[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        const f16x8 bv = frag_i(sV, LDP, 16 * wave, 32 * ks, lane);
+        const f16x8 bv = frag_i(sV, LDP, 16 * cg, 32 * ks, lane);
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt) R[tt] = mfma16h(frag_i(sDo, LDP, 16 * tt, 32 * ks, lane), bv, R[tt]);
       }
@@ -2189,23 +2201,26 @@ __global__ __launch_bounds__(NTHR, 1) void gla_bwd_kernel(Params p, GlaBwd w) {
 #pragma unroll
     for (int jk = 0; jk < 2; ++jk)
 #pragma unroll
-      for (int nt = 0; nt < 8; ++nt) DK[nt] = mfma16h(frag_t_i(sU, LDP, 32 * jk, 16 * nt, lane), rb[jk], DK[nt]);
+      for (int i = 0; i < 4; ++i)
+        DK[i] = mfma16h(frag_t_i(sU, LDP, 32 * jk, 16 * (4 * fh + i), lane), rb[jk], DK[i]);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      const f16x8 bv = frag_i(sV, LDP, 16 * wave, 32 * ks, lane);
+      const f16x8 bv = frag_i(sV, LDP, 16 * cg, 32 * ks, lane);
 #pragma unroll
-      for (int nt = 0; nt < 8; ++nt) DX[nt] = mfma16h(frag_i(sDS, LDP, 16 * nt, 32 * ks, lane), bv, DX[nt]);
+      for (int i = 0; i < 4; ++i)
+        DX[i] = mfma16h(frag_i(sDS, LDP, 16 * (4 * fh + i), 32 * ks, lane), bv, DX[i]);
     }
     const float ci = w.scale / (su * sdo), cx = ec / sds;
-    float kdk = 0.f;
+    float kdk = 0.f, kdkx = 0.f;
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
+    for (int i = 0; i < 4; ++i) {
+      const int nt = 4 * fh + i;
       const f16x4 kk = *reinterpret_cast<const f16x4*>(sK + s * LDP + icol(16 * nt + 4 * q4));
       f32x4 y;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const float xpart = cx * DX[nt][v];
-        y[v] = ci * DK[nt][v] + xpart;
+        const float xpart = cx * DX[i][v];
+        y[v] = ci * DK[i][v] + xpart;
         kdk += (float)kk[v] * y[v];
         kdkx += (float)kk[v] * xpart;
       }
@@ -2218,15 +2233,18 @@ __global__ __launch_bounds__(NTHR, 1) void gla_bwd_kernel(Params p, GlaBwd w) {
     kdk += __shfl_xor(kdk, 32, 64);
     kdkx += __shfl_xor(kdkx, 16, 64);
     kdkx += __shfl_xor(kdkx, 32, 64);
-    dG -= kdk;
+    if (q4 == 0) {
+      xo[2] = kdk;
+      xo[3] = kdkx;
+    }
   }
-  // ---- dv (rows f = V, column s) --------------------------------------------
+  // ---- dv (rows f = V of this half, column s) ----------------------------------
   {
-    f32x4 DV[8], DX[8];
+    f32x4 DV[4], DX[4];
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
-      DV[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      DX[nt] = DV[nt];
+    for (int i = 0; i < 4; ++i) {
+      DV[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      DX[i] = DV[i];
     }
     // U[t][s] = e^{G_t-G_s} (u_t.k_s), t >= s
     f16x8 ub[2];
@@ -2236,7 +2254,7 @@ __global__ __launch_bounds__(NTHR, 1) void gla_bwd_kernel(Params p, GlaBwd w) {
       for (int tt = 0; tt < 4; ++tt) U[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        const f16x8 bk = frag_i(sK, LDP, 16 * wave, 32 * ks, lane);
+        const f16x8 bk = frag_i(sK, LDP, 16 * cg, 32 * ks, lane);
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt) U[tt] = mfma16h(frag_i(sU, LDP, 16 * tt, 32 * ks, lane), bk, U[tt]);
       }
@@ -2255,34 +2273,47 @@ __global__ __launch_bounds__(NTHR, 1) void gla_bwd_kernel(Params p, GlaBwd w) {
 #pragma unroll
     for (int jk = 0; jk < 2; ++jk)
 #pragma unroll
-      for (int nt = 0; nt < 8; ++nt) DV[nt] = mfma16h(frag_t_i(sDo, LDP, 32 * jk, 16 * nt, lane), ub[jk], DV[nt]);
+      for (int i = 0; i < 4; ++i)
+        DV[i] = mfma16h(frag_t_i(sDo, LDP, 32 * jk, 16 * (4 * fh + i), lane), ub[jk], DV[i]);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      const f16x8 bk = frag_i(sK, LDP, 16 * wave, 32 * ks, lane);
+      const f16x8 bk = frag_i(sK, LDP, 16 * cg, 32 * ks, lane);
 #pragma unroll
-      for (int nt = 0; nt < 8; ++nt) DX[nt] = mfma16h(frag_t_i(sDS, LDP, 32 * ks, 16 * nt, lane), bk, DX[nt]);
+      for (int i = 0; i < 4; ++i)
+        DX[i] = mfma16h(frag_t_i(sDS, LDP, 32 * ks, 16 * (4 * fh + i), lane), bk, DX[i]);
     }
     const float ci = w.scale / (su * sdo), cx = ec / sds;
     if (s_ok) {
 #pragma unroll
-      for (int nt = 0; nt < 8; ++nt) {
+      for (int i = 0; i < 4; ++i) {
         f32x4 y;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) y[v] = ci * DV[nt][v] + cx * DX[nt][v];
-        *reinterpret_cast<bf16x4*>(w.dv + ro + 16 * nt) = bf4(y);
+        for (int v = 0; v < 4; ++v) y[v] = ci * DV[i][v] + cx * DX[i][v];
+        *reinterpret_cast<bf16x4*>(w.dv + ro + 16 * (4 * fh + i)) = bf4(y);
       }
     }
   }
+  lds_barrier();       // both halves' dot products, red[0..7]
   // ---- dg: dL/dG_t, the last token's <dSn, S_{c+1}>, the in-block reverse cumsum
-  float kx = s_ok ? kdkx : 0.f;
+  float dG = 0.f, kx = 0.f;
+  if (fh == 0 && s_ok) {
+    const float* xa = xch + s * 4;
+    const float* xb = xch + (CB + s) * 4;
+    dG = (xa[0] + xb[0]) - (xa[2] + xb[2]);
+    kx = xa[3] + xb[3];
+    if (q4 == 0 && w.solve) w.dalpha[ti] = xa[1] + xb[1];
+  }
 #pragma unroll
   for (int m = 1; m < 16; m <<= 1) kx += __shfl_xor(kx, m, 64);
-  if (lane == 0) red[4 + wave] = kx;
+  float dss_all = 0.f;
+#pragma unroll
+  for (int j = 0; j < GB_NTHR / 64; ++j) dss_all += red[j];
+  lds_barrier();       // every read of red[0..7]
+  if (fh == 0 && lane == 0) red[8 + cg] = kx;
   lds_barrier();
-  if (s_ok && q4 == 0) {
+  if (fh == 0 && s_ok && q4 == 0) {
     float d = dG;
-    if (s == b.nval - 1)
-      d += fast_exp(Gam) * (red[0] + red[1] + red[2] + red[3]) + red[4] + red[5] + red[6] + red[7];
+    if (s == b.nval - 1) d += fast_exp(Gam) * dss_all + red[8] + red[9] + red[10] + red[11];
     SC(GS_DG, s) = d;
   }
   lds_barrier();
@@ -2557,7 +2588,7 @@ extern "C" int hmx_gka_train_bwd(const void* q, const void* k, const void* v, in
   const dim3 grid(nblock_total, H), sgrid(N * H, 16);
   hipLaunchKernelGGL(train::gla_e_kernel, grid, dim3(NTHR), 0, s, p, gw);
   hipLaunchKernelGGL(train::cheb_dscan_kernel, sgrid, dim3(256), 0, s, p, cw);
-  hipLaunchKernelGGL(train::gla_bwd_kernel, grid, dim3(NTHR), 0, s, p, gw);
+  hipLaunchKernelGGL(train::gla_bwd_kernel, grid, dim3(train::GB_NTHR), 0, s, p, gw);
   if (solve_) {
     // the solve's backward on dx = alpha du: its dq is added to dq, its dk to dk
     Params pc = p;
