@@ -130,6 +130,9 @@ struct Params {
   const bf16* zg; int64_t zg_ts, zg_hs;   // gate rows, or null (plain RMSNorm)
   const void* onw; int onw_dt;            // weight [D]
   float on_eps;
+  // training: the fp16 state entering each output chunk, [cu_chunk[n] + c][H][D][D]
+  f16* ws_hc = nullptr;
+  const int* cu_chunk = nullptr;
 };
 
 __device__ __forceinline__ float ld_scalar(const void* p, int64_t i, int dt) {
@@ -559,6 +562,17 @@ __device__ __forceinline__ void chunk_walk(const Params& p, unsigned char* smem,
       const Stage cur = stage_at(smem, bi);
       const int tok0 = si.bos + c * C;
       const bool out_chunk = (MODE == MODE_OUT) && (c >= c_out);
+      if (MODE == MODE_OUT && out_chunk && p.ws_hc) {
+        // the state entering this chunk, fp16 row-major (the backward's S0)
+        f16* dst = p.ws_hc + ((int64_t)(p.cu_chunk[si.n] + c) * H + h) * D * D + 32 * wave + l16;
+#pragma unroll
+        for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+          for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+              dst[(16 * rt + 4 * q4 + v) * D + 16 * ct] = (f16)S[rt][ct][v];
+      }
 
       // ---- phase 1: stage the next chunk (its buffer was last read in the previous
       // chunk's phase 2) and prefetch the one after, so the loads have a whole chunk
@@ -1015,18 +1029,20 @@ __global__ __launch_bounds__(NTHR) void gdn_state_copy_kernel(Params p) {
 using namespace hmx;
 using namespace hmx::gdnp;
 
-extern "C" int hmx_gdn_chunk_fwd(const void* q, int64_t q_token_stride, const void* k,
-                                 int64_t k_token_stride, const void* v, int64_t v_token_stride,
-                                 int32_t qkv_dtype, const void* g, int32_t g_dtype,
-                                 const void* beta, int32_t beta_dtype, void* o, const void* h0,
-                                 void* ht, int64_t state_slot_stride, int32_t state_dtype,
-                                 const int32_t* state_indices, const uint8_t* has_initial_state,
-                                 const int32_t* seg_table, int32_t nseg_total, int32_t N,
-                                 int32_t H, int32_t HKV, int32_t K, int32_t V, float scale,
-                                 int32_t use_qk_l2norm, int32_t max_warm_chunks,
-                                 float decay_threshold, void* workspace, size_t workspace_bytes,
-                                 const hmx_gated_norm* o_norm, const hmx_gate_proj* gates,
-                                 void* stream) {
+// hmx_gdn_chunk_fwd, and with block_states / cu_blocks the training forward
+// (hmx_gdn_train_fwd) that also writes the state entering every chunk
+static int chunk_fwd_impl(const void* q, int64_t q_token_stride, const void* k,
+                          int64_t k_token_stride, const void* v, int64_t v_token_stride,
+                          int32_t qkv_dtype, const void* g, int32_t g_dtype, const void* beta,
+                          int32_t beta_dtype, void* o, const void* h0, void* ht,
+                          int64_t state_slot_stride, int32_t state_dtype,
+                          const int32_t* state_indices, const uint8_t* has_initial_state,
+                          const int32_t* seg_table, int32_t nseg_total, int32_t N, int32_t H,
+                          int32_t HKV, int32_t K, int32_t V, float scale, int32_t use_qk_l2norm,
+                          int32_t max_warm_chunks, float decay_threshold, void* workspace,
+                          size_t workspace_bytes, const hmx_gated_norm* o_norm,
+                          const hmx_gate_proj* gates, void* stream, f16* block_states,
+                          const int32_t* cu_blocks) {
   HMX_REQUIRE(qkv_dtype == HMX_BF16, HMX_EUNSUPPORTED,
               "hmx_gdn_chunk_fwd: q/k/v must be bfloat16 (got dtype code %d)", qkv_dtype);
   HMX_REQUIRE(K == D && V == D, HMX_EUNSUPPORTED,
@@ -1071,6 +1087,7 @@ extern "C" int hmx_gdn_chunk_fwd(const void* q, int64_t q_token_stride, const vo
   p.seg = seg_table; p.nseg_total = nseg_total; p.H = H; p.HKV = HKV; p.scale = scale;
   p.l2norm = use_qk_l2norm; p.max_warm = max_warm_chunks; p.decay_thresh = decay_threshold;
   p.zg = nullptr; p.zg_ts = p.zg_hs = 0; p.onw = nullptr; p.onw_dt = HMX_F32; p.on_eps = 0.f;
+  p.ws_hc = block_states; p.cu_chunk = cu_blocks;
   if (o_norm) {
     HMX_REQUIRE(o_norm->weight && o_norm->weight_dtype >= 0 && o_norm->weight_dtype <= 2,
                 HMX_EINVAL, "hmx_gdn_chunk_fwd: o_norm needs a weight (dtype code 0-2)");
@@ -1123,6 +1140,25 @@ extern "C" int hmx_gdn_chunk_fwd(const void* q, int64_t q_token_stride, const vo
     hipLaunchKernelGGL((gdn_chunk_kernel<false, false>), grid, dim3(NTHR), 0, s, p);
   if (staged) hipLaunchKernelGGL(gdn_state_copy_kernel, dim3(N, H), dim3(NTHR), 0, s, p);
   return check_launch("hmx_gdn_chunk_fwd");
+}
+
+extern "C" int hmx_gdn_chunk_fwd(const void* q, int64_t q_token_stride, const void* k,
+                                 int64_t k_token_stride, const void* v, int64_t v_token_stride,
+                                 int32_t qkv_dtype, const void* g, int32_t g_dtype,
+                                 const void* beta, int32_t beta_dtype, void* o, const void* h0,
+                                 void* ht, int64_t state_slot_stride, int32_t state_dtype,
+                                 const int32_t* state_indices, const uint8_t* has_initial_state,
+                                 const int32_t* seg_table, int32_t nseg_total, int32_t N,
+                                 int32_t H, int32_t HKV, int32_t K, int32_t V, float scale,
+                                 int32_t use_qk_l2norm, int32_t max_warm_chunks,
+                                 float decay_threshold, void* workspace, size_t workspace_bytes,
+                                 const hmx_gated_norm* o_norm, const hmx_gate_proj* gates,
+                                 void* stream) {
+  return chunk_fwd_impl(q, q_token_stride, k, k_token_stride, v, v_token_stride, qkv_dtype, g,
+                        g_dtype, beta, beta_dtype, o, h0, ht, state_slot_stride, state_dtype,
+                        state_indices, has_initial_state, seg_table, nseg_total, N, H, HKV, K, V,
+                        scale, use_qk_l2norm, max_warm_chunks, decay_threshold, workspace,
+                        workspace_bytes, o_norm, gates, stream, nullptr, nullptr);
 }
 
 extern "C" size_t hmx_gdn_chunk_workspace_bytes(int32_t nseg_total, int32_t N, int32_t H,
@@ -1201,4 +1237,666 @@ extern "C" int hmx_gdn_chunk_fwd_noalloc(
                            state_indices, has_initial_state, seg_table, nseg_total, N, H, HKV, K,
                            V, scale, use_qk_l2norm, max_warm_chunks, decay_threshold, ws,
                            (size_t)HMX_GDN_CHUNK_SCRATCH_BYTES, o_norm, gates, stream);
+}
+
+// ===========================================================================
+// Training: the backward of the chunked gated delta rule.
+//
+// Per 32-token block (the forward's chunk) with S0 the state entering it (written
+// by the training forward), gamma the in-block cumsum of g, E = diag(e^gamma),
+// F = diag(e^{gamma_L - gamma}), Gm_ij = e^{gamma_i - gamma_j}, unit rows q^, k^
+// (in-kernel L2 normalisation) and the forward's
+//   Mm = strict_lower(K^K^T . Gm),  T = (I + diag(beta) Mm)^-1,
+//   Ut = V - E K^ S0,  W = T diag(beta) Ut,  S_L = e^{gamma_L} S0 + K^T F W,
+//   O  = scale (E Q^ S0 + lower(Q^K^T . Gm) W),
+// the gradient dS of S_L gives
+//   dW = scale lower(Q^K^T . Gm)^T dO + F K^ dS,  Z = T^T dW,  dV = diag(beta) Z,
+//   dN = -strict_lower(Z W^T),  Dm = diag(beta) dN . Gm,  Dp = scale lower(dO W^T) . Gm,
+//   dQ^ = scale E dO S0^T + Dp K^,
+//   dK^ = -E diag(beta) Z S0^T + F W dS^T + Dp^T Q^ + (Dm + Dm^T) K^,
+//   dbeta = rowdot(Z, Ut) + rowsum(dN . Mm),
+//   dgamma = rowdot(Q^, scale E dO S0^T) + rowdot(K^, -E diag(beta) Z S0^T - F W dS^T)
+//            + (rowsum - colsum)(Dp . Q^K^T) + (rowsum - colsum)(Dm . K^K^T),
+//   dgamma_L += e^{gamma_L} <dS, S0> + sum_j k^_j . (F W dS^T)_j,
+//   dS0 = e^{gamma_L} dS + scale Q^T E dO - K^T E diag(beta) Z,
+// then dg = the in-block reverse cumsum of dgamma and the L2 backward
+// dq = (dq^ - q^ (q^ . dq^)) / sqrt(|q|^2 + 1e-6) (k likewise).
+//
+// Three launches: a block-parallel prep (T and scale lower(Q^K^T . Gm), fp16), the
+// reverse chain of dS over each sequence's blocks (one workgroup per sequence and
+// head, wave w owning value columns 16w.., the fp32 dS in MFMA accumulators; it
+// writes each block's dS in fp16), and the block-parallel gradient kernel.  Every
+// MFMA operand is fp16 (one rounding) with fp32 accumulation.
+// ===========================================================================
+namespace hmx {
+namespace gdnp {
+namespace train {
+
+constexpr int LR = 144;       // fp16 row stride of [rows][128] LDS arrays (72 dwords)
+constexpr int LL = 40;        // fp16 row stride of [32][32] LDS arrays
+constexpr int LF = 33;        // fp32 row stride of [32][32] LDS arrays
+constexpr int BNTHR = 512;    // 8 waves
+
+struct Bwd {
+  const bf16* q; const bf16* k; const bf16* v;
+  int64_t q_ts, kv_ts;        // token strides (elements); heads are D apart
+  const void* g; int g_dt;
+  const void* beta; int beta_dt;
+  const bf16* dout; int64_t do_ts;
+  const float* dht;           // [N][H][D][D] gradient of the final states, or null
+  const f16* hc;              // [nblk][H][D][D] state entering each block
+  f16* dhc;                   // [nblk][H][D][D] gradient of the state leaving each block
+  f16* tm;                    // [nblk][H][C][C] T
+  f16* pm;                    // [nblk][H][C][C] scale lower(Q^K^T . Gm)
+  const int* ctab;            // [nblk][4]: first token, tokens, sequence, block in sequence
+  const int* cu_blk;          // [N+1]
+  bf16* dq; bf16* dk; bf16* dv;   // [tokens][H][D]
+  float* dg; float* dbeta;        // [tokens][H]
+  float* dh0;                 // [N][H][D][D] or null
+  int H;
+  float scale;
+  int l2norm;
+};
+
+// B (or A^T) operand from a row-major fp16 array M: column c0 + (l & 15), k = rows
+// k0 + 8 (l >> 4) .. +7 (natural order; pairs with frag_h)
+__device__ __forceinline__ f16x8 frag_col(const f16* b, int ld, int k0, int c0, int lane) {
+  const int kq = k0 + 8 * (lane >> 4);
+  const f16x4 x = ld_tr_h(b, ld, kq, c0, lane);
+  const f16x4 y = ld_tr_h(b, ld, kq + 4, c0, lane);
+  return f16x8{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+}
+
+// One block's rows of src into an fp16 [32][LR] array, times 1 / sqrt(|x|^2 + 1e-6)
+// with l2 (that factor into rnorm[row] when given).  512 threads: row tid >> 4,
+// features 8 (tid & 15) .. +7.
+__device__ __forceinline__ void stage_rows(f16* dst, const bf16* src, int64_t ts, int tok0,
+                                           int nval, bool l2, float* rnorm, int tid) {
+  const int row = tid >> 4, f0 = (tid & 15) * 8;
+  const bf16x8 x =
+      row < nval ? *reinterpret_cast<const bf16x8*>(src + (int64_t)(tok0 + row) * ts + f0)
+                 : bf16x8{};
+  const float r = l2 ? row_inv_norm(x) : 1.f;
+  *reinterpret_cast<f16x8*>(dst + row * LR + f0) = scale_h8(x, r);
+  if (rnorm && (tid & 15) == 0) rnorm[row] = r;
+}
+
+struct Sc { float* G; float* E; float* F; float* B; };
+
+// wave 0: the block's in-block cumsum of g, e^gamma, e^{gamma_L - gamma} and beta
+// into LDS (lanes 0-31; 0 / 0 past the block's tokens)
+__device__ __forceinline__ void block_scalars(const Bwd& p, const Sc& s, int tok0, int nval, int h,
+                                              int lane) {
+  const bool ok = lane < nval;
+  const int64_t i = (int64_t)(tok0 + lane) * p.H + h;
+  const float gv = ok ? ld_scalar(p.g, i, p.g_dt) : 0.f;
+  const float bv = ok ? ld_scalar(p.beta, i, p.beta_dt) : 0.f;
+  const float gam = scan32(gv);
+  const float gl = __builtin_bit_cast(float,
+                                      __builtin_amdgcn_readlane(__builtin_bit_cast(int, gam), C - 1));
+  if (lane < C) {
+    s.G[lane] = gam;
+    s.E[lane] = fast_exp(gam);
+    s.F[lane] = fast_exp(gl - gam);
+    s.B[lane] = bv;
+  }
+}
+
+__device__ __forceinline__ Sc sc_at(unsigned char* base) {
+  float* f = reinterpret_cast<float*>(base);
+  return Sc{f, f + C, f + 2 * C, f + 3 * C};
+}
+
+// ---- prep: T and scale lower(Q^K^T . Gm) of every block ----------------------
+constexpr int PR_OFF_K = 0, PR_OFF_Q = C * LR * 2, PR_OFF_N = 2 * C * LR * 2;
+constexpr int PR_OFF_T = PR_OFF_N + C * LF * 4, PR_OFF_SC = PR_OFF_T + C * LF * 4;
+constexpr int PR_SMEM = PR_OFF_SC + 4 * C * 4;
+
+__global__ __launch_bounds__(BNTHR) void gdn_bwd_prep_kernel(Bwd p) {
+  __shared__ __align__(16) unsigned char smem[PR_SMEM];
+  f16* sK = reinterpret_cast<f16*>(smem + PR_OFF_K);
+  f16* sQ = reinterpret_cast<f16*>(smem + PR_OFF_Q);
+  float* sN = reinterpret_cast<float*>(smem + PR_OFF_N);
+  float* sT = reinterpret_cast<float*>(smem + PR_OFF_T);
+  const Sc sc = sc_at(smem + PR_OFF_SC);
+  const int cb = blockIdx.x, h = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q4 = lane >> 4, l16 = lane & 15;
+  const int tok0 = p.ctab[cb * 4], nval = p.ctab[cb * 4 + 1];
+  stage_rows(sK, p.k + (int64_t)h * D, p.kv_ts, tok0, nval, p.l2norm, nullptr, tid);
+  stage_rows(sQ, p.q + (int64_t)h * D, p.q_ts, tok0, nval, p.l2norm, nullptr, tid);
+  if (wave == 0) block_scalars(p, sc, tok0, nval, h, lane);
+  lds_barrier();
+  const int64_t mo = ((int64_t)cb * p.H + h) * C * C;
+  {  // waves 0-3: a tile of Q^K^T -> P; waves 4-7: a tile of K^K^T -> N = beta Mm
+    const int t = wave & 3, mt = t >> 1, nt = t & 1;
+    const f16* A = wave < 4 ? sQ : sK;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      acc = mfma16h(frag_h(A, LR, 16 * mt, 32 * ks, lane), frag_h(sK, LR, 16 * nt, 32 * ks, lane),
+                    acc);
+    const int j = 16 * nt + l16;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int i = 16 * mt + 4 * q4 + v;
+      const float gm = j <= i ? fast_exp(sc.G[i] - sc.G[j]) : 0.f;
+      if (wave < 4) p.pm[mo + i * C + j] = (f16)(p.scale * acc[v] * gm);
+      else sN[i * LF + j] = j < i ? sc.B[i] * acc[v] * gm : 0.f;
+    }
+  }
+  lds_barrier();
+  // T = (I + N)^-1: the diagonal 16x16 blocks by forward substitution (lane l of
+  // each half solves for column l of its block) ...
+  if (wave == 0 && lane < C) {
+    const int o = (lane >> 4) * 16, l = lane & 15;
+    float t[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float s = (i == l) ? 1.f : 0.f;
+#pragma unroll
+      for (int j = 0; j < i; ++j) s -= sN[(o + i) * LF + o + j] * t[j];
+      t[i] = s;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sT[(o + i) * LF + o + l] = t[i];
+  }
+  lds_barrier();
+  // ... then T_10 = -T_11 (N_10 T_00), the inner product held in T's upper-right block
+  if (tid < 256) {
+    const int i = tid >> 4, j = tid & 15;
+    float y = 0.f;
+    for (int k = j; k < 16; ++k) y += sN[(16 + i) * LF + k] * sT[k * LF + j];
+    sT[i * LF + 16 + j] = y;
+  }
+  lds_barrier();
+  if (tid < 256) {
+    const int i = tid >> 4, j = tid & 15;
+    float y = 0.f;
+    for (int k = 0; k <= i; ++k) y += sT[(16 + i) * LF + 16 + k] * sT[k * LF + 16 + j];
+    sT[(16 + i) * LF + j] = -y;
+  }
+  lds_barrier();
+  for (int e = tid; e < C * C; e += BNTHR) {
+    const int i = e >> 5, j = e & 31;
+    p.tm[mo + e] = (f16)(j > i ? 0.f : sT[i * LF + j]);
+  }
+}
+
+// ---- the reverse chain of the state gradient ---------------------------------
+constexpr int CH_OFF_K = 0, CH_OFF_Q = C * LR * 2, CH_OFF_DO = 2 * C * LR * 2;
+constexpr int CH_OFF_T = 3 * C * LR * 2, CH_OFF_P = CH_OFF_T + C * LL * 2;
+constexpr int CH_OFF_SC = CH_OFF_P + C * LL * 2;
+constexpr int CH_SMEM = CH_OFF_SC + 4 * C * 4;
+
+__global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_chain_kernel(Bwd p) {
+  __shared__ __align__(16) unsigned char smem[CH_SMEM];
+  f16* sK = reinterpret_cast<f16*>(smem + CH_OFF_K);
+  f16* sQ = reinterpret_cast<f16*>(smem + CH_OFF_Q);
+  f16* sDO = reinterpret_cast<f16*>(smem + CH_OFF_DO);
+  f16* sT = reinterpret_cast<f16*>(smem + CH_OFF_T);
+  f16* sP = reinterpret_cast<f16*>(smem + CH_OFF_P);
+  const Sc sc = sc_at(smem + CH_OFF_SC);
+  const int n = blockIdx.x, h = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q4 = lane >> 4, l16 = lane & 15;
+  const int c0 = 16 * wave;                      // this wave's value columns
+  const int64_t DD = (int64_t)D * D;
+  const int b0 = p.cu_blk[n], b1 = p.cu_blk[n + 1];
+  // dS[rt]: rows 16 rt + 4 q4 + v, column c0 + l16
+  f32x4 dS[8];
+  {
+    const float* src = p.dht ? p.dht + ((int64_t)n * p.H + h) * DD : nullptr;
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        dS[rt][v] = src ? src[(16 * rt + 4 * q4 + v) * D + c0 + l16] : 0.f;
+  }
+  for (int cb = b1 - 1; cb >= b0; --cb) {
+    const int tok0 = p.ctab[cb * 4], nval = p.ctab[cb * 4 + 1];
+    {  // the gradient of the state leaving block cb
+      f16* dst = p.dhc + ((int64_t)cb * p.H + h) * DD + c0 + l16;
+#pragma unroll
+      for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) dst[(16 * rt + 4 * q4 + v) * D] = (f16)dS[rt][v];
+    }
+    lds_barrier();   // the previous block's LDS reads are done
+    if (wave == 0) block_scalars(p, sc, tok0, nval, h, lane);
+    stage_rows(sK, p.k + (int64_t)h * D, p.kv_ts, tok0, nval, p.l2norm, nullptr, tid);
+    stage_rows(sQ, p.q + (int64_t)h * D, p.q_ts, tok0, nval, p.l2norm, nullptr, tid);
+    stage_rows(sDO, p.dout + (int64_t)h * D, p.do_ts, tok0, nval, false, nullptr, tid);
+    {
+      const int64_t mo = ((int64_t)cb * p.H + h) * C * C;
+      const int e = 2 * tid, i = e >> 5, j = e & 31;
+      *reinterpret_cast<uint32_t*>(sT + i * LL + j) = *reinterpret_cast<const uint32_t*>(p.tm + mo + e);
+      *reinterpret_cast<uint32_t*>(sP + i * LL + j) = *reinterpret_cast<const uint32_t*>(p.pm + mo + e);
+    }
+    lds_barrier();
+    // dW = F K^ dS + P^T dO (tokens x this wave's columns), Z' = -E beta T^T dW
+    f32x4 dW[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        acc = mfma16h(frag_perm_h(sK, LR, 16 * mt, 32 * m, lane), h8(dS[2 * m], dS[2 * m + 1]), acc);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) dW[mt][v] = sc.F[16 * mt + 4 * q4 + v] * acc[v];
+    }
+    const f16x8 bdo = frag_col(sDO, LR, 0, c0, lane);
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) dW[mt] = mfma16h(frag_col(sP, LL, 0, 16 * mt, lane), bdo, dW[mt]);
+    f32x4 Zp[2];
+    {
+      const f16x8 bw = h8(dW[0], dW[1]);
+      const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const f32x4 Z = mfma16h(frag_t_perm_h(sT, LL, 0, 16 * mt, lane), bw, z);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int r = 16 * mt + 4 * q4 + v;
+          Zp[mt][v] = -sc.E[r] * sc.B[r] * Z[v];
+        }
+      }
+    }
+    // dS <- e^{gamma_L} dS + K^T Z' + Q^T (scale E dO)
+    f16x8 bqe;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) bqe[j] = (f16)((float)bdo[j] * p.scale * sc.E[8 * q4 + j]);
+    const f16x8 bz = h8(Zp[0], Zp[1]);
+    const float eL = sc.E[C - 1];
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) dS[rt][v] *= eL;
+      dS[rt] = mfma16h(frag_t_perm_h(sK, LR, 0, 16 * rt, lane), bz, dS[rt]);
+      dS[rt] = mfma16h(frag_col(sQ, LR, 0, 16 * rt, lane), bqe, dS[rt]);
+    }
+  }
+  if (p.dh0) {
+    float* dst = p.dh0 + ((int64_t)n * p.H + h) * DD + c0 + l16;
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) dst[(16 * rt + 4 * q4 + v) * D] = dS[rt][v];
+  }
+}
+
+// ---- the per-block gradients -------------------------------------------------
+constexpr int SZR = C * LR * 2, SZS = D * LR * 2, SZL = C * LL * 2;
+constexpr int G_OFF_K = 0, G_OFF_Q = SZR, G_OFF_DO = 2 * SZR, G_OFF_X = 3 * SZR;
+constexpr int G_OFF_W = 4 * SZR, G_OFF_Z = 5 * SZR;
+constexpr int G_OFF_S0 = 6 * SZR, G_OFF_DS = G_OFF_S0 + SZS;
+constexpr int G_OFF_T = G_OFF_DS + SZS, G_OFF_PM = G_OFF_T + SZL;
+constexpr int G_OFF_DP = G_OFF_PM + SZL, G_OFF_DM = G_OFF_DP + SZL;
+constexpr int G_OFF_QK = G_OFF_DM + SZL, G_OFF_KK = G_OFF_QK + C * LF * 4;
+constexpr int G_OFF_SC = G_OFF_KK + C * LF * 4;            // G, E, F, B, rq, rk
+constexpr int NPG = 16, NPB = 10;
+constexpr int G_OFF_PG = G_OFF_SC + 6 * C * 4;             // [16][32] dgamma pieces
+constexpr int G_OFF_PB = G_OFF_PG + NPG * C * 4;           // [10][32] dbeta pieces
+constexpr int G_OFF_PC = G_OFF_PB + NPB * C * 4;           // [8][32] k^ . (F W dS^T) per wave
+constexpr int G_OFF_PQ = G_OFF_PC + 8 * C * 4;             // [8][32] q^ . dq^ per wave
+constexpr int G_OFF_PK = G_OFF_PQ + 8 * C * 4;             // [8][32] k^ . dk^ per wave
+constexpr int G_OFF_PD = G_OFF_PK + 8 * C * 4;             // [8] <dS, S0> per wave
+constexpr int G_SMEM = G_OFF_PD + 8 * 4;
+static_assert(G_SMEM <= 160 * 1024, "LDS budget");
+
+__global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_grad_kernel(Bwd p) {
+  __shared__ __align__(16) unsigned char smem[G_SMEM];
+  f16* sK = reinterpret_cast<f16*>(smem + G_OFF_K);
+  f16* sQ = reinterpret_cast<f16*>(smem + G_OFF_Q);
+  f16* sDO = reinterpret_cast<f16*>(smem + G_OFF_DO);
+  f16* sX = reinterpret_cast<f16*>(smem + G_OFF_X);
+  f16* sW = reinterpret_cast<f16*>(smem + G_OFF_W);
+  f16* sZ = reinterpret_cast<f16*>(smem + G_OFF_Z);
+  f16* sS0 = reinterpret_cast<f16*>(smem + G_OFF_S0);
+  f16* sDS = reinterpret_cast<f16*>(smem + G_OFF_DS);
+  f16* sT = reinterpret_cast<f16*>(smem + G_OFF_T);
+  f16* sPm = reinterpret_cast<f16*>(smem + G_OFF_PM);
+  f16* sDp = reinterpret_cast<f16*>(smem + G_OFF_DP);
+  f16* sDm = reinterpret_cast<f16*>(smem + G_OFF_DM);
+  float* sQK = reinterpret_cast<float*>(smem + G_OFF_QK);
+  float* sKK = reinterpret_cast<float*>(smem + G_OFF_KK);
+  const Sc sc = sc_at(smem + G_OFF_SC);
+  float* sRq = sc.B + C;
+  float* sRk = sRq + C;
+  float* sPG = reinterpret_cast<float*>(smem + G_OFF_PG);
+  float* sPB = reinterpret_cast<float*>(smem + G_OFF_PB);
+  float* sPC = reinterpret_cast<float*>(smem + G_OFF_PC);
+  float* sPQ = reinterpret_cast<float*>(smem + G_OFF_PQ);
+  float* sPK = reinterpret_cast<float*>(smem + G_OFF_PK);
+  float* sPD = reinterpret_cast<float*>(smem + G_OFF_PD);
+
+  const int cb = blockIdx.x, h = blockIdx.y, H = p.H;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q4 = lane >> 4, l16 = lane & 15;
+  const int c0 = 16 * wave;      // this wave's value columns (P1-P2) / key features (P3-P5)
+  const int tok0 = p.ctab[cb * 4], nval = p.ctab[cb * 4 + 1];
+  const int64_t DD = (int64_t)D * D, bh = (int64_t)cb * H + h;
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+
+  // ---- P0: stage the block's rows, S0, dS, T and P -----------------------------
+  if (wave == 0) block_scalars(p, sc, tok0, nval, h, lane);
+  stage_rows(sK, p.k + (int64_t)h * D, p.kv_ts, tok0, nval, p.l2norm, sRk, tid);
+  stage_rows(sQ, p.q + (int64_t)h * D, p.q_ts, tok0, nval, p.l2norm, sRq, tid);
+  stage_rows(sDO, p.dout + (int64_t)h * D, p.do_ts, tok0, nval, false, nullptr, tid);
+  stage_rows(sX, p.v + (int64_t)h * D, p.kv_ts, tok0, nval, false, nullptr, tid);
+#pragma unroll
+  for (int pass = 0; pass < 4; ++pass) {
+    const int e = (pass * BNTHR + tid) * 8, row = e >> 7, col = e & 127;
+    *reinterpret_cast<f16x8*>(sS0 + row * LR + col) = *reinterpret_cast<const f16x8*>(p.hc + bh * DD + e);
+    *reinterpret_cast<f16x8*>(sDS + row * LR + col) = *reinterpret_cast<const f16x8*>(p.dhc + bh * DD + e);
+  }
+  {
+    const int e = 2 * tid, i = e >> 5, j = e & 31;
+    *reinterpret_cast<uint32_t*>(sT + i * LL + j) = *reinterpret_cast<const uint32_t*>(p.tm + bh * C * C + e);
+    *reinterpret_cast<uint32_t*>(sPm + i * LL + j) = *reinterpret_cast<const uint32_t*>(p.pm + bh * C * C + e);
+  }
+  lds_barrier();
+
+  // ---- P1: K^ S0 and K^ dS (tokens x this wave's value columns), a tile of Q^K^T
+  // or K^K^T, this wave's share of <dS, S0>; Ut = V - E K^ S0, beta Ut over V ----
+  f32x4 Ut[2], KD[2];
+  {
+    f32x4 KS[2] = {zero, zero};
+    KD[0] = KD[1] = zero;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const f16x8 bs = frag_col(sS0, LR, 32 * ks, c0, lane), bd = frag_col(sDS, LR, 32 * ks, c0, lane);
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const f16x8 a = frag_h(sK, LR, 16 * mt, 32 * ks, lane);
+        KS[mt] = mfma16h(a, bs, KS[mt]);
+        KD[mt] = mfma16h(a, bd, KD[mt]);
+      }
+    }
+    {
+      const int t = wave & 3, mt = t >> 1, nt = t & 1;
+      const f16* A = wave < 4 ? sQ : sK;
+      f32x4 acc = zero;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+        acc = mfma16h(frag_h(A, LR, 16 * mt, 32 * ks, lane), frag_h(sK, LR, 16 * nt, 32 * ks, lane), acc);
+      float* dst = wave < 4 ? sQK : sKK;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) dst[(16 * mt + 4 * q4 + v) * LF + 16 * nt + l16] = acc[v];
+    }
+    {
+      float d = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = 16 * wave + 4 * i + q4, col = 8 * l16;
+        const f16x8 a = *reinterpret_cast<const f16x8*>(sS0 + row * LR + col);
+        const f16x8 b = *reinterpret_cast<const f16x8*>(sDS + row * LR + col);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) d += (float)a[j] * (float)b[j];
+      }
+      d = wave_sum(d);
+      if (lane == 0) sPD[wave] = d;
+    }
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int r = 16 * mt + 4 * q4 + v, idx = r * LR + c0 + l16;
+        Ut[mt][v] = (float)sX[idx] - sc.E[r] * KS[mt][v];
+        sX[idx] = (f16)(sc.B[r] * Ut[mt][v]);
+      }
+  }
+  lds_barrier();
+
+  // ---- P2: W = T (beta Ut); dW = P^T dO + F K^ dS; Z = T^T dW; dv; rowdot(Z, Ut) --
+  {
+    const f16x8 bx = frag_col(sX, LR, 0, c0, lane), bdo = frag_col(sDO, LR, 0, c0, lane);
+    f32x4 W[2], dW[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      W[mt] = mfma16h(frag_h(sT, LL, 16 * mt, 0, lane), bx, zero);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) dW[mt][v] = sc.F[16 * mt + 4 * q4 + v] * KD[mt][v];
+      dW[mt] = mfma16h(frag_col(sPm, LL, 0, 16 * mt, lane), bdo, dW[mt]);
+    }
+    const f16x8 bw = h8(dW[0], dW[1]);
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      const f32x4 Z = mfma16h(frag_t_perm_h(sT, LL, 0, 16 * mt, lane), bw, zero);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int r = 16 * mt + 4 * q4 + v, idx = r * LR + c0 + l16;
+        sW[idx] = (f16)W[mt][v];
+        sZ[idx] = (f16)Z[v];
+        if (r < nval) p.dv[((int64_t)(tok0 + r) * H + h) * D + c0 + l16] = (bf16)(sc.B[r] * Z[v]);
+        const float zu = row16_sum(Z[v] * Ut[mt][v]);
+        if (l16 == 0) sPB[wave * C + r] = zu;
+      }
+    }
+  }
+  lds_barrier();
+
+  // ---- P3: dO S0^T, Z S0^T, W dS^T (tokens x this wave's key features); a tile of
+  // Z W^T (-> dN, Dm) or dO W^T (-> Dp) with their row and column sums -------------
+  f32x4 DQ[2], DK[2];
+  {
+    f32x4 A0[2] = {zero, zero}, A1[2] = {zero, zero}, A2[2] = {zero, zero};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const f16x8 bs = frag_h(sS0, LR, c0, 32 * ks, lane), bd = frag_h(sDS, LR, c0, 32 * ks, lane);
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        A0[mt] = mfma16h(frag_h(sDO, LR, 16 * mt, 32 * ks, lane), bs, A0[mt]);
+        A1[mt] = mfma16h(frag_h(sZ, LR, 16 * mt, 32 * ks, lane), bs, A1[mt]);
+        A2[mt] = mfma16h(frag_h(sW, LR, 16 * mt, 32 * ks, lane), bd, A2[mt]);
+      }
+    }
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int r = 16 * mt + 4 * q4 + v, idx = r * LR + c0 + l16;
+        const float qt = p.scale * sc.E[r] * A0[mt][v];
+        const float ut = -sc.E[r] * sc.B[r] * A1[mt][v];
+        const float st = sc.F[r] * A2[mt][v];
+        const float qh = (float)sQ[idx], kh = (float)sK[idx];
+        DQ[mt][v] = qt;
+        DK[mt][v] = ut + st;
+        const float gq = row16_sum(qh * qt + kh * (ut - st));
+        const float cj = row16_sum(kh * st);
+        if (l16 == 0) {
+          sPG[(8 + wave) * C + r] = gq;
+          sPC[wave * C + r] = cj;
+        }
+      }
+  }
+  {
+    const int t = wave & 3, mt = t >> 1, nt = t & 1;
+    const f16* A = wave < 4 ? sZ : sDO;
+    f32x4 acc = zero;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      acc = mfma16h(frag_h(A, LR, 16 * mt, 32 * ks, lane), frag_h(sW, LR, 16 * nt, 32 * ks, lane), acc);
+    const int j = 16 * nt + l16;
+    float csum = 0.f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int i = 16 * mt + 4 * q4 + v;
+      const float gm = j <= i ? fast_exp(sc.G[i] - sc.G[j]) : 0.f;
+      float x;
+      if (wave < 4) {   // dN = -strict_lower(Z W^T), Dm = beta dN . Gm
+        const float dn = j < i ? -acc[v] : 0.f;
+        const float kk = sKK[i * LF + j];
+        const float d = sc.B[i] * dn * gm;
+        sDm[i * LL + j] = (f16)d;
+        x = d * kk;
+        const float db = row16_sum(dn * kk * gm);
+        if (l16 == 0) sPB[(8 + nt) * C + i] = db;
+      } else {          // Dp = scale lower(dO W^T) . Gm
+        const float d = p.scale * acc[v] * gm;
+        sDp[i * LL + j] = (f16)d;
+        x = d * sQK[i * LF + j];
+      }
+      const float rs = row16_sum(x);
+      if (l16 == 0) sPG[((wave < 4 ? 0 : 2) + nt) * C + i] = rs;
+      csum += x;
+    }
+    csum += __shfl_xor(csum, 16, 64);
+    csum += __shfl_xor(csum, 32, 64);
+    if (q4 == 0) sPG[((wave < 4 ? 4 : 6) + mt) * C + j] = -csum;
+  }
+  lds_barrier();
+
+  // ---- P4: dQ^ += Dp K^; dK^ += Dp^T Q^ + (Dm + Dm^T) K^; the L2 backward's row dots
+  {
+    const f16x8 bk = frag_col(sK, LR, 0, c0, lane), bq = frag_col(sQ, LR, 0, c0, lane);
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      DQ[mt] = mfma16h(frag_h(sDp, LL, 16 * mt, 0, lane), bk, DQ[mt]);
+      DK[mt] = mfma16h(frag_col(sDp, LL, 0, 16 * mt, lane), bq, DK[mt]);
+      DK[mt] = mfma16h(frag_h(sDm, LL, 16 * mt, 0, lane), bk, DK[mt]);
+      DK[mt] = mfma16h(frag_col(sDm, LL, 0, 16 * mt, lane), bk, DK[mt]);
+    }
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int r = 16 * mt + 4 * q4 + v, idx = r * LR + c0 + l16;
+        const float sq = row16_sum((float)sQ[idx] * DQ[mt][v]);
+        const float sk = row16_sum((float)sK[idx] * DK[mt][v]);
+        if (l16 == 0) {
+          sPQ[wave * C + r] = sq;
+          sPK[wave * C + r] = sk;
+        }
+      }
+  }
+  lds_barrier();
+
+  // ---- P5: dq, dk (through the L2 normalisation); dg, dbeta --------------------
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int r = 16 * mt + 4 * q4 + v, idx = r * LR + c0 + l16;
+      float dq = DQ[mt][v], dk = DK[mt][v];
+      if (p.l2norm) {
+        float sq = 0.f, sk = 0.f;
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+          sq += sPQ[w * C + r];
+          sk += sPK[w * C + r];
+        }
+        dq = sRq[r] * (dq - (float)sQ[idx] * sq);
+        dk = sRk[r] * (dk - (float)sK[idx] * sk);
+      }
+      if (r < nval) {
+        const int64_t o = ((int64_t)(tok0 + r) * H + h) * D + c0 + l16;
+        p.dq[o] = (bf16)dq;
+        p.dk[o] = (bf16)dk;
+      }
+    }
+  if (wave == 0) {
+    float dgam = 0.f, db = 0.f, cl = 0.f, dd = 0.f;
+    if (lane < C) {
+#pragma unroll
+      for (int s = 0; s < NPG; ++s) dgam += sPG[s * C + lane];
+#pragma unroll
+      for (int s = 0; s < NPB; ++s) db += sPB[s * C + lane];
+#pragma unroll
+      for (int w = 0; w < 8; ++w) cl += sPC[w * C + lane];
+    }
+#pragma unroll
+    for (int w = 0; w < 8; ++w) dd += sPD[w];
+    const float ctot = wave_sum(cl);
+    if (lane == C - 1) dgam += sc.E[C - 1] * dd + ctot;
+    // in-block reverse inclusive cumsum over lanes 0-31
+#pragma unroll
+    for (int off = 1; off < C; off <<= 1) {
+      const float y = __shfl_down(dgam, off, 64);
+      if (lane + off < C) dgam += y;
+    }
+    if (lane < nval) {
+      const int64_t o = (int64_t)(tok0 + lane) * H + h;
+      p.dg[o] = dgam;
+      p.dbeta[o] = db;
+    }
+  }
+}
+
+}  // namespace train
+}  // namespace gdnp
+}  // namespace hmx
+
+extern "C" int hmx_gdn_train_fwd(const void* q, int64_t q_token_stride, const void* k,
+                                 const void* v, int64_t kv_token_stride, const void* g,
+                                 int32_t g_dtype, const void* beta, int32_t beta_dtype, void* o,
+                                 const float* h0, float* ht, const int32_t* seg_table,
+                                 int32_t nseg_total, int32_t N, int32_t H, float scale,
+                                 int32_t use_qk_l2norm, int32_t max_warm_chunks,
+                                 float decay_threshold, void* workspace, size_t workspace_bytes,
+                                 void* block_states, const int32_t* cu_blocks, void* stream) {
+  HMX_REQUIRE(block_states && cu_blocks && (uintptr_t)block_states % 16 == 0, HMX_EINVAL,
+              "hmx_gdn_train_fwd: block_states (16-byte aligned) and cu_blocks are required");
+  return chunk_fwd_impl(q, q_token_stride, k, kv_token_stride, v, kv_token_stride, HMX_BF16, g,
+                        g_dtype, beta, beta_dtype, o, h0, ht, (int64_t)H * D * D, HMX_F32,
+                        nullptr, nullptr, seg_table, nseg_total, N, H, H, D, D, scale,
+                        use_qk_l2norm, max_warm_chunks, decay_threshold, workspace,
+                        workspace_bytes, nullptr, nullptr, stream,
+                        static_cast<f16*>(block_states), cu_blocks);
+}
+
+extern "C" size_t hmx_gdn_train_bwd_workspace_bytes(int32_t nblock_total, int32_t H) {
+  // dS per block (fp16 D x D), then T and P per block (fp16 C x C each)
+  return (size_t)nblock_total * H * ((size_t)D * D + 2 * C * C) * sizeof(f16);
+}
+
+extern "C" int hmx_gdn_train_bwd(const void* q, int64_t q_token_stride, const void* k,
+                                 const void* v, int64_t kv_token_stride, const void* g,
+                                 int32_t g_dtype, const void* beta, int32_t beta_dtype,
+                                 const void* dout, int64_t dout_token_stride, const float* dht,
+                                 const void* block_states, const int32_t* block_table,
+                                 const int32_t* cu_blocks, int32_t nblock_total, int32_t N,
+                                 int32_t H, float scale, int32_t use_qk_l2norm, void* dq,
+                                 void* dk, void* dv, float* dg, float* dbeta, float* dh0,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  using namespace hmx::gdnp::train;
+  HMX_REQUIRE(q && k && v && g && beta && dout && block_states && block_table && cu_blocks &&
+                  dq && dk && dv && dg && dbeta, HMX_EINVAL, "hmx_gdn_train_bwd: null pointer");
+  HMX_REQUIRE(N > 0 && H > 0 && nblock_total >= 0, HMX_EINVAL,
+              "hmx_gdn_train_bwd: bad sizes (N=%d H=%d nblock=%d)", N, H, nblock_total);
+  HMX_REQUIRE(g_dtype >= 0 && g_dtype <= 2 && beta_dtype >= 0 && beta_dtype <= 2,
+              HMX_EUNSUPPORTED, "hmx_gdn_train_bwd: g/beta dtype");
+  HMX_REQUIRE(q_token_stride % 8 == 0 && kv_token_stride % 8 == 0 && dout_token_stride % 8 == 0 &&
+                  ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)dout |
+                   (uintptr_t)block_states) % 16 == 0,
+              HMX_EINVAL, "hmx_gdn_train_bwd: rows must be 16-byte aligned");
+  const size_t need = hmx_gdn_train_bwd_workspace_bytes(nblock_total, H);
+  HMX_REQUIRE(workspace && workspace_bytes >= need && (uintptr_t)workspace % 16 == 0, HMX_EINVAL,
+              "hmx_gdn_train_bwd: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  Bwd p;
+  p.q = static_cast<const bf16*>(q); p.k = static_cast<const bf16*>(k);
+  p.v = static_cast<const bf16*>(v);
+  p.q_ts = q_token_stride; p.kv_ts = kv_token_stride;
+  p.g = g; p.g_dt = g_dtype; p.beta = beta; p.beta_dt = beta_dtype;
+  p.dout = static_cast<const bf16*>(dout); p.do_ts = dout_token_stride;
+  p.dht = dht;
+  p.hc = static_cast<const f16*>(block_states);
+  f16* ws = static_cast<f16*>(workspace);
+  p.dhc = ws;
+  p.tm = ws + (size_t)nblock_total * H * D * D;
+  p.pm = p.tm + (size_t)nblock_total * H * C * C;
+  p.ctab = block_table; p.cu_blk = cu_blocks;
+  p.dq = static_cast<bf16*>(dq); p.dk = static_cast<bf16*>(dk); p.dv = static_cast<bf16*>(dv);
+  p.dg = dg; p.dbeta = dbeta; p.dh0 = dh0;
+  p.H = H; p.scale = scale; p.l2norm = use_qk_l2norm;
+  hipStream_t s = (hipStream_t)stream;
+  if (nblock_total > 0)
+    hipLaunchKernelGGL(gdn_bwd_prep_kernel, dim3(nblock_total, H), dim3(BNTHR), 0, s, p);
+  hipLaunchKernelGGL(gdn_bwd_chain_kernel, dim3(N, H), dim3(BNTHR), 0, s, p);
+  if (nblock_total > 0)
+    hipLaunchKernelGGL(gdn_bwd_grad_kernel, dim3(nblock_total, H), dim3(BNTHR), 0, s, p);
+  return check_launch("hmx_gdn_train_bwd");
 }

@@ -71,6 +71,12 @@ SIGNATURES: dict[str, list] = {
                           _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I64, _I32, _F32, _F32,
                           _I32, _P, ctypes.c_size_t, _P, ctypes.c_size_t, _P],
     "hmx_gka_train_bwd_workspace_bytes": [_I32, _I32, _I64],
+    "hmx_gdn_train_fwd": [_P, _I64, _P, _P, _I64, _P, _I32, _P, _I32, _P, _P, _P, _P, _I32,
+                          _I32, _I32, _F32, _I32, _I32, _F32, _P, ctypes.c_size_t, _P, _P, _P],
+    "hmx_gdn_train_bwd": [_P, _I64, _P, _P, _I64, _P, _I32, _P, _I32, _P, _I64, _P, _P, _P, _P,
+                          _I32, _I32, _I32, _F32, _I32, _P, _P, _P, _P, _P, _P, _P,
+                          ctypes.c_size_t, _P],
+    "hmx_gdn_train_bwd_workspace_bytes": [_I32, _I32],
     "hmx_plan_segments": [_I32, _P, _I32, _I32, _I64, _I32, _I32, _I32, _P, _I32, _P, _P],
     "hmx_plan_segments_bounds": [_I32, _P, _I32, _I64, _I32, _I32, _I32, _P, _I32, _P, _P],
     "hmx_ssd_chunk_fwd": [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I32,
@@ -95,6 +101,7 @@ _RESTYPES = {"hmx_last_error": ctypes.c_char_p, "hmx_gdn_chunk_workspace_bytes":
              "hmx_gka_chunk_workspace_bytes": ctypes.c_size_t,
              "hmx_gka_cheb_bwd_workspace_bytes": ctypes.c_size_t,
              "hmx_gka_train_bwd_workspace_bytes": ctypes.c_size_t,
+             "hmx_gdn_train_bwd_workspace_bytes": ctypes.c_size_t,
              "hmx_ssd_chunk_workspace_bytes": ctypes.c_size_t}
 
 

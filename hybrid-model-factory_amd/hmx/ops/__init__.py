@@ -5,6 +5,7 @@ from .gka import (chebyshev_iteration_gqa, fused_gka_gating, gka_chebyshev_gla,
                   gka_chebyshev_gla_decode, gka_chebyshev_gla_prefill, torch_decoding_one_step)
 from .conv import causal_conv1d_fn, causal_conv1d_update
 from .gates import ProjGates
+from .gdn_train import ChunkGatedDeltaRule
 from .gka_train import ChebyshevIteration, GkaChebyshevGla, latent_chebyshev
 from .norm import rms_norm_gated
 from .ssd import (mamba_chunk_scan_combined, mamba_chunk_scan_combined_varlen,
@@ -23,6 +24,7 @@ __all__ = [
     "gka_chebyshev_gla_prefill",
     "gka_chebyshev_gla",
     "torch_decoding_one_step",
+    "ChunkGatedDeltaRule",
     "ChebyshevIteration",
     "GkaChebyshevGla",
     "latent_chebyshev",

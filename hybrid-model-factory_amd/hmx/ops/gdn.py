@@ -452,7 +452,20 @@ def chunk_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None,
     The training layer passes q, k, v in the model's dtype.  bf16/fp16 inputs run
     the chunked kernel; fp32 inputs (which the chunked kernel's bf16 MFMA products
     would round) run the fp32 recurrent kernel over the same tokens, so an fp32
-    model gets fp32 arithmetic throughout."""
+    model gets fp32 arithmetic throughout.
+
+    With autograd recording and an input that requires a gradient, bf16 inputs go
+    through hmx.ChunkGatedDeltaRule (the same forward, with the chunked backward);
+    fp32 inputs have no backward here and raise NotImplementedError."""
+    ins = (q, k, v, g, beta, initial_state)
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in ins):
+        if q.dtype == torch.float32:
+            raise NotImplementedError("hmx chunk_gated_delta_rule: the backward needs bfloat16 "
+                                      "q, k, v")
+        from .gdn_train import ChunkGatedDeltaRule
+        return ChunkGatedDeltaRule.apply(q, k, v, g, beta, scale, initial_state,
+                                         output_final_state, cu_seqlens,
+                                         use_qk_l2norm_in_kernel, None)
     if q.dtype == torch.float32:
         return fused_recurrent_gated_delta_rule(q, k, v, g, beta, scale, initial_state,
                                                 output_final_state, cu_seqlens,

@@ -259,6 +259,49 @@ int hmx_gdn_chunk_fwd_noalloc(const void* q, int64_t q_token_stride, const void*
 size_t hmx_gdn_chunk_workspace_bytes(int32_t nseg_total, int32_t N, int32_t H, int32_t pooled);
 
 /*
+ * Training forward of the chunked gated delta rule: hmx_gdn_chunk_fwd with H query
+ * and key/value heads (k, v already expanded, one token stride), fp32 h0 / ht
+ * [N][H][128][128] (either may be null), no state pool, and in addition the state
+ * entering every 32-token block written to block_states, fp16 [nblock_total][H]
+ * [128][128], block b = cu_blocks[n] + (block index within sequence n); cu_blocks
+ * is int32 [N+1].  The backward reads these states.
+ * Replaces: the state recomputation of fla's chunk_gated_delta_rule backward
+ *   (chunk_gated_delta_rule_fwd_h), called by the training layer at
+ *   training/src/hmf/model/hybrid_zoo/layers/gated_deltanet/gdn.py:462-476.
+ */
+int hmx_gdn_train_fwd(const void* q, int64_t q_token_stride, const void* k, const void* v,
+                      int64_t kv_token_stride, const void* g, int32_t g_dtype, const void* beta,
+                      int32_t beta_dtype, void* o, const float* h0, float* ht,
+                      const int32_t* seg_table, int32_t nseg_total, int32_t N, int32_t H,
+                      float scale, int32_t use_qk_l2norm, int32_t max_warm_chunks,
+                      float decay_threshold, void* workspace, size_t workspace_bytes,
+                      void* block_states, const int32_t* cu_blocks, void* stream);
+
+/*
+ * Backward of the chunked gated delta rule for dout [tokens][H][128] bf16 (token
+ * stride dout_token_stride) and, optionally, dht (the gradient of the final states,
+ * fp32 [N][H][128][128]).  block_states: hmx_gdn_train_fwd's; block_table int32
+ * [nblock_total][4] = (first token, tokens (1-32), sequence, block index within
+ * the sequence); cu_blocks [N+1].  Writes dq, dk, dv [tokens][H][128] bf16 (rows
+ * of the blocks' tokens only), dg and dbeta [tokens][H] fp32, and dh0 (the
+ * gradient of the initial states, fp32 [N][H][128][128]) when not null.
+ * workspace: hmx_gdn_train_bwd_workspace_bytes(nblock_total, H) bytes.
+ * Replaces: the backward of fla's chunk_gated_delta_rule (un-vendored; the training
+ *   layer's call at training/src/hmf/model/hybrid_zoo/layers/gated_deltanet/gdn.py:
+ *   462-476, whose torch fallback is the recurrence of
+ *   .../qwen3_5_moe_hmf/modeling_qwen3_5_moe_hmf.py:330-407 under autograd).
+ */
+int hmx_gdn_train_bwd(const void* q, int64_t q_token_stride, const void* k, const void* v,
+                      int64_t kv_token_stride, const void* g, int32_t g_dtype, const void* beta,
+                      int32_t beta_dtype, const void* dout, int64_t dout_token_stride,
+                      const float* dht, const void* block_states, const int32_t* block_table,
+                      const int32_t* cu_blocks, int32_t nblock_total, int32_t N, int32_t H,
+                      float scale, int32_t use_qk_l2norm, void* dq, void* dk, void* dv,
+                      float* dg, float* dbeta, float* dh0, void* workspace,
+                      size_t workspace_bytes, void* stream);
+size_t hmx_gdn_train_bwd_workspace_bytes(int32_t nblock_total, int32_t H);
+
+/*
  * GKA gating: g = -exp(A_log) * softplus(a + dt_bias), alpha = sigmoid(alpha_in),
  * beta_out = sigmoid(b) when b is not NULL.  [num_tokens, num_heads] inputs with
  * arbitrary strides; contiguous outputs in out_dtype.
