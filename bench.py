@@ -544,6 +544,50 @@ def bench_gka_train(dev, steps, warmup, num_iter=8, B=8, T=4096, H=32):
                 ms_gka_chebyshev_gla_fwd_bwd=ms_l)
 
 
+def bench_gdn_train(dev, steps, warmup, B=8, T=4096, H=32):
+    """F4: the training GDN op (hmx.chunk_gated_delta_rule with the in-kernel L2
+    normalisation, through hmx.ChunkGatedDeltaRule under autograd) forward and
+    forward + backward, B=8 x T=4096 tokens, H=32, d=128; inputs as the training
+    layer forms them (q, k, v ~ N(0, 1) bf16, g = -e^{A_log} softplus(x + dt_bias)
+    fp32, beta = sigmoid(x) bf16, do ~ N(0, 1)).  Also forward + backward at the C1
+    shape (B=1, T=32768), where the state-gradient chain has one workgroup per head."""
+    import torch
+    import torch.nn.functional as F
+    import hmx
+    from hmx import workloads as wl
+    D = 128
+    g = torch.Generator(device=dev).manual_seed(wl.SEED_BASE + 13)
+
+    def inputs(B, T):
+        r = lambda *s: torch.randn(*s, generator=g, device=dev)
+        q, k, v, do = (r(B, T, H, D).bfloat16() for _ in range(4))
+        A_log = torch.rand(H, generator=g, device=dev) * 2.0 - 1.0
+        gate = -A_log.exp() * F.softplus(r(B, T, H) - 2.0)
+        beta = torch.sigmoid(r(B, T, H)).bfloat16()
+        return q, k, v, gate, beta, do
+
+    def run(B, T, with_bwd):
+        q, k, v, gate, beta, do = inputs(B, T)
+        ins = [t.clone().requires_grad_(True) for t in (q, k, v, gate, beta)]
+
+        def fwd():
+            with torch.no_grad():
+                hmx.chunk_gated_delta_rule(q, k, v, gate, beta, use_qk_l2norm_in_kernel=True)
+
+        def fwd_bwd():   # the gradients returned, not accumulated into .grad
+            o, _ = hmx.chunk_gated_delta_rule(*ins, use_qk_l2norm_in_kernel=True)
+            torch.autograd.grad(o, ins, do)
+        return _timed(fwd_bwd if with_bwd else fwd, steps, warmup)
+
+    ms_f = run(B, T, False)
+    ms_fb = run(B, T, True)
+    ms_c1 = run(1, 32768, True)
+    ff, fb = wl.gdn_train_flops(B * T, H)
+    return dict(ms_fwd=ms_f, ms_fwd_bwd=ms_fb, ms_c1_fwd_bwd=ms_c1, flops_fwd=ff, flops_bwd=fb,
+                tokens_per_s=B * T / (ms_fb * 1e-3),
+                TFLOPs_fwd_bwd=(ff + fb) / (ms_fb * 1e-3) / 1e12)
+
+
 def bench_ssd(dev, steps, warmup, b=2, T=16384, H=64, P=64, N=128, G=8):
     """C4: mamba_chunk_scan_combined, b=2, T=16384, H=64, P=64, N=128, G=8, fp32 final
     state (other shapes through the keywords: the primed layout is P = N = 128, G = H)."""
@@ -697,11 +741,11 @@ def measured_traffic(key):
 # --only accepts beside single legs
 LEGS = ["c1", "prefill_gqa", "prefill_varlen", "prefill_layer_gates", "onorm", "conv", "gdn_core",
         "mamba2_core", "gka_core", "gdn_decode", "gka_decode", "ssd_c4", "ssd_primed",
-        "ssd_decode", "gka8", "gka32", "gka_train"]
+        "ssd_decode", "gka8", "gka32", "gka_train", "gdn_train"]
 GROUPS = {"prefill": ["c1", "prefill_gqa", "prefill_varlen", "prefill_layer_gates"],
           "core": ["gdn_core", "mamba2_core", "gka_core"], "decode": ["gdn_decode", "gka_decode"],
           "ssd": ["ssd_c4", "ssd_primed", "ssd_decode"], "gka": ["gka8", "gka32"],
-          "train": ["gka_train"]}
+          "train": ["gka_train", "gdn_train"]}
 
 
 def measured_mfma_busy(key):
@@ -767,6 +811,7 @@ def main():
         "gka8": lambda: out.setdefault("gka", {}).__setitem__(8, bench_gka(dev, max(2, S // 4), 1, 8)),
         "gka32": lambda: out.setdefault("gka", {}).__setitem__(32, bench_gka(dev, max(2, S // 4), 1, 32)),
         "gka_train": lambda: out.__setitem__("gka_train", bench_gka_train(dev, max(2, S // 4), 1)),
+        "gdn_train": lambda: out.__setitem__("gdn_train", bench_gdn_train(dev, max(2, S // 4), 1)),
     }
     for name in LEGS:           # run order: the long compute-bound GKA legs last
         if name in sel:
@@ -932,6 +977,20 @@ def main():
                              "algorithmic_flops": r["flops"],
                              "hbm_GBps": round(r["GBps"], 1)},
             }
+    if "gdn_train" in out:
+        r = out["gdn_train"]
+        line["gdn_train"] = {
+            "value": round(r["tokens_per_s"], 1), "unit": "tokens/s (forward + backward)",
+            "ms_fwd": round(r["ms_fwd"], 4), "ms_fwd_bwd": round(r["ms_fwd_bwd"], 4),
+            "ms_fwd_bwd_at_c1_shape": round(r["ms_c1_fwd_bwd"], 4),
+            "config": {"workload": "F4 GDN training op (chunk_gated_delta_rule fwd + bwd)",
+                       "B": 8, "T": 4096, "H": 32, "d": 128, "use_qk_l2norm_in_kernel": True},
+            "roofline": {"bound": "mfma", "achieved": round(r["TFLOPs_fwd_bwd"], 1),
+                         "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(r["TFLOPs_fwd_bwd"] / BF16_PEAK_TFLOPS, 4),
+                         "algorithmic_flops_fwd": r["flops_fwd"],
+                         "algorithmic_flops_bwd": r["flops_bwd"]},
+        }
     if "gka_train" in out:
         r = out["gka_train"]
         line["gka_train"] = {

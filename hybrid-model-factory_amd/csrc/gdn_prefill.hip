@@ -1307,15 +1307,17 @@ __device__ __forceinline__ f16x8 frag_col(const f16* b, int ld, int k0, int c0, 
   return f16x8{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
 }
 
-// One block's rows of src into an fp16 [32][LR] array, times 1 / sqrt(|x|^2 + 1e-6)
-// with l2 (that factor into rnorm[row] when given).  512 threads: row tid >> 4,
-// features 8 (tid & 15) .. +7.
-__device__ __forceinline__ void stage_rows(f16* dst, const bf16* src, int64_t ts, int tok0,
-                                           int nval, bool l2, float* rnorm, int tid) {
+// the row of a block that thread tid stages (features 8 (tid & 15) .. +7 of row
+// tid >> 4), or zeros past the block's tokens
+__device__ __forceinline__ bf16x8 ld_row(const bf16* src, int64_t ts, int tok0, int nval, int tid) {
   const int row = tid >> 4, f0 = (tid & 15) * 8;
-  const bf16x8 x =
-      row < nval ? *reinterpret_cast<const bf16x8*>(src + (int64_t)(tok0 + row) * ts + f0)
-                 : bf16x8{};
+  return row < nval ? *reinterpret_cast<const bf16x8*>(src + (int64_t)(tok0 + row) * ts + f0)
+                    : bf16x8{};
+}
+// ... and its store into an fp16 [32][LR] array, times 1 / sqrt(|x|^2 + 1e-6) with l2
+// (that factor into rnorm[row] when given)
+__device__ __forceinline__ void put_row(f16* dst, const bf16x8& x, bool l2, float* rnorm, int tid) {
+  const int row = tid >> 4, f0 = (tid & 15) * 8;
   const float r = l2 ? row_inv_norm(x) : 1.f;
   *reinterpret_cast<f16x8*>(dst + row * LR + f0) = scale_h8(x, r);
   if (rnorm && (tid & 15) == 0) rnorm[row] = r;
@@ -1325,12 +1327,14 @@ struct Sc { float* G; float* E; float* F; float* B; };
 
 // wave 0: the block's in-block cumsum of g, e^gamma, e^{gamma_L - gamma} and beta
 // into LDS (lanes 0-31; 0 / 0 past the block's tokens)
-__device__ __forceinline__ void block_scalars(const Bwd& p, const Sc& s, int tok0, int nval, int h,
-                                              int lane) {
+__device__ __forceinline__ void ld_gates(const Bwd& p, int tok0, int nval, int h, int lane,
+                                         float& gv, float& bv) {
   const bool ok = lane < nval;
   const int64_t i = (int64_t)(tok0 + lane) * p.H + h;
-  const float gv = ok ? ld_scalar(p.g, i, p.g_dt) : 0.f;
-  const float bv = ok ? ld_scalar(p.beta, i, p.beta_dt) : 0.f;
+  gv = ok ? ld_scalar(p.g, i, p.g_dt) : 0.f;
+  bv = ok ? ld_scalar(p.beta, i, p.beta_dt) : 0.f;
+}
+__device__ __forceinline__ void block_scalars(const Sc& s, float gv, float bv, int lane) {
   const float gam = scan32(gv);
   const float gl = __builtin_bit_cast(float,
                                       __builtin_amdgcn_readlane(__builtin_bit_cast(int, gam), C - 1));
@@ -1340,6 +1344,11 @@ __device__ __forceinline__ void block_scalars(const Bwd& p, const Sc& s, int tok
     s.F[lane] = fast_exp(gl - gam);
     s.B[lane] = bv;
   }
+}
+
+// rows 16 mt + 4 q4 .. +3 of a per-token LDS array (one 16-byte read)
+__device__ __forceinline__ f32x4 row4(const float* a, int mt, int q4) {
+  return *reinterpret_cast<const f32x4*>(a + 16 * mt + 4 * q4);
 }
 
 __device__ __forceinline__ Sc sc_at(unsigned char* base) {
@@ -1364,9 +1373,15 @@ __global__ __launch_bounds__(BNTHR) void gdn_bwd_prep_kernel(Bwd p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int q4 = lane >> 4, l16 = lane & 15;
   const int tok0 = p.ctab[cb * 4], nval = p.ctab[cb * 4 + 1];
-  stage_rows(sK, p.k + (int64_t)h * D, p.kv_ts, tok0, nval, p.l2norm, nullptr, tid);
-  stage_rows(sQ, p.q + (int64_t)h * D, p.q_ts, tok0, nval, p.l2norm, nullptr, tid);
-  if (wave == 0) block_scalars(p, sc, tok0, nval, h, lane);
+  {
+    const bf16x8 xk = ld_row(p.k + (int64_t)h * D, p.kv_ts, tok0, nval, tid);
+    const bf16x8 xq = ld_row(p.q + (int64_t)h * D, p.q_ts, tok0, nval, tid);
+    float gv = 0.f, bv = 0.f;
+    if (wave == 0) ld_gates(p, tok0, nval, h, lane, gv, bv);
+    put_row(sK, xk, p.l2norm, nullptr, tid);
+    put_row(sQ, xq, p.l2norm, nullptr, tid);
+    if (wave == 0) block_scalars(sc, gv, bv, lane);
+  }
   lds_barrier();
   const int64_t mo = ((int64_t)cb * p.H + h) * C * C;
   {  // waves 0-3: a tile of Q^K^T -> P; waves 4-7: a tile of K^K^T -> N = beta Mm
@@ -1428,7 +1443,38 @@ __global__ __launch_bounds__(BNTHR) void gdn_bwd_prep_kernel(Bwd p) {
 constexpr int CH_OFF_K = 0, CH_OFF_Q = C * LR * 2, CH_OFF_DO = 2 * C * LR * 2;
 constexpr int CH_OFF_T = 3 * C * LR * 2, CH_OFF_P = CH_OFF_T + C * LL * 2;
 constexpr int CH_OFF_SC = CH_OFF_P + C * LL * 2;
-constexpr int CH_SMEM = CH_OFF_SC + 4 * C * 4;
+constexpr int CH_OFF_DS = CH_OFF_SC + 4 * C * 4;               // fp16 [D][LR] dS staging
+constexpr int CH_SMEM = CH_OFF_DS + D * LR * 2;
+
+// One block's global inputs for this thread, loaded a block or two ahead of use:
+// its row of k, q and dO (features 8 (tid & 15) .. +7 of row tid >> 4), two
+// entries of T and P, and (wave 0, lanes 0-31) the token's g and beta.
+struct ChainPre {
+  bf16x8 k, q, o;
+  uint32_t t, pm;
+  float g, b;
+  int nval;
+};
+
+__device__ __forceinline__ void chain_load(const Bwd& p, ChainPre& r, int cb, int tok0, int nval,
+                                           int h, int tid, int wave, int lane) {
+  const int row = tid >> 4, f0 = (tid & 15) * 8;
+  const bool ok = row < nval;
+  const int64_t t = tok0 + row;
+  r.k = ok ? *reinterpret_cast<const bf16x8*>(p.k + t * p.kv_ts + (int64_t)h * D + f0) : bf16x8{};
+  r.q = ok ? *reinterpret_cast<const bf16x8*>(p.q + t * p.q_ts + (int64_t)h * D + f0) : bf16x8{};
+  r.o = ok ? *reinterpret_cast<const bf16x8*>(p.dout + t * p.do_ts + (int64_t)h * D + f0) : bf16x8{};
+  const int64_t mo = ((int64_t)cb * p.H + h) * C * C + 2 * tid;
+  r.t = *reinterpret_cast<const uint32_t*>(p.tm + mo);
+  r.pm = *reinterpret_cast<const uint32_t*>(p.pm + mo);
+  r.g = r.b = 0.f;
+  if (wave == 0 && lane < nval) {
+    const int64_t i = (int64_t)(tok0 + lane) * p.H + h;
+    r.g = ld_scalar(p.g, i, p.g_dt);
+    r.b = ld_scalar(p.beta, i, p.beta_dt);
+  }
+  r.nval = nval;
+}
 
 __global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_chain_kernel(Bwd p) {
   __shared__ __align__(16) unsigned char smem[CH_SMEM];
@@ -1438,6 +1484,7 @@ __global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_chain_kernel(Bwd p) {
   f16* sT = reinterpret_cast<f16*>(smem + CH_OFF_T);
   f16* sP = reinterpret_cast<f16*>(smem + CH_OFF_P);
   const Sc sc = sc_at(smem + CH_OFF_SC);
+  f16* sDS = reinterpret_cast<f16*>(smem + CH_OFF_DS);
   const int n = blockIdx.x, h = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1455,26 +1502,56 @@ __global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_chain_kernel(Bwd p) {
       for (int v = 0; v < 4; ++v)
         dS[rt][v] = src ? src[(16 * rt + 4 * q4 + v) * D + c0 + l16] : 0.f;
   }
+  // a sequence's blocks are consecutive 32-token runs from its first token
+  int bos = 0, eos = 0;
+  if (b1 > b0) {
+    bos = p.ctab[b0 * 4];
+    eos = p.ctab[(b1 - 1) * 4] + p.ctab[(b1 - 1) * 4 + 1];
+  }
+  auto blk_tok = [&](int cb) { return bos + (cb - b0) * C; };
+  ChainPre pa, pb;                               // blocks cb and cb - 1
+  if (b1 > b0) chain_load(p, pa, b1 - 1, blk_tok(b1 - 1), eos - blk_tok(b1 - 1), h, tid, wave, lane);
+  if (b1 - 1 > b0) chain_load(p, pb, b1 - 2, blk_tok(b1 - 2), C, h, tid, wave, lane);
   for (int cb = b1 - 1; cb >= b0; --cb) {
-    const int tok0 = p.ctab[cb * 4], nval = p.ctab[cb * 4 + 1];
-    {  // the gradient of the state leaving block cb
-      f16* dst = p.dhc + ((int64_t)cb * p.H + h) * DD + c0 + l16;
+    // the gradient of the state leaving block cb, through LDS to 16-byte stores
 #pragma unroll
-      for (int rt = 0; rt < 8; ++rt)
+    for (int rt = 0; rt < 8; ++rt)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) dst[(16 * rt + 4 * q4 + v) * D] = (f16)dS[rt][v];
-    }
-    lds_barrier();   // the previous block's LDS reads are done
-    if (wave == 0) block_scalars(p, sc, tok0, nval, h, lane);
-    stage_rows(sK, p.k + (int64_t)h * D, p.kv_ts, tok0, nval, p.l2norm, nullptr, tid);
-    stage_rows(sQ, p.q + (int64_t)h * D, p.q_ts, tok0, nval, p.l2norm, nullptr, tid);
-    stage_rows(sDO, p.dout + (int64_t)h * D, p.do_ts, tok0, nval, false, nullptr, tid);
+      for (int v = 0; v < 4; ++v) sDS[(16 * rt + 4 * q4 + v) * LR + c0 + l16] = (f16)dS[rt][v];
+    lds_barrier();   // also: the previous block's LDS reads are done
     {
-      const int64_t mo = ((int64_t)cb * p.H + h) * C * C;
-      const int e = 2 * tid, i = e >> 5, j = e & 31;
-      *reinterpret_cast<uint32_t*>(sT + i * LL + j) = *reinterpret_cast<const uint32_t*>(p.tm + mo + e);
-      *reinterpret_cast<uint32_t*>(sP + i * LL + j) = *reinterpret_cast<const uint32_t*>(p.pm + mo + e);
+      f16* dst = p.dhc + ((int64_t)cb * p.H + h) * DD;
+#pragma unroll
+      for (int pass = 0; pass < 4; ++pass) {
+        const int e = (pass * BNTHR + tid) * 8, row = e >> 7, col = e & 127;
+        *reinterpret_cast<f16x8*>(dst + e) = *reinterpret_cast<const f16x8*>(sDS + row * LR + col);
+      }
     }
+    {  // stage block cb from registers
+      const int row = tid >> 4, f0 = (tid & 15) * 8;
+      const float rk = p.l2norm ? row_inv_norm(pa.k) : 1.f;
+      const float rq = p.l2norm ? row_inv_norm(pa.q) : 1.f;
+      *reinterpret_cast<f16x8*>(sK + row * LR + f0) = scale_h8(pa.k, rk);
+      *reinterpret_cast<f16x8*>(sQ + row * LR + f0) = scale_h8(pa.q, rq);
+      *reinterpret_cast<f16x8*>(sDO + row * LR + f0) = scale_h8(pa.o, 1.f);
+      const int e = 2 * tid, i = e >> 5, j = e & 31;
+      *reinterpret_cast<uint32_t*>(sT + i * LL + j) = pa.t;
+      *reinterpret_cast<uint32_t*>(sP + i * LL + j) = pa.pm;
+      if (wave == 0) {
+        const float gam = scan32(pa.g);
+        const float gl = __builtin_bit_cast(
+            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gam), C - 1));
+        if (lane < C) {
+          sc.G[lane] = gam;
+          sc.E[lane] = fast_exp(gam);
+          sc.F[lane] = fast_exp(gl - gam);
+          sc.B[lane] = pa.b;
+        }
+      }
+    }
+    // the loads two blocks ahead, in flight through this block's products
+    pa = pb;
+    if (cb - 2 >= b0) chain_load(p, pb, cb - 2, blk_tok(cb - 2), C, h, tid, wave, lane);
     lds_barrier();
     // dW = F K^ dS + P^T dO (tokens x this wave's columns), Z' = -E beta T^T dW
     f32x4 dW[2];
@@ -1581,22 +1658,38 @@ __global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_grad_kernel(Bwd p) {
   const int64_t DD = (int64_t)D * D, bh = (int64_t)cb * H + h;
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
 
-  // ---- P0: stage the block's rows, S0, dS, T and P -----------------------------
-  if (wave == 0) block_scalars(p, sc, tok0, nval, h, lane);
-  stage_rows(sK, p.k + (int64_t)h * D, p.kv_ts, tok0, nval, p.l2norm, sRk, tid);
-  stage_rows(sQ, p.q + (int64_t)h * D, p.q_ts, tok0, nval, p.l2norm, sRq, tid);
-  stage_rows(sDO, p.dout + (int64_t)h * D, p.do_ts, tok0, nval, false, nullptr, tid);
-  stage_rows(sX, p.v + (int64_t)h * D, p.kv_ts, tok0, nval, false, nullptr, tid);
-#pragma unroll
-  for (int pass = 0; pass < 4; ++pass) {
-    const int e = (pass * BNTHR + tid) * 8, row = e >> 7, col = e & 127;
-    *reinterpret_cast<f16x8*>(sS0 + row * LR + col) = *reinterpret_cast<const f16x8*>(p.hc + bh * DD + e);
-    *reinterpret_cast<f16x8*>(sDS + row * LR + col) = *reinterpret_cast<const f16x8*>(p.dhc + bh * DD + e);
-  }
+  // ---- P0: stage the block's rows, S0, dS, T and P (every load issued first) ----
   {
-    const int e = 2 * tid, i = e >> 5, j = e & 31;
-    *reinterpret_cast<uint32_t*>(sT + i * LL + j) = *reinterpret_cast<const uint32_t*>(p.tm + bh * C * C + e);
-    *reinterpret_cast<uint32_t*>(sPm + i * LL + j) = *reinterpret_cast<const uint32_t*>(p.pm + bh * C * C + e);
+    const bf16x8 xk = ld_row(p.k + (int64_t)h * D, p.kv_ts, tok0, nval, tid);
+    const bf16x8 xq = ld_row(p.q + (int64_t)h * D, p.q_ts, tok0, nval, tid);
+    const bf16x8 xo = ld_row(p.dout + (int64_t)h * D, p.do_ts, tok0, nval, tid);
+    const bf16x8 xv = ld_row(p.v + (int64_t)h * D, p.kv_ts, tok0, nval, tid);
+    f16x8 s0[4], ds[4];
+#pragma unroll
+    for (int pass = 0; pass < 4; ++pass) {
+      const int e = (pass * BNTHR + tid) * 8;
+      s0[pass] = *reinterpret_cast<const f16x8*>(p.hc + bh * DD + e);
+      ds[pass] = *reinterpret_cast<const f16x8*>(p.dhc + bh * DD + e);
+    }
+    const int e2 = 2 * tid;
+    const uint32_t tw = *reinterpret_cast<const uint32_t*>(p.tm + bh * C * C + e2);
+    const uint32_t pw = *reinterpret_cast<const uint32_t*>(p.pm + bh * C * C + e2);
+    float gv = 0.f, bv = 0.f;
+    if (wave == 0) ld_gates(p, tok0, nval, h, lane, gv, bv);
+    put_row(sK, xk, p.l2norm, sRk, tid);
+    put_row(sQ, xq, p.l2norm, sRq, tid);
+    put_row(sDO, xo, false, nullptr, tid);
+    put_row(sX, xv, false, nullptr, tid);
+    if (wave == 0) block_scalars(sc, gv, bv, lane);
+#pragma unroll
+    for (int pass = 0; pass < 4; ++pass) {
+      const int e = (pass * BNTHR + tid) * 8, row = e >> 7, col = e & 127;
+      *reinterpret_cast<f16x8*>(sS0 + row * LR + col) = s0[pass];
+      *reinterpret_cast<f16x8*>(sDS + row * LR + col) = ds[pass];
+    }
+    const int i = e2 >> 5, j = e2 & 31;
+    *reinterpret_cast<uint32_t*>(sT + i * LL + j) = tw;
+    *reinterpret_cast<uint32_t*>(sPm + i * LL + j) = pw;
   }
   lds_barrier();
 
@@ -1641,13 +1734,15 @@ __global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_grad_kernel(Bwd p) {
       if (lane == 0) sPD[wave] = d;
     }
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+    for (int mt = 0; mt < 2; ++mt) {
+      const f32x4 e4 = row4(sc.E, mt, q4), b4 = row4(sc.B, mt, q4);
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int r = 16 * mt + 4 * q4 + v, idx = r * LR + c0 + l16;
-        Ut[mt][v] = (float)sX[idx] - sc.E[r] * KS[mt][v];
-        sX[idx] = (f16)(sc.B[r] * Ut[mt][v]);
+        Ut[mt][v] = (float)sX[idx] - e4[v] * KS[mt][v];
+        sX[idx] = (f16)(b4[v] * Ut[mt][v]);
       }
+    }
   }
   lds_barrier();
 
@@ -1658,20 +1753,22 @@ __global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_grad_kernel(Bwd p) {
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
       W[mt] = mfma16h(frag_h(sT, LL, 16 * mt, 0, lane), bx, zero);
+      const f32x4 f4r = row4(sc.F, mt, q4);
 #pragma unroll
-      for (int v = 0; v < 4; ++v) dW[mt][v] = sc.F[16 * mt + 4 * q4 + v] * KD[mt][v];
+      for (int v = 0; v < 4; ++v) dW[mt][v] = f4r[v] * KD[mt][v];
       dW[mt] = mfma16h(frag_col(sPm, LL, 0, 16 * mt, lane), bdo, dW[mt]);
     }
     const f16x8 bw = h8(dW[0], dW[1]);
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
       const f32x4 Z = mfma16h(frag_t_perm_h(sT, LL, 0, 16 * mt, lane), bw, zero);
+      const f32x4 b4 = row4(sc.B, mt, q4);
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int r = 16 * mt + 4 * q4 + v, idx = r * LR + c0 + l16;
         sW[idx] = (f16)W[mt][v];
         sZ[idx] = (f16)Z[v];
-        if (r < nval) p.dv[((int64_t)(tok0 + r) * H + h) * D + c0 + l16] = (bf16)(sc.B[r] * Z[v]);
+        if (r < nval) p.dv[((int64_t)(tok0 + r) * H + h) * D + c0 + l16] = (bf16)(b4[v] * Z[v]);
         const float zu = row16_sum(Z[v] * Ut[mt][v]);
         if (l16 == 0) sPB[wave * C + r] = zu;
       }
@@ -1682,6 +1779,7 @@ __global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_grad_kernel(Bwd p) {
   // ---- P3: dO S0^T, Z S0^T, W dS^T (tokens x this wave's key features); a tile of
   // Z W^T (-> dN, Dm) or dO W^T (-> Dp) with their row and column sums -------------
   f32x4 DQ[2], DK[2];
+  f32x4 qh[2], kh[2];      // q^, k^ at this lane's accumulator positions
   {
     f32x4 A0[2] = {zero, zero}, A1[2] = {zero, zero}, A2[2] = {zero, zero};
 #pragma unroll
@@ -1695,23 +1793,26 @@ __global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_grad_kernel(Bwd p) {
       }
     }
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+    for (int mt = 0; mt < 2; ++mt) {
+      const f32x4 e4 = row4(sc.E, mt, q4), b4 = row4(sc.B, mt, q4), f4r = row4(sc.F, mt, q4);
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int r = 16 * mt + 4 * q4 + v, idx = r * LR + c0 + l16;
-        const float qt = p.scale * sc.E[r] * A0[mt][v];
-        const float ut = -sc.E[r] * sc.B[r] * A1[mt][v];
-        const float st = sc.F[r] * A2[mt][v];
-        const float qh = (float)sQ[idx], kh = (float)sK[idx];
+        const float qt = p.scale * e4[v] * A0[mt][v];
+        const float ut = -e4[v] * b4[v] * A1[mt][v];
+        const float st = f4r[v] * A2[mt][v];
+        qh[mt][v] = (float)sQ[idx];
+        kh[mt][v] = (float)sK[idx];
         DQ[mt][v] = qt;
         DK[mt][v] = ut + st;
-        const float gq = row16_sum(qh * qt + kh * (ut - st));
-        const float cj = row16_sum(kh * st);
+        const float gq = row16_sum(qh[mt][v] * qt + kh[mt][v] * (ut - st));
+        const float cj = row16_sum(kh[mt][v] * st);
         if (l16 == 0) {
           sPG[(8 + wave) * C + r] = gq;
           sPC[wave * C + r] = cj;
         }
       }
+    }
   }
   {
     const int t = wave & 3, mt = t >> 1, nt = t & 1;
@@ -1721,16 +1822,18 @@ __global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_grad_kernel(Bwd p) {
     for (int ks = 0; ks < 4; ++ks)
       acc = mfma16h(frag_h(A, LR, 16 * mt, 32 * ks, lane), frag_h(sW, LR, 16 * nt, 32 * ks, lane), acc);
     const int j = 16 * nt + l16;
+    const float gj = sc.G[j];
+    const f32x4 gi4 = row4(sc.G, mt, q4), bi4 = row4(sc.B, mt, q4);
     float csum = 0.f;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int i = 16 * mt + 4 * q4 + v;
-      const float gm = j <= i ? fast_exp(sc.G[i] - sc.G[j]) : 0.f;
+      const float gm = j <= i ? fast_exp(gi4[v] - gj) : 0.f;
       float x;
       if (wave < 4) {   // dN = -strict_lower(Z W^T), Dm = beta dN . Gm
         const float dn = j < i ? -acc[v] : 0.f;
         const float kk = sKK[i * LF + j];
-        const float d = sc.B[i] * dn * gm;
+        const float d = bi4[v] * dn * gm;
         sDm[i * LL + j] = (f16)d;
         x = d * kk;
         const float db = row16_sum(dn * kk * gm);
@@ -1764,9 +1867,9 @@ __global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_grad_kernel(Bwd p) {
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const int r = 16 * mt + 4 * q4 + v, idx = r * LR + c0 + l16;
-        const float sq = row16_sum((float)sQ[idx] * DQ[mt][v]);
-        const float sk = row16_sum((float)sK[idx] * DK[mt][v]);
+        const int r = 16 * mt + 4 * q4 + v;
+        const float sq = row16_sum(qh[mt][v] * DQ[mt][v]);
+        const float sk = row16_sum(kh[mt][v] * DK[mt][v]);
         if (l16 == 0) {
           sPQ[wave * C + r] = sq;
           sPK[wave * C + r] = sk;
@@ -1777,20 +1880,23 @@ __global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_grad_kernel(Bwd p) {
 
   // ---- P5: dq, dk (through the L2 normalisation); dg, dbeta --------------------
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
+  for (int mt = 0; mt < 2; ++mt) {
+    f32x4 sq = zero, sk = zero;
+    if (p.l2norm) {
+#pragma unroll
+      for (int w = 0; w < 8; ++w) {
+        sq += row4(sPQ + w * C, mt, q4);
+        sk += row4(sPK + w * C, mt, q4);
+      }
+    }
+    const f32x4 rq4 = row4(sRq, mt, q4), rk4 = row4(sRk, mt, q4);
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      const int r = 16 * mt + 4 * q4 + v, idx = r * LR + c0 + l16;
+      const int r = 16 * mt + 4 * q4 + v;
       float dq = DQ[mt][v], dk = DK[mt][v];
       if (p.l2norm) {
-        float sq = 0.f, sk = 0.f;
-#pragma unroll
-        for (int w = 0; w < 8; ++w) {
-          sq += sPQ[w * C + r];
-          sk += sPK[w * C + r];
-        }
-        dq = sRq[r] * (dq - (float)sQ[idx] * sq);
-        dk = sRk[r] * (dk - (float)sK[idx] * sk);
+        dq = rq4[v] * (dq - qh[mt][v] * sq[v]);
+        dk = rk4[v] * (dk - kh[mt][v] * sk[v]);
       }
       if (r < nval) {
         const int64_t o = ((int64_t)(tok0 + r) * H + h) * D + c0 + l16;
@@ -1798,6 +1904,7 @@ __global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_grad_kernel(Bwd p) {
         p.dk[o] = (bf16)dk;
       }
     }
+  }
   if (wave == 0) {
     float dgam = 0.f, db = 0.f, cl = 0.f, dd = 0.f;
     if (lane < C) {

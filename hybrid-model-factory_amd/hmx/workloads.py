@@ -156,6 +156,17 @@ def gka_train_flops(T: int, H: int, num_iter: int, d: int = 128, C: int = 64):
             2.0 * T * H * ((n + 6) * d * d + (2 * n + 6) * C * d))
 
 
+def gdn_train_flops(T: int, H: int, d: int = 128, C: int = 32):
+    """(forward, backward) FLOPs of the chunked gated delta rule's training op over T
+    tokens x H heads, 32-token blocks.  Forward: the prefill's 2*T*H*(3 d^2 + 5 C d).
+    Backward: 2*T*H*(11 d^2 + 20 C d) = the forward's recomputation of the block
+    states, the prep (Q^K^T, K^K^T: 2 C d), the state-gradient chain (K^ dS, two
+    products back into dS: 3 d^2; P^T dO, T^T dW: 2 C d) and the per-block gradients
+    (K^ S0, K^ dS, dO S0^T, Z S0^T, W dS^T: 5 d^2; Q^K^T, K^K^T, W, P^T dO, Z, Z W^T,
+    dO W^T and four C x C x d products back: 11 C d)."""
+    return (2.0 * T * H * (3 * d * d + 5 * C * d), 2.0 * T * H * (11 * d * d + 20 * C * d))
+
+
 def gka_prefill_bytes(T: int, H: int, HKV: int, d: int = 128, n_seqs: int = 1) -> float:
     """q,o [T,H,d] + k,v [T,HKV,d] bf16 + alpha,beta,g fp32 + two fp32 final states."""
     return T * H * 2 * d * 2 + T * HKV * 2 * d * 2 + 3 * T * H * 4 + 2 * n_seqs * H * d * d * 4
