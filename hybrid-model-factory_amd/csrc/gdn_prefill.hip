@@ -1293,7 +1293,7 @@ struct Bwd {
   bf16* dq; bf16* dk; bf16* dv;   // [tokens][H][D]
   float* dg; float* dbeta;        // [tokens][H]
   float* dh0;                 // [N][H][D][D] or null
-  int H;
+  int H, nblk;
   float scale;
   int l2norm;
 };
@@ -1623,6 +1623,37 @@ constexpr int G_OFF_PD = G_OFF_PK + 8 * C * 4;             // [8] <dS, S0> per w
 constexpr int G_SMEM = G_OFF_PD + 8 * 4;
 static_assert(G_SMEM <= 160 * 1024, "LDS budget");
 
+// One block's global inputs for this thread (loaded while the previous block is
+// processed): its rows of k, q, dO, v; 1/4 of S0 and of dS; two entries of T and P;
+// (wave 0, lanes 0-31) the token's g and beta.
+struct GradPre {
+  bf16x8 k, q, o, v;
+  f16x8 s0[4], ds[4];
+  uint32_t t, pm;
+  float g, b;
+};
+
+__device__ __forceinline__ void grad_load(const Bwd& p, GradPre& r, int64_t bh, int h, int tok0,
+                                          int nval, int tid, int wave, int lane) {
+  r.k = ld_row(p.k + (int64_t)h * D, p.kv_ts, tok0, nval, tid);
+  r.q = ld_row(p.q + (int64_t)h * D, p.q_ts, tok0, nval, tid);
+  r.o = ld_row(p.dout + (int64_t)h * D, p.do_ts, tok0, nval, tid);
+  r.v = ld_row(p.v + (int64_t)h * D, p.kv_ts, tok0, nval, tid);
+  const int64_t DD = (int64_t)D * D;
+#pragma unroll
+  for (int pass = 0; pass < 4; ++pass) {
+    const int e = (pass * BNTHR + tid) * 8;
+    r.s0[pass] = *reinterpret_cast<const f16x8*>(p.hc + bh * DD + e);
+    r.ds[pass] = *reinterpret_cast<const f16x8*>(p.dhc + bh * DD + e);
+  }
+  r.t = *reinterpret_cast<const uint32_t*>(p.tm + bh * C * C + 2 * tid);
+  r.pm = *reinterpret_cast<const uint32_t*>(p.pm + bh * C * C + 2 * tid);
+  r.g = r.b = 0.f;
+  if (wave == 0) ld_gates(p, tok0, nval, h, lane, r.g, r.b);
+}
+
+// Persistent: workgroup w takes blocks (block, head) = w, w + gridDim.x, ... and
+// loads each one's inputs while it processes the one before.
 __global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_grad_kernel(Bwd p) {
   __shared__ __align__(16) unsigned char smem[G_SMEM];
   f16* sK = reinterpret_cast<f16*>(smem + G_OFF_K);
@@ -1649,48 +1680,48 @@ __global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_grad_kernel(Bwd p) {
   float* sPK = reinterpret_cast<float*>(smem + G_OFF_PK);
   float* sPD = reinterpret_cast<float*>(smem + G_OFF_PD);
 
-  const int cb = blockIdx.x, h = blockIdx.y, H = p.H;
+  const int H = p.H, total = p.nblk * H;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int q4 = lane >> 4, l16 = lane & 15;
   const int c0 = 16 * wave;      // this wave's value columns (P1-P2) / key features (P3-P5)
-  const int tok0 = p.ctab[cb * 4], nval = p.ctab[cb * 4 + 1];
-  const int64_t DD = (int64_t)D * D, bh = (int64_t)cb * H + h;
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  int it = blockIdx.x;
+  if (it >= total) return;
+  int cb = it / H, h = it - cb * H;
+  int tok0 = p.ctab[cb * 4], nval = p.ctab[cb * 4 + 1];
+  GradPre pre;
+  grad_load(p, pre, (int64_t)cb * H + h, h, tok0, nval, tid, wave, lane);
+  for (;;) {
+  const int nxt = it + gridDim.x;
+  int ncb = 0, nh = 0, ntok0 = 0, nnval = 0;
+  if (nxt < total) {
+    ncb = nxt / H;
+    nh = nxt - ncb * H;
+    ntok0 = p.ctab[ncb * 4];
+    nnval = p.ctab[ncb * 4 + 1];
+  }
+  const int64_t bh = (int64_t)cb * H + h;
 
-  // ---- P0: stage the block's rows, S0, dS, T and P (every load issued first) ----
+  // ---- P0: stage this block from registers; the next block's loads go out -------
+  lds_barrier();   // the previous block's LDS reads are done
   {
-    const bf16x8 xk = ld_row(p.k + (int64_t)h * D, p.kv_ts, tok0, nval, tid);
-    const bf16x8 xq = ld_row(p.q + (int64_t)h * D, p.q_ts, tok0, nval, tid);
-    const bf16x8 xo = ld_row(p.dout + (int64_t)h * D, p.do_ts, tok0, nval, tid);
-    const bf16x8 xv = ld_row(p.v + (int64_t)h * D, p.kv_ts, tok0, nval, tid);
-    f16x8 s0[4], ds[4];
-#pragma unroll
-    for (int pass = 0; pass < 4; ++pass) {
-      const int e = (pass * BNTHR + tid) * 8;
-      s0[pass] = *reinterpret_cast<const f16x8*>(p.hc + bh * DD + e);
-      ds[pass] = *reinterpret_cast<const f16x8*>(p.dhc + bh * DD + e);
-    }
-    const int e2 = 2 * tid;
-    const uint32_t tw = *reinterpret_cast<const uint32_t*>(p.tm + bh * C * C + e2);
-    const uint32_t pw = *reinterpret_cast<const uint32_t*>(p.pm + bh * C * C + e2);
-    float gv = 0.f, bv = 0.f;
-    if (wave == 0) ld_gates(p, tok0, nval, h, lane, gv, bv);
-    put_row(sK, xk, p.l2norm, sRk, tid);
-    put_row(sQ, xq, p.l2norm, sRq, tid);
-    put_row(sDO, xo, false, nullptr, tid);
-    put_row(sX, xv, false, nullptr, tid);
-    if (wave == 0) block_scalars(sc, gv, bv, lane);
+    put_row(sK, pre.k, p.l2norm, sRk, tid);
+    put_row(sQ, pre.q, p.l2norm, sRq, tid);
+    put_row(sDO, pre.o, false, nullptr, tid);
+    put_row(sX, pre.v, false, nullptr, tid);
+    if (wave == 0) block_scalars(sc, pre.g, pre.b, lane);
 #pragma unroll
     for (int pass = 0; pass < 4; ++pass) {
       const int e = (pass * BNTHR + tid) * 8, row = e >> 7, col = e & 127;
-      *reinterpret_cast<f16x8*>(sS0 + row * LR + col) = s0[pass];
-      *reinterpret_cast<f16x8*>(sDS + row * LR + col) = ds[pass];
+      *reinterpret_cast<f16x8*>(sS0 + row * LR + col) = pre.s0[pass];
+      *reinterpret_cast<f16x8*>(sDS + row * LR + col) = pre.ds[pass];
     }
-    const int i = e2 >> 5, j = e2 & 31;
-    *reinterpret_cast<uint32_t*>(sT + i * LL + j) = tw;
-    *reinterpret_cast<uint32_t*>(sPm + i * LL + j) = pw;
+    const int e2 = 2 * tid, i = e2 >> 5, j = e2 & 31;
+    *reinterpret_cast<uint32_t*>(sT + i * LL + j) = pre.t;
+    *reinterpret_cast<uint32_t*>(sPm + i * LL + j) = pre.pm;
   }
+  if (nxt < total) grad_load(p, pre, (int64_t)ncb * H + nh, nh, ntok0, nnval, tid, wave, lane);
   lds_barrier();
 
   // ---- P1: K^ S0 and K^ dS (tokens x this wave's value columns), a tile of Q^K^T
@@ -1931,6 +1962,13 @@ __global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_grad_kernel(Bwd p) {
       p.dbeta[o] = db;
     }
   }
+  if (nxt >= total) break;
+  it = nxt;
+  cb = ncb;
+  h = nh;
+  tok0 = ntok0;
+  nval = nnval;
+  }
 }
 
 }  // namespace train
@@ -1998,12 +2036,18 @@ extern "C" int hmx_gdn_train_bwd(const void* q, int64_t q_token_stride, const vo
   p.ctab = block_table; p.cu_blk = cu_blocks;
   p.dq = static_cast<bf16*>(dq); p.dk = static_cast<bf16*>(dk); p.dv = static_cast<bf16*>(dv);
   p.dg = dg; p.dbeta = dbeta; p.dh0 = dh0;
-  p.H = H; p.scale = scale; p.l2norm = use_qk_l2norm;
+  p.H = H; p.nblk = nblock_total; p.scale = scale; p.l2norm = use_qk_l2norm;
   hipStream_t s = (hipStream_t)stream;
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    cus = 256;
+  const int64_t work = (int64_t)nblock_total * H;
+  const int grad_grid = (int)std::min<int64_t>(work, (int64_t)cus);
   if (nblock_total > 0)
     hipLaunchKernelGGL(gdn_bwd_prep_kernel, dim3(nblock_total, H), dim3(BNTHR), 0, s, p);
   hipLaunchKernelGGL(gdn_bwd_chain_kernel, dim3(N, H), dim3(BNTHR), 0, s, p);
   if (nblock_total > 0)
-    hipLaunchKernelGGL(gdn_bwd_grad_kernel, dim3(nblock_total, H), dim3(BNTHR), 0, s, p);
+    hipLaunchKernelGGL(gdn_bwd_grad_kernel, dim3(grad_grid), dim3(BNTHR), 0, s, p);
   return check_launch("hmx_gdn_train_bwd");
 }
