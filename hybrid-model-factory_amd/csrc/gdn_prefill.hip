@@ -1290,6 +1290,9 @@ struct Bwd {
   f16* pm;                    // [nblk][H][C][C] scale lower(Q^K^T . Gm)
   const int* ctab;            // [nblk][4]: first token, tokens, sequence, block in sequence
   const int* cu_blk;          // [N+1]
+  const int* cseg;            // [nseg][3]: sequence, first block, end block of a chain segment
+  int max_warm;               // warm-up blocks a chain segment may add past its end
+  float decay_thresh;         // ... to bring the dropped history under e^-decay_thresh
   bf16* dq; bf16* dk; bf16* dv;   // [tokens][H][D]
   float* dg; float* dbeta;        // [tokens][H]
   float* dh0;                 // [N][H][D][D] or null
@@ -1485,41 +1488,74 @@ __global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_chain_kernel(Bwd p) {
   f16* sP = reinterpret_cast<f16*>(smem + CH_OFF_P);
   const Sc sc = sc_at(smem + CH_OFF_SC);
   f16* sDS = reinterpret_cast<f16*>(smem + CH_OFF_DS);
-  const int n = blockIdx.x, h = blockIdx.y;
+  const int sg = blockIdx.x, h = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int q4 = lane >> 4, l16 = lane & 15;
   const int c0 = 16 * wave;                      // this wave's value columns
   const int64_t DD = (int64_t)D * D;
-  const int b0 = p.cu_blk[n], b1 = p.cu_blk[n + 1];
+  const int n = p.cseg[sg * 3], ba = p.cseg[sg * 3 + 1], bb = p.cseg[sg * 3 + 2];
+  const int first = p.cu_blk[n], last = p.cu_blk[n + 1];   // the sequence's blocks
+  // a sequence's blocks are consecutive 32-token runs from its first token
+  int bos = 0, eos = 0;
+  if (last > first) {
+    bos = p.ctab[first * 4];
+    eos = p.ctab[(last - 1) * 4] + p.ctab[(last - 1) * 4 + 1];
+  }
+  auto blk_tok = [&](int cb) { return bos + (cb - first) * C; };
+  // Where this segment's chain starts.  A segment that ends before the sequence
+  // does starts from zero at the end of a warm-up over the following blocks, long
+  // enough that the dropped history, bounded by prod_t e^{g_t} max(1, |1 - beta_t|)
+  // (the spectral norm of e^g (I - beta k k^T) for |k| = 1, which the in-kernel
+  // L2 normalisation guarantees), is below e^-decay_thresh; without that bound
+  // within max_warm blocks, or without the normalisation, it starts from the
+  // sequence end (the exact chain).
+  int wend = last;
+  if (bb < last && p.l2norm) {
+    if (wave == 0) {
+      float acc = 0.f;
+      int w = last;
+      const int lim = min(last, bb + p.max_warm);
+      for (int cb = bb; cb < lim; ++cb) {
+        const int t0 = blk_tok(cb), nv = min(C, eos - t0);
+        float x = 0.f;
+        if (lane < nv) {
+          const int64_t i = (int64_t)(t0 + lane) * p.H + h;
+          x = ld_scalar(p.g, i, p.g_dt) + __logf(fmaxf(1.f, fabsf(1.f - ld_scalar(p.beta, i, p.beta_dt))));
+        }
+        acc += wave_sum(x);
+        if (acc < -p.decay_thresh) {
+          w = cb + 1;
+          break;
+        }
+      }
+      if (lane == 0) sc.G[0] = __builtin_bit_cast(float, w);
+    }
+    lds_barrier();
+    wend = __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sc.G[0]));
+  }
   // dS[rt]: rows 16 rt + 4 q4 + v, column c0 + l16
   f32x4 dS[8];
   {
-    const float* src = p.dht ? p.dht + ((int64_t)n * p.H + h) * DD : nullptr;
+    const float* src = (p.dht && wend == last) ? p.dht + ((int64_t)n * p.H + h) * DD : nullptr;
 #pragma unroll
     for (int rt = 0; rt < 8; ++rt)
 #pragma unroll
       for (int v = 0; v < 4; ++v)
         dS[rt][v] = src ? src[(16 * rt + 4 * q4 + v) * D + c0 + l16] : 0.f;
   }
-  // a sequence's blocks are consecutive 32-token runs from its first token
-  int bos = 0, eos = 0;
-  if (b1 > b0) {
-    bos = p.ctab[b0 * 4];
-    eos = p.ctab[(b1 - 1) * 4] + p.ctab[(b1 - 1) * 4 + 1];
-  }
-  auto blk_tok = [&](int cb) { return bos + (cb - b0) * C; };
   ChainPre pa, pb;                               // blocks cb and cb - 1
-  if (b1 > b0) chain_load(p, pa, b1 - 1, blk_tok(b1 - 1), eos - blk_tok(b1 - 1), h, tid, wave, lane);
-  if (b1 - 1 > b0) chain_load(p, pb, b1 - 2, blk_tok(b1 - 2), C, h, tid, wave, lane);
-  for (int cb = b1 - 1; cb >= b0; --cb) {
-    // the gradient of the state leaving block cb, through LDS to 16-byte stores
+  if (wend > ba) chain_load(p, pa, wend - 1, blk_tok(wend - 1), min(C, eos - blk_tok(wend - 1)), h, tid, wave, lane);
+  if (wend - 1 > ba) chain_load(p, pb, wend - 2, blk_tok(wend - 2), C, h, tid, wave, lane);
+  for (int cb = wend - 1; cb >= ba; --cb) {
+    // the gradient of the state leaving block cb (blocks of this segment), through
+    // LDS to 16-byte stores
 #pragma unroll
     for (int rt = 0; rt < 8; ++rt)
 #pragma unroll
       for (int v = 0; v < 4; ++v) sDS[(16 * rt + 4 * q4 + v) * LR + c0 + l16] = (f16)dS[rt][v];
     lds_barrier();   // also: the previous block's LDS reads are done
-    {
+    if (cb < bb) {
       f16* dst = p.dhc + ((int64_t)cb * p.H + h) * DD;
 #pragma unroll
       for (int pass = 0; pass < 4; ++pass) {
@@ -1551,7 +1587,7 @@ __global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_chain_kernel(Bwd p) {
     }
     // the loads two blocks ahead, in flight through this block's products
     pa = pb;
-    if (cb - 2 >= b0) chain_load(p, pb, cb - 2, blk_tok(cb - 2), C, h, tid, wave, lane);
+    if (cb - 2 >= ba) chain_load(p, pb, cb - 2, blk_tok(cb - 2), C, h, tid, wave, lane);
     lds_barrier();
     // dW = F K^ dS + P^T dO (tokens x this wave's columns), Z' = -E beta T^T dW
     f32x4 dW[2];
@@ -1595,7 +1631,7 @@ __global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_chain_kernel(Bwd p) {
       dS[rt] = mfma16h(frag_col(sQ, LR, 0, 16 * rt, lane), bqe, dS[rt]);
     }
   }
-  if (p.dh0) {
+  if (p.dh0 && ba == first) {
     float* dst = p.dh0 + ((int64_t)n * p.H + h) * DD + c0 + l16;
 #pragma unroll
     for (int rt = 0; rt < 8; ++rt)
@@ -2004,14 +2040,18 @@ extern "C" int hmx_gdn_train_bwd(const void* q, int64_t q_token_stride, const vo
                                  const void* dout, int64_t dout_token_stride, const float* dht,
                                  const void* block_states, const int32_t* block_table,
                                  const int32_t* cu_blocks, int32_t nblock_total, int32_t N,
-                                 int32_t H, float scale, int32_t use_qk_l2norm, void* dq,
-                                 void* dk, void* dv, float* dg, float* dbeta, float* dh0,
-                                 void* workspace, size_t workspace_bytes, void* stream) {
+                                 const int32_t* chain_segments, int32_t nchain_segments,
+                                 int32_t max_warm_blocks, float decay_threshold, int32_t H,
+                                 float scale, int32_t use_qk_l2norm, void* dq, void* dk,
+                                 void* dv, float* dg, float* dbeta, float* dh0, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
   using namespace hmx::gdnp::train;
   HMX_REQUIRE(q && k && v && g && beta && dout && block_states && block_table && cu_blocks &&
-                  dq && dk && dv && dg && dbeta, HMX_EINVAL, "hmx_gdn_train_bwd: null pointer");
-  HMX_REQUIRE(N > 0 && H > 0 && nblock_total >= 0, HMX_EINVAL,
-              "hmx_gdn_train_bwd: bad sizes (N=%d H=%d nblock=%d)", N, H, nblock_total);
+                  chain_segments && dq && dk && dv && dg && dbeta,
+              HMX_EINVAL, "hmx_gdn_train_bwd: null pointer");
+  HMX_REQUIRE(N > 0 && H > 0 && nblock_total >= 0 && nchain_segments >= N && max_warm_blocks >= 0,
+              HMX_EINVAL, "hmx_gdn_train_bwd: bad sizes (N=%d H=%d nblock=%d nseg=%d warm=%d)", N,
+              H, nblock_total, nchain_segments, max_warm_blocks);
   HMX_REQUIRE(g_dtype >= 0 && g_dtype <= 2 && beta_dtype >= 0 && beta_dtype <= 2,
               HMX_EUNSUPPORTED, "hmx_gdn_train_bwd: g/beta dtype");
   HMX_REQUIRE(q_token_stride % 8 == 0 && kv_token_stride % 8 == 0 && dout_token_stride % 8 == 0 &&
@@ -2034,6 +2074,7 @@ extern "C" int hmx_gdn_train_bwd(const void* q, int64_t q_token_stride, const vo
   p.tm = ws + (size_t)nblock_total * H * D * D;
   p.pm = p.tm + (size_t)nblock_total * H * C * C;
   p.ctab = block_table; p.cu_blk = cu_blocks;
+  p.cseg = chain_segments; p.max_warm = max_warm_blocks; p.decay_thresh = decay_threshold;
   p.dq = static_cast<bf16*>(dq); p.dk = static_cast<bf16*>(dk); p.dv = static_cast<bf16*>(dv);
   p.dg = dg; p.dbeta = dbeta; p.dh0 = dh0;
   p.H = H; p.nblk = nblock_total; p.scale = scale; p.l2norm = use_qk_l2norm;
@@ -2046,7 +2087,7 @@ extern "C" int hmx_gdn_train_bwd(const void* q, int64_t q_token_stride, const vo
   const int grad_grid = (int)std::min<int64_t>(work, (int64_t)cus);
   if (nblock_total > 0)
     hipLaunchKernelGGL(gdn_bwd_prep_kernel, dim3(nblock_total, H), dim3(BNTHR), 0, s, p);
-  hipLaunchKernelGGL(gdn_bwd_chain_kernel, dim3(N, H), dim3(BNTHR), 0, s, p);
+  hipLaunchKernelGGL(gdn_bwd_chain_kernel, dim3(nchain_segments, H), dim3(BNTHR), 0, s, p);
   if (nblock_total > 0)
     hipLaunchKernelGGL(gdn_bwd_grad_kernel, dim3(grad_grid), dim3(BNTHR), 0, s, p);
   return check_launch("hmx_gdn_train_bwd");

@@ -13,8 +13,10 @@ The forward is the serving prefill (hmx_gdn_chunk_fwd).  The backward
 recomputes the state entering every 32-token block (hmx_gdn_train_fwd: the
 same walk writing those states, fp16) instead of keeping them from the forward,
 as fla's backward recomputes them, then runs hmx_gdn_train_bwd: the blocks' T and
-masked Q K^T, the reverse chain of the state gradient over each sequence's
-blocks, and the per-block gradients.  bf16 q/k/v with head dim 128 only.
+masked Q K^T, the reverse chain of the state gradient (each sequence's blocks cut
+into runs walked in parallel, a run that ends early starting after a warm-up
+over the following blocks where the gates decay, as the forward's segments do),
+and the per-block gradients.  bf16 q/k/v with head dim 128 only.
 """
 from __future__ import annotations
 
@@ -22,8 +24,8 @@ import numpy as np
 import torch
 
 from .. import _lib
-from .gdn import (CHUNK, DECAY_THRESHOLD, MAX_WARM_CHUNKS, _device_table, _segment_table,
-                  chunk_gated_delta_rule_gqa, seq_bounds)
+from .gdn import (CHUNK, DECAY_THRESHOLD, MAX_WARM_CHUNKS, _cu_count, _device_table,
+                  _segment_table, chunk_gated_delta_rule_gqa, seq_bounds)
 
 
 def block_table(bounds: list[tuple[int, int]]):
@@ -35,6 +37,23 @@ def block_table(bounds: list[tuple[int, int]]):
             rows.append((t0, min(CHUNK, eos - t0), n, c))
         cu.append(len(rows))
     return np.asarray(rows, dtype=np.int32).reshape(-1, 4), np.asarray(cu, dtype=np.int32)
+
+
+def chain_segments(cu_blocks: np.ndarray, H: int, cu_count: int, seg_blocks: int | None = None):
+    """int32 rows (sequence, first block, end block): every sequence's blocks cut into
+    runs of at most ``seg_blocks`` blocks (by default as long as gives about two
+    workgroups per CU over all heads), one (empty) row for a sequence without blocks."""
+    total = int(cu_blocks[-1])
+    if seg_blocks is None:
+        seg_blocks = max(1, -(-total * H // (2 * cu_count)))
+    rows = []
+    for n in range(len(cu_blocks) - 1):
+        a, e = int(cu_blocks[n]), int(cu_blocks[n + 1])
+        if a == e:
+            rows.append((n, a, e))
+        for b in range(a, e, seg_blocks):
+            rows.append((n, b, min(b + seg_blocks, e)))
+    return np.asarray(rows, dtype=np.int32).reshape(-1, 3)
 
 
 def _check(q, k, v, g, beta):
@@ -62,7 +81,7 @@ def _rows(x):
 
 def block_states(q, k, v, g, beta, scale, h0, bounds, l2norm, segment_chunks=None):
     """The state entering every block, fp16 [nblk, H, D, D], and the block table
-    (host rows, device table, device cu_blocks)."""
+    (host rows, device table, device cu_blocks, host cu_blocks)."""
     B, T, H, D = q.shape
     N = len(bounds)
     rows_np, cu_np = block_table(bounds)
@@ -71,7 +90,7 @@ def block_states(q, k, v, g, beta, scale, h0, bounds, l2norm, segment_chunks=Non
     cu_dev = _device_table(cu_np, q.device)
     seg_rows, _ = _segment_table(_lib.PLAN_GDN, bounds, B * T, H, q.device, segment_chunks)
     if nblk == 0:
-        return hc, rows_np, _device_table(np.zeros((1, 4), np.int32), q.device), cu_dev
+        return hc, rows_np, _device_table(np.zeros((1, 4), np.int32), q.device), cu_dev, cu_np
     seg = _device_table(seg_rows, q.device)
     lib = _lib.load()
     ws_bytes = int(lib.hmx_gdn_chunk_workspace_bytes(len(seg_rows), N, H, 0))
@@ -86,18 +105,22 @@ def block_states(q, k, v, g, beta, scale, h0, bounds, l2norm, segment_chunks=Non
               _lib.ptr(o), _lib.ptr(h0), None, _lib.ptr(seg), len(seg_rows), N, H, float(scale),
               int(bool(l2norm)), MAX_WARM_CHUNKS, DECAY_THRESHOLD, _lib.ptr(ws), ws.numel(),
               _lib.ptr(hc), _lib.ptr(cu_dev), _lib.stream_of(q))
-    return hc, rows_np, _device_table(rows_np, q.device), cu_dev
+    return hc, rows_np, _device_table(rows_np, q.device), cu_dev, cu_np
 
 
 def chunk_backward(q, k, v, g, beta, scale, h0, do, dht, bounds, l2norm, segment_chunks=None,
                    want_dh0=False):
-    """(dq, dk, dv bf16, dg, dbeta, dh0 or None fp32) of the chunked gated delta rule."""
+    """(dq, dk, dv bf16, dg, dbeta, dh0 or None fp32) of the chunked gated delta rule.
+    ``segment_chunks`` (tests) bounds both the recomputing forward's segments and the
+    state-gradient chain's runs, in 32-token blocks."""
     B, T, H, D = q.shape
     N = len(bounds)
     g, beta = g.contiguous(), beta.contiguous()
-    hc, rows_np, tab, cu_dev = block_states(q, k, v, g, beta, scale, h0, bounds, l2norm,
-                                            segment_chunks)
+    hc, rows_np, tab, cu_dev, cu_np = block_states(q, k, v, g, beta, scale, h0, bounds, l2norm,
+                                                   segment_chunks)
     nblk = rows_np.shape[0]
+    cseg_np = chain_segments(cu_np, H, _cu_count(q.device), segment_chunks)
+    cseg = _device_table(cseg_np, q.device)
     covered = sum(e - b for b, e in bounds) == B * T
     alloc = torch.empty if covered else torch.zeros
     dq, dk, dv = (alloc(B, T, H, D, dtype=torch.bfloat16, device=q.device) for _ in range(3))
@@ -114,7 +137,8 @@ def chunk_backward(q, k, v, g, beta, scale, h0, do, dht, bounds, l2norm, segment
               _lib.ptr(q), q_ts, _lib.ptr(k), _lib.ptr(v), kv_ts,
               _lib.ptr(g), _lib.dtype_code(g), _lib.ptr(beta), _lib.dtype_code(beta),
               _lib.ptr(do), do_ts, _lib.ptr(dht), _lib.ptr(hc), _lib.ptr(tab), _lib.ptr(cu_dev),
-              nblk, N, H, float(scale), int(bool(l2norm)),
+              nblk, N, _lib.ptr(cseg), cseg_np.shape[0], MAX_WARM_CHUNKS, DECAY_THRESHOLD, H,
+              float(scale), int(bool(l2norm)),
               _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dg), _lib.ptr(dbeta),
               _lib.ptr(dh0), _lib.ptr(ws), ws.numel(), _lib.stream_of(q))
     return dq, dk, dv, dg, dbeta, dh0

@@ -282,7 +282,13 @@ int hmx_gdn_train_fwd(const void* q, int64_t q_token_stride, const void* k, cons
  * stride dout_token_stride) and, optionally, dht (the gradient of the final states,
  * fp32 [N][H][128][128]).  block_states: hmx_gdn_train_fwd's; block_table int32
  * [nblock_total][4] = (first token, tokens (1-32), sequence, block index within
- * the sequence); cu_blocks [N+1].  Writes dq, dk, dv [tokens][H][128] bf16 (rows
+ * the sequence); cu_blocks [N+1].  chain_segments int32 [nchain_segments][3] =
+ * (sequence, first block, end block) cuts every sequence's blocks into runs that
+ * one workgroup each walks backward (every sequence needs at least one row, an
+ * empty one for a sequence without tokens); a run that ends before its sequence
+ * starts from zero after a warm-up of up to max_warm_blocks following blocks whose
+ * gates bring the dropped history under e^-decay_threshold, and from the sequence
+ * end otherwise.  Writes dq, dk, dv [tokens][H][128] bf16 (rows
  * of the blocks' tokens only), dg and dbeta [tokens][H] fp32, and dh0 (the
  * gradient of the initial states, fp32 [N][H][128][128]) when not null.
  * workspace: hmx_gdn_train_bwd_workspace_bytes(nblock_total, H) bytes.
@@ -295,10 +301,12 @@ int hmx_gdn_train_bwd(const void* q, int64_t q_token_stride, const void* k, cons
                       int64_t kv_token_stride, const void* g, int32_t g_dtype, const void* beta,
                       int32_t beta_dtype, const void* dout, int64_t dout_token_stride,
                       const float* dht, const void* block_states, const int32_t* block_table,
-                      const int32_t* cu_blocks, int32_t nblock_total, int32_t N, int32_t H,
-                      float scale, int32_t use_qk_l2norm, void* dq, void* dk, void* dv,
-                      float* dg, float* dbeta, float* dh0, void* workspace,
-                      size_t workspace_bytes, void* stream);
+                      const int32_t* cu_blocks, int32_t nblock_total, int32_t N,
+                      const int32_t* chain_segments, int32_t nchain_segments,
+                      int32_t max_warm_blocks, float decay_threshold, int32_t H, float scale,
+                      int32_t use_qk_l2norm, void* dq, void* dk, void* dv, float* dg,
+                      float* dbeta, float* dh0, void* workspace, size_t workspace_bytes,
+                      void* stream);
 size_t hmx_gdn_train_bwd_workspace_bytes(int32_t nblock_total, int32_t H);
 
 /*

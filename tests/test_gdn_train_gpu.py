@@ -23,7 +23,7 @@ D = 128
 GRAD_REL = 1e-2
 
 
-def _inputs(B, T, H, seed, dev, beta2=False, l2=True):
+def _inputs(B, T, H, seed, dev, beta2=False, l2=True, weak=False):
     g0 = torch.Generator().manual_seed(seed)
     q = torch.randn(B, T, H, D, generator=g0)
     k = torch.randn(B, T, H, D, generator=g0)
@@ -33,27 +33,35 @@ def _inputs(B, T, H, seed, dev, beta2=False, l2=True):
     v = torch.randn(B, T, H, D, generator=g0)
     A_log = torch.rand(H, generator=g0) * 2.0 - 1.0
     g = -A_log.exp() * torch.nn.functional.softplus(torch.randn(B, T, H, generator=g0) - 2.0)
+    if weak:     # too little decay for any warm-up: the state-gradient chain runs exact
+        g = g * 1e-3
     beta = torch.sigmoid(torch.randn(B, T, H, generator=g0)) * (2.0 if beta2 else 1.0)
     do = torch.randn(B, T, H, D, generator=g0)
     bf = lambda t: t.bfloat16().to(dev)
     return bf(q), bf(k), bf(v), g.to(dev), beta.to(dev), bf(do)
 
 
-CASES = [  # B, T, H, l2, h0, final-state grad, cu_seqlens, segment chunks, beta in (0, 2), beta bf16
-    (2, 200, 2, True, False, False, None, None, False, False),
-    (1, 256, 2, True, True, True, None, None, False, False),
-    (1, 180, 2, True, True, True, [0, 50, 51, 180], None, False, True),
-    (1, 300, 2, True, True, False, None, 1, False, False),
-    (2, 100, 3, False, False, True, None, None, False, False),
-    (1, 160, 2, True, False, False, None, None, True, False),
-    (1, 2048, 2, True, True, True, None, None, False, False),
+# segment chunks: the recomputing forward's segments and the state-gradient chain's
+# runs, in 32-token blocks (None: the planners'; at these sizes the chain's runs are
+# one block each, every one after a warm-up)
+CASES = [  # B, T, H, l2, h0, final-state grad, cu_seqlens, segment chunks, beta in (0, 2), beta bf16, weak decay
+    (2, 200, 2, True, False, False, None, None, False, False, False),
+    (1, 256, 2, True, True, True, None, None, False, False, False),
+    (1, 180, 2, True, True, True, [0, 50, 51, 180], None, False, True, False),
+    (1, 300, 2, True, True, False, None, 1, False, False, False),
+    (2, 100, 3, False, False, True, None, None, False, False, False),
+    (1, 160, 2, True, False, False, None, None, True, False, False),
+    (1, 2048, 2, True, True, True, None, None, False, False, False),
+    (1, 2048, 2, True, True, True, None, 5, False, False, False),
+    (1, 700, 2, True, True, True, [0, 300, 300, 700], 3, False, False, True),
 ]
 
 
-@pytest.mark.parametrize("B,T,H,l2,use_h0,use_dht,cu,seg,beta2,beta_bf", CASES)
+@pytest.mark.parametrize("B,T,H,l2,use_h0,use_dht,cu,seg,beta2,beta_bf,weak", CASES)
 def test_chunk_gated_delta_rule_backward_matches_oracle(dev, B, T, H, l2, use_h0, use_dht, cu, seg,
-                                                        beta2, beta_bf):
-    q, k, v, g, beta, do = _inputs(B, T, H, 7, dev, beta2, l2)
+                                                        beta2, beta_bf, weak):
+    print("case", B, T, H, l2, use_h0, use_dht, cu, seg, beta2, beta_bf, weak, flush=True)
+    q, k, v, g, beta, do = _inputs(B, T, H, 7, dev, beta2, l2, weak)
     if beta_bf:
         beta = beta.bfloat16()
     N = B if cu is None else len(cu) - 1
