@@ -1349,6 +1349,23 @@ __device__ __forceinline__ void block_scalars(const Sc& s, float gv, float bv, i
   }
 }
 
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                               0xF, 0xF, false));
+}
+// The sums of x[0..3] over the 16 lanes of a DPP row, by a transposing reduction
+// (five DPP additions instead of sixteen): lane l16 receives the sum of x[l16 & 3].
+__device__ __forceinline__ float row16_sum4(const f32x4& x, int l16) {
+  const bool b = l16 & 1, c = l16 & 2;
+  const float y0 = (b ? x[1] : x[0]) + dppf<0xB1>(b ? x[0] : x[1]);   // x[b], lanes l, l ^ 1
+  const float y1 = (b ? x[3] : x[2]) + dppf<0xB1>(b ? x[2] : x[3]);   // x[b + 2]
+  float z = (c ? y1 : y0) + dppf<0x4E>(c ? y0 : y1);                   // x[l & 3], l ^ 2 too
+  z += dppf<0x124>(z);                                                  // row_ror:4
+  z += dppf<0x128>(z);                                                  // row_ror:8
+  return z;
+}
+
 // rows 16 mt + 4 q4 .. +3 of a per-token LDS array (one 16-byte read)
 __device__ __forceinline__ f32x4 row4(const float* a, int mt, int q4) {
   return *reinterpret_cast<const f32x4*>(a + 16 * mt + 4 * q4);
@@ -1652,7 +1669,7 @@ constexpr int G_OFF_SC = G_OFF_KK + C * LF * 4;            // G, E, F, B, rq, rk
 constexpr int NPG = 16, NPB = 10;
 constexpr int G_OFF_PG = G_OFF_SC + 6 * C * 4;             // [16][32] dgamma pieces
 constexpr int G_OFF_PB = G_OFF_PG + NPG * C * 4;           // [10][32] dbeta pieces
-constexpr int G_OFF_PC = G_OFF_PB + NPB * C * 4;           // [8][32] k^ . (F W dS^T) per wave
+constexpr int G_OFF_PC = G_OFF_PB + NPB * C * 4;           // [8] sum_j k^_j . (F W dS^T)_j per wave
 constexpr int G_OFF_PQ = G_OFF_PC + 8 * C * 4;             // [8][32] q^ . dq^ per wave
 constexpr int G_OFF_PK = G_OFF_PQ + 8 * C * 4;             // [8][32] k^ . dk^ per wave
 constexpr int G_OFF_PD = G_OFF_PK + 8 * C * 4;             // [8] <dS, S0> per wave
@@ -1830,15 +1847,17 @@ __global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_grad_kernel(Bwd p) {
     for (int mt = 0; mt < 2; ++mt) {
       const f32x4 Z = mfma16h(frag_t_perm_h(sT, LL, 0, 16 * mt, lane), bw, zero);
       const f32x4 b4 = row4(sc.B, mt, q4);
+      f32x4 zu;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int r = 16 * mt + 4 * q4 + v, idx = r * LR + c0 + l16;
         sW[idx] = (f16)W[mt][v];
         sZ[idx] = (f16)Z[v];
         if (r < nval) p.dv[((int64_t)(tok0 + r) * H + h) * D + c0 + l16] = (bf16)(b4[v] * Z[v]);
-        const float zu = row16_sum(Z[v] * Ut[mt][v]);
-        if (l16 == 0) sPB[wave * C + r] = zu;
+        zu[v] = Z[v] * Ut[mt][v];
       }
+      const float zs = row16_sum4(zu, l16);
+      if (l16 < 4) sPB[wave * C + 16 * mt + 4 * q4 + l16] = zs;
     }
   }
   lds_barrier();
@@ -1848,6 +1867,7 @@ __global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_grad_kernel(Bwd p) {
   f32x4 DQ[2], DK[2];
   f32x4 qh[2], kh[2];      // q^, k^ at this lane's accumulator positions
   {
+    float cs = 0.f;
     f32x4 A0[2] = {zero, zero}, A1[2] = {zero, zero}, A2[2] = {zero, zero};
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
@@ -1862,6 +1882,7 @@ __global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_grad_kernel(Bwd p) {
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
       const f32x4 e4 = row4(sc.E, mt, q4), b4 = row4(sc.B, mt, q4), f4r = row4(sc.F, mt, q4);
+      f32x4 gq;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int r = 16 * mt + 4 * q4 + v, idx = r * LR + c0 + l16;
@@ -1872,14 +1893,14 @@ __global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_grad_kernel(Bwd p) {
         kh[mt][v] = (float)sK[idx];
         DQ[mt][v] = qt;
         DK[mt][v] = ut + st;
-        const float gq = row16_sum(qh[mt][v] * qt + kh[mt][v] * (ut - st));
-        const float cj = row16_sum(kh[mt][v] * st);
-        if (l16 == 0) {
-          sPG[(8 + wave) * C + r] = gq;
-          sPC[wave * C + r] = cj;
-        }
+        gq[v] = qh[mt][v] * qt + kh[mt][v] * (ut - st);
+        cs += kh[mt][v] * st;
       }
+      const float gs = row16_sum4(gq, l16);
+      if (l16 < 4) sPG[(8 + wave) * C + 16 * mt + 4 * q4 + l16] = gs;
     }
+    cs = wave_sum(cs);
+    if (lane == 0) sPC[wave] = cs;
   }
   {
     const int t = wave & 3, mt = t >> 1, nt = t & 1;
@@ -1892,6 +1913,7 @@ __global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_grad_kernel(Bwd p) {
     const float gj = sc.G[j];
     const f32x4 gi4 = row4(sc.G, mt, q4), bi4 = row4(sc.B, mt, q4);
     float csum = 0.f;
+    f32x4 xs, dbs;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int i = 16 * mt + 4 * q4 + v;
@@ -1903,17 +1925,23 @@ __global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_grad_kernel(Bwd p) {
         const float d = bi4[v] * dn * gm;
         sDm[i * LL + j] = (f16)d;
         x = d * kk;
-        const float db = row16_sum(dn * kk * gm);
-        if (l16 == 0) sPB[(8 + nt) * C + i] = db;
+        dbs[v] = dn * kk * gm;
       } else {          // Dp = scale lower(dO W^T) . Gm
         const float d = p.scale * acc[v] * gm;
         sDp[i * LL + j] = (f16)d;
         x = d * sQK[i * LF + j];
+        dbs[v] = 0.f;
       }
-      const float rs = row16_sum(x);
-      if (l16 == 0) sPG[((wave < 4 ? 0 : 2) + nt) * C + i] = rs;
+      xs[v] = x;
       csum += x;
     }
+    const int ri = 16 * mt + 4 * q4 + l16;   // the row whose sums this lane holds (l16 < 4)
+    if (wave < 4) {
+      const float db = row16_sum4(dbs, l16);
+      if (l16 < 4) sPB[(8 + nt) * C + ri] = db;
+    }
+    const float rs = row16_sum4(xs, l16);
+    if (l16 < 4) sPG[((wave < 4 ? 0 : 2) + nt) * C + ri] = rs;
     csum += __shfl_xor(csum, 16, 64);
     csum += __shfl_xor(csum, 32, 64);
     if (q4 == 0) sPG[((wave < 4 ? 4 : 6) + mt) * C + j] = -csum;
@@ -1931,17 +1959,19 @@ __global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_grad_kernel(Bwd p) {
       DK[mt] = mfma16h(frag_col(sDm, LL, 0, 16 * mt, lane), bk, DK[mt]);
     }
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+    for (int mt = 0; mt < 2; ++mt) {
+      f32x4 xq, xk;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const int r = 16 * mt + 4 * q4 + v;
-        const float sq = row16_sum(qh[mt][v] * DQ[mt][v]);
-        const float sk = row16_sum(kh[mt][v] * DK[mt][v]);
-        if (l16 == 0) {
-          sPQ[wave * C + r] = sq;
-          sPK[wave * C + r] = sk;
-        }
+        xq[v] = qh[mt][v] * DQ[mt][v];
+        xk[v] = kh[mt][v] * DK[mt][v];
       }
+      const float sq = row16_sum4(xq, l16), sk = row16_sum4(xk, l16);
+      if (l16 < 4) {
+        sPQ[wave * C + 16 * mt + 4 * q4 + l16] = sq;
+        sPK[wave * C + 16 * mt + 4 * q4 + l16] = sk;
+      }
+    }
   }
   lds_barrier();
 
@@ -1973,18 +2003,18 @@ __global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_grad_kernel(Bwd p) {
     }
   }
   if (wave == 0) {
-    float dgam = 0.f, db = 0.f, cl = 0.f, dd = 0.f;
+    float dgam = 0.f, db = 0.f, ctot = 0.f, dd = 0.f;
     if (lane < C) {
 #pragma unroll
       for (int s = 0; s < NPG; ++s) dgam += sPG[s * C + lane];
 #pragma unroll
       for (int s = 0; s < NPB; ++s) db += sPB[s * C + lane];
-#pragma unroll
-      for (int w = 0; w < 8; ++w) cl += sPC[w * C + lane];
     }
 #pragma unroll
-    for (int w = 0; w < 8; ++w) dd += sPD[w];
-    const float ctot = wave_sum(cl);
+    for (int w = 0; w < 8; ++w) {
+      dd += sPD[w];
+      ctot += sPC[w];
+    }
     if (lane == C - 1) dgam += sc.E[C - 1] * dd + ctot;
     // in-block reverse inclusive cumsum over lanes 0-31
 #pragma unroll
