@@ -1746,294 +1746,294 @@ __global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_grad_kernel(Bwd p) {
   GradPre pre;
   grad_load(p, pre, (int64_t)cb * H + h, h, tok0, nval, tid, wave, lane);
   for (;;) {
-  const int nxt = it + gridDim.x;
-  int ncb = 0, nh = 0, ntok0 = 0, nnval = 0;
-  if (nxt < total) {
-    ncb = nxt / H;
-    nh = nxt - ncb * H;
-    ntok0 = p.ctab[ncb * 4];
-    nnval = p.ctab[ncb * 4 + 1];
-  }
-  const int64_t bh = (int64_t)cb * H + h;
-
-  // ---- P0: stage this block from registers; the next block's loads go out -------
-  lds_barrier();   // the previous block's LDS reads are done
-  {
-    put_row(sK, pre.k, p.l2norm, sRk, tid);
-    put_row(sQ, pre.q, p.l2norm, sRq, tid);
-    put_row(sDO, pre.o, false, nullptr, tid);
-    put_row(sX, pre.v, false, nullptr, tid);
-    if (wave == 0) block_scalars(sc, pre.g, pre.b, lane);
-#pragma unroll
-    for (int pass = 0; pass < 4; ++pass) {
-      const int e = (pass * BNTHR + tid) * 8, row = e >> 7, col = e & 127;
-      *reinterpret_cast<f16x8*>(sS0 + row * LR + col) = pre.s0[pass];
-      *reinterpret_cast<f16x8*>(sDS + row * LR + col) = pre.ds[pass];
+    const int nxt = it + gridDim.x;
+    int ncb = 0, nh = 0, ntok0 = 0, nnval = 0;
+    if (nxt < total) {
+      ncb = nxt / H;
+      nh = nxt - ncb * H;
+      ntok0 = p.ctab[ncb * 4];
+      nnval = p.ctab[ncb * 4 + 1];
     }
-    const int e2 = 2 * tid, i = e2 >> 5, j = e2 & 31;
-    *reinterpret_cast<uint32_t*>(sT + i * LL + j) = pre.t;
-    *reinterpret_cast<uint32_t*>(sPm + i * LL + j) = pre.pm;
-  }
-  if (nxt < total) grad_load(p, pre, (int64_t)ncb * H + nh, nh, ntok0, nnval, tid, wave, lane);
-  lds_barrier();
+    const int64_t bh = (int64_t)cb * H + h;
 
-  // ---- P1: K^ S0 and K^ dS (tokens x this wave's value columns), a tile of Q^K^T
-  // or K^K^T, this wave's share of <dS, S0>; Ut = V - E K^ S0, beta Ut over V ----
-  f32x4 Ut[2], KD[2];
-  {
-    f32x4 KS[2] = {zero, zero};
-    KD[0] = KD[1] = zero;
+    // ---- P0: stage this block from registers; the next block's loads go out -------
+    lds_barrier();   // the previous block's LDS reads are done
+    {
+      put_row(sK, pre.k, p.l2norm, sRk, tid);
+      put_row(sQ, pre.q, p.l2norm, sRq, tid);
+      put_row(sDO, pre.o, false, nullptr, tid);
+      put_row(sX, pre.v, false, nullptr, tid);
+      if (wave == 0) block_scalars(sc, pre.g, pre.b, lane);
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const f16x8 bs = frag_col(sS0, LR, 32 * ks, c0, lane), bd = frag_col(sDS, LR, 32 * ks, c0, lane);
+      for (int pass = 0; pass < 4; ++pass) {
+        const int e = (pass * BNTHR + tid) * 8, row = e >> 7, col = e & 127;
+        *reinterpret_cast<f16x8*>(sS0 + row * LR + col) = pre.s0[pass];
+        *reinterpret_cast<f16x8*>(sDS + row * LR + col) = pre.ds[pass];
+      }
+      const int e2 = 2 * tid, i = e2 >> 5, j = e2 & 31;
+      *reinterpret_cast<uint32_t*>(sT + i * LL + j) = pre.t;
+      *reinterpret_cast<uint32_t*>(sPm + i * LL + j) = pre.pm;
+    }
+    if (nxt < total) grad_load(p, pre, (int64_t)ncb * H + nh, nh, ntok0, nnval, tid, wave, lane);
+    lds_barrier();
+
+    // ---- P1: K^ S0 and K^ dS (tokens x this wave's value columns), a tile of Q^K^T
+    // or K^K^T, this wave's share of <dS, S0>; Ut = V - E K^ S0, beta Ut over V ----
+    f32x4 Ut[2], KD[2];
+    {
+      f32x4 KS[2] = {zero, zero};
+      KD[0] = KD[1] = zero;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const f16x8 bs = frag_col(sS0, LR, 32 * ks, c0, lane), bd = frag_col(sDS, LR, 32 * ks, c0, lane);
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+          const f16x8 a = frag_h(sK, LR, 16 * mt, 32 * ks, lane);
+          KS[mt] = mfma16h(a, bs, KS[mt]);
+          KD[mt] = mfma16h(a, bd, KD[mt]);
+        }
+      }
+      {
+        const int t = wave & 3, mt = t >> 1, nt = t & 1;
+        const f16* A = wave < 4 ? sQ : sK;
+        f32x4 acc = zero;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+          acc = mfma16h(frag_h(A, LR, 16 * mt, 32 * ks, lane), frag_h(sK, LR, 16 * nt, 32 * ks, lane), acc);
+        float* dst = wave < 4 ? sQK : sKK;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) dst[(16 * mt + 4 * q4 + v) * LF + 16 * nt + l16] = acc[v];
+      }
+      {
+        float d = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = 16 * wave + 4 * i + q4, col = 8 * l16;
+          const f16x8 a = *reinterpret_cast<const f16x8*>(sS0 + row * LR + col);
+          const f16x8 b = *reinterpret_cast<const f16x8*>(sDS + row * LR + col);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) d += (float)a[j] * (float)b[j];
+        }
+        d = wave_sum(d);
+        if (lane == 0) sPD[wave] = d;
+      }
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
-        const f16x8 a = frag_h(sK, LR, 16 * mt, 32 * ks, lane);
-        KS[mt] = mfma16h(a, bs, KS[mt]);
-        KD[mt] = mfma16h(a, bd, KD[mt]);
+        const f32x4 e4 = row4(sc.E, mt, q4), b4 = row4(sc.B, mt, q4);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int r = 16 * mt + 4 * q4 + v, idx = r * LR + c0 + l16;
+          Ut[mt][v] = (float)sX[idx] - e4[v] * KS[mt][v];
+          sX[idx] = (f16)(b4[v] * Ut[mt][v]);
+        }
       }
+    }
+    lds_barrier();
+
+    // ---- P2: W = T (beta Ut); dW = P^T dO + F K^ dS; Z = T^T dW; dv; rowdot(Z, Ut) --
+    {
+      const f16x8 bx = frag_col(sX, LR, 0, c0, lane), bdo = frag_col(sDO, LR, 0, c0, lane);
+      f32x4 W[2], dW[2];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        W[mt] = mfma16h(frag_h(sT, LL, 16 * mt, 0, lane), bx, zero);
+        const f32x4 f4r = row4(sc.F, mt, q4);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) dW[mt][v] = f4r[v] * KD[mt][v];
+        dW[mt] = mfma16h(frag_col(sPm, LL, 0, 16 * mt, lane), bdo, dW[mt]);
+      }
+      const f16x8 bw = h8(dW[0], dW[1]);
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const f32x4 Z = mfma16h(frag_t_perm_h(sT, LL, 0, 16 * mt, lane), bw, zero);
+        const f32x4 b4 = row4(sc.B, mt, q4);
+        f32x4 zu;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int r = 16 * mt + 4 * q4 + v, idx = r * LR + c0 + l16;
+          sW[idx] = (f16)W[mt][v];
+          sZ[idx] = (f16)Z[v];
+          if (r < nval) p.dv[((int64_t)(tok0 + r) * H + h) * D + c0 + l16] = (bf16)(b4[v] * Z[v]);
+          zu[v] = Z[v] * Ut[mt][v];
+        }
+        const float zs = row16_sum4(zu, l16);
+        if (l16 < 4) sPB[wave * C + 16 * mt + 4 * q4 + l16] = zs;
+      }
+    }
+    lds_barrier();
+
+    // ---- P3: dO S0^T, Z S0^T, W dS^T (tokens x this wave's key features); a tile of
+    // Z W^T (-> dN, Dm) or dO W^T (-> Dp) with their row and column sums -------------
+    f32x4 DQ[2], DK[2];
+    f32x4 qh[2], kh[2];      // q^, k^ at this lane's accumulator positions
+    {
+      float cs = 0.f;
+      f32x4 A0[2] = {zero, zero}, A1[2] = {zero, zero}, A2[2] = {zero, zero};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const f16x8 bs = frag_h(sS0, LR, c0, 32 * ks, lane), bd = frag_h(sDS, LR, c0, 32 * ks, lane);
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+          A0[mt] = mfma16h(frag_h(sDO, LR, 16 * mt, 32 * ks, lane), bs, A0[mt]);
+          A1[mt] = mfma16h(frag_h(sZ, LR, 16 * mt, 32 * ks, lane), bs, A1[mt]);
+          A2[mt] = mfma16h(frag_h(sW, LR, 16 * mt, 32 * ks, lane), bd, A2[mt]);
+        }
+      }
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const f32x4 e4 = row4(sc.E, mt, q4), b4 = row4(sc.B, mt, q4), f4r = row4(sc.F, mt, q4);
+        f32x4 gq;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int r = 16 * mt + 4 * q4 + v, idx = r * LR + c0 + l16;
+          const float qt = p.scale * e4[v] * A0[mt][v];
+          const float ut = -e4[v] * b4[v] * A1[mt][v];
+          const float st = f4r[v] * A2[mt][v];
+          qh[mt][v] = (float)sQ[idx];
+          kh[mt][v] = (float)sK[idx];
+          DQ[mt][v] = qt;
+          DK[mt][v] = ut + st;
+          gq[v] = qh[mt][v] * qt + kh[mt][v] * (ut - st);
+          cs += kh[mt][v] * st;
+        }
+        const float gs = row16_sum4(gq, l16);
+        if (l16 < 4) sPG[(8 + wave) * C + 16 * mt + 4 * q4 + l16] = gs;
+      }
+      cs = wave_sum(cs);
+      if (lane == 0) sPC[wave] = cs;
     }
     {
       const int t = wave & 3, mt = t >> 1, nt = t & 1;
-      const f16* A = wave < 4 ? sQ : sK;
+      const f16* A = wave < 4 ? sZ : sDO;
       f32x4 acc = zero;
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks)
-        acc = mfma16h(frag_h(A, LR, 16 * mt, 32 * ks, lane), frag_h(sK, LR, 16 * nt, 32 * ks, lane), acc);
-      float* dst = wave < 4 ? sQK : sKK;
+        acc = mfma16h(frag_h(A, LR, 16 * mt, 32 * ks, lane), frag_h(sW, LR, 16 * nt, 32 * ks, lane), acc);
+      const int j = 16 * nt + l16;
+      const float gj = sc.G[j];
+      const f32x4 gi4 = row4(sc.G, mt, q4), bi4 = row4(sc.B, mt, q4);
+      float csum = 0.f;
+      f32x4 xs, dbs;
 #pragma unroll
-      for (int v = 0; v < 4; ++v) dst[(16 * mt + 4 * q4 + v) * LF + 16 * nt + l16] = acc[v];
+      for (int v = 0; v < 4; ++v) {
+        const int i = 16 * mt + 4 * q4 + v;
+        const float gm = j <= i ? fast_exp(gi4[v] - gj) : 0.f;
+        float x;
+        if (wave < 4) {   // dN = -strict_lower(Z W^T), Dm = beta dN . Gm
+          const float dn = j < i ? -acc[v] : 0.f;
+          const float kk = sKK[i * LF + j];
+          const float d = bi4[v] * dn * gm;
+          sDm[i * LL + j] = (f16)d;
+          x = d * kk;
+          dbs[v] = dn * kk * gm;
+        } else {          // Dp = scale lower(dO W^T) . Gm
+          const float d = p.scale * acc[v] * gm;
+          sDp[i * LL + j] = (f16)d;
+          x = d * sQK[i * LF + j];
+          dbs[v] = 0.f;
+        }
+        xs[v] = x;
+        csum += x;
+      }
+      const int ri = 16 * mt + 4 * q4 + l16;   // the row whose sums this lane holds (l16 < 4)
+      if (wave < 4) {
+        const float db = row16_sum4(dbs, l16);
+        if (l16 < 4) sPB[(8 + nt) * C + ri] = db;
+      }
+      const float rs = row16_sum4(xs, l16);
+      if (l16 < 4) sPG[((wave < 4 ? 0 : 2) + nt) * C + ri] = rs;
+      csum += __shfl_xor(csum, 16, 64);
+      csum += __shfl_xor(csum, 32, 64);
+      if (q4 == 0) sPG[((wave < 4 ? 4 : 6) + mt) * C + j] = -csum;
     }
+    lds_barrier();
+
+    // ---- P4: dQ^ += Dp K^; dK^ += Dp^T Q^ + (Dm + Dm^T) K^; the L2 backward's row dots
     {
-      float d = 0.f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = 16 * wave + 4 * i + q4, col = 8 * l16;
-        const f16x8 a = *reinterpret_cast<const f16x8*>(sS0 + row * LR + col);
-        const f16x8 b = *reinterpret_cast<const f16x8*>(sDS + row * LR + col);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) d += (float)a[j] * (float)b[j];
-      }
-      d = wave_sum(d);
-      if (lane == 0) sPD[wave] = d;
-    }
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      const f32x4 e4 = row4(sc.E, mt, q4), b4 = row4(sc.B, mt, q4);
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int r = 16 * mt + 4 * q4 + v, idx = r * LR + c0 + l16;
-        Ut[mt][v] = (float)sX[idx] - e4[v] * KS[mt][v];
-        sX[idx] = (f16)(b4[v] * Ut[mt][v]);
-      }
-    }
-  }
-  lds_barrier();
-
-  // ---- P2: W = T (beta Ut); dW = P^T dO + F K^ dS; Z = T^T dW; dv; rowdot(Z, Ut) --
-  {
-    const f16x8 bx = frag_col(sX, LR, 0, c0, lane), bdo = frag_col(sDO, LR, 0, c0, lane);
-    f32x4 W[2], dW[2];
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      W[mt] = mfma16h(frag_h(sT, LL, 16 * mt, 0, lane), bx, zero);
-      const f32x4 f4r = row4(sc.F, mt, q4);
-#pragma unroll
-      for (int v = 0; v < 4; ++v) dW[mt][v] = f4r[v] * KD[mt][v];
-      dW[mt] = mfma16h(frag_col(sPm, LL, 0, 16 * mt, lane), bdo, dW[mt]);
-    }
-    const f16x8 bw = h8(dW[0], dW[1]);
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      const f32x4 Z = mfma16h(frag_t_perm_h(sT, LL, 0, 16 * mt, lane), bw, zero);
-      const f32x4 b4 = row4(sc.B, mt, q4);
-      f32x4 zu;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int r = 16 * mt + 4 * q4 + v, idx = r * LR + c0 + l16;
-        sW[idx] = (f16)W[mt][v];
-        sZ[idx] = (f16)Z[v];
-        if (r < nval) p.dv[((int64_t)(tok0 + r) * H + h) * D + c0 + l16] = (bf16)(b4[v] * Z[v]);
-        zu[v] = Z[v] * Ut[mt][v];
-      }
-      const float zs = row16_sum4(zu, l16);
-      if (l16 < 4) sPB[wave * C + 16 * mt + 4 * q4 + l16] = zs;
-    }
-  }
-  lds_barrier();
-
-  // ---- P3: dO S0^T, Z S0^T, W dS^T (tokens x this wave's key features); a tile of
-  // Z W^T (-> dN, Dm) or dO W^T (-> Dp) with their row and column sums -------------
-  f32x4 DQ[2], DK[2];
-  f32x4 qh[2], kh[2];      // q^, k^ at this lane's accumulator positions
-  {
-    float cs = 0.f;
-    f32x4 A0[2] = {zero, zero}, A1[2] = {zero, zero}, A2[2] = {zero, zero};
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const f16x8 bs = frag_h(sS0, LR, c0, 32 * ks, lane), bd = frag_h(sDS, LR, c0, 32 * ks, lane);
+      const f16x8 bk = frag_col(sK, LR, 0, c0, lane), bq = frag_col(sQ, LR, 0, c0, lane);
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
-        A0[mt] = mfma16h(frag_h(sDO, LR, 16 * mt, 32 * ks, lane), bs, A0[mt]);
-        A1[mt] = mfma16h(frag_h(sZ, LR, 16 * mt, 32 * ks, lane), bs, A1[mt]);
-        A2[mt] = mfma16h(frag_h(sW, LR, 16 * mt, 32 * ks, lane), bd, A2[mt]);
+        DQ[mt] = mfma16h(frag_h(sDp, LL, 16 * mt, 0, lane), bk, DQ[mt]);
+        DK[mt] = mfma16h(frag_col(sDp, LL, 0, 16 * mt, lane), bq, DK[mt]);
+        DK[mt] = mfma16h(frag_h(sDm, LL, 16 * mt, 0, lane), bk, DK[mt]);
+        DK[mt] = mfma16h(frag_col(sDm, LL, 0, 16 * mt, lane), bk, DK[mt]);
+      }
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        f32x4 xq, xk;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          xq[v] = qh[mt][v] * DQ[mt][v];
+          xk[v] = kh[mt][v] * DK[mt][v];
+        }
+        const float sq = row16_sum4(xq, l16), sk = row16_sum4(xk, l16);
+        if (l16 < 4) {
+          sPQ[wave * C + 16 * mt + 4 * q4 + l16] = sq;
+          sPK[wave * C + 16 * mt + 4 * q4 + l16] = sk;
+        }
       }
     }
+    lds_barrier();
+
+    // ---- P5: dq, dk (through the L2 normalisation); dg, dbeta --------------------
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
-      const f32x4 e4 = row4(sc.E, mt, q4), b4 = row4(sc.B, mt, q4), f4r = row4(sc.F, mt, q4);
-      f32x4 gq;
+      f32x4 sq = zero, sk = zero;
+      if (p.l2norm) {
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+          sq += row4(sPQ + w * C, mt, q4);
+          sk += row4(sPK + w * C, mt, q4);
+        }
+      }
+      const f32x4 rq4 = row4(sRq, mt, q4), rk4 = row4(sRk, mt, q4);
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const int r = 16 * mt + 4 * q4 + v, idx = r * LR + c0 + l16;
-        const float qt = p.scale * e4[v] * A0[mt][v];
-        const float ut = -e4[v] * b4[v] * A1[mt][v];
-        const float st = f4r[v] * A2[mt][v];
-        qh[mt][v] = (float)sQ[idx];
-        kh[mt][v] = (float)sK[idx];
-        DQ[mt][v] = qt;
-        DK[mt][v] = ut + st;
-        gq[v] = qh[mt][v] * qt + kh[mt][v] * (ut - st);
-        cs += kh[mt][v] * st;
-      }
-      const float gs = row16_sum4(gq, l16);
-      if (l16 < 4) sPG[(8 + wave) * C + 16 * mt + 4 * q4 + l16] = gs;
-    }
-    cs = wave_sum(cs);
-    if (lane == 0) sPC[wave] = cs;
-  }
-  {
-    const int t = wave & 3, mt = t >> 1, nt = t & 1;
-    const f16* A = wave < 4 ? sZ : sDO;
-    f32x4 acc = zero;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-      acc = mfma16h(frag_h(A, LR, 16 * mt, 32 * ks, lane), frag_h(sW, LR, 16 * nt, 32 * ks, lane), acc);
-    const int j = 16 * nt + l16;
-    const float gj = sc.G[j];
-    const f32x4 gi4 = row4(sc.G, mt, q4), bi4 = row4(sc.B, mt, q4);
-    float csum = 0.f;
-    f32x4 xs, dbs;
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int i = 16 * mt + 4 * q4 + v;
-      const float gm = j <= i ? fast_exp(gi4[v] - gj) : 0.f;
-      float x;
-      if (wave < 4) {   // dN = -strict_lower(Z W^T), Dm = beta dN . Gm
-        const float dn = j < i ? -acc[v] : 0.f;
-        const float kk = sKK[i * LF + j];
-        const float d = bi4[v] * dn * gm;
-        sDm[i * LL + j] = (f16)d;
-        x = d * kk;
-        dbs[v] = dn * kk * gm;
-      } else {          // Dp = scale lower(dO W^T) . Gm
-        const float d = p.scale * acc[v] * gm;
-        sDp[i * LL + j] = (f16)d;
-        x = d * sQK[i * LF + j];
-        dbs[v] = 0.f;
-      }
-      xs[v] = x;
-      csum += x;
-    }
-    const int ri = 16 * mt + 4 * q4 + l16;   // the row whose sums this lane holds (l16 < 4)
-    if (wave < 4) {
-      const float db = row16_sum4(dbs, l16);
-      if (l16 < 4) sPB[(8 + nt) * C + ri] = db;
-    }
-    const float rs = row16_sum4(xs, l16);
-    if (l16 < 4) sPG[((wave < 4 ? 0 : 2) + nt) * C + ri] = rs;
-    csum += __shfl_xor(csum, 16, 64);
-    csum += __shfl_xor(csum, 32, 64);
-    if (q4 == 0) sPG[((wave < 4 ? 4 : 6) + mt) * C + j] = -csum;
-  }
-  lds_barrier();
-
-  // ---- P4: dQ^ += Dp K^; dK^ += Dp^T Q^ + (Dm + Dm^T) K^; the L2 backward's row dots
-  {
-    const f16x8 bk = frag_col(sK, LR, 0, c0, lane), bq = frag_col(sQ, LR, 0, c0, lane);
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      DQ[mt] = mfma16h(frag_h(sDp, LL, 16 * mt, 0, lane), bk, DQ[mt]);
-      DK[mt] = mfma16h(frag_col(sDp, LL, 0, 16 * mt, lane), bq, DK[mt]);
-      DK[mt] = mfma16h(frag_h(sDm, LL, 16 * mt, 0, lane), bk, DK[mt]);
-      DK[mt] = mfma16h(frag_col(sDm, LL, 0, 16 * mt, lane), bk, DK[mt]);
-    }
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      f32x4 xq, xk;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        xq[v] = qh[mt][v] * DQ[mt][v];
-        xk[v] = kh[mt][v] * DK[mt][v];
-      }
-      const float sq = row16_sum4(xq, l16), sk = row16_sum4(xk, l16);
-      if (l16 < 4) {
-        sPQ[wave * C + 16 * mt + 4 * q4 + l16] = sq;
-        sPK[wave * C + 16 * mt + 4 * q4 + l16] = sk;
+        const int r = 16 * mt + 4 * q4 + v;
+        float dq = DQ[mt][v], dk = DK[mt][v];
+        if (p.l2norm) {
+          dq = rq4[v] * (dq - qh[mt][v] * sq[v]);
+          dk = rk4[v] * (dk - kh[mt][v] * sk[v]);
+        }
+        if (r < nval) {
+          const int64_t o = ((int64_t)(tok0 + r) * H + h) * D + c0 + l16;
+          p.dq[o] = (bf16)dq;
+          p.dk[o] = (bf16)dk;
+        }
       }
     }
-  }
-  lds_barrier();
-
-  // ---- P5: dq, dk (through the L2 normalisation); dg, dbeta --------------------
+    if (wave == 0) {
+      float dgam = 0.f, db = 0.f, ctot = 0.f, dd = 0.f;
+      if (lane < C) {
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
-    f32x4 sq = zero, sk = zero;
-    if (p.l2norm) {
+        for (int s = 0; s < NPG; ++s) dgam += sPG[s * C + lane];
+#pragma unroll
+        for (int s = 0; s < NPB; ++s) db += sPB[s * C + lane];
+      }
 #pragma unroll
       for (int w = 0; w < 8; ++w) {
-        sq += row4(sPQ + w * C, mt, q4);
-        sk += row4(sPK + w * C, mt, q4);
+        dd += sPD[w];
+        ctot += sPC[w];
+      }
+      if (lane == C - 1) dgam += sc.E[C - 1] * dd + ctot;
+      // in-block reverse inclusive cumsum over lanes 0-31
+#pragma unroll
+      for (int off = 1; off < C; off <<= 1) {
+        const float y = __shfl_down(dgam, off, 64);
+        if (lane + off < C) dgam += y;
+      }
+      if (lane < nval) {
+        const int64_t o = (int64_t)(tok0 + lane) * H + h;
+        p.dg[o] = dgam;
+        p.dbeta[o] = db;
       }
     }
-    const f32x4 rq4 = row4(sRq, mt, q4), rk4 = row4(sRk, mt, q4);
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int r = 16 * mt + 4 * q4 + v;
-      float dq = DQ[mt][v], dk = DK[mt][v];
-      if (p.l2norm) {
-        dq = rq4[v] * (dq - qh[mt][v] * sq[v]);
-        dk = rk4[v] * (dk - kh[mt][v] * sk[v]);
-      }
-      if (r < nval) {
-        const int64_t o = ((int64_t)(tok0 + r) * H + h) * D + c0 + l16;
-        p.dq[o] = (bf16)dq;
-        p.dk[o] = (bf16)dk;
-      }
-    }
-  }
-  if (wave == 0) {
-    float dgam = 0.f, db = 0.f, ctot = 0.f, dd = 0.f;
-    if (lane < C) {
-#pragma unroll
-      for (int s = 0; s < NPG; ++s) dgam += sPG[s * C + lane];
-#pragma unroll
-      for (int s = 0; s < NPB; ++s) db += sPB[s * C + lane];
-    }
-#pragma unroll
-    for (int w = 0; w < 8; ++w) {
-      dd += sPD[w];
-      ctot += sPC[w];
-    }
-    if (lane == C - 1) dgam += sc.E[C - 1] * dd + ctot;
-    // in-block reverse inclusive cumsum over lanes 0-31
-#pragma unroll
-    for (int off = 1; off < C; off <<= 1) {
-      const float y = __shfl_down(dgam, off, 64);
-      if (lane + off < C) dgam += y;
-    }
-    if (lane < nval) {
-      const int64_t o = (int64_t)(tok0 + lane) * H + h;
-      p.dg[o] = dgam;
-      p.dbeta[o] = db;
-    }
-  }
-  if (nxt >= total) break;
-  it = nxt;
-  cb = ncb;
-  h = nh;
-  tok0 = ntok0;
-  nval = nnval;
+    if (nxt >= total) break;
+    it = nxt;
+    cb = ncb;
+    h = nh;
+    tok0 = ntok0;
+    nval = nnval;
   }
 }
 
