@@ -1584,7 +1584,7 @@ __global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_chain_kernel(Bwd p) {
       const int row = tid >> 4, f0 = (tid & 15) * 8;
       const float rk = p.l2norm ? row_inv_norm(pa.k) : 1.f;
       const float rq = p.l2norm ? row_inv_norm(pa.q) : 1.f;
-      *reinterpret_cast<f16x8*>(sK + row * LR + f0) = scale_h8(pa.k, rk);
+      store8_i(sK + row * LR, f0, scale_h8(pa.k, rk));   // interleaved feature order
       *reinterpret_cast<f16x8*>(sQ + row * LR + f0) = scale_h8(pa.q, rq);
       *reinterpret_cast<f16x8*>(sDO + row * LR + f0) = scale_h8(pa.o, 1.f);
       const int e = 2 * tid, i = e >> 5, j = e & 31;
@@ -1613,7 +1613,7 @@ __global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_chain_kernel(Bwd p) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int m = 0; m < 4; ++m)
-        acc = mfma16h(frag_perm_h(sK, LR, 16 * mt, 32 * m, lane), h8(dS[2 * m], dS[2 * m + 1]), acc);
+        acc = mfma16h(frag_i(sK, LR, 16 * mt, 32 * m, lane), h8(dS[2 * m], dS[2 * m + 1]), acc);
 #pragma unroll
       for (int v = 0; v < 4; ++v) dW[mt][v] = sc.F[16 * mt + 4 * q4 + v] * acc[v];
     }
@@ -1644,7 +1644,7 @@ __global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_chain_kernel(Bwd p) {
     for (int rt = 0; rt < 8; ++rt) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) dS[rt][v] *= eL;
-      dS[rt] = mfma16h(frag_t_perm_h(sK, LR, 0, 16 * rt, lane), bz, dS[rt]);
+      dS[rt] = mfma16h(frag_t_i(sK, LR, 0, 16 * rt, lane), bz, dS[rt]);
       dS[rt] = mfma16h(frag_col(sQ, LR, 0, 16 * rt, lane), bqe, dS[rt]);
     }
   }
