@@ -136,3 +136,24 @@ def test_backward_rejects(dev):
         hmx.chunk_gated_delta_rule(q.float().requires_grad_(True), k.float(), v.float(), g, beta)
     with pytest.raises(ValueError):
         ChunkGatedDeltaRule.apply(q, k, v, g[:, :5], beta, None, None, False, None, True, None)
+
+
+def test_backward_all_heads_subset_against_oracle(dev):
+    """The training head count (H = 32) over two 1024-token sequences: every head runs
+    on the GPU, three of them (first, middle, last) are checked against the oracle
+    (heads are independent, so the others' indexing shows in these)."""
+    B, T, H = 2, 1024, 32
+    q, k, v, g, beta, do = _inputs(B, T, H, 12, dev)
+    ins = [t.clone().requires_grad_(True) for t in (q, k, v, g, beta)]
+    o, _ = ChunkGatedDeltaRule.apply(*ins, D ** -0.5, None, False, None, True, None)
+    (o.float() * do.float()).sum().backward()
+    for hh in (0, 13, 31):
+        sl = lambda t: t.detach()[:, :, hh:hh + 1].cpu()
+        for b in range(B):
+            r = gt.recurrent_grads(*(sl(t)[b] for t in (q, k, v, g, beta)), D ** -0.5, None,
+                                   sl(do)[b], None, True)
+            errs = {name: rel_err(t.grad[b, :, hh:hh + 1], e)
+                    for name, t, e in zip(["dq", "dk", "dv", "dg", "dbeta"], ins, r)}
+            print("head", hh, "seq", b, {n: f"{e:.2e}" for n, e in errs.items()})
+            for name, e in errs.items():
+                assert e < GRAD_REL, f"head {hh} seq {b} {name}: rel {e:.3e}"
