@@ -1463,8 +1463,7 @@ __global__ __launch_bounds__(BNTHR) void gdn_bwd_prep_kernel(Bwd p) {
 constexpr int CH_OFF_K = 0, CH_OFF_Q = C * LR * 2, CH_OFF_DO = 2 * C * LR * 2;
 constexpr int CH_OFF_T = 3 * C * LR * 2, CH_OFF_P = CH_OFF_T + C * LL * 2;
 constexpr int CH_OFF_SC = CH_OFF_P + C * LL * 2;
-constexpr int CH_OFF_DS = CH_OFF_SC + 4 * C * 4;               // fp16 [D][LR] dS staging
-constexpr int CH_SMEM = CH_OFF_DS + D * LR * 2;
+constexpr int CH_SMEM = CH_OFF_SC + 4 * C * 4;     // 33 KB: three workgroups per CU
 
 // One block's global inputs for this thread, loaded a block or two ahead of use:
 // its row of k, q and dO (features 8 (tid & 15) .. +7 of row tid >> 4), two
@@ -1504,7 +1503,6 @@ __global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_chain_kernel(Bwd p) {
   f16* sT = reinterpret_cast<f16*>(smem + CH_OFF_T);
   f16* sP = reinterpret_cast<f16*>(smem + CH_OFF_P);
   const Sc sc = sc_at(smem + CH_OFF_SC);
-  f16* sDS = reinterpret_cast<f16*>(smem + CH_OFF_DS);
   const int sg = blockIdx.x, h = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1565,21 +1563,14 @@ __global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_chain_kernel(Bwd p) {
   if (wend > ba) chain_load(p, pa, wend - 1, blk_tok(wend - 1), min(C, eos - blk_tok(wend - 1)), h, tid, wave, lane);
   if (wend - 1 > ba) chain_load(p, pb, wend - 2, blk_tok(wend - 2), C, h, tid, wave, lane);
   for (int cb = wend - 1; cb >= ba; --cb) {
-    // the gradient of the state leaving block cb (blocks of this segment), through
-    // LDS to 16-byte stores
+    if (cb < bb) {   // the gradient of the state leaving block cb (this run's blocks)
+      f16* dst = p.dhc + ((int64_t)cb * p.H + h) * DD + c0 + l16;
 #pragma unroll
-    for (int rt = 0; rt < 8; ++rt)
+      for (int rt = 0; rt < 8; ++rt)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) sDS[(16 * rt + 4 * q4 + v) * LR + c0 + l16] = (f16)dS[rt][v];
-    lds_barrier();   // also: the previous block's LDS reads are done
-    if (cb < bb) {
-      f16* dst = p.dhc + ((int64_t)cb * p.H + h) * DD;
-#pragma unroll
-      for (int pass = 0; pass < 4; ++pass) {
-        const int e = (pass * BNTHR + tid) * 8, row = e >> 7, col = e & 127;
-        *reinterpret_cast<f16x8*>(dst + e) = *reinterpret_cast<const f16x8*>(sDS + row * LR + col);
-      }
+        for (int v = 0; v < 4; ++v) dst[(16 * rt + 4 * q4 + v) * D] = (f16)dS[rt][v];
     }
+    lds_barrier();   // the previous block's LDS reads are done
     {  // stage block cb from registers
       const int row = tid >> 4, f0 = (tid & 15) * 8;
       const float rk = p.l2norm ? row_inv_norm(pa.k) : 1.f;

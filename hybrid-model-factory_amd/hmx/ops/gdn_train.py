@@ -41,11 +41,12 @@ def block_table(bounds: list[tuple[int, int]]):
 
 def chain_segments(cu_blocks: np.ndarray, H: int, cu_count: int, seg_blocks: int | None = None):
     """int32 rows (sequence, first block, end block): every sequence's blocks cut into
-    runs of at most ``seg_blocks`` blocks (by default as long as gives about two
-    workgroups per CU over all heads), one (empty) row for a sequence without blocks."""
+    runs of at most ``seg_blocks`` blocks (by default as long as gives about three
+    workgroups per CU over all heads, as many as fit one), one (empty) row for a
+    sequence without blocks."""
     total = int(cu_blocks[-1])
     if seg_blocks is None:
-        seg_blocks = max(1, -(-total * H // (2 * cu_count)))
+        seg_blocks = max(1, -(-total * H // (3 * cu_count)))
     rows = []
     for n in range(len(cu_blocks) - 1):
         a, e = int(cu_blocks[n]), int(cu_blocks[n + 1])

@@ -39,15 +39,15 @@ def test_chain_runs_partition_each_sequence(seg):
         assert mine[0][0] == cu[n] and mine[-1][1] == cu[n + 1]
         for (a, b), (c, _) in zip(mine, mine[1:]):
             assert b == c                        # consecutive, no gap or overlap
-        limit = seg if seg is not None else max(1, -(-int(cu[-1]) * 4 // 512))
+        limit = seg if seg is not None else max(1, -(-int(cu[-1]) * 4 // 768))
         assert all(0 < b - a <= limit for a, b in mine)
 
 
 def test_chain_runs_default_size():
-    """By default about two workgroups per CU over all heads."""
+    """By default about three workgroups per CU over all heads."""
     _, cu = block_table([(0, 32 * 1024)])
     runs = chain_segments(cu, H=32, cu_count=256)
-    assert len(runs) == 16 and all(b - a == 64 for _, a, b in runs)
+    assert len(runs) == 24 and all(b - a <= 43 for _, a, b in runs)
 
 
 def _bwd_args(**over):
