@@ -1472,7 +1472,6 @@ struct ChainPre {
   bf16x8 k, q, o;
   uint32_t t, pm;
   float g, b;
-  int nval;
 };
 
 __device__ __forceinline__ void chain_load(const Bwd& p, ChainPre& r, int cb, int tok0, int nval,
@@ -1492,10 +1491,9 @@ __device__ __forceinline__ void chain_load(const Bwd& p, ChainPre& r, int cb, in
     r.g = ld_scalar(p.g, i, p.g_dt);
     r.b = ld_scalar(p.beta, i, p.beta_dt);
   }
-  r.nval = nval;
 }
 
-__global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_chain_kernel(Bwd p) {
+__global__ __launch_bounds__(BNTHR, 3) void gdn_bwd_chain_kernel(Bwd p) {
   __shared__ __align__(16) unsigned char smem[CH_SMEM];
   f16* sK = reinterpret_cast<f16*>(smem + CH_OFF_K);
   f16* sQ = reinterpret_cast<f16*>(smem + CH_OFF_Q);
@@ -1518,31 +1516,46 @@ __global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_chain_kernel(Bwd p) {
     eos = p.ctab[(last - 1) * 4] + p.ctab[(last - 1) * 4 + 1];
   }
   auto blk_tok = [&](int cb) { return bos + (cb - first) * C; };
-  // Where this segment's chain starts.  A segment that ends before the sequence
-  // does starts from zero at the end of a warm-up over the following blocks, long
-  // enough that the dropped history, bounded by prod_t e^{g_t} max(1, |1 - beta_t|)
-  // (the spectral norm of e^g (I - beta k k^T) for |k| = 1, which the in-kernel
-  // L2 normalisation guarantees), is below e^-decay_thresh; without that bound
-  // within max_warm blocks, or without the normalisation, it starts from the
-  // sequence end (the exact chain).
+  // Where this run's chain starts.  A run that ends before its sequence does
+  // starts from zero at the end of a warm-up over the following blocks, long enough
+  // that the dropped history, bounded by prod_t e^{g_t} max(1, |1 - beta_t|) (the
+  // spectral norm of e^g (I - beta k k^T) for |k| = 1, which the in-kernel L2
+  // normalisation guarantees), is below e^-decay_thresh; without that bound within
+  // max_warm blocks, or without the normalisation, it starts from the sequence end
+  // (the exact chain).  Wave 0 reads 16 blocks' gates at a time: lane l sums tokens
+  // 8 (l & 3) .. +7 of block l >> 2, then a prefix over the blocks finds the first
+  // one that brings the bound below the threshold.
   int wend = last;
   if (bb < last && p.l2norm) {
     if (wave == 0) {
       float acc = 0.f;
       int w = last;
       const int lim = min(last, bb + p.max_warm);
-      for (int cb = bb; cb < lim; ++cb) {
-        const int t0 = blk_tok(cb), nv = min(C, eos - t0);
+      for (int base = bb; base < lim; base += 16) {
+        const int cb = base + (lane >> 2);
         float x = 0.f;
-        if (lane < nv) {
-          const int64_t i = (int64_t)(t0 + lane) * p.H + h;
-          x = ld_scalar(p.g, i, p.g_dt) + __logf(fmaxf(1.f, fabsf(1.f - ld_scalar(p.beta, i, p.beta_dt))));
+        if (cb < lim) {
+          const int t0 = blk_tok(cb) + 8 * (lane & 3), t1 = min(t0 + 8, eos);
+          for (int t = t0; t < t1; ++t) {
+            const int64_t i = (int64_t)t * p.H + h;
+            x += ld_scalar(p.g, i, p.g_dt) +
+                 __logf(fmaxf(1.f, fabsf(1.f - ld_scalar(p.beta, i, p.beta_dt))));
+          }
         }
-        acc += wave_sum(x);
-        if (acc < -p.decay_thresh) {
-          w = cb + 1;
+        x += __shfl_xor(x, 1, 64);
+        x += __shfl_xor(x, 2, 64);          // the block's sum, in its four lanes
+        float pre = x;                      // inclusive prefix over the blocks
+#pragma unroll
+        for (int off = 4; off < 64; off <<= 1) {
+          const float y = __shfl_up(pre, off, 64);
+          if (lane >= off) pre += y;
+        }
+        const unsigned long long hit = __ballot(cb < lim && acc + pre < -p.decay_thresh);
+        if (hit) {
+          w = base + (__builtin_ctzll(hit) >> 2) + 1;
           break;
         }
+        acc += __shfl(pre, 63, 64);
       }
       if (lane == 0) sc.G[0] = __builtin_bit_cast(float, w);
     }
