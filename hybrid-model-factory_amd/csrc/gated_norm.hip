@@ -14,7 +14,9 @@
 namespace hmx {
 namespace gnorm {
 
-__device__ __forceinline__ float silu(float z) { return z / (1.0f + fast_exp(-z)); }
+__device__ __forceinline__ float silu(float z) {
+  return z * __builtin_amdgcn_rcpf(1.0f + fast_exp(-z));
+}
 
 __device__ __forceinline__ float ld_w(const void* w, int i, int dt) {
   if (dt == HMX_F32) return static_cast<const float*>(w)[i];
@@ -51,7 +53,7 @@ __global__ __launch_bounds__(256) void rms_norm_gated_kernel(
     for (int j = 0; j < 8; ++j) ss += u[j] * u[j];
 #pragma unroll
     for (int m = LPR / 2; m >= 1; m >>= 1) ss += shfl_xor(ss, m);
-    const float rstd = 1.0f / sqrtf(ss * (1.0f / D) + eps);
+    const float rstd = __builtin_amdgcn_rsqf(ss * (1.0f / D) + eps);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       u[j] *= rstd * wv[j];
