@@ -550,7 +550,8 @@ def bench_gdn_train(dev, steps, warmup, B=8, T=4096, H=32):
     forward + backward, B=8 x T=4096 tokens, H=32, d=128; inputs as the training
     layer forms them (q, k, v ~ N(0, 1) bf16, g = -e^{A_log} softplus(x + dt_bias)
     fp32, beta = sigmoid(x) bf16, do ~ N(0, 1)).  Also forward + backward at the C1
-    shape (B=1, T=32768), where the state-gradient chain has one workgroup per head."""
+    shape (B=1, T=32768), with these gates and with a fresh layer's gates (many heads
+    decay too slowly for a warm-up: their state-gradient runs take the exact combine)."""
     import torch
     import torch.nn.functional as F
     import hmx
@@ -566,8 +567,11 @@ def bench_gdn_train(dev, steps, warmup, B=8, T=4096, H=32):
         beta = torch.sigmoid(r(B, T, H)).bfloat16()
         return q, k, v, gate, beta, do
 
-    def run(B, T, with_bwd):
+    def run(B, T, with_bwd, layer_gates=False):
         q, k, v, gate, beta, do = inputs(B, T)
+        if layer_gates:    # a fresh layer's gates: many heads decay slowly (exact runs)
+            gate, beta = wl.gdn_layer_gates(T, H, device=dev)
+            beta = beta.bfloat16()
         ins = [t.clone().requires_grad_(True) for t in (q, k, v, gate, beta)]
 
         def fwd():
@@ -582,8 +586,10 @@ def bench_gdn_train(dev, steps, warmup, B=8, T=4096, H=32):
     ms_f = run(B, T, False)
     ms_fb = run(B, T, True)
     ms_c1 = run(1, 32768, True)
+    ms_c1_layer = run(1, 32768, True, layer_gates=True)
     ff, fb = wl.gdn_train_flops(B * T, H)
-    return dict(ms_fwd=ms_f, ms_fwd_bwd=ms_fb, ms_c1_fwd_bwd=ms_c1, flops_fwd=ff, flops_bwd=fb,
+    return dict(ms_fwd=ms_f, ms_fwd_bwd=ms_fb, ms_c1_fwd_bwd=ms_c1,
+                ms_c1_layer_gates_fwd_bwd=ms_c1_layer, flops_fwd=ff, flops_bwd=fb,
                 tokens_per_s=B * T / (ms_fb * 1e-3),
                 TFLOPs_fwd_bwd=(ff + fb) / (ms_fb * 1e-3) / 1e12)
 
@@ -983,6 +989,7 @@ def main():
             "value": round(r["tokens_per_s"], 1), "unit": "tokens/s (forward + backward)",
             "ms_fwd": round(r["ms_fwd"], 4), "ms_fwd_bwd": round(r["ms_fwd_bwd"], 4),
             "ms_fwd_bwd_at_c1_shape": round(r["ms_c1_fwd_bwd"], 4),
+            "ms_fwd_bwd_at_c1_shape_layer_gates": round(r["ms_c1_layer_gates_fwd_bwd"], 4),
             "config": {"workload": "F4 GDN training op (chunk_gated_delta_rule fwd + bwd)",
                        "B": 8, "T": 4096, "H": 32, "d": 128, "use_qk_l2norm_in_kernel": True},
             "roofline": {"bound": "mfma", "achieved": round(r["TFLOPs_fwd_bwd"], 1),

@@ -1290,9 +1290,14 @@ struct Bwd {
   f16* pm;                    // [nblk][H][C][C] scale lower(Q^K^T . Gm)
   const int* ctab;            // [nblk][4]: first token, tokens, sequence, block in sequence
   const int* cu_blk;          // [N+1]
-  const int* cseg;            // [nseg][3]: sequence, first block, end block of a chain segment
-  int max_warm;               // warm-up blocks a chain segment may add past its end
+  const int* cseg;            // [nseg][3]: sequence, first block, end block of a chain run
+  int nseg;
+  int max_warm;               // warm-up blocks a chain run may add past its end
   float decay_thresh;         // ... to bring the dropped history under e^-decay_thresh
+  int* cplan;                 // [nseg][H]: where a run's chain starts (its warm-up end), or -1
+  float* cR;                  // [nseg][H][D][D] exact runs: the chain from zero over the run
+  float* cPsi;                // [nseg][H][D][D] ... and the product of its transposed transitions
+  float* cstart;              // [nseg][H][D][D] ... and the exact dS at the run's end
   bf16* dq; bf16* dk; bf16* dv;   // [tokens][H][D]
   float* dg; float* dbeta;        // [tokens][H]
   float* dh0;                 // [N][H][D][D] or null
@@ -1493,49 +1498,64 @@ __device__ __forceinline__ void chain_load(const Bwd& p, ChainPre& r, int cb, in
   }
 }
 
-__global__ __launch_bounds__(BNTHR, 3) void gdn_bwd_chain_kernel(Bwd p) {
-  __shared__ __align__(16) unsigned char smem[CH_SMEM];
-  f16* sK = reinterpret_cast<f16*>(smem + CH_OFF_K);
-  f16* sQ = reinterpret_cast<f16*>(smem + CH_OFF_Q);
-  f16* sDO = reinterpret_cast<f16*>(smem + CH_OFF_DO);
-  f16* sT = reinterpret_cast<f16*>(smem + CH_OFF_T);
-  f16* sP = reinterpret_cast<f16*>(smem + CH_OFF_P);
-  const Sc sc = sc_at(smem + CH_OFF_SC);
-  const int sg = blockIdx.x, h = blockIdx.y;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int q4 = lane >> 4, l16 = lane & 15;
-  const int c0 = 16 * wave;                      // this wave's value columns
-  const int64_t DD = (int64_t)D * D;
-  const int n = p.cseg[sg * 3], ba = p.cseg[sg * 3 + 1], bb = p.cseg[sg * 3 + 2];
-  const int first = p.cu_blk[n], last = p.cu_blk[n + 1];   // the sequence's blocks
-  // a sequence's blocks are consecutive 32-token runs from its first token
-  int bos = 0, eos = 0;
-  if (last > first) {
-    bos = p.ctab[first * 4];
-    eos = p.ctab[(last - 1) * 4] + p.ctab[(last - 1) * 4 + 1];
+enum ChainMode { CH_WALK = 0, CH_R = 1, CH_PSI = 2 };
+
+// The rows of the chain-run table that belong to sequence n (they are grouped by
+// sequence): [first, end), 64 rows per load round.
+__device__ __forceinline__ void seq_runs(const Bwd& p, int n, int lane, int& r0, int& r1) {
+  r0 = -1;
+  r1 = p.nseg;
+  for (int s0 = 0; s0 < p.nseg; s0 += 64) {
+    const int s = s0 + lane;
+    const int m = s < p.nseg ? p.cseg[s * 3] : 0x7fffffff;
+    const unsigned long long a = __ballot(m == n), b = __ballot(m > n);
+    if (r0 < 0 && a) r0 = s0 + __builtin_ctzll(a);
+    if (b) {
+      r1 = s0 + __builtin_ctzll(b);
+      break;
+    }
   }
-  auto blk_tok = [&](int cb) { return bos + (cb - first) * C; };
-  // Where this run's chain starts.  A run that ends before its sequence does
-  // starts from zero at the end of a warm-up over the following blocks, long enough
-  // that the dropped history, bounded by prod_t e^{g_t} max(1, |1 - beta_t|) (the
-  // spectral norm of e^g (I - beta k k^T) for |k| = 1, which the in-kernel L2
-  // normalisation guarantees), is below e^-decay_thresh; without that bound within
-  // max_warm blocks, or without the normalisation, it starts from the sequence end
-  // (the exact chain).  Wave 0 reads 16 blocks' gates at a time: lane l sums tokens
-  // 8 (l & 3) .. +7 of block l >> 2, then a prefix over the blocks finds the first
-  // one that brings the bound below the threshold.
-  int wend = last;
-  if (bb < last && p.l2norm) {
-    if (wave == 0) {
+  if (r0 < 0) r0 = r1;
+}
+
+// Whether any run of sequence n needs the exact combine for head h (wave-uniform).
+__device__ __forceinline__ bool head_exact(const Bwd& p, int n, int h, int lane) {
+  int r0, r1;
+  seq_runs(p, n, lane, r0, r1);
+  for (int s0 = r0; s0 < r1; s0 += 64) {
+    const int s = s0 + lane;
+    if (__ballot(s < r1 && p.cplan[s * p.H + h] < 0)) return true;
+  }
+  return false;
+}
+
+// ---- plan: where each run's chain starts --------------------------------------
+// A run that ends before its sequence does starts from zero at the end of a
+// warm-up over the following blocks, long enough that the dropped history, bounded
+// by prod_t e^{g_t} max(1, |1 - beta_t|) (the spectral norm of e^g (I - beta k k^T)
+// for |k| = 1, which the in-kernel L2 normalisation guarantees), is below
+// e^-decay_thresh.  Without that bound within max_warm blocks, or without the
+// normalisation, the run is exact (-1): its head then takes the combine.  One wave
+// per (run, head) reads 16 blocks' gates at a time: lane l sums tokens 8 (l & 3) ..
+// +7 of block l >> 2, then a prefix over the blocks finds the first one that brings
+// the bound below the threshold.
+__global__ __launch_bounds__(64) void gdn_bwd_plan_kernel(Bwd p) {
+  const int sg = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+  const int n = p.cseg[sg * 3], bb = p.cseg[sg * 3 + 2];
+  const int first = p.cu_blk[n], last = p.cu_blk[n + 1];
+  int w = last;
+  if (bb < last) {
+    w = -1;
+    if (p.l2norm) {
+      const int bos = p.ctab[first * 4];
+      const int eos = p.ctab[(last - 1) * 4] + p.ctab[(last - 1) * 4 + 1];
       float acc = 0.f;
-      int w = last;
       const int lim = min(last, bb + p.max_warm);
       for (int base = bb; base < lim; base += 16) {
         const int cb = base + (lane >> 2);
         float x = 0.f;
         if (cb < lim) {
-          const int t0 = blk_tok(cb) + 8 * (lane & 3), t1 = min(t0 + 8, eos);
+          const int t0 = bos + (cb - first) * C + 8 * (lane & 3), t1 = min(t0 + 8, eos);
           for (int t = t0; t < t1; ++t) {
             const int64_t i = (int64_t)t * p.H + h;
             x += ld_scalar(p.g, i, p.g_dt) +
@@ -1557,26 +1577,136 @@ __global__ __launch_bounds__(BNTHR, 3) void gdn_bwd_chain_kernel(Bwd p) {
         }
         acc += __shfl(pre, 63, 64);
       }
-      if (lane == 0) sc.G[0] = __builtin_bit_cast(float, w);
     }
-    lds_barrier();
-    wend = __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sc.G[0]));
   }
-  // dS[rt]: rows 16 rt + 4 q4 + v, column c0 + l16
-  f32x4 dS[8];
-  {
-    const float* src = (p.dht && wend == last) ? p.dht + ((int64_t)n * p.H + h) * DD : nullptr;
+  if (lane == 0) p.cplan[sg * p.H + h] = w;
+}
+
+// ---- combine: the exact dS at every run end of a head with an exact run ---------
+// Backward over the runs of sequence n: X = dht (or 0) at the sequence end; run r
+// starts from X, and X <- Psi_r X + R_r is the dS at the end of run r - 1.  X is
+// kept in fp32 accumulators (wave w owns columns 16w..); each product splits X into
+// fp16 hi + lo and rounds Psi_r (a product of contractions) to fp16 once.
+constexpr int CB_SMEM = D * LR * 2;
+__global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_combine_kernel(Bwd p) {
+  __shared__ __align__(16) unsigned char smem[CB_SMEM];
+  f16* sPsi = reinterpret_cast<f16*>(smem);
+  const int n = blockIdx.x, h = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q4 = lane >> 4, l16 = lane & 15, c0 = 16 * wave;
+  if (!head_exact(p, n, h, lane)) return;
+  int r0, r1;
+  seq_runs(p, n, lane, r0, r1);
+  const int64_t DD = (int64_t)D * D;
+  f32x4 X[8];
+  const float* src = p.dht ? p.dht + ((int64_t)n * p.H + h) * DD : nullptr;
+#pragma unroll
+  for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) X[rt][v] = src ? src[(16 * rt + 4 * q4 + v) * D + c0 + l16] : 0.f;
+  for (int r = r1 - 1; r >= r0; --r) {
+    const int64_t o = ((int64_t)r * p.H + h) * DD;
 #pragma unroll
     for (int rt = 0; rt < 8; ++rt)
 #pragma unroll
-      for (int v = 0; v < 4; ++v)
-        dS[rt][v] = src ? src[(16 * rt + 4 * q4 + v) * D + c0 + l16] : 0.f;
+      for (int v = 0; v < 4; ++v) p.cstart[o + (16 * rt + 4 * q4 + v) * D + c0 + l16] = X[rt][v];
+    if (r == r0) break;
+    lds_barrier();   // the previous run's Psi reads are done
+    for (int e = tid * 8; e < D * D; e += BNTHR * 8) {   // Psi_r into LDS, fp16, interleaved
+      float f[8];
+      load_vec<8>(p.cPsi + o + e, f);
+      f16x8 y;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) y[j] = (f16)f[j];
+      store8_i(sPsi + (e >> 7) * LR, e & 127, y);
+    }
+    lds_barrier();
+    f16x8 xh[4], xl[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      f32x4 lo0, lo1;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        lo0[v] = X[2 * m][v] - (float)(f16)X[2 * m][v];
+        lo1[v] = X[2 * m + 1][v] - (float)(f16)X[2 * m + 1][v];
+      }
+      xh[m] = h8(X[2 * m], X[2 * m + 1]);
+      xl[m] = h8(lo0, lo1);
+    }
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt) {
+      f32x4 acc;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[v] = p.cR[o + (16 * rt + 4 * q4 + v) * D + c0 + l16];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const f16x8 a = frag_i(sPsi, LR, 16 * rt, 32 * m, lane);
+        acc = mfma16h(a, xh[m], acc);
+        acc = mfma16h(a, xl[m], acc);
+      }
+      X[rt] = acc;
+    }
   }
+}
+
+__global__ __launch_bounds__(BNTHR, 3) void gdn_bwd_chain_kernel(Bwd p, int mode) {
+  __shared__ __align__(16) unsigned char smem[CH_SMEM];
+  f16* sK = reinterpret_cast<f16*>(smem + CH_OFF_K);
+  f16* sQ = reinterpret_cast<f16*>(smem + CH_OFF_Q);
+  f16* sDO = reinterpret_cast<f16*>(smem + CH_OFF_DO);
+  f16* sT = reinterpret_cast<f16*>(smem + CH_OFF_T);
+  f16* sP = reinterpret_cast<f16*>(smem + CH_OFF_P);
+  const Sc sc = sc_at(smem + CH_OFF_SC);
+  const int sg = blockIdx.x, h = blockIdx.y;
+  if (mode != CH_WALK) mode = blockIdx.z ? CH_PSI : CH_R;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q4 = lane >> 4, l16 = lane & 15;
+  const int c0 = 16 * wave;                      // this wave's value columns
+  const int64_t DD = (int64_t)D * D;
+  const int n = p.cseg[sg * 3], ba = p.cseg[sg * 3 + 1], bb = p.cseg[sg * 3 + 2];
+  const int first = p.cu_blk[n], last = p.cu_blk[n + 1];   // the sequence's blocks
+  // a sequence's blocks are consecutive 32-token runs from its first token
+  int bos = 0, eos = 0;
+  if (last > first) {
+    bos = p.ctab[first * 4];
+    eos = p.ctab[(last - 1) * 4] + p.ctab[(last - 1) * 4 + 1];
+  }
+  auto blk_tok = [&](int cb) { return bos + (cb - first) * C; };
+  // Where this run's chain starts and from what (the plan kernel's choice): after a
+  // warm-up from zero, or from the sequence end (the last run); for a head with an
+  // exact run, every run starts at its own end from the combine's exact dS.
+  const bool hexact = head_exact(p, n, h, lane);
+  int wend = p.cplan[sg * p.H + h];
+  const float* src = nullptr;
+  bool ident = false;
+  if (mode == CH_WALK) {
+    if (hexact) {
+      wend = bb;
+      if (bb < last) src = p.cstart + ((int64_t)sg * p.H + h) * DD;
+    }
+    if (wend == last && p.dht) src = p.dht + ((int64_t)n * p.H + h) * DD;
+  } else {           // pre-pass of an exact head's run: R from zero, Psi from I
+    if (!hexact || ba == first) return;
+    wend = bb;
+    ident = mode == CH_PSI;
+  }
+  // dS[rt]: rows 16 rt + 4 q4 + v, column c0 + l16
+  f32x4 dS[8];
+#pragma unroll
+  for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int row = 16 * rt + 4 * q4 + v, col = c0 + l16;
+      dS[rt][v] = src ? src[row * D + col] : ((ident && row == col) ? 1.f : 0.f);
+    }
+  const bool with_do = mode != CH_PSI;
   ChainPre pa, pb;                               // blocks cb and cb - 1
   if (wend > ba) chain_load(p, pa, wend - 1, blk_tok(wend - 1), min(C, eos - blk_tok(wend - 1)), h, tid, wave, lane);
   if (wend - 1 > ba) chain_load(p, pb, wend - 2, blk_tok(wend - 2), C, h, tid, wave, lane);
   for (int cb = wend - 1; cb >= ba; --cb) {
-    if (cb < bb) {   // the gradient of the state leaving block cb (this run's blocks)
+    if (mode == CH_WALK && cb < bb) {   // the gradient of the state leaving block cb
       f16* dst = p.dhc + ((int64_t)cb * p.H + h) * DD + c0 + l16;
 #pragma unroll
       for (int rt = 0; rt < 8; ++rt)
@@ -1622,8 +1752,10 @@ __global__ __launch_bounds__(BNTHR, 3) void gdn_bwd_chain_kernel(Bwd p) {
       for (int v = 0; v < 4; ++v) dW[mt][v] = sc.F[16 * mt + 4 * q4 + v] * acc[v];
     }
     const f16x8 bdo = frag_col(sDO, LR, 0, c0, lane);
+    if (with_do) {
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) dW[mt] = mfma16h(frag_col(sP, LL, 0, 16 * mt, lane), bdo, dW[mt]);
+      for (int mt = 0; mt < 2; ++mt) dW[mt] = mfma16h(frag_col(sP, LL, 0, 16 * mt, lane), bdo, dW[mt]);
+    }
     f32x4 Zp[2];
     {
       const f16x8 bw = h8(dW[0], dW[1]);
@@ -1649,8 +1781,16 @@ __global__ __launch_bounds__(BNTHR, 3) void gdn_bwd_chain_kernel(Bwd p) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) dS[rt][v] *= eL;
       dS[rt] = mfma16h(frag_t_i(sK, LR, 0, 16 * rt, lane), bz, dS[rt]);
-      dS[rt] = mfma16h(frag_col(sQ, LR, 0, 16 * rt, lane), bqe, dS[rt]);
+      if (with_do) dS[rt] = mfma16h(frag_col(sQ, LR, 0, 16 * rt, lane), bqe, dS[rt]);
     }
+  }
+  if (mode != CH_WALK) {   // the run's R or Psi
+    float* dst = (mode == CH_R ? p.cR : p.cPsi) + ((int64_t)sg * p.H + h) * DD + c0 + l16;
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) dst[(16 * rt + 4 * q4 + v) * D] = dS[rt][v];
+    return;
   }
   if (p.dh0 && ba == first) {
     float* dst = p.dh0 + ((int64_t)n * p.H + h) * DD + c0 + l16;
@@ -2063,9 +2203,12 @@ extern "C" int hmx_gdn_train_fwd(const void* q, int64_t q_token_stride, const vo
                         static_cast<f16*>(block_states), cu_blocks);
 }
 
-extern "C" size_t hmx_gdn_train_bwd_workspace_bytes(int32_t nblock_total, int32_t H) {
-  // dS per block (fp16 D x D), then T and P per block (fp16 C x C each)
-  return (size_t)nblock_total * H * ((size_t)D * D + 2 * C * C) * sizeof(f16);
+extern "C" size_t hmx_gdn_train_bwd_workspace_bytes(int32_t nblock_total,
+                                                    int32_t nchain_segments, int32_t H) {
+  // dS per block (fp16 D x D), T and P per block (fp16 C x C each); per chain run
+  // the plan entry and R, Psi and the exact start (fp32 D x D each)
+  return (size_t)nblock_total * H * ((size_t)D * D + 2 * C * C) * sizeof(f16) +
+         (size_t)nchain_segments * H * (sizeof(int) + 3 * (size_t)D * D * sizeof(float)) + 256;
 }
 
 extern "C" int hmx_gdn_train_bwd(const void* q, int64_t q_token_stride, const void* k,
@@ -2092,7 +2235,7 @@ extern "C" int hmx_gdn_train_bwd(const void* q, int64_t q_token_stride, const vo
                   ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)dout |
                    (uintptr_t)block_states) % 16 == 0,
               HMX_EINVAL, "hmx_gdn_train_bwd: rows must be 16-byte aligned");
-  const size_t need = hmx_gdn_train_bwd_workspace_bytes(nblock_total, H);
+  const size_t need = hmx_gdn_train_bwd_workspace_bytes(nblock_total, nchain_segments, H);
   HMX_REQUIRE(workspace && workspace_bytes >= need && (uintptr_t)workspace % 16 == 0, HMX_EINVAL,
               "hmx_gdn_train_bwd: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
   Bwd p;
@@ -2107,8 +2250,18 @@ extern "C" int hmx_gdn_train_bwd(const void* q, int64_t q_token_stride, const vo
   p.dhc = ws;
   p.tm = ws + (size_t)nblock_total * H * D * D;
   p.pm = p.tm + (size_t)nblock_total * H * C * C;
+  {
+    const size_t runs_hd = (size_t)nchain_segments * H * D * D;
+    char* tail = reinterpret_cast<char*>(p.pm + (size_t)nblock_total * H * C * C);
+    tail += (256 - reinterpret_cast<uintptr_t>(tail) % 256) % 256;
+    p.cR = reinterpret_cast<float*>(tail);
+    p.cPsi = p.cR + runs_hd;
+    p.cstart = p.cPsi + runs_hd;
+    p.cplan = reinterpret_cast<int*>(p.cstart + runs_hd);
+  }
   p.ctab = block_table; p.cu_blk = cu_blocks;
-  p.cseg = chain_segments; p.max_warm = max_warm_blocks; p.decay_thresh = decay_threshold;
+  p.cseg = chain_segments; p.nseg = nchain_segments;
+  p.max_warm = max_warm_blocks; p.decay_thresh = decay_threshold;
   p.dq = static_cast<bf16*>(dq); p.dk = static_cast<bf16*>(dk); p.dv = static_cast<bf16*>(dv);
   p.dg = dg; p.dbeta = dbeta; p.dh0 = dh0;
   p.H = H; p.nblk = nblock_total; p.scale = scale; p.l2norm = use_qk_l2norm;
@@ -2121,7 +2274,14 @@ extern "C" int hmx_gdn_train_bwd(const void* q, int64_t q_token_stride, const vo
   const int grad_grid = (int)std::min<int64_t>(work, (int64_t)cus);
   if (nblock_total > 0)
     hipLaunchKernelGGL(gdn_bwd_prep_kernel, dim3(nblock_total, H), dim3(BNTHR), 0, s, p);
-  hipLaunchKernelGGL(gdn_bwd_chain_kernel, dim3(nchain_segments, H), dim3(BNTHR), 0, s, p);
+  // where each chain run starts; for heads with an exact run, every run's R and
+  // Psi, then their exact starts; then the chain walk
+  hipLaunchKernelGGL(gdn_bwd_plan_kernel, dim3(nchain_segments, H), dim3(64), 0, s, p);
+  hipLaunchKernelGGL(gdn_bwd_chain_kernel, dim3(nchain_segments, H, 2), dim3(BNTHR), 0, s, p,
+                     (int)CH_R);
+  hipLaunchKernelGGL(gdn_bwd_combine_kernel, dim3(N, H), dim3(BNTHR), 0, s, p);
+  hipLaunchKernelGGL(gdn_bwd_chain_kernel, dim3(nchain_segments, H), dim3(BNTHR), 0, s, p,
+                     (int)CH_WALK);
   if (nblock_total > 0)
     hipLaunchKernelGGL(gdn_bwd_grad_kernel, dim3(grad_grid), dim3(BNTHR), 0, s, p);
   return check_launch("hmx_gdn_train_bwd");

@@ -131,7 +131,7 @@ def chunk_backward(q, k, v, g, beta, scale, h0, do, dht, bounds, l2norm, segment
     if dht is not None:
         dht = dht.to(torch.float32).contiguous()
     lib = _lib.load()
-    ws = torch.empty(max(int(lib.hmx_gdn_train_bwd_workspace_bytes(nblk, H)), 16),
+    ws = torch.empty(max(int(lib.hmx_gdn_train_bwd_workspace_bytes(nblk, cseg_np.shape[0], H)), 16),
                      dtype=torch.uint8, device=q.device)
     (q, q_ts), (k, kv_ts), (v, _), (do, do_ts) = _rows(q), _rows(k), _rows(v), _rows(do)
     _lib.call("hmx_gdn_train_bwd",

@@ -287,11 +287,13 @@ int hmx_gdn_train_fwd(const void* q, int64_t q_token_stride, const void* k, cons
  * one workgroup each walks backward (every sequence needs at least one row, an
  * empty one for a sequence without tokens); a run that ends before its sequence
  * starts from zero after a warm-up of up to max_warm_blocks following blocks whose
- * gates bring the dropped history under e^-decay_threshold, and from the sequence
- * end otherwise.  Writes dq, dk, dv [tokens][H][128] bf16 (rows
+ * gates bring the dropped history under e^-decay_threshold; a head with a run that
+ * finds no such warm-up takes every run's exact start from a combine over the runs
+ * (each run's chain from zero and its transposed transition product).  Writes dq,
+ * dk, dv [tokens][H][128] bf16 (rows
  * of the blocks' tokens only), dg and dbeta [tokens][H] fp32, and dh0 (the
  * gradient of the initial states, fp32 [N][H][128][128]) when not null.
- * workspace: hmx_gdn_train_bwd_workspace_bytes(nblock_total, H) bytes.
+ * workspace: hmx_gdn_train_bwd_workspace_bytes(nblock_total, nchain_segments, H) bytes.
  * Replaces: the backward of fla's chunk_gated_delta_rule (un-vendored; the training
  *   layer's call at training/src/hmf/model/hybrid_zoo/layers/gated_deltanet/gdn.py:
  *   462-476, whose torch fallback is the recurrence of
@@ -307,7 +309,8 @@ int hmx_gdn_train_bwd(const void* q, int64_t q_token_stride, const void* k, cons
                       int32_t use_qk_l2norm, void* dq, void* dk, void* dv, float* dg,
                       float* dbeta, float* dh0, void* workspace, size_t workspace_bytes,
                       void* stream);
-size_t hmx_gdn_train_bwd_workspace_bytes(int32_t nblock_total, int32_t H);
+size_t hmx_gdn_train_bwd_workspace_bytes(int32_t nblock_total, int32_t nchain_segments,
+                                         int32_t H);
 
 /*
  * GKA gating: g = -exp(A_log) * softplus(a + dt_bias), alpha = sigmoid(alpha_in),

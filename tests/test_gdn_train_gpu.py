@@ -157,3 +157,23 @@ def test_backward_all_heads_subset_against_oracle(dev):
             print("head", hh, "seq", b, {n: f"{e:.2e}" for n, e in errs.items()})
             for name, e in errs.items():
                 assert e < GRAD_REL, f"head {hh} seq {b} {name}: rel {e:.3e}"
+
+
+def test_backward_layer_gates_against_oracle(dev):
+    """The gates a freshly initialised layer forms (hmx.workloads.gdn_layer_gates:
+    A_log = log U(1, 16), Mamba2 dt_bias): several heads decay too slowly for any
+    warm-up, so their state-gradient runs take the exact combine."""
+    from hmx import workloads as wl
+    T, H = 2048, 4
+    q, k, v, _, _, do = _inputs(1, T, H, 13, dev)
+    g, beta = wl.gdn_layer_gates(T, H, device=dev)
+    ins = [t.clone().requires_grad_(True) for t in (q, k, v, g, beta)]
+    o, _ = ChunkGatedDeltaRule.apply(*ins, D ** -0.5, None, False, None, True, None)
+    (o.float() * do.float()).sum().backward()
+    r = gt.recurrent_grads(*(t.detach()[0].cpu() for t in (q, k, v, g, beta)), D ** -0.5, None,
+                           do[0].cpu(), None, True)
+    errs = {name: rel_err(t.grad[0], e) for name, t, e in zip(["dq", "dk", "dv", "dg", "dbeta"],
+                                                              ins, r)}
+    print("errors", {n: f"{e:.2e}" for n, e in errs.items()})
+    for name, e in errs.items():
+        assert e < GRAD_REL, f"{name}: rel {e:.3e}"

@@ -72,9 +72,9 @@ def test_train_bwd_rejects_bad_arguments():
     assert lib.hmx_gdn_train_bwd(*_bwd_args(**ptrs, q_ts=1001)) == _lib.HMX_EINVAL
     assert b"16-byte aligned" in lib.hmx_last_error()
     assert lib.hmx_gdn_train_bwd(*_bwd_args(**ptrs)) == _lib.HMX_EINVAL   # no workspace
-    need = lib.hmx_gdn_train_bwd_workspace_bytes(1, 8)
+    need = lib.hmx_gdn_train_bwd_workspace_bytes(1, 1, 8)
     assert b"workspace of %d bytes" % need in lib.hmx_last_error()
-    assert need == 8 * (128 * 128 + 2 * 32 * 32) * 2
+    assert need == 8 * (128 * 128 + 2 * 32 * 32) * 2 + 8 * (4 + 3 * 128 * 128 * 4) + 256
 
 
 def test_train_fwd_requires_block_states():
