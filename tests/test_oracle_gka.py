@@ -3,6 +3,10 @@
 The reference ships no torch implementation or vectors for GKA, so:
   - the solver is the Chebyshev semi-iteration: it converges to
     solve(H + lam I, q) and obeys the textbook error bound on [lam, lam + |H|_F];
+    at every finite num_iter its iterate equals the closed form x* - P(A) x*, with P
+    the scaled Chebyshev residual polynomial of degree num_iter + 1 evaluated on the
+    eigenvalues (both the serving solve and the training solve), and planted
+    transcription mistakes (omega_0, rho^2/4, momentum sign, ...) fail that check;
   - |H_t|_F by the reference's closed form (chebyshev_prefill_gqa.py:227-235)
     equals the explicit Frobenius norm of the per-token H_t;
   - with alpha = 0 (or num_iter = 0) the op is beta^2 GLA, which equals the
@@ -201,3 +205,112 @@ def test_training_decode_steps_equal_training_prefill():
                                                 gk[None, t:t + 1], 0.2, 0.02, 5, hk, hv)
         assert torch.allclose(o[0, 0], o_p[0, t])
     assert torch.allclose(hk, hk_p) and torch.allclose(hv, hv_p)
+
+
+# ---------------------------------------------------------------------------
+# The solver at finite num_iter.  The C3 runs (ridge 0.01, n = 8 / 32) stop far from
+# convergence, so the exact iterate is the contract.  The recurrence of
+# chebyshev_iteration_gqa.py:115-134 is the Chebyshev semi-iteration (Golub & Varga
+# 1961) on A = H + lam I over [a, b] = [lam, lam + |H|_F], started from y_0 = 0 with a
+# Richardson step y_1 = tau q (omega_1 = 1; the loop's first omega, 1/(1 - c 2), is
+# omega_2).  After n loop steps the iterate is y_{n+1}, whose error is the scaled
+# Chebyshev residual polynomial of degree n+1 applied to the initial error -x*:
+#     x* - y_{n+1} = P(A) x*,   P(mu) = T_{n+1}((b + a - 2 mu)/(b - a)) / T_{n+1}((b + a)/(b - a)).
+# On an eigenbasis A = Q diag(mu + lam) Q^T this is a closed form in the eigenvalues,
+# evaluated here with numpy's Chebyshev series (Clenshaw), independent of the
+# three-term recurrence the oracle runs.
+# ---------------------------------------------------------------------------
+def _cheb_residual(Qm, mu, q, ridge_ratio, n):
+    """x* - P(A) x* for H = Qm diag(mu) Qm^T, from the eigenvalues alone."""
+    import numpy as np
+    from numpy.polynomial import chebyshev as npc
+    f = float(np.sqrt((mu.numpy() ** 2).sum()))
+    lam = ridge_ratio * f
+    a, b = lam, lam + f
+    coef = np.zeros(n + 2)
+    coef[n + 1] = 1.0
+    s = mu.numpy() + lam
+    P = npc.chebval((b + a - 2 * s) / (b - a), coef) / npc.chebval((b + a) / (b - a), coef)
+    xs_eig = (Qm.T @ q).numpy() / s                       # x* in the eigenbasis
+    return Qm @ torch.from_numpy(xs_eig * (1.0 - P))
+
+
+def _spectra(seed, D=16):
+    """(Q, mu) pairs: a random orthogonal basis with a spread PSD spectrum (one
+    eigenvalue near 0, one near |H|_F), and the eigendecomposition of a real key
+    Gram sum_j k~_j k~_j^T as the prefill forms it."""
+    g0 = torch.Generator().manual_seed(seed)
+    Qm, _ = torch.linalg.qr(torch.randn(D, D, generator=g0, dtype=D64))
+    mu = torch.cat([torch.tensor([1e-4, 3.0], dtype=D64),
+                    torch.rand(D - 2, generator=g0, dtype=D64) * 0.7])
+    kk = ref.l2n(torch.randn(40, D, generator=g0, dtype=D64))
+    kk = kk * (torch.sigmoid(torch.randn(40, 1, generator=g0, dtype=D64)) + 1e-6)
+    mu2, Q2 = torch.linalg.eigh(kk.T @ kk)
+    return [(Qm, mu), (Q2, mu2.clamp_min(0.0))]
+
+
+@pytest.mark.parametrize("n", [0, 1, 2, 4, 8, 32])
+@pytest.mark.parametrize("r", [0.01, 0.02])
+def test_chebyshev_finite_n_equals_residual_polynomial(n, r):
+    """ref.chebyshev after n loop steps == x* - P_{n+1}(A) x* to 1e-12, for both
+    spectra, batched (leading dim) as the prefill calls it."""
+    g0 = torch.Generator().manual_seed(100 + n)
+    for Qm, mu in _spectra(7 + n):
+        D = mu.numel()
+        H = Qm @ torch.diag(mu) @ Qm.T
+        H = 0.5 * (H + H.T)
+        q = torch.randn(3, D, generator=g0, dtype=D64)
+        x, fro = ref.chebyshev(H.expand(3, D, D), q, r, n)
+        assert torch.allclose(fro, torch.linalg.matrix_norm(H).expand(3), rtol=1e-13)
+        for i in range(3):
+            want = _cheb_residual(Qm, mu, q[i], r, n)
+            err = (x[i] - want).norm() / want.norm()
+            assert err < 1e-12, (n, r, i, float(err))
+
+
+@pytest.mark.parametrize("n", [0, 1, 4, 8, 32])
+def test_training_chebyshev_fixed_equals_residual_polynomial(n):
+    """oracle/gka_train.py:chebyshev_fixed (|H|_F given, CI:397-406) obeys the same
+    closed form."""
+    from oracle import gka_train as tr
+    g0 = torch.Generator().manual_seed(200 + n)
+    for Qm, mu in _spectra(17 + n):
+        D = mu.numel()
+        H = Qm @ torch.diag(mu) @ Qm.T
+        H = 0.5 * (H + H.T)
+        q = torch.randn(D, generator=g0, dtype=D64)
+        x = tr.chebyshev_fixed(H[None], q[None], torch.linalg.matrix_norm(H)[None], 0.01, n)[0]
+        want = _cheb_residual(Qm, mu, q, 0.01, n)
+        assert (x - want).norm() / want.norm() < 1e-12
+
+
+# Mistakes a transcription of CI:115-134 could plausibly make.  Each is planted in a
+# copy of the oracle's own source (text substitution, then exec), which must still
+# run but fail the closed form: the check above would catch it.
+_MUTANTS = [
+    ("torch.full_like(fro, 2.0)", "torch.full_like(fro, 1.0)"),      # omega_0 = 1
+    ("(fro / denom * 0.5) ** 2", "(fro / denom) ** 2"),              # rho^2 without the 1/4
+    ("(w - 1.0)[..., None] * x_prev", "(1.0 - w)[..., None] * x_prev"),  # sign of the momentum
+    ("x = tau[..., None] * q", "x = q"),                             # no first Richardson step
+    ("range(num_iter)", "range(num_iter - 1)"),                      # one step short
+    ("hx + lam[..., None] * x - q", "hx - q"),                       # ridge dropped from A
+]
+
+
+@pytest.mark.parametrize("old,new", _MUTANTS)
+def test_planted_chebyshev_mistakes_fail(old, new):
+    import inspect
+    import textwrap
+    src = textwrap.dedent(inspect.getsource(ref.chebyshev))
+    assert src.count(old) == 1, old
+    ns = {"torch": torch}
+    exec(compile(src.replace(old, new), "<mutant>", "exec"), ns)
+    mutant = ns["chebyshev"]
+    Qm, mu = _spectra(3)[0]
+    H = Qm @ torch.diag(mu) @ Qm.T
+    q = torch.randn(16, generator=torch.Generator().manual_seed(5), dtype=D64)
+    want = _cheb_residual(Qm, mu, q, 0.01, 8)
+    x, _ = mutant(H, q, 0.01, 8)
+    assert (x - want).norm() / want.norm() > 1e-3, (old, new)
+    x_ok, _ = ref.chebyshev(H, q, 0.01, 8)
+    assert (x_ok - want).norm() / want.norm() < 1e-12
