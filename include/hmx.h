@@ -127,7 +127,8 @@ int hmx_gdn_gating(const void* A_log, int32_t A_log_dtype,
  *  Sequences: cu_seqlens [N+1] (varlen, B == 1) or N = B sequences of T tokens.
  *  Initial state of sequence n: row ssm_state_indices[n*idx_stride + c] with
  *    c = num_accepted_tokens[n]-1 (or 0), or row bos_n without indices.
- *  Final state: row ssm_state_indices[n*idx_stride] when inplace, else row n.
+ *  Final state: row ssm_state_indices[n*idx_stride] when inplace, else row bos_n
+ *    (fused_recurrent_gqa.py:137-139 stores the non-inplace state at the sequence's bos).
  *  Zero-length sequences and negative slot indices are skipped.
  *  Supported: K in {64,128,256}; V a multiple of 32, <= 256.
  * Replaces: fused_recurrent_gated_delta_rule_gqa
