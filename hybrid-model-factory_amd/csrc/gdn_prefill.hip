@@ -1295,9 +1295,13 @@ struct Bwd {
   int max_warm;               // warm-up blocks a chain run may add past its end
   float decay_thresh;         // ... to bring the dropped history under e^-decay_thresh
   int* cplan;                 // [nseg][H]: where a run's chain starts (its warm-up end), or -1
-  float* cR;                  // [nseg][H][D][D] exact runs: the chain from zero over the run
-  float* cPsi;                // [nseg][H][D][D] ... and the product of its transposed transitions
-  float* cstart;              // [nseg][H][D][D] ... and the exact dS at the run's end
+  // Exact runs, compact over the runs that need them (rows grouped by ascending
+  // sequence, each sequence's runs tiling its blocks in order; row s of sequence n):
+  float* cR;                  // [nseg-N][H][D][D] at s-n-1, runs after a sequence's first:
+                              //   the chain from zero over the run
+  float* cPsi;                // [nseg-N][H][D][D] ... and the product of its transposed transitions
+  float* cstart;              // [nseg-N][H][D][D] at s-n, runs before a sequence's last:
+                              //   the exact dS at the run's end
   bf16* dq; bf16* dk; bf16* dv;   // [tokens][H][D]
   float* dg; float* dbeta;        // [tokens][H]
   float* dh0;                 // [N][H][D][D] or null
@@ -1500,22 +1504,23 @@ __device__ __forceinline__ void chain_load(const Bwd& p, ChainPre& r, int cb, in
 
 enum ChainMode { CH_WALK = 0, CH_R = 1, CH_PSI = 2 };
 
-// The rows of the chain-run table that belong to sequence n (they are grouped by
-// sequence): [first, end), 64 rows per load round.
-__device__ __forceinline__ void seq_runs(const Bwd& p, int n, int lane, int& r0, int& r1) {
-  r0 = -1;
-  r1 = p.nseg;
-  for (int s0 = 0; s0 < p.nseg; s0 += 64) {
-    const int s = s0 + lane;
-    const int m = s < p.nseg ? p.cseg[s * 3] : 0x7fffffff;
-    const unsigned long long a = __ballot(m == n), b = __ballot(m > n);
-    if (r0 < 0 && a) r0 = s0 + __builtin_ctzll(a);
-    if (b) {
-      r1 = s0 + __builtin_ctzll(b);
-      break;
-    }
+// The first chain-run row whose sequence is >= n (rows are grouped by ascending
+// sequence): a wave-uniform binary search, log2(nseg) dependent loads.
+__device__ __forceinline__ int seq_lower_bound(const Bwd& p, int n) {
+  int lo = 0, hi = p.nseg;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (p.cseg[mid * 3] < n) lo = mid + 1;
+    else hi = mid;
   }
-  if (r0 < 0) r0 = r1;
+  return lo;
+}
+
+// The rows of the chain-run table that belong to sequence n: [r0, r1).
+__device__ __forceinline__ void seq_runs(const Bwd& p, int n, int lane, int& r0, int& r1) {
+  (void)lane;
+  r0 = seq_lower_bound(p, n);
+  r1 = seq_lower_bound(p, n + 1);
 }
 
 // Whether any run of sequence n needs the exact combine for head h (wave-uniform).
@@ -1606,12 +1611,15 @@ __global__ __launch_bounds__(BNTHR, 1) void gdn_bwd_combine_kernel(Bwd p) {
 #pragma unroll
     for (int v = 0; v < 4; ++v) X[rt][v] = src ? src[(16 * rt + 4 * q4 + v) * D + c0 + l16] : 0.f;
   for (int r = r1 - 1; r >= r0; --r) {
-    const int64_t o = ((int64_t)r * p.H + h) * DD;
+    if (r < r1 - 1) {   // the last run starts from dht itself
+      const int64_t os = ((int64_t)(r - n) * p.H + h) * DD;
 #pragma unroll
-    for (int rt = 0; rt < 8; ++rt)
+      for (int rt = 0; rt < 8; ++rt)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) p.cstart[o + (16 * rt + 4 * q4 + v) * D + c0 + l16] = X[rt][v];
+        for (int v = 0; v < 4; ++v) p.cstart[os + (16 * rt + 4 * q4 + v) * D + c0 + l16] = X[rt][v];
+    }
     if (r == r0) break;
+    const int64_t o = ((int64_t)(r - n - 1) * p.H + h) * DD;
     lds_barrier();   // the previous run's Psi reads are done
     for (int e = tid * 8; e < D * D; e += BNTHR * 8) {   // Psi_r into LDS, fp16, interleaved
       float f[8];
@@ -1684,7 +1692,7 @@ __global__ __launch_bounds__(BNTHR, 3) void gdn_bwd_chain_kernel(Bwd p, int mode
   if (mode == CH_WALK) {
     if (hexact) {
       wend = bb;
-      if (bb < last) src = p.cstart + ((int64_t)sg * p.H + h) * DD;
+      if (bb < last) src = p.cstart + ((int64_t)(sg - n) * p.H + h) * DD;
     }
     if (wend == last && p.dht) src = p.dht + ((int64_t)n * p.H + h) * DD;
   } else {           // pre-pass of an exact head's run: R from zero, Psi from I
@@ -1785,7 +1793,7 @@ __global__ __launch_bounds__(BNTHR, 3) void gdn_bwd_chain_kernel(Bwd p, int mode
     }
   }
   if (mode != CH_WALK) {   // the run's R or Psi
-    float* dst = (mode == CH_R ? p.cR : p.cPsi) + ((int64_t)sg * p.H + h) * DD + c0 + l16;
+    float* dst = (mode == CH_R ? p.cR : p.cPsi) + ((int64_t)(sg - n - 1) * p.H + h) * DD + c0 + l16;
 #pragma unroll
     for (int rt = 0; rt < 8; ++rt)
 #pragma unroll
@@ -2204,11 +2212,15 @@ extern "C" int hmx_gdn_train_fwd(const void* q, int64_t q_token_stride, const vo
 }
 
 extern "C" size_t hmx_gdn_train_bwd_workspace_bytes(int32_t nblock_total,
-                                                    int32_t nchain_segments, int32_t H) {
+                                                    int32_t nchain_segments, int32_t N,
+                                                    int32_t H) {
   // dS per block (fp16 D x D), T and P per block (fp16 C x C each); per chain run
-  // the plan entry and R, Psi and the exact start (fp32 D x D each)
+  // the plan entry; per run beyond a sequence's first, R, Psi and an exact start
+  // (fp32 D x D each): nothing for sequences walked as one run
+  const size_t extra = nchain_segments > N ? (size_t)(nchain_segments - N) : 0;
   return (size_t)nblock_total * H * ((size_t)D * D + 2 * C * C) * sizeof(f16) +
-         (size_t)nchain_segments * H * (sizeof(int) + 3 * (size_t)D * D * sizeof(float)) + 256;
+         (size_t)nchain_segments * H * sizeof(int) +
+         extra * H * 3 * (size_t)D * D * sizeof(float) + 256;
 }
 
 extern "C" int hmx_gdn_train_bwd(const void* q, int64_t q_token_stride, const void* k,
@@ -2235,7 +2247,7 @@ extern "C" int hmx_gdn_train_bwd(const void* q, int64_t q_token_stride, const vo
                   ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)dout |
                    (uintptr_t)block_states) % 16 == 0,
               HMX_EINVAL, "hmx_gdn_train_bwd: rows must be 16-byte aligned");
-  const size_t need = hmx_gdn_train_bwd_workspace_bytes(nblock_total, nchain_segments, H);
+  const size_t need = hmx_gdn_train_bwd_workspace_bytes(nblock_total, nchain_segments, N, H);
   HMX_REQUIRE(workspace && workspace_bytes >= need && (uintptr_t)workspace % 16 == 0, HMX_EINVAL,
               "hmx_gdn_train_bwd: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
   Bwd p;
@@ -2251,7 +2263,7 @@ extern "C" int hmx_gdn_train_bwd(const void* q, int64_t q_token_stride, const vo
   p.tm = ws + (size_t)nblock_total * H * D * D;
   p.pm = p.tm + (size_t)nblock_total * H * C * C;
   {
-    const size_t runs_hd = (size_t)nchain_segments * H * D * D;
+    const size_t runs_hd = (size_t)(nchain_segments - N) * H * D * D;
     char* tail = reinterpret_cast<char*>(p.pm + (size_t)nblock_total * H * C * C);
     tail += (256 - reinterpret_cast<uintptr_t>(tail) % 256) % 256;
     p.cR = reinterpret_cast<float*>(tail);

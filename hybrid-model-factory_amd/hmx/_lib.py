@@ -76,7 +76,7 @@ SIGNATURES: dict[str, list] = {
     "hmx_gdn_train_bwd": [_P, _I64, _P, _P, _I64, _P, _I32, _P, _I32, _P, _I64, _P, _P, _P, _P,
                           _I32, _I32, _P, _I32, _I32, _F32, _I32, _F32, _I32, _P, _P, _P, _P,
                           _P, _P, _P, ctypes.c_size_t, _P],
-    "hmx_gdn_train_bwd_workspace_bytes": [_I32, _I32, _I32],
+    "hmx_gdn_train_bwd_workspace_bytes": [_I32, _I32, _I32, _I32],
     "hmx_plan_segments": [_I32, _P, _I32, _I32, _I64, _I32, _I32, _I32, _P, _I32, _P, _P],
     "hmx_plan_segments_bounds": [_I32, _P, _I32, _I64, _I32, _I32, _I32, _P, _I32, _P, _P],
     "hmx_ssd_chunk_fwd": [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I32,

@@ -57,6 +57,29 @@ def chain_segments(cu_blocks: np.ndarray, H: int, cu_count: int, seg_blocks: int
     return np.asarray(rows, dtype=np.int32).reshape(-1, 3)
 
 
+def check_chain_segments(cseg: np.ndarray, cu_blocks: np.ndarray) -> None:
+    """Raise ValueError unless the chain-run rows are in the order hmx_gdn_train_bwd
+    requires: grouped by ascending sequence 0..N-1, every sequence with at least one
+    row, and each sequence's rows tiling its blocks [cu[n], cu[n+1]) in ascending
+    order (an empty sequence has the one row (n, cu[n], cu[n]))."""
+    cseg = np.asarray(cseg).reshape(-1, 3)
+    N = len(cu_blocks) - 1
+    n, a, e = cseg[:, 0].astype(np.int64), cseg[:, 1].astype(np.int64), cseg[:, 2].astype(np.int64)
+    if len(n) < N or (len(n) and (n[0] != 0 or n[-1] != N - 1)) or np.any(np.diff(n) < 0) \
+            or np.any(np.diff(n) > 1):
+        raise ValueError("chain_segments: rows must be grouped by ascending sequence, "
+                         "every sequence with at least one row")
+    first = np.r_[True, n[1:] != n[:-1]]
+    last = np.r_[n[1:] != n[:-1], True]
+    cu = np.asarray(cu_blocks, dtype=np.int64)
+    ok = (np.all(a[first] == cu[n[first]]) and np.all(e[last] == cu[n[last] + 1])
+          and np.all(a[~first] == e[np.flatnonzero(~first) - 1]) and np.all(e >= a)
+          and np.all((e > a) | (first & last)))
+    if not ok:
+        raise ValueError("chain_segments: each sequence's rows must tile its blocks in "
+                         "ascending order")
+
+
 def _check(q, k, v, g, beta):
     if q.dim() != 4 or k.shape != q.shape or v.shape != q.shape:
         raise ValueError(f"q, k, v must be [B, T, H, D] alike (k, v expanded to H heads), got "
@@ -121,6 +144,7 @@ def chunk_backward(q, k, v, g, beta, scale, h0, do, dht, bounds, l2norm, segment
                                                    segment_chunks)
     nblk = rows_np.shape[0]
     cseg_np = chain_segments(cu_np, H, _cu_count(q.device), segment_chunks)
+    check_chain_segments(cseg_np, cu_np)
     cseg = _device_table(cseg_np, q.device)
     covered = sum(e - b for b, e in bounds) == B * T
     alloc = torch.empty if covered else torch.zeros
@@ -131,7 +155,8 @@ def chunk_backward(q, k, v, g, beta, scale, h0, do, dht, bounds, l2norm, segment
     if dht is not None:
         dht = dht.to(torch.float32).contiguous()
     lib = _lib.load()
-    ws = torch.empty(max(int(lib.hmx_gdn_train_bwd_workspace_bytes(nblk, cseg_np.shape[0], H)), 16),
+    ws = torch.empty(max(int(lib.hmx_gdn_train_bwd_workspace_bytes(nblk, cseg_np.shape[0], N, H)),
+                         16),
                      dtype=torch.uint8, device=q.device)
     (q, q_ts), (k, kv_ts), (v, _), (do, do_ts) = _rows(q), _rows(k), _rows(v), _rows(do)
     _lib.call("hmx_gdn_train_bwd",

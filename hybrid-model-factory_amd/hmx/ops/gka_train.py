@@ -168,6 +168,9 @@ class GkaChebyshevGla(torch.autograd.Function):
                   _lib.ptr(seg), len(rows), nblk, B, H, D, n, float(ridge_strength),
                   float(gla_scale), _lib.ptr(ws), ws.numel(), _lib.stream_of(q2))
         ctx.save_for_backward(q2, k2, v2, a2, g2, gk2, x, fro, ws, seg)
+        # unused outputs give None gradients, so a loss that does use a final state is
+        # told apart from one that does not (see backward)
+        ctx.set_materialize_grads(False)
         ctx.meta = (len(rows), nblk, n, float(ridge_strength), float(gla_scale), bool(bp_lambda),
                     (q.dtype, k.dtype, v.dtype, alpha.dtype, g.dtype,
                      None if gk is None else gk.dtype))
@@ -175,6 +178,14 @@ class GkaChebyshevGla(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, do, d_kk=None, d_kv=None):
+        # d_kk is dropped, as the reference's ChebyshevIteration.backward drops
+        # d_kk_final (chebyshev_iteration.py:606-688).  fla's chunk_simple_gla
+        # (gka_chebyshev_solve.py:159) would carry d_kv into the readout's reverse
+        # scan; these kernels seed that scan with zero only, so refuse it.
+        if d_kv is not None:
+            raise NotImplementedError("hmx gka_chebyshev_gla backward: the gradient of the "
+                                      "final state kv_final is not supported; use the output o "
+                                      "in the loss")
         q, k, v, alpha, g, gk, x, fro, ws, seg = ctx.saved_tensors
         nrows, nblk, n, ridge, scale, bp_lambda, dts = ctx.meta
         B, T, H, D = q.shape

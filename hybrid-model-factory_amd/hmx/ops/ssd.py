@@ -227,7 +227,7 @@ def mamba_chunk_scan_combined(x, dt, A, B, C, chunk_size, D=None, z=None, dt_bia
             if (0, cs[i + 1]) not in end_at or cs[i + 1] == cs[i]:
                 raise ValueError("cu_seqlens boundaries must coincide with the scan's sequences")
             idx.append(end_at[(0, cs[i + 1])])
-        out.append(hT[torch.tensor(idx, device=x.device)])
+        out.append(hT.index_select(0, _device_table(idx, x.device)))
     return out[0] if len(out) == 1 else tuple(out)
 
 
@@ -302,26 +302,27 @@ def mamba_chunk_scan_combined_varlen(x, dt, A, B, C, chunk_size, cu_seqlens, cu_
     if return_intermediate_states:
         if cu_chunk_seqlens is None or seq_idx is None:
             raise ValueError("return_intermediate_states needs cu_chunk_seqlens and seq_idx")
+        # host metadata (vLLM's CPU copies) is read without a device sync
         cc = [int(v) for v in cu_chunk_seqlens.tolist()]
         cs_seq = [int(v) for v in seq_idx.reshape(-1).tolist()]
         rows = _chunk_rows(cc, cs_seq, bounds)
-        hT, starts = _ssd_scan(x, dt, A, B, C, D, z, dt_bias, dt_softplus, dt_limit, bounds, h0,
-                               out, True, None, pooled, seg_rows=rows)
-        # the state after chunk c: the next chunk's start state, or its sequence's end state
         nch = len(rows)
-        states = torch.empty(nch, H, P, N, dtype=torch.float32, device=x.device)
         last = [i for i, r in enumerate(rows) if r[5] == r[7] - 1]
-        mid = [i for i, r in enumerate(rows) if r[5] < r[7] - 1]
-        if mid:
-            ti = lambda v: torch.tensor(v, dtype=torch.int64, device=x.device)
-            states[ti(mid)] = starts[ti([i + 1 for i in mid])]
-        if last:
-            ti = lambda v: torch.tensor(v, dtype=torch.int64, device=x.device)
-            seqs = ti([rows[i][0] for i in last])
-            fin = hT[pooled[1].long()[seqs]] if pooled is not None else hT[seqs]
-            states[ti(last)] = fin.to(torch.float32)
+        # checked before the scan writes out and the caller's pool
         if last_chunk_indices is not None and [int(v) for v in last_chunk_indices.tolist()] != last:
             raise ValueError("last_chunk_indices must index each sequence's last chunk")
+        hT, starts = _ssd_scan(x, dt, A, B, C, D, z, dt_bias, dt_softplus, dt_limit, bounds, h0,
+                               out, True, None, pooled, seg_rows=rows)
+        # the state after chunk c: the next chunk's start state, or its sequence's end
+        # state; one gather over [starts; end states] with a host-built index
+        # (advanced indexing: a negative pad slot wraps around instead of faulting;
+        # such a sequence has no state in the pool, so its returned rows mean nothing)
+        fin = (hT[pooled[1].long()] if pooled is not None else hT).to(torch.float32)
+        src = fin if starts is None else torch.cat([starts, fin])
+        nst = 0 if starts is None else starts.shape[0]
+        gidx = [nst + r[0] if r[5] == r[7] - 1 else i + 1 for i, r in enumerate(rows)]
+        states = src.index_select(0, _device_table(gidx, x.device)) if nch else \
+            src.new_empty(0, H, P, N)
         return states if state_dtype in (None, torch.float32) else states.to(state_dtype)
     hT = _ssd_scan(x, dt, A, B, C, D, z, dt_bias, dt_softplus, dt_limit, bounds, h0, out, True,
                    _segment_chunks, pooled)

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define HMX_ABI_VERSION 7  /* 2: optional hmx_gated_norm output epilogue in the GDN ops;
+#define HMX_ABI_VERSION 8  /* 2: optional hmx_gated_norm output epilogue in the GDN ops;
                               3: q/k/v token strides in the GDN and GKA ops; slot-indexed
                               state pools and has_initial_state in the GDN, GKA and SSD
                               prefills;
@@ -34,7 +34,10 @@ extern "C" {
                               5: nblock_total in hmx_gka_chunk_fwd and its workspace size;
                               6: host segment planner hmx_plan_segments(_bounds);
                               7: gates from raw projections (hmx_gate_proj) in the GDN and
-                                 GKA prefill / decode entry points */
+                                 GKA prefill / decode entry points;
+                              8: N in hmx_gdn_train_bwd_workspace_bytes (the exact-run
+                                 buffers are sized by the runs beyond each sequence's
+                                 first) */
 
 enum hmx_status {
   HMX_OK = 0,
@@ -285,8 +288,12 @@ int hmx_gdn_train_fwd(const void* q, int64_t q_token_stride, const void* k, cons
  * [nblock_total][4] = (first token, tokens (1-32), sequence, block index within
  * the sequence); cu_blocks [N+1].  chain_segments int32 [nchain_segments][3] =
  * (sequence, first block, end block) cuts every sequence's blocks into runs that
- * one workgroup each walks backward (every sequence needs at least one row, an
- * empty one for a sequence without tokens); a run that ends before its sequence
+ * one workgroup each walks backward.  Required order (not checked here; the Python
+ * wrapper checks it on the host): rows grouped by ascending sequence 0..N-1, every
+ * sequence with at least one row (one empty row (n, b, b) for a sequence without
+ * tokens), and each sequence's rows tiling its blocks [cu_blocks[n], cu_blocks[n+1])
+ * in ascending order with no gap or overlap; another order gives wrong gradients
+ * for heads on the exact combine, with no error.  A run that ends before its sequence
  * starts from zero after a warm-up of up to max_warm_blocks following blocks whose
  * gates bring the dropped history under e^-decay_threshold; a head with a run that
  * finds no such warm-up takes every run's exact start from a combine over the runs
@@ -294,7 +301,7 @@ int hmx_gdn_train_fwd(const void* q, int64_t q_token_stride, const void* k, cons
  * dk, dv [tokens][H][128] bf16 (rows
  * of the blocks' tokens only), dg and dbeta [tokens][H] fp32, and dh0 (the
  * gradient of the initial states, fp32 [N][H][128][128]) when not null.
- * workspace: hmx_gdn_train_bwd_workspace_bytes(nblock_total, nchain_segments, H) bytes.
+ * workspace: hmx_gdn_train_bwd_workspace_bytes(nblock_total, nchain_segments, N, H) bytes.
  * Replaces: the backward of fla's chunk_gated_delta_rule (un-vendored; the training
  *   layer's call at training/src/hmf/model/hybrid_zoo/layers/gated_deltanet/gdn.py:
  *   462-476, whose torch fallback is the recurrence of
@@ -310,7 +317,7 @@ int hmx_gdn_train_bwd(const void* q, int64_t q_token_stride, const void* k, cons
                       int32_t use_qk_l2norm, void* dq, void* dk, void* dv, float* dg,
                       float* dbeta, float* dh0, void* workspace, size_t workspace_bytes,
                       void* stream);
-size_t hmx_gdn_train_bwd_workspace_bytes(int32_t nblock_total, int32_t nchain_segments,
+size_t hmx_gdn_train_bwd_workspace_bytes(int32_t nblock_total, int32_t nchain_segments, int32_t N,
                                          int32_t H);
 
 /*

@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 from hmx import _lib
-from hmx.ops.gdn_train import block_table, chain_segments
+from hmx.ops.gdn_train import block_table, chain_segments, check_chain_segments
 
 
 BOUNDS = [(0, 200), (200, 200), (200, 201), (201, 2249), (2249, 2281)]
@@ -72,9 +72,58 @@ def test_train_bwd_rejects_bad_arguments():
     assert lib.hmx_gdn_train_bwd(*_bwd_args(**ptrs, q_ts=1001)) == _lib.HMX_EINVAL
     assert b"16-byte aligned" in lib.hmx_last_error()
     assert lib.hmx_gdn_train_bwd(*_bwd_args(**ptrs)) == _lib.HMX_EINVAL   # no workspace
-    need = lib.hmx_gdn_train_bwd_workspace_bytes(1, 1, 8)
+    need = lib.hmx_gdn_train_bwd_workspace_bytes(1, 1, 1, 8)
     assert b"workspace of %d bytes" % need in lib.hmx_last_error()
-    assert need == 8 * (128 * 128 + 2 * 32 * 32) * 2 + 8 * (4 + 3 * 128 * 128 * 4) + 256
+    # one sequence walked as one run: no exact-run buffers
+    assert need == 8 * (128 * 128 + 2 * 32 * 32) * 2 + 8 * 4 + 256
+
+
+@pytest.mark.parametrize("nseq", [320, 2048])
+def test_bwd_workspace_single_run_sequences_cost_no_exact_buffers(nseq):
+    """Packed training batches of many short sequences (32768 tokens, H = 32, 256
+    CUs): every sequence is one run, so the workspace is the per-block part plus one
+    int per run and head; the R / Psi / exact-start buffers (3 x 64 KiB per run and
+    head) are sized by the runs beyond each sequence's first only."""
+    lib = _lib.load()
+    T, H = 32768, 32
+    L = T // nseq
+    bounds = [(i * L, (i + 1) * L) for i in range(nseq)]
+    rows, cu = block_table(bounds)
+    runs = chain_segments(cu, H, 256)
+    check_chain_segments(runs, cu)
+    assert len(runs) == nseq
+    nblk = rows.shape[0]
+    base = nblk * H * (128 * 128 + 2 * 32 * 32) * 2 + len(runs) * H * 4 + 256
+    assert lib.hmx_gdn_train_bwd_workspace_bytes(nblk, len(runs), nseq, H) == base
+    # one long sequence cut into 24 runs: 23 runs carry the exact-run buffers
+    rows1, cu1 = block_table([(0, T)])
+    runs1 = chain_segments(cu1, H, 256)
+    got = lib.hmx_gdn_train_bwd_workspace_bytes(rows1.shape[0], len(runs1), 1, H)
+    assert got == (rows1.shape[0] * H * (128 * 128 + 2 * 32 * 32) * 2 + len(runs1) * H * 4
+                   + (len(runs1) - 1) * H * 3 * 128 * 128 * 4 + 256)
+
+
+@pytest.mark.parametrize("seg", [None, 1, 3])
+def test_check_chain_segments_accepts_the_built_tables(seg):
+    _, cu = block_table(BOUNDS)
+    check_chain_segments(chain_segments(cu, H=4, cu_count=256, seg_blocks=seg), cu)
+
+
+def test_check_chain_segments_rejects_other_orders():
+    """The backward's compact exact-run indexing and its per-sequence binary search
+    need the grouped, tiling order; the host check refuses anything else."""
+    _, cu = block_table(BOUNDS)
+    good = chain_segments(cu, H=4, cu_count=256, seg_blocks=3)
+    bad = [good[::-1],                                   # sequences descending
+           np.delete(good, 0, axis=0),                   # a sequence's first run missing
+           good[[1, 0] + list(range(2, len(good)))],     # runs of a sequence swapped
+           np.delete(good, [i for i, r in enumerate(good) if r[0] == 1], axis=0)]  # empty seq
+    g2 = good.copy()
+    g2[0, 2] -= 1                                        # a gap between two runs
+    bad.append(g2)
+    for b in bad:
+        with pytest.raises(ValueError):
+            check_chain_segments(b, cu)
 
 
 def test_train_fwd_requires_block_states():

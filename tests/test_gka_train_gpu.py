@@ -178,3 +178,25 @@ def test_gka_chebyshev_gla_routes_through_autograd(dev):
     assert torch.equal(o0, o1) and torch.equal(kk0, kk1) and torch.equal(kv0, kv1)
     o1.float().sum().backward()
     assert qq.grad is not None and torch.isfinite(qq.grad.float()).all()
+
+
+def test_gka_chebyshev_gla_final_state_gradient_refused(dev):
+    """A loss that uses kv_final raises (its gradient would otherwise be dropped); a
+    loss that also uses kk_final alone is accepted, as the reference's
+    ChebyshevIteration.backward drops d_kk_final (chebyshev_iteration.py:606-688)."""
+    q, k, gk, _ = _inputs(1, 100, 2, 32, True, dev)
+    v = torch.randn(1, 100, 2, D, device=dev).bfloat16()
+    alpha = torch.rand(1, 100, 2, device=dev)
+    g = -0.1 * torch.rand(1, 100, 2, device=dev)
+    qq = q.clone().requires_grad_(True)
+    o, kk, kv = hmx.gka_chebyshev_gla(qq, k, v, alpha, g, gk, 0.3, 0.02, num_iter=4)
+    with pytest.raises(NotImplementedError):
+        (o.float().sum() + kv.sum()).backward()
+    qq.grad = None
+    o, kk, kv = hmx.gka_chebyshev_gla(qq, k, v, alpha, g, gk, 0.3, 0.02, num_iter=4)
+    (o.float().sum() + kk.sum()).backward()
+    g_kk = qq.grad.clone()
+    qq.grad = None
+    o, kk, kv = hmx.gka_chebyshev_gla(qq, k, v, alpha, g, gk, 0.3, 0.02, num_iter=4)
+    o.float().sum().backward()
+    assert torch.equal(qq.grad, g_kk)
