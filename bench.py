@@ -88,9 +88,11 @@ def bench_prefill(dev, steps, warmup, HKV=32):
     ms = _timed(step, steps, warmup)
     by = wl.gdn_prefill_bytes(T, H, HKV)
     fl = wl.gdn_prefill_flops(T, H)
+    fl32 = wl.gdn_prefill_flops(T, H, C=32)     # the same count at the kernel's 32-token chunk
     gbs = by / (ms * 1e-3) / 1e9
     tfs = fl / (ms * 1e-3) / 1e12
-    return dict(ms=ms, tokens_per_s=T / (ms * 1e-3), bytes=by, flops=fl, GBps=gbs, TFLOPs=tfs)
+    return dict(ms=ms, tokens_per_s=T / (ms * 1e-3), bytes=by, flops=fl, GBps=gbs, TFLOPs=tfs,
+                flops_c32=fl32, TFLOPs_c32=fl32 / (ms * 1e-3) / 1e12)
 
 
 def bench_prefill_layer_gates(dev, steps, warmup):
@@ -646,14 +648,45 @@ def bench_ssd_decode(dev, steps=64, warmup=4):
 
 
 def cpu_model():
-    """The host CPU's model name (as lscpu reports it), from /proc/cpuinfo."""
+    """The host CPU as lscpu reports it: model name, vendor, family / model /
+    stepping (the model name alone can be a bare "AMD EPYC" under virtualisation)."""
+    fields = {}
     try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
-    except OSError:
+        import subprocess
+        txt = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in txt.splitlines():
+            k, _, v = line.partition(":")
+            fields[k.strip()] = v.strip()
+    except (OSError, ValueError, subprocess.SubprocessError):
         pass
-    return None
+    if not fields.get("Model name"):
+        try:
+            for line in open("/proc/cpuinfo"):
+                k, _, v = line.partition(":")
+                k = {"model name": "Model name", "vendor_id": "Vendor ID",
+                     "cpu family": "CPU family", "model": "Model", "stepping": "Stepping"}.get(k.strip())
+                if k and k not in fields:
+                    fields[k] = v.strip()
+        except OSError:
+            pass
+    name = fields.get("Model name")
+    if name is None:
+        return None
+    ident = ", ".join(f"{k.lower()} {fields[k]}" for k in ("CPU family", "Model", "Stepping")
+                      if fields.get(k))
+    vend = fields.get("Vendor ID")
+    return f"{name} ({vend}{', ' if vend and ident else ''}{ident})" if (vend or ident) else name
+
+
+def _median_time(fn, reps=3):
+    """1 untimed warm-up call, then the median of ``reps`` timed calls (seconds)."""
+    fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2]
 
 
 def cpu_baseline(sample_tokens=32768):
@@ -666,22 +699,21 @@ def cpu_baseline(sample_tokens=32768):
     torch.set_num_threads(cores)
     d = wl.gdn_inputs(T=sample_tokens, H=32, HKV=32, D=128, config_id=1)
     args = [d[n] for n in ("q", "k", "v", "g", "beta")]
-    ref.chunk_gated_delta_rule_gqa(*[a[:, :256] for a in args], output_final_state=True,
-                                   use_qk_l2norm_in_kernel=True, dtype=torch.float32)
-    t0 = time.perf_counter()
-    ref.chunk_gated_delta_rule_gqa(*args, output_final_state=True, use_qk_l2norm_in_kernel=True,
-                                   dtype=torch.float32)
-    dt = time.perf_counter() - t0
+    dt = _median_time(lambda: ref.chunk_gated_delta_rule_gqa(
+        *args, output_final_state=True, use_qk_l2norm_in_kernel=True, dtype=torch.float32))
     return dict(value=sample_tokens / dt, unit="tokens/s", cores=torch.get_num_threads(),
                 cpu=cpu_model(), kind="port", sample=f"C1 {sample_tokens} tokens x 32 heads (the whole workload), "
-                f"oracle chunked form (chunk 64) in fp32 torch on CPU, {dt:.2f} s")
+                f"oracle chunked form (chunk 64) in fp32 torch on CPU, median of 3 after a warm-up: "
+                f"{dt:.2f} s")
 
 
-def cpu_baselines_more():
-    """The oracle on bounded samples of C2-C4, same host, fp32 torch on all cores:
-    C2 8 of the 512 decode steps (256 sequences x 32 heads, the 512 MiB pool), C3 the
-    whole workload at num_iter 8 (the per-token restatement, ~20 s), C4 the whole
-    workload (chunked form)."""
+def cpu_baselines_more(c3_n32_budget_s=300.0):
+    """The oracle beside C1 on every other config, same host, fp32 torch on all cores:
+    C0 whole (T=2048, H=16, chunked form) and C4 whole (chunked form), each the
+    median of 3 after a warm-up; C2 all 512 decode steps (256 sequences x 32 heads,
+    the 512 MiB pool) and C3 whole at num_iter 8 (per-token form, ~20 s), once each;
+    C3 at num_iter 32 whole if its first 4096 tokens project the whole run under
+    ``c3_n32_budget_s``, else those 4096 tokens, labelled."""
     import torch
     from hmx import workloads as wl
     from oracle import gdn as gref, gka as kref, ssd as sref
@@ -689,38 +721,65 @@ def cpu_baselines_more():
     torch.set_num_threads(cores)
     f32 = torch.float32
     out = {}
-    steps = 8
+    model = cpu_model()
+
+    def row(value, unit, sample):
+        return dict(value=value, unit=unit, cores=cores, cpu=model, kind="port", sample=sample)
+    d0 = wl.gdn_inputs(T=2048, H=16, HKV=16, D=128, dtype=f32, config_id=0)
+    a0 = [d0[n] for n in ("q", "k", "v", "g", "beta")]
+    dt = _median_time(lambda: gref.chunk_gated_delta_rule_gqa(
+        *a0, output_final_state=True, use_qk_l2norm_in_kernel=True, dtype=f32))
+    out["c0"] = row(2048 / dt, "tokens/s", f"C0 whole (2048 tokens x 16 heads, fp32 inputs), oracle "
+                    f"chunked form (chunk 64) in fp32 torch on CPU, median of 3: {dt:.3f} s")
+    steps = 512
     d = wl.decode_inputs(n_seqs=256, H=32, HKV=32, D=128, steps=steps)
     pool = d["pool"].clone()
     t0 = time.perf_counter()
     for s in range(steps):
-        gref.fused_recurrent_gated_delta_rule_gqa(
+        _, pool = gref.fused_recurrent_gated_delta_rule_gqa(
             d["q"][s], d["k"][s], d["v"][s], d["g"][s], d["beta"][s], initial_state=pool,
             inplace_final_state=True, cu_seqlens=d["cu_seqlens"], ssm_state_indices=d["idx"],
             use_qk_l2norm_in_kernel=True, dtype=f32)
     dt = time.perf_counter() - t0
-    out["decode"] = dict(value=steps / dt, unit="steps/s", cores=cores, cpu=cpu_model(), kind="port",
-                         sample=f"C2 {steps} of 512 steps (256 seqs x 32 heads), oracle "
-                                f"recurrence in fp32 torch on CPU, {dt:.2f} s")
+    del d, pool
+    out["decode"] = row(steps / dt, "steps/s", f"C2 all {steps} steps (256 seqs x 32 heads, the "
+                        f"state carried step to step), oracle recurrence in fp32 torch on CPU, "
+                        f"{dt:.2f} s")
     T = 32768
     g = wl.gka_inputs(T=T, H=32, HKV=32, D=128)
+    ga = [g[n] for n in ("q", "k", "v", "alpha", "g", "gk", "beta")]
+
+    def gka(n, t):
+        return kref.gka_chebyshev_gla_prefill(*[a[:, :t] for a in ga], 128 ** -0.5,
+                                              ridge_ratio=0.01, num_iter=n, dtype=f32)
     t0 = time.perf_counter()
-    kref.gka_chebyshev_gla_prefill(g["q"], g["k"], g["v"], g["alpha"], g["g"], g["gk"],
-                                   g["beta"], 128 ** -0.5, ridge_ratio=0.01, num_iter=8,
-                                   dtype=f32)
+    gka(8, T)
     dt = time.perf_counter() - t0
-    out["gka_num_iter_8"] = dict(value=T / dt, unit="tokens/s", cores=cores, cpu=cpu_model(), kind="port",
-                                 sample=f"C3 whole workload ({T} tokens x 32 heads), num_iter 8, "
-                                        f"oracle per-token form in fp32 torch on CPU, {dt:.2f} s")
+    out["gka_num_iter_8"] = row(T / dt, "tokens/s", f"C3 whole workload ({T} tokens x 32 heads), "
+                                f"num_iter 8, oracle per-token form in fp32 torch on CPU, {dt:.2f} s")
+    t_part = 4096
+    t0 = time.perf_counter()
+    gka(32, t_part)
+    dt = time.perf_counter() - t0
+    if dt * T / t_part < c3_n32_budget_s:
+        t0 = time.perf_counter()
+        gka(32, T)
+        dt = time.perf_counter() - t0
+        out["gka_num_iter_32"] = row(T / dt, "tokens/s", f"C3 whole workload ({T} tokens x 32 "
+                                     f"heads), num_iter 32, oracle per-token form in fp32 torch "
+                                     f"on CPU, {dt:.2f} s")
+    else:
+        out["gka_num_iter_32"] = row(t_part / dt, "tokens/s", f"C3 FIRST {t_part} TOKENS ONLY x 32 "
+                                     f"heads (the whole run projects past {c3_n32_budget_s:.0f} "
+                                     f"s), num_iter 32, oracle per-token form in fp32 torch on "
+                                     f"CPU, {dt:.2f} s")
+    del g, ga
     x = wl.ssd_inputs()
-    t0 = time.perf_counter()
-    sref.mamba_chunk_scan_combined(x["x"], x["dt"], x["A"], x["B"], x["C"], 256, D=x["D"],
-                                   dt_bias=x["dt_bias"], dt_softplus=True,
-                                   return_final_states=True, dtype=f32)
-    dt = time.perf_counter() - t0
-    out["ssd"] = dict(value=2 * 16384 / dt, unit="tokens/s", cores=cores, cpu=cpu_model(), kind="port",
-                      sample=f"C4 whole workload (2 x 16384 tokens x 64 heads), oracle chunked "
-                             f"form in fp32 torch on CPU, {dt:.2f} s")
+    dt = _median_time(lambda: sref.mamba_chunk_scan_combined(
+        x["x"], x["dt"], x["A"], x["B"], x["C"], 256, D=x["D"], dt_bias=x["dt_bias"],
+        dt_softplus=True, return_final_states=True, dtype=f32))
+    out["ssd"] = row(2 * 16384 / dt, "tokens/s", f"C4 whole workload (2 x 16384 tokens x 64 "
+                     f"heads), oracle chunked form in fp32 torch on CPU, median of 3: {dt:.2f} s")
     return out
 
 
@@ -844,6 +903,9 @@ def main():
                          "algorithmic_bytes": pf["bytes"],
                          "mfma_TFLOPs": round(pf["TFLOPs"], 1),
                          "mfma_frac": round(pf["TFLOPs"] / BF16_PEAK_TFLOPS, 4),
+                         "mfma_flops_basis": "2 T H (5 C d + 3 d^2) at C = 64: 188.98 GFLOP",
+                         "mfma_frac_chunk32": round(pf["TFLOPs_c32"] / BF16_PEAK_TFLOPS, 4),
+                         "mfma_flops_chunk32": pf["flops_c32"],
                          "mfma_busy_counter": measured_mfma_busy("gdn_prefill_c1")},
         })
     if "prefill_gqa" in out:

@@ -158,6 +158,34 @@ def test_decode_c2_shape_steps(dev):
     assert_state_close(pool_d, pool_ref)
 
 
+def test_decode_c2_all_512_steps_slice(dev):
+    """C2 over its whole run: 512 consecutive in-place steps of the full 256-sequence
+    x 32-head batch (randperm slots), with sequences 0-15 (all 32 heads, their 16
+    random slots) checked at every step against the fp64 recurrence: every step's
+    output and, at the end, their 16 slots; the other 240 slots against the GPU's own
+    run are covered by the 3-step full-batch test above."""
+    steps, ns = 512, 16
+    d = wl.decode_inputs(n_seqs=256, H=32, HKV=32, D=128, steps=steps, device=dev,
+                         gen_device=dev)
+    pool_d = d["pool"]
+    slots = d["idx"][:ns].long()
+    pool_ref = pool_d[slots].double().cpu()          # the slice's slots, compact
+    idx_ref = torch.arange(ns, dtype=torch.int32)
+    cu_ref = torch.arange(ns + 1, dtype=torch.int32)
+    for s in range(steps):
+        args = [d[n][s] for n in ("q", "k", "v", "g", "beta")]
+        o, _ = hmx.fused_recurrent_gated_delta_rule_gqa(
+            *args, initial_state=pool_d, inplace_final_state=True, cu_seqlens=d["cu_seqlens"],
+            ssm_state_indices=d["idx"], use_qk_l2norm_in_kernel=True)
+        sl = [a[:, :ns].cpu() for a in args]
+        o_ref, pool_ref = ref.fused_recurrent_gated_delta_rule_gqa(
+            *sl, initial_state=pool_ref, inplace_final_state=True, cu_seqlens=cu_ref,
+            ssm_state_indices=idx_ref, use_qk_l2norm_in_kernel=True)
+        assert_out_close(o[:, :ns], o_ref, what=f"o step {s}")
+    torch.cuda.synchronize()
+    assert_state_close(pool_d[slots], pool_ref, what="the slice's slots after 512 steps")
+
+
 def test_fla_style_fused_recurrent(dev):
     B, T, H, K, V = 2, 5, 2, 128, 128
     q, k, v, g, beta, gen = _mk(B * T, H, H, K, V, torch.bfloat16, 5)

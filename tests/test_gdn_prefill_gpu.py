@@ -202,6 +202,40 @@ def test_prefill_c1_varlen(dev):
     _check(dev, *(d[n] for n in ("q", "k", "v", "g", "beta")), cu=cu)
 
 
+def test_prefill_c1_varlen_h32(dev):
+    """C1-varlen at its real head count (8 sequences of randint(1024, 8193) tokens,
+    H = 32, zero initial states): the planner's H = 32 segment table.  All heads vs
+    the GPU recurrent kernel per sequence (a pool slot each); heads 0-3 vs the fp64
+    oracle, outputs and every sequence's final state."""
+    from hmx import _lib
+    from hmx.ops import gdn as gops
+    lens = wl.varlen_lengths()
+    cu = wl.cu_from_lengths(lens)
+    T, H, N = int(cu[-1]), 32, len(lens)
+    d = wl.gdn_inputs(T=T, H=H, HKV=H, D=128, config_id=1)
+    q, k, v, g, beta = (d[n] for n in ("q", "k", "v", "g", "beta"))
+    bounds = [(int(cu[i]), int(cu[i + 1])) for i in range(N)]
+    rows, _ = gops._segment_table(_lib.PLAN_GDN, bounds, T, H, torch.device(dev))
+    assert len(rows) > N, "the H = 32 plan is expected to split the sequences"
+    h0 = torch.zeros(N, H, 128, 128)
+    o, s = _run(dev, q, k, v, g, beta, h0=h0, cu=cu)
+    pool = torch.zeros(N, H, 128, 128, device=dev)
+    o_r, _ = hmx.fused_recurrent_gated_delta_rule_gqa(
+        *[x.to(dev) for x in (q, k, v, g, beta)], initial_state=pool, inplace_final_state=True,
+        cu_seqlens=cu.to(dev), ssm_state_indices=torch.arange(N, dtype=torch.int32, device=dev),
+        use_qk_l2norm_in_kernel=True)
+    torch.cuda.synchronize()
+    assert_out_close(o, o_r.float(), what="varlen H=32 chunked vs recurrent o")
+    assert_state_close(s, pool, what="varlen H=32 chunked vs recurrent states")
+    hs = 4
+    o_ref, s_ref = ref.chunk_gated_delta_rule_gqa(
+        q[:, :, :hs], k[:, :, :hs], v[:, :, :hs], g[:, :, :hs], beta[:, :, :hs],
+        initial_state=h0[:, :hs], output_final_state=True, cu_seqlens=cu,
+        use_qk_l2norm_in_kernel=True)
+    assert_out_close(o[:, :, :hs], o_ref, what="varlen H=32 o, heads 0-3 vs oracle")
+    assert_state_close(s[:, :hs], s_ref, what="varlen H=32 final states, heads 0-3 vs oracle")
+
+
 def test_c0_exact_shape(dev):
     """C0 at its exact shape (B=1, T=2048, H=16, d=128, fp32 inputs, zero initial
     state, in-kernel L2 norm): the fp32 inputs through the fp32 recurrent kernel and
