@@ -73,6 +73,12 @@ constexpr int NTHR = 256;      // 4 waves
 // rows (ds_read_b64_tr_b16) bank-conflict-free.  k and q are staged in the
 // interleaved feature order (icol), so every k / q operand is one 128-bit read.
 constexpr int LDQ = D + 16;
+// O staging row stride: 68 dwords (4 mod 64 banks).  The O tile is written as
+// 8-byte pieces (4 features of one token per lane), conflict-free for the
+// 16-lane groups that a 64-bit write serves together (rows 4 banks apart), and
+// read back by rows r and r + 16 per half-wave (68 * 16 = 64 mod 128 dwords),
+// which a 128-bit read serves together.
+constexpr int LDO = D + 8;
 constexpr int LDT = C + 8;     // [C][C] row stride (P, T blocks)
 static_assert(C == 32, "chunk length: the substitution and the g scan are written for 32");
 
@@ -86,8 +92,9 @@ constexpr int SZ_Q = C * LDQ * 2;
 constexpr int SZ_SC = 4 * C * 4;                 // per-token scalars (see Stage)
 constexpr int SZ_BUF = 3 * SZ_Q + SZ_SC;
 constexpr int SZ_P = C * LDT * 2;
+constexpr int SZ_O = C * LDO * 2;
 constexpr int OFF_O = 2 * SZ_BUF;
-constexpr int OFF_T = OFF_O + SZ_Q;    // rows 0-15: T'_00 | rows 16-31: -M_10, T'_11 (fp16)
+constexpr int OFF_T = OFF_O + SZ_O;    // rows 0-15: T'_00 | rows 16-31: -M_10, T'_11 (fp16)
 constexpr int OFF_P = OFF_T + SZ_P;    // P (fp16, lower triangle; the upper tile stays 0)
 constexpr int OFF_NW = OFF_P + SZ_P;   // fp32 [D] output-norm weight (NORM)
 constexpr int SMEM = OFF_NW + D * 4;
@@ -237,22 +244,50 @@ struct RawChunk {
   float gs, eg, edl;
 };
 
-template <int MODE, bool FG>
-__device__ __forceinline__ void load_raw(RawChunk& r, const Params& p, const bf16* qh,
-                                         const bf16* kh, const bf16* vh, int tok0, int nval,
-                                         bool need_q, bool with_v, int tid, int h) {
+// A raw buffer resource over rows 0 .. nrows-1 (D bf16 features each, ts elements
+// apart) from base: loads past them return zeros without touching memory, which
+// pads a chunk's missing rows with no per-row masks.  The base is uniform, so the
+// per-chunk addressing is scalar; each lane's offset within a chunk is fixed.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const bf16* base, int nrows,
+                                                           int64_t ts) {
+  const uint32_t bytes = nrows > 0 ? (uint32_t)(((int64_t)(nrows - 1) * ts + D) * 2) : 0u;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(base), 0, bytes, 0x00020000);
+}
+__device__ __forceinline__ bf16x8 ld_rows(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+// Byte offsets of a thread's row pieces within a chunk (row pass*16 + tid/16,
+// features 8 (tid % 16) ..), for k / v rows (kv_ts) and q rows (q_ts).
+struct RowOffs {
+  uint32_t kv[MT], q[MT];
+};
+__device__ __forceinline__ RowOffs row_offs(const Params& p, int tid) {
+  RowOffs o;
 #pragma unroll
   for (int pass = 0; pass < MT; ++pass) {
-    const int row = pass * 16 + (tid >> 4);
-    const int f0 = (tid & 15) * 8;
-    const bool ok = row < nval;
-    const int64_t tok = tok0 + row;
-    r.k[pass] = ok ? *reinterpret_cast<const bf16x8*>(kh + tok * p.kv_ts + f0) : bf16x8{};
-    if (MODE == MODE_OUT || with_v)
-      r.v[pass] = ok ? *reinterpret_cast<const bf16x8*>(vh + tok * p.kv_ts + f0) : bf16x8{};
-    if (MODE == MODE_OUT)
-      r.q[pass] = (ok && need_q) ? *reinterpret_cast<const bf16x8*>(qh + tok * p.q_ts + f0)
-                                 : bf16x8{};
+    const int64_t row = pass * 16 + (tid >> 4), f0 = (tid & 15) * 8;
+    o.kv[pass] = (uint32_t)((row * p.kv_ts + f0) * 2);
+    o.q[pass] = (uint32_t)((row * p.q_ts + f0) * 2);
+  }
+  return o;
+}
+
+template <int MODE, bool FG>
+__device__ __forceinline__ void load_raw(RawChunk& r, const Params& p, const RowOffs& ro,
+                                         const bf16* qh, const bf16* kh, const bf16* vh,
+                                         int tok0, int nval, bool need_q, bool with_v, int tid,
+                                         int h) {
+  const __amdgpu_buffer_rsrc_t rk = rows_rsrc(kh + (int64_t)tok0 * p.kv_ts, nval, p.kv_ts);
+  const __amdgpu_buffer_rsrc_t rv =
+      rows_rsrc(vh + (int64_t)tok0 * p.kv_ts, (MODE == MODE_OUT || with_v) ? nval : 0, p.kv_ts);
+  const __amdgpu_buffer_rsrc_t rq =
+      rows_rsrc(qh + (int64_t)tok0 * p.q_ts, (MODE == MODE_OUT && need_q) ? nval : 0, p.q_ts);
+#pragma unroll
+  for (int pass = 0; pass < MT; ++pass) {
+    r.k[pass] = ld_rows(rk, ro.kv[pass]);
+    if (MODE == MODE_OUT || with_v) r.v[pass] = ld_rows(rv, ro.kv[pass]);
+    if (MODE == MODE_OUT) r.q[pass] = ld_rows(rq, ro.q[pass]);
   }
   r.gb = r.bb = FG ? NO_TOKEN : 0u;
   if (tid < nval && tid < C) ld_gate_bits<FG>(p, (int64_t)(tok0 + tid), h, r.gb, r.bb);
@@ -476,15 +511,20 @@ __device__ __forceinline__ void chunk_walk(const Params& p, unsigned char* smem,
   const bf16* vh = p.v + (int64_t)hk * D;
   bf16* oh = p.o + (int64_t)h * D;
 
-  // Coalesced 16-byte store of the O tile staged in sO (chunk starting at tok0).
+  // The O tile staged in sO (rows LDO apart) leaves through coalesced 16-byte
+  // reads and stores: lane group g of wave w handles, in pass p, row 8p + 2w +
+  // (g >> 1) + 16 (g & 1) (rows r and r + 16 share a half-wave), features
+  // 8 (lane & 15) .. +7.
+  const int og = (tid & 63) >> 4;
+  const int o_f = (tid & 15) * 8;
+  auto o_row = [&](int pass) { return 8 * pass + 2 * wave + (og >> 1) + 16 * (og & 1); };
   auto store_o = [&](int tok0, int nval) {
 #pragma unroll
     for (int pass = 0; pass < MT; ++pass) {
-      const int row = pass * 16 + (tid >> 4);
-      const int f0 = (tid & 15) * 8;
+      const int row = o_row(pass);
       if (row < nval)
-        *reinterpret_cast<bf16x8*>(oh + (int64_t)(tok0 + row) * o_rs + f0) =
-            *reinterpret_cast<const bf16x8*>(sO + row * LDQ + f0);
+        *reinterpret_cast<bf16x8*>(oh + (int64_t)(tok0 + row) * o_rs + o_f) =
+            *reinterpret_cast<const bf16x8*>(sO + row * LDO + o_f);
     }
   };
   // NORM: the gate slices of this thread's two output rows (loaded a phase ahead),
@@ -495,28 +535,27 @@ __device__ __forceinline__ void chunk_walk(const Params& p, unsigned char* smem,
   auto load_gate = [&](bf16x8* zr, int tok0, int nval) {
 #pragma unroll
     for (int pass = 0; pass < MT; ++pass) {
-      const int row = pass * 16 + (tid >> 4);
+      const int row = o_row(pass);
       zr[pass] = (zh && row < nval)
-                     ? *reinterpret_cast<const bf16x8*>(zh + (int64_t)(tok0 + row) * p.zg_ts +
-                                                        (tid & 15) * 8)
+                     ? *reinterpret_cast<const bf16x8*>(zh + (int64_t)(tok0 + row) * p.zg_ts + o_f)
                      : bf16x8{};
     }
   };
   auto store_o_norm = [&](int tok0, int nval, const bf16x8* zr) {
 #pragma unroll
     for (int pass = 0; pass < MT; ++pass) {
-      const int row = pass * 16 + (tid >> 4);
-      const int f0 = (tid & 15) * 8;
-      const bf16x8 ov = *reinterpret_cast<const bf16x8*>(sO + row * LDQ + f0);
+      const int row = o_row(pass);
+      const bf16x8 ov = *reinterpret_cast<const bf16x8*>(sO + row * LDO + o_f);
       float f[8], ss = 0.f;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         f[j] = (float)ov[j];
         ss += f[j] * f[j];
       }
+      // the 16 lanes of a row group hold the whole row
       const float rstd = 1.0f / sqrtf(row16_sum(ss) * (1.0f / D) + p.on_eps);
-      const f32x4 w0 = *reinterpret_cast<const f32x4*>(sNW + f0);
-      const f32x4 w1 = *reinterpret_cast<const f32x4*>(sNW + f0 + 4);
+      const f32x4 w0 = *reinterpret_cast<const f32x4*>(sNW + o_f);
+      const f32x4 w1 = *reinterpret_cast<const f32x4*>(sNW + o_f + 4);
       const float w[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
       bf16x8 out;
 #pragma unroll
@@ -528,8 +567,7 @@ __device__ __forceinline__ void chunk_walk(const Params& p, unsigned char* smem,
         }
         out[j] = (bf16)y;
       }
-      if (row < nval)
-        *reinterpret_cast<bf16x8*>(oh + (int64_t)(tok0 + row) * o_rs + f0) = out;
+      if (row < nval) *reinterpret_cast<bf16x8*>(oh + (int64_t)(tok0 + row) * o_rs + o_f) = out;
     }
   };
   if (NORM && tid < D) {
@@ -541,17 +579,18 @@ __device__ __forceinline__ void chunk_walk(const Params& p, unsigned char* smem,
   }
 
   if (c_begin < si.c_end) {
+    const RowOffs ro = row_offs(p, tid);
     RawChunk raw;
     {
       const int t0 = si.bos + c_begin * C;
-      load_raw<MODE, FG>(raw, p, qh, kh, vh, t0, min(C, si.eos - t0), c_begin >= c_out,
+      load_raw<MODE, FG>(raw, p, ro, qh, kh, vh, t0, min(C, si.eos - t0), c_begin >= c_out,
                          with_v, tid, h);
       prep_rows<MODE>(raw, p.l2norm, p.scale);
       if (wave == 0) prep_scan(raw, lane, gc);
       stage_chunk<MODE>(stage_at(smem, 0), raw, c_begin >= c_out, with_v, tid, wave, lane, gc);
       if (c_begin + 1 < si.c_end) {
         const int t1 = t0 + C;
-        load_raw<MODE, FG>(raw, p, qh, kh, vh, t1, min(C, si.eos - t1),
+        load_raw<MODE, FG>(raw, p, ro, qh, kh, vh, t1, min(C, si.eos - t1),
                            c_begin + 1 >= c_out, with_v, tid, h);
       }
     }
@@ -584,7 +623,7 @@ __device__ __forceinline__ void chunk_walk(const Params& p, unsigned char* smem,
                           gc);
         if (c + 2 < si.c_end) {
           const int t2 = tok0 + 2 * C;
-          load_raw<MODE, FG>(raw, p, qh, kh, vh, t2, min(C, si.eos - t2), c + 2 >= c_out,
+          load_raw<MODE, FG>(raw, p, ro, qh, kh, vh, t2, min(C, si.eos - t2), c + 2 >= c_out,
                              with_v, tid, h);
         }
       }
@@ -759,7 +798,7 @@ __device__ __forceinline__ void chunk_walk(const Params& p, unsigned char* smem,
 #pragma unroll
             for (int v = 0; v < 4; ++v) O[v] = QT[ct][mt][v] * eg;
             O = mfma16h(Va[ct], bp, O);
-            *reinterpret_cast<bf16x4*>(sO + (16 * mt + l16) * LDQ + 32 * wave + 16 * ct + 4 * q4) =
+            *reinterpret_cast<bf16x4*>(sO + (16 * mt + l16) * LDO + 32 * wave + 16 * ct + 4 * q4) =
                 bf16x4{(bf16)O[0], (bf16)O[1], (bf16)O[2], (bf16)O[3]};
           }
         }
@@ -1063,6 +1102,10 @@ static int chunk_fwd_impl(const void* q, int64_t q_token_stride, const void* k,
   HMX_REQUIRE(k_token_stride == v_token_stride, HMX_EINVAL,
               "hmx_gdn_chunk_fwd: k and v must share a token stride (%lld vs %lld)",
               (long long)k_token_stride, (long long)v_token_stride);
+  // a chunk's rows are addressed by 32-bit byte offsets from its first row
+  HMX_REQUIRE(q_token_stride > 0 && k_token_stride > 0 && q_token_stride < (1 << 26) &&
+                  k_token_stride < (1 << 26),
+              HMX_EINVAL, "hmx_gdn_chunk_fwd: token strides must lie in [1, 2^26) elements");
   HMX_REQUIRE(!(h0 || ht) || ((state_dtype == HMX_F32 || state_dtype == HMX_BF16) &&
                               state_slot_stride % 4 == 0 &&
                               ((uintptr_t)h0 | (uintptr_t)ht) % 16 == 0),
