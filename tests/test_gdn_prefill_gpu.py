@@ -301,3 +301,23 @@ def test_fla_chunk_gated_delta_rule(dev, dtype):
     assert_out_close(o2, o_ref.reshape(1, B * T, H, 128))
     assert_state_close(s2, s_ref)
     assert s3 is None and o3.shape == (1, B * T, H, 128)
+
+
+@pytest.mark.parametrize("seg", [None, 2])
+def test_prefill_rows_outside_fp16_range(dev, seg):
+    """With the in-kernel L2 norm, k and q rows are normalised in fp32 before their
+    fp16 rounding, so bf16 rows far outside fp16's range (|x| ~ 1e5) or tiny
+    (~1e-6) stage safely.  Such rows and a zero key row, in the first chunk, a
+    later chunk and a multi-segment split, against the fp64 oracle."""
+    q, k, v, g, beta, g0 = _mk(1, 64 * 5 + 9, 4, 2, 31, normalize=False)
+    q, k = q.float(), k.float()
+    k[0, 3] *= 3e4          # first chunk: |k| elements past fp16's range
+    k[0, 70, 1] *= 1e5
+    q[0, 40] *= 4e4
+    q[0, 200, 2] *= 1e-6    # a tiny query row
+    k[0, 150, 0] *= 1e-6    # a tiny key row
+    k[0, 260, 1] = 0.0      # a zero key row (stays on the fast path)
+    q, k = q.bfloat16(), k.bfloat16()
+    assert k.float().abs().max() > 65504 and q.float().abs().max() > 65504
+    h0 = torch.randn(1, 4, 128, 128, generator=g0) * 0.05
+    _check(dev, q, k, v, g, beta, h0=h0, seg=seg)
