@@ -34,8 +34,10 @@
 //     barrier.
 //
 // Numerics.  MFMA operands are fp16 with fp32 accumulation: k~, v~, the block-start
-// states (one rounding each) and, as fp16 hi + lo pairs, the iterate X, the
-// masked in-block products X.k~ and the blended query (the iterate is large off
+// states (one rounding each).  The solve runs in direction form (x and the
+// residual in fp32; only the step d enters the products): d is one fp16 rounding
+// against H_c and an fp16 hi + lo pair against the in-block keys, as are the
+// masked in-block products d.k~ and the blended query (the iterate is large off
 // the key span, and a single rounding of it moves o by ~3e-2).  The walk keeps H
 // and S in fp32 accumulators; its update operands are single fp16 roundings.
 //
@@ -739,8 +741,9 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
   const int tb = 16 * wave + l16;
   const bool tok_ok = tb < nval;
   f32x4 Q[8];
+  const bf16* qr = p.q + (int64_t)(tok0 + tb) * p.q_ts + (int64_t)h * D + 4 * q4;
+  float rq;
   {
-    const bf16* qr = p.q + (int64_t)(tok0 + tb) * p.q_ts + (int64_t)h * D + 4 * q4;
     float ss = 0.f;
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt) {
@@ -758,7 +761,7 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
     }
     ss += __shfl_xor(ss, 16, 64);
     ss += __shfl_xor(ss, 32, 64);
-    const float rq = (!tok_ok) ? 0.f : (p.l2norm ? 1.0f / sqrtf(ss) : 1.f);
+    rq = (!tok_ok) ? 0.f : (p.l2norm ? 1.0f / sqrtf(ss) : 1.f);
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt)
 #pragma unroll
@@ -868,41 +871,47 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
       if (!tok_ok) { tau = 0.f; lam = 0.f; cc = 0.f; }
     }
 
-    // ---- the Chebyshev iterations -----------------------------------------
+    // ---- the Chebyshev iterations ------------------------------------------
+    // In direction form: with rho_k = q - A x_k (A = H_t + lam I) and d_k = x_{k+1} - x_k,
+    //   x_0 = tau q, d_{-1} = tau q, rho_0 = q - A d_{-1};  per step (w as the reference
+    //   updates it): d_k = w tau rho_k + (w - 1) d_{k-1}, x_{k+1} = x_k + d_k,
+    //   rho_{k+1} = rho_k - A d_k
+    // - the reference's x_{k+1} = w x_k - tau w (A x_k - q) - (w-1) x_{k-1} exactly.
+    // x and rho stay in fp32; only d enters the products.  d and rho carry no
+    // 1/lam growth (x does, off the key span), so the history part e^{Gk_t} H_c d
+    // takes d as one fp16 rounding; the in-block part K~^T (M . K~ d), which carries
+    // the early tokens, keeps the hi + lo pairs.  (A CPU emulation of both orders of
+    // rounding against the fp64 recurrence gives the same output error as hi + lo
+    // for every product.)
     {
-    f32x4 Xp[8];
+    f32x4 R[8], Dd[8];
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        X[nt][v] = tau * Q[nt][v];
-        Xp[nt][v] = 0.f;
+        Dd[nt][v] = tau * Q[nt][v];
+        X[nt][v] = Dd[nt][v];
+        R[nt][v] = Q[nt][v];
       }
-    // in-block decays m_tj = e^{Gk_t-Gk_j} (j <= t, else 0) of the four key tiles
+    // minus the in-block decays -m_tj = -e^{Gk_t-Gk_j} (j <= t, else 0) of the four key tiles
     f32x4 mz[4];
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt) {
       const f32x4 gkj = *reinterpret_cast<const f32x4*>(&SC(SC_GK, 16 * jt + 4 * q4));
 #pragma unroll
-      for (int v = 0; v < 4; ++v) mz[jt][v] = (16 * jt + 4 * q4 + v <= tb) ? fast_exp(GkT - gkj[v]) : 0.f;
+      for (int v = 0; v < 4; ++v)
+        mz[jt][v] = (16 * jt + 4 * q4 + v <= tb) ? -fast_exp(GkT - gkj[v]) : 0.f;
     }
-    float om = 2.f;
     const float egk = fast_exp(GkT);
-    // One step from (x = A, x_prev = B), written over B:
-    //   x' = w x - tau w (H x + lam x - q) - (w-1) x_prev = ca x - tw (H x - q) + cd x_prev
-    // with H x = e^{Gk_t} H_c x + K~^T Z~^T, eight 16-row tiles in two groups of four
-    // (four independent accumulation chains keep the MFMA pipe busy; w <= 2 since
-    // c <= 1/4, so the hardware reciprocal suffices).
-    auto step = [&](f32x4 (&A)[8], f32x4 (&B)[8]) {
-      // x^T as B operands (hi + lo): k = state rows 32ks + {4q4+v, 16+4q4+v}, n = token
-      f16x8 xh[4], xl[4];
+    // R <- R - A d: R - lam d - e^{Gk_t} H_c d first, then the in-block part
+    // accumulates on top through -Z~ (eight 16-row tiles in two groups of four, four
+    // independent accumulation chains)
+    auto apply = [&]() {
+      f16x8 dh[4], dl[4];
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) h8_hilo(A[2 * ks], A[2 * ks + 1], xh[ks], xl[ks], one);
-      // Z~^T[j][t] = m_tj (k~_j . x_t), as hi/lo B operands, over all four key tiles:
-      // the keys past this wave's tokens get m = 0.  Wave 3 needs all four and sets
-      // the block's pace, so the shorter ranges of waves 0-2 would save no time (two
-      // workgroups share each CU's SIMDs); one uniform instruction stream keeps the
-      // loop straight-line and small.
+      for (int ks = 0; ks < 4; ++ks) h8_hilo(Dd[2 * ks], Dd[2 * ks + 1], dh[ks], dl[ks], one);
+      // -Z~^T[j][t] = -m_tj (k~_j . d_t), hi/lo B operands over all four key tiles (the
+      // keys past this wave's tokens get m = 0; one uniform instruction stream)
       f16x8 zh[2], zl[2];
       {
         f32x4 Z[4];
@@ -914,9 +923,9 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
 #pragma unroll
           for (int jt = 0; jt < 4; ++jt) a[jt] = frag_i(sK, LDP, 16 * jt, 32 * ks, lane);
 #pragma unroll
-          for (int jt = 0; jt < 4; ++jt) Z[jt] = mfma16h(a[jt], xh[ks], Z[jt]);
+          for (int jt = 0; jt < 4; ++jt) Z[jt] = mfma16h(a[jt], dh[ks], Z[jt]);
 #pragma unroll
-          for (int jt = 0; jt < 4; ++jt) Z[jt] = mfma16h(a[jt], xl[ks], Z[jt]);
+          for (int jt = 0; jt < 4; ++jt) Z[jt] = mfma16h(a[jt], dl[ks], Z[jt]);
         }
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt)
@@ -925,8 +934,6 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
 #pragma unroll
         for (int jk = 0; jk < 2; ++jk) h8_hilo(Z[2 * jk], Z[2 * jk + 1], zh[jk], zl[jk], one);
       }
-      om = __builtin_amdgcn_rcpf(1.0f - cc * om);
-      const float tw = tau * om, ca = om - tw * lam, cd = 1.0f - om;
 #pragma unroll
       for (int g4 = 0; g4 < 8; g4 += 4) {
         f32x4 hx[4];
@@ -938,15 +945,13 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
 #pragma unroll
           for (int u = 0; u < 4; ++u) a[u] = frag_i(sH, LDP, 16 * (g4 + u), 32 * ks, lane);
 #pragma unroll
-          for (int u = 0; u < 4; ++u) hx[u] = mfma16h(a[u], xh[ks], hx[u]);
-#pragma unroll
-          for (int u = 0; u < 4; ++u) hx[u] = mfma16h(a[u], xl[ks], hx[u]);
+          for (int u = 0; u < 4; ++u) hx[u] = mfma16h(a[u], dh[ks], hx[u]);
         }
-        // e^{Gk_t} H_c x - q, then the in-block part accumulates on top
 #pragma unroll
         for (int u = 0; u < 4; ++u)
 #pragma unroll
-          for (int v = 0; v < 4; ++v) hx[u][v] = egk * hx[u][v] - Q[g4 + u][v];
+          for (int v = 0; v < 4; ++v)
+            hx[u][v] = R[g4 + u][v] - lam * Dd[g4 + u][v] - egk * hx[u][v];
 #pragma unroll
         for (int jk = 0; jk < 2; ++jk) {
           f16x8 a[4];
@@ -958,23 +963,25 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
           for (int u = 0; u < 4; ++u) hx[u] = mfma16h(a[u], zl[jk], hx[u]);
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-#pragma unroll
-          for (int v = 0; v < 4; ++v)
-            B[g4 + u][v] = ca * A[g4 + u][v] + cd * B[g4 + u][v] - tw * hx[u][v];
+        for (int u = 0; u < 4; ++u) R[g4 + u] = hx[u];
         // bound the scheduler's hoisting of LDS operands to one group of tiles
         __builtin_amdgcn_sched_barrier(0);
       }
     };
-    // two steps per trip, so x and x_prev trade registers instead of being copied
-    for (int it = 0; it < p.num_iter; it += 2) {
-      step(X, Xp);
-      if (it + 1 == p.num_iter) {
+    if (p.num_iter > 0) apply();
+    // w <= 2 since c <= 1/4, so the hardware reciprocal suffices
+    float om = 2.f;
+    for (int it = 0; it < p.num_iter; ++it) {
+      om = __builtin_amdgcn_rcpf(1.0f - cc * om);
+      const float wt = om * tau, wm = om - 1.0f;
 #pragma unroll
-        for (int nt = 0; nt < 8; ++nt) X[nt] = Xp[nt];
-        break;
-      }
-      step(Xp, X);
+      for (int nt = 0; nt < 8; ++nt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          Dd[nt][v] = wt * R[nt][v] + wm * Dd[nt][v];
+          X[nt][v] += Dd[nt][v];
+        }
+      if (it + 1 < p.num_iter) apply();
     }
     }
     if constexpr (MODE != SM_GLA) {
@@ -1001,12 +1008,17 @@ __global__ __launch_bounds__(NTHR, 2) void gka_solve_kernel(Params p) {
       }
       if constexpr (!GLA) return;
     }
-    // alpha blend
+    // alpha blend (q read again: the iterations keep x, d and rho in registers)
     const float al = SC(SC_AL, tb);
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt)
+    for (int nt = 0; nt < 8; ++nt) {
+      const bf16x4 xq = tok_ok ? *reinterpret_cast<const bf16x4*>(qr + 16 * nt) : bf16x4{};
 #pragma unroll
-      for (int v = 0; v < 4; ++v) X[nt][v] = Q[nt][v] + al * (X[nt][v] - Q[nt][v]);
+      for (int v = 0; v < 4; ++v) {
+        const float qv = (float)xq[v] * rq;
+        X[nt][v] = qv + al * (X[nt][v] - qv);
+      }
+    }
     lds_barrier();      // every wave is done with H_c
   } else {
 #pragma unroll
