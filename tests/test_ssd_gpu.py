@@ -294,3 +294,27 @@ def test_varlen_intermediate_chunk_states(dev, pooled):
     assert_out_close(out, y_r, what="y")
     for c in range(len(seq)):
         assert_state_close(st[c], exp_states[c], what=f"chunk {c}")
+
+
+@pytest.mark.parametrize("seg", [1, 2])
+def test_scan_split_fast_and_slow_decay_heads(dev, seg):
+    """Split sequences (forced 1- and 2-chunk segments) whose heads decay fast and
+    very slowly (A down to -5e-4, so the segment combine carries nearly all of the
+    state), with initial states, against the fp64 oracle: y of every head and the
+    final states."""
+    b, l, H, G, P, N = 2, 64 * 7 + 5, 4, 2, 64, 128
+    x, dt, A, B, C, D, bias, _, g0 = _inputs(b, l, H, G, P, N, 77)
+    A = torch.tensor([-8.0, -2e-3, -3.0, -5e-4])
+    h0 = torch.randn(b, H, P, N, generator=g0) * 0.1
+    y_r, f_r = ref.mamba_chunk_scan_combined(x, dt, A, B, C, 256, D=D, dt_bias=bias,
+                                             initial_states=h0, dt_softplus=True,
+                                             return_final_states=True)
+    y, f = hmx.mamba_chunk_scan_combined(*_d(dev, x, dt, A, B, C), 256, D=D.to(dev),
+                                         dt_bias=bias.to(dev), initial_states=h0.to(dev),
+                                         dt_softplus=True, return_final_states=True,
+                                         _segment_chunks=seg)
+    torch.cuda.synchronize()
+    assert_out_close(y, y_r, what="y")
+    assert_state_close(f, f_r, what="final_states")
+    for hh in range(H):
+        assert_out_close(y[:, :, hh], y_r[:, :, hh], what=f"y head {hh}")
