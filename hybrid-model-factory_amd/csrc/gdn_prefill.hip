@@ -48,10 +48,14 @@
 // substitution right-hand sides are rounded from their fp32 accumulators.  fp16
 // keeps 11 significant bits where bf16 keeps 8: one rounding per operand gives
 // ~5e-4 relative state error, inside the 1e-3 bound, where bf16 needed hi + lo
-// pairs (two MFMAs and a split per product).  The range is fp16's: without
-// in-kernel normalisation |k|, |q| must stay below 65504, and so must the state
-// and V_new entries (they are O(|v|) for normalised keys).  The state is kept
-// exact in fp32 and decayed explicitly each chunk.
+// pairs (two MFMAs and a split per product).  Without in-kernel normalisation
+// |k|, |q| must stay below 65504.  The state, the substitution's right-hand sides
+// and V_new are O(|v|) and may pass fp16's range for large v or a large initial
+// state: such a walk is detected (the inf reaches its end state, V_new through the
+// fp16 copy from which the state update is formed) and walked again with those
+// operands scaled per wave by a power of two from a running bound on the state's
+// column norms (chunk_walk), which is exact.  The state is kept in fp32 and
+// decayed explicitly each chunk.
 //
 // Roofline: HBM-bound at the algorithmic minimum (q,k,v,o bf16 + g,beta +
 // final state); FLOPs 2*T*H*(5*C*d + 3*d^2).
@@ -97,7 +101,8 @@ constexpr int OFF_O = 2 * SZ_BUF;
 constexpr int OFF_T = OFF_O + SZ_O;    // rows 0-15: T'_00 | rows 16-31: -M_10, T'_11 (fp16)
 constexpr int OFF_P = OFF_T + SZ_P;    // P (fp16, lower triangle; the upper tile stays 0)
 constexpr int OFF_NW = OFF_P + SZ_P;   // fp32 [D] output-norm weight (NORM)
-constexpr int SMEM = OFF_NW + D * 4;
+constexpr int OFF_FLAG = OFF_NW + D * 4;   // int [4]: the waves' range flags
+constexpr int SMEM = OFF_FLAG + 16;
 static_assert(SMEM <= 80 * 1024, "LDS budget: two workgroups per CU");
 
 struct SegInfo {     // one row of the host-built segment table (int32 x 8)
@@ -124,6 +129,7 @@ struct Params {
   float* ws_ht;              // [N][H][D][D] or null
   const int* seg;            // [nseg_total][8]
   int* plan;                 // [nseg_total][H]: warm-up start chunk, or -1 (null: 1 seg/seq)
+  int* redo;                 // [nseg_total][H]: 1 where the output walk left fp16's range
   float* ws_s0;              // [nseg_total][H][D][D]
   float* ws_phi;
   float* ws_init;
@@ -414,8 +420,8 @@ __device__ __forceinline__ f16x4 ld_blk(const f16* m, int r0, int c0, int lane) 
 // (norm before gate) on their way out of sO.
 // One workgroup's walk of segment s_id for head h: its output (OUT), or the S0
 // (phi false) or Phi (phi true) pre-pass walk of an exact pair's segment (PRE).
-template <int MODE, bool NORM, bool FG>
-__device__ __forceinline__ void chunk_walk(const Params& p, unsigned char* smem, int s_id, int h,
+template <int MODE, bool NORM, bool FG, bool SAFE>
+__device__ __forceinline__ bool chunk_walk(const Params& p, unsigned char* smem, int s_id, int h,
                                            bool phi) {
   bf16* sO = reinterpret_cast<bf16*>(smem + OFF_O);
   f16* sT = reinterpret_cast<f16*>(smem + OFF_T);
@@ -448,9 +454,9 @@ __device__ __forceinline__ void chunk_walk(const Params& p, unsigned char* smem,
       init_kind = (w == 0) ? 1 : 0;
     }
   } else {
-    if (!exact || si.seg_idx == si.nseg - 1) return;
+    if (!exact || si.seg_idx == si.nseg - 1) return true;
     if (phi) {
-      if (si.seg_idx == 0) return;
+      if (si.seg_idx == 0) return true;
       init_kind = 3;
     } else {
       init_kind = (si.seg_idx == 0) ? 1 : 0;
@@ -498,6 +504,48 @@ __device__ __forceinline__ void chunk_walk(const Params& p, unsigned char* smem,
             S[rt][ct][v] = (init_kind == 3 && row == col) ? 1.f : 0.f;
           }
     }
+  }
+
+  // ---- fp16 range.  The plain walk (SAFE false) rounds the state, Y, the
+  // substitution's right-hand sides and V_new to fp16 as they are; an entry past
+  // fp16's range becomes inf, which reaches the end state (V_new through its fp16
+  // copy, from which the state update is formed), so the walk reports it instead of
+  // writing the end state and the caller walks again with SAFE true.  The SAFE walk keeps
+  // 2^-se S in the registers (se >= 0, per wave) and bnd, a bound on the 2-norm of
+  // each of this wave's state columns at true scale.  A column s of the state
+  // follows s <- e^g (I - beta k k^T) s + beta k v_j, whose transition has norm
+  // <= 1 for |k| <= 1, beta in [0, 2] and g <= 0, so a chunk whose entries of v
+  // (this wave's columns) are at most vmax in magnitude keeps
+  //   |S|, |Y|, |V_new|, |e^{G_last-G} V_new|, the substitution's right-hand sides
+  //     <= 2 (bnd + vmax + 2 C vmax),   bnd <- e^{G_last} bnd + 2 C vmax.
+  // Each chunk scales its fp16 operands by 2^-fp16_range_exp of that bound; the
+  // scale enters only through multiplications by powers of two, which are exact,
+  // so both walks give the same result wherever the plain one stays in range.
+  float bnd = 0.f;
+  int se = 0;
+  if (!SAFE) {
+  } else if (init_kind == 1 || init_kind == 2) {
+    float ss = 0.f;   // the Frobenius norm of this wave's columns bounds each column's norm
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) ss += S[rt][ct][v] * S[rt][ct][v];
+    bnd = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(
+                                        __builtin_bit_cast(int, sqrtf(wave_sum(ss)))));
+    se = fp16_range_exp(2.f * bnd);
+    if (se) {
+      const float sig = pow2f(-se);
+#pragma unroll
+      for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) S[rt][ct][v] *= sig;
+    }
+  } else {
+    bnd = init_kind == 3 ? 1.f : 0.f;
   }
 
   // P's strictly-upper 16x16 tile is never written by phase 1: zero it once.
@@ -602,15 +650,17 @@ __device__ __forceinline__ void chunk_walk(const Params& p, unsigned char* smem,
       const int tok0 = si.bos + c * C;
       const bool out_chunk = (MODE == MODE_OUT) && (c >= c_out);
       if (MODE == MODE_OUT && out_chunk && p.ws_hc) {
-        // the state entering this chunk, fp16 row-major (the backward's S0)
+        // the state entering this chunk, fp16 row-major (the backward's S0; at true
+        // scale, so its entries must stay inside fp16's range)
         f16* dst = p.ws_hc + ((int64_t)(p.cu_chunk[si.n] + c) * H + h) * D * D + 32 * wave + l16;
+        const float isig = pow2f(se);
 #pragma unroll
         for (int rt = 0; rt < 8; ++rt)
 #pragma unroll
           for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
             for (int v = 0; v < 4; ++v)
-              dst[(16 * rt + 4 * q4 + v) * D + 16 * ct] = (f16)S[rt][ct][v];
+              dst[(16 * rt + 4 * q4 + v) * D + 16 * ct] = (f16)(S[rt][ct][v] * isig);
       }
 
       // ---- phase 1: stage the next chunk (its buffer was last read in the previous
@@ -635,6 +685,10 @@ __device__ __forceinline__ void chunk_walk(const Params& p, unsigned char* smem,
       // X[mt][ct] = (K S) tile (tokens 16mt.., state cols 32w+16ct..);
       // QT[ct][mt] = (Q S)^T tile (state cols 32w+16ct.., tokens 16mt..)
       f32x4 X[MT][2], QT[2][MT];
+      // VF: this wave's tile of the chunk's V (fp32), read in phase 1 so that the
+      // reduction of its magnitude overlaps the MFMAs; vmax bounds its entries
+      f32x4 VF[MT][2];
+      float vmax = 0.f;
       auto phase1 = [&](auto role_c, auto outq_c) {
         constexpr int R = decltype(role_c)::value;
         constexpr bool OQ = decltype(outq_c)::value;
@@ -706,6 +760,22 @@ __device__ __forceinline__ void chunk_walk(const Params& p, unsigned char* smem,
           put_row4(sP, 16 + l16, 4 * q4, v0);
           put_row4(sP, 16 + l16, 16 + 4 * q4, v1);
         }
+        if constexpr (SAFE) {
+          float vm = 0.f;
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) {
+              bf16x4 vt = {};
+              if (with_v) vt = ld_tr(cur.V, LDQ, 16 * mt + 4 * q4, 32 * wave + 16 * ct, lane);
+#pragma unroll
+              for (int v = 0; v < 4; ++v) {
+                VF[mt][ct][v] = (float)vt[v];
+                vm = fmaxf(vm, fabsf(VF[mt][ct][v]));
+              }
+            }
+          vmax = with_v ? wave_max_nonneg(vm) : 0.f;
+        }
         // K S and (Q S)^T for this wave's columns; one fp16 copy of the state
         // serves as the B operand of K S and the A operand of (Q S)^T
 #pragma unroll
@@ -758,6 +828,16 @@ __device__ __forceinline__ void chunk_walk(const Params& p, unsigned char* smem,
 
       __builtin_amdgcn_s_setprio(1);
       // ---- phase 2: Y = V - e^G K S; V_new by blockwise substitution --------------
+      // (SAFE: at operand scale 2^-te, with the registers' S, and so K S and Q S, at
+      // 2^-se: Y = 2^-te V - 2^(se-te) e^G K (2^-se S))
+      int te = 0;
+      float tau = 1.f, rho = 1.f, itau = 1.f;
+      if constexpr (SAFE) {
+        te = fp16_range_exp(2.f * (bnd + (2 * C + 1) * vmax));
+        tau = pow2f(-te);
+        rho = pow2f(se - te);
+        itau = pow2f(te);
+      }
       f32x4 Vn[MT][2];
       {
         f32x4 Y[MT][2];
@@ -765,11 +845,18 @@ __device__ __forceinline__ void chunk_walk(const Params& p, unsigned char* smem,
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
           for (int ct = 0; ct < 2; ++ct) {
-            bf16x4 vt = {};
-            if (with_v) vt = ld_tr(cur.V, LDQ, 16 * mt + 4 * q4, 32 * wave + 16 * ct, lane);
+            if constexpr (SAFE) {
 #pragma unroll
-            for (int v = 0; v < 4; ++v)
-              Y[mt][ct][v] = (float)vt[v] - cur.EG[16 * mt + 4 * q4 + v] * X[mt][ct][v];
+              for (int v = 0; v < 4; ++v)
+                Y[mt][ct][v] = VF[mt][ct][v] * tau -
+                               (cur.EG[16 * mt + 4 * q4 + v] * rho) * X[mt][ct][v];
+            } else {
+              bf16x4 vt = {};
+              if (with_v) vt = ld_tr(cur.V, LDQ, 16 * mt + 4 * q4, 32 * wave + 16 * ct, lane);
+#pragma unroll
+              for (int v = 0; v < 4; ++v)
+                Y[mt][ct][v] = (float)vt[v] - cur.EG[16 * mt + 4 * q4 + v] * X[mt][ct][v];
+            }
           }
         const f16x4 t00 = ld_blk(sT, 0, 0, lane);
         const f16x4 nm10 = ld_blk(sT, 16, 0, lane);
@@ -783,50 +870,67 @@ __device__ __forceinline__ void chunk_walk(const Params& p, unsigned char* smem,
         }
       }
 
+      // V_new's fp16 copy: the B operand of O and, widened again, the state update's
+      // right-hand side, so that an entry past fp16's range reaches the state
+      f16x8 Va[2];
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) Va[ct] = h8(Vn[0][ct], Vn[1][ct]);
+
       // ---- O^T = e^G (Q S)^T + V_new^T P^T -> sO (4 features of a token per lane) ----
       if (out_chunk) {
-        f16x8 Va[2];
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) Va[ct] = h8(Vn[0][ct], Vn[1][ct]);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
           const f16x8 bp = frag_perm_h(sP, LDT, 16 * mt, 0, lane);
-          const float eg = cur.EG[16 * mt + l16];
+          const float eg = SAFE ? cur.EG[16 * mt + l16] * rho : cur.EG[16 * mt + l16];
 #pragma unroll
           for (int ct = 0; ct < 2; ++ct) {
             f32x4 O;
 #pragma unroll
             for (int v = 0; v < 4; ++v) O[v] = QT[ct][mt][v] * eg;
-            O = mfma16h(Va[ct], bp, O);
+            O = mfma16h(Va[ct], bp, O);   // SAFE: 2^-te O
+            if constexpr (SAFE) {
+#pragma unroll
+              for (int v = 0; v < 4; ++v) O[v] *= itau;
+            }
             *reinterpret_cast<bf16x4*>(sO + (16 * mt + l16) * LDO + 32 * wave + 16 * ct + 4 * q4) =
                 bf16x4{(bf16)O[0], (bf16)O[1], (bf16)O[2], (bf16)O[3]};
           }
         }
       }
 
-      // ---- S <- e^{G_last} S + K_n^T (e^{G_last-G} V_new) --------------------------
+      // ---- S <- e^{G_last} S + K_n^T (e^{G_last-G} V_new) (SAFE: leaving the
+      // registers at 2^-te) ----------------------------------------------------------
       {
-        const float egl = cur.EG[C - 1];
+        float egl = cur.EG[C - 1];
+        if constexpr (SAFE)
+          egl = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, egl)));
+        const float egs = SAFE ? egl * rho : egl;
 #pragma unroll
         for (int rt = 0; rt < 8; ++rt)
 #pragma unroll
           for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) S[rt][ct][v] *= egl;
+            for (int v = 0; v < 4; ++v) S[rt][ct][v] *= egs;
+        if constexpr (SAFE) {
+          bnd = egl * bnd + (2 * C) * vmax;
+          se = te;
+        }
         float e0[4], e1[4];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           e0[v] = cur.EDL[4 * q4 + v];
           e1[v] = cur.EDL[16 + 4 * q4 + v];
         }
+        // W = e^{G_last-G} V_new from V_new's fp16 copy (mixed-precision multiplies)
         f16x8 Wb[2];
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) {
           f32x4 w0, w1;
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
-            w0[v] = Vn[0][ct][v] * e0[v];
-            w1[v] = Vn[1][ct][v] * e1[v];
+            // fma with a zero addend: one v_fma_mix_f32 (widening in the instruction)
+            w0[v] = __builtin_fmaf((float)Va[ct][v], e0[v], 0.f);
+            w1[v] = __builtin_fmaf((float)Va[ct][4 + v], e1[v], 0.f);
           }
           Wb[ct] = h8(w0, w1);
         }
@@ -853,6 +957,26 @@ __device__ __forceinline__ void chunk_walk(const Params& p, unsigned char* smem,
     }
   }
 
+  // ---- plain walk: did an fp16 operand leave its range?  Any inf there reaches the
+  // end state as inf or NaN (the sum below overflows to inf only when entries
+  // approach fp32's range, which the SAFE walk then handles as well).
+  if constexpr (!SAFE) {
+    float acc = 0.f;
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc += S[rt][ct][v];
+    int* flag = reinterpret_cast<int*>(smem + OFF_FLAG);
+    const bool bad = __ballot(!__builtin_isfinite(acc)) != 0;
+    if (lane == 0) flag[wave] = bad;
+    lds_barrier();
+    const int redo = flag[0] | flag[1] | flag[2] | flag[3];
+    if (MODE == MODE_OUT && tid == 0) p.redo[s_id * H + h] = redo;
+    if (redo) return false;   // the end state is not written
+  }
+
   // ---- write the end state ---------------------------------------------------
   float* dst = nullptr;
   bf16* dst16 = nullptr;
@@ -870,6 +994,7 @@ __device__ __forceinline__ void chunk_walk(const Params& p, unsigned char* smem,
     dst = (phi ? p.ws_phi : p.ws_s0) + ((int64_t)s_id * H + h) * D * D;
   }
   if (dst || dst16) {
+    const float isig = pow2f(se);   // back to true scale (exact)
 #pragma unroll
     for (int rt = 0; rt < 8; ++rt)
 #pragma unroll
@@ -877,26 +1002,41 @@ __device__ __forceinline__ void chunk_walk(const Params& p, unsigned char* smem,
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int i = (16 * rt + 4 * q4 + v) * D + 32 * wave + 16 * ct + l16;
-          if (dst) dst[i] = S[rt][ct][v];
-          else dst16[i] = (bf16)S[rt][ct][v];
+          if (dst) dst[i] = S[rt][ct][v] * isig;
+          else dst16[i] = (bf16)(S[rt][ct][v] * isig);
         }
   }
+  return true;
 }
 
 // The output walks (after the exact pairs' segment combine).
+// A walk whose fp16 operands left their range writes no end state and sets its
+// redo flag; gdn_redo_kernel walks it again with scaled operands.
 template <bool NORM, bool FG>
 __global__ __launch_bounds__(NTHR, 2) void gdn_chunk_kernel(Params p) {
   __shared__ __align__(16) unsigned char smem[SMEM];
-  chunk_walk<MODE_OUT, NORM, FG>(p, smem, blockIdx.x, blockIdx.y, false);
+  chunk_walk<MODE_OUT, NORM, FG, false>(p, smem, blockIdx.x, blockIdx.y, false);
+}
+
+// The flagged output walks again, with scaled fp16 operands (their outputs and end
+// states are written again); the other workgroups return at once.
+template <bool NORM, bool FG>
+__global__ __launch_bounds__(NTHR, 2) void gdn_redo_kernel(Params p) {
+  __shared__ __align__(16) unsigned char smem[SMEM];
+  if (!p.redo[blockIdx.x * p.H + blockIdx.y]) return;
+  chunk_walk<MODE_OUT, NORM, FG, true>(p, smem, blockIdx.x, blockIdx.y, false);
 }
 
 // The exact pairs' pre-pass: blockIdx.z 0 walks S0, 1 walks Phi.  The two are
 // independent and share the GPU in one launch; the output walks follow in a
-// launch of their own, which the warm-up pairs fill alongside the exact ones.
+// launch of their own, which the warm-up pairs fill alongside the exact ones.  A
+// walk whose fp16 operands left their range is walked again at once with scaled
+// operands (its end state feeds the segment combine).
 template <bool FG>
 __global__ __launch_bounds__(NTHR, 2) void gdn_pre_kernel(Params p) {
   __shared__ __align__(16) unsigned char smem[SMEM];
-  chunk_walk<MODE_PRE, false, FG>(p, smem, blockIdx.x, blockIdx.y, blockIdx.z == 1);
+  if (!chunk_walk<MODE_PRE, false, FG, false>(p, smem, blockIdx.x, blockIdx.y, blockIdx.z == 1))
+    chunk_walk<MODE_PRE, false, FG, true>(p, smem, blockIdx.x, blockIdx.y, blockIdx.z == 1);
 }
 
 // ---------------------------------------------------------------------------
@@ -1153,6 +1293,7 @@ static int chunk_fwd_impl(const void* q, int64_t q_token_stride, const void* k,
   p.ws_ht = staged ? reinterpret_cast<float*>(ws + 3 * st) : nullptr;
   char* tail = ws + (multi ? 3 * st : 0) + (multi && pooled ? (size_t)N * H * D * D * 4 : 0);
   p.plan = reinterpret_cast<int*>(tail);
+  p.redo = p.plan + (size_t)nseg_total * H;
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid(nseg_total, H);
   // multi-segment: plan; the exact pairs' S0 / Phi pre-pass; their segment
@@ -1173,14 +1314,20 @@ static int chunk_fwd_impl(const void* q, int64_t q_token_stride, const void* k,
   } else {
     p.plan = nullptr;
   }
-  if (o_norm && p.fused)
+  // every output walk, then again (scaled) the ones that left fp16's range
+  if (o_norm && p.fused) {
     hipLaunchKernelGGL((gdn_chunk_kernel<true, true>), grid, dim3(NTHR), 0, s, p);
-  else if (o_norm)
+    hipLaunchKernelGGL((gdn_redo_kernel<true, true>), grid, dim3(NTHR), 0, s, p);
+  } else if (o_norm) {
     hipLaunchKernelGGL((gdn_chunk_kernel<true, false>), grid, dim3(NTHR), 0, s, p);
-  else if (p.fused)
+    hipLaunchKernelGGL((gdn_redo_kernel<true, false>), grid, dim3(NTHR), 0, s, p);
+  } else if (p.fused) {
     hipLaunchKernelGGL((gdn_chunk_kernel<false, true>), grid, dim3(NTHR), 0, s, p);
-  else
+    hipLaunchKernelGGL((gdn_redo_kernel<false, true>), grid, dim3(NTHR), 0, s, p);
+  } else {
     hipLaunchKernelGGL((gdn_chunk_kernel<false, false>), grid, dim3(NTHR), 0, s, p);
+    hipLaunchKernelGGL((gdn_redo_kernel<false, false>), grid, dim3(NTHR), 0, s, p);
+  }
   if (staged) hipLaunchKernelGGL(gdn_state_copy_kernel, dim3(N, H), dim3(NTHR), 0, s, p);
   return check_launch("hmx_gdn_chunk_fwd");
 }
@@ -1209,7 +1356,7 @@ extern "C" size_t hmx_gdn_chunk_workspace_bytes(int32_t nseg_total, int32_t N, i
   const bool multi = nseg_total > N;
   size_t b = multi ? 3 * (size_t)nseg_total * H * D * D * sizeof(float) : 0;
   if (multi && pooled) b += (size_t)N * H * D * D * sizeof(float);   // staged end states
-  b += (size_t)nseg_total * H * sizeof(int);
+  b += 2 * (size_t)nseg_total * H * sizeof(int);                    // plan, redo flags
   return b;
 }
 

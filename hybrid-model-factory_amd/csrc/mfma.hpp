@@ -116,6 +116,42 @@ __device__ __forceinline__ float row16_sum(float x) {
   return x;
 }
 
+// Maximum over the wave of non-negative floats (compared as their bit patterns,
+// which order them; NaN and inf compare above every finite value): within each
+// DPP row by lane permutes, then across the four rows in scalar registers.  The
+// result is wave-uniform.
+__device__ __forceinline__ float wave_max_nonneg(float x) {
+  auto dpp = [](uint32_t v, int ctrl) -> uint32_t {
+    int r;
+    switch (ctrl) {
+      case 0: r = __builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false); break;
+      case 1: r = __builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false); break;
+      case 2: r = __builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false); break;
+      default: r = __builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false); break;
+    }
+    return (uint32_t)r;
+  };
+  uint32_t b = __builtin_bit_cast(uint32_t, x);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) b = max(b, dpp(b, i));
+  const uint32_t r0 = __builtin_amdgcn_readlane(b, 0), r1 = __builtin_amdgcn_readlane(b, 16);
+  const uint32_t r2 = __builtin_amdgcn_readlane(b, 32), r3 = __builtin_amdgcn_readlane(b, 48);
+  return __builtin_bit_cast(float, max(max(r0, r1), max(r2, r3)));
+}
+
+// The smallest e >= 0 with 2^-e m < 2^15 (m >= 0; inf and NaN act as 2^128):
+// scaling operands bounded by m by 2^-e keeps them inside fp16's range with a
+// factor-two margin, and the scaling is exact.  Integer work on a uniform m stays
+// in scalar registers.
+__device__ __forceinline__ int fp16_range_exp(float m) {
+  const int k = (int)((__builtin_bit_cast(uint32_t, m) >> 23) & 0xff) - 126;   // m < 2^k
+  return max(k, 15) - 15;
+}
+// 2^n as a float, for n in [-126, 127] (exact; no division or transcendental)
+__device__ __forceinline__ float pow2f(int n) {
+  return __builtin_bit_cast(float, (uint32_t)(127 + n) << 23);
+}
+
 // Inclusive prefix sum over lanes 0..31 (two DPP rows) with VALU lane shifts.
 #define HMX_DPP_F(v, ctrl, rmask) \
   __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, (v)), (ctrl), \

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define HMX_ABI_VERSION 8  /* 2: optional hmx_gated_norm output epilogue in the GDN ops;
+#define HMX_ABI_VERSION 9  /* 2: optional hmx_gated_norm output epilogue in the GDN ops;
                               3: q/k/v token strides in the GDN and GKA ops; slot-indexed
                               state pools and has_initial_state in the GDN, GKA and SSD
                               prefills;
@@ -37,7 +37,9 @@ extern "C" {
                                  GKA prefill / decode entry points;
                               8: N in hmx_gdn_train_bwd_workspace_bytes (the exact-run
                                  buffers are sized by the runs beyond each sequence's
-                                 first) */
+                                 first);
+                              9: hmx_gdn_chunk_workspace_bytes adds the per-walk fp16
+                                 range flags (any bf16 magnitude is supported) */
 
 enum hmx_status {
   HMX_OK = 0,
@@ -214,6 +216,10 @@ int hmx_plan_segments_bounds(int32_t op, const int64_t* bos_eos, int32_t nseq, i
  *    history is bounded below exp(-decay_threshold); otherwise the exact
  *    segment scan runs.
  *  workspace: device scratch of hmx_gdn_chunk_workspace_bytes(...) bytes.
+ *  Any finite bf16 v and f32/bf16 initial state is supported: a walk whose fp16
+ *  operands would leave fp16's range is detected and walked again with every
+ *  operand scaled by a power of two (exact), with keys of norm <= 1 (in-kernel L2
+ *  normalisation guarantees it), beta in [0, 2] and g <= 0.
  *  o_norm: NULL, or the output gated RMSNorm applied in the op's epilogue.
  * Replaces: chunk_gated_delta_rule_gqa
  *   vllm-inference/src/primed_vllm/gdn/ops/chunk_gqa.py:15-83 (and its kernels

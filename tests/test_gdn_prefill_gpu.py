@@ -321,3 +321,38 @@ def test_prefill_rows_outside_fp16_range(dev, seg):
     assert k.float().abs().max() > 65504 and q.float().abs().max() > 65504
     h0 = torch.randn(1, 4, 128, 128, generator=g0) * 0.05
     _check(dev, q, k, v, g, beta, h0=h0, seg=seg)
+
+
+@pytest.mark.parametrize("case", ["uniform", "uniform_seg", "weak_decay_exact", "spike"])
+def test_prefill_values_outside_fp16_range(dev, case):
+    """bf16 values (and an initial state) far outside fp16's range: the walk scales
+    its fp16 operands per wave by a power of two from a running bound on the state's
+    column norms, so the result is the same computation at any magnitude.
+
+    uniform*: v and h0 multiplied by 2^17 (|v| up to ~6e5) - the outputs and state
+    divided by 2^17 (exact in bf16 / fp32) meet the ordinary tolerances; single
+    walk, split into warm-up segments, and weak decay through the exact segment
+    scan (where the state grows over the whole sequence).  spike: one chunk's values
+    at 2^20 (~1e6) between ordinary chunks, so the scale drops and recovers within
+    one walk; compared at the spike's magnitude."""
+    gs = dict(gscale=0.1, gshift=7.0) if case == "weak_decay_exact" else {}
+    q, k, v, g, beta, g0 = _mk(1, 64 * 5 + 9, 4, 2, 41, **gs)
+    h0 = torch.randn(1, 4, 128, 128, generator=g0) * 0.05
+    if case == "spike":
+        a = 2.0 ** 20
+        v = v.float()
+        v[0, 96:128] *= a
+        v = v.bfloat16()
+    else:
+        a = 2.0 ** 17
+        v = (v.float() * a).bfloat16()
+        h0 = h0 * a
+    assert v.float().abs().max() > 65504 * 4
+    seg = {"uniform": None, "spike": None}.get(case, 2)
+    o_ref, s_ref = ref.chunk_gated_delta_rule_gqa(q, k, v, g, beta, initial_state=h0,
+                                                 output_final_state=True,
+                                                 use_qk_l2norm_in_kernel=True)
+    o, s = _run(dev, q, k, v, g, beta, h0=h0, seg=seg)
+    assert torch.isfinite(o.float()).all() and torch.isfinite(s).all()
+    assert_out_close(o / a, o_ref / a)     # a is a power of two: the division is exact
+    assert_state_close(s / a, s_ref / a)
