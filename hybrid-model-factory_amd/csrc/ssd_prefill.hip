@@ -78,6 +78,7 @@ struct Params {
   float* ws_loc;           // [nseg][H][P][N] zero-start segment end states
   float* ws_s0;            // [nseg][H][P][N] segment start states
   float* ws_dec;           // [nseg][H] segment log-decay sum_t a_t
+  int* redo;               // [nseg][H]: 1 where the pass's walk left fp16's range
   // x has HX heads and C has GC groups, B has G groups (each divides H): head h
   // reads x head h / (H/HX), B group h / (H/G) and C group h / (H/GC).
   int H, HX, G, GC, softplus;
@@ -104,9 +105,12 @@ struct Cfg {
   static constexpr int OFF_Y = OFF_M + L * LDM * 2;
   static constexpr int SMEM_LOCAL = OFF_C;              // x, B, scalars
   static constexpr int SMEM_OUT = OFF_Y + L * LDX * 2;
+  static constexpr int OFF_ML = SMEM_OUT;               // bf16 [L][L] M's low parts (SAFE)
+  static constexpr int SMEM_OUT_SAFE = OFF_ML + L * LDM * 2;
   // two workgroups per CU, except the OUT pass at P = 128 (one; see the kernel)
   static_assert(SMEM_LOCAL <= 80 * 1024, "LDS budget: two workgroups per CU");
   static_assert(SMEM_OUT <= (P == 128 ? 160 : 80) * 1024, "LDS budget");
+  static_assert(SMEM_OUT_SAFE <= (P == 128 ? 160 : 80) * 1024, "LDS budget");
   static_assert(P % 64 == 0 && N % 32 == 0, "tile shape");
 };
 
@@ -165,6 +169,11 @@ __device__ __forceinline__ void load_raw(Raw<P, N>& r, const Params& p, int tok0
     r.dt = t < nval ? ld_any(p.dt, (int64_t)(tok0 + t) * p.dt_ts + h * p.dt_hs, p.dt_dt) : 0.f;
 }
 
+// bf16 rows staged as they are (the SAFE pass): the 16-bit loads of the fp16 path
+// move them unchanged
+__device__ __forceinline__ f16x8 bits_h8(const bf16x8& x) { return __builtin_bit_cast(f16x8, x); }
+__device__ __forceinline__ bf16x8 bits_b8(const f16x8& x) { return __builtin_bit_cast(bf16x8, x); }
+
 __device__ __forceinline__ f16x8 to_h8(const bf16x8& x) {
   f16x8 y;
 #pragma unroll
@@ -175,17 +184,27 @@ __device__ __forceinline__ f16x8 to_h8(const bf16x8& x) {
 // Two workgroups per CU, except the OUT pass at P = 128: its 128x128 state needs
 // more than 256 registers, which at two waves per SIMD spill; at one wave per
 // SIMD it keeps them in VGPRs + AGPRs.
-template <int P, int N, int MODE>
+//
+// fp16 range.  The plain pass (SAFE false) rounds x, B, C, the state, M and w x to
+// fp16 as they are; an entry past fp16's range becomes inf, which reaches the end
+// state (x, B, w x) or y (C, M, the state's copy): the pass sums both and, when
+// the sum is not finite, writes no end state and sets the walk's redo flag.  The
+// SAFE pass walks the flagged ones again with bf16 operands: x, B and C as they
+// are (exact), the state, M and w x as bf16 hi + lo pairs (~16 significant bits,
+// two MFMAs per product), so any finite input stays in range.
+template <int P, int N, int MODE, bool SAFE>
 __global__ __launch_bounds__(NTHR, (P == 128 && MODE == MODE_OUT) ? 1 : 2) void ssd_chunk_kernel(Params p) {
   using K = Cfg<P, N>;
   constexpr int LDX = K::LDX, LDB = K::LDB, LDM = K::LDM, PB = K::PB, NB = K::NB;
-  __shared__ __align__(16) unsigned char smem[MODE == MODE_OUT ? K::SMEM_OUT : K::SMEM_LOCAL];
+  __shared__ __align__(16) unsigned char
+      smem[MODE == MODE_OUT ? (SAFE ? K::SMEM_OUT_SAFE : K::SMEM_OUT) : K::SMEM_LOCAL];
   f16* sX = reinterpret_cast<f16*>(smem + K::OFF_X);
   f16* sB = reinterpret_cast<f16*>(smem + K::OFF_B);
   float* sc = reinterpret_cast<float*>(smem + K::OFF_S);
   f16* sC = reinterpret_cast<f16*>(smem + K::OFF_C);     // OUT only
   f16* sM = reinterpret_cast<f16*>(smem + K::OFF_M);     // OUT only
   bf16* sY = reinterpret_cast<bf16*>(smem + K::OFF_Y);   // OUT only
+  f16* sML = reinterpret_cast<f16*>(smem + K::OFF_ML);   // OUT, SAFE only
   // per-token scalars, double-buffered by chunk parity: SC(buf, slot, t)
   auto SC = [&](int buf, int slot, int t) -> float& { return sc[(buf * 4 + slot) * L + t]; };
   auto SC4 = [&](int buf, int slot, int t) -> f32x4 {
@@ -202,7 +221,11 @@ __global__ __launch_bounds__(NTHR, (P == 128 && MODE == MODE_OUT) ? 1 : 2) void 
   const int s_id = sg / G, g = sg % G, h = g * HG + id / (p.nseg_total * G);
   const int hx = h / (H / p.HX), gc = h / (H / p.GC);
   const SegInfo si = load_seg(p.seg, s_id);
-  if (MODE == MODE_LOCAL && si.seg_idx == si.nseg - 1) return;
+  if (MODE == MODE_LOCAL && si.seg_idx == si.nseg - 1) {
+    if (!SAFE && tid == 0) p.redo[s_id * H + h] = 0;   // no LOCAL walk here
+    return;
+  }
+  if (SAFE && !p.redo[s_id * H + h]) return;
 
   const float A_h = p.A[h];
   const float bias = p.dt_bias ? p.dt_bias[h] : 0.f;
@@ -270,14 +293,22 @@ __global__ __launch_bounds__(NTHR, (P == 128 && MODE == MODE_OUT) ? 1 : 2) void 
   };
   if (si.c_start < si.c_end && wave == NTHR / 64 - 1) make_scalars(ra.dt, si.c_start, 0);
 
-  // coalesced store of the y tile staged in sY (chunk starting at tok0)
+  // coalesced store of the y tile staged in sY (chunk starting at tok0); the plain
+  // pass also sums the rows (ysum: inf or NaN there flags the walk)
+  float ysum = 0.f;
   const auto store_y = [&](int tok0, int nval) {
 #pragma unroll
     for (int i = 0; i < K::VX; ++i) {
       const int e = tid + NTHR * i, row = e / (P / 8), c8 = (e % (P / 8)) * 8;
+      const bf16x8 yr = *reinterpret_cast<const bf16x8*>(sY + row * LDX + c8);
+      if constexpr (!SAFE) {
+#pragma unroll
+        for (int j = 0; j < 8; j += 2)
+          ysum = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{yr[j], yr[j + 1]},
+                                                  bf16x2{(bf16)1.f, (bf16)1.f}, ysum, false);
+      }
       if (row < nval)
-        *reinterpret_cast<bf16x8*>(p.y + (int64_t)(tok0 + row) * p.y_ts + h * p.y_hs + c8) =
-            *reinterpret_cast<const bf16x8*>(sY + row * LDX + c8);
+        *reinterpret_cast<bf16x8*>(p.y + (int64_t)(tok0 + row) * p.y_ts + h * p.y_hs + c8) = yr;
     }
   };
 
@@ -290,13 +321,14 @@ __global__ __launch_bounds__(NTHR, (P == 128 && MODE == MODE_OUT) ? 1 : 2) void 
 #pragma unroll
     for (int i = 0; i < K::VX; ++i) {
       const int e = tid + NTHR * i, row = e / (P / 8), c8 = (e % (P / 8)) * 8;
-      *reinterpret_cast<f16x8*>(sX + row * LDX + c8) = to_h8(cur.x[i]);
+      *reinterpret_cast<f16x8*>(sX + row * LDX + c8) = SAFE ? bits_h8(cur.x[i]) : to_h8(cur.x[i]);
     }
 #pragma unroll
     for (int i = 0; i < K::VB; ++i) {
       const int e = tid + NTHR * i, row = e / (N / 8), c8 = (e % (N / 8)) * 8;
-      store8_i(sB + row * LDB, c8, to_h8(cur.b[i]));
-      if (MODE == MODE_OUT) store8_i(sC + row * LDB, c8, to_h8(cur.c[i]));
+      store8_i(sB + row * LDB, c8, SAFE ? bits_h8(cur.b[i]) : to_h8(cur.b[i]));
+      if (MODE == MODE_OUT)
+        store8_i(sC + row * LDB, c8, SAFE ? bits_h8(cur.c[i]) : to_h8(cur.c[i]));
     }
     if (MODE == MODE_OUT && c > si.c_start) store_y(tok0 - L, L);
     bf16x8 zst[K::VX];
@@ -336,14 +368,29 @@ __global__ __launch_bounds__(NTHR, (P == 128 && MODE == MODE_OUT) ? 1 : 2) void 
         for (int tb = 0; tb < 4; ++tb) YT[i][tb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < N / 32; ++ks) {
-        f16x8 sa[PB];
+        if constexpr (SAFE) {
+          bf16x8 sh[PB], sl[PB];
 #pragma unroll
-        for (int i = 0; i < PB; ++i) sa[i] = h8(ST[2 * ks][i], ST[2 * ks + 1][i]);
+          for (int i = 0; i < PB; ++i) pack_b_hilo(ST[2 * ks][i], ST[2 * ks + 1][i], sh[i], sl[i]);
 #pragma unroll
-        for (int tb = 0; tb < 4; ++tb) {
-          const f16x8 bc = frag_i(sC, LDB, 16 * tb, 32 * ks, lane);
+          for (int tb = 0; tb < 4; ++tb) {
+            const bf16x8 bc = bits_b8(frag_i(sC, LDB, 16 * tb, 32 * ks, lane));
 #pragma unroll
-          for (int i = 0; i < PB; ++i) YT[i][tb] = mfma16h(sa[i], bc, YT[i][tb]);
+            for (int i = 0; i < PB; ++i) {
+              YT[i][tb] = mfma16(sh[i], bc, YT[i][tb]);
+              YT[i][tb] = mfma16(sl[i], bc, YT[i][tb]);
+            }
+          }
+        } else {
+          f16x8 sa[PB];
+#pragma unroll
+          for (int i = 0; i < PB; ++i) sa[i] = h8(ST[2 * ks][i], ST[2 * ks + 1][i]);
+#pragma unroll
+          for (int tb = 0; tb < 4; ++tb) {
+            const f16x8 bc = frag_i(sC, LDB, 16 * tb, 32 * ks, lane);
+#pragma unroll
+            for (int i = 0; i < PB; ++i) YT[i][tb] = mfma16h(sa[i], bc, YT[i][tb]);
+          }
         }
       }
 #pragma unroll
@@ -371,21 +418,34 @@ __global__ __launch_bounds__(NTHR, (P == 128 && MODE == MODE_OUT) ? 1 : 2) void 
           if (tb < 0) continue;
           f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int ks = 0; ks < N / 32; ++ks)
-            acc = mfma16h(frag_i(sB, LDB, 16 * jb, 32 * ks, lane),
-                          frag_i(sC, LDB, 16 * tb, 32 * ks, lane), acc);
+          for (int ks = 0; ks < N / 32; ++ks) {
+            const f16x8 fb = frag_i(sB, LDB, 16 * jb, 32 * ks, lane);
+            const f16x8 fc = frag_i(sC, LDB, 16 * tb, 32 * ks, lane);
+            acc = SAFE ? mfma16(bits_b8(fb), bits_b8(fc), acc) : mfma16h(fb, fc, acc);
+          }
           const int t = 16 * tb + l16, j0 = 16 * jb + 4 * q4;
           const float at = SC(cb, S_ACS, t);
           const f32x4 aj = SC4(cb, S_ACS, j0), dj = SC4(cb, S_DT, j0);
           f32x4 m;
 #pragma unroll
           for (int v = 0; v < 4; ++v) m[v] = (t >= j0 + v) ? acc[v] * fast_exp(at - aj[v]) * dj[v] : 0.f;
-          *reinterpret_cast<f16x4*>(sM + t * LDM + icol(j0)) = h4(m);
+          if constexpr (SAFE) {
+            bf16x2 h01, l01, h23, l23;
+            split2(m[0], m[1], h01, l01);
+            split2(m[2], m[3], h23, l23);
+            *reinterpret_cast<bf16x4*>(sM + t * LDM + icol(j0)) =
+                bf16x4{h01[0], h01[1], h23[0], h23[1]};
+            *reinterpret_cast<bf16x4*>(sML + t * LDM + icol(j0)) =
+                bf16x4{l01[0], l01[1], l23[0], l23[1]};
+          } else {
+            *reinterpret_cast<f16x4*>(sM + t * LDM + icol(j0)) = h4(m);
+          }
         }
         if constexpr (W < 2) {
           constexpr int tb = W == 0 ? 0 : 2;
-          *reinterpret_cast<f16x4*>(sM + (16 * tb + l16) * LDM + icol(16 * (tb + 1) + 4 * q4)) =
-              f16x4{0.f, 0.f, 0.f, 0.f};
+          const int o = (16 * tb + l16) * LDM + icol(16 * (tb + 1) + 4 * q4);
+          *reinterpret_cast<f16x4*>(sM + o) = f16x4{0.f, 0.f, 0.f, 0.f};
+          if constexpr (SAFE) *reinterpret_cast<f16x4*>(sML + o) = f16x4{0.f, 0.f, 0.f, 0.f};
         }
       };
       using I0 = std::integral_constant<int, 0>;
@@ -416,19 +476,43 @@ __global__ __launch_bounds__(NTHR, (P == 128 && MODE == MODE_OUT) ? 1 : 2) void 
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         const f32x4 w0 = SC4(cb, S_W, 32 * ks + 4 * q4), w1 = SC4(cb, S_W, 32 * ks + 16 + 4 * q4);
-        f16x8 bw[PB];
+        if constexpr (SAFE) {
+          bf16x8 bh[PB], bl[PB];
 #pragma unroll
-        for (int i = 0; i < PB; ++i)
+          for (int i = 0; i < PB; ++i) {
+            const bf16x8 xb = bits_b8(xt[i][ks]);
+            f32x4 u0, u1;
 #pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            bw[i][v] = (f16)((float)xt[i][ks][v] * w0[v]);
-            bw[i][4 + v] = (f16)((float)xt[i][ks][4 + v] * w1[v]);
+            for (int v = 0; v < 4; ++v) {
+              u0[v] = (float)xb[v] * w0[v];
+              u1[v] = (float)xb[4 + v] * w1[v];
+            }
+            pack_b_hilo(u0, u1, bh[i], bl[i]);
           }
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-          const f16x8 a = frag_t_i(sB, LDB, 32 * ks, 16 * nb, lane);
+          for (int nb = 0; nb < NB; ++nb) {
+            const bf16x8 a = bits_b8(frag_t_i(sB, LDB, 32 * ks, 16 * nb, lane));
 #pragma unroll
-          for (int i = 0; i < PB; ++i) ST[nb][i] = mfma16h(a, bw[i], ST[nb][i]);
+            for (int i = 0; i < PB; ++i) {
+              ST[nb][i] = mfma16(a, bh[i], ST[nb][i]);
+              ST[nb][i] = mfma16(a, bl[i], ST[nb][i]);
+            }
+          }
+        } else {
+          f16x8 bw[PB];
+#pragma unroll
+          for (int i = 0; i < PB; ++i)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              bw[i][v] = (f16)((float)xt[i][ks][v] * w0[v]);
+              bw[i][4 + v] = (f16)((float)xt[i][ks][4 + v] * w1[v]);
+            }
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) {
+            const f16x8 a = frag_t_i(sB, LDB, 32 * ks, 16 * nb, lane);
+#pragma unroll
+            for (int i = 0; i < PB; ++i) ST[nb][i] = mfma16h(a, bw[i], ST[nb][i]);
+          }
         }
       }
     }
@@ -441,8 +525,17 @@ __global__ __launch_bounds__(NTHR, (P == 128 && MODE == MODE_OUT) ? 1 : 2) void 
 #pragma unroll
         for (int ks = 0; ks <= tb / 2; ++ks) {
           const f16x8 bm = frag_i(sM, LDM, 16 * tb, 32 * ks, lane);
+          if constexpr (SAFE) {
+            const bf16x8 bl = bits_b8(frag_i(sML, LDM, 16 * tb, 32 * ks, lane));
 #pragma unroll
-          for (int i = 0; i < PB; ++i) YT[i][tb] = mfma16h(xt[i][ks], bm, YT[i][tb]);
+            for (int i = 0; i < PB; ++i) {
+              YT[i][tb] = mfma16(bits_b8(xt[i][ks]), bits_b8(bm), YT[i][tb]);
+              YT[i][tb] = mfma16(bits_b8(xt[i][ks]), bl, YT[i][tb]);
+            }
+          } else {
+#pragma unroll
+            for (int i = 0; i < PB; ++i) YT[i][tb] = mfma16h(xt[i][ks], bm, YT[i][tb]);
+          }
         }
 #pragma unroll
       for (int i = 0; i < PB; ++i) {
@@ -453,12 +546,13 @@ __global__ __launch_bounds__(NTHR, (P == 128 && MODE == MODE_OUT) ? 1 : 2) void 
         for (int tb = 0; tb < 4; ++tb) {
           const int t = 16 * tb + l16;
           const f16x4 xv = *reinterpret_cast<const f16x4*>(sX + t * LDX + p0);
+          const bf16x4 xvb = __builtin_bit_cast(bf16x4, xv);
           bf16x4 zv;
           if (p.z) zv = *reinterpret_cast<const bf16x4*>(sY + t * LDX + p0);
           bf16x4 out;
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
-            float yv = YT[i][tb][v] + dv[v] * (float)xv[v];
+            float yv = YT[i][tb][v] + dv[v] * (SAFE ? (float)xvb[v] : (float)xv[v]);
             if (p.z) {
               const float zz = (float)zv[v];
               yv *= zz / (1.f + fast_exp(-zz));
@@ -481,6 +575,23 @@ __global__ __launch_bounds__(NTHR, (P == 128 && MODE == MODE_OUT) ? 1 : 2) void 
     for (int c = si.c_start; c < si.c_end; ++c) chunk(ra, ra, c);
   }
   if (MODE == MODE_OUT && si.c_start < si.c_end) store_y(si.bos + (si.c_end - 1) * L, nval_of(si.c_end - 1));
+
+  // ---- plain pass: did an fp16 operand leave its range? ----------------------------
+  if constexpr (!SAFE) {
+    float acc = ysum;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int i = 0; i < PB; ++i)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc += ST[nb][i][v];
+    int* flag = reinterpret_cast<int*>(sc);   // the scalar buffers are free after the loop
+    if (lane == 0) flag[wave] = __ballot(!__builtin_isfinite(acc)) != 0;
+    lds_barrier();
+    const int redo = flag[0] | flag[1] | flag[2] | flag[3];
+    if (tid == 0) p.redo[s_id * H + h] = redo;
+    if (redo) return;   // walked again by the SAFE pass (the end state is not written)
+  }
 
   // ---- segment end state --------------------------------------------------------
   float* dst = nullptr;
@@ -535,16 +646,19 @@ __global__ __launch_bounds__(256) void ssd_seg_combine_kernel(Params p, int PN) 
   }
 }
 
+// Each pass, then its flagged walks again with bf16 operands (SAFE).
 template <int P, int N>
 void launch(const Params& p, int nseq, hipStream_t s) {
   const bool multi = p.nseg_total > nseq;
   const dim3 grid(p.nseg_total * p.H);
   if (multi) {
-    hipLaunchKernelGGL((ssd_chunk_kernel<P, N, MODE_LOCAL>), grid, dim3(NTHR), 0, s, p);
+    hipLaunchKernelGGL((ssd_chunk_kernel<P, N, MODE_LOCAL, false>), grid, dim3(NTHR), 0, s, p);
+    hipLaunchKernelGGL((ssd_chunk_kernel<P, N, MODE_LOCAL, true>), grid, dim3(NTHR), 0, s, p);
     hipLaunchKernelGGL(ssd_seg_combine_kernel, dim3(nseq * p.H, (P * N + 1023) / 1024), dim3(256),
                        0, s, p, P * N);
   }
-  hipLaunchKernelGGL((ssd_chunk_kernel<P, N, MODE_OUT>), grid, dim3(NTHR), 0, s, p);
+  hipLaunchKernelGGL((ssd_chunk_kernel<P, N, MODE_OUT, false>), grid, dim3(NTHR), 0, s, p);
+  hipLaunchKernelGGL((ssd_chunk_kernel<P, N, MODE_OUT, true>), grid, dim3(NTHR), 0, s, p);
 }
 
 }  // namespace ssd
@@ -555,9 +669,10 @@ using namespace hmx::ssd;
 
 extern "C" size_t hmx_ssd_chunk_workspace_bytes(int32_t nseg_total, int32_t nseq, int32_t H,
                                                 int32_t P, int32_t N) {
-  if (nseg_total <= nseq) return 16;
+  const size_t flags = (size_t)nseg_total * H * sizeof(int);   // redo flags
+  if (nseg_total <= nseq) return flags;
   const size_t st = (size_t)nseg_total * H * P * N * sizeof(float);
-  return 2 * st + (size_t)nseg_total * H * sizeof(float);
+  return 2 * st + (size_t)nseg_total * H * sizeof(float) + flags;
 }
 
 extern "C" int hmx_ssd_chunk_fwd(const void* x, int64_t x_ts, int64_t x_hs, const void* B,
@@ -613,6 +728,7 @@ extern "C" int hmx_ssd_chunk_fwd(const void* x, int64_t x_ts, int64_t x_hs, cons
   p.ws_loc = multi ? ws : nullptr;
   p.ws_s0 = multi ? ws + st : nullptr;
   p.ws_dec = multi ? ws + 2 * st : nullptr;
+  p.redo = reinterpret_cast<int*>(multi ? ws + 2 * st + (size_t)nseg_total * H : ws);
   p.H = H; p.HX = HX; p.G = G; p.GC = GC; p.softplus = dt_softplus; p.dt_min = dt_min; p.dt_max = dt_max;
   hipStream_t s = (hipStream_t)stream;
   if (P == 64 && N == 128) launch<64, 128>(p, nseq, s);

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define HMX_ABI_VERSION 9  /* 2: optional hmx_gated_norm output epilogue in the GDN ops;
+#define HMX_ABI_VERSION 10  /* 2: optional hmx_gated_norm output epilogue in the GDN ops;
                               3: q/k/v token strides in the GDN and GKA ops; slot-indexed
                               state pools and has_initial_state in the GDN, GKA and SSD
                               prefills;
@@ -39,7 +39,9 @@ extern "C" {
                                  buffers are sized by the runs beyond each sequence's
                                  first);
                               9: hmx_gdn_chunk_workspace_bytes adds the per-walk fp16
-                                 range flags (any bf16 magnitude is supported) */
+                                 range flags (any bf16 magnitude is supported);
+                              10: the same in hmx_ssd_chunk_workspace_bytes (nonzero for
+                                  one segment per sequence too) */
 
 enum hmx_status {
   HMX_OK = 0,
@@ -529,6 +531,9 @@ size_t hmx_gka_train_bwd_workspace_bytes(int32_t nblock_total, int32_t H, int64_
  *  (updated in place).  P, N in {64, 128}; token/head strides multiples of 8
  *  elements.
  * workspace: hmx_ssd_chunk_workspace_bytes(...) bytes of device scratch.
+ * Any finite bf16 x, B, C and f32/bf16 initial state is supported: a walk whose
+ *  fp16 operands would leave fp16's range is detected and walked again with bf16
+ *  operands (hi + lo pairs for the computed ones).
  * Replaces: mamba_chunk_scan_combined (mamba_ssm 2.3.0; call site
  *   training/src/hmf/model/hybrid_zoo/layers/mamba/mamba2.py:555-580) and
  *   mamba_chunk_scan_combined_varlen (vLLM 0.15.1; call site

@@ -318,3 +318,46 @@ def test_scan_split_fast_and_slow_decay_heads(dev, seg):
     assert_state_close(f, f_r, what="final_states")
     for hh in range(H):
         assert_out_close(y[:, :, hh], y_r[:, :, hh], what=f"y head {hh}")
+
+
+@pytest.mark.parametrize("case,seg", [("x", None), ("x", 2), ("B", None), ("C", 2),
+                                      ("state", None), ("spike", 2)])
+def test_scan_values_outside_fp16_range(dev, case, seg):
+    """bf16 x, B or C (or an initial state) far outside fp16's range: the plain pass
+    detects the overflow (inf reaches the end state or y) and the flagged walks run
+    again with bf16 operands, so the result is the same computation at any
+    magnitude.  The outputs and states divided by the scale a (a power of two:
+    exact) meet the ordinary tolerances; seg 2 splits the sequences (the LOCAL pass
+    and the combine see the large values too).  spike: one chunk of x at 2^20 between
+    ordinary ones."""
+    b, l, H, G, P, N = 2, 300, 4, 2, 64, 128
+    x, dt, A, B, C, D, bias, _, g0 = _inputs(b, l, H, G, P, N, 61)
+    h0 = torch.randn(b, H, P, N, generator=g0) * 0.1
+    a = 2.0 ** 17
+    if case == "x":
+        x, h0 = (x.float() * a).bfloat16(), h0 * a
+    elif case == "B":
+        B = (B.float() * a).bfloat16()
+    elif case == "C":
+        C = (C.float() * a).bfloat16()
+    elif case == "state":
+        a = 2.0 ** 20
+        h0 = h0 * a
+    else:
+        a = 2.0 ** 20
+        x = x.float()
+        x[:, 128:192] *= a
+        x = x.bfloat16()
+    big = max(x.float().abs().max(), B.float().abs().max(), C.float().abs().max(), h0.abs().max())
+    assert big > 65504 * 4
+    y_r, f_r = ref.mamba_chunk_scan_combined(x, dt, A, B, C, 256, D=D, dt_bias=bias,
+                                             initial_states=h0, dt_softplus=True,
+                                             return_final_states=True)
+    y, f = hmx.mamba_chunk_scan_combined(*_d(dev, x, dt, A, B, C), 256, D=D.to(dev),
+                                         dt_bias=bias.to(dev), initial_states=h0.to(dev),
+                                         dt_softplus=True, return_final_states=True,
+                                         _segment_chunks=seg)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y.float()).all() and torch.isfinite(f).all()
+    assert_out_close(y / a, y_r / a, what="y")      # a is a power of two: the division is exact
+    assert_state_close(f / a, f_r / a, what="final_states")
