@@ -63,6 +63,7 @@ struct Params {
   const uint8_t* has_init;            // per sequence, or null (none: every sequence starts from zeros)
   int dim, pad;
   int64_t tile0;                      // prefill: first token tile of this launch
+  const int32_t* nacc;                // speculative update: accepted tokens per sequence
 };
 
 // Taps of 8 channels; the window holds the W-1 inputs before the current one
@@ -314,6 +315,83 @@ __global__ __launch_bounds__(NT) void conv_update_kernel(Params p) {
   st8(srow + (int64_t)(L - 1) * p.st_row, xt);
 }
 
+// Speculative update (multi-token, vLLM's num_accepted_tokens convention): sequence
+// b's tokens [qs[b], qs[b+1]) continue the history whose last W-1 inputs are state
+// rows a-1 .. a+W-3, a = num_accepted_tokens[b] (the previous step's accepted
+// tokens; the rows after them are its rejected drafts).  Afterwards the state is
+// rows a .. a+L-n-1 followed by the n new inputs, so the next step's window again
+// starts at its accepted count minus one.  a is clamped to [1, L-W+2] and n to at
+// most L-W+2 (the rows the state holds), so every access stays inside the slot; the
+// token offsets are clamped to [0, total] (rows of x and out).
+template <typename T, int W, bool ACT>
+__global__ __launch_bounds__(NT) void conv_spec_update_kernel(Params p) {
+  const int c0 = (blockIdx.y * NT + threadIdx.x) * 8;
+  const int b = blockIdx.x;
+  if (c0 >= p.dim) return;
+  const int L = p.st_len;
+  const int64_t t0 = min(max((int64_t)p.qs[b], (int64_t)0), p.total);
+  const int64_t t1 = min(max((int64_t)p.qs[b + 1], t0), p.total);
+  const int n = (int)min(t1 - t0, (int64_t)(L - W + 2));
+  const int64_t slot = p.idx ? p.idx[b] : b;
+  const float zero[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (slot == p.pad) {   // padded entry: zero outputs, no state access
+    for (int t = 0; t < n; ++t) st8(static_cast<T*>(p.out) + (t0 + t) * p.os + c0, zero);
+    return;
+  }
+  const int a = min(max(p.nacc[b], 1), L - W + 2);
+  T* srow = static_cast<T*>(p.st) + slot * p.st_slot + c0;
+  float rows[8][8];   // the slot's L (<= 8) rows of these channels
+#pragma unroll
+  for (int r = 0; r < 8; ++r)
+    if (r < L) ld8(srow + (int64_t)r * p.st_row, rows[r]);
+  Taps<W, ACT> tp;
+  tp.load(p, c0);
+  float win[W - 1][8];
+#pragma unroll
+  for (int i = 0; i < W - 1; ++i)
+#pragma unroll
+    for (int r = 0; r < 8; ++r)
+      if (r == a - 1 + i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) win[i][j] = rows[r][j];
+  float xs[8][8];     // the new inputs, for the state (n <= 8)
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    if (t < n) {
+      ld8(static_cast<const T*>(p.x) + (t0 + t) * p.xs + c0, xs[t]);
+      float y[8];
+      tp.apply(win, xs[t], y);
+      st8(static_cast<T*>(p.out) + (t0 + t) * p.os + c0, y);
+#pragma unroll
+      for (int i = 0; i + 1 < W - 1; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) win[i][j] = win[i + 1][j];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) win[W - 2][j] = xs[t][j];
+    }
+  }
+  // new state: rows a .. a+L-n-1, then the n inputs
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    if (r >= L) continue;
+    float v[8];
+    if (r < L - n) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        if (q == a + r)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) v[j] = rows[q][j];
+    } else {
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+        if (t == r - (L - n))
+#pragma unroll
+          for (int j = 0; j < 8; ++j) v[j] = xs[t][j];
+    }
+    st8(srow + (int64_t)r * p.st_row, v);
+  }
+}
+
 template <typename T, int W, bool ACT>
 void launch_fwd_w(const Params& p, hipStream_t s) {
   const unsigned cg = (unsigned)((p.dim / 8 + NT - 1) / NT);
@@ -337,11 +415,21 @@ void launch_update_w(const Params& p, hipStream_t s) {
                      p);
 }
 
-template <typename T, bool UPDATE>
+template <typename T, int W, bool ACT>
+void launch_spec_w(const Params& p, hipStream_t s) {
+  const unsigned cg = (unsigned)((p.dim / 8 + NT - 1) / NT);
+  hipLaunchKernelGGL((conv_spec_update_kernel<T, W, ACT>), dim3((unsigned)p.batch, cg), dim3(NT), 0,
+                     s, p);
+}
+
+// KIND 0: prefill, 1: decode update, 2: speculative update
+template <typename T, int KIND>
 void dispatch(const Params& p, int W, int act, hipStream_t s) {
 #define HMX_CONV_CASE(WW, AA)                                            \
   if (W == WW && (act != 0) == AA) {                                      \
-    if (UPDATE) launch_update_w<T, WW, AA>(p, s); else launch_fwd_w<T, WW, AA>(p, s); \
+    if (KIND == 1) launch_update_w<T, WW, AA>(p, s);                      \
+    else if (KIND == 2) launch_spec_w<T, WW, AA>(p, s);                   \
+    else launch_fwd_w<T, WW, AA>(p, s);                                   \
     return;                                                               \
   }
   HMX_CONV_CASE(2, false) HMX_CONV_CASE(2, true) HMX_CONV_CASE(3, false)
@@ -401,9 +489,9 @@ extern "C" int hmx_causal_conv1d_fwd(const void* x, int64_t x_token_stride, void
            conv_states ? state_len : width - 1, query_start_loc, batch, total_tokens,
            cache_indices, has_initial_state, dim, pad_slot_id};
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == HMX_BF16) dispatch<bf16, false>(p, width, activation, s);
-  else if (dtype == HMX_F16) dispatch<f16, false>(p, width, activation, s);
-  else dispatch<float, false>(p, width, activation, s);
+  if (dtype == HMX_BF16) dispatch<bf16, 0>(p, width, activation, s);
+  else if (dtype == HMX_F16) dispatch<f16, 0>(p, width, activation, s);
+  else dispatch<float, 0>(p, width, activation, s);
   return check_launch("hmx_causal_conv1d_fwd");
 }
 
@@ -427,8 +515,33 @@ extern "C" int hmx_causal_conv1d_update(const void* x, int64_t x_token_stride, v
            conv_state, state_slot_stride, state_row_stride, state_len, nullptr, batch, batch,
            conv_state_indices, nullptr, dim, pad_slot_id};
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == HMX_BF16) dispatch<bf16, true>(p, width, activation, s);
-  else if (dtype == HMX_F16) dispatch<f16, true>(p, width, activation, s);
-  else dispatch<float, true>(p, width, activation, s);
+  if (dtype == HMX_BF16) dispatch<bf16, 1>(p, width, activation, s);
+  else if (dtype == HMX_F16) dispatch<f16, 1>(p, width, activation, s);
+  else dispatch<float, 1>(p, width, activation, s);
   return check_launch("hmx_causal_conv1d_update");
+}
+
+extern "C" int hmx_causal_conv1d_update_spec(
+    const void* x, int64_t x_token_stride, void* out, int64_t out_token_stride, int32_t dtype,
+    const void* weight, int32_t weight_dtype, int32_t width, const void* bias, int32_t bias_dtype,
+    void* conv_state, int64_t state_slot_stride, int64_t state_row_stride, int32_t state_len,
+    const int32_t* conv_state_indices, const int32_t* num_accepted_tokens,
+    const int32_t* query_start_loc, int32_t batch, int64_t total_tokens, int32_t dim,
+    int32_t activation, int32_t pad_slot_id, void* stream) {
+  const int rc = check_common("hmx_causal_conv1d_update_spec", x, out, weight, dtype, width, dim,
+                              state_len, weight_dtype, bias, bias_dtype, x_token_stride,
+                              out_token_stride, state_row_stride, state_slot_stride, conv_state);
+  if (rc != HMX_OK) return rc;
+  HMX_REQUIRE(batch >= 0, HMX_EINVAL, "hmx_causal_conv1d_update_spec: batch %d", batch);
+  if (batch == 0) return HMX_OK;
+  HMX_REQUIRE(x && out && weight && conv_state && num_accepted_tokens && query_start_loc,
+              HMX_EINVAL, "hmx_causal_conv1d_update_spec: null pointer");
+  Params p{x, x_token_stride, out, out_token_stride, weight, weight_dtype, bias, bias_dtype,
+           conv_state, state_slot_stride, state_row_stride, state_len, query_start_loc, batch,
+           total_tokens, conv_state_indices, nullptr, dim, pad_slot_id, 0, num_accepted_tokens};
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == HMX_BF16) dispatch<bf16, 2>(p, width, activation, s);
+  else if (dtype == HMX_F16) dispatch<f16, 2>(p, width, activation, s);
+  else dispatch<float, 2>(p, width, activation, s);
+  return check_launch("hmx_causal_conv1d_update_spec");
 }

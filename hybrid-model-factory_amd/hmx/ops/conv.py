@@ -12,8 +12,10 @@ Per channel,
 
 with positions before a sequence's first token taken from its state (zeros
 without an initial state); the state then holds the sequence's last state_len
-inputs.  Speculative decoding (``num_accepted_tokens``) and prefix-cache block
-arguments are not supported (NotImplementedError).
+inputs.  Speculative decoding (``num_accepted_tokens`` with ``query_start_loc``) runs
+several tokens per sequence against a state with draft slack (see
+``causal_conv1d_update``); prefix-cache block arguments are not supported
+(NotImplementedError).
 """
 from __future__ import annotations
 
@@ -148,11 +150,23 @@ def causal_conv1d_update(x: torch.Tensor, conv_state: torch.Tensor, weight: torc
     ``conv_state`` [slots, dim, state_len] (channels contiguous; updated in place:
     the state shifts by one position).  Returns [batch, dim]; padded entries (slot ==
     pad_slot_id) give 0.  ``out`` [batch, dim] (keyword-only, no reference
-    counterpart) receives the rows when given."""
-    if num_accepted_tokens is not None or query_start_loc is not None:
-        raise NotImplementedError("speculative multi-token causal_conv1d_update")
+    counterpart) receives the rows when given.
+
+    Speculative form (``num_accepted_tokens`` and ``query_start_loc`` given, as
+    primed_gdn_layer.py:700-712 calls it): x is [tokens, dim], sequence b owning
+    rows query_start_loc[b] .. query_start_loc[b+1]-1 (at most state_len - width + 2
+    of them).  With a = num_accepted_tokens[b] (the previous step's accepted tokens)
+    the window before its first token is state positions a-1 .. a+width-3; the slot
+    then holds positions a .. a+state_len-n-1 followed by the n new inputs, so the
+    next step's window ends at its last accepted input.  vLLM's kernel is not
+    vendored: this position arithmetic is pinned by the invariant that a speculative
+    step followed by a step accepting a tokens computes the plain causal convolution
+    over the accepted inputs (tests/test_conv_gpu.py)."""
     if block_idx_last_scheduled_token is not None or initial_state_idx is not None:
         raise NotImplementedError("prefix-cache block arguments of causal_conv1d_update")
+    if num_accepted_tokens is not None or query_start_loc is not None:
+        return _update_spec(x, conv_state, weight, bias, activation, conv_state_indices,
+                            num_accepted_tokens, query_start_loc, pad_slot_id, out)
     _lib.require_gpu(x, conv_state, weight, bias, conv_state_indices)
     if x.dim() != 2:
         raise NotImplementedError(f"x must be [batch, dim], got {tuple(x.shape)}")
@@ -169,4 +183,35 @@ def causal_conv1d_update(x: torch.Tensor, conv_state: torch.Tensor, weight: torc
               0 if b is None else _lib.dtype_code(b), _lib.ptr(conv_state), sst, srs, st_len,
               _lib.ptr(_i32(conv_state_indices)),
               batch, dim, _act(activation), int(pad_slot_id), _lib.stream_of(x))
+    return out
+
+
+def _update_spec(x, conv_state, weight, bias, activation, conv_state_indices,
+                 num_accepted_tokens, query_start_loc, pad_slot_id, out):
+    if num_accepted_tokens is None or query_start_loc is None:
+        raise ValueError("the speculative causal_conv1d_update needs both num_accepted_tokens "
+                         "and query_start_loc")
+    _lib.require_gpu(x, conv_state, weight, bias, conv_state_indices, num_accepted_tokens,
+                     query_start_loc)
+    if x.dim() != 2:
+        raise NotImplementedError(f"x must be [tokens, dim], got {tuple(x.shape)}")
+    tokens, dim = x.shape
+    batch = query_start_loc.numel() - 1
+    if num_accepted_tokens.numel() < batch or (conv_state_indices is not None and
+                                               conv_state_indices.numel() < batch):
+        raise ValueError(f"num_accepted_tokens / conv_state_indices need {batch} entries")
+    W = weight.shape[-1]
+    if weight.shape != (dim, W):
+        raise ValueError(f"weight must be [{dim}, width], got {tuple(weight.shape)}")
+    st_len, sst, srs = _pool(conv_state, dim, x.dtype, "conv_state")
+    xr = _rows(x)
+    out = _out_rows(out, tokens, dim, x)
+    w, b = _aligned(weight), _aligned(bias)
+    _lib.call("hmx_causal_conv1d_update_spec", _lib.ptr(xr), xr.stride(0), _lib.ptr(out),
+              out.stride(0), _lib.dtype_code(x), _lib.ptr(w), _lib.dtype_code(w), W, _lib.ptr(b),
+              0 if b is None else _lib.dtype_code(b), _lib.ptr(conv_state), sst, srs, st_len,
+              _lib.ptr(_i32(conv_state_indices)), _lib.ptr(_i32(num_accepted_tokens)),
+              _lib.ptr(_i32(query_start_loc)), batch, tokens, dim, _act(activation),
+              int(pad_slot_id),
+              _lib.stream_of(x))
     return out

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define HMX_ABI_VERSION 10  /* 2: optional hmx_gated_norm output epilogue in the GDN ops;
+#define HMX_ABI_VERSION 11  /* 2: optional hmx_gated_norm output epilogue in the GDN ops;
                               3: q/k/v token strides in the GDN and GKA ops; slot-indexed
                               state pools and has_initial_state in the GDN, GKA and SSD
                               prefills;
@@ -41,7 +41,9 @@ extern "C" {
                               9: hmx_gdn_chunk_workspace_bytes adds the per-walk fp16
                                  range flags (any bf16 magnitude is supported);
                               10: the same in hmx_ssd_chunk_workspace_bytes (nonzero for
-                                  one segment per sequence too) */
+                                  one segment per sequence too);
+                              11: hmx_causal_conv1d_update_spec (speculative multi-token
+                                  conv update) */
 
 enum hmx_status {
   HMX_OK = 0,
@@ -644,8 +646,8 @@ int hmx_causal_conv1d_fwd(const void* x, int64_t x_token_stride, void* out,
  * (or b) followed by x[b]; the state then shifts by one row with x[b] appended.
  * Padded entries (slot == pad_slot_id) write 0 and leave the pool alone.
  * Replaces: causal_conv1d_update (vLLM, un-vendored; called at
- *   vllm-inference/src/primed_vllm/primed_gdn_layer.py:735-743, :775-785), without
- *   its speculative multi-token form.
+ *   vllm-inference/src/primed_vllm/primed_gdn_layer.py:735-743, :775-785); the
+ *   speculative multi-token form is hmx_causal_conv1d_update_spec.
  */
 int hmx_causal_conv1d_update(const void* x, int64_t x_token_stride, void* out,
                              int64_t out_token_stride, int32_t dtype, const void* weight,
@@ -654,6 +656,35 @@ int hmx_causal_conv1d_update(const void* x, int64_t x_token_stride, void* out,
                              int64_t state_row_stride, int32_t state_len,
                              const int32_t* conv_state_indices, int32_t batch, int32_t dim,
                              int32_t activation, int32_t pad_slot_id, void* stream);
+
+/*
+ * The speculative multi-token form: sequence b's tokens are rows
+ * query_start_loc[b] .. query_start_loc[b+1]-1 of x / out (offsets clamped to
+ * [0, total_tokens]; at most state_len - width + 2 of them are processed), against slot
+ * conv_state_indices[b] (or b).  With a = num_accepted_tokens[b] (the previous
+ * step's accepted tokens, clamped to [1, state_len - width + 2]) the window before
+ * the first token is state rows a-1 .. a+width-3; afterwards the slot holds rows
+ * a .. a+state_len-n-1 followed by the n new inputs, so the next step's window
+ * again ends at its last accepted input.  Padded entries (slot == pad_slot_id)
+ * write 0 and leave the pool alone.
+ * Replaces: causal_conv1d_update with num_accepted_tokens / query_start_loc / max_query_len
+ *   (vLLM, un-vendored; called at
+ *   vllm-inference/src/primed_vllm/primed_gdn_layer.py:700-712,
+ *   primed_gka_layer.py:1029-1040).  vLLM's state rows are not vendored here: the
+ *   row arithmetic above is pinned by the invariant that a speculative step followed
+ *   by a step accepting a tokens computes the plain causal convolution over the
+ *   accepted inputs.
+ */
+int hmx_causal_conv1d_update_spec(const void* x, int64_t x_token_stride, void* out,
+                                  int64_t out_token_stride, int32_t dtype, const void* weight,
+                                  int32_t weight_dtype, int32_t width, const void* bias,
+                                  int32_t bias_dtype, void* conv_state, int64_t state_slot_stride,
+                                  int64_t state_row_stride, int32_t state_len,
+                                  const int32_t* conv_state_indices,
+                                  const int32_t* num_accepted_tokens,
+                                  const int32_t* query_start_loc, int32_t batch,
+                                  int64_t total_tokens, int32_t dim, int32_t activation,
+                                  int32_t pad_slot_id, void* stream);
 
 #ifdef __cplusplus
 }

@@ -160,7 +160,7 @@ def test_errors(dev):
     x = torch.zeros(8, 64, dtype=torch.bfloat16, device=dev)
     w = torch.zeros(64, 4, device=dev)
     pool = torch.zeros(2, 3, 64, dtype=torch.bfloat16, device=dev).transpose(1, 2)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(ValueError):   # the speculative form needs query_start_loc as well
         hmx.causal_conv1d_update(x, pool, w, num_accepted_tokens=torch.ones(8, device=dev))
     with pytest.raises(NotImplementedError):
         hmx.causal_conv1d_fn(x.t(), torch.zeros(64, 5, device=dev))    # width 5
@@ -190,3 +190,53 @@ def test_prefill_more_tiles_than_one_launch(dev):
     torch.cuda.synchronize()
     _close(out.t(), out_r)
     assert torch.equal(pool_d.cpu(), pool_r.to(pool.dtype))
+
+
+@pytest.mark.parametrize("W,L,act", [(4, 6, "silu"), (3, 5, None), (2, 4, "silu"), (4, 8, "silu")])
+def test_update_spec_accepts_like_plain_conv(dev, W, L, act):
+    """Speculative multi-token update (num_accepted_tokens, query_start_loc): every
+    step carries 1 + L - W + 1 tokens per sequence (the draft slack the state holds).
+    Step 1 from a random state with any accepted count a1: its window is state rows
+    a1-1 .. a1+W-3, its outputs the plain causal conv over that window and the
+    tokens, and its state the kept rows followed by the inputs.  Step 2 accepting a2
+    of step 1's tokens then equals the plain conv over (window, the a2 accepted
+    inputs, the new tokens) - the invariant that pins vLLM's un-vendored row
+    arithmetic.  A padded sequence writes 0 and leaves the pool alone."""
+    S1 = L - W + 2
+    dim, slots = 64, 6
+    g = torch.Generator().manual_seed(900 + 10 * W + L)
+    idx = torch.tensor([4, 0, 2, -1], dtype=torch.int32)
+    N = idx.numel()
+    qs = torch.arange(0, N * S1 + 1, S1, dtype=torch.int32)
+    pool = torch.randn(slots, L, dim, generator=g).bfloat16()
+    w = torch.randn(dim, W, generator=g) * 0.5
+    b = torch.randn(dim, generator=g) * 0.1
+    a1 = torch.tensor([1, S1, min(2, S1), 1], dtype=torch.int32)
+    a2 = torch.tensor([S1, 1, min(2, S1), 1], dtype=torch.int32)
+    x1 = torch.randn(N * S1, dim, generator=g).bfloat16()
+    x2 = torch.randn(N * S1, dim, generator=g).bfloat16()
+    pool_d = pool.to(dev)
+    view = pool_d.transpose(1, 2)
+    o1 = hmx.causal_conv1d_update(x1.to(dev), view, w.to(dev), b.to(dev), act,
+                                  conv_state_indices=idx.to(dev), num_accepted_tokens=a1.to(dev),
+                                  query_start_loc=qs.to(dev), max_query_len=S1)
+    st1 = pool_d.cpu()
+    o2 = hmx.causal_conv1d_update(x2.to(dev), view, w.to(dev), b.to(dev), act,
+                                  conv_state_indices=idx.to(dev), num_accepted_tokens=a2.to(dev),
+                                  query_start_loc=qs.to(dev), max_query_len=S1)
+    torch.cuda.synchronize()
+    for n in range(N):
+        r = slice(int(qs[n]), int(qs[n + 1]))
+        if int(idx[n]) < 0:
+            assert (o1[r] == 0).all() and (o2[r] == 0).all()
+            continue
+        slot, a = int(idx[n]), int(a1[n])
+        win1 = pool[slot, a - 1:a + W - 2]
+        o_r, _ = ref.conv_sequence(x1[r], win1, w, b, act)
+        _close(o1[r], o_r)
+        assert torch.equal(st1[slot], torch.cat([pool[slot, a:a + L - S1], x1[r]]))
+        hist = torch.cat([win1, x1[r][:int(a2[n])]])           # accept a2 of step 1's tokens
+        o_r2, _ = ref.conv_sequence(x2[r], hist[-(W - 1):], w, b, act)
+        _close(o2[r], o_r2)
+    untouched = [s for s in range(slots) if s not in set(int(i) for i in idx if i >= 0)]
+    assert torch.equal(st1[untouched], pool[untouched])
