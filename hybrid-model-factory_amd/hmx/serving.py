@@ -5,8 +5,9 @@ These restate ``PrimedGatedDeltaNetAttention._forward_core``
 (vllm-inference/src/primed_vllm/primed_gdn_layer.py:635-936) and
 ``PrimedGKAAttention._forward_core`` (primed_gka_layer.py:962-1338) for the
 non-speculative batches (pure decode, pure prefill, and mixed batches with the
-decodes first), with the same inputs and the same effect: ``core_attn_out`` rows
-written, the conv and recurrent state pools updated in place.  Compared with the
+decodes first) and the speculative ones (``spec_sequence_masks``), with the same
+inputs and the same effect: ``core_attn_out`` rows written, the conv and recurrent
+state pools updated in place.  Compared with the
 reference sequence of calls they drop every copy around the ops:
 
 - the decode and prefill convs write one buffer (no ``torch.cat``);
@@ -40,7 +41,19 @@ With the low-rank k/v projection (``proj_k``, ``proj_v`` and the optional
 learnable residual mixes ``k_rep`` / ``v_rep``), k and v are upsampled to the
 query heads before the ops, as the layers' rearrange step does (a library GEMM
 through the layer's own modules plus the residual); it needs ``tp_size == 1``.
-Speculative decoding (``spec_sequence_masks``) raises NotImplementedError.
+
+Speculative batches follow primed_gdn_layer.py:686-712 / :819-836 and
+primed_gka_layer.py:1017-1040 / :1185-1205: the spec tokens' conv is the
+speculative ``causal_conv1d_update`` (slot ``spec_state_indices_tensor[:, 0]``,
+``num_accepted_tokens``), then GDN's recurrent decode reads slot
+``spec_state_indices_tensor[n, num_accepted_tokens[n] - 1]`` and leaves the state
+after the sequence's last token in slot ``[n, 0]`` (fused_recurrent_gqa.py:95-105,
+:135-144); GKA's decode, as the reference's, advances each spec sequence by its
+first token only (slot ``[n, 0]``).  With non-spec
+tokens in the batch too, each part runs on its index-selected rows and the outputs
+return by index (the reference's ``index_copy_``, :923-934); the host offsets
+(``query_start_loc_cpu``) then describe the whole batch, not the non-spec prefill,
+and are not used.
 
 ``mamba2_conv_ssm_forward`` restates ``PrimedMamba2Layer.conv_ssm_forward``
 (primed_mamba2_layer.py:615-1021) the same way: the decode and prefill convs write
@@ -61,9 +74,6 @@ from . import ops
 
 
 def _check(layer, md):
-    if md.spec_sequence_masks is not None:
-        raise NotImplementedError("speculative decoding batches (spec_sequence_masks) are not "
-                                  "supported by the hmx mixer cores")
     if getattr(layer, "proj_k", None) is not None and layer.tp_size != 1:
         raise NotImplementedError("the low-rank k/v projection needs the k/v all-gather of "
                                   "tensor parallelism, which the hmx mixer cores do not run; "
@@ -153,6 +163,36 @@ def _split(md, query_start_loc_cpu=None):
     return ndt, dec, pre
 
 
+def _spec_conv(layer, md, mixed_qkv, cs):
+    """The speculative tokens' conv (primed_gdn_layer.py:700-712): one call over
+    every spec sequence's draft tokens against slot spec_state_indices_tensor[n, 0]."""
+    w = layer.conv1d.weight
+    w = w.view(w.size(0), w.size(2))
+    nsd, sidx = md.num_spec_decodes, md.spec_state_indices_tensor
+    return ops.causal_conv1d_update(mixed_qkv, cs, w, None, layer.activation,
+                                    conv_state_indices=sidx[:nsd, 0],
+                                    num_accepted_tokens=md.num_accepted_tokens,
+                                    query_start_loc=md.spec_query_start_loc[:nsd + 1],
+                                    max_query_len=sidx.size(-1))
+
+
+def _by_spec(md, n, rows, core_attn_out, o_norm, run_spec, run_rest):
+    """A speculative batch: every token speculative -> run_spec(rows, out, o_norm) in
+    place; otherwise each part on its index-selected rows (spec_token_indx,
+    non_spec_token_indx) into a scratch output that is copied back by index."""
+    if md.num_prefills == 0 and md.num_decodes == 0:
+        run_spec(rows, core_attn_out[:n], o_norm)
+        return
+    z = None if o_norm is None or o_norm[1] is None else o_norm[1][:n]
+    for idx, run in ((md.spec_token_indx, run_spec), (md.non_spec_token_indx, run_rest)):
+        sub = [None if t is None else t.index_select(0, idx) for t in rows]
+        out = core_attn_out.new_empty((idx.numel(),) + tuple(core_attn_out.shape[1:]))
+        on = None if o_norm is None else (o_norm[0], None if z is None else z.index_select(0, idx),
+                                          o_norm[2])
+        run(sub, out, on)
+        core_attn_out.index_copy_(0, idx, out)
+
+
 def _norm_args(o_norm, lo, hi):
     if o_norm is None:
         return {}
@@ -174,28 +214,49 @@ def gdn_forward_core(layer, mixed_qkv: torch.Tensor, b: torch.Tensor, a: torch.T
     _check(layer, md)
     n = md.num_actual_tokens
     mixed_qkv, b, a = mixed_qkv[:n], b[:n], a[:n]
-    x = _conv(layer, md, mixed_qkv, conv_state)
-    q, k, v = _qkv(layer, x)
-    # g and beta as fused_gdn_gating and the layer form them (:798-802), computed in
-    # the mixer kernels' loads instead of a separate launch
-    gates = ops.ProjGates(layer.A, layer.dt_bias, a, b,
-                          beta_scale=2.0 if getattr(layer, "allow_neg_eigval", False) else 1.0)
-    out = core_attn_out[:n].unsqueeze(0)
-    ndt, dec, pre = _split(md, query_start_loc_cpu)
-    if dec is not None:
-        cu_d, idx_d = dec
+    beta_scale = 2.0 if getattr(layer, "allow_neg_eigval", False) else 1.0
+
+    def rest(rows, out, on, qsl_cpu=None):
+        mq, aa, bb = rows
+        x = _conv(layer, md, mq, conv_state)
+        q, k, v = _qkv(layer, x)
+        # g and beta as fused_gdn_gating and the layer form them (:798-802), computed
+        # in the mixer kernels' loads instead of a separate launch
+        gates = ops.ProjGates(layer.A, layer.dt_bias, aa, bb, beta_scale=beta_scale)
+        o = out.unsqueeze(0)
+        m = mq.shape[0]
+        ndt, dec, pre = _split(md, qsl_cpu)
+        if dec is not None:
+            cu_d, idx_d = dec
+            ops.fused_recurrent_gated_delta_rule_gqa(
+                q[:, :ndt], k[:, :ndt], v[:, :ndt], None, None,
+                initial_state=ssm_state, inplace_final_state=True, cu_seqlens=cu_d,
+                ssm_state_indices=idx_d, use_qk_l2norm_in_kernel=True, out=o[:, :ndt],
+                gates=gates.tokens(0, ndt), **_norm_args(on, 0, ndt))
+        if pre is not None:
+            cu_p, idx_p, has_p = pre
+            ops.chunk_gated_delta_rule_gqa(
+                q[:, ndt:], k[:, ndt:], v[:, ndt:], None, None,
+                initial_state=ssm_state, output_final_state=True, cu_seqlens=cu_p,
+                use_qk_l2norm_in_kernel=True, ssm_state_indices=idx_p, has_initial_state=has_p,
+                out=o[:, ndt:], gates=gates.tokens(ndt, m), **_norm_args(on, ndt, m))
+
+    def spec(rows, out, on):
+        mq, aa, bb = rows
+        q, k, v = _qkv(layer, _spec_conv(layer, md, mq, conv_state))
+        gates = ops.ProjGates(layer.A, layer.dt_bias, aa, bb, beta_scale=beta_scale)
+        nsd = md.num_spec_decodes
         ops.fused_recurrent_gated_delta_rule_gqa(
-            q[:, :ndt], k[:, :ndt], v[:, :ndt], None, None,
-            initial_state=ssm_state, inplace_final_state=True, cu_seqlens=cu_d,
-            ssm_state_indices=idx_d, use_qk_l2norm_in_kernel=True, out=out[:, :ndt],
-            gates=gates.tokens(0, ndt), **_norm_args(o_norm, 0, ndt))
-    if pre is not None:
-        cu_p, idx_p, has_p = pre
-        ops.chunk_gated_delta_rule_gqa(
-            q[:, ndt:], k[:, ndt:], v[:, ndt:], None, None,
-            initial_state=ssm_state, output_final_state=True, cu_seqlens=cu_p,
-            use_qk_l2norm_in_kernel=True, ssm_state_indices=idx_p, has_initial_state=has_p,
-            out=out[:, ndt:], gates=gates.tokens(ndt, n), **_norm_args(o_norm, ndt, n))
+            q, k, v, None, None, initial_state=ssm_state, inplace_final_state=True,
+            cu_seqlens=md.spec_query_start_loc[:nsd + 1],
+            ssm_state_indices=md.spec_state_indices_tensor,
+            num_accepted_tokens=md.num_accepted_tokens, use_qk_l2norm_in_kernel=True,
+            out=out.unsqueeze(0), gates=gates, **_norm_args(on, 0, mq.shape[0]))
+
+    if md.spec_sequence_masks is None:
+        rest((mixed_qkv, a, b), core_attn_out[:n], o_norm, query_start_loc_cpu)
+    else:
+        _by_spec(md, n, (mixed_qkv, a, b), core_attn_out, o_norm, spec, rest)
 
 
 def gka_forward_core(layer, mixed_qkv: torch.Tensor, a: torch.Tensor, alpha_in: torch.Tensor,
@@ -214,34 +275,57 @@ def gka_forward_core(layer, mixed_qkv: torch.Tensor, a: torch.Tensor, alpha_in: 
     use_beta = layer.use_beta_gate
     if use_beta:
         b = b[:n]
-    x = _conv(layer, md, mixed_qkv, conv_state)
-    q, k, v = _qkv(layer, x)
-    # gates as primed_gka_layer.py:1138-1153 form them (fused_gka_gating, or the
-    # sigmoids without a forgetting gate; alpha zeroed for num_iter 0 or + 0.5),
-    # computed in the mixer kernels' loads instead of separate launches
     fg = layer.use_forgetting_gate
-    gates = ops.ProjGates(
-        layer.A if fg else None, layer.dt_bias, a, b if use_beta else None, alpha_in,
-        alpha_add=0.5 if (layer.num_iter != 0 and layer._alpha_idx is None) else 0.0,
-        alpha_zero=layer.num_iter == 0, gk_from_g=fg and layer.use_forgetting_gate_kk)
-    out = core_attn_out[:n].unsqueeze(0)
-    ndt, dec, pre = _split(md, query_start_loc_cpu)
     common = dict(gla_scale=layer.gla_scale, ridge_ratio=layer.ridge_strength,
                   num_iter=layer.num_iter)
-    if dec is not None:
-        cu_d, idx_d = dec
+
+    def gates_of(aa, ai, bb):
+        # gates as primed_gka_layer.py:1138-1153 form them (fused_gka_gating, or the
+        # sigmoids without a forgetting gate; alpha zeroed for num_iter 0 or + 0.5),
+        # computed in the mixer kernels' loads instead of separate launches
+        return ops.ProjGates(
+            layer.A if fg else None, layer.dt_bias, aa, bb if use_beta else None, ai,
+            alpha_add=0.5 if (layer.num_iter != 0 and layer._alpha_idx is None) else 0.0,
+            alpha_zero=layer.num_iter == 0, gk_from_g=fg and layer.use_forgetting_gate_kk)
+
+    def rest(rows, out, on, qsl_cpu=None):
+        mq, aa, ai, bb = rows
+        x = _conv(layer, md, mq, conv_state)
+        q, k, v = _qkv(layer, x)
+        gates = gates_of(aa, ai, bb)
+        o = out.unsqueeze(0)
+        m = mq.shape[0]
+        ndt, dec, pre = _split(md, qsl_cpu)
+        if dec is not None:
+            cu_d, idx_d = dec
+            ops.gka_chebyshev_gla_decode(
+                q[:, :ndt], k[:, :ndt], v[:, :ndt], None, None, None, None,
+                h_kk=h_kk_state, h_kv=h_kv_state, cu_seqlens=cu_d, ssm_state_indices=idx_d,
+                out=o[:, :ndt], gates=gates.tokens(0, ndt), **common,
+                **_norm_args(on, 0, ndt))
+        if pre is not None:
+            cu_p, idx_p, has_p = pre
+            ops.gka_chebyshev_gla_prefill(
+                q[:, ndt:], k[:, ndt:], v[:, ndt:], None, None, None, None,
+                h_kk_initial=h_kk_state, h_kv_initial=h_kv_state, output_final_state=True,
+                cu_seqlens=cu_p, ssm_state_indices=idx_p, has_initial_state=has_p,
+                out=o[:, ndt:], gates=gates.tokens(ndt, m), **common, **_norm_args(on, ndt, m))
+
+    def spec(rows, out, on):
+        mq, aa, ai, bb = rows
+        q, k, v = _qkv(layer, _spec_conv(layer, md, mq, conv_state))
+        nsd = md.num_spec_decodes
         ops.gka_chebyshev_gla_decode(
-            q[:, :ndt], k[:, :ndt], v[:, :ndt], None, None, None, None,
-            h_kk=h_kk_state, h_kv=h_kv_state, cu_seqlens=cu_d, ssm_state_indices=idx_d,
-            out=out[:, :ndt], gates=gates.tokens(0, ndt), **common,
-            **_norm_args(o_norm, 0, ndt))
-    if pre is not None:
-        cu_p, idx_p, has_p = pre
-        ops.gka_chebyshev_gla_prefill(
-            q[:, ndt:], k[:, ndt:], v[:, ndt:], None, None, None, None,
-            h_kk_initial=h_kk_state, h_kv_initial=h_kv_state, output_final_state=True,
-            cu_seqlens=cu_p, ssm_state_indices=idx_p, has_initial_state=has_p, out=out[:, ndt:],
-            gates=gates.tokens(ndt, n), **common, **_norm_args(o_norm, ndt, n))
+            q, k, v, None, None, None, None, h_kk=h_kk_state, h_kv=h_kv_state,
+            cu_seqlens=md.spec_query_start_loc[:nsd + 1],
+            ssm_state_indices=md.spec_state_indices_tensor, out=out.unsqueeze(0),
+            gates=gates_of(aa, ai, bb), **common, **_norm_args(on, 0, mq.shape[0]))
+
+    rows = (mixed_qkv, a, alpha_in, b if use_beta else None)
+    if md.spec_sequence_masks is None:
+        rest(rows, core_attn_out[:n], o_norm, query_start_loc_cpu)
+    else:
+        _by_spec(md, n, rows, core_attn_out, o_norm, spec, rest)
 
 
 def mamba2_conv_ssm_forward(layer, projected_states: torch.Tensor, output: torch.Tensor,

@@ -293,10 +293,3 @@ def test_gka_core_without_forgetting_gate(dev, batch):
         for s in set(int(i) for i in r["idx"]):
             assert_state_close(got[s], exp[s], what=f"slot {s}")
 
-
-def test_forward_core_rejects_spec_decode(dev):
-    lay = _layer("gdn", 3)
-    md, *_ = _meta("decode", dev)
-    md.spec_sequence_masks = torch.ones(1, dtype=torch.bool, device=dev)
-    with pytest.raises(NotImplementedError):
-        srv.gdn_forward_core(lay, None, None, None, None, md, None, None)
