@@ -64,6 +64,14 @@ struct Params {
   int dim, pad;
   int64_t tile0;                      // prefill: first token tile of this launch
   const int32_t* nacc;                // speculative update: accepted tokens per sequence
+  // slot table rows: idx[b * idx_stride + column], idx_cols columns (1 and 1 for a
+  // plain [batch] table).  Prefix caching (vLLM's block arguments) picks columns:
+  int64_t idx_stride; int idx_cols;
+  const int32_t* blk_in;              // column of the slot read (initial_state_idx), or null: 0
+  const int32_t* blk_last;            // column of the slot written last (block_idx_last_scheduled_token)
+  const int32_t* blk_first;           // prefill: block_idx_first_scheduled_token
+  const int32_t* ncomp;               // prefill: tokens computed before this step
+  int blk_size;                       // prefill: block_size_to_align
 };
 
 // Taps of 8 channels; the window holds the W-1 inputs before the current one
@@ -145,10 +153,22 @@ __device__ __forceinline__ int seq_of(const int32_t* qs, int batch, int64_t t) {
   return lo;
 }
 
+// Slot of sequence b at table column col[b] (column 0 when col is null), the
+// column clamped into the table.
+__device__ __forceinline__ int64_t slot_col(const Params& p, int b, const int32_t* col) {
+  if (!p.idx) return b;
+  const int c = col ? min(max(col[b], 0), p.idx_cols - 1) : 0;
+  return p.idx[(int64_t)b * p.idx_stride + c];
+}
+
+// The slot sequence b reads its initial state from; false for a padded entry (its
+// written slot is pad_slot_id: zero output, no state access).
 __device__ __forceinline__ bool seq_slot(const Params& p, int b, int64_t& slot, bool& init) {
-  slot = p.idx ? p.idx[b] : b;
-  const bool ok = slot != p.pad;
-  init = ok && p.st && p.has_init && p.has_init[b] != 0;   // never read a pad slot
+  slot = slot_col(p, b, p.blk_in);
+  const int64_t wslot = p.blk_last ? slot_col(p, b, p.blk_last) : slot;
+  const bool ok = wslot != p.pad;
+  // never read a pad slot
+  init = ok && slot != p.pad && p.st && p.has_init && p.has_init[b] != 0;
   return ok;
 }
 
@@ -271,31 +291,94 @@ __global__ __launch_bounds__(NT) void conv_state_kernel(Params p) {
     if (r < p.st_len) st8(srow + r * p.st_row, rows[r]);
 }
 
+// New prefill states with prefix caching (vLLM's block arguments, as the Mamba2
+// layer passes them, vllm-inference/src/primed_vllm/primed_mamba2_layer.py:770-792):
+// sequence b's tokens continue ncomp[b] computed ones, and the blocks of
+// blk_size tokens from blk_first[b] to blk_last[b] - 1 end inside this step.  Block
+// k's slot (table column k) receives the state at its end, the last st_len inputs
+// before absolute position (k + 1) * blk_size; column blk_last[b] receives the state
+// after the sequence's last token.  Rows before the sequence's first token come
+// from the initial state (zeros without one), read into registers before any row is
+// written (the read slot may be one of the written ones).  The block range is
+// clamped to the table's columns, so the loop is bounded.
+template <typename T>
+__global__ __launch_bounds__(NT) void conv_state_blocks_kernel(Params p) {
+  const int c0 = (blockIdx.y * NT + threadIdx.x) * 8;
+  const int b = blockIdx.x;
+  if (c0 >= p.dim) return;
+  int64_t rslot;
+  bool init;
+  if (!seq_slot(p, b, rslot, init)) return;
+  int64_t s, e;
+  seq_range(p, b, s, e);
+  if (e == s) return;     // an empty sequence keeps its state
+  const int L = p.st_len;
+  float old[8][8];        // the initial state's rows, st_len <= 8
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) old[r][j] = 0.f;
+    if (r < L && init)
+      ld8(static_cast<const T*>(p.st) + rslot * p.st_slot + (int64_t)r * p.st_row + c0, old[r]);
+  }
+  const int last = min(max(p.blk_last[b], 0), p.idx_cols - 1);
+  const int first = min(max(p.blk_first[b], 0), last);
+  const int64_t nc = max(p.ncomp[b], 0);
+  for (int k = first; k <= last; ++k) {
+    // the state after `end` of the sequence's tokens
+    int64_t end = k < last ? (int64_t)(k + 1) * p.blk_size - nc : e - s;
+    end = min(max(end, (int64_t)0), e - s);
+    const int64_t wslot = p.idx[(int64_t)b * p.idx_stride + k];
+    if (wslot == p.pad) continue;
+    T* srow = static_cast<T*>(p.st) + wslot * p.st_slot + c0;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      if (r >= L) continue;
+      const int64_t pos = end - L + r;    // sequence position of state row r (>= -L)
+      float v[8];
+      if (pos >= 0) {
+        ld8(static_cast<const T*>(p.x) + (s + pos) * p.xs + c0, v);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+          if (q == L + pos)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = old[q][j];
+      }
+      st8(srow + (int64_t)r * p.st_row, v);
+    }
+  }
+}
+
 // Decode: one token per sequence against its slot; the state shifts by one row.
+// With prefix caching the state is read from table column blk_in[b] and written
+// to column blk_last[b] (every read precedes the writes).
 template <typename T, int W, bool ACT>
 __global__ __launch_bounds__(NT) void conv_update_kernel(Params p) {
   const int c0 = (blockIdx.y * NT + threadIdx.x) * 8;
   const int b = blockIdx.x;
   if (c0 >= p.dim) return;
-  const int64_t slot = p.idx ? p.idx[b] : b;
+  const int64_t slot = slot_col(p, b, p.blk_in);
+  const int64_t wslot = p.blk_last ? slot_col(p, b, p.blk_last) : slot;
   T* orow = static_cast<T*>(p.out) + (int64_t)b * p.os + c0;
-  if (slot == p.pad) {   // padded entry: zero output, no state access
+  if (slot == p.pad || wslot == p.pad) {   // padded entry: zero output, no state access
     const float zero[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     st8(orow, zero);
     return;
   }
-  T* srow = static_cast<T*>(p.st) + slot * p.st_slot + c0;
+  const T* sin = static_cast<const T*>(p.st) + slot * p.st_slot + c0;
+  T* srow = static_cast<T*>(p.st) + wslot * p.st_slot + c0;
   const int L = p.st_len;
   float xt[8], win[W - 1][8], y[8];
   ld8(static_cast<const T*>(p.x) + (int64_t)b * p.xs + c0, xt);
 #pragma unroll
-  for (int i = 0; i < W - 1; ++i) ld8(srow + (int64_t)(L - (W - 1) + i) * p.st_row, win[i]);
+  for (int i = 0; i < W - 1; ++i) ld8(sin + (int64_t)(L - (W - 1) + i) * p.st_row, win[i]);
   float rows[8][8];      // rows 1 .. L-1 of a state longer than the window
   const bool slack = L > W - 1;
   if (slack) {
 #pragma unroll
     for (int r = 1; r < 8; ++r)
-      if (r < L - (W - 1)) ld8(srow + r * p.st_row, rows[r]);
+      if (r < L - (W - 1)) ld8(sin + r * p.st_row, rows[r]);
   }
   Taps<W, ACT> tp;
   tp.load(p, c0);
@@ -404,8 +487,12 @@ void launch_fwd_w(const Params& p, hipStream_t s) {
     hipLaunchKernelGGL((conv_fwd_kernel<T, W, ACT>), dim3(cg, (unsigned)min(tiles - t, (int64_t)65535)),
                        dim3(NT), 0, s, q);
   }
-  if (p.st && p.batch > 0)
-    hipLaunchKernelGGL(conv_state_kernel<T>, dim3((unsigned)p.batch, cg), dim3(NT), 0, s, p);
+  if (p.st && p.batch > 0) {
+    if (p.blk_first)
+      hipLaunchKernelGGL(conv_state_blocks_kernel<T>, dim3((unsigned)p.batch, cg), dim3(NT), 0, s, p);
+    else
+      hipLaunchKernelGGL(conv_state_kernel<T>, dim3((unsigned)p.batch, cg), dim3(NT), 0, s, p);
+  }
 }
 
 template <typename T, int W, bool ACT>
@@ -488,11 +575,55 @@ extern "C" int hmx_causal_conv1d_fwd(const void* x, int64_t x_token_stride, void
            conv_states, state_slot_stride, state_row_stride,
            conv_states ? state_len : width - 1, query_start_loc, batch, total_tokens,
            cache_indices, has_initial_state, dim, pad_slot_id};
+  p.idx_stride = 1;
+  p.idx_cols = 1;
   hipStream_t s = (hipStream_t)stream;
   if (dtype == HMX_BF16) dispatch<bf16, 0>(p, width, activation, s);
   else if (dtype == HMX_F16) dispatch<f16, 0>(p, width, activation, s);
   else dispatch<float, 0>(p, width, activation, s);
   return check_launch("hmx_causal_conv1d_fwd");
+}
+
+extern "C" int hmx_causal_conv1d_fwd_blocks(
+    const void* x, int64_t x_token_stride, void* out, int64_t out_token_stride, int32_t dtype,
+    const void* weight, int32_t weight_dtype, int32_t width, const void* bias, int32_t bias_dtype,
+    void* conv_states, int64_t state_slot_stride, int64_t state_row_stride, int32_t state_len,
+    const int32_t* query_start_loc, int32_t batch, int64_t total_tokens,
+    const int32_t* cache_indices, int64_t cache_indices_row_stride, int32_t cache_indices_cols,
+    const uint8_t* has_initial_state, const int32_t* initial_state_idx,
+    const int32_t* block_idx_first_scheduled_token, const int32_t* block_idx_last_scheduled_token,
+    const int32_t* num_computed_tokens, int32_t block_size, int32_t dim, int32_t activation,
+    int32_t pad_slot_id, void* stream) {
+  const char* fn = "hmx_causal_conv1d_fwd_blocks";
+  const int rc = check_common(fn, x, out, weight, dtype, width, dim, state_len, weight_dtype,
+                              bias, bias_dtype, x_token_stride, out_token_stride,
+                              state_row_stride, state_slot_stride, conv_states);
+  if (rc != HMX_OK) return rc;
+  HMX_REQUIRE(batch >= 0 && total_tokens >= 0, HMX_EINVAL, "%s: sizes", fn);
+  HMX_REQUIRE(block_size > 0 && cache_indices_cols > 0 &&
+              cache_indices_row_stride >= cache_indices_cols, HMX_EINVAL,
+              "%s: block_size %d, cache_indices [batch, %d] with row stride %lld", fn, block_size,
+              cache_indices_cols, (long long)cache_indices_row_stride);
+  if (total_tokens == 0) return HMX_OK;
+  HMX_REQUIRE(x && out && weight && query_start_loc && conv_states && cache_indices &&
+              initial_state_idx && block_idx_first_scheduled_token &&
+              block_idx_last_scheduled_token && num_computed_tokens, HMX_EINVAL,
+              "%s: null pointer", fn);
+  Params p{x, x_token_stride, out, out_token_stride, weight, weight_dtype, bias, bias_dtype,
+           conv_states, state_slot_stride, state_row_stride, state_len, query_start_loc, batch,
+           total_tokens, cache_indices, has_initial_state, dim, pad_slot_id};
+  p.idx_stride = cache_indices_row_stride;
+  p.idx_cols = cache_indices_cols;
+  p.blk_in = initial_state_idx;
+  p.blk_last = block_idx_last_scheduled_token;
+  p.blk_first = block_idx_first_scheduled_token;
+  p.ncomp = num_computed_tokens;
+  p.blk_size = block_size;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == HMX_BF16) dispatch<bf16, 0>(p, width, activation, s);
+  else if (dtype == HMX_F16) dispatch<f16, 0>(p, width, activation, s);
+  else dispatch<float, 0>(p, width, activation, s);
+  return check_launch(fn);
 }
 
 extern "C" int hmx_causal_conv1d_update(const void* x, int64_t x_token_stride, void* out,
@@ -514,6 +645,8 @@ extern "C" int hmx_causal_conv1d_update(const void* x, int64_t x_token_stride, v
   Params p{x, x_token_stride, out, out_token_stride, weight, weight_dtype, bias, bias_dtype,
            conv_state, state_slot_stride, state_row_stride, state_len, nullptr, batch, batch,
            conv_state_indices, nullptr, dim, pad_slot_id};
+  p.idx_stride = 1;
+  p.idx_cols = 1;
   hipStream_t s = (hipStream_t)stream;
   if (dtype == HMX_BF16) dispatch<bf16, 1>(p, width, activation, s);
   else if (dtype == HMX_F16) dispatch<f16, 1>(p, width, activation, s);
@@ -539,9 +672,43 @@ extern "C" int hmx_causal_conv1d_update_spec(
   Params p{x, x_token_stride, out, out_token_stride, weight, weight_dtype, bias, bias_dtype,
            conv_state, state_slot_stride, state_row_stride, state_len, query_start_loc, batch,
            total_tokens, conv_state_indices, nullptr, dim, pad_slot_id, 0, num_accepted_tokens};
+  p.idx_stride = 1;
+  p.idx_cols = 1;
   hipStream_t s = (hipStream_t)stream;
   if (dtype == HMX_BF16) dispatch<bf16, 2>(p, width, activation, s);
   else if (dtype == HMX_F16) dispatch<f16, 2>(p, width, activation, s);
   else dispatch<float, 2>(p, width, activation, s);
   return check_launch("hmx_causal_conv1d_update_spec");
+}
+
+extern "C" int hmx_causal_conv1d_update_blocks(
+    const void* x, int64_t x_token_stride, void* out, int64_t out_token_stride, int32_t dtype,
+    const void* weight, int32_t weight_dtype, int32_t width, const void* bias, int32_t bias_dtype,
+    void* conv_state, int64_t state_slot_stride, int64_t state_row_stride, int32_t state_len,
+    const int32_t* conv_state_indices, int64_t indices_row_stride, int32_t indices_cols,
+    const int32_t* initial_state_idx, const int32_t* block_idx_last_scheduled_token,
+    int32_t batch, int32_t dim, int32_t activation, int32_t pad_slot_id, void* stream) {
+  const char* fn = "hmx_causal_conv1d_update_blocks";
+  const int rc = check_common(fn, x, out, weight, dtype, width, dim, state_len, weight_dtype,
+                              bias, bias_dtype, x_token_stride, out_token_stride,
+                              state_row_stride, state_slot_stride, conv_state);
+  if (rc != HMX_OK) return rc;
+  HMX_REQUIRE(batch >= 0 && indices_cols > 0 && indices_row_stride >= indices_cols, HMX_EINVAL,
+              "%s: batch %d, conv_state_indices [batch, %d] with row stride %lld", fn, batch,
+              indices_cols, (long long)indices_row_stride);
+  if (batch == 0) return HMX_OK;
+  HMX_REQUIRE(x && out && weight && conv_state && conv_state_indices && initial_state_idx &&
+              block_idx_last_scheduled_token, HMX_EINVAL, "%s: null pointer", fn);
+  Params p{x, x_token_stride, out, out_token_stride, weight, weight_dtype, bias, bias_dtype,
+           conv_state, state_slot_stride, state_row_stride, state_len, nullptr, batch, batch,
+           conv_state_indices, nullptr, dim, pad_slot_id};
+  p.idx_stride = indices_row_stride;
+  p.idx_cols = indices_cols;
+  p.blk_in = initial_state_idx;
+  p.blk_last = block_idx_last_scheduled_token;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == HMX_BF16) dispatch<bf16, 1>(p, width, activation, s);
+  else if (dtype == HMX_F16) dispatch<f16, 1>(p, width, activation, s);
+  else dispatch<float, 1>(p, width, activation, s);
+  return check_launch(fn);
 }

@@ -245,27 +245,42 @@ def _(state, x, dt, A, B, C, D, z, dt_bias, dt_softplus, state_batch_indices,
 def _conv_fwd(x: Tensor, weight: Tensor, bias: Optional[Tensor], conv_states: Optional[Tensor],
               query_start_loc: Optional[Tensor], cache_indices: Optional[Tensor],
               has_initial_state: Optional[Tensor], activation: Optional[str],
-              pad_slot_id: int) -> Tensor:
+              pad_slot_id: int, initial_state_idx: Optional[Tensor] = None,
+              block_idx_first_scheduled_token: Optional[Tensor] = None,
+              block_idx_last_scheduled_token: Optional[Tensor] = None,
+              num_computed_tokens: Optional[Tensor] = None,
+              block_size_to_align: int = 0) -> Tensor:
+    blocks = ops.conv.block_args(initial_state_idx, block_idx_first_scheduled_token,
+                                 block_idx_last_scheduled_token, num_computed_tokens,
+                                 block_size_to_align)
     return ops.conv.conv_fwd_rows(x, weight, bias, conv_states, query_start_loc, cache_indices,
-                                  has_initial_state, activation, pad_slot_id)
+                                  has_initial_state, activation, pad_slot_id, blocks=blocks)
 
 
 @_conv_fwd.register_fake
 def _(x, weight, bias, conv_states, query_start_loc, cache_indices, has_initial_state, activation,
-      pad_slot_id):
+      pad_slot_id, initial_state_idx=None, block_idx_first_scheduled_token=None,
+      block_idx_last_scheduled_token=None, num_computed_tokens=None, block_size_to_align=0):
     return x.new_empty(x.shape[1], x.shape[0])
 
 
 @torch.library.custom_op("hmx::causal_conv1d_update", mutates_args=("conv_state",))
 def _conv_update(x: Tensor, conv_state: Tensor, weight: Tensor, bias: Optional[Tensor],
                  activation: Optional[str], conv_state_indices: Optional[Tensor],
-                 pad_slot_id: int) -> Tensor:
+                 pad_slot_id: int, num_accepted_tokens: Optional[Tensor] = None,
+                 query_start_loc: Optional[Tensor] = None,
+                 block_idx_last_scheduled_token: Optional[Tensor] = None,
+                 initial_state_idx: Optional[Tensor] = None) -> Tensor:
     return ops.causal_conv1d_update(x, conv_state, weight, bias, activation, conv_state_indices,
-                                    pad_slot_id=pad_slot_id)
+                                    num_accepted_tokens, query_start_loc, pad_slot_id=pad_slot_id,
+                                    block_idx_last_scheduled_token=block_idx_last_scheduled_token,
+                                    initial_state_idx=initial_state_idx)
 
 
 @_conv_update.register_fake
-def _(x, conv_state, weight, bias, activation, conv_state_indices, pad_slot_id):
+def _(x, conv_state, weight, bias, activation, conv_state_indices, pad_slot_id,
+      num_accepted_tokens=None, query_start_loc=None, block_idx_last_scheduled_token=None,
+      initial_state_idx=None):
     return x.new_empty(x.shape)
 
 
@@ -375,14 +390,18 @@ def _act_name(activation):
 
 def causal_conv1d_fn(x, weight, bias=None, conv_states=None, query_start_loc=None,
                      cache_indices=None, has_initial_state=None, activation="silu",
-                     pad_slot_id=-1, metadata=None, validate_data=False, **block_args):
+                     pad_slot_id=-1, metadata=None, validate_data=False,
+                     block_idx_first_scheduled_token=None, block_idx_last_scheduled_token=None,
+                     initial_state_idx=None, num_computed_tokens=None, block_size_to_align=0):
     """``torch.ops.hmx.causal_conv1d_fn`` with vLLM's signature (called at
-    primed_gdn_layer.py:747-757); returns the [dim, total] view."""
-    if any(v is not None for v in block_args.values()):
-        raise NotImplementedError("prefix-cache block arguments of causal_conv1d_fn")
+    primed_gdn_layer.py:747-757, primed_mamba2_layer.py:782-793 with the prefix-cache
+    block arguments); returns the [dim, total] view."""
     return torch.ops.hmx.causal_conv1d_fn(x, weight, bias, conv_states, query_start_loc,
                                           cache_indices, has_initial_state,
-                                          _act_name(activation), int(pad_slot_id)).t()
+                                          _act_name(activation), int(pad_slot_id),
+                                          initial_state_idx, block_idx_first_scheduled_token,
+                                          block_idx_last_scheduled_token, num_computed_tokens,
+                                          int(block_size_to_align or 0)).t()
 
 
 def causal_conv1d_update(x, conv_state, weight, bias=None, activation=None,
@@ -390,13 +409,13 @@ def causal_conv1d_update(x, conv_state, weight, bias=None, activation=None,
                          max_query_len=-1, pad_slot_id=-1, validate_data=False,
                          block_idx_last_scheduled_token=None, initial_state_idx=None):
     """``torch.ops.hmx.causal_conv1d_update`` with vLLM's signature (called at
-    primed_gdn_layer.py:775-785); the state pool is updated in place."""
-    if num_accepted_tokens is not None or query_start_loc is not None:
-        raise NotImplementedError("speculative multi-token causal_conv1d_update")
-    if block_idx_last_scheduled_token is not None or initial_state_idx is not None:
-        raise NotImplementedError("prefix-cache block arguments of causal_conv1d_update")
+    primed_gdn_layer.py:775-785, :700-712 in the speculative form, and
+    primed_mamba2_layer.py:964-973 with the prefix-cache block arguments); the state
+    pool is updated in place."""
     return torch.ops.hmx.causal_conv1d_update(x, conv_state, weight, bias, _act_name(activation),
-                                              conv_state_indices, int(pad_slot_id))
+                                              conv_state_indices, int(pad_slot_id),
+                                              num_accepted_tokens, query_start_loc,
+                                              block_idx_last_scheduled_token, initial_state_idx)
 
 
 def rms_norm_gated(x, z, weight, eps=1e-5, norm_before_gate=True):

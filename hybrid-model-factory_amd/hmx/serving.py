@@ -63,8 +63,17 @@ by the SSD ops' grouped operands (no rearrange / repeat_kv / permute copies,
 gather and scatter, :812-824, :941), and both scans write ``output`` directly.
 The B/C RMSNorms and the rotary position embedding of B and C
 (``use_pos_embed``) run through the layer's own modules, where and as the
-reference calls them (:663-671).  Prefix caching (``mamba_cache_mode == "all"``)
-raises NotImplementedError.
+reference calls them (:663-671).  With prefix caching (``mamba_cache_mode ==
+"all"``, :728-792, :864-933, :943-1021) the state tables are [requests, blocks]:
+the conv reads and writes its states by block through the conv ops' block
+arguments; the prefill scan starts from the slot of the last computed token's
+block, returns the state after every chunk, and the states at the blocks' ends
+and after each sequence's last token are copied into the blocks' slots with the
+layer's chunk arithmetic (the block and chunk metadata are read on the host, as
+the layer's loop does); the decode reads the last computed token's block and
+writes the scheduled token's.  In the profile run (``attn_metadata`` None,
+:676-697) nothing is written and the x columns repeated over the heads are
+returned, as the layer returns them.
 """
 from __future__ import annotations
 
@@ -331,7 +340,7 @@ def gka_forward_core(layer, mixed_qkv: torch.Tensor, a: torch.Tensor, alpha_in: 
 def mamba2_conv_ssm_forward(layer, projected_states: torch.Tensor, output: torch.Tensor,
                             attn_metadata, conv_state: torch.Tensor,
                             ssm_state: torch.Tensor, *, query_start_loc_cpu=None,
-                            positions: torch.Tensor | None = None) -> None:
+                            positions: torch.Tensor | None = None) -> torch.Tensor | None:
     """primed_mamba2_layer.py:615-1021 over hmx ops (see the module docstring).
 
     ``layer`` carries the reference's attributes (tped_intermediate_size,
@@ -347,15 +356,18 @@ def mamba2_conv_ssm_forward(layer, projected_states: torch.Tensor, output: torch
     (:650-653).  Writes ``output[:num_actual_tokens]`` ([tokens, intermediate],
     decodes first) and updates both pools in place.  ``query_start_loc_cpu``
     (vLLM's host copy of the batch's query_start_loc) lets the prefill scan plan
-    without a device-to-host copy."""
+    without a device-to-host copy.
+
+    With ``cache_config.mamba_cache_mode == "all"`` the metadata also carries
+    block_idx_last_computed_token, block_idx_last_scheduled_token,
+    block_idx_first_scheduled_token_p, num_computed_tokens_p, chunk_size,
+    cu_chunk_seqlen_p, seq_idx_p and last_chunk_indices_p (:728-754, :844-863), the
+    state table is [requests, blocks] and ``cache_config.mamba_block_size`` is the
+    block size.  With ``attn_metadata`` None (the profile run) nothing is written and
+    the x columns repeated over the heads [tokens, H * head_dim] are returned."""
     md = attn_metadata
-    if md is None:
-        raise NotImplementedError("the profile run (attn_metadata None) is not handled by the "
-                                  "hmx Mamba2 core")
     cc = getattr(layer, "cache_config", None)
-    if cc is not None and getattr(cc, "mamba_cache_mode", None) == "all":
-        raise NotImplementedError("prefix caching (mamba_cache_mode 'all') is not supported by "
-                                  "the hmx Mamba2 core")
+    apc = cc is not None and getattr(cc, "mamba_cache_mode", None) == "all"
     rope = getattr(layer, "use_pos_embed", False)
     if rope and positions is None:
         raise ValueError("use_pos_embed needs the tokens' positions")
@@ -379,6 +391,8 @@ def mamba2_conv_ssm_forward(layer, projected_states: torch.Tensor, output: torch
         if rope:
             C, B = layer.rotary_emb(positions, C, B)
         hbc = torch.cat([hs, B, C], dim=-1)
+    if md is None:                                       # profile run (:676-697)
+        return hbc[:, :xb].reshape(-1, HX, P).repeat_interleave(H // HX, dim=1).reshape(-1, H * P)
     nd, npf = md.num_decode_tokens, md.num_prefills
     n = nd + md.num_prefill_tokens
     idx = md.state_indices_tensor
@@ -387,7 +401,13 @@ def mamba2_conv_ssm_forward(layer, projected_states: torch.Tensor, output: torch
     act = layer.activation
     x = torch.empty(n, CD, dtype=hbc.dtype, device=hbc.device)
     out = output[:n].view(n, H, P)
-    if npf > 0:
+    if apc:                                              # (:728-754)
+        lc, ls = md.block_idx_last_computed_token, md.block_idx_last_scheduled_token
+    if npf > 0 and apc:
+        _mamba2_prefill_blocks(layer, md, hbc[nd:n], dt[nd:n], x[nd:], out[nd:], idx[nd:nd + npf],
+                               lc[nd:nd + npf], ls[nd:nd + npf], conv_state, ssm_state, cc,
+                               (H, HX, P, N, xb))
+    elif npf > 0:
         idx_p = idx[nd:nd + npf]
         has_c = md.has_initial_states_p                  # the conv takes the flags as given (:788)
         has = has_c
@@ -406,12 +426,71 @@ def mamba2_conv_ssm_forward(layer, projected_states: torch.Tensor, output: torch
             dt_limit=(0.0, float("inf")), ssm_state_indices=idx_p, has_initial_state=has)
     if nd > 0:
         idx_d = idx[:nd]
-        ops.causal_conv1d_update(hbc[:nd], conv_state, w, bias, act, conv_state_indices=idx_d,
-                                 out=x[:nd])
+        src = dst = idx_d
+        if apc:                                          # (:943-973)
+            src = idx_d.gather(1, lc[:nd, None].long()).squeeze(1)
+            dst = idx_d.gather(1, ls[:nd, None].long()).squeeze(1)
+            ops.causal_conv1d_update(hbc[:nd], conv_state, w, bias, act, conv_state_indices=idx_d,
+                                     block_idx_last_scheduled_token=ls[:nd],
+                                     initial_state_idx=lc[:nd], out=x[:nd])
+        else:
+            ops.causal_conv1d_update(hbc[:nd], conv_state, w, bias, act, conv_state_indices=idx_d,
+                                     out=x[:nd])
         xd = x[:nd]
         ops.selective_state_update(
             ssm_state, xd[:, :xb].view(nd, HX, P), dt[:nd, :, None].expand(nd, H, P),
             layer.A[:, None, None].expand(H, P, N), xd[:, xb:2 * xb].view(nd, HX, N),
             xd[:, 2 * xb:].view(nd, H, N), layer.D[:, None].expand(H, P), z=None,
             dt_bias=layer.dt_bias[:, None].expand(H, P), dt_softplus=True,
-            state_batch_indices=idx_d, dst_state_batch_indices=idx_d, out=out[:nd])
+            state_batch_indices=src, dst_state_batch_indices=dst, out=out[:nd])
+
+
+def _mamba2_prefill_blocks(layer, md, hbc, dt, x, out, idx_p, lc_p, ls_p, conv_state, ssm_state,
+                           cc, dims):
+    """The prefill of primed_mamba2_layer.py:768-933 with prefix caching: the conv
+    with its block arguments (:782-793); the scan from the slot of each sequence's
+    last computed block (:811-824), returning the state after every chunk
+    (:844-863); the states at the ends of the blocks that end in this step and after
+    each sequence's last token copied into the blocks' slots (:864-933)."""
+    H, HX, P, N, xb = dims
+    npf = idx_p.shape[0]
+    bs = int(cc.mamba_block_size)
+    chunk = int(getattr(md, "chunk_size", layer.chunk_size))
+    fs_p, ncomp = md.block_idx_first_scheduled_token_p, md.num_computed_tokens_p
+    ops.conv.conv_fwd_rows(hbc.t(), layer.conv_weights, getattr(layer.conv1d, "bias", None),
+                           conv_state, md.query_start_loc_p, idx_p, md.has_initial_states_p,
+                           layer.activation, out=x, blocks=(lc_p, fs_p, ls_p, ncomp, bs))
+    h0 = None
+    has = md.has_initial_states_p
+    if has is not None and md.prep_initial_states:
+        src = idx_p.gather(1, lc_p[:, None].long()).squeeze(1)
+        h0 = torch.where(has[:, None, None, None], ssm_state[src.long()].float(), 0.0)
+    states = ops.mamba_chunk_scan_combined_varlen(
+        x[:, :xb].view(-1, HX, P), dt, layer.A, x[:, xb:2 * xb].view(-1, HX, N),
+        x[:, 2 * xb:].view(-1, H, N), chunk, cu_seqlens=md.query_start_loc_p,
+        cu_chunk_seqlens=md.cu_chunk_seqlen_p, last_chunk_indices=md.last_chunk_indices_p,
+        seq_idx=md.seq_idx_p, out=out, D=layer.D, dt_bias=layer.dt_bias, initial_states=h0,
+        dt_softplus=True, dt_limit=(0.0, float("inf")), return_intermediate_states=True,
+        state_dtype=ssm_state.dtype)
+    # which chunk's state goes to which slot: the layer's loop (:864-933) on host values
+    stride = bs // chunk
+    tab = idx_p.tolist()
+    fs, ls = [int(v) for v in fs_p.tolist()], [int(v) for v in ls_p.tolist()]
+    nc = [int(v) for v in ncomp.tolist()]
+    last_chunk = [int(v) for v in md.last_chunk_indices_p.tolist()]
+    blk_dst, blk_src, fin_dst, fin_src = [], [], [], []
+    for s in range(npf):
+        first_chunk = 0 if s == 0 else 1 + last_chunk[s - 1]
+        aligned = first_chunk + stride - 1 - (nc[s] % bs) // chunk
+        for k in range(ls[s] - fs[s]):
+            blk_dst.append(tab[s][fs[s] + k])
+            blk_src.append(aligned + k * stride)
+        fin_dst.append(tab[s][ls[s]])
+        fin_src.append(last_chunk[s])
+    for dst, src in ((blk_dst, blk_src), (fin_dst, fin_src)):   # block states, then final ones
+        keep = [i for i, d in enumerate(dst) if d >= 0]
+        if keep:
+            dev = ssm_state.device
+            ssm_state.index_copy_(0, torch.tensor([dst[i] for i in keep], device=dev),
+                                  states.index_select(0, torch.tensor([src[i] for i in keep],
+                                                                      device=dev)))

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define HMX_ABI_VERSION 11  /* 2: optional hmx_gated_norm output epilogue in the GDN ops;
+#define HMX_ABI_VERSION 12  /* 2: optional hmx_gated_norm output epilogue in the GDN ops;
                               3: q/k/v token strides in the GDN and GKA ops; slot-indexed
                               state pools and has_initial_state in the GDN, GKA and SSD
                               prefills;
@@ -43,7 +43,10 @@ extern "C" {
                               10: the same in hmx_ssd_chunk_workspace_bytes (nonzero for
                                   one segment per sequence too);
                               11: hmx_causal_conv1d_update_spec (speculative multi-token
-                                  conv update) */
+                                  conv update);
+                              12: hmx_causal_conv1d_fwd_blocks and
+                                  hmx_causal_conv1d_update_blocks (prefix-cache block
+                                  arguments) */
 
 enum hmx_status {
   HMX_OK = 0,
@@ -685,6 +688,65 @@ int hmx_causal_conv1d_update_spec(const void* x, int64_t x_token_stride, void* o
                                   const int32_t* query_start_loc, int32_t batch,
                                   int64_t total_tokens, int32_t dim, int32_t activation,
                                   int32_t pad_slot_id, void* stream);
+
+/*
+ * hmx_causal_conv1d_fwd with prefix caching (vLLM's block arguments, as the Mamba2
+ * layer passes them with mamba_cache_mode "all"): cache_indices is a
+ * [batch, cache_indices_cols] table (row stride cache_indices_row_stride elements)
+ * of one slot per block of block_size tokens.  Sequence b continues
+ * num_computed_tokens[b] computed tokens; it reads its initial state (where
+ * has_initial_state[b] != 0) from column initial_state_idx[b]; every block k from
+ * block_idx_first_scheduled_token[b] to block_idx_last_scheduled_token[b] - 1 ends in
+ * this step, and column k receives the state at its end (the last state_len inputs
+ * before absolute position (k + 1) * block_size); column
+ * block_idx_last_scheduled_token[b] receives the state after the sequence's last
+ * token.  Columns are clamped into the table; a written slot equal to pad_slot_id is
+ * skipped, and a sequence whose last column's slot is pad_slot_id gets output 0 and
+ * touches no state.  Outputs are those of hmx_causal_conv1d_fwd.
+ * Replaces: causal_conv1d_fn with block_idx_first_scheduled_token /
+ *   block_idx_last_scheduled_token / initial_state_idx / num_computed_tokens /
+ *   block_size_to_align (vLLM, un-vendored; called at
+ *   vllm-inference/src/primed_vllm/primed_mamba2_layer.py:770-793).  The block
+ *   positions follow the layer's own use of the same metadata for the SSD states
+ *   (:864-933: block k's state is the state after its last token).
+ */
+int hmx_causal_conv1d_fwd_blocks(const void* x, int64_t x_token_stride, void* out,
+                                 int64_t out_token_stride, int32_t dtype, const void* weight,
+                                 int32_t weight_dtype, int32_t width, const void* bias,
+                                 int32_t bias_dtype, void* conv_states, int64_t state_slot_stride,
+                                 int64_t state_row_stride, int32_t state_len,
+                                 const int32_t* query_start_loc, int32_t batch,
+                                 int64_t total_tokens, const int32_t* cache_indices,
+                                 int64_t cache_indices_row_stride, int32_t cache_indices_cols,
+                                 const uint8_t* has_initial_state,
+                                 const int32_t* initial_state_idx,
+                                 const int32_t* block_idx_first_scheduled_token,
+                                 const int32_t* block_idx_last_scheduled_token,
+                                 const int32_t* num_computed_tokens, int32_t block_size,
+                                 int32_t dim, int32_t activation, int32_t pad_slot_id,
+                                 void* stream);
+
+/*
+ * hmx_causal_conv1d_update with prefix caching: conv_state_indices is a
+ * [batch, indices_cols] table (row stride indices_row_stride); the window is read from
+ * the slot at column initial_state_idx[b] and the shifted state written to the slot at
+ * column block_idx_last_scheduled_token[b] (the same slot when both columns agree).
+ * An entry whose read or written slot is pad_slot_id writes 0 and touches no state.
+ * Replaces: causal_conv1d_update with block_idx_last_scheduled_token /
+ *   initial_state_idx (vLLM, un-vendored; called at
+ *   vllm-inference/src/primed_vllm/primed_mamba2_layer.py:964-973).
+ */
+int hmx_causal_conv1d_update_blocks(const void* x, int64_t x_token_stride, void* out,
+                                    int64_t out_token_stride, int32_t dtype, const void* weight,
+                                    int32_t weight_dtype, int32_t width, const void* bias,
+                                    int32_t bias_dtype, void* conv_state,
+                                    int64_t state_slot_stride, int64_t state_row_stride,
+                                    int32_t state_len, const int32_t* conv_state_indices,
+                                    int64_t indices_row_stride, int32_t indices_cols,
+                                    const int32_t* initial_state_idx,
+                                    const int32_t* block_idx_last_scheduled_token, int32_t batch,
+                                    int32_t dim, int32_t activation, int32_t pad_slot_id,
+                                    void* stream);
 
 #ifdef __cplusplus
 }

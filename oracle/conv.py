@@ -83,3 +83,64 @@ def causal_conv1d_update(x, conv_state, weight, bias, activation, conv_state_ind
         out[b] = o[0]
         states[slot] = ns
     return out, states
+
+
+def causal_conv1d_varlen_blocks(x, weight, bias, conv_states, query_start_loc, cache_indices,
+                                has_initial_state, initial_state_idx, first_block, last_block,
+                                num_computed_tokens, block_size, activation="silu",
+                                pad_slot_id=-1, dtype=DEFAULT):
+    """Prefill with prefix caching (vLLM's block arguments, as the Mamba2 layer passes
+    them, vllm-inference/src/primed_vllm/primed_mamba2_layer.py:770-793).
+    cache_indices [batch, blocks] holds one slot per block of block_size tokens.
+    Sequence b continues num_computed_tokens[b] tokens: it reads its initial state
+    from column initial_state_idx[b] (where has_initial_state[b]); block k in
+    first_block[b] .. last_block[b] - 1 ends inside this step and column k receives
+    the state at its end, the last state_len inputs before absolute position
+    (k + 1) * block_size (the position the layer's SSD states use for the same
+    blocks, :864-933); column last_block[b] receives the state after the last
+    token.  A sequence whose last column's slot is pad_slot_id is skipped (output
+    0); reads see the pool as it was before the call.  Returns (out, states)."""
+    qs = [int(v) for v in query_start_loc.tolist()]
+    before = conv_states.to(dtype)
+    states = before.clone()
+    L = before.shape[1]
+    out = torch.zeros(x.shape, dtype=dtype)
+    for b in range(len(qs) - 1):
+        row = [int(v) for v in cache_indices[b].tolist()]
+        last, first = int(last_block[b]), int(first_block[b])
+        if row[last] == pad_slot_id:
+            continue
+        rslot = row[int(initial_state_idx[b])]
+        init = has_initial_state is not None and bool(has_initial_state[b]) and \
+            rslot != pad_slot_id
+        st = before[rslot] if init else torch.zeros(L, x.shape[-1], dtype=dtype)
+        xb = x[qs[b]:qs[b + 1]].to(dtype)
+        o, _ = conv_sequence(xb, st, weight, bias, activation, dtype)
+        out[qs[b]:qs[b + 1]] = o
+        hist = torch.cat([st, xb])                 # position p of the sequence is row L + p
+        nc, T = int(num_computed_tokens[b]), xb.shape[0]
+        for k in range(first, last + 1):
+            end = (k + 1) * block_size - nc if k < last else T
+            if row[k] != pad_slot_id:
+                states[row[k]] = hist[end:end + L]
+    return out, states
+
+
+def causal_conv1d_update_blocks(x, conv_state, weight, bias, activation, cache_indices,
+                                initial_state_idx, last_block, pad_slot_id=-1, dtype=DEFAULT):
+    """Decode with prefix caching (primed_mamba2_layer.py:964-973): the window comes
+    from the slot at column initial_state_idx[b] of the [batch, blocks] table and
+    the shifted state goes to the slot at column last_block[b]; entries with a pad
+    slot are skipped.  Reads see the pool as it was before the call."""
+    before = conv_state.to(dtype)
+    states = before.clone()
+    out = torch.zeros(x.shape, dtype=dtype)
+    for b in range(x.shape[0]):
+        rs = int(cache_indices[b, int(initial_state_idx[b])])
+        ws = int(cache_indices[b, int(last_block[b])])
+        if rs == pad_slot_id or ws == pad_slot_id:
+            continue
+        o, ns = conv_sequence(x[b:b + 1], before[rs], weight, bias, activation, dtype)
+        out[b] = o[0]
+        states[ws] = ns
+    return out, states

@@ -168,8 +168,15 @@ def test_errors(dev):
         hmx.causal_conv1d_fn(x.t(), torch.zeros(32, 4, device=dev))    # weight/dim mismatch
     with pytest.raises(ValueError):    # the cache rows themselves, not the [slots, dim, len] view
         hmx.causal_conv1d_update(x, pool.transpose(1, 2).contiguous(), w)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(ValueError):    # the block arguments come together, with a slot table
         hmx.causal_conv1d_update(x, pool, w, initial_state_idx=torch.zeros(8, device=dev))
+    with pytest.raises(ValueError):
+        hmx.causal_conv1d_fn(x.t(), w, conv_states=pool, num_computed_tokens=torch.zeros(
+            1, dtype=torch.int32, device=dev))
+    with pytest.raises(ValueError):    # prefix caching needs a [batch, blocks] table
+        z = torch.zeros(8, dtype=torch.int32, device=dev)
+        hmx.causal_conv1d_update(x, pool, w, conv_state_indices=z, initial_state_idx=z,
+                                 block_idx_last_scheduled_token=z)
 
 
 def test_prefill_more_tiles_than_one_launch(dev):
@@ -240,3 +247,65 @@ def test_update_spec_accepts_like_plain_conv(dev, W, L, act):
         _close(o2[r], o_r2)
     untouched = [s for s in range(slots) if s not in set(int(i) for i in idx if i >= 0)]
     assert torch.equal(st1[untouched], pool[untouched])
+
+
+@pytest.mark.parametrize("W,bs", [(4, 16), (3, 64), (2, 8)])
+def test_prefill_prefix_cache_blocks(dev, W, bs):
+    """Prefix caching (vLLM's block arguments, primed_mamba2_layer.py:770-793): a
+    [batch, blocks] slot table, sequences continuing num_computed_tokens tokens (0,
+    unaligned, aligned, a block boundary inside the first state_len tokens, one
+    crossing 64-token tiles and several blocks), a padded last column and a pad
+    in a middle column.  Outputs within the output rounding; every written block
+    state and every untouched slot bit for bit."""
+    dim, L = 1024, W - 1
+    ncomp = [0, 2 * bs + 3, 3 * bs, bs - 1, 5, bs + 2]
+    lens = [3 * bs + 7, 2 * bs + 11, 1, 2, 150, 2 * bs]
+    slots = 128
+    qs, x, w, b, pool, g = _setup(lens, dim, W, slots, L, 40 + W)
+    nblk = max((n + t - 1) // bs + 1 for n, t in zip(ncomp, lens))
+    assert len(lens) * nblk <= slots
+    table = torch.randperm(slots, generator=g)[:len(lens) * nblk].view(len(lens), nblk)
+    table = table.to(torch.int32)
+    table[4, (ncomp[4] + lens[4] - 1) // bs] = -1    # sequence 4: padded entry
+    table[5, ncomp[5] // bs] = -1                    # sequence 5: its first block (and read slot) pad
+    init = torch.tensor([max(n - 1, 0) // bs for n in ncomp], dtype=torch.int32)
+    first = torch.tensor([n // bs for n in ncomp], dtype=torch.int32)
+    last = torch.tensor([(n + t - 1) // bs for n, t in zip(ncomp, lens)], dtype=torch.int32)
+    has = torch.tensor([n > 0 for n in ncomp])
+    nc = torch.tensor(ncomp, dtype=torch.int32)
+    out_r, pool_r = ref.causal_conv1d_varlen_blocks(x, w, b, pool, qs, table, has, init, first,
+                                                    last, nc, bs, "silu")
+    pool_d = pool.to(dev)
+    d = lambda t: t.to(dev)
+    out = hmx.causal_conv1d_fn(x.to(dev).t(), d(w), d(b), conv_states=pool_d.transpose(1, 2),
+                               query_start_loc=d(qs), cache_indices=d(table),
+                               has_initial_state=d(has), activation="silu",
+                               block_idx_first_scheduled_token=d(first),
+                               block_idx_last_scheduled_token=d(last), initial_state_idx=d(init),
+                               num_computed_tokens=d(nc), block_size_to_align=bs)
+    torch.cuda.synchronize()
+    _close(out.t(), out_r)
+    assert torch.equal(pool_d.cpu(), pool_r.to(pool.dtype))
+
+
+def test_update_prefix_cache_blocks(dev):
+    """Decode with prefix caching (primed_mamba2_layer.py:964-973): the window from
+    the column of the last computed token, the shifted state into the column of the
+    scheduled one (the same column or the next block's), pad entries skipped."""
+    W, dim = 4, 2048 + 512
+    g = torch.Generator().manual_seed(77)
+    pool = torch.randn(12, W - 1, dim, generator=g).bfloat16()
+    x = torch.randn(4, dim, generator=g).bfloat16()
+    w = torch.randn(dim, W, generator=g) * 0.5
+    table = torch.tensor([[4, 7, 0], [1, 2, 3], [-1, 9, 10], [5, 6, 11]], dtype=torch.int32)
+    init = torch.tensor([0, 2, 0, 1], dtype=torch.int32)
+    last = torch.tensor([1, 2, 1, 2], dtype=torch.int32)
+    out_r, pool_r = ref.causal_conv1d_update_blocks(x, pool, w, None, "silu", table, init, last)
+    pool_d = pool.to(dev)
+    out = hmx.causal_conv1d_update(x.to(dev), pool_d.transpose(1, 2), w.to(dev), None, "silu",
+                                   conv_state_indices=table.to(dev),
+                                   block_idx_last_scheduled_token=last.to(dev),
+                                   initial_state_idx=init.to(dev))
+    torch.cuda.synchronize()
+    _close(out, out_r)
+    assert torch.equal(pool_d.cpu(), pool_r.to(pool.dtype))

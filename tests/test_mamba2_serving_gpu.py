@@ -15,6 +15,9 @@ grouped operands it relies on.
   untouched), pool slots within the state tolerance (others untouched), conv
   cache bit for bit.  The layer and metadata are stand-ins with the reference's
   attribute names (vLLM is not installed here).
+- Prefix caching (mamba_cache_mode "all"): the same composition run piecewise
+  between the blocks' ends, every block slot checked.
+- The profile run (attn_metadata None) writes nothing.
 """
 from types import SimpleNamespace
 
@@ -242,16 +245,146 @@ def test_conv_ssm_forward_matches_oracle(dev, batch, rope):
             assert torch.equal(pool_g[s], pool[s])
 
 
-def test_conv_ssm_forward_rejects_prefix_caching(dev):
+def test_conv_ssm_forward_needs_positions_for_rope(dev):
     lay, _ = _layer(2, dev)
-    lay.cache_config.mamba_cache_mode = "all"
     md, *_ = _meta("decode", dev)
-    with pytest.raises(NotImplementedError):
-        srv.mamba2_conv_ssm_forward(lay, None, None, md, None, None)
-    lay.cache_config.mamba_cache_mode = "none"
     lay.use_pos_embed = True
     with pytest.raises(ValueError):                 # the rotary embedding needs positions
         srv.mamba2_conv_ssm_forward(lay, None, None, md, None, None)
+
+
+def test_conv_ssm_forward_profile_run(dev):
+    """attn_metadata None (vLLM's profile run, :676-697): nothing is written, and the
+    x columns repeated over the heads are returned, as the layer returns them."""
+    lay, dproj = _layer(4, dev)
+    g0 = torch.Generator().manual_seed(41)
+    proj = torch.randn(9, dproj, generator=g0).bfloat16().to(dev)
+    output = torch.zeros(9, I, dtype=torch.bfloat16, device=dev)
+    got = srv.mamba2_conv_ssm_forward(lay, proj, output, None, None, None)
+    torch.cuda.synchronize()
+    hs = proj[:, I:I + XB].reshape(9, HX, P)
+    assert torch.equal(got, hs.repeat_interleave(H // HX, 1).reshape(9, H * P))
+    assert torch.equal(output, torch.zeros_like(output))
+
+
+APC_BS, APC_CHUNK, APC_SLOTS = 128, 64, 24
+
+
+def _prefix_chunks(lens, computed, chunk):
+    """vLLM's prefix-cache chunking: a chunk ends where the absolute position
+    (num_computed_tokens plus the offset) is a multiple of chunk."""
+    cu, seq, last, pos = [0], [], [], 0
+    for n, (L, nc) in enumerate(zip(lens, computed)):
+        off = 0
+        while off < L:
+            off += min(chunk - (nc + off) % chunk, L - off)
+            cu.append(pos + off)
+            seq.append(n)
+        pos += L
+        last.append(len(seq) - 1)
+    return cu, seq, last
+
+
+def _meta_apc(dev, dec_nc, pre):
+    """Prefix-caching metadata (the fields primed_mamba2_layer.py:728-754, :844-863
+    read) for decodes continuing dec_nc tokens and prefills (num_computed, length),
+    with vLLM's block indices: the blocks of the last computed token, the first and
+    the last scheduled token (block 0 before any token)."""
+    reqs = [(nc, 1) for nc in dec_nc] + list(pre)
+    nblk = max((nc + L - 1) // APC_BS + 1 for nc, L in reqs)
+    g = torch.Generator().manual_seed(3)
+    table = torch.randperm(APC_SLOTS, generator=g)[:len(reqs) * nblk].view(len(reqs), nblk)
+    table = table.to(torch.int32)
+    lc = torch.tensor([max(nc - 1, 0) // APC_BS for nc, _ in reqs], dtype=torch.int32)
+    ls = torch.tensor([(nc + L - 1) // APC_BS for nc, L in reqs], dtype=torch.int32)
+    nd = len(dec_nc)
+    plens, pnc = [L for _, L in pre], [nc for nc, _ in pre]
+    cu_c, seq, last = _prefix_chunks(plens, pnc, APC_CHUNK)
+    t = lambda v: torch.tensor(v, dtype=torch.int32, device=dev)
+    md = SimpleNamespace(
+        num_prefills=len(pre), num_decode_tokens=nd, num_prefill_tokens=sum(plens),
+        state_indices_tensor=table.to(dev), has_initial_states_p=torch.tensor(
+            [nc > 0 for nc in pnc], device=dev), prep_initial_states=True,
+        query_start_loc_p=t([0] + list(torch.tensor(plens).cumsum(0).tolist())),
+        chunk_size=APC_CHUNK, cu_chunk_seqlen_p=t(cu_c), seq_idx_p=t(seq),
+        last_chunk_indices_p=t(last), block_idx_last_computed_token=lc.to(dev),
+        block_idx_last_scheduled_token=ls.to(dev),
+        block_idx_first_scheduled_token_p=t([nc // APC_BS for nc in pnc]),
+        num_computed_tokens_p=t(pnc))
+    return md, reqs, table
+
+
+def _expected_apc(lay, reqs, table, hbc, dt, conv_cache, pool):
+    """Per request: the conv and the SSD recurrence from the slot of its last
+    computed block (zeros for a request with no computed token), run piecewise
+    between the block ends of this step; each block's slot gets the conv and SSD
+    states at its end, the last scheduled block's slot those after the last token."""
+    w, bias = lay.conv_weights.cpu(), lay.conv1d.bias.cpu()
+    conv_new, pool_new = conv_cache.clone(), pool.clone().double()
+    outs, t0 = [], 0
+    for r, (nc, L) in enumerate(reqs):
+        lc, fs, ls = max(nc - 1, 0) // APC_BS, nc // APC_BS, (nc + L - 1) // APC_BS
+        rs, sl = int(table[r, lc]), slice(t0, t0 + L)
+        t0 += L
+        cst = conv_cache[rs] if nc > 0 else torch.zeros(W - 1, CD, dtype=conv_cache.dtype)
+        o_c, _ = cref.conv_sequence(hbc[sl], cst, w, bias, "silu")
+        hist = torch.cat([cst, hbc[sl]])
+        xc = o_c.bfloat16()
+        x = xc[:, :XB].reshape(L, HX, P).repeat_interleave(H // HX, 1)
+        Bh = xc[:, XB:2 * XB].reshape(L, HX, N).repeat_interleave(H // HX, 1)
+        Ch = xc[:, 2 * XB:].reshape(L, H, N)
+        dtp = sref.dt_transform(dt[sl], lay.dt_bias.cpu(), True)
+        S = pool[rs] if nc > 0 else None
+        ends = [(k + 1) * APC_BS - nc for k in range(fs, ls)] + [L]
+        a, ys = 0, []
+        for j, e in enumerate(ends):
+            y, S = sref.ssd_seq(x[a:e], dtp[a:e], lay.A.cpu(), Bh[a:e], Ch[a:e], lay.D.cpu(),
+                                None, S)
+            ys.append(y)
+            slot = int(table[r, fs + j])
+            pool_new[slot] = S
+            conv_new[slot] = hist[e:e + W - 1]
+            a = e
+        outs.append(torch.cat(ys))
+    return torch.cat(outs), conv_new, pool_new
+
+
+@pytest.mark.parametrize("batch", ["mixed", "prefill", "decode"])
+def test_conv_ssm_forward_prefix_caching(dev, batch):
+    """mamba_cache_mode "all" (primed_mamba2_layer.py:728-1021): requests continuing
+    0, unaligned, block-aligned and chunk-unaligned computed tokens, prefills
+    crossing several blocks and one ending on a block boundary; decodes in the
+    middle of a block and at a block boundary (reading block 0, writing block 1).
+    Outputs, every block slot's conv (bit for bit) and SSD state, untouched slots
+    unchanged."""
+    lay, dproj = _layer(5, dev)
+    lay.cache_config = SimpleNamespace(mamba_cache_mode="all", mamba_block_size=APC_BS)
+    dec = {"mixed": [127, 128], "prefill": [], "decode": [5, 128, 300]}[batch]
+    pre = {"mixed": [(100, 200), (0, 300), (256, 64)], "prefill": [(130, 3), (0, 256), (70, 90)],
+           "decode": []}[batch]
+    md, reqs, table = _meta_apc(dev, dec, pre)
+    n = sum(L for _, L in reqs)
+    g0 = torch.Generator().manual_seed(50)
+    proj = torch.randn(n + 3, dproj, generator=g0).bfloat16()
+    proj[:, I + CD:I + CD + H] = proj[:, I + CD:I + CD + H] * 0.5 - 1.5
+    conv_cache = torch.randn(APC_SLOTS, W - 1, CD, generator=g0).bfloat16()
+    pool = torch.randn(APC_SLOTS, H, P, N, generator=g0) * 0.1
+    cc_d, pool_d = conv_cache.to(dev), pool.to(dev)
+    output = torch.zeros(n + 3, I, dtype=torch.bfloat16, device=dev)
+    srv.mamba2_conv_ssm_forward(lay, proj.to(dev), output, md, cc_d.transpose(1, 2), pool_d)
+    torch.cuda.synchronize()
+    o_r, conv_r, pool_r = _expected_apc(lay, reqs, table, _normed(lay, proj.to(dev)).cpu(),
+                                        proj[:, I + CD:I + CD + H], conv_cache, pool)
+    got = output.cpu()
+    assert_out_close(got[:n].view(n, H, P), o_r)
+    assert torch.equal(got[n:], torch.zeros_like(got[n:]))
+    assert torch.equal(cc_d.cpu(), conv_r)
+    pool_g = pool_d.cpu()
+    for s in range(APC_SLOTS):
+        if not torch.equal(conv_r[s], conv_cache[s]) or not torch.equal(pool_r[s].float(), pool[s]):
+            assert_state_close(pool_g[s], pool_r[s], what=f"slot {s}")
+        else:
+            assert torch.equal(pool_g[s], pool[s]), f"slot {s} changed"
 
 
 def test_conv_ssm_forward_decode_graph_replays_match_eager(dev):
