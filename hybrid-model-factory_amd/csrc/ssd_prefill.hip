@@ -141,28 +141,56 @@ struct Raw {
   float dt;
 };
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// A raw buffer resource over rows 0 .. nrows-1 (w bf16 features each, ts elements
+// apart) from base: accesses past them read zeros and write nothing, which masks a
+// chunk's missing rows.  The base is uniform, so a chunk's addressing is scalar and
+// each lane keeps one fixed byte offset per array (row tid / (w/8), features
+// 8 (tid % (w/8)) ..); the i-th vector of a thread adds the uniform i * (rows per
+// pass) * ts (the hardware's scalar offset).  The host keeps 64 rows of any stride
+// inside 32-bit offsets.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const bf16* base, int nrows,
+                                                           int64_t ts, int w) {
+  const uint32_t bytes = nrows > 0 ? (uint32_t)(((int64_t)(nrows - 1) * ts + w) * 2) : 0u;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(base), 0, bytes, 0x00020000);
+}
+__device__ __forceinline__ bf16x8 ld_rows(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t soff) {
+  return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, off, soff, 0));
+}
+__device__ __forceinline__ uint32_t lane_off(int tid, int w, int64_t ts) {
+  return (uint32_t)(((int64_t)(tid / (w / 8)) * ts + (tid % (w / 8)) * 8) * 2);
+}
+
 template <int P, int N, int MODE>
 __device__ __forceinline__ void load_raw(Raw<P, N>& r, const Params& p, int tok0, int nval,
                                          int h, int hx, int g, int gc, int tid) {
   using K = Cfg<P, N>;
+  constexpr int RX = NTHR / (P / 8), RB = NTHR / (N / 8);   // rows per pass
+  const auto rx = rows_rsrc(p.x + (int64_t)tok0 * p.x_ts + (int64_t)hx * p.x_hs, nval, p.x_ts, P);
+  const uint32_t ox = lane_off(tid, P, p.x_ts);
 #pragma unroll
-  for (int i = 0; i < K::VX; ++i) {
-    const int e = tid + NTHR * i, row = e / (P / 8), c8 = (e % (P / 8)) * 8;
-    const bool ok = row < nval;
-    const int64_t tok = tok0 + row;
-    r.x[i] = ok ? *reinterpret_cast<const bf16x8*>(p.x + tok * p.x_ts + hx * p.x_hs + c8) : bf16x8{};
-    if (MODE == MODE_OUT)
-      r.z[i] = (ok && p.z) ? *reinterpret_cast<const bf16x8*>(p.z + tok * p.z_ts + h * p.z_hs + c8)
-                           : bf16x8{};
+  for (int i = 0; i < K::VX; ++i) r.x[i] = ld_rows(rx, ox, (uint32_t)(i * RX * p.x_ts * 2));
+  if (MODE == MODE_OUT) {
+    if (p.z) {
+      const auto rz = rows_rsrc(p.z + (int64_t)tok0 * p.z_ts + (int64_t)h * p.z_hs, nval, p.z_ts, P);
+      const uint32_t oz = lane_off(tid, P, p.z_ts);
+#pragma unroll
+      for (int i = 0; i < K::VX; ++i) r.z[i] = ld_rows(rz, oz, (uint32_t)(i * RX * p.z_ts * 2));
+    } else {
+#pragma unroll
+      for (int i = 0; i < K::VX; ++i) r.z[i] = bf16x8{};
+    }
   }
+  const auto rb = rows_rsrc(p.B + (int64_t)tok0 * p.b_ts + (int64_t)g * p.b_gs, nval, p.b_ts, N);
+  const uint32_t ob = lane_off(tid, N, p.b_ts);
 #pragma unroll
-  for (int i = 0; i < K::VB; ++i) {
-    const int e = tid + NTHR * i, row = e / (N / 8), c8 = (e % (N / 8)) * 8;
-    const bool ok = row < nval;
-    const int64_t tok = tok0 + row;
-    r.b[i] = ok ? *reinterpret_cast<const bf16x8*>(p.B + tok * p.b_ts + g * p.b_gs + c8) : bf16x8{};
-    if (MODE == MODE_OUT)
-      r.c[i] = ok ? *reinterpret_cast<const bf16x8*>(p.C + tok * p.c_ts + gc * p.c_gs + c8) : bf16x8{};
+  for (int i = 0; i < K::VB; ++i) r.b[i] = ld_rows(rb, ob, (uint32_t)(i * RB * p.b_ts * 2));
+  if (MODE == MODE_OUT) {
+    const auto rc = rows_rsrc(p.C + (int64_t)tok0 * p.c_ts + (int64_t)gc * p.c_gs, nval, p.c_ts, N);
+    const uint32_t oc = lane_off(tid, N, p.c_ts);
+#pragma unroll
+    for (int i = 0; i < K::VB; ++i) r.c[i] = ld_rows(rc, oc, (uint32_t)(i * RB * p.c_ts * 2));
   }
   const int t = tid - (NTHR - L);   // the last wave loads dt (lane t = token t)
   if (t >= 0)
@@ -296,7 +324,9 @@ __global__ __launch_bounds__(NTHR, (P == 128 && MODE == MODE_OUT) ? 1 : 2) void 
   // coalesced store of the y tile staged in sY (chunk starting at tok0); the plain
   // pass also sums the rows (ysum: inf or NaN there flags the walk)
   float ysum = 0.f;
+  const uint32_t oy = lane_off(tid, P, p.y_ts);
   const auto store_y = [&](int tok0, int nval) {
+    const auto ry = rows_rsrc(p.y + (int64_t)tok0 * p.y_ts + (int64_t)h * p.y_hs, nval, p.y_ts, P);
 #pragma unroll
     for (int i = 0; i < K::VX; ++i) {
       const int e = tid + NTHR * i, row = e / (P / 8), c8 = (e % (P / 8)) * 8;
@@ -307,8 +337,9 @@ __global__ __launch_bounds__(NTHR, (P == 128 && MODE == MODE_OUT) ? 1 : 2) void 
           ysum = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{yr[j], yr[j + 1]},
                                                   bf16x2{(bf16)1.f, (bf16)1.f}, ysum, false);
       }
-      if (row < nval)
-        *reinterpret_cast<bf16x8*>(p.y + (int64_t)(tok0 + row) * p.y_ts + h * p.y_hs + c8) = yr;
+      // rows from nval on fall outside the resource: not written
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, yr), ry, oy,
+                                             (uint32_t)(i * (NTHR / (P / 8)) * p.y_ts * 2), 0);
     }
   };
 
@@ -703,6 +734,11 @@ extern "C" int hmx_ssd_chunk_fwd(const void* x, int64_t x_ts, int64_t x_hs, cons
   for (int64_t st : strides)
     HMX_REQUIRE(st % 8 == 0, HMX_EINVAL,
                 "hmx_ssd_chunk_fwd: token/head strides must be multiples of 8 elements");
+  // a chunk's 64 rows are addressed with 32-bit byte offsets
+  for (int64_t ts : {x_ts, b_ts, c_ts, y_ts, z ? z_ts : (int64_t)0})
+    HMX_REQUIRE(ts >= 0 && ts < ((int64_t)1 << 24), HMX_EUNSUPPORTED,
+                "hmx_ssd_chunk_fwd: token strides must be below 2^24 elements (got %lld)",
+                (long long)ts);
   HMX_REQUIRE(!(h0 || h_final) || ((state_dtype == HMX_F32 || state_dtype == HMX_BF16) &&
                                     state_slot_stride % 4 == 0 &&
                                     ((uintptr_t)h0 | (uintptr_t)h_final) % 16 == 0),
