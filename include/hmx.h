@@ -251,7 +251,9 @@ int hmx_gdn_chunk_fwd(const void* q, int64_t q_token_stride, const void* k,
  * as hmx_gdn_chunk_fwd.  Returns HMX_EINVAL when the segment table needs more
  * workspace than the array holds (hmx_gdn_chunk_workspace_bytes > the limit).
  * The array's address is looked up once per device, on the first call with that
- * device current; later calls on the device reuse it.  The stream must belong to
+ * device current; later calls on the device reuse it.  The array has a code object
+ * of its own, loaded by that first lookup: a process reserves it only on devices
+ * where it calls this entry point.  The stream must belong to
  * the current device.  Calls that overlap on one device share the array and race:
  * serialise them (one stream, or events).
  * No counterpart in the reference: for callers that cannot allocate device memory

@@ -2,7 +2,8 @@
 workspace is a static device array: called through the C ABI, its outputs and end
 states equal hmx_gdn_chunk_fwd's (same kernels, same segment table, caller
 workspace) bit for bit, on two calls in a row, the second with a smaller input
-(the rejection of oversized tables is a CPU test in test_abi.py)."""
+(the rejection of oversized tables is a CPU test in test_abi.py), and that the
+array is placed in device memory only when the entry point is first called."""
 import pytest
 import torch
 import torch.nn.functional as F
@@ -48,6 +49,27 @@ def _call(name, q, k, v, g, beta, h0, bounds, seg_chunks, workspace):
     _lib.call(name, *args, None, None, _lib.stream_of(q))
     torch.cuda.synchronize()
     return o, ht, len(rows)
+
+
+def test_noalloc_scratch_reserved_at_first_call(dev):
+    """The scratch array sits in a code object of its own (no kernels), which the
+    runtime loads at the entry point's first call on a device: after the library's
+    other kernels have run (the workspace entry here), device memory still drops
+    by the array's size at that first call, and by nothing at the next.  Runs
+    first in this file, before any other call of the entry point in the process."""
+    inp = _inputs(1000, 4, 4, [300, 0, 700], 71, dev)
+    _call("hmx_gdn_chunk_fwd", *inp, 4, True)       # loads the prefill's code object
+    _call("hmx_gdn_chunk_fwd", *inp, 4, True)       # and fills torch's cache for o / ht
+    free0 = torch.cuda.mem_get_info()[0]
+    _call("hmx_gdn_chunk_fwd_noalloc", *inp, 4, False)
+    free1 = torch.cuda.mem_get_info()[0]
+    _call("hmx_gdn_chunk_fwd_noalloc", *inp, 4, False)
+    free2 = torch.cuda.mem_get_info()[0]
+    mib = 1 << 20
+    print(f"[no_alloc] free before / after the first call / after the second: "
+          f"{free0 // mib} / {free1 // mib} / {free2 // mib} MiB", flush=True)
+    assert free0 - free1 >= 64 * mib - 2 * mib
+    assert abs(free1 - free2) <= 2 * mib
 
 
 def test_noalloc_equals_workspace_entry(dev):
