@@ -49,7 +49,9 @@ speculative ``causal_conv1d_update`` (slot ``spec_state_indices_tensor[:, 0]``,
 ``spec_state_indices_tensor[n, num_accepted_tokens[n] - 1]`` and leaves the state
 after the sequence's last token in slot ``[n, 0]`` (fused_recurrent_gqa.py:95-105,
 :135-144); GKA's decode, as the reference's, advances each spec sequence by its
-first token only (slot ``[n, 0]``).  With non-spec
+first token only (slot ``[n, 0]``); the rows of its other draft tokens are left
+undefined, as the reference's ``new_empty`` output leaves them
+(chebyshev_iteration_gqa.py:211).  With non-spec
 tokens in the batch too, each part runs on its index-selected rows and the outputs
 return by index (the reference's ``index_copy_``, :923-934); the host offsets
 (``query_start_loc_cpu``) then describe the whole batch, not the non-spec prefill,

@@ -11,18 +11,20 @@ state after its last token in slot [n, 0] (fused_recurrent_gqa.py:95-105,
 :135-144); GKA's decode, as the reference's
 (chebyshev_iteration_gqa.py: one token per sequence), advances each spec sequence
 by its first token only, from and to slot [n, 0] (its other rows are not
-written).  The non-spec part is the composition of test_serving_gpu.py.
+written).  The non-spec part is the composition of test_serving_gpu.py.  With the
+output norm fused (o_norm), each part takes its rows of the gate.
 """
 from types import SimpleNamespace
 
 import pytest
 import torch
 
+import hmx
 import hmx.serving as srv
 from oracle import conv as cref
 from oracle import gdn as gref
 from oracle import gka as kref
-from util import assert_out_close, assert_state_close
+from util import assert_out_close, assert_state_close, half_ulp
 
 import test_serving_gpu as base
 
@@ -76,6 +78,62 @@ def _qkv(xb):
     L = xb.shape[0]
     return (xb[:, :H * D].view(L, H, D), xb[:, H * D:(H + HKV) * D].view(L, HKV, D),
             xb[:, (H + HKV) * D:].view(L, HKV, D))
+
+
+def _spec_run(kind, mixed, dev, o_norm):
+    """One core call on the spec batch; returns (core [n + pad, H, D], states, z, wn)."""
+    lay = base._layer(kind, 31)
+    md, m = _meta(mixed, dev)
+    n = md.num_actual_tokens
+    g0 = torch.Generator().manual_seed(77)
+    conv_cache = torch.randn(SLOTS, W - 1 + SPEC_S, CONV_DIM, generator=g0).bfloat16()
+    s1 = torch.randn(SLOTS, H, D, D, generator=g0) * 0.05
+    xk = torch.randn(SLOTS, H, D, 16, generator=g0) * 0.05
+    hkk = xk @ xk.transpose(-1, -2)
+    mixed_qkv = torch.randn(n + 5, CONV_DIM, generator=g0).bfloat16()
+    a, b, alpha_in = (torch.randn(n + 5, H, generator=g0).bfloat16() for _ in range(3))
+    z = torch.randn(n + 5, H, D, generator=g0).bfloat16()
+    wn = (torch.rand(D, generator=g0) + 0.5).bfloat16()
+    on = (wn.to(dev), z.to(dev), 1e-6) if o_norm else None
+    lay_d = base._to(lay, dev)
+    core = torch.zeros(n + 5, H, D, dtype=torch.bfloat16, device=dev)
+    if kind == "gdn":
+        ssm = s1.to(dev)
+        srv.gdn_forward_core(lay_d, mixed_qkv.to(dev), b.to(dev), a.to(dev), core, md,
+                             conv_cache.to(dev).transpose(1, 2), ssm, o_norm=on)
+        states = [ssm]
+    else:
+        hkv_d, hkk_d = s1.to(dev), hkk.to(dev)
+        srv.gka_forward_core(lay_d, mixed_qkv.to(dev), a.to(dev), alpha_in.to(dev), b.to(dev),
+                             core, md, conv_cache.to(dev).transpose(1, 2), hkk_d, hkv_d,
+                             o_norm=on)
+        states = [hkv_d, hkk_d]
+    torch.cuda.synchronize()
+    return core, [t.cpu() for t in states], z, wn, n
+
+
+@pytest.mark.parametrize("kind", ["gdn", "gka"])
+@pytest.mark.parametrize("mixed", [False, True])
+def test_forward_core_spec_fused_o_norm(dev, kind, mixed):
+    """o_norm on a speculative batch: the spec and non-spec parts each take their
+    rows of the gate z; the result equals the layer's norm of the plain core's
+    output (within the rounding of o before the norm), and the states are the same."""
+    plain, st_p, z, wn, n = _spec_run(kind, mixed, dev, False)
+    fused, st_f, _, _, _ = _spec_run(kind, mixed, dev, True)
+    rows = list(range(n))
+    if kind == "gka":   # only a spec sequence's first token has an output (as the reference's)
+        _, m = _meta(mixed, dev)
+        drafts = {t for j in range(m["nsd"]) for t in m["spec_tok"][j * T1 + 1:(j + 1) * T1]}
+        rows = [t for t in rows if t not in drafts]
+    sel = torch.tensor(rows, device=dev)
+    expect = hmx.rms_norm_gated(plain[sel], z.to(dev)[sel], wn.to(dev), 1e-6).cpu()
+    got = fused[sel].cpu()
+    assert ((got.double() - expect.double()).abs()
+            <= 2 * half_ulp(expect.double(), torch.bfloat16) + 1e-30).all()
+    assert (got == expect).double().mean().item() >= 0.98
+    assert torch.equal(fused[n:].cpu(), torch.zeros_like(fused[n:].cpu()))
+    for x, y in zip(st_p, st_f):
+        assert torch.equal(x, y)
 
 
 @pytest.mark.parametrize("kind", ["gdn", "gka"])
