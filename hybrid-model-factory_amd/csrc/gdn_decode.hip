@@ -43,13 +43,6 @@ struct RecurrentParams {
   const void* zg; int64_t zg_ts, zg_hs;   // gate rows in q's dtype, or null
   const void* onw; int onw_dt;            // weight [V]
   float on_eps;
-  // CONV kernels: q, k, v are the short causal conv of the layer's projection rows
-  // (one token per sequence), formed in the kernel; see gdn_recurrent_kernel
-  const bf16* cx; int64_t cx_ts;          // [N, conv_dim] rows: q (H K) | k (HKV K) | v (HKV V)
-  const void* cw; int cw_dt; int cwidth;  // [conv_dim, width]
-  const void* cb; int cb_dt;              // [conv_dim] or null
-  bf16* cst; int64_t cst_ss, cst_rs; int cst_len;   // [slots, state_len, conv_dim] pool
-  int cact;                               // silu or none
 };
 
 __device__ __forceinline__ float load_scalar(const void* p, int64_t i, int dtype) {
@@ -81,58 +74,7 @@ __device__ __forceinline__ float rowgroup_sum(float x) {
 // NORM: each output row (one workgroup holds all V <= 128 columns) passes through
 // the gated RMSNorm of hmx_rms_norm_gated (norm before gate) on its way out, from
 // o as rounded to q's dtype; the sum of squares crosses the waves through LDS.
-__device__ __forceinline__ float ld_wt(const void* p, int64_t i, int dt) {
-  return load_scalar(p, i, dt);
-}
-
-// CONV: q, k and v of this (sequence, head) are the short causal conv (vLLM's
-// causal_conv1d_update, decode form) of the projection row x: channel c gives
-// act(bias[c] + sum_{i<W-1} w[c,i] state[L-(W-1)+i][c] + w[c,W-1] x[c]), rounded to
-// bf16 as the conv op stores it, with the same fp32 operations in the same order,
-// so the result equals the conv op followed by this recurrence bit for bit.  The
-// workgroup's 256 threads form its head's K + K + V channels into LDS; the conv
-// state of the q channels (this head's own) and, when HKV == H, of the k and v
-// channels shifts by one row with x appended, in place.  With HKV < H the k / v
-// channels are shared by the heads of a group and their state is left for the
-// caller to shift after the launch.
-template <int K, int V>
-__device__ __forceinline__ void conv_prologue(const RecurrentParams& p, int n, int h, int hk,
-                                              int64_t slot, bf16* sqkv) {
-  const int W = p.cwidth, L = p.cst_len;
-  const bf16* xr = p.cx + (int64_t)n * p.cx_ts;
-  bf16* st = p.cst + slot * p.cst_ss;
-  for (int ch = threadIdx.x; ch < 2 * K + V; ch += blockDim.x) {
-    const int64_t c = ch < K ? (int64_t)h * K + ch
-                    : ch < 2 * K ? (int64_t)p.H * K + (int64_t)hk * K + (ch - K)
-                    : (int64_t)p.H * K + (int64_t)p.HKV * K + (int64_t)hk * V + (ch - 2 * K);
-    float win[3], wv[4];
-#pragma unroll
-    for (int i = 0; i < 3; ++i)
-      if (i < W - 1) win[i] = to_f32(st[(int64_t)(L - (W - 1) + i) * p.cst_rs + c]);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (i < W) wv[i] = ld_wt(p.cw, c * W + i, p.cw_dt);
-    const float xt = to_f32(xr[c]);
-    float a = p.cb ? ld_wt(p.cb, c, p.cb_dt) : 0.f;
-#pragma unroll
-    for (int i = 0; i < 3; ++i)
-      if (i < W - 1) a += wv[i] * win[i];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (i == W - 1) a += wv[i] * xt;
-    const float y = p.cact ? a * __builtin_amdgcn_rcpf(1.0f + fast_exp(-a)) : a;
-    sqkv[ch] = from_f32<bf16>(y);
-    if (ch < K || p.HKV == p.H) {
-      // row r <- row r + 1 for the rows before the window's last, then x last
-      for (int r = 0; r + 1 < L; ++r)
-        st[(int64_t)r * p.cst_rs + c] = st[(int64_t)(r + 1) * p.cst_rs + c];
-      st[(int64_t)(L - 1) * p.cst_rs + c] = xr[c];
-    }
-  }
-  __syncthreads();
-}
-
-template <int K, typename TQ, typename TS, bool NORM, typename TG, bool CONV = false>
+template <int K, typename TQ, typename TS, bool NORM, typename TG>
 __global__ __launch_bounds__(256) void gdn_recurrent_kernel(RecurrentParams p) {
   constexpr int R = K / 8;  // rows per lane
   const int lane = threadIdx.x & 63;
@@ -190,33 +132,20 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(RecurrentParams p) {
 #pragma unroll
     for (int i = 0; i < R; ++i) S[i][0] = S[i][1] = S[i][2] = S[i][3] = 0.f;
   }
-  // CONV: the state loads above are in flight while the conv forms q, k, v
-  __shared__ bf16 sqkv[CONV ? 3 * K : 1];
-  if constexpr (CONV) conv_prologue<K, K>(p, n, h, hk, write_row, sqkv);
 
   for (int64_t t = 0; t < T; ++t) {
     const int64_t tok = bos + t;
     float kr[R], qr[R], vv[4], bb[4];
-    if constexpr (CONV) {   // one token per sequence (T == 1)
+    {
+      const TQ* kp = static_cast<const TQ*>(p.k) + tok * p.k_ts + (int64_t)hk * K + r;
+      const TQ* qp = static_cast<const TQ*>(p.q) + tok * p.q_ts + (int64_t)h * K + r;
 #pragma unroll
       for (int i = 0; i < R; ++i) {
-        qr[i] = to_f32(sqkv[r + 8 * i]);
-        kr[i] = to_f32(sqkv[K + r + 8 * i]);
+        kr[i] = to_f32(kp[8 * i]);
+        qr[i] = to_f32(qp[8 * i]);
       }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) vv[j] = to_f32(sqkv[2 * K + col + j]);
-    } else {
-      {
-        const TQ* kp = static_cast<const TQ*>(p.k) + tok * p.k_ts + (int64_t)hk * K + r;
-        const TQ* qp = static_cast<const TQ*>(p.q) + tok * p.q_ts + (int64_t)h * K + r;
-#pragma unroll
-        for (int i = 0; i < R; ++i) {
-          kr[i] = to_f32(kp[8 * i]);
-          qr[i] = to_f32(qp[8 * i]);
-        }
-      }
-      load_vec<4>(static_cast<const TQ*>(p.v) + tok * p.v_ts + (int64_t)hk * V + col, vv);
     }
+    load_vec<4>(static_cast<const TQ*>(p.v) + tok * p.v_ts + (int64_t)hk * V + col, vv);
     float gt;
     if constexpr (std::is_same_v<TG, ProjG>) {
       gt = gp_g(p.gp, tok, h);
@@ -345,84 +274,7 @@ static int dispatch_qkv(const RecurrentParams& p, int64_t N, int qkv_dt, int sta
   return set_error(HMX_EUNSUPPORTED, "hmx_gdn_recurrent_fwd: qkv dtype %d", qkv_dt);
 }
 
-// The conv + decode kernels (K = V = 128, bf16 rows, one token per sequence).
-template <typename TS, typename TG>
-static void launch_conv_g(const RecurrentParams& p, int64_t N, hipStream_t s) {
-  const dim3 grid((unsigned)(N * p.H)), block(256);
-  if (p.onw)
-    hipLaunchKernelGGL((gdn_recurrent_kernel<128, bf16, TS, true, TG, true>), grid, block, 0, s, p);
-  else
-    hipLaunchKernelGGL((gdn_recurrent_kernel<128, bf16, TS, false, TG, true>), grid, block, 0, s,
-                       p);
-}
-
 }  // namespace hmx
-
-extern "C" int hmx_gdn_conv_recurrent_fwd(
-    const void* x, int64_t x_token_stride, int32_t x_dtype, const void* conv_weight,
-    int32_t conv_weight_dtype, int32_t width, const void* conv_bias, int32_t conv_bias_dtype,
-    void* conv_state, int64_t conv_state_slot_stride, int64_t conv_state_row_stride,
-    int32_t conv_state_len, int32_t activation, const void* g, int32_t g_dtype, const void* beta,
-    int32_t beta_dtype, void* o, void* state, int64_t state_row_stride, int32_t state_dtype,
-    const int32_t* state_indices, int64_t N, int32_t H, int32_t HKV, int32_t K, int32_t V,
-    float scale, int32_t use_qk_l2norm, const hmx_gated_norm* o_norm, const hmx_gate_proj* gates,
-    void* stream) {
-  using namespace hmx;
-  const char* fn = "hmx_gdn_conv_recurrent_fwd";
-  HMX_REQUIRE(K == 128 && V == 128, HMX_EUNSUPPORTED, "%s: K = V = 128 only (got %d, %d)", fn, K, V);
-  HMX_REQUIRE(H > 0 && HKV > 0 && H % HKV == 0, HMX_EINVAL,
-              "%s: H=%d must be a positive multiple of HKV=%d", fn, H, HKV);
-  HMX_REQUIRE(x_dtype == HMX_BF16, HMX_EUNSUPPORTED, "%s: projection rows must be bf16", fn);
-  HMX_REQUIRE(width >= 2 && width <= 4 && conv_state_len >= width - 1 && conv_state_len <= 8,
-              HMX_EUNSUPPORTED, "%s: conv width %d in 2..4, state_len %d in [width-1, 8]", fn,
-              width, conv_state_len);
-  HMX_REQUIRE(conv_weight_dtype >= 0 && conv_weight_dtype <= 2 &&
-                  (!conv_bias || (conv_bias_dtype >= 0 && conv_bias_dtype <= 2)),
-              HMX_EUNSUPPORTED, "%s: conv weight / bias dtype", fn);
-  if (gates) {
-    const int rc = check_gates(gates, false, fn);
-    if (rc != HMX_OK) return rc;
-  }
-  HMX_REQUIRE(x && conv_weight && conv_state && (gates || (g && beta)) && o && state &&
-                  state_indices, HMX_EINVAL, "%s: null pointer", fn);
-  HMX_REQUIRE(gates || (g_dtype >= 0 && g_dtype <= 2 && beta_dtype >= 0 && beta_dtype <= 2),
-              HMX_EUNSUPPORTED, "%s: g/beta dtype", fn);
-  if (N == 0) return HMX_OK;
-  RecurrentParams p{};
-  p.g = g; p.g_dt = g_dtype; p.beta = beta; p.beta_dt = beta_dtype; p.beta_headwise = 0;
-  p.gp = gates ? *gates : hmx_gate_proj{};
-  p.o = o; p.h0 = state; p.h0_rs = state_row_stride; p.ht = state; p.ht_rs = state_row_stride;
-  p.cu_seqlens = nullptr; p.idx = state_indices; p.idx_stride = 1; p.num_accepted = nullptr;
-  p.T = 1; p.H = H; p.HKV = HKV; p.V = V; p.scale = scale; p.l2norm = use_qk_l2norm;
-  p.inplace = 1;
-  p.zg = nullptr; p.zg_ts = p.zg_hs = 0; p.onw = nullptr; p.onw_dt = HMX_F32; p.on_eps = 0.f;
-  if (o_norm) {
-    HMX_REQUIRE(o_norm->weight && o_norm->weight_dtype >= 0 && o_norm->weight_dtype <= 2,
-                HMX_EINVAL, "%s: o_norm needs a weight (dtype code 0-2)", fn);
-    HMX_REQUIRE(!o_norm->gate || ((uintptr_t)o_norm->gate % 8 == 0 &&
-                                  o_norm->gate_token_stride % 8 == 0 &&
-                                  o_norm->gate_head_stride % 8 == 0),
-                HMX_EINVAL, "%s: o_norm gate rows must be aligned", fn);
-    p.zg = o_norm->gate; p.zg_ts = o_norm->gate_token_stride; p.zg_hs = o_norm->gate_head_stride;
-    p.onw = o_norm->weight; p.onw_dt = o_norm->weight_dtype; p.on_eps = o_norm->eps;
-  }
-  p.cx = static_cast<const bf16*>(x); p.cx_ts = x_token_stride;
-  p.cw = conv_weight; p.cw_dt = conv_weight_dtype; p.cwidth = width;
-  p.cb = conv_bias; p.cb_dt = conv_bias_dtype;
-  p.cst = static_cast<bf16*>(conv_state); p.cst_ss = conv_state_slot_stride;
-  p.cst_rs = conv_state_row_stride; p.cst_len = conv_state_len; p.cact = activation != 0;
-  hipStream_t s = (hipStream_t)stream;
-  if (state_dtype == HMX_F32) {
-    if (gates) launch_conv_g<float, ProjG>(p, N, s);
-    else launch_conv_g<float, DynG>(p, N, s);
-  } else if (state_dtype == HMX_BF16) {
-    if (gates) launch_conv_g<bf16, ProjG>(p, N, s);
-    else launch_conv_g<bf16, DynG>(p, N, s);
-  } else {
-    return set_error(HMX_EUNSUPPORTED, "%s: state dtype %d", fn, state_dtype);
-  }
-  return check_launch(fn);
-}
 
 extern "C" int hmx_gdn_recurrent_fwd(
     const void* q, int64_t q_token_stride, const void* k, int64_t k_token_stride, const void* v,

@@ -98,9 +98,6 @@ SIGNATURES: dict[str, list] = {
     "hmx_causal_conv1d_update_blocks": [_P, _I64, _P, _I64, _I32, _P, _I32, _I32, _P, _I32, _P,
                                         _I64, _I64, _I32, _P, _I64, _I32, _P, _P, _I32, _I32,
                                         _I32, _I32, _P],
-    "hmx_gdn_conv_recurrent_fwd": [_P, _I64, _I32, _P, _I32, _I32, _P, _I32, _P, _I64, _I64, _I32,
-                                   _I32, _P, _I32, _P, _I32, _P, _P, _I64, _I32, _P, _I64, _I32,
-                                   _I32, _I32, _I32, _F32, _I32, _P, _P, _P],
     "hmx_rms_norm_gated": [_P, _I64, _P, _I64, _I32, _P, _I32, _P, _I64, _I64, _I32, _F32, _I32, _P],
     "hmx_ssd_state_update": [_P, _I32, _I64, _P, _I32, _I64, _I64, _I64,
                              _P, _I32, _I64, _I64, _I64, _P, _I64, _I64, _I64,

@@ -4,7 +4,6 @@ from .gdn import (chunk_gated_delta_rule, chunk_gated_delta_rule_gqa, fused_gdn_
 from .gka import (chebyshev_iteration_gqa, fused_gka_gating, gka_chebyshev_gla,
                   gka_chebyshev_gla_decode, gka_chebyshev_gla_prefill, torch_decoding_one_step)
 from .conv import causal_conv1d_fn, causal_conv1d_update
-from .conv_decode import gdn_conv_decode
 from .gates import ProjGates
 from .gdn_train import ChunkGatedDeltaRule
 from .gka_train import ChebyshevIteration, GkaChebyshevGla, latent_chebyshev
@@ -16,7 +15,6 @@ __all__ = [
     "ProjGates",
     "fused_gdn_gating",
     "fused_recurrent_gated_delta_rule_gqa",
-    "gdn_conv_decode",
     "fused_recurrent_gated_delta_rule",
     "chunk_gated_delta_rule_gqa",
     "chunk_gated_delta_rule",

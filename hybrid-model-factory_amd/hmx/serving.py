@@ -91,36 +91,15 @@ def _check(layer, md):
                                   "tp_size must be 1")
 
 
-def _conv_weight(layer):
-    w = layer.conv1d.weight
-    return w.view(w.size(0), w.size(2))
-
-
-def _fuse_decode(layer, md, mixed_qkv):
-    """Whether the non-spec decode tokens take the conv + recurrent kernel
-    (ops.gdn_conv_decode): one token per decode, head sizes 128, bf16 rows and no
-    low-rank k/v projection (which needs the conv output before the recurrence)."""
-    return (md.num_decodes > 0 and md.num_decode_tokens == md.num_decodes
-            and getattr(layer, "proj_k", None) is None and layer.head_k_dim == 128
-            and layer.head_v_dim == 128 and mixed_qkv.dtype == torch.bfloat16)
-
-
-def _conv(layer, md, mixed_qkv, cs, skip_decode=False):
+def _conv(layer, md, mixed_qkv, cs):
     """(conv output [n, conv_dim], decode / prefill split) of the non-spec tokens,
-    decodes first, in one buffer; updates the conv state pool in place.  With
-    ``skip_decode`` the decode rows are left to ops.gdn_conv_decode (their rows of the
-    buffer are not written)."""
-    w = _conv_weight(layer)
+    decodes first, in one buffer; updates the conv state pool in place."""
+    w = layer.conv1d.weight
+    w = w.view(w.size(0), w.size(2))
     x = torch.empty_like(mixed_qkv)
     nd, ndt, npf = md.num_decodes, md.num_decode_tokens, md.num_prefills
     idx, has = md.non_spec_state_indices_tensor, md.has_initial_state
     act = layer.activation
-    if skip_decode:
-        if npf > 0:
-            qsl = md.non_spec_query_start_loc_p if nd > 0 else md.non_spec_query_start_loc
-            ops.conv.conv_fwd_rows(mixed_qkv[ndt:].t(), w, None, cs, qsl, idx[nd:],
-                                   None if has is None else has[nd:], act, out=x[ndt:])
-        return x
     if nd > 0 and npf > 0:
         ops.causal_conv1d_update(mixed_qkv[:ndt], cs, w, None, act,
                                  conv_state_indices=idx[:nd], out=x[:ndt])
@@ -250,8 +229,7 @@ def gdn_forward_core(layer, mixed_qkv: torch.Tensor, b: torch.Tensor, a: torch.T
 
     def rest(rows, out, on, qsl_cpu=None):
         mq, aa, bb = rows
-        fuse = _fuse_decode(layer, md, mq)
-        x = _conv(layer, md, mq, conv_state, skip_decode=fuse)
+        x = _conv(layer, md, mq, conv_state)
         q, k, v = _qkv(layer, x)
         # g and beta as fused_gdn_gating and the layer form them (:798-802), computed
         # in the mixer kernels' loads instead of a separate launch
@@ -259,15 +237,7 @@ def gdn_forward_core(layer, mixed_qkv: torch.Tensor, b: torch.Tensor, a: torch.T
         o = out.unsqueeze(0)
         m = mq.shape[0]
         ndt, dec, pre = _split(md, qsl_cpu)
-        if dec is not None and fuse:
-            # the decode conv in the recurrent kernel (:775-785 then :805-823, one launch)
-            tp = layer.tp_size
-            ops.gdn_conv_decode(
-                mq[:ndt], _conv_weight(layer), None, conv_state, layer.activation, ssm_state,
-                dec[1], layer.num_heads // tp, layer.num_kv_heads // tp,
-                use_qk_l2norm_in_kernel=True, gates=gates.tokens(0, ndt), out=o[:, :ndt],
-                **_norm_args(on, 0, ndt))
-        elif dec is not None:
+        if dec is not None:
             cu_d, idx_d = dec
             ops.fused_recurrent_gated_delta_rule_gqa(
                 q[:, :ndt], k[:, :ndt], v[:, :ndt], None, None,

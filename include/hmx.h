@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define HMX_ABI_VERSION 13  /* 2: optional hmx_gated_norm output epilogue in the GDN ops;
+#define HMX_ABI_VERSION 12  /* 2: optional hmx_gated_norm output epilogue in the GDN ops;
                               3: q/k/v token strides in the GDN and GKA ops; slot-indexed
                               state pools and has_initial_state in the GDN, GKA and SSD
                               prefills;
@@ -46,9 +46,7 @@ extern "C" {
                                   conv update);
                               12: hmx_causal_conv1d_fwd_blocks and
                                   hmx_causal_conv1d_update_blocks (prefix-cache block
-                                  arguments);
-                              13: hmx_gdn_conv_recurrent_fwd (the decode conv fused into the
-                                  recurrent step) */
+                                  arguments) */
 
 enum hmx_status {
   HMX_OK = 0,
@@ -164,37 +162,6 @@ int hmx_gdn_recurrent_fwd(const void* q, int64_t q_token_stride, const void* k,
                           int32_t H, int32_t HKV, int32_t K, int32_t V,
                           float scale, int32_t use_qk_l2norm, int32_t inplace_final_state,
                           const hmx_gated_norm* o_norm, const hmx_gate_proj* gates, void* stream);
-
-/*
- * The GDN layer's decode conv and recurrent step in one launch: N sequences of one
- * token, x [N, conv_dim] bf16 projection rows (token stride x_token_stride; channels
- * q H*K | k HKV*K | v HKV*V, K = V = 128), the short causal conv of those rows against
- * the conv state pool (as hmx_causal_conv1d_update: [slots, conv_state_len, conv_dim]
- * bf16 rows, conv_weight [conv_dim, width], optional bias, activation silu (1) or none
- * (0)) gives q, k, v, rounded to bf16 as the conv op stores them, and the recurrence
- * of hmx_gdn_recurrent_fwd follows (in-place final state: h0 = ht = state, one slot
- * per sequence in state_indices [N], shared by both pools; entries < 0 skipped).  The
- * outputs and both pools equal the two ops run one after the other, bit for bit.
- * The conv state of the q channels, and with HKV == H of all channels, shifts in
- * place; with HKV < H the k / v channels are shared by the heads of a group, and the
- * caller shifts their conv state after the launch (hmx_causal_conv1d_update over
- * those channels).  g / beta as in hmx_gdn_recurrent_fwd, or gates from the raw
- * projections; o [N, H, V] (optionally the gated RMSNorm epilogue).
- * No reference counterpart: an hmx fusion of causal_conv1d_update
- *   (vllm-inference/src/primed_vllm/primed_gdn_layer.py:775-785) with
- *   fused_recurrent_gated_delta_rule_gqa (:805-823).
- */
-int hmx_gdn_conv_recurrent_fwd(const void* x, int64_t x_token_stride, int32_t x_dtype,
-                               const void* conv_weight, int32_t conv_weight_dtype, int32_t width,
-                               const void* conv_bias, int32_t conv_bias_dtype, void* conv_state,
-                               int64_t conv_state_slot_stride, int64_t conv_state_row_stride,
-                               int32_t conv_state_len, int32_t activation, const void* g,
-                               int32_t g_dtype, const void* beta, int32_t beta_dtype, void* o,
-                               void* state, int64_t state_row_stride, int32_t state_dtype,
-                               const int32_t* state_indices, int64_t N, int32_t H, int32_t HKV,
-                               int32_t K, int32_t V, float scale, int32_t use_qk_l2norm,
-                               const hmx_gated_norm* o_norm, const hmx_gate_proj* gates,
-                               void* stream);
 
 /*
  * Segment planner (host code: host pointers, no GPU access, no allocation the
