@@ -15,7 +15,8 @@ against HBM.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only LEGS]
   --only takes comma-separated legs (c1, prefill_gqa, prefill_varlen,
-  prefill_layer_gates, onorm, conv, gdn_core, mamba2_core, gka_core, gdn_decode,
+  prefill_layer_gates, onorm, conv, gdn_core, gdn_decode_core, mamba2_core, gka_core,
+  gdn_decode,
   gka_decode, ssd_c4, ssd_primed, ssd_decode, gka8, gka32) or groups (prefill, core,
   decode, ssd, gka); one leg alone is what the committed rocprofv3 counter runs
   profile.
@@ -417,6 +418,76 @@ def bench_core(dev, steps, warmup):
     return dict(ms_ref=ms_ref, ms_core=ms_core, tokens=T)
 
 
+def bench_core_decode(dev, steps=64, warmup=8):
+    """The GDN layer's core on a decode batch at the C2 shape (256 sequences x 1 token,
+    H = HKV = 32, d = 128, conv width 4, fp32 state pool, randperm slots), with the
+    output norm: the reference layer's call sequence over hmx ops (conv update into a
+    new tensor, contiguous q/k/v, gating, recurrent step in place, copy into
+    core_attn_out, separate norm; primed_gdn_layer.py:775-823, :925-936, :621-626)
+    against hmx.serving.gdn_forward_core (the conv update, then the recurrent step on
+    views of its output with the gating and the norm in its loads and epilogue)."""
+    from types import SimpleNamespace
+    import torch
+    import hmx
+    import hmx.serving as srv
+    from hmx import workloads as wl
+    N, H, D = 256, 32, 128
+    cd = 3 * H * D
+    g = torch.Generator(device=dev).manual_seed(wl.SEED_BASE + 14)
+    lay = SimpleNamespace(
+        conv1d=SimpleNamespace(weight=(torch.randn(cd, 1, 4, generator=g, device=dev) * 0.4)
+                               .bfloat16()),
+        activation="silu", A=torch.rand(H, generator=g, device=dev),
+        dt_bias=torch.randn(H, generator=g, device=dev), key_dim=H * D, kv_k_dim=H * D,
+        kv_v_dim=H * D, num_heads=H, num_kv_heads=H, head_k_dim=D, head_v_dim=D, tp_size=1,
+        proj_k=None, allow_neg_eigval=False)
+    nstep = 8                              # distinct inputs, cycled
+    mixed = torch.randn(nstep, N, cd, generator=g, device=dev).bfloat16()
+    a = torch.randn(nstep, N, H, generator=g, device=dev).bfloat16()
+    b = torch.randn(nstep, N, H, generator=g, device=dev).bfloat16()
+    z = torch.randn(nstep, N, H, D, generator=g, device=dev).bfloat16()
+    wn = torch.rand(D, generator=g, device=dev) + 0.5
+    conv_cache = torch.randn(N, 3, cd, generator=g, device=dev).bfloat16()
+    ssm = torch.randn(N, H, D, D, generator=g, device=dev) * 0.02
+    idx = torch.randperm(N, generator=g, device=dev).to(torch.int32)
+    cu = torch.arange(N + 1, dtype=torch.int32, device=dev)
+    md = SimpleNamespace(spec_sequence_masks=None, num_actual_tokens=N, num_decodes=N,
+                         num_decode_tokens=N, num_prefills=0, non_spec_query_start_loc=cu,
+                         non_spec_state_indices_tensor=idx, has_initial_state=None,
+                         non_spec_query_start_loc_d=None, non_spec_query_start_loc_p=None)
+    core = torch.zeros(N, H, D, dtype=torch.bfloat16, device=dev)
+    cs = conv_cache.transpose(1, 2)
+    w2 = lay.conv1d.weight.view(cd, 4)
+    it = {"s": 0}
+
+    def nxt():
+        s = it["s"] % nstep
+        it["s"] += 1
+        return s
+
+    def reference_sequence():
+        s = nxt()
+        x = hmx.causal_conv1d_update(mixed[s], cs, w2, None, "silu", conv_state_indices=idx)
+        q = x[:, :H * D].reshape(1, N, H, D).contiguous()
+        k = x[:, H * D:2 * H * D].reshape(1, N, H, D).contiguous()
+        v = x[:, 2 * H * D:].reshape(1, N, H, D).contiguous()
+        gg, beta = hmx.fused_gdn_gating(lay.A, a[s], b[s], lay.dt_bias)
+        o, _ = hmx.fused_recurrent_gated_delta_rule_gqa(
+            q, k, v, gg, beta, initial_state=ssm, inplace_final_state=True, cu_seqlens=cu,
+            ssm_state_indices=idx, use_qk_l2norm_in_kernel=True)
+        core[:N] = o.squeeze(0)
+        return hmx.rms_norm_gated(core, z[s], wn, 1e-6)
+
+    def hmx_core():
+        s = nxt()
+        srv.gdn_forward_core(lay, mixed[s], b[s], a[s], core, md, cs, ssm,
+                             o_norm=(wn, z[s], 1e-6))
+
+    ms_ref = _timed(reference_sequence, steps, warmup)
+    ms_core = _timed(hmx_core, steps, warmup)
+    return dict(ms_ref=ms_ref, ms_core=ms_core, tokens=N)
+
+
 def bench_decode(dev, steps_total=512, warmup=8):
     import torch
     import hmx
@@ -805,10 +876,10 @@ def measured_traffic(key):
 # bench legs in run order (the long compute-bound GKA legs last), and the groups
 # --only accepts beside single legs
 LEGS = ["c1", "prefill_gqa", "prefill_varlen", "prefill_layer_gates", "onorm", "conv", "gdn_core",
-        "mamba2_core", "gka_core", "gdn_decode", "gka_decode", "ssd_c4", "ssd_primed",
+        "gdn_decode_core", "mamba2_core", "gka_core", "gdn_decode", "gka_decode", "ssd_c4", "ssd_primed",
         "ssd_decode", "gka8", "gka32", "gka_train", "gdn_train"]
 GROUPS = {"prefill": ["c1", "prefill_gqa", "prefill_varlen", "prefill_layer_gates"],
-          "core": ["gdn_core", "mamba2_core", "gka_core"], "decode": ["gdn_decode", "gka_decode"],
+          "core": ["gdn_core", "gdn_decode_core", "mamba2_core", "gka_core"], "decode": ["gdn_decode", "gka_decode"],
           "ssd": ["ssd_c4", "ssd_primed", "ssd_decode"], "gka": ["gka8", "gka32"],
           "train": ["gka_train", "gdn_train"]}
 
@@ -865,6 +936,7 @@ def main():
         "onorm": lambda: out.__setitem__("onorm", bench_onorm(dev, S, W)),
         "conv": lambda: out.__setitem__("conv", bench_conv(dev, S, W)),
         "gdn_core": lambda: out.__setitem__("core", bench_core(dev, max(2, S // 2), W)),
+        "gdn_decode_core": lambda: out.__setitem__("decode_core", bench_core_decode(dev)),
         "mamba2_core": lambda: out.__setitem__("mamba2_core", bench_mamba2_core(dev, max(2, S // 2), W)),
         "gka_core": lambda: out.__setitem__("gka_core", bench_gka_core(dev, max(2, S // 4), 1)),
         "gdn_decode": lambda: out.__setitem__("decode", bench_decode(dev)),
@@ -1006,6 +1078,15 @@ def main():
         line["gdn_layer_core"] = {
             "config": {"workload": "GDN layer core + output norm at C1 (8 seqs x 4096 tokens, "
                                    "H=HKV=32, d=128, conv width 4, pooled states)"},
+            "reference_call_sequence_ms": round(r["ms_ref"], 4),
+            "hmx_serving_core_ms": round(r["ms_core"], 4),
+            "tokens_per_s": round(r["tokens"] / (r["ms_core"] * 1e-3), 1),
+        }
+    if "decode_core" in out:
+        r = out["decode_core"]
+        line["gdn_decode_core"] = {
+            "config": {"workload": "GDN layer core + output norm on a decode batch (256 seqs x "
+                                   "1 token, H=HKV=32, d=128, conv width 4, fp32 pool)"},
             "reference_call_sequence_ms": round(r["ms_ref"], 4),
             "hmx_serving_core_ms": round(r["ms_core"], 4),
             "tokens_per_s": round(r["tokens"] / (r["ms_core"] * 1e-3), 1),

@@ -126,10 +126,20 @@ __device__ __forceinline__ float fast_exp(float x) {
 // standalone gating kernels and the mixer kernels' fused loads, so both paths
 // give the same values
 // ----------------------------------------------------------------------------
+// Element i of a tensor whose dtype is known only at run time.  Two 16-bit loads,
+// the element's low and high halves (for a 16-bit type the same half twice), both in
+// bounds for every dtype and issued unconditionally: a load inside a branch on the
+// dtype would be waited for inside the branch (a full round trip per call), while
+// here the wait lands at the value's first use and the loads overlap the caller's.
 __device__ __forceinline__ float load_any(const void* p, int64_t i, int dtype) {
-  if (dtype == HMX_F32) return static_cast<const float*>(p)[i];
-  if (dtype == HMX_BF16) return (float)static_cast<const bf16*>(p)[i];
-  return (float)static_cast<const f16*>(p)[i];
+  const uint16_t* u = static_cast<const uint16_t*>(p);
+  const bool f32 = dtype == HMX_F32;
+  const int64_t e = f32 ? 2 * i : i;
+  const uint32_t lo = u[e], hi = u[f32 ? e + 1 : e];
+  const float vf = __uint_as_float(lo | (hi << 16));
+  const float vb = __uint_as_float(lo << 16);
+  const float vh = (float)__builtin_bit_cast(f16, (uint16_t)lo);
+  return f32 ? vf : dtype == HMX_BF16 ? vb : vh;
 }
 
 // x as stored in a tensor of `dtype` and read back

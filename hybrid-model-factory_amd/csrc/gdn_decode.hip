@@ -46,9 +46,7 @@ struct RecurrentParams {
 };
 
 __device__ __forceinline__ float load_scalar(const void* p, int64_t i, int dtype) {
-  if (dtype == HMX_F32) return static_cast<const float*>(p)[i];
-  if (dtype == HMX_BF16) return (float)static_cast<const bf16*>(p)[i];
-  return (float)static_cast<const f16*>(p)[i];
+  return load_any(p, i, dtype);
 }
 
 // Loads of g and beta: a fixed element type (one code path, so the state and
