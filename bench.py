@@ -16,10 +16,9 @@ against HBM.
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only LEGS]
   --only takes comma-separated legs (c1, prefill_gqa, prefill_varlen,
   prefill_layer_gates, onorm, conv, gdn_core, gdn_decode_core, mamba2_core, gka_core,
-  gdn_decode,
-  gka_decode, ssd_c4, ssd_primed, ssd_decode, gka8, gka32) or groups (prefill, core,
-  decode, ssd, gka); one leg alone is what the committed rocprofv3 counter runs
-  profile.
+  gdn_decode, gka_decode, ssd_c4, ssd_primed, ssd_decode, gka8, gka32, gka_train,
+  gdn_train, ssd_train) or groups (prefill, core, decode, ssd, gka, train); one leg
+  alone is what the committed rocprofv3 counter runs profile.
 """
 from __future__ import annotations
 
@@ -667,6 +666,43 @@ def bench_gdn_train(dev, steps, warmup, B=8, T=4096, H=32):
                 TFLOPs_fwd_bwd=(ff + fb) / (ms_fb * 1e-3) / 1e12)
 
 
+def bench_ssd_train(dev, steps, warmup):
+    """F4 Mamba2: the training scan (hmx.mamba_chunk_scan_combined through
+    hmx.MambaChunkScanCombined under autograd, mamba2.py:555-580) at the C4 shape
+    (b=2, T=16384, H=64, P=64, N=128, G=8, D, dt_bias, softplus), forward alone and
+    forward + backward with dy ~ N(0, 1).  The backward recomputes the forward (one
+    segment per 64-token chunk, for the chunk start states), then runs the local,
+    reverse-scan and chunk-gradient launches."""
+    import torch
+    import hmx
+    from hmx import workloads as wl
+    d = wl.ssd_inputs(config_id=4, device=dev, gen_device=dev)
+    b, T, H, P = d["x"].shape
+    G, N = d["B"].shape[2], d["B"].shape[3]
+    g = torch.Generator(device=dev).manual_seed(wl.SEED_BASE + 15)
+    dy = torch.randn(b, T, H, P, generator=g, device=dev).bfloat16()
+    leaves = [d[k].clone().requires_grad_(True) for k in ("x", "dt", "A", "B", "C", "D",
+                                                          "dt_bias")]
+
+    def fwd():
+        with torch.no_grad():
+            hmx.mamba_chunk_scan_combined(d["x"], d["dt"], d["A"], d["B"], d["C"], 256,
+                                          D=d["D"], dt_bias=d["dt_bias"], dt_softplus=True)
+
+    def fwd_bwd():   # the gradients returned, not accumulated into .grad
+        x, dt, A, B, C, D, bias = leaves
+        y = hmx.mamba_chunk_scan_combined(x, dt, A, B, C, 256, D=D, dt_bias=bias,
+                                          dt_softplus=True)
+        torch.autograd.grad(y, leaves, dy)
+
+    ms_f = _timed(fwd, steps, warmup)
+    ms_fb = _timed(fwd_bwd, steps, warmup)
+    L = 64   # the backward's chunk: per (chunk, head) 3 L^2 N + 3 L^2 P + 5 L P N MACs
+    flops_bwd = 2.0 * (b * T // L) * H * (3 * L * L * N + 3 * L * L * P + 5 * L * P * N)
+    return dict(ms_fwd=ms_f, ms_fwd_bwd=ms_fb, tokens=b * T, flops_bwd=flops_bwd,
+                tokens_per_s=b * T / (ms_fb * 1e-3))
+
+
 def bench_ssd(dev, steps, warmup, b=2, T=16384, H=64, P=64, N=128, G=8):
     """C4: mamba_chunk_scan_combined, b=2, T=16384, H=64, P=64, N=128, G=8, fp32 final
     state (other shapes through the keywords: the primed layout is P = N = 128, G = H)."""
@@ -877,11 +913,11 @@ def measured_traffic(key):
 # --only accepts beside single legs
 LEGS = ["c1", "prefill_gqa", "prefill_varlen", "prefill_layer_gates", "onorm", "conv", "gdn_core",
         "gdn_decode_core", "mamba2_core", "gka_core", "gdn_decode", "gka_decode", "ssd_c4", "ssd_primed",
-        "ssd_decode", "gka8", "gka32", "gka_train", "gdn_train"]
+        "ssd_decode", "gka8", "gka32", "gka_train", "gdn_train", "ssd_train"]
 GROUPS = {"prefill": ["c1", "prefill_gqa", "prefill_varlen", "prefill_layer_gates"],
           "core": ["gdn_core", "gdn_decode_core", "mamba2_core", "gka_core"], "decode": ["gdn_decode", "gka_decode"],
           "ssd": ["ssd_c4", "ssd_primed", "ssd_decode"], "gka": ["gka8", "gka32"],
-          "train": ["gka_train", "gdn_train"]}
+          "train": ["gka_train", "gdn_train", "ssd_train"]}
 
 
 def measured_mfma_busy(key):
@@ -949,6 +985,7 @@ def main():
         "gka32": lambda: out.setdefault("gka", {}).__setitem__(32, bench_gka(dev, max(2, S // 4), 1, 32)),
         "gka_train": lambda: out.__setitem__("gka_train", bench_gka_train(dev, max(2, S // 4), 1)),
         "gdn_train": lambda: out.__setitem__("gdn_train", bench_gdn_train(dev, max(2, S // 4), 1)),
+        "ssd_train": lambda: out.__setitem__("ssd_train", bench_ssd_train(dev, max(2, S // 4), 1)),
     }
     for name in LEGS:           # run order: the long compute-bound GKA legs last
         if name in sel:
@@ -1140,6 +1177,17 @@ def main():
                          "frac": round(r["TFLOPs_fwd_bwd"] / BF16_PEAK_TFLOPS, 4),
                          "algorithmic_flops_fwd": r["flops_fwd"],
                          "algorithmic_flops_bwd": r["flops_bwd"]},
+        }
+    if "ssd_train" in out:
+        r = out["ssd_train"]
+        line["ssd_train"] = {
+            "value": round(r["tokens_per_s"], 1), "unit": "tokens/s (forward + backward)",
+            "ms_fwd": round(r["ms_fwd"], 4), "ms_fwd_bwd": round(r["ms_fwd_bwd"], 4),
+            "config": {"workload": "F4 Mamba2 training scan (mamba_chunk_scan_combined fwd + bwd)",
+                       "B": 2, "T": 16384, "H": 64, "P": 64, "N": 128, "G": 8},
+            "backward_TFLOPs": round(r["flops_bwd"] / ((r["ms_fwd_bwd"] - r["ms_fwd"]) * 1e-3)
+                                     / 1e12, 1),
+            "algorithmic_flops_bwd": r["flops_bwd"],
         }
     if "gka_train" in out:
         r = out["gka_train"]

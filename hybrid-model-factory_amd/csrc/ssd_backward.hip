@@ -1,0 +1,697 @@
+// Mamba2 SSD chunk scan backward (the gradients of mamba_chunk_scan_combined) for
+// gfx950: bf16 MFMA products with fp32 accumulation, fp32 scalar chains.
+//
+// The forward (ssd_prefill.hip) per head h, chunk of L = 64 tokens, a_t = dt'_t A_h,
+// A_t = sum_{s<=t} a_s from the chunk start (inclusive), chunk start state S0 and
+// end state S1 (both P x N):
+//   y'_t = sum_{s<=t} (C_t . B_s) e^{A_t - A_s} dt'_s x_s + e^{A_t} S0 C_t + D x_t
+//   y_t  = y'_t silu(z_t)                        (y_t = y'_t without z)
+//   S1   = e^{A_L} S0 + sum_s e^{A_L - A_s} dt'_s x_s B_s^T
+// With g_t = dy_t silu(z_t) (dy_t without z), the gradient dS1 of the chunk's end
+// state and, for s <= t,
+//   M_ts = (C_t . B_s) e^{A_t - A_s},  Q_ts = g_t . x_s,  W_ts = dt'_s Q_ts e^{A_t - A_s}
+// the backward is:
+//   dS0   = e^{A_L} dS1 + sum_t e^{A_t} g_t C_t^T           (reverse scan over chunks)
+//   dx_s  = sum_t M_ts dt'_s g_t + e^{A_L - A_s} dt'_s dS1 B_s + D g_s
+//   dC_t  = sum_s W_ts B_s + e^{A_t} S0^T g_t
+//   dB_s  = sum_t W_ts C_t + e^{A_L - A_s} dt'_s dS1^T x_s
+//   ddt'_s = sum_t M_ts Q_ts + e^{A_L - A_s} x_s . (dS1 B_s)  +  A_h da_s
+//   dA_t  (the cumulated log-decay): sum_s W_ts (C_t.B_s) - sum_u W_ut (C_u.B_t)
+//           + g_t . (e^{A_t} S0 C_t) - dt'_t e^{A_L - A_t} x_t . (dS1 B_t)
+//           + [t = L-1] <dS1, S1>
+//   da_s  = sum_{t>=s} dA_t,   dA_h += sum_s dt'_s da_s
+//   dz    = dy y' silu'(z),    dD_p += sum_t g_t[p] x_t[p]
+//   d dt  = ddt' * [dt_min <= dt' <= dt_max] * (softplus ? sigmoid(dt + bias) : 1)
+// with <dS1, S1> = e^{A_L} <dS1, S0> + sum_s dt'_s e^{A_L - A_s} x_s . (dS1 B_s), so
+// S1 is never read.  These are the chain rule through the recurrence of
+// oracle/ssd.py; mamba_ssm's backward (un-vendored) computes the same gradients
+// with its own kernels (training/.../layers/mamba/mamba2.py:555-580 calls it).
+//
+// Three launches over the forward's 64-token chunks (rows of the segment table,
+// one chunk each, with the chunk start states S0 of the recomputed forward):
+//   ssd_bwd_local_kernel  (chunk, head): sum_t e^{A_t} g_t C_t^T and A_L
+//   ssd_bwd_scan_kernel   (sequence, head, 1024 state elements): dS1 of every chunk
+//                          by the reverse scan, and dS0 of the sequence's start
+//   ssd_bwd_chunk_kernel  (chunk, head): everything else
+// Operands shared by several heads (x of HX < H heads, B of G < H groups, C of
+// GC < H groups) accumulate with fp32 atomics; the others are stored.
+
+#include <type_traits>
+
+#include "common.hpp"
+#include "mfma.hpp"
+
+namespace hmx {
+namespace ssdb {
+
+constexpr int L = 64;
+constexpr int NTHR = 256;
+
+struct Params {
+  const bf16* x; int64_t x_ts, x_hs;         // [T][HX][P]
+  const bf16* B; int64_t b_ts, b_gs;         // [T][G][N]
+  const bf16* C; int64_t c_ts, c_gs;         // [T][GC][N]
+  const void* dt; int dt_dt; int64_t dt_ts, dt_hs;   // raw dt [T][H]
+  const float* A;                            // [H]
+  const float* D;                            // [H][P] or null
+  const float* dt_bias;                      // [H] or null
+  const bf16* z; int64_t z_ts, z_hs;         // [T][H][P] or null
+  const bf16* dy; int64_t dy_ts, dy_hs;      // [T][H][P]
+  const float* h0;                           // [nseq][H][P][N] or null (zero start)
+  const float* s0;                           // [nrows][H][P][N] chunk start states, or null
+  const float* dT;                           // [nseq][H][P][N] end-state gradients, or null
+  const int* seg;                            // [nrows][8] segment rows (one chunk each)
+  const int* seqs;                           // [nseq][2]: first row, rows
+  int nrows, nseq;
+  float* loc;                                // ws [nrows][H][P][N]
+  float* aend;                               // ws [nrows][H]
+  bf16* dS1;                                 // ws [nrows][H][P][N]
+  // outputs (contiguous)
+  float* dx;   int x_shared;                 // [T][HX][P] fp32
+  float* dB;   int b_shared;                 // [T][G][N] fp32
+  float* dC;   int c_shared;                 // [T][GC][N] fp32
+  bf16* dz;                                  // [T][H][P] or null
+  float* ddt;                                // [T][H]
+  float* dA;                                 // [H] (accumulated)
+  float* dD;                                 // [H][P] (accumulated) or null
+  float* dbias;                              // [H] (accumulated) or null
+  float* dh0;                                // [nseq][H][P][N] or null
+  int H, HX, G, GC, softplus;
+  float dt_min, dt_max;
+};
+
+// segment row: sequence, first token, end token, chunk range, index in the
+// sequence, first row of the sequence, rows of the sequence
+struct Row { int n, bos, eos, c0, c1, idx, first, nseg; };
+__device__ __forceinline__ Row load_row(const int* seg, int r) {
+  const int* q = seg + r * 8;
+  return Row{q[0], q[1], q[2], q[3], q[4], q[5], q[6], q[7]};
+}
+
+__device__ __forceinline__ float scan64(float x, int lane) {
+  x = scan32(x);
+  const float lo = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 31));
+  return lane >= 32 ? x + lo : x;
+}
+
+__device__ __forceinline__ float silu(float z) { return z / (1.f + fast_exp(-z)); }
+
+// Per-token scalars of a chunk, lane t of one wave: dt' (0 past the chunk's
+// tokens), A_t, and the factor d dt'/d dt (clamp pass times the softplus slope).
+struct Tok { float dtv, acs, fac; };
+__device__ __forceinline__ Tok token_scalars(const Params& p, int h, int tok0, int nval, int lane) {
+  float d = 0.f;
+  if (lane < nval) d = load_any(p.dt, (int64_t)(tok0 + lane) * p.dt_ts + (int64_t)h * p.dt_hs, p.dt_dt);
+  d += p.dt_bias ? p.dt_bias[h] : 0.f;
+  float sp = d, slope = 1.f;
+  if (p.softplus) {
+    sp = softplus20(d);
+    slope = d > 20.f ? 1.f : 1.f / (1.f + fast_exp(-d));
+  }
+  float dtv = fminf(fmaxf(sp, p.dt_min), p.dt_max);
+  // torch.clamp's gradient passes on [min, max]
+  float fac = (sp >= p.dt_min && sp <= p.dt_max) ? slope : 0.f;
+  if (lane >= nval) { dtv = 0.f; fac = 0.f; }
+  const float acs = scan64(dtv * p.A[h], lane);
+  return Tok{dtv, acs, fac};
+}
+
+// ---------------------------------------------------------------------------
+// local: loc[r][h] = sum_t e^{A_t} g_t C_t^T  (P x N), aend[r][h] = A_L
+// ---------------------------------------------------------------------------
+template <int P, int N>
+__global__ __launch_bounds__(NTHR) void ssd_bwd_local_kernel(Params p) {
+  constexpr int LDX = P + 8, LDB = N + 8;
+  __shared__ __align__(16) bf16 sG[L * LDX];   // e^{A_t} g_t
+  __shared__ __align__(16) bf16 sC[L * LDB];
+  __shared__ float sEA[L];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int H = p.H;
+  const int r = blockIdx.x / H, h = blockIdx.x % H;
+  const Row ro = load_row(p.seg, r);
+  const int tok0 = ro.bos, nval = ro.eos - ro.bos;
+  const int gc = h / (H / p.GC);
+  if (wave == 0) {
+    const Tok tk = token_scalars(p, h, tok0, nval, lane);
+    sEA[lane] = fast_exp(tk.acs);
+    if (lane == L - 1) p.aend[(int64_t)r * H + h] = tk.acs;
+  }
+  // C rows (zero past the chunk)
+#pragma unroll
+  for (int i = 0; i < L * N / 8 / NTHR; ++i) {
+    const int e = (i * NTHR + tid) * 8, t = e / N, c = e % N;
+    bf16x8 v = {};
+    if (t < nval) v = *reinterpret_cast<const bf16x8*>(p.C + (int64_t)(tok0 + t) * p.c_ts +
+                                                       (int64_t)gc * p.c_gs + c);
+    *reinterpret_cast<bf16x8*>(sC + t * LDB + c) = v;
+  }
+  __syncthreads();   // sEA
+#pragma unroll
+  for (int i = 0; i < L * P / 8 / NTHR; ++i) {
+    const int e = (i * NTHR + tid) * 8, t = e / P, c = e % P;
+    bf16x8 o = {};
+    if (t < nval) {
+      const int64_t off = (int64_t)(tok0 + t) * p.dy_ts + (int64_t)h * p.dy_hs + c;
+      const bf16x8 g = *reinterpret_cast<const bf16x8*>(p.dy + off);
+      bf16x8 zz = {};
+      if (p.z) zz = *reinterpret_cast<const bf16x8*>(p.z + (int64_t)(tok0 + t) * p.z_ts +
+                                                    (int64_t)h * p.z_hs + c);
+      const float ea = sEA[t];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float v = (float)g[j];
+        if (p.z) v *= silu((float)zz[j]);
+        o[j] = (bf16)(v * ea);
+      }
+    }
+    *reinterpret_cast<bf16x8*>(sG + t * LDX + c) = o;
+  }
+  __syncthreads();
+  // wave w: p rows [16w', ...) for P/16 row blocks over 4 waves, all n tiles
+  const int q4 = lane >> 4, l16 = lane & 15;
+  constexpr int PBW = P / 16 / 4;   // p blocks per wave
+  f32x4 acc[PBW][N / 16];
+#pragma unroll
+  for (int i = 0; i < PBW; ++i)
+#pragma unroll
+    for (int j = 0; j < N / 16; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int k0 = 0; k0 < L; k0 += 32) {
+    bf16x8 bf[N / 16];
+#pragma unroll
+    for (int j = 0; j < N / 16; ++j) bf[j] = frag_t(sC, LDB, k0, 16 * j, lane);
+#pragma unroll
+    for (int i = 0; i < PBW; ++i) {
+      const bf16x8 af = frag_t(sG, LDX, k0, 16 * (wave * PBW + i), lane);
+#pragma unroll
+      for (int j = 0; j < N / 16; ++j) acc[i][j] = mfma16(af, bf[j], acc[i][j]);
+    }
+  }
+  float* dst = p.loc + ((int64_t)r * H + h) * P * N;
+#pragma unroll
+  for (int i = 0; i < PBW; ++i)
+#pragma unroll
+    for (int j = 0; j < N / 16; ++j)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        dst[(16 * (wave * PBW + i) + 4 * q4 + v) * N + 16 * j + l16] = acc[i][j][v];
+}
+
+// ---------------------------------------------------------------------------
+// reverse scan: dS1[last] = dT; dS1[c-1] = e^{A_L(c)} dS1[c] + loc[c]; dh0 = the
+// value before the first chunk
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void ssd_bwd_scan_kernel(Params p, int PN) {
+  const int H = p.H;
+  const int n = blockIdx.x / H, h = blockIdx.x % H;
+  const int first = p.seqs[2 * n], cnt = p.seqs[2 * n + 1];
+  for (int e = blockIdx.y * 256 + threadIdx.x; e < PN; e += gridDim.y * 256) {
+    float g = p.dT ? p.dT[((int64_t)n * H + h) * PN + e] : 0.f;
+    for (int k = cnt - 1; k >= 0; --k) {
+      const int64_t b = (int64_t)(first + k) * H + h;
+      p.dS1[b * PN + e] = (bf16)g;
+      g = g * expf(p.aend[b]) + p.loc[b * PN + e];
+    }
+    if (p.dh0) p.dh0[((int64_t)n * H + h) * PN + e] = g;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// chunk kernel
+// ---------------------------------------------------------------------------
+template <int P, int N>
+struct Lay {
+  static constexpr int LDX = P + 8, LDB = N + 8, LDM = L + 8;
+  static constexpr int OFF_X = 0;                          // x        [L][LDX]
+  static constexpr int OFF_G = OFF_X + L * LDX * 2;        // g        [L][LDX]
+  static constexpr int OFF_DY = OFF_G + L * LDX * 2;       // dy       [L][LDX] (z only)
+  static constexpr int OFF_Z = OFF_DY + L * LDX * 2;       // z        [L][LDX] (z only)
+  static constexpr int OFF_B = OFF_Z + L * LDX * 2;        // B        [L][LDB]
+  static constexpr int OFF_C = OFF_B + L * LDB * 2;        // C        [L][LDB]
+  static constexpr int OFF_S = OFF_C + L * LDB * 2;        // S0       [P][LDB]
+  static constexpr int OFF_DS = OFF_S + P * LDB * 2;       // dS1      [P][LDB]
+  static constexpr int OFF_M = OFF_DS + P * LDB * 2;       // M dt'    [L][LDM]
+  static constexpr int OFF_W = OFF_M + L * LDM * 2;        // W        [L][LDM]
+  static constexpr int OFF_F = OFF_W + L * LDM * 2;        // fp32 scalars
+  static constexpr int NF = 17;                            // scalar arrays of L floats
+  static constexpr int BYTES = OFF_F + NF * L * 4 + 64;
+  static_assert(BYTES <= 160 * 1024, "LDS budget");
+};
+// scalar arrays
+enum { F_DT, F_ACS, F_EA, F_E, F_FAC, F_ROWR, F_DAS, F_DDS,
+       F_CMQ0, F_CR0 = F_CMQ0 + 4, F_DD = F_CR0 + 4 };   // F_DD: P = 64 floats
+static_assert(F_DD + 1 == 17, "scalar arrays");
+
+template <int P, int N>
+__global__ __launch_bounds__(NTHR, 1) void ssd_bwd_chunk_kernel(Params p) {
+  static_assert(P == 64, "headdim 64");
+  using K = Lay<P, N>;
+  constexpr int LDX = K::LDX, LDB = K::LDB, LDM = K::LDM, NT = N / 16;
+  extern __shared__ __align__(16) unsigned char smem[];
+  bf16* sX = reinterpret_cast<bf16*>(smem + K::OFF_X);
+  bf16* sG = reinterpret_cast<bf16*>(smem + K::OFF_G);
+  bf16* sDY = reinterpret_cast<bf16*>(smem + K::OFF_DY);
+  bf16* sZ = reinterpret_cast<bf16*>(smem + K::OFF_Z);
+  bf16* sB = reinterpret_cast<bf16*>(smem + K::OFF_B);
+  bf16* sC = reinterpret_cast<bf16*>(smem + K::OFF_C);
+  bf16* sS = reinterpret_cast<bf16*>(smem + K::OFF_S);
+  bf16* sDS = reinterpret_cast<bf16*>(smem + K::OFF_DS);
+  bf16* sM = reinterpret_cast<bf16*>(smem + K::OFF_M);
+  bf16* sW = reinterpret_cast<bf16*>(smem + K::OFF_W);
+  float* sF = reinterpret_cast<float*>(smem + K::OFF_F);
+  auto F = [&](int a, int t) -> float& { return sF[a * L + t]; };
+  float* sHD = sF + K::NF * L;   // [0]: <dS1, S0>
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q4 = lane >> 4, l16 = lane & 15;
+  const int H = p.H;
+  const int r = blockIdx.x / H, h = blockIdx.x % H;
+  const Row ro = load_row(p.seg, r);
+  const int tok0 = ro.bos, nval = ro.eos - ro.bos;
+  const int hx = h / (H / p.HX), g = h / (H / p.G), gc = h / (H / p.GC);
+  const float A_h = p.A[h];
+
+  if (tid == 0) sHD[0] = 0.f;
+  if (tid < P) F(F_DD, tid) = 0.f;
+  if (wave == 0) {
+    const Tok tk = token_scalars(p, h, tok0, nval, lane);
+    const float aend = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, tk.acs), 63));
+    F(F_DT, lane) = tk.dtv;
+    F(F_ACS, lane) = tk.acs;
+    F(F_EA, lane) = fast_exp(tk.acs);
+    F(F_E, lane) = fast_exp(aend - tk.acs);
+    F(F_FAC, lane) = tk.fac;
+  }
+  __syncthreads();   // sHD, F_DD cleared
+
+  // ---- staging ----------------------------------------------------------------
+  // x, g = dy silu(z), dy and z; the thread's dD partials (its 8 features)
+  {
+    float dd[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < L * P / 8 / NTHR; ++i) {
+      const int e = (i * NTHR + tid) * 8, t = e / P, c = e % P;
+      bf16x8 xv = {}, dv = {}, zv = {}, gv = {};
+      if (t < nval) {
+        xv = *reinterpret_cast<const bf16x8*>(p.x + (int64_t)(tok0 + t) * p.x_ts + (int64_t)hx * p.x_hs + c);
+        dv = *reinterpret_cast<const bf16x8*>(p.dy + (int64_t)(tok0 + t) * p.dy_ts + (int64_t)h * p.dy_hs + c);
+        if (p.z) zv = *reinterpret_cast<const bf16x8*>(p.z + (int64_t)(tok0 + t) * p.z_ts + (int64_t)h * p.z_hs + c);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float gj = (float)dv[j];
+        if (p.z) gj *= silu((float)zv[j]);
+        gv[j] = (bf16)gj;
+        dd[j] += gj * (float)xv[j];
+      }
+      *reinterpret_cast<bf16x8*>(sX + t * LDX + c) = xv;
+      *reinterpret_cast<bf16x8*>(sG + t * LDX + c) = gv;
+      if (p.z) {
+        *reinterpret_cast<bf16x8*>(sDY + t * LDX + c) = dv;
+        *reinterpret_cast<bf16x8*>(sZ + t * LDX + c) = zv;
+      }
+    }
+    if (p.dD) {
+      const int c = (tid * 8) % P;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) atomicAdd(&F(F_DD, c + j), dd[j]);
+    }
+  }
+  // B (group g) and C (group gc)
+#pragma unroll
+  for (int i = 0; i < L * N / 8 / NTHR; ++i) {
+    const int e = (i * NTHR + tid) * 8, t = e / N, c = e % N;
+    bf16x8 bv = {}, cv = {};
+    if (t < nval) {
+      bv = *reinterpret_cast<const bf16x8*>(p.B + (int64_t)(tok0 + t) * p.b_ts + (int64_t)g * p.b_gs + c);
+      cv = *reinterpret_cast<const bf16x8*>(p.C + (int64_t)(tok0 + t) * p.c_ts + (int64_t)gc * p.c_gs + c);
+    }
+    *reinterpret_cast<bf16x8*>(sB + t * LDB + c) = bv;
+    *reinterpret_cast<bf16x8*>(sC + t * LDB + c) = cv;
+  }
+  // S0 (fp32, the sequence's start state for its first chunk) and dS1, with <dS1, S0>
+  {
+    const float* s0 = nullptr;
+    if (ro.idx == 0) {
+      if (p.h0) s0 = p.h0 + ((int64_t)ro.n * H + h) * P * N;
+    } else if (p.s0) {
+      s0 = p.s0 + ((int64_t)r * H + h) * P * N;
+    }
+    const bf16* ds = p.dS1 + ((int64_t)r * H + h) * P * N;
+    float hd = 0.f;
+#pragma unroll
+    for (int i = 0; i < P * N / 8 / NTHR; ++i) {
+      const int e = (i * NTHR + tid) * 8, pr = e / N, c = e % N;
+      f32x4 a = {0.f, 0.f, 0.f, 0.f}, b = {0.f, 0.f, 0.f, 0.f};
+      if (s0) {
+        a = *reinterpret_cast<const f32x4*>(s0 + e);
+        b = *reinterpret_cast<const f32x4*>(s0 + e + 4);
+      }
+      const bf16x8 dv = *reinterpret_cast<const bf16x8*>(ds + e);
+      const bf16x8 sv = {(bf16)a[0], (bf16)a[1], (bf16)a[2], (bf16)a[3],
+                         (bf16)b[0], (bf16)b[1], (bf16)b[2], (bf16)b[3]};
+      *reinterpret_cast<bf16x8*>(sS + pr * LDB + c) = sv;
+      *reinterpret_cast<bf16x8*>(sDS + pr * LDB + c) = dv;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) hd += a[j] * (float)dv[j] + b[j] * (float)dv[4 + j];
+    }
+    hd = wave_sum(hd);
+    if (lane == 0) atomicAdd(sHD, hd);
+  }
+  __syncthreads();
+  if (p.dD && tid < P) unsafeAtomicAdd(p.dD + (int64_t)h * P + tid, F(F_DD, tid));
+
+  // ---- step A: CB and Q (rows t of wave's block, all s), M dt' and W to LDS ----
+  {
+    f32x4 cb[4], qq[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { cb[j] = f32x4{0.f, 0.f, 0.f, 0.f}; qq[j] = cb[j]; }
+#pragma unroll
+    for (int k0 = 0; k0 < N; k0 += 32) {
+      const bf16x8 a = frag(sC, LDB, 16 * wave, k0, lane);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) cb[j] = mfma16(a, frag(sB, LDB, 16 * j, k0, lane), cb[j]);
+    }
+#pragma unroll
+    for (int k0 = 0; k0 < P; k0 += 32) {
+      const bf16x8 a = frag(sG, LDX, 16 * wave, k0, lane);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) qq[j] = mfma16(a, frag(sX, LDX, 16 * j, k0, lane), qq[j]);
+    }
+    float rowr[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int s = 16 * j + l16;
+      const float acs_s = F(F_ACS, s), dt_s = F(F_DT, s);
+      float cmq = 0.f, cr = 0.f;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int t = 16 * wave + 4 * q4 + v;
+        const float dec = s <= t ? fast_exp(F(F_ACS, t) - acs_s) : 0.f;
+        const float m = cb[j][v] * dec;
+        const float w = dt_s * qq[j][v] * dec;
+        const float rr = w * cb[j][v];
+        cmq += m * qq[j][v];
+        cr += rr;
+        rowr[v] += rr;
+        sM[t * LDM + s] = (bf16)(m * dt_s);
+        sW[t * LDM + s] = (bf16)w;
+      }
+      // column sums over the wave's 16 rows: the four lane groups
+      cmq += shfl_xor(cmq, 16);
+      cmq += shfl_xor(cmq, 32);
+      cr += shfl_xor(cr, 16);
+      cr += shfl_xor(cr, 32);
+      if (q4 == 0) {
+        F(F_CMQ0 + wave, s) = cmq;
+        F(F_CR0 + wave, s) = cr;
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float rs = row16_sum(rowr[v]);
+      if (l16 == 0) F(F_ROWR, 16 * wave + 4 * q4 + v) = rs;
+    }
+  }
+  __syncthreads();
+
+  // ---- step B1: y' = M dt' x + e^{A_t} C S0^T + D x -> dz, and g . (e^A C S0^T) --
+  {
+    f32x4 yi[P / 16], ys[P / 16];
+#pragma unroll
+    for (int i = 0; i < P / 16; ++i) { yi[i] = f32x4{0.f, 0.f, 0.f, 0.f}; ys[i] = yi[i]; }
+#pragma unroll
+    for (int k0 = 0; k0 < L; k0 += 32) {
+      const bf16x8 a = frag(sM, LDM, 16 * wave, k0, lane);
+#pragma unroll
+      for (int i = 0; i < P / 16; ++i) yi[i] = mfma16(a, frag_t(sX, LDX, k0, 16 * i, lane), yi[i]);
+    }
+#pragma unroll
+    for (int k0 = 0; k0 < N; k0 += 32) {
+      const bf16x8 a = frag(sC, LDB, 16 * wave, k0, lane);
+#pragma unroll
+      for (int i = 0; i < P / 16; ++i) ys[i] = mfma16(a, frag(sS, LDB, 16 * i, k0, lane), ys[i]);
+    }
+    float das[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int t = 16 * wave + 4 * q4 + v;
+      const float ea = F(F_EA, t);
+#pragma unroll
+      for (int i = 0; i < P / 16; ++i) {
+        const int pc = 16 * i + l16;
+        const float y_s = ea * ys[i][v];
+        das[v] += (float)sG[t * LDX + pc] * y_s;
+        if (p.z && t < nval) {
+          float yp = yi[i][v] + y_s;
+          if (p.D) yp += p.D[(int64_t)h * P + pc] * (float)sX[t * LDX + pc];
+          const float zf = (float)sZ[t * LDX + pc];
+          const float sg = 1.f / (1.f + fast_exp(-zf));
+          const float dsilu = sg * (1.f + zf * (1.f - sg));
+          p.dz[(int64_t)(tok0 + t) * H * P + (int64_t)h * P + pc] =
+              (bf16)((float)sDY[t * LDX + pc] * yp * dsilu);
+        }
+      }
+      const float rs = row16_sum(das[v]);
+      if (l16 == 0) F(F_DAS, t) = rs;
+    }
+  }
+
+  // ---- step B2: dx = (M dt')^T g + e dt' (dS1 B)^T + D g, and x . (dS1 B) -------
+  {
+    f32x4 dxi[P / 16], dhb[P / 16];
+#pragma unroll
+    for (int i = 0; i < P / 16; ++i) { dxi[i] = f32x4{0.f, 0.f, 0.f, 0.f}; dhb[i] = dxi[i]; }
+#pragma unroll
+    for (int k0 = 0; k0 < L; k0 += 32) {
+      const bf16x8 a = frag_t(sM, LDM, k0, 16 * wave, lane);
+#pragma unroll
+      for (int i = 0; i < P / 16; ++i) dxi[i] = mfma16(a, frag_t(sG, LDX, k0, 16 * i, lane), dxi[i]);
+    }
+#pragma unroll
+    for (int k0 = 0; k0 < N; k0 += 32) {
+      const bf16x8 a = frag(sB, LDB, 16 * wave, k0, lane);
+#pragma unroll
+      for (int i = 0; i < P / 16; ++i) dhb[i] = mfma16(a, frag(sDS, LDB, 16 * i, k0, lane), dhb[i]);
+    }
+    float dds[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int s = 16 * wave + 4 * q4 + v;
+      const float e = F(F_E, s), dt_s = F(F_DT, s);
+#pragma unroll
+      for (int i = 0; i < P / 16; ++i) {
+        const int pc = 16 * i + l16;
+        dds[v] += (float)sX[s * LDX + pc] * dhb[i][v];
+        if (s < nval) {
+          float d = dxi[i][v] + e * dt_s * dhb[i][v];
+          if (p.D) d += p.D[(int64_t)h * P + pc] * (float)sG[s * LDX + pc];
+          float* dst = p.dx + (int64_t)(tok0 + s) * p.HX * P + (int64_t)hx * P + pc;
+          if (p.x_shared) unsafeAtomicAdd(dst, d);
+          else *dst = d;
+        }
+      }
+      const float rs = row16_sum(dds[v]);
+      if (l16 == 0) F(F_DDS, s) = e * rs;
+    }
+  }
+
+  // ---- step B3: dC = e^{A_t} g S0 + W B ------------------------------------------
+  {
+    f32x4 acc[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k0 = 0; k0 < P; k0 += 32) {
+      const bf16x8 a = frag(sG, LDX, 16 * wave, k0, lane);
+#pragma unroll
+      for (int j = 0; j < NT; ++j) acc[j] = mfma16(a, frag_t(sS, LDB, k0, 16 * j, lane), acc[j]);
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float ea = F(F_EA, 16 * wave + 4 * q4 + v);
+#pragma unroll
+      for (int j = 0; j < NT; ++j) acc[j][v] *= ea;
+    }
+#pragma unroll
+    for (int k0 = 0; k0 < L; k0 += 32) {
+      const bf16x8 a = frag(sW, LDM, 16 * wave, k0, lane);
+#pragma unroll
+      for (int j = 0; j < NT; ++j) acc[j] = mfma16(a, frag_t(sB, LDB, k0, 16 * j, lane), acc[j]);
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int t = 16 * wave + 4 * q4 + v;
+      if (t >= nval) continue;
+      float* row = p.dC + (int64_t)(tok0 + t) * p.GC * N + (int64_t)gc * N;
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        if (p.c_shared) unsafeAtomicAdd(row + 16 * j + l16, acc[j][v]);
+        else row[16 * j + l16] = acc[j][v];
+      }
+    }
+  }
+
+  // ---- step B4: dB = e dt' x dS1 + W^T C -------------------------------------------
+  {
+    f32x4 acc[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k0 = 0; k0 < P; k0 += 32) {
+      const bf16x8 a = frag(sX, LDX, 16 * wave, k0, lane);
+#pragma unroll
+      for (int j = 0; j < NT; ++j) acc[j] = mfma16(a, frag_t(sDS, LDB, k0, 16 * j, lane), acc[j]);
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int s = 16 * wave + 4 * q4 + v;
+      const float f = F(F_E, s) * F(F_DT, s);
+#pragma unroll
+      for (int j = 0; j < NT; ++j) acc[j][v] *= f;
+    }
+#pragma unroll
+    for (int k0 = 0; k0 < L; k0 += 32) {
+      const bf16x8 a = frag_t(sW, LDM, k0, 16 * wave, lane);
+#pragma unroll
+      for (int j = 0; j < NT; ++j) acc[j] = mfma16(a, frag_t(sC, LDB, k0, 16 * j, lane), acc[j]);
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int s = 16 * wave + 4 * q4 + v;
+      if (s >= nval) continue;
+      float* row = p.dB + (int64_t)(tok0 + s) * p.G * N + (int64_t)g * N;
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        if (p.b_shared) unsafeAtomicAdd(row + 16 * j + l16, acc[j][v]);
+        else row[16 * j + l16] = acc[j][v];
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- scalar chain: dA_t, da (reverse cumsum), d dt, dA_h, d dt_bias --------------
+  if (wave == 0) {
+    const int t = lane;
+    const float dt_t = F(F_DT, t), dds = F(F_DDS, t);
+    float dacs = F(F_ROWR, t) + F(F_DAS, t) - dt_t * dds;
+    float cmq = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      dacs -= F(F_CR0 + w, t);
+      cmq += F(F_CMQ0 + w, t);
+    }
+    // <dS1, S1> = e^{A_L} <dS1, S0> + sum_s dt'_s e_s x_s . (dS1 B_s), on the last token
+    const float tail = wave_sum(dt_t * dds);
+    const float aend = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+        __builtin_bit_cast(int, F(F_ACS, t)), 63));
+    if (t == L - 1) dacs += fast_exp(aend) * sHD[0] + tail;
+    const float incl = scan64(dacs, lane);
+    const float total = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, incl), 63));
+    const float da = total - incl + dacs;   // sum_{u >= t} dA_u
+    const float ddtv = cmq + dds + A_h * da;
+    const float ddt_raw = ddtv * F(F_FAC, t);
+    if (t < nval) p.ddt[(int64_t)(tok0 + t) * H + h] = ddt_raw;
+    const float sa = wave_sum(dt_t * da);
+    const float sb = wave_sum(ddt_raw);
+    if (lane == 0) {
+      unsafeAtomicAdd(p.dA + h, sa);
+      if (p.dbias) unsafeAtomicAdd(p.dbias + h, sb);
+    }
+  }
+}
+
+template <int P, int N>
+void launch(const Params& p, hipStream_t s) {
+  const dim3 grid(p.nrows * p.H);
+  hipLaunchKernelGGL((ssd_bwd_local_kernel<P, N>), grid, dim3(NTHR), 0, s, p);
+  hipLaunchKernelGGL(ssd_bwd_scan_kernel, dim3(p.nseq * p.H, (P * N + 1023) / 1024), dim3(256), 0,
+                     s, p, P * N);
+  constexpr int smem = Lay<P, N>::BYTES;
+  hipLaunchKernelGGL((ssd_bwd_chunk_kernel<P, N>), grid, dim3(NTHR), smem, s, p);
+}
+
+}  // namespace ssdb
+}  // namespace hmx
+
+using namespace hmx;
+using namespace hmx::ssdb;
+
+extern "C" size_t hmx_ssd_chunk_bwd_workspace_bytes(int32_t nrows, int32_t H, int32_t P, int32_t N) {
+  const size_t st = (size_t)nrows * H * P * N;
+  return st * 4 + st * 2 + (size_t)nrows * H * 4 + 256;
+}
+
+extern "C" int hmx_ssd_chunk_bwd(
+    const void* x, int64_t x_ts, int64_t x_hs, const void* B, int64_t b_ts, int64_t b_gs,
+    const void* C, int64_t c_ts, int64_t c_gs, int32_t xbc_dtype, const void* dt, int32_t dt_dtype,
+    int64_t dt_ts, int64_t dt_hs, const float* A, const float* D, const float* dt_bias,
+    const void* z, int64_t z_ts, int64_t z_hs, const void* dy, int64_t dy_ts, int64_t dy_hs,
+    const float* h0, const float* chunk_states, const float* d_final, const int32_t* seg_table,
+    int32_t nrows, const int32_t* seq_table, int32_t nseq, int32_t H, int32_t HX, int32_t G,
+    int32_t GC, int32_t P, int32_t N, int32_t dt_softplus, float dt_min, float dt_max, float* dx,
+    float* dB, float* dC, void* dz, float* ddt, float* dA, float* dD, float* ddt_bias,
+    float* dh0, void* workspace, size_t workspace_bytes, void* stream) {
+  const char* fn = "hmx_ssd_chunk_bwd";
+  HMX_REQUIRE(xbc_dtype == HMX_BF16, HMX_EUNSUPPORTED, "%s: x/B/C/z/dy must be bfloat16", fn);
+  HMX_REQUIRE(P == 64 && (N == 64 || N == 128), HMX_EUNSUPPORTED,
+              "%s: headdim 64 and d_state in {64,128} (got %d, %d)", fn, P, N);
+  HMX_REQUIRE(H > 0 && HX > 0 && G > 0 && GC > 0 && H % HX == 0 && H % G == 0 && H % GC == 0,
+              HMX_EINVAL, "%s: H=%d must be a multiple of HX=%d, G=%d and GC=%d", fn, H, HX, G, GC);
+  HMX_REQUIRE(x && B && C && dt && A && dy && seg_table && seq_table && dx && dB && dC && ddt && dA &&
+                  (!z || dz) && nrows >= 0 && nseq >= 0,
+              HMX_EINVAL, "%s: null pointer", fn);
+  HMX_REQUIRE(dt_dtype == HMX_F32 || dt_dtype == HMX_BF16 || dt_dtype == HMX_F16, HMX_EINVAL,
+              "%s: dt dtype code %d", fn, dt_dtype);
+  const int64_t strides[] = {x_ts, x_hs, b_ts, b_gs, c_ts, c_gs, dy_ts, dy_hs,
+                             z ? z_ts : 8, z ? z_hs : 8};
+  for (int64_t st : strides)
+    HMX_REQUIRE(st % 8 == 0, HMX_EINVAL, "%s: token/head strides must be multiples of 8", fn);
+  HMX_REQUIRE(((uintptr_t)x | (uintptr_t)B | (uintptr_t)C | (uintptr_t)dy | (uintptr_t)z |
+               (uintptr_t)h0 | (uintptr_t)chunk_states) % 16 == 0,
+              HMX_EINVAL, "%s: operands must be 16-byte aligned", fn);
+  if (nrows == 0 && nseq == 0) return HMX_OK;
+  const size_t need = hmx_ssd_chunk_bwd_workspace_bytes(nrows, H, P, N);
+  HMX_REQUIRE(workspace && workspace_bytes >= need, HMX_EINVAL,
+              "%s: workspace of %zu bytes needed, %zu given", fn, need, workspace_bytes);
+  Params p;
+  p.x = static_cast<const bf16*>(x); p.x_ts = x_ts; p.x_hs = x_hs;
+  p.B = static_cast<const bf16*>(B); p.b_ts = b_ts; p.b_gs = b_gs;
+  p.C = static_cast<const bf16*>(C); p.c_ts = c_ts; p.c_gs = c_gs;
+  p.dt = dt; p.dt_dt = dt_dtype; p.dt_ts = dt_ts; p.dt_hs = dt_hs;
+  p.A = A; p.D = D; p.dt_bias = dt_bias;
+  p.z = static_cast<const bf16*>(z); p.z_ts = z_ts; p.z_hs = z_hs;
+  p.dy = static_cast<const bf16*>(dy); p.dy_ts = dy_ts; p.dy_hs = dy_hs;
+  p.h0 = h0; p.s0 = chunk_states; p.dT = d_final;
+  p.seg = seg_table; p.seqs = seq_table; p.nrows = nrows; p.nseq = nseq;
+  const size_t st = (size_t)nrows * H * P * N;
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  p.loc = reinterpret_cast<float*>(ws);
+  p.dS1 = reinterpret_cast<bf16*>(ws + st * 4);
+  p.aend = reinterpret_cast<float*>(ws + st * 6);
+  p.dx = dx; p.x_shared = HX < H;
+  p.dB = dB; p.b_shared = G < H;
+  p.dC = dC; p.c_shared = GC < H;
+  p.dz = static_cast<bf16*>(dz); p.ddt = ddt; p.dA = dA; p.dD = dD; p.dbias = ddt_bias;
+  p.dh0 = dh0;
+  p.H = H; p.HX = HX; p.G = G; p.GC = GC; p.softplus = dt_softplus;
+  p.dt_min = dt_min; p.dt_max = dt_max;
+  hipStream_t s = (hipStream_t)stream;
+  if (nrows == 0) {   // empty sequences only: dh0 = dT
+    hipLaunchKernelGGL(ssd_bwd_scan_kernel, dim3(nseq * H, (P * N + 1023) / 1024), dim3(256), 0, s,
+                       p, P * N);
+    return check_launch(fn);
+  }
+  if (N == 128) {
+    (void)hipFuncSetAttribute((const void*)ssd_bwd_chunk_kernel<64, 128>,
+                        hipFuncAttributeMaxDynamicSharedMemorySize, Lay<64, 128>::BYTES);
+    launch<64, 128>(p, s);
+  } else {
+    (void)hipFuncSetAttribute((const void*)ssd_bwd_chunk_kernel<64, 64>,
+                        hipFuncAttributeMaxDynamicSharedMemorySize, Lay<64, 64>::BYTES);
+    launch<64, 64>(p, s);
+  }
+  return check_launch(fn);
+}

@@ -85,6 +85,12 @@ SIGNATURES: dict[str, list] = {
                           _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _F32, _P, ctypes.c_size_t,
                           _P],
     "hmx_ssd_chunk_workspace_bytes": [_I32, _I32, _I32, _I32, _I32],
+    "hmx_ssd_chunk_bwd": [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I32,
+                          _P, _I32, _I64, _I64, _P, _P, _P, _P, _I64, _I64,
+                          _P, _I64, _I64, _P, _P, _P, _P, _I32, _P, _I32,
+                          _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _F32,
+                          _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _P],
+    "hmx_ssd_chunk_bwd_workspace_bytes": [_I32, _I32, _I32, _I32],
     "hmx_causal_conv1d_fwd": [_P, _I64, _P, _I64, _I32, _P, _I32, _I32, _P, _I32, _P, _I64, _I64,
                               _I32, _P, _I32, _I64, _P, _P, _I32, _I32, _I32, _P],
     "hmx_causal_conv1d_update": [_P, _I64, _P, _I64, _I32, _P, _I32, _I32, _P, _I32, _P, _I64,
@@ -111,7 +117,8 @@ _RESTYPES = {"hmx_last_error": ctypes.c_char_p, "hmx_gdn_chunk_workspace_bytes":
              "hmx_gka_cheb_bwd_workspace_bytes": ctypes.c_size_t,
              "hmx_gka_train_bwd_workspace_bytes": ctypes.c_size_t,
              "hmx_gdn_train_bwd_workspace_bytes": ctypes.c_size_t,
-             "hmx_ssd_chunk_workspace_bytes": ctypes.c_size_t}
+             "hmx_ssd_chunk_workspace_bytes": ctypes.c_size_t,
+             "hmx_ssd_chunk_bwd_workspace_bytes": ctypes.c_size_t}
 
 
 

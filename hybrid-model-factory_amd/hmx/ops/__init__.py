@@ -7,6 +7,7 @@ from .conv import causal_conv1d_fn, causal_conv1d_update
 from .gates import ProjGates
 from .gdn_train import ChunkGatedDeltaRule
 from .gka_train import ChebyshevIteration, GkaChebyshevGla, latent_chebyshev
+from .ssd_train import MambaChunkScanCombined
 from .norm import rms_norm_gated
 from .ssd import (mamba_chunk_scan_combined, mamba_chunk_scan_combined_varlen,
                   selective_state_update)
@@ -26,6 +27,7 @@ __all__ = [
     "torch_decoding_one_step",
     "ChunkGatedDeltaRule",
     "ChebyshevIteration",
+    "MambaChunkScanCombined",
     "GkaChebyshevGla",
     "latent_chebyshev",
     "mamba_chunk_scan_combined",

@@ -157,6 +157,40 @@ def _runs(row: list[int]) -> list[tuple[int, int]]:
     return out
 
 
+def seq_layout(b: int, l: int, seq_idx=None, cu_seqlens=None):
+    """The scan's sequences over the flattened [b*l] token axis: (bounds [(bos,
+    eos)], first_of_row [sequence starting row r's tokens or -1], last_of_row
+    [sequence ending row r or -1], end_at {(row, end): sequence}).  The state
+    restarts where seq_idx changes; without it at the cu_seqlens boundaries (b = 1);
+    otherwise each row is one sequence."""
+    if seq_idx is not None:
+        runs_per_row = [_runs(r) for r in seq_idx.to(torch.int64).cpu().tolist()]
+    elif cu_seqlens is not None:
+        runs_per_row = [[(a, e) for a, e in seq_bounds(cu_seqlens, 1, l) if e > a]]
+    else:
+        runs_per_row = [[(0, l)] for _ in range(b)]
+    bounds, first_of_row, last_of_row, end_at = [], [], [], {}
+    for r, runs in enumerate(runs_per_row):
+        first_of_row.append(len(bounds) if runs and runs[0][0] == 0 else -1)
+        for s0, s1 in runs:
+            end_at[(r, s1)] = len(bounds)
+            bounds.append((r * l + s0, r * l + s1))
+        last_of_row.append(len(bounds) - 1 if runs else -1)
+    return bounds, first_of_row, last_of_row, end_at
+
+
+def start_states(initial_states, first_of_row, nseq: int, shape):
+    """fp32 [nseq, *shape] start states with row r's initial state on the sequence
+    that starts it (zeros elsewhere), or None without initial states."""
+    if initial_states is None:
+        return None
+    h0 = torch.zeros(nseq, *shape, dtype=torch.float32, device=initial_states.device)
+    for r, f in enumerate(first_of_row):
+        if f >= 0:
+            h0[f] = initial_states[r].to(torch.float32)
+    return h0
+
+
 def mamba_chunk_scan_combined(x, dt, A, B, C, chunk_size, D=None, z=None, dt_bias=None,
                               initial_states=None, seq_idx=None, cu_seqlens=None,
                               dt_softplus=False, dt_limit=(0.0, float("inf")),
@@ -174,6 +208,15 @@ def mamba_chunk_scan_combined(x, dt, A, B, C, chunk_size, D=None, z=None, dt_bia
     accepted for signature compatibility: the kernel tiles by 64 tokens and the
     result does not depend on the chunking beyond fp32 rounding.
     """
+    ins = (x, dt, A, B, C, D, z, dt_bias, initial_states)
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in ins):
+        if return_varlen_states:
+            raise NotImplementedError("hmx mamba_chunk_scan_combined: return_varlen_states has "
+                                      "no backward here")
+        from .ssd_train import MambaChunkScanCombined
+        return MambaChunkScanCombined.apply(x, dt, A, B, C, chunk_size, D, z, dt_bias,
+                                            initial_states, seq_idx, cu_seqlens, dt_softplus,
+                                            dt_limit, return_final_states)
     if return_varlen_states and cu_seqlens is None:
         raise ValueError("return_varlen_states requires cu_seqlens")
     if cu_seqlens is not None and x.shape[0] != 1:
@@ -184,28 +227,8 @@ def mamba_chunk_scan_combined(x, dt, A, B, C, chunk_size, D=None, z=None, dt_bia
     G, N = B.shape[2], B.shape[3]
     if initial_states is not None and tuple(initial_states.shape) != (b, H, P, N):
         raise ValueError(f"initial_states must be {(b, H, P, N)}, got {tuple(initial_states.shape)}")
-    # sequences over the flattened token axis
-    runs_per_row: list[list[tuple[int, int]]] = []
-    if seq_idx is not None:
-        rows = seq_idx.to(torch.int64).cpu().tolist()
-        runs_per_row = [_runs(r) for r in rows]
-    elif cu_seqlens is not None:
-        runs_per_row = [[(a, e) for a, e in seq_bounds(cu_seqlens, 1, l) if e > a]]
-    else:
-        runs_per_row = [[(0, l)] for _ in range(b)]
-    bounds, first_of_row, last_of_row, end_at = [], [], [], {}
-    for r, runs in enumerate(runs_per_row):
-        first_of_row.append(len(bounds) if runs and runs[0][0] == 0 else -1)
-        for s0, s1 in runs:
-            end_at[(r, s1)] = len(bounds)
-            bounds.append((r * l + s0, r * l + s1))
-        last_of_row.append(len(bounds) - 1 if runs else -1)
-    h0 = None
-    if initial_states is not None:
-        h0 = torch.zeros(len(bounds), H, P, N, dtype=torch.float32, device=x.device)
-        for r, f in enumerate(first_of_row):
-            if f >= 0:
-                h0[f] = initial_states[r].to(torch.float32)
+    bounds, first_of_row, last_of_row, end_at = seq_layout(b, l, seq_idx, cu_seqlens)
+    h0 = start_states(initial_states, first_of_row, len(bounds), (H, P, N))
     xf, zf = _tokens_view(x), (None if z is None else _tokens_view(z))
     y = torch.empty(b, l, H, P, dtype=x.dtype, device=x.device)
     want = return_final_states or return_varlen_states

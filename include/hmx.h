@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define HMX_ABI_VERSION 12  /* 2: optional hmx_gated_norm output epilogue in the GDN ops;
+#define HMX_ABI_VERSION 13  /* 2: optional hmx_gated_norm output epilogue in the GDN ops;
                               3: q/k/v token strides in the GDN and GKA ops; slot-indexed
                               state pools and has_initial_state in the GDN, GKA and SSD
                               prefills;
@@ -46,7 +46,8 @@ extern "C" {
                                   conv update);
                               12: hmx_causal_conv1d_fwd_blocks and
                                   hmx_causal_conv1d_update_blocks (prefix-cache block
-                                  arguments) */
+                                  arguments);
+                              13: hmx_ssd_chunk_bwd (the SSD scan's backward) */
 
 enum hmx_status {
   HMX_OK = 0,
@@ -566,6 +567,48 @@ int hmx_ssd_chunk_fwd(const void* x, int64_t x_ts, int64_t x_hs,
  * states inside the op). */
 size_t hmx_ssd_chunk_workspace_bytes(int32_t nseg_total, int32_t nseq, int32_t H,
                                      int32_t P, int32_t N);
+
+/*
+ * Mamba2 SSD chunk scan backward: the gradients of hmx_ssd_chunk_fwd's output y
+ * (and end states) with respect to x, dt, A, B, C, D, z, dt_bias and the start
+ * states, for the chunk table of a forward whose every segment is one chunk
+ * (rows (n, bos, eos, 0, 1, index in the sequence, first row, rows), 1..64 tokens,
+ * a sequence's rows consecutive; seq_table [nseq][2] = (first row, rows)).
+ *  Inputs as in hmx_ssd_chunk_fwd (bf16 x [tokens, HX, P], B [tokens, G, N],
+ *  C [tokens, GC, N], z and dy [tokens, H, P], dt [tokens, H] f32/bf16/f16, fp32 A,
+ *  D [H, P], dt_bias).  h0: fp32 [nseq, H, P, N] start states or NULL (zero);
+ *  chunk_states: fp32 [nrows, H, P, N], the start state of every row that is not
+ *  its sequence's first (the segment start states of that forward); d_final: fp32
+ *  [nseq, H, P, N] gradient of the end states, or NULL.
+ *  Outputs, contiguous: dx fp32 [tokens, HX, P], dB fp32 [tokens, G, N], dC fp32
+ *  [tokens, GC, N] (each zero-filled by the caller when shared by several heads,
+ *  i.e. HX, G or GC < H: they accumulate); dz bf16 [tokens, H, P] (when z is
+ *  given); ddt fp32 [tokens, H] (gradient of the raw dt); dA fp32 [H], dD fp32
+ *  [H, P] (or NULL), ddt_bias fp32 [H] (or NULL), all zero-filled by the caller
+ *  (they accumulate); dh0 fp32 [nseq, H, P, N] or NULL.  P = 64, N in {64, 128}.
+ * workspace: hmx_ssd_chunk_bwd_workspace_bytes(nrows, H, P, N) bytes.
+ * Replaces: the backward of mamba_chunk_scan_combined (mamba_ssm 2.3.0, which the
+ *   training layer calls under autograd: training/src/hmf/model/hybrid_zoo/
+ *   layers/mamba/mamba2.py:555-580).
+ */
+int hmx_ssd_chunk_bwd(const void* x, int64_t x_ts, int64_t x_hs,
+                      const void* B, int64_t b_ts, int64_t b_gs,
+                      const void* C, int64_t c_ts, int64_t c_gs, int32_t xbc_dtype,
+                      const void* dt, int32_t dt_dtype, int64_t dt_ts, int64_t dt_hs,
+                      const float* A, const float* D, const float* dt_bias,
+                      const void* z, int64_t z_ts, int64_t z_hs,
+                      const void* dy, int64_t dy_ts, int64_t dy_hs,
+                      const float* h0, const float* chunk_states, const float* d_final,
+                      const int32_t* seg_table, int32_t nrows, const int32_t* seq_table,
+                      int32_t nseq, int32_t H, int32_t HX, int32_t G, int32_t GC, int32_t P,
+                      int32_t N, int32_t dt_softplus, float dt_min, float dt_max,
+                      float* dx, float* dB, float* dC, void* dz, float* ddt, float* dA,
+                      float* dD, float* ddt_bias, float* dh0,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes hmx_ssd_chunk_bwd needs (host-only arithmetic).  Companion of
+ * hmx_ssd_chunk_bwd; no reference counterpart. */
+size_t hmx_ssd_chunk_bwd_workspace_bytes(int32_t nrows, int32_t H, int32_t P, int32_t N);
 
 /*
  * Mamba2 single-token state update, in place on a slot-indexed state pool.

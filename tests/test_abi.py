@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_string():
     lib = _lib.load()
-    assert lib.hmx_abi_version() == 12
+    assert lib.hmx_abi_version() == 13
     assert isinstance(lib.hmx_last_error(), bytes)
 
 
