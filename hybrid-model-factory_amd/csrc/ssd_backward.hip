@@ -27,11 +27,14 @@
 // oracle/ssd.py; mamba_ssm's backward (un-vendored) computes the same gradients
 // with its own kernels (training/.../layers/mamba/mamba2.py:555-580 calls it).
 //
-// Three launches over the forward's 64-token chunks (rows of the segment table,
-// one chunk each, with the chunk start states S0 of the recomputed forward):
-//   ssd_bwd_local_kernel  (chunk, head): sum_t e^{A_t} g_t C_t^T and A_L
-//   ssd_bwd_scan_kernel   (sequence, head, 1024 state elements): dS1 of every chunk
-//                          by the reverse scan, and dS0 of the sequence's start
+// Three launches over 64-token chunks (rows of a segment table, one chunk each):
+//   ssd_bwd_local_kernel  (chunk, head): the chunk's zero-start end state
+//                          sum_s e^{A_L - A_s} dt'_s x_s B_s^T, its share
+//                          sum_t e^{A_t} g_t C_t^T of dS0, and e^{A_L}
+//   ssd_bwd_scan_kernel   (sequence, head, 1024 state elements): the forward chain
+//                          S0(c+1) = e^{A_L(c)} S0(c) + local(c) gives every chunk's
+//                          start state, the reverse chain dS1 of every chunk and dS0
+//                          of the sequence's start
 //   ssd_bwd_chunk_kernel  (chunk, head): everything else
 // Operands shared by several heads (x of HX < H heads, B of G < H groups, C of
 // GC < H groups) accumulate with fp32 atomics; the others are stored.
@@ -58,14 +61,15 @@ struct Params {
   const bf16* z; int64_t z_ts, z_hs;         // [T][H][P] or null
   const bf16* dy; int64_t dy_ts, dy_hs;      // [T][H][P]
   const float* h0;                           // [nseq][H][P][N] or null (zero start)
-  const float* s0;                           // [nrows][H][P][N] chunk start states, or null
   const float* dT;                           // [nseq][H][P][N] end-state gradients, or null
   const int* seg;                            // [nrows][8] segment rows (one chunk each)
   const int* seqs;                           // [nseq][2]: first row, rows
   int nrows, nseq;
-  float* loc;                                // ws [nrows][H][P][N]
-  float* aend;                               // ws [nrows][H]
-  bf16* dS1;                                 // ws [nrows][H][P][N]
+  bf16* loc;                                 // ws [nrows][H][P][N]: dS0 shares
+  bf16* sloc;                                // ws [nrows][H][P][N]: zero-start end states
+  float* edec;                               // ws [nrows][H]: e^{A_L}
+  bf16* S0;                                  // ws [nrows][H][P][N]: chunk start states
+  bf16* dS1;                                 // ws [nrows][H][P][N]: end-state gradients
   // outputs (contiguous)
   float* dx;   int x_shared;                 // [T][HX][P] fp32
   float* dB;   int b_shared;                 // [T][G][N] fp32
@@ -117,103 +121,166 @@ __device__ __forceinline__ Tok token_scalars(const Params& p, int h, int tok0, i
 }
 
 // ---------------------------------------------------------------------------
-// local: loc[r][h] = sum_t e^{A_t} g_t C_t^T  (P x N), aend[r][h] = A_L
+// local: sloc[r][h] = sum_s dt'_s e^{A_L - A_s} x_s B_s^T, loc[r][h] = sum_t e^{A_t}
+// g_t C_t^T (P x N each, stored in bf16: the scans accumulate them in fp32),
+// edec[r][h] = e^{A_L}
 // ---------------------------------------------------------------------------
 template <int P, int N>
 __global__ __launch_bounds__(NTHR) void ssd_bwd_local_kernel(Params p) {
   constexpr int LDX = P + 8, LDB = N + 8;
-  __shared__ __align__(16) bf16 sG[L * LDX];   // e^{A_t} g_t
+  __shared__ __align__(16) bf16 sG[L * LDX];    // e^{A_t} g_t
+  __shared__ __align__(16) bf16 sXW[L * LDX];   // dt'_s e^{A_L - A_s} x_s
   __shared__ __align__(16) bf16 sC[L * LDB];
-  __shared__ float sEA[L];
+  __shared__ __align__(16) bf16 sB[L * LDB];
+  __shared__ float sEA[L], sWT[L];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int H = p.H;
   const int r = blockIdx.x / H, h = blockIdx.x % H;
   const Row ro = load_row(p.seg, r);
   const int tok0 = ro.bos, nval = ro.eos - ro.bos;
-  const int gc = h / (H / p.GC);
+  const int hx = h / (H / p.HX), g = h / (H / p.G), gc = h / (H / p.GC);
   if (wave == 0) {
     const Tok tk = token_scalars(p, h, tok0, nval, lane);
+    const float aend = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, tk.acs), 63));
     sEA[lane] = fast_exp(tk.acs);
-    if (lane == L - 1) p.aend[(int64_t)r * H + h] = tk.acs;
+    sWT[lane] = tk.dtv * fast_exp(aend - tk.acs);
+    if (lane == L - 1) p.edec[(int64_t)r * H + h] = expf(aend);
   }
-  // C rows (zero past the chunk)
+  // B and C rows (zero past the chunk)
 #pragma unroll
   for (int i = 0; i < L * N / 8 / NTHR; ++i) {
     const int e = (i * NTHR + tid) * 8, t = e / N, c = e % N;
-    bf16x8 v = {};
-    if (t < nval) v = *reinterpret_cast<const bf16x8*>(p.C + (int64_t)(tok0 + t) * p.c_ts +
-                                                       (int64_t)gc * p.c_gs + c);
-    *reinterpret_cast<bf16x8*>(sC + t * LDB + c) = v;
+    bf16x8 bv = {}, cv = {};
+    if (t < nval) {
+      bv = *reinterpret_cast<const bf16x8*>(p.B + (int64_t)(tok0 + t) * p.b_ts + (int64_t)g * p.b_gs + c);
+      cv = *reinterpret_cast<const bf16x8*>(p.C + (int64_t)(tok0 + t) * p.c_ts + (int64_t)gc * p.c_gs + c);
+    }
+    *reinterpret_cast<bf16x8*>(sB + t * LDB + c) = bv;
+    *reinterpret_cast<bf16x8*>(sC + t * LDB + c) = cv;
   }
-  __syncthreads();   // sEA
+  __syncthreads();   // sEA, sWT
 #pragma unroll
   for (int i = 0; i < L * P / 8 / NTHR; ++i) {
     const int e = (i * NTHR + tid) * 8, t = e / P, c = e % P;
-    bf16x8 o = {};
+    bf16x8 o = {}, xw = {};
     if (t < nval) {
-      const int64_t off = (int64_t)(tok0 + t) * p.dy_ts + (int64_t)h * p.dy_hs + c;
-      const bf16x8 g = *reinterpret_cast<const bf16x8*>(p.dy + off);
+      const bf16x8 dv = *reinterpret_cast<const bf16x8*>(p.dy + (int64_t)(tok0 + t) * p.dy_ts +
+                                                          (int64_t)h * p.dy_hs + c);
+      const bf16x8 xv = *reinterpret_cast<const bf16x8*>(p.x + (int64_t)(tok0 + t) * p.x_ts +
+                                                          (int64_t)hx * p.x_hs + c);
       bf16x8 zz = {};
       if (p.z) zz = *reinterpret_cast<const bf16x8*>(p.z + (int64_t)(tok0 + t) * p.z_ts +
                                                     (int64_t)h * p.z_hs + c);
-      const float ea = sEA[t];
+      const float ea = sEA[t], wt = sWT[t];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        float v = (float)g[j];
+        float v = (float)dv[j];
         if (p.z) v *= silu((float)zz[j]);
         o[j] = (bf16)(v * ea);
+        xw[j] = (bf16)((float)xv[j] * wt);
       }
     }
     *reinterpret_cast<bf16x8*>(sG + t * LDX + c) = o;
+    *reinterpret_cast<bf16x8*>(sXW + t * LDX + c) = xw;
   }
   __syncthreads();
-  // wave w: p rows [16w', ...) for P/16 row blocks over 4 waves, all n tiles
+  // wave w: p rows [16 (w PBW + i), ...), all n tiles, for both products
   const int q4 = lane >> 4, l16 = lane & 15;
   constexpr int PBW = P / 16 / 4;   // p blocks per wave
-  f32x4 acc[PBW][N / 16];
 #pragma unroll
-  for (int i = 0; i < PBW; ++i)
+  for (int which = 0; which < 2; ++which) {
+    const bf16* sa = which ? sXW : sG;
+    const bf16* sb = which ? sB : sC;
+    f32x4 acc[PBW][N / 16];
 #pragma unroll
-    for (int j = 0; j < N / 16; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < PBW; ++i)
 #pragma unroll
-  for (int k0 = 0; k0 < L; k0 += 32) {
-    bf16x8 bf[N / 16];
+      for (int j = 0; j < N / 16; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < N / 16; ++j) bf[j] = frag_t(sC, LDB, k0, 16 * j, lane);
+    for (int k0 = 0; k0 < L; k0 += 32) {
+      bf16x8 bf[N / 16];
 #pragma unroll
-    for (int i = 0; i < PBW; ++i) {
-      const bf16x8 af = frag_t(sG, LDX, k0, 16 * (wave * PBW + i), lane);
+      for (int j = 0; j < N / 16; ++j) bf[j] = frag_t(sb, LDB, k0, 16 * j, lane);
 #pragma unroll
-      for (int j = 0; j < N / 16; ++j) acc[i][j] = mfma16(af, bf[j], acc[i][j]);
+      for (int i = 0; i < PBW; ++i) {
+        const bf16x8 af = frag_t(sa, LDX, k0, 16 * (wave * PBW + i), lane);
+#pragma unroll
+        for (int j = 0; j < N / 16; ++j) acc[i][j] = mfma16(af, bf[j], acc[i][j]);
+      }
     }
+    bf16* dst = (which ? p.sloc : p.loc) + ((int64_t)r * H + h) * P * N;
+#pragma unroll
+    for (int i = 0; i < PBW; ++i)
+#pragma unroll
+      for (int j = 0; j < N / 16; ++j)
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          dst[(16 * (wave * PBW + i) + 4 * q4 + v) * N + 16 * j + l16] = (bf16)acc[i][j][v];
   }
-  float* dst = p.loc + ((int64_t)r * H + h) * P * N;
-#pragma unroll
-  for (int i = 0; i < PBW; ++i)
-#pragma unroll
-    for (int j = 0; j < N / 16; ++j)
-#pragma unroll
-      for (int v = 0; v < 4; ++v)
-        dst[(16 * (wave * PBW + i) + 4 * q4 + v) * N + 16 * j + l16] = acc[i][j][v];
 }
 
 // ---------------------------------------------------------------------------
-// reverse scan: dS1[last] = dT; dS1[c-1] = e^{A_L(c)} dS1[c] + loc[c]; dh0 = the
-// value before the first chunk
+// scans over a sequence's chunks, 4 state elements per thread, PF chunks' loads in
+// flight ahead of the dependent chain:
+//   forward: S0(first) = h0 (or 0), S0(c+1) = e^{A_L(c)} S0(c) + sloc(c)
+//   reverse: dS1(last) = dT (or 0), dS1(c-1) = e^{A_L(c)} dS1(c) + loc(c); dh0 =
+//            the value before the first chunk
 // ---------------------------------------------------------------------------
+constexpr int PF = 4;
+__device__ __forceinline__ f32x4 ld4(const float* q) { return *reinterpret_cast<const f32x4*>(q); }
+__device__ __forceinline__ f32x4 ld4(const bf16* q) {
+  const bf16x4 v = *reinterpret_cast<const bf16x4*>(q);
+  return f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+}
+__device__ __forceinline__ void st4b(bf16* q, f32x4 v) {
+  *reinterpret_cast<bf16x4*>(q) = bf16x4{(bf16)v[0], (bf16)v[1], (bf16)v[2], (bf16)v[3]};
+}
+
 __global__ __launch_bounds__(256) void ssd_bwd_scan_kernel(Params p, int PN) {
   const int H = p.H;
   const int n = blockIdx.x / H, h = blockIdx.x % H;
   const int first = p.seqs[2 * n], cnt = p.seqs[2 * n + 1];
-  for (int e = blockIdx.y * 256 + threadIdx.x; e < PN; e += gridDim.y * 256) {
-    float g = p.dT ? p.dT[((int64_t)n * H + h) * PN + e] : 0.f;
-    for (int k = cnt - 1; k >= 0; --k) {
-      const int64_t b = (int64_t)(first + k) * H + h;
-      p.dS1[b * PN + e] = (bf16)g;
-      g = g * expf(p.aend[b]) + p.loc[b * PN + e];
+  const int e = (blockIdx.y * 256 + threadIdx.x) * 4;
+  if (e >= PN) return;
+  const int64_t sb = ((int64_t)n * H + h) * PN + e;
+  auto off = [&](int k) { return ((int64_t)(first + k) * H + h) * PN + e; };
+  auto dec = [&](int k) { return p.edec[(int64_t)(first + k) * H + h]; };
+  // Chain position m of a direction: chunk k = m (forward) or cnt-1-m (reverse).
+  // Full groups of PF run without branches (the prefetch index is clamped in
+  // bounds), so each load is waited for only where it is used; the tail is guarded.
+  auto chain = [&](bool fwd, f32x4 X, const bf16* src, bf16* dst) -> f32x4 {
+    if (cnt == 0) return X;
+    auto kk = [&](int m) { return fwd ? m : cnt - 1 - m; };
+    f32x4 buf[PF];
+#pragma unroll
+    for (int j = 0; j < PF; ++j) buf[j] = ld4(src + off(kk(min(j, cnt - 1))));
+    int m = 0;
+    for (; m + PF <= cnt; m += PF) {
+#pragma unroll
+      for (int j = 0; j < PF; ++j) {
+        const int k = kk(m + j);
+        st4b(dst + off(k), X);
+        const float d = dec(k);
+        const f32x4 l = buf[j];
+        buf[j] = ld4(src + off(kk(min(m + j + PF, cnt - 1))));
+        X = X * d + l;
+      }
     }
-    if (p.dh0) p.dh0[((int64_t)n * H + h) * PN + e] = g;
+#pragma unroll
+    for (int j = 0; j < PF; ++j) {
+      if (m + j < cnt) {
+        const int k = kk(m + j);
+        st4b(dst + off(k), X);
+        X = X * dec(k) + buf[j];
+      }
+    }
+    return X;
+  };
+  chain(true, p.h0 ? ld4(p.h0 + sb) : f32x4{0.f, 0.f, 0.f, 0.f}, p.sloc, p.S0);
+  {
+    const f32x4 G = chain(false, p.dT ? ld4(p.dT + sb) : f32x4{0.f, 0.f, 0.f, 0.f}, p.loc, p.dS1);
+    if (p.dh0) *reinterpret_cast<f32x4*>(p.dh0 + sb) = G;
   }
 }
 
@@ -331,31 +398,21 @@ __global__ __launch_bounds__(NTHR, 1) void ssd_bwd_chunk_kernel(Params p) {
     *reinterpret_cast<bf16x8*>(sB + t * LDB + c) = bv;
     *reinterpret_cast<bf16x8*>(sC + t * LDB + c) = cv;
   }
-  // S0 (fp32, the sequence's start state for its first chunk) and dS1, with <dS1, S0>
+  // the chunk's start state S0 and end-state gradient dS1 (bf16, from the scans),
+  // with <dS1, S0>
   {
-    const float* s0 = nullptr;
-    if (ro.idx == 0) {
-      if (p.h0) s0 = p.h0 + ((int64_t)ro.n * H + h) * P * N;
-    } else if (p.s0) {
-      s0 = p.s0 + ((int64_t)r * H + h) * P * N;
-    }
+    const bf16* s0 = p.S0 + ((int64_t)r * H + h) * P * N;
     const bf16* ds = p.dS1 + ((int64_t)r * H + h) * P * N;
     float hd = 0.f;
 #pragma unroll
     for (int i = 0; i < P * N / 8 / NTHR; ++i) {
       const int e = (i * NTHR + tid) * 8, pr = e / N, c = e % N;
-      f32x4 a = {0.f, 0.f, 0.f, 0.f}, b = {0.f, 0.f, 0.f, 0.f};
-      if (s0) {
-        a = *reinterpret_cast<const f32x4*>(s0 + e);
-        b = *reinterpret_cast<const f32x4*>(s0 + e + 4);
-      }
+      const bf16x8 sv = *reinterpret_cast<const bf16x8*>(s0 + e);
       const bf16x8 dv = *reinterpret_cast<const bf16x8*>(ds + e);
-      const bf16x8 sv = {(bf16)a[0], (bf16)a[1], (bf16)a[2], (bf16)a[3],
-                         (bf16)b[0], (bf16)b[1], (bf16)b[2], (bf16)b[3]};
       *reinterpret_cast<bf16x8*>(sS + pr * LDB + c) = sv;
       *reinterpret_cast<bf16x8*>(sDS + pr * LDB + c) = dv;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) hd += a[j] * (float)dv[j] + b[j] * (float)dv[4 + j];
+      for (int j = 0; j < 8; ++j) hd += (float)sv[j] * (float)dv[j];
     }
     hd = wave_sum(hd);
     if (lane == 0) atomicAdd(sHD, hd);
@@ -621,7 +678,7 @@ using namespace hmx::ssdb;
 
 extern "C" size_t hmx_ssd_chunk_bwd_workspace_bytes(int32_t nrows, int32_t H, int32_t P, int32_t N) {
   const size_t st = (size_t)nrows * H * P * N;
-  return st * 4 + st * 2 + (size_t)nrows * H * 4 + 256;
+  return st * (2 + 2 + 2 + 2) + (size_t)nrows * H * 4 + 256;
 }
 
 extern "C" int hmx_ssd_chunk_bwd(
@@ -629,7 +686,7 @@ extern "C" int hmx_ssd_chunk_bwd(
     const void* C, int64_t c_ts, int64_t c_gs, int32_t xbc_dtype, const void* dt, int32_t dt_dtype,
     int64_t dt_ts, int64_t dt_hs, const float* A, const float* D, const float* dt_bias,
     const void* z, int64_t z_ts, int64_t z_hs, const void* dy, int64_t dy_ts, int64_t dy_hs,
-    const float* h0, const float* chunk_states, const float* d_final, const int32_t* seg_table,
+    const float* h0, const float* d_final, const int32_t* seg_table,
     int32_t nrows, const int32_t* seq_table, int32_t nseq, int32_t H, int32_t HX, int32_t G,
     int32_t GC, int32_t P, int32_t N, int32_t dt_softplus, float dt_min, float dt_max, float* dx,
     float* dB, float* dC, void* dz, float* ddt, float* dA, float* dD, float* ddt_bias,
@@ -650,7 +707,7 @@ extern "C" int hmx_ssd_chunk_bwd(
   for (int64_t st : strides)
     HMX_REQUIRE(st % 8 == 0, HMX_EINVAL, "%s: token/head strides must be multiples of 8", fn);
   HMX_REQUIRE(((uintptr_t)x | (uintptr_t)B | (uintptr_t)C | (uintptr_t)dy | (uintptr_t)z |
-               (uintptr_t)h0 | (uintptr_t)chunk_states) % 16 == 0,
+               (uintptr_t)h0 | (uintptr_t)d_final | (uintptr_t)dh0) % 16 == 0,
               HMX_EINVAL, "%s: operands must be 16-byte aligned", fn);
   if (nrows == 0 && nseq == 0) return HMX_OK;
   const size_t need = hmx_ssd_chunk_bwd_workspace_bytes(nrows, H, P, N);
@@ -664,13 +721,15 @@ extern "C" int hmx_ssd_chunk_bwd(
   p.A = A; p.D = D; p.dt_bias = dt_bias;
   p.z = static_cast<const bf16*>(z); p.z_ts = z_ts; p.z_hs = z_hs;
   p.dy = static_cast<const bf16*>(dy); p.dy_ts = dy_ts; p.dy_hs = dy_hs;
-  p.h0 = h0; p.s0 = chunk_states; p.dT = d_final;
+  p.h0 = h0; p.dT = d_final;
   p.seg = seg_table; p.seqs = seq_table; p.nrows = nrows; p.nseq = nseq;
   const size_t st = (size_t)nrows * H * P * N;
   unsigned char* ws = static_cast<unsigned char*>(workspace);
-  p.loc = reinterpret_cast<float*>(ws);
-  p.dS1 = reinterpret_cast<bf16*>(ws + st * 4);
-  p.aend = reinterpret_cast<float*>(ws + st * 6);
+  p.loc = reinterpret_cast<bf16*>(ws);
+  p.sloc = reinterpret_cast<bf16*>(ws + st * 2);
+  p.S0 = reinterpret_cast<bf16*>(ws + st * 4);
+  p.dS1 = reinterpret_cast<bf16*>(ws + st * 6);
+  p.edec = reinterpret_cast<float*>(ws + st * 8);
   p.dx = dx; p.x_shared = HX < H;
   p.dB = dB; p.b_shared = G < H;
   p.dC = dC; p.c_shared = GC < H;

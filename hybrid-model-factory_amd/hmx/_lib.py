@@ -87,7 +87,7 @@ SIGNATURES: dict[str, list] = {
     "hmx_ssd_chunk_workspace_bytes": [_I32, _I32, _I32, _I32, _I32],
     "hmx_ssd_chunk_bwd": [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I32,
                           _P, _I32, _I64, _I64, _P, _P, _P, _P, _I64, _I64,
-                          _P, _I64, _I64, _P, _P, _P, _P, _I32, _P, _I32,
+                          _P, _I64, _I64, _P, _P, _P, _I32, _P, _I32,
                           _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _F32,
                           _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _P],
     "hmx_ssd_chunk_bwd_workspace_bytes": [_I32, _I32, _I32, _I32],

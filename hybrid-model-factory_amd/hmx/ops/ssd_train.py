@@ -2,11 +2,11 @@
 
 The training layer calls mamba_ssm's ``mamba_chunk_scan_combined`` under autograd
 (training/src/hmf/model/hybrid_zoo/layers/mamba/mamba2.py:555-580).  The forward
-here is the HIP scan of ops/ssd.py.  The backward (csrc/ssd_backward.hip) needs the
-state at the start of every 64-token chunk: it recomputes the forward with one
-segment per chunk, whose combine forms those states (nothing beyond the inputs is
-kept between forward and backward), then runs the reverse scan of the state
-gradients and the per-chunk gradient kernel.
+here is the HIP scan of ops/ssd.py.  The backward (csrc/ssd_backward.hip) forms
+the state at the start of every 64-token chunk again from the inputs (nothing
+beyond them is kept between forward and backward): a local pass per chunk, one
+scan launch running the forward state chain and the reverse chain of the state
+gradients, then the per-chunk gradient kernel.
 """
 from __future__ import annotations
 
@@ -14,8 +14,8 @@ import torch
 
 from .. import _lib
 from .gdn import _device_table
-from .ssd import (SSD_CHUNK, _prep3, _ssd_scan, _tokens_view, mamba_chunk_scan_combined,
-                  seq_layout, start_states)
+from .ssd import (SSD_CHUNK, _prep3, _tokens_view, mamba_chunk_scan_combined, seq_layout,
+                  start_states)
 
 
 def _chunk_table(bounds):
@@ -49,13 +49,6 @@ def ssd_chunk_scan_bwd(x, dt, A, B, C, D, z, dt_bias, dt_softplus, dt_limit, bou
     x, B, C = _prep3(x), _prep3(B), _prep3(C)
     z = None if z is None else _prep3(z.to(torch.bfloat16))
     dy = _prep3(dy.to(torch.bfloat16))
-    # the chunk start states: the forward again, one segment per chunk
-    s0 = None
-    if nrows:
-        y_scratch = torch.empty(T, H, P, dtype=torch.bfloat16, device=dev)
-        _, s0 = _ssd_scan(x, dt, A, B, C, D, z, dt_bias, dt_softplus, dt_limit, bounds, h0,
-                          y_scratch, False, seg_rows=rows)
-        del y_scratch
     A32 = A.to(torch.float32).contiguous()
     Dm = None
     if D is not None:
@@ -90,7 +83,7 @@ def ssd_chunk_scan_bwd(x, dt, A, B, C, D, z, dt_bias, dt_softplus, dt_limit, bou
               _lib.ptr(A32), _lib.ptr(Dm), _lib.ptr(bias),
               _lib.ptr(z), 0 if z is None else z.stride(0), 0 if z is None else z.stride(1),
               _lib.ptr(dy), dy.stride(0), dy.stride(1),
-              _lib.ptr(h0), _lib.ptr(s0), _lib.ptr(d_final),
+              _lib.ptr(h0), _lib.ptr(d_final),
               _lib.ptr(seg), nrows, _lib.ptr(sq), nseq, H, HX, G, GC, P, N,
               int(bool(dt_softplus)), lo, hi,
               _lib.ptr(dx), _lib.ptr(dB), _lib.ptr(dC), _lib.ptr(dz), _lib.ptr(ddt),

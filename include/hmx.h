@@ -571,15 +571,14 @@ size_t hmx_ssd_chunk_workspace_bytes(int32_t nseg_total, int32_t nseq, int32_t H
 /*
  * Mamba2 SSD chunk scan backward: the gradients of hmx_ssd_chunk_fwd's output y
  * (and end states) with respect to x, dt, A, B, C, D, z, dt_bias and the start
- * states, for the chunk table of a forward whose every segment is one chunk
- * (rows (n, bos, eos, 0, 1, index in the sequence, first row, rows), 1..64 tokens,
- * a sequence's rows consecutive; seq_table [nseq][2] = (first row, rows)).
+ * states.  The sequences are cut into chunks of at most 64 tokens, one row each of
+ * seg_table (n, bos, eos, 0, 1, index in the sequence, first row, rows; a
+ * sequence's rows consecutive); seq_table [nseq][2] = (first row, rows).  The
+ * chunk start states are formed here (from h0), not taken from the forward.
  *  Inputs as in hmx_ssd_chunk_fwd (bf16 x [tokens, HX, P], B [tokens, G, N],
  *  C [tokens, GC, N], z and dy [tokens, H, P], dt [tokens, H] f32/bf16/f16, fp32 A,
  *  D [H, P], dt_bias).  h0: fp32 [nseq, H, P, N] start states or NULL (zero);
- *  chunk_states: fp32 [nrows, H, P, N], the start state of every row that is not
- *  its sequence's first (the segment start states of that forward); d_final: fp32
- *  [nseq, H, P, N] gradient of the end states, or NULL.
+ *  d_final: fp32 [nseq, H, P, N] gradient of the end states, or NULL.
  *  Outputs, contiguous: dx fp32 [tokens, HX, P], dB fp32 [tokens, G, N], dC fp32
  *  [tokens, GC, N] (each zero-filled by the caller when shared by several heads,
  *  i.e. HX, G or GC < H: they accumulate); dz bf16 [tokens, H, P] (when z is
@@ -598,7 +597,7 @@ int hmx_ssd_chunk_bwd(const void* x, int64_t x_ts, int64_t x_hs,
                       const float* A, const float* D, const float* dt_bias,
                       const void* z, int64_t z_ts, int64_t z_hs,
                       const void* dy, int64_t dy_ts, int64_t dy_hs,
-                      const float* h0, const float* chunk_states, const float* d_final,
+                      const float* h0, const float* d_final,
                       const int32_t* seg_table, int32_t nrows, const int32_t* seq_table,
                       int32_t nseq, int32_t H, int32_t HX, int32_t G, int32_t GC, int32_t P,
                       int32_t N, int32_t dt_softplus, float dt_min, float dt_max,
