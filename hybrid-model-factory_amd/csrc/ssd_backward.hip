@@ -35,9 +35,12 @@
 //                          S0(c+1) = e^{A_L(c)} S0(c) + local(c) gives every chunk's
 //                          start state, the reverse chain dS1 of every chunk and dS0
 //                          of the sequence's start
-//   ssd_bwd_chunk_kernel  (chunk, head): everything else
-// Operands shared by several heads (x of HX < H heads, B of G < H groups, C of
-// GC < H groups) accumulate with fp32 atomics; the others are stored.
+//   ssd_bwd_chunk_kernel  (chunk, C group): everything else, for the group's heads
+//                          in turn, the next head's inputs loading into registers
+//                          during the current head's products
+// dC (and dB when B's groups are C's) sum over the workgroup's heads in registers;
+// x shared by several heads (HX < H), or B shared wider than a C group, accumulate
+// with fp32 atomics; everything else is stored.
 
 #include <type_traits>
 
@@ -73,7 +76,7 @@ struct Params {
   // outputs (contiguous)
   float* dx;   int x_shared;                 // [T][HX][P] fp32
   float* dB;   int b_shared;                 // [T][G][N] fp32
-  float* dC;   int c_shared;                 // [T][GC][N] fp32
+  float* dC;                                 // [T][GC][N] fp32
   bf16* dz;                                  // [T][H][P] or null
   float* ddt;                                // [T][H]
   float* dA;                                 // [H] (accumulated)
@@ -103,10 +106,9 @@ __device__ __forceinline__ float silu(float z) { return z / (1.f + fast_exp(-z))
 // Per-token scalars of a chunk, lane t of one wave: dt' (0 past the chunk's
 // tokens), A_t, and the factor d dt'/d dt (clamp pass times the softplus slope).
 struct Tok { float dtv, acs, fac; };
-__device__ __forceinline__ Tok token_scalars(const Params& p, int h, int tok0, int nval, int lane) {
-  float d = 0.f;
-  if (lane < nval) d = load_any(p.dt, (int64_t)(tok0 + lane) * p.dt_ts + (int64_t)h * p.dt_hs, p.dt_dt);
-  d += p.dt_bias ? p.dt_bias[h] : 0.f;
+__device__ __forceinline__ Tok token_scalars_raw(const Params& p, int h, float dt_raw, int nval,
+                                                 int lane) {
+  float d = dt_raw + (p.dt_bias ? p.dt_bias[h] : 0.f);
   float sp = d, slope = 1.f;
   if (p.softplus) {
     sp = softplus20(d);
@@ -118,6 +120,11 @@ __device__ __forceinline__ Tok token_scalars(const Params& p, int h, int tok0, i
   if (lane >= nval) { dtv = 0.f; fac = 0.f; }
   const float acs = scan64(dtv * p.A[h], lane);
   return Tok{dtv, acs, fac};
+}
+__device__ __forceinline__ Tok token_scalars(const Params& p, int h, int tok0, int nval, int lane) {
+  float d = 0.f;
+  if (lane < nval) d = load_any(p.dt, (int64_t)(tok0 + lane) * p.dt_ts + (int64_t)h * p.dt_hs, p.dt_dt);
+  return token_scalars_raw(p, h, d, nval, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -301,14 +308,25 @@ struct Lay {
   static constexpr int OFF_M = OFF_DS + P * LDB * 2;       // M dt'    [L][LDM]
   static constexpr int OFF_W = OFF_M + L * LDM * 2;        // W        [L][LDM]
   static constexpr int OFF_F = OFF_W + L * LDM * 2;        // fp32 scalars
-  static constexpr int NF = 17;                            // scalar arrays of L floats
+  static constexpr int NF = 18;                            // scalar arrays of L floats
   static constexpr int BYTES = OFF_F + NF * L * 4 + 64;
   static_assert(BYTES <= 160 * 1024, "LDS budget");
 };
 // scalar arrays
 enum { F_DT, F_ACS, F_EA, F_E, F_FAC, F_ROWR, F_DAS, F_DDS,
-       F_CMQ0, F_CR0 = F_CMQ0 + 4, F_DD = F_CR0 + 4 };   // F_DD: P = 64 floats
-static_assert(F_DD + 1 == 17, "scalar arrays");
+       F_CMQ0, F_CR0 = F_CMQ0 + 4, F_DD = F_CR0 + 4, F_DV };   // F_DD, F_DV: P = 64 floats
+static_assert(F_DV + 1 == 18, "scalar arrays");
+
+// One head's inputs for the chunk, loaded into registers while the head before it
+// is computed: x, dy, z rows (2 vectors per thread), S0 and dS1 (4 each), B rows
+// (4, when B is not staged once per workgroup), the raw dt of token `lane` (wave 0)
+// and D of feature `tid` (tid < 64).
+template <int P, int N>
+struct HeadIn {
+  bf16x8 x[L * P / 8 / NTHR], dy[L * P / 8 / NTHR], z[L * P / 8 / NTHR];
+  bf16x8 s0[P * N / 8 / NTHR], ds[P * N / 8 / NTHR], b[L * N / 8 / NTHR];
+  float dt, d;
+};
 
 template <int P, int N>
 __global__ __launch_bounds__(NTHR, 1) void ssd_bwd_chunk_kernel(Params p) {
@@ -333,51 +351,99 @@ __global__ __launch_bounds__(NTHR, 1) void ssd_bwd_chunk_kernel(Params p) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int q4 = lane >> 4, l16 = lane & 15;
-  const int H = p.H;
-  const int r = blockIdx.x / H, h = blockIdx.x % H;
+  const int H = p.H, GC = p.GC, HC = H / GC, HB = H / p.G, HXS = H / p.HX;
+  // one workgroup per (chunk, C group): the group's HC heads in turn
+  const int r = blockIdx.x / GC, gc = blockIdx.x % GC;
   const Row ro = load_row(p.seg, r);
   const int tok0 = ro.bos, nval = ro.eos - ro.bos;
-  const int hx = h / (H / p.HX), g = h / (H / p.G), gc = h / (H / p.GC);
-  const float A_h = p.A[h];
+  const int h_first = gc * HC;
+  // B staged once when the workgroup's heads are exactly one B group; dB then sums
+  // over them in registers.  Otherwise B is per head (stored) or shared wider
+  // (atomics).
+  const bool b_once = p.G == GC;
+  constexpr int VX = L * P / 8 / NTHR, VS = P * N / 8 / NTHR, VB = L * N / 8 / NTHR;
 
   if (tid == 0) sHD[0] = 0.f;
   if (tid < P) F(F_DD, tid) = 0.f;
-  if (wave == 0) {
-    const Tok tk = token_scalars(p, h, tok0, nval, lane);
-    const float aend = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, tk.acs), 63));
-    F(F_DT, lane) = tk.dtv;
-    F(F_ACS, lane) = tk.acs;
-    F(F_EA, lane) = fast_exp(tk.acs);
-    F(F_E, lane) = fast_exp(aend - tk.acs);
-    F(F_FAC, lane) = tk.fac;
+  // C (and B when shared by all the heads) once
+#pragma unroll
+  for (int i = 0; i < VB; ++i) {
+    const int e = (i * NTHR + tid) * 8, t = e / N, c = e % N;
+    bf16x8 cv = {}, bv = {};
+    if (t < nval) {
+      cv = *reinterpret_cast<const bf16x8*>(p.C + (int64_t)(tok0 + t) * p.c_ts + (int64_t)gc * p.c_gs + c);
+      if (b_once)
+        bv = *reinterpret_cast<const bf16x8*>(p.B + (int64_t)(tok0 + t) * p.b_ts +
+                                              (int64_t)(h_first / HB) * p.b_gs + c);
+    }
+    *reinterpret_cast<bf16x8*>(sC + t * LDB + c) = cv;
+    if (b_once) *reinterpret_cast<bf16x8*>(sB + t * LDB + c) = bv;
   }
-  __syncthreads();   // sHD, F_DD cleared
 
-  // ---- staging ----------------------------------------------------------------
-  // x, g = dy silu(z), dy and z; the thread's dD partials (its 8 features)
+  const auto fetch = [&](int h, HeadIn<P, N>& q) {
+    const int hx = h / HXS, g = h / HB;
+#pragma unroll
+    for (int i = 0; i < VX; ++i) {
+      const int e = (i * NTHR + tid) * 8, t = e / P, c = e % P;
+      q.x[i] = q.dy[i] = q.z[i] = bf16x8{};
+      if (t < nval) {
+        q.x[i] = *reinterpret_cast<const bf16x8*>(p.x + (int64_t)(tok0 + t) * p.x_ts + (int64_t)hx * p.x_hs + c);
+        q.dy[i] = *reinterpret_cast<const bf16x8*>(p.dy + (int64_t)(tok0 + t) * p.dy_ts + (int64_t)h * p.dy_hs + c);
+        if (p.z) q.z[i] = *reinterpret_cast<const bf16x8*>(p.z + (int64_t)(tok0 + t) * p.z_ts + (int64_t)h * p.z_hs + c);
+      }
+    }
+    const bf16* s0 = p.S0 + ((int64_t)r * H + h) * P * N;
+    const bf16* ds = p.dS1 + ((int64_t)r * H + h) * P * N;
+#pragma unroll
+    for (int i = 0; i < VS; ++i) {
+      const int e = (i * NTHR + tid) * 8;
+      q.s0[i] = *reinterpret_cast<const bf16x8*>(s0 + e);
+      q.ds[i] = *reinterpret_cast<const bf16x8*>(ds + e);
+    }
+    if (!b_once) {
+#pragma unroll
+      for (int i = 0; i < VB; ++i) {
+        const int e = (i * NTHR + tid) * 8, t = e / N, c = e % N;
+        q.b[i] = bf16x8{};
+        if (t < nval)
+          q.b[i] = *reinterpret_cast<const bf16x8*>(p.B + (int64_t)(tok0 + t) * p.b_ts + (int64_t)g * p.b_gs + c);
+      }
+    }
+    q.dt = (wave == 0 && lane < nval)
+               ? load_any(p.dt, (int64_t)(tok0 + lane) * p.dt_ts + (int64_t)h * p.dt_hs, p.dt_dt) : 0.f;
+    q.d = (p.D && tid < P) ? p.D[(int64_t)h * P + tid] : 0.f;
+  };
+
+  HeadIn<P, N> in;
+  fetch(h_first, in);
+  f32x4 dCacc[NT], dBacc[NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) { dCacc[j] = f32x4{0.f, 0.f, 0.f, 0.f}; dBacc[j] = dCacc[j]; }
+
+  for (int ih = 0; ih < HC; ++ih) {
+  const int h = h_first + ih, hx = h / HXS, g = h / HB;
+  const float A_h = p.A[h];
+
+  // ---- staging from registers: x, g = dy silu(z), dy and z with the dD partials;
+  // S0 and dS1 with <dS1, S0>; B when per head; the token scalars and D ----------
   {
     float dd[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < L * P / 8 / NTHR; ++i) {
+    for (int i = 0; i < VX; ++i) {
       const int e = (i * NTHR + tid) * 8, t = e / P, c = e % P;
-      bf16x8 xv = {}, dv = {}, zv = {}, gv = {};
-      if (t < nval) {
-        xv = *reinterpret_cast<const bf16x8*>(p.x + (int64_t)(tok0 + t) * p.x_ts + (int64_t)hx * p.x_hs + c);
-        dv = *reinterpret_cast<const bf16x8*>(p.dy + (int64_t)(tok0 + t) * p.dy_ts + (int64_t)h * p.dy_hs + c);
-        if (p.z) zv = *reinterpret_cast<const bf16x8*>(p.z + (int64_t)(tok0 + t) * p.z_ts + (int64_t)h * p.z_hs + c);
-      }
+      bf16x8 gv;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        float gj = (float)dv[j];
-        if (p.z) gj *= silu((float)zv[j]);
+        float gj = (float)in.dy[i][j];
+        if (p.z) gj *= silu((float)in.z[i][j]);
         gv[j] = (bf16)gj;
-        dd[j] += gj * (float)xv[j];
+        dd[j] += gj * (float)in.x[i][j];
       }
-      *reinterpret_cast<bf16x8*>(sX + t * LDX + c) = xv;
+      *reinterpret_cast<bf16x8*>(sX + t * LDX + c) = in.x[i];
       *reinterpret_cast<bf16x8*>(sG + t * LDX + c) = gv;
       if (p.z) {
-        *reinterpret_cast<bf16x8*>(sDY + t * LDX + c) = dv;
-        *reinterpret_cast<bf16x8*>(sZ + t * LDX + c) = zv;
+        *reinterpret_cast<bf16x8*>(sDY + t * LDX + c) = in.dy[i];
+        *reinterpret_cast<bf16x8*>(sZ + t * LDX + c) = in.z[i];
       }
     }
     if (p.dD) {
@@ -385,40 +451,43 @@ __global__ __launch_bounds__(NTHR, 1) void ssd_bwd_chunk_kernel(Params p) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) atomicAdd(&F(F_DD, c + j), dd[j]);
     }
-  }
-  // B (group g) and C (group gc)
-#pragma unroll
-  for (int i = 0; i < L * N / 8 / NTHR; ++i) {
-    const int e = (i * NTHR + tid) * 8, t = e / N, c = e % N;
-    bf16x8 bv = {}, cv = {};
-    if (t < nval) {
-      bv = *reinterpret_cast<const bf16x8*>(p.B + (int64_t)(tok0 + t) * p.b_ts + (int64_t)g * p.b_gs + c);
-      cv = *reinterpret_cast<const bf16x8*>(p.C + (int64_t)(tok0 + t) * p.c_ts + (int64_t)gc * p.c_gs + c);
-    }
-    *reinterpret_cast<bf16x8*>(sB + t * LDB + c) = bv;
-    *reinterpret_cast<bf16x8*>(sC + t * LDB + c) = cv;
-  }
-  // the chunk's start state S0 and end-state gradient dS1 (bf16, from the scans),
-  // with <dS1, S0>
-  {
-    const bf16* s0 = p.S0 + ((int64_t)r * H + h) * P * N;
-    const bf16* ds = p.dS1 + ((int64_t)r * H + h) * P * N;
     float hd = 0.f;
 #pragma unroll
-    for (int i = 0; i < P * N / 8 / NTHR; ++i) {
+    for (int i = 0; i < VS; ++i) {
       const int e = (i * NTHR + tid) * 8, pr = e / N, c = e % N;
-      const bf16x8 sv = *reinterpret_cast<const bf16x8*>(s0 + e);
-      const bf16x8 dv = *reinterpret_cast<const bf16x8*>(ds + e);
-      *reinterpret_cast<bf16x8*>(sS + pr * LDB + c) = sv;
-      *reinterpret_cast<bf16x8*>(sDS + pr * LDB + c) = dv;
+      *reinterpret_cast<bf16x8*>(sS + pr * LDB + c) = in.s0[i];
+      *reinterpret_cast<bf16x8*>(sDS + pr * LDB + c) = in.ds[i];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) hd += (float)sv[j] * (float)dv[j];
+      for (int j = 0; j < 8; ++j) hd += (float)in.s0[i][j] * (float)in.ds[i][j];
     }
     hd = wave_sum(hd);
     if (lane == 0) atomicAdd(sHD, hd);
+    if (!b_once) {
+#pragma unroll
+      for (int i = 0; i < VB; ++i) {
+        const int e = (i * NTHR + tid) * 8, t = e / N, c = e % N;
+        *reinterpret_cast<bf16x8*>(sB + t * LDB + c) = in.b[i];
+      }
+    }
+    if (tid < P) F(F_DV, tid) = in.d;
+    if (wave == 0) {
+      const Tok tk = token_scalars_raw(p, h, in.dt, nval, lane);
+      const float aend = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, tk.acs), 63));
+      F(F_DT, lane) = tk.dtv;
+      F(F_ACS, lane) = tk.acs;
+      F(F_EA, lane) = fast_exp(tk.acs);
+      F(F_E, lane) = fast_exp(aend - tk.acs);
+      F(F_FAC, lane) = tk.fac;
+    }
   }
   __syncthreads();
-  if (p.dD && tid < P) unsafeAtomicAdd(p.dD + (int64_t)h * P + tid, F(F_DD, tid));
+  // the next head's inputs load during this head's products (no other vector load
+  // is issued until they are used)
+  if (ih + 1 < HC) fetch(h + 1, in);
+  if (p.dD && tid < P) {
+    unsafeAtomicAdd(p.dD + (int64_t)h * P + tid, F(F_DD, tid));
+    F(F_DD, tid) = 0.f;   // the next head's staging adds after the closing barrier
+  }
 
   // ---- step A: CB and Q (rows t of wave's block, all s), M dt' and W to LDS ----
   {
@@ -503,7 +572,7 @@ __global__ __launch_bounds__(NTHR, 1) void ssd_bwd_chunk_kernel(Params p) {
         das[v] += (float)sG[t * LDX + pc] * y_s;
         if (p.z && t < nval) {
           float yp = yi[i][v] + y_s;
-          if (p.D) yp += p.D[(int64_t)h * P + pc] * (float)sX[t * LDX + pc];
+          if (p.D) yp += F(F_DV, pc) * (float)sX[t * LDX + pc];
           const float zf = (float)sZ[t * LDX + pc];
           const float sg = 1.f / (1.f + fast_exp(-zf));
           const float dsilu = sg * (1.f + zf * (1.f - sg));
@@ -544,7 +613,7 @@ __global__ __launch_bounds__(NTHR, 1) void ssd_bwd_chunk_kernel(Params p) {
         dds[v] += (float)sX[s * LDX + pc] * dhb[i][v];
         if (s < nval) {
           float d = dxi[i][v] + e * dt_s * dhb[i][v];
-          if (p.D) d += p.D[(int64_t)h * P + pc] * (float)sG[s * LDX + pc];
+          if (p.D) d += F(F_DV, pc) * (float)sG[s * LDX + pc];
           float* dst = p.dx + (int64_t)(tok0 + s) * p.HX * P + (int64_t)hx * P + pc;
           if (p.x_shared) unsafeAtomicAdd(dst, d);
           else *dst = d;
@@ -555,7 +624,7 @@ __global__ __launch_bounds__(NTHR, 1) void ssd_bwd_chunk_kernel(Params p) {
     }
   }
 
-  // ---- step B3: dC = e^{A_t} g S0 + W B ------------------------------------------
+  // ---- step B3: dC += e^{A_t} g S0 + W B (summed over the workgroup's heads) -------
   {
     f32x4 acc[NT];
 #pragma unroll
@@ -570,28 +639,18 @@ __global__ __launch_bounds__(NTHR, 1) void ssd_bwd_chunk_kernel(Params p) {
     for (int v = 0; v < 4; ++v) {
       const float ea = F(F_EA, 16 * wave + 4 * q4 + v);
 #pragma unroll
-      for (int j = 0; j < NT; ++j) acc[j][v] *= ea;
+      for (int j = 0; j < NT; ++j) dCacc[j][v] += acc[j][v] * ea;
     }
 #pragma unroll
     for (int k0 = 0; k0 < L; k0 += 32) {
       const bf16x8 a = frag(sW, LDM, 16 * wave, k0, lane);
 #pragma unroll
-      for (int j = 0; j < NT; ++j) acc[j] = mfma16(a, frag_t(sB, LDB, k0, 16 * j, lane), acc[j]);
-    }
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int t = 16 * wave + 4 * q4 + v;
-      if (t >= nval) continue;
-      float* row = p.dC + (int64_t)(tok0 + t) * p.GC * N + (int64_t)gc * N;
-#pragma unroll
-      for (int j = 0; j < NT; ++j) {
-        if (p.c_shared) unsafeAtomicAdd(row + 16 * j + l16, acc[j][v]);
-        else row[16 * j + l16] = acc[j][v];
-      }
+      for (int j = 0; j < NT; ++j) dCacc[j] = mfma16(a, frag_t(sB, LDB, k0, 16 * j, lane), dCacc[j]);
     }
   }
 
-  // ---- step B4: dB = e dt' x dS1 + W^T C -------------------------------------------
+  // ---- step B4: dB = e dt' x dS1 + W^T C (summed over the heads when B is staged
+  // once; otherwise this head's, stored or added) ------------------------------------
   {
     f32x4 acc[NT];
 #pragma unroll
@@ -602,28 +661,34 @@ __global__ __launch_bounds__(NTHR, 1) void ssd_bwd_chunk_kernel(Params p) {
 #pragma unroll
       for (int j = 0; j < NT; ++j) acc[j] = mfma16(a, frag_t(sDS, LDB, k0, 16 * j, lane), acc[j]);
     }
+    if (!b_once) {
+#pragma unroll
+      for (int j = 0; j < NT; ++j) dBacc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      const int s = 16 * wave + 4 * q4 + v;
-      const float f = F(F_E, s) * F(F_DT, s);
+      const int s_ = 16 * wave + 4 * q4 + v;
+      const float f = F(F_E, s_) * F(F_DT, s_);
 #pragma unroll
-      for (int j = 0; j < NT; ++j) acc[j][v] *= f;
+      for (int j = 0; j < NT; ++j) dBacc[j][v] += acc[j][v] * f;
     }
 #pragma unroll
     for (int k0 = 0; k0 < L; k0 += 32) {
       const bf16x8 a = frag_t(sW, LDM, k0, 16 * wave, lane);
 #pragma unroll
-      for (int j = 0; j < NT; ++j) acc[j] = mfma16(a, frag_t(sC, LDB, k0, 16 * j, lane), acc[j]);
+      for (int j = 0; j < NT; ++j) dBacc[j] = mfma16(a, frag_t(sC, LDB, k0, 16 * j, lane), dBacc[j]);
     }
+    if (!b_once) {
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int s = 16 * wave + 4 * q4 + v;
-      if (s >= nval) continue;
-      float* row = p.dB + (int64_t)(tok0 + s) * p.G * N + (int64_t)g * N;
+      for (int v = 0; v < 4; ++v) {
+        const int s_ = 16 * wave + 4 * q4 + v;
+        if (s_ >= nval) continue;
+        float* row = p.dB + (int64_t)(tok0 + s_) * p.G * N + (int64_t)g * N;
 #pragma unroll
-      for (int j = 0; j < NT; ++j) {
-        if (p.b_shared) unsafeAtomicAdd(row + 16 * j + l16, acc[j][v]);
-        else row[16 * j + l16] = acc[j][v];
+        for (int j = 0; j < NT; ++j) {
+          if (p.b_shared) unsafeAtomicAdd(row + 16 * j + l16, dBacc[j][v]);
+          else row[16 * j + l16] = dBacc[j][v];
+        }
       }
     }
   }
@@ -656,18 +721,34 @@ __global__ __launch_bounds__(NTHR, 1) void ssd_bwd_chunk_kernel(Params p) {
     if (lane == 0) {
       unsafeAtomicAdd(p.dA + h, sa);
       if (p.dbias) unsafeAtomicAdd(p.dbias + h, sb);
+      sHD[0] = 0.f;   // lane 63 read it above; the next head adds after the barrier
+    }
+  }
+  __syncthreads();   // LDS free for the next head
+  }   // heads
+
+  // dC of the C group (and dB of the B group staged once), summed over the heads
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int t = 16 * wave + 4 * q4 + v;
+    if (t >= nval) continue;
+    float* rc = p.dC + (int64_t)(tok0 + t) * GC * N + (int64_t)gc * N;
+    float* rb = p.dB + (int64_t)(tok0 + t) * p.G * N + (int64_t)gc * N;
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      rc[16 * j + l16] = dCacc[j][v];
+      if (b_once) rb[16 * j + l16] = dBacc[j][v];
     }
   }
 }
 
 template <int P, int N>
 void launch(const Params& p, hipStream_t s) {
-  const dim3 grid(p.nrows * p.H);
-  hipLaunchKernelGGL((ssd_bwd_local_kernel<P, N>), grid, dim3(NTHR), 0, s, p);
+  hipLaunchKernelGGL((ssd_bwd_local_kernel<P, N>), dim3(p.nrows * p.H), dim3(NTHR), 0, s, p);
   hipLaunchKernelGGL(ssd_bwd_scan_kernel, dim3(p.nseq * p.H, (P * N + 1023) / 1024), dim3(256), 0,
                      s, p, P * N);
   constexpr int smem = Lay<P, N>::BYTES;
-  hipLaunchKernelGGL((ssd_bwd_chunk_kernel<P, N>), grid, dim3(NTHR), smem, s, p);
+  hipLaunchKernelGGL((ssd_bwd_chunk_kernel<P, N>), dim3(p.nrows * p.GC), dim3(NTHR), smem, s, p);
 }
 
 }  // namespace ssdb
@@ -732,7 +813,7 @@ extern "C" int hmx_ssd_chunk_bwd(
   p.edec = reinterpret_cast<float*>(ws + st * 8);
   p.dx = dx; p.x_shared = HX < H;
   p.dB = dB; p.b_shared = G < H;
-  p.dC = dC; p.c_shared = GC < H;
+  p.dC = dC;
   p.dz = static_cast<bf16*>(dz); p.ddt = ddt; p.dA = dA; p.dD = dD; p.dbias = ddt_bias;
   p.dh0 = dh0;
   p.H = H; p.HX = HX; p.G = G; p.GC = GC; p.softplus = dt_softplus;

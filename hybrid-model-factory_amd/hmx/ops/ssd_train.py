@@ -60,8 +60,8 @@ def ssd_chunk_scan_bwd(x, dt, A, B, C, D, z, dt_bias, dt_softplus, dt_limit, bou
     full = sum(e - a for a, e in bounds) == T
     alloc = lambda shared: torch.empty if (full and not shared) else torch.zeros
     dx = alloc(HX < H)(T, HX, P, **f32)
-    dB = alloc(G < H)(T, G, N, **f32)
-    dC = alloc(GC < H)(T, GC, N, **f32)
+    dB = alloc(G < H and G != GC)(T, G, N, **f32)
+    dC = alloc(False)(T, GC, N, **f32)
     dz = None if z is None else alloc(False)(T, H, P, dtype=torch.bfloat16, device=dev)
     ddt = alloc(False)(T, H, **f32)
     dA = torch.zeros(H, **f32)

@@ -579,9 +579,9 @@ size_t hmx_ssd_chunk_workspace_bytes(int32_t nseg_total, int32_t nseq, int32_t H
  *  C [tokens, GC, N], z and dy [tokens, H, P], dt [tokens, H] f32/bf16/f16, fp32 A,
  *  D [H, P], dt_bias).  h0: fp32 [nseq, H, P, N] start states or NULL (zero);
  *  d_final: fp32 [nseq, H, P, N] gradient of the end states, or NULL.
- *  Outputs, contiguous: dx fp32 [tokens, HX, P], dB fp32 [tokens, G, N], dC fp32
- *  [tokens, GC, N] (each zero-filled by the caller when shared by several heads,
- *  i.e. HX, G or GC < H: they accumulate); dz bf16 [tokens, H, P] (when z is
+ *  Outputs, contiguous: dx fp32 [tokens, HX, P] (zero-filled by the caller when
+ *  HX < H: it accumulates), dB fp32 [tokens, G, N] (zero-filled when G < H and
+ *  G != GC), dC fp32 [tokens, GC, N]; dz bf16 [tokens, H, P] (when z is
  *  given); ddt fp32 [tokens, H] (gradient of the raw dt); dA fp32 [H], dD fp32
  *  [H, P] (or NULL), ddt_bias fp32 [H] (or NULL), all zero-filled by the caller
  *  (they accumulate); dh0 fp32 [nseq, H, P, N] or NULL.  P = 64, N in {64, 128}.

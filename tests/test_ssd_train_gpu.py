@@ -10,7 +10,11 @@ clamp), A, B, C (groups shared by several heads: atomics), D per head and per
 chunks, sequences shorter than one chunk.  Tolerance: the backward's products take
 bf16 operands (as mamba_ssm's do) with fp32 accumulation; each gradient must match
 to 2% of its norm with cosine above 1 - 1e-4 (measured: 0.1-0.9%, cosine above
-1 - 2e-5), far below what a dropped or mis-signed term gives.
+1 - 2e-5), far below what a dropped or mis-signed term gives.  dA is a per-head sum
+over every token of dt'_t da_t whose terms can cancel (23x in the B-groups-wider
+case), so its error is measured against the norm of the per-head sums of |dt'_t
+da_t| (from the fp64 chunked backward of oracle/ssd_train.py) and must stay under
+1% of it (measured up to 0.4%).
 """
 import math
 
@@ -19,6 +23,7 @@ import torch
 
 import hmx
 from oracle import ssd as ref
+from oracle import ssd_train as oref
 
 pytestmark = pytest.mark.gpu
 
@@ -61,10 +66,39 @@ def _grads(inp, wy, wf, kw, dev, dtype):
     return {k: v.grad for k, v in leaves.items() if v is not None}
 
 
-def _check(g, g_ref, name, tol=2e-2):
+def _dA_scale(inp, wy, wf, kw):
+    """Per head, sum over every chunk of every sequence of |dt'_t da_t| (the fp64
+    chunked backward): dA is the sum of these terms, which can cancel (23x in one
+    case here), so dA's rounding error is measured against this scale."""
+    b, l, H, _ = inp["x"].shape
+    total = torch.zeros(H, dtype=torch.float64)
+    seq_idx = kw.get("seq_idx")
+    for row in range(b):
+        runs = [(0, l)] if seq_idx is None else ref._runs(seq_idx[row])
+        for i, (s0, s1) in enumerate(runs):
+            h0 = inp["initial_states"]
+            h0 = h0[row] if (h0 is not None and i == 0 and s0 == 0) else None
+            fin = wf[row] if (kw.get("return_final_states") and s1 == l) else None
+            sl = slice(s0, s1)
+            o = oref.chunk_grads(inp["x"][row, sl], inp["dt"][row, sl], inp["A"], inp["B"][row, sl],
+                                 inp["C"][row, sl], D=inp["D"],
+                                 z=None if inp["z"] is None else inp["z"][row, sl],
+                                 dt_bias=inp["dt_bias"], h0=h0, dy=wy[row, sl], d_final=fin,
+                                 dt_softplus=kw.get("dt_softplus", False),
+                                 dt_limit=kw.get("dt_limit", (0.0, float("inf"))))
+            total += o["A_abs"]
+    return total
+
+
+def _check(g, g_ref, name, tol=2e-2, scale=None):
     a = g.detach().double().cpu().flatten()
     b = g_ref.detach().double().cpu().flatten()
     assert torch.isfinite(a).all(), f"{name}: non-finite gradient"
+    if scale is not None:   # a sum of cancelling terms: error against the terms' scale
+        err = (a - b).norm().item() / scale.norm().item()
+        print(f"  {name}: error / ||sum|dt' da|||  {err:.2e}")
+        assert err <= tol * 0.5, f"{name}: error {err:.3e} of the terms' scale"
+        return
     nb = b.norm().item()
     err = (a - b).norm().item() / max(nb, 1e-30)
     cos = (a @ b).item() / max(a.norm().item() * nb, 1e-30)
@@ -101,8 +135,9 @@ def test_scan_backward_matches_oracle_autograd(dev, case):
     torch.cuda.synchronize()
     g_ref = _grads(inp, wy, wf, kw, None, torch.float64)
     assert set(g) == set(g_ref)
+    sA = _dA_scale(inp, wy, wf, kw)
     for k in g_ref:
-        _check(g[k], g_ref[k], f"{case} d{k}")
+        _check(g[k], g_ref[k], f"{case} d{k}", scale=sA if k == "A" else None)
 
 
 def test_backward_needs_headdim_64(dev):
@@ -114,17 +149,20 @@ def test_backward_needs_headdim_64(dev):
         y.float().sum().backward()
 
 
-def test_backward_training_layer_layout(dev):
+@pytest.mark.parametrize("gb,gc", [(4, 2), (1, 2)])
+def test_backward_training_layer_layout(dev, gb, gc):
     """The training layer's operands (mamba2.py:541-556): x and B repeated to the H
-    heads, C with its own ngroups, D per head, no z."""
-    inp, wy, wf = _inputs(1, 200, 4, 4, 64, 128, 900, False, False)
+    heads, C with its own ngroups, D per head, no z (gb = 4); and B groups wider than
+    C's (gb = 1: B's gradient accumulates across workgroups)."""
+    inp, wy, wf = _inputs(1, 200, 4, gb, 64, 128, 900 + gb, False, False)
     g0 = torch.Generator().manual_seed(901)
-    inp["C"] = torch.randn(1, 200, 2, 128, generator=g0).bfloat16()
+    inp["C"] = torch.randn(1, 200, gc, 128, generator=g0).bfloat16()
     inp["initial_states"] = None
     kw = dict(dt_softplus=True)
     g = _grads(inp, wy, wf, kw, dev, None)
     torch.cuda.synchronize()
     g_ref = _grads(inp, wy, wf, kw, None, torch.float64)
     assert g["C"].shape == inp["C"].shape
+    sA = _dA_scale(inp, wy, wf, kw)
     for k in g_ref:
-        _check(g[k], g_ref[k], f"train_layout d{k}")
+        _check(g[k], g_ref[k], f"train_layout d{k}", scale=sA if k == "A" else None)
