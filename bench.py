@@ -699,8 +699,35 @@ def bench_ssd_train(dev, steps, warmup):
     ms_fb = _timed(fwd_bwd, steps, warmup)
     L = 64   # the backward's chunk: per (chunk, head) 3 L^2 N + 3 L^2 P + 5 L P N MACs
     flops_bwd = 2.0 * (b * T // L) * H * (3 * L * L * N + 3 * L * L * P + 5 * L * P * N)
+    del leaves, d, dy
+
+    # the hybrid layer's training shape (mamba2.py:541-580 with headdim = d_state =
+    # 128 as mamba2.py:146 sets it): 8 x 4096 tokens, 32 heads, x and B repeated to
+    # the heads, C in 32 groups, D per head, no z (the layer's RMSNorm path)
+    b2, T2, H2, P2 = 8, 4096, 32, 128
+    r = lambda *sh: torch.randn(*sh, generator=g, device=dev)
+    x2, B2, C2, dy2 = (r(b2, T2, H2, P2).bfloat16() for _ in range(4))
+    dt2 = r(b2, T2, H2) * 0.5 - 2.0
+    A2 = -torch.rand(H2, generator=g, device=dev) * 15.0 - 1.0
+    D2, bias2 = torch.ones(H2, device=dev), torch.full((H2,), -4.0, device=dev)
+    leaves2 = [t.clone().requires_grad_(True) for t in (x2, dt2, A2, B2, C2, D2, bias2)]
+
+    def fwd_bwd_hybrid():
+        x, dt, A, B, C, D, bias = leaves2
+        y = hmx.mamba_chunk_scan_combined(x, dt, A, B, C, 256, D=D, dt_bias=bias,
+                                          dt_softplus=True)
+        torch.autograd.grad(y, leaves2, dy2)
+
+    def fwd_hybrid():
+        with torch.no_grad():
+            hmx.mamba_chunk_scan_combined(x2, dt2, A2, B2, C2, 256, D=D2, dt_bias=bias2,
+                                          dt_softplus=True)
+
+    ms_f2 = _timed(fwd_hybrid, steps, warmup)
+    ms_fb2 = _timed(fwd_bwd_hybrid, steps, warmup)
     return dict(ms_fwd=ms_f, ms_fwd_bwd=ms_fb, tokens=b * T, flops_bwd=flops_bwd,
-                tokens_per_s=b * T / (ms_fb * 1e-3))
+                tokens_per_s=b * T / (ms_fb * 1e-3), ms_fwd_hybrid=ms_f2,
+                ms_fwd_bwd_hybrid=ms_fb2)
 
 
 def bench_ssd(dev, steps, warmup, b=2, T=16384, H=64, P=64, N=128, G=8):
@@ -1188,6 +1215,12 @@ def main():
             "backward_TFLOPs": round(r["flops_bwd"] / ((r["ms_fwd_bwd"] - r["ms_fwd"]) * 1e-3)
                                      / 1e12, 1),
             "algorithmic_flops_bwd": r["flops_bwd"],
+            "hybrid_layer_shape": {
+                "config": {"B": 8, "T": 4096, "H": 32, "P": 128, "N": 128, "G": 32,
+                           "note": "x and B repeated to the heads, headdim = d_state"},
+                "ms_fwd": round(r["ms_fwd_hybrid"], 4),
+                "ms_fwd_bwd": round(r["ms_fwd_bwd_hybrid"], 4),
+                "tokens_per_s": round(8 * 4096 / (r["ms_fwd_bwd_hybrid"] * 1e-3), 1)},
         }
     if "gka_train" in out:
         r = out["gka_train"]

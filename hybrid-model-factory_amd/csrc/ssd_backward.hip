@@ -133,13 +133,18 @@ __device__ __forceinline__ Tok token_scalars(const Params& p, int h, int tok0, i
 // edec[r][h] = e^{A_L}
 // ---------------------------------------------------------------------------
 template <int P, int N>
+constexpr int local_lds_bytes() { return 2 * L * (P + 8) * 2 + 2 * L * (N + 8) * 2 + 2 * L * 4; }
+
+template <int P, int N>
 __global__ __launch_bounds__(NTHR) void ssd_bwd_local_kernel(Params p) {
   constexpr int LDX = P + 8, LDB = N + 8;
-  __shared__ __align__(16) bf16 sG[L * LDX];    // e^{A_t} g_t
-  __shared__ __align__(16) bf16 sXW[L * LDX];   // dt'_s e^{A_L - A_s} x_s
-  __shared__ __align__(16) bf16 sC[L * LDB];
-  __shared__ __align__(16) bf16 sB[L * LDB];
-  __shared__ float sEA[L], sWT[L];
+  extern __shared__ __align__(16) unsigned char lsm[];
+  bf16* sG = reinterpret_cast<bf16*>(lsm);                     // e^{A_t} g_t       [L][LDX]
+  bf16* sXW = sG + L * LDX;                                    // dt'_s e^{A_L-A_s} x_s
+  bf16* sC = sXW + L * LDX;                                    // [L][LDB]
+  bf16* sB = sC + L * LDB;
+  float* sEA = reinterpret_cast<float*>(sB + L * LDB);
+  float* sWT = sEA + L;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int H = p.H;
@@ -299,23 +304,25 @@ struct Lay {
   static constexpr int LDX = P + 8, LDB = N + 8, LDM = L + 8;
   static constexpr int OFF_X = 0;                          // x        [L][LDX]
   static constexpr int OFF_G = OFF_X + L * LDX * 2;        // g        [L][LDX]
+  // dy and z (for dz) fit only at P = 64; headdim 128 takes no z
+  static constexpr int ZW = P == 64 ? L * LDX * 2 : 0;
   static constexpr int OFF_DY = OFF_G + L * LDX * 2;       // dy       [L][LDX] (z only)
-  static constexpr int OFF_Z = OFF_DY + L * LDX * 2;       // z        [L][LDX] (z only)
-  static constexpr int OFF_B = OFF_Z + L * LDX * 2;        // B        [L][LDB]
+  static constexpr int OFF_Z = OFF_DY + ZW;                // z        [L][LDX] (z only)
+  static constexpr int OFF_B = OFF_Z + ZW;                 // B        [L][LDB]
   static constexpr int OFF_C = OFF_B + L * LDB * 2;        // C        [L][LDB]
   static constexpr int OFF_S = OFF_C + L * LDB * 2;        // S0       [P][LDB]
   static constexpr int OFF_DS = OFF_S + P * LDB * 2;       // dS1      [P][LDB]
   static constexpr int OFF_M = OFF_DS + P * LDB * 2;       // M dt'    [L][LDM]
   static constexpr int OFF_W = OFF_M + L * LDM * 2;        // W        [L][LDM]
   static constexpr int OFF_F = OFF_W + L * LDM * 2;        // fp32 scalars
-  static constexpr int NF = 18;                            // scalar arrays of L floats
+  static constexpr int FDD = 16, FDV = 16 + P / L;         // dD and D: P floats each
+  static constexpr int NF = 16 + 2 * (P / L);              // scalar arrays of L floats
   static constexpr int BYTES = OFF_F + NF * L * 4 + 64;
   static_assert(BYTES <= 160 * 1024, "LDS budget");
 };
 // scalar arrays
 enum { F_DT, F_ACS, F_EA, F_E, F_FAC, F_ROWR, F_DAS, F_DDS,
-       F_CMQ0, F_CR0 = F_CMQ0 + 4, F_DD = F_CR0 + 4, F_DV };   // F_DD, F_DV: P = 64 floats
-static_assert(F_DV + 1 == 18, "scalar arrays");
+       F_CMQ0, F_CR0 = F_CMQ0 + 4 };   // F_CR0 + 4 = 16 arrays, then dD and D (Lay)
 
 // One head's inputs for the chunk, loaded into registers while the head before it
 // is computed: x, dy, z rows (2 vectors per thread), S0 and dS1 (4 each), B rows
@@ -330,7 +337,10 @@ struct HeadIn {
 
 template <int P, int N>
 __global__ __launch_bounds__(NTHR, 1) void ssd_bwd_chunk_kernel(Params p) {
-  static_assert(P == 64, "headdim 64");
+  static_assert((P == 64 || P == 128) && (N == 64 || N == 128), "tile shape");
+  // headdim 64 loads the next head's inputs during the current head's products;
+  // at 128 they would not fit in registers beside the products' tiles
+  constexpr bool AHEAD = P == 64;
   using K = Lay<P, N>;
   constexpr int LDX = K::LDX, LDB = K::LDB, LDM = K::LDM, NT = N / 16;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -364,7 +374,7 @@ __global__ __launch_bounds__(NTHR, 1) void ssd_bwd_chunk_kernel(Params p) {
   constexpr int VX = L * P / 8 / NTHR, VS = P * N / 8 / NTHR, VB = L * N / 8 / NTHR;
 
   if (tid == 0) sHD[0] = 0.f;
-  if (tid < P) F(F_DD, tid) = 0.f;
+  if (tid < P) F(K::FDD, tid) = 0.f;
   // C (and B when shared by all the heads) once
 #pragma unroll
   for (int i = 0; i < VB; ++i) {
@@ -415,7 +425,7 @@ __global__ __launch_bounds__(NTHR, 1) void ssd_bwd_chunk_kernel(Params p) {
   };
 
   HeadIn<P, N> in;
-  fetch(h_first, in);
+  if constexpr (AHEAD) fetch(h_first, in);
   f32x4 dCacc[NT], dBacc[NT];
 #pragma unroll
   for (int j = 0; j < NT; ++j) { dCacc[j] = f32x4{0.f, 0.f, 0.f, 0.f}; dBacc[j] = dCacc[j]; }
@@ -423,6 +433,7 @@ __global__ __launch_bounds__(NTHR, 1) void ssd_bwd_chunk_kernel(Params p) {
   for (int ih = 0; ih < HC; ++ih) {
   const int h = h_first + ih, hx = h / HXS, g = h / HB;
   const float A_h = p.A[h];
+  if constexpr (!AHEAD) fetch(h, in);
 
   // ---- staging from registers: x, g = dy silu(z), dy and z with the dD partials;
   // S0 and dS1 with <dS1, S0>; B when per head; the token scalars and D ----------
@@ -441,15 +452,17 @@ __global__ __launch_bounds__(NTHR, 1) void ssd_bwd_chunk_kernel(Params p) {
       }
       *reinterpret_cast<bf16x8*>(sX + t * LDX + c) = in.x[i];
       *reinterpret_cast<bf16x8*>(sG + t * LDX + c) = gv;
-      if (p.z) {
-        *reinterpret_cast<bf16x8*>(sDY + t * LDX + c) = in.dy[i];
-        *reinterpret_cast<bf16x8*>(sZ + t * LDX + c) = in.z[i];
+      if constexpr (P == 64) {
+        if (p.z) {
+          *reinterpret_cast<bf16x8*>(sDY + t * LDX + c) = in.dy[i];
+          *reinterpret_cast<bf16x8*>(sZ + t * LDX + c) = in.z[i];
+        }
       }
     }
     if (p.dD) {
       const int c = (tid * 8) % P;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) atomicAdd(&F(F_DD, c + j), dd[j]);
+      for (int j = 0; j < 8; ++j) atomicAdd(&F(K::FDD, c + j), dd[j]);
     }
     float hd = 0.f;
 #pragma unroll
@@ -469,7 +482,7 @@ __global__ __launch_bounds__(NTHR, 1) void ssd_bwd_chunk_kernel(Params p) {
         *reinterpret_cast<bf16x8*>(sB + t * LDB + c) = in.b[i];
       }
     }
-    if (tid < P) F(F_DV, tid) = in.d;
+    if (tid < P) F(K::FDV, tid) = in.d;
     if (wave == 0) {
       const Tok tk = token_scalars_raw(p, h, in.dt, nval, lane);
       const float aend = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, tk.acs), 63));
@@ -483,10 +496,12 @@ __global__ __launch_bounds__(NTHR, 1) void ssd_bwd_chunk_kernel(Params p) {
   __syncthreads();
   // the next head's inputs load during this head's products (no other vector load
   // is issued until they are used)
-  if (ih + 1 < HC) fetch(h + 1, in);
+  if constexpr (AHEAD) {
+    if (ih + 1 < HC) fetch(h + 1, in);
+  }
   if (p.dD && tid < P) {
-    unsafeAtomicAdd(p.dD + (int64_t)h * P + tid, F(F_DD, tid));
-    F(F_DD, tid) = 0.f;   // the next head's staging adds after the closing barrier
+    unsafeAtomicAdd(p.dD + (int64_t)h * P + tid, F(K::FDD, tid));
+    F(K::FDD, tid) = 0.f;   // the next head's staging adds after the closing barrier
   }
 
   // ---- step A: CB and Q (rows t of wave's block, all s), M dt' and W to LDS ----
@@ -548,11 +563,13 @@ __global__ __launch_bounds__(NTHR, 1) void ssd_bwd_chunk_kernel(Params p) {
     f32x4 yi[P / 16], ys[P / 16];
 #pragma unroll
     for (int i = 0; i < P / 16; ++i) { yi[i] = f32x4{0.f, 0.f, 0.f, 0.f}; ys[i] = yi[i]; }
+    if (P == 64 && p.z) {   // y' only feeds dz
 #pragma unroll
-    for (int k0 = 0; k0 < L; k0 += 32) {
-      const bf16x8 a = frag(sM, LDM, 16 * wave, k0, lane);
+      for (int k0 = 0; k0 < L; k0 += 32) {
+        const bf16x8 a = frag(sM, LDM, 16 * wave, k0, lane);
 #pragma unroll
-      for (int i = 0; i < P / 16; ++i) yi[i] = mfma16(a, frag_t(sX, LDX, k0, 16 * i, lane), yi[i]);
+        for (int i = 0; i < P / 16; ++i) yi[i] = mfma16(a, frag_t(sX, LDX, k0, 16 * i, lane), yi[i]);
+      }
     }
 #pragma unroll
     for (int k0 = 0; k0 < N; k0 += 32) {
@@ -570,9 +587,9 @@ __global__ __launch_bounds__(NTHR, 1) void ssd_bwd_chunk_kernel(Params p) {
         const int pc = 16 * i + l16;
         const float y_s = ea * ys[i][v];
         das[v] += (float)sG[t * LDX + pc] * y_s;
-        if (p.z && t < nval) {
+        if (P == 64 && p.z && t < nval) {
           float yp = yi[i][v] + y_s;
-          if (p.D) yp += F(F_DV, pc) * (float)sX[t * LDX + pc];
+          if (p.D) yp += F(K::FDV, pc) * (float)sX[t * LDX + pc];
           const float zf = (float)sZ[t * LDX + pc];
           const float sg = 1.f / (1.f + fast_exp(-zf));
           const float dsilu = sg * (1.f + zf * (1.f - sg));
@@ -613,7 +630,7 @@ __global__ __launch_bounds__(NTHR, 1) void ssd_bwd_chunk_kernel(Params p) {
         dds[v] += (float)sX[s * LDX + pc] * dhb[i][v];
         if (s < nval) {
           float d = dxi[i][v] + e * dt_s * dhb[i][v];
-          if (p.D) d += F(F_DV, pc) * (float)sG[s * LDX + pc];
+          if (p.D) d += F(K::FDV, pc) * (float)sG[s * LDX + pc];
           float* dst = p.dx + (int64_t)(tok0 + s) * p.HX * P + (int64_t)hx * P + pc;
           if (p.x_shared) unsafeAtomicAdd(dst, d);
           else *dst = d;
@@ -744,10 +761,15 @@ __global__ __launch_bounds__(NTHR, 1) void ssd_bwd_chunk_kernel(Params p) {
 
 template <int P, int N>
 void launch(const Params& p, hipStream_t s) {
-  hipLaunchKernelGGL((ssd_bwd_local_kernel<P, N>), dim3(p.nrows * p.H), dim3(NTHR), 0, s, p);
+  constexpr int lsm = local_lds_bytes<P, N>();
+  constexpr int smem = Lay<P, N>::BYTES;
+  (void)hipFuncSetAttribute((const void*)ssd_bwd_local_kernel<P, N>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, lsm);
+  (void)hipFuncSetAttribute((const void*)ssd_bwd_chunk_kernel<P, N>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+  hipLaunchKernelGGL((ssd_bwd_local_kernel<P, N>), dim3(p.nrows * p.H), dim3(NTHR), lsm, s, p);
   hipLaunchKernelGGL(ssd_bwd_scan_kernel, dim3(p.nseq * p.H, (P * N + 1023) / 1024), dim3(256), 0,
                      s, p, P * N);
-  constexpr int smem = Lay<P, N>::BYTES;
   hipLaunchKernelGGL((ssd_bwd_chunk_kernel<P, N>), dim3(p.nrows * p.GC), dim3(NTHR), smem, s, p);
 }
 
@@ -774,8 +796,9 @@ extern "C" int hmx_ssd_chunk_bwd(
     float* dh0, void* workspace, size_t workspace_bytes, void* stream) {
   const char* fn = "hmx_ssd_chunk_bwd";
   HMX_REQUIRE(xbc_dtype == HMX_BF16, HMX_EUNSUPPORTED, "%s: x/B/C/z/dy must be bfloat16", fn);
-  HMX_REQUIRE(P == 64 && (N == 64 || N == 128), HMX_EUNSUPPORTED,
-              "%s: headdim 64 and d_state in {64,128} (got %d, %d)", fn, P, N);
+  HMX_REQUIRE((P == 64 || P == 128) && (N == 64 || N == 128), HMX_EUNSUPPORTED,
+              "%s: headdim and d_state in {64,128} (got %d, %d)", fn, P, N);
+  HMX_REQUIRE(P == 64 || !z, HMX_EUNSUPPORTED, "%s: the z gate needs headdim 64", fn);
   HMX_REQUIRE(H > 0 && HX > 0 && G > 0 && GC > 0 && H % HX == 0 && H % G == 0 && H % GC == 0,
               HMX_EINVAL, "%s: H=%d must be a multiple of HX=%d, G=%d and GC=%d", fn, H, HX, G, GC);
   HMX_REQUIRE(x && B && C && dt && A && dy && seg_table && seq_table && dx && dB && dC && ddt && dA &&
@@ -824,14 +847,9 @@ extern "C" int hmx_ssd_chunk_bwd(
                        p, P * N);
     return check_launch(fn);
   }
-  if (N == 128) {
-    (void)hipFuncSetAttribute((const void*)ssd_bwd_chunk_kernel<64, 128>,
-                        hipFuncAttributeMaxDynamicSharedMemorySize, Lay<64, 128>::BYTES);
-    launch<64, 128>(p, s);
-  } else {
-    (void)hipFuncSetAttribute((const void*)ssd_bwd_chunk_kernel<64, 64>,
-                        hipFuncAttributeMaxDynamicSharedMemorySize, Lay<64, 64>::BYTES);
-    launch<64, 64>(p, s);
-  }
+  if (P == 64 && N == 128) launch<64, 128>(p, s);
+  else if (P == 64) launch<64, 64>(p, s);
+  else if (N == 128) launch<128, 128>(p, s);
+  else launch<128, 64>(p, s);
   return check_launch(fn);
 }

@@ -41,9 +41,12 @@ def ssd_chunk_scan_bwd(x, dt, A, B, C, D, z, dt_bias, dt_softplus, dt_limit, bou
     H = dt.shape[1]
     G, N, GC = B.shape[1], B.shape[2], C.shape[1]
     dev = x.device
-    if P != 64 or N not in (64, 128):
-        raise NotImplementedError(f"hmx SSD backward: headdim 64 and d_state 64/128 "
+    if P not in (64, 128) or N not in (64, 128):
+        raise NotImplementedError(f"hmx SSD backward: headdim and d_state in 64/128 "
                                   f"(got {P}, {N})")
+    if P == 128 and z is not None:
+        raise NotImplementedError("hmx SSD backward: the z gate needs headdim 64 (the training "
+                                  "layer with its RMSNorm passes z = None)")
     rows, seqs = _chunk_table(bounds)
     nseq, nrows = len(bounds), len(rows)
     x, B, C = _prep3(x), _prep3(B), _prep3(C)

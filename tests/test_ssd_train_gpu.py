@@ -140,12 +140,29 @@ def test_scan_backward_matches_oracle_autograd(dev, case):
         _check(g[k], g_ref[k], f"{case} d{k}", scale=sA if k == "A" else None)
 
 
-def test_backward_needs_headdim_64(dev):
-    inp, _, _ = _inputs(1, 64, 2, 1, 128, 64, 1, False, False)
+@pytest.mark.parametrize("N", [128, 64])
+def test_backward_headdim_128(dev, N):
+    """headdim 128 (the hybrid layers' headdim = d_state, mamba2.py:146): C shared by
+    two heads, seq_idx restarts, initial and final states, D per head, no z."""
+    inp, wy, wf = _inputs(1, 230, 4, 2, 128, N, 950 + N, False, False)
+    kw = dict(dt_softplus=True, return_final_states=True,
+              seq_idx=torch.cat([torch.zeros(150, dtype=torch.int32),
+                                 torch.ones(80, dtype=torch.int32)])[None])
+    kw_dev = dict(kw, seq_idx=kw["seq_idx"].to(dev))
+    g = _grads(inp, wy, wf, kw_dev, dev, None)
+    torch.cuda.synchronize()
+    g_ref = _grads(inp, wy, wf, kw, None, torch.float64)
+    sA = _dA_scale(inp, wy, wf, kw)
+    for k in g_ref:
+        _check(g[k], g_ref[k], f"hdim128 N={N} d{k}", scale=sA if k == "A" else None)
+
+
+def test_backward_headdim_128_with_z_raises(dev):
+    inp, _, _ = _inputs(1, 64, 2, 1, 128, 64, 1, True, False)
     x = inp["x"].to(dev).requires_grad_(True)
     y = hmx.mamba_chunk_scan_combined(x, inp["dt"].to(dev), inp["A"].to(dev), inp["B"].to(dev),
-                                      inp["C"].to(dev), 256, dt_softplus=True)
-    with pytest.raises(NotImplementedError, match="headdim 64"):
+                                      inp["C"].to(dev), 256, z=inp["z"].to(dev), dt_softplus=True)
+    with pytest.raises(NotImplementedError, match="z gate needs headdim 64"):
         y.float().sum().backward()
 
 
