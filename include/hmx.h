@@ -584,7 +584,8 @@ size_t hmx_ssd_chunk_workspace_bytes(int32_t nseg_total, int32_t nseq, int32_t H
  *  G != GC), dC fp32 [tokens, GC, N]; dz bf16 [tokens, H, P] (when z is
  *  given); ddt fp32 [tokens, H] (gradient of the raw dt); dA fp32 [H], dD fp32
  *  [H, P] (or NULL), ddt_bias fp32 [H] (or NULL), all zero-filled by the caller
- *  (they accumulate); dh0 fp32 [nseq, H, P, N] or NULL.  P = 64, N in {64, 128}.
+ *  (they accumulate); dh0 fp32 [nseq, H, P, N] or NULL.  P, N in {64, 128}; z only
+ *  with P = 64.
  * workspace: hmx_ssd_chunk_bwd_workspace_bytes(nrows, H, P, N) bytes.
  * Replaces: the backward of mamba_chunk_scan_combined (mamba_ssm 2.3.0, which the
  *   training layer calls under autograd: training/src/hmf/model/hybrid_zoo/
