@@ -74,9 +74,10 @@ struct Params {
   bf16* S0;                                  // ws [nrows][H][P][N]: chunk start states
   bf16* dS1;                                 // ws [nrows][H][P][N]: end-state gradients
   // outputs (contiguous)
-  float* dx;   int x_shared;                 // [T][HX][P] fp32
-  float* dB;   int b_shared;                 // [T][G][N] fp32
-  float* dC;                                 // [T][GC][N] fp32
+  void* dx;    int x_shared;                 // [T][HX][P]
+  void* dB;    int b_shared;                 // [T][G][N]
+  void* dC;                                  // [T][GC][N]
+  int gbf16;                                 // dx, dB, dC stored in bf16 (else fp32)
   bf16* dz;                                  // [T][H][P] or null
   float* ddt;                                // [T][H]
   float* dA;                                 // [H] (accumulated)
@@ -102,6 +103,12 @@ __device__ __forceinline__ float scan64(float x, int lane) {
 }
 
 __device__ __forceinline__ float silu(float z) { return z / (1.f + fast_exp(-z)); }
+
+// a stored (not accumulated) gradient element, bf16 or fp32
+__device__ __forceinline__ void st_grad(void* base, int64_t i, float v, int bf) {
+  if (bf) static_cast<bf16*>(base)[i] = (bf16)v;
+  else static_cast<float*>(base)[i] = v;
+}
 
 // Per-token scalars of a chunk, lane t of one wave: dt' (0 past the chunk's
 // tokens), A_t, and the factor d dt'/d dt (clamp pass times the softplus slope).
@@ -631,9 +638,9 @@ __global__ __launch_bounds__(NTHR, 1) void ssd_bwd_chunk_kernel(Params p) {
         if (s < nval) {
           float d = dxi[i][v] + e * dt_s * dhb[i][v];
           if (p.D) d += F(K::FDV, pc) * (float)sG[s * LDX + pc];
-          float* dst = p.dx + (int64_t)(tok0 + s) * p.HX * P + (int64_t)hx * P + pc;
-          if (p.x_shared) unsafeAtomicAdd(dst, d);
-          else *dst = d;
+          const int64_t ix = (int64_t)(tok0 + s) * p.HX * P + (int64_t)hx * P + pc;
+          if (p.x_shared) unsafeAtomicAdd(static_cast<float*>(p.dx) + ix, d);
+          else st_grad(p.dx, ix, d, p.gbf16);
         }
       }
       const float rs = row16_sum(dds[v]);
@@ -700,11 +707,11 @@ __global__ __launch_bounds__(NTHR, 1) void ssd_bwd_chunk_kernel(Params p) {
       for (int v = 0; v < 4; ++v) {
         const int s_ = 16 * wave + 4 * q4 + v;
         if (s_ >= nval) continue;
-        float* row = p.dB + (int64_t)(tok0 + s_) * p.G * N + (int64_t)g * N;
+        const int64_t row = (int64_t)(tok0 + s_) * p.G * N + (int64_t)g * N;
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
-          if (p.b_shared) unsafeAtomicAdd(row + 16 * j + l16, dBacc[j][v]);
-          else row[16 * j + l16] = dBacc[j][v];
+          if (p.b_shared) unsafeAtomicAdd(static_cast<float*>(p.dB) + row + 16 * j + l16, dBacc[j][v]);
+          else st_grad(p.dB, row + 16 * j + l16, dBacc[j][v], p.gbf16);
         }
       }
     }
@@ -749,12 +756,12 @@ __global__ __launch_bounds__(NTHR, 1) void ssd_bwd_chunk_kernel(Params p) {
   for (int v = 0; v < 4; ++v) {
     const int t = 16 * wave + 4 * q4 + v;
     if (t >= nval) continue;
-    float* rc = p.dC + (int64_t)(tok0 + t) * GC * N + (int64_t)gc * N;
-    float* rb = p.dB + (int64_t)(tok0 + t) * p.G * N + (int64_t)gc * N;
+    const int64_t rc = (int64_t)(tok0 + t) * GC * N + (int64_t)gc * N;
+    const int64_t rb = (int64_t)(tok0 + t) * p.G * N + (int64_t)gc * N;
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
-      rc[16 * j + l16] = dCacc[j][v];
-      if (b_once) rb[16 * j + l16] = dBacc[j][v];
+      st_grad(p.dC, rc + 16 * j + l16, dCacc[j][v], p.gbf16);
+      if (b_once) st_grad(p.dB, rb + 16 * j + l16, dBacc[j][v], p.gbf16);
     }
   }
 }
@@ -791,14 +798,18 @@ extern "C" int hmx_ssd_chunk_bwd(
     const void* z, int64_t z_ts, int64_t z_hs, const void* dy, int64_t dy_ts, int64_t dy_hs,
     const float* h0, const float* d_final, const int32_t* seg_table,
     int32_t nrows, const int32_t* seq_table, int32_t nseq, int32_t H, int32_t HX, int32_t G,
-    int32_t GC, int32_t P, int32_t N, int32_t dt_softplus, float dt_min, float dt_max, float* dx,
-    float* dB, float* dC, void* dz, float* ddt, float* dA, float* dD, float* ddt_bias,
+    int32_t GC, int32_t P, int32_t N, int32_t dt_softplus, float dt_min, float dt_max, void* dx,
+    void* dB, void* dC, int32_t grad_dtype, void* dz, float* ddt, float* dA, float* dD, float* ddt_bias,
     float* dh0, void* workspace, size_t workspace_bytes, void* stream) {
   const char* fn = "hmx_ssd_chunk_bwd";
   HMX_REQUIRE(xbc_dtype == HMX_BF16, HMX_EUNSUPPORTED, "%s: x/B/C/z/dy must be bfloat16", fn);
   HMX_REQUIRE((P == 64 || P == 128) && (N == 64 || N == 128), HMX_EUNSUPPORTED,
               "%s: headdim and d_state in {64,128} (got %d, %d)", fn, P, N);
   HMX_REQUIRE(P == 64 || !z, HMX_EUNSUPPORTED, "%s: the z gate needs headdim 64", fn);
+  HMX_REQUIRE(grad_dtype == HMX_F32 ||
+                  (grad_dtype == HMX_BF16 && HX == H && (G == H || G == GC)),
+              HMX_EUNSUPPORTED,
+              "%s: dx / dB / dC in bf16 need unshared x and B (HX = H; G = H or G = GC)", fn);
   HMX_REQUIRE(H > 0 && HX > 0 && G > 0 && GC > 0 && H % HX == 0 && H % G == 0 && H % GC == 0,
               HMX_EINVAL, "%s: H=%d must be a multiple of HX=%d, G=%d and GC=%d", fn, H, HX, G, GC);
   HMX_REQUIRE(x && B && C && dt && A && dy && seg_table && seq_table && dx && dB && dC && ddt && dA &&
@@ -836,7 +847,7 @@ extern "C" int hmx_ssd_chunk_bwd(
   p.edec = reinterpret_cast<float*>(ws + st * 8);
   p.dx = dx; p.x_shared = HX < H;
   p.dB = dB; p.b_shared = G < H;
-  p.dC = dC;
+  p.dC = dC; p.gbf16 = grad_dtype == HMX_BF16;
   p.dz = static_cast<bf16*>(dz); p.ddt = ddt; p.dA = dA; p.dD = dD; p.dbias = ddt_bias;
   p.dh0 = dh0;
   p.H = H; p.HX = HX; p.G = G; p.GC = GC; p.softplus = dt_softplus;

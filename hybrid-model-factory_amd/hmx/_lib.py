@@ -89,7 +89,7 @@ SIGNATURES: dict[str, list] = {
                           _P, _I32, _I64, _I64, _P, _P, _P, _P, _I64, _I64,
                           _P, _I64, _I64, _P, _P, _P, _I32, _P, _I32,
                           _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _F32,
-                          _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _P],
+                          _P, _P, _P, _I32, _P, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _P],
     "hmx_ssd_chunk_bwd_workspace_bytes": [_I32, _I32, _I32, _I32],
     "hmx_causal_conv1d_fwd": [_P, _I64, _P, _I64, _I32, _P, _I32, _I32, _P, _I32, _P, _I64, _I64,
                               _I32, _P, _I32, _I64, _P, _P, _I32, _I32, _I32, _P],

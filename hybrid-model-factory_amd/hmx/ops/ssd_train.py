@@ -35,8 +35,9 @@ def ssd_chunk_scan_bwd(x, dt, A, B, C, D, z, dt_bias, dt_softplus, dt_limit, bou
                        d_final=None, want_dh0=False):
     """Gradients of the flattened scan (the _ssd_scan layout: x [T,HX,P], dt [T,H],
     B [T,G,N], C [T,GC,N], z, dy [T,H,P]; h0 fp32 [nseq,H,P,N] or None; d_final fp32
-    [nseq,H,P,N] or None).  Returns fp32 (dx, ddt, dA [H], dB, dC, dD [H,P] or None,
-    ddt_bias [H] or None, dh0 or None) and dz (bf16) or None."""
+    [nseq,H,P,N] or None).  Returns (dx, ddt, dA [H], dB, dC, dD [H,P] or None,
+    ddt_bias [H] or None, dh0 or None, dz or None): dx, dB, dC in bf16 unless x or B
+    is shared by several heads (then fp32), dz bf16, the rest fp32."""
     T, HX, P = x.shape
     H = dt.shape[1]
     G, N, GC = B.shape[1], B.shape[2], C.shape[1]
@@ -59,12 +60,15 @@ def ssd_chunk_scan_bwd(x, dt, A, B, C, D, z, dt_bias, dt_softplus, dt_limit, bou
               else D.to(torch.float32)).contiguous()
     bias = None if dt_bias is None else dt_bias.to(torch.float32).contiguous()
     f32 = dict(dtype=torch.float32, device=dev)
-    # shared operands accumulate; tokens outside every sequence keep zero gradients
+    # shared operands accumulate (fp32); otherwise dx, dB, dC are written in bf16;
+    # tokens outside every sequence keep zero gradients
     full = sum(e - a for a, e in bounds) == T
     alloc = lambda shared: torch.empty if (full and not shared) else torch.zeros
-    dx = alloc(HX < H)(T, HX, P, **f32)
-    dB = alloc(G < H and G != GC)(T, G, N, **f32)
-    dC = alloc(False)(T, GC, N, **f32)
+    acc_x, acc_b = HX < H, G < H and G != GC
+    gdt = torch.float32 if (acc_x or acc_b) else torch.bfloat16
+    dx = alloc(acc_x)(T, HX, P, dtype=gdt, device=dev)
+    dB = alloc(acc_b)(T, G, N, dtype=gdt, device=dev)
+    dC = alloc(False)(T, GC, N, dtype=gdt, device=dev)
     dz = None if z is None else alloc(False)(T, H, P, dtype=torch.bfloat16, device=dev)
     ddt = alloc(False)(T, H, **f32)
     dA = torch.zeros(H, **f32)
@@ -89,7 +93,8 @@ def ssd_chunk_scan_bwd(x, dt, A, B, C, D, z, dt_bias, dt_softplus, dt_limit, bou
               _lib.ptr(h0), _lib.ptr(d_final),
               _lib.ptr(seg), nrows, _lib.ptr(sq), nseq, H, HX, G, GC, P, N,
               int(bool(dt_softplus)), lo, hi,
-              _lib.ptr(dx), _lib.ptr(dB), _lib.ptr(dC), _lib.ptr(dz), _lib.ptr(ddt),
+              _lib.ptr(dx), _lib.ptr(dB), _lib.ptr(dC), _lib.dtype_code(dx), _lib.ptr(dz),
+              _lib.ptr(ddt),
               _lib.ptr(dA), _lib.ptr(dD), _lib.ptr(dbias), _lib.ptr(dh0),
               _lib.ptr(ws), ws.numel(), _lib.stream_of(x))
     return dx, ddt, dA, dB, dC, dD, dbias, dh0, dz

@@ -579,9 +579,10 @@ size_t hmx_ssd_chunk_workspace_bytes(int32_t nseg_total, int32_t nseq, int32_t H
  *  C [tokens, GC, N], z and dy [tokens, H, P], dt [tokens, H] f32/bf16/f16, fp32 A,
  *  D [H, P], dt_bias).  h0: fp32 [nseq, H, P, N] start states or NULL (zero);
  *  d_final: fp32 [nseq, H, P, N] gradient of the end states, or NULL.
- *  Outputs, contiguous: dx fp32 [tokens, HX, P] (zero-filled by the caller when
- *  HX < H: it accumulates), dB fp32 [tokens, G, N] (zero-filled when G < H and
- *  G != GC), dC fp32 [tokens, GC, N]; dz bf16 [tokens, H, P] (when z is
+ *  Outputs, contiguous: dx [tokens, HX, P], dB [tokens, G, N], dC [tokens, GC, N]
+ *  in grad_dtype (HMX_F32, or HMX_BF16 when none accumulates: HX = H and G = H or
+ *  G = GC); dx accumulates when HX < H and dB when G < H and G != GC (then fp32,
+ *  zero-filled by the caller); dz bf16 [tokens, H, P] (when z is
  *  given); ddt fp32 [tokens, H] (gradient of the raw dt); dA fp32 [H], dD fp32
  *  [H, P] (or NULL), ddt_bias fp32 [H] (or NULL), all zero-filled by the caller
  *  (they accumulate); dh0 fp32 [nseq, H, P, N] or NULL.  P, N in {64, 128}; z only
@@ -602,7 +603,8 @@ int hmx_ssd_chunk_bwd(const void* x, int64_t x_ts, int64_t x_hs,
                       const int32_t* seg_table, int32_t nrows, const int32_t* seq_table,
                       int32_t nseq, int32_t H, int32_t HX, int32_t G, int32_t GC, int32_t P,
                       int32_t N, int32_t dt_softplus, float dt_min, float dt_max,
-                      float* dx, float* dB, float* dC, void* dz, float* ddt, float* dA,
+                      void* dx, void* dB, void* dC, int32_t grad_dtype, void* dz,
+                      float* ddt, float* dA,
                       float* dD, float* ddt_bias, float* dh0,
                       void* workspace, size_t workspace_bytes, void* stream);
 
