@@ -28,7 +28,8 @@
 // with its own kernels (training/.../layers/mamba/mamba2.py:555-580 calls it).
 //
 // Three launches over 64-token chunks (rows of a segment table, one chunk each):
-//   ssd_bwd_local_kernel  (chunk, head): the chunk's zero-start end state
+//   ssd_bwd_local_kernel  (chunk, C group's heads in turn; chunk, head at headdim
+//                          128): the chunk's zero-start end state
 //                          sum_s e^{A_L - A_s} dt'_s x_s B_s^T, its share
 //                          sum_t e^{A_t} g_t C_t^T of dS0, and e^{A_L}
 //   ssd_bwd_scan_kernel   (sequence, head, 1024 state elements): the forward chain
@@ -145,6 +146,7 @@ constexpr int local_lds_bytes() { return 2 * L * (P + 8) * 2 + 2 * L * (N + 8) *
 template <int P, int N>
 __global__ __launch_bounds__(NTHR) void ssd_bwd_local_kernel(Params p) {
   constexpr int LDX = P + 8, LDB = N + 8;
+  constexpr int VX = L * P / 8 / NTHR, VB = L * N / 8 / NTHR;
   extern __shared__ __align__(16) unsigned char lsm[];
   bf16* sG = reinterpret_cast<bf16*>(lsm);                     // e^{A_t} g_t       [L][LDX]
   bf16* sXW = sG + L * LDX;                                    // dt'_s e^{A_L-A_s} x_s
@@ -154,88 +156,156 @@ __global__ __launch_bounds__(NTHR) void ssd_bwd_local_kernel(Params p) {
   float* sWT = sEA + L;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int H = p.H;
-  const int r = blockIdx.x / H, h = blockIdx.x % H;
+  const int q4 = lane >> 4, l16 = lane & 15;
+  const int H = p.H, GC = p.GC, HC = H / GC, HB = H / p.G, HXS = H / p.HX;
+  // headdim 64: one workgroup per (chunk, C group), C staged once (B too when its
+  // groups are C's), the group's heads in turn with the next one's rows loading
+  // into registers during the current one's products.  Headdim 128: one workgroup
+  // per (chunk, head) (the rows of a second head would not fit in registers).
+  constexpr bool AHEAD = P == 64;
+  const int per_row = AHEAD ? GC : H, nh = AHEAD ? HC : 1;
+  const int r = blockIdx.x / per_row;
+  const int h_first = AHEAD ? (blockIdx.x % per_row) * HC : blockIdx.x % per_row;
+  const int gc = h_first / HC;
   const Row ro = load_row(p.seg, r);
   const int tok0 = ro.bos, nval = ro.eos - ro.bos;
-  const int hx = h / (H / p.HX), g = h / (H / p.G), gc = h / (H / p.GC);
-  if (wave == 0) {
-    const Tok tk = token_scalars(p, h, tok0, nval, lane);
-    const float aend = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, tk.acs), 63));
-    sEA[lane] = fast_exp(tk.acs);
-    sWT[lane] = tk.dtv * fast_exp(aend - tk.acs);
-    if (lane == L - 1) p.edec[(int64_t)r * H + h] = expf(aend);
-  }
-  // B and C rows (zero past the chunk)
+  const bool b_once = AHEAD && p.G == GC;
 #pragma unroll
-  for (int i = 0; i < L * N / 8 / NTHR; ++i) {
+  for (int i = 0; i < VB; ++i) {
     const int e = (i * NTHR + tid) * 8, t = e / N, c = e % N;
-    bf16x8 bv = {}, cv = {};
+    bf16x8 cv = {}, bv = {};
     if (t < nval) {
-      bv = *reinterpret_cast<const bf16x8*>(p.B + (int64_t)(tok0 + t) * p.b_ts + (int64_t)g * p.b_gs + c);
       cv = *reinterpret_cast<const bf16x8*>(p.C + (int64_t)(tok0 + t) * p.c_ts + (int64_t)gc * p.c_gs + c);
+      if (b_once)
+        bv = *reinterpret_cast<const bf16x8*>(p.B + (int64_t)(tok0 + t) * p.b_ts +
+                                              (int64_t)(h_first / HB) * p.b_gs + c);
     }
-    *reinterpret_cast<bf16x8*>(sB + t * LDB + c) = bv;
     *reinterpret_cast<bf16x8*>(sC + t * LDB + c) = cv;
+    if (b_once) *reinterpret_cast<bf16x8*>(sB + t * LDB + c) = bv;
   }
-  __syncthreads();   // sEA, sWT
+  constexpr int VZ = P == 64 ? VX : 1;
+  struct In { bf16x8 x[VX], dy[VX], z[VZ], b[VB]; float dt; };
+  const auto fetch = [&](int h, In& q) {
+    const int hx = h / HXS, g = h / HB;
 #pragma unroll
-  for (int i = 0; i < L * P / 8 / NTHR; ++i) {
-    const int e = (i * NTHR + tid) * 8, t = e / P, c = e % P;
-    bf16x8 o = {}, xw = {};
-    if (t < nval) {
-      const bf16x8 dv = *reinterpret_cast<const bf16x8*>(p.dy + (int64_t)(tok0 + t) * p.dy_ts +
-                                                          (int64_t)h * p.dy_hs + c);
-      const bf16x8 xv = *reinterpret_cast<const bf16x8*>(p.x + (int64_t)(tok0 + t) * p.x_ts +
-                                                          (int64_t)hx * p.x_hs + c);
-      bf16x8 zz = {};
-      if (p.z) zz = *reinterpret_cast<const bf16x8*>(p.z + (int64_t)(tok0 + t) * p.z_ts +
-                                                    (int64_t)h * p.z_hs + c);
+    for (int i = 0; i < VX; ++i) {
+      const int e = (i * NTHR + tid) * 8, t = e / P, c = e % P;
+      q.x[i] = q.dy[i] = bf16x8{};
+      if constexpr (P == 64) q.z[i] = bf16x8{};
+      if (t < nval) {
+        q.dy[i] = *reinterpret_cast<const bf16x8*>(p.dy + (int64_t)(tok0 + t) * p.dy_ts + (int64_t)h * p.dy_hs + c);
+        q.x[i] = *reinterpret_cast<const bf16x8*>(p.x + (int64_t)(tok0 + t) * p.x_ts + (int64_t)hx * p.x_hs + c);
+        if constexpr (P == 64) {
+          if (p.z) q.z[i] = *reinterpret_cast<const bf16x8*>(p.z + (int64_t)(tok0 + t) * p.z_ts + (int64_t)h * p.z_hs + c);
+        }
+      }
+    }
+    if (!b_once) {
+#pragma unroll
+      for (int i = 0; i < VB; ++i) {
+        const int e = (i * NTHR + tid) * 8, t = e / N, c = e % N;
+        q.b[i] = bf16x8{};
+        if (t < nval)
+          q.b[i] = *reinterpret_cast<const bf16x8*>(p.B + (int64_t)(tok0 + t) * p.b_ts + (int64_t)g * p.b_gs + c);
+      }
+    }
+    q.dt = (wave == 0 && lane < nval)
+               ? load_any(p.dt, (int64_t)(tok0 + lane) * p.dt_ts + (int64_t)h * p.dt_hs, p.dt_dt) : 0.f;
+  };
+  In in;
+  if constexpr (AHEAD) fetch(h_first, in);
+  constexpr int PBW = P / 16 / 4;   // p blocks per wave
+  for (int ih = 0; ih < nh; ++ih) {
+    const int h = h_first + ih;
+    if (wave == 0) {
+      const Tok tk = AHEAD ? token_scalars_raw(p, h, in.dt, nval, lane)
+                           : token_scalars(p, h, tok0, nval, lane);
+      const float aend = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, tk.acs), 63));
+      sEA[lane] = fast_exp(tk.acs);
+      sWT[lane] = tk.dtv * fast_exp(aend - tk.acs);
+      if (lane == L - 1) p.edec[(int64_t)r * H + h] = expf(aend);
+    }
+    __syncthreads();   // the scalars; the previous head's products have read the tiles
+    if constexpr (!AHEAD) {   // headdim 128: the rows straight from memory
+      const int hx = h / HXS, g = h / HB;
+#pragma unroll
+      for (int i = 0; i < VX; ++i) {
+        const int e = (i * NTHR + tid) * 8, t = e / P, c = e % P;
+        in.x[i] = in.dy[i] = bf16x8{};
+        if (t < nval) {
+          in.dy[i] = *reinterpret_cast<const bf16x8*>(p.dy + (int64_t)(tok0 + t) * p.dy_ts + (int64_t)h * p.dy_hs + c);
+          in.x[i] = *reinterpret_cast<const bf16x8*>(p.x + (int64_t)(tok0 + t) * p.x_ts + (int64_t)hx * p.x_hs + c);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < VB; ++i) {
+        const int e = (i * NTHR + tid) * 8, t = e / N, c = e % N;
+        bf16x8 bv = {};
+        if (t < nval)
+          bv = *reinterpret_cast<const bf16x8*>(p.B + (int64_t)(tok0 + t) * p.b_ts + (int64_t)g * p.b_gs + c);
+        *reinterpret_cast<bf16x8*>(sB + t * LDB + c) = bv;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < VX; ++i) {
+      const int e = (i * NTHR + tid) * 8, t = e / P, c = e % P;
       const float ea = sEA[t], wt = sWT[t];
+      bf16x8 o, xw;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        float v = (float)dv[j];
-        if (p.z) v *= silu((float)zz[j]);
+        float v = (float)in.dy[i][j];
+        if constexpr (P == 64) {
+          if (p.z) v *= silu((float)in.z[i][j]);
+        }
         o[j] = (bf16)(v * ea);
-        xw[j] = (bf16)((float)xv[j] * wt);
+        xw[j] = (bf16)((float)in.x[i][j] * wt);
+      }
+      *reinterpret_cast<bf16x8*>(sG + t * LDX + c) = o;
+      *reinterpret_cast<bf16x8*>(sXW + t * LDX + c) = xw;
+    }
+    if (AHEAD && !b_once) {
+#pragma unroll
+      for (int i = 0; i < VB; ++i) {
+        const int e = (i * NTHR + tid) * 8, t = e / N, c = e % N;
+        *reinterpret_cast<bf16x8*>(sB + t * LDB + c) = in.b[i];
       }
     }
-    *reinterpret_cast<bf16x8*>(sG + t * LDX + c) = o;
-    *reinterpret_cast<bf16x8*>(sXW + t * LDX + c) = xw;
-  }
-  __syncthreads();
-  // wave w: p rows [16 (w PBW + i), ...), all n tiles, for both products
-  const int q4 = lane >> 4, l16 = lane & 15;
-  constexpr int PBW = P / 16 / 4;   // p blocks per wave
-#pragma unroll
-  for (int which = 0; which < 2; ++which) {
-    const bf16* sa = which ? sXW : sG;
-    const bf16* sb = which ? sB : sC;
-    f32x4 acc[PBW][N / 16];
-#pragma unroll
-    for (int i = 0; i < PBW; ++i)
-#pragma unroll
-      for (int j = 0; j < N / 16; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int k0 = 0; k0 < L; k0 += 32) {
-      bf16x8 bf[N / 16];
-#pragma unroll
-      for (int j = 0; j < N / 16; ++j) bf[j] = frag_t(sb, LDB, k0, 16 * j, lane);
-#pragma unroll
-      for (int i = 0; i < PBW; ++i) {
-        const bf16x8 af = frag_t(sa, LDX, k0, 16 * (wave * PBW + i), lane);
-#pragma unroll
-        for (int j = 0; j < N / 16; ++j) acc[i][j] = mfma16(af, bf[j], acc[i][j]);
-      }
+    __syncthreads();
+    if constexpr (AHEAD) {
+      if (ih + 1 < nh) fetch(h + 1, in);
     }
-    bf16* dst = (which ? p.sloc : p.loc) + ((int64_t)r * H + h) * P * N;
+    // wave w: p rows [16 (w PBW + i), ...), all n tiles, for both products (one after
+    // the other: their tiles would not fit in registers together at headdim 128)
+#pragma unroll 1
+    for (int which = 0; which < 2; ++which) {
+      const bf16* sa = which ? sXW : sG;
+      const bf16* sb = which ? sB : sC;
+      f32x4 acc[PBW][N / 16];
 #pragma unroll
-    for (int i = 0; i < PBW; ++i)
+      for (int i = 0; i < PBW; ++i)
 #pragma unroll
-      for (int j = 0; j < N / 16; ++j)
+        for (int j = 0; j < N / 16; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int v = 0; v < 4; ++v)
-          dst[(16 * (wave * PBW + i) + 4 * q4 + v) * N + 16 * j + l16] = (bf16)acc[i][j][v];
+      for (int k0 = 0; k0 < L; k0 += 32) {
+        bf16x8 bf[N / 16];
+#pragma unroll
+        for (int j = 0; j < N / 16; ++j) bf[j] = frag_t(sb, LDB, k0, 16 * j, lane);
+#pragma unroll
+        for (int i = 0; i < PBW; ++i) {
+          const bf16x8 af = frag_t(sa, LDX, k0, 16 * (wave * PBW + i), lane);
+#pragma unroll
+          for (int j = 0; j < N / 16; ++j) acc[i][j] = mfma16(af, bf[j], acc[i][j]);
+        }
+      }
+      bf16* dst = (which ? p.sloc : p.loc) + ((int64_t)r * H + h) * P * N;
+#pragma unroll
+      for (int i = 0; i < PBW; ++i)
+#pragma unroll
+        for (int j = 0; j < N / 16; ++j)
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            dst[(16 * (wave * PBW + i) + 4 * q4 + v) * N + 16 * j + l16] = (bf16)acc[i][j][v];
+    }
   }
 }
 
@@ -774,7 +844,8 @@ void launch(const Params& p, hipStream_t s) {
                             hipFuncAttributeMaxDynamicSharedMemorySize, lsm);
   (void)hipFuncSetAttribute((const void*)ssd_bwd_chunk_kernel<P, N>,
                             hipFuncAttributeMaxDynamicSharedMemorySize, smem);
-  hipLaunchKernelGGL((ssd_bwd_local_kernel<P, N>), dim3(p.nrows * p.H), dim3(NTHR), lsm, s, p);
+  hipLaunchKernelGGL((ssd_bwd_local_kernel<P, N>), dim3(p.nrows * (P == 64 ? p.GC : p.H)),
+                     dim3(NTHR), lsm, s, p);
   hipLaunchKernelGGL(ssd_bwd_scan_kernel, dim3(p.nseq * p.H, (P * N + 1023) / 1024), dim3(256), 0,
                      s, p, P * N);
   hipLaunchKernelGGL((ssd_bwd_chunk_kernel<P, N>), dim3(p.nrows * p.GC), dim3(NTHR), smem, s, p);
