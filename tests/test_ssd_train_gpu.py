@@ -166,20 +166,25 @@ def test_backward_headdim_128_with_z_raises(dev):
         y.float().sum().backward()
 
 
-@pytest.mark.parametrize("gb,gc", [(4, 2), (1, 2)])
-def test_backward_training_layer_layout(dev, gb, gc):
+@pytest.mark.parametrize("gb,gc,bf16_params", [(4, 2, False), (1, 2, False), (4, 2, True)])
+def test_backward_training_layer_layout(dev, gb, gc, bf16_params):
     """The training layer's operands (mamba2.py:541-556): x and B repeated to the H
-    heads, C with its own ngroups, D per head, no z (gb = 4); and B groups wider than
-    C's (gb = 1: B's gradient accumulates across workgroups)."""
+    heads, C with its own ngroups, D per head, no z (gb = 4); B groups wider than C's
+    (gb = 1: B's gradient accumulates across workgroups); and dt, D, dt_bias in the
+    model's bf16 (their gradients come back in bf16)."""
     inp, wy, wf = _inputs(1, 200, 4, gb, 64, 128, 900 + gb, False, False)
     g0 = torch.Generator().manual_seed(901)
     inp["C"] = torch.randn(1, 200, gc, 128, generator=g0).bfloat16()
+    if bf16_params:
+        for k in ("dt", "D", "dt_bias"):
+            inp[k] = inp[k].bfloat16()
     inp["initial_states"] = None
     kw = dict(dt_softplus=True)
     g = _grads(inp, wy, wf, kw, dev, None)
     torch.cuda.synchronize()
     g_ref = _grads(inp, wy, wf, kw, None, torch.float64)
     assert g["C"].shape == inp["C"].shape
+    assert all(g[k].dtype == inp[k].dtype for k in g)
     sA = _dA_scale(inp, wy, wf, kw)
     for k in g_ref:
         _check(g[k], g_ref[k], f"train_layout d{k}", scale=sA if k == "A" else None)
