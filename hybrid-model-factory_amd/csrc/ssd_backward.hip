@@ -103,7 +103,7 @@ __device__ __forceinline__ float scan64(float x, int lane) {
   return lane >= 32 ? x + lo : x;
 }
 
-__device__ __forceinline__ float silu(float z) { return z / (1.f + fast_exp(-z)); }
+__device__ __forceinline__ float silu(float z) { return z * __builtin_amdgcn_rcpf(1.f + fast_exp(-z)); }
 
 // a stored (not accumulated) gradient element, bf16 or fp32
 __device__ __forceinline__ void st_grad(void* base, int64_t i, float v, int bf) {
@@ -668,7 +668,7 @@ __global__ __launch_bounds__(NTHR, 1) void ssd_bwd_chunk_kernel(Params p) {
           float yp = yi[i][v] + y_s;
           if (p.D) yp += F(K::FDV, pc) * (float)sX[t * LDX + pc];
           const float zf = (float)sZ[t * LDX + pc];
-          const float sg = 1.f / (1.f + fast_exp(-zf));
+          const float sg = __builtin_amdgcn_rcpf(1.f + fast_exp(-zf));
           const float dsilu = sg * (1.f + zf * (1.f - sg));
           p.dz[(int64_t)(tok0 + t) * H * P + (int64_t)h * P + pc] =
               (bf16)((float)sDY[t * LDX + pc] * yp * dsilu);

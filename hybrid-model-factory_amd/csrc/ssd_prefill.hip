@@ -319,7 +319,16 @@ __global__ __launch_bounds__(NTHR, (P == 128 && MODE == MODE_OUT) ? 1 : 2) void 
     SC(buf, S_W, lane) = d * fast_exp(alast - acs);
     SC(buf, S_EA, lane) = fast_exp(acs);
   };
-  if (si.c_start < si.c_end && wave == NTHR / 64 - 1) make_scalars(ra.dt, si.c_start, 0);
+  if (MODE == MODE_LOCAL && si.c_start < si.c_end && wave == NTHR / 64 - 1)
+    make_scalars(ra.dt, si.c_start, 0);
+  // D of this wave's p-rows, loaded once (a load inside the loop would be waited
+  // for with everything issued before it, the next chunk's rows included)
+  f32x4 dreg[PB];
+#pragma unroll
+  for (int i = 0; i < PB; ++i)
+    dreg[i] = (MODE == MODE_OUT && p.D)
+                  ? *reinterpret_cast<const f32x4*>(p.D + h * P + 16 * (PB * wave + i) + 4 * q4)
+                  : f32x4{0.f, 0.f, 0.f, 0.f};
 
   // coalesced store of the y tile staged in sY (chunk starting at tok0); the plain
   // pass also sums the rows (ysum: inf or NaN there flags the walk)
@@ -367,6 +376,10 @@ __global__ __launch_bounds__(NTHR, (P == 128 && MODE == MODE_OUT) ? 1 : 2) void 
 #pragma unroll
       for (int i = 0; i < K::VX; ++i) zst[i] = cur.z[i];
     }
+    // OUT keeps one raw chunk in flight: its scalars come from the chunk's own dt
+    // here, before the refill (the staging above has waited for these rows), so the
+    // chunk's work never waits for the rows in flight
+    if (MODE == MODE_OUT && wave == NTHR / 64 - 1) make_scalars(cur.dt, c, cb);
     if (c + AHEAD < si.c_end)
       load_raw<P, N, MODE>(cur, p, tok0 + AHEAD * L, nval_of(c + AHEAD), h, hx, g, gc, tid);
     lds_barrier();
@@ -487,8 +500,6 @@ __global__ __launch_bounds__(NTHR, (P == 128 && MODE == MODE_OUT) ? 1 : 2) void 
       else if (wave == 1) m_tile(I1{});
       else if (wave == 2) m_tile(I2{});
       else m_tile(I3{});
-      // the last wave (fewest tiles) turns the next chunk's dt into its scalars
-      if (wave == NTHR / 64 - 1 && c + 1 < si.c_end) make_scalars(nxt.dt, c + 1, cb ^ 1);
     } else if (wave == NTHR / 64 - 1 && c + 1 < si.c_end) {
       make_scalars(nxt.dt, c + 1, cb ^ 1);
     }
@@ -571,8 +582,7 @@ __global__ __launch_bounds__(NTHR, (P == 128 && MODE == MODE_OUT) ? 1 : 2) void 
 #pragma unroll
       for (int i = 0; i < PB; ++i) {
         const int p0 = 16 * (PB * wave + i) + 4 * q4;
-        const f32x4 dv = p.D ? *reinterpret_cast<const f32x4*>(p.D + h * P + p0)
-                             : f32x4{0.f, 0.f, 0.f, 0.f};
+        const f32x4 dv = dreg[i];
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) {
           const int t = 16 * tb + l16;
@@ -586,7 +596,7 @@ __global__ __launch_bounds__(NTHR, (P == 128 && MODE == MODE_OUT) ? 1 : 2) void 
             float yv = YT[i][tb][v] + dv[v] * (SAFE ? (float)xvb[v] : (float)xv[v]);
             if (p.z) {
               const float zz = (float)zv[v];
-              yv *= zz / (1.f + fast_exp(-zz));
+              yv *= zz * __builtin_amdgcn_rcpf(1.f + fast_exp(-zz));
             }
             out[v] = (bf16)yv;
           }
