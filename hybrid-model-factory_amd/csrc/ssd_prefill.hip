@@ -117,10 +117,17 @@ struct Cfg {
 // per-token scalar arrays (fp32 [L] each)
 enum { S_DT, S_ACS, S_W, S_EA };
 
-__device__ __forceinline__ float ld_any(const void* p, int64_t i, int dt) {
-  if (dt == HMX_F32) return static_cast<const float*>(p)[i];
-  if (dt == HMX_BF16) return (float)static_cast<const bf16*>(p)[i];
-  return (float)static_cast<const f16*>(p)[i];
+// The raw bits of element i (one load in either dtype branch, so the wait for it
+// can be placed where the value is used, after the loads issued later) and their
+// value as a float.
+__device__ __forceinline__ uint32_t ld_bits(const void* p, int64_t i, int dt) {
+  if (dt == HMX_F32) return static_cast<const uint32_t*>(p)[i];
+  return static_cast<const uint16_t*>(p)[i];
+}
+__device__ __forceinline__ float bits_f32(uint32_t b, int dt) {
+  if (dt == HMX_F32) return __builtin_bit_cast(float, b);
+  if (dt == HMX_BF16) return __builtin_bit_cast(float, b << 16);
+  return (float)__builtin_bit_cast(f16, (uint16_t)b);
 }
 
 __device__ __forceinline__ SegInfo load_seg(const int* seg, int s) {
@@ -138,7 +145,7 @@ __device__ __forceinline__ float scan64(float x, int lane) {
 template <int P, int N>
 struct Raw {
   bf16x8 x[Cfg<P, N>::VX], z[Cfg<P, N>::VX], b[Cfg<P, N>::VB], c[Cfg<P, N>::VB];
-  float dt;
+  uint32_t dt;   // dt of token `lane` (last wave) as stored: converted when used
 };
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -194,7 +201,7 @@ __device__ __forceinline__ void load_raw(Raw<P, N>& r, const Params& p, int tok0
   }
   const int t = tid - (NTHR - L);   // the last wave loads dt (lane t = token t)
   if (t >= 0)
-    r.dt = t < nval ? ld_any(p.dt, (int64_t)(tok0 + t) * p.dt_ts + h * p.dt_hs, p.dt_dt) : 0.f;
+    r.dt = t < nval ? ld_bits(p.dt, (int64_t)(tok0 + t) * p.dt_ts + h * p.dt_hs, p.dt_dt) : 0u;
 }
 
 // bf16 rows staged as they are (the SAFE pass): the 16-bit loads of the fp16 path
@@ -307,8 +314,8 @@ __global__ __launch_bounds__(NTHR, (P == 128 && MODE == MODE_OUT) ? 1 : 2) void 
 
   // dt' = clamp(softplus(dt + bias)), A_t = cumsum(dt' A), w_t = dt' e^{A_L - A_t},
   // e^{A_t} of chunk c into scalar buffer `buf` (the last wave; lane = token)
-  const auto make_scalars = [&](float dt_raw, int c, int buf) {
-    float d = dt_raw + bias;
+  const auto make_scalars = [&](uint32_t dt_bits, int c, int buf) {
+    float d = bits_f32(dt_bits, p.dt_dt) + bias;
     if (p.softplus) d = softplus20(d);
     d = fminf(fmaxf(d, p.dt_min), p.dt_max);
     if (lane >= nval_of(c)) d = 0.f;
