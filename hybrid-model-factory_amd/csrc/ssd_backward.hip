@@ -114,6 +114,19 @@ __device__ __forceinline__ void st_grad(void* base, int64_t i, float v, int bf) 
 // Per-token scalars of a chunk, lane t of one wave: dt' (0 past the chunk's
 // tokens), A_t, and the factor d dt'/d dt (clamp pass times the softplus slope).
 struct Tok { float dtv, acs, fac; };
+// dt prefetched for the next head: its raw bits (one load in either dtype
+// branch), converted where the scalars are formed.  Converting at the load (as
+// load_any does) would wait there for every load issued before it, the rest of
+// the prefetch included.
+__device__ __forceinline__ uint32_t ld_bits(const void* p, int64_t i, int dt) {
+  if (dt == HMX_F32) return static_cast<const uint32_t*>(p)[i];
+  return static_cast<const uint16_t*>(p)[i];
+}
+__device__ __forceinline__ float bits_f32(uint32_t b, int dt) {
+  if (dt == HMX_F32) return __builtin_bit_cast(float, b);
+  if (dt == HMX_BF16) return __builtin_bit_cast(float, b << 16);
+  return (float)__builtin_bit_cast(f16, (uint16_t)b);
+}
 __device__ __forceinline__ Tok token_scalars_raw(const Params& p, int h, float dt_raw, int nval,
                                                  int lane) {
   float d = dt_raw + (p.dt_bias ? p.dt_bias[h] : 0.f);
@@ -184,7 +197,7 @@ __global__ __launch_bounds__(NTHR) void ssd_bwd_local_kernel(Params p) {
     if (b_once) *reinterpret_cast<bf16x8*>(sB + t * LDB + c) = bv;
   }
   constexpr int VZ = P == 64 ? VX : 1;
-  struct In { bf16x8 x[VX], dy[VX], z[VZ], b[VB]; float dt; };
+  struct In { bf16x8 x[VX], dy[VX], z[VZ], b[VB]; uint32_t dt; };
   const auto fetch = [&](int h, In& q) {
     const int hx = h / HXS, g = h / HB;
 #pragma unroll
@@ -210,7 +223,7 @@ __global__ __launch_bounds__(NTHR) void ssd_bwd_local_kernel(Params p) {
       }
     }
     q.dt = (wave == 0 && lane < nval)
-               ? load_any(p.dt, (int64_t)(tok0 + lane) * p.dt_ts + (int64_t)h * p.dt_hs, p.dt_dt) : 0.f;
+               ? ld_bits(p.dt, (int64_t)(tok0 + lane) * p.dt_ts + (int64_t)h * p.dt_hs, p.dt_dt) : 0u;
   };
   In in;
   if constexpr (AHEAD) fetch(h_first, in);
@@ -218,7 +231,7 @@ __global__ __launch_bounds__(NTHR) void ssd_bwd_local_kernel(Params p) {
   for (int ih = 0; ih < nh; ++ih) {
     const int h = h_first + ih;
     if (wave == 0) {
-      const Tok tk = AHEAD ? token_scalars_raw(p, h, in.dt, nval, lane)
+      const Tok tk = AHEAD ? token_scalars_raw(p, h, bits_f32(in.dt, p.dt_dt), nval, lane)
                            : token_scalars(p, h, tok0, nval, lane);
       const float aend = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, tk.acs), 63));
       sEA[lane] = fast_exp(tk.acs);
@@ -409,7 +422,8 @@ template <int P, int N>
 struct HeadIn {
   bf16x8 x[L * P / 8 / NTHR], dy[L * P / 8 / NTHR], z[L * P / 8 / NTHR];
   bf16x8 s0[P * N / 8 / NTHR], ds[P * N / 8 / NTHR], b[L * N / 8 / NTHR];
-  float dt, d;
+  uint32_t dt;   // as stored (converted where the scalars are formed)
+  float d;
 };
 
 template <int P, int N>
@@ -497,7 +511,7 @@ __global__ __launch_bounds__(NTHR, 1) void ssd_bwd_chunk_kernel(Params p) {
       }
     }
     q.dt = (wave == 0 && lane < nval)
-               ? load_any(p.dt, (int64_t)(tok0 + lane) * p.dt_ts + (int64_t)h * p.dt_hs, p.dt_dt) : 0.f;
+               ? ld_bits(p.dt, (int64_t)(tok0 + lane) * p.dt_ts + (int64_t)h * p.dt_hs, p.dt_dt) : 0u;
     q.d = (p.D && tid < P) ? p.D[(int64_t)h * P + tid] : 0.f;
   };
 
@@ -561,7 +575,7 @@ __global__ __launch_bounds__(NTHR, 1) void ssd_bwd_chunk_kernel(Params p) {
     }
     if (tid < P) F(K::FDV, tid) = in.d;
     if (wave == 0) {
-      const Tok tk = token_scalars_raw(p, h, in.dt, nval, lane);
+      const Tok tk = token_scalars_raw(p, h, bits_f32(in.dt, p.dt_dt), nval, lane);
       const float aend = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, tk.acs), 63));
       F(F_DT, lane) = tk.dtv;
       F(F_ACS, lane) = tk.acs;
