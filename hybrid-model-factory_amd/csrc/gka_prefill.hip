@@ -113,6 +113,20 @@ struct Params {
   const float* rhs32;                     // SM_DQ: an fp32 right-hand side in place of p.q
 };
 
+// The fused gates' raw projection values as bits (one load in either dtype
+// branch), held in a float register and converted where the gates are formed: a
+// conversion at the load would wait there for the rows loaded just before.
+__device__ __forceinline__ uint32_t ld_bits(const void* p, int64_t i, int dt) {
+  if (dt == HMX_F32) return static_cast<const uint32_t*>(p)[i];
+  return static_cast<const uint16_t*>(p)[i];
+}
+__device__ __forceinline__ float bits_as_f(uint32_t b) { return __builtin_bit_cast(float, b); }
+__device__ __forceinline__ float bits_f32(float held, int dt) {
+  const uint32_t b = __builtin_bit_cast(uint32_t, held);
+  if (dt == HMX_F32) return held;
+  if (dt == HMX_BF16) return __builtin_bit_cast(float, b << 16);
+  return (float)__builtin_bit_cast(f16, (uint16_t)b);
+}
 __device__ __forceinline__ float ldsc(const void* p, int64_t i, int dt) {
   if (dt == HMX_F32) return static_cast<const float*>(p)[i];
   if (dt == HMX_BF16) return (float)static_cast<const bf16*>(p)[i];
@@ -216,8 +230,8 @@ __device__ __forceinline__ void load_raw(Raw& r, const Params& p, const bf16* kh
     r.v[pass] = ok ? *reinterpret_cast<const bf16x8*>(vh + tok * p.kv_ts + f0) : bf16x8{};
     // fused: b itself (the gate is formed at staging, so no load is waited for here)
     r.b[pass] = !(ok && has_beta(p)) ? 0.f
-                : FG ? load_any(p.gp.b, tok * p.gp.b_token_stride + h * p.gp.b_head_stride,
-                                     p.gp.in_dtype)
+                : FG ? bits_as_f(ld_bits(p.gp.b, tok * p.gp.b_token_stride + h * p.gp.b_head_stride,
+                                         p.gp.in_dtype))
                           : ldsc(p.beta, tok * p.H + h, p.beta_dt);
   }
   const int lane = tid & 63;
@@ -225,7 +239,8 @@ __device__ __forceinline__ void load_raw(Raw& r, const Params& p, const bf16* kh
   const int64_t tk = tok0 + lane, gi = tk * p.H + h;
   if constexpr (FG) {     // a itself (fused: g and gk are formed at staging)
     r.g = (okg && p.gp.A_log)
-              ? load_any(p.gp.a, tk * p.gp.a_token_stride + h * p.gp.a_head_stride, p.gp.in_dtype)
+              ? bits_as_f(ld_bits(p.gp.a, tk * p.gp.a_token_stride + h * p.gp.a_head_stride,
+                                  p.gp.in_dtype))
               : 0.f;
     r.gk = 0.f;
   } else {
@@ -244,7 +259,7 @@ __device__ __forceinline__ void stage(const Stage& st, const Raw& r, const Param
   float gt = r.g, gkt = r.gk;
   if constexpr (FG) {     // the gates from the raw a (lanes of valid tokens)
     gt = (lane < nval && p.gp.A_log)
-             ? gp_g_of(p.gp, r.g, gate_exp(load_any(p.gp.A_log, h, p.gp.A_log_dtype)),
+             ? gp_g_of(p.gp, bits_f32(r.g, p.gp.in_dtype), gate_exp(load_any(p.gp.A_log, h, p.gp.A_log_dtype)),
                        load_any(p.gp.dt_bias, h, p.gp.dt_bias_dtype))
              : 0.f;
     gkt = p.gp.gk_from_g ? gt : 0.f;
@@ -261,7 +276,7 @@ __device__ __forceinline__ void stage(const Stage& st, const Raw& r, const Param
     const float ss = row_sumsq(r.k[pass]);
     const float be = !ok ? 0.f
                      : !has_beta(p) ? 1.f
-                     : (FG ? gp_beta_of(p.gp, r.b[pass]) : r.b[pass]) + EPS;
+                     : (FG ? gp_beta_of(p.gp, bits_f32(r.b[pass], p.gp.in_dtype)) : r.b[pass]) + EPS;
     const float sk = !ok ? 0.f : (p.l2norm ? be / sqrtf(ss) : be);
     const float sv = be;
     const float drow = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(row << 2, __builtin_bit_cast(int, dl)));
